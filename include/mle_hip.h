@@ -1,0 +1,285 @@
+/*
+ * mle_hip.h -- C ABI of the MI355X (gfx950) backward / optimizer hot path.
+ *
+ * This is the boundary that replaces the `<<<...>>>` call sites inside the
+ * GraphOperations lambdas of ML_Engine (Engine/engine.cu) and the host wrappers
+ * of Includes/kernels.h.  The C++ graph layer (ml_engine_amd/engine/engine.h)
+ * calls only these functions; a different host language binds the same symbols.
+ *
+ * Conventions
+ *  - Every function returns int: 0 = MLE_OK, < 0 = an mle_status.  The message
+ *    of the last failure on the calling thread is returned by mle_last_error().
+ *  - Tensors are plain device pointers to fp32 (int32 for token ids), row-major,
+ *    with the reference's [batch, channels, rows, cols] layout.
+ *  - Calls enqueue work on `stream` (a hipStream_t; NULL = the null stream) and
+ *    never synchronise, except mle_stream_sync, the mle_memcpy_h2d/d2h helpers
+ *    (which wait for their own copy) and mle_probe_read.
+ *  - Calls never allocate device memory, except mle_device_alloc and the arena
+ *    calls.  Kernels that need scratch take (ws, ws_bytes); the required size is
+ *    returned by the matching *_ws_bytes query.
+ *  - "accumulate" means the kernel adds into its destination (`+=`), as the
+ *    reference backward kernels do; "assign" overwrites.
+ */
+#ifndef MLE_HIP_H
+#define MLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mle_stream;              /* hipStream_t */
+typedef struct mle_arena_s* mle_arena; /* bump allocator over one device buffer */
+
+enum mle_status {
+  MLE_OK = 0,
+  MLE_ERR_INVALID = -1,     /* bad shape / argument (reference: print + exit) */
+  MLE_ERR_HIP = -2,         /* HIP runtime error (reference: CheckError)       */
+  MLE_ERR_OOM = -3,         /* allocation failed (reference: SafeCudaMalloc)   */
+  MLE_ERR_UNSUPPORTED = -4, /* shape outside what a kernel supports           */
+  MLE_ERR_WORKSPACE = -5    /* workspace smaller than *_ws_bytes reported      */
+};
+
+enum mle_act_kind { MLE_RELU = 0, MLE_GELU = 1, MLE_SILU = 2, MLE_TANH = 3, MLE_SIGMOID = 4, MLE_LEAKY_RELU = 5 };
+
+/* ------------------------------------------------------------------------- */
+/* Runtime: errors, device memory, streams, arena                            */
+/* ------------------------------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mle_last_error(void);
+/* Library version string, e.g. "mle_hip 0.1 gfx950". */
+const char* mle_version(void);
+/* Make `device` current and check that it is gfx950.  Replaces the implicit
+ * CUDA context creation of the reference. */
+int mle_init(int device);
+
+/* Device allocation.  Replaces SafeCudaMalloc (Includes/debugging_utils.h:98-110):
+ * returns MLE_ERR_OOM with the free/total memory in the message. */
+int mle_device_alloc(void** ptr, size_t bytes);
+int mle_device_free(void* ptr);
+int mle_memcpy_h2d(void* dst, const void* src, size_t bytes, mle_stream stream);
+/* Synchronous device-to-host copy (ReadValueAt, Engine/engine.cu:3-9). */
+int mle_memcpy_d2h(void* dst, const void* src, size_t bytes, mle_stream stream);
+int mle_memcpy_d2d(void* dst, const void* src, size_t bytes, mle_stream stream);
+
+int mle_stream_create(mle_stream* stream);
+int mle_stream_destroy(mle_stream stream);
+/* Wait for the stream; reports asynchronous kernel faults like CheckError
+ * (Engine/debug.cu:15-25). */
+int mle_stream_sync(mle_stream stream);
+
+/* Static arena: one device buffer, 256-byte aligned bump allocation.  Replaces
+ * the per-node cudaMalloc of NodeBackProp (Engine/engine.cu:45-64). */
+int mle_arena_create(size_t bytes, mle_arena* arena);
+int mle_arena_alloc(mle_arena arena, size_t bytes, void** ptr);
+int mle_arena_reset(mle_arena arena);
+int mle_arena_destroy(mle_arena arena);
+size_t mle_arena_used(mle_arena arena);
+size_t mle_arena_capacity(mle_arena arena);
+
+/* ------------------------------------------------------------------------- */
+/* Elementwise / data movement                                               */
+/* ------------------------------------------------------------------------- */
+
+/* x[i] = value.  fillKernel (Includes/kernels.h:13-19), Zerograd (Engine/engine.cu:312-326). */
+int mle_fill(mle_stream stream, float* x, float value, size_t n);
+/* z = x + scale*y.  ScaleAdd (Engine/kernels.cu:1718-1724). */
+int mle_scale_add(mle_stream stream, const float* x, const float* y, float* z, float scale, size_t n);
+/* y += scale*x (double scale, float storage).  Accumulate (Engine/kernels.cu:1693-1699). */
+int mle_accumulate(mle_stream stream, const float* x, float* y, double scale, size_t n);
+/* y = scale*x.  Scale_Write (Engine/kernels.cu:1677-1682), Write (Engine/kernels.cu:1670-1675) with scale 1. */
+int mle_scale_write(mle_stream stream, const float* x, float* y, float scale, size_t n);
+/* divide==0: x *= factor; divide==1: x /= factor.  SV (Includes/kernels.h:272-280). */
+int mle_scale_inplace(mle_stream stream, float* x, float factor, int divide, size_t n);
+/* x *= (float)s[0] or x /= (float)s[0] with s a device double.  SP (Includes/kernels.h:293-300). */
+int mle_scale_by_device(mle_stream stream, float* x, const double* s, int divide, size_t n);
+/* y[r, :] += b[:] for r < rows.  BCumAdd (Engine/kernels.cu:1586-1592). */
+int mle_bias_add_rows(mle_stream stream, float* y, const float* b, size_t rows, int cols);
+/* y = x + b[channel] over [B, C, HW].  broadcast_add (Engine/kernels.cu:1661-1668). */
+int mle_broadcast_channel_add(mle_stream stream, const float* x, const float* b, float* y, int batch, int channels, size_t hw);
+/* [B,1,S,H*D] <-> [B,H,S,D].  HeadifyColChannel (Engine/kernels.cu:1371-1406):
+ * flag 0: out[headified] = in[flat]   (HeadifytoChannel forward)
+ * flag 1: out[flat]     += in[headified] (HeadifytoChannel backward)
+ * flag 2: out[flat]      = in[headified] (DeHeadify forward)
+ * flag 3: out[headified] += in[flat]   (DeHeadify backward)
+ * The accumulating flags are plain adds: every destination is written once. */
+int mle_headify(mle_stream stream, const float* in, float* out, int batch, int heads, int seq, int head_dim, int flag);
+/* y = x + PE, PE = sin (even dims) / cos (odd dims) of pos/10000^(2i/cols).
+ * MatPEncoding (Engine/kernels.cu:166-185). */
+int mle_matpe(mle_stream stream, const float* x, float* y, int batch, int rows, int cols, int start_idx);
+/* Timestep embedding: cos half then sin half.  PEncoding (Engine/kernels.cu:147-164). */
+int mle_timestep_pe(mle_stream stream, float* y, int t, int dim);
+
+/* ------------------------------------------------------------------------- */
+/* Activations                                                               */
+/* ------------------------------------------------------------------------- */
+
+/* y = f(x).  ReLU/GeLU/SiLU/TaNH/Sigmoid/LeakyReLU (Engine/kernels.cu:1214-1328). */
+int mle_act_fwd(mle_stream stream, int kind, const float* x, float* y, size_t n);
+/* dx += dy * f'(x)  (accumulate).  deriv_* (Engine/kernels.cu:1223-1328). */
+int mle_act_bwd(mle_stream stream, int kind, const float* x, const float* dy, float* dx, size_t n);
+
+/* ------------------------------------------------------------------------- */
+/* GEMM (fp32 MFMA)                                                          */
+/* ------------------------------------------------------------------------- */
+
+/* C[b] = alpha * op(A[b]) * op(B[b]) + beta * C[b],  b < batch, row-major.
+ *   op(A) is M x K: trans_a == 0 -> A[i*lda + k],  trans_a == 1 -> A[k*lda + i]
+ *   op(B) is K x N: trans_b == 0 -> B[k*ldb + j],  trans_b == 1 -> B[j*ldb + k]
+ * Strides are in elements between consecutive batch items; a stride of 0
+ * broadcasts that operand (the reference's batch_chan_offset flags 0-2,
+ * Engine/kernels.cu:371-385).  beta == 0 assigns (bcmm*, backward == 0),
+ * beta == 1 accumulates (backward == 1, which the reference does with atomicAdd).
+ * If colsum != NULL (batch == 1 only) the kernel also adds column sums of op(B)
+ * over K into colsum[N] -- the Linear bias gradient fused into the dW pass
+ * (BCompress, Engine/kernels.cu:1562-1584).
+ * Replaces bcmm / bcmmABT / bcmmATB / bcmmT (Engine/kernels.cu:387-539). */
+int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+             const float* A, int64_t lda, int64_t stride_a,
+             const float* B, int64_t ldb, int64_t stride_b, float beta,
+             float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum);
+
+/* out[c] (+)= sum_r x[r, c].  BCompress (Engine/kernels.cu:1562-1584); beta 0/1. */
+int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* out, float beta);
+/* out[c] += sum_{b, s} x[b, c, s] for c < nreduce (nreduce <= channels).
+ * Channel_Squeeze1D (Engine/kernels.cu:1734-1761); `nreduce` is the launch's
+ * block count, which the reference sets to `out` in Convolute2D and to the
+ * width in Broadcast_Channel (Engine/engine.cu:1435). */
+int mle_channel_sum(mle_stream stream, const float* x, int batch, int channels, size_t hw, int nreduce, float* out);
+
+/* ------------------------------------------------------------------------- */
+/* Softmax and losses                                                        */
+/* ------------------------------------------------------------------------- */
+
+/* Softmax over [BC, rows, cols].  axis 0 = along each row (type 0), axis 1 =
+ * along each column (type 1).  causal: entries with col > row are 0 and the
+ * max still runs over all entries of the line.  Sums below 1e-45 become 1.
+ * SoftMax / SoftMask (Engine/kernels.cu:2183-2235). */
+int mle_softmax_fwd(mle_stream stream, const float* x, float* y, int bc, int rows, int cols, int axis, int causal);
+/* dx += y * (dy - <dy, y>) along the same axis.  deriv_softmax (Engine/kernels.cu:2149-2181). */
+int mle_softmax_bwd(mle_stream stream, const float* y, const float* dy, float* dx, int bc, int rows, int cols, int axis);
+
+size_t mle_loss_ws_bytes(size_t n);
+/* loss[0] = sum((t - x)^2) / n.  scalar_mse_kernel (Engine/kernels.cu:1808-1816). */
+int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws, size_t ws_bytes);
+/* dx += 2 (x - t) / n * (upstream ? upstream[0] : 1).  deriv_mse_kernel (Engine/kernels.cu:1838-1848). */
+int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n);
+/* probs = row softmax(logits) over [rows, cols]; loss[0] = sum(-t log(p + 1e-27)) / (rows*cols).
+ * SoftMaxCrossEntropy forward (Engine/engine.cu:2088-2100, Engine/kernels.cu:1818-1826). */
+int mle_softmax_xent_fwd(mle_stream stream, const float* logits, const float* target, float* probs,
+                         int rows, int cols, float* loss, void* ws, size_t ws_bytes);
+/* dlogits = (probs - t) * (upstream ? upstream[0] : 1) / batch  (assign).
+ * SoftMaxCrossEntropy backward (Engine/engine.cu:2104-2110). */
+int mle_softmax_xent_bwd(mle_stream stream, const float* probs, const float* target, const float* upstream,
+                         float* dlogits, size_t n, int batch);
+
+/* ------------------------------------------------------------------------- */
+/* Normalisation (gamma = 1, beta = 0, as the reference)                     */
+/* ------------------------------------------------------------------------- */
+
+/* Statistics over each (batch item, group): groups == 1 is LayerNorm over the
+ * whole C*H*W sample (LayerMean/LayerStd/LNorm, Engine/kernels.cu:541-572,
+ * 670-699, 794-804); groups > 1 is GroupNorm (GroupMean/GroupStd/GNorm,
+ * Engine/kernels.cu:607-639, 732-763, 818-834).
+ * stats[2*g] = mean, stats[2*g+1] = sum of squared deviations (the reference's
+ * `std` array).  y = (x - mean) * rsqrt(ssd / N + eps). */
+size_t mle_norm_ws_bytes(int batch, int channels, size_t hw, int groups);
+int mle_norm_fwd(mle_stream stream, const float* x, float* y, float* stats,
+                 int batch, int channels, size_t hw, int groups, float eps, void* ws, size_t ws_bytes);
+/* dx += r * (dy - sum(dy)/N - y * sum(dy*y)/N), r = rsqrt(ssd/N + eps)  (accumulate).
+ * LayerBackward / GroupBackward (Engine/kernels.cu:849-896) after the ggamma
+ * reductions of Engine/engine.cu:3116-3130 / 3262-3276.  With
+ * reference_layout != 0 and groups == 1 only the first batch*hw elements are
+ * written, as LayerBackward's guard does for channels > 1. */
+int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, const float* stats,
+                 int batch, int channels, size_t hw, int groups, float eps, int reference_layout,
+                 void* ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------------- */
+/* Convolution (NCHW input, OIHW weights), implicit GEMM on fp32 MFMA        */
+/* ------------------------------------------------------------------------- */
+
+/* y = conv(x, w) + b (b may be NULL).  CV2D (Engine/kernels.cu:985-1019). */
+int mle_conv2d_fwd(mle_stream stream, const float* x, const float* w, const float* b, float* y,
+                   int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride);
+/* dx += conv_transpose(dy, w).  CV2D_GradInput (Engine/kernels.cu:1053-1089). */
+int mle_conv2d_dgrad(mle_stream stream, const float* dy, const float* w, float* dx,
+                     int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride);
+size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride);
+/* dw = sum_{n,oh,ow} x * dy  (assign).  GV2D (Engine/kernels.cu:1021-1051). */
+int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* dw,
+                     int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride,
+                     void* ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------------- */
+/* Optimizer                                                                 */
+/* ------------------------------------------------------------------------- */
+
+size_t mle_sqnorm_ws_bytes(size_t n);
+/* accum[0] += sum(g^2) in double, deterministic order; nonfinite[0] (if not
+ * NULL) is set to 1 when a NaN/Inf gradient is seen.
+ * SumSquared + atomicAddDouble (Engine/kernels.cu:1486-1506, 51-63). */
+int mle_grad_sqnorm(mle_stream stream, const float* g, size_t n, double* accum, int* nonfinite,
+                    void* ws, size_t ws_bytes);
+/* s = sqrt(s); s = (s > 1) ? s*scale : scale.  Left unchanged when NaN.
+ * Sqrt_Scale type 0 (Engine/kernels.cu:1763-1773). */
+int mle_sqrt_scale(mle_stream stream, double* s, double scale);
+/* One Adam (adamw == 0) or AdamW (adamw != 0) step.  When clip != NULL the
+ * gradient is read as g / (float)clip[0] (clipNorm fused into the update).
+ * AdamUpdate / AdamWUpdate (Engine/kernels.cu:1508-1534), including the double
+ * promotion of (1.0 - b) and powf (Adam) vs pow (AdamW) bias correction. */
+int mle_adam_update(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t,
+                    float lr, float b1, float b2, float eps, float weight_decay, int adamw,
+                    const double* clip);
+size_t mle_adamw_clip_ws_bytes(size_t n);
+/* Fused global-norm clip + Adam(W) over one flat parameter span (p, g, m, v
+ * each contiguous n floats): accumulate -> Sqrt_Scale(scale) -> update with
+ * g / s, in three launches and two passes over g (32 bytes per parameter).
+ * norm_out (nullable, device double) receives s.  The gradient buffer is not
+ * rewritten.  GraphOperations::accumulate + clipNorm + ParameterUpdate
+ * (Engine/engine.cu:3362-3384). */
+int mle_adamw_clip_fused(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t,
+                         float lr, float b1, float b2, float eps, float weight_decay, int adamw,
+                         double clip_scale, double* norm_out, void* ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------------- */
+/* Integer / index paths (bit-exact)                                         */
+/* ------------------------------------------------------------------------- */
+
+/* out[b, s, :] = table[keys[b*max_clen + s], :]; keys < 0 (incl. INT_MIN) give 0.
+ * GatherEmbeddings (Engine/kernels.cu:2279-2296). */
+int mle_embed_gather(mle_stream stream, float* out, const float* table, const int32_t* keys,
+                     int batch, int clen, int max_clen, int dim);
+size_t mle_embed_scatter_ws_bytes(int batch, int clen);
+/* table[keys[b, s], :] += scale * grad[b, s, :] for keys in [0, vocab),
+ * summed per row in token order (deterministic).  With scale = -lr it is
+ * KeyUpdate (Engine/kernels.cu:1536-1549) without the race; with scale = 1 and
+ * `table` a gradient buffer it is the embedding-table gradient. */
+int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, const int32_t* keys,
+                          int batch, int clen, int max_clen, int dim, int vocab, float scale,
+                          void* ws, size_t ws_bytes);
+/* out[(b*clen + s)*vocab + key] = 1 for valid keys (out must be zeroed).
+ * OneHotEmbeddings (Engine/kernels.cu:1551-1560). */
+int mle_onehot(mle_stream stream, float* out, const int32_t* keys, int batch, int clen, int max_clen, int vocab);
+/* out[r] = first index of the maximum of row r (strict >).  ArgMax (Engine/kernels.cu:2353-2366). */
+int mle_argmax(mle_stream stream, const float* x, int rows, int cols, int32_t* out);
+
+/* ------------------------------------------------------------------------- */
+/* Launch probe (measurement)                                                */
+/* ------------------------------------------------------------------------- */
+
+/* Arm the probe for one kernel family ("gemm_nn", "gemm_nt", "gemm_tn",
+ * "gemm_tt", "adamw_update", ...): every later launch of it records a HIP
+ * event pair on its own stream together with its algorithmic flop and byte
+ * counts.  NULL or "" disarms.  Host-side bookkeeping only. */
+int mle_probe_arm(const char* kernel);
+/* Synchronise the recorded events and return totals since arming. */
+int mle_probe_read(int* launches, double* total_ms, double* total_flop, double* total_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MLE_HIP_H */

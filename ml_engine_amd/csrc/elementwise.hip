@@ -1,0 +1,365 @@
+// Elementwise and data-movement kernels: HBM streaming, dwordx4 where the
+// operands are 16-byte aligned, grid-stride loops sized for 256 CUs.
+#include "common.hpp"
+#include <math.h>
+
+using namespace mle;
+
+namespace {
+
+constexpr float kPI = 3.14159265359f;  // Includes/kernels.h:10
+
+__device__ __forceinline__ f32x4 ld4(const float* p, size_t i) { return *reinterpret_cast<const f32x4*>(p + i); }
+__device__ __forceinline__ void st4(float* p, size_t i, f32x4 v) { *reinterpret_cast<f32x4*>(p + i) = v; }
+
+template <class Op>
+__global__ __launch_bounds__(256) void map4_kernel(size_t n4, Op op) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) op.vec(i * 4);
+}
+
+template <class Op>
+__global__ __launch_bounds__(256) void map1_kernel(size_t begin, size_t n, Op op) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t i = begin + (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) op.one(i);
+}
+
+template <class Op>
+int run_map(hipStream_t s, size_t n, bool vec, const Op& op, const char* name) {
+  if (n == 0) return MLE_OK;
+  const size_t n4 = vec ? n / 4 : 0;
+  if (n4) map4_kernel<Op><<<stream_grid(n4, 256, 8192), 256, 0, s>>>(n4, op);
+  const size_t tail = n4 * 4;
+  if (tail < n) map1_kernel<Op><<<stream_grid(n - tail, 256, 8192), 256, 0, s>>>(tail, n, op);
+  return check_launch(name);
+}
+
+// ---- ops ---------------------------------------------------------------
+struct FillOp {
+  float* x;
+  float v;
+  __device__ void one(size_t i) const { x[i] = v; }
+  __device__ void vec(size_t i) const { st4(x, i, f32x4{v, v, v, v}); }
+};
+
+struct ScaleAddOp {  // z = x + scale*y
+  const float* x;
+  const float* y;
+  float* z;
+  float s;
+  __device__ void one(size_t i) const { z[i] = x[i] + s * y[i]; }
+  __device__ void vec(size_t i) const { st4(z, i, ld4(x, i) + s * ld4(y, i)); }
+};
+
+struct AccumOneOp {  // y += x
+  const float* x;
+  float* y;
+  __device__ void one(size_t i) const { y[i] += x[i]; }
+  __device__ void vec(size_t i) const { st4(y, i, ld4(y, i) + ld4(x, i)); }
+};
+
+struct AccumOp {  // y = (float)((double)y + scale*(double)x)
+  const float* x;
+  float* y;
+  double s;
+  __device__ void one(size_t i) const { y[i] = (float)((double)y[i] + s * (double)x[i]); }
+  __device__ void vec(size_t i) const {
+    f32x4 a = ld4(x, i), b = ld4(y, i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = (float)((double)b[j] + s * (double)a[j]);
+    st4(y, i, b);
+  }
+};
+
+struct ScaleWriteOp {
+  const float* x;
+  float* y;
+  float s;
+  __device__ void one(size_t i) const { y[i] = s * x[i]; }
+  __device__ void vec(size_t i) const { st4(y, i, s * ld4(x, i)); }
+};
+
+struct ScaleInplaceOp {
+  float* x;
+  float f;
+  int div;
+  __device__ void one(size_t i) const { x[i] = div ? x[i] / f : x[i] * f; }
+  __device__ void vec(size_t i) const {
+    f32x4 a = ld4(x, i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = div ? a[j] / f : a[j] * f;
+    st4(x, i, a);
+  }
+};
+
+struct ScaleDevOp {
+  float* x;
+  const double* s;
+  int div;
+  __device__ void one(size_t i) const {
+    const float f = (float)s[0];
+    x[i] = div ? x[i] / f : x[i] * f;
+  }
+  __device__ void vec(size_t i) const {
+    const float f = (float)s[0];
+    f32x4 a = ld4(x, i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = div ? a[j] / f : a[j] * f;
+    st4(x, i, a);
+  }
+};
+
+struct BiasRowsOp {  // y[r, c] += b[c]
+  float* y;
+  const float* b;
+  int cols;
+  __device__ void one(size_t i) const { y[i] += b[i % cols]; }
+  __device__ void vec(size_t i) const { st4(y, i, ld4(y, i) + ld4(b, i % cols)); }
+};
+
+struct ChanAddOp {  // y = x + b[(i / hw) % C]
+  const float* x;
+  const float* b;
+  float* y;
+  size_t hw;
+  int C;
+  __device__ void one(size_t i) const { y[i] = x[i] + b[(i / hw) % C]; }
+  __device__ void vec(size_t i) const { st4(y, i, ld4(x, i) + b[(i / hw) % C]); }
+};
+
+// ---- activations ---------------------------------------------------------
+template <int K>
+__device__ __forceinline__ float act_f(float x) {
+  if (K == MLE_RELU) return (x < 0) ? 0.0f : x;
+  if (K == MLE_GELU) {
+    const float val = sqrtf(2.0f / kPI) * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(val));
+  }
+  if (K == MLE_SILU) return x * (1.0f / (1.0f + expf(-x)));
+  if (K == MLE_TANH) return tanhf(x);
+  if (K == MLE_SIGMOID) return 1.0f / (1.0f + expf(-1.0f * x));
+  return (x < 0) ? 0.01f * x : x;  // leaky
+}
+
+template <int K>
+__device__ __forceinline__ float act_df(float x) {
+  if (K == MLE_RELU) return (x > 0.0f) ? 1.0f : 0.0f;
+  if (K == MLE_GELU) {
+    const float root = sqrtf(2.0f / kPI);
+    const float u = root * (x + 0.044715f * x * x * x);
+    const float du = root * (1.0f + 0.134145f * x * x);
+    const float t = tanhf(u);
+    return 0.5f + 0.5f * t + 0.5f * x * (1.0f - t * t) * du;
+  }
+  if (K == MLE_SILU) {
+    const float e = expf(x);
+    const float ne = 1.0f / e;
+    const float sg = 1.0f / (1.0f + ne);
+    return sg + (x / (e + ne + 2.0f));
+  }
+  if (K == MLE_TANH) {
+    const float e2 = expf(2.0f * x);
+    const float ne2 = 1.0f / e2;
+    return 4.0f / (e2 + ne2 + 2.0f);
+  }
+  if (K == MLE_SIGMOID) {
+    const float e = expf(x);
+    const float ne = 1.0f / e;
+    return 1.0f / (e + ne + 2.0f);
+  }
+  return (x < 0.0f) ? 0.01f : 1.0f;
+}
+
+template <int K>
+struct ActFwdOp {
+  const float* x;
+  float* y;
+  __device__ void one(size_t i) const { y[i] = act_f<K>(x[i]); }
+  __device__ void vec(size_t i) const {
+    f32x4 a = ld4(x, i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = act_f<K>(a[j]);
+    st4(y, i, a);
+  }
+};
+
+template <int K>
+struct ActBwdOp {  // dx += dy * f'(x)
+  const float* x;
+  const float* dy;
+  float* dx;
+  __device__ void one(size_t i) const { dx[i] += act_df<K>(x[i]) * dy[i]; }
+  __device__ void vec(size_t i) const {
+    f32x4 a = ld4(x, i), g = ld4(dy, i), d = ld4(dx, i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d[j] += act_df<K>(a[j]) * g[j];
+    st4(dx, i, d);
+  }
+};
+
+// ---- layout / encodings -----------------------------------------------------
+__global__ __launch_bounds__(256) void headify_kernel(const float* __restrict__ in, float* __restrict__ out, int B,
+                                                      int H, int S, int D, int flag) {
+  const size_t total = (size_t)B * H * S * D;
+  const size_t stride = (size_t)gridDim.x * 256;
+  const size_t E = (size_t)H * D;
+  for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += stride) {
+    const size_t d = idx % D;
+    const size_t s = (idx / D) % S;
+    const size_t h = (idx / ((size_t)D * S)) % H;
+    const size_t b = idx / ((size_t)D * S * H);
+    const size_t flat = b * (S * E) + s * E + h * D + d;  // idx is the headified index
+    if (flag == 0) out[idx] = in[flat];
+    else if (flag == 1) out[flat] += in[idx];
+    else if (flag == 2) out[flat] = in[idx];
+    else out[idx] += in[flat];
+  }
+}
+
+__global__ __launch_bounds__(256) void matpe_kernel(const float* __restrict__ x, float* __restrict__ y, size_t total,
+                                                    int rows, int cols, int start) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t g = (size_t)blockIdx.x * 256 + threadIdx.x; g < total; g += stride) {
+    const int pos = (int)((g % ((size_t)rows * cols)) / cols) + start;
+    const int dim = (int)(g % cols);
+    const int i = dim / 2;
+    const double expo = (2.0 * i) / cols;
+    const double freq = 1.0 / pow(10000.0, expo);
+    const double ang = (double)pos * freq;
+    y[g] = x[g] + ((dim % 2 == 0) ? (float)sin(ang) : (float)cos(ang));
+  }
+}
+
+__global__ void tpe_kernel(float* __restrict__ y, int t, int dim) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= dim) return;
+  const int half = dim / 2;
+  const int fi = (g < half) ? g : g - half;
+  const double expo = -(double)fi * log(10000.0) / (half - 1);
+  const double ang = (double)t * exp(expo);
+  y[g] = (g < half) ? (float)cos(ang) : (float)sin(ang);
+}
+
+template <int K>
+int act_fwd_t(hipStream_t s, const float* x, float* y, size_t n) {
+  return run_map(s, n, aligned16(x) && aligned16(y), ActFwdOp<K>{x, y}, "mle_act_fwd");
+}
+template <int K>
+int act_bwd_t(hipStream_t s, const float* x, const float* dy, float* dx, size_t n) {
+  return run_map(s, n, aligned16(x) && aligned16(dy) && aligned16(dx), ActBwdOp<K>{x, dy, dx}, "mle_act_bwd");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mle_fill(mle_stream stream, float* x, float value, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x, "mle_fill: null pointer");
+  return run_map(as_stream(stream), n, aligned16(x), FillOp{x, value}, "mle_fill");
+}
+
+int mle_scale_add(mle_stream stream, const float* x, const float* y, float* z, float scale, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x && y && z, "mle_scale_add: null pointer");
+  return run_map(as_stream(stream), n, aligned16(x) && aligned16(y) && aligned16(z), ScaleAddOp{x, y, z, scale},
+                 "mle_scale_add");
+}
+
+int mle_accumulate(mle_stream stream, const float* x, float* y, double scale, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x && y, "mle_accumulate: null pointer");
+  const bool v = aligned16(x) && aligned16(y);
+  // With scale == 1 the double sum of two floats rounds to the float sum.
+  if (scale == 1.0) return run_map(as_stream(stream), n, v, AccumOneOp{x, y}, "mle_accumulate");
+  return run_map(as_stream(stream), n, v, AccumOp{x, y, scale}, "mle_accumulate");
+}
+
+int mle_scale_write(mle_stream stream, const float* x, float* y, float scale, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x && y, "mle_scale_write: null pointer");
+  return run_map(as_stream(stream), n, aligned16(x) && aligned16(y), ScaleWriteOp{x, y, scale}, "mle_scale_write");
+}
+
+int mle_scale_inplace(mle_stream stream, float* x, float factor, int divide, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x, "mle_scale_inplace: null pointer");
+  return run_map(as_stream(stream), n, aligned16(x), ScaleInplaceOp{x, factor, divide}, "mle_scale_inplace");
+}
+
+int mle_scale_by_device(mle_stream stream, float* x, const double* s, int divide, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x && s, "mle_scale_by_device: null pointer");
+  return run_map(as_stream(stream), n, aligned16(x), ScaleDevOp{x, s, divide}, "mle_scale_by_device");
+}
+
+int mle_bias_add_rows(mle_stream stream, float* y, const float* b, size_t rows, int cols) {
+  MLE_CHECK_ARG(y && b && cols > 0, "mle_bias_add_rows: bad argument");
+  const size_t n = rows * (size_t)cols;
+  return run_map(as_stream(stream), n, aligned16(y) && aligned16(b) && (cols % 4 == 0), BiasRowsOp{y, b, cols},
+                 "mle_bias_add_rows");
+}
+
+int mle_broadcast_channel_add(mle_stream stream, const float* x, const float* b, float* y, int batch, int channels,
+                              size_t hw) {
+  MLE_CHECK_ARG(x && b && y && channels > 0 && hw > 0, "mle_broadcast_channel_add: bad argument");
+  const size_t n = (size_t)batch * channels * hw;
+  return run_map(as_stream(stream), n, aligned16(x) && aligned16(y) && (hw % 4 == 0), ChanAddOp{x, b, y, hw, channels},
+                 "mle_broadcast_channel_add");
+}
+
+int mle_headify(mle_stream stream, const float* in, float* out, int batch, int heads, int seq, int head_dim,
+                int flag) {
+  MLE_CHECK_ARG(in && out && flag >= 0 && flag <= 3, "mle_headify: bad argument");
+  const size_t total = (size_t)batch * heads * seq * head_dim;
+  if (total == 0) return MLE_OK;
+  headify_kernel<<<stream_grid(total, 256, 8192), 256, 0, as_stream(stream)>>>(in, out, batch, heads, seq, head_dim,
+                                                                               flag);
+  return check_launch("mle_headify");
+}
+
+int mle_matpe(mle_stream stream, const float* x, float* y, int batch, int rows, int cols, int start_idx) {
+  MLE_CHECK_ARG(x && y && rows > 0 && cols > 0, "mle_matpe: bad argument");
+  const size_t total = (size_t)batch * rows * cols;
+  if (total == 0) return MLE_OK;
+  matpe_kernel<<<stream_grid(total, 256, 8192), 256, 0, as_stream(stream)>>>(x, y, total, rows, cols, start_idx);
+  return check_launch("mle_matpe");
+}
+
+int mle_timestep_pe(mle_stream stream, float* y, int t, int dim) {
+  MLE_CHECK_ARG(y && dim > 2, "mle_timestep_pe: bad argument");
+  tpe_kernel<<<(dim + 255) / 256, 256, 0, as_stream(stream)>>>(y, t, dim);
+  return check_launch("mle_timestep_pe");
+}
+
+int mle_act_fwd(mle_stream stream, int kind, const float* x, float* y, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x && y, "mle_act_fwd: null pointer");
+  hipStream_t s = as_stream(stream);
+  switch (kind) {
+    case MLE_RELU: return act_fwd_t<MLE_RELU>(s, x, y, n);
+    case MLE_GELU: return act_fwd_t<MLE_GELU>(s, x, y, n);
+    case MLE_SILU: return act_fwd_t<MLE_SILU>(s, x, y, n);
+    case MLE_TANH: return act_fwd_t<MLE_TANH>(s, x, y, n);
+    case MLE_SIGMOID: return act_fwd_t<MLE_SIGMOID>(s, x, y, n);
+    case MLE_LEAKY_RELU: return act_fwd_t<MLE_LEAKY_RELU>(s, x, y, n);
+  }
+  return set_error(MLE_ERR_INVALID, "mle_act_fwd: unknown kind %d", kind);
+}
+
+int mle_act_bwd(mle_stream stream, int kind, const float* x, const float* dy, float* dx, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x && dy && dx, "mle_act_bwd: null pointer");
+  hipStream_t s = as_stream(stream);
+  switch (kind) {
+    case MLE_RELU: return act_bwd_t<MLE_RELU>(s, x, dy, dx, n);
+    case MLE_GELU: return act_bwd_t<MLE_GELU>(s, x, dy, dx, n);
+    case MLE_SILU: return act_bwd_t<MLE_SILU>(s, x, dy, dx, n);
+    case MLE_TANH: return act_bwd_t<MLE_TANH>(s, x, dy, dx, n);
+    case MLE_SIGMOID: return act_bwd_t<MLE_SIGMOID>(s, x, dy, dx, n);
+    case MLE_LEAKY_RELU: return act_bwd_t<MLE_LEAKY_RELU>(s, x, dy, dx, n);
+  }
+  return set_error(MLE_ERR_INVALID, "mle_act_bwd: unknown kind %d", kind);
+}
+
+}  // extern "C"

@@ -1,0 +1,253 @@
+// Integer / index paths: embedding gather, deterministic scatter-add, one-hot,
+// argmax (GatherEmbeddings, KeyUpdate, OneHotEmbeddings, ArgMax:
+// Engine/kernels.cu:2279-2296, 1536-1560, 2353-2366), plus the column and
+// channel reductions used by bias gradients (BCompress, Channel_Squeeze1D:
+// Engine/kernels.cu:1562-1584, 1734-1761).
+#include "common.hpp"
+#include <limits.h>
+
+using namespace mle;
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int SORT_CAP = 16384;  // tokens sorted per chunk in LDS (128 KB of keys)
+constexpr int SORT_NT = 1024;
+
+__global__ __launch_bounds__(NT) void gather_kernel(float* __restrict__ out, const float* __restrict__ table,
+                                                    const int32_t* __restrict__ keys, int clen, int max_clen, int dim,
+                                                    size_t total) {
+  const size_t stride = (size_t)gridDim.x * NT;
+  for (size_t g = (size_t)blockIdx.x * NT + threadIdx.x; g < total; g += stride) {
+    const size_t tok = g / dim;
+    const int d = (int)(g % dim);
+    const size_t b = tok / clen, s = tok % clen;
+    const int key = keys[b * max_clen + s];
+    out[g] = (key == INT_MIN || key < 0) ? 0.0f : table[(size_t)key * dim + d];
+  }
+}
+
+__global__ __launch_bounds__(NT) void gather4_kernel(float* __restrict__ out, const float* __restrict__ table,
+                                                     const int32_t* __restrict__ keys, int clen, int max_clen, int dim,
+                                                     size_t total4) {
+  const size_t stride = (size_t)gridDim.x * NT;
+  const int dim4 = dim / 4;
+  for (size_t g = (size_t)blockIdx.x * NT + threadIdx.x; g < total4; g += stride) {
+    const size_t tok = g / dim4;
+    const int d = (int)(g % dim4) * 4;
+    const size_t b = tok / clen, s = tok % clen;
+    const int key = keys[b * max_clen + s];
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (!(key == INT_MIN || key < 0)) v = *reinterpret_cast<const f32x4*>(table + (size_t)key * dim + d);
+    *reinterpret_cast<f32x4*>(out + tok * dim + d) = v;
+  }
+}
+
+__global__ __launch_bounds__(NT) void onehot_kernel(float* __restrict__ out, const int32_t* __restrict__ keys, int clen,
+                                                    int max_clen, int vocab, size_t total) {
+  const size_t stride = (size_t)gridDim.x * NT;
+  for (size_t g = (size_t)blockIdx.x * NT + threadIdx.x; g < total; g += stride) {
+    const size_t row = g / clen, col = g % clen;
+    const int key = keys[row * max_clen + col];
+    if (key == INT_MIN || key < 0 || key >= vocab) continue;
+    out[g * vocab + key] = 1.0f;
+  }
+}
+
+// One wave per row.  Each lane keeps its first maximum (strict >), then the
+// wave keeps the larger value, ties to the lower index: the first maximum of
+// the row.  A NaN at index 0 makes the row's answer 0, as in the serial scan.
+__global__ __launch_bounds__(64) void argmax_kernel(const float* __restrict__ x, int cols, int32_t* __restrict__ out) {
+  const float* r = x + (size_t)blockIdx.x * cols;
+  const int lane = threadIdx.x;
+  float best = 0.f;
+  int bi = INT_MAX;
+  for (int c = lane; c < cols; c += 64) {
+    const float v = r[c];
+    if (v != v) continue;
+    if (bi == INT_MAX || v > best) {
+      best = v;
+      bi = c;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ob = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (oi != INT_MAX && (bi == INT_MAX || ob > best || (ob == best && oi < bi))) {
+      best = ob;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    const float first = r[0];
+    out[blockIdx.x] = (first != first || bi == INT_MAX) ? 0 : bi;
+  }
+}
+
+// Sort (key, token) pairs of one chunk in LDS: bitonic sort of 64-bit values
+// key << 32 | token.  Invalid keys sort last with key 0x7fffffff.
+__global__ __launch_bounds__(SORT_NT) void sort_chunk_kernel(const int32_t* __restrict__ keys, int clen, int max_clen,
+                                                             int vocab, int tok0, int count,
+                                                             unsigned long long* __restrict__ sorted) {
+  __shared__ unsigned long long s[SORT_CAP];
+  int np = 2;
+  while (np < count) np <<= 1;
+  for (int i = threadIdx.x; i < np; i += SORT_NT) {
+    unsigned long long v = ~0ull;
+    if (i < count) {
+      const int t = tok0 + i;
+      const int key = keys[(size_t)(t / clen) * max_clen + (t % clen)];
+      const unsigned k = (key < 0 || key >= vocab) ? 0x7fffffffu : (unsigned)key;
+      v = ((unsigned long long)k << 32) | (unsigned)t;
+    }
+    s[i] = v;
+  }
+  __syncthreads();
+  for (int k = 2; k <= np; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < np; i += SORT_NT) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const unsigned long long a = s[i], b = s[ixj];
+          const bool up = (i & k) == 0;
+          if ((a > b) == up) {
+            s[i] = b;
+            s[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = threadIdx.x; i < count; i += SORT_NT) sorted[i] = s[i];
+}
+
+// One workgroup per sorted position; the head of each run of equal keys sums
+// the run's gradient rows in token order and adds scale * sum to the table row.
+__global__ __launch_bounds__(NT) void segment_add_kernel(float* __restrict__ table, const float* __restrict__ grad,
+                                                         const unsigned long long* __restrict__ sorted, int count,
+                                                         int dim, float scale) {
+  const int i = blockIdx.x;
+  const unsigned key = (unsigned)(sorted[i] >> 32);
+  if (key == 0x7fffffffu) return;
+  if (i > 0 && (unsigned)(sorted[i - 1] >> 32) == key) return;
+  int end = i + 1;
+  while (end < count && (unsigned)(sorted[end] >> 32) == key) ++end;
+  for (int d = threadIdx.x; d < dim; d += NT) {
+    float acc = 0.f;
+    for (int j = i; j < end; ++j) {
+      const unsigned tok = (unsigned)(sorted[j] & 0xffffffffu);
+      acc += grad[(size_t)tok * dim + d];
+    }
+    table[(size_t)key * dim + d] += scale * acc;
+  }
+}
+
+// out[c] (+)= sum_r x[r, c]: 64 columns per block, 16 row lanes, fixed order.
+__global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ x, size_t rows, int cols,
+                                                      float* __restrict__ out, float beta) {
+  __shared__ float red[16][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + tx;
+  float acc = 0.f;
+  if (c < cols)
+    for (size_t r = ty; r < rows; r += 16) acc += x[r * cols + c];
+  red[ty][tx] = acc;
+  __syncthreads();
+  if (ty == 0 && c < cols) {
+    float t = 0.f;
+    for (int k = 0; k < 16; ++k) t += red[k][tx];
+    out[c] = (beta != 0.f ? beta * out[c] : 0.f) + t;
+  }
+}
+
+// out[c] += sum over (batch, hw) of x[b, c, :]; one block per channel.
+__global__ __launch_bounds__(NT) void channel_sum_kernel(const float* __restrict__ x, int batch, int channels, size_t hw,
+                                                         float* __restrict__ out) {
+  __shared__ float red[NT / 64];
+  const int c = blockIdx.x;
+  float acc = 0.f;
+  for (int b = 0; b < batch; ++b) {
+    const float* p = x + ((size_t)b * channels + c) * hw;
+    for (size_t i = threadIdx.x; i < hw; i += NT) acc += p[i];
+  }
+  acc = block_sum<NT>(acc, red);
+  if (threadIdx.x == 0) out[c] += acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mle_embed_gather(mle_stream stream, float* out, const float* table, const int32_t* keys, int batch, int clen,
+                     int max_clen, int dim) {
+  MLE_CHECK_ARG(out && table && keys && clen > 0 && max_clen >= clen && dim > 0, "mle_embed_gather: bad argument");
+  const size_t total = (size_t)batch * clen * dim;
+  if (total == 0) return MLE_OK;
+  hipStream_t s = as_stream(stream);
+  if (dim % 4 == 0 && aligned16(out) && aligned16(table))
+    gather4_kernel<<<stream_grid(total / 4, NT, 8192), NT, 0, s>>>(out, table, keys, clen, max_clen, dim, total / 4);
+  else
+    gather_kernel<<<stream_grid(total, NT, 8192), NT, 0, s>>>(out, table, keys, clen, max_clen, dim, total);
+  return check_launch("mle_embed_gather");
+}
+
+size_t mle_embed_scatter_ws_bytes(int batch, int clen) {
+  size_t n = (size_t)batch * clen;
+  if (n > (size_t)SORT_CAP) n = SORT_CAP;
+  return (n < 32 ? 32 : n) * sizeof(unsigned long long);
+}
+
+int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, const int32_t* keys, int batch, int clen,
+                          int max_clen, int dim, int vocab, float scale, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(table && grad && keys && ws && clen > 0 && max_clen >= clen && dim > 0 && vocab > 0,
+                "mle_embed_scatter_add: bad argument");
+  const long long ntok = (long long)batch * clen;
+  if (ntok == 0) return MLE_OK;
+  MLE_CHECK_ARG(ntok < 2147483647LL, "mle_embed_scatter_add: too many tokens");
+  if (ws_bytes < mle_embed_scatter_ws_bytes(batch, clen))
+    return set_error(MLE_ERR_WORKSPACE, "mle_embed_scatter_add: workspace too small");
+  hipStream_t s = as_stream(stream);
+  unsigned long long* sorted = static_cast<unsigned long long*>(ws);
+  // Chunks of SORT_CAP tokens are applied in token order, so every table row
+  // receives its updates in a fixed order.
+  for (long long t0 = 0; t0 < ntok; t0 += SORT_CAP) {
+    const int count = (int)((ntok - t0 < SORT_CAP) ? ntok - t0 : SORT_CAP);
+    sort_chunk_kernel<<<1, SORT_NT, 0, s>>>(keys, clen, max_clen, vocab, (int)t0, count, sorted);
+    segment_add_kernel<<<count, NT, 0, s>>>(table, grad, sorted, count, dim, scale);
+    int rc = check_launch("mle_embed_scatter_add");
+    if (rc) return rc;
+  }
+  return MLE_OK;
+}
+
+int mle_onehot(mle_stream stream, float* out, const int32_t* keys, int batch, int clen, int max_clen, int vocab) {
+  MLE_CHECK_ARG(out && keys && clen > 0 && max_clen >= clen && vocab > 0, "mle_onehot: bad argument");
+  const size_t total = (size_t)batch * clen;
+  if (total == 0) return MLE_OK;
+  onehot_kernel<<<stream_grid(total, NT, 8192), NT, 0, as_stream(stream)>>>(out, keys, clen, max_clen, vocab, total);
+  return check_launch("mle_onehot");
+}
+
+int mle_argmax(mle_stream stream, const float* x, int rows, int cols, int32_t* out) {
+  MLE_CHECK_ARG(x && out && rows >= 0 && cols > 0, "mle_argmax: bad argument");
+  if (rows == 0) return MLE_OK;
+  argmax_kernel<<<rows, 64, 0, as_stream(stream)>>>(x, cols, out);
+  return check_launch("mle_argmax");
+}
+
+int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* out, float beta) {
+  MLE_CHECK_ARG(x && out && cols > 0, "mle_colsum: bad argument");
+  colsum_kernel<<<(cols + 63) / 64, 1024, 0, as_stream(stream)>>>(x, rows, cols, out, beta);
+  return check_launch("mle_colsum");
+}
+
+int mle_channel_sum(mle_stream stream, const float* x, int batch, int channels, size_t hw, int nreduce, float* out) {
+  MLE_CHECK_ARG(x && out && channels > 0 && nreduce >= 0, "mle_channel_sum: bad argument");
+  if (nreduce > channels) nreduce = channels;  // the reference would read and write out of bounds here
+  if (nreduce == 0) return MLE_OK;
+  channel_sum_kernel<<<nreduce, NT, 0, as_stream(stream)>>>(x, batch, channels, hw, out);
+  return check_launch("mle_channel_sum");
+}
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// fp32 MFMA tile machinery for gfx950 (v_mfma_f32_16x16x4_f32, wave64).
+//
+// Workgroup tile BM x BN = 128 x 128, K staged through LDS BK = 32 at a time,
+// double-buffered.  Four waves in a 2 x 2 arrangement each own a 64 x 64 block
+// of C held as 4 x 4 MFMA tiles of 16 x 16 (64 accumulator VGPRs per lane).
+//
+// MFMA 16x16x4 operand layout (one block): lane l supplies A[l % 16][l / 16]
+// and B[l / 16][l % 16]; the result lane l holds D[4 * (l / 16) + r][l % 16],
+// r = 0..3.  Within a 16-wide K slice, lane group q = l / 16 feeds k = 4q + j
+// to MFMA step j (j = 0..3), so a k-contiguous LDS row is read with one
+// ds_read_b128 per 16 x 16 sub-tile and four MFMA steps.  A and B use the same
+// k permutation, so the contraction is unchanged.
+//
+// LDS layouts (row strides padded by 4 floats so the 16-lane groups of a wave
+// hit disjoint banks):
+//   A "k-contiguous"  [BM][BK+4]  (A stored M x K)      -> ds_read_b128
+//   A "m-contiguous"  [BK][BM+4]  (A stored K x M)      -> 4 x ds_read_b32
+//   B "k-contiguous"  [BN][BK+4]  (B stored N x K)      -> ds_read_b128
+//   B "n-contiguous"  [BK][BN+4]  (B stored K x N)      -> 4 x ds_read_b32
+#pragma once
+#include "common.hpp"
+
+namespace gemm {
+
+constexpr int BM = 128, BN = 128, BK = 32, NT = 256, PAD = 4;
+constexpr int LDK = BK + PAD;   // row stride of k-contiguous tiles
+constexpr int LDMN = BM + PAD;  // row stride of m/n-contiguous tiles (BM == BN)
+
+// A_MC: A tile is m-contiguous; B_KC: B tile is k-contiguous.
+template <bool A_MC>
+constexpr int a_tile_floats() {
+  return A_MC ? BK * LDMN : BM * LDK;
+}
+template <bool B_KC>
+constexpr int b_tile_floats() {
+  return B_KC ? BN * LDK : BK * LDMN;
+}
+
+// One BK-deep slice of MFMAs for this wave's 64 x 64 block.
+template <bool A_MC, bool B_KC>
+__device__ __forceinline__ void mma_stage(const float* __restrict__ As, const float* __restrict__ Bs,
+                                          f32x4 (&acc)[4][4], int wm, int wn, int lr, int q) {
+#pragma unroll
+  for (int kb = 0; kb < BK / 16; ++kb) {
+    f32x4 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = wm * 64 + i * 16 + lr;
+      if (!A_MC) {
+        a[i] = *reinterpret_cast<const f32x4*>(As + row * LDK + kb * 16 + 4 * q);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[i][j] = As[(kb * 16 + 4 * q + j) * LDMN + row];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = wn * 64 + i * 16 + lr;
+      if (B_KC) {
+        b[i] = *reinterpret_cast<const f32x4*>(Bs + col * LDK + kb * 16 + 4 * q);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[i][j] = Bs[(kb * 16 + 4 * q + j) * LDMN + col];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][j], b[n][j], acc[i][n], 0, 0, 0);
+  }
+}
+
+// Row/column of accumulator element (i, n, r) of this lane inside the tile.
+__device__ __forceinline__ int acc_row(int wm, int i, int q, int r) { return wm * 64 + i * 16 + 4 * q + r; }
+__device__ __forceinline__ int acc_col(int wn, int n, int lr) { return wn * 64 + n * 16 + lr; }
+
+}  // namespace gemm

@@ -1,0 +1,258 @@
+// Optimizer: global gradient norm (SumSquared + Sqrt_Scale), clip, and the
+// Adam / AdamW update, optionally fused into one bandwidth-bound pass that reads
+// g / s on the fly (Engine/kernels.cu:1486-1534, 1763-1773; Includes/kernels.h:293-300).
+//
+// The reference sums squares with thread 0 of every 512-thread block looping
+// serially and then a CAS loop on one double (SumSquared / atomicAddDouble).
+// Here every lane accumulates float4 loads in double, waves reduce with
+// shuffles, and one block adds the per-block partials in a fixed order, so the
+// norm is bit-reproducible.
+#include "common.hpp"
+#include <math.h>
+
+using namespace mle;
+
+namespace {
+
+constexpr int NT = 256;
+constexpr unsigned kPartCap = 2048;
+
+__device__ __forceinline__ f32x4 ld4(const float* p, size_t i) { return *reinterpret_cast<const f32x4*>(p + i); }
+__device__ __forceinline__ void st4(float* p, size_t i, f32x4 v) { *reinterpret_cast<f32x4*>(p + i) = v; }
+
+template <bool VEC>
+__global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g, size_t n, double* __restrict__ part,
+                                                     int* __restrict__ nonfinite) {
+  __shared__ double red[NT / 64];
+  double acc = 0.0;
+  bool bad = false;
+  const size_t stride = (size_t)gridDim.x * NT;
+  if (VEC) {
+    const size_t n4 = n / 4;
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n4; i += stride) {
+      const f32x4 v = ld4(g, i * 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const double d = (double)v[j];
+        acc += d * d;
+        bad |= !isfinite(v[j]);
+      }
+    }
+    for (size_t i = n4 * 4 + (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
+      const double d = (double)g[i];
+      acc += d * d;
+      bad |= !isfinite(g[i]);
+    }
+  } else {
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
+      const double d = (double)g[i];
+      acc += d * d;
+      bad |= !isfinite(g[i]);
+    }
+  }
+  acc = block_sum<NT>(acc, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = acc;
+  if (bad && nonfinite) nonfinite[0] = 1;
+}
+
+// accum[0] (+)= sum(part).  With do_scale, then s = sqrt(accum);
+// s = s > 1 ? s*scale : scale (Sqrt_Scale type 0), skipped when accum is NaN.
+__global__ __launch_bounds__(NT) void sqnorm_finish(const double* __restrict__ part, unsigned nparts,
+                                                    double* __restrict__ accum, int add_existing, int do_scale,
+                                                    double scale, double* __restrict__ copy_out) {
+  __shared__ double red[NT / 64];
+  double acc = 0.0;
+  for (unsigned i = threadIdx.x; i < nparts; i += NT) acc += part[i];
+  acc = block_sum<NT>(acc, red);
+  if (threadIdx.x == 0) {
+    double v = add_existing ? accum[0] + acc : acc;
+    if (do_scale && v == v) {
+      const double cur = sqrt(v);
+      v = (cur > 1.0) ? cur * scale : scale;
+    }
+    accum[0] = v;
+    if (copy_out) copy_out[0] = v;
+  }
+}
+
+__global__ void sqrt_scale_kernel(double* s, double scale) {
+  const double x = s[0];
+  if (x == x) {
+    const double cur = sqrt(x);
+    s[0] = (cur > 1.0) ? cur * scale : scale;
+  }
+}
+
+struct AdamArgs {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  size_t n;
+  float lr, b1, b2, eps, wd;
+  double omb1, omb2;  // 1.0 - b (double, as the reference's (1.0 - b1) literal)
+  double c1, c2;      // 1 - b^t bias corrections
+  const double* clip; // g is read as g / (float)clip[0] when set
+};
+
+// One element of AdamUpdate / AdamWUpdate (Engine/kernels.cu:1508-1534).
+template <bool ADAMW>
+__device__ __forceinline__ void adam_elem(const AdamArgs& a, float& p, float g, float& m, float& v, float sf,
+                                          bool clip) {
+  if (clip) g = g / sf;
+  m = (float)((double)(a.b1 * m) + a.omb1 * (double)g);
+  v = (float)((double)(a.b2 * v) + (a.omb2 * (double)g) * (double)g);
+  const float m_hat = (float)((double)m / a.c1);
+  const float v_hat = (float)((double)v / a.c2);
+  const float vs = sqrtf(v_hat);
+  if (ADAMW) p -= a.lr * ((m_hat / (vs + a.eps)) + a.wd * p);
+  else p -= a.lr * m_hat / (vs + a.eps);
+}
+
+template <bool ADAMW, bool CLIP, bool VEC>
+__global__ __launch_bounds__(NT) void adam_kernel(AdamArgs a) {
+  const float sf = CLIP ? (float)a.clip[0] : 1.0f;
+  const size_t stride = (size_t)gridDim.x * NT;
+  size_t start = 0;
+  if (VEC) {
+    const size_t n4 = a.n / 4;
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n4; i += stride) {
+      const size_t e = i * 4;
+      f32x4 p = ld4(a.p, e), g = ld4(a.g, e), m = ld4(a.m, e), v = ld4(a.v, e);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float pj = p[j], mj = m[j], vj = v[j];
+        adam_elem<ADAMW>(a, pj, g[j], mj, vj, sf, CLIP);
+        p[j] = pj;
+        m[j] = mj;
+        v[j] = vj;
+      }
+      st4(a.p, e, p);
+      st4(a.m, e, m);
+      st4(a.v, e, v);
+    }
+    start = n4 * 4;
+  }
+  for (size_t e = start + (size_t)blockIdx.x * NT + threadIdx.x; e < a.n; e += stride) {
+    float pj = a.p[e], mj = a.m[e], vj = a.v[e];
+    adam_elem<ADAMW>(a, pj, a.g[e], mj, vj, sf, CLIP);
+    a.p[e] = pj;
+    a.m[e] = mj;
+    a.v[e] = vj;
+  }
+}
+
+template <bool ADAMW, bool CLIP>
+void launch_adam(hipStream_t s, const AdamArgs& a, bool vec) {
+  const unsigned grid = stream_grid(vec ? (a.n + 3) / 4 : a.n, NT, 8192);
+  if (vec) adam_kernel<ADAMW, CLIP, true><<<grid, NT, 0, s>>>(a);
+  else adam_kernel<ADAMW, CLIP, false><<<grid, NT, 0, s>>>(a);
+}
+
+int launch_update(hipStream_t s, float* p, const float* g, float* m, float* v, size_t n, int t, float lr, float b1,
+                  float b2, float eps, float wd, int adamw, const double* clip) {
+  AdamArgs a;
+  a.p = p;
+  a.g = g;
+  a.m = m;
+  a.v = v;
+  a.n = n;
+  a.lr = lr;
+  a.b1 = b1;
+  a.b2 = b2;
+  a.eps = eps;
+  a.wd = wd;
+  a.omb1 = 1.0 - (double)b1;
+  a.omb2 = 1.0 - (double)b2;
+  if (adamw) {  // pow in double (AdamWUpdate)
+    a.c1 = 1.0 - pow((double)b1, (double)t);
+    a.c2 = 1.0 - pow((double)b2, (double)t);
+  } else {  // powf (AdamUpdate)
+    a.c1 = 1.0 - (double)powf(b1, (float)t);
+    a.c2 = 1.0 - (double)powf(b2, (float)t);
+  }
+  a.clip = clip;
+  const bool vec = aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v);
+  const double bytes = 28.0 * (double)n;
+  ProbeScope probe("adam_update", s, 0.0, bytes);
+  if (adamw) {
+    if (clip) launch_adam<true, true>(s, a, vec);
+    else launch_adam<true, false>(s, a, vec);
+  } else {
+    if (clip) launch_adam<false, true>(s, a, vec);
+    else launch_adam<false, false>(s, a, vec);
+  }
+  return check_launch("mle_adam_update");
+}
+
+unsigned sqnorm_grid(size_t n) { return stream_grid((n + 3) / 4, NT, kPartCap); }
+
+}  // namespace
+
+extern "C" {
+
+size_t mle_sqnorm_ws_bytes(size_t n) { return (size_t)sqnorm_grid(n) * sizeof(double); }
+
+int mle_grad_sqnorm(mle_stream stream, const float* g, size_t n, double* accum, int* nonfinite, void* ws,
+                    size_t ws_bytes) {
+  MLE_CHECK_ARG(g && accum && ws, "mle_grad_sqnorm: null pointer");
+  if (n == 0) return MLE_OK;
+  const unsigned grid = sqnorm_grid(n);
+  if (ws_bytes < grid * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "mle_grad_sqnorm: workspace too small");
+  hipStream_t s = as_stream(stream);
+  double* part = static_cast<double*>(ws);
+  {
+    ProbeScope probe("sqnorm", s, 0.0, 4.0 * (double)n);
+    if (aligned16(g)) sqnorm_partial<true><<<grid, NT, 0, s>>>(g, n, part, nonfinite);
+    else sqnorm_partial<false><<<grid, NT, 0, s>>>(g, n, part, nonfinite);
+  }
+  sqnorm_finish<<<1, NT, 0, s>>>(part, grid, accum, 1, 0, 1.0, nullptr);
+  return check_launch("mle_grad_sqnorm");
+}
+
+int mle_sqrt_scale(mle_stream stream, double* s, double scale) {
+  MLE_CHECK_ARG(s, "mle_sqrt_scale: null pointer");
+  sqrt_scale_kernel<<<1, 1, 0, as_stream(stream)>>>(s, scale);
+  return check_launch("mle_sqrt_scale");
+}
+
+int mle_adam_update(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t, float lr,
+                    float b1, float b2, float eps, float weight_decay, int adamw, const double* clip) {
+  MLE_CHECK_ARG(p && g && m && v, "mle_adam_update: null pointer");
+  MLE_CHECK_ARG(t >= 1, "mle_adam_update: step t = %d must be >= 1", t);
+  if (n == 0) return MLE_OK;
+  return launch_update(as_stream(stream), p, g, m, v, n, t, lr, b1, b2, eps, weight_decay, adamw, clip);
+}
+
+size_t mle_adamw_clip_ws_bytes(size_t n) { return 256 + mle_sqnorm_ws_bytes(n); }
+
+int mle_adamw_clip_fused(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t, float lr,
+                         float b1, float b2, float eps, float weight_decay, int adamw, double clip_scale,
+                         double* norm_out, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(p && g && m && v && ws, "mle_adamw_clip_fused: null pointer");
+  MLE_CHECK_ARG(t >= 1, "mle_adamw_clip_fused: step t = %d must be >= 1", t);
+  if (n == 0) return MLE_OK;
+  if (ws_bytes < mle_adamw_clip_ws_bytes(n)) return set_error(MLE_ERR_WORKSPACE, "mle_adamw_clip_fused: workspace too small");
+  hipStream_t s = as_stream(stream);
+  const double* clip = nullptr;
+  if (clip_scale > 0.0) {
+    double* sdev = static_cast<double*>(ws);  // first 256 bytes hold the scale s
+    double* part = reinterpret_cast<double*>(static_cast<char*>(ws) + 256);
+    const unsigned grid = sqnorm_grid(n);
+    {
+      ProbeScope probe("sqnorm", s, 0.0, 4.0 * (double)n);
+      if (aligned16(g)) sqnorm_partial<true><<<grid, NT, 0, s>>>(g, n, part, nullptr);
+      else sqnorm_partial<false><<<grid, NT, 0, s>>>(g, n, part, nullptr);
+    }
+    // s = Sqrt_Scale(sum g^2) computed from zero, so nothing is cleared beforehand.
+    sqnorm_finish<<<1, NT, 0, s>>>(part, grid, sdev, 0, 1, clip_scale, norm_out);
+    int rc = check_launch("mle_adamw_clip_fused");
+    if (rc) return rc;
+    clip = sdev;
+  }
+  int rc = launch_update(s, p, g, m, v, n, t, lr, b1, b2, eps, weight_decay, adamw, clip);
+  if (rc) return rc;
+  return check_launch("mle_adamw_clip_fused");
+}
+
+}  // extern "C"

@@ -1,0 +1,240 @@
+// Runtime part of the C ABI: errors, device memory, streams, arena, probe, fill.
+#include "common.hpp"
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace mle {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_error(hipError_t e, const char* where) {
+  if (e == hipErrorOutOfMemory) {
+    size_t fr = 0, tot = 0;
+    (void)hipGetLastError();
+    (void)hipMemGetInfo(&fr, &tot);
+    return set_error(MLE_ERR_OOM, "%s: %s (device free %zu MB of %zu MB)", where, hipGetErrorString(e), fr >> 20,
+                     tot >> 20);
+  }
+  return set_error(MLE_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+int check_launch(const char* kernel) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_error(e, kernel);
+  return MLE_OK;
+}
+
+// ---- probe ---------------------------------------------------------------
+struct ProbeRec {
+  hipEvent_t a, b;
+  double flop, bytes;
+};
+static std::mutex g_probe_mu;
+static std::string g_probe_kernel;
+static std::vector<ProbeRec> g_probe_recs;
+static std::vector<hipEvent_t> g_event_pool;
+static hipEvent_t g_pending_begin = nullptr;
+
+static hipEvent_t take_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+bool probe_armed(const char* kernel) {
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  return !g_probe_kernel.empty() && g_probe_kernel == kernel;
+}
+
+void probe_begin(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  g_pending_begin = take_event();
+  if (g_pending_begin) (void)hipEventRecord(g_pending_begin, s);
+}
+
+void probe_end(hipStream_t s, double flop, double bytes) {
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  if (!g_pending_begin) return;
+  hipEvent_t e = take_event();
+  if (!e) return;
+  (void)hipEventRecord(e, s);
+  g_probe_recs.push_back({g_pending_begin, e, flop, bytes});
+  g_pending_begin = nullptr;
+}
+
+}  // namespace mle
+
+using namespace mle;
+
+// ---- arena -----------------------------------------------------------------
+struct mle_arena_s {
+  char* base;
+  size_t cap;
+  size_t used;
+};
+
+extern "C" {
+
+const char* mle_last_error(void) { return g_last_error.c_str(); }
+
+const char* mle_version(void) { return "mle_hip 0.1 gfx950"; }
+
+int mle_init(int device) {
+  int n = 0;
+  MLE_HIP(hipGetDeviceCount(&n));
+  MLE_CHECK_ARG(device >= 0 && device < n, "mle_init: device %d out of range (%d devices)", device, n);
+  MLE_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  MLE_HIP(hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return set_error(MLE_ERR_UNSUPPORTED, "mle_init: device %d is %s; this library is built for gfx950", device,
+                     prop.gcnArchName);
+  return MLE_OK;
+}
+
+int mle_device_alloc(void** ptr, size_t bytes) {
+  MLE_CHECK_ARG(ptr != nullptr, "mle_device_alloc: null out pointer");
+  *ptr = nullptr;
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(ptr, bytes);
+  if (e != hipSuccess) {
+    *ptr = nullptr;
+    return hip_error(e, "mle_device_alloc");
+  }
+  return MLE_OK;
+}
+
+int mle_device_free(void* ptr) {
+  if (ptr) MLE_HIP(hipFree(ptr));
+  return MLE_OK;
+}
+
+int mle_memcpy_h2d(void* dst, const void* src, size_t bytes, mle_stream stream) {
+  if (bytes == 0) return MLE_OK;
+  MLE_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)));
+  MLE_HIP(hipStreamSynchronize(as_stream(stream)));
+  return MLE_OK;
+}
+
+int mle_memcpy_d2h(void* dst, const void* src, size_t bytes, mle_stream stream) {
+  if (bytes == 0) return MLE_OK;
+  MLE_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
+  MLE_HIP(hipStreamSynchronize(as_stream(stream)));
+  return MLE_OK;
+}
+
+int mle_memcpy_d2d(void* dst, const void* src, size_t bytes, mle_stream stream) {
+  if (bytes == 0) return MLE_OK;
+  MLE_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+  return MLE_OK;
+}
+
+int mle_stream_create(mle_stream* stream) {
+  MLE_CHECK_ARG(stream != nullptr, "mle_stream_create: null out pointer");
+  hipStream_t s = nullptr;
+  MLE_HIP(hipStreamCreate(&s));  // default priority, as required on this hardware pool
+  *stream = reinterpret_cast<mle_stream>(s);
+  return MLE_OK;
+}
+
+int mle_stream_destroy(mle_stream stream) {
+  if (stream) MLE_HIP(hipStreamDestroy(as_stream(stream)));
+  return MLE_OK;
+}
+
+int mle_stream_sync(mle_stream stream) {
+  MLE_HIP(hipStreamSynchronize(as_stream(stream)));
+  MLE_HIP(hipGetLastError());
+  return MLE_OK;
+}
+
+int mle_arena_create(size_t bytes, mle_arena* arena) {
+  MLE_CHECK_ARG(arena != nullptr, "mle_arena_create: null out pointer");
+  *arena = nullptr;
+  bytes = (bytes + 255) & ~size_t(255);
+  if (bytes == 0) bytes = 256;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return hip_error(e, "mle_arena_create");
+  *arena = new mle_arena_s{static_cast<char*>(p), bytes, 0};
+  return MLE_OK;
+}
+
+int mle_arena_alloc(mle_arena arena, size_t bytes, void** ptr) {
+  MLE_CHECK_ARG(arena && ptr, "mle_arena_alloc: null argument");
+  size_t need = (bytes + 255) & ~size_t(255);
+  if (need == 0) need = 256;
+  if (arena->used + need > arena->cap)
+    return set_error(MLE_ERR_OOM, "mle_arena_alloc: %zu bytes requested, %zu of %zu used", bytes, arena->used,
+                     arena->cap);
+  *ptr = arena->base + arena->used;
+  arena->used += need;
+  return MLE_OK;
+}
+
+int mle_arena_reset(mle_arena arena) {
+  MLE_CHECK_ARG(arena, "mle_arena_reset: null arena");
+  arena->used = 0;
+  return MLE_OK;
+}
+
+int mle_arena_destroy(mle_arena arena) {
+  if (!arena) return MLE_OK;
+  hipError_t e = hipFree(arena->base);
+  delete arena;
+  if (e != hipSuccess) return hip_error(e, "mle_arena_destroy");
+  return MLE_OK;
+}
+
+size_t mle_arena_used(mle_arena arena) { return arena ? arena->used : 0; }
+size_t mle_arena_capacity(mle_arena arena) { return arena ? arena->cap : 0; }
+
+int mle_probe_arm(const char* kernel) {
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  for (auto& r : g_probe_recs) {
+    g_event_pool.push_back(r.a);
+    g_event_pool.push_back(r.b);
+  }
+  g_probe_recs.clear();
+  g_probe_kernel = kernel ? kernel : "";
+  return MLE_OK;
+}
+
+int mle_probe_read(int* launches, double* total_ms, double* total_flop, double* total_bytes) {
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  double ms = 0, fl = 0, by = 0;
+  for (auto& r : g_probe_recs) {
+    MLE_HIP(hipEventSynchronize(r.b));
+    float t = 0;
+    MLE_HIP(hipEventElapsedTime(&t, r.a, r.b));
+    ms += t;
+    fl += r.flop;
+    by += r.bytes;
+  }
+  if (launches) *launches = (int)g_probe_recs.size();
+  if (total_ms) *total_ms = ms;
+  if (total_flop) *total_flop = fl;
+  if (total_bytes) *total_bytes = by;
+  return MLE_OK;
+}
+
+}  // extern "C"

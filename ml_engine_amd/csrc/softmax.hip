@@ -1,0 +1,363 @@
+// Softmax (row / column, optional causal mask), its backward, and the
+// softmax-cross-entropy and MSE losses.  One pass over HBM per direction: a
+// line (row or column) is held in registers while its max and sum are reduced
+// with wave64 shuffles, instead of the reference's 4 launches with one thread
+// per line (SoftMax/SoftMask/deriv_softmax, Engine/kernels.cu:2003-2244).
+#include "common.hpp"
+#include <float.h>
+
+using namespace mle;
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int ROW_CPT = 32;  // row kernels cache up to NT*ROW_CPT = 8192 columns
+constexpr int COL_W = 64;    // column kernels: 64 columns per workgroup
+constexpr int COL_RL = 4;    // ... and 4 row lanes
+constexpr int COL_RPT = 64;  // ... caching up to COL_RL*COL_RPT = 256 rows
+
+// ---------------------------------------------------------------------------
+// Row softmax (type 0).  One workgroup per line of `cols` elements.  With
+// `target` set, also writes this row's -sum(t log(p + 1e-27)) (double) to
+// loss_part[row] (scalar_ce_kernel, Engine/kernels.cu:1818-1826).
+template <bool CACHED>
+__global__ __launch_bounds__(NT) void softmax_row_kernel(const float* __restrict__ x, float* __restrict__ y, int rows,
+                                                         int cols, int causal, const float* __restrict__ target,
+                                                         double* __restrict__ loss_part) {
+  __shared__ float redf[NT / 64];
+  __shared__ double redd[NT / 64];
+  const size_t line = blockIdx.x;
+  const int r_in = (int)(line % rows);
+  const float* xr = x + line * cols;
+  float* yr = y + line * cols;
+  const int lim = causal ? min(cols, r_in + 1) : cols;  // entries c > r are masked
+  float v[CACHED ? ROW_CPT : 1];
+  float mx = -FLT_MAX;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < ROW_CPT; ++i) {
+      const int c = threadIdx.x + i * NT;
+      v[i] = (c < cols) ? xr[c] : -FLT_MAX;
+      mx = fmaxf(mx, v[i]);
+    }
+  } else {
+    for (int c = threadIdx.x; c < cols; c += NT) mx = fmaxf(mx, xr[c]);
+  }
+  mx = block_max<NT>(mx, redf);
+  float sum = 0.f;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < ROW_CPT; ++i) {
+      const int c = threadIdx.x + i * NT;
+      v[i] = (c < lim) ? expf(v[i] - mx) : 0.f;
+      sum += v[i];
+    }
+  } else {
+    for (int c = threadIdx.x; c < lim; c += NT) sum += expf(xr[c] - mx);
+  }
+  sum = block_sum<NT>(sum, redf);
+  if (sum < 1e-45f) sum = 1.0f;
+  double lp = 0.0;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < ROW_CPT; ++i) {
+      const int c = threadIdx.x + i * NT;
+      if (c < cols) {
+        const float p = v[i] / sum;
+        yr[c] = p;
+        if (target) lp += -(double)target[line * cols + c] * log((double)p + 1e-27);
+      }
+    }
+  } else {
+    for (int c = threadIdx.x; c < cols; c += NT) {
+      const float p = (c < lim) ? expf(xr[c] - mx) / sum : 0.f;
+      yr[c] = p;
+      if (target) lp += -(double)target[line * cols + c] * log((double)p + 1e-27);
+    }
+  }
+  if (target) {
+    lp = block_sum<NT>(lp, redd);
+    if (threadIdx.x == 0) loss_part[line] = lp;
+  }
+}
+
+// Row softmax backward: dx += y (dy - <dy, y>).
+template <bool CACHED>
+__global__ __launch_bounds__(NT) void softmax_row_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dy,
+                                                             float* __restrict__ dx, int cols) {
+  __shared__ float redf[NT / 64];
+  const size_t line = blockIdx.x;
+  const float* yr = y + line * cols;
+  const float* gr = dy + line * cols;
+  float* dr = dx + line * cols;
+  float yv[CACHED ? ROW_CPT : 1], gv[CACHED ? ROW_CPT : 1];
+  float dot = 0.f;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < ROW_CPT; ++i) {
+      const int c = threadIdx.x + i * NT;
+      yv[i] = (c < cols) ? yr[c] : 0.f;
+      gv[i] = (c < cols) ? gr[c] : 0.f;
+      dot += gv[i] * yv[i];
+    }
+  } else {
+    for (int c = threadIdx.x; c < cols; c += NT) dot += gr[c] * yr[c];
+  }
+  dot = block_sum<NT>(dot, redf);
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < ROW_CPT; ++i) {
+      const int c = threadIdx.x + i * NT;
+      if (c < cols) dr[c] += yv[i] * (gv[i] - dot);
+    }
+  } else {
+    for (int c = threadIdx.x; c < cols; c += NT) dr[c] += yr[c] * (gr[c] - dot);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Column softmax (type 1): for each column, max / exp / sum over the rows.  A
+// workgroup owns COL_W consecutive columns of one matrix; a wave reads one
+// row's COL_W columns (256 contiguous bytes) per step.
+template <bool CACHED>
+__global__ __launch_bounds__(NT) void softmax_col_kernel(const float* __restrict__ x, float* __restrict__ y, int rows,
+                                                         int cols, int causal) {
+  __shared__ float red[COL_RL][COL_W];
+  const int tx = threadIdx.x % COL_W, ty = threadIdx.x / COL_W;
+  const int c = blockIdx.x * COL_W + tx;
+  const size_t base = (size_t)blockIdx.y * rows * cols;
+  const bool cv = c < cols;
+  float v[CACHED ? COL_RPT : 1];
+  float mx = -FLT_MAX;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < COL_RPT; ++i) {
+      const int r = ty + i * COL_RL;
+      v[i] = (cv && r < rows) ? x[base + (size_t)r * cols + c] : -FLT_MAX;
+      mx = fmaxf(mx, v[i]);
+    }
+  } else if (cv) {
+    for (int r = ty; r < rows; r += COL_RL) mx = fmaxf(mx, x[base + (size_t)r * cols + c]);
+  }
+  red[ty][tx] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0][tx], red[1][tx]), fmaxf(red[2][tx], red[3][tx]));
+  __syncthreads();
+  float sum = 0.f;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < COL_RPT; ++i) {
+      const int r = ty + i * COL_RL;
+      const bool keep = cv && r < rows && !(causal && c > r);
+      v[i] = keep ? expf(v[i] - mx) : 0.f;
+      sum += v[i];
+    }
+  } else if (cv) {
+    for (int r = ty; r < rows; r += COL_RL)
+      if (!(causal && c > r)) sum += expf(x[base + (size_t)r * cols + c] - mx);
+  }
+  red[ty][tx] = sum;
+  __syncthreads();
+  sum = (red[0][tx] + red[1][tx]) + (red[2][tx] + red[3][tx]);
+  if (sum < 1e-45f) sum = 1.0f;
+  if (!cv) return;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < COL_RPT; ++i) {
+      const int r = ty + i * COL_RL;
+      if (r < rows) y[base + (size_t)r * cols + c] = v[i] / sum;
+    }
+  } else {
+    for (int r = ty; r < rows; r += COL_RL) {
+      const size_t o = base + (size_t)r * cols + c;
+      y[o] = (causal && c > r) ? 0.f : expf(x[o] - mx) / sum;
+    }
+  }
+}
+
+template <bool CACHED>
+__global__ __launch_bounds__(NT) void softmax_col_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dy,
+                                                             float* __restrict__ dx, int rows, int cols) {
+  __shared__ float red[COL_RL][COL_W];
+  const int tx = threadIdx.x % COL_W, ty = threadIdx.x / COL_W;
+  const int c = blockIdx.x * COL_W + tx;
+  const size_t base = (size_t)blockIdx.y * rows * cols;
+  const bool cv = c < cols;
+  float yv[CACHED ? COL_RPT : 1], gv[CACHED ? COL_RPT : 1];
+  float dot = 0.f;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < COL_RPT; ++i) {
+      const int r = ty + i * COL_RL;
+      const bool ok = cv && r < rows;
+      yv[i] = ok ? y[base + (size_t)r * cols + c] : 0.f;
+      gv[i] = ok ? dy[base + (size_t)r * cols + c] : 0.f;
+      dot += gv[i] * yv[i];
+    }
+  } else if (cv) {
+    for (int r = ty; r < rows; r += COL_RL) {
+      const size_t o = base + (size_t)r * cols + c;
+      dot += dy[o] * y[o];
+    }
+  }
+  red[ty][tx] = dot;
+  __syncthreads();
+  dot = (red[0][tx] + red[1][tx]) + (red[2][tx] + red[3][tx]);
+  if (!cv) return;
+  if (CACHED) {
+#pragma unroll
+    for (int i = 0; i < COL_RPT; ++i) {
+      const int r = ty + i * COL_RL;
+      if (r < rows) dx[base + (size_t)r * cols + c] += yv[i] * (gv[i] - dot);
+    }
+  } else {
+    for (int r = ty; r < rows; r += COL_RL) {
+      const size_t o = base + (size_t)r * cols + c;
+      dx[o] += y[o] * (dy[o] - dot);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic sums into a scalar: per-block double partials, then one block
+// adds them in a fixed order.
+__global__ __launch_bounds__(NT) void mse_partial_kernel(const float* __restrict__ x, const float* __restrict__ t,
+                                                         size_t n, double* __restrict__ part) {
+  __shared__ double red[NT / 64];
+  double acc = 0.0;
+  const size_t stride = (size_t)gridDim.x * NT;
+  for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
+    const double d = (double)t[i] - (double)x[i];
+    acc += d * d;
+  }
+  acc = block_sum<NT>(acc, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(NT) void finish_scalar_kernel(const double* __restrict__ part, size_t nparts,
+                                                           double denom, float* __restrict__ out) {
+  __shared__ double red[NT / 64];
+  double acc = 0.0;
+  for (size_t i = threadIdx.x; i < nparts; i += NT) acc += part[i];
+  acc = block_sum<NT>(acc, red);
+  if (threadIdx.x == 0) out[0] = (float)(acc / denom);
+}
+
+__global__ __launch_bounds__(NT) void mse_bwd_kernel(const float* __restrict__ x, const float* __restrict__ t,
+                                                     const float* __restrict__ up, float* __restrict__ dx, size_t n) {
+  const size_t stride = (size_t)gridDim.x * NT;
+  const float fn = (float)n;
+  for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
+    const float d = x[i] - t[i];
+    if (up) dx[i] += (2.0f * d * up[0]) / fn;
+    else dx[i] += 2.0f * d / fn;
+  }
+}
+
+__global__ __launch_bounds__(NT) void xent_bwd_kernel(const float* __restrict__ p, const float* __restrict__ t,
+                                                      const float* __restrict__ up, float* __restrict__ dl, size_t n,
+                                                      float batch) {
+  const size_t stride = (size_t)gridDim.x * NT;
+  for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
+    float g = p[i] + (-1.0f) * t[i];
+    if (up) g *= up[0];
+    dl[i] = g / batch;
+  }
+}
+
+constexpr unsigned kMsePartCap = 2048;
+
+}  // namespace
+
+extern "C" {
+
+int mle_softmax_fwd(mle_stream stream, const float* x, float* y, int bc, int rows, int cols, int axis, int causal) {
+  MLE_CHECK_ARG(x && y && bc >= 0 && rows >= 0 && cols >= 0 && (axis == 0 || axis == 1), "mle_softmax_fwd: bad argument");
+  if ((size_t)bc * rows * cols == 0) return MLE_OK;
+  hipStream_t s = as_stream(stream);
+  if (axis == 0) {
+    const size_t lines = (size_t)bc * rows;
+    MLE_CHECK_ARG(lines <= 2147483647u, "mle_softmax_fwd: too many rows");
+    if (cols <= NT * ROW_CPT)
+      softmax_row_kernel<true><<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr);
+    else
+      softmax_row_kernel<false><<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr);
+  } else {
+    MLE_CHECK_ARG(bc <= 65535, "mle_softmax_fwd: bc %d > 65535", bc);
+    dim3 grid((cols + COL_W - 1) / COL_W, bc);
+    if (rows <= COL_RL * COL_RPT) softmax_col_kernel<true><<<grid, NT, 0, s>>>(x, y, rows, cols, causal);
+    else softmax_col_kernel<false><<<grid, NT, 0, s>>>(x, y, rows, cols, causal);
+  }
+  return check_launch("mle_softmax_fwd");
+}
+
+int mle_softmax_bwd(mle_stream stream, const float* y, const float* dy, float* dx, int bc, int rows, int cols,
+                    int axis) {
+  MLE_CHECK_ARG(y && dy && dx && (axis == 0 || axis == 1), "mle_softmax_bwd: bad argument");
+  if ((size_t)bc * rows * cols == 0) return MLE_OK;
+  hipStream_t s = as_stream(stream);
+  if (axis == 0) {
+    const size_t lines = (size_t)bc * rows;
+    MLE_CHECK_ARG(lines <= 2147483647u, "mle_softmax_bwd: too many rows");
+    if (cols <= NT * ROW_CPT) softmax_row_bwd_kernel<true><<<(unsigned)lines, NT, 0, s>>>(y, dy, dx, cols);
+    else softmax_row_bwd_kernel<false><<<(unsigned)lines, NT, 0, s>>>(y, dy, dx, cols);
+  } else {
+    MLE_CHECK_ARG(bc <= 65535, "mle_softmax_bwd: bc %d > 65535", bc);
+    dim3 grid((cols + COL_W - 1) / COL_W, bc);
+    if (rows <= COL_RL * COL_RPT) softmax_col_bwd_kernel<true><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
+    else softmax_col_bwd_kernel<false><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
+  }
+  return check_launch("mle_softmax_bwd");
+}
+
+size_t mle_loss_ws_bytes(size_t n) {
+  // MSE: one double per partial block; cross-entropy: one double per row (<= n).
+  size_t parts = n < kMsePartCap ? n : kMsePartCap;
+  size_t rows = n;
+  size_t b = (parts > rows ? parts : rows) * sizeof(double);
+  return b < 256 ? 256 : b;
+}
+
+int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(x && t && loss && ws && n > 0, "mle_mse_fwd: bad argument");
+  const unsigned g = stream_grid(n, NT, kMsePartCap);
+  if (ws_bytes < g * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "mle_mse_fwd: workspace too small");
+  hipStream_t s = as_stream(stream);
+  double* part = static_cast<double*>(ws);
+  mse_partial_kernel<<<g, NT, 0, s>>>(x, t, n, part);
+  finish_scalar_kernel<<<1, NT, 0, s>>>(part, g, (double)n, loss);
+  return check_launch("mle_mse_fwd");
+}
+
+int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n) {
+  MLE_CHECK_ARG(x && t && dx, "mle_mse_bwd: bad argument");
+  if (n == 0) return MLE_OK;
+  mse_bwd_kernel<<<stream_grid(n, NT, 8192), NT, 0, as_stream(stream)>>>(x, t, upstream, dx, n);
+  return check_launch("mle_mse_bwd");
+}
+
+int mle_softmax_xent_fwd(mle_stream stream, const float* logits, const float* target, float* probs, int rows, int cols,
+                         float* loss, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(logits && target && probs && loss && ws && rows > 0 && cols > 0, "mle_softmax_xent_fwd: bad argument");
+  if (ws_bytes < (size_t)rows * sizeof(double))
+    return set_error(MLE_ERR_WORKSPACE, "mle_softmax_xent_fwd: workspace too small");
+  hipStream_t s = as_stream(stream);
+  double* part = static_cast<double*>(ws);
+  if (cols <= NT * ROW_CPT)
+    softmax_row_kernel<true><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part);
+  else
+    softmax_row_kernel<false><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part);
+  finish_scalar_kernel<<<1, NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
+  return check_launch("mle_softmax_xent_fwd");
+}
+
+int mle_softmax_xent_bwd(mle_stream stream, const float* probs, const float* target, const float* upstream,
+                         float* dlogits, size_t n, int batch) {
+  MLE_CHECK_ARG(probs && target && dlogits && batch > 0, "mle_softmax_xent_bwd: bad argument");
+  if (n == 0) return MLE_OK;
+  xent_bwd_kernel<<<stream_grid(n, NT, 8192), NT, 0, as_stream(stream)>>>(probs, target, upstream, dlogits, n,
+                                                                         (float)batch);
+  return check_launch("mle_softmax_xent_bwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,567 @@
+// ORACLE -- test infrastructure only.
+//
+// A CPU (OpenMP C++) restatement of the ML_Engine arithmetic on the backward /
+// optimizer hot path.  Only tests/, __graft_entry__.smoke() and bench.py's
+// cpu_baseline leg load it, as the checker and the CPU baseline; the product
+// (ml_engine_amd) never calls it.  Each function names the reference code it
+// restates (paths relative to the reference repository root).
+//
+// Accumulation rule: where the reference's summation order is not reproducible
+// (fp32 atomicAdd epilogues of bcmm*, per-thread serial sums inside blocks whose
+// partials are combined by atomics) the oracle accumulates in double and rounds
+// once, giving an order-independent value to compare against.  Element-wise
+// formulas keep the reference's float/double promotions exactly.
+//
+// How each function is pinned (tests/test_oracle_pins.py): torch CPU autograd /
+// matmul / conv2d cross-checks, central finite differences, closed forms and
+// brute-force identities -- see the test file for the list per function.
+#include <math.h>
+#include <float.h>
+#include <limits.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdlib.h>
+#include <vector>
+#include <algorithm>
+#include <omp.h>
+
+#define OEXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+constexpr float kPI = 3.14159265359f;  // Includes/kernels.h:10
+
+// batch_chan_offset (Engine/kernels.cu:371-385)
+inline long long bco(int flag, int b, int c, int C, long long inner) {
+  const int hb = flag & 1, hc = (flag >> 1) & 1;
+  const long long cs = hc ? C : 1;
+  return (hb ? (long long)b * cs : 0) * inner + (hc ? (long long)c : 0) * inner;
+}
+}  // namespace
+
+OEXPORT int orc_num_threads(void) { return omp_get_max_threads(); }
+OEXPORT void orc_set_threads(int n) { if (n > 0) omp_set_num_threads(n); }
+
+// ---------------------------------------------------------------------------
+// GEMM family: bcmm / bcmmABT / bcmmATB / bcmmT (Engine/kernels.cu:387-539).
+// kind 0: C[m x p] (+)= s * A[m x n] B[n x p]
+// kind 1: C[m x p] (+)= s * A[m x n] B[p x n]^T
+// kind 2: C[m x p] (+)= s * A[n x m]^T B[n x p]
+// kind 3: C[m x p] (+)= s * A[n x m]^T B[p x n]^T
+// backward == 0 assigns, 1 accumulates (the reference's atomicAdd); flags are
+// the batch/channel broadcast codes A, B, C of batch_chan_offset.
+OEXPORT void orc_bcmm(int kind, const float* a, const float* b, float* c, int batch, int channels, int m, int n, int p,
+                      int backward, int fa, int fb, int fc, float scale) {
+  for (int z = 0; z < batch * channels; ++z) {
+    const int bi = z / channels, ci = z % channels;
+    const long long oa = bco(fa, bi, ci, channels, (long long)m * n);
+    const long long ob = bco(fb, bi, ci, channels, (long long)n * p);
+    const long long oc = bco(fc, bi, ci, channels, (long long)m * p);
+#pragma omp parallel for schedule(static)
+    for (int row = 0; row < m; ++row) {
+      for (int col = 0; col < p; ++col) {
+        double acc = 0.0;
+        for (int k = 0; k < n; ++k) {
+          float av, bv;
+          switch (kind) {
+            case 0: av = a[oa + (long long)row * n + k]; bv = b[ob + (long long)k * p + col]; break;
+            case 1: av = a[oa + (long long)row * n + k]; bv = b[ob + (long long)col * n + k]; break;
+            case 2: av = a[oa + (long long)k * m + row]; bv = b[ob + (long long)k * p + col]; break;
+            default: av = a[oa + (long long)k * m + row]; bv = b[ob + (long long)col * n + k]; break;
+          }
+          acc += (double)av * (double)bv;
+        }
+        const float sum = (float)acc;
+        float* dst = c + oc + (long long)row * p + col;
+        if (backward == 0) *dst = scale * sum;
+        else *dst += scale * sum;
+      }
+    }
+  }
+}
+
+// BCompress (Engine/kernels.cu:1562-1584): Y[col] += scale * sum over all rows.
+OEXPORT void orc_bcompress(const float* x, float* y, long long rows, int cols, float scale) {
+#pragma omp parallel for schedule(static)
+  for (int c = 0; c < cols; ++c) {
+    double acc = 0.0;
+    for (long long r = 0; r < rows; ++r) acc += x[r * cols + c];
+    y[c] += (float)acc * scale;
+  }
+}
+
+// BCumAdd (Engine/kernels.cu:1586-1592): X[row, :] += Y[:].
+OEXPORT void orc_bcumadd(float* x, const float* y, long long rows, int cols) {
+#pragma omp parallel for schedule(static)
+  for (long long r = 0; r < rows; ++r)
+    for (int c = 0; c < cols; ++c) x[r * cols + c] += y[c];
+}
+
+// Channel_Squeeze1D (Engine/kernels.cu:1734-1761) launched with `nblocks`
+// blocks: average[c] += sum_{b,s} X[b, c, s] for c < nblocks.
+OEXPORT void orc_channel_squeeze(const float* x, float* avg, int batch, int depth, long long spatial, int nblocks) {
+  const int nb = std::min(nblocks, depth);
+#pragma omp parallel for schedule(static)
+  for (int c = 0; c < nb; ++c) {
+    double acc = 0.0;
+    for (int b = 0; b < batch; ++b)
+      for (long long s = 0; s < spatial; ++s) acc += x[((long long)b * depth + c) * spatial + s];
+    avg[c] += (float)acc;
+  }
+}
+
+// broadcast_add (Engine/kernels.cu:1661-1668).
+OEXPORT void orc_broadcast_add(const float* x, const float* bias, float* out, int batch, int kernels, long long hw) {
+  const long long total = (long long)batch * kernels * hw;
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < total; ++i) out[i] = x[i] + bias[(i / hw) % kernels];
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise ops.
+// ScaleAdd (Engine/kernels.cu:1718-1724)
+OEXPORT void orc_scale_add(const float* x, const float* y, float* z, float scale, long long n) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) z[i] = x[i] + scale * y[i];
+}
+// Accumulate (Engine/kernels.cu:1693-1699): Y += scale*X in double, stored float.
+OEXPORT void orc_accumulate(const float* x, float* y, double scale, long long n) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) y[i] = (float)((double)y[i] + scale * (double)x[i]);
+}
+// Scale_Write (Engine/kernels.cu:1677-1682)
+OEXPORT void orc_scale_write(const float* x, float* y, float scale, long long n) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) y[i] = scale * x[i];
+}
+
+// Activations and derivatives (Engine/kernels.cu:1214-1328).  kind: 0 ReLU,
+// 1 GELU (tanh form), 2 SiLU, 3 tanh, 4 sigmoid, 5 leaky ReLU.
+static inline float act_f(int kind, float x) {
+  switch (kind) {
+    case 0: return (x < 0) ? 0.0f : x;
+    case 1: {
+      const float val = sqrtf(2.0f / kPI) * (x + 0.044715f * x * x * x);
+      return 0.5f * x * (1.0f + tanhf(val));
+    }
+    case 2: return x * (1.0f / (1.0f + expf(-x)));
+    case 3: return tanhf(x);
+    case 4: return 1.0f / (1.0f + expf(-1.0f * x));
+    default: return (x < 0) ? 0.01f * x : x;
+  }
+}
+static inline float act_df(int kind, float x) {
+  switch (kind) {
+    case 0: return (x > 0.0f) ? 1.0f : 0.0f;
+    case 1: {
+      const float root = sqrtf(2.0f / kPI);
+      const float u = root * (x + 0.044715f * x * x * x);
+      const float du = root * (1.0f + 0.134145f * x * x);
+      const float t = tanhf(u);
+      return 0.5f + 0.5f * t + 0.5f * x * (1.0f - t * t) * du;
+    }
+    case 2: {
+      const float e = expf(x), ne = 1.0f / e, sg = 1.0f / (1.0f + ne);
+      return sg + (x / (e + ne + 2.0f));
+    }
+    case 3: {
+      const float e2 = expf(2.0f * x), ne2 = 1.0f / e2;
+      return 4.0f / (e2 + ne2 + 2.0f);
+    }
+    case 4: {
+      const float e = expf(x), ne = 1.0f / e;
+      return 1.0f / (e + ne + 2.0f);
+    }
+    default: return (x < 0.0f) ? 0.01f : 1.0f;
+  }
+}
+OEXPORT void orc_act_fwd(int kind, const float* x, float* y, long long n) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) y[i] = act_f(kind, x[i]);
+}
+// deriv_*: grad_out += f'(x) * grad_in
+OEXPORT void orc_act_bwd(int kind, const float* x, const float* dy, float* dx, long long n) {
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) dx[i] += act_df(kind, x[i]) * dy[i];
+}
+
+// HeadifyColChannel (Engine/kernels.cu:1371-1406), flags 0..3.
+OEXPORT void orc_headify(const float* in, float* out, int batch, int heads, int seq, int hd, int flag) {
+  const long long total = (long long)batch * heads * seq * hd;
+  const long long embed = (long long)heads * hd;
+#pragma omp parallel for schedule(static)
+  for (long long idx = 0; idx < total; ++idx) {
+    const long long d = idx % hd, s = (idx / hd) % seq, h = (idx / ((long long)hd * seq)) % heads;
+    const long long b = idx / ((long long)hd * seq * heads);
+    const long long hidx = b * (heads * (long long)seq * hd) + h * ((long long)seq * hd) + s * hd + d;
+    const long long fidx = b * ((long long)seq * embed) + s * embed + h * hd + d;
+    if (flag == 0) out[hidx] = in[fidx];
+    else if (flag == 1) out[fidx] += in[hidx];
+    else if (flag == 2) out[fidx] = in[hidx];
+    else out[hidx] += in[fidx];
+  }
+}
+
+// MatPEncoding (Engine/kernels.cu:166-185)
+OEXPORT void orc_matpe(const float* x, float* out, int batch, int row, int col, int start_idx) {
+  const long long total = (long long)batch * row * col;
+#pragma omp parallel for schedule(static)
+  for (long long g = 0; g < total; ++g) {
+    const int pos = (int)((g % ((long long)row * col)) / col) + start_idx;
+    const int dim = (int)(g % col);
+    const int i = dim / 2;
+    const double expo = (2.0 * i) / col;
+    const double freq = 1.0 / pow(10000.0, expo);
+    const double ang = (double)pos * freq;
+    out[g] = x[g] + ((dim % 2 == 0) ? (float)sin(ang) : (float)cos(ang));
+  }
+}
+
+// PEncoding (Engine/kernels.cu:147-164)
+OEXPORT void orc_pe(float* x, int t, int dim) {
+  const int half = dim / 2;
+  for (int g = 0; g < dim; ++g) {
+    const int fi = (g < half) ? g : g - half;
+    const double expo = -(double)fi * log(10000.0) / (half - 1);
+    const double ang = (double)t * exp(expo);
+    x[g] = (g < half) ? (float)cos(ang) : (float)sin(ang);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax: SoftMax / SoftMask (Engine/kernels.cu:2183-2235) = FindMax,
+// exponentiate(M), SumCols/SumRows (sum < 1e-45 -> 1), Scale_arr(divide).
+// type 0 normalises each row, type 1 each column; masked: c > r -> 0.
+OEXPORT void orc_softmax(const float* x, float* y, int bc, int rows, int cols, int type, int masked) {
+  if (type == 0) {
+#pragma omp parallel for schedule(static)
+    for (long long line = 0; line < (long long)bc * rows; ++line) {
+      const int r = (int)(line % rows);
+      const float* xr = x + line * cols;
+      float* yr = y + line * cols;
+      float m = -FLT_MAX;
+      for (int c = 0; c < cols; ++c) m = fmaxf(m, xr[c]);
+      for (int c = 0; c < cols; ++c) yr[c] = (masked && c > r) ? 0.0f : expf(xr[c] - m);
+      double acc = 0.0;
+      for (int c = 0; c < cols; ++c) acc += yr[c];
+      float sum = (float)acc;
+      if (sum < 1e-45f) sum = 1.0f;
+      for (int c = 0; c < cols; ++c) yr[c] /= sum;
+    }
+  } else {
+#pragma omp parallel for schedule(static)
+    for (long long line = 0; line < (long long)bc * cols; ++line) {
+      const long long bcI = line / cols;
+      const int c = (int)(line % cols);
+      const float* xb = x + bcI * rows * cols;
+      float* yb = y + bcI * rows * cols;
+      float m = -FLT_MAX;
+      for (int r = 0; r < rows; ++r) m = fmaxf(m, xb[(long long)r * cols + c]);
+      double acc = 0.0;
+      for (int r = 0; r < rows; ++r) {
+        const float e = (masked && c > r) ? 0.0f : expf(xb[(long long)r * cols + c] - m);
+        yb[(long long)r * cols + c] = e;
+        acc += e;
+      }
+      float sum = (float)acc;
+      if (sum < 1e-45f) sum = 1.0f;
+      for (int r = 0; r < rows; ++r) yb[(long long)r * cols + c] /= sum;
+    }
+  }
+}
+
+// deriv_softmax (Engine/kernels.cu:2149-2181): dx += y (dy - <dy, y>).
+OEXPORT void orc_softmax_bwd(const float* y, const float* dy, float* dx, int bc, int rows, int cols, int type) {
+  if (type == 0) {
+#pragma omp parallel for schedule(static)
+    for (long long line = 0; line < (long long)bc * rows; ++line) {
+      const long long o = line * cols;
+      double dot = 0.0;
+      for (int c = 0; c < cols; ++c) dot += (double)dy[o + c] * (double)y[o + c];
+      const float d = (float)dot;
+      for (int c = 0; c < cols; ++c) dx[o + c] += y[o + c] * (dy[o + c] - d);
+    }
+  } else {
+#pragma omp parallel for schedule(static)
+    for (long long line = 0; line < (long long)bc * cols; ++line) {
+      const long long base = (line / cols) * rows * cols;
+      const int c = (int)(line % cols);
+      double dot = 0.0;
+      for (int r = 0; r < rows; ++r) dot += (double)dy[base + (long long)r * cols + c] * (double)y[base + (long long)r * cols + c];
+      const float d = (float)dot;
+      for (int r = 0; r < rows; ++r) {
+        const long long o = base + (long long)r * cols + c;
+        dx[o] += y[o] * (dy[o] - d);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Normalisation.  Group g covers N = (channels/groups)*hw contiguous floats;
+// groups == 1 is LayerNorm (LayerMean/LayerStd/LNorm, Engine/kernels.cu:541-572,
+// 670-699, 794-804), groups > 1 GroupNorm (GroupMean/GroupStd/GNorm,
+// Engine/kernels.cu:607-639, 732-763, 818-834).  stats[2g] = mean,
+// stats[2g+1] = sum (x - mean)^2.  gamma = 1, beta = 0, eps as passed.
+OEXPORT void orc_norm_fwd(const float* x, float* y, float* stats, int batch, int channels, long long hw, int groups,
+                          float eps) {
+  const long long N = (long long)(channels / groups) * hw;
+#pragma omp parallel for schedule(static)
+  for (int g = 0; g < batch * groups; ++g) {
+    const float* xg = x + (long long)g * N;
+    float* yg = y + (long long)g * N;
+    double s = 0.0;
+    for (long long i = 0; i < N; ++i) s += xg[i];
+    const float mean = (float)(s / (double)N);
+    double ss = 0.0;
+    for (long long i = 0; i < N; ++i) {
+      const float d = xg[i] - mean;
+      ss += (double)d * (double)d;
+    }
+    const float ssd = (float)ss;
+    const float r = 1.0f / sqrtf((1.0f / (float)N) * ssd + eps);
+    for (long long i = 0; i < N; ++i) yg[i] = (xg[i] - mean) * r;
+    stats[2 * g] = mean;
+    stats[2 * g + 1] = ssd;
+  }
+}
+
+// LayerBackward / GroupBackward (Engine/kernels.cu:849-896) after ggamma =
+// dy (gamma = 1), ggammanode = dy*y and their per-group sums
+// (Engine/engine.cu:3116-3130, 3262-3276).  reference_layout reproduces
+// LayerBackward's `idx >= batch*row*col` guard for channels > 1.
+OEXPORT void orc_norm_bwd(const float* y, const float* dy, float* dx, const float* stats, int batch, int channels,
+                          long long hw, int groups, float eps, int reference_layout) {
+  const long long N = (long long)(channels / groups) * hw;
+  const int G = batch * groups;
+  std::vector<float> sg(G), sgy(G);
+#pragma omp parallel for schedule(static)
+  for (int g = 0; g < G; ++g) {
+    double a = 0.0, b = 0.0;
+    for (long long i = 0; i < N; ++i) {
+      const long long o = (long long)g * N + i;
+      a += dy[o];
+      b += (double)(dy[o] * y[o]);
+    }
+    sg[g] = (float)a;
+    sgy[g] = (float)b;
+  }
+  const bool quirk = reference_layout && groups == 1 && channels > 1;
+  const long long total = quirk ? (long long)batch * hw : (long long)G * N;
+  const float fN = (float)N;
+#pragma omp parallel for schedule(static)
+  for (long long idx = 0; idx < total; ++idx) {
+    const int g = quirk ? (int)(idx / hw) : (int)(idx / N);
+    const float r = 1.0f / sqrtf(stats[2 * g + 1] / fN + eps);
+    dx[idx] += r * (dy[idx] - (sg[g] / fN) - y[idx] * (sgy[g] / fN));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Convolution (NCHW, OIHW).
+// CV2D (Engine/kernels.cu:985-1019)
+OEXPORT void orc_conv_fwd(const float* x, const float* w, const float* bias, float* y, int N, int Cin, int H, int W,
+                          int Cout, int KH, int KW, int pad, int stride) {
+  const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int co = 0; co < Cout; ++co)
+      for (int oy = 0; oy < OH; ++oy)
+        for (int ox = 0; ox < OW; ++ox) {
+          double acc = 0.0;
+          for (int ci = 0; ci < Cin; ++ci)
+            for (int kh = 0; kh < KH; ++kh)
+              for (int kw = 0; kw < KW; ++kw) {
+                const int iy = oy * stride - pad + kh, ix = ox * stride - pad + kw;
+                if (iy < 0 || iy >= H || ix < 0 || ix >= W) continue;
+                acc += (double)x[(((long long)n * Cin + ci) * H + iy) * W + ix] *
+                       (double)w[(((long long)co * Cin + ci) * KH + kh) * KW + kw];
+              }
+          const float s = (float)acc;
+          y[(((long long)n * Cout + co) * OH + oy) * OW + ox] = bias ? s + bias[co] : s;
+        }
+}
+
+// CV2D_GradInput (Engine/kernels.cu:1053-1089): dX += ...
+OEXPORT void orc_conv_dgrad(const float* dy, const float* w, float* dx, int N, int Cin, int H, int W, int Cout, int KH,
+                            int KW, int pad, int stride) {
+  const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int ic = 0; ic < Cin; ++ic)
+      for (int ih = 0; ih < H; ++ih)
+        for (int iw = 0; iw < W; ++iw) {
+          double acc = 0.0;
+          for (int oc = 0; oc < Cout; ++oc)
+            for (int kh = 0; kh < KH; ++kh) {
+              const int nr = ih + pad - kh;
+              if (nr < 0 || nr % stride != 0) continue;
+              const int oy = nr / stride;
+              if (oy >= OH) continue;
+              for (int kw = 0; kw < KW; ++kw) {
+                const int nc = iw + pad - kw;
+                if (nc < 0 || nc % stride != 0) continue;
+                const int ox = nc / stride;
+                if (ox >= OW) continue;
+                acc += (double)dy[(((long long)n * Cout + oc) * OH + oy) * OW + ox] *
+                       (double)w[(((long long)oc * Cin + ic) * KH + kh) * KW + kw];
+              }
+            }
+          dx[(((long long)n * Cin + ic) * H + ih) * W + iw] += (float)acc;
+        }
+}
+
+// GV2D (Engine/kernels.cu:1021-1051): dK = ... (assign)
+OEXPORT void orc_conv_wgrad(const float* x, const float* dy, float* dw, int N, int Cin, int H, int W, int Cout, int KH,
+                            int KW, int pad, int stride) {
+  const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int co = 0; co < Cout; ++co)
+    for (int ci = 0; ci < Cin; ++ci)
+      for (int kh = 0; kh < KH; ++kh)
+        for (int kw = 0; kw < KW; ++kw) {
+          double acc = 0.0;
+          for (int n = 0; n < N; ++n)
+            for (int oy = 0; oy < OH; ++oy)
+              for (int ox = 0; ox < OW; ++ox) {
+                const int iy = oy * stride - pad + kh, ix = ox * stride - pad + kw;
+                if (iy < 0 || iy >= H || ix < 0 || ix >= W) continue;
+                acc += (double)x[(((long long)n * Cin + ci) * H + iy) * W + ix] *
+                       (double)dy[(((long long)n * Cout + co) * OH + oy) * OW + ox];
+              }
+          dw[(((long long)co * Cin + ci) * KH + kh) * KW + kw] = (float)acc;
+        }
+}
+
+// ---------------------------------------------------------------------------
+// Losses.
+// scalar_mse_kernel (Engine/kernels.cu:1808-1816): sum (t - x)^2 / n.
+OEXPORT float orc_mse_loss(const float* x, const float* t, long long n) {
+  double acc = 0.0;
+#pragma omp parallel for reduction(+ : acc) schedule(static)
+  for (long long i = 0; i < n; ++i) {
+    const double d = (double)t[i] - (double)x[i];
+    acc += d * d;
+  }
+  return (float)(acc / (double)n);
+}
+// deriv_mse_kernel (Engine/kernels.cu:1838-1848), full == false.
+OEXPORT void orc_mse_bwd(const float* x, const float* t, const float* up, float* dx, long long n) {
+  const float fn = (float)n;
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) {
+    if (up) dx[i] += (2.0f * (x[i] - t[i]) * up[0]) / fn;
+    else dx[i] += 2.0f * (x[i] - t[i]) / fn;
+  }
+}
+// SoftMaxCrossEntropy forward (Engine/engine.cu:2088-2100): row softmax, then
+// scalar_ce_kernel (Engine/kernels.cu:1818-1826).
+OEXPORT float orc_softmax_xent_fwd(const float* logits, const float* target, float* probs, int rows, int cols) {
+  orc_softmax(logits, probs, 1, rows, cols, 0, 0);
+  const long long n = (long long)rows * cols;
+  double acc = 0.0;
+#pragma omp parallel for reduction(+ : acc) schedule(static)
+  for (long long i = 0; i < n; ++i) acc += -(double)target[i] * log((double)probs[i] + 1e-27);
+  return (float)(acc / (double)n);
+}
+// SoftMaxCrossEntropy backward (Engine/engine.cu:2104-2110): ScaleAdd(-1),
+// optional ScalePtr(upstream), ScaleValue(/batch).  Assigns.
+OEXPORT void orc_softmax_xent_bwd(const float* probs, const float* target, const float* up, float* dl, long long n,
+                                  int batch) {
+  const float fb = (float)batch;
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) {
+    float g = probs[i] + (-1.0f) * target[i];
+    if (up) g *= up[0];
+    dl[i] = g / fb;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Optimizer.
+// SumSquared (Engine/kernels.cu:1486-1506): *scale += sum (double)g^2.
+OEXPORT void orc_sumsq(const float* g, long long n, double* accum) {
+  long double acc = 0.0L;  // order-independent at double precision
+  for (long long i = 0; i < n; ++i) acc += (long double)((double)g[i] * (double)g[i]);
+  *accum += (double)acc;
+}
+// Sqrt_Scale type 0 (Engine/kernels.cu:1763-1773).
+OEXPORT void orc_sqrt_scale(double* x, double scale) {
+  if (x[0] == x[0]) {
+    const double cur = sqrt(x[0]);
+    x[0] = (cur > 1.0) ? cur * scale : scale;
+  }
+}
+// SP type 1 via ScalePtr (Includes/kernels.h:293-300): g /= (float)s.
+OEXPORT void orc_clip(float* g, long long n, const double* s) {
+  const float f = (float)s[0];
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) g[i] /= f;
+}
+// AdamUpdate / AdamWUpdate (Engine/kernels.cu:1508-1534).
+OEXPORT void orc_adam(float* out, const float* grad, long long n, int t, float* m, float* v, float b1, float b2,
+                      float eps, float lambda, float lr, int adamw) {
+  const double c1 = adamw ? (1.0 - pow((double)b1, (double)t)) : (1.0 - (double)powf(b1, (float)t));
+  const double c2 = adamw ? (1.0 - pow((double)b2, (double)t)) : (1.0 - (double)powf(b2, (float)t));
+#pragma omp parallel for schedule(static)
+  for (long long i = 0; i < n; ++i) {
+    const float g = grad[i];
+    m[i] = (float)((double)(b1 * m[i]) + (1.0 - (double)b1) * (double)g);
+    v[i] = (float)((double)(b2 * v[i]) + ((1.0 - (double)b2) * (double)g) * (double)g);
+    const float m_hat = (float)((double)m[i] / c1);
+    const float v_hat = (float)((double)v[i] / c2);
+    const float vs = sqrtf(v_hat);
+    if (adamw) out[i] -= lr * ((m_hat / (vs + eps)) + lambda * out[i]);
+    else out[i] -= lr * m_hat / (vs + eps);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Integer / index paths.
+// GatherEmbeddings (Engine/kernels.cu:2279-2296)
+OEXPORT void orc_gather(float* out, const float* table, const int32_t* keys, int batch, int c, int max_c, int dim) {
+  const long long total = (long long)batch * c * dim;
+#pragma omp parallel for schedule(static)
+  for (long long g = 0; g < total; ++g) {
+    const long long b = g / ((long long)c * dim), kr = g % ((long long)c * dim);
+    const long long tok = kr / dim, d = kr % dim;
+    const int key = keys[b * max_c + tok];
+    out[g] = (key == INT_MIN || key < 0) ? 0.0f : table[(long long)key * dim + d];
+  }
+}
+// KeyUpdate (Engine/kernels.cu:1536-1549) applied serially in token order
+// (the reference races on repeated keys): table[key] += scale * grad[token].
+// Keys >= vocab are skipped (the reference would write out of bounds).
+OEXPORT void orc_scatter_add(float* table, const float* grad, const int32_t* keys, int batch, int c, int max_c,
+                             int dim, int vocab, float scale) {
+  for (int b = 0; b < batch; ++b)
+    for (int s = 0; s < c; ++s) {
+      const int key = keys[(long long)b * max_c + s];
+      if (key == INT_MIN || key < 0 || key >= vocab) continue;
+      const float* gr = grad + ((long long)b * c + s) * dim;
+      float* tr = table + (long long)key * dim;
+      for (int d = 0; d < dim; ++d) tr[d] += scale * gr[d];
+    }
+}
+// OneHotEmbeddings (Engine/kernels.cu:1551-1560); out must be zeroed.
+OEXPORT void orc_onehot(float* out, const int32_t* keys, int batch, int clen, int max_clen, int vocab) {
+  for (long long g = 0; g < (long long)batch * clen; ++g) {
+    const long long row = g / clen, col = g % clen;
+    const int key = keys[row * max_clen + col];
+    if (key == INT_MIN || key < 0 || key >= vocab) continue;
+    out[g * vocab + key] = 1.0f;
+  }
+}
+// ArgMax (Engine/kernels.cu:2353-2366), per row.
+OEXPORT void orc_argmax(const float* x, int rows, int cols, int32_t* out) {
+  for (int r = 0; r < rows; ++r) {
+    const float* a = x + (long long)r * cols;
+    int mi = 0;
+    float mv = a[0];
+    for (int i = 1; i < cols; ++i)
+      if (a[i] > mv) {
+        mv = a[i];
+        mi = i;
+      }
+    out[r] = mi;
+  }
+}

@@ -1,0 +1,388 @@
+"""Kernel-level parity: every C ABI entry point against the CPU oracle.
+
+Bars: integer/index paths bit-exact; elementwise,
+reduction and optimizer results within 1e-5 relative; GEMM and convolution
+within 1e-4 relative (absolute floor scaled by the output's largest value,
+which is where fp32 accumulation error lives for a K-long dot product).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+EW = dict(rtol=1e-5, atol_scale=1e-6)      # elementwise / reductions / optimizer
+MM = dict(rtol=1e-4, atol_scale=1e-5)      # GEMM / conv
+
+
+def B(h, a):
+    return h.Buffer.from_array(np.ascontiguousarray(a))
+
+
+# --------------------------------------------------------------------------- GEMM
+GEMM_CASES = [
+    # (ta, tb, M, N, K, batch)
+    (0, 0, 64, 64, 32, 1),
+    (0, 1, 130, 70, 37, 1),
+    (1, 0, 129, 257, 45, 1),
+    (1, 1, 33, 100, 64, 1),
+    (0, 0, 256, 384, 512, 1),
+    (0, 1, 200, 136, 256, 3),
+    (1, 0, 64, 96, 300, 2),
+    (1, 1, 256, 256, 64, 2),
+]
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K,batch", GEMM_CASES)
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_gemm(hip, orc, ta, tb, M, N, K, batch, beta):
+    r = rng(1000 + M + N + K + batch + ta * 7 + tb * 11)
+    a_shape = (batch, K, M) if ta else (batch, M, K)
+    b_shape = (batch, N, K) if tb else (batch, K, N)
+    A = r.standard_normal(a_shape, dtype=np.float32)
+    Bm = r.standard_normal(b_shape, dtype=np.float32)
+    C0 = r.standard_normal((batch, M, N), dtype=np.float32)
+    alpha = 0.5
+    ref = C0.copy()
+    kind = ta * 2 + tb
+    # orc_bcmm dims: kind 0 (m,n,p)=(M,K,N), 1 (M,K,N), 2 (M,K,N), 3 (M,K,N)
+    orc.call("orc_bcmm", kind, orc.ptr(A), orc.ptr(Bm), orc.ptr(ref), batch, 1, M, K, N, int(beta != 0), 3, 3, 3, alpha)
+    dA, dB, dC = B(hip, A), B(hip, Bm), B(hip, C0)
+    lda = M if ta else K
+    ldb = K if tb else N
+    hip.call("mle_gemm", None, ta, tb, M, N, K, alpha, dA.ptr, lda, A[0].size, dB.ptr, ldb, Bm[0].size, beta,
+             dC.ptr, N, M * N, batch, None)
+    assert_close(dC.numpy(), ref, what=f"gemm ta={ta} tb={tb}", **MM)
+
+
+def test_gemm_broadcast_and_colsum(hip, orc):
+    r = rng(7)
+    M, N, K, batch = 96, 80, 72, 3
+    A = r.standard_normal((batch, M, K), dtype=np.float32)
+    W = r.standard_normal((K, N), dtype=np.float32)  # broadcast operand (stride 0)
+    ref = np.zeros((batch, M, N), np.float32)
+    orc.call("orc_bcmm", 0, orc.ptr(A), orc.ptr(W), orc.ptr(ref), batch, 1, M, K, N, 0, 3, 0, 3, 1.0)
+    dA, dW, dC = B(hip, A), B(hip, W), hip.Buffer.zeros((batch, M, N))
+    hip.call("mle_gemm", None, 0, 0, M, N, K, 1.0, dA.ptr, K, M * K, dW.ptr, N, 0, 0.0, dC.ptr, N, M * N, batch, None)
+    assert_close(dC.numpy(), ref, what="gemm broadcast B", **MM)
+    # dW = X^T dY with fused db = colsum(dY) (Linear backward)
+    X = r.standard_normal((300, 64), dtype=np.float32)
+    dY = r.standard_normal((300, 130), dtype=np.float32)
+    dWr = np.ones((64, 130), np.float32)
+    dbr = np.full(130, 0.25, np.float32)
+    orc.call("orc_bcmm", 2, orc.ptr(X), orc.ptr(dY), orc.ptr(dWr), 1, 1, 64, 300, 130, 1, 3, 3, 0, 1.0)
+    orc.call("orc_bcompress", orc.ptr(dY), orc.ptr(dbr), 300, 130, 1.0)
+    gX, gY = B(hip, X), B(hip, dY)
+    gW, gb = B(hip, np.ones((64, 130), np.float32)), B(hip, np.full(130, 0.25, np.float32))
+    hip.call("mle_gemm", None, 1, 0, 64, 130, 300, 1.0, gX.ptr, 64, 0, gY.ptr, 130, 0, 1.0, gW.ptr, 130, 0, 1, gb.ptr)
+    assert_close(gW.numpy(), dWr, what="dW", **MM)
+    assert_close(gb.numpy(), dbr, what="db (fused colsum)", **EW)
+
+
+# ------------------------------------------------------------------- activations
+@pytest.mark.parametrize("kind", ["relu", "gelu", "silu", "tanh", "sigmoid", "leaky_relu"])
+def test_activation(hip, orc, kind):
+    r = rng(11)
+    n = 10007
+    x = (r.standard_normal(n, dtype=np.float32) * 4).astype(np.float32)
+    x[:8] = [0.0, -0.0, 1e-30, -1e-30, 90.0, -90.0, 20.0, -20.0]
+    dy = r.standard_normal(n, dtype=np.float32)
+    dx0 = r.standard_normal(n, dtype=np.float32)
+    k = hip.ACT[kind]
+    yr = np.zeros_like(x)
+    orc.call("orc_act_fwd", k, orc.ptr(x), orc.ptr(yr), n)
+    dxr = dx0.copy()
+    orc.call("orc_act_bwd", k, orc.ptr(x), orc.ptr(dy), orc.ptr(dxr), n)
+    gx, gy, gdy, gdx = B(hip, x), hip.Buffer.zeros(n), B(hip, dy), B(hip, dx0)
+    hip.call("mle_act_fwd", None, k, gx.ptr, gy.ptr, n)
+    hip.call("mle_act_bwd", None, k, gx.ptr, gdy.ptr, gdx.ptr, n)
+    assert_close(gy.numpy(), yr, what=f"{kind} fwd", **EW)
+    assert_close(gdx.numpy(), dxr, what=f"{kind} bwd", **EW)
+
+
+# ----------------------------------------------------------------------- softmax
+@pytest.mark.parametrize("bc,rows,cols", [(3, 37, 45), (2, 256, 256), (1, 300, 20), (2, 5, 9000)])
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("causal", [0, 1])
+def test_softmax(hip, orc, bc, rows, cols, axis, causal):
+    r = rng(bc * 131 + rows + cols)
+    x = (r.standard_normal((bc, rows, cols), dtype=np.float32) * 3).astype(np.float32)
+    dy = r.standard_normal((bc, rows, cols), dtype=np.float32)
+    dx0 = r.standard_normal((bc, rows, cols), dtype=np.float32)
+    yr = np.zeros_like(x)
+    orc.call("orc_softmax", orc.ptr(x), orc.ptr(yr), bc, rows, cols, axis, causal)
+    dxr = dx0.copy()
+    orc.call("orc_softmax_bwd", orc.ptr(yr), orc.ptr(dy), orc.ptr(dxr), bc, rows, cols, axis)
+    gx, gy = B(hip, x), hip.Buffer.zeros(x.shape)
+    hip.call("mle_softmax_fwd", None, gx.ptr, gy.ptr, bc, rows, cols, axis, causal)
+    y = gy.numpy()
+    assert_close(y, yr, what="softmax fwd", **EW)
+    gyr, gdy, gdx = B(hip, yr), B(hip, dy), B(hip, dx0)
+    hip.call("mle_softmax_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, bc, rows, cols, axis)
+    assert_close(gdx.numpy(), dxr, what="softmax bwd", **EW)
+
+
+def test_softmax_xent(hip, orc):
+    r = rng(5)
+    rows, cols, batch = 96, 1000, 4
+    logits = (r.standard_normal((rows, cols), dtype=np.float32) * 2).astype(np.float32)
+    tgt = np.zeros((rows, cols), np.float32)
+    tgt[np.arange(rows), r.integers(0, cols, rows)] = 1.0
+    pr = np.zeros_like(logits)
+    lr_ = orc.call("orc_softmax_xent_fwd", orc.ptr(logits), orc.ptr(tgt), orc.ptr(pr), rows, cols)
+    dl = np.zeros_like(logits)
+    orc.call("orc_softmax_xent_bwd", orc.ptr(pr), orc.ptr(tgt), None, orc.ptr(dl), rows * cols, batch)
+    gl, gt, gp, gloss = B(hip, logits), B(hip, tgt), hip.Buffer.zeros((rows, cols)), hip.Buffer.zeros(1)
+    ws = hip.Buffer(hip.lib().mle_loss_ws_bytes(rows * cols))
+    hip.call("mle_softmax_xent_fwd", None, gl.ptr, gt.ptr, gp.ptr, rows, cols, gloss.ptr, ws.ptr, ws.nbytes)
+    assert_close(gp.numpy(), pr, what="xent probs", **EW)
+    assert_close(gloss.numpy(), np.array([lr_], np.float32), what="xent loss", **EW)
+    gd = hip.Buffer.zeros((rows, cols))
+    hip.call("mle_softmax_xent_bwd", None, gp.ptr, gt.ptr, None, gd.ptr, rows * cols, batch)
+    assert_close(gd.numpy(), dl, what="xent bwd", **EW)
+
+
+def test_mse(hip, orc):
+    r = rng(6)
+    n = 123457
+    x = r.standard_normal(n, dtype=np.float32)
+    t = r.standard_normal(n, dtype=np.float32)
+    dx0 = r.standard_normal(n, dtype=np.float32)
+    lref = orc.call("orc_mse_loss", orc.ptr(x), orc.ptr(t), n)
+    dxr = dx0.copy()
+    orc.call("orc_mse_bwd", orc.ptr(x), orc.ptr(t), None, orc.ptr(dxr), n)
+    gx, gt, gl, gdx = B(hip, x), B(hip, t), hip.Buffer.zeros(1), B(hip, dx0)
+    ws = hip.Buffer(hip.lib().mle_loss_ws_bytes(n))
+    hip.call("mle_mse_fwd", None, gx.ptr, gt.ptr, n, gl.ptr, ws.ptr, ws.nbytes)
+    hip.call("mle_mse_bwd", None, gx.ptr, gt.ptr, None, gdx.ptr, n)
+    assert_close(gl.numpy(), np.array([lref], np.float32), what="mse loss", **EW)
+    assert_close(gdx.numpy(), dxr, what="mse bwd", **EW)
+
+
+# ------------------------------------------------------------------------ norms
+@pytest.mark.parametrize("batch,channels,hw,groups", [(3, 1, 37 * 45, 1), (2, 1, 256 * 512, 1), (2, 8, 700, 4),
+                                                     (2, 64, 4096, 32), (2, 3, 33, 1)])
+def test_norm(hip, orc, batch, channels, hw, groups):
+    r = rng(batch + channels + hw + groups)
+    shape = (batch, channels, hw)
+    x = (r.standard_normal(shape, dtype=np.float32) * 2 + 0.5).astype(np.float32)
+    dy = r.standard_normal(shape, dtype=np.float32)
+    dx0 = r.standard_normal(shape, dtype=np.float32)
+    yr = np.zeros_like(x)
+    st = np.zeros(2 * batch * groups, np.float32)
+    orc.call("orc_norm_fwd", orc.ptr(x), orc.ptr(yr), orc.ptr(st), batch, channels, hw, groups, 1e-5)
+    dxr = dx0.copy()
+    orc.call("orc_norm_bwd", orc.ptr(yr), orc.ptr(dy), orc.ptr(dxr), orc.ptr(st), batch, channels, hw, groups, 1e-5, 1)
+    L = hip.lib()
+    ws = hip.Buffer(L.mle_norm_ws_bytes(batch, channels, hw, groups))
+    gx, gy, gst = B(hip, x), hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * batch * groups)
+    hip.call("mle_norm_fwd", None, gx.ptr, gy.ptr, gst.ptr, batch, channels, hw, groups, 1e-5, ws.ptr, ws.nbytes)
+    assert_close(gy.numpy(), yr, what="norm fwd", **EW)
+    assert_close(gst.numpy(), st, what="norm stats", **EW)
+    gyr, gdy, gdx, gstr = B(hip, yr), B(hip, dy), B(hip, dx0), B(hip, st)
+    hip.call("mle_norm_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, gstr.ptr, batch, channels, hw, groups, 1e-5, 1,
+             ws.ptr, ws.nbytes)
+    assert_close(gdx.numpy(), dxr, what="norm bwd", **EW)
+
+
+# ---------------------------------------------------------------------- conv
+@pytest.mark.parametrize("n,cin,h,w,cout,k,pad,stride", [
+    (2, 3, 9, 9, 5, 3, 1, 1), (2, 4, 8, 10, 6, 1, 0, 1), (1, 3, 11, 11, 4, 3, 1, 2),
+    (2, 16, 16, 16, 32, 3, 1, 1), (1, 8, 7, 7, 8, 5, 0, 1),
+])
+def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
+    r = rng(n * 7 + cin + h + cout + k)
+    oh = (2 * pad + h - k) // stride + 1
+    ow = (2 * pad + w - k) // stride + 1
+    x = r.standard_normal((n, cin, h, w), dtype=np.float32)
+    wt = r.standard_normal((cout, cin, k, k), dtype=np.float32)
+    b = r.standard_normal(cout, dtype=np.float32)
+    dy = r.standard_normal((n, cout, oh, ow), dtype=np.float32)
+    dx0 = r.standard_normal(x.shape, dtype=np.float32)
+    yr = np.zeros((n, cout, oh, ow), np.float32)
+    orc.call("orc_conv_fwd", orc.ptr(x), orc.ptr(wt), orc.ptr(b), orc.ptr(yr), n, cin, h, w, cout, k, k, pad, stride)
+    dxr = dx0.copy()
+    orc.call("orc_conv_dgrad", orc.ptr(dy), orc.ptr(wt), orc.ptr(dxr), n, cin, h, w, cout, k, k, pad, stride)
+    dwr = np.zeros_like(wt)
+    orc.call("orc_conv_wgrad", orc.ptr(x), orc.ptr(dy), orc.ptr(dwr), n, cin, h, w, cout, k, k, pad, stride)
+    gx, gw, gb, gy = B(hip, x), B(hip, wt), B(hip, b), hip.Buffer.zeros(yr.shape)
+    hip.call("mle_conv2d_fwd", None, gx.ptr, gw.ptr, gb.ptr, gy.ptr, n, cin, h, w, cout, k, k, pad, stride)
+    assert_close(gy.numpy(), yr, what="conv fwd", **MM)
+    gdy, gdx = B(hip, dy), B(hip, dx0)
+    hip.call("mle_conv2d_dgrad", None, gdy.ptr, gw.ptr, gdx.ptr, n, cin, h, w, cout, k, k, pad, stride)
+    assert_close(gdx.numpy(), dxr, what="conv dgrad", **MM)
+    L = hip.lib()
+    ws = hip.Buffer(L.mle_conv2d_wgrad_ws_bytes(n, cin, h, w, cout, k, k, pad, stride))
+    gdw = B(hip, np.full(wt.shape, 7.0, np.float32))  # wgrad assigns
+    hip.call("mle_conv2d_wgrad", None, gx.ptr, gdy.ptr, gdw.ptr, n, cin, h, w, cout, k, k, pad, stride, ws.ptr, ws.nbytes)
+    assert_close(gdw.numpy(), dwr, what="conv wgrad", **MM)
+
+
+# ----------------------------------------------------------------- optimizer
+@pytest.mark.parametrize("adamw", [0, 1])
+@pytest.mark.parametrize("t", [1, 7])
+def test_adam(hip, orc, adamw, t):
+    r = rng(20 + adamw + t)
+    n = 100003
+    p = (r.standard_normal(n) * 0.02).astype(np.float32)
+    g = (r.standard_normal(n) * 1e-3).astype(np.float32)
+    m = (r.standard_normal(n) * 1e-4).astype(np.float32)
+    v = np.abs(r.standard_normal(n) * 1e-6).astype(np.float32)
+    pr, mr, vr = p.copy(), m.copy(), v.copy()
+    orc.call("orc_adam", orc.ptr(pr), orc.ptr(g), n, t, orc.ptr(mr), orc.ptr(vr), 0.9, 0.999, 1e-8, 0.01, 3e-4, adamw)
+    gp, gg, gm, gv = B(hip, p), B(hip, g), B(hip, m), B(hip, v)
+    hip.call("mle_adam_update", None, gp.ptr, gg.ptr, gm.ptr, gv.ptr, n, t, 3e-4, 0.9, 0.999, 1e-8, 0.01, adamw, None)
+    assert_close(gm.numpy(), mr, what="m", **EW)
+    assert_close(gv.numpy(), vr, what="v", **EW)
+    assert_close(gp.numpy(), pr, what="p", **EW)
+
+
+def test_sqnorm_and_fused_clip(hip, orc):
+    r = rng(31)
+    n = 1_000_003
+    p = (r.standard_normal(n) * 0.02).astype(np.float32)
+    g = (r.standard_normal(n) * 1e-3).astype(np.float32)
+    g[r.random(n) < 0.01] *= 100.0
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    acc = np.zeros(1, np.float64)
+    orc.call("orc_sumsq", orc.ptr(g), n, orc.ptr(acc))
+    s = acc.copy()
+    orc.call("orc_sqrt_scale", orc.ptr(s), 1.0)
+    gc = g.copy()
+    orc.call("orc_clip", orc.ptr(gc), n, orc.ptr(s))
+    pr, mr, vr = p.copy(), m.copy(), v.copy()
+    orc.call("orc_adam", orc.ptr(pr), orc.ptr(gc), n, 1, orc.ptr(mr), orc.ptr(vr), 0.9, 0.999, 1e-8, 0.01, 3e-4, 1)
+    L = hip.lib()
+    gg = B(hip, g)
+    gacc = B(hip, np.array([0.5], np.float64))
+    ws = hip.Buffer(L.mle_sqnorm_ws_bytes(n))
+    hip.call("mle_grad_sqnorm", None, gg.ptr, n, gacc.ptr, None, ws.ptr, ws.nbytes)
+    np.testing.assert_allclose(gacc.numpy(dtype=np.float64), acc + 0.5, rtol=1e-12)
+    hip.call("mle_sqrt_scale", None, gacc.ptr, 1.0)
+    gp, gm, gv, gnorm = B(hip, p), B(hip, m), B(hip, v), hip.Buffer.zeros(1, np.float64)
+    ws2 = hip.Buffer(L.mle_adamw_clip_ws_bytes(n))
+    hip.call("mle_adamw_clip_fused", None, gp.ptr, gg.ptr, gm.ptr, gv.ptr, n, 1, 3e-4, 0.9, 0.999, 1e-8, 0.01, 1, 1.0,
+             gnorm.ptr, ws2.ptr, ws2.nbytes)
+    np.testing.assert_allclose(gnorm.numpy(dtype=np.float64), s, rtol=1e-12)
+    assert_close(gm.numpy(), mr, what="m", **EW)
+    assert_close(gv.numpy(), vr, what="v", **EW)
+    assert_close(gp.numpy(), pr, what="p", **EW)
+    np.testing.assert_array_equal(gg.numpy(), g)  # the fused path leaves g unclipped
+
+
+# ------------------------------------------------------------ integer paths
+def test_gather_onehot_argmax_scatter(hip, orc):
+    r = rng(41)
+    batch, clen, maxc, dim, vocab = 4, 50, 64, 48, 37
+    keys = r.integers(0, vocab, (batch, maxc)).astype(np.int32)
+    keys[0, 3] = -1
+    keys[1, 5] = np.iinfo(np.int32).min
+    keys[2, 7] = vocab + 3  # out of range for one-hot and scatter
+    table = r.standard_normal((vocab + 8, dim), dtype=np.float32)
+    out_r = np.zeros((batch, clen, dim), np.float32)
+    orc.call("orc_gather", orc.ptr(out_r), orc.ptr(table), orc.ptr(keys), batch, clen, maxc, dim)
+    gk, gt, go = B(hip, keys), B(hip, table), hip.Buffer.zeros((batch, clen, dim))
+    hip.call("mle_embed_gather", None, go.ptr, gt.ptr, gk.ptr, batch, clen, maxc, dim)
+    np.testing.assert_array_equal(go.numpy(), out_r)
+
+    oh_r = np.zeros((batch * clen, vocab), np.float32)
+    orc.call("orc_onehot", orc.ptr(oh_r), orc.ptr(keys), batch, clen, maxc, vocab)
+    goh = hip.Buffer.zeros((batch * clen, vocab))
+    hip.call("mle_onehot", None, goh.ptr, gk.ptr, batch, clen, maxc, vocab)
+    np.testing.assert_array_equal(goh.numpy(), oh_r)
+
+    x = r.standard_normal((33, 501), dtype=np.float32)
+    x[3, 10] = x[3, 400] = 50.0  # tie -> first index
+    x[5, :] = -np.inf
+    x[6, 0] = np.nan
+    am_r = np.zeros(33, np.int32)
+    orc.call("orc_argmax", orc.ptr(x), 33, 501, orc.ptr(am_r))
+    gx, gam = B(hip, x), hip.Buffer.zeros(33, np.int32)
+    hip.call("mle_argmax", None, gx.ptr, 33, 501, gam.ptr)
+    np.testing.assert_array_equal(gam.numpy(), am_r)
+
+    grad = r.standard_normal((batch, clen, dim), dtype=np.float32)
+    tab_r = table[:vocab].copy()
+    orc.call("orc_scatter_add", orc.ptr(tab_r), orc.ptr(grad), orc.ptr(keys), batch, clen, maxc, dim, vocab, 1.0)
+    gtab, gg = B(hip, table[:vocab].copy()), B(hip, grad)
+    ws = hip.Buffer(hip.lib().mle_embed_scatter_ws_bytes(batch, clen))
+    hip.call("mle_embed_scatter_add", None, gtab.ptr, gg.ptr, gk.ptr, batch, clen, maxc, dim, vocab, 1.0, ws.ptr, ws.nbytes)
+    assert_close(gtab.numpy(), tab_r, what="scatter add", **EW)
+
+
+# ------------------------------------------------------ elementwise / layout
+def test_elementwise_and_layout(hip, orc):
+    r = rng(51)
+    n = 4099
+    x = r.standard_normal(n, dtype=np.float32)
+    y = r.standard_normal(n, dtype=np.float32)
+    z = np.zeros(n, np.float32)
+    orc.call("orc_scale_add", orc.ptr(x), orc.ptr(y), orc.ptr(z), -1.0, n)
+    gx, gy, gz = B(hip, x), B(hip, y), hip.Buffer.zeros(n)
+    hip.call("mle_scale_add", None, gx.ptr, gy.ptr, gz.ptr, -1.0, n)
+    np.testing.assert_array_equal(gz.numpy(), z)
+    acc = y.copy()
+    orc.call("orc_accumulate", orc.ptr(x), orc.ptr(acc), 0.125, n)
+    hip.call("mle_accumulate", None, gx.ptr, gy.ptr, 0.125, n)
+    np.testing.assert_array_equal(gy.numpy(), acc)
+
+    bsz, heads, seq, hd = 2, 4, 9, 8
+    flat = r.standard_normal((bsz, 1, seq, heads * hd), dtype=np.float32)
+    for flag in range(4):
+        src = flat if flag in (0, 3) else r.standard_normal((bsz, heads, seq, hd), dtype=np.float32)
+        init = r.standard_normal(flat.size).astype(np.float32)
+        ref = init.copy()
+        orc.call("orc_headify", orc.ptr(np.ascontiguousarray(src)), orc.ptr(ref), bsz, heads, seq, hd, flag)
+        gs, gd = B(hip, src), B(hip, init)
+        hip.call("mle_headify", None, gs.ptr, gd.ptr, bsz, heads, seq, hd, flag)
+        np.testing.assert_array_equal(gd.numpy(), ref)
+
+    xs = r.standard_normal((3, 17, 24), dtype=np.float32)
+    pe_r = np.zeros_like(xs)
+    orc.call("orc_matpe", orc.ptr(xs), orc.ptr(pe_r), 3, 17, 24, 0)
+    gxs, gpe = B(hip, xs), hip.Buffer.zeros(xs.shape)
+    hip.call("mle_matpe", None, gxs.ptr, gpe.ptr, 3, 17, 24, 0)
+    assert_close(gpe.numpy(), pe_r, what="matpe", rtol=1e-6, atol_scale=1e-7)
+    tp_r = np.zeros(256, np.float32)
+    orc.call("orc_pe", orc.ptr(tp_r), 517, 256)
+    gtp = hip.Buffer.zeros(256)
+    hip.call("mle_timestep_pe", None, gtp.ptr, 517, 256)
+    assert_close(gtp.numpy(), tp_r, what="timestep pe", rtol=1e-6, atol_scale=1e-7)
+
+    rows, cols = 37, 12
+    yb = r.standard_normal((rows, cols), dtype=np.float32)
+    bb = r.standard_normal(cols, dtype=np.float32)
+    ybr = yb.copy()
+    orc.call("orc_bcumadd", orc.ptr(ybr), orc.ptr(bb), rows, cols)
+    gyb, gbb = B(hip, yb), B(hip, bb)
+    hip.call("mle_bias_add_rows", None, gyb.ptr, gbb.ptr, rows, cols)
+    np.testing.assert_array_equal(gyb.numpy(), ybr)
+
+    cs_r = np.full(cols, 0.5, np.float32)
+    orc.call("orc_bcompress", orc.ptr(yb), orc.ptr(cs_r), rows, cols, 1.0)
+    gcs, gyb2 = B(hip, np.full(cols, 0.5, np.float32)), B(hip, yb)
+    hip.call("mle_colsum", None, gyb2.ptr, rows, cols, gcs.ptr, 1.0)
+    assert_close(gcs.numpy(), cs_r, what="colsum", **EW)
+
+    bt, ch, hw = 3, 16, 50
+    xc = r.standard_normal((bt, ch, hw), dtype=np.float32)
+    bc_ = r.standard_normal(ch, dtype=np.float32)
+    outc = np.zeros_like(xc)
+    orc.call("orc_broadcast_add", orc.ptr(xc), orc.ptr(bc_), orc.ptr(outc), bt, ch, hw)
+    gxc, gbc, goc = B(hip, xc), B(hip, bc_), hip.Buffer.zeros(xc.shape)
+    hip.call("mle_broadcast_channel_add", None, gxc.ptr, gbc.ptr, goc.ptr, bt, ch, hw)
+    np.testing.assert_array_equal(goc.numpy(), outc)
+    for nred in (ch, 7):
+        sq = np.full(ch, 0.25, np.float32)
+        orc.call("orc_channel_squeeze", orc.ptr(xc), orc.ptr(sq), bt, ch, hw, nred)
+        gsq = B(hip, np.full(ch, 0.25, np.float32))
+        hip.call("mle_channel_sum", None, gxc.ptr, bt, ch, hw, nred, gsq.ptr)
+        assert_close(gsq.numpy(), sq, what=f"channel_sum {nred}", **EW)
+
+    gf = hip.Buffer.zeros(1001)
+    hip.call("mle_fill", None, gf.ptr, 3.5, 1001)
+    np.testing.assert_array_equal(gf.numpy(), np.full(1001, 3.5, np.float32))
