@@ -1,0 +1,902 @@
+// Runtime, memory, NodeBackProp, AdamParameter, dispatch (GraphOperations
+// forward / backward / zero_grad / ParameterUpdate / accumulate / clipNorm),
+// Linear, Convolute2D and Embedding.  Reference: Engine/engine.cu:1-330,
+// 652-673, 3349-3606, 3723-3817; Engine/transformer.cu:176-245.
+#include "engine.h"
+
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <random>
+
+namespace mle {
+
+// ---------------------------------------------------------------------------
+// stream and errors
+static mle_stream g_stream = nullptr;
+static bool g_stream_made = false;
+
+void check(int rc, const str& what) {
+  if (rc != MLE_OK) {
+    std::cerr << what << ": " << mle_last_error() << std::endl;
+    std::exit(1);
+  }
+}
+
+mle_stream stream() {
+  if (!g_stream_made) {
+    check(mle_init(0), "mle_init");
+    check(mle_stream_create(&g_stream), "stream create");
+    g_stream_made = true;
+  }
+  return g_stream;
+}
+
+void set_stream(mle_stream s) {
+  g_stream = s;
+  g_stream_made = true;
+}
+
+void sync(const str& what) { check(mle_stream_sync(stream()), what); }
+
+// ---------------------------------------------------------------------------
+// chunked device arenas with exact-size reuse
+namespace {
+struct Arena {
+  std::vector<std::pair<char*, size_t>> chunks;  // base, capacity
+  size_t used = 0;                               // in the last chunk
+  std::multimap<size_t, char*> free_blocks;      // size -> block
+  size_t chunk_bytes = size_t(1) << 30;
+
+  char* take(size_t bytes) {
+    bytes = (bytes + 255) & ~size_t(255);
+    if (bytes == 0) bytes = 256;
+    auto it = free_blocks.find(bytes);
+    if (it != free_blocks.end()) {
+      char* p = it->second;
+      free_blocks.erase(it);
+      return p;
+    }
+    if (chunks.empty() || used + bytes > chunks.back().second) {
+      const size_t cap = std::max(chunk_bytes, bytes);
+      void* p = nullptr;
+      check(mle_device_alloc(&p, cap), "SafeCudaMalloc (arena chunk)");
+      chunks.push_back({static_cast<char*>(p), cap});
+      used = 0;
+    }
+    char* p = chunks.back().first + used;
+    used += bytes;
+    return p;
+  }
+  void give(char* p, size_t bytes) {
+    bytes = (bytes + 255) & ~size_t(255);
+    if (bytes == 0) bytes = 256;
+    free_blocks.insert({bytes, p});
+  }
+};
+Arena g_out, g_grad, g_scratch;
+std::mutex g_mem_mu;
+}  // namespace
+
+float* alloc_output(size_t n) {
+  std::lock_guard<std::mutex> lk(g_mem_mu);
+  return reinterpret_cast<float*>(g_out.take(n * sizeof(float)));
+}
+float* alloc_grad(size_t n) {
+  std::lock_guard<std::mutex> lk(g_mem_mu);
+  return reinterpret_cast<float*>(g_grad.take(n * sizeof(float)));
+}
+void release(float* p, size_t n, bool grad) {
+  if (!p) return;
+  std::lock_guard<std::mutex> lk(g_mem_mu);
+  (grad ? g_grad : g_out).give(reinterpret_cast<char*>(p), n * sizeof(float));
+}
+void* alloc_scratch(size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_mem_mu);
+  return g_scratch.take(bytes);
+}
+
+// ---------------------------------------------------------------------------
+// batched zeroing
+namespace {
+int g_zero_depth = 0;
+std::vector<std::pair<float*, size_t>> g_zero_ranges;
+}  // namespace
+
+void zero(float* p, size_t n) {
+  if (!p || n == 0) return;
+  if (g_zero_depth > 0) {
+    g_zero_ranges.push_back({p, n});
+    return;
+  }
+  check(mle_fill(stream(), p, 0.0f, n), "Zero_grad");
+}
+
+ZeroBatch::ZeroBatch() { ++g_zero_depth; }
+ZeroBatch::~ZeroBatch() {
+  if (--g_zero_depth > 0) return;
+  auto r = std::move(g_zero_ranges);
+  g_zero_ranges.clear();
+  std::sort(r.begin(), r.end());
+  // Every tensor starts on a 256-byte boundary and owns the padding up to the
+  // next one, so a range may be merged with the next when that one starts
+  // inside its padded extent; the padding cleared in between belongs to no
+  // other tensor.
+  auto padded_end = [](const std::pair<float*, size_t>& x) { return x.first + ((x.second + 63) & ~size_t(63)); };
+  size_t i = 0;
+  while (i < r.size()) {
+    float* b = r[i].first;
+    float* e = r[i].first + r[i].second;
+    float* ep = padded_end(r[i]);
+    size_t j = i + 1;
+    while (j < r.size() && r[j].first <= ep) {
+      e = std::max(e, r[j].first + r[j].second);
+      ep = std::max(ep, padded_end(r[j]));
+      ++j;
+    }
+    check(mle_fill(stream(), b, 0.0f, (size_t)(e - b)), "Zero_grad");
+    i = j;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// flat parameter arena
+namespace {
+struct Slab {
+  float* base;
+  size_t cap;
+  size_t used;
+};
+std::vector<Slab> g_slabs;
+size_t g_next_slab = size_t(64) << 20;
+uint64_t g_seed = 0;
+bool g_seed_set = false;
+}  // namespace
+
+void param_reserve(size_t floats) { g_next_slab = std::max<size_t>(floats, 64); }
+
+ParamSlot param_alloc(size_t n, float** p, float** g, float** m, float** v) {
+  const size_t need = (n + 63) & ~size_t(63);
+  if (g_slabs.empty() || g_slabs.back().used + need > g_slabs.back().cap) {
+    const size_t cap = std::max(g_next_slab, need);
+    void* base = nullptr;
+    check(mle_device_alloc(&base, cap * 4 * sizeof(float)), "SafeCudaMalloc (parameter arena)");
+    // Zero all four regions once: the padding between parameters must read as
+    // 0 when the optimizer and the norm sweep a contiguous span.
+    check(mle_fill(stream(), static_cast<float*>(base), 0.0f, cap * 4), "parameter arena clear");
+    g_slabs.push_back({static_cast<float*>(base), cap, 0});
+  }
+  Slab& s = g_slabs.back();
+  const size_t off = s.used;
+  s.used += need;
+  *p = s.base + off;
+  *g = s.base + s.cap + off;
+  *m = s.base + 2 * s.cap + off;
+  *v = s.base + 3 * s.cap + off;
+  return ParamSlot{(int)g_slabs.size() - 1, off};
+}
+
+void set_init_seed(uint64_t seed) {
+  g_seed = seed;
+  g_seed_set = true;
+}
+
+static uint64_t next_seed() {
+  if (g_seed_set) return g_seed++;
+  std::random_device rd;
+  return ((uint64_t)rd() << 32) | rd();
+}
+
+Quirks& quirks() {
+  static Quirks q;
+  return q;
+}
+
+}  // namespace mle
+
+using mle::check;
+
+// ---------------------------------------------------------------------------
+// NodeBackProp (Engine/engine.cu:45-124)
+NodeBackProp::NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation) : op_name(name) {
+  dim[0] = batch;
+  dim[1] = d1;
+  dim[2] = d2;
+  dim[3] = d3;
+  total = (long long)batch * d1 * d2 * d3;
+  if (allocation == 1) {
+    output = mle::alloc_output(total);
+    grad = mle::alloc_grad(total);
+    check(mle_fill(mle::stream(), grad, 0.0f, total), "Fill Kernel for Gradient");
+    owns_ = true;
+  }
+}
+
+void NodeBackProp::clear() {
+  if (owns_) {
+    mle::release(output, total, false);
+    mle::release(grad, total, true);
+    owns_ = false;
+  }
+  output = grad = nullptr;
+  inputs.clear();
+  op_name.clear();
+}
+
+static void reshape_check(NodeBackProp* n, const int* d, int size) {
+  if (size != 4) {
+    std::cerr << "Reshape only supports 4D tensors\n";
+    std::exit(1);
+  }
+  const long long nt = (long long)d[0] * d[1] * d[2] * d[3];
+  if (nt != n->total) {
+    std::cerr << "Reshape cannot change total size of tensor\n";
+    std::cout << "Dimensions for node: " << n->op_name << "\n";
+    std::exit(1);
+  }
+  for (int i = 0; i < 4; ++i) n->dim[i] = d[i];
+}
+void NodeBackProp::reshape(std::vector<int> nd) { reshape_check(this, nd.data(), (int)nd.size()); }
+void NodeBackProp::reshape(int arr[], const int size) { reshape_check(this, arr, size); }
+
+float ReadValueAt(const graph& X, const int& idx, const bool g) {
+  float out = 0.f;
+  check(mle_memcpy_d2h(&out, (g ? X->grad : X->output) + idx, sizeof(float), mle::stream()), "ReadValueAt");
+  return out;
+}
+
+void WriteValueAt(const graph& X, const float value, const int& idx, const bool g) {
+  check(mle_memcpy_h2d((g ? X->grad : X->output) + idx, &value, sizeof(float), mle::stream()), "WriteValueAt");
+}
+
+// ---------------------------------------------------------------------------
+// AdamParameter (Engine/engine.cu:126-302)
+AdamParameter::AdamParameter(str n, int out, int in, int row, int col, double norm)
+    : NodeBackProp(n, out, in, row, col, 0),
+      t(1),
+      b1(0.9f),
+      b2(0.999f),
+      epsilon(1e-8f),
+      batch_size(0),
+      group_norm((float)norm),
+      weight_decay(0.01f) {
+  slot = mle::param_alloc(total, &output, &grad, &m, &v);
+  // Standard_Weights: U(-1, 1) * sqrt(XAVIER / (in*row*col)) (Engine/kernels.cu:953-960),
+  // drawn on the host from a seeded engine (the reference draws curand Philox
+  // seeded from std::random_device).
+  std::mt19937_64 gen(mle::next_seed());
+  std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
+  const float scale = sqrtf(XAVIER / (float)((long long)in * row * col));
+  std::vector<float> host(total);
+  for (auto& x : host) x = dist(gen) * scale;
+  check(mle_memcpy_h2d(output, host.data(), total * sizeof(float), mle::stream()), "AdamParameter init");
+  check(mle_fill(mle::stream(), grad, 0.0f, total), "AdamParameter grad");
+  check(mle_fill(mle::stream(), m, 0.0f, total), "AdamParameter m");
+  check(mle_fill(mle::stream(), v, 0.0f, total), "AdamParameter v");
+}
+
+// File layout: [u32 name_len][name][i32 total][f32 W * total][f32 m * total][f32 v * total]
+// (Engine/engine.cu:139-184); `t` is not stored, as in the reference.
+void AdamParameter::save(std::ofstream& f) const {
+  const uint32_t name_len = (uint32_t)op_name.size();
+  f.write(reinterpret_cast<const char*>(&name_len), sizeof(uint32_t));
+  f.write(op_name.data(), name_len);
+  const int tot = (int)total;
+  f.write(reinterpret_cast<const char*>(&tot), sizeof(int));
+  if (!f) {
+    std::cerr << "File write failed saving parameter header: " << op_name << "\n";
+    std::exit(1);
+  }
+  std::vector<float> host(total);
+  const float* src[3] = {output, m, v};
+  for (int i = 0; i < 3; ++i) {
+    check(mle_memcpy_d2h(host.data(), src[i], total * sizeof(float), mle::stream()), "save " + op_name);
+    f.write(reinterpret_cast<const char*>(host.data()), total * sizeof(float));
+    if (!f) {
+      std::cerr << "File write failed saving " << op_name << "\n";
+      std::exit(1);
+    }
+  }
+}
+
+void AdamParameter::load(std::ifstream& f) {
+  uint32_t name_len = 0;
+  f.read(reinterpret_cast<char*>(&name_len), sizeof(uint32_t));
+  if (!f) {
+    std::cerr << "File read failed reading name length for: " << op_name << "\n";
+    std::exit(1);
+  }
+  std::string loaded(name_len, '\0');
+  f.read(&loaded[0], name_len);
+  if (!f) {
+    std::cerr << "File read failed reading name for: " << op_name << "\n";
+    std::exit(1);
+  }
+  if (loaded != op_name) {
+    std::cerr << "Parameter name mismatch: expected '" << op_name << "' but got '" << loaded << "'\n";
+    std::exit(1);
+  }
+  int tot = 0;
+  f.read(reinterpret_cast<char*>(&tot), sizeof(int));
+  if (!f) {
+    std::cerr << "File read failed reading size for: " << op_name << "\n";
+    std::exit(1);
+  }
+  if (tot != total) {
+    std::cerr << "Parameter size mismatch for '" << op_name << "': expected " << total << " but loaded " << tot << "\n";
+    std::exit(1);
+  }
+  std::vector<float> host(total);
+  float* dst[3] = {output, m, v};
+  for (int i = 0; i < 3; ++i) {
+    f.read(reinterpret_cast<char*>(host.data()), total * sizeof(float));
+    if (!f) {
+      std::cerr << "File read failed loading " << op_name << "\n";
+      std::exit(1);
+    }
+    check(mle_memcpy_h2d(dst[i], host.data(), total * sizeof(float), mle::stream()), "load " + op_name);
+  }
+}
+
+void AdamParameter::update(const float lr, const bool W) {
+  check(mle_adam_update(mle::stream(), output, grad, m, v, total, t, lr, b1, b2, epsilon, weight_decay, W ? 1 : 0,
+                        nullptr),
+        "AdamUpdate in AdamParameter update");
+  t++;
+}
+
+void AdamParameter::accumulate_grad(double* global_scale) {
+  const size_t ws_bytes = mle_sqnorm_ws_bytes(total);
+  static void* ws = nullptr;
+  static size_t ws_cap = 0;
+  if (ws_cap < ws_bytes) {
+    ws = mle::alloc_scratch(ws_bytes);
+    ws_cap = ws_bytes;
+  }
+  check(mle_grad_sqnorm(mle::stream(), grad, total, global_scale, nullptr, ws, ws_cap), "SumSquared of " + op_name);
+}
+
+void AdamParameter::gradnorm(const double* global_scale) {
+  check(mle_scale_by_device(mle::stream(), grad, global_scale, 1, total), "ScalePtr of " + op_name);
+}
+
+void AdamParameter::operator=(const AdamParameter& other) {
+  for (int i = 0; i < 4; ++i)
+    if (dim[i] != other.dim[i]) {
+      std::cout << "Shape Mismatch in equator operator of AdamParameter " << op_name << " and " << other.op_name;
+      std::exit(1);
+    }
+  check(mle_scale_write(mle::stream(), other.output, output, 1.0f, other.total), op_name + " = " + other.op_name);
+}
+
+// ---------------------------------------------------------------------------
+// small host helpers
+void Dimension(graph X) {
+  std::cout << "Dimensions for node: " << X->op_name << " ";
+  printf("(%i x %i x %i x %i) \n", X->dim[0], X->dim[1], X->dim[2], X->dim[3]);
+}
+void Dimension(AdamParameter X) {
+  std::cout << "Dimensions for node: " << X.op_name << " ";
+  printf("(%i x %i x %i x %i) \n", X.dim[0], X.dim[1], X.dim[2], X.dim[3]);
+}
+void Zerograd(AdamParameter& X) { mle::zero(X.grad, X.total); }
+void Zerograd(graph X) { mle::zero(X->grad, X->total); }
+
+static void print_head(const graph& X, int type, int rows_max, int cols_max) {
+  const int ch = X->dim[1], rows = X->dim[2], cols = X->dim[3];
+  const long long n = std::min<long long>(X->total, (long long)ch * rows * cols);
+  std::vector<float> cpu(n);
+  check(mle_memcpy_d2h(cpu.data(), type ? X->grad : X->output, n * sizeof(float), mle::stream()), "print");
+  std::cout << "Printing dimensions for node " << X->op_name << (type ? "->grad \n" : "->output \n");
+  for (int c = 0; c < std::min(3, ch); ++c) {
+    std::cout << "Channel " << c << ":\n";
+    for (int r = 0; r < std::min(rows_max, rows); ++r) {
+      for (int k = 0; k < std::min(cols_max, cols); ++k) std::cout << cpu[(long long)c * rows * cols + r * cols + k] << "\t";
+      std::cout << "\n";
+    }
+    std::cout << "------------------------------\n";
+  }
+}
+void printGPU(const graph X, const int type) { print_head(X, type, X->dim[2], X->dim[3]); }
+void printHeadGPU(const graph X, const int type) { print_head(X, type, 5, 5); }
+
+int ArgMaxToCPU(const graph& input) {
+  static int32_t* d = nullptr;
+  if (!d) d = static_cast<int32_t*>(mle::alloc_scratch(256));
+  check(mle_argmax(mle::stream(), input->output, 1, (int)input->total, d), "ArgMax");
+  int32_t out = 0;
+  check(mle_memcpy_d2h(&out, d, sizeof(int32_t), mle::stream()), "ArgMax readback");
+  return out;
+}
+
+// topological_sort (Engine/engine.cu:652-673): DFS post-order from the root.
+graph_tree topological_sort(const graph& root) {
+  std::unordered_set<NodeBackProp*> visited;
+  graph_tree result;
+  std::function<void(const graph&)> dfs = [&](const graph& node) {
+    if (!node || visited.count(node.get())) return;
+    visited.insert(node.get());
+    for (const auto& in : node->inputs) dfs(in);
+    result.push_back(node);
+  };
+  dfs(root);
+  return result;
+}
+
+// ---------------------------------------------------------------------------
+// GraphOperations dispatch (Engine/engine.cu:3362-3503)
+double GraphOperations::GB = 0.0;
+bool GraphOperations::calculate_loss = false;
+float GraphOperations::loss = 0.0f;
+
+namespace {
+// Parameters reached from `nodes`, in hook order.
+std::vector<AdamParameter*> collect_params(const graph_tree& nodes, bool& duplicates) {
+  std::vector<AdamParameter*> ps;
+  std::unordered_set<AdamParameter*> seen;
+  duplicates = false;
+  for (auto& n : nodes)
+    for (auto* p : n->params) {
+      if (!seen.insert(p).second) duplicates = true;
+      ps.push_back(p);
+    }
+  return ps;
+}
+
+struct Span {
+  float *p, *g, *m, *v;
+  size_t n;
+};
+
+// Maximal runs of parameters that are contiguous in one slab.
+std::vector<Span> contiguous_spans(std::vector<AdamParameter*> ps) {
+  std::sort(ps.begin(), ps.end(), [](AdamParameter* a, AdamParameter* b) {
+    return a->slot.slab != b->slot.slab ? a->slot.slab < b->slot.slab : a->slot.offset < b->slot.offset;
+  });
+  std::vector<Span> out;
+  for (size_t i = 0; i < ps.size();) {
+    AdamParameter* a = ps[i];
+    size_t end = a->slot.offset + (((size_t)a->total + 63) & ~size_t(63));
+    size_t j = i + 1;
+    while (j < ps.size() && ps[j]->slot.slab == a->slot.slab && ps[j]->slot.offset == end) {
+      end = ps[j]->slot.offset + (((size_t)ps[j]->total + 63) & ~size_t(63));
+      ++j;
+    }
+    // The padding between parameters belongs to no tensor: grads there stay 0.
+    const size_t n = end - a->slot.offset;
+    out.push_back({a->output, a->grad, a->m, a->v, n});
+    i = j;
+  }
+  return out;
+}
+
+void* span_ws(size_t bytes) {
+  static void* ws = nullptr;
+  static size_t cap = 0;
+  if (cap < bytes) {
+    ws = mle::alloc_scratch(bytes);
+    cap = bytes;
+  }
+  return ws;
+}
+}  // namespace
+
+void GraphOperations::clipNorm(double* global_scale) {
+  // Deferred: ParameterUpdate reads g / s inside the update pass.  Anything
+  // else that consumes the gradients first applies the division in place.
+  flush_clip();
+  pending_clip_ = global_scale;
+}
+
+void GraphOperations::flush_clip() {
+  if (!pending_clip_) return;
+  const double* s = pending_clip_;
+  pending_clip_ = nullptr;
+  for (auto& node : nodes)
+    if (node->clipnorm) node->clipnorm(s);
+}
+
+void GraphOperations::accumulate(double* global_scale) {
+  flush_clip();
+  bool dup = false;
+  auto ps = collect_params(nodes, dup);
+  bool all_hooks_known = true;
+  for (auto& n : nodes)
+    if (n->accumulate && n->params.empty()) all_hooks_known = false;
+  if (!all_hooks_known || dup) {
+    for (auto& node : nodes)
+      if (node->accumulate) node->accumulate(global_scale);
+  } else {
+    for (auto& sp : contiguous_spans(ps)) {
+      const size_t ws = mle_sqnorm_ws_bytes(sp.n);
+      check(mle_grad_sqnorm(mle::stream(), sp.g, sp.n, global_scale, nullptr, span_ws(ws), ws), "SumSquared");
+    }
+  }
+  check(mle_sqrt_scale(mle::stream(), global_scale, 1.0), "Sqrt_Scale");
+}
+
+void GraphOperations::ParameterUpdate(const graph& X, const bool show, const float lr, const bool adamw) {
+  if (X) nodes = topological_sort(X);
+  if (nodes.empty()) {
+    printf("Warning... Nodes list is empty and parameter update cannot run.. \n");
+    return;
+  }
+  bool dup = false;
+  auto ps = collect_params(nodes, dup);
+  bool fusable = !dup && !ps.empty();
+  for (auto& n : nodes)
+    if (n->updateParams && n->params.empty()) fusable = false;
+  for (auto* p : ps)
+    if (p->t != ps[0]->t || p->b1 != ps[0]->b1 || p->b2 != ps[0]->b2 || p->epsilon != ps[0]->epsilon ||
+        p->weight_decay != ps[0]->weight_decay)
+      fusable = false;
+  if (fusable) {
+    AdamParameter* p0 = ps[0];
+    for (auto& sp : contiguous_spans(ps))
+      check(mle_adam_update(mle::stream(), sp.p, sp.g, sp.m, sp.v, sp.n, p0->t, lr, p0->b1, p0->b2, p0->epsilon,
+                            p0->weight_decay, adamw ? 1 : 0, pending_clip_),
+            "AdamUpdate (fused over the parameter arena)");
+    for (auto* p : ps) p->t++;
+    pending_clip_ = nullptr;
+  } else {
+    flush_clip();
+    for (auto& node : nodes)
+      if (node->updateParams) node->updateParams(lr, adamw);
+  }
+  if (show)
+    for (auto& node : nodes)
+      if (node->updateParams) printHeadGPU(node, 1);
+}
+
+static void nan_check(const graph& node, int type) {
+  static double* acc = nullptr;
+  static int* flag = nullptr;
+  static void* ws = nullptr;
+  static size_t wcap = 0;
+  if (!acc) {
+    acc = static_cast<double*>(mle::alloc_scratch(256));
+    flag = static_cast<int*>(mle::alloc_scratch(256));
+  }
+  const float* p = type ? node->grad : node->output;
+  if (!p) return;
+  const size_t need = mle_sqnorm_ws_bytes(node->total);
+  if (wcap < need) {
+    ws = mle::alloc_scratch(need);
+    wcap = need;
+  }
+  const int zero = 0;
+  const double dz = 0.0;
+  check(mle_memcpy_h2d(flag, &zero, sizeof(int), mle::stream()), "isNan");
+  check(mle_memcpy_h2d(acc, &dz, sizeof(double), mle::stream()), "isNan");
+  check(mle_grad_sqnorm(mle::stream(), p, node->total, acc, flag, ws, wcap), "isNan");
+  int bad = 0;
+  check(mle_memcpy_d2h(&bad, flag, sizeof(int), mle::stream()), "isNan");
+  if (bad) {
+    std::cerr << "IsNan of " << node->op_name << ": non-finite value\n";
+    std::exit(1);
+  }
+}
+
+void GraphOperations::forward(const graph& X, const bool calc_loss, const bool show, const bool time,
+                              const bool check_nan) {
+  if (X) nodes = topological_sort(X);
+  if (calc_loss) calculate_loss = true;
+  if (nodes.empty()) {
+    printf("Warning... Nodes list is empty and forward cannot run.. \n");
+    return;
+  }
+  for (auto& node : nodes) {
+    std::chrono::high_resolution_clock::time_point t0;
+    if (time) {
+      mle::sync("Before " + node->op_name + " forward");
+      t0 = std::chrono::high_resolution_clock::now();
+    }
+    if (node->forward) {
+      node->forward();
+      node->forward_called = true;
+      if (check_nan) nan_check(node, 0);
+      if (show) {
+        Dimension(node);
+        printHeadGPU(node);
+      }
+    }
+    if (time) {
+      mle::sync("After " + node->op_name + " forward");
+      const double ms =
+          std::chrono::duration<double, std::milli>(std::chrono::high_resolution_clock::now() - t0).count();
+      std::cout << "Time elapsed for " << node->op_name << " forward: " << ms << "ms \n";
+    }
+  }
+  calculate_loss = false;
+}
+
+void GraphOperations::backward(const graph& X, const bool show, const bool time, const bool check_nan) {
+  if (X) nodes = topological_sort(X);
+  if (nodes.empty()) {
+    printf("Warning... Nodes list is empty and bacward cannot run.. \n");
+    return;
+  }
+  flush_clip();
+  for (auto it = nodes.rbegin(); it != nodes.rend(); ++it) {
+    std::chrono::high_resolution_clock::time_point t0;
+    if (time) {
+      mle::sync("Previous");
+      t0 = std::chrono::high_resolution_clock::now();
+    }
+    if ((*it)->backward) {
+      (*it)->backward();
+      if (check_nan) nan_check(*it, 1);
+      if (show) printHeadGPU(*it, 1);
+    }
+    if (time) {
+      mle::sync("After " + (*it)->op_name + " backward");
+      const double ms =
+          std::chrono::duration<double, std::milli>(std::chrono::high_resolution_clock::now() - t0).count();
+      std::cout << "Time elapsed for " << (*it)->op_name << " backward: " << ms << "ms \n";
+    }
+  }
+}
+
+void GraphOperations::zero_grad(const graph& X, const bool show) {
+  if (X) nodes = topological_sort(X);
+  if (nodes.empty()) {
+    printf("Warning... Nodes list is empty and Zero grad cannot run.. \n");
+    return;
+  }
+  pending_clip_ = nullptr;  // the clipped gradients are being cleared anyway
+  mle::ZeroBatch batch;
+  for (auto it = nodes.rbegin(); it != nodes.rend(); ++it) {
+    if ((*it)->zero_grad) {
+      if (show) std::cout << "Zeroing gradient of" + (*it)->op_name + "\n";
+      (*it)->zero_grad();
+    }
+  }
+}
+
+void GraphOperations::printNodes(const graph& X, const int show) {
+  if (X) nodes = topological_sort(X);
+  for (auto& node : nodes)
+    if (node->zero_grad) {
+      std::cout << "Calling Node: " << node->op_name << "\n";
+      Dimension(node);
+      if (show == 1) printHeadGPU(node);
+      if (show == 2) printHeadGPU(node, 1);
+    }
+}
+
+void GraphOperations::printParams(const graph& X, const bool show) {
+  if (X) nodes = topological_sort(X);
+  for (auto& node : nodes)
+    if (node->printparams) node->printparams(show);
+}
+
+void GraphOperations::clear_graph(const graph& X, const bool show) {
+  if (X) nodes = topological_sort(X);
+  mle::sync("clear_graph");
+  for (auto& node : nodes)
+    if (node->free) {
+      if (show) std::cout << "Freeing Node: " << node->op_name << "\n";
+      node->free();
+    }
+  nodes.clear();
+}
+
+void GraphOperations::clean_clear_graph(const graph& X, const bool show) {
+  if (X) nodes = topological_sort(X);
+  mle::sync("clean_clear_graph");
+  for (auto& node : nodes) {
+    if (node->free) {
+      if (show) std::cout << "Freeing Node: " << node->op_name << "\n";
+      node->free();
+    }
+    if (node->serious_free) {
+      if (show) std::cout << "Deleting Parameters for Node: " << node->op_name << "\n";
+      node->serious_free();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Linear (Engine/engine.cu:3505-3606).  W1 [1,1,in,out], B1 [1,1,1,out].  The
+// batch and channel dimensions are folded into the GEMM's rows (the weight is
+// broadcast, flags 3/0/3), so dW = X^T dY is one K = B*C*m contraction with
+// the bias gradient fused into it.
+Linear::Linear(const int input, const int output, const str name, const bool bias)
+    : in(input), out(output), bias(bias), W1(name + " W1", 1, 1, input, output), B1(name + " B1", 1, 1, 1, output) {
+  if (name != "") op_name = name;
+}
+void Linear::save(std::ofstream& f) const {
+  W1.save(f);
+  if (bias) B1.save(f);
+}
+void Linear::load(std::ifstream& f) {
+  W1.load(f);
+  if (bias) B1.load(f);
+}
+void Linear::operator=(const Linear& other) {
+  W1 = other.W1;
+  if (bias) B1 = other.B1;
+}
+
+graph Linear::forward(const graph& X) {
+  if (X->dim[3] != W1.dim[2]) {
+    std::cout << "Shape Mismatch in Linear Layer of " << X->op_name << ": \n";
+    std::cout << "Dimensions are input " << X->op_name << "and " << op_name << ":  (" << X->dim[2] << "," << X->dim[3]
+              << ") and (" << W1.dim[2] << "," << W1.dim[3] << ") \n";
+    std::exit(1);
+  }
+  const int batch = X->dim[0], channels = X->dim[1], m = X->dim[2], n = X->dim[3], p = out;
+  auto node = std::make_shared<NodeBackProp>(op_name, batch, channels, m, p, 1);
+  node->inputs = {X};
+  GraphOperations::GB += (double)node->total * sizeof(float) / (1ULL << 30);
+  const long long rows = (long long)batch * channels * m;
+  AdamParameter* W = &W1;
+  AdamParameter* Bb = &B1;
+  const bool has_bias = bias;
+  NodeBackProp* nd = node.get();
+  NodeBackProp* x = X.get();
+  const str name = op_name;
+  node->params = has_bias ? std::vector<AdamParameter*>{W, Bb} : std::vector<AdamParameter*>{W};
+  node->forward = [=]() {
+    check(mle_gemm(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, 0, W->output, p, 0, 0.0f, nd->output, p, 0,
+                   1, nullptr),
+          "MatMul... X*W1 in " + name + " forward");
+    if (has_bias) check(mle_bias_add_rows(mle::stream(), nd->output, Bb->output, rows, p), "BCumAdd in " + name);
+  };
+  node->backward = [=]() {
+    check(mle_gemm(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, 0, W->output, p, 0, 1.0f, x->grad, n, 0, 1,
+                   nullptr),
+          "MatMul... dZ*W^T in " + name + " backward");
+    check(mle_gemm(mle::stream(), 1, 0, n, p, (int)rows, 1.0f, x->output, n, 0, nd->grad, p, 0, 1.0f, W->grad, p, 0, 1,
+                   has_bias ? Bb->grad : nullptr),
+          "MatMul... X^T*dZ in " + name + " backward");
+  };
+  node->free = [=]() { nd->clear(); };
+  node->serious_free = [=]() {};
+  node->zero_grad = [=]() {
+    mle::zero(nd->grad, nd->total);
+    mle::zero(W->grad, W->total);
+    if (has_bias) mle::zero(Bb->grad, Bb->total);
+  };
+  node->accumulate = [=](double* s) {
+    W->accumulate_grad(s);
+    if (has_bias) Bb->accumulate_grad(s);
+  };
+  node->clipnorm = [=](const double* s) {
+    W->gradnorm(s);
+    if (has_bias) Bb->gradnorm(s);
+  };
+  node->updateParams = [=](const float lr, const bool adamw) {
+    W->update(lr, adamw);
+    if (has_bias) Bb->update(lr, adamw);
+  };
+  node->printparams = [=](const bool) {};
+  return node;
+}
+
+// ---------------------------------------------------------------------------
+// Convolute2D (Engine/engine.cu:3723-3817).  W1 [out, inp, c, d], B1 [1, out, 1, 1].
+Convolute2D::Convolute2D(int Input, int Output, int C, int D, int stride_, int padding, str param)
+    : inp(Input),
+      out(Output),
+      c(C),
+      d(D),
+      pad(padding),
+      stride(stride_),
+      name(param),
+      W1(param + " Weight ", Output, Input, C, D),
+      B1(param + " Bias ", 1, Output, 1, 1) {}
+void Convolute2D::save(std::ofstream& f) const {
+  W1.save(f);
+  B1.save(f);
+}
+void Convolute2D::load(std::ifstream& f) {
+  W1.load(f);
+  B1.load(f);
+}
+
+graph Convolute2D::forward(const graph& X) {
+  if (X->dim[1] != inp) {
+    std::cout << "Dimension Mismatch! in " << name << ": \n";
+    Dimension(X);
+    std::exit(1);
+  }
+  const int batch = X->dim[0], a = X->dim[2], b = X->dim[3];
+  const int outR = (2 * pad + a - c) / stride + 1, outC = (2 * pad + b - d) / stride + 1;
+  auto node = std::make_shared<NodeBackProp>(name, batch, out, outR, outC, 1);
+  node->inputs = {X};
+  GraphOperations::GB += (double)node->total * sizeof(float) / (1ULL << 30);
+  const size_t ws_bytes = mle_conv2d_wgrad_ws_bytes(batch, inp, a, b, out, c, d, pad, stride);
+  void* ws = mle::alloc_scratch(ws_bytes);
+  AdamParameter* W = &W1;
+  AdamParameter* Bb = &B1;
+  NodeBackProp* nd = node.get();
+  NodeBackProp* x = X.get();
+  const int inp_ = inp, out_ = out, c_ = c, d_ = d, pad_ = pad, st = stride;
+  const str nm = name;
+  node->params = {W, Bb};
+  node->forward = [=]() {
+    check(mle_conv2d_fwd(mle::stream(), x->output, W->output, Bb->output, nd->output, batch, inp_, a, b, out_, c_, d_,
+                         pad_, st),
+          "Forward Convolution in " + nm);
+  };
+  node->backward = [=]() {
+    check(mle_conv2d_wgrad(mle::stream(), x->output, nd->grad, W->grad, batch, inp_, a, b, out_, c_, d_, pad_, st, ws,
+                           ws_bytes),
+          "Weight Gradient in " + nm);
+    check(mle_channel_sum(mle::stream(), nd->grad, batch, out_, (size_t)outR * outC, out_, Bb->grad),
+          "Bias Gradient in " + nm);
+    check(mle_conv2d_dgrad(mle::stream(), nd->grad, W->output, x->grad, batch, inp_, a, b, out_, c_, d_, pad_, st),
+          "Input Gradient in " + nm);
+  };
+  node->zero_grad = [=]() {
+    mle::zero(nd->grad, nd->total);
+    mle::zero(W->grad, W->total);
+    mle::zero(Bb->grad, Bb->total);
+  };
+  node->free = [=]() { nd->clear(); };
+  node->serious_free = [=]() {};
+  node->accumulate = [=](double* s) {
+    W->accumulate_grad(s);
+    Bb->accumulate_grad(s);
+  };
+  node->clipnorm = [=](const double* s) {
+    W->gradnorm(s);
+    Bb->gradnorm(s);
+  };
+  node->updateParams = [=](const float lr, const bool adamw) {
+    W->update(lr, adamw);
+    Bb->update(lr, adamw);
+  };
+  node->printparams = [=](const bool) {};
+  return node;
+}
+
+// ---------------------------------------------------------------------------
+// Embedding
+Embedding::Embedding(int vocab_, int dim_, const str name) : vocab(vocab_), dim(dim_), E(name, 1, 1, vocab_, dim_) {}
+void Embedding::save(std::ofstream& f) const { E.save(f); }
+void Embedding::load(std::ifstream& f) { E.load(f); }
+
+graph Embedding::forward(const int32_t* keys, int batch, int clen, int max_clen) {
+  auto node = std::make_shared<NodeBackProp>(E.op_name + " lookup", batch, 1, clen, dim, 1);
+  keys_ = keys;
+  batch_ = batch;
+  clen_ = clen;
+  max_clen_ = max_clen;
+  ws_bytes_ = mle_embed_scatter_ws_bytes(batch, clen);
+  ws_ = mle::alloc_scratch(ws_bytes_);
+  AdamParameter* T = &E;
+  NodeBackProp* nd = node.get();
+  const int V = vocab, D = dim;
+  void* ws = ws_;
+  const size_t wsb = ws_bytes_;
+  node->params = {T};
+  node->forward = [=]() {
+    check(mle_embed_gather(mle::stream(), nd->output, T->output, keys, batch, clen, max_clen, D), "GatherEmbeddings");
+  };
+  node->backward = [=]() {
+    check(mle_embed_scatter_add(mle::stream(), T->grad, nd->grad, keys, batch, clen, max_clen, D, V, 1.0f, ws, wsb),
+          "Embedding gradient");
+  };
+  node->zero_grad = [=]() {
+    mle::zero(nd->grad, nd->total);
+    mle::zero(T->grad, T->total);
+  };
+  node->free = [=]() { nd->clear(); };
+  node->accumulate = [=](double* s) { T->accumulate_grad(s); };
+  node->clipnorm = [=](const double* s) { T->gradnorm(s); };
+  node->updateParams = [=](const float lr, const bool adamw) { T->update(lr, adamw); };
+  return node;
+}
+
+void Embedding::UpdateSGD(const graph& X, float lr) {
+  check(mle_embed_scatter_add(mle::stream(), E.output, X->grad, keys_, batch_, clen_, max_clen_, dim, vocab, -lr, ws_,
+                              ws_bytes_),
+        "Key Update in Embedding Space update");
+}

@@ -1,0 +1,263 @@
+// GraphOperations / NodeBackProp / AdamParameter -- the ML_Engine C++ surface
+// (Includes/engine.h:33-255), kept source-compatible for the ops on the
+// training hot path, with every kernel launch going through the C ABI of
+// include/mle_hip.h on one HIP stream.
+//
+// What changes underneath (the API does not):
+//  * Memory: node outputs and gradients come from two chunked device arenas
+//    (one for outputs, one for gradients, so a graph's gradients are contiguous
+//    and zero_grad merges into a few fills); parameters live in a flat
+//    parameter arena whose slabs hold [params | grads | m | v] contiguously, so
+//    the optimizer, the global norm and the clip run as one pass over a span.
+//  * Dispatch: forward / backward enqueue the nodes' lambdas in topological
+//    order on one stream with no host synchronisation, except where the
+//    reference reads a value back (loss of a `last` node).
+//  * accumulate() and clipNorm() are public (the reference declares them
+//    private and never calls them, Includes/engine.h:112-113).
+#pragma once
+#include <stdint.h>
+#include <fstream>
+#include <functional>
+#include <iostream>
+#include <memory>
+#include <string>
+#include <unordered_set>
+#include <vector>
+
+#include "mle_hip.h"
+
+using str = std::string;
+
+// Includes/debugging_utils.h:10-14 and Includes/kernels.h:7-8
+static constexpr float XAVIER = 6.0f;
+static constexpr bool ADAMW = true;
+static constexpr float NORM = 1.0f;
+static constexpr float LEARNING_RATE = 1e-4f;
+static constexpr bool SHOULDNORM = false;
+static constexpr int BLOCK_SIZE = 32;
+static constexpr int THREADSPERBLOCK = 512;
+
+struct NodeBackProp;
+struct AdamParameter;
+using graph = std::shared_ptr<NodeBackProp>;
+using graph_tree = std::vector<graph>;
+using graphFn = std::function<graph(graph)>;
+
+namespace mle {
+
+// The stream every engine kernel is enqueued on (created on first use).
+mle_stream stream();
+void set_stream(mle_stream s);
+// Abort with the library's message, as CheckError / SafeCudaMalloc do
+// (Engine/debug.cu:15-25, Includes/debugging_utils.h:98-110).
+void check(int rc, const str& what);
+void sync(const str& what = "sync");
+
+// Device allocation for node tensors.  Released blocks are reused by later
+// allocations of the same size (graphs rebuilt with the same shapes).
+float* alloc_output(size_t n);
+float* alloc_grad(size_t n);
+void release(float* p, size_t n, bool grad);
+// Scratch owned by a node (workspaces, statistics).
+void* alloc_scratch(size_t bytes);
+
+// Zero a gradient range.  Inside a ZeroBatch scope the range is recorded and
+// merged with its neighbours instead of launching one fill per node.
+void zero(float* p, size_t n);
+struct ZeroBatch {
+  ZeroBatch();
+  ~ZeroBatch();
+};
+
+// Flat parameter arena.  reserve(n) sizes the next slab (default 64 Mi floats).
+struct ParamSlot {
+  int slab;
+  size_t offset;
+};
+void param_reserve(size_t floats);
+ParamSlot param_alloc(size_t n, float** p, float** g, float** m, float** v);
+
+// Seed for parameter initialisation (the reference seeds from std::random_device).
+void set_init_seed(uint64_t seed);
+
+// Reference behaviours that are bugs, reproduced by default for parity:
+//  bmmabt_reference_grad: BMMABT's B gradient is bcmmT(A, dZ) written into B's
+//    buffer (Engine/engine.cu:2307), not dZ^T A.
+//  broadcast_channel_reference_grad: Broadcast_Channel reduces only the first
+//    `width` channels of B's gradient (Channel_Squeeze1D<<<b, ...>>>,
+//    Engine/engine.cu:1435).
+struct Quirks {
+  bool bmmabt_reference_grad = true;
+  bool broadcast_channel_reference_grad = true;
+};
+Quirks& quirks();
+
+}  // namespace mle
+
+struct NodeBackProp {
+  str op_name;
+  graph_tree inputs;
+  float* output = nullptr;
+  float* grad = nullptr;
+  int dim[4];
+  long long total;
+  bool forward_called = false;
+  std::function<void()> forward;
+  std::function<void()> backward;
+  std::function<void()> free;
+  std::function<void()> zero_grad;
+  std::function<void()> serious_free;
+  std::function<void(const float lr, const bool adamw)> updateParams;
+  std::function<void(const double*)> clipnorm;
+  std::function<void(double*)> accumulate;
+  std::function<void(const bool full)> printparams;
+  // Parameters whose hooks this node carries (additive: lets GraphOperations
+  // fuse the optimizer, norm and clip over the flat parameter arena).
+  std::vector<AdamParameter*> params;
+  virtual void update(const float lr = LEARNING_RATE, const bool W = ADAMW) {}
+  NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation);
+  virtual ~NodeBackProp() = default;
+  void clear();
+  void reshape(std::vector<int> new_dims);
+  void reshape(int arr[], const int size = 4);
+
+ private:
+  bool owns_ = false;
+};
+
+float ReadValueAt(const graph& X, const int& idx, const bool flag = false);
+void WriteValueAt(const graph& X, const float value, const int& idx, const bool flag = false);
+
+struct AdamParameter : public NodeBackProp {
+  float *m, *v;
+  int t;
+  float b1, b2, epsilon;
+  int batch_size;
+  float group_norm;
+  float weight_decay;
+  mle::ParamSlot slot;
+
+  AdamParameter(str n, int out, int in, int row, int col, double norm = NORM);
+  void save(std::ofstream& f) const;
+  void load(std::ifstream& f);
+  void update(const float lr = LEARNING_RATE, const bool W = ADAMW) override;
+  void accumulate_grad(double* global_scale);
+  void gradnorm(const double* global_scale);
+  void operator=(const AdamParameter& other);
+};
+
+void Dimension(graph X);
+void Dimension(AdamParameter X);
+void Zerograd(AdamParameter& X);
+void Zerograd(graph X);
+void printGPU(const graph X, const int type = 0);
+void printHeadGPU(const graph X, const int type = 0);
+int ArgMaxToCPU(const graph& input);
+graph_tree topological_sort(const graph& root);
+
+class GraphOperations {
+ private:
+  static bool calculate_loss;
+  const double* pending_clip_ = nullptr;
+  void flush_clip();
+
+ public:
+  graph_tree nodes;
+
+  static double GB;
+  static float loss;
+
+  // Public here; the reference declares both private and never calls them.
+  void clipNorm(double* global_scale);
+  void accumulate(double* global_scale);
+
+  void ParameterUpdate(const graph& X = nullptr, const bool show = false, const float lr = LEARNING_RATE,
+                       const bool adamw = ADAMW);
+  void forward(const graph& X = nullptr, const bool calc_loss = false, const bool show = false, const bool time = false,
+               const bool check_nan = false);
+  void backward(const graph& X = nullptr, const bool show = false, const bool time = false,
+                const bool check_nan = false);
+  void zero_grad(const graph& X = nullptr, const bool show = false);
+  void printParams(const graph& X = nullptr, const bool show = false);
+  void printNodes(const graph& X = nullptr, const int show = 0);
+  void clear_graph(const graph& X = nullptr, const bool show = false);
+  void clean_clear_graph(const graph& X = nullptr, const bool show = false);
+
+  static graph Copy(const graph& X);
+  static graph track(const graph_tree& X);
+  static graph identity(const graph& X);
+  static graph like(const graph& X, const str name = "");
+  static graph HeadifytoChannel(const graph& X, const int new_channels);
+  static graph DeHeadify(const graph& X);
+  static graph PositionalEncoding(const int& t, const int d_model);
+  static graph MatrixPositionalEncoding(const graph& X, const int start_idx = 0);
+  static graph Broadcast_Channel(const graph& A, const graph& B);
+  static graph Scale(const graph& input, const float scale, const bool last = false);
+  static graph Add(const graph& A, const graph& B, const bool last = false);
+  static graph MeanSquaredError(const graph& prediction, const graph& target, const bool last);
+  static graph SoftMaxCrossEntropy(const graph& prediction, const graph& target, const bool last);
+  static graph BMM(const graph& A, const graph& B);     // m x n * n x p = m x p
+  static graph BMMABT(const graph& A, const graph& B);  // m x n * p x n = m x p
+  static graph SOFTMAX(const graph& X, const int type = 0);
+  static graph SOFTMASK(const graph& X, const int type = 0);
+  static graph RELU(const graph& input);
+  static graph SILU(const graph& input);
+  static graph TANH(const graph& input);
+  static graph GELU(const graph& input);
+  static graph SIGMOID(const graph& input);
+  static graph LeakyRELU(const graph& input);
+  static graph LayerNorm(const graph& X);
+  static graph GroupNorm(const graph& X, const int group = 8);
+  // Token-id inputs (TextualEmbedding::forward key "T", Engine/transformer.cu:190-196).
+  static graph OneHot(const int32_t* keys, int batch, int clen, int max_clen, int vocab);
+};
+
+inline graph operator+(const graph& A, const graph& B) { return GraphOperations::Add(A, B); }
+
+class Linear {
+ private:
+  int in, out;
+  const bool bias;
+
+ public:
+  AdamParameter W1;
+  AdamParameter B1;
+  str op_name = "Linear Layer";
+  Linear(const int input, const int output, const str name = "", const bool bias = true);
+  graph forward(const graph& X);
+  void save(std::ofstream& f) const;
+  void load(std::ifstream& f);
+  void operator=(const Linear& other);
+};
+
+class Convolute2D {
+ public:
+  int inp, out, c, d, pad, stride;
+  str name;
+  AdamParameter W1, B1;
+  Convolute2D(int Input, int Output, int C = 3, int D = 3, int stride = 1, int padding = 1, str param = "");
+  void save(std::ofstream& f) const;
+  void load(std::ifstream& f);
+  graph forward(const graph& X);
+};
+
+// Token embedding table as an AdamParameter: GatherEmbeddings forward
+// (Engine/transformer.cu:176-205) and a deterministic scatter-add backward into
+// the table gradient.  UpdateSGD applies the reference's KeyUpdate step
+// (Engine/transformer.cu:236-245) without its race.
+class Embedding {
+ public:
+  int vocab, dim;
+  AdamParameter E;
+  Embedding(int vocab, int dim, const str name = "Embedding");
+  graph forward(const int32_t* keys, int batch, int clen, int max_clen);
+  void UpdateSGD(const graph& X, float lr = LEARNING_RATE);
+  void save(std::ofstream& f) const;
+  void load(std::ifstream& f);
+
+ private:
+  const int32_t* keys_ = nullptr;
+  int batch_ = 0, clen_ = 0, max_clen_ = 0;
+  void* ws_ = nullptr;
+  size_t ws_bytes_ = 0;
+};

@@ -1,0 +1,223 @@
+// Model harness: builds the benchmark configurations with the GraphOperations
+// API and exposes them through a small C interface for the tests and bench.py.
+// It drives the engine exactly as a reference application does
+// (use_cases/mnist.cu:284-293: zero_grad, forward(calc_loss), backward,
+// ParameterUpdate) and adds host access to parameters and gradients.
+#include <string.h>
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "engine.h"
+#include "mle_models.h"
+#include "modules.h"
+
+using mle::check;
+
+namespace {
+
+struct Model {
+  int kind = 0;
+  GraphOperations go;
+  graph root;
+  std::vector<AdamParameter*> params;
+  std::vector<std::pair<void*, size_t>> inputs;  // device buffers by slot
+  std::vector<graph> keep;                       // nodes whose outputs are inputs
+  // owned modules
+  std::unique_ptr<Linear> l1, l2, ffn1, ffn2, lm;
+  std::unique_ptr<MultiHeadAttention> mha;
+  std::unique_ptr<Embedding> emb;
+  std::unique_ptr<ResidualBlock> rb;
+  std::vector<std::unique_ptr<AdamParameter>> loose;  // C2 parameters
+  double* clip_scale = nullptr;
+  bool adamw = true;
+};
+
+void* input_buffer(Model* m, size_t bytes) {
+  void* p = mle::alloc_scratch(bytes);
+  m->inputs.push_back({p, bytes});
+  return p;
+}
+
+graph input_node(Model* m, const str& name, int a, int b, int c, int d) {
+  auto n = std::make_shared<NodeBackProp>(name, a, b, c, d, 1);
+  NodeBackProp* nd = n.get();
+  n->zero_grad = [=]() { mle::zero(nd->grad, nd->total); };
+  m->inputs.push_back({n->output, (size_t)n->total * sizeof(float)});
+  m->keep.push_back(n);
+  return n;
+}
+
+void build_c1(Model* m, const long long* d) {
+  const int batch = (int)d[0], in = (int)d[1], hid = (int)d[2], cls = (int)d[3];
+  auto x = input_node(m, "Input", batch, 1, 1, in);
+  auto* labels = static_cast<int32_t*>(input_buffer(m, sizeof(int32_t) * batch));
+  m->l1.reset(new Linear(in, hid, "First Linear"));
+  m->l2.reset(new Linear(hid, cls, "Projection"));
+  auto pred = m->l2->forward(GraphOperations::RELU(m->l1->forward(x)));
+  auto target = GraphOperations::OneHot(labels, batch, 1, 1, cls);
+  m->root = GraphOperations::SoftMaxCrossEntropy(pred, target, true);
+  m->params = {&m->l1->W1, &m->l1->B1, &m->l2->W1, &m->l2->B1};
+  m->adamw = false;
+}
+
+void build_c4(Model* m, const long long* d) {
+  const int B = (int)d[0], S = (int)d[1], D = (int)d[2], H = (int)d[3], F = (int)d[4], V = (int)d[5];
+  auto* ids = static_cast<int32_t*>(input_buffer(m, sizeof(int32_t) * B * S));
+  auto* tgt = static_cast<int32_t*>(input_buffer(m, sizeof(int32_t) * B * S));
+  m->emb.reset(new Embedding(V, D, "Token Embedding"));
+  m->mha.reset(new MultiHeadAttention(D, D, H, "Block MHA"));
+  m->ffn1.reset(new Linear(D, F, "FFN1"));
+  m->ffn2.reset(new Linear(F, D, "FFN2"));
+  m->lm.reset(new Linear(D, V, "Projection"));
+  auto x0 = m->emb->forward(ids, B, S, S);
+  auto x = GraphOperations::MatrixPositionalEncoding(x0);
+  auto h = GraphOperations::LayerNorm(x);
+  auto a = m->mha->forward(h, true);
+  auto x2 = GraphOperations::Add(x, a);
+  auto f = m->ffn2->forward(GraphOperations::GELU(m->ffn1->forward(GraphOperations::LayerNorm(x2))));
+  auto x3 = GraphOperations::Add(x2, f);
+  auto logits = m->lm->forward(x3);
+  auto target = GraphOperations::OneHot(tgt, B, S, S, V);
+  m->root = GraphOperations::SoftMaxCrossEntropy(logits, target, true);
+  auto& mh = *m->mha;
+  m->params = {&m->emb->E, &mh.q.W1, &mh.q.B1, &mh.k.W1, &mh.k.B1, &mh.v.W1, &mh.v.B1, &mh.o.W1, &mh.o.B1,
+               &m->ffn1->W1, &m->ffn1->B1, &m->ffn2->W1, &m->ffn2->B1, &m->lm->W1, &m->lm->B1};
+}
+
+void build_c5(Model* m, const long long* d) {
+  const int N = (int)d[0], Cin = (int)d[1], C = (int)d[2], Hs = (int)d[3], Ws = (int)d[4], groups = (int)d[5],
+            tdim = (int)d[6], t = (int)d[7];
+  auto x = input_node(m, "Input images", N, Cin, Hs, Ws);
+  auto noise = input_node(m, "Noise target", N, C, Hs, Ws);
+  m->rb.reset(new ResidualBlock(Cin, C, tdim, 1, groups));
+  auto temb = GraphOperations::PositionalEncoding(t, tdim);
+  auto out = m->rb->forward(x, temb);
+  m->root = GraphOperations::MeanSquaredError(out, noise, true);
+  auto& r = *m->rb;
+  m->params = {&r.conv1->W1, &r.conv1->B1, &r.conv2->W1, &r.conv2->B1,
+               &r.skipconv->W1, &r.skipconv->B1, &r.time_mlp->W1, &r.time_mlp->B1};
+}
+
+// C2: a flat set of parameters; each parameter is carried by a hook node (as
+// Linear's output node carries W1/B1) under one track() root.
+void build_c2(Model* m, const long long* d, int nd) {
+  const int n = (int)d[0];
+  size_t total = 0;
+  for (int i = 0; i < n; ++i) total += ((size_t)d[1 + i] + 63) & ~size_t(63);
+  mle::param_reserve(total);
+  graph_tree holders;
+  for (int i = 0; i < n; ++i) {
+    m->loose.emplace_back(new AdamParameter("param " + std::to_string(i), 1, 1, 1, (int)d[1 + i]));
+    AdamParameter* p = m->loose.back().get();
+    auto h = std::make_shared<NodeBackProp>("holder " + std::to_string(i), 1, 1, 1, 1, 0);
+    h->params = {p};
+    h->zero_grad = [=]() { mle::zero(p->grad, p->total); };
+    h->accumulate = [=](double* s) { p->accumulate_grad(s); };
+    h->clipnorm = [=](const double* s) { p->gradnorm(s); };
+    h->updateParams = [=](const float lr, const bool adamw) { p->update(lr, adamw); };
+    holders.push_back(h);
+    m->params.push_back(p);
+  }
+  m->root = GraphOperations::track(holders);
+  m->clip_scale = static_cast<double*>(mle::alloc_scratch(256));
+  (void)nd;
+}
+
+}  // namespace
+
+extern "C" {
+
+void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad) {
+  mle::quirks().bmmabt_reference_grad = bmmabt_reference_grad != 0;
+  mle::quirks().broadcast_channel_reference_grad = broadcast_channel_reference_grad != 0;
+}
+
+void mle_model_set_seed(unsigned long long seed) { mle::set_init_seed(seed); }
+
+void* mle_model_create(int kind, const long long* dims, int ndims) {
+  auto* m = new Model();
+  m->kind = kind;
+  switch (kind) {
+    case 1: build_c1(m, dims); break;
+    case 2: build_c2(m, dims, ndims); break;
+    case 4: build_c4(m, dims); break;
+    case 5: build_c5(m, dims); break;
+    default:
+      delete m;
+      return nullptr;
+  }
+  m->go.nodes = topological_sort(m->root);
+  mle::sync("model build");
+  return m;
+}
+
+void mle_model_destroy(void* h) {
+  auto* m = static_cast<Model*>(h);
+  if (!m) return;
+  mle::sync("model destroy");
+  m->go.clear_graph();
+  delete m;
+}
+
+int mle_model_num_params(void* h) { return (int)static_cast<Model*>(h)->params.size(); }
+
+const char* mle_model_param_name(void* h, int i) { return static_cast<Model*>(h)->params[i]->op_name.c_str(); }
+
+long long mle_model_param_numel(void* h, int i) { return static_cast<Model*>(h)->params[i]->total; }
+
+int mle_model_param_t(void* h, int i) { return static_cast<Model*>(h)->params[i]->t; }
+
+int mle_model_param_io(void* h, int i, int which, void* host, int to_device) {
+  auto* m = static_cast<Model*>(h);
+  if (i < 0 || i >= (int)m->params.size() || which < 0 || which > 3) return MLE_ERR_INVALID;
+  AdamParameter* p = m->params[i];
+  float* dev = which == 0 ? p->output : which == 1 ? p->grad : which == 2 ? p->m : p->v;
+  const size_t bytes = (size_t)p->total * sizeof(float);
+  return to_device ? mle_memcpy_h2d(dev, host, bytes, mle::stream()) : mle_memcpy_d2h(host, dev, bytes, mle::stream());
+}
+
+int mle_model_input(void* h, int slot, const void* host, size_t bytes) {
+  auto* m = static_cast<Model*>(h);
+  if (slot < 0 || slot >= (int)m->inputs.size() || bytes > m->inputs[slot].second) return MLE_ERR_INVALID;
+  return mle_memcpy_h2d(m->inputs[slot].first, host, bytes, mle::stream());
+}
+
+int mle_model_step(void* h, float lr, int mode, float clip) {
+  auto* m = static_cast<Model*>(h);
+  if (m->kind == 2) {
+    if (mode & MLE_STEP_ZERO) m->go.zero_grad();
+    if (clip > 0.0f) {
+      check(mle_fill(mle::stream(), reinterpret_cast<float*>(m->clip_scale), 0.0f, 2), "clip scale reset");
+      m->go.accumulate(m->clip_scale);
+      m->go.clipNorm(m->clip_scale);
+    }
+    if (mode & MLE_STEP_UPDATE) m->go.ParameterUpdate(nullptr, false, lr, true);
+    return MLE_OK;
+  }
+  if (mode & MLE_STEP_ZERO) m->go.zero_grad();
+  if (mode & MLE_STEP_FORWARD) m->go.forward(nullptr, true);
+  if (mode & MLE_STEP_BACKWARD) m->go.backward();
+  if (mode & MLE_STEP_UPDATE) m->go.ParameterUpdate(nullptr, false, lr, m->adamw);
+  return MLE_OK;
+}
+
+float mle_model_loss(void* h) {
+  (void)h;
+  return GraphOperations::loss;
+}
+
+int mle_model_sync(void* h) {
+  (void)h;
+  return mle_stream_sync(mle::stream());
+}
+
+void* mle_model_stream(void* h) {
+  (void)h;
+  return mle::stream();
+}
+
+int mle_model_num_nodes(void* h) { return (int)static_cast<Model*>(h)->go.nodes.size(); }
+
+}  // extern "C"

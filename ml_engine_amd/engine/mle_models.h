@@ -1,0 +1,39 @@
+/* Model harness of libmle_engine.so: builds the benchmark configurations with
+ * the GraphOperations API and steps them.  Test and benchmark plumbing, not
+ * part of the drop-in boundary (include/mle_hip.h). */
+#ifndef MLE_MODELS_H
+#define MLE_MODELS_H
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { MLE_STEP_ZERO = 1, MLE_STEP_FORWARD = 2, MLE_STEP_BACKWARD = 4, MLE_STEP_UPDATE = 8, MLE_STEP_ALL = 15 };
+
+/* kind 1: MLP   dims {batch, in, hidden, classes}            inputs: x f32, labels i32
+ * kind 2: flat  dims {n, size_0 .. size_{n-1}}                (accumulate + clip + AdamW)
+ * kind 4: block dims {B, S, D, heads, F, V}                   inputs: ids i32, targets i32
+ * kind 5: resblock dims {N, Cin, C, H, W, groups, tdim, t}   inputs: x f32, noise f32 */
+void* mle_model_create(int kind, const long long* dims, int ndims);
+void mle_model_destroy(void* h);
+void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad);
+void mle_model_set_seed(unsigned long long seed);
+int mle_model_num_params(void* h);
+const char* mle_model_param_name(void* h, int i);
+long long mle_model_param_numel(void* h, int i);
+int mle_model_param_t(void* h, int i);
+/* which: 0 params, 1 grads, 2 m, 3 v */
+int mle_model_param_io(void* h, int i, int which, void* host, int to_device);
+int mle_model_input(void* h, int slot, const void* host, size_t bytes);
+/* mode: MLE_STEP_* bits; clip > 0 (kind 2) applies accumulate + clipNorm. */
+int mle_model_step(void* h, float lr, int mode, float clip);
+float mle_model_loss(void* h);
+int mle_model_sync(void* h);
+void* mle_model_stream(void* h);
+int mle_model_num_nodes(void* h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

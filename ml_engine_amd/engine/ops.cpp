@@ -1,0 +1,478 @@
+// GraphOperations op factories on the hot path (Engine/engine.cu:675-3347):
+// each builds a node whose forward / backward lambdas enqueue C ABI kernels on
+// the engine stream.  Backward hooks accumulate (+=) into their inputs'
+// gradients, except where the reference assigns (identity, SoftMaxCrossEntropy).
+#include "engine.h"
+
+#include <math.h>
+#include <stdio.h>
+
+using mle::check;
+
+namespace {
+
+inline mle_stream S() { return mle::stream(); }
+
+graph make_node(const str& name, int a, int b, int c, int d) {
+  auto n = std::make_shared<NodeBackProp>(name, a, b, c, d, 1);
+  GraphOperations::GB += (double)n->total * sizeof(float) / (1ULL << 30);
+  return n;
+}
+
+void std_hooks(const graph& node) {
+  NodeBackProp* nd = node.get();
+  node->free = [=]() { nd->clear(); };
+  node->zero_grad = [=]() { mle::zero(nd->grad, nd->total); };
+}
+
+// Operand case of BMM-family inputs: (dim0 > 1) + 2*(dim1 > 1) (Engine/engine.cu:2221-2223).
+int bcase(const graph& X) { return (X->dim[0] > 1) + 2 * (X->dim[1] > 1); }
+
+// Element offset of batch item (b, c) for an operand with broadcast code `flag`
+// (batch_chan_offset, Engine/kernels.cu:371-385).
+long long bc_off(int flag, int b, int c, int C, long long inner) {
+  const int hb = flag & 1, hc = (flag >> 1) & 1;
+  const long long cs = hc ? C : 1;
+  return (hb ? (long long)b * cs : 0) * inner + (hc ? (long long)c : 0) * inner;
+}
+
+// Batched GEMM over the batch x channel grid with the reference's broadcast
+// codes.  When every operand's offset is linear in the item index and no two
+// items share an output, one batched launch covers the grid.  Otherwise the
+// items run one launch at a time, in order: with beta == 1 items that share an
+// output accumulate into it (the reference's atomicAdd epilogue), with beta == 0
+// the last item's product stays (the reference's unordered assignment).
+void grid_gemm(int ta, int tb, int M, int N, int K, const float* A, int64_t lda, int fa, long long asz, const float* B,
+               int64_t ldb, int fb, long long bsz, float beta, float* Cc, int64_t ldc, int fc, long long csz,
+               int batch, int channels, const str& what) {
+  const int z = batch * channels;
+  auto stride_of = [&](int flag, long long inner, int64_t& stride) -> bool {
+    // offset(b, c) must equal stride * (b*channels + c)
+    if (flag == 0) {
+      stride = 0;
+      return true;
+    }
+    if (flag == 3) {
+      stride = inner;
+      return true;
+    }
+    if (flag == 1 && channels == 1) {
+      stride = inner;
+      return true;
+    }
+    if (flag == 2 && batch == 1) {
+      stride = inner;
+      return true;
+    }
+    return false;
+  };
+  int64_t sa = 0, sb = 0, sc = 0;
+  const bool lin = stride_of(fa, asz, sa) && stride_of(fb, bsz, sb) && stride_of(fc, csz, sc);
+  const bool shared_out = (sc == 0 && z > 1) || !lin;
+  if (!shared_out) {
+    check(mle_gemm(S(), ta, tb, M, N, K, 1.0f, A, lda, sa, B, ldb, sb, beta, Cc, ldc, sc, z, nullptr), what);
+    return;
+  }
+  for (int b = 0; b < batch; ++b)
+    for (int c = 0; c < channels; ++c) {
+      const long long oa = bc_off(fa, b, c, channels, asz), ob = bc_off(fb, b, c, channels, bsz),
+                      oc = bc_off(fc, b, c, channels, csz);
+      check(mle_gemm(S(), ta, tb, M, N, K, 1.0f, A + oa, lda, 0, B + ob, ldb, 0, beta, Cc + oc, ldc, 0, 1, nullptr),
+            what);
+    }
+}
+
+graph act_node(const graph& input, int kind, const str& name) {
+  const int a = input->dim[0], b = input->dim[1], c = input->dim[2], d = input->dim[3];
+  auto node = make_node(name, a, b, c, d);
+  node->inputs = {input};
+  NodeBackProp *nd = node.get(), *x = input.get();
+  node->forward = [=]() { check(mle_act_fwd(S(), kind, x->output, nd->output, nd->total), name + " forward"); };
+  node->backward = [=]() {
+    check(mle_act_bwd(S(), kind, x->output, nd->grad, x->grad, nd->total), "Deriv " + name);
+  };
+  std_hooks(node);
+  return node;
+}
+
+graph softmax_node(const graph& X, int type, bool masked, const str& name) {
+  const int a = X->dim[0], b = X->dim[1], c = X->dim[2], d = X->dim[3];
+  auto node = make_node(name, a, b, c, d);
+  node->inputs = {X};
+  NodeBackProp *nd = node.get(), *x = X.get();
+  const int axis = type == 0 ? 0 : 1;
+  node->forward = [=]() {
+    check(mle_softmax_fwd(S(), x->output, nd->output, a * b, c, d, axis, masked ? 1 : 0), name + " forward");
+  };
+  node->backward = [=]() {
+    check(mle_softmax_bwd(S(), nd->output, nd->grad, x->grad, a * b, c, d, axis), "Deriv " + name);
+  };
+  std_hooks(node);
+  return node;
+}
+
+graph norm_node(const graph& X, int groups, const str& name) {
+  const int a = X->dim[0], b = X->dim[1], c = X->dim[2], d = X->dim[3];
+  const float eps = 1e-5f;  // gamma = 1, beta = 0 (Engine/engine.cu:3083, 3223)
+  auto node = make_node(name, a, b, c, d);
+  node->inputs = {X};
+  const size_t hw = (size_t)c * d;
+  const size_t ws_bytes = mle_norm_ws_bytes(a, b, hw, groups);
+  void* ws = mle::alloc_scratch(ws_bytes);
+  float* stats = static_cast<float*>(mle::alloc_scratch(2 * sizeof(float) * a * groups));
+  GraphOperations::GB += (double)(2 * a * groups) * sizeof(float) / (1ULL << 30);
+  NodeBackProp *nd = node.get(), *x = X.get();
+  node->forward = [=]() {
+    check(mle_norm_fwd(S(), x->output, nd->output, stats, a, b, hw, groups, eps, ws, ws_bytes), name + " forward");
+  };
+  node->backward = [=]() {
+    check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, 1, ws, ws_bytes),
+          name + " backward");
+  };
+  std_hooks(node);
+  return node;
+}
+
+}  // namespace
+
+// Copy (Engine/engine.cu:675-687)
+graph GraphOperations::Copy(const graph& X) {
+  auto node = make_node("Copy of " + X->op_name, X->dim[0], X->dim[1], X->dim[2], X->dim[3]);
+  node->inputs = {X};
+  NodeBackProp *nd = node.get(), *x = X.get();
+  node->forward = [=]() { check(mle_scale_write(S(), x->output, nd->output, 1.0f, nd->total), "Copy forward"); };
+  node->backward = [=]() { check(mle_accumulate(S(), nd->grad, x->grad, 1.0, nd->total), "Copy backward"); };
+  std_hooks(node);
+  return node;
+}
+
+// like (Engine/engine.cu:689-700)
+graph GraphOperations::like(const graph& X, const str name) {
+  auto node = make_node(name, X->dim[0], X->dim[1], X->dim[2], X->dim[3]);
+  node->inputs = {X};
+  node->forward = []() {};
+  node->backward = []() {};
+  std_hooks(node);
+  return node;
+}
+
+// identity (Engine/engine.cu:701-713): backward assigns.
+graph GraphOperations::identity(const graph& X) {
+  auto node = make_node(X->op_name, X->dim[0], X->dim[1], X->dim[2], X->dim[3]);
+  node->inputs = {X};
+  NodeBackProp *nd = node.get(), *x = X.get();
+  node->forward = [=]() { check(mle_scale_write(S(), x->output, nd->output, 1.0f, nd->total), "identity forward"); };
+  node->backward = [=]() { check(mle_scale_write(S(), nd->grad, x->grad, 1.0f, nd->total), "identity backward"); };
+  std_hooks(node);
+  return node;
+}
+
+// track (Engine/engine.cu:3349-3360): groups roots without allocating.
+graph GraphOperations::track(const graph_tree& X) {
+  str name = "Tracking: [";
+  for (const auto& p : X) name += (p->op_name + " ");
+  name += "]";
+  auto node = std::make_shared<NodeBackProp>(name, 1, 1, 1, 1, 0);
+  node->inputs = X;
+  NodeBackProp* nd = node.get();
+  node->free = [=]() { nd->clear(); };
+  return node;
+}
+
+// HeadifytoChannel (Engine/engine.cu:1144-1164)
+graph GraphOperations::HeadifytoChannel(const graph& X, const int heads) {
+  if (X->dim[1] != 1 || X->dim[3] % heads != 0) {
+    std::cerr << "Headify: channel must be 1 and embed must be divisible by heads\n";
+    Dimension(X);
+    std::exit(1);
+  }
+  const int b = X->dim[0], seq = X->dim[2], embed = X->dim[3], hd = embed / heads;
+  auto node = make_node("Headified " + X->op_name, b, heads, seq, hd);
+  node->inputs = {X};
+  NodeBackProp *nd = node.get(), *x = X.get();
+  node->forward = [=]() { check(mle_headify(S(), x->output, nd->output, b, heads, seq, hd, 0), "Headify forward"); };
+  node->backward = [=]() { check(mle_headify(S(), nd->grad, x->grad, b, heads, seq, hd, 1), "Headify backward"); };
+  std_hooks(node);
+  return node;
+}
+
+// DeHeadify (Engine/engine.cu:1166-1178)
+graph GraphOperations::DeHeadify(const graph& X) {
+  const int b = X->dim[0], heads = X->dim[1], seq = X->dim[2], hd = X->dim[3];
+  auto node = make_node("Deheadified " + X->op_name, b, 1, seq, heads * hd);
+  node->inputs = {X};
+  NodeBackProp *nd = node.get(), *x = X.get();
+  node->forward = [=]() { check(mle_headify(S(), x->output, nd->output, b, heads, seq, hd, 2), "DeHeadify forward"); };
+  node->backward = [=]() { check(mle_headify(S(), nd->grad, x->grad, b, heads, seq, hd, 3), "DeHeadify backward"); };
+  std_hooks(node);
+  return node;
+}
+
+// PositionalEncoding (Engine/engine.cu:1244-1261): no backward.
+graph GraphOperations::PositionalEncoding(const int& t, const int d_model) {
+  auto node = make_node("SinoSuodalPosEncoding", 1, 1, 1, d_model);
+  node->inputs = {};
+  NodeBackProp* nd = node.get();
+  const int tt = t;
+  node->forward = [=]() { check(mle_timestep_pe(S(), nd->output, tt, d_model), "PositionalEncoding forward"); };
+  std_hooks(node);
+  return node;
+}
+
+// MatrixPositionalEncoding (Engine/engine.cu:1263-1296)
+graph GraphOperations::MatrixPositionalEncoding(const graph& X, const int start_idx) {
+  if (X->dim[1] != 1) {
+    std::cerr << "MatrixPositionalEncoding expects input with channel dimension of 1\n";
+    Dimension(X);
+    std::exit(1);
+  }
+  const int batch = X->dim[0], rows = X->dim[2], cols = X->dim[3];
+  auto node = make_node("MatrixSinoSuodalPosEncoding", batch, 1, rows, cols);
+  node->inputs = {X};
+  NodeBackProp *nd = node.get(), *x = X.get();
+  node->forward = [=]() { check(mle_matpe(S(), x->output, nd->output, batch, rows, cols, start_idx), "MatPE forward"); };
+  node->backward = [=]() { check(mle_accumulate(S(), nd->grad, x->grad, 1.0, nd->total), "MatPE backward"); };
+  std_hooks(node);
+  return node;
+}
+
+// Broadcast_Channel (Engine/engine.cu:1401-1446)
+graph GraphOperations::Broadcast_Channel(const graph& A, const graph& B) {
+  if (A->dim[1] != B->dim[3] || B->dim[1] != 1 || B->dim[2] != 1) {
+    std::cout << "Channel mismatch in broadcast channel \n";
+    Dimension(A);
+    Dimension(B);
+    std::exit(1);
+  }
+  const int batch = A->dim[0], channels = A->dim[1], a = A->dim[2], b = A->dim[3];
+  auto node = make_node("Broadcast Channel", batch, channels, a, b);
+  node->inputs = {A, B};
+  NodeBackProp *nd = node.get(), *pa = A.get(), *pb = B.get();
+  const size_t hw = (size_t)a * b;
+  const int nreduce = mle::quirks().broadcast_channel_reference_grad ? b : channels;
+  node->forward = [=]() {
+    check(mle_broadcast_channel_add(S(), pa->output, pb->output, nd->output, batch, channels, hw),
+          "Broadcast Add forward");
+  };
+  node->backward = [=]() {
+    check(mle_accumulate(S(), nd->grad, pa->grad, 1.0, nd->total), "Broadcast Add backward - A grad");
+    check(mle_channel_sum(S(), nd->grad, batch, channels, hw, nreduce, pb->grad), "Broadcast Add backward - B grad");
+  };
+  std_hooks(node);
+  return node;
+}
+
+// Scale (Engine/engine.cu:2523-2551)
+graph GraphOperations::Scale(const graph& input, const float scale, const bool last) {
+  const int a = input->dim[0], b = input->dim[1], c = input->dim[2], d = input->dim[3];
+  auto node = make_node("Scale", a, b, c, d);
+  node->inputs = {input};
+  NodeBackProp *nd = node.get(), *x = input.get();
+  node->forward = [=]() { check(mle_scale_write(S(), x->output, nd->output, scale, nd->total), "Scale forward"); };
+  node->backward = [=]() {
+    if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Scale seed");
+    check(mle_accumulate(S(), nd->grad, x->grad, (double)scale, nd->total), "Deriv Scale");
+  };
+  std_hooks(node);
+  return node;
+}
+
+// Add (Engine/engine.cu:1630-1672)
+graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
+  for (int i = 0; i < 4; ++i)
+    if (A->dim[i] != B->dim[i]) {
+      std::cout << "Dimension mismatch in Add \n";
+      Dimension(A);
+      Dimension(B);
+      std::exit(1);
+    }
+  auto node = make_node("Add", A->dim[0], A->dim[1], A->dim[2], A->dim[3]);
+  node->inputs = {A, B};
+  NodeBackProp *nd = node.get(), *pa = A.get(), *pb = B.get();
+  node->forward = [=]() {
+    check(mle_scale_add(S(), pa->output, pb->output, nd->output, 1.0f, nd->total), "Add forward");
+    if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "Add loss");
+  };
+  node->backward = [=]() {
+    if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
+    check(mle_accumulate(S(), nd->grad, pa->grad, 1.0, nd->total), "Add backward - A grad");
+    check(mle_accumulate(S(), nd->grad, pb->grad, 1.0, nd->total), "Add backward - B grad");
+  };
+  std_hooks(node);
+  return node;
+}
+
+// MeanSquaredError (Engine/engine.cu:1900-1949).  zero_grad clears the loss.
+graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& target, const bool last) {
+  for (int i = 0; i < 4; ++i)
+    if (prediction->dim[i] != target->dim[i]) {
+      std::cout << "Dimension mismatch \n MSE dimensions are: \n";
+      Dimension(prediction);
+      Dimension(target);
+      std::exit(1);
+    }
+  auto node = std::make_shared<NodeBackProp>("MSE", 1, 1, 1, 1, 1);
+  node->inputs = {prediction, target};
+  GB += (double)(prediction->total + target->total + 1) * sizeof(float) / (1ULL << 30);
+  NodeBackProp *nd = node.get(), *pr = prediction.get(), *tg = target.get();
+  const size_t n = prediction->total;
+  const size_t ws_bytes = mle_loss_ws_bytes(n);
+  void* ws = mle::alloc_scratch(ws_bytes);
+  node->forward = [=]() {
+    if (calculate_loss || !last) {
+      check(mle_mse_fwd(S(), pr->output, tg->output, n, nd->output, ws, ws_bytes), "Scalar MSE in MSE forward");
+      if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "MSE loss");
+    }
+  };
+  node->backward = [=]() {
+    check(mle_mse_bwd(S(), pr->output, tg->output, last ? nullptr : nd->grad, pr->grad, n), "deriv MSE");
+  };
+  node->free = [=]() { nd->clear(); };
+  node->zero_grad = [=]() { mle::zero(nd->output, 1); };
+  return node;
+}
+
+// SoftMaxCrossEntropy (Engine/engine.cu:2064-2124).  The softmax buffer holds
+// the whole prediction (the reference allocates node->total == 1 float for it,
+// Engine/engine.cu:2080, and writes past it).  Backward assigns.
+graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph& target, const bool last) {
+  for (int i = 0; i < 4; ++i)
+    if (prediction->dim[i] != target->dim[i]) {
+      std::cout << "Dimension mismatch \n CrossEntropy dimensions are: \n";
+      Dimension(prediction);
+      Dimension(target);
+      std::exit(1);
+    }
+  const int batch = target->dim[0], channels = target->dim[1], c = target->dim[2], d = target->dim[3];
+  auto node = std::make_shared<NodeBackProp>("SoftMaxCrossEntropy Loss", 1, 1, 1, 1, 1);
+  node->inputs = {prediction, target};
+  GB += (double)(target->total + 1) * sizeof(float) / (1ULL << 30);
+  const size_t n = prediction->total;
+  float* probs = mle::alloc_output(n);
+  const int rows = batch * channels * c;
+  const size_t ws_bytes = mle_loss_ws_bytes(n);
+  void* ws = mle::alloc_scratch(ws_bytes);
+  NodeBackProp *nd = node.get(), *pr = prediction.get(), *tg = target.get();
+  node->forward = [=]() {
+    if (calculate_loss || !last) {
+      check(mle_softmax_xent_fwd(S(), pr->output, tg->output, probs, rows, d, nd->output, ws, ws_bytes),
+            "SoftMaxCrossEntropy");
+      if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "CE loss");
+    }
+  };
+  node->backward = [=]() {
+    check(mle_softmax_xent_bwd(S(), probs, tg->output, last ? nullptr : nd->grad, pr->grad, n, batch),
+          "derivative of CE in CE backward");
+  };
+  node->free = [=]() {
+    nd->clear();
+    mle::release(probs, n, false);
+  };
+  node->zero_grad = [=]() { mle::zero(nd->output, 1); };
+  return node;
+}
+
+// BMM (Engine/engine.cu:2205-2258): C = A B; dA += dZ B^T; dB += A^T dZ.
+graph GraphOperations::BMM(const graph& A, const graph& B) {
+  if (A->dim[3] != B->dim[2]) {
+    std::cout << "Dimension mismatch in BMM \n";
+    Dimension(A);
+    Dimension(B);
+    std::exit(1);
+  }
+  const bool bc_ok = ((A->dim[0] == B->dim[0]) || A->dim[0] == 1 || B->dim[0] == 1) &&
+                     ((A->dim[1] == B->dim[1]) || A->dim[1] == 1 || B->dim[1] == 1);
+  if (!bc_ok) {
+    std::cout << "Batch and Channel mismatch in BMM...\n";
+    std::exit(1);
+  }
+  const int fa = bcase(A), fb = bcase(B), fc = fa > fb ? fa : fb;
+  // The node takes A's batch and channel sizes, as the reference does.
+  const int batch = A->dim[0], channels = A->dim[1], m = A->dim[2], n = A->dim[3], p = B->dim[3];
+  auto node = make_node("BMM", batch, channels, m, p);
+  node->inputs = {A, B};
+  NodeBackProp *nd = node.get(), *pa = A.get(), *pb = B.get();
+  const long long asz = (long long)m * n, bsz = (long long)n * p, csz = (long long)m * p;
+  node->forward = [=]() {
+    grid_gemm(0, 0, m, p, n, pa->output, n, fa, asz, pb->output, p, fb, bsz, 0.0f, nd->output, p, fc, csz, batch,
+              channels, "BMM forward");
+  };
+  node->backward = [=]() {
+    grid_gemm(0, 1, m, n, p, nd->grad, p, fc, csz, pb->output, p, fb, bsz, 1.0f, pa->grad, n, fa, asz, batch, channels,
+              "BMM dA = dZ B^T");
+    grid_gemm(1, 0, n, p, m, pa->output, n, fa, asz, nd->grad, p, fc, csz, 1.0f, pb->grad, p, fb, bsz, batch, channels,
+              "BMM dB = A^T dZ");
+  };
+  std_hooks(node);
+  return node;
+}
+
+// BMMABT (Engine/engine.cu:2260-2314): C = A B^T; dA += dZ B.  The reference's
+// dB is bcmmT(A, dZ) with dims (n, m, p): C'[n x p] = A^T (dZ viewed as p x m)^T
+// written into B's gradient buffer; mle::quirks() selects it (default) or dZ^T A.
+graph GraphOperations::BMMABT(const graph& A, const graph& B) {
+  if (A->dim[3] != B->dim[3]) {
+    std::cout << "Dimension mismatch in BMMABT \n";
+    Dimension(A);
+    Dimension(B);
+    std::exit(1);
+  }
+  const int fa = bcase(A), fb = bcase(B), fc = fa > fb ? fa : fb;
+  const int batch = A->dim[0], channels = A->dim[1], m = A->dim[2], n = A->dim[3], p = B->dim[2];
+  auto node = make_node("BMMABT", batch, channels, m, p);
+  node->inputs = {A, B};
+  NodeBackProp *nd = node.get(), *pa = A.get(), *pb = B.get();
+  const long long asz = (long long)m * n, bsz = (long long)p * n, csz = (long long)m * p;
+  const bool ref_grad = mle::quirks().bmmabt_reference_grad;
+  node->forward = [=]() {
+    grid_gemm(0, 1, m, p, n, pa->output, n, fa, asz, pb->output, n, fb, bsz, 0.0f, nd->output, p, fc, csz, batch,
+              channels, "BMMABT forward");
+  };
+  node->backward = [=]() {
+    grid_gemm(0, 0, m, n, p, nd->grad, p, fc, csz, pb->output, n, fb, bsz, 1.0f, pa->grad, n, fa, asz, batch, channels,
+              "BMMABT dA = dZ B");
+    if (ref_grad)
+      grid_gemm(1, 1, n, p, m, pa->output, n, fa, asz, nd->grad, m, fc, csz, 1.0f, pb->grad, p, fb, bsz, batch,
+                channels, "BMMABT dB (reference bcmmT)");
+    else
+      grid_gemm(1, 0, p, n, m, nd->grad, p, fc, csz, pa->output, n, fa, asz, 1.0f, pb->grad, n, fb, bsz, batch,
+                channels, "BMMABT dB = dZ^T A");
+  };
+  std_hooks(node);
+  return node;
+}
+
+graph GraphOperations::SOFTMAX(const graph& X, const int type) { return softmax_node(X, type, false, "Softmax"); }
+graph GraphOperations::SOFTMASK(const graph& X, const int type) { return softmax_node(X, type, true, "Softmask"); }
+graph GraphOperations::RELU(const graph& input) { return act_node(input, MLE_RELU, "ReLU"); }
+graph GraphOperations::SILU(const graph& input) { return act_node(input, MLE_SILU, "SiLU"); }
+graph GraphOperations::TANH(const graph& input) { return act_node(input, MLE_TANH, "TANH"); }
+graph GraphOperations::GELU(const graph& input) { return act_node(input, MLE_GELU, "GELU"); }
+graph GraphOperations::SIGMOID(const graph& input) { return act_node(input, MLE_SIGMOID, "Sigmoid"); }
+graph GraphOperations::LeakyRELU(const graph& input) { return act_node(input, MLE_LEAKY_RELU, "LeakyReLU"); }
+
+// LayerNorm (Engine/engine.cu:3080-3146): statistics over C*H*W of each item.
+graph GraphOperations::LayerNorm(const graph& X) { return norm_node(X, 1, "LayerNorm"); }
+
+// GroupNorm (Engine/engine.cu:3212-3282)
+graph GraphOperations::GroupNorm(const graph& X, const int group) {
+  if (X->dim[1] % group != 0) {
+    std::cout << "Groups cannot be cleanly split \n";
+    Dimension(X);
+    std::exit(1);
+  }
+  return norm_node(X, group, "GroupNorm");
+}
+
+// One-hot targets from device token ids (TextualEmbedding::forward key "T").
+graph GraphOperations::OneHot(const int32_t* keys, int batch, int clen, int max_clen, int vocab) {
+  auto node = make_node("OneHot targets", batch, 1, clen, vocab);
+  node->inputs = {};
+  NodeBackProp* nd = node.get();
+  node->forward = [=]() {
+    check(mle_fill(S(), nd->output, 0.0f, nd->total), "OneHot fill");
+    check(mle_onehot(S(), nd->output, keys, batch, clen, max_clen, vocab), "OneHotEmbeddings");
+  };
+  std_hooks(node);
+  return node;
+}

@@ -1,0 +1,107 @@
+"""ctypes driver for the engine's model harness (libmle_engine.so).
+
+Builds the benchmark configurations with the C++ GraphOperations API and steps
+them; used by the tests and bench.py.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import hip
+
+KIND = {"mlp": 1, "flat": 2, "block": 4, "resblock": 5}
+STEP_ZERO, STEP_FORWARD, STEP_BACKWARD, STEP_UPDATE, STEP_ALL = 1, 2, 4, 8, 15
+P, I, LL, F, SZ = C.c_void_p, C.c_int, C.c_longlong, C.c_float, C.c_size_t
+
+_SIGS = {
+    "mle_model_create": (P, [I, C.POINTER(LL), I]),
+    "mle_model_destroy": (None, [P]),
+    "mle_model_set_quirks": (None, [I, I]),
+    "mle_model_set_seed": (None, [C.c_ulonglong]),
+    "mle_model_num_params": (I, [P]),
+    "mle_model_param_name": (C.c_char_p, [P, I]),
+    "mle_model_param_numel": (LL, [P, I]),
+    "mle_model_param_t": (I, [P, I]),
+    "mle_model_param_io": (I, [P, I, I, P, I]),
+    "mle_model_input": (I, [P, I, P, SZ]),
+    "mle_model_step": (I, [P, F, I, F]),
+    "mle_model_loss": (F, [P]),
+    "mle_model_sync": (I, [P]),
+    "mle_model_stream": (P, [P]),
+    "mle_model_num_nodes": (I, [P]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        hip.lib()  # libmle_hip.so first: the engine links against it
+        path = hip.LIB_DIR / "libmle_engine.so"
+        if not path.exists():
+            raise hip.MLEError(f"{path} is missing: run `python -m ml_engine_amd.build`")
+        _lib = C.CDLL(str(path))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+class Model:
+    """One configuration built with the engine (parameters in the flat arena)."""
+
+    def __init__(self, kind: str, dims, seed: int = 0, reference_quirks: bool = True):
+        L = lib()
+        hip.init(0)
+        L.mle_model_set_quirks(int(reference_quirks), int(reference_quirks))
+        L.mle_model_set_seed(seed)
+        arr = (LL * len(dims))(*[int(d) for d in dims])
+        self.h = L.mle_model_create(KIND[kind], arr, len(dims))
+        if not self.h:
+            raise hip.MLEError(f"model {kind} {dims} not created")
+        self.kind = kind
+        self.dims = list(dims)
+        n = L.mle_model_num_params(self.h)
+        self.names = [L.mle_model_param_name(self.h, i).decode() for i in range(n)]
+        self.numel = [int(L.mle_model_param_numel(self.h, i)) for i in range(n)]
+
+    # which: 0 params, 1 grads, 2 m, 3 v
+    def get(self, i: int, which: int = 0) -> np.ndarray:
+        out = np.empty(self.numel[i], np.float32)
+        hip.check(lib().mle_model_param_io(self.h, i, which, out.ctypes.data, 0))
+        return out
+
+    def set(self, i: int, arr: np.ndarray, which: int = 0) -> None:
+        a = np.ascontiguousarray(arr, dtype=np.float32).reshape(-1)
+        assert a.size == self.numel[i], (self.names[i], a.size, self.numel[i])
+        hip.check(lib().mle_model_param_io(self.h, i, which, a.ctypes.data, 1))
+
+    def input(self, slot: int, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr)
+        hip.check(lib().mle_model_input(self.h, slot, a.ctypes.data, a.nbytes))
+
+    def step(self, lr: float, mode: int = STEP_ALL, clip: float = 0.0) -> None:
+        hip.check(lib().mle_model_step(self.h, lr, mode, clip))
+
+    def sync(self) -> None:
+        hip.check(lib().mle_model_sync(self.h))
+
+    @property
+    def loss(self) -> float:
+        return float(lib().mle_model_loss(self.h))
+
+    @property
+    def stream(self):
+        return lib().mle_model_stream(self.h)
+
+    def t(self, i: int) -> int:
+        return int(lib().mle_model_param_t(self.h, i))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().mle_model_destroy(self.h)
+            self.h = None
