@@ -35,12 +35,15 @@ def rng(seed: int) -> np.random.Generator:
     return np.random.default_rng(seed)
 
 
-def assert_close(got: np.ndarray, ref: np.ndarray, rtol: float, atol_scale: float = 0.0, what: str = ""):
-    """|got - ref| <= rtol*|ref| + atol_scale*max|ref| element-wise.
+def assert_close(got: np.ndarray, ref: np.ndarray, rtol: float, atol_scale: float = 0.0, what: str = "",
+                 scale: float | None = None):
+    """|got - ref| <= rtol*|ref| + atol_scale*S element-wise, S = max|ref| or `scale`.
 
-    The absolute floor is relative to the tensor's largest magnitude: GEMM and
-    reduction outputs near zero carry cancellation error of the size of the
-    summed terms, not of the result.
+    The absolute floor is relative to the magnitude of the summed terms: GEMM
+    and reduction outputs near zero carry cancellation error of that size, not
+    of the result.  A result that is zero by symmetry (for example a bias
+    gradient whose row sums cancel exactly) passes the magnitude of its terms
+    as `scale`.
     """
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
@@ -49,7 +52,8 @@ def assert_close(got: np.ndarray, ref: np.ndarray, rtol: float, atol_scale: floa
         return
     assert np.all(np.isfinite(got) == np.isfinite(ref)), f"{what}: finiteness differs"
     fin = np.isfinite(ref)
-    scale = np.max(np.abs(ref[fin])) if fin.any() else 0.0
+    if scale is None:
+        scale = np.max(np.abs(ref[fin])) if fin.any() else 0.0
     err = np.abs(got - ref)
     tol = rtol * np.abs(ref) + atol_scale * scale
     bad = fin & (err > tol)

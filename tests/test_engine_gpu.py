@@ -81,7 +81,12 @@ def test_block_step(hip, orc, quirks):
                     orc.ptr(tgt), T(op), T(og), T(om), T(ov), 0.0, 1, int(not quirks))
     assert abs(m.loss - loss) <= 1e-5 * abs(loss), (m.loss, loss)
     for i in range(len(params)):
-        assert_close(m.get(i, 1), og[i], what=f"grad {m.names[i]}", **GRAD)
+        # Parameters 1..14 are (W, b) pairs.  The query bias gradient is zero by
+        # symmetry (a per-column shift of the scores does not change a
+        # column-normalised softmax), so biases are judged on the scale of
+        # their layer's weight gradient, which sums the same dY terms.
+        s = max(np.abs(og[i]).max(), np.abs(og[i - 1]).max()) if i >= 2 and i % 2 == 0 else None
+        assert_close(m.get(i, 1), og[i], what=f"grad {m.names[i]}", scale=s, **GRAD)
     check_update(orc, m, params, cfg.lr, 1, True, "block")
     m.close()
 
