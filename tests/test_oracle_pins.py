@@ -1,0 +1,395 @@
+"""Pins for the CPU oracle (no GPU): every oracle function is checked against
+an independent implementation -- numpy / torch CPU library routines in float64,
+closed forms, identities and brute force on tiny inputs -- chosen so that a
+plausible slip (a transposed operand, a wrong index or sign, a dropped term)
+fails.  The reference ships no tests or golden vectors; the committed fixtures
+in tests/golden/ come from the torch references below (make_golden.py)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as Fn
+
+import torch_ref
+from conftest import assert_close, rng
+
+D64 = torch.float64
+
+
+def p(a):
+    import oracle_lib
+
+    return oracle_lib.ptr(a)
+
+
+# ------------------------------------------------------------------ GEMM family
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+def test_bcmm_matches_numpy_with_broadcast_flags(orc, kind):
+    r = rng(kind)
+    batch, ch, m, n, pp = 2, 3, 5, 7, 4
+    # operand shapes per kind: A m x n | n x m, B n x p | p x n
+    a_inner = (m, n) if kind in (0, 1) else (n, m)
+    b_inner = (n, pp) if kind in (0, 2) else (pp, n)
+    for fa, fb in [(3, 3), (3, 0), (0, 3), (1, 2), (3, 1)]:
+        fc = max(fa, fb)
+        shp = lambda f, inner: ((batch if f & 1 else 1), (ch if f & 2 else 1)) + inner
+        A = r.standard_normal(shp(fa, a_inner)).astype(np.float32)
+        B = r.standard_normal(shp(fb, b_inner)).astype(np.float32)
+        C = np.zeros(shp(fc, (m, pp)), np.float32)
+        orc.call("orc_bcmm", kind, p(A), p(B), p(C), batch, ch, m, n, pp, 0, fa, fb, fc, 0.5)
+        Am = A.astype(np.float64) if kind in (0, 1) else np.swapaxes(A, -1, -2).astype(np.float64)
+        Bm = B.astype(np.float64) if kind in (0, 2) else np.swapaxes(B, -1, -2).astype(np.float64)
+        want = 0.5 * np.matmul(Am, Bm)  # broadcasts the size-1 batch/channel axes
+        assert_close(C, want.reshape(C.shape), rtol=1e-6, atol_scale=1e-6, what=f"kind {kind} flags {fa}{fb}")
+
+
+def test_bcmm_accumulates_over_broadcast_output(orc):
+    """backward == 1 with a broadcast output sums every batch item (the dW reduction)."""
+    r = rng(9)
+    X = r.standard_normal((4, 1, 6, 3)).astype(np.float32)   # [B, 1, rows, in]
+    dY = r.standard_normal((4, 1, 6, 5)).astype(np.float32)  # [B, 1, rows, out]
+    dW = np.ones((3, 5), np.float32)
+    orc.call("orc_bcmm", 2, p(X), p(dY), p(dW), 4, 1, 3, 6, 5, 1, 3, 3, 0, 1.0)
+    want = 1.0 + np.einsum("bri,bro->io", X.astype(np.float64), dY.astype(np.float64))
+    assert_close(dW, want, rtol=1e-6, atol_scale=1e-6)
+
+
+def test_bmmabt_reference_gradient_identity(orc):
+    """The reference's B-gradient of BMMABT, bcmmT(A, dZ) with (n, m, p), is
+    (dZ A)^T written row-major into B's buffer when m == p (attention's S x S)."""
+    r = rng(10)
+    S, d = 6, 4
+    A = r.standard_normal((S, d)).astype(np.float32)
+    dZ = r.standard_normal((S, S)).astype(np.float32)
+    out = np.zeros(S * d, np.float32)
+    orc.call("orc_bcmm", 3, p(A), p(dZ), p(out), 1, 1, d, S, S, 1, 3, 3, 3, 1.0)
+    want = (dZ.astype(np.float64) @ A.astype(np.float64)).T.reshape(-1)
+    assert_close(out, want, rtol=1e-6, atol_scale=1e-6)
+    true_grad = (dZ.astype(np.float64).T @ A.astype(np.float64)).reshape(-1)
+    assert np.abs(out - true_grad).max() > 1e-3  # it is not dZ^T A
+
+
+def test_bcompress_bcumadd_channel_squeeze(orc):
+    r = rng(11)
+    x = r.standard_normal((37, 9)).astype(np.float32)
+    y = np.full(9, 0.5, np.float32)
+    orc.call("orc_bcompress", p(x), p(y), 37, 9, 2.0)
+    assert_close(y, 0.5 + 2.0 * x.astype(np.float64).sum(0), rtol=1e-6, atol_scale=1e-6)
+    z = x.copy()
+    b = r.standard_normal(9).astype(np.float32)
+    orc.call("orc_bcumadd", p(z), p(b), 37, 9)
+    np.testing.assert_array_equal(z, x + b)
+    t = r.standard_normal((3, 8, 20)).astype(np.float32)
+    for nb in (8, 5):
+        s = np.zeros(8, np.float32)
+        orc.call("orc_channel_squeeze", p(t), p(s), 3, 8, 20, nb)
+        want = t.astype(np.float64).sum((0, 2))
+        want[nb:] = 0.0
+        assert_close(s, want, rtol=1e-6, atol_scale=1e-6)
+
+
+# ---------------------------------------------------------------- activations
+ACTS = {
+    0: (torch.relu, None),
+    1: (lambda x: Fn.gelu(x, approximate="tanh"), None),
+    2: (Fn.silu, None),
+    3: (torch.tanh, None),
+    4: (torch.sigmoid, None),
+    5: (lambda x: Fn.leaky_relu(x, 0.01), None),
+}
+
+
+@pytest.mark.parametrize("kind", sorted(ACTS))
+def test_activation_and_derivative_vs_autograd(orc, kind):
+    r = rng(20 + kind)
+    x = (r.standard_normal(4001) * 3).astype(np.float32)
+    x[:3] = [0.5, -0.5, 2.0]
+    dy = r.standard_normal(4001).astype(np.float32)
+    y = np.zeros_like(x)
+    orc.call("orc_act_fwd", kind, p(x), p(y), x.size)
+    dx = np.zeros_like(x)
+    orc.call("orc_act_bwd", kind, p(x), p(dy), p(dx), x.size)
+    xt = torch.tensor(x, dtype=D64, requires_grad=True)
+    yt = ACTS[kind][0](xt)
+    (g,) = torch.autograd.grad(yt, xt, torch.tensor(dy, dtype=D64))
+    assert_close(y, yt.detach().numpy(), rtol=2e-6, atol_scale=1e-7, what="fwd")
+    assert_close(dx, g.numpy(), rtol=2e-5, atol_scale=1e-6, what="bwd")
+
+
+def test_activation_special_values(orc):
+    x = np.array([0.0, 100.0, -100.0, 1e-3], np.float32)
+    dy = np.ones(4, np.float32)
+    d = np.zeros(4, np.float32)
+    orc.call("orc_act_bwd", 0, p(x), p(dy), p(d), 4)
+    assert d[0] == 0.0  # ReLU'(0) = 0 (strict >)
+    d[:] = 0
+    orc.call("orc_act_bwd", 1, p(x), p(dy), p(d), 4)
+    assert d[0] == pytest.approx(0.5, abs=1e-7)  # GELU'(0) = 1/2
+    d[:] = 0
+    orc.call("orc_act_bwd", 2, p(x), p(dy), p(d), 4)
+    assert d[1] == 1.0 and d[2] == 0.0  # SiLU' limits
+
+
+# -------------------------------------------------------------------- softmax
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("masked", [0, 1])
+def test_softmax_vs_torch(orc, axis, masked):
+    r = rng(30 + axis * 2 + masked)
+    bc, rows, cols = 3, 7, 7
+    x = (r.standard_normal((bc, rows, cols)) * 2).astype(np.float32)
+    dy = r.standard_normal((bc, rows, cols)).astype(np.float32)
+    y = np.zeros_like(x)
+    orc.call("orc_softmax", p(x), p(y), bc, rows, cols, axis, masked)
+    dx = np.zeros_like(x)
+    orc.call("orc_softmax_bwd", p(y), p(dy), p(dx), bc, rows, cols, axis)
+    xt = torch.tensor(x, dtype=D64, requires_grad=True)
+    z = xt
+    if masked:
+        z = z.masked_fill(torch.triu(torch.ones(rows, cols, dtype=torch.bool), 1), float("-inf"))
+    yt = torch.softmax(z, dim=-1 if axis == 0 else -2)
+    (g,) = torch.autograd.grad(yt, xt, torch.tensor(dy, dtype=D64))
+    assert_close(y, yt.detach().numpy(), rtol=1e-6, atol_scale=1e-7, what="softmax")
+    assert_close(dx, g.numpy(), rtol=1e-5, atol_scale=1e-6, what="softmax bwd")
+    sums = y.sum(-1 if axis == 0 else -2)
+    np.testing.assert_allclose(sums, 1.0, rtol=1e-6)
+
+
+# ---------------------------------------------------------------------- norms
+@pytest.mark.parametrize("batch,channels,hw,groups", [(3, 1, 40, 1), (2, 4, 30, 1), (2, 8, 25, 4)])
+def test_norm_vs_torch(orc, batch, channels, hw, groups):
+    r = rng(40 + channels + groups)
+    x = (r.standard_normal((batch, channels, hw)) * 2 + 1).astype(np.float32)
+    dy = r.standard_normal(x.shape).astype(np.float32)
+    y = np.zeros_like(x)
+    st = np.zeros(2 * batch * groups, np.float32)
+    orc.call("orc_norm_fwd", p(x), p(y), p(st), batch, channels, hw, groups, 1e-5)
+    dx = np.zeros_like(x)
+    orc.call("orc_norm_bwd", p(y), p(dy), p(dx), p(st), batch, channels, hw, groups, 1e-5, 0)
+    xt = torch.tensor(x, dtype=D64, requires_grad=True)
+    yt = Fn.layer_norm(xt, xt.shape[1:], eps=1e-5) if groups == 1 else Fn.group_norm(xt, groups, eps=1e-5)
+    (g,) = torch.autograd.grad(yt, xt, torch.tensor(dy, dtype=D64))
+    assert_close(y, yt.detach().numpy(), rtol=1e-5, atol_scale=1e-6, what="norm fwd")
+    assert_close(dx, g.numpy(), rtol=1e-4, atol_scale=1e-5, what="norm bwd")
+    xs = x.reshape(batch * groups, -1).astype(np.float64)
+    np.testing.assert_allclose(st[0::2], xs.mean(1), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(st[1::2], ((xs - xs.mean(1, keepdims=True)) ** 2).sum(1), rtol=1e-5)
+
+
+def test_layernorm_reference_layout_writes_prefix_only(orc):
+    """LayerBackward guards with idx < batch*row*col, so for channels > 1 only
+    that prefix receives a gradient, each element with group idx / (row*col)."""
+    r = rng(45)
+    batch, channels, hw = 2, 3, 10
+    y = r.standard_normal((batch, channels, hw)).astype(np.float32)
+    dy = r.standard_normal(y.shape).astype(np.float32)
+    st = np.abs(r.standard_normal(2 * batch)).astype(np.float32) + 1
+    dx = np.zeros_like(y)
+    orc.call("orc_norm_bwd", p(y), p(dy), p(dx), p(st), batch, channels, hw, 1, 1e-5, 1)
+    flat = dx.reshape(-1)
+    assert np.all(flat[batch * hw:] == 0) and np.any(flat[: batch * hw] != 0)
+
+
+# ----------------------------------------------------------------------- conv
+@pytest.mark.parametrize("k,pad,stride", [(3, 1, 1), (1, 0, 1), (3, 1, 2), (5, 2, 1)])
+def test_conv_vs_torch(orc, k, pad, stride):
+    r = rng(50 + k + stride)
+    n, cin, h, w, cout = 2, 3, 9, 8, 4
+    x = r.standard_normal((n, cin, h, w)).astype(np.float32)
+    wt = r.standard_normal((cout, cin, k, k)).astype(np.float32)
+    b = r.standard_normal(cout).astype(np.float32)
+    xt, wtt, bt = (torch.tensor(a, dtype=D64, requires_grad=True) for a in (x, wt, b))
+    yt = Fn.conv2d(xt, wtt, bt, stride=stride, padding=pad)
+    dy = r.standard_normal(tuple(yt.shape)).astype(np.float32)
+    gx, gw = torch.autograd.grad(yt, (xt, wtt), torch.tensor(dy, dtype=D64))
+    y = np.zeros(tuple(yt.shape), np.float32)
+    orc.call("orc_conv_fwd", p(x), p(wt), p(b), p(y), n, cin, h, w, cout, k, k, pad, stride)
+    dx = np.zeros_like(x)
+    orc.call("orc_conv_dgrad", p(dy), p(wt), p(dx), n, cin, h, w, cout, k, k, pad, stride)
+    dw = np.zeros_like(wt)
+    orc.call("orc_conv_wgrad", p(x), p(dy), p(dw), n, cin, h, w, cout, k, k, pad, stride)
+    assert_close(y, yt.detach().numpy(), rtol=1e-6, atol_scale=1e-6, what="conv fwd")
+    assert_close(dx, gx.numpy(), rtol=1e-6, atol_scale=1e-6, what="conv dgrad")
+    assert_close(dw, gw.numpy(), rtol=1e-6, atol_scale=1e-6, what="conv wgrad")
+
+
+# --------------------------------------------------------------------- losses
+def test_losses_closed_form(orc):
+    r = rng(60)
+    x = r.standard_normal(1000).astype(np.float32)
+    t = r.standard_normal(1000).astype(np.float32)
+    assert orc.call("orc_mse_loss", p(x), p(t), 1000) == pytest.approx(np.mean((x - t) ** 2.0), rel=1e-6)
+    dx = np.zeros_like(x)
+    orc.call("orc_mse_bwd", p(x), p(t), None, p(dx), 1000)
+    assert_close(dx, 2 * (x.astype(np.float64) - t) / 1000, rtol=1e-6, atol_scale=1e-7)
+    rows, cols, batch = 12, 9, 3
+    lg = r.standard_normal((rows, cols)).astype(np.float32)
+    tg = np.eye(cols, dtype=np.float32)[r.integers(0, cols, rows)]
+    pr = np.zeros_like(lg)
+    loss = orc.call("orc_softmax_xent_fwd", p(lg), p(tg), p(pr), rows, cols)
+    ref_p = np.exp(lg - lg.max(1, keepdims=True))
+    ref_p /= ref_p.sum(1, keepdims=True)
+    assert loss == pytest.approx(-(tg * np.log(ref_p + 1e-27)).sum() / (rows * cols), rel=1e-6)
+    dl = np.zeros_like(lg)
+    orc.call("orc_softmax_xent_bwd", p(pr), p(tg), None, p(dl), rows * cols, batch)
+    assert_close(dl, (ref_p - tg) / batch, rtol=1e-5, atol_scale=1e-7)
+
+
+# ------------------------------------------------------------------ optimizer
+@pytest.mark.parametrize("adamw", [0, 1])
+def test_adam_matches_torch_optim_over_steps(orc, adamw):
+    r = rng(70 + adamw)
+    n, lr = 5000, 3e-3
+    p0 = (r.standard_normal(n) * 0.1).astype(np.float32)
+    grads = [(r.standard_normal(n) * 0.01).astype(np.float32) for _ in range(5)]
+    w = p0.copy()
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    pt = torch.tensor(p0, dtype=D64, requires_grad=True)
+    opt = (torch.optim.AdamW([pt], lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01) if adamw
+           else torch.optim.Adam([pt], lr=lr, betas=(0.9, 0.999), eps=1e-8))
+    for t, g in enumerate(grads, start=1):
+        orc.call("orc_adam", p(w), p(g), n, t, p(m), p(v), 0.9, 0.999, 1e-8, 0.01, lr, adamw)
+        pt.grad = torch.tensor(g, dtype=D64)
+        opt.step()
+    assert_close(w, pt.detach().numpy(), rtol=1e-5, atol_scale=1e-6)
+
+
+def test_clip_closed_form(orc):
+    r = rng(80)
+    g = (r.standard_normal(20000) * 0.05).astype(np.float32)
+    acc = np.zeros(1, np.float64)
+    orc.call("orc_sumsq", p(g), g.size, p(acc))
+    assert acc[0] == pytest.approx(float(np.sum(g.astype(np.float64) ** 2)), rel=1e-12)
+    s = acc.copy()
+    orc.call("orc_sqrt_scale", p(s), 1.0)
+    assert s[0] == pytest.approx(max(math.sqrt(acc[0]), 1.0), rel=1e-15)
+    gc = g.copy()
+    orc.call("orc_clip", p(gc), gc.size, p(s))
+    assert np.linalg.norm(gc.astype(np.float64)) == pytest.approx(min(math.sqrt(acc[0]), 1.0), rel=1e-6)
+    small = np.array([0.25], np.float64)
+    orc.call("orc_sqrt_scale", p(small), 1.0)
+    assert small[0] == 1.0  # norm below 1: no clipping
+
+
+def test_adamw_single_step_closed_form(orc):
+    """From zero moments, t = 1: p1 = p0 - lr (g/(|g| + eps) + wd p0)."""
+    r = rng(81)
+    n, lr = 1000, 1e-3
+    p0 = (r.standard_normal(n) * 0.02).astype(np.float32)
+    g = (r.standard_normal(n) * 1e-2).astype(np.float32)
+    w, m, v = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    orc.call("orc_adam", p(w), p(g), n, 1, p(m), p(v), 0.9, 0.999, 1e-8, 0.01, lr, 1)
+    g64 = g.astype(np.float64)
+    assert_close(w, p0 - lr * (g64 / (np.abs(g64) + 1e-8) + 0.01 * p0), rtol=1e-6, atol_scale=1e-6)
+
+
+# ------------------------------------------------------------- index paths
+def test_index_paths(orc):
+    r = rng(90)
+    batch, clen, maxc, dim, vocab = 3, 5, 7, 4, 6
+    keys = r.integers(0, vocab, (batch, maxc)).astype(np.int32)
+    keys[0, 1] = -3
+    keys[2, 4] = np.iinfo(np.int32).min
+    table = r.standard_normal((vocab, dim)).astype(np.float32)
+    out = np.zeros((batch, clen, dim), np.float32)
+    orc.call("orc_gather", p(out), p(table), p(keys), batch, clen, maxc, dim)
+    k = keys[:, :clen]
+    want = np.where((k >= 0)[..., None], table[np.clip(k, 0, None)], 0.0)
+    np.testing.assert_array_equal(out, want)
+    grad = r.standard_normal((batch, clen, dim)).astype(np.float32)
+    tab = np.zeros_like(table)
+    orc.call("orc_scatter_add", p(tab), p(grad), p(keys), batch, clen, maxc, dim, vocab, 1.0)
+    ref = np.zeros((vocab, dim), np.float64)
+    valid = k >= 0
+    np.add.at(ref, k[valid], grad[valid].astype(np.float64))
+    assert_close(tab, ref, rtol=1e-6, atol_scale=1e-7)
+    oh = np.zeros((batch * clen, vocab), np.float32)
+    orc.call("orc_onehot", p(oh), p(keys), batch, clen, maxc, vocab)
+    assert oh.sum() == valid.sum() and np.all(oh.argmax(1)[valid.reshape(-1)] == k[valid])
+    x = r.standard_normal((4, 9)).astype(np.float32)
+    x[1, 2] = x[1, 7] = 9.0
+    am = np.zeros(4, np.int32)
+    orc.call("orc_argmax", p(x), 4, 9, p(am))
+    np.testing.assert_array_equal(am, np.argmax(x, 1))
+
+
+def test_layout_and_encodings(orc):
+    r = rng(91)
+    B, H, S, d = 2, 3, 4, 5
+    flat = r.standard_normal((B, S, H * d)).astype(np.float32)
+    out = np.zeros(B * H * S * d, np.float32)
+    orc.call("orc_headify", p(flat), p(out), B, H, S, d, 0)
+    np.testing.assert_array_equal(out.reshape(B, H, S, d), flat.reshape(B, S, H, d).transpose(0, 2, 1, 3))
+    back = np.zeros_like(flat)
+    orc.call("orc_headify", p(out), p(back), B, H, S, d, 2)
+    np.testing.assert_array_equal(back, flat)
+    x = np.zeros((2, 6, 8), np.float32)
+    y = np.zeros_like(x)
+    orc.call("orc_matpe", p(x), p(y), 2, 6, 8, 0)
+    assert_close(y[0], torch_ref.sinusoid(6, 8).numpy(), rtol=1e-6, atol_scale=1e-7)
+    te = np.zeros(16, np.float32)
+    orc.call("orc_pe", p(te), 37, 16)
+    assert_close(te, torch_ref.pe_timestep(37, 16).numpy(), rtol=1e-6, atol_scale=1e-7)
+
+
+# ------------------------------------------------------ whole training steps
+def _tables(params):
+    op = [np.ascontiguousarray(q.reshape(-1)).copy() for q in params]
+    return op, [np.zeros_like(q) for q in op], [np.zeros_like(q) for q in op], [np.zeros_like(q) for q in op]
+
+
+def test_c1_step_vs_torch(orc):
+    from ml_engine_amd.configs import MLPConfig, mlp_data
+
+    cfg = MLPConfig(batch=16, inp=30, hidden=20, classes=7)
+    x, labels, params = mlp_data(cfg)
+    op, og, om, ov = _tables(params)
+    T = orc.ptr_table
+    loss = orc.call("orc_c1_step", cfg.batch, cfg.inp, cfg.hidden, cfg.classes, p(x), p(labels), T(op), T(og), T(om),
+                    T(ov), 0.0, 1, 0, None)
+    rl, rg = torch_ref.c1_step(x, labels, params, cfg.batch, cfg.classes)
+    assert loss == pytest.approx(rl, rel=1e-5)
+    for a, b in zip(og, rg):
+        assert_close(a, b.reshape(-1), rtol=1e-4, atol_scale=1e-5)
+
+
+def test_c4_step_vs_torch(orc):
+    from ml_engine_amd.configs import BlockConfig, block_data
+
+    cfg = BlockConfig(batch=2, seq=8, d_model=16, heads=2, ffn=32, vocab=11)
+    ids, tgt, params = block_data(cfg)
+    op, og, om, ov = _tables(params)
+    T = orc.ptr_table
+    loss = orc.call("orc_c4_step", cfg.batch, cfg.seq, cfg.d_model, cfg.heads, cfg.ffn, cfg.vocab, p(ids), p(tgt),
+                    T(op), T(og), T(om), T(ov), 0.0, 1, 1)
+    rl, rg = torch_ref.c4_step(ids, tgt, params, cfg.batch, cfg.seq, cfg.d_model, cfg.heads, cfg.ffn, cfg.vocab)
+    assert loss == pytest.approx(rl, rel=1e-5)
+    for i, (a, b) in enumerate(zip(og, rg)):
+        s = max(np.abs(rg[i]).max(), np.abs(rg[i - 1]).max()) if i >= 2 and i % 2 == 0 else None
+        assert_close(a, b, rtol=1e-4, atol_scale=1e-4, scale=s, what=f"c4 grad {i}")
+
+
+@pytest.mark.parametrize("exact", [0, 1])
+def test_c5_step_vs_torch(orc, exact):
+    from ml_engine_amd.configs import ResBlockConfig, resblock_data
+
+    cfg = ResBlockConfig(batch=2, cin=3, cout=8, h=6, w=5, groups=4, tdim=8)
+    x, noise, t, params = resblock_data(cfg)
+    op, og, om, ov = _tables(params)
+    T = orc.ptr_table
+    loss = orc.call("orc_c5_step", cfg.batch, cfg.cin, cfg.cout, cfg.h, cfg.w, cfg.groups, cfg.tdim, t, p(x), p(noise),
+                    T(op), T(og), T(om), T(ov), 0.0, 1, exact)
+    rl, rg = torch_ref.c5_step(x, noise, t, params, cfg.groups)
+    assert loss == pytest.approx(rl, rel=1e-5)
+    for i, (a, b) in enumerate(zip(og, rg)):
+        if not exact and i in (6, 7):
+            # Broadcast_Channel reduces only the first `width` channels of the
+            # time projection's gradient: those match, the rest stay zero.
+            keep = np.zeros(cfg.cout, bool)
+            keep[: cfg.w] = True
+            mask = np.tile(keep, b.size // cfg.cout)
+            assert_close(a[mask], b[mask], rtol=1e-4, atol_scale=1e-4, scale=np.abs(b).max(), what=f"c5 grad {i}")
+            assert np.all(a[~mask] == 0)
+            continue
+        assert_close(a, b, rtol=1e-4, atol_scale=1e-4, what=f"c5 grad {i}")
