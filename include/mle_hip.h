@@ -142,6 +142,17 @@ int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, f
              const float* B, int64_t ldb, int64_t stride_b, float beta,
              float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum);
 
+/* Workspace that lets mle_gemm_ws split K across workgroups when the tile grid
+ * alone would leave most CUs idle (0 when no split is used for this shape). */
+size_t mle_gemm_ws_bytes(int M, int N, int K, int batch);
+/* mle_gemm with a workspace: the K range is split over workgroups and the
+ * partial tiles are summed in split order (deterministic for a given shape). */
+int mle_gemm_ws(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+                const float* A, int64_t lda, int64_t stride_a,
+                const float* B, int64_t ldb, int64_t stride_b, float beta,
+                float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum,
+                void* ws, size_t ws_bytes);
+
 /* out[c] (+)= sum_r x[r, c].  BCompress (Engine/kernels.cu:1562-1584); beta 0/1. */
 int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* out, float beta);
 /* out[c] += sum_{b, s} x[b, c, s] for c < nreduce (nreduce <= channels).

@@ -18,6 +18,12 @@ struct GemmArgs {
   int64_t lda, ldb, ldc, sa, sb, sc;
   int M, N, K;
   float alpha, beta;
+  // split-K: blockIdx.z = batch item * splits + split; each split covers
+  // kchunk of K and writes its raw tile to part (and its column sums to
+  // part_cs); split_reduce_kernel combines them in split order.
+  int splits, kchunk;
+  float* part;
+  float* part_cs;
 };
 
 // Load 4 consecutive elements base[r*ld + c .. c+3] with bounds (R rows, Cc cols).
@@ -39,22 +45,25 @@ __device__ __forceinline__ f32x4 ld_guard(const float* __restrict__ base, int64_
 
 // Global -> registers for one stage.  Tiles are 4096 floats = 1024 float4,
 // four per thread.  A_MC == trans_a (A stored K x M); B_KC == trans_b.
+// `kend` bounds K for this workgroup's split.
 template <bool A_MC, bool VEC>
-__device__ __forceinline__ void load_a(const GemmArgs& g, const float* A, int m0, int k0, int tid, f32x4 (&r)[4]) {
+__device__ __forceinline__ void load_a(const GemmArgs& g, const float* A, int m0, int k0, int kend, int tid,
+                                       f32x4 (&r)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int f = tid + NT * i;
-    if (!A_MC) r[i] = ld_guard<VEC>(A, g.lda, m0 + (f >> 3), k0 + (f & 7) * 4, g.M, g.K);
-    else r[i] = ld_guard<VEC>(A, g.lda, k0 + (f >> 5), m0 + (f & 31) * 4, g.K, g.M);
+    if (!A_MC) r[i] = ld_guard<VEC>(A, g.lda, m0 + (f >> 3), k0 + (f & 7) * 4, g.M, kend);
+    else r[i] = ld_guard<VEC>(A, g.lda, k0 + (f >> 5), m0 + (f & 31) * 4, kend, g.M);
   }
 }
 template <bool B_KC, bool VEC>
-__device__ __forceinline__ void load_b(const GemmArgs& g, const float* B, int n0, int k0, int tid, f32x4 (&r)[4]) {
+__device__ __forceinline__ void load_b(const GemmArgs& g, const float* B, int n0, int k0, int kend, int tid,
+                                       f32x4 (&r)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int f = tid + NT * i;
-    if (B_KC) r[i] = ld_guard<VEC>(B, g.ldb, n0 + (f >> 3), k0 + (f & 7) * 4, g.N, g.K);
-    else r[i] = ld_guard<VEC>(B, g.ldb, k0 + (f >> 5), n0 + (f & 31) * 4, g.K, g.N);
+    if (B_KC) r[i] = ld_guard<VEC>(B, g.ldb, n0 + (f >> 3), k0 + (f & 7) * 4, g.N, kend);
+    else r[i] = ld_guard<VEC>(B, g.ldb, k0 + (f >> 5), n0 + (f & 31) * 4, kend, g.N);
   }
 }
 // Registers -> LDS (same element mapping as the loads).
@@ -81,10 +90,13 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   const int lr = lane & 15, q = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int64_t z = blockIdx.z;
+  const int64_t z = blockIdx.z / g.splits;
+  const int split = blockIdx.z % g.splits;
   const float* A = g.A + z * g.sa;
   const float* B = g.B + z * g.sb;
   float* C = g.C + z * g.sc;
+  const int kbeg = split * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -94,11 +106,11 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
 
   const bool do_cs = COLSUM && blockIdx.y == 0;
   float csum = 0.f;
-  const int nk = (g.K + BK - 1) / BK;
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   f32x4 ra[4], rb[4];
   if (nk > 0) {
-    load_a<A_MC, VEC>(g, A, m0, 0, tid, ra);
-    load_b<B_KC, VEC>(g, B, n0, 0, tid, rb);
+    load_a<A_MC, VEC>(g, A, m0, kbeg, kend, tid, ra);
+    load_b<B_KC, VEC>(g, B, n0, kbeg, kend, tid, rb);
     store_tile<!A_MC>(smem, tid, ra);
     store_tile<B_KC>(smem + 2 * ASZ, tid, rb);
   }
@@ -110,8 +122,8 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
     const float* Bs = smem + 2 * ASZ + cur * BSZ;
     const bool more = kt + 1 < nk;
     if (more) {
-      load_a<A_MC, VEC>(g, A, m0, (kt + 1) * BK, tid, ra);
-      load_b<B_KC, VEC>(g, B, n0, (kt + 1) * BK, tid, rb);
+      load_a<A_MC, VEC>(g, A, m0, kbeg + (kt + 1) * BK, kend, tid, ra);
+      load_b<B_KC, VEC>(g, B, n0, kbeg + (kt + 1) * BK, kend, tid, rb);
     }
     mma_stage<A_MC, B_KC>(As, Bs, acc, wm, wn, lr, q);
     if (do_cs) {
@@ -127,6 +139,8 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   }
 
   const float alpha = g.alpha, beta = g.beta;
+  const bool split_mode = g.splits > 1;
+  float* P = split_mode ? g.part + (int64_t)blockIdx.z * g.M * g.N : nullptr;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -137,10 +151,14 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + acc_row(wm, i, q, r);
         if (row < g.M) {
-          float* p = C + (int64_t)row * g.ldc + col;
-          float v = alpha * acc[i][n][r];
-          if (beta != 0.f) v += beta * *p;
-          *p = v;
+          if (split_mode) {
+            P[(int64_t)row * g.N + col] = acc[i][n][r];
+          } else {
+            float* p = C + (int64_t)row * g.ldc + col;
+            float v = alpha * acc[i][n][r];
+            if (beta != 0.f) v += beta * *p;
+            *p = v;
+          }
         }
       }
     }
@@ -149,8 +167,54 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
     // smem is free after the final barrier of the K loop.
     smem[tid] = csum;
     __syncthreads();
-    if (tid < 128 && n0 + tid < g.N) g.colsum[n0 + tid] += smem[tid] + smem[tid + 128];
+    if (tid < 128 && n0 + tid < g.N) {
+      const float cs = smem[tid] + smem[tid + 128];
+      if (split_mode) g.part_cs[(int64_t)split * g.N + n0 + tid] = cs;
+      else g.colsum[n0 + tid] += cs;
+    }
   }
+}
+
+// C = alpha * sum_s part[s] + beta * C and colsum += sum_s part_cs[s], in split order.
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g, int batch) {
+  const int64_t mn = (int64_t)g.M * g.N;
+  const int64_t total = mn * batch;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    const int64_t b = i / mn, e = i - b * mn;
+    const int row = (int)(e / g.N), col = (int)(e - (int64_t)row * g.N);
+    const float* p = g.part + b * g.splits * mn + e;
+    float acc = 0.f;
+    for (int s = 0; s < g.splits; ++s) acc += p[s * mn];
+    float* c = g.C + b * g.sc + (int64_t)row * g.ldc + col;
+    float v = g.alpha * acc;
+    if (g.beta != 0.f) v += g.beta * *c;
+    *c = v;
+  }
+  if (g.colsum) {
+    for (int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x; n < g.N; n += stride) {
+      float acc = 0.f;
+      for (int s = 0; s < g.splits; ++s) acc += g.part_cs[(int64_t)s * g.N + n];
+      g.colsum[n] += acc;
+    }
+  }
+}
+
+// Split count: a function of the shape only.  Splits are used when the tile
+// grid leaves most of the 256 CUs idle and K is long enough to share.
+int choose_splits(int M, int N, int K, int batch, int& kchunk) {
+  kchunk = K;
+  const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN) * batch;
+  if (tiles >= 384) return 1;
+  int s = (int)((768 + tiles - 1) / tiles);
+  const int smax = K / 256;
+  if (s > smax) s = smax;
+  if (s < 2) return 1;
+  kchunk = (K + s - 1) / s;
+  kchunk = ((kchunk + BK - 1) / BK) * BK;
+  s = (K + kchunk - 1) / kchunk;
+  if ((long long)s * batch > 65535) return 1;
+  return s;
 }
 
 template <int TA, int TB>
@@ -166,34 +230,74 @@ void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, bool vec, bool cs) {
 
 }  // namespace
 
-extern "C" int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
-                        const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
-                        int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c, int batch,
-                        float* colsum) {
+static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                     int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
+                     int64_t ldc, int64_t stride_c, int batch, float* colsum, void* ws, size_t ws_bytes) {
   MLE_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "mle_gemm: negative size");
   if (M == 0 || N == 0 || batch == 0) return MLE_OK;
   MLE_CHECK_ARG(C != nullptr && (K == 0 || (A != nullptr && B != nullptr)), "mle_gemm: null operand");
   MLE_CHECK_ARG(ldc >= N, "mle_gemm: ldc %lld < N %d", (long long)ldc, N);
   MLE_CHECK_ARG(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "mle_gemm: leading dimension too small");
   MLE_CHECK_ARG(colsum == nullptr || batch == 1, "mle_gemm: fused colsum needs batch == 1");
-  MLE_CHECK_ARG((N + BN - 1) / BN <= 2147483647 && (M + BM - 1) / BM <= 65535 && batch <= 65535,
-                "mle_gemm: grid too large (M %d, batch %d)", M, batch);
-  GemmArgs g{A, B, C, colsum, lda, ldb, ldc, stride_a, stride_b, stride_c, M, N, K, alpha, beta};
+  MLE_CHECK_ARG((M + BM - 1) / BM <= 65535 && batch <= 65535, "mle_gemm: grid too large (M %d, batch %d)", M, batch);
+  GemmArgs g{A, B, C, colsum, lda, ldb, ldc, stride_a, stride_b, stride_c, M, N, K, alpha, beta, 1, K, nullptr, nullptr};
+  int kchunk = K;
+  const int splits = ws ? choose_splits(M, N, K, batch, kchunk) : 1;
+  if (splits > 1) {
+    const size_t need = mle_gemm_ws_bytes(M, N, K, batch);
+    if (ws_bytes >= need) {
+      g.splits = splits;
+      g.kchunk = kchunk;
+      g.part = static_cast<float*>(ws);
+      g.part_cs = g.part + (size_t)splits * batch * M * N;
+    }
+  }
   const bool vec = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
                    aligned16(A) && aligned16(B);
   const bool cs = colsum != nullptr;
-  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, batch);
+  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, batch * g.splits);
   hipStream_t s = as_stream(stream);
   static const char* names[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
   const int which = (trans_a ? 2 : 0) + (trans_b ? 1 : 0);
   const double flop = 2.0 * M * (double)N * K * batch;
   const double bytes = 4.0 * batch * ((double)M * K + (double)K * N + (double)M * N * (beta != 0.f ? 2 : 1));
-  ProbeScope probe(names[which], s, flop, bytes);
-  switch (which) {
-    case 0: launch_t<0, 0>(s, g, grid, vec, cs); break;
-    case 1: launch_t<0, 1>(s, g, grid, vec, cs); break;
-    case 2: launch_t<1, 0>(s, g, grid, vec, cs); break;
-    default: launch_t<1, 1>(s, g, grid, vec, cs); break;
+  {
+    ProbeScope probe(names[which], s, flop, bytes);
+    switch (which) {
+      case 0: launch_t<0, 0>(s, g, grid, vec, cs); break;
+      case 1: launch_t<0, 1>(s, g, grid, vec, cs); break;
+      case 2: launch_t<1, 0>(s, g, grid, vec, cs); break;
+      default: launch_t<1, 1>(s, g, grid, vec, cs); break;
+    }
+    if (g.splits > 1) {
+      const size_t total = (size_t)M * N * batch;
+      split_reduce_kernel<<<stream_grid(total, 256, 4096), 256, 0, s>>>(g, batch);
+    }
   }
   return check_launch(names[which]);
 }
+
+extern "C" {
+
+size_t mle_gemm_ws_bytes(int M, int N, int K, int batch) {
+  int kchunk;
+  const int splits = choose_splits(M, N, K, batch, kchunk);
+  if (splits <= 1) return 0;
+  return ((size_t)splits * batch * M * N + (size_t)splits * N) * sizeof(float);
+}
+
+int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+             int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
+             int64_t ldc, int64_t stride_c, int batch, float* colsum) {
+  return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                   stride_c, batch, colsum, nullptr, 0);
+}
+
+int mle_gemm_ws(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
+                int64_t ldc, int64_t stride_c, int batch, float* colsum, void* ws, size_t ws_bytes) {
+  return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                   stride_c, batch, colsum, ws, ws_bytes);
+}
+
+}  // extern "C"

@@ -101,6 +101,17 @@ void* alloc_scratch(size_t bytes) {
   return g_scratch.take(bytes);
 }
 
+void* gemm_workspace(size_t bytes) {
+  static void* ws = nullptr;
+  static size_t cap = 0;
+  if (bytes == 0) return ws;
+  if (bytes > cap) {
+    ws = alloc_scratch(bytes);
+    cap = bytes;
+  }
+  return ws;
+}
+
 // ---------------------------------------------------------------------------
 // batched zeroing
 namespace {
@@ -742,18 +753,23 @@ graph Linear::forward(const graph& X) {
   NodeBackProp* x = X.get();
   const str name = op_name;
   node->params = has_bias ? std::vector<AdamParameter*>{W, Bb} : std::vector<AdamParameter*>{W};
+  const size_t ws_f = mle_gemm_ws_bytes((int)rows, p, n, 1);
+  const size_t ws_dx = mle_gemm_ws_bytes((int)rows, n, p, 1);
+  const size_t ws_dw = mle_gemm_ws_bytes(n, p, (int)rows, 1);
+  const size_t ws_bytes = std::max(ws_f, std::max(ws_dx, ws_dw));
+  void* ws = mle::gemm_workspace(ws_bytes);
   node->forward = [=]() {
-    check(mle_gemm(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, 0, W->output, p, 0, 0.0f, nd->output, p, 0,
-                   1, nullptr),
+    check(mle_gemm_ws(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, 0, W->output, p, 0, 0.0f, nd->output,
+                      p, 0, 1, nullptr, ws, ws_bytes),
           "MatMul... X*W1 in " + name + " forward");
     if (has_bias) check(mle_bias_add_rows(mle::stream(), nd->output, Bb->output, rows, p), "BCumAdd in " + name);
   };
   node->backward = [=]() {
-    check(mle_gemm(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, 0, W->output, p, 0, 1.0f, x->grad, n, 0, 1,
-                   nullptr),
+    check(mle_gemm_ws(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, 0, W->output, p, 0, 1.0f, x->grad, n, 0,
+                      1, nullptr, ws, ws_bytes),
           "MatMul... dZ*W^T in " + name + " backward");
-    check(mle_gemm(mle::stream(), 1, 0, n, p, (int)rows, 1.0f, x->output, n, 0, nd->grad, p, 0, 1.0f, W->grad, p, 0, 1,
-                   has_bias ? Bb->grad : nullptr),
+    check(mle_gemm_ws(mle::stream(), 1, 0, n, p, (int)rows, 1.0f, x->output, n, 0, nd->grad, p, 0, 1.0f, W->grad, p, 0,
+                      1, has_bias ? Bb->grad : nullptr, ws, ws_bytes),
           "MatMul... X^T*dZ in " + name + " backward");
   };
   node->free = [=]() { nd->clear(); };

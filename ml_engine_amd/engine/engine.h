@@ -60,6 +60,10 @@ float* alloc_grad(size_t n);
 void release(float* p, size_t n, bool grad);
 // Scratch owned by a node (workspaces, statistics).
 void* alloc_scratch(size_t bytes);
+// Shared GEMM split-K workspace of at least `bytes`.  All engine kernels run
+// in order on one stream, so one buffer serves every GEMM; a larger request
+// allocates a larger buffer (earlier ones stay valid for their users).
+void* gemm_workspace(size_t bytes);
 
 // Zero a gradient range.  Inside a ZeroBatch scope the range is recorded and
 // merged with its neighbours instead of launching one fill per node.

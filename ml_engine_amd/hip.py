@@ -53,6 +53,8 @@ SIGNATURES: dict[str, tuple] = {
     "mle_act_fwd": (I, [P, I, P, P, SZ]),
     "mle_act_bwd": (I, [P, I, P, P, P, SZ]),
     "mle_gemm": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P]),
+    "mle_gemm_ws_bytes": (SZ, [I, I, I, I]),
+    "mle_gemm_ws": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P, P, SZ]),
     "mle_colsum": (I, [P, P, SZ, I, P, F]),
     "mle_channel_sum": (I, [P, P, I, I, SZ, I, P]),
     "mle_softmax_fwd": (I, [P, P, P, I, I, I, I, I]),

@@ -58,6 +58,36 @@ def test_gemm(hip, orc, ta, tb, M, N, K, batch, beta):
     assert_close(dC.numpy(), ref, what=f"gemm ta={ta} tb={tb}", **MM)
 
 
+@pytest.mark.parametrize("ta,tb,M,N,K,batch,cs", [
+    (1, 0, 256, 256, 8192, 1, True),    # dW of a small Linear: split over K
+    (1, 0, 512, 1000, 4100, 1, True),   # ragged N and K
+    (0, 1, 300, 200, 3000, 1, False),
+    (0, 0, 128, 130, 2048, 3, False),   # batched split
+])
+def test_gemm_split_k(hip, orc, ta, tb, M, N, K, batch, cs):
+    r = rng(M + N + K)
+    a_shape = (batch, K, M) if ta else (batch, M, K)
+    b_shape = (batch, N, K) if tb else (batch, K, N)
+    A = r.standard_normal(a_shape, dtype=np.float32)
+    Bm = r.standard_normal(b_shape, dtype=np.float32)
+    C0 = r.standard_normal((batch, M, N), dtype=np.float32)
+    ref = C0.copy()
+    orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(A), orc.ptr(Bm), orc.ptr(ref), batch, 1, M, K, N, 1, 3, 3, 3, 0.75)
+    L = hip.lib()
+    need = L.mle_gemm_ws_bytes(M, N, K, batch)
+    assert need > 0, "shape expected to split"
+    ws = hip.Buffer(need)
+    dA, dB, dC = B(hip, A), B(hip, Bm), B(hip, C0)
+    cs0 = r.standard_normal(N, dtype=np.float32)
+    dcs = B(hip, cs0) if cs else None
+    hip.call("mle_gemm_ws", None, ta, tb, M, N, K, 0.75, dA.ptr, M if ta else K, A[0].size, dB.ptr, K if tb else N,
+             Bm[0].size, 1.0, dC.ptr, N, M * N, batch, dcs.ptr if cs else None, ws.ptr, ws.nbytes)
+    assert_close(dC.numpy(), ref, what="split-K gemm", **MM)
+    if cs:
+        bsum = Bm[0].astype(np.float64).sum(1 if tb else 0)
+        assert_close(dcs.numpy(), cs0 + bsum, what="split-K colsum", **EW)
+
+
 def test_gemm_broadcast_and_colsum(hip, orc):
     r = rng(7)
     M, N, K, batch = 96, 80, 72, 3

@@ -40,7 +40,7 @@ def c1_step(x, labels, params, batch, classes):
     onehot = Fn.one_hot(torch.tensor(labels, dtype=torch.long), classes).to(D64)
     (-(onehot * Fn.log_softmax(z, dim=-1)).sum() / batch).backward()
     p = torch.softmax(z, dim=-1)
-    loss = float((-(onehot * torch.log(p + 1e-27))).sum() / p.numel())
+    loss = float((-(onehot * torch.log(p.detach() + 1e-27))).sum() / p.numel())
     return loss, [t.grad.numpy() for t in (W1, b1, W2, b2)]
 
 
@@ -63,7 +63,7 @@ def c4_step(ids, tgt, params, B, S, D, H, F, V):
     onehot = Fn.one_hot(torch.tensor(tgt, dtype=torch.long), V).to(D64)
     (-(onehot * Fn.log_softmax(logits, dim=-1)).sum() / B).backward()
     p = torch.softmax(logits, dim=-1)
-    loss = float((-(onehot * torch.log(p + 1e-27))).sum() / p.numel())
+    loss = float((-(onehot * torch.log(p.detach() + 1e-27))).sum() / p.numel())
     return loss, [t.grad.numpy().reshape(-1) for t in ps]
 
 
@@ -85,4 +85,4 @@ def c5_step(x, noise, t, params, groups):
     out = Fn.silu(h + Fn.conv2d(xt, Ws, bs))
     loss = Fn.mse_loss(out, t64(noise, grad=False))
     loss.backward()
-    return float(loss), [q.grad.numpy().reshape(-1) for q in ps]
+    return float(loss.detach()), [q.grad.numpy().reshape(-1) for q in ps]
