@@ -142,16 +142,19 @@ int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, f
              const float* B, int64_t ldb, int64_t stride_b, float beta,
              float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum);
 
-/* Workspace that lets mle_gemm_ws split K across workgroups when the tile grid
+/* Workspace that lets mle_gemm_ex split K across workgroups when the tile grid
  * alone would leave most CUs idle (0 when no split is used for this shape). */
 size_t mle_gemm_ws_bytes(int M, int N, int K, int batch);
-/* mle_gemm with a workspace: the K range is split over workgroups and the
- * partial tiles are summed in split order (deterministic for a given shape). */
-int mle_gemm_ws(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+/* mle_gemm plus two fusions:
+ *   bias (nullable): C[b][r, c] += bias[c] after alpha/beta -- the Linear
+ *     forward's BCumAdd (Engine/kernels.cu:1586-1592) in the GEMM epilogue;
+ *   ws (nullable): split K over workgroups; partial tiles are summed in split
+ *     order, so results are deterministic for a given shape. */
+int mle_gemm_ex(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
                 const float* A, int64_t lda, int64_t stride_a,
                 const float* B, int64_t ldb, int64_t stride_b, float beta,
                 float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum,
-                void* ws, size_t ws_bytes);
+                const float* bias, void* ws, size_t ws_bytes);
 
 /* out[c] (+)= sum_r x[r, c].  BCompress (Engine/kernels.cu:1562-1584); beta 0/1. */
 int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* out, float beta);
@@ -275,6 +278,13 @@ int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, co
 /* out[(b*clen + s)*vocab + key] = 1 for valid keys (out must be zeroed).
  * OneHotEmbeddings (Engine/kernels.cu:1551-1560). */
 int mle_onehot(mle_stream stream, float* out, const int32_t* keys, int batch, int clen, int max_clen, int vocab);
+/* One-hot targets kept up to date across steps: for each token, clear
+ * out[token, prev_keys[token]], set out[token, key] and store the key in
+ * prev_keys (-1 when invalid).  `out` must be all zero when prev_keys is all -1.
+ * Equivalent to fill(0) + OneHotEmbeddings (Engine/transformer.cu:190-196)
+ * without rewriting the whole [tokens x vocab] matrix every step. */
+int mle_onehot_update(mle_stream stream, float* out, int32_t* prev_keys, const int32_t* keys,
+                      int batch, int clen, int max_clen, int vocab);
 /* out[r] = first index of the maximum of row r (strict >).  ArgMax (Engine/kernels.cu:2353-2366). */
 int mle_argmax(mle_stream stream, const float* x, int rows, int cols, int32_t* out);
 

@@ -216,17 +216,42 @@ __global__ __launch_bounds__(256) void headify_kernel(const float* __restrict__ 
   }
 }
 
-__global__ __launch_bounds__(256) void matpe_kernel(const float* __restrict__ x, float* __restrict__ y, size_t total,
-                                                    int rows, int cols, int start) {
+// Same mapping moving 4 consecutive head_dim elements per thread (head_dim % 4 == 0).
+__global__ __launch_bounds__(256) void headify4_kernel(const float* __restrict__ in, float* __restrict__ out, int B,
+                                                       int H, int S, int D, int flag) {
+  const int D4 = D / 4;
+  const size_t total4 = (size_t)B * H * S * D4;
   const size_t stride = (size_t)gridDim.x * 256;
-  for (size_t g = (size_t)blockIdx.x * 256 + threadIdx.x; g < total; g += stride) {
-    const int pos = (int)((g % ((size_t)rows * cols)) / cols) + start;
+  const size_t E = (size_t)H * D;
+  for (size_t i4 = (size_t)blockIdx.x * 256 + threadIdx.x; i4 < total4; i4 += stride) {
+    const size_t d = (i4 % D4) * 4;
+    const size_t s = (i4 / D4) % S;
+    const size_t h = (i4 / ((size_t)D4 * S)) % H;
+    const size_t b = i4 / ((size_t)D4 * S * H);
+    const size_t idx = i4 * 4;
+    const size_t flat = b * (S * E) + s * E + h * D + d;
+    if (flag == 0) *reinterpret_cast<f32x4*>(out + idx) = ld4(in, flat);
+    else if (flag == 1) st4(out, flat, ld4(out, flat) + ld4(in, idx));
+    else if (flag == 2) st4(out, flat, ld4(in, idx));
+    else st4(out, idx, ld4(out, idx) + ld4(in, flat));
+  }
+}
+
+// Each thread evaluates the encoding of one (position, dim) once -- in double,
+// as MatPEncoding does -- and applies it to every batch item.
+__global__ __launch_bounds__(256) void matpe_kernel(const float* __restrict__ x, float* __restrict__ y, int batch,
+                                                    int rows, int cols, int start) {
+  const size_t plane = (size_t)rows * cols;
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t g = (size_t)blockIdx.x * 256 + threadIdx.x; g < plane; g += stride) {
+    const int pos = (int)(g / cols) + start;
     const int dim = (int)(g % cols);
     const int i = dim / 2;
     const double expo = (2.0 * i) / cols;
     const double freq = 1.0 / pow(10000.0, expo);
     const double ang = (double)pos * freq;
-    y[g] = x[g] + ((dim % 2 == 0) ? (float)sin(ang) : (float)cos(ang));
+    const float pe = (dim % 2 == 0) ? (float)sin(ang) : (float)cos(ang);
+    for (int b = 0; b < batch; ++b) y[b * plane + g] = x[b * plane + g] + pe;
   }
 }
 
@@ -313,8 +338,12 @@ int mle_headify(mle_stream stream, const float* in, float* out, int batch, int h
   MLE_CHECK_ARG(in && out && flag >= 0 && flag <= 3, "mle_headify: bad argument");
   const size_t total = (size_t)batch * heads * seq * head_dim;
   if (total == 0) return MLE_OK;
-  headify_kernel<<<stream_grid(total, 256, 8192), 256, 0, as_stream(stream)>>>(in, out, batch, heads, seq, head_dim,
-                                                                               flag);
+  if (head_dim % 4 == 0 && aligned16(in) && aligned16(out))
+    headify4_kernel<<<stream_grid(total / 4, 256, 8192), 256, 0, as_stream(stream)>>>(in, out, batch, heads, seq,
+                                                                                      head_dim, flag);
+  else
+    headify_kernel<<<stream_grid(total, 256, 8192), 256, 0, as_stream(stream)>>>(in, out, batch, heads, seq, head_dim,
+                                                                                 flag);
   return check_launch("mle_headify");
 }
 
@@ -322,7 +351,8 @@ int mle_matpe(mle_stream stream, const float* x, float* y, int batch, int rows, 
   MLE_CHECK_ARG(x && y && rows > 0 && cols > 0, "mle_matpe: bad argument");
   const size_t total = (size_t)batch * rows * cols;
   if (total == 0) return MLE_OK;
-  matpe_kernel<<<stream_grid(total, 256, 8192), 256, 0, as_stream(stream)>>>(x, y, total, rows, cols, start_idx);
+  matpe_kernel<<<stream_grid((size_t)rows * cols, 256, 8192), 256, 0, as_stream(stream)>>>(x, y, batch, rows, cols,
+                                                                                         start_idx);
   return check_launch("mle_matpe");
 }
 

@@ -143,6 +143,72 @@ __global__ __launch_bounds__(NT) void segment_add_kernel(float* __restrict__ tab
   }
 }
 
+// Row-centric scatter-add: one wave per table row scans every token's key (a
+// chunk at a time, staged in LDS) and sums the matching gradient rows in token
+// order.  No sort and no atomics; used when vocab * tokens is moderate.
+constexpr int ROW_CHUNK = 2048;
+constexpr int ROW_DMAX = 16;  // dims per lane -> dim <= 1024
+__global__ __launch_bounds__(256) void row_scatter_kernel(float* __restrict__ table, const float* __restrict__ grad,
+                                                          const int32_t* __restrict__ keys, int clen, int max_clen,
+                                                          int ntok, int dim, int vocab, float scale) {
+  __shared__ int sk[ROW_CHUNK];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int v = blockIdx.x * 4 + wave;
+  float acc[ROW_DMAX];
+#pragma unroll
+  for (int j = 0; j < ROW_DMAX; ++j) acc[j] = 0.f;
+  bool hit = false;
+  for (int t0 = 0; t0 < ntok; t0 += ROW_CHUNK) {
+    const int cnt = min(ROW_CHUNK, ntok - t0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < cnt; i += 256) {
+      const int t = t0 + i;
+      sk[i] = keys[(size_t)(t / clen) * max_clen + (t % clen)];
+    }
+    __syncthreads();
+    if (v >= vocab) continue;
+    for (int c = 0; c < cnt; c += 64) {
+      const int i = c + lane;
+      const bool m = (i < cnt) && sk[i] == v;
+      unsigned long long mask = __ballot(m);
+      while (mask) {
+        const int bit = __ffsll((long long)mask) - 1;
+        mask &= mask - 1;
+        const float* gr = grad + (size_t)(t0 + c + bit) * dim;
+        hit = true;
+#pragma unroll
+        for (int j = 0; j < ROW_DMAX; ++j) {
+          const int d = lane + 64 * j;
+          if (d < dim) acc[j] += gr[d];
+        }
+      }
+    }
+  }
+  if (v >= vocab || !hit) return;
+  float* tr = table + (size_t)v * dim;
+#pragma unroll
+  for (int j = 0; j < ROW_DMAX; ++j) {
+    const int d = lane + 64 * j;
+    if (d < dim) tr[d] += scale * acc[j];
+  }
+}
+
+// Incremental one-hot: clear each token's previous position, set the new one,
+// remember it.  Rows belong to tokens, so tokens never touch the same element.
+__global__ __launch_bounds__(256) void onehot_update_kernel(float* __restrict__ out, int32_t* __restrict__ prev,
+                                                            const int32_t* __restrict__ keys, int clen, int max_clen,
+                                                            int vocab, size_t total) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t g = (size_t)blockIdx.x * 256 + threadIdx.x; g < total; g += stride) {
+    const int old = prev[g];
+    if (old >= 0 && old < vocab) out[g * vocab + old] = 0.0f;
+    const int key = keys[(g / clen) * max_clen + (g % clen)];
+    const bool ok = !(key == INT_MIN || key < 0 || key >= vocab);
+    if (ok) out[g * vocab + key] = 1.0f;
+    prev[g] = ok ? key : -1;
+  }
+}
+
 // out[c] (+)= sum_r x[r, c]: 64 columns per block, 16 row lanes, fixed order.
 __global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ x, size_t rows, int cols,
                                                       float* __restrict__ out, float beta) {
@@ -208,6 +274,10 @@ int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, co
   if (ws_bytes < mle_embed_scatter_ws_bytes(batch, clen))
     return set_error(MLE_ERR_WORKSPACE, "mle_embed_scatter_add: workspace too small");
   hipStream_t s = as_stream(stream);
+  if ((double)vocab * (double)ntok <= (double)(1u << 30) && dim <= 64 * ROW_DMAX) {
+    row_scatter_kernel<<<(vocab + 3) / 4, 256, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab, scale);
+    return check_launch("mle_embed_scatter_add");
+  }
   unsigned long long* sorted = static_cast<unsigned long long*>(ws);
   // Chunks of SORT_CAP tokens are applied in token order, so every table row
   // receives its updates in a fixed order.
@@ -227,6 +297,16 @@ int mle_onehot(mle_stream stream, float* out, const int32_t* keys, int batch, in
   if (total == 0) return MLE_OK;
   onehot_kernel<<<stream_grid(total, NT, 8192), NT, 0, as_stream(stream)>>>(out, keys, clen, max_clen, vocab, total);
   return check_launch("mle_onehot");
+}
+
+int mle_onehot_update(mle_stream stream, float* out, int32_t* prev_keys, const int32_t* keys, int batch, int clen,
+                      int max_clen, int vocab) {
+  MLE_CHECK_ARG(out && prev_keys && keys && clen > 0 && max_clen >= clen && vocab > 0, "mle_onehot_update: bad argument");
+  const size_t total = (size_t)batch * clen;
+  if (total == 0) return MLE_OK;
+  onehot_update_kernel<<<stream_grid(total, NT, 8192), NT, 0, as_stream(stream)>>>(out, prev_keys, keys, clen, max_clen,
+                                                                                   vocab, total);
+  return check_launch("mle_onehot_update");
 }
 
 int mle_argmax(mle_stream stream, const float* x, int rows, int cols, int32_t* out) {

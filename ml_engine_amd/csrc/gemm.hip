@@ -24,6 +24,7 @@ struct GemmArgs {
   int splits, kchunk;
   float* part;
   float* part_cs;
+  const float* bias;  // nullable: C[r, c] += bias[c] after alpha/beta
 };
 
 // Load 4 consecutive elements base[r*ld + c .. c+3] with bounds (R rows, Cc cols).
@@ -157,6 +158,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
             float* p = C + (int64_t)row * g.ldc + col;
             float v = alpha * acc[i][n][r];
             if (beta != 0.f) v += beta * *p;
+            if (g.bias) v += g.bias[col];
             *p = v;
           }
         }
@@ -189,6 +191,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g, int batch
     float* c = g.C + b * g.sc + (int64_t)row * g.ldc + col;
     float v = g.alpha * acc;
     if (g.beta != 0.f) v += g.beta * *c;
+    if (g.bias) v += g.bias[col];
     *c = v;
   }
   if (g.colsum) {
@@ -232,7 +235,8 @@ void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, bool vec, bool cs) {
 
 static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
                      int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
-                     int64_t ldc, int64_t stride_c, int batch, float* colsum, void* ws, size_t ws_bytes) {
+                     int64_t ldc, int64_t stride_c, int batch, float* colsum, const float* bias, void* ws,
+                     size_t ws_bytes) {
   MLE_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "mle_gemm: negative size");
   if (M == 0 || N == 0 || batch == 0) return MLE_OK;
   MLE_CHECK_ARG(C != nullptr && (K == 0 || (A != nullptr && B != nullptr)), "mle_gemm: null operand");
@@ -240,7 +244,8 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   MLE_CHECK_ARG(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "mle_gemm: leading dimension too small");
   MLE_CHECK_ARG(colsum == nullptr || batch == 1, "mle_gemm: fused colsum needs batch == 1");
   MLE_CHECK_ARG((M + BM - 1) / BM <= 65535 && batch <= 65535, "mle_gemm: grid too large (M %d, batch %d)", M, batch);
-  GemmArgs g{A, B, C, colsum, lda, ldb, ldc, stride_a, stride_b, stride_c, M, N, K, alpha, beta, 1, K, nullptr, nullptr};
+  GemmArgs g{A, B, C, colsum, lda, ldb, ldc, stride_a, stride_b, stride_c, M, N, K, alpha, beta, 1, K, nullptr, nullptr,
+             bias};
   int kchunk = K;
   const int splits = ws ? choose_splits(M, N, K, batch, kchunk) : 1;
   if (splits > 1) {
@@ -290,14 +295,15 @@ int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, f
              int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
              int64_t ldc, int64_t stride_c, int batch, float* colsum) {
   return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
-                   stride_c, batch, colsum, nullptr, 0);
+                   stride_c, batch, colsum, nullptr, nullptr, 0);
 }
 
-int mle_gemm_ws(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+int mle_gemm_ex(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
                 int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
-                int64_t ldc, int64_t stride_c, int batch, float* colsum, void* ws, size_t ws_bytes) {
+                int64_t ldc, int64_t stride_c, int batch, float* colsum, const float* bias, void* ws,
+                size_t ws_bytes) {
   return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
-                   stride_c, batch, colsum, ws, ws_bytes);
+                   stride_c, batch, colsum, bias, ws, ws_bytes);
 }
 
 }  // extern "C"

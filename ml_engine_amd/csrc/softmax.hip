@@ -81,6 +81,65 @@ __global__ __launch_bounds__(NT) void softmax_row_kernel(const float* __restrict
   }
 }
 
+// Row softmax with float4 accesses (cols % 4 == 0, cols <= 4*NT*RV4).
+constexpr int RV4 = 8;
+__device__ __forceinline__ f32x4 ldv(const float* p, size_t i) { return *reinterpret_cast<const f32x4*>(p + i); }
+__device__ __forceinline__ void stv(float* p, size_t i, f32x4 v) { *reinterpret_cast<f32x4*>(p + i) = v; }
+
+__global__ __launch_bounds__(NT) void softmax_row4_kernel(const float* __restrict__ x, float* __restrict__ y, int rows,
+                                                          int cols, int causal, const float* __restrict__ target,
+                                                          double* __restrict__ loss_part) {
+  __shared__ float redf[NT / 64];
+  __shared__ double redd[NT / 64];
+  const size_t line = blockIdx.x;
+  const int r_in = (int)(line % rows);
+  const size_t base = line * cols;
+  const int lim = causal ? min(cols, r_in + 1) : cols;
+  f32x4 v[RV4];
+  float mx = -FLT_MAX;
+#pragma unroll
+  for (int i = 0; i < RV4; ++i) {
+    const int c = (threadIdx.x + i * NT) * 4;
+    v[i] = (c < cols) ? ldv(x, base + c) : f32x4{-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, v[i][j]);
+  }
+  mx = block_max<NT>(mx, redf);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < RV4; ++i) {
+    const int c = (threadIdx.x + i * NT) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i][j] = (c + j < lim) ? expf(v[i][j] - mx) : 0.f;
+      sum += v[i][j];
+    }
+  }
+  sum = block_sum<NT>(sum, redf);
+  if (sum < 1e-45f) sum = 1.0f;
+  double lp = 0.0;
+#pragma unroll
+  for (int i = 0; i < RV4; ++i) {
+    const int c = (threadIdx.x + i * NT) * 4;
+    if (c < cols) {
+      f32x4 p;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p[j] = v[i][j] / sum;
+      stv(y, base + c, p);
+      if (target) {
+        const f32x4 t = ldv(target, base + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (t[j] != 0.f) lp += -(double)t[j] * log((double)p[j] + 1e-27);
+      }
+    }
+  }
+  if (target) {
+    lp = block_sum<NT>(lp, redd);
+    if (threadIdx.x == 0) loss_part[line] = lp;
+  }
+}
+
 // Row softmax backward: dx += y (dy - <dy, y>).
 template <bool CACHED>
 __global__ __launch_bounds__(NT) void softmax_row_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dy,
@@ -219,6 +278,100 @@ __global__ __launch_bounds__(NT) void softmax_col_bwd_kernel(const float* __rest
 }
 
 // ---------------------------------------------------------------------------
+// Column softmax, float4 lanes: a workgroup owns 64 columns; lane (tx, ty) with
+// tx < 16 covers columns 4tx..4tx+3 and rows ty, ty+16, ... (rows <= 16*C4_RPT).
+constexpr int C4_RL = 16, C4_RPT = 16;
+
+__global__ __launch_bounds__(NT) void softmax_col4_kernel(const float* __restrict__ x, float* __restrict__ y, int rows,
+                                                          int cols, int causal) {
+  __shared__ f32x4 red[C4_RL][16];
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const int c0 = blockIdx.x * 64 + tx * 4;
+  const size_t base = (size_t)blockIdx.y * rows * cols;
+  const bool cv = c0 < cols;
+  f32x4 v[C4_RPT];
+  f32x4 mx = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+#pragma unroll
+  for (int i = 0; i < C4_RPT; ++i) {
+    const int r = ty + i * C4_RL;
+    v[i] = (cv && r < rows) ? ldv(x, base + (size_t)r * cols + c0) : f32x4{-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx[j] = fmaxf(mx[j], v[i][j]);
+  }
+  red[ty][tx] = mx;
+  __syncthreads();
+  mx = red[0][tx];
+#pragma unroll
+  for (int k = 1; k < C4_RL; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx[j] = fmaxf(mx[j], red[k][tx][j]);
+  __syncthreads();
+  f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < C4_RPT; ++i) {
+    const int r = ty + i * C4_RL;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool keep = cv && r < rows && !(causal && c0 + j > r);
+      v[i][j] = keep ? expf(v[i][j] - mx[j]) : 0.f;
+      sum[j] += v[i][j];
+    }
+  }
+  red[ty][tx] = sum;
+  __syncthreads();
+  sum = red[0][tx];
+#pragma unroll
+  for (int k = 1; k < C4_RL; ++k) sum += red[k][tx];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (sum[j] < 1e-45f) sum[j] = 1.0f;
+  if (!cv) return;
+#pragma unroll
+  for (int i = 0; i < C4_RPT; ++i) {
+    const int r = ty + i * C4_RL;
+    if (r < rows) {
+      f32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = v[i][j] / sum[j];
+      stv(y, base + (size_t)r * cols + c0, o);
+    }
+  }
+}
+
+__global__ __launch_bounds__(NT) void softmax_col4_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dy,
+                                                              float* __restrict__ dx, int rows, int cols) {
+  __shared__ f32x4 red[C4_RL][16];
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const int c0 = blockIdx.x * 64 + tx * 4;
+  const size_t base = (size_t)blockIdx.y * rows * cols;
+  const bool cv = c0 < cols;
+  f32x4 yv[C4_RPT], gv[C4_RPT];
+  f32x4 dot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < C4_RPT; ++i) {
+    const int r = ty + i * C4_RL;
+    const bool ok = cv && r < rows;
+    yv[i] = ok ? ldv(y, base + (size_t)r * cols + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+    gv[i] = ok ? ldv(dy, base + (size_t)r * cols + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+    dot += gv[i] * yv[i];
+  }
+  red[ty][tx] = dot;
+  __syncthreads();
+  dot = red[0][tx];
+#pragma unroll
+  for (int k = 1; k < C4_RL; ++k) dot += red[k][tx];
+  if (!cv) return;
+#pragma unroll
+  for (int i = 0; i < C4_RPT; ++i) {
+    const int r = ty + i * C4_RL;
+    if (r < rows) {
+      const size_t o = base + (size_t)r * cols + c0;
+      stv(dx, o, ldv(dx, o) + yv[i] * (gv[i] - dot));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Deterministic sums into a scalar: per-block double partials, then one block
 // adds them in a fixed order.
 __global__ __launch_bounds__(NT) void mse_partial_kernel(const float* __restrict__ x, const float* __restrict__ t,
@@ -265,6 +418,17 @@ __global__ __launch_bounds__(NT) void xent_bwd_kernel(const float* __restrict__ 
   }
 }
 
+__global__ __launch_bounds__(NT) void xent_bwd4_kernel(const float* __restrict__ p, const float* __restrict__ t,
+                                                       const float* __restrict__ up, float* __restrict__ dl, size_t n4,
+                                                       float batch) {
+  const size_t stride = (size_t)gridDim.x * NT;
+  for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n4; i += stride) {
+    f32x4 g = ldv(p, i * 4) + (-1.0f) * ldv(t, i * 4);
+    if (up) g *= up[0];
+    stv(dl, i * 4, g / batch);
+  }
+}
+
 constexpr unsigned kMsePartCap = 2048;
 
 }  // namespace
@@ -275,17 +439,21 @@ int mle_softmax_fwd(mle_stream stream, const float* x, float* y, int bc, int row
   MLE_CHECK_ARG(x && y && bc >= 0 && rows >= 0 && cols >= 0 && (axis == 0 || axis == 1), "mle_softmax_fwd: bad argument");
   if ((size_t)bc * rows * cols == 0) return MLE_OK;
   hipStream_t s = as_stream(stream);
+  const bool vec = cols % 4 == 0 && aligned16(x) && aligned16(y);
   if (axis == 0) {
     const size_t lines = (size_t)bc * rows;
     MLE_CHECK_ARG(lines <= 2147483647u, "mle_softmax_fwd: too many rows");
-    if (cols <= NT * ROW_CPT)
+    if (vec && cols <= 4 * NT * RV4)
+      softmax_row4_kernel<<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr);
+    else if (cols <= NT * ROW_CPT)
       softmax_row_kernel<true><<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr);
     else
       softmax_row_kernel<false><<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr);
   } else {
     MLE_CHECK_ARG(bc <= 65535, "mle_softmax_fwd: bc %d > 65535", bc);
     dim3 grid((cols + COL_W - 1) / COL_W, bc);
-    if (rows <= COL_RL * COL_RPT) softmax_col_kernel<true><<<grid, NT, 0, s>>>(x, y, rows, cols, causal);
+    if (vec && rows <= C4_RL * C4_RPT) softmax_col4_kernel<<<grid, NT, 0, s>>>(x, y, rows, cols, causal);
+    else if (rows <= COL_RL * COL_RPT) softmax_col_kernel<true><<<grid, NT, 0, s>>>(x, y, rows, cols, causal);
     else softmax_col_kernel<false><<<grid, NT, 0, s>>>(x, y, rows, cols, causal);
   }
   return check_launch("mle_softmax_fwd");
@@ -304,7 +472,9 @@ int mle_softmax_bwd(mle_stream stream, const float* y, const float* dy, float* d
   } else {
     MLE_CHECK_ARG(bc <= 65535, "mle_softmax_bwd: bc %d > 65535", bc);
     dim3 grid((cols + COL_W - 1) / COL_W, bc);
-    if (rows <= COL_RL * COL_RPT) softmax_col_bwd_kernel<true><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
+    const bool vec = cols % 4 == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
+    if (vec && rows <= C4_RL * C4_RPT) softmax_col4_bwd_kernel<<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
+    else if (rows <= COL_RL * COL_RPT) softmax_col_bwd_kernel<true><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
     else softmax_col_bwd_kernel<false><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
   }
   return check_launch("mle_softmax_bwd");
@@ -343,7 +513,9 @@ int mle_softmax_xent_fwd(mle_stream stream, const float* logits, const float* ta
     return set_error(MLE_ERR_WORKSPACE, "mle_softmax_xent_fwd: workspace too small");
   hipStream_t s = as_stream(stream);
   double* part = static_cast<double*>(ws);
-  if (cols <= NT * ROW_CPT)
+  if (cols % 4 == 0 && cols <= 4 * NT * RV4 && aligned16(logits) && aligned16(probs) && aligned16(target))
+    softmax_row4_kernel<<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part);
+  else if (cols <= NT * ROW_CPT)
     softmax_row_kernel<true><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part);
   else
     softmax_row_kernel<false><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part);
@@ -355,8 +527,12 @@ int mle_softmax_xent_bwd(mle_stream stream, const float* probs, const float* tar
                          float* dlogits, size_t n, int batch) {
   MLE_CHECK_ARG(probs && target && dlogits && batch > 0, "mle_softmax_xent_bwd: bad argument");
   if (n == 0) return MLE_OK;
-  xent_bwd_kernel<<<stream_grid(n, NT, 8192), NT, 0, as_stream(stream)>>>(probs, target, upstream, dlogits, n,
-                                                                         (float)batch);
+  if (n % 4 == 0 && aligned16(probs) && aligned16(target) && aligned16(dlogits))
+    xent_bwd4_kernel<<<stream_grid(n / 4, NT, 8192), NT, 0, as_stream(stream)>>>(probs, target, upstream, dlogits,
+                                                                                n / 4, (float)batch);
+  else
+    xent_bwd_kernel<<<stream_grid(n, NT, 8192), NT, 0, as_stream(stream)>>>(probs, target, upstream, dlogits, n,
+                                                                           (float)batch);
   return check_launch("mle_softmax_xent_bwd");
 }
 

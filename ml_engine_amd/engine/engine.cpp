@@ -759,17 +759,17 @@ graph Linear::forward(const graph& X) {
   const size_t ws_bytes = std::max(ws_f, std::max(ws_dx, ws_dw));
   void* ws = mle::gemm_workspace(ws_bytes);
   node->forward = [=]() {
-    check(mle_gemm_ws(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, 0, W->output, p, 0, 0.0f, nd->output,
-                      p, 0, 1, nullptr, ws, ws_bytes),
-          "MatMul... X*W1 in " + name + " forward");
-    if (has_bias) check(mle_bias_add_rows(mle::stream(), nd->output, Bb->output, rows, p), "BCumAdd in " + name);
+    // Y = X W + b: BCumAdd is fused into the GEMM epilogue.
+    check(mle_gemm_ex(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, 0, W->output, p, 0, 0.0f, nd->output,
+                      p, 0, 1, nullptr, has_bias ? Bb->output : nullptr, ws, ws_bytes),
+          "MatMul... X*W1 + B1 in " + name + " forward");
   };
   node->backward = [=]() {
-    check(mle_gemm_ws(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, 0, W->output, p, 0, 1.0f, x->grad, n, 0,
-                      1, nullptr, ws, ws_bytes),
+    check(mle_gemm_ex(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, 0, W->output, p, 0, 1.0f, x->grad, n, 0,
+                      1, nullptr, nullptr, ws, ws_bytes),
           "MatMul... dZ*W^T in " + name + " backward");
-    check(mle_gemm_ws(mle::stream(), 1, 0, n, p, (int)rows, 1.0f, x->output, n, 0, nd->grad, p, 0, 1.0f, W->grad, p, 0,
-                      1, has_bias ? Bb->grad : nullptr, ws, ws_bytes),
+    check(mle_gemm_ex(mle::stream(), 1, 0, n, p, (int)rows, 1.0f, x->output, n, 0, nd->grad, p, 0, 1.0f, W->grad, p, 0,
+                      1, has_bias ? Bb->grad : nullptr, nullptr, ws, ws_bytes),
           "MatMul... X^T*dZ in " + name + " backward");
   };
   node->free = [=]() { nd->clear(); };

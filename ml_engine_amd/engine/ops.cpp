@@ -7,6 +7,8 @@
 #include <math.h>
 #include <stdio.h>
 
+#include <vector>
+
 using mle::check;
 
 namespace {
@@ -469,9 +471,14 @@ graph GraphOperations::OneHot(const int32_t* keys, int batch, int clen, int max_
   auto node = make_node("OneHot targets", batch, 1, clen, vocab);
   node->inputs = {};
   NodeBackProp* nd = node.get();
+  // The matrix is cleared once; each forward then only moves the ones.
+  const size_t ntok = (size_t)batch * clen;
+  auto* prev = static_cast<int32_t*>(mle::alloc_scratch(ntok * sizeof(int32_t)));
+  std::vector<int32_t> none(ntok, -1);
+  check(mle_memcpy_h2d(prev, none.data(), ntok * sizeof(int32_t), S()), "OneHot init");
+  check(mle_fill(S(), nd->output, 0.0f, nd->total), "OneHot fill");
   node->forward = [=]() {
-    check(mle_fill(S(), nd->output, 0.0f, nd->total), "OneHot fill");
-    check(mle_onehot(S(), nd->output, keys, batch, clen, max_clen, vocab), "OneHotEmbeddings");
+    check(mle_onehot_update(S(), nd->output, prev, keys, batch, clen, max_clen, vocab), "OneHotEmbeddings");
   };
   std_hooks(node);
   return node;

@@ -54,7 +54,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_act_bwd": (I, [P, I, P, P, P, SZ]),
     "mle_gemm": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P]),
     "mle_gemm_ws_bytes": (SZ, [I, I, I, I]),
-    "mle_gemm_ws": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P, P, SZ]),
+    "mle_gemm_ex": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P, P, P, SZ]),
     "mle_colsum": (I, [P, P, SZ, I, P, F]),
     "mle_channel_sum": (I, [P, P, I, I, SZ, I, P]),
     "mle_softmax_fwd": (I, [P, P, P, I, I, I, I, I]),
@@ -81,6 +81,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_embed_scatter_ws_bytes": (SZ, [I, I]),
     "mle_embed_scatter_add": (I, [P, P, P, P, I, I, I, I, I, F, P, SZ]),
     "mle_onehot": (I, [P, P, P, I, I, I, I]),
+    "mle_onehot_update": (I, [P, P, P, P, I, I, I, I]),
     "mle_argmax": (I, [P, P, I, I, P]),
     "mle_probe_arm": (I, [C.c_char_p]),
     "mle_probe_read": (I, [C.POINTER(I), C.POINTER(D), C.POINTER(D), C.POINTER(D)]),

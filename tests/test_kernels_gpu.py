@@ -80,9 +80,11 @@ def test_gemm_split_k(hip, orc, ta, tb, M, N, K, batch, cs):
     dA, dB, dC = B(hip, A), B(hip, Bm), B(hip, C0)
     cs0 = r.standard_normal(N, dtype=np.float32)
     dcs = B(hip, cs0) if cs else None
-    hip.call("mle_gemm_ws", None, ta, tb, M, N, K, 0.75, dA.ptr, M if ta else K, A[0].size, dB.ptr, K if tb else N,
-             Bm[0].size, 1.0, dC.ptr, N, M * N, batch, dcs.ptr if cs else None, ws.ptr, ws.nbytes)
-    assert_close(dC.numpy(), ref, what="split-K gemm", **MM)
+    bias = r.standard_normal(N, dtype=np.float32)
+    dbias = B(hip, bias)
+    hip.call("mle_gemm_ex", None, ta, tb, M, N, K, 0.75, dA.ptr, M if ta else K, A[0].size, dB.ptr, K if tb else N,
+             Bm[0].size, 1.0, dC.ptr, N, M * N, batch, dcs.ptr if cs else None, dbias.ptr, ws.ptr, ws.nbytes)
+    assert_close(dC.numpy(), ref + bias, what="split-K gemm + bias", **MM)
     if cs:
         bsum = Bm[0].astype(np.float64).sum(1 if tb else 0)
         assert_close(dcs.numpy(), cs0 + bsum, what="split-K colsum", **EW)
@@ -98,6 +100,11 @@ def test_gemm_broadcast_and_colsum(hip, orc):
     dA, dW, dC = B(hip, A), B(hip, W), hip.Buffer.zeros((batch, M, N))
     hip.call("mle_gemm", None, 0, 0, M, N, K, 1.0, dA.ptr, K, M * K, dW.ptr, N, 0, 0.0, dC.ptr, N, M * N, batch, None)
     assert_close(dC.numpy(), ref, what="gemm broadcast B", **MM)
+    bias = r.standard_normal(N, dtype=np.float32)
+    dbias, dC2 = B(hip, bias), hip.Buffer.zeros((batch, M, N))
+    hip.call("mle_gemm_ex", None, 0, 0, M, N, K, 1.0, dA.ptr, K, M * K, dW.ptr, N, 0, 0.0, dC2.ptr, N, M * N, batch,
+             None, dbias.ptr, None, 0)
+    assert_close(dC2.numpy(), ref + bias, what="gemm + bias epilogue", **MM)
     # dW = X^T dY with fused db = colsum(dY) (Linear backward)
     X = r.standard_normal((300, 64), dtype=np.float32)
     dY = r.standard_normal((300, 130), dtype=np.float32)
@@ -319,6 +326,17 @@ def test_gather_onehot_argmax_scatter(hip, orc):
     hip.call("mle_embed_gather", None, go.ptr, gt.ptr, gk.ptr, batch, clen, maxc, dim)
     np.testing.assert_array_equal(go.numpy(), out_r)
 
+    # incremental one-hot over two different key sets
+    prev = B(hip, np.full(batch * clen, -1, np.int32))
+    goh2 = hip.Buffer.zeros((batch * clen, vocab))
+    keys2 = r.integers(0, vocab, (batch, maxc)).astype(np.int32)
+    for kk in (keys, keys2):
+        oh_k = np.zeros((batch * clen, vocab), np.float32)
+        orc.call("orc_onehot", orc.ptr(oh_k), orc.ptr(kk), batch, clen, maxc, vocab)
+        gkk = B(hip, kk)
+        hip.call("mle_onehot_update", None, goh2.ptr, prev.ptr, gkk.ptr, batch, clen, maxc, vocab)
+        np.testing.assert_array_equal(goh2.numpy(), oh_k)
+
     oh_r = np.zeros((batch * clen, vocab), np.float32)
     orc.call("orc_onehot", orc.ptr(oh_r), orc.ptr(keys), batch, clen, maxc, vocab)
     goh = hip.Buffer.zeros((batch * clen, vocab))
@@ -342,6 +360,22 @@ def test_gather_onehot_argmax_scatter(hip, orc):
     ws = hip.Buffer(hip.lib().mle_embed_scatter_ws_bytes(batch, clen))
     hip.call("mle_embed_scatter_add", None, gtab.ptr, gg.ptr, gk.ptr, batch, clen, maxc, dim, vocab, 1.0, ws.ptr, ws.nbytes)
     assert_close(gtab.numpy(), tab_r, what="scatter add", **EW)
+
+
+@pytest.mark.parametrize("batch,clen,dim,vocab", [(4, 600, 64, 300), (2, 50, 1100, 40), (64, 1024, 8, 20000)])
+def test_scatter_add_paths(hip, orc, batch, clen, dim, vocab):
+    """Row-centric path (moderate vocab*tokens, dim <= 1024) and sorted path."""
+    r = rng(batch + clen + dim)
+    keys = r.integers(-2, vocab, (batch, clen)).astype(np.int32)
+    keys[:, :5] = 3  # repeated key
+    grad = r.standard_normal((batch, clen, dim), dtype=np.float32)
+    table = r.standard_normal((vocab, dim), dtype=np.float32)
+    ref = table.copy()
+    orc.call("orc_scatter_add", orc.ptr(ref), orc.ptr(grad), orc.ptr(keys), batch, clen, clen, dim, vocab, -0.5)
+    gt, gg, gk = B(hip, table), B(hip, grad), B(hip, keys)
+    ws = hip.Buffer(hip.lib().mle_embed_scatter_ws_bytes(batch, clen))
+    hip.call("mle_embed_scatter_add", None, gt.ptr, gg.ptr, gk.ptr, batch, clen, clen, dim, vocab, -0.5, ws.ptr, ws.nbytes)
+    assert_close(gt.numpy(), ref, what="scatter add", **EW)
 
 
 # ------------------------------------------------------ elementwise / layout
