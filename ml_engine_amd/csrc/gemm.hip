@@ -44,6 +44,26 @@ __device__ __forceinline__ f32x4 ld_guard(const float* __restrict__ base, int64_
   return v;
 }
 
+// Branch-free operand reads through a raw buffer resource: lanes outside the
+// matrix use an offset beyond the resource's extent and the hardware range
+// check returns zeros (buffer_load_dwordx4 ... offen).  Used when every
+// operand extent is below 2 GiB and the contiguous bound is a multiple of 4,
+// so a float4 is either wholly inside or wholly outside.
+constexpr uint32_t kBufOOB = 0x80000000u;
+constexpr int kBufWord3 = 0x00020000;  // gfx9-family raw buffer descriptor word 3
+
+struct BufOperand {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int64_t ld;
+  __device__ BufOperand(const float* base, int64_t ld_, uint32_t bytes)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes, kBufWord3)), ld(ld_) {}
+  __device__ __forceinline__ f32x4 load(int r, int c, int R, int Cc) const {
+    const bool ok = (r < R) & (c < Cc);
+    const uint32_t off = ok ? (uint32_t)(((int64_t)r * ld + c) * 4) : kBufOOB;
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)off, 0, 0));
+  }
+};
+
 // Global -> registers for one stage.  Tiles are 4096 floats = 1024 float4,
 // four per thread.  A_MC == trans_a (A stored K x M); B_KC == trans_b.
 // `kend` bounds K for this workgroup's split.
@@ -67,6 +87,30 @@ __device__ __forceinline__ void load_b(const GemmArgs& g, const float* B, int n0
     else r[i] = ld_guard<VEC>(B, g.ldb, k0 + (f >> 5), n0 + (f & 31) * 4, kend, g.N);
   }
 }
+template <bool A_MC>
+__device__ __forceinline__ void load_a_buf(const GemmArgs& g, const BufOperand& A, int m0, int k0, int kend, int tid,
+                                           f32x4 (&r)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = tid + NT * i;
+    if (!A_MC) r[i] = A.load(m0 + (f >> 3), k0 + (f & 7) * 4, g.M, kend);
+    else r[i] = A.load(k0 + (f >> 5), m0 + (f & 31) * 4, kend, g.M);
+  }
+}
+template <bool B_KC>
+__device__ __forceinline__ void load_b_buf(const GemmArgs& g, const BufOperand& B, int n0, int k0, int kend, int tid,
+                                           f32x4 (&r)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = tid + NT * i;
+    if (B_KC) r[i] = B.load(n0 + (f >> 3), k0 + (f & 7) * 4, g.N, kend);
+    else r[i] = B.load(k0 + (f >> 5), n0 + (f & 31) * 4, kend, g.N);
+  }
+}
+
+// Row stride of the epilogue staging tile (32 x 64 per wave, 16-byte aligned rows).
+constexpr int EPI_LD = 68;
+
 // Registers -> LDS (same element mapping as the loads).
 template <bool KC>
 __device__ __forceinline__ void store_tile(float* S, int tid, const f32x4 (&r)[4]) {
@@ -78,7 +122,8 @@ __device__ __forceinline__ void store_tile(float* S, int tid, const f32x4 (&r)[4
   }
 }
 
-template <int TA, int TB, bool VEC, bool COLSUM>
+// VEC: 0 = guarded scalar loads, 1 = guarded float4 loads, 2 = buffer loads.
+template <int TA, int TB, int VEC, bool COLSUM>
 __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
@@ -98,6 +143,18 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   float* C = g.C + z * g.sc;
   const int kbeg = split * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
+  const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
+  const uint32_t b_bytes = (uint32_t)(((int64_t)((B_KC ? g.N : g.K) - 1) * g.ldb + (B_KC ? g.K : g.N)) * 4);
+  const BufOperand Ab(A, g.lda, a_bytes), Bb(B, g.ldb, b_bytes);
+  auto load_stage = [&](int k0, f32x4(&ra_)[4], f32x4(&rb_)[4]) {
+    if (VEC == 2) {
+      load_a_buf<A_MC>(g, Ab, m0, k0, kend, tid, ra_);
+      load_b_buf<B_KC>(g, Bb, n0, k0, kend, tid, rb_);
+    } else {
+      load_a<A_MC, VEC == 1>(g, A, m0, k0, kend, tid, ra_);
+      load_b<B_KC, VEC == 1>(g, B, n0, k0, kend, tid, rb_);
+    }
+  };
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -110,8 +167,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   f32x4 ra[4], rb[4];
   if (nk > 0) {
-    load_a<A_MC, VEC>(g, A, m0, kbeg, kend, tid, ra);
-    load_b<B_KC, VEC>(g, B, n0, kbeg, kend, tid, rb);
+    load_stage(kbeg, ra, rb);
     store_tile<!A_MC>(smem, tid, ra);
     store_tile<B_KC>(smem + 2 * ASZ, tid, rb);
   }
@@ -122,10 +178,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
     const float* As = smem + cur * ASZ;
     const float* Bs = smem + 2 * ASZ + cur * BSZ;
     const bool more = kt + 1 < nk;
-    if (more) {
-      load_a<A_MC, VEC>(g, A, m0, kbeg + (kt + 1) * BK, kend, tid, ra);
-      load_b<B_KC, VEC>(g, B, n0, kbeg + (kt + 1) * BK, kend, tid, rb);
-    }
+    if (more) load_stage(kbeg + (kt + 1) * BK, ra, rb);
     mma_stage<A_MC, B_KC>(As, Bs, acc, wm, wn, lr, q);
     if (do_cs) {
       const int c = tid & 127, h = tid >> 7;
@@ -142,6 +195,44 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   const float alpha = g.alpha, beta = g.beta;
   const bool split_mode = g.splits > 1;
   float* P = split_mode ? g.part + (int64_t)blockIdx.z * g.M * g.N : nullptr;
+  if (VEC == 2 && (g.N & 3) == 0 && (g.ldc & 3) == 0 && ((reinterpret_cast<uintptr_t>(C) & 15) == 0)) {
+    // Stage each wave's 64 x 64 block through LDS, 32 rows at a time, and
+    // write rows back with 16-byte stores (a wave covers 4 full 256-byte row
+    // segments per instruction instead of 16 x 64-byte pieces).
+    float* T = smem + wave * (32 * EPI_LD);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = half * 2 + ii;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) T[(ii * 16 + 4 * q + r) * EPI_LD + n * 16 + lr] = acc[i][n][r];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int rr = it * 4 + (lane >> 4);  // 0..31
+        const int cc = (lane & 15) * 4;       // 0..60
+        const int row = m0 + wm * 64 + half * 32 + rr;
+        const int col = n0 + wn * 64 + cc;
+        if (row < g.M && col < g.N) {
+          f32x4 v = *reinterpret_cast<const f32x4*>(T + rr * EPI_LD + cc);
+          if (split_mode) {
+            *reinterpret_cast<f32x4*>(P + (int64_t)row * g.N + col) = v;
+          } else {
+            float* p = C + (int64_t)row * g.ldc + col;
+            v = alpha * v;
+            if (beta != 0.f) v += beta * *reinterpret_cast<const f32x4*>(p);
+            if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + col);
+            *reinterpret_cast<f32x4*>(p) = v;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  } else {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -164,6 +255,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
         }
       }
     }
+  }
 
   if (do_cs) {
     // smem is free after the final barrier of the K loop.
@@ -208,7 +300,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g, int batch
 int choose_splits(int M, int N, int K, int batch, int& kchunk) {
   kchunk = K;
   const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN) * batch;
-  if (tiles >= 384) return 1;
+  // Measured on MI355X: with ~256 tiles a split only pays off for long K.
+  if (tiles >= 384 || (tiles >= 128 && K < 4096)) return 1;
   int s = (int)((768 + tiles - 1) / tiles);
   const int smax = K / 256;
   if (s > smax) s = smax;
@@ -221,15 +314,21 @@ int choose_splits(int M, int N, int K, int batch, int& kchunk) {
 }
 
 template <int TA, int TB>
-void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, bool vec, bool cs) {
-  if (vec) {
-    if (cs) gemm_kernel<TA, TB, true, true><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, true, false><<<grid, NT, 0, s>>>(g);
+void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, int vec, bool cs) {
+  if (vec == 2) {
+    if (cs) gemm_kernel<TA, TB, 2, true><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 2, false><<<grid, NT, 0, s>>>(g);
+  } else if (vec == 1) {
+    if (cs) gemm_kernel<TA, TB, 1, true><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 1, false><<<grid, NT, 0, s>>>(g);
   } else {
-    if (cs) gemm_kernel<TA, TB, false, true><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, false, false><<<grid, NT, 0, s>>>(g);
+    if (cs) gemm_kernel<TA, TB, 0, true><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 0, false><<<grid, NT, 0, s>>>(g);
   }
 }
+
+// Bytes spanned by one batch item of an operand stored rows x cols with leading dimension ld.
+double extent_bytes(int rows, int cols, int64_t ld) { return ((double)(rows - 1) * (double)ld + cols) * 4.0; }
 
 }  // namespace
 
@@ -257,8 +356,16 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
       g.part_cs = g.part + (size_t)splits * batch * M * N;
     }
   }
-  const bool vec = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
-                   aligned16(A) && aligned16(B);
+  const bool v4 = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
+                  aligned16(A) && aligned16(B);
+  // Buffer loads need the contiguous bound of each operand to be a multiple of
+  // 4 and every extent addressable with a 31-bit byte offset.
+  const int a_rows = trans_a ? K : M, a_cols = trans_a ? M : K;
+  const int b_rows = trans_b ? N : K, b_cols = trans_b ? K : N;
+  const bool buf = v4 && a_cols % 4 == 0 && b_cols % 4 == 0 && K > 0 &&
+                   extent_bytes(a_rows, a_cols, lda) < 2147483648.0 - 64 &&
+                   extent_bytes(b_rows, b_cols, ldb) < 2147483648.0 - 64;
+  const int vec = buf ? 2 : (v4 ? 1 : 0);
   const bool cs = colsum != nullptr;
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, batch * g.splits);
   hipStream_t s = as_stream(stream);
