@@ -255,6 +255,14 @@ static void reshape_check(NodeBackProp* n, const int* d, int size) {
 void NodeBackProp::reshape(std::vector<int> nd) { reshape_check(this, nd.data(), (int)nd.size()); }
 void NodeBackProp::reshape(int arr[], const int size) { reshape_check(this, arr, size); }
 
+void CheckError(const str& reason) {
+  const int rc = mle_stream_sync(mle::stream());
+  if (rc != MLE_OK) {
+    std::cerr << "Runtime error in " << reason << ": " << mle_last_error() << std::endl;
+    std::exit(1);
+  }
+}
+
 float ReadValueAt(const graph& X, const int& idx, const bool g) {
   float out = 0.f;
   check(mle_memcpy_d2h(&out, (g ? X->grad : X->output) + idx, sizeof(float), mle::stream()), "ReadValueAt");

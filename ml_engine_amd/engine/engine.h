@@ -129,6 +129,10 @@ struct NodeBackProp {
   bool owns_ = false;
 };
 
+// Wait for all enqueued work; print and exit on a launch or runtime error
+// (Includes/debugging_utils.h:95, Engine/debug.cu:15-25).
+void CheckError(const str& reason);
+
 float ReadValueAt(const graph& X, const int& idx, const bool flag = false);
 void WriteValueAt(const graph& X, const float value, const int& idx, const bool flag = false);
 
