@@ -174,3 +174,54 @@ def test_block_full_size_properties(hip):
     for i in range(len(params)):
         np.testing.assert_array_equal(m.get(i, 1), g1[i])
     m.close()
+
+
+# --------------------------------------------- engine against golden fixtures
+def _engine_grads(kind, dims, params, inputs, lr):
+    m = Model(kind, dims, reference_quirks=False)
+    for i, p in enumerate(params):
+        m.set(i, p)
+    for slot, x in enumerate(inputs):
+        m.input(slot, x)
+    m.step(lr, STEP_ALL)
+    m.sync()
+    out = [m.get(i, 1) for i in range(len(params))], m.loss
+    m.close()
+    return out
+
+
+def test_golden_c1_engine(hip):
+    from golden import make_golden as G
+    from test_golden import grads, load
+
+    (x, labels, params), d = G.inputs_c1()
+    fx = load("c1_mlp_step.npz", d)
+    got, loss = _engine_grads("mlp", G.C1.dims(), params, [x, labels], G.C1.lr)
+    assert abs(loss - float(fx["loss"])) <= 1e-5 * abs(float(fx["loss"]))
+    for i, (a, b) in enumerate(zip(got, grads(fx))):
+        assert_close(a, b, what=f"golden c1 grad {i}", **GRAD)
+
+
+def test_golden_c4_engine(hip):
+    from golden import make_golden as G
+    from test_golden import bias_scale, grads, load
+
+    (ids, tgt, params), d = G.inputs_c4()
+    fx = load("c4_block_step.npz", d)
+    got, loss = _engine_grads("block", G.C4.dims(), params, [ids, tgt], G.C4.lr)
+    assert abs(loss - float(fx["loss"])) <= 1e-5 * abs(float(fx["loss"]))
+    ref = grads(fx)
+    for i, (a, b) in enumerate(zip(got, ref)):
+        assert_close(a, b, what=f"golden c4 grad {i}", scale=bias_scale(ref, i), **GRAD)
+
+
+def test_golden_c5_engine(hip):
+    from golden import make_golden as G
+    from test_golden import grads, load
+
+    (x, noise, t, params), d = G.inputs_c5()
+    fx = load("c5_resblock_step.npz", d)
+    got, loss = _engine_grads("resblock", G.C5.dims(t), params, [x, noise], G.C5.lr)
+    assert abs(loss - float(fx["loss"])) <= 1e-5 * abs(float(fx["loss"]))
+    for i, (a, b) in enumerate(zip(got, grads(fx))):
+        assert_close(a, b, what=f"golden c5 grad {i}", **GRAD)
