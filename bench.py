@@ -10,8 +10,9 @@ carries:
                 timed steps; achieved = algorithmic flop per launch / duration
   cpu_baseline  the CPU oracle (OpenMP restatement of the reference math) on a
                 bounded sample of the same step, scaled to steps/s
-  extras        C3 (Linear GEMM backward) TFLOP/s and C2 (fused clip + AdamW
-                over 100 M parameters) GB/s, measured in the same run
+  extras        C3 (Linear GEMM backward) TFLOP/s, C2 (fused clip + AdamW
+                over 100 M parameters) GB/s, C1 (MLP, latency-bound) and C5
+                (U-Net residual block, conv-bound) steps/s, measured in the same run
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras]
 """
 from __future__ import annotations
@@ -30,8 +31,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from ml_engine_amd import hip  # noqa: E402
-from ml_engine_amd.configs import (BlockConfig, FlatConfig, GemmConfig, block_data, flat_data,  # noqa: E402
-                                   gemm_data)
+from ml_engine_amd.configs import (BlockConfig, FlatConfig, GemmConfig, MLPConfig, ResBlockConfig,  # noqa: E402
+                                   block_data, flat_data, gemm_data, mlp_data, resblock_data)
 from ml_engine_amd.models import STEP_ALL, Model  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
@@ -148,6 +149,49 @@ def extras_adamw(steps: int = 10) -> dict:
             "gb_per_s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4), "bytes_per_param": 32}
 
 
+def timed_steps(m: Model, lr: float, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        m.step(lr, STEP_ALL)
+    m.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        m.step(lr, STEP_ALL)
+    m.sync()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def extras_mlp(steps: int = 200) -> dict:
+    """C1: Linear 784->256 -> ReLU -> Linear 256->10 -> softmax CE, batch 64, Adam."""
+    cfg = MLPConfig()
+    x, labels, params = mlp_data(cfg, seed=0)
+    m = Model("mlp", cfg.dims())
+    for i, p in enumerate(params):
+        m.set(i, p)
+    m.input(0, x)
+    m.input(1, labels)
+    ms = timed_steps(m, cfg.lr, steps, 5)
+    m.close()
+    return {"workload": "C1 MLP 784-256-10 step (fwd + bwd + Adam), batch 64", "ms_per_step": round(ms, 4),
+            "steps_per_s": round(1e3 / ms, 1)}
+
+
+def extras_resblock(steps: int = 10) -> dict:
+    """C5: conv3x3 64->128, GN(32), SiLU, time projection, conv3x3 128->128, GN, 1x1 skip, MSE; AdamW."""
+    cfg = ResBlockConfig()
+    x, noise, t, params = resblock_data(cfg, seed=4)
+    m = Model("resblock", cfg.dims(t))
+    for i, p in enumerate(params):
+        m.set(i, p)
+    m.input(0, x)
+    m.input(1, noise)
+    ms = timed_steps(m, cfg.lr, steps, 2)
+    m.close()
+    tf = cfg.conv_flop / (ms * 1e-3) / 1e12
+    return {"workload": "C5 U-Net residual block step (fwd + bwd + AdamW), 16x64x64x64", "ms_per_step": round(ms, 4),
+            "steps_per_s": round(1e3 / ms, 2), "conv_gflop_per_step": round(cfg.conv_flop / 1e9, 2),
+            "conv_tflops_whole_step": round(tf, 2)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,6 +242,10 @@ def main() -> int:
         extras["gemm_backward"] = extras_gemm()
         log("[bench] extras: C2 fused clip + AdamW")
         extras["adamw_clip"] = extras_adamw()
+        log("[bench] extras: C1 MLP")
+        extras["mlp"] = extras_mlp()
+        log("[bench] extras: C5 residual block")
+        extras["resblock"] = extras_resblock()
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle)")

@@ -167,13 +167,21 @@ std::vector<Slab> g_slabs;
 size_t g_next_slab = size_t(64) << 20;
 uint64_t g_seed = 0;
 bool g_seed_set = false;
+
+bool g_open_new_slab = false;
 }  // namespace
 
-void param_reserve(size_t floats) { g_next_slab = std::max<size_t>(floats, 64); }
+// The next `floats` of parameters are meant to be contiguous: if the current
+// slab cannot hold them all, the next allocation opens a slab that can.
+void param_reserve(size_t floats) {
+  g_next_slab = std::max<size_t>(floats, 64);
+  g_open_new_slab = g_slabs.empty() || g_slabs.back().used + floats > g_slabs.back().cap;
+}
 
 ParamSlot param_alloc(size_t n, float** p, float** g, float** m, float** v) {
   const size_t need = (n + 63) & ~size_t(63);
-  if (g_slabs.empty() || g_slabs.back().used + need > g_slabs.back().cap) {
+  if (g_slabs.empty() || g_open_new_slab || g_slabs.back().used + need > g_slabs.back().cap) {
+    g_open_new_slab = false;
     const size_t cap = std::max(g_next_slab, need);
     void* base = nullptr;
     check(mle_device_alloc(&base, cap * 4 * sizeof(float)), "SafeCudaMalloc (parameter arena)");

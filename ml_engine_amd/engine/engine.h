@@ -73,7 +73,9 @@ struct ZeroBatch {
   ~ZeroBatch();
 };
 
-// Flat parameter arena.  reserve(n) sizes the next slab (default 64 Mi floats).
+// Flat parameter arena.  param_reserve(n) announces n floats of parameters that
+// should be contiguous: it sizes the next slab (default 64 Mi floats) and, if
+// the current slab cannot hold n more, makes the next allocation open it.
 struct ParamSlot {
   int slab;
   size_t offset;
