@@ -229,6 +229,10 @@ def test_norm(hip, orc, batch, channels, hw, groups):
 @pytest.mark.parametrize("n,cin,h,w,cout,k,pad,stride", [
     (2, 3, 9, 9, 5, 3, 1, 1), (2, 4, 8, 10, 6, 1, 0, 1), (1, 3, 11, 11, 4, 3, 1, 2),
     (2, 16, 16, 16, 32, 3, 1, 1), (1, 8, 7, 7, 8, 5, 0, 1),
+    # stride-1 3x3 / 1x1 fast path: two row tiles (cout 130), images straddling
+    # a K stage (36 pixels), pad 0 (output smaller than input), multi-stage K
+    (3, 20, 6, 6, 130, 3, 1, 1), (2, 8, 12, 12, 16, 3, 0, 1), (4, 64, 16, 16, 128, 3, 1, 1),
+    (2, 32, 8, 8, 64, 1, 0, 1),
 ])
 def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
     r = rng(n * 7 + cin + h + cout + k)
