@@ -177,14 +177,32 @@ __global__ __launch_bounds__(NT, 2) void igemm_kernel(Ops op, int kchunk) {
     }
 }
 
+// out = sum_s part[s] in split order; float4 per thread when possible, with the
+// loads of four splits issued together.
+template <bool VEC>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, int splits, size_t mn,
                                                            float* __restrict__ out) {
-  const size_t stride = (size_t)gridDim.x * 256;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < mn; i += stride) {
-    float acc = 0.f;
-    for (int s = 0; s < splits; ++s) acc += part[(size_t)s * mn + i];
-    out[i] = acc;
+  constexpr int W = VEC ? 4 : 1;
+  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * W;
+  if (i >= mn) return;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int s = 0;
+  for (; s + 4 <= splits; s += 4) {
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (VEC) v[u] = *reinterpret_cast<const f32x4*>(part + (size_t)(s + u) * mn + i);
+      else v[u][0] = part[(size_t)(s + u) * mn + i];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc += v[u];
   }
+  for (; s < splits; ++s) {
+    if (VEC) acc += *reinterpret_cast<const f32x4*>(part + (size_t)s * mn + i);
+    else acc[0] += part[(size_t)s * mn + i];
+  }
+  if (VEC) *reinterpret_cast<f32x4*>(out + i) = acc;
+  else out[i] = acc[0];
 }
 
 // ---------------------------------------------------------------------------
@@ -531,7 +549,10 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
     }
   }
   const size_t mn = (size_t)op.M * op.N;
-  split_reduce_kernel<<<stream_grid(mn, 256, 4096), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
+  if (mn % 4 == 0 && aligned16(ws) && aligned16(dw))
+    split_reduce_kernel<true><<<(unsigned)((mn / 4 + 255) / 256), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
+  else
+    split_reduce_kernel<false><<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
   return check_launch("mle_conv2d_wgrad");
 }
 

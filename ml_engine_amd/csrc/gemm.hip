@@ -5,6 +5,8 @@
 // so results are deterministic.
 #include "gemm_core.hpp"
 
+#include <algorithm>
+
 using namespace mle;
 using namespace gemm;
 
@@ -269,28 +271,55 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   }
 }
 
-// C = alpha * sum_s part[s] + beta * C and colsum += sum_s part_cs[s], in split order.
-__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g, int batch) {
+// C = alpha * sum_s part[s] + beta * C and colsum += sum_s part_cs[s], in split
+// order.  Grid: x over column groups of W (4 with VEC, else 1) columns, y over
+// rows (looping when M > 65535), z over batch items -- no integer division.
+// Loads of four splits are issued together; the additions keep split order.
+template <bool VEC>
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
+  constexpr int W = VEC ? 4 : 1;
+  const int col = (blockIdx.x * 256 + threadIdx.x) * W;
   const int64_t mn = (int64_t)g.M * g.N;
-  const int64_t total = mn * batch;
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
-    const int64_t b = i / mn, e = i - b * mn;
-    const int row = (int)(e / g.N), col = (int)(e - (int64_t)row * g.N);
-    const float* p = g.part + b * g.splits * mn + e;
-    float acc = 0.f;
-    for (int s = 0; s < g.splits; ++s) acc += p[s * mn];
-    float* c = g.C + b * g.sc + (int64_t)row * g.ldc + col;
-    float v = g.alpha * acc;
-    if (g.beta != 0.f) v += g.beta * *c;
-    if (g.bias) v += g.bias[col];
-    *c = v;
-  }
-  if (g.colsum) {
-    for (int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x; n < g.N; n += stride) {
-      float acc = 0.f;
-      for (int s = 0; s < g.splits; ++s) acc += g.part_cs[(int64_t)s * g.N + n];
-      g.colsum[n] += acc;
+  const int64_t b = blockIdx.z;
+  if (col < g.N) {
+    for (int row = blockIdx.y; row < g.M; row += gridDim.y) {
+      const float* p = g.part + b * g.splits * mn + (int64_t)row * g.N + col;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      int sp = 0;
+      for (; sp + 4 <= g.splits; sp += 4) {
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (VEC) v[u] = *reinterpret_cast<const f32x4*>(p + (sp + u) * mn);
+          else v[u][0] = p[(sp + u) * mn];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc += v[u];
+      }
+      for (; sp < g.splits; ++sp) {
+        if (VEC) acc += *reinterpret_cast<const f32x4*>(p + sp * mn);
+        else acc[0] += p[sp * mn];
+      }
+      float* c = g.C + b * g.sc + (int64_t)row * g.ldc + col;
+      if (VEC) {
+        f32x4 v = g.alpha * acc;
+        if (g.beta != 0.f) v += g.beta * *reinterpret_cast<const f32x4*>(c);
+        if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + col);
+        *reinterpret_cast<f32x4*>(c) = v;
+      } else {
+        float v = g.alpha * acc[0];
+        if (g.beta != 0.f) v += g.beta * *c;
+        if (g.bias) v += g.bias[col];
+        *c = v;
+      }
+    }
+    if (g.colsum && blockIdx.y == 0 && b == 0) {
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        float acc = 0.f;
+        for (int sp = 0; sp < g.splits; ++sp) acc += g.part_cs[(int64_t)sp * g.N + col + j];
+        g.colsum[col + j] += acc;
+      }
     }
   }
 }
@@ -382,8 +411,12 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
       default: launch_t<1, 1>(s, g, grid, vec, cs); break;
     }
     if (g.splits > 1) {
-      const size_t total = (size_t)M * N * batch;
-      split_reduce_kernel<<<stream_grid(total, 256, 4096), 256, 0, s>>>(g, batch);
+      const bool rv = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(C) && aligned16(g.part) &&
+                      (!bias || aligned16(bias));
+      const int w = rv ? 4 : 1;
+      dim3 rgrid((unsigned)((N / w + 255) / 256), (unsigned)std::min(M, 65535), (unsigned)batch);
+      if (rv) split_reduce_kernel<true><<<rgrid, 256, 0, s>>>(g);
+      else split_reduce_kernel<false><<<rgrid, 256, 0, s>>>(g);
     }
   }
   return check_launch(names[which]);
