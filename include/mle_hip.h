@@ -18,7 +18,10 @@
  *    calls.  Kernels that need scratch take (ws, ws_bytes); the required size is
  *    returned by the matching *_ws_bytes query.
  *  - "accumulate" means the kernel adds into its destination (`+=`), as the
- *    reference backward kernels do; "assign" overwrites.
+ *    reference backward kernels do; "assign" overwrites.  Backward entry points
+ *    that take `int accumulate` do either: 1 is the reference's `+=`, 0 writes
+ *    the value that `+=` would leave in a zeroed destination without reading
+ *    it (callers use it for the first write after zero_grad).
  */
 #ifndef MLE_HIP_H
 #define MLE_HIP_H
@@ -90,6 +93,8 @@ int mle_fill(mle_stream stream, float* x, float value, size_t n);
 int mle_scale_add(mle_stream stream, const float* x, const float* y, float* z, float scale, size_t n);
 /* y += scale*x (double scale, float storage).  Accumulate (Engine/kernels.cu:1693-1699). */
 int mle_accumulate(mle_stream stream, const float* x, float* y, double scale, size_t n);
+/* y = (float)(scale*(double)x): mle_accumulate into a zeroed y, without reading y. */
+int mle_scale_assign(mle_stream stream, const float* x, float* y, double scale, size_t n);
 /* y = scale*x.  Scale_Write (Engine/kernels.cu:1677-1682), Write (Engine/kernels.cu:1670-1675) with scale 1. */
 int mle_scale_write(mle_stream stream, const float* x, float* y, float scale, size_t n);
 /* divide==0: x *= factor; divide==1: x /= factor.  SV (Includes/kernels.h:272-280). */
@@ -119,8 +124,8 @@ int mle_timestep_pe(mle_stream stream, float* y, int t, int dim);
 
 /* y = f(x).  ReLU/GeLU/SiLU/TaNH/Sigmoid/LeakyReLU (Engine/kernels.cu:1214-1328). */
 int mle_act_fwd(mle_stream stream, int kind, const float* x, float* y, size_t n);
-/* dx += dy * f'(x)  (accumulate).  deriv_* (Engine/kernels.cu:1223-1328). */
-int mle_act_bwd(mle_stream stream, int kind, const float* x, const float* dy, float* dx, size_t n);
+/* dx (+)= dy * f'(x).  deriv_* (Engine/kernels.cu:1223-1328). */
+int mle_act_bwd(mle_stream stream, int kind, const float* x, const float* dy, float* dx, size_t n, int accumulate);
 
 /* ------------------------------------------------------------------------- */
 /* GEMM (fp32 MFMA)                                                          */
@@ -173,14 +178,16 @@ int mle_channel_sum(mle_stream stream, const float* x, int batch, int channels, 
  * max still runs over all entries of the line.  Sums below 1e-45 become 1.
  * SoftMax / SoftMask (Engine/kernels.cu:2183-2235). */
 int mle_softmax_fwd(mle_stream stream, const float* x, float* y, int bc, int rows, int cols, int axis, int causal);
-/* dx += y * (dy - <dy, y>) along the same axis.  deriv_softmax (Engine/kernels.cu:2149-2181). */
-int mle_softmax_bwd(mle_stream stream, const float* y, const float* dy, float* dx, int bc, int rows, int cols, int axis);
+/* dx (+)= y * (dy - <dy, y>) along the same axis.  deriv_softmax (Engine/kernels.cu:2149-2181). */
+int mle_softmax_bwd(mle_stream stream, const float* y, const float* dy, float* dx, int bc, int rows, int cols, int axis,
+                    int accumulate);
 
 size_t mle_loss_ws_bytes(size_t n);
 /* loss[0] = sum((t - x)^2) / n.  scalar_mse_kernel (Engine/kernels.cu:1808-1816). */
 int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws, size_t ws_bytes);
-/* dx += 2 (x - t) / n * (upstream ? upstream[0] : 1).  deriv_mse_kernel (Engine/kernels.cu:1838-1848). */
-int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n);
+/* dx (+)= 2 (x - t) / n * (upstream ? upstream[0] : 1).  deriv_mse_kernel (Engine/kernels.cu:1838-1848). */
+int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,
+                int accumulate);
 /* probs = row softmax(logits) over [rows, cols]; loss[0] = sum(-t log(p + 1e-27)) / (rows*cols).
  * SoftMaxCrossEntropy forward (Engine/engine.cu:2088-2100, Engine/kernels.cu:1818-1826). */
 int mle_softmax_xent_fwd(mle_stream stream, const float* logits, const float* target, float* probs,
@@ -203,14 +210,15 @@ int mle_softmax_xent_bwd(mle_stream stream, const float* probs, const float* tar
 size_t mle_norm_ws_bytes(int batch, int channels, size_t hw, int groups);
 int mle_norm_fwd(mle_stream stream, const float* x, float* y, float* stats,
                  int batch, int channels, size_t hw, int groups, float eps, void* ws, size_t ws_bytes);
-/* dx += r * (dy - sum(dy)/N - y * sum(dy*y)/N), r = rsqrt(ssd/N + eps)  (accumulate).
+/* dx (+)= r * (dy - sum(dy)/N - y * sum(dy*y)/N), r = rsqrt(ssd/N + eps).
  * LayerBackward / GroupBackward (Engine/kernels.cu:849-896) after the ggamma
  * reductions of Engine/engine.cu:3116-3130 / 3262-3276.  With
- * reference_layout != 0 and groups == 1 only the first batch*hw elements are
- * written, as LayerBackward's guard does for channels > 1. */
+ * reference_layout != 0 and groups == 1 only the first batch*hw elements get
+ * a gradient, as LayerBackward's guard does for channels > 1 (the rest are
+ * untouched, or 0 when assigning). */
 int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, const float* stats,
                  int batch, int channels, size_t hw, int groups, float eps, int reference_layout,
-                 void* ws, size_t ws_bytes);
+                 void* ws, size_t ws_bytes, int accumulate);
 
 /* ------------------------------------------------------------------------- */
 /* Convolution (NCHW input, OIHW weights), implicit GEMM on fp32 MFMA        */
@@ -219,9 +227,9 @@ int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, 
 /* y = conv(x, w) + b (b may be NULL).  CV2D (Engine/kernels.cu:985-1019). */
 int mle_conv2d_fwd(mle_stream stream, const float* x, const float* w, const float* b, float* y,
                    int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride);
-/* dx += conv_transpose(dy, w).  CV2D_GradInput (Engine/kernels.cu:1053-1089). */
+/* dx (+)= conv_transpose(dy, w).  CV2D_GradInput (Engine/kernels.cu:1053-1089). */
 int mle_conv2d_dgrad(mle_stream stream, const float* dy, const float* w, float* dx,
-                     int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride);
+                     int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride, int accumulate);
 size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride);
 /* dw = sum_{n,oh,ow} x * dy  (assign).  GV2D (Engine/kernels.cu:1021-1051). */
 int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* dw,

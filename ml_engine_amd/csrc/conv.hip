@@ -51,6 +51,7 @@ struct DgradOps {
   float* dx;
   ConvGeom g;
   int M, N, K;
+  int acc;
   __device__ float a(int m, int k) const {
     if (m >= M || k >= K) return 0.f;
     const int khw = g.kh * g.kw;
@@ -72,7 +73,8 @@ struct DgradOps {
   __device__ void store(int m, int n, float v, int) const {
     const int hw = g.h * g.w;
     const int bb = n / hw, pix = n - bb * hw;
-    dx[((size_t)bb * g.cin + m) * hw + pix] += v;
+    float* d = dx + ((size_t)bb * g.cin + m) * hw + pix;
+    *d = acc ? *d + v : v;
   }
 };
 
@@ -233,6 +235,7 @@ struct FastConv {
   int ph, pw, phw;
   int pad;
   int cout, cin;  // for the A / output index maps
+  int acc;        // dgrad: 1 accumulates into dx, 0 assigns
 };
 
 __device__ __forceinline__ float buf_ld1(__amdgpu_buffer_rsrc_t r, uint32_t off_bytes) {
@@ -413,7 +416,7 @@ __global__ __launch_bounds__(NT, 2) void conv_fast_kernel(FastConv c) {
           f32x4* dst = reinterpret_cast<f32x4*>(c.out + ((size_t)b * oc + row) * c.phw + pix);
           if (KIND == CONV_FWD) {
             if (c.bias) v += c.bias[row];
-          } else {
+          } else if (c.acc) {
             v += *dst;
           }
           *dst = v;
@@ -482,7 +485,7 @@ int mle_conv2d_fwd(mle_stream stream, const float* x, const float* w, const floa
   if (fast_filter(g) && ohw % 4 == 0 && op.K % 4 == 0 && a16(y) && fits_2g((double)n * cin * h * w_in) &&
       fits_2g((double)n * cout * ohw) && fits_2g((double)cout * op.K)) {
     FastConv c{x, w, b, y, (uint32_t)((size_t)n * cin * h * w_in * 4), (uint32_t)((size_t)cout * op.K * 4),
-               op.M, op.N, op.K, op.K, cin, h, w_in, h * w_in, g.oh, g.ow, ohw, pad, cout, cin};
+               op.M, op.N, op.K, op.K, cin, h, w_in, h * w_in, g.oh, g.ow, ohw, pad, cout, cin, 0};
     launch_fast<CONV_FWD>(s, c, kh, 1);
   } else {
     dim3 grid((op.N + BN - 1) / BN, (op.M + BM - 1) / BM, 1);
@@ -492,12 +495,12 @@ int mle_conv2d_fwd(mle_stream stream, const float* x, const float* w, const floa
 }
 
 int mle_conv2d_dgrad(mle_stream stream, const float* dy, const float* w, float* dx, int n, int cin, int h, int w_in,
-                     int cout, int kh, int kw, int pad, int stride) {
+                     int cout, int kh, int kw, int pad, int stride, int accumulate) {
   MLE_CHECK_ARG(dy && w && dx, "mle_conv2d_dgrad: null pointer");
   ConvGeom g;
   int rc = geom(n, cin, h, w_in, cout, kh, kw, pad, stride, g);
   if (rc) return rc;
-  DgradOps op{dy, w, dx, g, cin, n * h * w_in, cout * kh * kw};
+  DgradOps op{dy, w, dx, g, cin, n * h * w_in, cout * kh * kw, accumulate != 0};
   hipStream_t s = as_stream(stream);
   ProbeScope probe("conv_dgrad", s, 2.0 * op.M * (double)op.N * op.K, 0.0);
   const int hw = h * w_in;
@@ -505,7 +508,7 @@ int mle_conv2d_dgrad(mle_stream stream, const float* dy, const float* w, float* 
       fits_2g((double)n * cout * g.oh * g.ow) && fits_2g((double)cout * cin * kh * kw)) {
     FastConv c{dy, w, nullptr, dx, (uint32_t)((size_t)n * cout * g.oh * g.ow * 4),
                (uint32_t)((size_t)cout * cin * kh * kw * 4), op.M, op.N, op.K, op.K, cout, g.oh, g.ow, g.oh * g.ow,
-               h, w_in, hw, pad, cout, cin};
+               h, w_in, hw, pad, cout, cin, accumulate != 0};
     launch_fast<CONV_DGRAD>(s, c, kh, 1);
   } else {
     dim3 grid((op.N + BN - 1) / BN, (op.M + BM - 1) / BM, 1);
@@ -541,7 +544,7 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
         fits_2g((double)n * cin * h * w_in) && fits_2g((double)n * cout * ohw)) {
       FastConv c{x, dy, nullptr, static_cast<float*>(ws), (uint32_t)((size_t)n * cin * h * w_in * 4),
                  (uint32_t)((size_t)n * cout * ohw * 4), op.M, op.N, op.K, kchunk, cin, h, w_in, h * w_in,
-                 g.oh, g.ow, ohw, pad, cout, cin};
+                 g.oh, g.ow, ohw, pad, cout, cin, 0};
       launch_fast<CONV_WGRAD>(s, c, kh, splits);
     } else {
       dim3 grid((op.N + BN - 1) / BN, (op.M + BM - 1) / BM, splits);

@@ -58,6 +58,19 @@ struct AccumOneOp {  // y += x
   __device__ void vec(size_t i) const { st4(y, i, ld4(y, i) + ld4(x, i)); }
 };
 
+struct ScaleAssignOp {  // y = (float)(scale*(double)x): AccumOp applied to y == 0
+  const float* x;
+  float* y;
+  double s;
+  __device__ void one(size_t i) const { y[i] = (float)(s * (double)x[i]); }
+  __device__ void vec(size_t i) const {
+    f32x4 a = ld4(x, i), b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = (float)(s * (double)a[j]);
+    st4(y, i, b);
+  }
+};
+
 struct AccumOp {  // y = (float)((double)y + scale*(double)x)
   const float* x;
   float* y;
@@ -184,16 +197,20 @@ struct ActFwdOp {
 };
 
 template <int K>
-struct ActBwdOp {  // dx += dy * f'(x)
+struct ActBwdOp {  // dx (+)= dy * f'(x); acc = false assigns (dx is not read)
   const float* x;
   const float* dy;
   float* dx;
-  __device__ void one(size_t i) const { dx[i] += act_df<K>(x[i]) * dy[i]; }
+  bool acc;
+  __device__ void one(size_t i) const {
+    const float v = act_df<K>(x[i]) * dy[i];
+    dx[i] = acc ? dx[i] + v : v;
+  }
   __device__ void vec(size_t i) const {
-    f32x4 a = ld4(x, i), g = ld4(dy, i), d = ld4(dx, i);
+    f32x4 a = ld4(x, i), g = ld4(dy, i), d;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) d[j] += act_df<K>(a[j]) * g[j];
-    st4(dx, i, d);
+    for (int j = 0; j < 4; ++j) d[j] = act_df<K>(a[j]) * g[j];
+    st4(dx, i, acc ? ld4(dx, i) + d : d);
   }
 };
 
@@ -270,8 +287,8 @@ int act_fwd_t(hipStream_t s, const float* x, float* y, size_t n) {
   return run_map(s, n, aligned16(x) && aligned16(y), ActFwdOp<K>{x, y}, "mle_act_fwd");
 }
 template <int K>
-int act_bwd_t(hipStream_t s, const float* x, const float* dy, float* dx, size_t n) {
-  return run_map(s, n, aligned16(x) && aligned16(dy) && aligned16(dx), ActBwdOp<K>{x, dy, dx}, "mle_act_bwd");
+int act_bwd_t(hipStream_t s, const float* x, const float* dy, float* dx, size_t n, bool acc) {
+  return run_map(s, n, aligned16(x) && aligned16(dy) && aligned16(dx), ActBwdOp<K>{x, dy, dx, acc}, "mle_act_bwd");
 }
 
 }  // namespace
@@ -298,6 +315,12 @@ int mle_accumulate(mle_stream stream, const float* x, float* y, double scale, si
   // With scale == 1 the double sum of two floats rounds to the float sum.
   if (scale == 1.0) return run_map(as_stream(stream), n, v, AccumOneOp{x, y}, "mle_accumulate");
   return run_map(as_stream(stream), n, v, AccumOp{x, y, scale}, "mle_accumulate");
+}
+
+int mle_scale_assign(mle_stream stream, const float* x, float* y, double scale, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x && y, "mle_scale_assign: null pointer");
+  return run_map(as_stream(stream), n, aligned16(x) && aligned16(y), ScaleAssignOp{x, y, scale}, "mle_scale_assign");
 }
 
 int mle_scale_write(mle_stream stream, const float* x, float* y, float scale, size_t n) {
@@ -377,17 +400,17 @@ int mle_act_fwd(mle_stream stream, int kind, const float* x, float* y, size_t n)
   return set_error(MLE_ERR_INVALID, "mle_act_fwd: unknown kind %d", kind);
 }
 
-int mle_act_bwd(mle_stream stream, int kind, const float* x, const float* dy, float* dx, size_t n) {
+int mle_act_bwd(mle_stream stream, int kind, const float* x, const float* dy, float* dx, size_t n, int accumulate) {
   if (n == 0) return MLE_OK;
   MLE_CHECK_ARG(x && dy && dx, "mle_act_bwd: null pointer");
   hipStream_t s = as_stream(stream);
   switch (kind) {
-    case MLE_RELU: return act_bwd_t<MLE_RELU>(s, x, dy, dx, n);
-    case MLE_GELU: return act_bwd_t<MLE_GELU>(s, x, dy, dx, n);
-    case MLE_SILU: return act_bwd_t<MLE_SILU>(s, x, dy, dx, n);
-    case MLE_TANH: return act_bwd_t<MLE_TANH>(s, x, dy, dx, n);
-    case MLE_SIGMOID: return act_bwd_t<MLE_SIGMOID>(s, x, dy, dx, n);
-    case MLE_LEAKY_RELU: return act_bwd_t<MLE_LEAKY_RELU>(s, x, dy, dx, n);
+    case MLE_RELU: return act_bwd_t<MLE_RELU>(s, x, dy, dx, n, accumulate != 0);
+    case MLE_GELU: return act_bwd_t<MLE_GELU>(s, x, dy, dx, n, accumulate != 0);
+    case MLE_SILU: return act_bwd_t<MLE_SILU>(s, x, dy, dx, n, accumulate != 0);
+    case MLE_TANH: return act_bwd_t<MLE_TANH>(s, x, dy, dx, n, accumulate != 0);
+    case MLE_SIGMOID: return act_bwd_t<MLE_SIGMOID>(s, x, dy, dx, n, accumulate != 0);
+    case MLE_LEAKY_RELU: return act_bwd_t<MLE_LEAKY_RELU>(s, x, dy, dx, n, accumulate != 0);
   }
   return set_error(MLE_ERR_INVALID, "mle_act_bwd: unknown kind %d", kind);
 }

@@ -36,40 +36,49 @@ constexpr int b_tile_floats() {
   return B_KC ? BN * LDK : BK * LDMN;
 }
 
-// One BK-deep slice of MFMAs for this wave's 64 x 64 block.
+// One BK-deep slice of MFMAs for this wave's 64 x 64 block.  All fragment
+// reads of the slice are issued first and a scheduling barrier keeps the
+// compiler from sinking them between the MFMAs: otherwise m/n-contiguous tiles
+// (four ds_read_b32 per fragment) end up with an LDS wait before every few
+// MFMAs.  The hardware waits only for the reads of the current 16-deep step.
 template <bool A_MC, bool B_KC>
 __device__ __forceinline__ void mma_stage(const float* __restrict__ As, const float* __restrict__ Bs,
                                           f32x4 (&acc)[4][4], int wm, int wn, int lr, int q) {
+  constexpr int KB = BK / 16;
+  f32x4 a[KB][4], b[KB][4];
 #pragma unroll
-  for (int kb = 0; kb < BK / 16; ++kb) {
-    f32x4 a[4], b[4];
+  for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = wm * 64 + i * 16 + lr;
       if (!A_MC) {
-        a[i] = *reinterpret_cast<const f32x4*>(As + row * LDK + kb * 16 + 4 * q);
+        a[kb][i] = *reinterpret_cast<const f32x4*>(As + row * LDK + kb * 16 + 4 * q);
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[i][j] = As[(kb * 16 + 4 * q + j) * LDMN + row];
+        for (int j = 0; j < 4; ++j) a[kb][i][j] = As[(kb * 16 + 4 * q + j) * LDMN + row];
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int col = wn * 64 + i * 16 + lr;
       if (B_KC) {
-        b[i] = *reinterpret_cast<const f32x4*>(Bs + col * LDK + kb * 16 + 4 * q);
+        b[kb][i] = *reinterpret_cast<const f32x4*>(Bs + col * LDK + kb * 16 + 4 * q);
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[i][j] = Bs[(kb * 16 + 4 * q + j) * LDMN + col];
+        for (int j = 0; j < 4; ++j) b[kb][i][j] = Bs[(kb * 16 + 4 * q + j) * LDMN + col];
       }
     }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][j], b[n][j], acc[i][n], 0, 0, 0);
-  }
+        for (int n = 0; n < 4; ++n)
+          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[kb][i][j], b[kb][n][j], acc[i][n], 0, 0, 0);
 }
 
 // Row/column of accumulator element (i, n, r) of this lane inside the tile.

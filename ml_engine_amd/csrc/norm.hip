@@ -129,13 +129,15 @@ __global__ __launch_bounds__(NT) void norm_bwd_partial(const float* __restrict__
   }
 }
 
-// dx += r (dy - sum(dy)/N - y sum(dy*y)/N)  (LayerBackward/GroupBackward,
-// Engine/kernels.cu:849-896).  `quirk_hw` != 0 reproduces LayerBackward for
-// channels > 1: only elements e < batch*hw are written, with group e / hw.
+// dx (+)= r (dy - sum(dy)/N - y sum(dy*y)/N)  (LayerBackward/GroupBackward,
+// Engine/kernels.cu:849-896); acc = 0 assigns.  `quirk_hw` != 0 reproduces
+// LayerBackward for channels > 1: only elements e < batch*hw receive a
+// gradient, with group e / hw (the others are left alone, or set to 0 when
+// assigning, which is what adding nothing to a cleared gradient gives).
 __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y, const float* __restrict__ dy,
                                                      float* __restrict__ dx, const float* __restrict__ stats,
                                                      NormShape sh, const double* __restrict__ part, float eps,
-                                                     size_t quirk_hw) {
+                                                     size_t quirk_hw, int acc) {
   const int g = blockIdx.y, ck = blockIdx.x;
   const size_t off = (size_t)g * sh.N, c0 = (size_t)ck * CH;
   const float fN = (float)(int)sh.N;
@@ -158,10 +160,14 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
     if (e >= sh.N) continue;
     const size_t idx = off + e;
     if (quirk_hw) {
-      if (idx >= (size_t)sh.groups_tot * quirk_hw) continue;
+      if (idx >= (size_t)sh.groups_tot * quirk_hw) {
+        if (!acc) dx[idx] = 0.f;
+        continue;
+      }
       group_terms((int)(idx / quirk_hw), sg, sgy, r);
     }
-    dx[idx] += r * (dy[idx] - (sg / fN) - y[idx] * (sgy / fN));
+    const float v = r * (dy[idx] - (sg / fN) - y[idx] * (sgy / fN));
+    dx[idx] = acc ? dx[idx] + v : v;
   }
 }
 
@@ -203,7 +209,8 @@ int mle_norm_fwd(mle_stream stream, const float* x, float* y, float* stats, int 
 }
 
 int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, const float* stats, int batch,
-                 int channels, size_t hw, int groups, float eps, int reference_layout, void* ws, size_t ws_bytes) {
+                 int channels, size_t hw, int groups, float eps, int reference_layout, void* ws, size_t ws_bytes,
+                 int accumulate) {
   MLE_CHECK_ARG(y && dy && dx && stats && ws, "mle_norm_bwd: null pointer");
   NormShape sh;
   int rc = shape_of(batch, channels, hw, groups, sh);
@@ -215,7 +222,7 @@ int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, 
   double* part = static_cast<double*>(ws);
   const size_t quirk = (reference_layout && groups == 1 && channels > 1) ? hw : 0;
   norm_bwd_partial<<<grid, NT, 0, s>>>(y, dy, sh, part);
-  norm_bwd_apply<<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, eps, quirk);
+  norm_bwd_apply<<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, eps, quirk, accumulate);
   return check_launch("mle_norm_bwd");
 }
 

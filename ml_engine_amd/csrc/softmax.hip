@@ -140,10 +140,10 @@ __global__ __launch_bounds__(NT) void softmax_row4_kernel(const float* __restric
   }
 }
 
-// Row softmax backward: dx += y (dy - <dy, y>).
+// Row softmax backward: dx (+)= y (dy - <dy, y>); acc = 0 assigns.
 template <bool CACHED>
 __global__ __launch_bounds__(NT) void softmax_row_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dy,
-                                                             float* __restrict__ dx, int cols) {
+                                                             float* __restrict__ dx, int cols, int acc) {
   __shared__ float redf[NT / 64];
   const size_t line = blockIdx.x;
   const float* yr = y + line * cols;
@@ -167,10 +167,10 @@ __global__ __launch_bounds__(NT) void softmax_row_bwd_kernel(const float* __rest
 #pragma unroll
     for (int i = 0; i < ROW_CPT; ++i) {
       const int c = threadIdx.x + i * NT;
-      if (c < cols) dr[c] += yv[i] * (gv[i] - dot);
+      if (c < cols) dr[c] = (acc ? dr[c] : 0.f) + yv[i] * (gv[i] - dot);
     }
   } else {
-    for (int c = threadIdx.x; c < cols; c += NT) dr[c] += yr[c] * (gr[c] - dot);
+    for (int c = threadIdx.x; c < cols; c += NT) dr[c] = (acc ? dr[c] : 0.f) + yr[c] * (gr[c] - dot);
   }
 }
 
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(NT) void softmax_col_kernel(const float* __restrict
 
 template <bool CACHED>
 __global__ __launch_bounds__(NT) void softmax_col_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dy,
-                                                             float* __restrict__ dx, int rows, int cols) {
+                                                             float* __restrict__ dx, int rows, int cols, int acc) {
   __shared__ float red[COL_RL][COL_W];
   const int tx = threadIdx.x % COL_W, ty = threadIdx.x / COL_W;
   const int c = blockIdx.x * COL_W + tx;
@@ -267,12 +267,15 @@ __global__ __launch_bounds__(NT) void softmax_col_bwd_kernel(const float* __rest
 #pragma unroll
     for (int i = 0; i < COL_RPT; ++i) {
       const int r = ty + i * COL_RL;
-      if (r < rows) dx[base + (size_t)r * cols + c] += yv[i] * (gv[i] - dot);
+      if (r < rows) {
+        const size_t o = base + (size_t)r * cols + c;
+        dx[o] = (acc ? dx[o] : 0.f) + yv[i] * (gv[i] - dot);
+      }
     }
   } else {
     for (int r = ty; r < rows; r += COL_RL) {
       const size_t o = base + (size_t)r * cols + c;
-      dx[o] += y[o] * (dy[o] - dot);
+      dx[o] = (acc ? dx[o] : 0.f) + y[o] * (dy[o] - dot);
     }
   }
 }
@@ -339,7 +342,7 @@ __global__ __launch_bounds__(NT) void softmax_col4_kernel(const float* __restric
 }
 
 __global__ __launch_bounds__(NT) void softmax_col4_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dy,
-                                                              float* __restrict__ dx, int rows, int cols) {
+                                                              float* __restrict__ dx, int rows, int cols, int acc) {
   __shared__ f32x4 red[C4_RL][16];
   const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
   const int c0 = blockIdx.x * 64 + tx * 4;
@@ -366,7 +369,8 @@ __global__ __launch_bounds__(NT) void softmax_col4_bwd_kernel(const float* __res
     const int r = ty + i * C4_RL;
     if (r < rows) {
       const size_t o = base + (size_t)r * cols + c0;
-      stv(dx, o, ldv(dx, o) + yv[i] * (gv[i] - dot));
+      const f32x4 v = yv[i] * (gv[i] - dot);
+      stv(dx, o, acc ? ldv(dx, o) + v : v);
     }
   }
 }
@@ -397,13 +401,32 @@ __global__ __launch_bounds__(NT) void finish_scalar_kernel(const double* __restr
 }
 
 __global__ __launch_bounds__(NT) void mse_bwd_kernel(const float* __restrict__ x, const float* __restrict__ t,
-                                                     const float* __restrict__ up, float* __restrict__ dx, size_t n) {
+                                                     const float* __restrict__ up, float* __restrict__ dx, size_t n,
+                                                     int acc) {
   const size_t stride = (size_t)gridDim.x * NT;
   const float fn = (float)n;
   for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
     const float d = x[i] - t[i];
-    if (up) dx[i] += (2.0f * d * up[0]) / fn;
-    else dx[i] += 2.0f * d / fn;
+    const float g = up ? (2.0f * d * up[0]) / fn : 2.0f * d / fn;
+    dx[i] = (acc ? dx[i] : 0.f) + g;
+  }
+}
+
+// Vector form, used when n % 4 == 0 and every operand is 16-byte aligned.
+__global__ __launch_bounds__(NT) void mse_bwd4_kernel(const float* __restrict__ x, const float* __restrict__ t,
+                                                      const float* __restrict__ up, float* __restrict__ dx, size_t n4,
+                                                      float fn, int acc) {
+  const size_t stride = (size_t)gridDim.x * NT;
+  const float u = up ? up[0] : 1.0f;
+  for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n4; i += stride) {
+    const f32x4 xv = ldv(x, i * 4), tv = ldv(t, i * 4);
+    f32x4 g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float d = xv[j] - tv[j];
+      g[j] = up ? (2.0f * d * u) / fn : 2.0f * d / fn;
+    }
+    stv(dx, i * 4, acc ? ldv(dx, i * 4) + g : g);
   }
 }
 
@@ -460,22 +483,25 @@ int mle_softmax_fwd(mle_stream stream, const float* x, float* y, int bc, int row
 }
 
 int mle_softmax_bwd(mle_stream stream, const float* y, const float* dy, float* dx, int bc, int rows, int cols,
-                    int axis) {
+                    int axis, int accumulate) {
   MLE_CHECK_ARG(y && dy && dx && (axis == 0 || axis == 1), "mle_softmax_bwd: bad argument");
   if ((size_t)bc * rows * cols == 0) return MLE_OK;
   hipStream_t s = as_stream(stream);
   if (axis == 0) {
     const size_t lines = (size_t)bc * rows;
     MLE_CHECK_ARG(lines <= 2147483647u, "mle_softmax_bwd: too many rows");
-    if (cols <= NT * ROW_CPT) softmax_row_bwd_kernel<true><<<(unsigned)lines, NT, 0, s>>>(y, dy, dx, cols);
-    else softmax_row_bwd_kernel<false><<<(unsigned)lines, NT, 0, s>>>(y, dy, dx, cols);
+    if (cols <= NT * ROW_CPT) softmax_row_bwd_kernel<true><<<(unsigned)lines, NT, 0, s>>>(y, dy, dx, cols, accumulate);
+    else softmax_row_bwd_kernel<false><<<(unsigned)lines, NT, 0, s>>>(y, dy, dx, cols, accumulate);
   } else {
     MLE_CHECK_ARG(bc <= 65535, "mle_softmax_bwd: bc %d > 65535", bc);
     dim3 grid((cols + COL_W - 1) / COL_W, bc);
     const bool vec = cols % 4 == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
-    if (vec && rows <= C4_RL * C4_RPT) softmax_col4_bwd_kernel<<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
-    else if (rows <= COL_RL * COL_RPT) softmax_col_bwd_kernel<true><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
-    else softmax_col_bwd_kernel<false><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols);
+    if (vec && rows <= C4_RL * C4_RPT)
+      softmax_col4_bwd_kernel<<<grid, NT, 0, s>>>(y, dy, dx, rows, cols, accumulate);
+    else if (rows <= COL_RL * COL_RPT)
+      softmax_col_bwd_kernel<true><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols, accumulate);
+    else
+      softmax_col_bwd_kernel<false><<<grid, NT, 0, s>>>(y, dy, dx, rows, cols, accumulate);
   }
   return check_launch("mle_softmax_bwd");
 }
@@ -499,10 +525,15 @@ int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, flo
   return check_launch("mle_mse_fwd");
 }
 
-int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n) {
+int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,
+                int accumulate) {
   MLE_CHECK_ARG(x && t && dx, "mle_mse_bwd: bad argument");
   if (n == 0) return MLE_OK;
-  mse_bwd_kernel<<<stream_grid(n, NT, 8192), NT, 0, as_stream(stream)>>>(x, t, upstream, dx, n);
+  if (n % 4 == 0 && aligned16(x) && aligned16(t) && aligned16(dx))
+    mse_bwd4_kernel<<<stream_grid(n / 4, NT, 8192), NT, 0, as_stream(stream)>>>(x, t, upstream, dx, n / 4, (float)n,
+                                                                               accumulate);
+  else
+    mse_bwd_kernel<<<stream_grid(n, NT, 8192), NT, 0, as_stream(stream)>>>(x, t, upstream, dx, n, accumulate);
   return check_launch("mle_mse_bwd");
 }
 

@@ -155,6 +155,29 @@ ZeroBatch::~ZeroBatch() {
   }
 }
 
+static bool g_lazy_zero = true;
+void set_lazy_zero(bool on) { g_lazy_zero = on; }
+
+void defer_zero(NodeBackProp* n) {
+  if (!n || !n->grad || n->total <= 0) return;
+  if (g_lazy_zero) n->grad_pending_zero = true;
+  else zero(n->grad, n->total);
+}
+
+int accumulate_flag(NodeBackProp* n) {
+  if (n->grad_pending_zero) {
+    n->grad_pending_zero = false;
+    return 0;
+  }
+  return 1;
+}
+
+void materialize(NodeBackProp* n) {
+  if (!n || !n->grad_pending_zero) return;
+  n->grad_pending_zero = false;
+  zero(n->grad, n->total);
+}
+
 // ---------------------------------------------------------------------------
 // flat parameter arena
 namespace {
@@ -272,12 +295,14 @@ void CheckError(const str& reason) {
 }
 
 float ReadValueAt(const graph& X, const int& idx, const bool g) {
+  if (g) mle::materialize(X.get());
   float out = 0.f;
   check(mle_memcpy_d2h(&out, (g ? X->grad : X->output) + idx, sizeof(float), mle::stream()), "ReadValueAt");
   return out;
 }
 
 void WriteValueAt(const graph& X, const float value, const int& idx, const bool g) {
+  if (g) mle::materialize(X.get());
   check(mle_memcpy_h2d((g ? X->grad : X->output) + idx, &value, sizeof(float), mle::stream()), "WriteValueAt");
 }
 
@@ -415,6 +440,7 @@ void Zerograd(AdamParameter& X) { mle::zero(X.grad, X.total); }
 void Zerograd(graph X) { mle::zero(X->grad, X->total); }
 
 static void print_head(const graph& X, int type, int rows_max, int cols_max) {
+  if (type) mle::materialize(X.get());
   const int ch = X->dim[1], rows = X->dim[2], cols = X->dim[3];
   const long long n = std::min<long long>(X->total, (long long)ch * rows * cols);
   std::vector<float> cpu(n);
@@ -591,6 +617,7 @@ static void nan_check(const graph& node, int type) {
   }
   const float* p = type ? node->grad : node->output;
   if (!p) return;
+  if (type) mle::materialize(node.get());
   const size_t need = mle_sqnorm_ws_bytes(node->total);
   if (wcap < need) {
     ws = mle::alloc_scratch(need);
@@ -656,6 +683,11 @@ void GraphOperations::backward(const graph& X, const bool show, const bool time,
       t0 = std::chrono::high_resolution_clock::now();
     }
     if ((*it)->backward) {
+      // The node reads its own gradient; a backward that does not know about
+      // lazy clearing may add into its inputs' gradients.
+      mle::materialize(it->get());
+      if (!(*it)->lazy_grad_writer)
+        for (auto& in : (*it)->inputs) mle::materialize(in.get());
       (*it)->backward();
       if (check_nan) nan_check(*it, 1);
       if (show) printHeadGPU(*it, 1);
@@ -759,6 +791,7 @@ graph Linear::forward(const graph& X) {
   }
   const int batch = X->dim[0], channels = X->dim[1], m = X->dim[2], n = X->dim[3], p = out;
   auto node = std::make_shared<NodeBackProp>(op_name, batch, channels, m, p, 1);
+  node->lazy_grad_writer = true;
   node->inputs = {X};
   GraphOperations::GB += (double)node->total * sizeof(float) / (1ULL << 30);
   const long long rows = (long long)batch * channels * m;
@@ -781,7 +814,8 @@ graph Linear::forward(const graph& X) {
           "MatMul... X*W1 + B1 in " + name + " forward");
   };
   node->backward = [=]() {
-    check(mle_gemm_ex(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, 0, W->output, p, 0, 1.0f, x->grad, n, 0,
+    const float beta = (float)mle::accumulate_flag(x);
+    check(mle_gemm_ex(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, 0, W->output, p, 0, beta, x->grad, n, 0,
                       1, nullptr, nullptr, ws, ws_bytes),
           "MatMul... dZ*W^T in " + name + " backward");
     check(mle_gemm_ex(mle::stream(), 1, 0, n, p, (int)rows, 1.0f, x->output, n, 0, nd->grad, p, 0, 1.0f, W->grad, p, 0,
@@ -791,7 +825,7 @@ graph Linear::forward(const graph& X) {
   node->free = [=]() { nd->clear(); };
   node->serious_free = [=]() {};
   node->zero_grad = [=]() {
-    mle::zero(nd->grad, nd->total);
+    mle::defer_zero(nd);
     mle::zero(W->grad, W->total);
     if (has_bias) mle::zero(Bb->grad, Bb->total);
   };
@@ -841,6 +875,7 @@ graph Convolute2D::forward(const graph& X) {
   const int batch = X->dim[0], a = X->dim[2], b = X->dim[3];
   const int outR = (2 * pad + a - c) / stride + 1, outC = (2 * pad + b - d) / stride + 1;
   auto node = std::make_shared<NodeBackProp>(name, batch, out, outR, outC, 1);
+  node->lazy_grad_writer = true;
   node->inputs = {X};
   GraphOperations::GB += (double)node->total * sizeof(float) / (1ULL << 30);
   const size_t ws_bytes = mle_conv2d_wgrad_ws_bytes(batch, inp, a, b, out, c, d, pad, stride);
@@ -863,11 +898,12 @@ graph Convolute2D::forward(const graph& X) {
           "Weight Gradient in " + nm);
     check(mle_channel_sum(mle::stream(), nd->grad, batch, out_, (size_t)outR * outC, out_, Bb->grad),
           "Bias Gradient in " + nm);
-    check(mle_conv2d_dgrad(mle::stream(), nd->grad, W->output, x->grad, batch, inp_, a, b, out_, c_, d_, pad_, st),
+    check(mle_conv2d_dgrad(mle::stream(), nd->grad, W->output, x->grad, batch, inp_, a, b, out_, c_, d_, pad_, st,
+                           mle::accumulate_flag(x)),
           "Input Gradient in " + nm);
   };
   node->zero_grad = [=]() {
-    mle::zero(nd->grad, nd->total);
+    mle::defer_zero(nd);
     mle::zero(W->grad, W->total);
     mle::zero(Bb->grad, Bb->total);
   };
@@ -897,6 +933,7 @@ void Embedding::load(std::ifstream& f) { E.load(f); }
 
 graph Embedding::forward(const int32_t* keys, int batch, int clen, int max_clen) {
   auto node = std::make_shared<NodeBackProp>(E.op_name + " lookup", batch, 1, clen, dim, 1);
+  node->lazy_grad_writer = true;
   keys_ = keys;
   batch_ = batch;
   clen_ = clen;
@@ -917,7 +954,7 @@ graph Embedding::forward(const int32_t* keys, int batch, int clen, int max_clen)
           "Embedding gradient");
   };
   node->zero_grad = [=]() {
-    mle::zero(nd->grad, nd->total);
+    mle::defer_zero(nd);
     mle::zero(T->grad, T->total);
   };
   node->free = [=]() { nd->clear(); };

@@ -73,6 +73,19 @@ struct ZeroBatch {
   ~ZeroBatch();
 };
 
+// Lazy gradient clearing for node (non-parameter) gradients.  zero_grad marks
+// a node's gradient as logically zero instead of filling it; the first
+// backward kernel that writes the whole gradient assigns instead of adding
+// (accumulate_flag returns 0 once, then 1), so neither the fill nor the read
+// of the destination happens.  Anything that reads a marked gradient, or
+// writes only part of it, calls materialize() first, which fills it.
+void defer_zero(NodeBackProp* n);
+int accumulate_flag(NodeBackProp* n);
+void materialize(NodeBackProp* n);
+// Off: defer_zero fills at once (the reference's behaviour; results are the
+// same either way).  On by default.
+void set_lazy_zero(bool on);
+
 // Flat parameter arena.  param_reserve(n) announces n floats of parameters that
 // should be contiguous: it sizes the next slab (default 64 Mi floats) and, if
 // the current slab cannot hold n more, makes the next allocation open it.
@@ -120,6 +133,12 @@ struct NodeBackProp {
   // Parameters whose hooks this node carries (additive: lets GraphOperations
   // fuse the optimizer, norm and clip over the flat parameter arena).
   std::vector<AdamParameter*> params;
+  // Lazy clearing state (additive): the gradient is logically zero but not
+  // filled; and whether this node's backward honours that for its inputs (the
+  // engine's ops do; for any other backward the dispatcher fills its inputs'
+  // marked gradients first).
+  bool grad_pending_zero = false;
+  bool lazy_grad_writer = false;
   virtual void update(const float lr = LEARNING_RATE, const bool W = ADAMW) {}
   NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation);
   virtual ~NodeBackProp() = default;

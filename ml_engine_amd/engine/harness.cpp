@@ -43,7 +43,8 @@ void* input_buffer(Model* m, size_t bytes) {
 graph input_node(Model* m, const str& name, int a, int b, int c, int d) {
   auto n = std::make_shared<NodeBackProp>(name, a, b, c, d, 1);
   NodeBackProp* nd = n.get();
-  n->zero_grad = [=]() { mle::zero(nd->grad, nd->total); };
+  n->lazy_grad_writer = true;  // no backward
+  n->zero_grad = [=]() { mle::defer_zero(nd); };
   m->inputs.push_back({n->output, (size_t)n->total * sizeof(float)});
   m->keep.push_back(n);
   return n;
@@ -128,6 +129,8 @@ void build_c2(Model* m, const long long* d, int nd) {
 }  // namespace
 
 extern "C" {
+
+void mle_model_set_lazy_zero(int on) { mle::set_lazy_zero(on != 0); }
 
 void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad) {
   mle::quirks().bmmabt_reference_grad = bmmabt_reference_grad != 0;

@@ -19,6 +19,9 @@ void* mle_model_create(int kind, const long long* dims, int ndims);
 void mle_model_destroy(void* h);
 void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad);
 void mle_model_set_seed(unsigned long long seed);
+/* 1 (default): zero_grad marks node gradients clear and first writers assign;
+ * 0: zero_grad fills them. */
+void mle_model_set_lazy_zero(int on);
 int mle_model_num_params(void* h);
 const char* mle_model_param_name(void* h, int i);
 long long mle_model_param_numel(void* h, int i);

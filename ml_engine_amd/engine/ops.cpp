@@ -2,11 +2,15 @@
 // each builds a node whose forward / backward lambdas enqueue C ABI kernels on
 // the engine stream.  Backward hooks accumulate (+=) into their inputs'
 // gradients, except where the reference assigns (identity, SoftMaxCrossEntropy).
+// A gradient that zero_grad only marked as clear is written by its first
+// writer with assign semantics (mle::accumulate_flag), which gives the same
+// values as adding into zeros without filling or reading the buffer.
 #include "engine.h"
 
 #include <math.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <vector>
 
 using mle::check;
@@ -17,6 +21,7 @@ inline mle_stream S() { return mle::stream(); }
 
 graph make_node(const str& name, int a, int b, int c, int d) {
   auto n = std::make_shared<NodeBackProp>(name, a, b, c, d, 1);
+  n->lazy_grad_writer = true;
   GraphOperations::GB += (double)n->total * sizeof(float) / (1ULL << 30);
   return n;
 }
@@ -24,11 +29,27 @@ graph make_node(const str& name, int a, int b, int c, int d) {
 void std_hooks(const graph& node) {
   NodeBackProp* nd = node.get();
   node->free = [=]() { nd->clear(); };
-  node->zero_grad = [=]() { mle::zero(nd->grad, nd->total); };
+  node->zero_grad = [=]() { mle::defer_zero(nd); };
+}
+
+// dst (+)= scale * src over n floats; assigns when dst's gradient is clear.
+void add_grad(NodeBackProp* dst, const float* src, double scale, size_t n, const str& what) {
+  if (mle::accumulate_flag(dst)) check(mle_accumulate(S(), src, dst->grad, scale, n), what);
+  else check(mle_scale_assign(S(), src, dst->grad, scale, n), what);
 }
 
 // Operand case of BMM-family inputs: (dim0 > 1) + 2*(dim1 > 1) (Engine/engine.cu:2221-2223).
 int bcase(const graph& X) { return (X->dim[0] > 1) + 2 * (X->dim[1] > 1); }
+
+// First-write beta for B's gradient in the BMM family.  The grid follows A's
+// batch and channel sizes, so when B is larger along one of them some of B's
+// blocks receive no gradient: then the clear gradient is filled and added to.
+float b_grad_beta(NodeBackProp* b, int batch, int channels) {
+  const bool covered = (b->dim[0] == 1 || b->dim[0] == batch) && (b->dim[1] == 1 || b->dim[1] == channels);
+  if (covered) return (float)mle::accumulate_flag(b);
+  mle::materialize(b);
+  return 1.0f;
+}
 
 // Element offset of batch item (b, c) for an operand with broadcast code `flag`
 // (batch_chan_offset, Engine/kernels.cu:371-385).
@@ -44,9 +65,11 @@ long long bc_off(int flag, int b, int c, int C, long long inner) {
 // items run one launch at a time, in order: with beta == 1 items that share an
 // output accumulate into it (the reference's atomicAdd epilogue), with beta == 0
 // the last item's product stays (the reference's unordered assignment).
+// first_beta (accumulating calls only): beta of the first write into each
+// output block -- 0 when the destination gradient is clear.
 void grid_gemm(int ta, int tb, int M, int N, int K, const float* A, int64_t lda, int fa, long long asz, const float* B,
                int64_t ldb, int fb, long long bsz, float beta, float* Cc, int64_t ldc, int fc, long long csz,
-               int batch, int channels, const str& what) {
+               int batch, int channels, const str& what, float first_beta = 1.0f) {
   const int z = batch * channels;
   auto stride_of = [&](int flag, long long inner, int64_t& stride) -> bool {
     // offset(b, c) must equal stride * (b*channels + c)
@@ -71,15 +94,25 @@ void grid_gemm(int ta, int tb, int M, int N, int K, const float* A, int64_t lda,
   int64_t sa = 0, sb = 0, sc = 0;
   const bool lin = stride_of(fa, asz, sa) && stride_of(fb, bsz, sb) && stride_of(fc, csz, sc);
   const bool shared_out = (sc == 0 && z > 1) || !lin;
+  const bool accumulating = beta != 0.0f;
   if (!shared_out) {
-    check(mle_gemm(S(), ta, tb, M, N, K, 1.0f, A, lda, sa, B, ldb, sb, beta, Cc, ldc, sc, z, nullptr), what);
+    check(mle_gemm(S(), ta, tb, M, N, K, 1.0f, A, lda, sa, B, ldb, sb, accumulating ? first_beta : beta, Cc, ldc, sc,
+                   z, nullptr),
+          what);
     return;
   }
+  std::vector<long long> written;
   for (int b = 0; b < batch; ++b)
     for (int c = 0; c < channels; ++c) {
       const long long oa = bc_off(fa, b, c, channels, asz), ob = bc_off(fb, b, c, channels, bsz),
                       oc = bc_off(fc, b, c, channels, csz);
-      check(mle_gemm(S(), ta, tb, M, N, K, 1.0f, A + oa, lda, 0, B + ob, ldb, 0, beta, Cc + oc, ldc, 0, 1, nullptr),
+      float bt = beta;
+      if (accumulating) {
+        const bool first = std::find(written.begin(), written.end(), oc) == written.end();
+        if (first) written.push_back(oc);
+        bt = first ? first_beta : 1.0f;
+      }
+      check(mle_gemm(S(), ta, tb, M, N, K, 1.0f, A + oa, lda, 0, B + ob, ldb, 0, bt, Cc + oc, ldc, 0, 1, nullptr),
             what);
     }
 }
@@ -91,7 +124,7 @@ graph act_node(const graph& input, int kind, const str& name) {
   NodeBackProp *nd = node.get(), *x = input.get();
   node->forward = [=]() { check(mle_act_fwd(S(), kind, x->output, nd->output, nd->total), name + " forward"); };
   node->backward = [=]() {
-    check(mle_act_bwd(S(), kind, x->output, nd->grad, x->grad, nd->total), "Deriv " + name);
+    check(mle_act_bwd(S(), kind, x->output, nd->grad, x->grad, nd->total, mle::accumulate_flag(x)), "Deriv " + name);
   };
   std_hooks(node);
   return node;
@@ -107,7 +140,8 @@ graph softmax_node(const graph& X, int type, bool masked, const str& name) {
     check(mle_softmax_fwd(S(), x->output, nd->output, a * b, c, d, axis, masked ? 1 : 0), name + " forward");
   };
   node->backward = [=]() {
-    check(mle_softmax_bwd(S(), nd->output, nd->grad, x->grad, a * b, c, d, axis), "Deriv " + name);
+    check(mle_softmax_bwd(S(), nd->output, nd->grad, x->grad, a * b, c, d, axis, mle::accumulate_flag(x)),
+          "Deriv " + name);
   };
   std_hooks(node);
   return node;
@@ -128,7 +162,8 @@ graph norm_node(const graph& X, int groups, const str& name) {
     check(mle_norm_fwd(S(), x->output, nd->output, stats, a, b, hw, groups, eps, ws, ws_bytes), name + " forward");
   };
   node->backward = [=]() {
-    check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, 1, ws, ws_bytes),
+    check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, 1, ws, ws_bytes,
+                       mle::accumulate_flag(x)),
           name + " backward");
   };
   std_hooks(node);
@@ -143,7 +178,7 @@ graph GraphOperations::Copy(const graph& X) {
   node->inputs = {X};
   NodeBackProp *nd = node.get(), *x = X.get();
   node->forward = [=]() { check(mle_scale_write(S(), x->output, nd->output, 1.0f, nd->total), "Copy forward"); };
-  node->backward = [=]() { check(mle_accumulate(S(), nd->grad, x->grad, 1.0, nd->total), "Copy backward"); };
+  node->backward = [=]() { add_grad(x, nd->grad, 1.0, nd->total, "Copy backward"); };
   std_hooks(node);
   return node;
 }
@@ -164,7 +199,10 @@ graph GraphOperations::identity(const graph& X) {
   node->inputs = {X};
   NodeBackProp *nd = node.get(), *x = X.get();
   node->forward = [=]() { check(mle_scale_write(S(), x->output, nd->output, 1.0f, nd->total), "identity forward"); };
-  node->backward = [=]() { check(mle_scale_write(S(), nd->grad, x->grad, 1.0f, nd->total), "identity backward"); };
+  node->backward = [=]() {
+    mle::accumulate_flag(x);  // assigns whole gradient: it is no longer clear
+    check(mle_scale_write(S(), nd->grad, x->grad, 1.0f, nd->total), "identity backward");
+  };
   std_hooks(node);
   return node;
 }
@@ -193,7 +231,10 @@ graph GraphOperations::HeadifytoChannel(const graph& X, const int heads) {
   node->inputs = {X};
   NodeBackProp *nd = node.get(), *x = X.get();
   node->forward = [=]() { check(mle_headify(S(), x->output, nd->output, b, heads, seq, hd, 0), "Headify forward"); };
-  node->backward = [=]() { check(mle_headify(S(), nd->grad, x->grad, b, heads, seq, hd, 1), "Headify backward"); };
+  node->backward = [=]() {
+    const int flag = mle::accumulate_flag(x) ? 1 : 2;  // 2: the assigning form of the same permutation
+    check(mle_headify(S(), nd->grad, x->grad, b, heads, seq, hd, flag), "Headify backward");
+  };
   std_hooks(node);
   return node;
 }
@@ -205,7 +246,10 @@ graph GraphOperations::DeHeadify(const graph& X) {
   node->inputs = {X};
   NodeBackProp *nd = node.get(), *x = X.get();
   node->forward = [=]() { check(mle_headify(S(), x->output, nd->output, b, heads, seq, hd, 2), "DeHeadify forward"); };
-  node->backward = [=]() { check(mle_headify(S(), nd->grad, x->grad, b, heads, seq, hd, 3), "DeHeadify backward"); };
+  node->backward = [=]() {
+    const int flag = mle::accumulate_flag(x) ? 3 : 0;  // 0: the assigning form of the same permutation
+    check(mle_headify(S(), nd->grad, x->grad, b, heads, seq, hd, flag), "DeHeadify backward");
+  };
   std_hooks(node);
   return node;
 }
@@ -233,7 +277,7 @@ graph GraphOperations::MatrixPositionalEncoding(const graph& X, const int start_
   node->inputs = {X};
   NodeBackProp *nd = node.get(), *x = X.get();
   node->forward = [=]() { check(mle_matpe(S(), x->output, nd->output, batch, rows, cols, start_idx), "MatPE forward"); };
-  node->backward = [=]() { check(mle_accumulate(S(), nd->grad, x->grad, 1.0, nd->total), "MatPE backward"); };
+  node->backward = [=]() { add_grad(x, nd->grad, 1.0, nd->total, "MatPE backward"); };
   std_hooks(node);
   return node;
 }
@@ -257,7 +301,8 @@ graph GraphOperations::Broadcast_Channel(const graph& A, const graph& B) {
           "Broadcast Add forward");
   };
   node->backward = [=]() {
-    check(mle_accumulate(S(), nd->grad, pa->grad, 1.0, nd->total), "Broadcast Add backward - A grad");
+    add_grad(pa, nd->grad, 1.0, nd->total, "Broadcast Add backward - A grad");
+    mle::materialize(pb);  // reduces into (possibly only some of) B's channels
     check(mle_channel_sum(S(), nd->grad, batch, channels, hw, nreduce, pb->grad), "Broadcast Add backward - B grad");
   };
   std_hooks(node);
@@ -273,7 +318,7 @@ graph GraphOperations::Scale(const graph& input, const float scale, const bool l
   node->forward = [=]() { check(mle_scale_write(S(), x->output, nd->output, scale, nd->total), "Scale forward"); };
   node->backward = [=]() {
     if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Scale seed");
-    check(mle_accumulate(S(), nd->grad, x->grad, (double)scale, nd->total), "Deriv Scale");
+    add_grad(x, nd->grad, (double)scale, nd->total, "Deriv Scale");
   };
   std_hooks(node);
   return node;
@@ -297,8 +342,8 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
   };
   node->backward = [=]() {
     if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
-    check(mle_accumulate(S(), nd->grad, pa->grad, 1.0, nd->total), "Add backward - A grad");
-    check(mle_accumulate(S(), nd->grad, pb->grad, 1.0, nd->total), "Add backward - B grad");
+    add_grad(pa, nd->grad, 1.0, nd->total, "Add backward - A grad");
+    add_grad(pb, nd->grad, 1.0, nd->total, "Add backward - B grad");
   };
   std_hooks(node);
   return node;
@@ -314,6 +359,7 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
       std::exit(1);
     }
   auto node = std::make_shared<NodeBackProp>("MSE", 1, 1, 1, 1, 1);
+  node->lazy_grad_writer = true;
   node->inputs = {prediction, target};
   GB += (double)(prediction->total + target->total + 1) * sizeof(float) / (1ULL << 30);
   NodeBackProp *nd = node.get(), *pr = prediction.get(), *tg = target.get();
@@ -327,7 +373,8 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
     }
   };
   node->backward = [=]() {
-    check(mle_mse_bwd(S(), pr->output, tg->output, last ? nullptr : nd->grad, pr->grad, n), "deriv MSE");
+    check(mle_mse_bwd(S(), pr->output, tg->output, last ? nullptr : nd->grad, pr->grad, n, mle::accumulate_flag(pr)),
+          "deriv MSE");
   };
   node->free = [=]() { nd->clear(); };
   node->zero_grad = [=]() { mle::zero(nd->output, 1); };
@@ -347,6 +394,7 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
     }
   const int batch = target->dim[0], channels = target->dim[1], c = target->dim[2], d = target->dim[3];
   auto node = std::make_shared<NodeBackProp>("SoftMaxCrossEntropy Loss", 1, 1, 1, 1, 1);
+  node->lazy_grad_writer = true;
   node->inputs = {prediction, target};
   GB += (double)(target->total + 1) * sizeof(float) / (1ULL << 30);
   const size_t n = prediction->total;
@@ -363,6 +411,7 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
     }
   };
   node->backward = [=]() {
+    mle::accumulate_flag(pr);  // the reference assigns the whole gradient
     check(mle_softmax_xent_bwd(S(), probs, tg->output, last ? nullptr : nd->grad, pr->grad, n, batch),
           "derivative of CE in CE backward");
   };
@@ -401,9 +450,9 @@ graph GraphOperations::BMM(const graph& A, const graph& B) {
   };
   node->backward = [=]() {
     grid_gemm(0, 1, m, n, p, nd->grad, p, fc, csz, pb->output, p, fb, bsz, 1.0f, pa->grad, n, fa, asz, batch, channels,
-              "BMM dA = dZ B^T");
+              "BMM dA = dZ B^T", (float)mle::accumulate_flag(pa));
     grid_gemm(1, 0, n, p, m, pa->output, n, fa, asz, nd->grad, p, fc, csz, 1.0f, pb->grad, p, fb, bsz, batch, channels,
-              "BMM dB = A^T dZ");
+              "BMM dB = A^T dZ", b_grad_beta(pb, batch, channels));
   };
   std_hooks(node);
   return node;
@@ -432,13 +481,13 @@ graph GraphOperations::BMMABT(const graph& A, const graph& B) {
   };
   node->backward = [=]() {
     grid_gemm(0, 0, m, n, p, nd->grad, p, fc, csz, pb->output, n, fb, bsz, 1.0f, pa->grad, n, fa, asz, batch, channels,
-              "BMMABT dA = dZ B");
+              "BMMABT dA = dZ B", (float)mle::accumulate_flag(pa));
     if (ref_grad)
       grid_gemm(1, 1, n, p, m, pa->output, n, fa, asz, nd->grad, m, fc, csz, 1.0f, pb->grad, p, fb, bsz, batch,
-                channels, "BMMABT dB (reference bcmmT)");
+                channels, "BMMABT dB (reference bcmmT)", b_grad_beta(pb, batch, channels));
     else
       grid_gemm(1, 0, p, n, m, nd->grad, p, fc, csz, pa->output, n, fa, asz, 1.0f, pb->grad, n, fb, bsz, batch,
-                channels, "BMMABT dB = dZ^T A");
+                channels, "BMMABT dB = dZ^T A", b_grad_beta(pb, batch, channels));
   };
   std_hooks(node);
   return node;

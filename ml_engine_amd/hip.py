@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_scale_add": (I, [P, P, P, P, F, SZ]),
     "mle_accumulate": (I, [P, P, P, D, SZ]),
     "mle_scale_write": (I, [P, P, P, F, SZ]),
+    "mle_scale_assign": (I, [P, P, P, D, SZ]),
     "mle_scale_inplace": (I, [P, P, F, I, SZ]),
     "mle_scale_by_device": (I, [P, P, P, I, SZ]),
     "mle_bias_add_rows": (I, [P, P, P, SZ, I]),
@@ -51,24 +52,24 @@ SIGNATURES: dict[str, tuple] = {
     "mle_matpe": (I, [P, P, P, I, I, I, I]),
     "mle_timestep_pe": (I, [P, P, I, I]),
     "mle_act_fwd": (I, [P, I, P, P, SZ]),
-    "mle_act_bwd": (I, [P, I, P, P, P, SZ]),
+    "mle_act_bwd": (I, [P, I, P, P, P, SZ, I]),
     "mle_gemm": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P]),
     "mle_gemm_ws_bytes": (SZ, [I, I, I, I]),
     "mle_gemm_ex": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P, P, P, SZ]),
     "mle_colsum": (I, [P, P, SZ, I, P, F]),
     "mle_channel_sum": (I, [P, P, I, I, SZ, I, P]),
     "mle_softmax_fwd": (I, [P, P, P, I, I, I, I, I]),
-    "mle_softmax_bwd": (I, [P, P, P, P, I, I, I, I]),
+    "mle_softmax_bwd": (I, [P, P, P, P, I, I, I, I, I]),
     "mle_loss_ws_bytes": (SZ, [SZ]),
     "mle_mse_fwd": (I, [P, P, P, SZ, P, P, SZ]),
-    "mle_mse_bwd": (I, [P, P, P, P, P, SZ]),
+    "mle_mse_bwd": (I, [P, P, P, P, P, SZ, I]),
     "mle_softmax_xent_fwd": (I, [P, P, P, P, I, I, P, P, SZ]),
     "mle_softmax_xent_bwd": (I, [P, P, P, P, P, SZ, I]),
     "mle_norm_ws_bytes": (SZ, [I, I, SZ, I]),
     "mle_norm_fwd": (I, [P, P, P, P, I, I, SZ, I, F, P, SZ]),
-    "mle_norm_bwd": (I, [P, P, P, P, P, I, I, SZ, I, F, I, P, SZ]),
+    "mle_norm_bwd": (I, [P, P, P, P, P, I, I, SZ, I, F, I, P, SZ, I]),
     "mle_conv2d_fwd": (I, [P, P, P, P, P, I, I, I, I, I, I, I, I, I]),
-    "mle_conv2d_dgrad": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I]),
+    "mle_conv2d_dgrad": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, I]),
     "mle_conv2d_wgrad_ws_bytes": (SZ, [I, I, I, I, I, I, I, I, I]),
     "mle_conv2d_wgrad": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P, SZ]),
     "mle_sqnorm_ws_bytes": (SZ, [SZ]),

@@ -225,3 +225,47 @@ def test_golden_c5_engine(hip):
     assert abs(loss - float(fx["loss"])) <= 1e-5 * abs(float(fx["loss"]))
     for i, (a, b) in enumerate(zip(got, grads(fx))):
         assert_close(a, b, what=f"golden c5 grad {i}", **GRAD)
+
+
+# ------------------------------------ lazy gradient clearing is invisible
+def _run_sequence(kind, dims, params, inputs, lr, lazy):
+    """zero+fwd+bwd, then fwd+bwd again without zero_grad (the reference keeps
+    adding into node and parameter gradients), then a full step with update."""
+    from ml_engine_amd.models import STEP_BACKWARD, STEP_FORWARD, STEP_ZERO
+    m = Model(kind, dims, reference_quirks=True, lazy_zero=lazy)
+    for i, p in enumerate(params):
+        m.set(i, p)
+    for slot, x in enumerate(inputs):
+        m.input(slot, x)
+    out = []
+    m.step(lr, STEP_ZERO | STEP_FORWARD | STEP_BACKWARD)
+    m.sync()
+    out.append([m.get(i, 1) for i in range(len(params))])
+    m.step(lr, STEP_FORWARD | STEP_BACKWARD)
+    m.sync()
+    out.append([m.get(i, 1) for i in range(len(params))])
+    m.step(lr, STEP_ALL)
+    m.step(lr, STEP_ALL)
+    m.sync()
+    out.append([m.get(i, 0) for i in range(len(params))])
+    m.close()
+    return out
+
+
+@pytest.mark.parametrize("kind", ["block", "resblock"])
+def test_lazy_zero_matches_eager(hip, kind):
+    if kind == "block":
+        cfg = BlockConfig(batch=2, seq=32, d_model=64, heads=4, ffn=128, vocab=97)
+        ids, tgt, params = block_data(cfg, seed=3)
+        dims, inputs = cfg.dims(), [ids, tgt]
+    else:
+        cfg = ResBlockConfig(batch=2, cin=8, cout=16, h=12, w=12, groups=4, tdim=32)
+        x, noise, t, params = resblock_data(cfg, seed=4)
+        dims, inputs = cfg.dims(t), [x, noise]
+    lazy = _run_sequence(kind, dims, params, inputs, cfg.lr, True)
+    eager = _run_sequence(kind, dims, params, inputs, cfg.lr, False)
+    for phase, (a, b) in enumerate(zip(lazy, eager)):
+        for i, (u, v) in enumerate(zip(a, b)):
+            assert np.array_equal(u, v), f"{kind}: phase {phase} tensor {i} differs between lazy and eager clearing"
+    # the second backward without zero_grad really accumulated
+    assert not np.array_equal(lazy[0][-1], lazy[1][-1])

@@ -135,9 +135,15 @@ def test_activation(hip, orc, kind):
     orc.call("orc_act_bwd", k, orc.ptr(x), orc.ptr(dy), orc.ptr(dxr), n)
     gx, gy, gdy, gdx = B(hip, x), hip.Buffer.zeros(n), B(hip, dy), B(hip, dx0)
     hip.call("mle_act_fwd", None, k, gx.ptr, gy.ptr, n)
-    hip.call("mle_act_bwd", None, k, gx.ptr, gdy.ptr, gdx.ptr, n)
+    hip.call("mle_act_bwd", None, k, gx.ptr, gdy.ptr, gdx.ptr, n, 1)
     assert_close(gy.numpy(), yr, what=f"{kind} fwd", **EW)
     assert_close(gdx.numpy(), dxr, what=f"{kind} bwd", **EW)
+    # assign: the destination is not read (NaN stays out), value = the sum into zeros
+    dxz = np.zeros_like(x)
+    orc.call("orc_act_bwd", k, orc.ptr(x), orc.ptr(dy), orc.ptr(dxz), n)
+    hip.call("mle_fill", None, gdx.ptr, float("nan"), n)
+    hip.call("mle_act_bwd", None, k, gx.ptr, gdy.ptr, gdx.ptr, n, 0)
+    assert_close(gdx.numpy(), dxz, what=f"{kind} bwd assign", **EW)
 
 
 # ----------------------------------------------------------------------- softmax
@@ -158,8 +164,13 @@ def test_softmax(hip, orc, bc, rows, cols, axis, causal):
     y = gy.numpy()
     assert_close(y, yr, what="softmax fwd", **EW)
     gyr, gdy, gdx = B(hip, yr), B(hip, dy), B(hip, dx0)
-    hip.call("mle_softmax_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, bc, rows, cols, axis)
+    hip.call("mle_softmax_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, bc, rows, cols, axis, 1)
     assert_close(gdx.numpy(), dxr, what="softmax bwd", **EW)
+    dxz = np.zeros_like(x)
+    orc.call("orc_softmax_bwd", orc.ptr(yr), orc.ptr(dy), orc.ptr(dxz), bc, rows, cols, axis)
+    hip.call("mle_fill", None, gdx.ptr, float("nan"), x.size)
+    hip.call("mle_softmax_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, bc, rows, cols, axis, 0)
+    assert_close(gdx.numpy(), dxz, what="softmax bwd assign", **EW)
 
 
 def test_softmax_xent(hip, orc):
@@ -182,9 +193,9 @@ def test_softmax_xent(hip, orc):
     assert_close(gd.numpy(), dl, what="xent bwd", **EW)
 
 
-def test_mse(hip, orc):
+@pytest.mark.parametrize("n", [123457, 123456])
+def test_mse(hip, orc, n):
     r = rng(6)
-    n = 123457
     x = r.standard_normal(n, dtype=np.float32)
     t = r.standard_normal(n, dtype=np.float32)
     dx0 = r.standard_normal(n, dtype=np.float32)
@@ -194,9 +205,14 @@ def test_mse(hip, orc):
     gx, gt, gl, gdx = B(hip, x), B(hip, t), hip.Buffer.zeros(1), B(hip, dx0)
     ws = hip.Buffer(hip.lib().mle_loss_ws_bytes(n))
     hip.call("mle_mse_fwd", None, gx.ptr, gt.ptr, n, gl.ptr, ws.ptr, ws.nbytes)
-    hip.call("mle_mse_bwd", None, gx.ptr, gt.ptr, None, gdx.ptr, n)
+    hip.call("mle_mse_bwd", None, gx.ptr, gt.ptr, None, gdx.ptr, n, 1)
     assert_close(gl.numpy(), np.array([lref], np.float32), what="mse loss", **EW)
     assert_close(gdx.numpy(), dxr, what="mse bwd", **EW)
+    dxz = np.zeros_like(x)
+    orc.call("orc_mse_bwd", orc.ptr(x), orc.ptr(t), None, orc.ptr(dxz), n)
+    hip.call("mle_fill", None, gdx.ptr, float("nan"), n)
+    hip.call("mle_mse_bwd", None, gx.ptr, gt.ptr, None, gdx.ptr, n, 0)
+    assert_close(gdx.numpy(), dxz, what="mse bwd assign", **EW)
 
 
 # ------------------------------------------------------------------------ norms
@@ -221,8 +237,14 @@ def test_norm(hip, orc, batch, channels, hw, groups):
     assert_close(gst.numpy(), st, what="norm stats", **EW)
     gyr, gdy, gdx, gstr = B(hip, yr), B(hip, dy), B(hip, dx0), B(hip, st)
     hip.call("mle_norm_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, gstr.ptr, batch, channels, hw, groups, 1e-5, 1,
-             ws.ptr, ws.nbytes)
+             ws.ptr, ws.nbytes, 1)
     assert_close(gdx.numpy(), dxr, what="norm bwd", **EW)
+    dxz = np.zeros_like(x)
+    orc.call("orc_norm_bwd", orc.ptr(yr), orc.ptr(dy), orc.ptr(dxz), orc.ptr(st), batch, channels, hw, groups, 1e-5, 1)
+    hip.call("mle_fill", None, gdx.ptr, float("nan"), x.size)
+    hip.call("mle_norm_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, gstr.ptr, batch, channels, hw, groups, 1e-5, 1,
+             ws.ptr, ws.nbytes, 0)
+    assert_close(gdx.numpy(), dxz, what="norm bwd assign", **EW)
 
 
 # ---------------------------------------------------------------------- conv
@@ -253,8 +275,13 @@ def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
     hip.call("mle_conv2d_fwd", None, gx.ptr, gw.ptr, gb.ptr, gy.ptr, n, cin, h, w, cout, k, k, pad, stride)
     assert_close(gy.numpy(), yr, what="conv fwd", **MM)
     gdy, gdx = B(hip, dy), B(hip, dx0)
-    hip.call("mle_conv2d_dgrad", None, gdy.ptr, gw.ptr, gdx.ptr, n, cin, h, w, cout, k, k, pad, stride)
+    hip.call("mle_conv2d_dgrad", None, gdy.ptr, gw.ptr, gdx.ptr, n, cin, h, w, cout, k, k, pad, stride, 1)
     assert_close(gdx.numpy(), dxr, what="conv dgrad", **MM)
+    dxz = np.zeros_like(x)
+    orc.call("orc_conv_dgrad", orc.ptr(dy), orc.ptr(wt), orc.ptr(dxz), n, cin, h, w, cout, k, k, pad, stride)
+    hip.call("mle_fill", None, gdx.ptr, float("nan"), x.size)
+    hip.call("mle_conv2d_dgrad", None, gdy.ptr, gw.ptr, gdx.ptr, n, cin, h, w, cout, k, k, pad, stride, 0)
+    assert_close(gdx.numpy(), dxz, what="conv dgrad assign", **MM)
     L = hip.lib()
     ws = hip.Buffer(L.mle_conv2d_wgrad_ws_bytes(n, cin, h, w, cout, k, k, pad, stride))
     gdw = B(hip, np.full(wt.shape, 7.0, np.float32))  # wgrad assigns
@@ -397,6 +424,13 @@ def test_elementwise_and_layout(hip, orc):
     orc.call("orc_accumulate", orc.ptr(x), orc.ptr(acc), 0.125, n)
     hip.call("mle_accumulate", None, gx.ptr, gy.ptr, 0.125, n)
     np.testing.assert_array_equal(gy.numpy(), acc)
+    # scale_assign is accumulate into zeros, bit for bit, without reading y
+    for sc in (0.125, 0.3, 1.0):
+        acc0 = np.zeros(n, np.float32)
+        orc.call("orc_accumulate", orc.ptr(x), orc.ptr(acc0), sc, n)
+        hip.call("mle_fill", None, gy.ptr, float("nan"), n)
+        hip.call("mle_scale_assign", None, gx.ptr, gy.ptr, sc, n)
+        np.testing.assert_array_equal(gy.numpy(), acc0)
 
     bsz, heads, seq, hd = 2, 4, 9, 8
     flat = r.standard_normal((bsz, 1, seq, heads * hd), dtype=np.float32)
