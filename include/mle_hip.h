@@ -197,6 +197,19 @@ int mle_softmax_xent_fwd(mle_stream stream, const float* logits, const float* ta
 int mle_softmax_xent_bwd(mle_stream stream, const float* probs, const float* target, const float* upstream,
                          float* dlogits, size_t n, int batch);
 
+/* Cross-entropy against one-hot rows given by token ids: row r = b*clen + s
+ * has its 1 at column keys[b*max_clen + s] if that id is in [0, cols), else
+ * no 1 -- the matrix OneHotEmbeddings builds (Engine/kernels.cu:1551-1560).
+ * Forward writes the loss (as mle_softmax_xent_fwd, bit for bit) and each
+ * row's (max, sum) to stats[rows][2] instead of the probabilities; backward
+ * assigns dlogits = (p - t) * (upstream ? upstream[0] : 1) / batch with p
+ * recomputed from logits and stats (as mle_softmax_xent_bwd, bit for bit). */
+int mle_softmax_xent_keys_fwd(mle_stream stream, const float* logits, const int32_t* keys, int clen, int max_clen,
+                              float* stats, int rows, int cols, float* loss, void* ws, size_t ws_bytes);
+int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const float* stats, const int32_t* keys,
+                              int clen, int max_clen, const float* upstream, float* dlogits, int rows, int cols,
+                              int batch);
+
 /* ------------------------------------------------------------------------- */
 /* Normalisation (gamma = 1, beta = 0, as the reference)                     */
 /* ------------------------------------------------------------------------- */

@@ -4,6 +4,8 @@
 // with wave64 shuffles, instead of the reference's 4 launches with one thread
 // per line (SoftMax/SoftMask/deriv_softmax, Engine/kernels.cu:2003-2244).
 #include "common.hpp"
+
+#include <algorithm>
 #include <float.h>
 
 using namespace mle;
@@ -16,21 +18,39 @@ constexpr int COL_W = 64;    // column kernels: 64 columns per workgroup
 constexpr int COL_RL = 4;    // ... and 4 row lanes
 constexpr int COL_RPT = 64;  // ... caching up to COL_RL*COL_RPT = 256 rows
 
+// Cross-entropy target given as token ids (the one-hot matrix OneHotEmbeddings
+// would build, Engine/kernels.cu:1551-1560): row r = b*clen + s has its single
+// 1 at column keys[b*max_clen + s] when that id is in [0, cols), else no 1.
+// With it the row kernels store each row's (max, sum) in stats instead of the
+// probabilities, and the backward recomputes p from them.
+struct KeyTargets {
+  const int32_t* keys;  // nullptr: dense target (or none)
+  int clen, max_clen;
+  float* stats;         // [rows][2] = (max, sum)
+  __device__ int key(size_t line, int cols) const {
+    const int k = keys[(line / clen) * max_clen + (line % clen)];
+    return (k >= 0 && k < cols) ? k : -1;
+  }
+};
+
 // ---------------------------------------------------------------------------
 // Row softmax (type 0).  One workgroup per line of `cols` elements.  With
 // `target` set, also writes this row's -sum(t log(p + 1e-27)) (double) to
-// loss_part[row] (scalar_ce_kernel, Engine/kernels.cu:1818-1826).
+// loss_part[row] (scalar_ce_kernel, Engine/kernels.cu:1818-1826).  With key
+// targets the term of the one column whose t is 1 is the row's sum (the other
+// terms are zeros), and y may be null.
 template <bool CACHED>
 __global__ __launch_bounds__(NT) void softmax_row_kernel(const float* __restrict__ x, float* __restrict__ y, int rows,
                                                          int cols, int causal, const float* __restrict__ target,
-                                                         double* __restrict__ loss_part) {
+                                                         double* __restrict__ loss_part, KeyTargets kt) {
   __shared__ float redf[NT / 64];
   __shared__ double redd[NT / 64];
   const size_t line = blockIdx.x;
   const int r_in = (int)(line % rows);
   const float* xr = x + line * cols;
-  float* yr = y + line * cols;
+  float* yr = y ? y + line * cols : nullptr;
   const int lim = causal ? min(cols, r_in + 1) : cols;  // entries c > r are masked
+  const int key = kt.keys ? kt.key(line, cols) : -1;
   float v[CACHED ? ROW_CPT : 1];
   float mx = -FLT_MAX;
   if (CACHED) {
@@ -64,20 +84,26 @@ __global__ __launch_bounds__(NT) void softmax_row_kernel(const float* __restrict
       const int c = threadIdx.x + i * NT;
       if (c < cols) {
         const float p = v[i] / sum;
-        yr[c] = p;
+        if (yr) yr[c] = p;
         if (target) lp += -(double)target[line * cols + c] * log((double)p + 1e-27);
+        if (c == key) lp = -log((double)p + 1e-27);
       }
     }
   } else {
     for (int c = threadIdx.x; c < cols; c += NT) {
       const float p = (c < lim) ? expf(xr[c] - mx) / sum : 0.f;
-      yr[c] = p;
+      if (yr) yr[c] = p;
       if (target) lp += -(double)target[line * cols + c] * log((double)p + 1e-27);
+      if (c == key) lp = -log((double)p + 1e-27);
     }
   }
-  if (target) {
+  if (target || kt.keys) {
     lp = block_sum<NT>(lp, redd);
     if (threadIdx.x == 0) loss_part[line] = lp;
+  }
+  if (kt.stats && threadIdx.x == 0) {
+    kt.stats[2 * line] = mx;
+    kt.stats[2 * line + 1] = sum;
   }
 }
 
@@ -88,13 +114,14 @@ __device__ __forceinline__ void stv(float* p, size_t i, f32x4 v) { *reinterpret_
 
 __global__ __launch_bounds__(NT) void softmax_row4_kernel(const float* __restrict__ x, float* __restrict__ y, int rows,
                                                           int cols, int causal, const float* __restrict__ target,
-                                                          double* __restrict__ loss_part) {
+                                                          double* __restrict__ loss_part, KeyTargets kt) {
   __shared__ float redf[NT / 64];
   __shared__ double redd[NT / 64];
   const size_t line = blockIdx.x;
   const int r_in = (int)(line % rows);
   const size_t base = line * cols;
   const int lim = causal ? min(cols, r_in + 1) : cols;
+  const int key = kt.keys ? kt.key(line, cols) : -1;
   f32x4 v[RV4];
   float mx = -FLT_MAX;
 #pragma unroll
@@ -125,18 +152,23 @@ __global__ __launch_bounds__(NT) void softmax_row4_kernel(const float* __restric
       f32x4 p;
 #pragma unroll
       for (int j = 0; j < 4; ++j) p[j] = v[i][j] / sum;
-      stv(y, base + c, p);
+      if (y) stv(y, base + c, p);
       if (target) {
         const f32x4 t = ldv(target, base + c);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (t[j] != 0.f) lp += -(double)t[j] * log((double)p[j] + 1e-27);
       }
+      if (key >= c && key < c + 4) lp = -log((double)p[key - c] + 1e-27);
     }
   }
-  if (target) {
+  if (target || kt.keys) {
     lp = block_sum<NT>(lp, redd);
     if (threadIdx.x == 0) loss_part[line] = lp;
+  }
+  if (kt.stats && threadIdx.x == 0) {
+    kt.stats[2 * line] = mx;
+    kt.stats[2 * line + 1] = sum;
   }
 }
 
@@ -452,6 +484,45 @@ __global__ __launch_bounds__(NT) void xent_bwd4_kernel(const float* __restrict__
   }
 }
 
+// dlogits = (p - t) * (upstream ? upstream[0] : 1) / batch with t from key
+// targets and p = exp(x - max) / sum recomputed from the forward's row stats,
+// in the operations the probability path uses (same values, bit for bit).
+// Grid: x over float4 column groups, y over rows (looping past 65535).
+__global__ __launch_bounds__(NT) void xent_keys_bwd4_kernel(const float* __restrict__ x, const float* __restrict__ stats,
+                                                            KeyTargets kt, const float* __restrict__ up,
+                                                            float* __restrict__ dl, int rows, int cols, float batch) {
+  const int c = (blockIdx.x * NT + threadIdx.x) * 4;
+  if (c >= cols) return;
+  for (int line = blockIdx.y; line < rows; line += gridDim.y) {
+    const float mx = stats[2 * line], sum = stats[2 * line + 1];
+    const int key = kt.key(line, cols);
+    const size_t o = (size_t)line * cols + c;
+    const f32x4 xv = ldv(x, o);
+    f32x4 g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = expf(xv[j] - mx) / sum;
+      g[j] = p + (-1.0f) * (c + j == key ? 1.0f : 0.0f);
+    }
+    if (up) g *= up[0];
+    stv(dl, o, g / batch);
+  }
+}
+
+__global__ __launch_bounds__(NT) void xent_keys_bwd_kernel(const float* __restrict__ x, const float* __restrict__ stats,
+                                                           KeyTargets kt, const float* __restrict__ up,
+                                                           float* __restrict__ dl, int rows, int cols, float batch) {
+  const int c = blockIdx.x * NT + threadIdx.x;
+  if (c >= cols) return;
+  for (int line = blockIdx.y; line < rows; line += gridDim.y) {
+    const float mx = stats[2 * line], sum = stats[2 * line + 1];
+    const float p = expf(x[(size_t)line * cols + c] - mx) / sum;
+    float g = p + (-1.0f) * (c == kt.key(line, cols) ? 1.0f : 0.0f);
+    if (up) g *= up[0];
+    dl[(size_t)line * cols + c] = g / batch;
+  }
+}
+
 constexpr unsigned kMsePartCap = 2048;
 
 }  // namespace
@@ -467,11 +538,11 @@ int mle_softmax_fwd(mle_stream stream, const float* x, float* y, int bc, int row
     const size_t lines = (size_t)bc * rows;
     MLE_CHECK_ARG(lines <= 2147483647u, "mle_softmax_fwd: too many rows");
     if (vec && cols <= 4 * NT * RV4)
-      softmax_row4_kernel<<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr);
+      softmax_row4_kernel<<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr, KeyTargets{});
     else if (cols <= NT * ROW_CPT)
-      softmax_row_kernel<true><<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr);
+      softmax_row_kernel<true><<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr, KeyTargets{});
     else
-      softmax_row_kernel<false><<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr);
+      softmax_row_kernel<false><<<(unsigned)lines, NT, 0, s>>>(x, y, rows, cols, causal, nullptr, nullptr, KeyTargets{});
   } else {
     MLE_CHECK_ARG(bc <= 65535, "mle_softmax_fwd: bc %d > 65535", bc);
     dim3 grid((cols + COL_W - 1) / COL_W, bc);
@@ -545,11 +616,11 @@ int mle_softmax_xent_fwd(mle_stream stream, const float* logits, const float* ta
   hipStream_t s = as_stream(stream);
   double* part = static_cast<double*>(ws);
   if (cols % 4 == 0 && cols <= 4 * NT * RV4 && aligned16(logits) && aligned16(probs) && aligned16(target))
-    softmax_row4_kernel<<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part);
+    softmax_row4_kernel<<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part, KeyTargets{});
   else if (cols <= NT * ROW_CPT)
-    softmax_row_kernel<true><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part);
+    softmax_row_kernel<true><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part, KeyTargets{});
   else
-    softmax_row_kernel<false><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part);
+    softmax_row_kernel<false><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part, KeyTargets{});
   finish_scalar_kernel<<<1, NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
   return check_launch("mle_softmax_xent_fwd");
 }
@@ -565,6 +636,44 @@ int mle_softmax_xent_bwd(mle_stream stream, const float* probs, const float* tar
     xent_bwd_kernel<<<stream_grid(n, NT, 8192), NT, 0, as_stream(stream)>>>(probs, target, upstream, dlogits, n,
                                                                            (float)batch);
   return check_launch("mle_softmax_xent_bwd");
+}
+
+int mle_softmax_xent_keys_fwd(mle_stream stream, const float* logits, const int32_t* keys, int clen, int max_clen,
+                              float* stats, int rows, int cols, float* loss, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(logits && keys && stats && loss && ws && rows > 0 && cols > 0 && clen > 0 && max_clen >= clen &&
+                    rows % clen == 0,
+                "mle_softmax_xent_keys_fwd: bad argument");
+  if (ws_bytes < (size_t)rows * sizeof(double))
+    return set_error(MLE_ERR_WORKSPACE, "mle_softmax_xent_keys_fwd: workspace too small");
+  hipStream_t s = as_stream(stream);
+  double* part = static_cast<double*>(ws);
+  const KeyTargets kt{keys, clen, max_clen, stats};
+  // The kernel choice matches mle_softmax_xent_fwd's, so sums and loss agree bit for bit.
+  if (cols % 4 == 0 && cols <= 4 * NT * RV4 && aligned16(logits))
+    softmax_row4_kernel<<<rows, NT, 0, s>>>(logits, nullptr, rows, cols, 0, nullptr, part, kt);
+  else if (cols <= NT * ROW_CPT)
+    softmax_row_kernel<true><<<rows, NT, 0, s>>>(logits, nullptr, rows, cols, 0, nullptr, part, kt);
+  else
+    softmax_row_kernel<false><<<rows, NT, 0, s>>>(logits, nullptr, rows, cols, 0, nullptr, part, kt);
+  finish_scalar_kernel<<<1, NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
+  return check_launch("mle_softmax_xent_keys_fwd");
+}
+
+int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const float* stats, const int32_t* keys, int clen,
+                              int max_clen, const float* upstream, float* dlogits, int rows, int cols, int batch) {
+  MLE_CHECK_ARG(logits && stats && keys && dlogits && batch > 0 && rows > 0 && cols > 0 && clen > 0 &&
+                    max_clen >= clen && rows % clen == 0,
+                "mle_softmax_xent_keys_bwd: bad argument");
+  hipStream_t s = as_stream(stream);
+  const KeyTargets kt{keys, clen, max_clen, nullptr};
+  const unsigned gy = (unsigned)std::min(rows, 65535);
+  if (cols % 4 == 0 && aligned16(logits) && aligned16(dlogits))
+    xent_keys_bwd4_kernel<<<dim3((cols / 4 + NT - 1) / NT, gy), NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows,
+                                                                           cols, (float)batch);
+  else
+    xent_keys_bwd_kernel<<<dim3((cols + NT - 1) / NT, gy), NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows,
+                                                                       cols, (float)batch);
+  return check_launch("mle_softmax_xent_keys_bwd");
 }
 
 }  // extern "C"

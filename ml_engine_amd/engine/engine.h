@@ -39,6 +39,13 @@ static constexpr int THREADSPERBLOCK = 512;
 
 struct NodeBackProp;
 struct AdamParameter;
+
+// Set on the output of GraphOperations::OneHot: the token ids the one-hot
+// matrix is built from, so a consumer can read them instead of the matrix.
+struct OneHotSource {
+  const int32_t* keys;  // device, [batch][max_clen]
+  int batch, clen, max_clen, vocab;
+};
 using graph = std::shared_ptr<NodeBackProp>;
 using graph_tree = std::vector<graph>;
 using graphFn = std::function<graph(graph)>;
@@ -139,6 +146,8 @@ struct NodeBackProp {
   // marked gradients first).
   bool grad_pending_zero = false;
   bool lazy_grad_writer = false;
+  // Non-null when this node's output is a one-hot matrix of `keys` (additive).
+  std::shared_ptr<OneHotSource> onehot;
   virtual void update(const float lr = LEARNING_RATE, const bool W = ADAMW) {}
   NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation);
   virtual ~NodeBackProp() = default;

@@ -383,7 +383,10 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
 
 // SoftMaxCrossEntropy (Engine/engine.cu:2064-2124).  The softmax buffer holds
 // the whole prediction (the reference allocates node->total == 1 float for it,
-// Engine/engine.cu:2080, and writes past it).  Backward assigns.
+// Engine/engine.cu:2080, and writes past it).  Backward assigns.  When the
+// target is a OneHot node, the loss and gradient read its ids instead of the
+// dense matrix and the backward recomputes the probabilities from per-row
+// (max, sum): the same values with a third of the memory traffic.
 graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph& target, const bool last) {
   for (int i = 0; i < 4; ++i)
     if (prediction->dim[i] != target->dim[i]) {
@@ -398,26 +401,40 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
   node->inputs = {prediction, target};
   GB += (double)(target->total + 1) * sizeof(float) / (1ULL << 30);
   const size_t n = prediction->total;
-  float* probs = mle::alloc_output(n);
   const int rows = batch * channels * c;
+  const std::shared_ptr<OneHotSource> oh = target->onehot;
+  const bool by_keys = oh && channels == 1 && oh->batch == batch && oh->clen == c && oh->vocab == d;
+  float* probs = by_keys ? nullptr : mle::alloc_output(n);
+  float* stats = by_keys ? mle::alloc_output(2 * (size_t)rows) : nullptr;
   const size_t ws_bytes = mle_loss_ws_bytes(n);
   void* ws = mle::alloc_scratch(ws_bytes);
   NodeBackProp *nd = node.get(), *pr = prediction.get(), *tg = target.get();
   node->forward = [=]() {
     if (calculate_loss || !last) {
-      check(mle_softmax_xent_fwd(S(), pr->output, tg->output, probs, rows, d, nd->output, ws, ws_bytes),
-            "SoftMaxCrossEntropy");
+      if (by_keys)
+        check(mle_softmax_xent_keys_fwd(S(), pr->output, oh->keys, oh->clen, oh->max_clen, stats, rows, d, nd->output,
+                                        ws, ws_bytes),
+              "SoftMaxCrossEntropy");
+      else
+        check(mle_softmax_xent_fwd(S(), pr->output, tg->output, probs, rows, d, nd->output, ws, ws_bytes),
+              "SoftMaxCrossEntropy");
       if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "CE loss");
     }
   };
   node->backward = [=]() {
     mle::accumulate_flag(pr);  // the reference assigns the whole gradient
-    check(mle_softmax_xent_bwd(S(), probs, tg->output, last ? nullptr : nd->grad, pr->grad, n, batch),
-          "derivative of CE in CE backward");
+    const float* up = last ? nullptr : nd->grad;
+    if (by_keys)
+      check(mle_softmax_xent_keys_bwd(S(), pr->output, stats, oh->keys, oh->clen, oh->max_clen, up, pr->grad, rows, d,
+                                      batch),
+            "derivative of CE in CE backward");
+    else
+      check(mle_softmax_xent_bwd(S(), probs, tg->output, up, pr->grad, n, batch), "derivative of CE in CE backward");
   };
   node->free = [=]() {
     nd->clear();
-    mle::release(probs, n, false);
+    if (probs) mle::release(probs, n, false);
+    if (stats) mle::release(stats, 2 * (size_t)rows, false);
   };
   node->zero_grad = [=]() { mle::zero(nd->output, 1); };
   return node;
@@ -529,6 +546,7 @@ graph GraphOperations::OneHot(const int32_t* keys, int batch, int clen, int max_
   node->forward = [=]() {
     check(mle_onehot_update(S(), nd->output, prev, keys, batch, clen, max_clen, vocab), "OneHotEmbeddings");
   };
+  node->onehot = std::make_shared<OneHotSource>(OneHotSource{keys, batch, clen, max_clen, vocab});
   std_hooks(node);
   return node;
 }

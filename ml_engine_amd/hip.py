@@ -63,6 +63,8 @@ SIGNATURES: dict[str, tuple] = {
     "mle_loss_ws_bytes": (SZ, [SZ]),
     "mle_mse_fwd": (I, [P, P, P, SZ, P, P, SZ]),
     "mle_mse_bwd": (I, [P, P, P, P, P, SZ, I]),
+    "mle_softmax_xent_keys_fwd": (I, [P, P, P, I, I, P, I, I, P, P, SZ]),
+    "mle_softmax_xent_keys_bwd": (I, [P, P, P, P, I, I, P, P, I, I, I]),
     "mle_softmax_xent_fwd": (I, [P, P, P, P, I, I, P, P, SZ]),
     "mle_softmax_xent_bwd": (I, [P, P, P, P, P, SZ, I]),
     "mle_norm_ws_bytes": (SZ, [I, I, SZ, I]),

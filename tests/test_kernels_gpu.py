@@ -488,3 +488,45 @@ def test_elementwise_and_layout(hip, orc):
     gf = hip.Buffer.zeros(1001)
     hip.call("mle_fill", None, gf.ptr, 3.5, 1001)
     np.testing.assert_array_equal(gf.numpy(), np.full(1001, 3.5, np.float32))
+
+
+# ----------------------------------------- cross-entropy from token-id targets
+@pytest.mark.parametrize("batch,clen,max_clen,cols", [(4, 24, 24, 1000), (3, 10, 13, 10), (2, 7, 9, 9001),
+                                                      (2, 16, 16, 8000)])
+def test_softmax_xent_keys_matches_dense(hip, orc, batch, clen, max_clen, cols):
+    """The id path equals the dense one-hot path bit for bit (loss and
+    gradient), ids outside [0, cols) included, and matches the oracle."""
+    r = rng(batch * 17 + clen + cols)
+    rows = batch * clen
+    logits = (r.standard_normal((rows, cols), dtype=np.float32) * 3).astype(np.float32)
+    keys = r.integers(0, cols, (batch, max_clen)).astype(np.int32)
+    keys[0, 1] = -1
+    keys[-1, 0] = cols + 3
+    keys[-1, -1] = np.iinfo(np.int32).min
+    tgt = np.zeros((rows, cols), np.float32)
+    for b in range(batch):
+        for s in range(clen):
+            k = keys[b, s]
+            if 0 <= k < cols:
+                tgt[b * clen + s, k] = 1.0
+    L = hip.lib()
+    n = rows * cols
+    gl, gt, gk = B(hip, logits), B(hip, tgt), B(hip, keys)
+    gp, gloss, gloss2 = hip.Buffer.zeros((rows, cols)), hip.Buffer.zeros(1), hip.Buffer.zeros(1)
+    gst = hip.Buffer.zeros(2 * rows)
+    ws = hip.Buffer(L.mle_loss_ws_bytes(n))
+    hip.call("mle_softmax_xent_fwd", None, gl.ptr, gt.ptr, gp.ptr, rows, cols, gloss.ptr, ws.ptr, ws.nbytes)
+    hip.call("mle_softmax_xent_keys_fwd", None, gl.ptr, gk.ptr, clen, max_clen, gst.ptr, rows, cols, gloss2.ptr,
+             ws.ptr, ws.nbytes)
+    np.testing.assert_array_equal(gloss2.numpy(), gloss.numpy())
+    up = B(hip, np.array([0.75], np.float32))
+    for upstream in (None, up.ptr):
+        gd, gd2 = hip.Buffer.zeros((rows, cols)), hip.Buffer.zeros((rows, cols))
+        hip.call("mle_softmax_xent_bwd", None, gp.ptr, gt.ptr, upstream, gd.ptr, n, batch)
+        hip.call("mle_fill", None, gd2.ptr, float("nan"), n)
+        hip.call("mle_softmax_xent_keys_bwd", None, gl.ptr, gst.ptr, gk.ptr, clen, max_clen, upstream, gd2.ptr, rows,
+                 cols, batch)
+        np.testing.assert_array_equal(gd2.numpy(), gd.numpy())
+    pr = np.zeros_like(logits)
+    lref = orc.call("orc_softmax_xent_fwd", orc.ptr(logits), orc.ptr(tgt), orc.ptr(pr), rows, cols)
+    assert_close(gloss2.numpy(), np.array([lref], np.float32), what="keys loss", **EW)
