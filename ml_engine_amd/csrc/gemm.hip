@@ -66,78 +66,73 @@ struct BufOperand {
   }
 };
 
-// Global -> registers for one stage.  Tiles are 4096 floats = 1024 float4,
-// four per thread.  A_MC == trans_a (A stored K x M); B_KC == trans_b.
-// `kend` bounds K for this workgroup's split.
-template <bool A_MC, bool VEC>
-__device__ __forceinline__ void load_a(const GemmArgs& g, const float* A, int m0, int k0, int kend, int tid,
-                                       f32x4 (&r)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = tid + NT * i;
-    if (!A_MC) r[i] = ld_guard<VEC>(A, g.lda, m0 + (f >> 3), k0 + (f & 7) * 4, g.M, kend);
-    else r[i] = ld_guard<VEC>(A, g.lda, k0 + (f >> 5), m0 + (f & 31) * 4, kend, g.M);
-  }
-}
-template <bool B_KC, bool VEC>
-__device__ __forceinline__ void load_b(const GemmArgs& g, const float* B, int n0, int k0, int kend, int tid,
-                                       f32x4 (&r)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = tid + NT * i;
-    if (B_KC) r[i] = ld_guard<VEC>(B, g.ldb, n0 + (f >> 3), k0 + (f & 7) * 4, g.N, kend);
-    else r[i] = ld_guard<VEC>(B, g.ldb, k0 + (f >> 5), n0 + (f & 31) * 4, kend, g.N);
-  }
-}
-template <bool A_MC>
-__device__ __forceinline__ void load_a_buf(const GemmArgs& g, const BufOperand& A, int m0, int k0, int kend, int tid,
-                                           f32x4 (&r)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = tid + NT * i;
-    if (!A_MC) r[i] = A.load(m0 + (f >> 3), k0 + (f & 7) * 4, g.M, kend);
-    else r[i] = A.load(k0 + (f >> 5), m0 + (f & 31) * 4, kend, g.M);
-  }
-}
-template <bool B_KC>
-__device__ __forceinline__ void load_b_buf(const GemmArgs& g, const BufOperand& B, int n0, int k0, int kend, int tid,
-                                           f32x4 (&r)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = tid + NT * i;
-    if (B_KC) r[i] = B.load(n0 + (f >> 3), k0 + (f & 7) * 4, g.N, kend);
-    else r[i] = B.load(k0 + (f >> 5), n0 + (f & 31) * 4, kend, g.N);
+// Global -> registers for one stage.  A tile is TM x BK (TM/32 float4 per
+// thread), a B tile BK x TN.  A_MC == trans_a (A stored K x M); B_KC ==
+// trans_b.  `kend` bounds K for this workgroup's split.  k-contiguous tiles
+// give each row 8 float4 (BK = 32); m/n-contiguous ones TM/4 per k row.
+template <bool MC, int T>
+__device__ __forceinline__ void tile_coord(int f, int& r, int& c) {
+  if (!MC) {  // [T][BK]: r = row along M/N, c = k
+    r = f >> 3;
+    c = (f & 7) * 4;
+  } else {  // [BK][T]: r = k, c = along M/N
+    r = f / (T / 4);
+    c = (f % (T / 4)) * 4;
   }
 }
 
-// Row stride of the epilogue staging tile (32 x 64 per wave, 16-byte aligned rows).
-constexpr int EPI_LD = 68;
-
-// Registers -> LDS (same element mapping as the loads).
-template <bool KC>
-__device__ __forceinline__ void store_tile(float* S, int tid, const f32x4 (&r)[4]) {
+template <bool A_MC, int VEC, int TM>
+__device__ __forceinline__ void load_a(const GemmArgs& g, const float* A, const BufOperand& Ab, int m0, int k0,
+                                       int kend, int tid, f32x4 (&r)[TM / 32]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = tid + NT * i;
-    if (KC) *reinterpret_cast<f32x4*>(S + (f >> 3) * LDK + (f & 7) * 4) = r[i];
-    else *reinterpret_cast<f32x4*>(S + (f >> 5) * LDMN + (f & 31) * 4) = r[i];
+  for (int i = 0; i < TM / 32; ++i) {
+    int a, b;
+    tile_coord<A_MC, TM>(tid + NT * i, a, b);
+    if (!A_MC) r[i] = VEC == 2 ? Ab.load(m0 + a, k0 + b, g.M, kend) : ld_guard<VEC == 1>(A, g.lda, m0 + a, k0 + b, g.M, kend);
+    else r[i] = VEC == 2 ? Ab.load(k0 + a, m0 + b, kend, g.M) : ld_guard<VEC == 1>(A, g.lda, k0 + a, m0 + b, kend, g.M);
+  }
+}
+template <bool B_KC, int VEC, int TN>
+__device__ __forceinline__ void load_b(const GemmArgs& g, const float* B, const BufOperand& Bb, int n0, int k0,
+                                       int kend, int tid, f32x4 (&r)[TN / 32]) {
+#pragma unroll
+  for (int i = 0; i < TN / 32; ++i) {
+    int a, b;
+    tile_coord<!B_KC, TN>(tid + NT * i, a, b);
+    if (B_KC) r[i] = VEC == 2 ? Bb.load(n0 + a, k0 + b, g.N, kend) : ld_guard<VEC == 1>(B, g.ldb, n0 + a, k0 + b, g.N, kend);
+    else r[i] = VEC == 2 ? Bb.load(k0 + a, n0 + b, kend, g.N) : ld_guard<VEC == 1>(B, g.ldb, k0 + a, n0 + b, kend, g.N);
+  }
+}
+
+// Registers -> LDS (same element mapping as the loads).  KC: k-contiguous.
+template <bool KC, int T>
+__device__ __forceinline__ void store_tile(float* S, int tid, const f32x4 (&r)[T / 32]) {
+#pragma unroll
+  for (int i = 0; i < T / 32; ++i) {
+    int a, b;
+    tile_coord<!KC, T>(tid + NT * i, a, b);
+    *reinterpret_cast<f32x4*>(S + a * (KC ? LDK : T + PAD) + b) = r[i];
   }
 }
 
 // VEC: 0 = guarded scalar loads, 1 = guarded float4 loads, 2 = buffer loads.
-template <int TA, int TB, int VEC, bool COLSUM>
+// WM x WN MFMA blocks per wave: the workgroup tile is (32 WM) x (32 WN).
+template <int TA, int TB, int VEC, bool COLSUM, int WM, int WN>
 __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
-  constexpr int ASZ = a_tile_floats<A_MC>();
-  constexpr int BSZ = b_tile_floats<B_KC>();
+  constexpr int TM = 32 * WM, TN = 32 * WN;
+  constexpr int ASZ = a_tile_floats<A_MC, TM>();
+  constexpr int BSZ = b_tile_floats<B_KC, TN>();
+  constexpr int EPI_LD = 16 * WN + 4;  // epilogue staging row stride (16-byte aligned rows)
+  static_assert(4 * 32 * EPI_LD <= 2 * (ASZ + BSZ), "epilogue staging does not fit");
   __shared__ __attribute__((aligned(16))) float smem[2 * (ASZ + BSZ)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, q = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
   const int64_t z = blockIdx.z / g.splits;
   const int split = blockIdx.z % g.splits;
   const float* A = g.A + z * g.sa;
@@ -148,30 +143,23 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
   const uint32_t b_bytes = (uint32_t)(((int64_t)((B_KC ? g.N : g.K) - 1) * g.ldb + (B_KC ? g.K : g.N)) * 4);
   const BufOperand Ab(A, g.lda, a_bytes), Bb(B, g.ldb, b_bytes);
-  auto load_stage = [&](int k0, f32x4(&ra_)[4], f32x4(&rb_)[4]) {
-    if (VEC == 2) {
-      load_a_buf<A_MC>(g, Ab, m0, k0, kend, tid, ra_);
-      load_b_buf<B_KC>(g, Bb, n0, k0, kend, tid, rb_);
-    } else {
-      load_a<A_MC, VEC == 1>(g, A, m0, k0, kend, tid, ra_);
-      load_b<B_KC, VEC == 1>(g, B, n0, k0, kend, tid, rb_);
-    }
-  };
 
-  f32x4 acc[4][4];
+  f32x4 acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int n = 0; n < WN; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const bool do_cs = COLSUM && blockIdx.y == 0;
+  constexpr int CS_T = NT / TN;  // threads per column of the column sum
   float csum = 0.f;
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-  f32x4 ra[4], rb[4];
+  f32x4 ra[TM / 32], rb[TN / 32];
   if (nk > 0) {
-    load_stage(kbeg, ra, rb);
-    store_tile<!A_MC>(smem, tid, ra);
-    store_tile<B_KC>(smem + 2 * ASZ, tid, rb);
+    load_a<A_MC, VEC, TM>(g, A, Ab, m0, kbeg, kend, tid, ra);
+    load_b<B_KC, VEC, TN>(g, B, Bb, n0, kbeg, kend, tid, rb);
+    store_tile<!A_MC, TM>(smem, tid, ra);
+    store_tile<B_KC, TN>(smem + 2 * ASZ, tid, rb);
   }
   __syncthreads();
 
@@ -180,16 +168,22 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
     const float* As = smem + cur * ASZ;
     const float* Bs = smem + 2 * ASZ + cur * BSZ;
     const bool more = kt + 1 < nk;
-    if (more) load_stage(kbeg + (kt + 1) * BK, ra, rb);
-    mma_stage<A_MC, B_KC>(As, Bs, acc, wm, wn, lr, q);
+    if (more) {
+      load_a<A_MC, VEC, TM>(g, A, Ab, m0, kbeg + (kt + 1) * BK, kend, tid, ra);
+      load_b<B_KC, VEC, TN>(g, B, Bb, n0, kbeg + (kt + 1) * BK, kend, tid, rb);
+    }
+    mma_stage<A_MC, B_KC, WM, WN>(As, Bs, acc, wm, wn, lr, q);
     if (do_cs) {
-      const int c = tid & 127, h = tid >> 7;
+      const int c = tid % TN, h = tid / TN;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) csum += B_KC ? Bs[c * LDK + h * 16 + k] : Bs[(h * 16 + k) * LDMN + c];
+      for (int k = 0; k < BK / CS_T; ++k) {
+        const int kk = h * (BK / CS_T) + k;
+        csum += B_KC ? Bs[c * LDK + kk] : Bs[kk * (TN + PAD) + c];
+      }
     }
     if (more) {
-      store_tile<!A_MC>(smem + (cur ^ 1) * ASZ, tid, ra);
-      store_tile<B_KC>(smem + 2 * ASZ + (cur ^ 1) * BSZ, tid, rb);
+      store_tile<!A_MC, TM>(smem + (cur ^ 1) * ASZ, tid, ra);
+      store_tile<B_KC, TN>(smem + 2 * ASZ + (cur ^ 1) * BSZ, tid, rb);
     }
     __syncthreads();
   }
@@ -198,27 +192,28 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   const bool split_mode = g.splits > 1;
   float* P = split_mode ? g.part + (int64_t)blockIdx.z * g.M * g.N : nullptr;
   if (VEC == 2 && (g.N & 3) == 0 && (g.ldc & 3) == 0 && ((reinterpret_cast<uintptr_t>(C) & 15) == 0)) {
-    // Stage each wave's 64 x 64 block through LDS, 32 rows at a time, and
-    // write rows back with 16-byte stores (a wave covers 4 full 256-byte row
-    // segments per instruction instead of 16 x 64-byte pieces).
+    // Stage each wave's (16 WM) x (16 WN) block through LDS, 32 rows at a
+    // time, and write rows back with 16-byte stores.
+    constexpr int F4_ROW = 4 * WN;          // float4 per staged row
+    constexpr int ROWS_PASS = 64 / F4_ROW;  // rows a wave writes per pass
     float* T = smem + wave * (32 * EPI_LD);
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
+    for (int half = 0; half < WM / 2; ++half) {
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) {
         const int i = half * 2 + ii;
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < WN; ++n)
 #pragma unroll
           for (int r = 0; r < 4; ++r) T[(ii * 16 + 4 * q + r) * EPI_LD + n * 16 + lr] = acc[i][n][r];
       }
       __syncthreads();
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int rr = it * 4 + (lane >> 4);  // 0..31
-        const int cc = (lane & 15) * 4;       // 0..60
-        const int row = m0 + wm * 64 + half * 32 + rr;
-        const int col = n0 + wn * 64 + cc;
+      for (int it = 0; it < 32 / ROWS_PASS; ++it) {
+        const int rr = it * ROWS_PASS + lane / F4_ROW;
+        const int cc = (lane % F4_ROW) * 4;
+        const int row = m0 + wm * 16 * WM + half * 32 + rr;
+        const int col = n0 + wn * 16 * WN + cc;
         if (row < g.M && col < g.N) {
           f32x4 v = *reinterpret_cast<const f32x4*>(T + rr * EPI_LD + cc);
           if (split_mode) {
@@ -236,35 +231,37 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
     }
   } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int col = n0 + acc_col(wn, n, lr);
-      if (col >= g.N) continue;
+      for (int n = 0; n < WN; ++n) {
+        const int col = n0 + acc_col<WN>(wn, n, lr);
+        if (col >= g.N) continue;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + acc_row(wm, i, q, r);
-        if (row < g.M) {
-          if (split_mode) {
-            P[(int64_t)row * g.N + col] = acc[i][n][r];
-          } else {
-            float* p = C + (int64_t)row * g.ldc + col;
-            float v = alpha * acc[i][n][r];
-            if (beta != 0.f) v += beta * *p;
-            if (g.bias) v += g.bias[col];
-            *p = v;
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + acc_row<WM>(wm, i, q, r);
+          if (row < g.M) {
+            if (split_mode) {
+              P[(int64_t)row * g.N + col] = acc[i][n][r];
+            } else {
+              float* p = C + (int64_t)row * g.ldc + col;
+              float v = alpha * acc[i][n][r];
+              if (beta != 0.f) v += beta * *p;
+              if (g.bias) v += g.bias[col];
+              *p = v;
+            }
           }
         }
       }
-    }
   }
 
   if (do_cs) {
     // smem is free after the final barrier of the K loop.
     smem[tid] = csum;
     __syncthreads();
-    if (tid < 128 && n0 + tid < g.N) {
-      const float cs = smem[tid] + smem[tid + 128];
+    if (tid < TN && n0 + tid < g.N) {
+      float cs = 0.f;
+#pragma unroll
+      for (int h = 0; h < CS_T; ++h) cs += smem[tid + h * TN];
       if (split_mode) g.part_cs[(int64_t)split * g.N + n0 + tid] = cs;
       else g.colsum[n0 + tid] += cs;
     }
@@ -324,11 +321,33 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
   }
 }
 
+// Workgroup tile: 128 x 128 unless a side is <= 64 (the 64-wide variants waste
+// nothing there) or the 128 x 128 grid would leave CUs idle and K is too short
+// for split-K to fill them (half-width tiles double the workgroups; measured
+// on MI355X, for K >= 4096 full tiles plus split-K are faster).  A function of
+// the shape only, as mle_gemm_ws_bytes needs.
+struct Tile {
+  int wm, wn;  // MFMA blocks per wave along M / N
+  int tm() const { return 32 * wm; }
+  int tn() const { return 32 * wn; }
+};
+
+Tile choose_tile(int M, int N, int K, int batch) {
+  (void)K;
+  if (M <= 64 && N <= 64) return {2, 2};
+  if (N <= 64) return {4, 2};
+  if (M <= 64) return {2, 4};
+  const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * batch;
+  if (t128 >= 512 || K >= 4096) return {4, 4};
+  return N >= M ? Tile{2, 4} : Tile{4, 2};
+}
+
 // Split count: a function of the shape only.  Splits are used when the tile
 // grid leaves most of the 256 CUs idle and K is long enough to share.
 int choose_splits(int M, int N, int K, int batch, int& kchunk) {
   kchunk = K;
-  const long long tiles = (long long)((M + BM - 1) / BM) * ((N + BN - 1) / BN) * batch;
+  const Tile t = choose_tile(M, N, K, batch);
+  const long long tiles = (long long)((M + t.tm() - 1) / t.tm()) * ((N + t.tn() - 1) / t.tn()) * batch;
   // Measured on MI355X: with ~256 tiles a split only pays off for long K.
   if (tiles >= 384 || (tiles >= 128 && K < 4096)) return 1;
   int s = (int)((768 + tiles - 1) / tiles);
@@ -342,18 +361,26 @@ int choose_splits(int M, int N, int K, int batch, int& kchunk) {
   return s;
 }
 
-template <int TA, int TB>
+template <int TA, int TB, int WM, int WN>
 void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, int vec, bool cs) {
   if (vec == 2) {
-    if (cs) gemm_kernel<TA, TB, 2, true><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 2, false><<<grid, NT, 0, s>>>(g);
+    if (cs) gemm_kernel<TA, TB, 2, true, WM, WN><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 2, false, WM, WN><<<grid, NT, 0, s>>>(g);
   } else if (vec == 1) {
-    if (cs) gemm_kernel<TA, TB, 1, true><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 1, false><<<grid, NT, 0, s>>>(g);
+    if (cs) gemm_kernel<TA, TB, 1, true, WM, WN><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 1, false, WM, WN><<<grid, NT, 0, s>>>(g);
   } else {
-    if (cs) gemm_kernel<TA, TB, 0, true><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 0, false><<<grid, NT, 0, s>>>(g);
+    if (cs) gemm_kernel<TA, TB, 0, true, WM, WN><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 0, false, WM, WN><<<grid, NT, 0, s>>>(g);
   }
+}
+
+template <int TA, int TB>
+void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, bool cs) {
+  if (t.wm == 4 && t.wn == 4) launch_t<TA, TB, 4, 4>(s, g, grid, vec, cs);
+  else if (t.wm == 4) launch_t<TA, TB, 4, 2>(s, g, grid, vec, cs);
+  else if (t.wn == 4) launch_t<TA, TB, 2, 4>(s, g, grid, vec, cs);
+  else launch_t<TA, TB, 2, 2>(s, g, grid, vec, cs);
 }
 
 // Bytes spanned by one batch item of an operand stored rows x cols with leading dimension ld.
@@ -371,7 +398,9 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   MLE_CHECK_ARG(ldc >= N, "mle_gemm: ldc %lld < N %d", (long long)ldc, N);
   MLE_CHECK_ARG(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "mle_gemm: leading dimension too small");
   MLE_CHECK_ARG(colsum == nullptr || batch == 1, "mle_gemm: fused colsum needs batch == 1");
-  MLE_CHECK_ARG((M + BM - 1) / BM <= 65535 && batch <= 65535, "mle_gemm: grid too large (M %d, batch %d)", M, batch);
+  const Tile tile = choose_tile(M, N, K, batch);
+  MLE_CHECK_ARG((M + tile.tm() - 1) / tile.tm() <= 65535 && batch <= 65535, "mle_gemm: grid too large (M %d, batch %d)",
+                M, batch);
   GemmArgs g{A, B, C, colsum, lda, ldb, ldc, stride_a, stride_b, stride_c, M, N, K, alpha, beta, 1, K, nullptr, nullptr,
              bias};
   int kchunk = K;
@@ -396,7 +425,7 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
                    extent_bytes(b_rows, b_cols, ldb) < 2147483648.0 - 64;
   const int vec = buf ? 2 : (v4 ? 1 : 0);
   const bool cs = colsum != nullptr;
-  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, batch * g.splits);
+  dim3 grid((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
   hipStream_t s = as_stream(stream);
   static const char* names[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
   const int which = (trans_a ? 2 : 0) + (trans_b ? 1 : 0);
@@ -405,10 +434,10 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   {
     ProbeScope probe(names[which], s, flop, bytes);
     switch (which) {
-      case 0: launch_t<0, 0>(s, g, grid, vec, cs); break;
-      case 1: launch_t<0, 1>(s, g, grid, vec, cs); break;
-      case 2: launch_t<1, 0>(s, g, grid, vec, cs); break;
-      default: launch_t<1, 1>(s, g, grid, vec, cs); break;
+      case 0: launch_tile<0, 0>(s, g, tile, grid, vec, cs); break;
+      case 1: launch_tile<0, 1>(s, g, tile, grid, vec, cs); break;
+      case 2: launch_tile<1, 0>(s, g, tile, grid, vec, cs); break;
+      default: launch_tile<1, 1>(s, g, tile, grid, vec, cs); break;
     }
     if (g.splits > 1) {
       const bool rv = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(C) && aligned16(g.part) &&

@@ -22,50 +22,55 @@
 
 namespace gemm {
 
-constexpr int BM = 128, BN = 128, BK = 32, NT = 256, PAD = 4;
+constexpr int BK = 32, NT = 256, PAD = 4;
 constexpr int LDK = BK + PAD;   // row stride of k-contiguous tiles
-constexpr int LDMN = BM + PAD;  // row stride of m/n-contiguous tiles (BM == BN)
+// Default workgroup tile (and the one the convolution kernels use).
+constexpr int BM = 128, BN = 128;
+constexpr int LDMN = BM + PAD;  // row stride of m/n-contiguous 128-wide tiles
 
-// A_MC: A tile is m-contiguous; B_KC: B tile is k-contiguous.
-template <bool A_MC>
+// A_MC: A tile is m-contiguous; B_KC: B tile is k-contiguous.  TM / TN: tile
+// extent along M / N (128 or 64).
+template <bool A_MC, int TM = BM>
 constexpr int a_tile_floats() {
-  return A_MC ? BK * LDMN : BM * LDK;
+  return A_MC ? BK * (TM + PAD) : TM * LDK;
 }
-template <bool B_KC>
+template <bool B_KC, int TN = BN>
 constexpr int b_tile_floats() {
-  return B_KC ? BN * LDK : BK * LDMN;
+  return B_KC ? TN * LDK : BK * (TN + PAD);
 }
 
-// One BK-deep slice of MFMAs for this wave's 64 x 64 block.  All fragment
-// reads of the slice are issued first and a scheduling barrier keeps the
-// compiler from sinking them between the MFMAs: otherwise m/n-contiguous tiles
-// (four ds_read_b32 per fragment) end up with an LDS wait before every few
-// MFMAs.  The hardware waits only for the reads of the current 16-deep step.
-template <bool A_MC, bool B_KC>
+// One BK-deep slice of MFMAs for this wave's (16*WM) x (16*WN) block; the
+// workgroup's four waves sit 2 x 2, so the tile is (32*WM) x (32*WN).  All
+// fragment reads of the slice are issued first and a scheduling barrier keeps
+// the compiler from sinking them between the MFMAs: otherwise m/n-contiguous
+// tiles (four ds_read_b32 per fragment) end up with an LDS wait before every
+// few MFMAs.  The hardware waits only for the reads of the current 16-deep step.
+template <bool A_MC, bool B_KC, int WM = 4, int WN = 4>
 __device__ __forceinline__ void mma_stage(const float* __restrict__ As, const float* __restrict__ Bs,
-                                          f32x4 (&acc)[4][4], int wm, int wn, int lr, int q) {
+                                          f32x4 (&acc)[WM][WN], int wm, int wn, int lr, int q) {
   constexpr int KB = BK / 16;
-  f32x4 a[KB][4], b[KB][4];
+  constexpr int LDA = 32 * WM + PAD, LDB = 32 * WN + PAD;
+  f32x4 a[KB][WM], b[KB][WN];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wm * 64 + i * 16 + lr;
+    for (int i = 0; i < WM; ++i) {
+      const int row = wm * 16 * WM + i * 16 + lr;
       if (!A_MC) {
         a[kb][i] = *reinterpret_cast<const f32x4*>(As + row * LDK + kb * 16 + 4 * q);
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[kb][i][j] = As[(kb * 16 + 4 * q + j) * LDMN + row];
+        for (int j = 0; j < 4; ++j) a[kb][i][j] = As[(kb * 16 + 4 * q + j) * LDA + row];
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int col = wn * 64 + i * 16 + lr;
+    for (int i = 0; i < WN; ++i) {
+      const int col = wn * 16 * WN + i * 16 + lr;
       if (B_KC) {
         b[kb][i] = *reinterpret_cast<const f32x4*>(Bs + col * LDK + kb * 16 + 4 * q);
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[kb][i][j] = Bs[(kb * 16 + 4 * q + j) * LDMN + col];
+        for (int j = 0; j < 4; ++j) b[kb][i][j] = Bs[(kb * 16 + 4 * q + j) * LDB + col];
       }
     }
   }
@@ -75,14 +80,20 @@ __device__ __forceinline__ void mma_stage(const float* __restrict__ As, const fl
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < WN; ++n)
           acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[kb][i][j], b[kb][n][j], acc[i][n], 0, 0, 0);
 }
 
 // Row/column of accumulator element (i, n, r) of this lane inside the tile.
-__device__ __forceinline__ int acc_row(int wm, int i, int q, int r) { return wm * 64 + i * 16 + 4 * q + r; }
-__device__ __forceinline__ int acc_col(int wn, int n, int lr) { return wn * 64 + n * 16 + lr; }
+template <int WM = 4>
+__device__ __forceinline__ int acc_row(int wm, int i, int q, int r) {
+  return wm * 16 * WM + i * 16 + 4 * q + r;
+}
+template <int WN = 4>
+__device__ __forceinline__ int acc_col(int wn, int n, int lr) {
+  return wn * 16 * WN + n * 16 + lr;
+}
 
 }  // namespace gemm

@@ -33,6 +33,11 @@ GEMM_CASES = [
     (0, 1, 200, 136, 256, 3),
     (1, 0, 64, 96, 300, 2),
     (1, 1, 256, 256, 64, 2),
+    # grids large enough for the 128 x 128 tile, with ragged edges and batches
+    (0, 0, 2048, 4096, 40, 1),
+    (1, 0, 2050, 4100, 36, 1),
+    (0, 1, 1024, 1024, 20, 8),
+    (1, 1, 2064, 2056, 24, 2),
 ]
 
 
@@ -88,6 +93,23 @@ def test_gemm_split_k(hip, orc, ta, tb, M, N, K, batch, cs):
     if cs:
         bsum = Bm[0].astype(np.float64).sum(1 if tb else 0)
         assert_close(dcs.numpy(), cs0 + bsum, what="split-K colsum", **EW)
+
+
+@pytest.mark.parametrize("M,N,K", [(100, 40, 300), (40, 40, 500), (300, 90, 77), (2048, 4096, 40), (64, 130, 300)])
+def test_gemm_colsum_tiles(hip, orc, M, N, K):
+    """dW = X^T dY with the fused column sum, on every workgroup tile shape."""
+    r = rng(M * 3 + N + K)
+    X = r.standard_normal((K, M), dtype=np.float32)
+    dY = r.standard_normal((K, N), dtype=np.float32)
+    dWr = np.ones((M, N), np.float32)
+    dbr = np.full(N, 0.25, np.float32)
+    orc.call("orc_bcmm", 2, orc.ptr(X), orc.ptr(dY), orc.ptr(dWr), 1, 1, M, K, N, 1, 3, 3, 0, 1.0)
+    orc.call("orc_bcompress", orc.ptr(dY), orc.ptr(dbr), K, N, 1.0)
+    gX, gY = B(hip, X), B(hip, dY)
+    gW, gb = B(hip, np.ones((M, N), np.float32)), B(hip, np.full(N, 0.25, np.float32))
+    hip.call("mle_gemm", None, 1, 0, M, N, K, 1.0, gX.ptr, M, 0, gY.ptr, N, 0, 1.0, gW.ptr, N, 0, 1, gb.ptr)
+    assert_close(gW.numpy(), dWr, what="dW", **MM)
+    assert_close(gb.numpy(), dbr, what="db", **EW)
 
 
 def test_gemm_broadcast_and_colsum(hip, orc):
