@@ -66,73 +66,95 @@ struct BufOperand {
   }
 };
 
-// Global -> registers for one stage.  A tile is TM x BK (TM/32 float4 per
-// thread), a B tile BK x TN.  A_MC == trans_a (A stored K x M); B_KC ==
+// Global -> registers for one stage.  A tile is TM x KD (TM*KD/1024 float4
+// per thread), a B tile KD x TN.  A_MC == trans_a (A stored K x M); B_KC ==
 // trans_b.  `kend` bounds K for this workgroup's split.  k-contiguous tiles
-// give each row 8 float4 (BK = 32); m/n-contiguous ones TM/4 per k row.
-template <bool MC, int T>
+// give each row KD/4 float4; m/n-contiguous ones T/4 per k row.
+template <bool MC, int T, int KD>
 __device__ __forceinline__ void tile_coord(int f, int& r, int& c) {
-  if (!MC) {  // [T][BK]: r = row along M/N, c = k
-    r = f >> 3;
-    c = (f & 7) * 4;
-  } else {  // [BK][T]: r = k, c = along M/N
+  if (!MC) {  // [T][KD]: r = row along M/N, c = k
+    r = f / (KD / 4);
+    c = (f % (KD / 4)) * 4;
+  } else {  // [KD][T]: r = k, c = along M/N
     r = f / (T / 4);
     c = (f % (T / 4)) * 4;
   }
 }
 
-template <bool A_MC, int VEC, int TM>
+template <bool A_MC, int VEC, int TM, int KD>
 __device__ __forceinline__ void load_a(const GemmArgs& g, const float* A, const BufOperand& Ab, int m0, int k0,
-                                       int kend, int tid, f32x4 (&r)[TM / 32]) {
+                                       int kend, int tid, f32x4 (&r)[TM * KD / 1024]) {
 #pragma unroll
-  for (int i = 0; i < TM / 32; ++i) {
+  for (int i = 0; i < TM * KD / 1024; ++i) {
     int a, b;
-    tile_coord<A_MC, TM>(tid + NT * i, a, b);
+    tile_coord<A_MC, TM, KD>(tid + NT * i, a, b);
     if (!A_MC) r[i] = VEC == 2 ? Ab.load(m0 + a, k0 + b, g.M, kend) : ld_guard<VEC == 1>(A, g.lda, m0 + a, k0 + b, g.M, kend);
     else r[i] = VEC == 2 ? Ab.load(k0 + a, m0 + b, kend, g.M) : ld_guard<VEC == 1>(A, g.lda, k0 + a, m0 + b, kend, g.M);
   }
 }
-template <bool B_KC, int VEC, int TN>
+template <bool B_KC, int VEC, int TN, int KD>
 __device__ __forceinline__ void load_b(const GemmArgs& g, const float* B, const BufOperand& Bb, int n0, int k0,
-                                       int kend, int tid, f32x4 (&r)[TN / 32]) {
+                                       int kend, int tid, f32x4 (&r)[TN * KD / 1024]) {
 #pragma unroll
-  for (int i = 0; i < TN / 32; ++i) {
+  for (int i = 0; i < TN * KD / 1024; ++i) {
     int a, b;
-    tile_coord<!B_KC, TN>(tid + NT * i, a, b);
+    tile_coord<!B_KC, TN, KD>(tid + NT * i, a, b);
     if (B_KC) r[i] = VEC == 2 ? Bb.load(n0 + a, k0 + b, g.N, kend) : ld_guard<VEC == 1>(B, g.ldb, n0 + a, k0 + b, g.N, kend);
     else r[i] = VEC == 2 ? Bb.load(k0 + a, n0 + b, kend, g.N) : ld_guard<VEC == 1>(B, g.ldb, k0 + a, n0 + b, kend, g.N);
   }
 }
 
 // Registers -> LDS (same element mapping as the loads).  KC: k-contiguous.
-template <bool KC, int T>
-__device__ __forceinline__ void store_tile(float* S, int tid, const f32x4 (&r)[T / 32]) {
+template <bool KC, int T, int KD>
+__device__ __forceinline__ void store_tile(float* S, int tid, const f32x4 (&r)[T * KD / 1024]) {
 #pragma unroll
-  for (int i = 0; i < T / 32; ++i) {
+  for (int i = 0; i < T * KD / 1024; ++i) {
     int a, b;
-    tile_coord<!KC, T>(tid + NT * i, a, b);
-    *reinterpret_cast<f32x4*>(S + a * (KC ? LDK : T + PAD) + b) = r[i];
+    tile_coord<!KC, T, KD>(tid + NT * i, a, b);
+    *reinterpret_cast<f32x4*>(S + a * (KC ? KD + PAD : T + PAD) + b) = r[i];
   }
+}
+
+// Tile order.  Workgroups are handed to the 8 XCDs round-robin (linear id
+// L on XCD L % 8), and each XCD has its own L2.  XCD x therefore gets the
+// contiguous logical range [x*T/8, (x+1)*T/8) of the T tiles, walked in
+// groups of 8 tile-rows with the columns inside a group, so the workgroups
+// resident on one XCD share a few A row-panels and B column-panels.  A
+// bijection on [0, T): every tile is still computed by exactly one workgroup.
+constexpr int kXcds = 8, kGroupRows = 8;
+__device__ __forceinline__ void tile_of(int gx, int gy, int& tm, int& tn) {
+  const int T = gx * gy;
+  const int L = blockIdx.x + gx * blockIdx.y;
+  const int q = T / kXcds, r = T % kXcds, x = L % kXcds;
+  const int logical = x * q + min(x, r) + L / kXcds;
+  const int per_group = kGroupRows * gx;
+  const int first_m = (logical / per_group) * kGroupRows;
+  const int rows = min(gy - first_m, kGroupRows);
+  const int in_group = logical % per_group;
+  tm = first_m + in_group % rows;
+  tn = in_group / rows;
 }
 
 // VEC: 0 = guarded scalar loads, 1 = guarded float4 loads, 2 = buffer loads.
 // WM x WN MFMA blocks per wave: the workgroup tile is (32 WM) x (32 WN).
-template <int TA, int TB, int VEC, bool COLSUM, int WM, int WN>
-__global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
+template <int TA, int TB, int VEC, bool COLSUM, int WM, int WN, int KD>
+__global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) {
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
   constexpr int TM = 32 * WM, TN = 32 * WN;
-  constexpr int ASZ = a_tile_floats<A_MC, TM>();
-  constexpr int BSZ = b_tile_floats<B_KC, TN>();
+  constexpr int ASZ = a_tile_floats<A_MC, TM, KD>();
+  constexpr int BSZ = b_tile_floats<B_KC, TN, KD>();
   constexpr int EPI_LD = 16 * WN + 4;  // epilogue staging row stride (16-byte aligned rows)
-  static_assert(4 * 32 * EPI_LD <= 2 * (ASZ + BSZ), "epilogue staging does not fit");
-  __shared__ __attribute__((aligned(16))) float smem[2 * (ASZ + BSZ)];
+  constexpr int SMEM = 2 * (ASZ + BSZ) > 4 * 32 * EPI_LD ? 2 * (ASZ + BSZ) : 4 * 32 * EPI_LD;
+  __shared__ __attribute__((aligned(16))) float smem[SMEM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, q = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+  int tm, tn;
+  tile_of(gridDim.x, gridDim.y, tm, tn);
+  const int m0 = tm * TM, n0 = tn * TN;
   const int64_t z = blockIdx.z / g.splits;
   const int split = blockIdx.z % g.splits;
   const float* A = g.A + z * g.sa;
@@ -150,16 +172,16 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int n = 0; n < WN; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const bool do_cs = COLSUM && blockIdx.y == 0;
+  const bool do_cs = COLSUM && tm == 0;
   constexpr int CS_T = NT / TN;  // threads per column of the column sum
   float csum = 0.f;
-  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-  f32x4 ra[TM / 32], rb[TN / 32];
+  const int nk = kend > kbeg ? (kend - kbeg + KD - 1) / KD : 0;
+  f32x4 ra[TM * KD / 1024], rb[TN * KD / 1024];
   if (nk > 0) {
-    load_a<A_MC, VEC, TM>(g, A, Ab, m0, kbeg, kend, tid, ra);
-    load_b<B_KC, VEC, TN>(g, B, Bb, n0, kbeg, kend, tid, rb);
-    store_tile<!A_MC, TM>(smem, tid, ra);
-    store_tile<B_KC, TN>(smem + 2 * ASZ, tid, rb);
+    load_a<A_MC, VEC, TM, KD>(g, A, Ab, m0, kbeg, kend, tid, ra);
+    load_b<B_KC, VEC, TN, KD>(g, B, Bb, n0, kbeg, kend, tid, rb);
+    store_tile<!A_MC, TM, KD>(smem, tid, ra);
+    store_tile<B_KC, TN, KD>(smem + 2 * ASZ, tid, rb);
   }
   __syncthreads();
 
@@ -169,21 +191,21 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
     const float* Bs = smem + 2 * ASZ + cur * BSZ;
     const bool more = kt + 1 < nk;
     if (more) {
-      load_a<A_MC, VEC, TM>(g, A, Ab, m0, kbeg + (kt + 1) * BK, kend, tid, ra);
-      load_b<B_KC, VEC, TN>(g, B, Bb, n0, kbeg + (kt + 1) * BK, kend, tid, rb);
+      load_a<A_MC, VEC, TM, KD>(g, A, Ab, m0, kbeg + (kt + 1) * KD, kend, tid, ra);
+      load_b<B_KC, VEC, TN, KD>(g, B, Bb, n0, kbeg + (kt + 1) * KD, kend, tid, rb);
     }
-    mma_stage<A_MC, B_KC, WM, WN>(As, Bs, acc, wm, wn, lr, q);
+    mma_stage<A_MC, B_KC, WM, WN, KD>(As, Bs, acc, wm, wn, lr, q);
     if (do_cs) {
       const int c = tid % TN, h = tid / TN;
 #pragma unroll
-      for (int k = 0; k < BK / CS_T; ++k) {
-        const int kk = h * (BK / CS_T) + k;
-        csum += B_KC ? Bs[c * LDK + kk] : Bs[kk * (TN + PAD) + c];
+      for (int k = 0; k < KD / CS_T; ++k) {
+        const int kk = h * (KD / CS_T) + k;
+        csum += B_KC ? Bs[c * (KD + PAD) + kk] : Bs[kk * (TN + PAD) + c];
       }
     }
     if (more) {
-      store_tile<!A_MC, TM>(smem + (cur ^ 1) * ASZ, tid, ra);
-      store_tile<B_KC, TN>(smem + 2 * ASZ + (cur ^ 1) * BSZ, tid, rb);
+      store_tile<!A_MC, TM, KD>(smem + (cur ^ 1) * ASZ, tid, ra);
+      store_tile<B_KC, TN, KD>(smem + 2 * ASZ + (cur ^ 1) * BSZ, tid, rb);
     }
     __syncthreads();
   }
@@ -268,6 +290,191 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(GemmArgs g) {
   }
 }
 
+// Register-direct variant for 128 x 128 tiles: no LDS and no barrier in the
+// K loop.  Each lane loads its own MFMA fragments from global memory with
+// 16-byte reads, two K stages (16 deep) ahead of the MFMAs:
+//  * an operand stored k-contiguous gives lane (lr, q) the 4 k values
+//    4q..4q+3 of row 16 i + lr in one load (one load per 16-row block i);
+//  * an operand stored m- (or n-) contiguous is read along m instead: the
+//    wave's 64 rows are permuted so that block i, lane row lr is row
+//    4 lr + i, and one load of 4 consecutive rows at k = 4q + j holds that
+//    lane's values for all four blocks (one load per MFMA step j).
+// Either way a wave issues 4 loads per operand per stage; the two waves that
+// share a row (column) panel hit the same lines, which the L1 serves.  The
+// epilogue undoes the row/column permutation while staging C through LDS.
+template <int TA, int TB, bool COLSUM>
+__global__ __launch_bounds__(NT, 2) void gemm_direct_kernel(GemmArgs g) {
+  constexpr bool A_MC = TA != 0;
+  constexpr bool B_KC = TB != 0;
+  constexpr int KD = 16, TM = 128, TN = 128, EPI_LD = 68;
+  __shared__ __attribute__((aligned(16))) float smem[4 * 32 * EPI_LD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, q = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  int tm, tn;
+  tile_of(gridDim.x, gridDim.y, tm, tn);
+  const int m0 = tm * TM + wm * 64, n0 = tn * TN + wn * 64;  // this wave's 64 x 64 block
+  const int64_t z = blockIdx.z / g.splits;
+  const int split = blockIdx.z % g.splits;
+  const float* A = g.A + z * g.sa;
+  const float* B = g.B + z * g.sb;
+  float* C = g.C + z * g.sc;
+  const int kbeg = split * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
+  const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
+  const uint32_t b_bytes = (uint32_t)(((int64_t)((B_KC ? g.N : g.K) - 1) * g.ldb + (B_KC ? g.K : g.N)) * 4);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), (short)0, (int)a_bytes, kBufWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), (short)0, (int)b_bytes, kBufWord3);
+  const int nk = kend > kbeg ? (kend - kbeg + KD - 1) / KD : 0;
+
+  // Byte offsets at k = kbeg of the four loads per operand, and the
+  // per-stage advance.  K and the split's chunk are multiples of 16 (checked
+  // on the host), so every stage is full.  A row (column) outside the matrix
+  // starts at kBufOOB and stays past the buffer's extent for every stage
+  // (kt * step < 2^31), so the hardware range check returns zeros.  Stages
+  // fetched past the end of K are never consumed.
+  uint32_t a_off[4], b_off[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    if (!A_MC) {  // x = block i: row m0 + 16 x + lr, k = kbeg + 4 q
+      const int row = m0 + 16 * x + lr;
+      a_off[x] = row < g.M ? (uint32_t)(row * (int)g.lda + kbeg + 4 * q) * 4u : kBufOOB;
+    } else {  // x = step j: k = kbeg + 4 q + x, rows m0 + 4 lr .. + 3
+      a_off[x] = m0 + 4 * lr < g.M ? (uint32_t)((kbeg + 4 * q + x) * (int)g.lda + m0 + 4 * lr) * 4u : kBufOOB;
+    }
+    if (B_KC) {  // x = block n: column n0 + 16 x + lr, k = kbeg + 4 q
+      const int col = n0 + 16 * x + lr;
+      b_off[x] = col < g.N ? (uint32_t)(col * (int)g.ldb + kbeg + 4 * q) * 4u : kBufOOB;
+    } else {  // x = step j: k = kbeg + 4 q + x, columns n0 + 4 lr .. + 3
+      b_off[x] = n0 + 4 * lr < g.N ? (uint32_t)((kbeg + 4 * q + x) * (int)g.ldb + n0 + 4 * lr) * 4u : kBufOOB;
+    }
+  }
+  const uint32_t a_step = 4u * (A_MC ? KD * (uint32_t)g.lda : KD);
+  const uint32_t b_step = 4u * (B_KC ? KD : KD * (uint32_t)g.ldb);
+
+  auto load = [&](int kt, f32x4(&fa)[4], f32x4(&fb)[4]) {
+    const uint32_t da = (uint32_t)kt * a_step, db = (uint32_t)kt * b_step;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      fa[x] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(a_off[x] + da), 0, 0));
+      fb[x] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(b_off[x] + db), 0, 0));
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const bool do_cs = COLSUM && tm == 0 && wm == 0;
+  float csum[4] = {0.f, 0.f, 0.f, 0.f};  // per lane: its 4 columns' partial sums
+
+  // fragment value for (block i, step j) and the MFMA step
+  auto mfma = [&](const f32x4(&fa)[4], const f32x4(&fb)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const float av = A_MC ? fa[j][i] : fa[i][j];
+          const float bv = B_KC ? fb[n][j] : fb[j][n];
+          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i][n], 0, 0, 0);
+        }
+    if (do_cs) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) csum[n] += B_KC ? fb[n][j] : fb[j][n];
+    }
+  };
+
+  f32x4 fa0[4], fb0[4], fa1[4], fb1[4], fa2[4], fb2[4];
+  load(0, fa0, fb0);
+  load(1, fa1, fb1);
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 3) {
+    load(kt + 2, fa2, fb2);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(kt + 3, fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    load(kt + 4, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(fa2, fb2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (kt < nk) mfma(fa0, fb0);
+  if (kt + 1 < nk) mfma(fa1, fb1);
+
+  // Epilogue: undo the permutation and write 16-byte row segments.
+  const float alpha = g.alpha, beta = g.beta;
+  const bool split_mode = g.splits > 1;
+  float* P = split_mode ? g.part + (int64_t)blockIdx.z * g.M * g.N : nullptr;
+  float* T = smem + wave * (32 * EPI_LD);
+  // Row of D element (block i, d) and column of (block n, lane column c) inside the wave's block.
+  auto rmap = [&](int i, int d) { return A_MC ? 4 * d + i : 16 * i + d; };
+  auto cmap = [&](int n, int c) { return B_KC ? 16 * n + c : 4 * c + n; };
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    // rows [32 half, 32 half + 32) of the wave block
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = rmap(i, 4 * q + r);
+          if ((row >> 5) == half) T[(row & 31) * EPI_LD + cmap(n, lr)] = acc[i][n][r];
+        }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int rr = it * 4 + (lane >> 4), cc = (lane & 15) * 4;
+      const int row = m0 + half * 32 + rr, col = n0 + cc;
+      if (row < g.M && col < g.N) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(T + rr * EPI_LD + cc);
+        if (split_mode) {
+          *reinterpret_cast<f32x4*>(P + (int64_t)row * g.N + col) = v;
+        } else {
+          float* p = C + (int64_t)row * g.ldc + col;
+          v = alpha * v;
+          if (beta != 0.f) v += beta * *reinterpret_cast<const f32x4*>(p);
+          if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + col);
+          *reinterpret_cast<f32x4*>(p) = v;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (COLSUM && tm == 0) {
+    // lanes lr + 16 q hold partial sums of the same 4 columns: fixed-order reduction over q
+    float* S = smem;  // 4 waves x 64 columns... only the wm == 0 waves contribute
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float v = csum[n];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      csum[n] = v;
+    }
+    if (wm == 0 && q == 0) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) S[wn * 64 + cmap(n, lr)] = csum[n];
+    }
+    __syncthreads();
+    if (tid < TN && tn * TN + tid < g.N) {
+      const float cs = S[tid];
+      if (split_mode) g.part_cs[(int64_t)split * g.N + tn * TN + tid] = cs;
+      else g.colsum[tn * TN + tid] += cs;
+    }
+  }
+}
+
 // C = alpha * sum_s part[s] + beta * C and colsum += sum_s part_cs[s], in split
 // order.  Grid: x over column groups of W (4 with VEC, else 1) columns, y over
 // rows (looping when M > 65535), z over batch items -- no integer division.
@@ -327,7 +534,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
 // on MI355X, for K >= 4096 full tiles plus split-K are faster).  A function of
 // the shape only, as mle_gemm_ws_bytes needs.
 struct Tile {
-  int wm, wn;  // MFMA blocks per wave along M / N
+  int wm, wn;         // MFMA blocks per wave along M / N
+  int kd = 32;        // K depth of a stage
+  bool direct = false;  // register-direct kernel (128 x 128, no LDS in the K loop)
   int tm() const { return 32 * wm; }
   int tn() const { return 32 * wn; }
 };
@@ -338,7 +547,7 @@ Tile choose_tile(int M, int N, int K, int batch) {
   if (N <= 64) return {4, 2};
   if (M <= 64) return {2, 4};
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * batch;
-  if (t128 >= 512 || K >= 4096) return {4, 4};
+  if (t128 >= 512 || K >= 4096) return {4, 4, 16, true};
   return N >= M ? Tile{2, 4} : Tile{4, 2};
 }
 
@@ -348,39 +557,56 @@ int choose_splits(int M, int N, int K, int batch, int& kchunk) {
   kchunk = K;
   const Tile t = choose_tile(M, N, K, batch);
   const long long tiles = (long long)((M + t.tm() - 1) / t.tm()) * ((N + t.tn() - 1) / t.tn()) * batch;
-  // Measured on MI355X: with ~256 tiles a split only pays off for long K.
-  if (tiles >= 384 || (tiles >= 128 && K < 4096)) return 1;
-  int s = (int)((768 + tiles - 1) / tiles);
-  const int smax = K / 256;
+  int s, smax;
+  if (t.direct) {
+    // A grid of >= 3/4 of the 256 CUs runs unsplit.
+    if (tiles >= 192) return 1;
+    s = (int)((256 + tiles - 1) / tiles);
+    smax = K / 512;
+  } else {
+    // Measured on MI355X: with ~256 tiles a split only pays off for long K.
+    if (tiles >= 384 || (tiles >= 128 && K < 4096)) return 1;
+    s = (int)((768 + tiles - 1) / tiles);
+    smax = K / 256;
+  }
   if (s > smax) s = smax;
   if (s < 2) return 1;
   kchunk = (K + s - 1) / s;
-  kchunk = ((kchunk + BK - 1) / BK) * BK;
+  kchunk = ((kchunk + 31) / 32) * 32;  // whole stages of either depth
   s = (K + kchunk - 1) / kchunk;
   if ((long long)s * batch > 65535) return 1;
   return s;
 }
 
-template <int TA, int TB, int WM, int WN>
+template <int TA, int TB, int WM, int WN, int KD>
 void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, int vec, bool cs) {
   if (vec == 2) {
-    if (cs) gemm_kernel<TA, TB, 2, true, WM, WN><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 2, false, WM, WN><<<grid, NT, 0, s>>>(g);
+    if (cs) gemm_kernel<TA, TB, 2, true, WM, WN, KD><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 2, false, WM, WN, KD><<<grid, NT, 0, s>>>(g);
   } else if (vec == 1) {
-    if (cs) gemm_kernel<TA, TB, 1, true, WM, WN><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 1, false, WM, WN><<<grid, NT, 0, s>>>(g);
+    if (cs) gemm_kernel<TA, TB, 1, true, WM, WN, KD><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 1, false, WM, WN, KD><<<grid, NT, 0, s>>>(g);
   } else {
-    if (cs) gemm_kernel<TA, TB, 0, true, WM, WN><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 0, false, WM, WN><<<grid, NT, 0, s>>>(g);
+    if (cs) gemm_kernel<TA, TB, 0, true, WM, WN, KD><<<grid, NT, 0, s>>>(g);
+    else gemm_kernel<TA, TB, 0, false, WM, WN, KD><<<grid, NT, 0, s>>>(g);
   }
 }
 
 template <int TA, int TB>
 void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, bool cs) {
-  if (t.wm == 4 && t.wn == 4) launch_t<TA, TB, 4, 4>(s, g, grid, vec, cs);
-  else if (t.wm == 4) launch_t<TA, TB, 4, 2>(s, g, grid, vec, cs);
-  else if (t.wn == 4) launch_t<TA, TB, 2, 4>(s, g, grid, vec, cs);
-  else launch_t<TA, TB, 2, 2>(s, g, grid, vec, cs);
+  if (t.direct && vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0) {
+    if (cs) gemm_direct_kernel<TA, TB, true><<<grid, NT, 0, s>>>(g);
+    else gemm_direct_kernel<TA, TB, false><<<grid, NT, 0, s>>>(g);
+  } else if (t.wm == 4 && t.wn == 4) {
+    if (t.kd == 16) launch_t<TA, TB, 4, 4, 16>(s, g, grid, vec, cs);
+    else launch_t<TA, TB, 4, 4, 32>(s, g, grid, vec, cs);
+  } else if (t.wm == 4) {
+    launch_t<TA, TB, 4, 2, 32>(s, g, grid, vec, cs);
+  } else if (t.wn == 4) {
+    launch_t<TA, TB, 2, 4, 32>(s, g, grid, vec, cs);
+  } else {
+    launch_t<TA, TB, 2, 2, 32>(s, g, grid, vec, cs);
+  }
 }
 
 // Bytes spanned by one batch item of an operand stored rows x cols with leading dimension ld.

@@ -29,14 +29,14 @@ constexpr int BM = 128, BN = 128;
 constexpr int LDMN = BM + PAD;  // row stride of m/n-contiguous 128-wide tiles
 
 // A_MC: A tile is m-contiguous; B_KC: B tile is k-contiguous.  TM / TN: tile
-// extent along M / N (128 or 64).
-template <bool A_MC, int TM = BM>
+// extent along M / N (128 or 64); KD: K depth of a stage (32 or 16).
+template <bool A_MC, int TM = BM, int KD = BK>
 constexpr int a_tile_floats() {
-  return A_MC ? BK * (TM + PAD) : TM * LDK;
+  return A_MC ? KD * (TM + PAD) : TM * (KD + PAD);
 }
-template <bool B_KC, int TN = BN>
+template <bool B_KC, int TN = BN, int KD = BK>
 constexpr int b_tile_floats() {
-  return B_KC ? TN * LDK : BK * (TN + PAD);
+  return B_KC ? TN * (KD + PAD) : KD * (TN + PAD);
 }
 
 // One BK-deep slice of MFMAs for this wave's (16*WM) x (16*WN) block; the
@@ -45,11 +45,11 @@ constexpr int b_tile_floats() {
 // the compiler from sinking them between the MFMAs: otherwise m/n-contiguous
 // tiles (four ds_read_b32 per fragment) end up with an LDS wait before every
 // few MFMAs.  The hardware waits only for the reads of the current 16-deep step.
-template <bool A_MC, bool B_KC, int WM = 4, int WN = 4>
+template <bool A_MC, bool B_KC, int WM = 4, int WN = 4, int KD = BK>
 __device__ __forceinline__ void mma_stage(const float* __restrict__ As, const float* __restrict__ Bs,
                                           f32x4 (&acc)[WM][WN], int wm, int wn, int lr, int q) {
-  constexpr int KB = BK / 16;
-  constexpr int LDA = 32 * WM + PAD, LDB = 32 * WN + PAD;
+  constexpr int KB = KD / 16;
+  constexpr int LDA = 32 * WM + PAD, LDB = 32 * WN + PAD, LDKK = KD + PAD;
   f32x4 a[KB][WM], b[KB][WN];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
@@ -57,7 +57,7 @@ __device__ __forceinline__ void mma_stage(const float* __restrict__ As, const fl
     for (int i = 0; i < WM; ++i) {
       const int row = wm * 16 * WM + i * 16 + lr;
       if (!A_MC) {
-        a[kb][i] = *reinterpret_cast<const f32x4*>(As + row * LDK + kb * 16 + 4 * q);
+        a[kb][i] = *reinterpret_cast<const f32x4*>(As + row * LDKK + kb * 16 + 4 * q);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) a[kb][i][j] = As[(kb * 16 + 4 * q + j) * LDA + row];
@@ -67,7 +67,7 @@ __device__ __forceinline__ void mma_stage(const float* __restrict__ As, const fl
     for (int i = 0; i < WN; ++i) {
       const int col = wn * 16 * WN + i * 16 + lr;
       if (B_KC) {
-        b[kb][i] = *reinterpret_cast<const f32x4*>(Bs + col * LDK + kb * 16 + 4 * q);
+        b[kb][i] = *reinterpret_cast<const f32x4*>(Bs + col * LDKK + kb * 16 + 4 * q);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) b[kb][i][j] = Bs[(kb * 16 + 4 * q + j) * LDB + col];
