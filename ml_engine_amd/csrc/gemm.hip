@@ -302,12 +302,17 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
 // Either way a wave issues 4 loads per operand per stage; the two waves that
 // share a row (column) panel hit the same lines, which the L1 serves.  The
 // epilogue undoes the row/column permutation while staging C through LDS.
+// The LDS footprint is padded to 56 KiB so that at most 2 workgroups share a
+// CU: with 3, a grid of a few thousand tiles ends in a mostly empty last round.
+constexpr int kDirectSmem = 14336;
+
 template <int TA, int TB, bool COLSUM>
 __global__ __launch_bounds__(NT, 2) void gemm_direct_kernel(GemmArgs g) {
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
   constexpr int KD = 16, TM = 128, TN = 128, EPI_LD = 68;
-  __shared__ __attribute__((aligned(16))) float smem[4 * 32 * EPI_LD];
+  static_assert(4 * 32 * EPI_LD <= kDirectSmem, "epilogue staging does not fit");
+  __shared__ __attribute__((aligned(16))) float smem[kDirectSmem];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -547,7 +552,7 @@ Tile choose_tile(int M, int N, int K, int batch) {
   if (N <= 64) return {4, 2};
   if (M <= 64) return {2, 4};
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * batch;
-  if (t128 >= 512 || K >= 4096) return {4, 4, 16, true};
+  if (t128 >= 192 || K >= 4096) return {4, 4, 16, true};
   return N >= M ? Tile{2, 4} : Tile{4, 2};
 }
 
