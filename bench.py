@@ -7,7 +7,9 @@ vocab 8000), with inputs and parameters resident in HBM.  The JSON line also
 carries:
   roofline      the dominant kernel family (the GEMM layout with the most time),
                 timed per launch with HIP events on the engine stream during the
-                timed steps; achieved = algorithmic flop per launch / duration
+                timed steps; achieved = algorithmic flop per launch / duration;
+                traffic = that family's HBM bytes per launch from the committed
+                rocprofv3 counter passes (profiles/c4_gemm_traffic.md)
   cpu_baseline  the CPU oracle (OpenMP restatement of the reference math) on a
                 bounded sample of the same step, scaled to steps/s
   extras        C3 (Linear GEMM backward) TFLOP/s, C2 (fused clip + AdamW
@@ -59,6 +61,16 @@ def build_block(cfg: BlockConfig) -> Model:
     m.input(1, tgt)
     m.sync()
     return m
+
+
+def measured_traffic(fam: str):
+    """HBM bytes per launch of a GEMM family from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (profiles/c4_gemm_traffic.md), or None."""
+    try:
+        data = json.loads((ROOT / "profiles" / "c4_gemm_traffic.json").read_text())
+        return round(data[fam]["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def dominant_family(m: Model, lr: float) -> str:
@@ -223,7 +235,7 @@ def main() -> int:
         m.step(cfg.lr, STEP_ALL)
     m.sync()
     dt = time.perf_counter() - t0
-    n, kms, kflop, _ = probe_read()
+    n, kms, kflop, kbytes = probe_read()
     hip.call("mle_probe_arm", None)
     ms_step = dt * 1e3 / args.steps
     log(f"[bench] {args.steps} steps in {dt:.3f} s: {ms_step:.3f} ms/step, loss {m.loss:.6g}")
@@ -231,7 +243,8 @@ def main() -> int:
     avg_ms = kms / max(n, 1)
     achieved = (kflop / max(n, 1)) / (avg_ms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": fam, "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
+                "traffic": measured_traffic(fam), "alg_bytes_per_launch": round(kbytes / max(n, 1)),
                 "launches": n, "avg_launch_ms": round(avg_ms, 5),
                 "flop_per_launch": kflop / max(n, 1)}
     m.close()
