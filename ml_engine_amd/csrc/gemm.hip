@@ -290,29 +290,33 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
   }
 }
 
-// Register-direct variant for 128 x 128 tiles: no LDS and no barrier in the
-// K loop.  Each lane loads its own MFMA fragments from global memory with
-// 16-byte reads, two K stages (16 deep) ahead of the MFMAs:
-//  * an operand stored k-contiguous gives lane (lr, q) the 4 k values
-//    4q..4q+3 of row 16 i + lr in one load (one load per 16-row block i);
-//  * an operand stored m- (or n-) contiguous is read along m instead: the
-//    wave's 64 rows are permuted so that block i, lane row lr is row
-//    4 lr + i, and one load of 4 consecutive rows at k = 4q + j holds that
-//    lane's values for all four blocks (one load per MFMA step j).
-// Either way a wave issues 4 loads per operand per stage; the two waves that
-// share a row (column) panel hit the same lines, which the L1 serves.  The
-// epilogue undoes the row/column permutation while staging C through LDS.
-// The LDS footprint is padded to 56 KiB so that at most 2 workgroups share a
-// CU: with 3, a grid of a few thousand tiles ends in a mostly empty last round.
-constexpr int kDirectSmem = 14336;
-
-template <int TA, int TB, bool COLSUM>
-__global__ __launch_bounds__(NT, 2) void gemm_direct_kernel(GemmArgs g) {
+// Register-direct variant for 128 x 128 tiles: no LDS and no barrier.  Each
+// lane loads its own MFMA fragments from global memory with 16-byte reads,
+// D - 1 K stages (KD deep each) ahead of the MFMAs, through D register sets.
+// Within a stage, lane group q = lane / 16 feeds k = (KD/4) q + j to MFMA
+// step j (j < KD/4); A and B use the same k permutation, so the contraction
+// is unchanged.
+//  * an operand stored k-contiguous gives lane (lr, q) KD/4 consecutive k
+//    values of one row (column) in KD/16 loads per 16-row block; with KD = 32
+//    the four lane groups cover a full 128-byte line of each row per stage;
+//  * an operand stored m- (or n-) contiguous is read along m instead: one
+//    load of 4 consecutive rows at k = (KD/4) q + j holds that lane's values
+//    for all four blocks (one load per MFMA step j).
+// Rows and columns inside the wave's 64 x 64 block are permuted so that
+// every lane ends with 4 consecutive C columns per row: block n, lane column
+// c is column 4c + n for both B layouts, and block i, accumulator row d is
+// row 4d + i (A m-contiguous) or 16i + d (A k-contiguous).  The epilogue
+// therefore writes 16-byte row segments straight from the accumulators.
+// A wave issues KD/4 loads per operand per stage; the two waves that share a
+// row (column) panel hit the same lines, which the L1 serves.
+template <int TA, int TB, bool COLSUM, int KD, int D, int OCC>
+__global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
-  constexpr int KD = 16, TM = 128, TN = 128, EPI_LD = 68;
-  static_assert(4 * 32 * EPI_LD <= kDirectSmem, "epilogue staging does not fit");
-  __shared__ __attribute__((aligned(16))) float smem[kDirectSmem];
+  constexpr int TM = 128, TN = 128;
+  constexpr int S = KD / 4;   // MFMA steps (and loads per operand) per stage
+  constexpr int H = KD / 16;  // loads per 16-row block of a k-contiguous operand
+  static_assert(D >= 2 && (KD == 16 || KD == 32), "unsupported stage shape");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -334,35 +338,37 @@ __global__ __launch_bounds__(NT, 2) void gemm_direct_kernel(GemmArgs g) {
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), (short)0, (int)b_bytes, kBufWord3);
   const int nk = kend > kbeg ? (kend - kbeg + KD - 1) / KD : 0;
 
-  // Byte offsets at k = kbeg of the four loads per operand, and the
-  // per-stage advance.  K and the split's chunk are multiples of 16 (checked
-  // on the host), so every stage is full.  A row (column) outside the matrix
-  // starts at kBufOOB and stays past the buffer's extent for every stage
-  // (kt * step < 2^31), so the hardware range check returns zeros.  Stages
-  // fetched past the end of K are never consumed.
-  uint32_t a_off[4], b_off[4];
+  // Byte offsets at k = kbeg of the S loads per operand, and the per-stage
+  // advance.  K and the split's chunk are multiples of KD (checked on the
+  // host), so every stage is full.  A row (column) outside the matrix starts
+  // at kBufOOB, past the buffer's extent; the hardware range check returns
+  // zeros for it, and its products only reach C rows (columns) that are never
+  // stored.  Stages fetched past the end of K (up to D - 1) are never
+  // consumed; a buffer load never faults, whatever its offset.
+  const int kq = kbeg + S * q;  // first k of this lane group
+  uint32_t a_off[S], b_off[S];
 #pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    if (!A_MC) {  // x = block i: row m0 + 16 x + lr, k = kbeg + 4 q
-      const int row = m0 + 16 * x + lr;
-      a_off[x] = row < g.M ? (uint32_t)(row * (int)g.lda + kbeg + 4 * q) * 4u : kBufOOB;
-    } else {  // x = step j: k = kbeg + 4 q + x, rows m0 + 4 lr .. + 3
-      a_off[x] = m0 + 4 * lr < g.M ? (uint32_t)((kbeg + 4 * q + x) * (int)g.lda + m0 + 4 * lr) * 4u : kBufOOB;
+  for (int x = 0; x < S; ++x) {
+    if (!A_MC) {  // x = (block i, half h): row m0 + 16 i + lr, k = kq + 4 h
+      const int row = m0 + 16 * (x / H) + lr;
+      a_off[x] = row < g.M ? (uint32_t)(row * (int)g.lda + kq + 4 * (x % H)) * 4u : kBufOOB;
+    } else {  // x = step j: k = kq + x, rows m0 + 4 lr .. + 3
+      a_off[x] = m0 + 4 * lr < g.M ? (uint32_t)((kq + x) * (int)g.lda + m0 + 4 * lr) * 4u : kBufOOB;
     }
-    if (B_KC) {  // x = block n: column n0 + 16 x + lr, k = kbeg + 4 q
-      const int col = n0 + 16 * x + lr;
-      b_off[x] = col < g.N ? (uint32_t)(col * (int)g.ldb + kbeg + 4 * q) * 4u : kBufOOB;
-    } else {  // x = step j: k = kbeg + 4 q + x, columns n0 + 4 lr .. + 3
-      b_off[x] = n0 + 4 * lr < g.N ? (uint32_t)((kbeg + 4 * q + x) * (int)g.ldb + n0 + 4 * lr) * 4u : kBufOOB;
+    if (B_KC) {  // x = (block n, half h): column n0 + 4 lr + n, k = kq + 4 h
+      const int col = n0 + 4 * lr + x / H;
+      b_off[x] = col < g.N ? (uint32_t)(col * (int)g.ldb + kq + 4 * (x % H)) * 4u : kBufOOB;
+    } else {  // x = step j: k = kq + x, columns n0 + 4 lr .. + 3
+      b_off[x] = n0 + 4 * lr < g.N ? (uint32_t)((kq + x) * (int)g.ldb + n0 + 4 * lr) * 4u : kBufOOB;
     }
   }
   const uint32_t a_step = 4u * (A_MC ? KD * (uint32_t)g.lda : KD);
   const uint32_t b_step = 4u * (B_KC ? KD : KD * (uint32_t)g.ldb);
 
-  auto load = [&](int kt, f32x4(&fa)[4], f32x4(&fb)[4]) {
+  auto load = [&](int kt, f32x4(&fa)[S], f32x4(&fb)[S]) {
     const uint32_t da = (uint32_t)kt * a_step, db = (uint32_t)kt * b_step;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
+    for (int x = 0; x < S; ++x) {
       fa[x] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(a_off[x] + da), 0, 0));
       fb[x] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(b_off[x] + db), 0, 0));
     }
@@ -374,92 +380,79 @@ __global__ __launch_bounds__(NT, 2) void gemm_direct_kernel(GemmArgs g) {
 #pragma unroll
     for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bool do_cs = COLSUM && tm == 0 && wm == 0;
-  float csum[4] = {0.f, 0.f, 0.f, 0.f};  // per lane: its 4 columns' partial sums
+  float csum[4] = {0.f, 0.f, 0.f, 0.f};  // per lane: partial sums of columns 4 lr + n
 
-  // fragment value for (block i, step j) and the MFMA step
-  auto mfma = [&](const f32x4(&fa)[4], const f32x4(&fb)[4]) {
+  // Operand value of (block i or n, step j).
+  auto av = [&](const f32x4(&fa)[S], int i, int j) { return A_MC ? fa[j][i] : fa[i * H + j / 4][j % 4]; };
+  auto bv = [&](const f32x4(&fb)[S], int n, int j) { return B_KC ? fb[n * H + j / 4][j % 4] : fb[j][n]; };
+  auto mfma = [&](const f32x4(&fa)[S], const f32x4(&fb)[S]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < S; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const float av = A_MC ? fa[j][i] : fa[i][j];
-          const float bv = B_KC ? fb[n][j] : fb[j][n];
-          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[i][n], 0, 0, 0);
-        }
+        for (int n = 0; n < 4; ++n)
+          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av(fa, i, j), bv(fb, n, j), acc[i][n], 0, 0, 0);
     if (do_cs) {
 #pragma unroll
       for (int n = 0; n < 4; ++n)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) csum[n] += B_KC ? fb[n][j] : fb[j][n];
+        for (int j = 0; j < S; ++j) csum[n] += bv(fb, n, j);
     }
   };
 
-  f32x4 fa0[4], fb0[4], fa1[4], fb1[4], fa2[4], fb2[4];
-  load(0, fa0, fb0);
-  load(1, fa1, fb1);
+  // Stage s lives in register set s % D.  Each pass of the loop consumes D
+  // stages and issues the loads D - 1 stages ahead of each.
+  f32x4 fa[D][S], fb[D][S];
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load(s, fa[s], fb[s]);
   int kt = 0;
-  for (; kt + 2 < nk; kt += 3) {
-    load(kt + 2, fa2, fb2);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma(fa0, fb0);
-    __builtin_amdgcn_sched_barrier(0);
-    load(kt + 3, fa0, fb0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma(fa1, fb1);
-    __builtin_amdgcn_sched_barrier(0);
-    load(kt + 4, fa1, fb1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma(fa2, fb2);
-    __builtin_amdgcn_sched_barrier(0);
+  for (; kt + D - 1 < nk; kt += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      load(kt + s + D - 1, fa[(s + D - 1) % D], fb[(s + D - 1) % D]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(fa[s], fb[s]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
-  if (kt < nk) mfma(fa0, fb0);
-  if (kt + 1 < nk) mfma(fa1, fb1);
+  // Fewer than D stages remain, all of them already loaded (sets 0 .. D - 2).
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s)
+    if (kt + s < nk) mfma(fa[s], fb[s]);
 
-  // Epilogue: undo the permutation and write 16-byte row segments.
-  const float alpha = g.alpha, beta = g.beta;
+  // Epilogue: lane (lr, q) holds C[row(i, 4q + r)][4 lr + n] in acc[i][n][r],
+  // so each (i, r) is one 16-byte store of 4 consecutive columns.  N, ldc and
+  // C are 16-byte aligned on this path (checked on the host).
   const bool split_mode = g.splits > 1;
   float* P = split_mode ? g.part + (int64_t)blockIdx.z * g.M * g.N : nullptr;
-  float* T = smem + wave * (32 * EPI_LD);
-  // Row of D element (block i, d) and column of (block n, lane column c) inside the wave's block.
+  const int col = n0 + 4 * lr;
   auto rmap = [&](int i, int d) { return A_MC ? 4 * d + i : 16 * i + d; };
-  auto cmap = [&](int n, int c) { return B_KC ? 16 * n + c : 4 * c + n; };
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    // rows [32 half, 32 half + 32) of the wave block
+  if (col < g.N) {
+    const float alpha = g.alpha, beta = g.beta;
+    f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
+    if (!split_mode && g.bias) b4 = *reinterpret_cast<const f32x4*>(g.bias + col);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = rmap(i, 4 * q + r);
-          if ((row >> 5) == half) T[(row & 31) * EPI_LD + cmap(n, lr)] = acc[i][n][r];
-        }
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int rr = it * 4 + (lane >> 4), cc = (lane & 15) * 4;
-      const int row = m0 + half * 32 + rr, col = n0 + cc;
-      if (row < g.M && col < g.N) {
-        f32x4 v = *reinterpret_cast<const f32x4*>(T + rr * EPI_LD + cc);
-        if (split_mode) {
-          *reinterpret_cast<f32x4*>(P + (int64_t)row * g.N + col) = v;
-        } else {
-          float* p = C + (int64_t)row * g.ldc + col;
-          v = alpha * v;
-          if (beta != 0.f) v += beta * *reinterpret_cast<const f32x4*>(p);
-          if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + col);
-          *reinterpret_cast<f32x4*>(p) = v;
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + rmap(i, 4 * q + r);
+        if (row < g.M) {
+          f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+          if (split_mode) {
+            *reinterpret_cast<f32x4*>(P + (int64_t)row * g.N + col) = v;
+          } else {
+            float* p = C + (int64_t)row * g.ldc + col;
+            v = alpha * v;
+            if (beta != 0.f) v += beta * *reinterpret_cast<const f32x4*>(p);
+            *reinterpret_cast<f32x4*>(p) = v + b4;
+          }
         }
       }
-    }
-    __syncthreads();
   }
-  if (COLSUM && tm == 0) {
-    // lanes lr + 16 q hold partial sums of the same 4 columns: fixed-order reduction over q
-    float* S = smem;  // 4 waves x 64 columns... only the wm == 0 waves contribute
+  if (do_cs) {
+    // lanes lr + 16 q hold partial sums of the same 4 columns: fixed-order
+    // reduction over q, then lane q == 0 owns columns col .. col + 3.
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       float v = csum[n];
@@ -467,15 +460,12 @@ __global__ __launch_bounds__(NT, 2) void gemm_direct_kernel(GemmArgs g) {
       v += __shfl_xor(v, 32, 64);
       csum[n] = v;
     }
-    if (wm == 0 && q == 0) {
+    if (q == 0 && col < g.N) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n) S[wn * 64 + cmap(n, lr)] = csum[n];
-    }
-    __syncthreads();
-    if (tid < TN && tn * TN + tid < g.N) {
-      const float cs = S[tid];
-      if (split_mode) g.part_cs[(int64_t)split * g.N + tn * TN + tid] = cs;
-      else g.colsum[tn * TN + tid] += cs;
+      for (int n = 0; n < 4; ++n) {
+        if (split_mode) g.part_cs[(int64_t)split * g.N + col + n] = csum[n];
+        else g.colsum[col + n] += csum[n];
+      }
     }
   }
 }
@@ -597,11 +587,21 @@ void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, int vec, bool cs) {
   }
 }
 
+// Direct kernel configuration, measured on MI355X over the C3/C4 shapes:
+// 16-deep stages, 3 register sets (2 stages in flight), 2 workgroups per CU.
+// Deeper prefetch (up to 8 sets at 1 workgroup per CU), 32-deep stages and
+// 8-wave 256 x 128 tiles were all equal or slower: the kernel is held by the
+// shader clock it sustains (~2.15 GHz under load), not by load latency.
 template <int TA, int TB>
-void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, bool cs) {
-  if (t.direct && vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0) {
-    if (cs) gemm_direct_kernel<TA, TB, true><<<grid, NT, 0, s>>>(g);
-    else gemm_direct_kernel<TA, TB, false><<<grid, NT, 0, s>>>(g);
+void launch_direct(hipStream_t s, const GemmArgs& g, dim3 grid, bool cs) {
+  if (cs) gemm_direct_kernel<TA, TB, true, 16, 3, 2><<<grid, NT, 0, s>>>(g);
+  else gemm_direct_kernel<TA, TB, false, 16, 3, 2><<<grid, NT, 0, s>>>(g);
+}
+
+template <int TA, int TB>
+void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, bool cs, bool direct_ok) {
+  if (t.direct && direct_ok && vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0) {
+    launch_direct<TA, TB>(s, g, grid, cs);
   } else if (t.wm == 4 && t.wn == 4) {
     if (t.kd == 16) launch_t<TA, TB, 4, 4, 16>(s, g, grid, vec, cs);
     else launch_t<TA, TB, 4, 4, 32>(s, g, grid, vec, cs);
@@ -656,6 +656,9 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
                    extent_bytes(b_rows, b_cols, ldb) < 2147483648.0 - 64;
   const int vec = buf ? 2 : (v4 ? 1 : 0);
   const bool cs = colsum != nullptr;
+  // The direct kernel stores 16-byte row segments of C (and reads bias as float4).
+  const bool direct_ok = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(C) &&
+                         (bias == nullptr || aligned16(bias));
   dim3 grid((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
   hipStream_t s = as_stream(stream);
   static const char* names[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
@@ -665,10 +668,10 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   {
     ProbeScope probe(names[which], s, flop, bytes);
     switch (which) {
-      case 0: launch_tile<0, 0>(s, g, tile, grid, vec, cs); break;
-      case 1: launch_tile<0, 1>(s, g, tile, grid, vec, cs); break;
-      case 2: launch_tile<1, 0>(s, g, tile, grid, vec, cs); break;
-      default: launch_tile<1, 1>(s, g, tile, grid, vec, cs); break;
+      case 0: launch_tile<0, 0>(s, g, tile, grid, vec, cs, direct_ok); break;
+      case 1: launch_tile<0, 1>(s, g, tile, grid, vec, cs, direct_ok); break;
+      case 2: launch_tile<1, 0>(s, g, tile, grid, vec, cs, direct_ok); break;
+      default: launch_tile<1, 1>(s, g, tile, grid, vec, cs, direct_ok); break;
     }
     if (g.splits > 1) {
       const bool rv = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(C) && aligned16(g.part) &&

@@ -38,6 +38,20 @@ GEMM_CASES = [
     (1, 0, 2050, 4100, 36, 1),
     (0, 1, 1024, 1024, 20, 8),
     (1, 1, 2064, 2056, 24, 2),
+    # register-direct kernel (K % 16 == 0, >= 192 tiles): one workgroup per CU
+    # (<= 256 workgroups, deep prefetch) and two per CU, every layout, ragged
+    # M and N, K shorter and longer than the prefetch depth
+    (0, 0, 2000, 1700, 48, 1),
+    (0, 1, 2000, 1700, 16, 1),
+    (1, 0, 1990, 1708, 112, 1),
+    (1, 1, 2010, 1696, 80, 1),
+    (0, 0, 2100, 2052, 32, 1),
+    (0, 1, 2100, 2052, 208, 1),
+    (1, 0, 2098, 2060, 48, 1),
+    (1, 1, 2060, 2100, 16, 1),
+    (0, 1, 1000, 1000, 96, 2),
+    # N not a multiple of 4 with float4-able operands: not the direct kernel
+    (0, 1, 2000, 1702, 48, 1),
 ]
 
 
@@ -95,7 +109,8 @@ def test_gemm_split_k(hip, orc, ta, tb, M, N, K, batch, cs):
         assert_close(dcs.numpy(), cs0 + bsum, what="split-K colsum", **EW)
 
 
-@pytest.mark.parametrize("M,N,K", [(100, 40, 300), (40, 40, 500), (300, 90, 77), (2048, 4096, 40), (64, 130, 300)])
+@pytest.mark.parametrize("M,N,K", [(100, 40, 300), (40, 40, 500), (300, 90, 77), (2048, 4096, 40), (64, 130, 300),
+                                   (2048, 4096, 48), (2000, 1700, 48), (1000, 2052, 4112)])
 def test_gemm_colsum_tiles(hip, orc, M, N, K):
     """dW = X^T dY with the fused column sum, on every workgroup tile shape."""
     r = rng(M * 3 + N + K)
