@@ -233,6 +233,55 @@ int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, 
                  int batch, int channels, size_t hw, int groups, float eps, int reference_layout,
                  void* ws, size_t ws_bytes, int accumulate);
 
+/* BatchNorm: per-channel statistics over (batch, H, W), gamma 1, beta 0.
+ * stats[2c] = mean, stats[2c+1] = sum (x - mean)^2; y = (x - mean) * r with
+ * r = rsqrt(ssd/N + eps), N = batch * hw.  BatchMean / BatchStd / BNorm
+ * (Engine/kernels.cu:574-604, 701-730, 806-816) as composed by
+ * GraphOperations::BatchNorm (Engine/engine.cu:3148-3210). */
+size_t mle_batchnorm_ws_bytes(int batch, int channels, size_t hw);
+int mle_batchnorm_fwd(mle_stream stream, const float* x, float* y, float* stats,
+                      int batch, int channels, size_t hw, float eps, void* ws, size_t ws_bytes);
+/* dx (+)= r * (dy - sum(dy)/N - y * sum(dy*y)/N) per channel.  BatchBackward
+ * (Engine/kernels.cu:864-876) after the ggamma reductions of
+ * Engine/engine.cu:3185-3194; accumulate = 0 assigns. */
+int mle_batchnorm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, const float* stats,
+                      int batch, int channels, size_t hw, float eps, void* ws, size_t ws_bytes, int accumulate);
+
+/* The reference's RMSNorm: an L2 normalisation y = x / sqrtf(sum x^2) along
+ * each row (type 0) or each column (type 1) of every [rows x cols] matrix;
+ * norms[] gets one value per line.  SumSquaredSqrtCols / SumSquaredSqrtRows +
+ * Scale_arr (Engine/kernels.cu:2246-2277, 2058-2071), GraphOperations::RMSNorm
+ * (Engine/engine.cu:2613-2648). */
+int mle_rmsnorm_fwd(mle_stream stream, const float* x, float* y, float* norms, int bc, int rows, int cols, int type);
+/* dx (+)= (dy - y * <dy, y>) / norm along the same line.
+ * Accumulate_rmsnorm_kernel (Engine/kernels.cu:2073-2105). */
+int mle_rmsnorm_bwd(mle_stream stream, const float* y, const float* dy, const float* norms, float* dx,
+                    int bc, int rows, int cols, int type, int accumulate);
+
+/* ------------------------------------------------------------------------- */
+/* Layout (U-Net skip concatenation, transposed-convolution weights)         */
+/* ------------------------------------------------------------------------- */
+
+/* y [batch][c1 + c2][h][w]: the first c1 channels are x1 [batch][c1][h1][w1]
+ * cropped to its centred h x w window (offsets (h1-h)/2, (w1-w)/2), the rest
+ * are x2 [batch][c2][h][w].  CopynCrop + Channel_Concat (Engine/kernels.cu:
+ * 1330-1348, 1408-1419) as composed by GraphOperations::CopyCrop
+ * (Engine/engine.cu:2855-2920).  h1 < h or w1 < w is rejected
+ * (MLE_ERR_UNSUPPORTED): the reference reads outside x1 there. */
+int mle_copy_crop_fwd(mle_stream stream, const float* x1, const float* x2, float* y,
+                      int batch, int c1, int h1, int w1, int c2, int h, int w);
+/* dx1 (+)= dy[:, :c1] at the centred window (outside it: unchanged, or 0 when
+ * assigning); dx2 (+)= dy[:, c1:].  Channel_Split + PaddingCrop
+ * (Engine/kernels.cu:1421-1433, 1350-1369).  accumulate* = 0 assigns. */
+int mle_copy_crop_bwd(mle_stream stream, const float* dy, float* dx1, float* dx2,
+                      int batch, int c1, int h1, int w1, int c2, int h, int w, int accumulate1, int accumulate2);
+/* dst[i][o][k] (+)= src[o][i][k] for k < khw: swaps the two leading axes of a
+ * convolution weight.  Convolute2DT keeps [out][inp][kh][kw] weights
+ * (Includes/engine.h:257-280); with them swapped its forward, input gradient
+ * and weight gradient (CVT2D / CVT2D_GradInput / GVT2D, Engine/kernels.cu:
+ * 1091-1212) are the convolution's dgrad, forward and wgrad below. */
+int mle_weight_swap(mle_stream stream, const float* src, float* dst, int o, int i, int khw, int accumulate);
+
 /* ------------------------------------------------------------------------- */
 /* Convolution (NCHW input, OIHW weights), implicit GEMM on fp32 MFMA        */
 /* ------------------------------------------------------------------------- */

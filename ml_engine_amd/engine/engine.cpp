@@ -926,6 +926,100 @@ graph Convolute2D::forward(const graph& X) {
 }
 
 // ---------------------------------------------------------------------------
+// Convolute2DT (Engine/engine.cu:3819-3900).  W1 [out, inp, c, d], B1 [1, out, 1, 1].
+Convolute2DT::Convolute2DT(int Input, int Output, int C, int D, int stride_, int padding, str param)
+    : inp(Input),
+      out(Output),
+      c(C),
+      d(D),
+      pad(padding),
+      stride(stride_),
+      name(param),
+      W1(param + " Weight ", Output, Input, C, D),
+      B1(param + " Bias ", 1, Output, 1, 1) {}
+void Convolute2DT::save(std::ofstream& f) const {
+  W1.save(f);
+  B1.save(f);
+}
+void Convolute2DT::load(std::ifstream& f) {
+  W1.load(f);
+  B1.load(f);
+}
+
+graph Convolute2DT::forward(const graph& X) {
+  if (X->dim[1] != inp) {
+    std::cout << "Dimension Mismatch! in " << name << ": \n";
+    Dimension(X);
+    std::cout << "Actual input (Batch x depth): (" << X->dim[0] << "x" << X->dim[1] << ") \n";
+    std::cout << "Expected input (Batch x depth): (" << X->dim[0] << "x" << inp << ") \n";
+    std::exit(1);
+  }
+  const int batch = X->dim[0], ih = X->dim[2], iw = X->dim[3];
+  const int oh = (ih - 1) * stride - 2 * pad + c, ow = (iw - 1) * stride - 2 * pad + d;
+  if (oh <= 0 || ow <= 0) {
+    std::cout << "Non-positive output size in " << name << "\n";
+    std::exit(1);
+  }
+  auto node = std::make_shared<NodeBackProp>(name, batch, out, oh, ow, 1);
+  node->lazy_grad_writer = true;
+  node->inputs = {X};
+  GraphOperations::GB += (double)(node->total + W1.total + B1.total) * sizeof(float) / (1ULL << 30);
+  // The convolution this is the adjoint of maps [batch, out, oh, ow] to
+  // [batch, inp, ih, iw] with weights [inp, out, c, d] (W1 swapped).
+  const size_t wn = (size_t)W1.total;
+  float* wt = static_cast<float*>(mle::alloc_scratch(2 * wn * sizeof(float)));  // swapped weight | its gradient
+  float* wtg = wt + wn;
+  const size_t ws_bytes = mle_conv2d_wgrad_ws_bytes(batch, out, oh, ow, inp, c, d, pad, stride);
+  void* ws = mle::alloc_scratch(ws_bytes);
+  AdamParameter* W = &W1;
+  AdamParameter* Bb = &B1;
+  NodeBackProp* nd = node.get();
+  NodeBackProp* x = X.get();
+  const int inp_ = inp, out_ = out, c_ = c, d_ = d, pad_ = pad, st = stride;
+  const str nm = name;
+  node->params = {W, Bb};
+  node->forward = [=]() {
+    check(mle_weight_swap(mle::stream(), W->output, wt, out_, inp_, c_ * d_, 0), "Weight swap in " + nm);
+    check(mle_conv2d_dgrad(mle::stream(), x->output, wt, nd->output, batch, out_, oh, ow, inp_, c_, d_, pad_, st, 0),
+          "ConvTranspose2D Forward in " + nm);
+    check(mle_broadcast_channel_add(mle::stream(), nd->output, Bb->output, nd->output, batch, out_, (size_t)oh * ow),
+          "ConvTranspose2D bias in " + nm);
+  };
+  node->backward = [=]() {
+    check(mle_conv2d_wgrad(mle::stream(), nd->grad, x->output, wtg, batch, out_, oh, ow, inp_, c_, d_, pad_, st, ws,
+                           ws_bytes),
+          "Weight Gradient in " + nm);
+    check(mle_weight_swap(mle::stream(), wtg, W->grad, inp_, out_, c_ * d_, 0), "Weight gradient swap in " + nm);
+    check(mle_channel_sum(mle::stream(), nd->grad, batch, out_, (size_t)oh * ow, out_, Bb->grad),
+          "Bias Gradient in " + nm);
+    mle::accumulate_flag(x);  // assigned, as CVT2D_GradInput does
+    check(mle_conv2d_fwd(mle::stream(), nd->grad, wt, nullptr, x->grad, batch, out_, oh, ow, inp_, c_, d_, pad_, st),
+          "Input Gradient in " + nm);
+  };
+  node->zero_grad = [=]() {
+    mle::defer_zero(nd);
+    mle::zero(W->grad, W->total);
+    mle::zero(Bb->grad, Bb->total);
+  };
+  node->free = [=]() { nd->clear(); };
+  node->serious_free = [=]() {};
+  node->accumulate = [=](double* s) {
+    W->accumulate_grad(s);
+    Bb->accumulate_grad(s);
+  };
+  node->clipnorm = [=](const double* s) {
+    W->gradnorm(s);
+    Bb->gradnorm(s);
+  };
+  node->updateParams = [=](const float lr, const bool adamw) {
+    W->update(lr, adamw);
+    Bb->update(lr, adamw);
+  };
+  node->printparams = [=](const bool) {};
+  return node;
+}
+
+// ---------------------------------------------------------------------------
 // Embedding
 Embedding::Embedding(int vocab_, int dim_, const str name) : vocab(vocab_), dim(dim_), E(name, 1, 1, vocab_, dim_) {}
 void Embedding::save(std::ofstream& f) const { E.save(f); }

@@ -245,7 +245,11 @@ class GraphOperations {
   static graph SIGMOID(const graph& input);
   static graph LeakyRELU(const graph& input);
   static graph LayerNorm(const graph& X);
+  static graph BatchNorm(const graph& X);
   static graph GroupNorm(const graph& X, const int group = 8);
+  static graph InstanceNorm(const graph& X);
+  static graph RMSNorm(const graph& input, const int type = 0);  // type 0: row-wise, type 1: column-wise
+  static graph CopyCrop(const graph& input1, const graph& input2);
   // Token-id inputs (TextualEmbedding::forward key "T", Engine/transformer.cu:190-196).
   static graph OneHot(const int32_t* keys, int batch, int clen, int max_clen, int vocab);
 };
@@ -274,6 +278,23 @@ class Convolute2D {
   str name;
   AdamParameter W1, B1;
   Convolute2D(int Input, int Output, int C = 3, int D = 3, int stride = 1, int padding = 1, str param = "");
+  void save(std::ofstream& f) const;
+  void load(std::ifstream& f);
+  graph forward(const graph& X);
+};
+
+// Transposed convolution (Includes/engine.h:257-280, Engine/engine.cu:3819-3900):
+// W1 [out, inp, c, d], B1 [1, out, 1, 1]; output (H - 1) * stride - 2 pad + c.
+// Runs on the convolution kernels with W1's two leading axes swapped: forward
+// is the convolution's dgrad, the input gradient its forward and the weight
+// gradient its wgrad.  Input and weight gradients are assigned, as the
+// reference's CVT2D_GradInput and GVT2D do.
+class Convolute2DT {
+ public:
+  int inp, out, c, d, pad, stride;
+  str name;
+  AdamParameter W1, B1;
+  Convolute2DT(int Input, int Output, int C = 2, int D = 2, int stride = 2, int padding = 0, str param = "");
   void save(std::ofstream& f) const;
   void load(std::ifstream& f);
   graph forward(const graph& X);

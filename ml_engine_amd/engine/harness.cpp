@@ -29,6 +29,7 @@ struct Model {
   std::unique_ptr<MultiHeadAttention> mha;
   std::unique_ptr<Embedding> emb;
   std::unique_ptr<ResidualBlock> rb;
+  std::unique_ptr<Convolute2DT> up;
   std::vector<std::unique_ptr<AdamParameter>> loose;  // C2 parameters
   double* clip_scale = nullptr;
   bool adamw = true;
@@ -101,6 +102,26 @@ void build_c5(Model* m, const long long* d) {
                &r.skipconv->W1, &r.skipconv->B1, &r.time_mlp->W1, &r.time_mlp->B1};
 }
 
+// U-Net decoder step (the ops of SURVEY's "remaining backward ops"): a
+// transposed convolution upsamples x, CopyCrop concatenates the centred crop
+// of a skip tensor in front of it, then BatchNorm, row RMSNorm, InstanceNorm
+// and column RMSNorm, with an MSE loss against a target.
+// dims {N, Cin, Cout, H, W, Cskip, Hs, Ws, k, stride, pad}
+void build_c6(Model* m, const long long* d) {
+  const int N = (int)d[0], Cin = (int)d[1], Cout = (int)d[2], H = (int)d[3], W = (int)d[4], Cs = (int)d[5],
+            Hs = (int)d[6], Ws = (int)d[7], k = (int)d[8], stride = (int)d[9], pad = (int)d[10];
+  const int Ho = (H - 1) * stride - 2 * pad + k, Wo = (W - 1) * stride - 2 * pad + k;
+  auto x = input_node(m, "Decoder input", N, Cin, H, W);
+  auto skip = input_node(m, "Skip features", N, Cs, Hs, Ws);
+  auto target = input_node(m, "Target", N, Cs + Cout, Ho, Wo);
+  m->up.reset(new Convolute2DT(Cin, Cout, k, k, stride, pad, "Up"));
+  auto h = GraphOperations::CopyCrop(skip, m->up->forward(x));
+  h = GraphOperations::RMSNorm(GraphOperations::BatchNorm(h), 0);
+  h = GraphOperations::RMSNorm(GraphOperations::InstanceNorm(h), 1);
+  m->root = GraphOperations::MeanSquaredError(h, target, true);
+  m->params = {&m->up->W1, &m->up->B1};
+}
+
 // C2: a flat set of parameters; each parameter is carried by a hook node (as
 // Linear's output node carries W1/B1) under one track() root.
 void build_c2(Model* m, const long long* d, int nd) {
@@ -147,6 +168,7 @@ void* mle_model_create(int kind, const long long* dims, int ndims) {
     case 2: build_c2(m, dims, ndims); break;
     case 4: build_c4(m, dims); break;
     case 5: build_c5(m, dims); break;
+    case 6: build_c6(m, dims); break;
     default:
       delete m;
       return nullptr;

@@ -14,7 +14,10 @@ enum { MLE_STEP_ZERO = 1, MLE_STEP_FORWARD = 2, MLE_STEP_BACKWARD = 4, MLE_STEP_
 /* kind 1: MLP   dims {batch, in, hidden, classes}            inputs: x f32, labels i32
  * kind 2: flat  dims {n, size_0 .. size_{n-1}}                (accumulate + clip + AdamW)
  * kind 4: block dims {B, S, D, heads, F, V}                   inputs: ids i32, targets i32
- * kind 5: resblock dims {N, Cin, C, H, W, groups, tdim, t}   inputs: x f32, noise f32 */
+ * kind 5: resblock dims {N, Cin, C, H, W, groups, tdim, t}   inputs: x f32, noise f32
+ * kind 6: U-Net decoder step dims {N, Cin, Cout, H, W, Cskip, Hs, Ws, k, stride, pad}
+ *         (Convolute2DT, CopyCrop, BatchNorm, RMSNorm, InstanceNorm, MSE)
+ *                                                             inputs: x, skip, target f32 */
 void* mle_model_create(int kind, const long long* dims, int ndims);
 void mle_model_destroy(void* h);
 void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad);

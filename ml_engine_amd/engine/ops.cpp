@@ -532,6 +532,83 @@ graph GraphOperations::GroupNorm(const graph& X, const int group) {
   return norm_node(X, group, "GroupNorm");
 }
 
+// InstanceNorm (Engine/engine.cu:3284-3347): per (batch, channel) statistics
+// over H*W -- InstanceMean/InstanceStd/INorm/InstanceBackward are the group
+// normalisation with one group per channel.
+graph GraphOperations::InstanceNorm(const graph& X) { return norm_node(X, X->dim[1], "InstanceNorm"); }
+
+// BatchNorm (Engine/engine.cu:3148-3210): per-channel statistics over
+// (batch, H, W), gamma 1, beta 0, eps 1e-5; no running statistics.
+graph GraphOperations::BatchNorm(const graph& X) {
+  const int a = X->dim[0], b = X->dim[1], c = X->dim[2], d = X->dim[3];
+  const float eps = 1e-5f;
+  auto node = make_node("BatchNorm", a, b, c, d);
+  node->inputs = {X};
+  const size_t hw = (size_t)c * d;
+  const size_t ws_bytes = mle_batchnorm_ws_bytes(a, b, hw);
+  void* ws = mle::alloc_scratch(ws_bytes);
+  float* stats = static_cast<float*>(mle::alloc_scratch(2 * sizeof(float) * b));
+  GraphOperations::GB += (double)(2 * b) * sizeof(float) / (1ULL << 30);
+  NodeBackProp *nd = node.get(), *x = X.get();
+  node->forward = [=]() {
+    check(mle_batchnorm_fwd(S(), x->output, nd->output, stats, a, b, hw, eps, ws, ws_bytes), "BatchNorm forward");
+  };
+  node->backward = [=]() {
+    check(mle_batchnorm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, eps, ws, ws_bytes,
+                            mle::accumulate_flag(x)),
+          "BatchNorm backward");
+  };
+  std_hooks(node);
+  return node;
+}
+
+// RMSNorm (Engine/engine.cu:2613-2648): y = x / ||x|| along each row (type 0)
+// or each column (type 1) of every [H x W] matrix.
+graph GraphOperations::RMSNorm(const graph& X, const int type) {
+  const int a = X->dim[0], b = X->dim[1], c = X->dim[2], d = X->dim[3];
+  auto node = make_node("RMSNorm", a, b, c, d);
+  node->inputs = {X};
+  const size_t lines = (size_t)a * b * (type == 0 ? c : d);
+  float* norms = static_cast<float*>(mle::alloc_scratch(sizeof(float) * lines));
+  GraphOperations::GB += (double)lines * sizeof(float) / (1ULL << 30);
+  NodeBackProp *nd = node.get(), *x = X.get();
+  const int t = type == 0 ? 0 : 1;
+  node->forward = [=]() { check(mle_rmsnorm_fwd(S(), x->output, nd->output, norms, a * b, c, d, t), "RMSNorm forward"); };
+  node->backward = [=]() {
+    check(mle_rmsnorm_bwd(S(), nd->output, nd->grad, norms, x->grad, a * b, c, d, t, mle::accumulate_flag(x)),
+          "RMSNorm backward");
+  };
+  std_hooks(node);
+  return node;
+}
+
+// CopyCrop (Engine/engine.cu:2855-2920): input1's channels, cropped to
+// input2's centred H x W window, followed by input2's channels.
+graph GraphOperations::CopyCrop(const graph& input1, const graph& input2) {
+  const int batch = input2->dim[0], c2 = input2->dim[1], h = input2->dim[2], w = input2->dim[3];
+  const int c1 = input1->dim[1], h1 = input1->dim[2], w1 = input1->dim[3];
+  if (input1->dim[0] != batch || h1 < h || w1 < w) {
+    std::cout << "CopyCrop needs the same batch and input1 at least as large as input2 \n";
+    Dimension(input1);
+    Dimension(input2);
+    std::exit(1);
+  }
+  auto node = make_node("CopyNCrop", batch, c1 + c2, h, w);
+  node->inputs = {input1, input2};
+  NodeBackProp *nd = node.get(), *x1 = input1.get(), *x2 = input2.get();
+  node->forward = [=]() {
+    check(mle_copy_crop_fwd(S(), x1->output, x2->output, nd->output, batch, c1, h1, w1, c2, h, w),
+          "Concatenation in CopynCrop");
+  };
+  node->backward = [=]() {
+    const int acc1 = mle::accumulate_flag(x1), acc2 = mle::accumulate_flag(x2);
+    check(mle_copy_crop_bwd(S(), nd->grad, x1->grad, x2->grad, batch, c1, h1, w1, c2, h, w, acc1, acc2),
+          "Backward CopynCrop");
+  };
+  std_hooks(node);
+  return node;
+}
+
 // One-hot targets from device token ids (TextualEmbedding::forward key "T").
 graph GraphOperations::OneHot(const int32_t* keys, int batch, int clen, int max_clen, int vocab) {
   auto node = make_node("OneHot targets", batch, 1, clen, vocab);

@@ -70,6 +70,14 @@ SIGNATURES: dict[str, tuple] = {
     "mle_norm_ws_bytes": (SZ, [I, I, SZ, I]),
     "mle_norm_fwd": (I, [P, P, P, P, I, I, SZ, I, F, P, SZ]),
     "mle_norm_bwd": (I, [P, P, P, P, P, I, I, SZ, I, F, I, P, SZ, I]),
+    "mle_batchnorm_ws_bytes": (SZ, [I, I, SZ]),
+    "mle_batchnorm_fwd": (I, [P, P, P, P, I, I, SZ, F, P, SZ]),
+    "mle_batchnorm_bwd": (I, [P, P, P, P, P, I, I, SZ, F, P, SZ, I]),
+    "mle_rmsnorm_fwd": (I, [P, P, P, P, I, I, I, I]),
+    "mle_rmsnorm_bwd": (I, [P, P, P, P, P, I, I, I, I, I]),
+    "mle_copy_crop_fwd": (I, [P, P, P, P, I, I, I, I, I, I, I]),
+    "mle_copy_crop_bwd": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I]),
+    "mle_weight_swap": (I, [P, P, P, I, I, I, I]),
     "mle_conv2d_fwd": (I, [P, P, P, P, P, I, I, I, I, I, I, I, I, I]),
     "mle_conv2d_dgrad": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, I]),
     "mle_conv2d_wgrad_ws_bytes": (SZ, [I, I, I, I, I, I, I, I, I]),

@@ -11,7 +11,7 @@ import numpy as np
 
 from . import hip
 
-KIND = {"mlp": 1, "flat": 2, "block": 4, "resblock": 5}
+KIND = {"mlp": 1, "flat": 2, "block": 4, "resblock": 5, "unet_up": 6}
 STEP_ZERO, STEP_FORWARD, STEP_BACKWARD, STEP_UPDATE, STEP_ALL = 1, 2, 4, 8, 15
 P, I, LL, F, SZ = C.c_void_p, C.c_int, C.c_longlong, C.c_float, C.c_size_t
 

@@ -565,3 +565,219 @@ OEXPORT void orc_argmax(const float* x, int rows, int cols, int32_t* out) {
     out[r] = mi;
   }
 }
+
+// ---------------------------------------------------------------------------
+// RMSNorm (Engine/engine.cu:2613-2648): a copy of x, then SumSquaredSqrtCols
+// (type 0, per row over the columns) or SumSquaredSqrtRows (type 1, per column
+// over the rows) (Engine/kernels.cu:2246-2277), then Scale_arr divide
+// (Engine/kernels.cu:2058-2071).  No 1/N and no epsilon: an L2 normalisation.
+// norms[line] = sqrtf(sum x^2).
+OEXPORT void orc_rmsnorm_fwd(const float* x, float* y, float* norms, int bc, int rows, int cols, int type) {
+  const long long lines = type == 0 ? (long long)bc * rows : (long long)bc * cols;
+  const int len = type == 0 ? cols : rows;
+#pragma omp parallel for schedule(static)
+  for (long long line = 0; line < lines; ++line) {
+    long long base, step;
+    if (type == 0) {
+      base = line * cols;
+      step = 1;
+    } else {
+      base = (line / cols) * (long long)rows * cols + line % cols;
+      step = cols;
+    }
+    double s = 0.0;
+    for (int i = 0; i < len; ++i) {
+      const float v = x[base + i * step];
+      s += (double)v * (double)v;
+    }
+    const float n = sqrtf((float)s);
+    norms[line] = n;
+    for (int i = 0; i < len; ++i) y[base + i * step] = x[base + i * step] / n;
+  }
+}
+
+// Accumulate_rmsnorm_kernel (Engine/kernels.cu:2073-2105):
+// dx += (dy - y * <dy, y>) / norm along the same axis.
+OEXPORT void orc_rmsnorm_bwd(const float* y, const float* dy, const float* norms, float* dx, int bc, int rows, int cols,
+                             int type) {
+  const long long lines = type == 0 ? (long long)bc * rows : (long long)bc * cols;
+  const int len = type == 0 ? cols : rows;
+#pragma omp parallel for schedule(static)
+  for (long long line = 0; line < lines; ++line) {
+    long long base, step;
+    if (type == 0) {
+      base = line * cols;
+      step = 1;
+    } else {
+      base = (line / cols) * (long long)rows * cols + line % cols;
+      step = cols;
+    }
+    double dot = 0.0;
+    for (int i = 0; i < len; ++i) dot += (double)dy[base + i * step] * (double)y[base + i * step];
+    const float d = (float)dot, inv = 1.0f / norms[line];
+    for (int i = 0; i < len; ++i) {
+      const long long o = base + i * step;
+      dx[o] += (dy[o] - y[o] * d) * inv;
+    }
+  }
+}
+
+// BatchNorm (Engine/engine.cu:3148-3210): per channel over (batch, H, W) --
+// BatchMean / BatchStd / BNorm (Engine/kernels.cu:574-604, 701-730, 806-816),
+// gamma 1, beta 0.  stats[2c] = mean, stats[2c+1] = sum (x - mean)^2.
+OEXPORT void orc_batchnorm_fwd(const float* x, float* y, float* stats, int batch, int channels, long long hw,
+                               float eps) {
+  const long long N = (long long)batch * hw;
+#pragma omp parallel for schedule(static)
+  for (int c = 0; c < channels; ++c) {
+    double s = 0.0;
+    for (int b = 0; b < batch; ++b)
+      for (long long i = 0; i < hw; ++i) s += x[((long long)b * channels + c) * hw + i];
+    const float mean = (float)(s / (double)N);
+    double ss = 0.0;
+    for (int b = 0; b < batch; ++b)
+      for (long long i = 0; i < hw; ++i) {
+        const float d = x[((long long)b * channels + c) * hw + i] - mean;
+        ss += (double)d * (double)d;
+      }
+    const float ssd = (float)ss;
+    const float r = 1.0f / sqrtf((1.0f / (float)N) * ssd + eps);
+    for (int b = 0; b < batch; ++b)
+      for (long long i = 0; i < hw; ++i) {
+        const long long o = ((long long)b * channels + c) * hw + i;
+        y[o] = (x[o] - mean) * r;
+      }
+    stats[2 * c] = mean;
+    stats[2 * c + 1] = ssd;
+  }
+}
+
+// BatchBackward (Engine/kernels.cu:864-876) after the per-channel sums of
+// ggamma = dy and ggammanode = dy * y (Engine/engine.cu:3185-3194).
+OEXPORT void orc_batchnorm_bwd(const float* y, const float* dy, float* dx, const float* stats, int batch, int channels,
+                               long long hw, float eps) {
+  const long long N = (long long)batch * hw;
+  const float fN = (float)N;
+#pragma omp parallel for schedule(static)
+  for (int c = 0; c < channels; ++c) {
+    double a = 0.0, b2 = 0.0;
+    for (int b = 0; b < batch; ++b)
+      for (long long i = 0; i < hw; ++i) {
+        const long long o = ((long long)b * channels + c) * hw + i;
+        a += dy[o];
+        b2 += (double)(dy[o] * y[o]);
+      }
+    const float sg = (float)a, sgy = (float)b2;
+    const float r = 1.0f / sqrtf(stats[2 * c + 1] / fN + eps);
+    for (int b = 0; b < batch; ++b)
+      for (long long i = 0; i < hw; ++i) {
+        const long long o = ((long long)b * channels + c) * hw + i;
+        dx[o] += r * (dy[o] - (sg / fN) - y[o] * (sgy / fN));
+      }
+  }
+}
+
+// CopyCrop (Engine/engine.cu:2855-2920) for the cropping case h1 >= h, w1 >= w:
+// CopynCrop centres x1's (h1, w1) window on (h, w) (Engine/kernels.cu:1330-1348),
+// then Channel_Concat puts its c1 channels before x2's c2 (Engine/kernels.cu:1408-1419).
+OEXPORT void orc_copy_crop_fwd(const float* x1, const float* x2, float* y, int batch, int c1, int h1, int w1, int c2,
+                               int h, int w) {
+  const int dr = (h1 - h) / 2, dc = (w1 - w) / 2;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < batch; ++b)
+    for (int ch = 0; ch < c1 + c2; ++ch)
+      for (int r = 0; r < h; ++r)
+        for (int c = 0; c < w; ++c) {
+          const long long o = (((long long)b * (c1 + c2) + ch) * h + r) * w + c;
+          y[o] = ch < c1 ? x1[(((long long)b * c1 + ch) * h1 + r + dr) * w1 + c + dc]
+                         : x2[(((long long)b * c2 + ch - c1) * h + r) * w + c];
+        }
+}
+
+// CopyCrop backward: Channel_Split (Engine/kernels.cu:1421-1433) into a
+// (c1, h, w) temporary and x2's gradient, then PaddingCrop adds the temporary
+// back into x1's gradient at the centred window (Engine/kernels.cu:1350-1369).
+OEXPORT void orc_copy_crop_bwd(const float* dy, float* dx1, float* dx2, int batch, int c1, int h1, int w1, int c2, int h,
+                               int w) {
+  const int dr = (h1 - h) / 2, dc = (w1 - w) / 2;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < batch; ++b)
+    for (int ch = 0; ch < c1 + c2; ++ch)
+      for (int r = 0; r < h; ++r)
+        for (int c = 0; c < w; ++c) {
+          const float g = dy[(((long long)b * (c1 + c2) + ch) * h + r) * w + c];
+          if (ch < c1) dx1[(((long long)b * c1 + ch) * h1 + r + dr) * w1 + c + dc] += g;
+          else dx2[(((long long)b * c2 + ch - c1) * h + r) * w + c] += g;
+        }
+}
+
+// Transposed convolution, weights [out][inp][kh][kw] (Includes/engine.h:257-280).
+// CVT2D (Engine/kernels.cu:1091-1135): out_h = (H - 1) * stride - 2 pad + kh.
+OEXPORT void orc_convT_fwd(const float* x, const float* w, const float* bias, float* y, int N, int Cin, int H, int W,
+                           int Cout, int KH, int KW, int pad, int stride) {
+  const int OH = (H - 1) * stride - 2 * pad + KH, OW = (W - 1) * stride - 2 * pad + KW;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int oc = 0; oc < Cout; ++oc)
+      for (int row = 0; row < OH; ++row)
+        for (int col = 0; col < OW; ++col) {
+          double acc = 0.0;
+          for (int ic = 0; ic < Cin; ++ic)
+            for (int kh = 0; kh < KH; ++kh)
+              for (int kw = 0; kw < KW; ++kw) {
+                int ir = row + pad - kh, icl = col + pad - kw;
+                if (ir % stride != 0 || icl % stride != 0) continue;
+                ir /= stride;
+                icl /= stride;
+                if (ir < 0 || ir >= H || icl < 0 || icl >= W) continue;
+                acc += (double)x[(((long long)n * Cin + ic) * H + ir) * W + icl] *
+                       (double)w[(((long long)oc * Cin + ic) * KH + kh) * KW + kw];
+              }
+          const float s = (float)acc;
+          y[(((long long)n * Cout + oc) * OH + row) * OW + col] = bias ? s + bias[oc] : s;
+        }
+}
+
+// CVT2D_GradInput (Engine/kernels.cu:1178-1212): dx = ... (assign).
+OEXPORT void orc_convT_dgrad(const float* dy, const float* w, float* dx, int N, int Cin, int H, int W, int Cout, int KH,
+                             int KW, int pad, int stride) {
+  const int OH = (H - 1) * stride - 2 * pad + KH, OW = (W - 1) * stride - 2 * pad + KW;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int ic = 0; ic < Cin; ++ic)
+      for (int row = 0; row < H; ++row)
+        for (int col = 0; col < W; ++col) {
+          double acc = 0.0;
+          for (int oc = 0; oc < Cout; ++oc)
+            for (int kh = 0; kh < KH; ++kh)
+              for (int kw = 0; kw < KW; ++kw) {
+                const int orow = row * stride - pad + kh, ocol = col * stride - pad + kw;
+                if (orow < 0 || orow >= OH || ocol < 0 || ocol >= OW) continue;
+                acc += (double)dy[(((long long)n * Cout + oc) * OH + orow) * OW + ocol] *
+                       (double)w[(((long long)oc * Cin + ic) * KH + kh) * KW + kw];
+              }
+          dx[(((long long)n * Cin + ic) * H + row) * W + col] = (float)acc;
+        }
+}
+
+// GVT2D (Engine/kernels.cu:1137-1176): dW = ... (assign).
+OEXPORT void orc_convT_wgrad(const float* x, const float* dy, float* dw, int N, int Cin, int H, int W, int Cout, int KH,
+                             int KW, int pad, int stride) {
+  const int OH = (H - 1) * stride - 2 * pad + KH, OW = (W - 1) * stride - 2 * pad + KW;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int oc = 0; oc < Cout; ++oc)
+    for (int ic = 0; ic < Cin; ++ic)
+      for (int kh = 0; kh < KH; ++kh)
+        for (int kw = 0; kw < KW; ++kw) {
+          double acc = 0.0;
+          for (int n = 0; n < N; ++n)
+            for (int ir = 0; ir < H; ++ir)
+              for (int icl = 0; icl < W; ++icl) {
+                const int orow = ir * stride - pad + kh, ocol = icl * stride - pad + kw;
+                if (orow < 0 || orow >= OH || ocol < 0 || ocol >= OW) continue;
+                acc += (double)x[(((long long)n * Cin + ic) * H + ir) * W + icl] *
+                       (double)dy[(((long long)n * Cout + oc) * OH + orow) * OW + ocol];
+              }
+          dw[(((long long)oc * Cin + ic) * KH + kh) * KW + kw] = (float)acc;
+        }
+}

@@ -49,6 +49,15 @@ SIGS = {
     "orc_scatter_add": (None, [P, P, P, I, I, I, I, I, F]),
     "orc_onehot": (None, [P, P, I, I, I, I]),
     "orc_argmax": (None, [P, I, I, P]),
+    "orc_rmsnorm_fwd": (None, [P, P, P, I, I, I, I]),
+    "orc_rmsnorm_bwd": (None, [P, P, P, P, I, I, I, I]),
+    "orc_batchnorm_fwd": (None, [P, P, P, I, I, LL, F]),
+    "orc_batchnorm_bwd": (None, [P, P, P, P, I, I, LL, F]),
+    "orc_copy_crop_fwd": (None, [P, P, P, I, I, I, I, I, I, I]),
+    "orc_copy_crop_bwd": (None, [P, P, P, I, I, I, I, I, I, I]),
+    "orc_convT_fwd": (None, [P, P, P, P, I, I, I, I, I, I, I, I, I]),
+    "orc_convT_dgrad": (None, [P, P, P, I, I, I, I, I, I, I, I, I]),
+    "orc_convT_wgrad": (None, [P, P, P, I, I, I, I, I, I, I, I, I]),
     "orc_c1_step": (F, [I, I, I, I, P, P, PP, PP, PP, PP, F, I, I, P]),
     "orc_c4_step": (F, [I, I, I, I, I, I, P, P, PP, PP, PP, PP, F, I, I]),
     "orc_c5_step": (F, [I, I, I, I, I, I, I, I, P, P, PP, PP, PP, PP, F, I, I]),

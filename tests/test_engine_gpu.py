@@ -269,3 +269,75 @@ def test_lazy_zero_matches_eager(hip, kind):
             assert np.array_equal(u, v), f"{kind}: phase {phase} tensor {i} differs between lazy and eager clearing"
     # the second backward without zero_grad really accumulated
     assert not np.array_equal(lazy[0][-1], lazy[1][-1])
+
+
+def unet_up_oracle(orc, x, skip, target, W, b, k, stride, pad):
+    """Oracle composition of the harness's U-Net decoder step: forward chain,
+    MSE loss, backward chain; returns (loss, dW, db)."""
+    N, Cin, H, Wd = x.shape
+    Cout = W.shape[0]
+    Cs, Hs, Ws = skip.shape[1:]
+    Ho, Wo = (H - 1) * stride - 2 * pad + k, (Wd - 1) * stride - 2 * pad + k
+    C = Cs + Cout
+    P = orc.ptr
+    up = np.zeros((N, Cout, Ho, Wo), np.float32)
+    orc.call("orc_convT_fwd", P(x), P(W), P(b), P(up), N, Cin, H, Wd, Cout, k, k, pad, stride)
+    cat = np.zeros((N, C, Ho, Wo), np.float32)
+    orc.call("orc_copy_crop_fwd", P(skip), P(up), P(cat), N, Cs, Hs, Ws, Cout, Ho, Wo)
+    bn, st_bn = np.zeros_like(cat), np.zeros(2 * C, np.float32)
+    orc.call("orc_batchnorm_fwd", P(cat), P(bn), P(st_bn), N, C, Ho * Wo, 1e-5)
+    r0, n0 = np.zeros_like(cat), np.zeros(N * C * Ho, np.float32)
+    orc.call("orc_rmsnorm_fwd", P(bn), P(r0), P(n0), N * C, Ho, Wo, 0)
+    inn, st_in = np.zeros_like(cat), np.zeros(2 * N * C, np.float32)
+    orc.call("orc_norm_fwd", P(r0), P(inn), P(st_in), N, C, Ho * Wo, C, 1e-5)
+    r1, n1 = np.zeros_like(cat), np.zeros(N * C * Wo, np.float32)
+    orc.call("orc_rmsnorm_fwd", P(inn), P(r1), P(n1), N * C, Ho, Wo, 1)
+    loss = orc.call("orc_mse_loss", P(r1), P(target), r1.size)
+    d = np.zeros_like(cat)
+    orc.call("orc_mse_bwd", P(r1), P(target), None, P(d), d.size)
+    d_inn = np.zeros_like(cat)
+    orc.call("orc_rmsnorm_bwd", P(r1), P(d), P(n1), P(d_inn), N * C, Ho, Wo, 1)
+    d_r0 = np.zeros_like(cat)
+    orc.call("orc_norm_bwd", P(inn), P(d_inn), P(d_r0), P(st_in), N, C, Ho * Wo, C, 1e-5, 1)
+    d_bn = np.zeros_like(cat)
+    orc.call("orc_rmsnorm_bwd", P(r0), P(d_r0), P(n0), P(d_bn), N * C, Ho, Wo, 0)
+    d_cat = np.zeros_like(cat)
+    orc.call("orc_batchnorm_bwd", P(bn), P(d_bn), P(d_cat), P(st_bn), N, C, Ho * Wo, 1e-5)
+    d_skip, d_up = np.zeros_like(skip), np.zeros_like(up)
+    orc.call("orc_copy_crop_bwd", P(d_cat), P(d_skip), P(d_up), N, Cs, Hs, Ws, Cout, Ho, Wo)
+    dW = np.zeros_like(W)
+    orc.call("orc_convT_wgrad", P(x), P(d_up), P(dW), N, Cin, H, Wd, Cout, k, k, pad, stride)
+    db = d_up.astype(np.float64).sum(axis=(0, 2, 3))
+    return loss, dW, db, np.abs(d_up).max() * d_up[:, 0].size
+
+
+@pytest.mark.parametrize("N,Cin,Cout,H,Cs,Hs,k,stride,pad", [(2, 8, 6, 8, 4, 20, 2, 2, 0), (2, 5, 3, 9, 2, 9, 3, 1, 1),
+                                                            (4, 32, 16, 16, 16, 36, 4, 2, 1)])
+def test_unet_up_step(hip, orc, N, Cin, Cout, H, Cs, Hs, k, stride, pad):
+    """Convolute2DT, CopyCrop, BatchNorm, RMSNorm (both axes) and InstanceNorm
+    composed through the C++ API: loss, weight and bias gradients against the
+    oracle composition, then the AdamW update."""
+    r = np.random.default_rng(N * 100 + Cin + k)
+    Ho = (H - 1) * stride - 2 * pad + k
+    x = r.standard_normal((N, Cin, H, H), dtype=np.float32)
+    skip = r.standard_normal((N, Cs, Hs, Hs), dtype=np.float32)
+    target = r.standard_normal((N, Cs + Cout, Ho, Ho), dtype=np.float32)
+    W = (r.standard_normal((Cout, Cin, k, k)) * 0.2).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    m = Model("unet_up", [N, Cin, Cout, H, H, Cs, Hs, Hs, k, stride, pad])
+    m.set(0, W)
+    m.set(1, b)
+    m.input(0, x)
+    m.input(1, skip)
+    m.input(2, target)
+    lr = 1e-3
+    m.step(lr, STEP_ALL)
+    m.sync()
+    loss, dW, db, db_scale = unet_up_oracle(orc, x, skip, target, W, b, k, stride, pad)
+    assert abs(m.loss - loss) <= 1e-5 * abs(loss), (m.loss, loss)
+    assert_close(m.get(0, 1), dW.reshape(-1), what="convT weight grad", **GRAD)
+    # the bias gradient is a sum of terms that nearly cancel (BatchNorm removes
+    # the channel mean): scale its floor by the size of the summed terms
+    assert_close(m.get(1, 1), db, what="convT bias grad", rtol=1e-4, atol_scale=1e-4, scale=db_scale)
+    check_update(orc, m, [W, b], lr, 1, True, "unet_up")
+    m.close()

@@ -284,6 +284,135 @@ def test_norm(hip, orc, batch, channels, hw, groups):
     assert_close(gdx.numpy(), dxz, what="norm bwd assign", **EW)
 
 
+@pytest.mark.parametrize("batch,channels,hw", [(4, 3, 25), (16, 128, 64 * 64), (3, 5, 4099), (1, 1, 9000)])
+def test_batchnorm(hip, orc, batch, channels, hw):
+    r = rng(batch * 3 + channels + hw)
+    shape = (batch, channels, hw)
+    x = (r.standard_normal(shape, dtype=np.float32) * 1.5 - 0.3).astype(np.float32)
+    dy = r.standard_normal(shape, dtype=np.float32)
+    dx0 = r.standard_normal(shape, dtype=np.float32)
+    yr, st = np.zeros_like(x), np.zeros(2 * channels, np.float32)
+    orc.call("orc_batchnorm_fwd", orc.ptr(x), orc.ptr(yr), orc.ptr(st), batch, channels, hw, 1e-5)
+    dxr = dx0.copy()
+    orc.call("orc_batchnorm_bwd", orc.ptr(yr), orc.ptr(dy), orc.ptr(dxr), orc.ptr(st), batch, channels, hw, 1e-5)
+    ws = hip.Buffer(hip.lib().mle_batchnorm_ws_bytes(batch, channels, hw))
+    gx, gy, gst = B(hip, x), hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * channels)
+    hip.call("mle_batchnorm_fwd", None, gx.ptr, gy.ptr, gst.ptr, batch, channels, hw, 1e-5, ws.ptr, ws.nbytes)
+    assert_close(gy.numpy(), yr, what="batchnorm fwd", **EW)
+    assert_close(gst.numpy(), st, what="batchnorm stats", **EW)
+    gyr, gdy, gdx, gstr = B(hip, yr), B(hip, dy), B(hip, dx0), B(hip, st)
+    hip.call("mle_batchnorm_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, gstr.ptr, batch, channels, hw, 1e-5, ws.ptr,
+             ws.nbytes, 1)
+    assert_close(gdx.numpy(), dxr, what="batchnorm bwd", **EW)
+    dxz = np.zeros_like(x)
+    orc.call("orc_batchnorm_bwd", orc.ptr(yr), orc.ptr(dy), orc.ptr(dxz), orc.ptr(st), batch, channels, hw, 1e-5)
+    hip.call("mle_fill", None, gdx.ptr, float("nan"), x.size)
+    hip.call("mle_batchnorm_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, gstr.ptr, batch, channels, hw, 1e-5, ws.ptr,
+             ws.nbytes, 0)
+    assert_close(gdx.numpy(), dxz, what="batchnorm bwd assign", **EW)
+
+
+@pytest.mark.parametrize("bc,rows,cols", [(3, 7, 9), (4, 64, 1000), (2, 300, 33), (16, 64, 64)])
+@pytest.mark.parametrize("type_", [0, 1])
+def test_rmsnorm(hip, orc, bc, rows, cols, type_):
+    r = rng(bc + rows * 3 + cols + type_)
+    shape = (bc, rows, cols)
+    x = r.standard_normal(shape, dtype=np.float32)
+    dy = r.standard_normal(shape, dtype=np.float32)
+    dx0 = r.standard_normal(shape, dtype=np.float32)
+    nl = bc * (rows if type_ == 0 else cols)
+    yr, nr = np.zeros_like(x), np.zeros(nl, np.float32)
+    orc.call("orc_rmsnorm_fwd", orc.ptr(x), orc.ptr(yr), orc.ptr(nr), bc, rows, cols, type_)
+    dxr = dx0.copy()
+    orc.call("orc_rmsnorm_bwd", orc.ptr(yr), orc.ptr(dy), orc.ptr(nr), orc.ptr(dxr), bc, rows, cols, type_)
+    gx, gy, gn = B(hip, x), hip.Buffer.zeros(shape), hip.Buffer.zeros(nl)
+    hip.call("mle_rmsnorm_fwd", None, gx.ptr, gy.ptr, gn.ptr, bc, rows, cols, type_)
+    assert_close(gy.numpy(), yr, what="rmsnorm fwd", **EW)
+    assert_close(gn.numpy(), nr, what="rmsnorm norms", **EW)
+    gyr, gdy, gnr, gdx = B(hip, yr), B(hip, dy), B(hip, nr), B(hip, dx0)
+    hip.call("mle_rmsnorm_bwd", None, gyr.ptr, gdy.ptr, gnr.ptr, gdx.ptr, bc, rows, cols, type_, 1)
+    assert_close(gdx.numpy(), dxr, what="rmsnorm bwd", **EW)
+    dxz = np.zeros_like(x)
+    orc.call("orc_rmsnorm_bwd", orc.ptr(yr), orc.ptr(dy), orc.ptr(nr), orc.ptr(dxz), bc, rows, cols, type_)
+    hip.call("mle_fill", None, gdx.ptr, float("nan"), x.size)
+    hip.call("mle_rmsnorm_bwd", None, gyr.ptr, gdy.ptr, gnr.ptr, gdx.ptr, bc, rows, cols, type_, 0)
+    assert_close(gdx.numpy(), dxz, what="rmsnorm bwd assign", **EW)
+
+
+@pytest.mark.parametrize("batch,c1,h1,w1,c2,h,w", [(2, 3, 8, 10, 2, 5, 6), (2, 4, 6, 6, 5, 6, 6),
+                                                   (1, 64, 68, 68, 64, 56, 56), (3, 1, 9, 7, 2, 4, 3)])
+def test_copy_crop(hip, orc, batch, c1, h1, w1, c2, h, w):
+    """Pure data movement: bit-exact against the oracle, both accumulate modes."""
+    r = rng(batch + c1 + h1 + w1 + c2)
+    x1 = r.standard_normal((batch, c1, h1, w1), dtype=np.float32)
+    x2 = r.standard_normal((batch, c2, h, w), dtype=np.float32)
+    yr = np.zeros((batch, c1 + c2, h, w), np.float32)
+    orc.call("orc_copy_crop_fwd", orc.ptr(x1), orc.ptr(x2), orc.ptr(yr), batch, c1, h1, w1, c2, h, w)
+    g1, g2, gy = B(hip, x1), B(hip, x2), hip.Buffer.zeros(yr.shape)
+    hip.call("mle_copy_crop_fwd", None, g1.ptr, g2.ptr, gy.ptr, batch, c1, h1, w1, c2, h, w)
+    np.testing.assert_array_equal(gy.numpy(), yr)
+    dy = r.standard_normal(yr.shape, dtype=np.float32)
+    d1, d2 = r.standard_normal(x1.shape, dtype=np.float32), r.standard_normal(x2.shape, dtype=np.float32)
+    r1, r2 = d1.copy(), d2.copy()
+    orc.call("orc_copy_crop_bwd", orc.ptr(dy), orc.ptr(r1), orc.ptr(r2), batch, c1, h1, w1, c2, h, w)
+    gdy, gd1, gd2 = B(hip, dy), B(hip, d1), B(hip, d2)
+    hip.call("mle_copy_crop_bwd", None, gdy.ptr, gd1.ptr, gd2.ptr, batch, c1, h1, w1, c2, h, w, 1, 1)
+    np.testing.assert_array_equal(gd1.numpy(), r1)
+    np.testing.assert_array_equal(gd2.numpy(), r2)
+    z1, z2 = np.zeros_like(x1), np.zeros_like(x2)
+    orc.call("orc_copy_crop_bwd", orc.ptr(dy), orc.ptr(z1), orc.ptr(z2), batch, c1, h1, w1, c2, h, w)
+    hip.call("mle_fill", None, gd1.ptr, float("nan"), x1.size)
+    hip.call("mle_fill", None, gd2.ptr, float("nan"), x2.size)
+    hip.call("mle_copy_crop_bwd", None, gdy.ptr, gd1.ptr, gd2.ptr, batch, c1, h1, w1, c2, h, w, 0, 0)
+    np.testing.assert_array_equal(gd1.numpy(), z1)
+    np.testing.assert_array_equal(gd2.numpy(), z2)
+
+
+def test_copy_crop_rejects_padding_direction(hip):
+    g = hip.Buffer.zeros(64)
+    with pytest.raises(hip.MLEError):
+        hip.call("mle_copy_crop_fwd", None, g.ptr, g.ptr, g.ptr, 1, 1, 3, 3, 1, 4, 4)
+
+
+@pytest.mark.parametrize("n,cin,h,w,cout,k,pad,stride", [(2, 3, 5, 4, 4, 2, 0, 2), (2, 8, 7, 7, 6, 3, 1, 1),
+                                                        (1, 4, 6, 5, 3, 3, 1, 2), (2, 16, 16, 16, 8, 4, 1, 2),
+                                                        (4, 128, 32, 32, 64, 2, 0, 2)])
+def test_conv_transpose_composition(hip, orc, n, cin, h, w, cout, k, pad, stride):
+    """Convolute2DT's kernels: swapped weights + convolution dgrad (forward),
+    forward (input gradient) and wgrad (weight gradient), against the oracle's
+    restatement of CVT2D / CVT2D_GradInput / GVT2D."""
+    r = rng(n + cin * 3 + h + cout + k + stride)
+    oh, ow = (h - 1) * stride - 2 * pad + k, (w - 1) * stride - 2 * pad + k
+    x = r.standard_normal((n, cin, h, w), dtype=np.float32)
+    wt = r.standard_normal((cout, cin, k, k), dtype=np.float32)
+    b = r.standard_normal(cout, dtype=np.float32)
+    dy = r.standard_normal((n, cout, oh, ow), dtype=np.float32)
+    yr = np.zeros((n, cout, oh, ow), np.float32)
+    orc.call("orc_convT_fwd", orc.ptr(x), orc.ptr(wt), orc.ptr(b), orc.ptr(yr), n, cin, h, w, cout, k, k, pad, stride)
+    dxr, dwr = np.zeros_like(x), np.zeros_like(wt)
+    orc.call("orc_convT_dgrad", orc.ptr(dy), orc.ptr(wt), orc.ptr(dxr), n, cin, h, w, cout, k, k, pad, stride)
+    orc.call("orc_convT_wgrad", orc.ptr(x), orc.ptr(dy), orc.ptr(dwr), n, cin, h, w, cout, k, k, pad, stride)
+    gx, gw, gb, gdy = B(hip, x), B(hip, wt), B(hip, b), B(hip, dy)
+    gsw, gy = hip.Buffer.zeros((cin, cout, k, k)), hip.Buffer.zeros(yr.shape)
+    hip.call("mle_weight_swap", None, gw.ptr, gsw.ptr, cout, cin, k * k, 0)
+    np.testing.assert_array_equal(gsw.numpy(), wt.transpose(1, 0, 2, 3))
+    hip.call("mle_fill", None, gy.ptr, float("nan"), yr.size)
+    hip.call("mle_conv2d_dgrad", None, gx.ptr, gsw.ptr, gy.ptr, n, cout, oh, ow, cin, k, k, pad, stride, 0)
+    hip.call("mle_broadcast_channel_add", None, gy.ptr, gb.ptr, gy.ptr, n, cout, oh * ow)
+    assert_close(gy.numpy(), yr, what="convT fwd", **MM)
+    gdx = hip.Buffer.zeros(x.shape)
+    hip.call("mle_fill", None, gdx.ptr, float("nan"), x.size)
+    hip.call("mle_conv2d_fwd", None, gdy.ptr, gsw.ptr, None, gdx.ptr, n, cout, oh, ow, cin, k, k, pad, stride)
+    assert_close(gdx.numpy(), dxr, what="convT input gradient", **MM)
+    L = hip.lib()
+    ws = hip.Buffer(max(1, L.mle_conv2d_wgrad_ws_bytes(n, cout, oh, ow, cin, k, k, pad, stride)))
+    gdw_s, gdw = hip.Buffer.zeros((cin, cout, k, k)), hip.Buffer.zeros(wt.shape)
+    hip.call("mle_conv2d_wgrad", None, gdy.ptr, gx.ptr, gdw_s.ptr, n, cout, oh, ow, cin, k, k, pad, stride, ws.ptr,
+             ws.nbytes)
+    hip.call("mle_weight_swap", None, gdw_s.ptr, gdw.ptr, cin, cout, k * k, 0)
+    assert_close(gdw.numpy(), dwr, what="convT weight gradient", **MM)
+
+
 # ---------------------------------------------------------------------- conv
 @pytest.mark.parametrize("n,cin,h,w,cout,k,pad,stride", [
     (2, 3, 9, 9, 5, 3, 1, 1), (2, 4, 8, 10, 6, 1, 0, 1), (1, 3, 11, 11, 4, 3, 1, 2),

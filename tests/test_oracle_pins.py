@@ -194,6 +194,117 @@ def test_layernorm_reference_layout_writes_prefix_only(orc):
     assert np.all(flat[batch * hw:] == 0) and np.any(flat[: batch * hw] != 0)
 
 
+@pytest.mark.parametrize("type_", [0, 1])
+def test_rmsnorm_closed_forms(orc, type_):
+    """The reference's RMSNorm is an L2 normalisation along rows (type 0) or
+    columns (type 1): y = x / ||x||.  Pinned against the same map written with
+    torch autograd in float64, plus ||y|| = 1 and <dx, y> = 0 along the axis."""
+    r = rng(46 + type_)
+    bc, rows, cols = 3, 7, 9
+    x = r.standard_normal((bc, rows, cols)).astype(np.float32)
+    dy = r.standard_normal(x.shape).astype(np.float32)
+    nl = bc * (rows if type_ == 0 else cols)
+    y, norms = np.zeros_like(x), np.zeros(nl, np.float32)
+    orc.call("orc_rmsnorm_fwd", p(x), p(y), p(norms), bc, rows, cols, type_)
+    dx = np.full_like(x, 0.5)
+    orc.call("orc_rmsnorm_bwd", p(y), p(dy), p(norms), p(dx), bc, rows, cols, type_)
+    axis = 2 if type_ == 0 else 1
+    xt = torch.tensor(x, dtype=D64, requires_grad=True)
+    yt = xt / torch.sqrt((xt * xt).sum(axis, keepdim=True))
+    (g,) = torch.autograd.grad(yt, xt, torch.tensor(dy, dtype=D64))
+    assert_close(y, yt.detach().numpy(), rtol=1e-6, atol_scale=1e-6, what="rmsnorm fwd")
+    assert_close(dx, 0.5 + g.numpy(), rtol=1e-5, atol_scale=1e-6, what="rmsnorm bwd (accumulates)")
+    np.testing.assert_allclose(np.linalg.norm(y.astype(np.float64), axis=axis), 1.0, rtol=1e-6)
+    np.testing.assert_allclose(((dx - 0.5).astype(np.float64) * y).sum(axis), 0.0, atol=1e-5)
+    want_norms = np.sqrt((x.astype(np.float64) ** 2).sum(axis)).reshape(-1)
+    np.testing.assert_allclose(norms, want_norms, rtol=1e-6)
+
+
+@pytest.mark.parametrize("batch,channels,hw", [(4, 3, 25), (2, 5, 64), (1, 2, 7)])
+def test_batchnorm_vs_torch(orc, batch, channels, hw):
+    """BatchNorm in training mode (batch statistics, biased variance, eps 1e-5,
+    gamma 1, beta 0) against torch's batch_norm with autograd in float64."""
+    r = rng(47 + hw)
+    x = (r.standard_normal((batch, channels, hw)) * 1.5 - 0.5).astype(np.float32)
+    dy = r.standard_normal(x.shape).astype(np.float32)
+    y, st = np.zeros_like(x), np.zeros(2 * channels, np.float32)
+    orc.call("orc_batchnorm_fwd", p(x), p(y), p(st), batch, channels, hw, 1e-5)
+    dx = np.zeros_like(x)
+    orc.call("orc_batchnorm_bwd", p(y), p(dy), p(dx), p(st), batch, channels, hw, 1e-5)
+    xt = torch.tensor(x, dtype=D64, requires_grad=True)
+    yt = Fn.batch_norm(xt, None, None, training=True, eps=1e-5)
+    (g,) = torch.autograd.grad(yt, xt, torch.tensor(dy, dtype=D64))
+    assert_close(y, yt.detach().numpy(), rtol=1e-5, atol_scale=1e-6, what="batchnorm fwd")
+    assert_close(dx, g.numpy(), rtol=1e-4, atol_scale=1e-5, what="batchnorm bwd")
+    xc = x.transpose(1, 0, 2).reshape(channels, -1).astype(np.float64)
+    np.testing.assert_allclose(st[0::2], xc.mean(1), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(st[1::2], ((xc - xc.mean(1, keepdims=True)) ** 2).sum(1), rtol=1e-5)
+
+
+def test_instancenorm_is_groupnorm_per_channel(orc):
+    """InstanceNorm (InstanceMean/InstanceStd/INorm/InstanceBackward) is the
+    group normalisation with one group per channel: torch instance_norm."""
+    r = rng(48)
+    batch, channels, hw = 2, 3, 20
+    x = (r.standard_normal((batch, channels, hw)) + 0.3).astype(np.float32)
+    dy = r.standard_normal(x.shape).astype(np.float32)
+    y, st = np.zeros_like(x), np.zeros(2 * batch * channels, np.float32)
+    orc.call("orc_norm_fwd", p(x), p(y), p(st), batch, channels, hw, channels, 1e-5)
+    dx = np.zeros_like(x)
+    orc.call("orc_norm_bwd", p(y), p(dy), p(dx), p(st), batch, channels, hw, channels, 1e-5, 1)
+    xt = torch.tensor(x, dtype=D64, requires_grad=True)
+    yt = Fn.instance_norm(xt, eps=1e-5)
+    (g,) = torch.autograd.grad(yt, xt, torch.tensor(dy, dtype=D64))
+    assert_close(y, yt.detach().numpy(), rtol=1e-5, atol_scale=1e-6, what="instancenorm fwd")
+    assert_close(dx, g.numpy(), rtol=1e-4, atol_scale=1e-5, what="instancenorm bwd")
+
+
+@pytest.mark.parametrize("h1,w1", [(8, 10), (5, 6), (9, 6)])
+def test_copy_crop_matches_slicing(orc, h1, w1):
+    """Channel concatenation of x1's centred crop with x2 (numpy slicing), and
+    the backward adds each part of dy back into its source window."""
+    r = rng(49 + h1 + w1)
+    batch, c1, c2, h, w = 2, 3, 2, 5, 6
+    x1 = r.standard_normal((batch, c1, h1, w1)).astype(np.float32)
+    x2 = r.standard_normal((batch, c2, h, w)).astype(np.float32)
+    y = np.zeros((batch, c1 + c2, h, w), np.float32)
+    orc.call("orc_copy_crop_fwd", p(x1), p(x2), p(y), batch, c1, h1, w1, c2, h, w)
+    dr, dc = (h1 - h) // 2, (w1 - w) // 2
+    np.testing.assert_array_equal(y, np.concatenate([x1[:, :, dr:dr + h, dc:dc + w], x2], axis=1))
+    dy = r.standard_normal(y.shape).astype(np.float32)
+    dx1, dx2 = np.ones_like(x1), np.ones_like(x2)
+    orc.call("orc_copy_crop_bwd", p(dy), p(dx1), p(dx2), batch, c1, h1, w1, c2, h, w)
+    want1 = np.ones_like(x1)
+    want1[:, :, dr:dr + h, dc:dc + w] += dy[:, :c1]
+    np.testing.assert_array_equal(dx1, want1)
+    np.testing.assert_array_equal(dx2, 1 + dy[:, c1:])
+
+
+@pytest.mark.parametrize("k,pad,stride", [(2, 0, 2), (3, 1, 1), (3, 1, 2), (4, 1, 2)])
+def test_conv_transpose_vs_torch(orc, k, pad, stride):
+    """Convolute2DT with weights [out][inp][kh][kw]: torch conv_transpose2d
+    takes [inp][out][kh][kw], so the reference weight is passed transposed."""
+    r = rng(55 + k + stride)
+    n, cin, h, w, cout = 2, 3, 5, 4, 4
+    x = r.standard_normal((n, cin, h, w)).astype(np.float32)
+    wt = r.standard_normal((cout, cin, k, k)).astype(np.float32)
+    b = r.standard_normal(cout).astype(np.float32)
+    xt, wtt, bt = (torch.tensor(a, dtype=D64, requires_grad=True) for a in (x, wt, b))
+    yt = Fn.conv_transpose2d(xt, wtt.transpose(0, 1), bt, stride=stride, padding=pad)
+    assert yt.shape[2] == (h - 1) * stride - 2 * pad + k
+    dy = r.standard_normal(tuple(yt.shape)).astype(np.float32)
+    gx, gw = torch.autograd.grad(yt, (xt, wtt), torch.tensor(dy, dtype=D64))
+    y = np.zeros(tuple(yt.shape), np.float32)
+    orc.call("orc_convT_fwd", p(x), p(wt), p(b), p(y), n, cin, h, w, cout, k, k, pad, stride)
+    dx = np.full_like(x, 7.0)  # assigned, not accumulated
+    orc.call("orc_convT_dgrad", p(dy), p(wt), p(dx), n, cin, h, w, cout, k, k, pad, stride)
+    dw = np.full_like(wt, 7.0)
+    orc.call("orc_convT_wgrad", p(x), p(dy), p(dw), n, cin, h, w, cout, k, k, pad, stride)
+    assert_close(y, yt.detach().numpy(), rtol=1e-6, atol_scale=1e-6, what="convT fwd")
+    assert_close(dx, gx.numpy(), rtol=1e-6, atol_scale=1e-6, what="convT dgrad")
+    assert_close(dw, gw.numpy(), rtol=1e-6, atol_scale=1e-6, what="convT wgrad")
+
+
 # ----------------------------------------------------------------------- conv
 @pytest.mark.parametrize("k,pad,stride", [(3, 1, 1), (1, 0, 1), (3, 1, 2), (5, 2, 1)])
 def test_conv_vs_torch(orc, k, pad, stride):
