@@ -1058,6 +1058,144 @@ graph Embedding::forward(const int32_t* keys, int batch, int clen, int max_clen)
   return node;
 }
 
+namespace {
+constexpr uint32_t kTembMagic = 0x54454D42u;  // "TEMB"
+constexpr uint32_t kTembVersion = 1u;
+
+// Header and vocabulary of a TEMB file; false (after printing) on a bad file.
+bool temb_read_header(std::ifstream& f, const str& who, int dim, std::vector<std::pair<str, int>>& words) {
+  uint32_t magic = 0, version = 0;
+  f.read(reinterpret_cast<char*>(&magic), sizeof(magic));
+  f.read(reinterpret_cast<char*>(&version), sizeof(version));
+  if (!f || magic != kTembMagic) {
+    std::cerr << who << " -- bad magic number; not a TEMB file\n";
+    return false;
+  }
+  if (version != kTembVersion) {
+    std::cerr << who << " -- unsupported version " << version << "\n";
+    return false;
+  }
+  int saved_dim = 0, n = 0;
+  f.read(reinterpret_cast<char*>(&saved_dim), sizeof(saved_dim));
+  f.read(reinterpret_cast<char*>(&n), sizeof(n));
+  if (!f || n < 0) {
+    std::cerr << who << " -- read error in the header\n";
+    return false;
+  }
+  if (saved_dim != dim) {
+    std::cerr << who << " -- embed_dim mismatch: file=" << saved_dim << " object=" << dim << "\n";
+    return false;
+  }
+  words.clear();
+  words.reserve(n);
+  for (int i = 0; i < n; ++i) {
+    uint32_t wlen = 0;
+    f.read(reinterpret_cast<char*>(&wlen), sizeof(wlen));
+    str w(wlen, '\0');
+    if (wlen) f.read(&w[0], wlen);
+    int idx = 0;
+    f.read(reinterpret_cast<char*>(&idx), sizeof(idx));
+    if (!f) {
+      std::cerr << who << " -- read error in the vocabulary\n";
+      return false;
+    }
+    words.emplace_back(std::move(w), idx);
+  }
+  return true;
+}
+}  // namespace
+
+void Embedding::save(const str& filepath, const std::unordered_map<str, int>& words) const {
+  std::ofstream f(filepath, std::ios::binary);
+  if (!f.is_open()) {
+    std::cerr << "TextualEmbedding::save -- could not open '" << filepath << "' for writing\n";
+    return;
+  }
+  const int n = (int)words.size();
+  if (n > vocab) {
+    std::cerr << "TextualEmbedding::save -- " << n << " words for a table of " << vocab << " rows\n";
+    return;
+  }
+  f.write(reinterpret_cast<const char*>(&kTembMagic), sizeof(kTembMagic));
+  f.write(reinterpret_cast<const char*>(&kTembVersion), sizeof(kTembVersion));
+  f.write(reinterpret_cast<const char*>(&dim), sizeof(dim));
+  f.write(reinterpret_cast<const char*>(&n), sizeof(n));
+  for (const auto& [word, idx] : words) {
+    const uint32_t wlen = (uint32_t)word.size();
+    f.write(reinterpret_cast<const char*>(&wlen), sizeof(wlen));
+    f.write(word.data(), wlen);
+    f.write(reinterpret_cast<const char*>(&idx), sizeof(idx));
+  }
+  // Rows 0 .. n-1 of the table, one device-to-host copy.
+  std::vector<float> host((size_t)n * dim);
+  if (n) check(mle_memcpy_d2h(host.data(), E.output, host.size() * sizeof(float), mle::stream()), "TEMB save");
+  f.write(reinterpret_cast<const char*>(host.data()), (std::streamsize)(host.size() * sizeof(float)));
+  if (!f.good()) std::cerr << "TextualEmbedding::save -- write error on '" << filepath << "'\n";
+}
+
+int Embedding::load(const str& filepath, std::unordered_map<str, int>& words) {
+  const str who = "TextualEmbedding::load";
+  std::ifstream f(filepath, std::ios::binary);
+  if (!f.is_open()) {
+    std::cerr << who << " -- could not open '" << filepath << "'\n";
+    return -1;
+  }
+  std::vector<std::pair<str, int>> saved;
+  if (!temb_read_header(f, who, dim, saved)) return -1;
+  const int n = (int)saved.size();
+  if (n > vocab) {
+    std::cerr << who << " -- saved vocab (" << n << ") exceeds MAX_VOCAB_SIZE (" << vocab << ")\n";
+    return -1;
+  }
+  std::vector<float> host((size_t)n * dim);
+  f.read(reinterpret_cast<char*>(host.data()), (std::streamsize)(host.size() * sizeof(float)));
+  if (!f.good()) {
+    std::cerr << who << " -- read error on '" << filepath << "'\n";
+    return -1;
+  }
+  words.clear();
+  for (auto& [w, idx] : saved) words[w] = idx;
+  if (n) check(mle_memcpy_h2d(E.output, host.data(), host.size() * sizeof(float), mle::stream()), "TEMB load");
+  return n;
+}
+
+int Embedding::load_replace(const str& filepath, const std::unordered_map<str, int>& words) {
+  const str who = "TextualEmbedding::load_replace";
+  std::ifstream f(filepath, std::ios::binary);
+  if (!f.is_open()) {
+    std::cerr << who << " -- could not open '" << filepath << "'\n";
+    return -1;
+  }
+  std::vector<std::pair<str, int>> saved;
+  if (!temb_read_header(f, who, dim, saved)) return -1;
+  // (local row, saved row) for the words both vocabularies hold, in file-row order.
+  std::vector<std::pair<int, int>> match;
+  for (const auto& [w, sidx] : saved) {
+    auto it = words.find(w);
+    if (it != words.end() && it->second >= 0 && it->second < vocab) match.emplace_back(it->second, sidx);
+  }
+  if (match.empty()) return 0;
+  std::sort(match.begin(), match.end(), [](const auto& a, const auto& b) { return a.second < b.second; });
+  std::vector<float> row(dim);
+  size_t cur = 0;
+  int replaced = 0;
+  for (int s = 0; s < (int)saved.size() && cur < match.size(); ++s) {
+    f.read(reinterpret_cast<char*>(row.data()), (std::streamsize)(dim * sizeof(float)));
+    if (!f.good()) {
+      std::cerr << who << " -- read error at embedding row " << s << "\n";
+      return replaced;
+    }
+    while (cur < match.size() && match[cur].second == s) {
+      check(mle_memcpy_h2d(E.output + (size_t)match[cur].first * dim, row.data(), dim * sizeof(float), mle::stream()),
+            "TEMB load_replace");
+      ++replaced;
+      ++cur;
+    }
+    while (cur < match.size() && match[cur].second < s) ++cur;  // saved row index outside the file
+  }
+  return replaced;
+}
+
 void Embedding::UpdateSGD(const graph& X, float lr) {
   check(mle_embed_scatter_add(mle::stream(), E.output, X->grad, keys_, batch_, clen_, max_clen_, dim, vocab, -lr, ws_,
                               ws_bytes_),

@@ -21,6 +21,7 @@
 #include <iostream>
 #include <memory>
 #include <string>
+#include <unordered_map>
 #include <unordered_set>
 #include <vector>
 
@@ -311,8 +312,20 @@ class Embedding {
   Embedding(int vocab, int dim, const str name = "Embedding");
   graph forward(const int32_t* keys, int batch, int clen, int max_clen);
   void UpdateSGD(const graph& X, float lr = LEARNING_RATE);
+  // AdamParameter checkpoint record of the table (with its Adam moments).
   void save(std::ofstream& f) const;
   void load(std::ifstream& f);
+  // TEMB files (TextualEmbedding::save / load / load_replace,
+  // Engine/transformer.cu:246-484): [u32 magic "TEMB"][u32 version 1]
+  // [i32 dim][i32 n] then n x ([u32 len][word][i32 row]) then rows 0..n-1 of
+  // the table.  `vocab` is the tokenizer's word -> row map (the reference's
+  // WordSpace).  Errors are printed and the call returns, as the reference's do.
+  // load: replaces `vocab` and table rows 0..n-1; returns n, or -1.
+  // load_replace: copies each saved row whose word is in `vocab` to that
+  // word's row; returns how many rows were replaced, or -1.
+  void save(const str& filepath, const std::unordered_map<str, int>& vocab) const;
+  int load(const str& filepath, std::unordered_map<str, int>& vocab);
+  int load_replace(const str& filepath, const std::unordered_map<str, int>& vocab);
 
  private:
   const int32_t* keys_ = nullptr;

@@ -5,6 +5,9 @@
 // ParameterUpdate) and adds host access to parameters and gradients.
 #include <string.h>
 
+#include <fstream>
+#include <unordered_map>
+
 #include <memory>
 #include <string>
 #include <vector>
@@ -244,5 +247,47 @@ void* mle_model_stream(void* h) {
 }
 
 int mle_model_num_nodes(void* h) { return (int)static_cast<Model*>(h)->go.nodes.size(); }
+
+// Checkpoints: every parameter's AdamParameter record, in the model's
+// parameter order (the modules' save order, e.g. Linear: W1 then B1).
+int mle_model_save(void* h, const char* path) {
+  auto* m = static_cast<Model*>(h);
+  std::ofstream f(path, std::ios::binary);
+  if (!f.is_open()) return MLE_ERR_INVALID;
+  for (AdamParameter* p : m->params) p->save(f);
+  return f.good() ? MLE_OK : MLE_ERR_INVALID;
+}
+
+int mle_model_load(void* h, const char* path) {
+  auto* m = static_cast<Model*>(h);
+  std::ifstream f(path, std::ios::binary);
+  if (!f.is_open()) return MLE_ERR_INVALID;
+  for (AdamParameter* p : m->params) p->load(f);
+  return MLE_OK;
+}
+
+namespace {
+std::unordered_map<str, int> vocab_of(const char* const* words, int n) {
+  std::unordered_map<str, int> v;
+  for (int i = 0; i < n; ++i)
+    if (words[i]) v[words[i]] = i;
+  return v;
+}
+}  // namespace
+
+int mle_model_temb_save(void* h, const char* path, const char* const* words, int n) {
+  auto* m = static_cast<Model*>(h);
+  if (!m->emb) return MLE_ERR_INVALID;
+  m->emb->save(str(path), vocab_of(words, n));
+  return MLE_OK;
+}
+
+int mle_model_temb_load(void* h, const char* path, int replace, const char* const* words, int n) {
+  auto* m = static_cast<Model*>(h);
+  if (!m->emb) return MLE_ERR_INVALID;
+  if (replace) return m->emb->load_replace(str(path), vocab_of(words, n));
+  std::unordered_map<str, int> v;
+  return m->emb->load(str(path), v);
+}
 
 }  // extern "C"

@@ -38,6 +38,14 @@ float mle_model_loss(void* h);
 int mle_model_sync(void* h);
 void* mle_model_stream(void* h);
 int mle_model_num_nodes(void* h);
+/* Checkpoint of every parameter (AdamParameter::save records, parameter order). */
+int mle_model_save(void* h, const char* path);
+int mle_model_load(void* h, const char* path);
+/* TEMB file of the block model's embedding table; words[i] is the word of row
+ * i (NULL skips).  load: replace = 0 full load (returns the saved vocabulary
+ * size), 1 load_replace (returns the rows replaced); -1 on a bad file. */
+int mle_model_temb_save(void* h, const char* path, const char* const* words, int n);
+int mle_model_temb_load(void* h, const char* path, int replace, const char* const* words, int n);
 
 #ifdef __cplusplus
 }

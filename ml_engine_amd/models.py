@@ -32,6 +32,10 @@ _SIGS = {
     "mle_model_sync": (I, [P]),
     "mle_model_stream": (P, [P]),
     "mle_model_num_nodes": (I, [P]),
+    "mle_model_save": (I, [P, C.c_char_p]),
+    "mle_model_load": (I, [P, C.c_char_p]),
+    "mle_model_temb_save": (I, [P, C.c_char_p, C.POINTER(C.c_char_p), I]),
+    "mle_model_temb_load": (I, [P, C.c_char_p, I, C.POINTER(C.c_char_p), I]),
 }
 
 _lib = None
@@ -102,6 +106,25 @@ class Model:
 
     def t(self, i: int) -> int:
         return int(lib().mle_model_param_t(self.h, i))
+
+    def save(self, path: str) -> None:
+        hip.check(lib().mle_model_save(self.h, str(path).encode()))
+
+    def load(self, path: str) -> None:
+        hip.check(lib().mle_model_load(self.h, str(path).encode()))
+
+    @staticmethod
+    def _words(words):
+        arr = (C.c_char_p * len(words))(*[None if w is None else w.encode() for w in words])
+        return arr, len(words)
+
+    def temb_save(self, path: str, words) -> None:
+        arr, n = self._words(words)
+        hip.check(lib().mle_model_temb_save(self.h, str(path).encode(), arr, n))
+
+    def temb_load(self, path: str, replace: bool = False, words=()) -> int:
+        arr, n = self._words(list(words))
+        return int(lib().mle_model_temb_load(self.h, str(path).encode(), int(replace), arr, n))
 
     def close(self) -> None:
         if getattr(self, "h", None):
