@@ -50,6 +50,11 @@ GEMM_CASES = [
     (1, 0, 2098, 2060, 48, 1),
     (1, 1, 2060, 2100, 16, 1),
     (0, 1, 1000, 1000, 96, 2),
+    # K a multiple of 64 (deepest stage shapes), ragged M and N
+    (0, 0, 2100, 2052, 128, 1),
+    (0, 1, 1990, 2100, 192, 1),
+    (1, 0, 2098, 2060, 256, 1),
+    (1, 1, 2060, 2004, 64, 1),
     # N not a multiple of 4 with float4-able operands: not the direct kernel
     (0, 1, 2000, 1702, 48, 1),
 ]
