@@ -143,53 +143,69 @@ __global__ __launch_bounds__(NT) void segment_add_kernel(float* __restrict__ tab
   }
 }
 
-// Row-centric scatter-add: one wave per table row scans every token's key (a
-// chunk at a time, staged in LDS) and sums the matching gradient rows in token
-// order.  No sort and no atomics; used when vocab * tokens is moderate.
+// Row-centric scatter-add: each wave owns R consecutive table rows and scans
+// every token's key (a chunk at a time, staged in LDS), summing the matching
+// gradient rows in token order.  No sort and no atomics; used when
+// vocab * tokens is moderate.  Lane l holds dims l + 64 j of each of its rows.
 constexpr int ROW_CHUNK = 2048;
-constexpr int ROW_DMAX = 16;  // dims per lane -> dim <= 1024
+template <int DMAX, int R>
 __global__ __launch_bounds__(256) void row_scatter_kernel(float* __restrict__ table, const float* __restrict__ grad,
                                                           const int32_t* __restrict__ keys, int clen, int max_clen,
                                                           int ntok, int dim, int vocab, float scale) {
   __shared__ int sk[ROW_CHUNK];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int v = blockIdx.x * 4 + wave;
-  float acc[ROW_DMAX];
+  const int v0 = (blockIdx.x * 4 + wave) * R;  // this wave's rows v0 .. v0 + R - 1
+  float acc[R][DMAX];
 #pragma unroll
-  for (int j = 0; j < ROW_DMAX; ++j) acc[j] = 0.f;
-  bool hit = false;
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < DMAX; ++j) acc[r][j] = 0.f;
+  unsigned hit = 0;
   for (int t0 = 0; t0 < ntok; t0 += ROW_CHUNK) {
     const int cnt = min(ROW_CHUNK, ntok - t0);
     __syncthreads();
-    for (int i = threadIdx.x; i < cnt; i += 256) {
-      const int t = t0 + i;
-      sk[i] = keys[(size_t)(t / clen) * max_clen + (t % clen)];
+    if (clen == max_clen) {  // dense ids: token t at keys[t]
+      for (int i = threadIdx.x; i < cnt; i += 256) sk[i] = keys[t0 + i];
+    } else {
+      for (int i = threadIdx.x; i < cnt; i += 256) {
+        const int t = t0 + i;
+        sk[i] = keys[(size_t)(t / clen) * max_clen + (t % clen)];
+      }
     }
     __syncthreads();
-    if (v >= vocab) continue;
+    if (v0 >= vocab) continue;
     for (int c = 0; c < cnt; c += 64) {
       const int i = c + lane;
-      const bool m = (i < cnt) && sk[i] == v;
-      unsigned long long mask = __ballot(m);
-      while (mask) {
+      const unsigned rel = (i < cnt) ? (unsigned)(sk[i] - v0) : 0xffffffffu;
+      unsigned long long mask = __ballot(rel < (unsigned)R);
+      while (mask) {  // tokens in order; the row is uniform across the wave
         const int bit = __ffsll((long long)mask) - 1;
         mask &= mask - 1;
+        const int row = __shfl(sk[c + bit] - v0, 0, 64);
         const float* gr = grad + (size_t)(t0 + c + bit) * dim;
-        hit = true;
+        hit |= 1u << row;
 #pragma unroll
-        for (int j = 0; j < ROW_DMAX; ++j) {
-          const int d = lane + 64 * j;
-          if (d < dim) acc[j] += gr[d];
+        for (int r = 0; r < R; ++r) {
+          if (r != row) continue;
+#pragma unroll
+          for (int j = 0; j < DMAX; ++j) {
+            const int d = lane + 64 * j;
+            if (d < dim) acc[r][j] += gr[d];
+          }
         }
       }
     }
   }
-  if (v >= vocab || !hit) return;
-  float* tr = table + (size_t)v * dim;
 #pragma unroll
-  for (int j = 0; j < ROW_DMAX; ++j) {
-    const int d = lane + 64 * j;
-    if (d < dim) tr[d] += scale * acc[j];
+  for (int r = 0; r < R; ++r) {
+    const int v = v0 + r;
+    if (v >= vocab || !(hit & (1u << r))) continue;
+    float* tr = table + (size_t)v * dim;
+#pragma unroll
+    for (int j = 0; j < DMAX; ++j) {
+      const int d = lane + 64 * j;
+      if (d < dim) tr[d] += scale * acc[r][j];
+    }
   }
 }
 
@@ -295,8 +311,15 @@ int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, co
   if (ws_bytes < mle_embed_scatter_ws_bytes(batch, clen))
     return set_error(MLE_ERR_WORKSPACE, "mle_embed_scatter_add: workspace too small");
   hipStream_t s = as_stream(stream);
-  if ((double)vocab * (double)ntok <= (double)(1u << 30) && dim <= 64 * ROW_DMAX) {
-    row_scatter_kernel<<<(vocab + 3) / 4, 256, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab, scale);
+  if ((double)vocab * (double)ntok <= (double)(1u << 30) && dim <= 1024) {
+    // One row per wave (measured on MI355X: 2, 4 or 8 rows per wave, or 8-16
+    // waves per workgroup, are equal or slower -- the key scan bounds it).
+    if (dim <= 512)
+      row_scatter_kernel<8, 1><<<(vocab + 3) / 4, 256, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab,
+                                                               scale);
+    else
+      row_scatter_kernel<16, 1><<<(vocab + 3) / 4, 256, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim,
+                                                                vocab, scale);
     return check_launch("mle_embed_scatter_add");
   }
   unsigned long long* sorted = static_cast<unsigned long long*>(ws);

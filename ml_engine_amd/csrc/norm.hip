@@ -15,6 +15,8 @@
 // The backward uses the same split for sum(dy) and sum(dy*y).
 #include "common.hpp"
 
+#include <initializer_list>
+
 using namespace mle;
 
 namespace {
@@ -41,27 +43,46 @@ __device__ __forceinline__ size_t at(const NormShape& sh, int g, size_t e) {
   return (size_t)g * sh.group_stride + (size_t)(e32 / sh.seg) * sh.seg_stride + e32 % sh.seg;
 }
 
-template <bool SEG>
+// Element e of thread slot i in a chunk starting at c0.  VEC: thread t owns
+// the float4s t, t + NT, t + 2 NT, t + 3 NT of the chunk (16-byte loads; the
+// host checks that N, the segment length and the base are multiples of 4, so
+// a float4 never straddles a group or segment end); otherwise floats
+// t + i NT.
+template <bool VEC>
+__device__ __forceinline__ size_t elem(size_t c0, int i) {
+  return VEC ? c0 + 4 * (threadIdx.x + (size_t)(i / 4) * NT) + (i % 4) : c0 + threadIdx.x + (size_t)i * NT;
+}
+
+template <bool SEG, bool VEC>
 __device__ __forceinline__ void load_chunk(const float* __restrict__ src, const NormShape& sh, int g, size_t c0,
-                                           float (&v)[VPT], int& cnt) {
-  cnt = 0;
+                                           float (&v)[VPT]) {
+  if (VEC) {
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const size_t e = c0 + threadIdx.x + (size_t)i * NT;
-    v[i] = (e < sh.N) ? src[at<SEG>(sh, g, e)] : 0.f;
-    cnt += (e < sh.N) ? 1 : 0;
+    for (int u = 0; u < VPT / 4; ++u) {
+      const size_t e = elem<true>(c0, 4 * u);
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      if (e < sh.N) t = *reinterpret_cast<const f32x4*>(src + at<SEG>(sh, g, e));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * u + k] = t[k];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const size_t e = elem<false>(c0, i);
+      v[i] = (e < sh.N) ? src[at<SEG>(sh, g, e)] : 0.f;
+    }
   }
 }
 
-template <bool SEG>
+// Pass 1 of the forward: per chunk (mean, M2) in double.
+template <bool SEG, bool VEC>
 __global__ __launch_bounds__(NT) void norm_stats_partial(const float* __restrict__ x, NormShape sh,
                                                          double* __restrict__ part) {
   __shared__ double red[NT / 64];
   const int g = blockIdx.y, ck = blockIdx.x;
   const size_t c0 = (size_t)ck * CH;
   float v[VPT];
-  int cnt;
-  load_chunk<SEG>(x, sh, g, c0, v, cnt);
+  load_chunk<SEG, VEC>(x, sh, g, c0, v);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) s += v[i];
@@ -72,7 +93,7 @@ __global__ __launch_bounds__(NT) void norm_stats_partial(const float* __restrict
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const double d = (double)v[i] - mean;
-    if (c0 + threadIdx.x + (size_t)i * NT < sh.N) m2 += d * d;
+    if (elem<VEC>(c0, i) < sh.N) m2 += d * d;
   }
   m2 = block_sum<NT>(m2, red);
   if (threadIdx.x == 0) {
@@ -82,32 +103,70 @@ __global__ __launch_bounds__(NT) void norm_stats_partial(const float* __restrict
   }
 }
 
-// Fixed-order combination of the chunk partials of group g.
-__device__ __forceinline__ void combine_stats(const double* __restrict__ part, const NormShape& sh, int g, double& mean,
-                                              double& m2) {
-  const double* p = part + (size_t)g * sh.nchunk * 2;
-  double n_a = 0, mu = 0, M = 0;
-  for (int c = 0; c < sh.nchunk; ++c) {
-    const size_t c0 = (size_t)c * CH;
-    const double n_b = (double)((sh.N - c0 < (size_t)CH) ? sh.N - c0 : (size_t)CH);
-    const double mu_b = p[2 * c], M_b = p[2 * c + 1];
-    const double n = n_a + n_b;
-    const double d = mu_b - mu;
-    mu += d * (n_b / n);
-    M += M_b + d * d * (n_a * n_b / n);
-    n_a = n;
-  }
-  mean = mu;
-  m2 = M;
+// Chunk c's element count.
+__device__ __forceinline__ double chunk_n(const NormShape& sh, int c) {
+  const size_t c0 = (size_t)c * CH;
+  return (double)((sh.N - c0 < (size_t)CH) ? sh.N - c0 : (size_t)CH);
 }
 
-template <bool SEG>
+// Chan et al. pairwise update: (n, mean, M2) of a followed by b.
+__device__ __forceinline__ void chan_merge(double& n, double& mu, double& M, double nb, double mub, double Mb) {
+  const double nn = n + nb;
+  if (nb == 0.0) return;
+  const double d = mub - mu;
+  mu += d * (nb / nn);
+  M += Mb + d * d * (n * nb / nn);
+  n = nn;
+}
+
+// The group's (mean, M2) from its chunk partials, computed by every wave of
+// the workgroup with the same fixed order: lane l first merges chunks l,
+// l + 64, ... in turn, then lanes merge pairwise in a tree (lower lane first).
+__device__ __forceinline__ void group_stats(const double* __restrict__ part, const NormShape& sh, int g, double& mean,
+                                            double& m2) {
+  const int lane = threadIdx.x & 63;
+  const double* p = part + (size_t)g * sh.nchunk * 2;
+  double n = 0.0, mu = 0.0, M = 0.0;
+  for (int c = lane; c < sh.nchunk; c += 64) chan_merge(n, mu, M, chunk_n(sh, c), p[2 * c], p[2 * c + 1]);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const double nb = __shfl_down(n, off, 64), mub = __shfl_down(mu, off, 64), Mb = __shfl_down(M, off, 64);
+    if ((lane & (2 * off - 1)) == 0 && lane + off < 64) chan_merge(n, mu, M, nb, mub, Mb);
+  }
+  mean = __shfl(mu, 0, 64);
+  m2 = __shfl(M, 0, 64);
+}
+
+// The group's sum(dy) and sum(dy * y), same fixed order.
+__device__ __forceinline__ void group_sums(const double* __restrict__ part, const NormShape& sh, int g, double& a,
+                                           double& b) {
+  const int lane = threadIdx.x & 63;
+  const double* p = part + (size_t)g * sh.nchunk * 2;
+  a = 0.0;
+  b = 0.0;
+  for (int c = lane; c < sh.nchunk; c += 64) {
+    a += p[2 * c];
+    b += p[2 * c + 1];
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const double ab = __shfl_down(a, off, 64), bb = __shfl_down(b, off, 64);
+    if ((lane & (2 * off - 1)) == 0 && lane + off < 64) {
+      a += ab;
+      b += bb;
+    }
+  }
+  a = __shfl(a, 0, 64);
+  b = __shfl(b, 0, 64);
+}
+
+template <bool SEG, bool VEC>
 __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, float* __restrict__ y,
                                                  float* __restrict__ stats, NormShape sh, const double* __restrict__ part,
                                                  float eps) {
   const int g = blockIdx.y, ck = blockIdx.x;
   double mean_d, m2_d;
-  combine_stats(part, sh, g, mean_d, m2_d);
+  group_stats(part, sh, g, mean_d, m2_d);
   const float mean = (float)mean_d, ssd = (float)m2_d;
   const float r = rsqrtf((1.0f / (float)sh.N) * ssd + eps);  // LNorm/GNorm (Engine/kernels.cu:794-834)
   if (ck == 0 && threadIdx.x == 0) {
@@ -115,32 +174,46 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
     stats[2 * g + 1] = ssd;
   }
   const size_t c0 = (size_t)ck * CH;
+  if (VEC) {
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const size_t e = c0 + threadIdx.x + (size_t)i * NT;
-    if (e < sh.N) {
-      const size_t o = at<SEG>(sh, g, e);
-      y[o] = (x[o] - mean) * r;
+    for (int u = 0; u < VPT / 4; ++u) {
+      const size_t e = elem<true>(c0, 4 * u);
+      if (e < sh.N) {
+        const size_t o = at<SEG>(sh, g, e);
+        const f32x4 xv = *reinterpret_cast<const f32x4*>(x + o);
+        f32x4 yv;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) yv[k] = (xv[k] - mean) * r;
+        *reinterpret_cast<f32x4*>(y + o) = yv;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const size_t e = elem<false>(c0, i);
+      if (e < sh.N) {
+        const size_t o = at<SEG>(sh, g, e);
+        y[o] = (x[o] - mean) * r;
+      }
     }
   }
 }
 
-template <bool SEG>
+// Backward pass 1: per chunk sum(dy) and sum(dy * y) in double.
+template <bool SEG, bool VEC>
 __global__ __launch_bounds__(NT) void norm_bwd_partial(const float* __restrict__ y, const float* __restrict__ dy,
                                                        NormShape sh, double* __restrict__ part) {
   __shared__ double red[NT / 64];
   const int g = blockIdx.y, ck = blockIdx.x;
   const size_t c0 = (size_t)ck * CH;
+  float yv[VPT], gv[VPT];
+  load_chunk<SEG, VEC>(y, sh, g, c0, yv);
+  load_chunk<SEG, VEC>(dy, sh, g, c0, gv);
   double sg = 0.0, sgy = 0.0;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const size_t e = c0 + threadIdx.x + (size_t)i * NT;
-    if (e < sh.N) {
-      const size_t o = at<SEG>(sh, g, e);
-      const float gv = dy[o];
-      sg += gv;
-      sgy += (double)(gv * y[o]);
-    }
+    sg += gv[i];
+    sgy += (double)(gv[i] * yv[i]);
   }
   sg = block_sum<NT>(sg, red);
   sgy = block_sum<NT>(sgy, red);
@@ -151,35 +224,70 @@ __global__ __launch_bounds__(NT) void norm_bwd_partial(const float* __restrict__
   }
 }
 
+// Per group, once (the LayerNorm layout quirk reads other groups' sums per
+// element): fin[2g] = sum(dy), fin[2g+1] = sum(dy * y), same order as group_sums.
+__global__ __launch_bounds__(64) void norm_bwd_final(const double* __restrict__ part, NormShape sh,
+                                                     double* __restrict__ fin) {
+  double a, b;
+  group_sums(part, sh, blockIdx.x, a, b);
+  if (threadIdx.x == 0) {
+    fin[2 * blockIdx.x] = a;
+    fin[2 * blockIdx.x + 1] = b;
+  }
+}
+
 // dx (+)= r (dy - sum(dy)/N - y sum(dy*y)/N)  (LayerBackward/GroupBackward,
 // Engine/kernels.cu:849-896); acc = 0 assigns.  `quirk_hw` != 0 reproduces
 // LayerBackward for channels > 1: only elements e < batch*hw receive a
 // gradient, with group e / hw (the others are left alone, or set to 0 when
 // assigning, which is what adding nothing to a cleared gradient gives).
-template <bool SEG>
+template <bool SEG, bool VEC>
 __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y, const float* __restrict__ dy,
                                                      float* __restrict__ dx, const float* __restrict__ stats,
-                                                     NormShape sh, const double* __restrict__ part, float eps,
-                                                     size_t quirk_hw, int acc) {
+                                                     NormShape sh, const double* __restrict__ part,
+                                                     const double* __restrict__ fin, float eps, size_t quirk_hw,
+                                                     int acc) {
   const int g = blockIdx.y, ck = blockIdx.x;
   const size_t c0 = (size_t)ck * CH;
   const float fN = (float)(int)sh.N;
-  auto group_terms = [&](int gs, float& sg, float& sgy, float& r) {
-    const double* p = part + (size_t)gs * sh.nchunk * 2;
-    double sgd = 0.0, sgyd = 0.0;
-    for (int c = 0; c < sh.nchunk; ++c) {
-      sgd += p[2 * c];
-      sgyd += p[2 * c + 1];
-    }
-    sg = (float)sgd;
-    sgy = (float)sgyd;
+  // fin: precomputed per-group sums (quirk path); otherwise this group's own.
+  auto terms = [&](int gs, float& sg, float& sgy, float& r) {
+    sg = (float)fin[2 * gs];
+    sgy = (float)fin[2 * gs + 1];
     r = rsqrtf(stats[2 * gs + 1] / fN + eps);
   };
   float sg, sgy, r;
-  group_terms(g, sg, sgy, r);
+  if (quirk_hw) {
+    terms(g, sg, sgy, r);
+  } else {
+    double a, b;
+    group_sums(part, sh, g, a, b);
+    sg = (float)a;
+    sgy = (float)b;
+    r = rsqrtf(stats[2 * g + 1] / fN + eps);
+  }
+  if (VEC && !quirk_hw) {
+#pragma unroll
+    for (int u = 0; u < VPT / 4; ++u) {
+      const size_t e = elem<true>(c0, 4 * u);
+      if (e < sh.N) {
+        const size_t o = at<SEG>(sh, g, e);
+        const f32x4 yv = *reinterpret_cast<const f32x4*>(y + o);
+        const f32x4 gv = *reinterpret_cast<const f32x4*>(dy + o);
+        f32x4 d = acc ? *reinterpret_cast<const f32x4*>(dx + o) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float v = r * (gv[k] - (sg / fN) - yv[k] * (sgy / fN));
+          d[k] = acc ? d[k] + v : v;
+        }
+        *reinterpret_cast<f32x4*>(dx + o) = d;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const size_t e = c0 + threadIdx.x + (size_t)i * NT;
+    const size_t e = elem<false>(c0, i);
     if (e >= sh.N) continue;
     const size_t idx = at<SEG>(sh, g, e);
     if (!SEG && quirk_hw) {
@@ -187,10 +295,59 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
         if (!acc) dx[idx] = 0.f;
         continue;
       }
-      group_terms((int)(idx / quirk_hw), sg, sgy, r);
+      terms((int)(idx / quirk_hw), sg, sgy, r);
     }
     const float v = r * (dy[idx] - (sg / fN) - y[idx] * (sgy / fN));
     dx[idx] = acc ? dx[idx] + v : v;
+  }
+}
+
+// The 16-byte path: every group (segment) length and base a multiple of 4 floats.
+bool vec_ok(const NormShape& sh, std::initializer_list<const void*> ptrs) {
+  if (sh.N % 4 != 0) return false;
+  if (sh.seg && (sh.seg % 4 != 0 || sh.seg_stride % 4 != 0 || sh.group_stride % 4 != 0)) return false;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  return true;
+}
+
+// Workspace: per-chunk partials, then the per-group finals.
+size_t ws_need(const NormShape& sh) { return ((size_t)sh.groups_tot * sh.nchunk * 2 + (size_t)sh.groups_tot * 2) * sizeof(double); }
+
+void launch_fwd(hipStream_t s, const NormShape& sh, const float* x, float* y, float* stats, void* ws, float eps) {
+  dim3 grid(sh.nchunk, sh.groups_tot);
+  double* part = static_cast<double*>(ws);
+  const bool v = vec_ok(sh, {x, y});
+  if (sh.seg) {
+    if (v) norm_stats_partial<true, true><<<grid, NT, 0, s>>>(x, sh, part);
+    else norm_stats_partial<true, false><<<grid, NT, 0, s>>>(x, sh, part);
+    if (v) norm_apply<true, true><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+    else norm_apply<true, false><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+  } else {
+    if (v) norm_stats_partial<false, true><<<grid, NT, 0, s>>>(x, sh, part);
+    else norm_stats_partial<false, false><<<grid, NT, 0, s>>>(x, sh, part);
+    if (v) norm_apply<false, true><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+    else norm_apply<false, false><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+  }
+}
+
+void launch_bwd(hipStream_t s, const NormShape& sh, const float* y, const float* dy, float* dx, const float* stats,
+                void* ws, float eps, size_t quirk, int accumulate) {
+  dim3 grid(sh.nchunk, sh.groups_tot);
+  double* part = static_cast<double*>(ws);
+  double* fin = part + (size_t)sh.groups_tot * sh.nchunk * 2;
+  const bool v = vec_ok(sh, {y, dy, dx});
+  if (sh.seg) {
+    if (v) norm_bwd_partial<true, true><<<grid, NT, 0, s>>>(y, dy, sh, part);
+    else norm_bwd_partial<true, false><<<grid, NT, 0, s>>>(y, dy, sh, part);
+    if (v) norm_bwd_apply<true, true><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, 0, accumulate);
+    else norm_bwd_apply<true, false><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, 0, accumulate);
+  } else {
+    if (v) norm_bwd_partial<false, true><<<grid, NT, 0, s>>>(y, dy, sh, part);
+    else norm_bwd_partial<false, false><<<grid, NT, 0, s>>>(y, dy, sh, part);
+    if (quirk) norm_bwd_final<<<sh.groups_tot, 64, 0, s>>>(part, sh, fin);
+    if (v) norm_bwd_apply<false, true><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, quirk, accumulate);
+    else norm_bwd_apply<false, false><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, quirk, accumulate);
   }
 }
 
@@ -309,7 +466,7 @@ extern "C" {
 size_t mle_norm_ws_bytes(int batch, int channels, size_t hw, int groups) {
   NormShape sh;
   if (shape_of(batch, channels, hw, groups, sh) != MLE_OK) return 0;
-  return (size_t)sh.groups_tot * sh.nchunk * 2 * sizeof(double);
+  return ws_need(sh);
 }
 
 int mle_norm_fwd(mle_stream stream, const float* x, float* y, float* stats, int batch, int channels, size_t hw,
@@ -318,13 +475,8 @@ int mle_norm_fwd(mle_stream stream, const float* x, float* y, float* stats, int 
   NormShape sh;
   int rc = shape_of(batch, channels, hw, groups, sh);
   if (rc) return rc;
-  if (ws_bytes < mle_norm_ws_bytes(batch, channels, hw, groups))
-    return set_error(MLE_ERR_WORKSPACE, "mle_norm_fwd: workspace too small");
-  hipStream_t s = as_stream(stream);
-  dim3 grid(sh.nchunk, sh.groups_tot);
-  double* part = static_cast<double*>(ws);
-  norm_stats_partial<false><<<grid, NT, 0, s>>>(x, sh, part);
-  norm_apply<false><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_fwd: workspace too small");
+  launch_fwd(as_stream(stream), sh, x, y, stats, ws, eps);
   return check_launch("mle_norm_fwd");
 }
 
@@ -335,21 +487,16 @@ int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, 
   NormShape sh;
   int rc = shape_of(batch, channels, hw, groups, sh);
   if (rc) return rc;
-  if (ws_bytes < mle_norm_ws_bytes(batch, channels, hw, groups))
-    return set_error(MLE_ERR_WORKSPACE, "mle_norm_bwd: workspace too small");
-  hipStream_t s = as_stream(stream);
-  dim3 grid(sh.nchunk, sh.groups_tot);
-  double* part = static_cast<double*>(ws);
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_bwd: workspace too small");
   const size_t quirk = (reference_layout && groups == 1 && channels > 1) ? hw : 0;
-  norm_bwd_partial<false><<<grid, NT, 0, s>>>(y, dy, sh, part);
-  norm_bwd_apply<false><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, eps, quirk, accumulate);
+  launch_bwd(as_stream(stream), sh, y, dy, dx, stats, ws, eps, quirk, accumulate);
   return check_launch("mle_norm_bwd");
 }
 
 size_t mle_batchnorm_ws_bytes(int batch, int channels, size_t hw) {
   NormShape sh;
   if (bn_shape_of(batch, channels, hw, sh) != MLE_OK) return 0;
-  return (size_t)sh.groups_tot * sh.nchunk * 2 * sizeof(double);
+  return ws_need(sh);
 }
 
 int mle_batchnorm_fwd(mle_stream stream, const float* x, float* y, float* stats, int batch, int channels, size_t hw,
@@ -358,13 +505,8 @@ int mle_batchnorm_fwd(mle_stream stream, const float* x, float* y, float* stats,
   NormShape sh;
   int rc = bn_shape_of(batch, channels, hw, sh);
   if (rc) return rc;
-  if (ws_bytes < mle_batchnorm_ws_bytes(batch, channels, hw))
-    return set_error(MLE_ERR_WORKSPACE, "mle_batchnorm_fwd: workspace too small");
-  hipStream_t s = as_stream(stream);
-  dim3 grid(sh.nchunk, sh.groups_tot);
-  double* part = static_cast<double*>(ws);
-  norm_stats_partial<true><<<grid, NT, 0, s>>>(x, sh, part);
-  norm_apply<true><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_batchnorm_fwd: workspace too small");
+  launch_fwd(as_stream(stream), sh, x, y, stats, ws, eps);
   return check_launch("mle_batchnorm_fwd");
 }
 
@@ -374,13 +516,8 @@ int mle_batchnorm_bwd(mle_stream stream, const float* y, const float* dy, float*
   NormShape sh;
   int rc = bn_shape_of(batch, channels, hw, sh);
   if (rc) return rc;
-  if (ws_bytes < mle_batchnorm_ws_bytes(batch, channels, hw))
-    return set_error(MLE_ERR_WORKSPACE, "mle_batchnorm_bwd: workspace too small");
-  hipStream_t s = as_stream(stream);
-  dim3 grid(sh.nchunk, sh.groups_tot);
-  double* part = static_cast<double*>(ws);
-  norm_bwd_partial<true><<<grid, NT, 0, s>>>(y, dy, sh, part);
-  norm_bwd_apply<true><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, eps, 0, accumulate);
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_batchnorm_bwd: workspace too small");
+  launch_bwd(as_stream(stream), sh, y, dy, dx, stats, ws, eps, 0, accumulate);
   return check_launch("mle_batchnorm_bwd");
 }
 

@@ -423,12 +423,20 @@ __global__ __launch_bounds__(NT) void mse_partial_kernel(const float* __restrict
   if (threadIdx.x == 0) part[blockIdx.x] = acc;
 }
 
-__global__ __launch_bounds__(NT) void finish_scalar_kernel(const double* __restrict__ part, size_t nparts,
-                                                           double denom, float* __restrict__ out) {
-  __shared__ double red[NT / 64];
-  double acc = 0.0;
-  for (size_t i = threadIdx.x; i < nparts; i += NT) acc += part[i];
-  acc = block_sum<NT>(acc, red);
+// One 1024-thread workgroup; four loads in flight per thread, fixed order.
+constexpr int FIN_NT = 1024;
+__global__ __launch_bounds__(FIN_NT) void finish_scalar_kernel(const double* __restrict__ part, size_t nparts,
+                                                               double denom, float* __restrict__ out) {
+  __shared__ double red[FIN_NT / 64];
+  double a[4] = {0.0, 0.0, 0.0, 0.0};
+  size_t i = threadIdx.x;
+  for (; i + 3 * FIN_NT < nparts; i += 4 * FIN_NT) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] += part[i + u * FIN_NT];
+  }
+  for (; i < nparts; i += FIN_NT) a[0] += part[i];
+  double acc = (a[0] + a[1]) + (a[2] + a[3]);
+  acc = block_sum<FIN_NT>(acc, red);
   if (threadIdx.x == 0) out[0] = (float)(acc / denom);
 }
 
@@ -592,7 +600,7 @@ int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, flo
   hipStream_t s = as_stream(stream);
   double* part = static_cast<double*>(ws);
   mse_partial_kernel<<<g, NT, 0, s>>>(x, t, n, part);
-  finish_scalar_kernel<<<1, NT, 0, s>>>(part, g, (double)n, loss);
+  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, g, (double)n, loss);
   return check_launch("mle_mse_fwd");
 }
 
@@ -621,7 +629,7 @@ int mle_softmax_xent_fwd(mle_stream stream, const float* logits, const float* ta
     softmax_row_kernel<true><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part, KeyTargets{});
   else
     softmax_row_kernel<false><<<rows, NT, 0, s>>>(logits, probs, rows, cols, 0, target, part, KeyTargets{});
-  finish_scalar_kernel<<<1, NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
+  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
   return check_launch("mle_softmax_xent_fwd");
 }
 
@@ -655,7 +663,7 @@ int mle_softmax_xent_keys_fwd(mle_stream stream, const float* logits, const int3
     softmax_row_kernel<true><<<rows, NT, 0, s>>>(logits, nullptr, rows, cols, 0, nullptr, part, kt);
   else
     softmax_row_kernel<false><<<rows, NT, 0, s>>>(logits, nullptr, rows, cols, 0, nullptr, part, kt);
-  finish_scalar_kernel<<<1, NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
+  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
   return check_launch("mle_softmax_xent_keys_fwd");
 }
 

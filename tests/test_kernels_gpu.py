@@ -564,7 +564,8 @@ def test_gather_onehot_argmax_scatter(hip, orc):
     assert_close(gtab.numpy(), tab_r, what="scatter add", **EW)
 
 
-@pytest.mark.parametrize("batch,clen,dim,vocab", [(4, 600, 64, 300), (2, 50, 1100, 40), (64, 1024, 8, 20000)])
+@pytest.mark.parametrize("batch,clen,dim,vocab", [(4, 600, 64, 300), (2, 50, 1100, 40), (64, 1024, 8, 20000),
+                                                 (3, 300, 700, 500), (32, 256, 512, 8000)])
 def test_scatter_add_paths(hip, orc, batch, clen, dim, vocab):
     """Row-centric path (moderate vocab*tokens, dim <= 1024) and sorted path."""
     r = rng(batch + clen + dim)
