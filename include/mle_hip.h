@@ -161,6 +161,20 @@ int mle_gemm_ex(mle_stream stream, int trans_a, int trans_b, int M, int N, int K
                 float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum,
                 const float* bias, void* ws, size_t ws_bytes);
 
+/* mle_gemm_ex over a two-level batch: item (o, i), o < outer, i < inner,
+ * reads A at A + o*sa_outer + i*sa_inner (likewise B, C).  With inner = heads
+ * and the head stride as *_inner, the per-head products of attention address
+ * Q, K, V and the output in their [batch, seq, heads * dim] layout directly:
+ * it replaces HeadifytoChannel / DeHeadify (HeadifyColChannel,
+ * Engine/kernels.cu:1371-1406) around the BMM / BMMABT bcmm calls of
+ * MultiHeadAttention (Engine/transformer.cu:647-661).  ws as mle_gemm_ex with
+ * batch = outer * inner. */
+int mle_gemm_grid(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+                  const float* A, int64_t lda, int64_t sa_outer, int64_t sa_inner,
+                  const float* B, int64_t ldb, int64_t sb_outer, int64_t sb_inner, float beta,
+                  float* C, int64_t ldc, int64_t sc_outer, int64_t sc_inner, int outer, int inner,
+                  void* ws, size_t ws_bytes);
+
 /* out[c] (+)= sum_r x[r, c].  BCompress (Engine/kernels.cu:1562-1584); beta 0/1. */
 int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* out, float beta);
 /* out[c] += sum_{b, s} x[b, c, s] for c < nreduce (nreduce <= channels).

@@ -27,7 +27,17 @@ struct GemmArgs {
   float* part;
   float* part_cs;
   const float* bias;  // nullable: C[r, c] += bias[c] after alpha/beta
+  // Two-level batch: item z = zo * inner + zi sits at zo * s + zi * s2 of
+  // each operand (inner == 1: one stride).  Lets per-head products address
+  // the heads of a [batch, seq, heads * dim] tensor in place.
+  int inner;
+  int64_t sa2, sb2, sc2;
 };
+
+__device__ __forceinline__ int64_t batch_off(int64_t z, const GemmArgs& g, int64_t s, int64_t s2) {
+  if (g.inner == 1) return z * s;
+  return (z / g.inner) * s + (z % g.inner) * s2;
+}
 
 // Load 4 consecutive elements base[r*ld + c .. c+3] with bounds (R rows, Cc cols).
 template <bool VEC>
@@ -157,9 +167,9 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
   const int m0 = tm * TM, n0 = tn * TN;
   const int64_t z = blockIdx.z / g.splits;
   const int split = blockIdx.z % g.splits;
-  const float* A = g.A + z * g.sa;
-  const float* B = g.B + z * g.sb;
-  float* C = g.C + z * g.sc;
+  const float* A = g.A + batch_off(z, g, g.sa, g.sa2);
+  const float* B = g.B + batch_off(z, g, g.sb, g.sb2);
+  float* C = g.C + batch_off(z, g, g.sc, g.sc2);
   const int kbeg = split * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
   const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
@@ -327,9 +337,9 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   const int m0 = tm * TM + wm * 64, n0 = tn * TN + wn * 64;  // this wave's 64 x 64 block
   const int64_t z = blockIdx.z / g.splits;
   const int split = blockIdx.z % g.splits;
-  const float* A = g.A + z * g.sa;
-  const float* B = g.B + z * g.sb;
-  float* C = g.C + z * g.sc;
+  const float* A = g.A + batch_off(z, g, g.sa, g.sa2);
+  const float* B = g.B + batch_off(z, g, g.sb, g.sb2);
+  float* C = g.C + batch_off(z, g, g.sc, g.sc2);
   const int kbeg = split * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
   const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
@@ -499,7 +509,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
         if (VEC) acc += *reinterpret_cast<const f32x4*>(p + sp * mn);
         else acc[0] += p[sp * mn];
       }
-      float* c = g.C + b * g.sc + (int64_t)row * g.ldc + col;
+      float* c = g.C + batch_off(b, g, g.sc, g.sc2) + (int64_t)row * g.ldc + col;
       if (VEC) {
         f32x4 v = g.alpha * acc;
         if (g.beta != 0.f) v += g.beta * *reinterpret_cast<const f32x4*>(c);
@@ -622,7 +632,7 @@ double extent_bytes(int rows, int cols, int64_t ld) { return ((double)(rows - 1)
 static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
                      int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
                      int64_t ldc, int64_t stride_c, int batch, float* colsum, const float* bias, void* ws,
-                     size_t ws_bytes) {
+                     size_t ws_bytes, int inner = 1, int64_t sa2 = 0, int64_t sb2 = 0, int64_t sc2 = 0) {
   MLE_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "mle_gemm: negative size");
   if (M == 0 || N == 0 || batch == 0) return MLE_OK;
   MLE_CHECK_ARG(C != nullptr && (K == 0 || (A != nullptr && B != nullptr)), "mle_gemm: null operand");
@@ -632,8 +642,9 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   const Tile tile = choose_tile(M, N, K, batch);
   MLE_CHECK_ARG((M + tile.tm() - 1) / tile.tm() <= 65535 && batch <= 65535, "mle_gemm: grid too large (M %d, batch %d)",
                 M, batch);
-  GemmArgs g{A, B, C, colsum, lda, ldb, ldc, stride_a, stride_b, stride_c, M, N, K, alpha, beta, 1, K, nullptr, nullptr,
-             bias};
+  MLE_CHECK_ARG(inner >= 1 && batch % inner == 0, "mle_gemm: batch %d not a multiple of inner %d", batch, inner);
+  GemmArgs g{A,    B,    C,       colsum,  lda,  ldb,    ldc,  stride_a, stride_b, stride_c, M,  N,  K,
+             alpha, beta, 1,       K,       nullptr, nullptr, bias, inner,    sa2,      sb2,      sc2};
   int kchunk = K;
   const int splits = ws ? choose_splits(M, N, K, batch, kchunk) : 1;
   if (splits > 1) {
@@ -646,7 +657,7 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
     }
   }
   const bool v4 = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
-                  aligned16(A) && aligned16(B);
+                  (sa2 % 4 == 0) && (sb2 % 4 == 0) && aligned16(A) && aligned16(B);
   // Buffer loads need the contiguous bound of each operand to be a multiple of
   // 4 and every extent addressable with a 31-bit byte offset.
   const int a_rows = trans_a ? K : M, a_cols = trans_a ? M : K;
@@ -657,7 +668,7 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   const int vec = buf ? 2 : (v4 ? 1 : 0);
   const bool cs = colsum != nullptr;
   // The direct kernel stores 16-byte row segments of C (and reads bias as float4).
-  const bool direct_ok = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(C) &&
+  const bool direct_ok = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && sc2 % 4 == 0 && aligned16(C) &&
                          (bias == nullptr || aligned16(bias));
   dim3 grid((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
   hipStream_t s = as_stream(stream);
@@ -674,7 +685,8 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
       default: launch_tile<1, 1>(s, g, tile, grid, vec, cs, direct_ok); break;
     }
     if (g.splits > 1) {
-      const bool rv = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(C) && aligned16(g.part) &&
+      const bool rv = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && sc2 % 4 == 0 && aligned16(C) &&
+                      aligned16(g.part) &&
                       (!bias || aligned16(bias));
       const int w = rv ? 4 : 1;
       dim3 rgrid((unsigned)((N / w + 255) / 256), (unsigned)std::min(M, 65535), (unsigned)batch);
@@ -707,6 +719,15 @@ int mle_gemm_ex(mle_stream stream, int trans_a, int trans_b, int M, int N, int K
                 size_t ws_bytes) {
   return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
                    stride_c, batch, colsum, bias, ws, ws_bytes);
+}
+
+int mle_gemm_grid(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                  int64_t lda, int64_t sa_outer, int64_t sa_inner, const float* B, int64_t ldb, int64_t sb_outer,
+                  int64_t sb_inner, float beta, float* C, int64_t ldc, int64_t sc_outer, int64_t sc_inner, int outer,
+                  int inner, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(outer >= 0 && inner >= 1, "mle_gemm_grid: bad batch grid %d x %d", outer, inner);
+  return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, sa_outer, B, ldb, sb_outer, beta, C, ldc,
+                   sc_outer, outer * inner, nullptr, nullptr, ws, ws_bytes, inner, sa_inner, sb_inner, sc_inner);
 }
 
 }  // extern "C"

@@ -237,6 +237,12 @@ class GraphOperations {
   static graph SoftMaxCrossEntropy(const graph& prediction, const graph& target, const bool last);
   static graph BMM(const graph& A, const graph& B);     // m x n * n x p = m x p
   static graph BMMABT(const graph& A, const graph& B);  // m x n * p x n = m x p
+  // Multi-head attention products over [batch, 1, seq, heads * dim]
+  // projections without head permutes (additive; MultiHeadAttention uses them):
+  // HeadScores = Scale(BMMABT(Headify(Q), Headify(K)), scale) -> [batch, heads, m, p];
+  // HeadMix = DeHeadify(BMM(P, Headify(V))) -> [batch, 1, m, heads * dim].
+  static graph HeadScores(const graph& Q, const graph& K, const int heads, const float scale);
+  static graph HeadMix(const graph& P, const graph& V, const int heads);
   static graph SOFTMAX(const graph& X, const int type = 0);
   static graph SOFTMASK(const graph& X, const int type = 0);
   static graph RELU(const graph& input);

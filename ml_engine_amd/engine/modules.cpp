@@ -30,15 +30,16 @@ void MultiHeadAttention::load(std::ifstream& f) {
   o.load(f);
 }
 
+// The reference composes Headify x3, BMMABT, Scale, SOFTMASK, BMM and
+// DeHeadify; HeadScores and HeadMix compute the same products on the heads in
+// place (no permuted copies, the scale in the GEMM).
 graph MultiHeadAttention::forward(const graph& X, const bool mask) {
-  auto Q = GraphOperations::HeadifytoChannel(q.forward(X), num_heads);
-  auto K = GraphOperations::HeadifytoChannel(k.forward(X), num_heads);
-  auto V = GraphOperations::HeadifytoChannel(v.forward(X), num_heads);
-  auto scores = GraphOperations::BMMABT(Q, K);
-  auto scaled = GraphOperations::Scale(scores, 1.0f / sqrtf((float)head_dim));
+  auto Q = q.forward(X);
+  auto K = k.forward(X);
+  auto V = v.forward(X);
+  auto scaled = GraphOperations::HeadScores(Q, K, num_heads, 1.0f / sqrtf((float)head_dim));
   auto weights = (mask && scaled->dim[2] > 1) ? GraphOperations::SOFTMASK(scaled, 1) : GraphOperations::SOFTMAX(scaled, 1);
-  auto attn = GraphOperations::BMM(weights, V);
-  auto concat = GraphOperations::DeHeadify(attn);
+  auto concat = GraphOperations::HeadMix(weights, V, num_heads);
   auto output = o.forward(concat);
   output->op_name = "Multi Head Attention Output";
   return output;

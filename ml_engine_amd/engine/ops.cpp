@@ -510,6 +510,89 @@ graph GraphOperations::BMMABT(const graph& A, const graph& B) {
   return node;
 }
 
+// Attention scores per head, scale * Q_h K_h^T, read straight from the
+// [batch, 1, seq, heads * dim] projections: HeadifytoChannel(Q), HeadifytoChannel(K),
+// BMMABT and Scale of MultiHeadAttention (Engine/transformer.cu:647-654,
+// Engine/engine.cu:1144-1164, 2260-2314, 2523-2551) in one node.  The scale is
+// the GEMM's alpha (exactly the reference's multiply when it is a power of two).
+// Backward: dQ += scale dY K; K's gradient is the reference's bcmmT(Q, dZ) in
+// the headified layout (mle::quirks) or the true scale dY^T Q.
+graph GraphOperations::HeadScores(const graph& Q, const graph& K, const int heads, const float scale) {
+  if (Q->dim[1] != 1 || K->dim[1] != 1 || Q->dim[3] != K->dim[3] || Q->dim[0] != K->dim[0] || Q->dim[3] % heads != 0) {
+    std::cerr << "HeadScores: Q and K must be [batch, 1, seq, heads * dim] with the same batch and width\n";
+    Dimension(Q);
+    Dimension(K);
+    std::exit(1);
+  }
+  const int b = Q->dim[0], m = Q->dim[2], p = K->dim[2], E = Q->dim[3], hd = E / heads;
+  auto node = make_node("Head scores", b, heads, m, p);
+  node->inputs = {Q, K};
+  NodeBackProp *nd = node.get(), *pq = Q.get(), *pk = K.get();
+  const bool ref_grad = mle::quirks().bmmabt_reference_grad;
+  // The reference's K gradient lands in a headified [b, heads, p, hd] buffer first.
+  float* kh = ref_grad ? static_cast<float*>(mle::alloc_scratch(sizeof(float) * (size_t)b * heads * p * hd)) : nullptr;
+  const long long qs = (long long)m * E, ks = (long long)p * E, ys = (long long)heads * m * p, yh = (long long)m * p;
+  node->forward = [=]() {
+    check(mle_gemm_grid(S(), 0, 1, m, p, hd, scale, pq->output, E, qs, hd, pk->output, E, ks, hd, 0.0f, nd->output, p,
+                        ys, yh, b, heads, nullptr, 0),
+          "HeadScores forward");
+  };
+  node->backward = [=]() {
+    check(mle_gemm_grid(S(), 0, 0, m, hd, p, scale, nd->grad, p, ys, yh, pk->output, E, ks, hd,
+                        (float)mle::accumulate_flag(pq), pq->grad, E, qs, hd, b, heads, nullptr, 0),
+          "HeadScores dQ = s dY K");
+    if (ref_grad) {
+      // bcmmT(Q_h, dZ) with dims (hd, m, p): C[hd x p] = Q_h^T (dZ viewed as p x m)^T,
+      // written row-major into the head's [p x hd] gradient block.
+      check(mle_gemm_grid(S(), 1, 1, hd, p, m, scale, pq->output, E, qs, hd, nd->grad, m, ys, yh, 0.0f, kh, p,
+                          (long long)heads * p * hd, (long long)p * hd, b, heads, nullptr, 0),
+            "HeadScores dK (reference bcmmT)");
+      const int flag = mle::accumulate_flag(pk) ? 1 : 2;
+      check(mle_headify(S(), kh, pk->grad, b, heads, p, hd, flag), "HeadScores dK headify backward");
+    } else {
+      check(mle_gemm_grid(S(), 1, 0, p, hd, m, scale, nd->grad, p, ys, yh, pq->output, E, qs, hd,
+                          (float)mle::accumulate_flag(pk), pk->grad, E, ks, hd, b, heads, nullptr, 0),
+            "HeadScores dK = s dY^T Q");
+    }
+  };
+  std_hooks(node);
+  return node;
+}
+
+// Per-head P_h V_h written straight into the [batch, 1, seq, heads * dim]
+// concatenation: HeadifytoChannel(V), BMM and DeHeadify of MultiHeadAttention
+// (Engine/transformer.cu:655-658, Engine/engine.cu:2205-2258, 1166-1178) in one
+// node.  Backward: dP += dO_h V_h^T, dV += P_h^T dO_h.
+graph GraphOperations::HeadMix(const graph& P, const graph& V, const int heads) {
+  if (V->dim[1] != 1 || P->dim[1] != heads || P->dim[0] != V->dim[0] || P->dim[3] != V->dim[2] ||
+      V->dim[3] % heads != 0) {
+    std::cerr << "HeadMix: P must be [batch, heads, m, n] and V [batch, 1, n, heads * dim]\n";
+    Dimension(P);
+    Dimension(V);
+    std::exit(1);
+  }
+  const int b = P->dim[0], m = P->dim[2], n = P->dim[3], E = V->dim[3], hd = E / heads;
+  auto node = make_node("Head mix", b, 1, m, E);
+  node->inputs = {P, V};
+  NodeBackProp *nd = node.get(), *pp = P.get(), *pv = V.get();
+  const long long ps = (long long)heads * m * n, ph = (long long)m * n, vs = (long long)n * E, os = (long long)m * E;
+  node->forward = [=]() {
+    check(mle_gemm_grid(S(), 0, 0, m, hd, n, 1.0f, pp->output, n, ps, ph, pv->output, E, vs, hd, 0.0f, nd->output, E,
+                        os, hd, b, heads, nullptr, 0),
+          "HeadMix forward");
+  };
+  node->backward = [=]() {
+    check(mle_gemm_grid(S(), 0, 1, m, n, hd, 1.0f, nd->grad, E, os, hd, pv->output, E, vs, hd,
+                        (float)mle::accumulate_flag(pp), pp->grad, n, ps, ph, b, heads, nullptr, 0),
+          "HeadMix dP = dO V^T");
+    check(mle_gemm_grid(S(), 1, 0, n, hd, m, 1.0f, pp->output, n, ps, ph, nd->grad, E, os, hd,
+                        (float)mle::accumulate_flag(pv), pv->grad, E, vs, hd, b, heads, nullptr, 0),
+          "HeadMix dV = P^T dO");
+  };
+  std_hooks(node);
+  return node;
+}
+
 graph GraphOperations::SOFTMAX(const graph& X, const int type) { return softmax_node(X, type, false, "Softmax"); }
 graph GraphOperations::SOFTMASK(const graph& X, const int type) { return softmax_node(X, type, true, "Softmask"); }
 graph GraphOperations::RELU(const graph& input) { return act_node(input, MLE_RELU, "ReLU"); }

@@ -82,6 +82,54 @@ def test_gemm(hip, orc, ta, tb, M, N, K, batch, beta):
     assert_close(dC.numpy(), ref, what=f"gemm ta={ta} tb={tb}", **MM)
 
 
+@pytest.mark.parametrize("case", ["scores_nt", "xty_tn", "mix_nn", "tt"])
+@pytest.mark.parametrize("b,heads,seq,hd", [(2, 3, 40, 16), (4, 8, 256, 64)])
+def test_gemm_grid_heads_in_place(hip, orc, case, b, heads, seq, hd):
+    """Per-head products addressed in the [b, seq, heads*hd] layout (two-level
+    batch: batch stride seq*E, head stride hd) against the oracle's bcmm on
+    explicitly headified copies, for every layout."""
+    r = rng(b * 13 + heads + seq + len(case))
+    E = heads * hd
+    X = r.standard_normal((b, seq, E), dtype=np.float32)
+    Y = r.standard_normal((b, seq, E), dtype=np.float32)
+    P = r.standard_normal((b, heads, seq, seq), dtype=np.float32)
+    hf = lambda T: np.ascontiguousarray(T.reshape(b, seq, heads, hd).transpose(0, 2, 1, 3))  # [b, heads, seq, hd]
+    proj = (E, seq * E, hd)            # (ld, outer stride, inner stride) of a head slice of X / Y
+    sq = (seq, heads * seq * seq, seq * seq)
+    # (ta, tb, M, N, K, A device/explicit/addr, B ..., C shape, C addr or None for contiguous [b, heads, M, N])
+    if case == "scores_nt":
+        ta, tb, M, N, K = 0, 1, seq, seq, hd
+        Ad, Ae, Aa, Bd, Be, Ba = X, hf(X), proj, Y, hf(Y), proj
+    elif case == "xty_tn":
+        ta, tb, M, N, K = 1, 0, hd, hd, seq
+        Ad, Ae, Aa, Bd, Be, Ba = X, hf(X), proj, Y, hf(Y), proj
+    elif case == "mix_nn":
+        ta, tb, M, N, K = 0, 0, seq, hd, seq
+        Ad, Ae, Aa, Bd, Be, Ba = P, P, sq, Y, hf(Y), proj
+    else:
+        ta, tb, M, N, K = 1, 1, hd, seq, seq
+        Ad, Ae, Aa, Bd, Be, Ba = X, hf(X), proj, P, P, sq
+    alpha = 0.25
+    ref = r.standard_normal((b, heads, M, N), dtype=np.float32)
+    C0 = ref.copy()
+    orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(np.ascontiguousarray(Ae)), orc.ptr(np.ascontiguousarray(Be)),
+             orc.ptr(ref), b, heads, M, K, N, 1, 3, 3, 3, alpha)
+    if case == "mix_nn":  # result written in the projection layout [b, seq, heads * hd]
+        C0p = np.ascontiguousarray(C0.transpose(0, 2, 1, 3).reshape(b, seq, E))
+        gC = B(hip, C0p)
+        cl, cs, ci = E, seq * E, hd
+    else:
+        gC = B(hip, C0)
+        cl, cs, ci = N, heads * M * N, M * N
+    gA, gB = B(hip, Ad), B(hip, Bd)
+    hip.call("mle_gemm_grid", None, ta, tb, M, N, K, alpha, gA.ptr, *Aa, gB.ptr, *Ba, 1.0, gC.ptr, cl, cs, ci, b, heads,
+             None, 0)
+    got = gC.numpy()
+    if case == "mix_nn":
+        got = got.reshape(b, seq, heads, hd).transpose(0, 2, 1, 3)
+    assert_close(got, ref, what=f"gemm_grid {case}", **MM)
+
+
 @pytest.mark.parametrize("ta,tb,M,N,K,batch,cs", [
     (1, 0, 256, 256, 8192, 1, True),    # dW of a small Linear: split over K
     (1, 0, 512, 1000, 4100, 1, True),   # ragged N and K
