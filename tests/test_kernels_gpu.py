@@ -263,9 +263,10 @@ def test_softmax(hip, orc, bc, rows, cols, axis, causal):
     assert_close(gdx.numpy(), dxz, what="softmax bwd assign", **EW)
 
 
-def test_softmax_xent(hip, orc):
-    r = rng(5)
-    rows, cols, batch = 96, 1000, 4
+@pytest.mark.parametrize("cols", [1000, 1500, 2052, 8000])
+def test_softmax_xent(hip, orc, cols):
+    r = rng(5 + cols)
+    rows, batch = 96, 4
     logits = (r.standard_normal((rows, cols), dtype=np.float32) * 2).astype(np.float32)
     tgt = np.zeros((rows, cols), np.float32)
     tgt[np.arange(rows), r.integers(0, cols, rows)] = 1.0
@@ -712,7 +713,7 @@ def test_elementwise_and_layout(hip, orc):
 
 # ----------------------------------------- cross-entropy from token-id targets
 @pytest.mark.parametrize("batch,clen,max_clen,cols", [(4, 24, 24, 1000), (3, 10, 13, 10), (2, 7, 9, 9001),
-                                                      (2, 16, 16, 8000)])
+                                                      (2, 16, 16, 8000), (3, 9, 11, 1500), (2, 5, 5, 4096)])
 def test_softmax_xent_keys_matches_dense(hip, orc, batch, clen, max_clen, cols):
     """The id path equals the dense one-hot path bit for bit (loss and
     gradient), ids outside [0, cols) included, and matches the oracle."""
