@@ -161,6 +161,30 @@ int mle_gemm_ex(mle_stream stream, int trans_a, int trans_b, int M, int N, int K
                 float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum,
                 const float* bias, void* ws, size_t ws_bytes);
 
+/* mle_gemm_ex over a batch with a bias and a fused column sum per item:
+ * item b adds bias + b*stride_bias and accumulates its column sums of op(B)
+ * into colsum + b*stride_colsum.  Several Linear layers that read the same
+ * input (attention's Q, K and V projections, Engine/transformer.cu:650-652)
+ * run as one launch: their forward (A broadcast with stride_a 0) and their
+ * dW + db (Linear backward, Engine/engine.cu:3553-3560). */
+int mle_gemm_batched_ex(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+                        const float* A, int64_t lda, int64_t stride_a,
+                        const float* B, int64_t ldb, int64_t stride_b, float beta,
+                        float* C, int64_t ldc, int64_t stride_c, int batch,
+                        float* colsum, int64_t stride_colsum, const float* bias, int64_t stride_bias,
+                        void* ws, size_t ws_bytes);
+
+/* C = alpha * sum_{t < terms} op(A + t*stride_a_term) op(B + t*stride_b_term) + beta * C,
+ * the terms reduced in order (deterministic).  The input gradient of several
+ * Linear layers that share an input, dX = sum_t dY_t W_t^T, in one launch
+ * instead of `terms` accumulating bcmmABT calls (Engine/engine.cu:3553).
+ * Needs mle_gemm_sum_ws_bytes(M, N, terms) bytes of workspace. */
+size_t mle_gemm_sum_ws_bytes(int M, int N, int terms);
+int mle_gemm_sum(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+                 const float* A, int64_t lda, int64_t stride_a_term,
+                 const float* B, int64_t ldb, int64_t stride_b_term, float beta,
+                 float* C, int64_t ldc, int terms, void* ws, size_t ws_bytes);
+
 /* mle_gemm_ex over a two-level batch: item (o, i), o < outer, i < inner,
  * reads A at A + o*sa_outer + i*sa_inner (likewise B, C).  With inner = heads
  * and the head stride as *_inner, the per-head products of attention address

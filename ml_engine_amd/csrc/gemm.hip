@@ -32,6 +32,13 @@ struct GemmArgs {
   // the heads of a [batch, seq, heads * dim] tensor in place.
   int inner;
   int64_t sa2, sb2, sc2;
+  // Per batch item bias and column-sum strides (0: shared).
+  int64_t sbias, scs;
+  // Sum of products: when grouped, split s multiplies A + s*gsa by B + s*gsb
+  // over the whole K (the splits are the terms), and the reduce adds them in
+  // term order.
+  int grouped;
+  int64_t gsa, gsb;
 };
 
 __device__ __forceinline__ int64_t batch_off(int64_t z, const GemmArgs& g, int64_t s, int64_t s2) {
@@ -167,11 +174,11 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
   const int m0 = tm * TM, n0 = tn * TN;
   const int64_t z = blockIdx.z / g.splits;
   const int split = blockIdx.z % g.splits;
-  const float* A = g.A + batch_off(z, g, g.sa, g.sa2);
-  const float* B = g.B + batch_off(z, g, g.sb, g.sb2);
+  const float* A = g.A + batch_off(z, g, g.sa, g.sa2) + (g.grouped ? split * g.gsa : 0);
+  const float* B = g.B + batch_off(z, g, g.sb, g.sb2) + (g.grouped ? split * g.gsb : 0);
   float* C = g.C + batch_off(z, g, g.sc, g.sc2);
-  const int kbeg = split * g.kchunk;
-  const int kend = min(g.K, kbeg + g.kchunk);
+  const int kbeg = g.grouped ? 0 : split * g.kchunk;
+  const int kend = g.grouped ? g.K : min(g.K, kbeg + g.kchunk);
   const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
   const uint32_t b_bytes = (uint32_t)(((int64_t)((B_KC ? g.N : g.K) - 1) * g.ldb + (B_KC ? g.K : g.N)) * 4);
   const BufOperand Ab(A, g.lda, a_bytes), Bb(B, g.ldb, b_bytes);
@@ -254,7 +261,7 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
             float* p = C + (int64_t)row * g.ldc + col;
             v = alpha * v;
             if (beta != 0.f) v += beta * *reinterpret_cast<const f32x4*>(p);
-            if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + col);
+            if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + z * g.sbias + col);
             *reinterpret_cast<f32x4*>(p) = v;
           }
         }
@@ -278,7 +285,7 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
               float* p = C + (int64_t)row * g.ldc + col;
               float v = alpha * acc[i][n][r];
               if (beta != 0.f) v += beta * *p;
-              if (g.bias) v += g.bias[col];
+              if (g.bias) v += g.bias[z * g.sbias + col];
               *p = v;
             }
           }
@@ -294,8 +301,8 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
       float cs = 0.f;
 #pragma unroll
       for (int h = 0; h < CS_T; ++h) cs += smem[tid + h * TN];
-      if (split_mode) g.part_cs[(int64_t)split * g.N + n0 + tid] = cs;
-      else g.colsum[n0 + tid] += cs;
+      if (split_mode) g.part_cs[(int64_t)blockIdx.z * g.N + n0 + tid] = cs;
+      else g.colsum[z * g.scs + n0 + tid] += cs;
     }
   }
 }
@@ -337,11 +344,11 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   const int m0 = tm * TM + wm * 64, n0 = tn * TN + wn * 64;  // this wave's 64 x 64 block
   const int64_t z = blockIdx.z / g.splits;
   const int split = blockIdx.z % g.splits;
-  const float* A = g.A + batch_off(z, g, g.sa, g.sa2);
-  const float* B = g.B + batch_off(z, g, g.sb, g.sb2);
+  const float* A = g.A + batch_off(z, g, g.sa, g.sa2) + (g.grouped ? split * g.gsa : 0);
+  const float* B = g.B + batch_off(z, g, g.sb, g.sb2) + (g.grouped ? split * g.gsb : 0);
   float* C = g.C + batch_off(z, g, g.sc, g.sc2);
-  const int kbeg = split * g.kchunk;
-  const int kend = min(g.K, kbeg + g.kchunk);
+  const int kbeg = g.grouped ? 0 : split * g.kchunk;
+  const int kend = g.grouped ? g.K : min(g.K, kbeg + g.kchunk);
   const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
   const uint32_t b_bytes = (uint32_t)(((int64_t)((B_KC ? g.N : g.K) - 1) * g.ldb + (B_KC ? g.K : g.N)) * 4);
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), (short)0, (int)a_bytes, kBufWord3);
@@ -441,7 +448,7 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   if (col < g.N) {
     const float alpha = g.alpha, beta = g.beta;
     f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
-    if (!split_mode && g.bias) b4 = *reinterpret_cast<const f32x4*>(g.bias + col);
+    if (!split_mode && g.bias) b4 = *reinterpret_cast<const f32x4*>(g.bias + z * g.sbias + col);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -473,8 +480,8 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
     if (q == 0 && col < g.N) {
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        if (split_mode) g.part_cs[(int64_t)split * g.N + col + n] = csum[n];
-        else g.colsum[col + n] += csum[n];
+        if (split_mode) g.part_cs[(int64_t)blockIdx.z * g.N + col + n] = csum[n];
+        else g.colsum[z * g.scs + col + n] += csum[n];
       }
     }
   }
@@ -513,21 +520,21 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
       if (VEC) {
         f32x4 v = g.alpha * acc;
         if (g.beta != 0.f) v += g.beta * *reinterpret_cast<const f32x4*>(c);
-        if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + col);
+        if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + b * g.sbias + col);
         *reinterpret_cast<f32x4*>(c) = v;
       } else {
         float v = g.alpha * acc[0];
         if (g.beta != 0.f) v += g.beta * *c;
-        if (g.bias) v += g.bias[col];
+        if (g.bias) v += g.bias[b * g.sbias + col];
         *c = v;
       }
     }
-    if (g.colsum && blockIdx.y == 0 && b == 0) {
+    if (g.colsum && blockIdx.y == 0) {
 #pragma unroll
       for (int j = 0; j < W; ++j) {
         float acc = 0.f;
-        for (int sp = 0; sp < g.splits; ++sp) acc += g.part_cs[(int64_t)sp * g.N + col + j];
-        g.colsum[col + j] += acc;
+        for (int sp = 0; sp < g.splits; ++sp) acc += g.part_cs[(b * g.splits + sp) * g.N + col + j];
+        g.colsum[b * g.scs + col + j] += acc;
       }
     }
   }
@@ -632,32 +639,46 @@ double extent_bytes(int rows, int cols, int64_t ld) { return ((double)(rows - 1)
 static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
                      int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
                      int64_t ldc, int64_t stride_c, int batch, float* colsum, const float* bias, void* ws,
-                     size_t ws_bytes, int inner = 1, int64_t sa2 = 0, int64_t sb2 = 0, int64_t sc2 = 0) {
+                     size_t ws_bytes, int inner = 1, int64_t sa2 = 0, int64_t sb2 = 0, int64_t sc2 = 0,
+                     int64_t sbias = 0, int64_t scs = 0, int terms = 0, int64_t gsa = 0, int64_t gsb = 0) {
   MLE_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "mle_gemm: negative size");
   if (M == 0 || N == 0 || batch == 0) return MLE_OK;
   MLE_CHECK_ARG(C != nullptr && (K == 0 || (A != nullptr && B != nullptr)), "mle_gemm: null operand");
   MLE_CHECK_ARG(ldc >= N, "mle_gemm: ldc %lld < N %d", (long long)ldc, N);
   MLE_CHECK_ARG(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "mle_gemm: leading dimension too small");
-  MLE_CHECK_ARG(colsum == nullptr || batch == 1, "mle_gemm: fused colsum needs batch == 1");
+  MLE_CHECK_ARG(colsum == nullptr || batch == 1 || scs != 0, "mle_gemm: fused colsum over a batch needs a stride");
   const Tile tile = choose_tile(M, N, K, batch);
   MLE_CHECK_ARG((M + tile.tm() - 1) / tile.tm() <= 65535 && batch <= 65535, "mle_gemm: grid too large (M %d, batch %d)",
                 M, batch);
   MLE_CHECK_ARG(inner >= 1 && batch % inner == 0, "mle_gemm: batch %d not a multiple of inner %d", batch, inner);
-  GemmArgs g{A,    B,    C,       colsum,  lda,  ldb,    ldc,  stride_a, stride_b, stride_c, M,  N,  K,
-             alpha, beta, 1,       K,       nullptr, nullptr, bias, inner,    sa2,      sb2,      sc2};
-  int kchunk = K;
-  const int splits = ws ? choose_splits(M, N, K, batch, kchunk) : 1;
-  if (splits > 1) {
-    const size_t need = mle_gemm_ws_bytes(M, N, K, batch);
-    if (ws_bytes >= need) {
-      g.splits = splits;
-      g.kchunk = kchunk;
-      g.part = static_cast<float*>(ws);
-      g.part_cs = g.part + (size_t)splits * batch * M * N;
+  GemmArgs g{A,    B,    C,       colsum,  lda,  ldb,    ldc,  stride_a, stride_b, stride_c, M,    N,   K,
+             alpha, beta, 1,       K,       nullptr, nullptr, bias, inner,    sa2,      sb2,      sc2,      sbias, scs,
+             0,     gsa,  gsb};
+  if (terms > 1) {
+    // Sum of `terms` products: one split per term, reduced in term order.
+    const size_t need = ((size_t)terms * batch * M * N + (size_t)terms * batch * N) * sizeof(float);
+    MLE_CHECK_ARG(ws && ws_bytes >= need, "mle_gemm_sum: workspace of %zu bytes needed", need);
+    MLE_CHECK_ARG(terms * batch <= 65535, "mle_gemm_sum: too many terms");
+    g.grouped = 1;
+    g.splits = terms;
+    g.part = static_cast<float*>(ws);
+    g.part_cs = g.part + (size_t)terms * batch * M * N;
+  } else {
+    int kchunk = K;
+    const int splits = ws ? choose_splits(M, N, K, batch, kchunk) : 1;
+    if (splits > 1) {
+      const size_t need = mle_gemm_ws_bytes(M, N, K, batch);
+      if (ws_bytes >= need) {
+        g.splits = splits;
+        g.kchunk = kchunk;
+        g.part = static_cast<float*>(ws);
+        g.part_cs = g.part + (size_t)splits * batch * M * N;
+      }
     }
   }
   const bool v4 = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
-                  (sa2 % 4 == 0) && (sb2 % 4 == 0) && aligned16(A) && aligned16(B);
+                  (sa2 % 4 == 0) && (sb2 % 4 == 0) && (gsa % 4 == 0) && (gsb % 4 == 0) && aligned16(A) &&
+                  aligned16(B);
   // Buffer loads need the contiguous bound of each operand to be a multiple of
   // 4 and every extent addressable with a 31-bit byte offset.
   const int a_rows = trans_a ? K : M, a_cols = trans_a ? M : K;
@@ -669,12 +690,12 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   const bool cs = colsum != nullptr;
   // The direct kernel stores 16-byte row segments of C (and reads bias as float4).
   const bool direct_ok = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && sc2 % 4 == 0 && aligned16(C) &&
-                         (bias == nullptr || aligned16(bias));
+                         (bias == nullptr || (aligned16(bias) && sbias % 4 == 0));
   dim3 grid((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
   hipStream_t s = as_stream(stream);
   static const char* names[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
   const int which = (trans_a ? 2 : 0) + (trans_b ? 1 : 0);
-  const double flop = 2.0 * M * (double)N * K * batch;
+  const double flop = 2.0 * M * (double)N * K * batch * (terms > 1 ? terms : 1);
   const double bytes = 4.0 * batch * ((double)M * K + (double)K * N + (double)M * N * (beta != 0.f ? 2 : 1));
   {
     ProbeScope probe(names[which], s, flop, bytes);
@@ -686,8 +707,7 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
     }
     if (g.splits > 1) {
       const bool rv = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && sc2 % 4 == 0 && aligned16(C) &&
-                      aligned16(g.part) &&
-                      (!bias || aligned16(bias));
+                      aligned16(g.part) && (!bias || (aligned16(bias) && sbias % 4 == 0));
       const int w = rv ? 4 : 1;
       dim3 rgrid((unsigned)((N / w + 255) / 256), (unsigned)std::min(M, 65535), (unsigned)batch);
       if (rv) split_reduce_kernel<true><<<rgrid, 256, 0, s>>>(g);
@@ -703,7 +723,28 @@ size_t mle_gemm_ws_bytes(int M, int N, int K, int batch) {
   int kchunk;
   const int splits = choose_splits(M, N, K, batch, kchunk);
   if (splits <= 1) return 0;
-  return ((size_t)splits * batch * M * N + (size_t)splits * N) * sizeof(float);
+  return ((size_t)splits * batch * M * N + (size_t)splits * batch * N) * sizeof(float);
+}
+
+size_t mle_gemm_sum_ws_bytes(int M, int N, int terms) {
+  if (terms <= 1) return 0;
+  return ((size_t)terms * M * N + (size_t)terms * N) * sizeof(float);
+}
+
+int mle_gemm_batched_ex(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                        int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta,
+                        float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum, int64_t stride_colsum,
+                        const float* bias, int64_t stride_bias, void* ws, size_t ws_bytes) {
+  return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                   stride_c, batch, colsum, bias, ws, ws_bytes, 1, 0, 0, 0, stride_bias, stride_colsum);
+}
+
+int mle_gemm_sum(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                 int64_t lda, int64_t stride_a_term, const float* B, int64_t ldb, int64_t stride_b_term, float beta,
+                 float* C, int64_t ldc, int terms, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(terms >= 1, "mle_gemm_sum: terms %d", terms);
+  return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, nullptr,
+                   nullptr, ws, ws_bytes, 1, 0, 0, 0, 0, 0, terms, stride_a_term, stride_b_term);
 }
 
 int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,

@@ -846,6 +846,82 @@ graph Linear::forward(const graph& X) {
 }
 
 // ---------------------------------------------------------------------------
+// Sibling Linear fusion (see engine.h).
+namespace mle {
+
+namespace {
+bool g_sibling_fusion = true;
+}
+
+void set_sibling_fusion(bool on) { g_sibling_fusion = on; }
+
+bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Linear*>& layers) {
+  const size_t n = outs.size();
+  if (!g_sibling_fusion || n < 2 || layers.size() != n) return false;
+  NodeBackProp* x = outs[0]->inputs.size() == 1 ? outs[0]->inputs[0].get() : nullptr;
+  if (!x) return false;
+  const Linear* l0 = layers[0];
+  for (size_t i = 0; i < n; ++i) {
+    if (outs[i]->inputs.size() != 1 || outs[i]->inputs[0].get() != x) return false;
+    if (layers[i]->in_features() != l0->in_features() || layers[i]->out_features() != l0->out_features() ||
+        layers[i]->has_bias() != l0->has_bias())
+      return false;
+    for (int d = 0; d < 4; ++d)
+      if (outs[i]->dim[d] != outs[0]->dim[d]) return false;
+  }
+  // Equal strides between consecutive layers, in elements.
+  auto stride_of = [&](auto get, long long& st) {
+    st = (long long)(get(1) - get(0));
+    if (st <= 0) return false;
+    for (size_t i = 2; i < n; ++i)
+      if ((long long)(get(i) - get(i - 1)) != st) return false;
+    return st % 4 == 0;
+  };
+  long long dw, dgrad;
+  const bool has_bias = l0->has_bias();
+  if (!stride_of([&](size_t i) { return layers[i]->W1.output; }, dw) ||
+      !stride_of([&](size_t i) { return outs[i]->grad; }, dgrad))
+    return false;
+
+  const int nl = (int)n;
+  const int p = l0->out_features(), k = l0->in_features();
+  const long long rows = outs[0]->total / p;
+  AdamParameter* W0 = &layers[0]->W1;
+  NodeBackProp* o0 = outs[0].get();
+  const size_t ws_dx = mle_gemm_sum_ws_bytes((int)rows, k, nl);
+  const size_t ws_dw = mle_gemm_ws_bytes(k, p, (int)rows, 1);
+  const size_t ws_bytes = std::max(ws_dx, ws_dw);
+  void* ws = gemm_workspace(ws_bytes);
+  auto bwd_count = std::make_shared<int>(0);
+  const str name = outs[0]->op_name;
+  for (size_t i = 0; i < n; ++i) {
+    NodeBackProp* oi = outs[i].get();
+    AdamParameter* Wi = &layers[i]->W1;
+    AdamParameter* Bi = &layers[i]->B1;
+    const str name_i = outs[i]->op_name;
+    // The forward stays one GEMM per layer: each 8192 x 512 projection already
+    // fills the chip, and a batch of three measured slower (a half-empty last
+    // round of tiles).  Batching the dW products measured slower as well.
+    outs[i]->backward = [=]() {
+      check(mle_gemm_ex(stream(), 1, 0, k, p, (int)rows, 1.0f, x->output, k, 0, oi->grad, p, 0, 1.0f, Wi->grad, p, 0,
+                        1, has_bias ? Bi->grad : nullptr, nullptr, ws, ws_bytes),
+            "MatMul... X^T*dZ in " + name_i + " backward");
+      if (++(*bwd_count) < nl) return;
+      *bwd_count = 0;
+      // Every sibling's gradient is complete now (this is the last of their
+      // backward calls): dX = sum_i dZ_i W_i^T in one launch.
+      const float beta = (float)accumulate_flag(x);
+      check(mle_gemm_sum(stream(), 0, 1, (int)rows, k, p, 1.0f, o0->grad, p, dgrad, W0->output, p, dw, beta, x->grad,
+                         k, nl, ws, ws_bytes),
+            "Fused sum dZ_i*W_i^T in " + name + " backward");
+    };
+  }
+  return true;
+}
+
+}  // namespace mle
+
+// ---------------------------------------------------------------------------
 // Convolute2D (Engine/engine.cu:3723-3817).  W1 [out, inp, c, d], B1 [1, out, 1, 1].
 Convolute2D::Convolute2D(int Input, int Output, int C, int D, int stride_, int padding, str param)
     : inp(Input),

@@ -274,10 +274,27 @@ class Linear {
   str op_name = "Linear Layer";
   Linear(const int input, const int output, const str name = "", const bool bias = true);
   graph forward(const graph& X);
+  bool has_bias() const { return bias; }
+  int in_features() const { return in; }
+  int out_features() const { return out; }
   void save(std::ofstream& f) const;
   void load(std::ifstream& f);
   void operator=(const Linear& other);
 };
+
+// Horizontal fusion of Linear layers that read the same input (e.g. the Q, K
+// and V projections of attention).  `outs` are the layers' forward nodes.
+// When the layers' weights and their outputs' gradients sit at equal strides
+// in their arenas, the nodes' backward lambdas are rewired so that each still
+// computes its own dW_i, db_i and the last to run computes
+// dX = sum_i dY_i W_i^T in one grouped launch (instead of one accumulating
+// GEMM per layer).  Returns false (and changes nothing) otherwise.
+namespace mle {
+bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Linear*>& layers);
+// Global switch for fuse_sibling_linears (on by default); graphs built while it
+// is off keep one GEMM per layer.
+void set_sibling_fusion(bool on);
+}  // namespace mle
 
 class Convolute2D {
  public:

@@ -156,6 +156,8 @@ extern "C" {
 
 void mle_model_set_lazy_zero(int on) { mle::set_lazy_zero(on != 0); }
 
+void mle_model_set_fusion(int on) { mle::set_sibling_fusion(on != 0); }
+
 void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad) {
   mle::quirks().bmmabt_reference_grad = bmmabt_reference_grad != 0;
   mle::quirks().broadcast_channel_reference_grad = broadcast_channel_reference_grad != 0;

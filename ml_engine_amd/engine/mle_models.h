@@ -25,6 +25,10 @@ void mle_model_set_seed(unsigned long long seed);
 /* 1 (default): zero_grad marks node gradients clear and first writers assign;
  * 0: zero_grad fills them. */
 void mle_model_set_lazy_zero(int on);
+/* Horizontal fusion of Linear layers that share an input (attention's Q, K, V
+ * projections: their input gradient is one grouped sum-of-products GEMM).
+ * On by default; applies to models created afterwards. */
+void mle_model_set_fusion(int on);
 int mle_model_num_params(void* h);
 const char* mle_model_param_name(void* h, int i);
 long long mle_model_param_numel(void* h, int i);

@@ -37,6 +37,8 @@ graph MultiHeadAttention::forward(const graph& X, const bool mask) {
   auto Q = q.forward(X);
   auto K = k.forward(X);
   auto V = v.forward(X);
+  // The three projections read X: one launch each way when the arenas allow.
+  qkv_fused = mle::fuse_sibling_linears({Q, K, V}, {&q, &k, &v});
   auto scaled = GraphOperations::HeadScores(Q, K, num_heads, 1.0f / sqrtf((float)head_dim));
   auto weights = (mask && scaled->dim[2] > 1) ? GraphOperations::SOFTMASK(scaled, 1) : GraphOperations::SOFTMAX(scaled, 1);
   auto concat = GraphOperations::HeadMix(weights, V, num_heads);

@@ -12,6 +12,7 @@ class MultiHeadAttention {
   int hidden, embed_dim, num_heads, head_dim;
   str name;
   Linear q, k, v, o;
+  bool qkv_fused = false;  // set by forward: dX of the Q, K, V projections is one grouped GEMM
   MultiHeadAttention(const int embed_dim, const int hidden, const int num_heads, const str& name = "MHA");
   graph forward(const graph& X, const bool mask = true);
   void save(std::ofstream& f) const;

@@ -56,6 +56,9 @@ SIGNATURES: dict[str, tuple] = {
     "mle_gemm": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P]),
     "mle_gemm_ws_bytes": (SZ, [I, I, I, I]),
     "mle_gemm_ex": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P, P, P, SZ]),
+    "mle_gemm_batched_ex": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P, I64, P, I64, P, SZ]),
+    "mle_gemm_sum_ws_bytes": (SZ, [I, I, I]),
+    "mle_gemm_sum": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I, P, SZ]),
     "mle_gemm_grid": (I, [P, I, I, I, I, I, F, P, I64, I64, I64, P, I64, I64, I64, F, P, I64, I64, I64, I, I, P, SZ]),
     "mle_colsum": (I, [P, P, SZ, I, P, F]),
     "mle_channel_sum": (I, [P, P, I, I, SZ, I, P]),

@@ -21,6 +21,7 @@ _SIGS = {
     "mle_model_set_quirks": (None, [I, I]),
     "mle_model_set_seed": (None, [C.c_ulonglong]),
     "mle_model_set_lazy_zero": (None, [I]),
+    "mle_model_set_fusion": (None, [I]),
     "mle_model_num_params": (I, [P]),
     "mle_model_param_name": (C.c_char_p, [P, I]),
     "mle_model_param_numel": (LL, [P, I]),
@@ -59,11 +60,13 @@ def lib() -> C.CDLL:
 class Model:
     """One configuration built with the engine (parameters in the flat arena)."""
 
-    def __init__(self, kind: str, dims, seed: int = 0, reference_quirks: bool = True, lazy_zero: bool = True):
+    def __init__(self, kind: str, dims, seed: int = 0, reference_quirks: bool = True, lazy_zero: bool = True,
+                 fuse: bool = True):
         L = lib()
         hip.init(0)
         L.mle_model_set_quirks(int(reference_quirks), int(reference_quirks))
         L.mle_model_set_lazy_zero(int(lazy_zero))
+        L.mle_model_set_fusion(int(fuse))
         L.mle_model_set_seed(seed)
         arr = (LL * len(dims))(*[int(d) for d in dims])
         self.h = L.mle_model_create(KIND[kind], arr, len(dims))

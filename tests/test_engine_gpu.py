@@ -7,6 +7,8 @@ gradients: at t = 1 the step is lr * g/(|g| + eps), so a gradient element whose
 sign sits inside fp32 noise would flip a whole lr-sized step and hide what is
 being tested (the fused update over the parameter arena).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -148,6 +150,54 @@ def test_flat_clip_adamw(hip, orc):
         assert_close(m.get(i, 0), ref_p[i], what=f"p {i}", **EW)
         assert m.t(i) == cfg.steps + 1
     m.close()
+
+
+def _probe_step(hip, m, lr, fam):
+    """One full step with the launch probe armed for one GEMM family; returns
+    the number of launches of that family."""
+    n, ms, fl, by = C.c_int(0), C.c_double(0), C.c_double(0), C.c_double(0)
+    hip.call("mle_probe_arm", fam.encode())
+    m.step(lr, STEP_ALL)
+    m.sync()
+    hip.call("mle_probe_read", C.byref(n), C.byref(ms), C.byref(fl), C.byref(by))
+    hip.call("mle_probe_arm", None)
+    return n.value
+
+
+@pytest.mark.parametrize("quirks", [True, False])
+def test_block_qkv_fusion(hip, quirks):
+    """The fused input gradient of the Q/K/V projections (one grouped
+    sum-of-products GEMM) agrees with one accumulating GEMM per projection and
+    removes exactly two NT launches (the NN and TN counts are unchanged)."""
+    cfg = BlockConfig(batch=4, seq=64, d_model=128, heads=4, ffn=256, vocab=300)
+    ids, tgt, params = block_data(cfg, seed=5)
+    runs = {}
+    for fuse in (True, False):
+        m = Model("block", cfg.dims(), reference_quirks=quirks, fuse=fuse)
+        for i, p in enumerate(params):
+            m.set(i, p)
+        m.input(0, ids)
+        m.input(1, tgt)
+        counts = {}
+        for fam in ("gemm_nn", "gemm_nt", "gemm_tn"):
+            for i, p in enumerate(params):  # same starting point for every probed step
+                m.set(i, p)
+                m.set(i, np.zeros_like(p), 2)
+                m.set(i, np.zeros_like(p), 3)
+            counts[fam] = _probe_step(hip, m, cfg.lr, fam)
+        runs[fuse] = (counts, m.loss, [m.get(i, 1) for i in range(len(params))])
+        m.close()
+    (cf, lf, gf), (cu, lu, gu) = runs[True], runs[False]
+    for fam, d in (("gemm_nn", 0), ("gemm_nt", 2), ("gemm_tn", 0)):
+        assert cu[fam] - cf[fam] == d, (fam, cu[fam], cf[fam])
+    assert abs(lf - lu) <= 1e-5 * abs(lu)
+    for i in range(len(params)):
+        # Biases are judged on the scale of their layer's weight gradient (the
+        # query bias gradient is zero up to rounding by symmetry).
+        scale = float(np.abs(gu[i]).max())
+        if i >= 2 and i % 2 == 0:
+            scale = max(scale, float(np.abs(gu[i - 1]).max()))
+        assert np.abs(gf[i] - gu[i]).max() <= 1e-4 * scale, (i, np.abs(gf[i] - gu[i]).max(), scale)
 
 
 def test_block_full_size_properties(hip):

@@ -162,6 +162,98 @@ def test_gemm_split_k(hip, orc, ta, tb, M, N, K, batch, cs):
         assert_close(dcs.numpy(), cs0 + bsum, what="split-K colsum", **EW)
 
 
+@pytest.mark.parametrize("ta,tb,M,N,K,batch,with_ws", [
+    (0, 0, 1000, 512, 512, 3, False),   # sibling projections: X broadcast, W_i, b_i strided
+    (0, 0, 257, 132, 100, 2, True),
+    (1, 0, 512, 512, 8192, 3, True),    # sibling dW_i = X^T dY_i, db_i: split over K
+    (1, 0, 128, 200, 3000, 3, True),
+    (1, 0, 96, 64, 300, 3, False),
+])
+def test_gemm_batched_ex(hip, orc, ta, tb, M, N, K, batch, with_ws):
+    """Batched GEMM whose items carry their own bias and column-sum vectors
+    (stride_bias / stride_colsum), with item strides that leave gaps between
+    items as the parameter arena does."""
+    r = rng(M + 3 * N + K + batch)
+    gap = 8                                            # floats between consecutive items
+    a_shape = (K, M) if ta else (M, K)                 # A broadcast over the batch (stride 0)
+    A = r.standard_normal(a_shape, dtype=np.float32)
+    b_item = (N, K) if tb else (K, N)
+    sb = int(np.prod(b_item)) + gap
+    Bflat = r.standard_normal(batch * sb, dtype=np.float32)
+    Bi = [Bflat[i * sb:i * sb + int(np.prod(b_item))].reshape(b_item) for i in range(batch)]
+    sc = M * N + gap
+    Cflat = r.standard_normal(batch * sc, dtype=np.float32)
+    beta = 1.0 if ta else 0.0
+    ref = []
+    for i in range(batch):
+        c = Cflat[i * sc:i * sc + M * N].reshape(M, N).copy()
+        orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(np.ascontiguousarray(A)), orc.ptr(np.ascontiguousarray(Bi[i])),
+                 orc.ptr(c), 1, 1, M, K, N, int(beta != 0), 3, 3, 3, 0.5)
+        ref.append(c)
+    svec = N + 4
+    gA, gB, gC = B(hip, A), B(hip, Bflat), B(hip, Cflat)
+    L = hip.lib()
+    need = L.mle_gemm_ws_bytes(M, N, K, batch) if with_ws else 0
+    ws = hip.Buffer(max(need, 4)) if with_ws else None
+    if ta:  # dW-style: fused column sums of each B_i into its own vector
+        cs0 = r.standard_normal(batch * svec, dtype=np.float32)
+        gcs = B(hip, cs0)
+        hip.call("mle_gemm_batched_ex", None, ta, tb, M, N, K, 0.5, gA.ptr, M, 0, gB.ptr, K if tb else N, sb, beta,
+                 gC.ptr, N, sc, batch, gcs.ptr, svec, None, 0, ws.ptr if ws else None, need)
+        cs = gcs.numpy()
+        for i in range(batch):
+            want = cs0[i * svec:i * svec + N] + Bi[i].astype(np.float64).sum(1 if tb else 0)
+            assert_close(cs[i * svec:i * svec + N], want, what=f"colsum item {i}", **EW)
+            assert np.array_equal(cs[i * svec + N:(i + 1) * svec], cs0[i * svec + N:(i + 1) * svec]), "gap written"
+    else:   # forward-style: per-item bias
+        bias = r.standard_normal(batch * svec, dtype=np.float32)
+        gbias = B(hip, bias)
+        hip.call("mle_gemm_batched_ex", None, ta, tb, M, N, K, 0.5, gA.ptr, M if ta else K, 0, gB.ptr,
+                 K if tb else N, sb, beta, gC.ptr, N, sc, batch, None, 0, gbias.ptr, svec, ws.ptr if ws else None, need)
+        for i in range(batch):
+            ref[i] += bias[i * svec:i * svec + N]
+    got = gC.numpy()
+    for i in range(batch):
+        assert_close(got[i * sc:i * sc + M * N].reshape(M, N), ref[i], what=f"batched_ex item {i}", **MM)
+        assert np.array_equal(got[i * sc + M * N:(i + 1) * sc], Cflat[i * sc + M * N:(i + 1) * sc]), "gap written"
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K,terms", [
+    (0, 1, 8192, 512, 512, 3),   # dX = sum_i dY_i W_i^T of sibling projections
+    (0, 1, 1000, 132, 260, 3),
+    (0, 0, 300, 200, 100, 2),
+    (1, 0, 64, 96, 500, 4),
+    (0, 1, 200, 64, 64, 1),
+])
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_gemm_sum(hip, orc, ta, tb, M, N, K, terms, beta):
+    """C = alpha * sum_t A_t B_t + beta C over term-strided operands."""
+    r = rng(M + N + 5 * K + terms)
+    gap = 4
+    a_item = (K, M) if ta else (M, K)
+    b_item = (N, K) if tb else (K, N)
+    sa, sb = int(np.prod(a_item)) + gap, int(np.prod(b_item)) + 2 * gap
+    Af = r.standard_normal(terms * sa, dtype=np.float32)
+    Bf = r.standard_normal(terms * sb, dtype=np.float32)
+    C0 = r.standard_normal((M, N), dtype=np.float32)
+    ref = C0.copy() if beta else np.zeros((M, N), np.float32)
+    for t in range(terms):
+        At = np.ascontiguousarray(Af[t * sa:t * sa + int(np.prod(a_item))].reshape(a_item))
+        Bt = np.ascontiguousarray(Bf[t * sb:t * sb + int(np.prod(b_item))].reshape(b_item))
+        orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(At), orc.ptr(Bt), orc.ptr(ref), 1, 1, M, K, N, 1, 3, 3, 3, 0.75)
+    L = hip.lib()
+    need = L.mle_gemm_sum_ws_bytes(M, N, terms)
+    ws = hip.Buffer(max(need, 4))
+    gA, gB, gC = B(hip, Af), B(hip, Bf), B(hip, C0)
+    hip.call("mle_gemm_sum", None, ta, tb, M, N, K, 0.75, gA.ptr, M if ta else K, sa, gB.ptr, K if tb else N, sb, beta,
+             gC.ptr, N, terms, ws.ptr, need)
+    assert_close(gC.numpy(), ref, what=f"gemm_sum terms={terms}", **MM)
+    if terms > 1:
+        with pytest.raises(hip.MLEError):
+            hip.call("mle_gemm_sum", None, ta, tb, M, N, K, 0.75, gA.ptr, M if ta else K, sa, gB.ptr,
+                     K if tb else N, sb, beta, gC.ptr, N, terms, ws.ptr, need - 4)
+
+
 @pytest.mark.parametrize("M,N,K", [(100, 40, 300), (40, 40, 500), (300, 90, 77), (2048, 4096, 40), (64, 130, 300),
                                    (2048, 4096, 48), (2000, 1700, 48), (1000, 2052, 4112)])
 def test_gemm_colsum_tiles(hip, orc, M, N, K):
