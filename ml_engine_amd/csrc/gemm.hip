@@ -487,6 +487,200 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   }
 }
 
+// Tile (tm, tn) and batch item z of work item L of a persistent launch over
+// `items` = gx * gy * batch tiles.  The same XCD-aware order as tile_of: item
+// L runs on XCD L % 8 (the grid is a multiple of 8 workgroups, dispatched
+// round-robin), XCD x owns a contiguous logical range, walked in groups of 8
+// tile-rows per batch item.  A bijection on [0, items).
+__device__ __forceinline__ void item_tile(int L, int items, int gx, int gy, int& tm, int& tn, int& z) {
+  const int q = items / kXcds, r = items % kXcds, x = L % kXcds;
+  const int logical = x * q + min(x, r) + L / kXcds;
+  const int T = gx * gy;
+  z = logical / T;
+  const int t = logical - z * T;
+  const int per_group = kGroupRows * gx;
+  const int grp = t / per_group;
+  const int first_m = grp * kGroupRows;
+  const int rows = min(gy - first_m, kGroupRows);
+  const int in_group = t - grp * per_group;
+  tm = first_m + in_group % rows;
+  tn = in_group / rows;
+}
+
+// Persistent register-direct GEMM for grids of more 128 x 128 tiles than two
+// per CU: two workgroups per CU walk work items L = blockIdx.x + j * gridDim.x.
+// Each wave computes its 64 x 64 block of a tile exactly as
+// gemm_direct_kernel does (same fragment loads, same MFMA order, so the same
+// bits).  The operand loads run D - 1 stages ahead straight across tile
+// boundaries: in the last D stages of a tile they fetch the next tile's first
+// D - 1 stages (offsets selected without branches), so a new tile starts with
+// its operands in registers instead of waiting for a prologue, and no
+// workgroup is launched or retired per tile.  One loop with a straight-line
+// body: every pass issues the same loads in the same places, so the
+// compiler's load waits stay tight.  At a tile boundary the wave writes its
+// block from the accumulators through a buffer resource (elements outside
+// the matrix get offset kBufOOB: the store is dropped, a read returns zeros);
+// those stores are issued after the next tile's first loads, so the waits
+// for those loads never include them.
+// Measured on MI355X against the per-tile launch of gemm_direct_kernel:
+// equal or faster on every C4 shape with more than 512 tiles (LM-head
+// forward 604 -> 581 us, 8192 x 2048 x 512 NT 150 -> 135 us).  A variant
+// with one workgroup per CU and a fifth wave writing C from an LDS staging
+// tile was slower (one compute wave per SIMD hides less load latency).
+// Requires: one split, no column sum, K a positive multiple of KD * D, C
+// addressable by a buffer resource, and the direct kernel's alignment
+// conditions (checked on the host).
+template <int TA, int TB, int KD, int D>
+__global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, int gy, int items) {
+  constexpr bool A_MC = TA != 0;
+  constexpr bool B_KC = TB != 0;
+  constexpr int S = KD / 4;   // MFMA steps (and loads per operand) per stage
+  constexpr int H = KD / 16;  // loads per 16-row block of a k-contiguous operand
+  static_assert(D >= 2 && (KD == 16 || KD == 32), "unsupported stage shape");
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int G = gridDim.x;
+
+  const int lr = lane & 15, q = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int nk = g.K / KD;
+  const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
+  const uint32_t b_bytes = (uint32_t)(((int64_t)((B_KC ? g.N : g.K) - 1) * g.ldb + (B_KC ? g.K : g.N)) * 4);
+  const uint32_t a_step = 4u * (A_MC ? KD * (uint32_t)g.lda : KD);
+  const uint32_t b_step = 4u * (B_KC ? KD : KD * (uint32_t)g.ldb);
+  const uint32_t c_bytes = (uint32_t)(((int64_t)(g.M - 1) * g.ldc + g.N) * 4);
+
+  // Buffer resources and this lane's byte offsets at stage 0 of an item (the
+  // direct kernel's offsets with kbeg = 0).  Past the last item the first
+  // item is decoded and every offset becomes kBufOOB, so those (never
+  // consumed) loads return zeros.
+  auto locate = [&](int L, __amdgpu_buffer_rsrc_t& ra, __amdgpu_buffer_rsrc_t& rb, uint32_t(&ao)[S],
+                    uint32_t(&bo)[S]) {
+    const bool live = L < items;
+    int tm, tn, z;
+    item_tile(live ? L : (int)blockIdx.x, items, gx, gy, tm, tn, z);
+    const float* A = g.A + batch_off(z, g, g.sa, g.sa2);
+    const float* B = g.B + batch_off(z, g, g.sb, g.sb2);
+    ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), (short)0, (int)a_bytes, kBufWord3);
+    rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), (short)0, (int)b_bytes, kBufWord3);
+    const int m0 = tm * 128 + wm * 64, n0 = tn * 128 + wn * 64;
+    const int kq = S * q;
+#pragma unroll
+    for (int x = 0; x < S; ++x) {
+      if (!A_MC) {
+        const int row = m0 + 16 * (x / H) + lr;
+        ao[x] = live && row < g.M ? (uint32_t)(row * (int)g.lda + kq + 4 * (x % H)) * 4u : kBufOOB;
+      } else {
+        ao[x] = live && m0 + 4 * lr < g.M ? (uint32_t)((kq + x) * (int)g.lda + m0 + 4 * lr) * 4u : kBufOOB;
+      }
+      if (B_KC) {
+        const int col = n0 + 4 * lr + x / H;
+        bo[x] = live && col < g.N ? (uint32_t)(col * (int)g.ldb + kq + 4 * (x % H)) * 4u : kBufOOB;
+      } else {
+        bo[x] = live && n0 + 4 * lr < g.N ? (uint32_t)((kq + x) * (int)g.ldb + n0 + 4 * lr) * 4u : kBufOOB;
+      }
+    }
+  };
+  __amdgpu_buffer_rsrc_t ra, rb, ra_n, rb_n;  // current and next item
+  uint32_t a_off[S], b_off[S], a_nx[S], b_nx[S];
+  locate(blockIdx.x, ra, rb, a_off, b_off);
+  locate(blockIdx.x + G, ra_n, rb_n, a_nx, b_nx);
+
+  // Stage ks of the current item, or stage kn of the next one when `nxt`.
+  auto load = [&](bool nxt, int ks, int kn, f32x4(&fa)[S], f32x4(&fb)[S]) {
+    const __amdgpu_buffer_rsrc_t xa = nxt ? ra_n : ra, xb = nxt ? rb_n : rb;
+    const uint32_t da = (uint32_t)(nxt ? kn : ks) * a_step, db = (uint32_t)(nxt ? kn : ks) * b_step;
+#pragma unroll
+    for (int x = 0; x < S; ++x) {
+      const uint32_t oa = (nxt ? a_nx[x] : a_off[x]) + da, ob = (nxt ? b_nx[x] : b_off[x]) + db;
+      fa[x] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xa, (int)oa, 0, 0));
+      fb[x] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xb, (int)ob, 0, 0));
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto av = [&](const f32x4(&fa)[S], int i, int j) { return A_MC ? fa[j][i] : fa[i * H + j / 4][j % 4]; };
+  auto bv = [&](const f32x4(&fb)[S], int n, int j) { return B_KC ? fb[n * H + j / 4][j % 4] : fb[j][n]; };
+  auto mfma = [&](const f32x4(&fa)[S], const f32x4(&fb)[S]) {
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(av(fa, i, j), bv(fb, n, j), acc[i][n], 0, 0, 0);
+  };
+
+  // Stage kt of every item lives in register set kt % D (nk is a multiple of
+  // D, so each item starts at set 0).
+  f32x4 fa[D][S], fb[D][S];
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load(false, s, 0, fa[s], fb[s]);
+  int kt = 0, c_item = blockIdx.x;
+  for (;;) {
+    const bool last = kt + D == nk;  // the item's last D stages
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int ls = kt + s + D - 1;  // stage to fetch; past nk it is the next item's
+      load(s > 0 && last, ls, ls - nk, fa[(s + D - 1) % D], fb[(s + D - 1) % D]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(fa[s], fb[s]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!last) {
+      kt += D;
+      continue;
+    }
+    {
+      // Epilogue: lane (lr, q) holds C[row(i, 4q + r)][4 lr + n] of the
+      // wave's block in acc[i][n][r] (the direct kernel's permutation), so
+      // each (i, r) is one 16-byte store of 4 consecutive columns.
+      int tm, tn, z;
+      item_tile(c_item, items, gx, gy, tm, tn, z);
+      float* C = g.C + batch_off(z, g, g.sc, g.sc2);
+      const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, (int)c_bytes, kBufWord3);
+      const int m0 = tm * 128 + wm * 64, col = tn * 128 + wn * 64 + 4 * lr;
+      f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
+      if (g.bias && col < g.N) b4 = *reinterpret_cast<const f32x4*>(g.bias + z * g.sbias + col);
+      const float alpha = g.alpha, beta = g.beta;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + (A_MC ? 4 * (4 * q + r) + i : 16 * i + 4 * q + r);
+          const uint32_t off = row < g.M && col < g.N ? (uint32_t)(row * (int)g.ldc + col) * 4u : kBufOOB;
+          f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+          v = alpha * v;
+          if (beta != 0.f)
+            v += beta * __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, (int)off, 0, 0));
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v + b4), rc, (int)off, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    c_item += G;
+    if (c_item >= items) break;
+    kt = 0;
+    ra = ra_n;
+    rb = rb_n;
+#pragma unroll
+    for (int x = 0; x < S; ++x) {
+      a_off[x] = a_nx[x];
+      b_off[x] = b_nx[x];
+    }
+    locate(c_item + G, ra_n, rb_n, a_nx, b_nx);
+  }
+}
+
 // C = alpha * sum_s part[s] + beta * C and colsum += sum_s part_cs[s], in split
 // order.  Grid: x over column groups of W (4 with VEC, else 1) columns, y over
 // rows (looping when M > 65535), z over batch items -- no integer division.
@@ -615,10 +809,33 @@ void launch_direct(hipStream_t s, const GemmArgs& g, dim3 grid, bool cs) {
   else gemm_direct_kernel<TA, TB, false, 16, 3, 2><<<grid, NT, 0, s>>>(g);
 }
 
+// Compute units of the current device (queried once per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int TA, int TB>
 void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, bool cs, bool direct_ok) {
   if (t.direct && direct_ok && vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0) {
-    launch_direct<TA, TB>(s, g, grid, cs);
+    // More tiles than two per CU, one split, no column sum: the persistent
+    // kernel (two workgroups per CU, tiles streamed without per-tile
+    // prologues).
+    const long long items = (long long)grid.x * grid.y * grid.z;
+    const int ncu = cu_count();
+    const bool c_buf = ((double)(g.M - 1) * (double)g.ldc + g.N) * 4.0 < 2147483648.0 - 64;
+    if (g.splits == 1 && !cs && g.K >= 64 && g.K % 64 == 0 && items > 2 * ncu && items < (1LL << 30) && c_buf) {
+      gemm_stream_kernel<TA, TB, 16, 4><<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
+    } else {
+      launch_direct<TA, TB>(s, g, grid, cs);
+    }
   } else if (t.wm == 4 && t.wn == 4) {
     if (t.kd == 16) launch_t<TA, TB, 4, 4, 16>(s, g, grid, vec, cs);
     else launch_t<TA, TB, 4, 4, 32>(s, g, grid, vec, cs);

@@ -57,6 +57,14 @@ GEMM_CASES = [
     (1, 1, 2060, 2004, 64, 1),
     # N not a multiple of 4 with float4-able operands: not the direct kernel
     (0, 1, 2000, 1702, 48, 1),
+    # persistent kernel (more 128 x 128 tiles than two per CU, K % 64 == 0): each
+    # workgroup walks several tiles, the loads of the next tile overlapping
+    # the last stages of the current one; ragged edges and batches
+    (0, 0, 4100, 4000, 64, 1),
+    (0, 1, 3000, 2900, 192, 1),
+    (1, 0, 2500, 4096, 128, 1),
+    (1, 1, 2100, 2052, 64, 2),
+    (0, 0, 1000, 1000, 256, 9),
 ]
 
 
@@ -164,6 +172,7 @@ def test_gemm_split_k(hip, orc, ta, tb, M, N, K, batch, cs):
 
 @pytest.mark.parametrize("ta,tb,M,N,K,batch,with_ws", [
     (0, 0, 1000, 512, 512, 3, False),   # sibling projections: X broadcast, W_i, b_i strided
+    (0, 0, 4000, 1536, 128, 3, False),  # persistent kernel with per-item bias
     (0, 0, 257, 132, 100, 2, True),
     (1, 0, 512, 512, 8192, 3, True),    # sibling dW_i = X^T dY_i, db_i: split over K
     (1, 0, 128, 200, 3000, 3, True),
