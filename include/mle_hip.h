@@ -175,7 +175,9 @@ int mle_gemm_batched_ex(mle_stream stream, int trans_a, int trans_b, int M, int 
                         void* ws, size_t ws_bytes);
 
 /* C = alpha * sum_{t < terms} op(A + t*stride_a_term) op(B + t*stride_b_term) + beta * C,
- * the terms reduced in order (deterministic).  The input gradient of several
+ * the terms summed in order (deterministic: on the register-direct kernel
+ * they extend one K loop; otherwise each term is a split whose partial
+ * products are reduced in term order).  The input gradient of several
  * Linear layers that share an input, dX = sum_t dY_t W_t^T, in one launch
  * instead of `terms` accumulating bcmmABT calls (Engine/engine.cu:3553).
  * Needs mle_gemm_sum_ws_bytes(M, N, terms) bytes of workspace. */

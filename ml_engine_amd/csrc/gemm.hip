@@ -39,6 +39,9 @@ struct GemmArgs {
   // term order.
   int grouped;
   int64_t gsa, gsb;
+  // Sum of products folded into K (register-direct kernel, one split): stage
+  // kt of the K loop reads term kt / (K / KD) of A + t*gsa and B + t*gsb.
+  int kterms;
 };
 
 __device__ __forceinline__ int64_t batch_off(int64_t z, const GemmArgs& g, int64_t s, int64_t s2) {
@@ -326,7 +329,7 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
 // therefore writes 16-byte row segments straight from the accumulators.
 // A wave issues KD/4 loads per operand per stage; the two waves that share a
 // row (column) panel hit the same lines, which the L1 serves.
-template <int TA, int TB, bool COLSUM, int KD, int D, int OCC>
+template <int TA, int TB, bool COLSUM, int KD, int D, int OCC, bool TERMS = false>
 __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
@@ -349,11 +352,17 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   float* C = g.C + batch_off(z, g, g.sc, g.sc2);
   const int kbeg = g.grouped ? 0 : split * g.kchunk;
   const int kend = g.grouped ? g.K : min(g.K, kbeg + g.kchunk);
-  const uint32_t a_bytes = (uint32_t)(((int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
-  const uint32_t b_bytes = (uint32_t)(((int64_t)((B_KC ? g.N : g.K) - 1) * g.ldb + (B_KC ? g.K : g.N)) * 4);
+  // With TERMS the resources span every term (the host checks the extent).
+  const int64_t a_terms = TERMS ? (int64_t)(g.kterms - 1) * g.gsa : 0;
+  const int64_t b_terms = TERMS ? (int64_t)(g.kterms - 1) * g.gsb : 0;
+  const uint32_t a_bytes =
+      (uint32_t)((a_terms + (int64_t)((A_MC ? g.K : g.M) - 1) * g.lda + (A_MC ? g.M : g.K)) * 4);
+  const uint32_t b_bytes =
+      (uint32_t)((b_terms + (int64_t)((B_KC ? g.N : g.K) - 1) * g.ldb + (B_KC ? g.K : g.N)) * 4);
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), (short)0, (int)a_bytes, kBufWord3);
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), (short)0, (int)b_bytes, kBufWord3);
-  const int nk = kend > kbeg ? (kend - kbeg + KD - 1) / KD : 0;
+  const int nkt = kend > kbeg ? (kend - kbeg + KD - 1) / KD : 0;  // stages per term
+  const int nk = TERMS ? g.kterms * nkt : nkt;
 
   // Byte offsets at k = kbeg of the S loads per operand, and the per-stage
   // advance.  K and the split's chunk are multiples of KD (checked on the
@@ -382,8 +391,19 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   const uint32_t a_step = 4u * (A_MC ? KD * (uint32_t)g.lda : KD);
   const uint32_t b_step = 4u * (B_KC ? KD : KD * (uint32_t)g.ldb);
 
+  // Terms: stage kt is stage kt % nkt of term kt / nkt, so the offset jumps
+  // by (term stride - nkt stages) at each term boundary (modulo 2^32; the
+  // true offsets stay below 2^31, OOB rows included).  Stages prefetched past
+  // the last term are never consumed.
+  const uint32_t a_jump = TERMS ? (uint32_t)(g.gsa * 4) - (uint32_t)nkt * a_step : 0u;
+  const uint32_t b_jump = TERMS ? (uint32_t)(g.gsb * 4) - (uint32_t)nkt * b_step : 0u;
   auto load = [&](int kt, f32x4(&fa)[S], f32x4(&fb)[S]) {
-    const uint32_t da = (uint32_t)kt * a_step, db = (uint32_t)kt * b_step;
+    uint32_t da = (uint32_t)kt * a_step, db = (uint32_t)kt * b_step;
+    if (TERMS) {
+      const uint32_t t = (uint32_t)min(kt / nkt, g.kterms - 1);
+      da += t * a_jump;
+      db += t * b_jump;
+    }
 #pragma unroll
     for (int x = 0; x < S; ++x) {
       fa[x] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(a_off[x] + da), 0, 0));
@@ -765,9 +785,12 @@ int choose_splits(int M, int N, int K, int batch, int& kchunk) {
   const long long tiles = (long long)((M + t.tm() - 1) / t.tm()) * ((N + t.tn() - 1) / t.tn()) * batch;
   int s, smax;
   if (t.direct) {
-    // A grid of >= 3/4 of the 256 CUs runs unsplit.
+    // A grid of >= 3/4 of the 256 CUs runs unsplit.  Below that, at most one
+    // workgroup per CU: a few CUs running two would take twice as long as the
+    // rest (measured on MI355X: 48 tiles x 8192 deep, 5 splits 113 us against
+    // 176 us for 6 and 122 us for 10; 16 tiles: 16 splits best, 64 tiles: 4).
     if (tiles >= 192) return 1;
-    s = (int)((256 + tiles - 1) / tiles);
+    s = tiles <= 128 ? (int)(256 / tiles) : 2;
     smax = K / 512;
   } else {
     // Measured on MI355X: with ~256 tiles a split only pays off for long K.
@@ -805,7 +828,8 @@ void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, int vec, bool cs) {
 // shader clock it sustains (~2.15 GHz under load), not by load latency.
 template <int TA, int TB>
 void launch_direct(hipStream_t s, const GemmArgs& g, dim3 grid, bool cs) {
-  if (cs) gemm_direct_kernel<TA, TB, true, 16, 3, 2><<<grid, NT, 0, s>>>(g);
+  if (g.kterms > 1) gemm_direct_kernel<TA, TB, false, 16, 3, 2, true><<<grid, NT, 0, s>>>(g);
+  else if (cs) gemm_direct_kernel<TA, TB, true, 16, 3, 2><<<grid, NT, 0, s>>>(g);
   else gemm_direct_kernel<TA, TB, false, 16, 3, 2><<<grid, NT, 0, s>>>(g);
 }
 
@@ -831,7 +855,8 @@ void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, b
     const long long items = (long long)grid.x * grid.y * grid.z;
     const int ncu = cu_count();
     const bool c_buf = ((double)(g.M - 1) * (double)g.ldc + g.N) * 4.0 < 2147483648.0 - 64;
-    if (g.splits == 1 && !cs && g.K >= 64 && g.K % 64 == 0 && items > 2 * ncu && items < (1LL << 30) && c_buf) {
+    if (g.splits == 1 && g.kterms == 1 && !cs && g.K >= 64 && g.K % 64 == 0 && items > 2 * ncu &&
+        items < (1LL << 30) && c_buf) {
       gemm_stream_kernel<TA, TB, 16, 4><<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
     } else {
       launch_direct<TA, TB>(s, g, grid, cs);
@@ -870,16 +895,39 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   MLE_CHECK_ARG(inner >= 1 && batch % inner == 0, "mle_gemm: batch %d not a multiple of inner %d", batch, inner);
   GemmArgs g{A,    B,    C,       colsum,  lda,  ldb,    ldc,  stride_a, stride_b, stride_c, M,    N,   K,
              alpha, beta, 1,       K,       nullptr, nullptr, bias, inner,    sa2,      sb2,      sc2,      sbias, scs,
-             0,     gsa,  gsb};
+             0,     gsa,  gsb,     1};
+  const bool v4 = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
+                  (sa2 % 4 == 0) && (sb2 % 4 == 0) && (gsa % 4 == 0) && (gsb % 4 == 0) && aligned16(A) &&
+                  aligned16(B);
+  // Buffer loads need the contiguous bound of each operand to be a multiple of
+  // 4 and every extent (all terms of a sum) addressable with a 31-bit offset.
+  const int a_rows = trans_a ? K : M, a_cols = trans_a ? M : K;
+  const int b_rows = trans_b ? N : K, b_cols = trans_b ? K : N;
+  const double t_extra = terms > 1 ? (double)(terms - 1) : 0.0;
+  const bool buf = v4 && a_cols % 4 == 0 && b_cols % 4 == 0 && K > 0 &&
+                   extent_bytes(a_rows, a_cols, lda) + t_extra * 4.0 * (double)gsa < 2147483648.0 - 64 &&
+                   extent_bytes(b_rows, b_cols, ldb) + t_extra * 4.0 * (double)gsb < 2147483648.0 - 64;
+  const int vec = buf ? 2 : (v4 ? 1 : 0);
+  const bool cs = colsum != nullptr;
+  // The direct kernel stores 16-byte row segments of C (and reads bias as float4).
+  const bool direct_ok = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && sc2 % 4 == 0 && aligned16(C) &&
+                         (bias == nullptr || (aligned16(bias) && sbias % 4 == 0));
   if (terms > 1) {
-    // Sum of `terms` products: one split per term, reduced in term order.
+    // Sum of `terms` products.  The workspace is part of the contract either
+    // way.  On the register-direct kernel the terms extend its K loop (one
+    // accumulator, terms in order, no partials); otherwise one split per
+    // term, reduced in term order.
     const size_t need = ((size_t)terms * batch * M * N + (size_t)terms * batch * N) * sizeof(float);
     MLE_CHECK_ARG(ws && ws_bytes >= need, "mle_gemm_sum: workspace of %zu bytes needed", need);
     MLE_CHECK_ARG(terms * batch <= 65535, "mle_gemm_sum: too many terms");
-    g.grouped = 1;
-    g.splits = terms;
-    g.part = static_cast<float*>(ws);
-    g.part_cs = g.part + (size_t)terms * batch * M * N;
+    if (tile.direct && direct_ok && vec == 2 && K % 16 == 0 && (long long)terms * (K / 16) < (1LL << 24)) {
+      g.kterms = terms;
+    } else {
+      g.grouped = 1;
+      g.splits = terms;
+      g.part = static_cast<float*>(ws);
+      g.part_cs = g.part + (size_t)terms * batch * M * N;
+    }
   } else {
     int kchunk = K;
     const int splits = ws ? choose_splits(M, N, K, batch, kchunk) : 1;
@@ -893,21 +941,6 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
       }
     }
   }
-  const bool v4 = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
-                  (sa2 % 4 == 0) && (sb2 % 4 == 0) && (gsa % 4 == 0) && (gsb % 4 == 0) && aligned16(A) &&
-                  aligned16(B);
-  // Buffer loads need the contiguous bound of each operand to be a multiple of
-  // 4 and every extent addressable with a 31-bit byte offset.
-  const int a_rows = trans_a ? K : M, a_cols = trans_a ? M : K;
-  const int b_rows = trans_b ? N : K, b_cols = trans_b ? K : N;
-  const bool buf = v4 && a_cols % 4 == 0 && b_cols % 4 == 0 && K > 0 &&
-                   extent_bytes(a_rows, a_cols, lda) < 2147483648.0 - 64 &&
-                   extent_bytes(b_rows, b_cols, ldb) < 2147483648.0 - 64;
-  const int vec = buf ? 2 : (v4 ? 1 : 0);
-  const bool cs = colsum != nullptr;
-  // The direct kernel stores 16-byte row segments of C (and reads bias as float4).
-  const bool direct_ok = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && sc2 % 4 == 0 && aligned16(C) &&
-                         (bias == nullptr || (aligned16(bias) && sbias % 4 == 0));
   dim3 grid((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
   hipStream_t s = as_stream(stream);
   static const char* names[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};

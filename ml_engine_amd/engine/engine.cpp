@@ -877,39 +877,54 @@ bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Line
       if ((long long)(get(i) - get(i - 1)) != st) return false;
     return st % 4 == 0;
   };
-  long long dw, dgrad;
+  long long dw, dgrad, dout, dbias = 0;
   const bool has_bias = l0->has_bias();
   if (!stride_of([&](size_t i) { return layers[i]->W1.output; }, dw) ||
-      !stride_of([&](size_t i) { return outs[i]->grad; }, dgrad))
+      !stride_of([&](size_t i) { return outs[i]->grad; }, dgrad) ||
+      !stride_of([&](size_t i) { return outs[i]->output; }, dout) ||
+      (has_bias && !stride_of([&](size_t i) { return layers[i]->B1.output; }, dbias)))
     return false;
+  // A parameter's gradient sits at the same offset from its value in every
+  // arena region, so gradient strides equal value strides.
+  for (size_t i = 1; i < n; ++i)
+    if (layers[i]->W1.grad - layers[0]->W1.grad != (long long)i * dw ||
+        (has_bias && layers[i]->B1.grad - layers[0]->B1.grad != (long long)i * dbias))
+      return false;
 
   const int nl = (int)n;
   const int p = l0->out_features(), k = l0->in_features();
   const long long rows = outs[0]->total / p;
   AdamParameter* W0 = &layers[0]->W1;
+  AdamParameter* B0 = &layers[0]->B1;
   NodeBackProp* o0 = outs[0].get();
+  const size_t ws_f = mle_gemm_ws_bytes((int)rows, p, k, nl);
   const size_t ws_dx = mle_gemm_sum_ws_bytes((int)rows, k, nl);
-  const size_t ws_dw = mle_gemm_ws_bytes(k, p, (int)rows, 1);
-  const size_t ws_bytes = std::max(ws_dx, ws_dw);
+  const size_t ws_dw = mle_gemm_ws_bytes(k, p, (int)rows, nl);
+  const size_t ws_bytes = std::max(ws_f, std::max(ws_dx, ws_dw));
   void* ws = gemm_workspace(ws_bytes);
+  auto fwd_count = std::make_shared<int>(0);
   auto bwd_count = std::make_shared<int>(0);
   const str name = outs[0]->op_name;
   for (size_t i = 0; i < n; ++i) {
-    NodeBackProp* oi = outs[i].get();
-    AdamParameter* Wi = &layers[i]->W1;
-    AdamParameter* Bi = &layers[i]->B1;
-    const str name_i = outs[i]->op_name;
-    // The forward stays one GEMM per layer: each 8192 x 512 projection already
-    // fills the chip, and a batch of three measured slower (a half-empty last
-    // round of tiles).  Batching the dW products measured slower as well.
+    // Forward: the first sibling of a pass computes Y_i = X W_i + b_i for all
+    // (X broadcast, weights, biases and outputs strided).
+    outs[i]->forward = [=]() {
+      if ((*fwd_count)++ == 0)
+        check(mle_gemm_batched_ex(stream(), 0, 0, (int)rows, p, k, 1.0f, x->output, k, 0, W0->output, p, dw, 0.0f,
+                                  o0->output, p, dout, nl, nullptr, 0, has_bias ? B0->output : nullptr, dbias, ws,
+                                  ws_bytes),
+              "Batched X*W_i + B_i in " + name + " forward");
+      if (*fwd_count == nl) *fwd_count = 0;
+    };
     outs[i]->backward = [=]() {
-      check(mle_gemm_ex(stream(), 1, 0, k, p, (int)rows, 1.0f, x->output, k, 0, oi->grad, p, 0, 1.0f, Wi->grad, p, 0,
-                        1, has_bias ? Bi->grad : nullptr, nullptr, ws, ws_bytes),
-            "MatMul... X^T*dZ in " + name_i + " backward");
       if (++(*bwd_count) < nl) return;
       *bwd_count = 0;
       // Every sibling's gradient is complete now (this is the last of their
-      // backward calls): dX = sum_i dZ_i W_i^T in one launch.
+      // backward calls): dW_i += X^T dZ_i and db_i += colsum dZ_i in one
+      // batched launch, then dX = sum_i dZ_i W_i^T in one grouped launch.
+      check(mle_gemm_batched_ex(stream(), 1, 0, k, p, (int)rows, 1.0f, x->output, k, 0, o0->grad, p, dgrad, 1.0f,
+                                W0->grad, p, dw, nl, has_bias ? B0->grad : nullptr, dbias, nullptr, 0, ws, ws_bytes),
+            "Batched X^T*dZ_i in " + name + " backward");
       const float beta = (float)accumulate_flag(x);
       check(mle_gemm_sum(stream(), 0, 1, (int)rows, k, p, 1.0f, o0->grad, p, dgrad, W0->output, p, dw, beta, x->grad,
                          k, nl, ws, ws_bytes),

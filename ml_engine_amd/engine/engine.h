@@ -284,11 +284,16 @@ class Linear {
 
 // Horizontal fusion of Linear layers that read the same input (e.g. the Q, K
 // and V projections of attention).  `outs` are the layers' forward nodes.
-// When the layers' weights and their outputs' gradients sit at equal strides
-// in their arenas, the nodes' backward lambdas are rewired so that each still
-// computes its own dW_i, db_i and the last to run computes
-// dX = sum_i dY_i W_i^T in one grouped launch (instead of one accumulating
-// GEMM per layer).  Returns false (and changes nothing) otherwise.
+// When the layers' weights, biases, outputs and output gradients sit at equal
+// strides in their arenas, the nodes' lambdas are rewired:
+//  * forward: whichever sibling runs first in a pass computes every
+//    Y_i = X W_i + b_i in one batched launch; the others do nothing (every
+//    sibling must be evaluated in each forward pass, as the attention
+//    projections are);
+//  * backward: the last sibling to run computes every dW_i, db_i in one
+//    batched launch and dX = sum_i dY_i W_i^T in one grouped launch.
+// Same values as one GEMM per layer up to summation order.  Returns false
+// (and changes nothing) otherwise.
 namespace mle {
 bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Linear*>& layers);
 // Global switch for fuse_sibling_linears (on by default); graphs built while it

@@ -229,6 +229,13 @@ def test_gemm_batched_ex(hip, orc, ta, tb, M, N, K, batch, with_ws):
 
 @pytest.mark.parametrize("ta,tb,M,N,K,terms", [
     (0, 1, 8192, 512, 512, 3),   # dX = sum_i dY_i W_i^T of sibling projections
+    # register-direct kernel: the terms extend its K loop (every layout,
+    # ragged M and N)
+    (0, 1, 2000, 1700, 64, 3),
+    (1, 0, 1990, 1708, 48, 2),
+    (0, 0, 2100, 2052, 32, 4),
+    (1, 1, 2060, 2004, 80, 3),
+    # one split per term, reduced in term order
     (0, 1, 1000, 132, 260, 3),
     (0, 0, 300, 200, 100, 2),
     (1, 0, 64, 96, 500, 4),
