@@ -39,7 +39,7 @@ from ml_engine_amd.models import STEP_ALL, Model  # noqa: E402
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 PEAK_HBM = 8000.0       # GB/s
-GEMM_FAMILIES = ["gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"]
+GEMM_FAMILIES = ["gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt", "gemm_pair"]
 
 
 def log(msg: str) -> None:

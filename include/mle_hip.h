@@ -201,6 +201,23 @@ int mle_gemm_grid(mle_stream stream, int trans_a, int trans_b, int M, int N, int
                   float* C, int64_t ldc, int64_t sc_outer, int64_t sc_inner, int outer, int inner,
                   void* ws, size_t ws_bytes);
 
+/* Linear backward (Engine/engine.cu:3553-3560: bcmmABT for dX, bcmmATB for
+ * dW, BCompress for db) in as few launches as the shapes allow, for `layers`
+ * Linear layers of shape in -> out that read the same X [rows, in]:
+ *   dX      (+)= sum_l dY_l W_l^T      (accumulate_dx: 1 adds, 0 assigns)
+ *   dW_l     += X^T dY_l
+ *   db_l     += sum_rows dY_l          (db may be NULL)
+ * Layer l's dY, W (and dW), db sit at l * stride_dy, l * stride_w, l * stride_db
+ * floats (strides unused when layers == 1).  When both products run on the
+ * register-direct GEMM at most one workgroup per CU each, they share one
+ * launch (two workgroups per CU); otherwise dX then dW.  Needs
+ * mle_linear_bwd_ws_bytes(rows, in, out, layers) bytes of workspace. */
+size_t mle_linear_bwd_ws_bytes(int rows, int in, int out, int layers);
+int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers,
+                   const float* X, const float* dY, int64_t stride_dy,
+                   const float* W, int64_t stride_w, float* dX, int accumulate_dx,
+                   float* dW, float* db, int64_t stride_db, void* ws, size_t ws_bytes);
+
 /* out[c] (+)= sum_r x[r, c].  BCompress (Engine/kernels.cu:1562-1584); beta 0/1. */
 int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* out, float beta);
 /* out[c] += sum_{b, s} x[b, c, s] for c < nreduce (nreduce <= channels).

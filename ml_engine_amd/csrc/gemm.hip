@@ -329,8 +329,10 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
 // therefore writes 16-byte row segments straight from the accumulators.
 // A wave issues KD/4 loads per operand per stage; the two waves that share a
 // row (column) panel hit the same lines, which the L1 serves.
-template <int TA, int TB, bool COLSUM, int KD, int D, int OCC, bool TERMS = false>
-__global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
+// One 128 x 128 tile (tm, tn) of batch item / split bz of the register-direct
+// kernel; shared by gemm_direct_kernel and gemm_pair_kernel.
+template <int TA, int TB, bool COLSUM, int KD, int D, bool TERMS>
+__device__ __forceinline__ void direct_tile(const GemmArgs& g, int tm, int tn, int bz) {
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
   constexpr int TM = 128, TN = 128;
@@ -342,11 +344,9 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   const int lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, q = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
-  int tm, tn;
-  tile_of(gridDim.x, gridDim.y, tm, tn);
   const int m0 = tm * TM + wm * 64, n0 = tn * TN + wn * 64;  // this wave's 64 x 64 block
-  const int64_t z = blockIdx.z / g.splits;
-  const int split = blockIdx.z % g.splits;
+  const int64_t z = bz / g.splits;
+  const int split = bz % g.splits;
   const float* A = g.A + batch_off(z, g, g.sa, g.sa2) + (g.grouped ? split * g.gsa : 0);
   const float* B = g.B + batch_off(z, g, g.sb, g.sb2) + (g.grouped ? split * g.gsb : 0);
   float* C = g.C + batch_off(z, g, g.sc, g.sc2);
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
   // so each (i, r) is one 16-byte store of 4 consecutive columns.  N, ldc and
   // C are 16-byte aligned on this path (checked on the host).
   const bool split_mode = g.splits > 1;
-  float* P = split_mode ? g.part + (int64_t)blockIdx.z * g.M * g.N : nullptr;
+  float* P = split_mode ? g.part + (int64_t)bz * g.M * g.N : nullptr;
   const int col = n0 + 4 * lr;
   auto rmap = [&](int i, int d) { return A_MC ? 4 * d + i : 16 * i + d; };
   if (col < g.N) {
@@ -500,11 +500,18 @@ __global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
     if (q == 0 && col < g.N) {
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        if (split_mode) g.part_cs[(int64_t)blockIdx.z * g.N + col + n] = csum[n];
+        if (split_mode) g.part_cs[(int64_t)bz * g.N + col + n] = csum[n];
         else g.colsum[z * g.scs + col + n] += csum[n];
       }
     }
   }
+}
+
+template <int TA, int TB, bool COLSUM, int KD, int D, int OCC, bool TERMS = false>
+__global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
+  int tm, tn;
+  tile_of(gridDim.x, gridDim.y, tm, tn);
+  direct_tile<TA, TB, COLSUM, KD, D, TERMS>(g, tm, tn, (int)blockIdx.z);
 }
 
 // Tile (tm, tn) and batch item z of work item L of a persistent launch over
@@ -701,6 +708,31 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
   }
 }
 
+// Two independent register-direct GEMMs in one launch, one tile per
+// workgroup: workgroups [0, items0) take problem 0 and the rest problem 1,
+// each tile decoded by item_tile and computed by direct_tile exactly as
+// gemm_direct_kernel computes it.  A Linear layer's dX and dW products
+// (Engine/engine.cu:3553-3560) usually each fill about one workgroup per CU
+// with work items of equal depth; launched together they run two per CU in
+// a single round.
+struct PairGrid {
+  int items0, gx0, gy0;
+  int items1, gx1, gy1;
+};
+
+template <int TA0, int TB0, bool CS0, bool T0, int TA1, int TB1, bool CS1, bool T1>
+__global__ __launch_bounds__(NT, 2) void gemm_pair_kernel(GemmArgs g0, GemmArgs g1, PairGrid pg) {
+  const int w = blockIdx.x;
+  int tm, tn, bz;
+  if (w < pg.items0) {
+    item_tile(w, pg.items0, pg.gx0, pg.gy0, tm, tn, bz);
+    direct_tile<TA0, TB0, CS0, 16, 3, T0>(g0, tm, tn, bz);
+  } else {
+    item_tile(w - pg.items0, pg.items1, pg.gx1, pg.gy1, tm, tn, bz);
+    direct_tile<TA1, TB1, CS1, 16, 3, T1>(g1, tm, tn, bz);
+  }
+}
+
 // C = alpha * sum_s part[s] + beta * C and colsum += sum_s part_cs[s], in split
 // order.  Grid: x over column groups of W (4 with VEC, else 1) columns, y over
 // rows (looping when M > 65535), z over batch items -- no integer division.
@@ -878,13 +910,26 @@ double extent_bytes(int rows, int cols, int64_t ld) { return ((double)(rows - 1)
 
 }  // namespace
 
-static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+// A GEMM call resolved to its arguments, tile shape, grid and kernel family.
+struct GemmPlan {
+  GemmArgs g;
+  Tile tile;
+  dim3 grid;
+  int vec = 0, which = 0;
+  bool cs = false, direct_ok = false, empty = false;
+  double flop = 0, bytes = 0;
+};
+
+const char* const kFamily[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
+
+static int gemm_plan(GemmPlan& P, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
                      int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
                      int64_t ldc, int64_t stride_c, int batch, float* colsum, const float* bias, void* ws,
                      size_t ws_bytes, int inner = 1, int64_t sa2 = 0, int64_t sb2 = 0, int64_t sc2 = 0,
                      int64_t sbias = 0, int64_t scs = 0, int terms = 0, int64_t gsa = 0, int64_t gsb = 0) {
   MLE_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "mle_gemm: negative size");
-  if (M == 0 || N == 0 || batch == 0) return MLE_OK;
+  P.empty = M == 0 || N == 0 || batch == 0;
+  if (P.empty) return MLE_OK;
   MLE_CHECK_ARG(C != nullptr && (K == 0 || (A != nullptr && B != nullptr)), "mle_gemm: null operand");
   MLE_CHECK_ARG(ldc >= N, "mle_gemm: ldc %lld < N %d", (long long)ldc, N);
   MLE_CHECK_ARG(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "mle_gemm: leading dimension too small");
@@ -941,30 +986,68 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
       }
     }
   }
-  dim3 grid((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
-  hipStream_t s = as_stream(stream);
-  static const char* names[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
-  const int which = (trans_a ? 2 : 0) + (trans_b ? 1 : 0);
-  const double flop = 2.0 * M * (double)N * K * batch * (terms > 1 ? terms : 1);
-  const double bytes = 4.0 * batch * ((double)M * K + (double)K * N + (double)M * N * (beta != 0.f ? 2 : 1));
-  {
-    ProbeScope probe(names[which], s, flop, bytes);
-    switch (which) {
-      case 0: launch_tile<0, 0>(s, g, tile, grid, vec, cs, direct_ok); break;
-      case 1: launch_tile<0, 1>(s, g, tile, grid, vec, cs, direct_ok); break;
-      case 2: launch_tile<1, 0>(s, g, tile, grid, vec, cs, direct_ok); break;
-      default: launch_tile<1, 1>(s, g, tile, grid, vec, cs, direct_ok); break;
-    }
-    if (g.splits > 1) {
-      const bool rv = N % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && sc2 % 4 == 0 && aligned16(C) &&
-                      aligned16(g.part) && (!bias || (aligned16(bias) && sbias % 4 == 0));
-      const int w = rv ? 4 : 1;
-      dim3 rgrid((unsigned)((N / w + 255) / 256), (unsigned)std::min(M, 65535), (unsigned)batch);
-      if (rv) split_reduce_kernel<true><<<rgrid, 256, 0, s>>>(g);
-      else split_reduce_kernel<false><<<rgrid, 256, 0, s>>>(g);
-    }
+  P.g = g;
+  P.tile = tile;
+  P.grid = dim3((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
+  P.vec = vec;
+  P.cs = cs;
+  P.direct_ok = direct_ok;
+  P.which = (trans_a ? 2 : 0) + (trans_b ? 1 : 0);
+  P.flop = 2.0 * M * (double)N * K * batch * (terms > 1 ? terms : 1);
+  P.bytes = 4.0 * batch * ((double)M * K + (double)K * N + (double)M * N * (beta != 0.f ? 2 : 1));
+  return MLE_OK;
+}
+
+static void gemm_launch_main(hipStream_t s, const GemmPlan& P) {
+  switch (P.which) {
+    case 0: launch_tile<0, 0>(s, P.g, P.tile, P.grid, P.vec, P.cs, P.direct_ok); break;
+    case 1: launch_tile<0, 1>(s, P.g, P.tile, P.grid, P.vec, P.cs, P.direct_ok); break;
+    case 2: launch_tile<1, 0>(s, P.g, P.tile, P.grid, P.vec, P.cs, P.direct_ok); break;
+    default: launch_tile<1, 1>(s, P.g, P.tile, P.grid, P.vec, P.cs, P.direct_ok); break;
   }
-  return check_launch(names[which]);
+}
+
+static void gemm_launch_reduce(hipStream_t s, const GemmPlan& P) {
+  const GemmArgs& g = P.g;
+  if (g.splits <= 1) return;
+  const bool rv = g.N % 4 == 0 && g.ldc % 4 == 0 && g.sc % 4 == 0 && g.sc2 % 4 == 0 && aligned16(g.C) &&
+                  aligned16(g.part) && (!g.bias || (aligned16(g.bias) && g.sbias % 4 == 0));
+  const int w = rv ? 4 : 1;
+  const int batch = (int)P.grid.z / g.splits;
+  dim3 rgrid((unsigned)((g.N / w + 255) / 256), (unsigned)std::min(g.M, 65535), (unsigned)batch);
+  if (rv) split_reduce_kernel<true><<<rgrid, 256, 0, s>>>(g);
+  else split_reduce_kernel<false><<<rgrid, 256, 0, s>>>(g);
+}
+
+// Work items of a plan that launch_tile would run on gemm_direct_kernel (one
+// per workgroup), or 0 when it would pick another kernel.
+static long long direct_items(const GemmPlan& P) {
+  const GemmArgs& g = P.g;
+  if (P.empty || !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0)) return 0;
+  const long long items = (long long)P.grid.x * P.grid.y * P.grid.z;
+  const bool c_buf = ((double)(g.M - 1) * (double)g.ldc + g.N) * 4.0 < 2147483648.0 - 64;
+  const bool stream = g.splits == 1 && g.kterms == 1 && !P.cs && g.K >= 64 && g.K % 64 == 0 &&
+                      items > 2 * cu_count() && items < (1LL << 30) && c_buf;
+  return stream ? 0 : items;
+}
+
+static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                     int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
+                     int64_t ldc, int64_t stride_c, int batch, float* colsum, const float* bias, void* ws,
+                     size_t ws_bytes, int inner = 1, int64_t sa2 = 0, int64_t sb2 = 0, int64_t sc2 = 0,
+                     int64_t sbias = 0, int64_t scs = 0, int terms = 0, int64_t gsa = 0, int64_t gsb = 0) {
+  GemmPlan P;
+  const int rc = gemm_plan(P, trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                           stride_c, batch, colsum, bias, ws, ws_bytes, inner, sa2, sb2, sc2, sbias, scs, terms, gsa,
+                           gsb);
+  if (rc != MLE_OK || P.empty) return rc;
+  hipStream_t s = as_stream(stream);
+  {
+    ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
+    gemm_launch_main(s, P);
+    gemm_launch_reduce(s, P);
+  }
+  return check_launch(kFamily[P.which]);
 }
 
 extern "C" {
@@ -995,6 +1078,63 @@ int mle_gemm_sum(mle_stream stream, int trans_a, int trans_b, int M, int N, int 
   MLE_CHECK_ARG(terms >= 1, "mle_gemm_sum: terms %d", terms);
   return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, nullptr,
                    nullptr, ws, ws_bytes, 1, 0, 0, 0, 0, 0, terms, stride_a_term, stride_b_term);
+}
+
+size_t mle_linear_bwd_ws_bytes(int rows, int in, int out, int layers) {
+  const size_t dx = layers > 1 ? mle_gemm_sum_ws_bytes(rows, in, layers) : mle_gemm_ws_bytes(rows, in, out, 1);
+  const size_t dw = mle_gemm_ws_bytes(in, out, rows, layers);
+  return std::max(dx, dw);
+}
+
+int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers, const float* X, const float* dY,
+                   int64_t stride_dy, const float* W, int64_t stride_w, float* dX, int accumulate_dx, float* dW,
+                   float* db, int64_t stride_db, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(rows >= 0 && in >= 0 && out >= 0 && layers >= 1, "mle_linear_bwd: bad sizes");
+  MLE_CHECK_ARG(layers == 1 || (stride_dy != 0 && stride_w != 0 && (db == nullptr || stride_db != 0)),
+                "mle_linear_bwd: %d layers need strides", layers);
+  MLE_CHECK_ARG(ws_bytes >= mle_linear_bwd_ws_bytes(rows, in, out, layers) && (ws || ws_bytes == 0),
+                "mle_linear_bwd: workspace of %zu bytes needed", mle_linear_bwd_ws_bytes(rows, in, out, layers));
+  // dX (+)= sum_l dY_l W_l^T: NT, rows x in, depth out (terms over layers).
+  GemmPlan P0, P1;
+  int rc = gemm_plan(P0, 0, 1, rows, in, out, 1.0f, dY, out, 0, W, out, 0, accumulate_dx ? 1.0f : 0.0f, dX, in, 0, 1,
+                     nullptr, nullptr, ws, ws_bytes, 1, 0, 0, 0, 0, 0, layers > 1 ? layers : 0, stride_dy, stride_w);
+  if (rc != MLE_OK) return rc;
+  // dW_l += X^T dY_l and db_l += colsum dY_l: TN, in x out, depth rows.
+  rc = gemm_plan(P1, 1, 0, in, out, rows, 1.0f, X, in, 0, dY, out, stride_dy, 1.0f, dW, out, stride_w, layers, db,
+                 nullptr, ws, ws_bytes, 1, 0, 0, 0, 0, stride_db);
+  if (rc != MLE_OK) return rc;
+  hipStream_t s = as_stream(stream);
+  const long long n0 = direct_items(P0), n1 = direct_items(P1);
+  const int ncu = cu_count();
+  // One launch when both would run on the register-direct kernel at most one
+  // workgroup per CU each, and the dX product needs no workspace (the dW
+  // product's split partials own it).
+  if (n0 > 0 && n1 > 0 && n0 <= ncu && n1 <= ncu && P0.g.splits == 1) {
+    const PairGrid pg{(int)n0, (int)P0.grid.x, (int)P0.grid.y, (int)n1, (int)P1.grid.x, (int)P1.grid.y};
+    const dim3 grid((unsigned)(n0 + n1));
+    const bool t0 = P0.g.kterms > 1;
+    ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
+    if (t0 && P1.cs) gemm_pair_kernel<0, 1, false, true, 1, 0, true, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+    else if (t0) gemm_pair_kernel<0, 1, false, true, 1, 0, false, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+    else if (P1.cs) gemm_pair_kernel<0, 1, false, false, 1, 0, true, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+    else gemm_pair_kernel<0, 1, false, false, 1, 0, false, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+    gemm_launch_reduce(s, P1);
+    return check_launch("gemm_pair");
+  }
+  // Otherwise one launch each, in order (they may share the workspace).
+  if (!P0.empty) {
+    ProbeScope probe(kFamily[P0.which], s, P0.flop, P0.bytes);
+    gemm_launch_main(s, P0);
+    gemm_launch_reduce(s, P0);
+  }
+  rc = check_launch(kFamily[P0.which]);
+  if (rc != MLE_OK || P1.empty) return rc;
+  {
+    ProbeScope probe(kFamily[P1.which], s, P1.flop, P1.bytes);
+    gemm_launch_main(s, P1);
+    gemm_launch_reduce(s, P1);
+  }
+  return check_launch(kFamily[P1.which]);
 }
 
 int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,

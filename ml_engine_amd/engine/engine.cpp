@@ -803,9 +803,8 @@ graph Linear::forward(const graph& X) {
   const str name = op_name;
   node->params = has_bias ? std::vector<AdamParameter*>{W, Bb} : std::vector<AdamParameter*>{W};
   const size_t ws_f = mle_gemm_ws_bytes((int)rows, p, n, 1);
-  const size_t ws_dx = mle_gemm_ws_bytes((int)rows, n, p, 1);
-  const size_t ws_dw = mle_gemm_ws_bytes(n, p, (int)rows, 1);
-  const size_t ws_bytes = std::max(ws_f, std::max(ws_dx, ws_dw));
+  const size_t ws_b = mle_linear_bwd_ws_bytes((int)rows, n, p, 1);
+  const size_t ws_bytes = std::max(ws_f, ws_b);
   void* ws = mle::gemm_workspace(ws_bytes);
   node->forward = [=]() {
     // Y = X W + b: BCumAdd is fused into the GEMM epilogue.
@@ -814,13 +813,10 @@ graph Linear::forward(const graph& X) {
           "MatMul... X*W1 + B1 in " + name + " forward");
   };
   node->backward = [=]() {
-    const float beta = (float)mle::accumulate_flag(x);
-    check(mle_gemm_ex(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, 0, W->output, p, 0, beta, x->grad, n, 0,
-                      1, nullptr, nullptr, ws, ws_bytes),
-          "MatMul... dZ*W^T in " + name + " backward");
-    check(mle_gemm_ex(mle::stream(), 1, 0, n, p, (int)rows, 1.0f, x->output, n, 0, nd->grad, p, 0, 1.0f, W->grad, p, 0,
-                      1, has_bias ? Bb->grad : nullptr, nullptr, ws, ws_bytes),
-          "MatMul... X^T*dZ in " + name + " backward");
+    // dX (+)= dZ W^T, dW += X^T dZ, db += colsum dZ (one launch when they fit).
+    check(mle_linear_bwd(mle::stream(), (int)rows, n, p, 1, x->output, nd->grad, 0, W->output, 0, x->grad,
+                         mle::accumulate_flag(x), W->grad, has_bias ? Bb->grad : nullptr, 0, ws, ws_bytes),
+          "MatMul... dZ*W^T and X^T*dZ in " + name + " backward");
   };
   node->free = [=]() { nd->clear(); };
   node->serious_free = [=]() {};
@@ -898,9 +894,8 @@ bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Line
   AdamParameter* B0 = &layers[0]->B1;
   NodeBackProp* o0 = outs[0].get();
   const size_t ws_f = mle_gemm_ws_bytes((int)rows, p, k, nl);
-  const size_t ws_dx = mle_gemm_sum_ws_bytes((int)rows, k, nl);
-  const size_t ws_dw = mle_gemm_ws_bytes(k, p, (int)rows, nl);
-  const size_t ws_bytes = std::max(ws_f, std::max(ws_dx, ws_dw));
+  const size_t ws_b = mle_linear_bwd_ws_bytes((int)rows, k, p, nl);
+  const size_t ws_bytes = std::max(ws_f, ws_b);
   void* ws = gemm_workspace(ws_bytes);
   auto fwd_count = std::make_shared<int>(0);
   auto bwd_count = std::make_shared<int>(0);
@@ -920,15 +915,11 @@ bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Line
       if (++(*bwd_count) < nl) return;
       *bwd_count = 0;
       // Every sibling's gradient is complete now (this is the last of their
-      // backward calls): dW_i += X^T dZ_i and db_i += colsum dZ_i in one
-      // batched launch, then dX = sum_i dZ_i W_i^T in one grouped launch.
-      check(mle_gemm_batched_ex(stream(), 1, 0, k, p, (int)rows, 1.0f, x->output, k, 0, o0->grad, p, dgrad, 1.0f,
-                                W0->grad, p, dw, nl, has_bias ? B0->grad : nullptr, dbias, nullptr, 0, ws, ws_bytes),
-            "Batched X^T*dZ_i in " + name + " backward");
-      const float beta = (float)accumulate_flag(x);
-      check(mle_gemm_sum(stream(), 0, 1, (int)rows, k, p, 1.0f, o0->grad, p, dgrad, W0->output, p, dw, beta, x->grad,
-                         k, nl, ws, ws_bytes),
-            "Fused sum dZ_i*W_i^T in " + name + " backward");
+      // backward calls): dX = sum_i dZ_i W_i^T, dW_i += X^T dZ_i and
+      // db_i += colsum dZ_i for all siblings at once.
+      check(mle_linear_bwd(stream(), (int)rows, k, p, nl, x->output, o0->grad, dgrad, W0->output, dw, x->grad,
+                           accumulate_flag(x), W0->grad, has_bias ? B0->grad : nullptr, dbias, ws, ws_bytes),
+            "Sibling Linear backward in " + name);
     };
   }
   return true;

@@ -270,6 +270,62 @@ def test_gemm_sum(hip, orc, ta, tb, M, N, K, terms, beta):
                      K if tb else N, sb, beta, gC.ptr, N, terms, ws.ptr, need - 4)
 
 
+@pytest.mark.parametrize("rows,inp,out,layers,bias,acc", [
+    (8192, 384, 128, 1, True, 0),     # dX and dW share one launch
+    (8192, 384, 256, 3, True, 1),     # three layers: dX terms folded into K, dW batched
+    (8192, 512, 512, 1, False, 1),    # the attention output projection's shape
+    (8192, 2048, 128, 1, True, 0),    # dX on the persistent kernel: two launches
+    (300, 130, 70, 2, True, 1),       # small: LDS kernels, split partials
+])
+def test_linear_bwd(hip, orc, rows, inp, out, layers, bias, acc):
+    """mle_linear_bwd against the oracle's bcmm products and column sums, with
+    gaps between the layers' dY, W/dW and db (the parameter arena's padding),
+    which must stay untouched."""
+    r = rng(rows + inp + 7 * out + layers)
+    gap = 8
+    sdy, sw, sb = rows * out + gap, inp * out + gap, out + gap
+    X = r.standard_normal((rows, inp), dtype=np.float32)
+    dYf = r.standard_normal(layers * sdy, dtype=np.float32)
+    Wf = r.standard_normal(layers * sw, dtype=np.float32)
+    dX0 = r.standard_normal((rows, inp), dtype=np.float32)
+    dWf = r.standard_normal(layers * sw, dtype=np.float32)
+    dbf = r.standard_normal(layers * sb, dtype=np.float32)
+    dY = [np.ascontiguousarray(dYf[l * sdy:l * sdy + rows * out].reshape(rows, out)) for l in range(layers)]
+    W = [np.ascontiguousarray(Wf[l * sw:l * sw + inp * out].reshape(inp, out)) for l in range(layers)]
+    want_dx = dX0.copy() if acc else np.zeros_like(dX0)
+    for l in range(layers):
+        orc.call("orc_bcmm", 1, orc.ptr(dY[l]), orc.ptr(W[l]), orc.ptr(want_dx), 1, 1, rows, out, inp, 1, 3, 3, 3, 1.0)
+    want_dw, want_db = [], []
+    for l in range(layers):
+        w = np.ascontiguousarray(dWf[l * sw:l * sw + inp * out].reshape(inp, out)).copy()
+        orc.call("orc_bcmm", 2, orc.ptr(X), orc.ptr(dY[l]), orc.ptr(w), 1, 1, inp, rows, out, 1, 3, 3, 3, 1.0)
+        want_dw.append(w)
+        want_db.append(dbf[l * sb:l * sb + out] + dY[l].astype(np.float64).sum(0))
+    L = hip.lib()
+    need = L.mle_linear_bwd_ws_bytes(rows, inp, out, layers)
+    ws = hip.Buffer(max(need, 4))
+    gX, gdY, gW, gdX, gdW, gdb = (B(hip, a) for a in (X, dYf, Wf, dX0, dWf, dbf))
+    hip.call("mle_linear_bwd", None, rows, inp, out, layers, gX.ptr, gdY.ptr, sdy, gW.ptr, sw, gdX.ptr, acc, gdW.ptr,
+             gdb.ptr if bias else None, sb, ws.ptr, need)
+    assert_close(gdX.numpy(), want_dx, what="linear_bwd dX", **MM)
+    got_w, got_b = gdW.numpy(), gdb.numpy()
+    for l in range(layers):
+        assert_close(got_w[l * sw:l * sw + inp * out].reshape(inp, out), want_dw[l], what=f"linear_bwd dW {l}", **MM)
+        assert np.array_equal(got_w[l * sw + inp * out:(l + 1) * sw], dWf[l * sw + inp * out:(l + 1) * sw]), "dW gap"
+        if bias:
+            assert_close(got_b[l * sb:l * sb + out], want_db[l], what=f"linear_bwd db {l}", **EW)
+        else:
+            assert np.array_equal(got_b, dbf), "db written without bias"
+    # errors: a short workspace (when one is needed) and zero layers
+    if need:
+        with pytest.raises(hip.MLEError):
+            hip.call("mle_linear_bwd", None, rows, inp, out, layers, gX.ptr, gdY.ptr, sdy, gW.ptr, sw, gdX.ptr, acc,
+                     gdW.ptr, None, sb, ws.ptr, need - 4)
+    with pytest.raises(hip.MLEError):
+        hip.call("mle_linear_bwd", None, rows, inp, out, 0, gX.ptr, gdY.ptr, sdy, gW.ptr, sw, gdX.ptr, acc, gdW.ptr,
+                 None, sb, ws.ptr, need)
+
+
 @pytest.mark.parametrize("M,N,K", [(100, 40, 300), (40, 40, 500), (300, 90, 77), (2048, 4096, 40), (64, 130, 300),
                                    (2048, 4096, 48), (2000, 1700, 48), (1000, 2052, 4112)])
 def test_gemm_colsum_tiles(hip, orc, M, N, K):
