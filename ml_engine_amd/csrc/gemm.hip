@@ -1043,10 +1043,12 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   if (rc != MLE_OK || P.empty) return rc;
   hipStream_t s = as_stream(stream);
   {
+    // The probe times the GEMM kernel itself (the split reduce is a separate,
+    // HBM-bound kernel).
     ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
     gemm_launch_main(s, P);
-    gemm_launch_reduce(s, P);
   }
+  gemm_launch_reduce(s, P);
   return check_launch(kFamily[P.which]);
 }
 
@@ -1113,18 +1115,22 @@ int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers, con
     const PairGrid pg{(int)n0, (int)P0.grid.x, (int)P0.grid.y, (int)n1, (int)P1.grid.x, (int)P1.grid.y};
     const dim3 grid((unsigned)(n0 + n1));
     const bool t0 = P0.g.kterms > 1;
-    ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
-    if (t0 && P1.cs) gemm_pair_kernel<0, 1, false, true, 1, 0, true, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
-    else if (t0) gemm_pair_kernel<0, 1, false, true, 1, 0, false, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
-    else if (P1.cs) gemm_pair_kernel<0, 1, false, false, 1, 0, true, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
-    else gemm_pair_kernel<0, 1, false, false, 1, 0, false, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+    {
+      ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
+      if (t0 && P1.cs) gemm_pair_kernel<0, 1, false, true, 1, 0, true, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+      else if (t0) gemm_pair_kernel<0, 1, false, true, 1, 0, false, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+      else if (P1.cs) gemm_pair_kernel<0, 1, false, false, 1, 0, true, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+      else gemm_pair_kernel<0, 1, false, false, 1, 0, false, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+    }
     gemm_launch_reduce(s, P1);
     return check_launch("gemm_pair");
   }
   // Otherwise one launch each, in order (they may share the workspace).
   if (!P0.empty) {
-    ProbeScope probe(kFamily[P0.which], s, P0.flop, P0.bytes);
-    gemm_launch_main(s, P0);
+    {
+      ProbeScope probe(kFamily[P0.which], s, P0.flop, P0.bytes);
+      gemm_launch_main(s, P0);
+    }
     gemm_launch_reduce(s, P0);
   }
   rc = check_launch(kFamily[P0.which]);
@@ -1132,8 +1138,8 @@ int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers, con
   {
     ProbeScope probe(kFamily[P1.which], s, P1.flop, P1.bytes);
     gemm_launch_main(s, P1);
-    gemm_launch_reduce(s, P1);
   }
+  gemm_launch_reduce(s, P1);
   return check_launch(kFamily[P1.which]);
 }
 

@@ -10,8 +10,9 @@ Usage (on the GPU box; rocprofv3 puts the program itself after `--`):
   python3 -m ml_engine_amd.pmc_traffic copy N
       a plain copy of N floats (mle_scale_write with scale 1), run 5 times
   python3 -m ml_engine_amd.pmc_traffic summarize FAMILY FETCH.db WRITE.db COPY_FETCH.db COPY_WRITE.db N OUT.json
-      average fetch / write bytes per launch of the GEMM layout FAMILY
-      (gemm_nn, gemm_nt, gemm_tn, gemm_tt), raw and calibrated
+      average fetch / write bytes per launch of the GEMM family FAMILY (a
+      layout: gemm_nn, gemm_nt, gemm_tn, gemm_tt; or gemm_pair, the Linear
+      backward dX + dW launch), raw and calibrated
 """
 from __future__ import annotations
 
@@ -21,7 +22,8 @@ import sqlite3
 import sys
 
 FAMILIES = {"gemm_nn": (0, 0), "gemm_nt": (0, 1), "gemm_tn": (1, 0), "gemm_tt": (1, 1)}
-GEMM_KERNEL = re.compile(r"gemm_(?:direct_)?kernel<(\d), (\d)")
+GEMM_KERNEL = re.compile(r"gemm_(?:direct_|stream_)?kernel<(\d), (\d)")
+PAIR_KERNEL = re.compile(r"gemm_pair_kernel<")
 
 
 def per_dispatch(db: str, counter: str) -> list[tuple[str, float]]:
@@ -34,6 +36,8 @@ def per_dispatch(db: str, counter: str) -> list[tuple[str, float]]:
 
 
 def family_of(name: str) -> str | None:
+    if PAIR_KERNEL.search(name):
+        return "gemm_pair"
     m = GEMM_KERNEL.search(name)
     if not m:
         return None
