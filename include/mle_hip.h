@@ -201,6 +201,18 @@ int mle_gemm_grid(mle_stream stream, int trans_a, int trans_b, int M, int N, int
                   float* C, int64_t ldc, int64_t sc_outer, int64_t sc_inner, int outer, int inner,
                   void* ws, size_t ws_bytes);
 
+/* mle_gemm_ex (one batch item) that also writes row statistics of C for a
+ * following softmax cross-entropy (SoftMaxCrossEntropy, Engine/engine.cu:
+ * 2064-2124, reads the logits again to find them): for row r and 64-column
+ * block b, rowpart[r * ldp + 2b] = max of C over the block and [.. + 1] = sum
+ * of exp(C - max).  On the persistent GEMM kernel the epilogue computes them
+ * from the tile in registers; otherwise a second kernel reads C.  ldp >=
+ * 2 * ceil(N / 64), even; rowpart 8-byte aligned. */
+int mle_gemm_rowstats(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+                      const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                      float* C, int64_t ldc, const float* bias, float* rowpart, int64_t ldp,
+                      void* ws, size_t ws_bytes);
+
 /* Linear backward (Engine/engine.cu:3553-3560: bcmmABT for dX, bcmmATB for
  * dW, BCompress for db) in as few launches as the shapes allow, for `layers`
  * Linear layers of shape in -> out that read the same X [rows, in]:
@@ -266,6 +278,15 @@ int mle_softmax_xent_keys_fwd(mle_stream stream, const float* logits, const int3
 int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const float* stats, const int32_t* keys,
                               int clen, int max_clen, const float* upstream, float* dlogits, int rows, int cols,
                               int batch);
+/* mle_softmax_xent_keys_fwd from row statistics instead of the logits: rowpart
+ * holds, per row r and 64-column block b, the block's max and sum of
+ * exp(x - max) at rowpart[r * ldp + 2b], [.. + 1] (mle_gemm_rowstats writes
+ * them with the logits).  The pairs combine into the row max and sum the
+ * backward reads from `stats`; only the key's logit is read.  Same loss and
+ * stats as mle_softmax_xent_keys_fwd up to float summation order. */
+int mle_softmax_xent_keys_fwd_rowstats(mle_stream stream, const float* logits, const float* rowpart, int64_t ldp,
+                                       const int32_t* keys, int clen, int max_clen, float* stats, int rows, int cols,
+                                       float* loss, void* ws, size_t ws_bytes);
 
 /* ------------------------------------------------------------------------- */
 /* Normalisation (gamma = 1, beta = 0, as the reference)                     */

@@ -5,6 +5,8 @@
 // so results are deterministic.
 #include "gemm_core.hpp"
 
+#include <float.h>
+
 #include <algorithm>
 
 using namespace mle;
@@ -42,6 +44,11 @@ struct GemmArgs {
   // Sum of products folded into K (register-direct kernel, one split): stage
   // kt of the K loop reads term kt / (K / KD) of A + t*gsa and B + t*gsb.
   int kterms;
+  // Row statistics of C (persistent kernel): for row r and 64-column block b,
+  // rowpart[r * rp_ld + 2 b] = max over the block, [.. + 1] = sum of
+  // exp(C - max).  nullptr: none.
+  float* rowpart;
+  int64_t rp_ld;
 };
 
 __device__ __forceinline__ int64_t batch_off(int64_t z, const GemmArgs& g, int64_t s, int64_t s2) {
@@ -557,13 +564,15 @@ __device__ __forceinline__ void item_tile(int L, int items, int gx, int gy, int&
 // Requires: one split, no column sum, K a positive multiple of KD * D, C
 // addressable by a buffer resource, and the direct kernel's alignment
 // conditions (checked on the host).
-template <int TA, int TB, int KD, int D>
+template <int TA, int TB, int KD, int D, bool ROWSTATS = false>
 __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, int gy, int items) {
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
   constexpr int S = KD / 4;   // MFMA steps (and loads per operand) per stage
   constexpr int H = KD / 16;  // loads per 16-row block of a k-contiguous operand
   static_assert(D >= 2 && (KD == 16 || KD == 32), "unsupported stage shape");
+  constexpr int kRsLd = 64 + 4;  // ROWSTATS staging row stride (floats)
+  __shared__ __attribute__((aligned(16))) float rs_lds[ROWSTATS ? 4 * 64 * kRsLd : 4];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -676,6 +685,9 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
       f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
       if (g.bias && col < g.N) b4 = *reinterpret_cast<const f32x4*>(g.bias + z * g.sbias + col);
       const float alpha = g.alpha, beta = g.beta;
+      // ROWSTATS: the wave's 64 x 64 block goes to LDS (row slot
+      // d' = 16 i + 4 q + r, columns outside the matrix as -FLT_MAX), then lane
+      // l reduces slot l's 64 columns to (max, sum of exp(x - max)).
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -686,9 +698,37 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
           v = alpha * v;
           if (beta != 0.f)
             v += beta * __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, (int)off, 0, 0));
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v + b4), rc, (int)off, 0, 0);
+          v += b4;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v),
+                                                 rc, (int)off, 0, 0);
+          if (ROWSTATS) {
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+              if (col + n >= g.N) v[n] = -FLT_MAX;
+            *reinterpret_cast<f32x4*>(rs_lds + (wave * 64 + 16 * i + 4 * q + r) * kRsLd + 4 * lr) = v;
+          }
         }
+      if (ROWSTATS) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const float* rp = rs_lds + (wave * 64 + lane) * kRsLd;
+        f32x4 x[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) x[c] = *reinterpret_cast<const f32x4*>(rp + 4 * c);
+        float m = -FLT_MAX;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) m = fmaxf(fmaxf(m, fmaxf(x[c][0], x[c][1])), fmaxf(x[c][2], x[c][3]));
+        float e = 0.f;
+#pragma unroll
+        for (int c = 0; c < 16; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) e += __expf(x[c][j] - m);
+        const int i = lane >> 4, d = lane & 15;
+        const int row = m0 + (A_MC ? 4 * d + i : 16 * i + d);
+        const int c0 = tn * 128 + wn * 64;  // this wave's 64-column block
+        if (row < g.M && c0 < g.N)
+          *reinterpret_cast<float2*>(g.rowpart + (int64_t)row * g.rp_ld + 2 * (c0 >> 6)) = make_float2(m, e);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -706,6 +746,25 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
     }
     locate(c_item + G, ra_n, rb_n, a_nx, b_nx);
   }
+}
+
+// Row statistics of a finished C when the GEMM did not produce them in its
+// epilogue: one wave per (row, 64-column block): max and sum of exp(C - max).
+__global__ __launch_bounds__(256) void rowstats_kernel(const float* __restrict__ C, int64_t ldc, int M, int N,
+                                                       float* __restrict__ part, int64_t ld) {
+  const int nblk = (N + 63) / 64;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (int64_t)M * nblk) return;
+  const int row = (int)(w / nblk), blk = (int)(w % nblk);
+  const int lane = threadIdx.x & 63, c = blk * 64 + lane;
+  const float x = c < N ? C[(int64_t)row * ldc + c] : -FLT_MAX;
+  float m = x;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float e = c < N ? expf(x - m) : 0.f;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, 64);
+  if (lane == 0) *reinterpret_cast<float2*>(part + (int64_t)row * ld + 2 * blk) = make_float2(m, e);
 }
 
 // Two independent register-direct GEMMs in one launch, one tile per
@@ -889,7 +948,11 @@ void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, b
     const bool c_buf = ((double)(g.M - 1) * (double)g.ldc + g.N) * 4.0 < 2147483648.0 - 64;
     if (g.splits == 1 && g.kterms == 1 && !cs && g.K >= 64 && g.K % 64 == 0 && items > 2 * ncu &&
         items < (1LL << 30) && c_buf) {
-      gemm_stream_kernel<TA, TB, 16, 4><<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
+      if (g.rowpart)
+        gemm_stream_kernel<TA, TB, 16, 4, true>
+            <<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
+      else
+        gemm_stream_kernel<TA, TB, 16, 4><<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
     } else {
       launch_direct<TA, TB>(s, g, grid, cs);
     }
@@ -940,7 +1003,7 @@ static int gemm_plan(GemmPlan& P, int trans_a, int trans_b, int M, int N, int K,
   MLE_CHECK_ARG(inner >= 1 && batch % inner == 0, "mle_gemm: batch %d not a multiple of inner %d", batch, inner);
   GemmArgs g{A,    B,    C,       colsum,  lda,  ldb,    ldc,  stride_a, stride_b, stride_c, M,    N,   K,
              alpha, beta, 1,       K,       nullptr, nullptr, bias, inner,    sa2,      sb2,      sc2,      sbias, scs,
-             0,     gsa,  gsb,     1};
+             0,     gsa,  gsb,     1,       nullptr, 0};
   const bool v4 = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
                   (sa2 % 4 == 0) && (sb2 % 4 == 0) && (gsa % 4 == 0) && (gsb % 4 == 0) && aligned16(A) &&
                   aligned16(B);
@@ -1031,6 +1094,13 @@ static long long direct_items(const GemmPlan& P) {
   return stream ? 0 : items;
 }
 
+// True when launch_tile would run the plan on the persistent kernel.
+static bool uses_stream(const GemmPlan& P) {
+  const GemmArgs& g = P.g;
+  if (P.empty || !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0)) return false;
+  return direct_items(P) == 0;
+}
+
 static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
                      int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
                      int64_t ldc, int64_t stride_c, int batch, float* colsum, const float* bias, void* ws,
@@ -1080,6 +1150,32 @@ int mle_gemm_sum(mle_stream stream, int trans_a, int trans_b, int M, int N, int 
   MLE_CHECK_ARG(terms >= 1, "mle_gemm_sum: terms %d", terms);
   return gemm_impl(stream, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, nullptr,
                    nullptr, ws, ws_bytes, 1, 0, 0, 0, 0, 0, terms, stride_a_term, stride_b_term);
+}
+
+int mle_gemm_rowstats(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                      int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc, const float* bias,
+                      float* rowpart, int64_t ldp, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(rowpart != nullptr && ldp >= 2 * (int64_t)((N + 63) / 64) && (ldp % 2) == 0 &&
+                    (reinterpret_cast<uintptr_t>(rowpart) & 7) == 0,
+                "mle_gemm_rowstats: rowpart needs %d float pairs per row (8-byte aligned)", (N + 63) / 64);
+  GemmPlan P;
+  const int rc = gemm_plan(P, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, nullptr,
+                           bias, ws, ws_bytes);
+  if (rc != MLE_OK || P.empty) return rc;
+  hipStream_t s = as_stream(stream);
+  const bool fused = uses_stream(P);
+  if (fused) P.g.rowpart = rowpart, P.g.rp_ld = ldp;
+  {
+    ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
+    gemm_launch_main(s, P);
+  }
+  gemm_launch_reduce(s, P);
+  if (!fused) {
+    const int64_t waves = (int64_t)M * ((N + 63) / 64);
+    MLE_CHECK_ARG((waves + 3) / 4 <= 2147483647LL, "mle_gemm_rowstats: too many rows");
+    rowstats_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(C, ldc, M, N, rowpart, ldp);
+  }
+  return check_launch("mle_gemm_rowstats");
 }
 
 size_t mle_linear_bwd_ws_bytes(int rows, int in, int out, int layers) {

@@ -172,6 +172,37 @@ __global__ __launch_bounds__(NT) void softmax_row4_kernel(const float* __restric
   }
 }
 
+// Cross-entropy against key targets from row statistics a GEMM epilogue
+// produced (mle_gemm_rowstats): per row, the nblk (max, sum of exp) pairs of
+// its 64-column blocks combine into the row's max M and sum S (the same
+// quantities softmax_row4_kernel reduces from the logits), then the key's
+// probability expf(x_key - M) / S gives the row's loss term.  One wave per row;
+// only the key's logit is read.
+__global__ __launch_bounds__(256) void xent_keys_partials_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ part, int64_t ldp, int nblk,
+                                                                 int rows, int cols, KeyTargets kt,
+                                                                 double* __restrict__ loss_part) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const float* pr = part + (size_t)row * ldp;
+  float mx = -FLT_MAX;
+  for (int b = lane; b < nblk; b += 64) mx = fmaxf(mx, pr[2 * b]);
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int b = lane; b < nblk; b += 64) sum += pr[2 * b + 1] * expf(pr[2 * b] - mx);
+  sum = wave_sum(sum);
+  if (sum < 1e-45f) sum = 1.0f;
+  if (lane == 0) {
+    const int key = kt.key((size_t)row, cols);
+    double lp = 0.0;
+    if (key >= 0) lp = -log((double)(expf(x[(size_t)row * cols + key] - mx) / sum) + 1e-27);
+    loss_part[row] = lp;
+    kt.stats[2 * row] = mx;
+    kt.stats[2 * row + 1] = sum;
+  }
+}
+
 // Row softmax backward: dx (+)= y (dy - <dy, y>); acc = 0 assigns.
 template <bool CACHED>
 __global__ __launch_bounds__(NT) void softmax_row_bwd_kernel(const float* __restrict__ y, const float* __restrict__ dy,
@@ -665,6 +696,24 @@ int mle_softmax_xent_keys_fwd(mle_stream stream, const float* logits, const int3
     softmax_row_kernel<false><<<rows, NT, 0, s>>>(logits, nullptr, rows, cols, 0, nullptr, part, kt);
   finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
   return check_launch("mle_softmax_xent_keys_fwd");
+}
+
+int mle_softmax_xent_keys_fwd_rowstats(mle_stream stream, const float* logits, const float* rowpart, int64_t ldp,
+                                       const int32_t* keys, int clen, int max_clen, float* stats, int rows, int cols,
+                                       float* loss, void* ws, size_t ws_bytes) {
+  const int nblk = (cols + 63) / 64;
+  MLE_CHECK_ARG(logits && rowpart && keys && stats && loss && ws && rows > 0 && cols > 0 && clen > 0 &&
+                    max_clen >= clen && rows % clen == 0 && ldp >= 2 * (int64_t)nblk,
+                "mle_softmax_xent_keys_fwd_rowstats: bad argument");
+  if (ws_bytes < (size_t)rows * sizeof(double))
+    return set_error(MLE_ERR_WORKSPACE, "mle_softmax_xent_keys_fwd_rowstats: workspace too small");
+  hipStream_t s = as_stream(stream);
+  double* part = static_cast<double*>(ws);
+  const KeyTargets kt{keys, clen, max_clen, stats};
+  xent_keys_partials_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(logits, rowpart, ldp, nblk, rows, cols, kt,
+                                                                       part);
+  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
+  return check_launch("mle_softmax_xent_keys_fwd_rowstats");
 }
 
 int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const float* stats, const int32_t* keys, int clen,

@@ -812,6 +812,11 @@ graph Linear::forward(const graph& X) {
                       p, 0, 1, nullptr, has_bias ? Bb->output : nullptr, ws, ws_bytes),
           "MatMul... X*W1 + B1 in " + name + " forward");
   };
+  node->forward_rowstats = [=](float* rowpart, int64_t ldp) {
+    check(mle_gemm_rowstats(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, W->output, p, 0.0f,
+                            nd->output, p, has_bias ? Bb->output : nullptr, rowpart, ldp, ws, ws_bytes),
+          "MatMul... X*W1 + B1 (with row statistics) in " + name + " forward");
+  };
   node->backward = [=]() {
     // dX (+)= dZ W^T, dW += X^T dZ, db += colsum dZ (one launch when they fit).
     check(mle_linear_bwd(mle::stream(), (int)rows, n, p, 1, x->output, nd->grad, 0, W->output, 0, x->grad,
@@ -850,6 +855,7 @@ bool g_sibling_fusion = true;
 }
 
 void set_sibling_fusion(bool on) { g_sibling_fusion = on; }
+bool fusion_enabled() { return g_sibling_fusion; }
 
 bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Linear*>& layers) {
   const size_t n = outs.size();
@@ -903,6 +909,7 @@ bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Line
   for (size_t i = 0; i < n; ++i) {
     // Forward: the first sibling of a pass computes Y_i = X W_i + b_i for all
     // (X broadcast, weights, biases and outputs strided).
+    outs[i]->forward_rowstats = nullptr;
     outs[i]->forward = [=]() {
       if ((*fwd_count)++ == 0)
         check(mle_gemm_batched_ex(stream(), 0, 0, (int)rows, p, k, 1.0f, x->output, k, 0, W0->output, p, dw, 0.0f,

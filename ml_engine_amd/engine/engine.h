@@ -149,6 +149,12 @@ struct NodeBackProp {
   bool lazy_grad_writer = false;
   // Non-null when this node's output is a one-hot matrix of `keys` (additive).
   std::shared_ptr<OneHotSource> onehot;
+  // Set by Linear::forward (additive): computes this node's output as its
+  // forward does and also, per row and 64-column block, the max and sum of
+  // exp(output - max) into rowpart (row stride ldp floats).  A following
+  // softmax cross-entropy with key targets takes over the node's forward with
+  // it and never reads the output again (the hook is cleared then).
+  std::function<void(float* rowpart, int64_t ldp)> forward_rowstats;
   virtual void update(const float lr = LEARNING_RATE, const bool W = ADAMW) {}
   NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation);
   virtual ~NodeBackProp() = default;
@@ -296,9 +302,11 @@ class Linear {
 // (and changes nothing) otherwise.
 namespace mle {
 bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Linear*>& layers);
-// Global switch for fuse_sibling_linears (on by default); graphs built while it
-// is off keep one GEMM per layer.
+// Global switch for the graph fusions (on by default): fuse_sibling_linears
+// and the Linear -> SoftMaxCrossEntropy row statistics.  Graphs built while it
+// is off keep one GEMM per layer and a loss that reads the logits.
 void set_sibling_fusion(bool on);
+bool fusion_enabled();
 }  // namespace mle
 
 class Convolute2D {

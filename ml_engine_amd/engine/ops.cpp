@@ -409,9 +409,23 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
   const size_t ws_bytes = mle_loss_ws_bytes(n);
   void* ws = mle::alloc_scratch(ws_bytes);
   NodeBackProp *nd = node.get(), *pr = prediction.get(), *tg = target.get();
+  // A Linear prediction writes the row statistics with its output (GEMM
+  // epilogue), so the loss never reads the logits back.
+  const int64_t ldp = 2 * (int64_t)((d + 63) / 64);
+  float* rowpart = nullptr;
+  if (by_keys && mle::fusion_enabled() && prediction->forward_rowstats && prediction->total == (long long)rows * d) {
+    rowpart = mle::alloc_output((size_t)rows * ldp);
+    auto fr = prediction->forward_rowstats;
+    prediction->forward = [fr, rowpart, ldp]() { fr(rowpart, ldp); };
+    prediction->forward_rowstats = nullptr;
+  }
   node->forward = [=]() {
     if (calculate_loss || !last) {
-      if (by_keys)
+      if (rowpart)
+        check(mle_softmax_xent_keys_fwd_rowstats(S(), pr->output, rowpart, ldp, oh->keys, oh->clen, oh->max_clen,
+                                                 stats, rows, d, nd->output, ws, ws_bytes),
+              "SoftMaxCrossEntropy");
+      else if (by_keys)
         check(mle_softmax_xent_keys_fwd(S(), pr->output, oh->keys, oh->clen, oh->max_clen, stats, rows, d, nd->output,
                                         ws, ws_bytes),
               "SoftMaxCrossEntropy");
@@ -435,6 +449,7 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
     nd->clear();
     if (probs) mle::release(probs, n, false);
     if (stats) mle::release(stats, 2 * (size_t)rows, false);
+    if (rowpart) mle::release(rowpart, (size_t)rows * ldp, false);
   };
   node->zero_grad = [=]() { mle::zero(nd->output, 1); };
   return node;

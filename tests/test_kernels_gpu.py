@@ -915,3 +915,80 @@ def test_softmax_xent_keys_matches_dense(hip, orc, batch, clen, max_clen, cols):
     pr = np.zeros_like(logits)
     lref = orc.call("orc_softmax_xent_fwd", orc.ptr(logits), orc.ptr(tgt), orc.ptr(pr), rows, cols)
     assert_close(gloss2.numpy(), np.array([lref], np.float32), what="keys loss", **EW)
+
+
+def _rowstats_ref(c: np.ndarray) -> np.ndarray:
+    """(max, sum exp(c - max)) per row and 64-column block, in float64."""
+    rows, cols = c.shape
+    nblk = (cols + 63) // 64
+    out = np.zeros((rows, nblk, 2))
+    for b in range(nblk):
+        blk = c[:, b * 64:(b + 1) * 64].astype(np.float64)
+        m = blk.max(1)
+        out[:, b, 0] = m
+        out[:, b, 1] = np.exp(blk - m[:, None]).sum(1)
+    return out
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K", [
+    (0, 0, 4100, 4000, 64),    # persistent kernel: statistics from the epilogue (ragged last block and rows)
+    (0, 1, 3000, 2900, 192),
+    (0, 0, 300, 130, 70),      # other kernels: statistics from a second pass over C
+    (1, 0, 1000, 8000, 48),
+])
+def test_gemm_rowstats(hip, orc, ta, tb, M, N, K):
+    """mle_gemm_rowstats writes the GEMM result (with bias) and, per row and
+    64-column block, the block max (exactly the max of the written C) and the
+    sum of exp(C - max) (1e-5 relative)."""
+    r = rng(M + 3 * N + K)
+    A = r.standard_normal((K, M) if ta else (M, K), dtype=np.float32)
+    Bm = r.standard_normal((N, K) if tb else (K, N), dtype=np.float32)
+    bias = r.standard_normal(N, dtype=np.float32)
+    ref = np.zeros((M, N), np.float32)
+    orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(A), orc.ptr(Bm), orc.ptr(ref), 1, 1, M, K, N, 0, 3, 3, 3, 1.0)
+    ref += bias
+    nblk = (N + 63) // 64
+    ldp = 2 * nblk + 2
+    gA, gB, gbias = B(hip, A), B(hip, Bm), B(hip, bias)
+    gC = hip.Buffer.zeros((M, N))
+    gp = B(hip, np.full(M * ldp, 7.0, np.float32))
+    L = hip.lib()
+    ws = hip.Buffer(max(L.mle_gemm_ws_bytes(M, N, K, 1), 4))
+    hip.call("mle_gemm_rowstats", None, ta, tb, M, N, K, 1.0, gA.ptr, M if ta else K, gB.ptr, K if tb else N, 0.0,
+             gC.ptr, N, gbias.ptr, gp.ptr, ldp, ws.ptr, ws.nbytes)
+    c = gC.numpy()
+    assert_close(c, ref, what="gemm_rowstats C", **MM)
+    part = gp.numpy().reshape(M, ldp)
+    want = _rowstats_ref(c)
+    np.testing.assert_array_equal(part[:, 0:2 * nblk:2], want[:, :, 0].astype(np.float32))
+    assert_close(part[:, 1:2 * nblk:2], want[:, :, 1], what="block sum of exp", **EW)
+    assert np.all(part[:, 2 * nblk:] == 7.0), "padding of a row's partials written"
+
+
+@pytest.mark.parametrize("batch,clen,cols", [(4, 64, 8000), (3, 10, 1000), (2, 7, 130)])
+def test_softmax_xent_keys_rowstats(hip, batch, clen, cols):
+    """The loss from row statistics equals the keys path that reads the logits:
+    the row max bit for bit, the row sum and the loss within 1e-5."""
+    r = rng(batch * 31 + clen + cols)
+    rows = batch * clen
+    logits = (r.standard_normal((rows, cols), dtype=np.float32) * 3).astype(np.float32)
+    keys = r.integers(0, cols, (batch, clen)).astype(np.int32)
+    keys[0, 1] = -1
+    keys[-1, 0] = cols + 3
+    nblk = (cols + 63) // 64
+    part = _rowstats_ref(logits)
+    ldp = 2 * nblk
+    gl, gk = B(hip, logits), B(hip, keys)
+    gpart = B(hip, part.astype(np.float32).reshape(rows, ldp))
+    gst, gst2 = hip.Buffer.zeros(2 * rows), hip.Buffer.zeros(2 * rows)
+    gloss, gloss2 = hip.Buffer.zeros(1), hip.Buffer.zeros(1)
+    L = hip.lib()
+    ws = hip.Buffer(L.mle_loss_ws_bytes(rows * cols))
+    hip.call("mle_softmax_xent_keys_fwd", None, gl.ptr, gk.ptr, clen, clen, gst.ptr, rows, cols, gloss.ptr, ws.ptr,
+             ws.nbytes)
+    hip.call("mle_softmax_xent_keys_fwd_rowstats", None, gl.ptr, gpart.ptr, ldp, gk.ptr, clen, clen, gst2.ptr, rows,
+             cols, gloss2.ptr, ws.ptr, ws.nbytes)
+    st, st2 = gst.numpy().reshape(rows, 2), gst2.numpy().reshape(rows, 2)
+    np.testing.assert_array_equal(st2[:, 0], st[:, 0])
+    assert_close(st2[:, 1], st[:, 1], what="row sums", **EW)
+    assert_close(gloss2.numpy(), gloss.numpy(), what="loss", **EW)
