@@ -213,6 +213,24 @@ int mle_gemm_rowstats(mle_stream stream, int trans_a, int trans_b, int M, int N,
                       float* C, int64_t ldc, const float* bias, float* rowpart, int64_t ldp,
                       void* ws, size_t ws_bytes);
 
+/* A Linear layer and the activation after it (ReLU / GELU / SiLU / ...; the
+ * RELU / GELU / SILU ops, Engine/engine.cu:2650-2780) with C and Y
+ * contiguous rows of N floats (ldc = N), batch 1:
+ *   mle_gemm_act_fwd:  C = alpha op(A) op(B) + beta C + bias;  Y = act(C)
+ *   mle_gemm_act_bwd:  C = alpha op(A) op(B) + beta C  (the activation
+ *                      output's gradient);  dX (+)= C * act'(X)  (its input's
+ *                      gradient; accumulate_dx 1 adds, 0 assigns)
+ * On the persistent GEMM kernel (NN forward / NT backward, ReLU, GELU or SiLU)
+ * the epilogue computes Y or dX from the tile in registers; otherwise the
+ * activation kernels run after the GEMM.  Same values either way. */
+int mle_gemm_act_fwd(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+                     const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                     float* C, const float* bias, int kind, float* Y, void* ws, size_t ws_bytes);
+int mle_gemm_act_bwd(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
+                     const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                     float* C, int kind, const float* X, float* dX, int accumulate_dx,
+                     void* ws, size_t ws_bytes);
+
 /* Linear backward (Engine/engine.cu:3553-3560: bcmmABT for dX, bcmmATB for
  * dW, BCompress for db) in as few launches as the shapes allow, for `layers`
  * Linear layers of shape in -> out that read the same X [rows, in]:

@@ -1,0 +1,57 @@
+// Activation functions and their derivatives (the reference's formulas), shared
+// by the elementwise kernels and the GEMM epilogues so both compute the same
+// values: forward (Engine/kernels.cu:1214, 1248, 1286) and derivative
+// (Engine/kernels.cu:1223, 1256, 1297) kernels of ReLU, SiLU, GELU, plus
+// tanh, sigmoid and leaky ReLU.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include "../../include/mle_hip.h"
+
+namespace mle {
+
+constexpr float kPI = 3.14159265359f;  // Includes/kernels.h:10
+
+template <int K>
+__device__ __forceinline__ float act_f(float x) {
+  if (K == MLE_RELU) return (x < 0) ? 0.0f : x;
+  if (K == MLE_GELU) {
+    const float val = sqrtf(2.0f / kPI) * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(val));
+  }
+  if (K == MLE_SILU) return x * (1.0f / (1.0f + expf(-x)));
+  if (K == MLE_TANH) return tanhf(x);
+  if (K == MLE_SIGMOID) return 1.0f / (1.0f + expf(-1.0f * x));
+  return (x < 0) ? 0.01f * x : x;  // leaky
+}
+
+template <int K>
+__device__ __forceinline__ float act_df(float x) {
+  if (K == MLE_RELU) return (x > 0.0f) ? 1.0f : 0.0f;
+  if (K == MLE_GELU) {
+    const float root = sqrtf(2.0f / kPI);
+    const float u = root * (x + 0.044715f * x * x * x);
+    const float du = root * (1.0f + 0.134145f * x * x);
+    const float t = tanhf(u);
+    return 0.5f + 0.5f * t + 0.5f * x * (1.0f - t * t) * du;
+  }
+  if (K == MLE_SILU) {
+    const float e = expf(x);
+    const float ne = 1.0f / e;
+    const float sg = 1.0f / (1.0f + ne);
+    return sg + (x / (e + ne + 2.0f));
+  }
+  if (K == MLE_TANH) {
+    const float e2 = expf(2.0f * x);
+    const float ne2 = 1.0f / e2;
+    return 4.0f / (e2 + ne2 + 2.0f);
+  }
+  if (K == MLE_SIGMOID) {
+    const float e = expf(x);
+    const float ne = 1.0f / e;
+    return 1.0f / (e + ne + 2.0f);
+  }
+  return (x < 0.0f) ? 0.01f : 1.0f;
+}
+
+}  // namespace mle

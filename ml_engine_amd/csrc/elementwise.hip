@@ -1,13 +1,12 @@
 // Elementwise and data-movement kernels: HBM streaming, dwordx4 where the
 // operands are 16-byte aligned, grid-stride loops sized for 256 CUs.
+#include "activation.hpp"
 #include "common.hpp"
 #include <math.h>
 
 using namespace mle;
 
 namespace {
-
-constexpr float kPI = 3.14159265359f;  // Includes/kernels.h:10
 
 __device__ __forceinline__ f32x4 ld4(const float* p, size_t i) { return *reinterpret_cast<const f32x4*>(p + i); }
 __device__ __forceinline__ void st4(float* p, size_t i, f32x4 v) { *reinterpret_cast<f32x4*>(p + i) = v; }
@@ -139,49 +138,6 @@ struct ChanAddOp {  // y = x + b[(i / hw) % C]
   __device__ void one(size_t i) const { y[i] = x[i] + b[(i / hw) % C]; }
   __device__ void vec(size_t i) const { st4(y, i, ld4(x, i) + b[(i / hw) % C]); }
 };
-
-// ---- activations ---------------------------------------------------------
-template <int K>
-__device__ __forceinline__ float act_f(float x) {
-  if (K == MLE_RELU) return (x < 0) ? 0.0f : x;
-  if (K == MLE_GELU) {
-    const float val = sqrtf(2.0f / kPI) * (x + 0.044715f * x * x * x);
-    return 0.5f * x * (1.0f + tanhf(val));
-  }
-  if (K == MLE_SILU) return x * (1.0f / (1.0f + expf(-x)));
-  if (K == MLE_TANH) return tanhf(x);
-  if (K == MLE_SIGMOID) return 1.0f / (1.0f + expf(-1.0f * x));
-  return (x < 0) ? 0.01f * x : x;  // leaky
-}
-
-template <int K>
-__device__ __forceinline__ float act_df(float x) {
-  if (K == MLE_RELU) return (x > 0.0f) ? 1.0f : 0.0f;
-  if (K == MLE_GELU) {
-    const float root = sqrtf(2.0f / kPI);
-    const float u = root * (x + 0.044715f * x * x * x);
-    const float du = root * (1.0f + 0.134145f * x * x);
-    const float t = tanhf(u);
-    return 0.5f + 0.5f * t + 0.5f * x * (1.0f - t * t) * du;
-  }
-  if (K == MLE_SILU) {
-    const float e = expf(x);
-    const float ne = 1.0f / e;
-    const float sg = 1.0f / (1.0f + ne);
-    return sg + (x / (e + ne + 2.0f));
-  }
-  if (K == MLE_TANH) {
-    const float e2 = expf(2.0f * x);
-    const float ne2 = 1.0f / e2;
-    return 4.0f / (e2 + ne2 + 2.0f);
-  }
-  if (K == MLE_SIGMOID) {
-    const float e = expf(x);
-    const float ne = 1.0f / e;
-    return 1.0f / (e + ne + 2.0f);
-  }
-  return (x < 0.0f) ? 0.01f : 1.0f;
-}
 
 template <int K>
 struct ActFwdOp {

@@ -3,6 +3,7 @@
 // scalar-FMA tiles and atomicAdd epilogues of bcmm / bcmmABT / bcmmATB / bcmmT
 // (Engine/kernels.cu:387-539): every C element is written by exactly one lane,
 // so results are deterministic.
+#include "activation.hpp"
 #include "gemm_core.hpp"
 
 #include <float.h>
@@ -49,7 +50,16 @@ struct GemmArgs {
   // exp(C - max).  nullptr: none.
   float* rowpart;
   int64_t rp_ld;
+  // Activation epilogues (persistent kernel, C's layout): forward writes
+  // act_y = act(C); backward writes act_dx (+)= C * act'(act_x).
+  float* act_y;
+  const float* act_x;
+  float* act_dx;
+  int act_acc;
 };
+
+// Epilogue modes of the persistent kernel.
+constexpr int kEpiPlain = 0, kEpiRowstats = 1, kEpiActFwd = 2, kEpiActBwd = 3;
 
 __device__ __forceinline__ int64_t batch_off(int64_t z, const GemmArgs& g, int64_t s, int64_t s2) {
   if (g.inner == 1) return z * s;
@@ -564,8 +574,9 @@ __device__ __forceinline__ void item_tile(int L, int items, int gx, int gy, int&
 // Requires: one split, no column sum, K a positive multiple of KD * D, C
 // addressable by a buffer resource, and the direct kernel's alignment
 // conditions (checked on the host).
-template <int TA, int TB, int KD, int D, bool ROWSTATS = false>
+template <int TA, int TB, int KD, int D, int EPI = kEpiPlain, int ACT = 0>
 __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, int gy, int items) {
+  constexpr bool ROWSTATS = EPI == kEpiRowstats;
   constexpr bool A_MC = TA != 0;
   constexpr bool B_KC = TB != 0;
   constexpr int S = KD / 4;   // MFMA steps (and loads per operand) per stage
@@ -681,6 +692,14 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
       item_tile(c_item, items, gx, gy, tm, tn, z);
       float* C = g.C + batch_off(z, g, g.sc, g.sc2);
       const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, (int)c_bytes, kBufWord3);
+      // Activation operands share C's layout (and batch offsets).
+      const int64_t zc = batch_off(z, g, g.sc, g.sc2);
+      __amdgpu_buffer_rsrc_t ry = rc, rx = rc, rd = rc;
+      if (EPI == kEpiActFwd) ry = __builtin_amdgcn_make_buffer_rsrc(g.act_y + zc, (short)0, (int)c_bytes, kBufWord3);
+      if (EPI == kEpiActBwd) {
+        rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.act_x) + zc, (short)0, (int)c_bytes, kBufWord3);
+        rd = __builtin_amdgcn_make_buffer_rsrc(g.act_dx + zc, (short)0, (int)c_bytes, kBufWord3);
+      }
       const int m0 = tm * 128 + wm * 64, col = tn * 128 + wn * 64 + 4 * lr;
       f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
       if (g.bias && col < g.N) b4 = *reinterpret_cast<const f32x4*>(g.bias + z * g.sbias + col);
@@ -701,6 +720,22 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
           v += b4;
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v),
                                                  rc, (int)off, 0, 0);
+          if (EPI == kEpiActFwd) {
+            f32x4 y;
+#pragma unroll
+            for (int n = 0; n < 4; ++n) y[n] = act_f<ACT>(v[n]);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, y), ry, (int)off, 0, 0);
+          }
+          if (EPI == kEpiActBwd) {
+            const f32x4 xh = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
+            f32x4 d;
+#pragma unroll
+            for (int n = 0; n < 4; ++n) d[n] = act_df<ACT>(xh[n]) * v[n];
+            if (g.act_acc) d += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, (int)off, 0, 0));
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, d), rd, (int)off, 0, 0);
+          }
           if (ROWSTATS) {
 #pragma unroll
             for (int n = 0; n < 4; ++n)
@@ -949,7 +984,7 @@ void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, b
     if (g.splits == 1 && g.kterms == 1 && !cs && g.K >= 64 && g.K % 64 == 0 && items > 2 * ncu &&
         items < (1LL << 30) && c_buf) {
       if (g.rowpart)
-        gemm_stream_kernel<TA, TB, 16, 4, true>
+        gemm_stream_kernel<TA, TB, 16, 4, kEpiRowstats>
             <<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
       else
         gemm_stream_kernel<TA, TB, 16, 4><<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
@@ -1003,7 +1038,7 @@ static int gemm_plan(GemmPlan& P, int trans_a, int trans_b, int M, int N, int K,
   MLE_CHECK_ARG(inner >= 1 && batch % inner == 0, "mle_gemm: batch %d not a multiple of inner %d", batch, inner);
   GemmArgs g{A,    B,    C,       colsum,  lda,  ldb,    ldc,  stride_a, stride_b, stride_c, M,    N,   K,
              alpha, beta, 1,       K,       nullptr, nullptr, bias, inner,    sa2,      sb2,      sc2,      sbias, scs,
-             0,     gsa,  gsb,     1,       nullptr, 0};
+             0,     gsa,  gsb,     1,       nullptr, 0,       nullptr, nullptr, nullptr, 0};
   const bool v4 = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
                   (sa2 % 4 == 0) && (sb2 % 4 == 0) && (gsa % 4 == 0) && (gsb % 4 == 0) && aligned16(A) &&
                   aligned16(B);
@@ -1101,6 +1136,21 @@ static bool uses_stream(const GemmPlan& P) {
   return direct_items(P) == 0;
 }
 
+// The persistent kernel with an activation epilogue (plan already known to
+// run on it).
+template <int TA, int TB, int EPI>
+static void launch_stream_act(hipStream_t s, const GemmPlan& P, int kind) {
+  const dim3 grid((unsigned)(2 * cu_count()));
+  const int gx = (int)P.grid.x, gy = (int)P.grid.y, items = (int)((long long)P.grid.x * P.grid.y * P.grid.z);
+  switch (kind) {
+    case MLE_RELU: gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_RELU><<<grid, NT, 0, s>>>(P.g, gx, gy, items); break;
+    case MLE_GELU: gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_GELU><<<grid, NT, 0, s>>>(P.g, gx, gy, items); break;
+    default: gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_SILU><<<grid, NT, 0, s>>>(P.g, gx, gy, items); break;
+  }
+}
+
+static bool epilogue_act(int kind) { return kind == MLE_RELU || kind == MLE_GELU || kind == MLE_SILU; }
+
 static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
                      int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b, float beta, float* C,
                      int64_t ldc, int64_t stride_c, int batch, float* colsum, const float* bias, void* ws,
@@ -1176,6 +1226,63 @@ int mle_gemm_rowstats(mle_stream stream, int trans_a, int trans_b, int M, int N,
     rowstats_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(C, ldc, M, N, rowpart, ldp);
   }
   return check_launch("mle_gemm_rowstats");
+}
+
+int mle_gemm_act_fwd(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                     int64_t lda, const float* B, int64_t ldb, float beta, float* C, const float* bias, int kind,
+                     float* Y, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(Y != nullptr && kind >= MLE_RELU && kind <= MLE_LEAKY_RELU, "mle_gemm_act_fwd: bad argument");
+  GemmPlan P;
+  int rc = gemm_plan(P, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, N, 0, 1, nullptr, bias, ws,
+                     ws_bytes);
+  if (rc != MLE_OK || P.empty) return rc;
+  hipStream_t s = as_stream(stream);
+  if (uses_stream(P) && P.which == 0 && epilogue_act(kind) && aligned16(Y)) {
+    P.g.act_y = Y;
+    {
+      ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
+      launch_stream_act<0, 0, kEpiActFwd>(s, P, kind);
+    }
+    return check_launch("mle_gemm_act_fwd");
+  }
+  {
+    ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
+    gemm_launch_main(s, P);
+  }
+  gemm_launch_reduce(s, P);
+  rc = check_launch("mle_gemm_act_fwd");
+  if (rc != MLE_OK) return rc;
+  return mle_act_fwd(stream, kind, C, Y, (size_t)M * N);
+}
+
+int mle_gemm_act_bwd(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,
+                     int64_t lda, const float* B, int64_t ldb, float beta, float* C, int kind, const float* X,
+                     float* dX, int accumulate_dx, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(X != nullptr && dX != nullptr && kind >= MLE_RELU && kind <= MLE_LEAKY_RELU,
+                "mle_gemm_act_bwd: bad argument");
+  GemmPlan P;
+  int rc = gemm_plan(P, trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, N, 0, 1, nullptr, nullptr,
+                     ws, ws_bytes);
+  if (rc != MLE_OK || P.empty) return rc;
+  hipStream_t s = as_stream(stream);
+  if (uses_stream(P) && P.which == 1 && epilogue_act(kind) && aligned16(X) && aligned16(dX)) {
+    P.g.act_x = X;
+    P.g.act_dx = dX;
+    P.g.act_acc = accumulate_dx ? 1 : 0;
+    {
+      ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
+      launch_stream_act<0, 1, kEpiActBwd>(s, P, kind);
+    }
+    return check_launch("mle_gemm_act_bwd");
+  }
+  {
+    ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
+    gemm_launch_main(s, P);
+  }
+  gemm_launch_reduce(s, P);
+  rc = check_launch("mle_gemm_act_bwd");
+  if (rc != MLE_OK) return rc;
+  return mle_act_bwd(stream, kind, X, C, dX, (size_t)M * N, accumulate_dx);
 }
 
 size_t mle_linear_bwd_ws_bytes(int rows, int in, int out, int layers) {

@@ -62,6 +62,8 @@ SIGNATURES: dict[str, tuple] = {
     "mle_gemm_grid": (I, [P, I, I, I, I, I, F, P, I64, I64, I64, P, I64, I64, I64, F, P, I64, I64, I64, I, I, P, SZ]),
     "mle_gemm_rowstats": (I, [P, I, I, I, I, I, F, P, I64, P, I64, F, P, I64, P, P, I64, P, SZ]),
     "mle_softmax_xent_keys_fwd_rowstats": (I, [P, P, P, I64, P, I, I, P, I, I, P, P, SZ]),
+    "mle_gemm_act_fwd": (I, [P, I, I, I, I, I, F, P, I64, P, I64, F, P, P, I, P, P, SZ]),
+    "mle_gemm_act_bwd": (I, [P, I, I, I, I, I, F, P, I64, P, I64, F, P, I, P, P, I, P, SZ]),
     "mle_linear_bwd_ws_bytes": (SZ, [I, I, I, I]),
     "mle_linear_bwd": (I, [P, I, I, I, I, P, P, I64, P, I64, P, I, P, P, I64, P, SZ]),
     "mle_colsum": (I, [P, P, SZ, I, P, F]),

@@ -200,6 +200,35 @@ def test_block_qkv_fusion(hip, quirks):
         assert np.abs(gf[i] - gu[i]).max() <= 1e-4 * scale, (i, np.abs(gf[i] - gu[i]).max(), scale)
 
 
+def test_block_fusion_full_size(hip):
+    """Full C4 shape, where the fused epilogues run on the persistent GEMM
+    kernel (FFN-in forward with GELU, FFN-out input gradient with GELU',
+    LM-head row statistics for the loss, batched Q/K/V): one step agrees with
+    the unfused graph (one GEMM per layer, separate activation and loss
+    kernels) -- loss within 1e-5, every parameter gradient within 1e-4 of its
+    scale."""
+    cfg = BlockConfig()
+    ids, tgt, params = block_data(cfg, seed=3)
+    runs = {}
+    for fuse in (True, False):
+        m = Model("block", cfg.dims(), fuse=fuse)
+        for i, p in enumerate(params):
+            m.set(i, p)
+        m.input(0, ids)
+        m.input(1, tgt)
+        m.step(0.0, 7)  # zero_grad + forward + backward
+        m.sync()
+        runs[fuse] = (m.loss, [m.get(i, 1) for i in range(len(params))])
+        m.close()
+    (lf, gf), (lu, gu) = runs[True], runs[False]
+    assert abs(lf - lu) <= 1e-5 * abs(lu), (lf, lu)
+    for i in range(len(params)):
+        scale = float(np.abs(gu[i]).max())
+        if i >= 2 and i % 2 == 0:
+            scale = max(scale, float(np.abs(gu[i - 1]).max()))
+        assert np.abs(gf[i] - gu[i]).max() <= 1e-4 * scale, (i, np.abs(gf[i] - gu[i]).max(), scale)
+
+
 def test_block_full_size_properties(hip):
     """Full C4 shape: one step runs, the loss is near ln(V) for random init, every
     gradient is finite, and a second step reproduces the first bit for bit when

@@ -992,3 +992,55 @@ def test_softmax_xent_keys_rowstats(hip, batch, clen, cols):
     np.testing.assert_array_equal(st2[:, 0], st[:, 0])
     assert_close(st2[:, 1], st[:, 1], what="row sums", **EW)
     assert_close(gloss2.numpy(), gloss.numpy(), what="loss", **EW)
+
+
+@pytest.mark.parametrize("kind", ["relu", "gelu", "silu", "tanh"])
+@pytest.mark.parametrize("M,N,K", [(4100, 4000, 64), (300, 130, 70)])
+def test_gemm_act_fwd(hip, orc, kind, M, N, K):
+    """C = A B + bias and Y = act(C) (the persistent kernel's epilogue for
+    ReLU / GELU / SiLU on the large shape, the activation kernel otherwise)
+    against the oracle's GEMM and activation."""
+    r = rng(M + N + K + hip.ACT[kind])
+    A = r.standard_normal((M, K), dtype=np.float32) * 0.25
+    Bm = r.standard_normal((K, N), dtype=np.float32) * 0.25
+    bias = r.standard_normal(N, dtype=np.float32)
+    c_ref = np.zeros((M, N), np.float32)
+    orc.call("orc_bcmm", 0, orc.ptr(A), orc.ptr(Bm), orc.ptr(c_ref), 1, 1, M, K, N, 0, 3, 3, 3, 1.0)
+    c_ref += bias
+    y_ref = np.zeros_like(c_ref)
+    orc.call("orc_act_fwd", hip.ACT[kind], orc.ptr(c_ref), orc.ptr(y_ref), M * N)
+    gA, gB, gb = B(hip, A), B(hip, Bm), B(hip, bias)
+    gC, gY = hip.Buffer.zeros((M, N)), hip.Buffer.zeros((M, N))
+    hip.call("mle_gemm_act_fwd", None, 0, 0, M, N, K, 1.0, gA.ptr, K, gB.ptr, N, 0.0, gC.ptr, gb.ptr, hip.ACT[kind],
+             gY.ptr, None, 0)
+    assert_close(gC.numpy(), c_ref, what=f"gemm_act_fwd C", **MM)
+    assert_close(gY.numpy(), y_ref, what=f"gemm_act_fwd {kind}", **MM)
+    # the epilogue applies the activation kernels' function to the stored C
+    gY2 = hip.Buffer.zeros((M, N))
+    hip.call("mle_act_fwd", None, hip.ACT[kind], gC.ptr, gY2.ptr, M * N)
+    assert_close(gY.numpy(), gY2.numpy(), what=f"{kind} of the stored C", rtol=1e-6, atol_scale=1e-7)
+
+
+@pytest.mark.parametrize("kind", ["relu", "gelu", "silu", "tanh"])
+@pytest.mark.parametrize("M,N,K,beta,acc", [(3000, 2900, 192, 0.0, 0), (3000, 2900, 192, 1.0, 1),
+                                            (300, 130, 70, 1.0, 1)])
+def test_gemm_act_bwd(hip, orc, kind, M, N, K, beta, acc):
+    """C (+)= A B^T (the activation output's gradient) and dX (+)= C * act'(X)
+    against the oracle's GEMM and activation derivative."""
+    r = rng(M + 2 * N + K + hip.ACT[kind] + acc)
+    A = r.standard_normal((M, K), dtype=np.float32) * 0.25
+    Bm = r.standard_normal((N, K), dtype=np.float32) * 0.25
+    C0 = r.standard_normal((M, N), dtype=np.float32)
+    X = (r.standard_normal((M, N), dtype=np.float32) * 2).astype(np.float32)
+    dX0 = r.standard_normal((M, N), dtype=np.float32)
+    c_ref = C0.copy() if beta else np.zeros((M, N), np.float32)
+    orc.call("orc_bcmm", 1, orc.ptr(A), orc.ptr(Bm), orc.ptr(c_ref), 1, 1, M, K, N, 1, 3, 3, 3, 1.0)
+    dx_ref = dX0.copy() if acc else np.zeros_like(dX0)
+    orc.call("orc_act_bwd", hip.ACT[kind], orc.ptr(X), orc.ptr(c_ref), orc.ptr(dx_ref), M * N)
+    gA, gB, gC, gX, gdX = B(hip, A), B(hip, Bm), B(hip, C0), B(hip, X), B(hip, dX0)
+    if not acc:
+        hip.call("mle_fill", None, gdX.ptr, float("nan"), M * N)  # assign: dX is not read
+    hip.call("mle_gemm_act_bwd", None, 0, 1, M, N, K, 1.0, gA.ptr, K, gB.ptr, K, beta, gC.ptr, hip.ACT[kind], gX.ptr,
+             gdX.ptr, acc, None, 0)
+    assert_close(gC.numpy(), c_ref, what="gemm_act_bwd C", **MM)
+    assert_close(gdX.numpy(), dx_ref, what=f"gemm_act_bwd d{kind}", **MM)
