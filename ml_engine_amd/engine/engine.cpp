@@ -478,10 +478,6 @@ graph_tree topological_sort(const graph& root) {
     result.push_back(node);
   };
   dfs(root);
-  for (auto& n : result) n->consumers = 0;
-  for (auto& n : result)
-    for (auto& in : n->inputs)
-      if (in) ++in->consumers;
   return result;
 }
 
@@ -816,32 +812,12 @@ graph Linear::forward(const graph& X) {
                       p, 0, 1, nullptr, has_bias ? Bb->output : nullptr, ws, ws_bytes),
           "MatMul... X*W1 + B1 in " + name + " forward");
   };
-  node->forward_act = [=](int kind, float* y) {
-    check(mle_gemm_act_fwd(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, W->output, p, 0.0f, nd->output,
-                           has_bias ? Bb->output : nullptr, kind, y, ws, ws_bytes),
-          "MatMul... X*W1 + B1 (with the activation) in " + name + " forward");
-  };
   node->forward_rowstats = [=](float* rowpart, int64_t ldp) {
     check(mle_gemm_rowstats(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, W->output, p, 0.0f,
                             nd->output, p, has_bias ? Bb->output : nullptr, rowpart, ldp, ws, ws_bytes),
           "MatMul... X*W1 + B1 (with row statistics) in " + name + " forward");
   };
   node->backward = [=]() {
-    NodeBackProp* src = x->act_input;
-    if (src && x->consumers == 1 && mle::fusion_enabled()) {
-      // X is an activation's output and this layer its only consumer, so
-      // dX = dZ W^T is X's whole gradient: the activation's input gradient
-      // (deriv_ReLU/GeLU/SiLU) comes out of the same GEMM epilogue.
-      const int acc_x = mle::accumulate_flag(x);
-      check(mle_gemm_act_bwd(mle::stream(), 0, 1, (int)rows, n, p, 1.0f, nd->grad, p, W->output, p, (float)acc_x,
-                             x->grad, x->act_kind, src->output, src->grad, mle::accumulate_flag(src), ws, ws_bytes),
-            "MatMul... dZ*W^T (with the activation derivative) in " + name + " backward");
-      x->act_bwd_done = true;
-      check(mle_gemm_ex(mle::stream(), 1, 0, n, p, (int)rows, 1.0f, x->output, n, 0, nd->grad, p, 0, 1.0f, W->grad,
-                        p, 0, 1, has_bias ? Bb->grad : nullptr, nullptr, ws, ws_bytes),
-            "MatMul... X^T*dZ in " + name + " backward");
-      return;
-    }
     // dX (+)= dZ W^T, dW += X^T dZ, db += colsum dZ (one launch when they fit).
     check(mle_linear_bwd(mle::stream(), (int)rows, n, p, 1, x->output, nd->grad, 0, W->output, 0, x->grad,
                          mle::accumulate_flag(x), W->grad, has_bias ? Bb->grad : nullptr, 0, ws, ws_bytes),
@@ -934,7 +910,6 @@ bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Line
     // Forward: the first sibling of a pass computes Y_i = X W_i + b_i for all
     // (X broadcast, weights, biases and outputs strided).
     outs[i]->forward_rowstats = nullptr;
-    outs[i]->forward_act = nullptr;
     outs[i]->forward = [=]() {
       if ((*fwd_count)++ == 0)
         check(mle_gemm_batched_ex(stream(), 0, 0, (int)rows, p, k, 1.0f, x->output, k, 0, W0->output, p, dw, 0.0f,

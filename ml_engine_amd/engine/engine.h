@@ -155,20 +155,7 @@ struct NodeBackProp {
   // softmax cross-entropy with key targets takes over the node's forward with
   // it and never reads the output again (the hook is cleared then).
   std::function<void(float* rowpart, int64_t ldp)> forward_rowstats;
-  // Set by Linear::forward (additive): computes this node's output as its
-  // forward does and also act(output) into y (MLE_RELU, ...).  An activation
-  // node on this output takes over the node's forward with it.
-  std::function<void(int kind, float* y)> forward_act;
-  // Number of nodes that list this one among their inputs in the graph last
-  // sorted topologically (additive; set by topological_sort).
-  int consumers = 0;
-  // Activation nodes (additive): the node whose output the activation reads,
-  // its kind, and whether a Linear consuming this node's output already wrote
-  // act_input's gradient during the current backward (its only consumer,
-  // fused GEMM epilogue), so this node's backward has nothing left to do.
-  NodeBackProp* act_input = nullptr;
-  int act_kind = -1;
-  bool act_bwd_done = false;
+
   virtual void update(const float lr = LEARNING_RATE, const bool W = ADAMW) {}
   NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation);
   virtual ~NodeBackProp() = default;

@@ -122,23 +122,8 @@ graph act_node(const graph& input, int kind, const str& name) {
   auto node = make_node(name, a, b, c, d);
   node->inputs = {input};
   NodeBackProp *nd = node.get(), *x = input.get();
-  node->act_input = x;
-  node->act_kind = kind;
   node->forward = [=]() { check(mle_act_fwd(S(), kind, x->output, nd->output, nd->total), name + " forward"); };
-  if (mle::fusion_enabled() && input->forward_act) {
-    // A Linear's output: its GEMM epilogue writes the activation too.
-    auto fa = input->forward_act;
-    float* y = nd->output;
-    input->forward = [fa, kind, y]() { fa(kind, y); };
-    input->forward_act = nullptr;
-    input->forward_rowstats = nullptr;
-    node->forward = []() {};
-  }
   node->backward = [=]() {
-    if (nd->act_bwd_done) {  // the consuming Linear's epilogue wrote x's gradient
-      nd->act_bwd_done = false;
-      return;
-    }
     check(mle_act_bwd(S(), kind, x->output, nd->grad, x->grad, nd->total, mle::accumulate_flag(x)), "Deriv " + name);
   };
   std_hooks(node);

@@ -201,12 +201,10 @@ def test_block_qkv_fusion(hip, quirks):
 
 
 def test_block_fusion_full_size(hip):
-    """Full C4 shape, where the fused epilogues run on the persistent GEMM
-    kernel (FFN-in forward with GELU, FFN-out input gradient with GELU',
-    LM-head row statistics for the loss, batched Q/K/V): one step agrees with
-    the unfused graph (one GEMM per layer, separate activation and loss
-    kernels) -- loss within 1e-5, every parameter gradient within 1e-4 of its
-    scale."""
+    """Full C4 shape, where the graph fusions run on the persistent GEMM kernel
+    (LM-head row statistics for the loss, batched Q/K/V): one step agrees with
+    the unfused graph (one GEMM per layer, a loss that reads the logits) --
+    loss within 1e-5, every parameter gradient within 1e-4 of its scale."""
     cfg = BlockConfig()
     ids, tgt, params = block_data(cfg, seed=3)
     runs = {}
