@@ -427,8 +427,228 @@ __global__ __launch_bounds__(NT, 2) void conv_fast_kernel(FastConv c) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Register-direct 3 x 3 convolution, stride 1, pad 1 (output grid = input
+// grid): forward and input gradient with no LDS in the K loop.
+//
+//   C[m][pixel] = sum over (c, kh, kw) of A(m, c, kh, kw) * S[c][pixel + shift(kh, kw)]
+//   forward: S = x,  m = output channel, A = w[m][c][kh][kw], shift (kh - 1, kw - 1)
+//   dgrad:   S = dy, m = input channel,  A = w[c][m][kh][kw], shift (1 - kh, 1 - kw)
+//
+// Each wave owns a 64 x 64 block of C (64 channels x 64 pixels) as 4 x 4 MFMA
+// blocks of 16 x 16.  Lane (lr, q) owns pixels g .. g + 3 (g = the wave's
+// first pixel + 4 lr) and feeds channel c0 + q to every MFMA step: its B
+// operand for block n is S at pixel g + n, so one float4 of S serves the four
+// blocks, and each (block i, r) of the result is one 16-byte store.  The K
+// loop walks (kh, channel); the three kw taps are three MFMA steps sharing
+// that float4: the column shifts by -1 and +1 take the edge element of the
+// neighbouring lane with a DPP row shift (a DPP row is the 16 lanes of one q
+// group, 64 consecutive pixels), and the three taps' weights arrive in one
+// dwordx3 load (w[..][..][kh][0..2] is contiguous).  The tap that falls in
+// the padding of column 0 or W - 1 reads zero.  When 64 is not a multiple of
+// W, lanes 0 and 15 of a DPP row can need a pixel owned by another wave; they
+// load that element themselves (HALO).  A row shift out of the image, a pixel
+// past the batch or a row past M reads at kOOB and gets 0; stores there are
+// dropped by the buffer range check.
+struct Conv3Args {
+  const float* src;   // S [batch][cs][h][w]
+  const float* wt;    // [cout][cin][3][3]
+  const float* bias;  // forward only, nullable
+  float* out;         // [batch][M][h][w]
+  uint32_t src_bytes, wt_bytes, out_bytes;
+  int M, cs, h, w, hw, npix;
+  int a_rs, a_cs;  // weight offset (floats) per row m and per source channel c
+  int acc;         // dgrad: 1 accumulates into out
+  int tiles_m, tiles;
+};
+
+typedef float f32x3 __attribute__((ext_vector_type(3)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float lane_from_left(float v) {  // lane i gets lane i - 1 of its DPP row, 0 at lane 0
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float lane_from_right(float v) {  // lane i gets lane i + 1, 0 at lane 15
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x101, 0xF, 0xF, true));
+}
+
+template <bool DG, bool HALO, int WM, int WN, int U, int D>
+__global__ __launch_bounds__(64 * WM * WN, 2) void conv3_direct_kernel(Conv3Args c) {
+  constexpr int SG = DG ? -1 : 1;  // shift of tap t is SG * (t - 1)
+  constexpr int CPS = 4 * U;       // channels per stage
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, q = lane >> 4;
+  const int wm = wave % WM, wn = wave / WM;
+  // Workgroup -> tile: consecutive tiles on one XCD (workgroups are dealt to
+  // the 8 XCDs round robin), so neighbouring pixel tiles share its L2.
+  const int L = blockIdx.x, xq = c.tiles / 8, xr = c.tiles % 8, xc = L % 8;
+  const int item = xc * xq + min(xc, xr) + L / 8;
+  const int tm = item % c.tiles_m, tn = item / c.tiles_m;
+  const int m0 = (tm * WM + wm) * 64;
+  const int g = (tn * WN + wn) * 64 + 4 * lr;
+  const bool gok = g < c.npix;
+  const int b = g / c.hw, p = g - b * c.hw, py = p / c.w, px = p - py * c.w;
+  const bool lpad = px == 0, rpad = px + 4 == c.w;
+  bool rok[3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t) rok[t] = gok && (unsigned)(py + SG * (t - 1)) < (unsigned)c.h;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(c.src, c.src_bytes);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(c.wt, c.wt_bytes);
+  const uint32_t b_base = (uint32_t)((b * c.cs + q) * c.hw + p) * 4u;
+  uint32_t a_base[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + 16 * i + lr;
+    a_base[i] = row < c.M ? (uint32_t)(row * c.a_rs + q * c.a_cs) * 4u : kOOB;
+  }
+  const int spk = c.cs / CPS;  // stages per tap row
+  const int nk = 3 * spk;
+
+  // Stage kt: tap row t, channels cb .. cb + CPS - 1.  Stages fetched past
+  // the end (up to D - 1) stay in bounds of the 32-bit offsets (the host
+  // checks the extents) and are never consumed.
+  auto load = [&](int kt, f32x3(&fa)[U][4], f32x4(&fb)[U], float(&fh)[U]) {
+    const int t = (kt >= spk) + (kt >= 2 * spk);
+    const int cb = (kt - t * spk) * CPS;
+    const bool ok = t == 0 ? rok[0] : (t == 1 ? rok[1] : rok[2]);
+    const int rsh = SG * (t - 1) * c.w;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t da = (uint32_t)((cb + 4 * u) * c.a_cs + 3 * t) * 4u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        fa[u][i] = __builtin_bit_cast(f32x3, __builtin_amdgcn_raw_buffer_load_b96(ra, (int)(a_base[i] + da), 0, 0));
+      const uint32_t off = b_base + (uint32_t)((cb + 4 * u) * c.hw + rsh) * 4u;
+      fb[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(ok ? off : kOOB), 0, 0));
+      if (HALO) {
+        const uint32_t ho = lr == 0 ? (lpad ? kOOB : off - 4u) : (lr == 15 ? (rpad ? kOOB : off + 16u) : kOOB);
+        fh[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(ok ? ho : kOOB), 0, 0));
+      }
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto mfma = [&](const f32x3(&fa)[U][4], const f32x4(&fb)[U], const float(&fh)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const f32x4 v = fb[u];
+      float lf = lane_from_left(v[3]), rt = lane_from_right(v[0]);
+      if (HALO) {
+        lf = lr == 0 ? fh[u] : lf;
+        rt = lr == 15 ? fh[u] : rt;
+      }
+      lf = lpad ? 0.f : lf;
+      rt = rpad ? 0.f : rt;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const int d = SG * (j - 1);
+        float bv[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) bv[n] = d == 0 ? v[n] : (d < 0 ? (n == 0 ? lf : v[n - 1]) : (n == 3 ? rt : v[n + 1]));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int n = 0; n < 4; ++n)
+            acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[u][i][j], bv[n], acc[i][n], 0, 0, 0);
+      }
+    }
+  };
+
+  // Stage s lives in register set s % D; loads run D - 1 stages ahead.
+  f32x3 fa[D][U][4];
+  f32x4 fb[D][U];
+  float fh[D][U];
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load(s, fa[s], fb[s], fh[s]);
+  int kt = 0;
+  for (; kt + D - 1 < nk; kt += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      load(kt + s + D - 1, fa[(s + D - 1) % D], fb[(s + D - 1) % D], fh[(s + D - 1) % D]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(fa[s], fb[s], fh[s]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s)
+    if (kt + s < nk) mfma(fa[s], fb[s], fh[s]);
+
+  // Epilogue: (i, r) is row m0 + 16 i + 4 q + r, pixels g .. g + 3.
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + 16 * i + 4 * q + r;
+      const bool ok = gok && row < c.M;
+      const uint32_t off = ok ? (uint32_t)((b * c.M + row) * c.hw + p) * 4u : kOOB;
+      f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+      if (!DG && c.bias && ok) v += c.bias[row];
+      if (DG && c.acc) v += buf_ld4(ro, off);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, (int)off, 0, 0);
+    }
+}
+
 bool fits_2g(double elems) { return elems * 4.0 < 2147483647.0; }
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+constexpr int kC3U = 2, kC3D = 4;  // channel quads per stage, stages in flight
+
+template <bool DG, bool HALO, int WM>
+void launch_conv3(hipStream_t s, const Conv3Args& c) {
+  conv3_direct_kernel<DG, HALO, WM, 2, kC3U, kC3D><<<c.tiles, 64 * WM * 2, 0, s>>>(c);
+}
+
+// Register-direct path for a 3 x 3, stride 1, pad 1 forward (dg = 0: src = x,
+// M = cout) or input gradient (dg = 1: src = dy, M = cin).  Returns false,
+// launching nothing, when the shape is outside what the kernel assumes.
+bool conv3_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, const float* wt, const float* bias,
+                  float* out, int acc) {
+  if (g.kh != 3 || g.kw != 3 || g.pad != 1 || g.stride != 1 || g.w % 4 != 0) return false;
+  const int M = dg ? g.cin : g.cout, cs = dg ? g.cout : g.cin;
+  if (cs % (4 * kC3U) != 0 || !a16(out)) return false;
+  const double hw = (double)g.h * g.w;
+  // 32-bit byte offsets: tensors below 2 GiB, weights below 1 GiB (an
+  // out-of-range row's kOOB offset plus a weight offset must not wrap).
+  if ((double)g.n * cs * hw * 4.0 >= 2147483647.0 || (double)g.n * M * hw * 4.0 >= 2147483647.0 ||
+      (double)g.cout * g.cin * 9 * 4.0 >= 1073741824.0)
+    return false;
+  Conv3Args c{};
+  c.src = src;
+  c.wt = wt;
+  c.bias = dg ? nullptr : bias;
+  c.out = out;
+  c.src_bytes = (uint32_t)((size_t)g.n * cs * g.h * g.w * 4);
+  c.wt_bytes = (uint32_t)((size_t)g.cout * g.cin * 9 * 4);
+  c.out_bytes = (uint32_t)((size_t)g.n * M * g.h * g.w * 4);
+  c.M = M;
+  c.cs = cs;
+  c.h = g.h;
+  c.w = g.w;
+  c.hw = g.h * g.w;
+  c.npix = g.n * c.hw;
+  c.a_rs = dg ? 9 : g.cin * 9;
+  c.a_cs = dg ? g.cin * 9 : 9;
+  c.acc = acc;
+  const int wm = M <= 64 ? 1 : 2;
+  c.tiles_m = (M + 64 * wm - 1) / (64 * wm);
+  c.tiles = c.tiles_m * ((c.npix + 127) / 128);
+  const bool halo = 64 % g.w != 0;
+  if (dg) {
+    if (halo) wm == 1 ? launch_conv3<true, true, 1>(s, c) : launch_conv3<true, true, 2>(s, c);
+    else wm == 1 ? launch_conv3<true, false, 1>(s, c) : launch_conv3<true, false, 2>(s, c);
+  } else {
+    if (halo) wm == 1 ? launch_conv3<false, true, 1>(s, c) : launch_conv3<false, true, 2>(s, c);
+    else wm == 1 ? launch_conv3<false, false, 1>(s, c) : launch_conv3<false, false, 2>(s, c);
+  }
+  return true;
+}
 
 template <int KIND>
 void launch_fast(hipStream_t s, const FastConv& c, int kh, int splits) {
@@ -482,7 +702,8 @@ int mle_conv2d_fwd(mle_stream stream, const float* x, const float* w, const floa
   hipStream_t s = as_stream(stream);
   ProbeScope probe("conv_fwd", s, 2.0 * op.M * (double)op.N * op.K, 0.0);
   const int ohw = g.oh * g.ow;
-  if (fast_filter(g) && ohw % 4 == 0 && op.K % 4 == 0 && a16(y) && fits_2g((double)n * cin * h * w_in) &&
+  if (conv3_direct(s, false, g, x, w, b, y, 0)) {
+  } else if (fast_filter(g) && ohw % 4 == 0 && op.K % 4 == 0 && a16(y) && fits_2g((double)n * cin * h * w_in) &&
       fits_2g((double)n * cout * ohw) && fits_2g((double)cout * op.K)) {
     FastConv c{x, w, b, y, (uint32_t)((size_t)n * cin * h * w_in * 4), (uint32_t)((size_t)cout * op.K * 4),
                op.M, op.N, op.K, op.K, cin, h, w_in, h * w_in, g.oh, g.ow, ohw, pad, cout, cin, 0};
@@ -504,7 +725,8 @@ int mle_conv2d_dgrad(mle_stream stream, const float* dy, const float* w, float* 
   hipStream_t s = as_stream(stream);
   ProbeScope probe("conv_dgrad", s, 2.0 * op.M * (double)op.N * op.K, 0.0);
   const int hw = h * w_in;
-  if (fast_filter(g) && hw % 4 == 0 && a16(dx) && fits_2g((double)n * cin * hw) &&
+  if (conv3_direct(s, true, g, dy, w, nullptr, dx, accumulate != 0)) {
+  } else if (fast_filter(g) && hw % 4 == 0 && a16(dx) && fits_2g((double)n * cin * hw) &&
       fits_2g((double)n * cout * g.oh * g.ow) && fits_2g((double)cout * cin * kh * kw)) {
     FastConv c{dy, w, nullptr, dx, (uint32_t)((size_t)n * cout * g.oh * g.ow * 4),
                (uint32_t)((size_t)cout * cin * kh * kw * 4), op.M, op.N, op.K, op.K, cout, g.oh, g.ow, g.oh * g.ow,
