@@ -10,6 +10,8 @@
 // in the workspace and one pass adds them in split order (assign semantics).
 #include "gemm_core.hpp"
 
+#include <algorithm>
+
 using namespace mle;
 using namespace gemm;
 
@@ -472,13 +474,13 @@ __device__ __forceinline__ float lane_from_right(float v) {  // lane i gets lane
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x101, 0xF, 0xF, true));
 }
 
-template <bool DG, bool HALO, int WM, int WN, int U, int D>
-__global__ __launch_bounds__(64 * WM * WN, 2) void conv3_direct_kernel(Conv3Args c) {
+template <bool DG, bool HALO, int WM, int WN, int KS, int U, int D>
+__global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv3_direct_kernel(Conv3Args c) {
   constexpr int SG = DG ? -1 : 1;  // shift of tap t is SG * (t - 1)
   constexpr int CPS = 4 * U;       // channels per stage
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, q = lane >> 4;
-  const int wm = wave % WM, wn = wave / WM;
+  const int wm = wave % WM, wn = (wave / WM) % WN, ks = wave / (WM * WN);
   // Workgroup -> tile: consecutive tiles on one XCD (workgroups are dealt to
   // the 8 XCDs round robin), so neighbouring pixel tiles share its L2.
   const int L = blockIdx.x, xq = c.tiles / 8, xr = c.tiles % 8, xc = L % 8;
@@ -502,7 +504,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void conv3_direct_kernel(Conv3Args
     a_base[i] = row < c.M ? (uint32_t)(row * c.a_rs + q * c.a_cs) * 4u : kOOB;
   }
   const int spk = c.cs / CPS;  // stages per tap row
-  const int nk = 3 * spk;
+  // KS waves share each 64 x 64 block, splitting its stages: wave ks runs
+  // [k0, k1) and the partial sums meet in LDS at the end.
+  const int nks = (3 * spk + KS - 1) / KS;
+  const int k0 = ks * nks, k1 = min(3 * spk, k0 + nks);
 
   // Stage kt: tap row t, channels cb .. cb + CPS - 1.  Stages fetched past
   // the end (up to D - 1) stay in bounds of the 32-bit offsets (the host
@@ -564,9 +569,9 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void conv3_direct_kernel(Conv3Args
   f32x4 fb[D][U];
   float fh[D][U];
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) load(s, fa[s], fb[s], fh[s]);
-  int kt = 0;
-  for (; kt + D - 1 < nk; kt += D) {
+  for (int s = 0; s < D - 1; ++s) load(k0 + s, fa[s], fb[s], fh[s]);
+  int kt = k0;
+  for (; kt + D - 1 < k1; kt += D) {
 #pragma unroll
     for (int s = 0; s < D; ++s) {
       load(kt + s + D - 1, fa[(s + D - 1) % D], fb[(s + D - 1) % D], fh[(s + D - 1) % D]);
@@ -577,7 +582,36 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void conv3_direct_kernel(Conv3Args
   }
 #pragma unroll
   for (int s = 0; s < D - 1; ++s)
-    if (kt + s < nk) mfma(fa[s], fb[s], fh[s]);
+    if (kt + s < k1) mfma(fa[s], fb[s], fh[s]);
+
+  if (KS > 1) {
+    // Waves ks > 0 hand their partial blocks to wave ks = 0 through LDS
+    // (lane-major, so each write and read is conflict free), which adds them
+    // in ks order and stores.
+    __shared__ float red[KS > 1 ? (KS - 1) * WM * WN * 64 * 64 : 1];
+    const int blk = wave % (WM * WN);
+    if (ks > 0) {
+      float* dst = red + ((ks - 1) * WM * WN + blk) * 64 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[((i * 4 + n) * 4 + r) * 64] = acc[i][n][r];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int k = 1; k < KS; ++k) {
+      const float* src = red + ((k - 1) * WM * WN + blk) * 64 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][n][r] += src[((i * 4 + n) * 4 + r) * 64];
+    }
+  }
 
   // Epilogue: (i, r) is row m0 + 16 i + 4 q + r, pixels g .. g + 3.
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
@@ -595,14 +629,175 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void conv3_direct_kernel(Conv3Args
     }
 }
 
+// ---------------------------------------------------------------------------
+// Register-direct 3 x 3 weight gradient, stride 1, pad 1:
+//   dW[co][ci][kh][kw] = sum over pixels p of dy[co][p] * x[ci][p + (kh - 1, kw - 1)]
+// as C[co][(ci, kh, kw)] with K = the batch's pixels, split across workgroups
+// (each split writes its partial C; a second pass adds them in split order).
+// Lane (lr, q) of a wave owns one (ci, kh) pair (16 pairs per wave) and its
+// three kw taps are the wave's three MFMA column blocks, so a wave's block is
+// 64 output channels x 48 columns.  Per 16-pixel stage lane group q feeds
+// pixels P .. P + 3 (P = stage start + 4 q) to the four MFMA steps: dy as one
+// aligned float4 per 16-row block, x of its (ci, kh) row as one aligned
+// float4 plus the two neighbours x[P - 1] and x[P + 4], from which the three
+// taps' operands are picked in registers.  A neighbour in the column padding,
+// a row shift out of the image, a pixel past the split, a pair past cin * 3
+// or a row past cout reads at kOOB and gets 0.  The lane's pixel position
+// advances by 16 per stage with at most one row and one image carry (W >= 16).
+struct Wgrad3Args {
+  const float* x;   // [n][cin][h][w]
+  const float* dy;  // [n][cout][h][w]
+  float* out;       // one split: dW [cout][cin * 9]; else partials [splits][cout][cin * 9]
+  uint32_t x_bytes, dy_bytes, out_bytes;
+  int cout, cin, h, w, hw, npix;
+  int chunk;  // pixels per split, a multiple of 16
+  int tiles_m, tiles, items;
+};
+
+template <int WM, int D>
+__global__ __launch_bounds__(256, 2) void conv3_wgrad_kernel(Wgrad3Args c) {
+  constexpr int WN = 4 / WM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, q = lane >> 4;
+  const int wm = wave % WM, wn = wave / WM;
+  // Workgroup -> (tile, split): consecutive items on one XCD, tiles of one
+  // split adjacent (they read the same dy and x pixels).
+  const int L = blockIdx.x, xq = c.items / 8, xr = c.items % 8, xc = L % 8;
+  const int item = xc * xq + min(xc, xr) + L / 8;
+  const int tile = item % c.tiles, split = item / c.tiles;
+  const int tm = tile % c.tiles_m, tn = tile / c.tiles_m;
+  const int m0 = (tm * WM + wm) * 64;
+  const int pair = (tn * WN + wn) * 16 + lr;
+  const bool pok = pair < 3 * c.cin;
+  const int ci = pair / 3, kh = pair - 3 * ci;
+  const int kbeg = split * c.chunk, kend = min(c.npix, kbeg + c.chunk);
+  const int nk = (kend - kbeg + 15) / 16;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(c.x, c.x_bytes);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(c.dy, c.dy_bytes);
+  uint32_t a_row[4];
+  bool a_ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int co = m0 + 16 * i + lr;
+    a_ok[i] = co < c.cout;
+    a_row[i] = (uint32_t)(co * c.hw) * 4u;
+  }
+  const uint32_t x_lane = (uint32_t)(ci * c.hw + (kh - 1) * c.w) * 4u;  // modulo 2^32
+  // Load cursor: the next stage's pixel P of this lane, its column px and row
+  // py, and its pixel byte offsets in dy and x (without the channel part).
+  // Advancing 16 pixels adds 64 bytes, plus the rest of an image's channel
+  // planes when P crosses into the next image; W >= 16, so at most one row
+  // and one image carry.  Only adds and selects: no multiplies in the loop.
+  int P = kbeg + 4 * q;
+  int py, px;
+  uint32_t dpix, xpix;
+  {
+    const int b = P / c.hw, pp = P - b * c.hw;
+    py = pp / c.w;
+    px = pp - py * c.w;
+    dpix = (uint32_t)(b * c.cout * c.hw + pp) * 4u;
+    xpix = (uint32_t)(b * c.cin * c.hw + pp) * 4u;
+  }
+  const uint32_t d_img = (uint32_t)((c.cout - 1) * c.hw) * 4u, x_img = (uint32_t)((c.cin - 1) * c.hw) * 4u;
+
+  auto load = [&](f32x4(&fa)[4], f32x4& fb, float& fl, float& fr) {
+    const bool pix = P < kend;
+    const bool rowok = (unsigned)(py + kh - 1) < (unsigned)c.h;
+    // Offsets are selected (bitwise conditions, no short circuit) so the
+    // loads stay unconditional.
+    uint32_t ao[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ao[i] = (pix & a_ok[i]) ? a_row[i] + dpix : kOOB;
+    const bool ok = pix & rowok & pok;
+    const uint32_t xo = x_lane + xpix;
+    const uint32_t xc = ok ? xo : kOOB;
+    const uint32_t xl = (ok & (px != 0)) ? xo - 4u : kOOB;
+    const uint32_t xr = (ok & (px + 4 != c.w)) ? xo + 16u : kOOB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, (int)ao[i], 0, 0));
+    fb = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xc, 0, 0));
+    fl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, (int)xl, 0, 0));
+    fr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, (int)xr, 0, 0));
+    P += 16;
+    px += 16;
+    dpix += 64u;
+    xpix += 64u;
+    const bool cx = px >= c.w;
+    px = cx ? px - c.w : px;
+    py += cx ? 1 : 0;
+    const bool cy = py >= c.h;
+    py = cy ? 0 : py;
+    dpix += cy ? d_img : 0u;
+    xpix += cy ? x_img : 0u;
+  };
+
+  f32x4 acc[4][3];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 3; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto mfma = [&](const f32x4(&fa)[4], const f32x4& v, float fl, float fr) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float b0 = j == 0 ? fl : v[j - 1];
+      const float b2 = j == 3 ? fr : v[j + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][j], b0, acc[i][0], 0, 0, 0);
+        acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][j], v[j], acc[i][1], 0, 0, 0);
+        acc[i][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][j], b2, acc[i][2], 0, 0, 0);
+      }
+    }
+  };
+
+  f32x4 fa[D][4], fb[D];
+  float fl[D], fr[D];
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load(fa[s], fb[s], fl[s], fr[s]);
+  int kt = 0;
+  for (; kt + D - 1 < nk; kt += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int ls = (s + D - 1) % D;
+      load(fa[ls], fb[ls], fl[ls], fr[ls]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(fa[s], fb[s], fl[s], fr[s]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s)
+    if (kt + s < nk) mfma(fa[s], fb[s], fl[s], fr[s]);
+
+  // (i, r) is row m0 + 16 i + 4 q + r, columns 3 pair .. 3 pair + 2.
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
+  const int ncol = 9 * c.cin;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + 16 * i + 4 * q + r;
+      const bool ok = pok && row < c.cout;
+      const uint32_t off = ok ? (uint32_t)(((split * c.cout + row) * ncol) + 3 * pair) * 4u : kOOB;
+      const f32x3 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r]};
+      __builtin_amdgcn_raw_buffer_store_b96(__builtin_bit_cast(__attribute__((ext_vector_type(3))) unsigned, v), ro,
+                                            (int)off, 0, 0);
+    }
+}
+
 bool fits_2g(double elems) { return elems * 4.0 < 2147483647.0; }
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 constexpr int kC3U = 2, kC3D = 4;  // channel quads per stage, stages in flight
 
+// 64-row blocks (M <= 64) split each block's stages over two waves, so the
+// grid still holds two waves per SIMD.
 template <bool DG, bool HALO, int WM>
 void launch_conv3(hipStream_t s, const Conv3Args& c) {
-  conv3_direct_kernel<DG, HALO, WM, 2, kC3U, kC3D><<<c.tiles, 64 * WM * 2, 0, s>>>(c);
+  constexpr int KS = WM == 1 ? 2 : 1;
+  conv3_direct_kernel<DG, HALO, WM, 2, KS, kC3U, kC3D><<<c.tiles, 64 * WM * 2 * KS, 0, s>>>(c);
 }
 
 // Register-direct path for a 3 x 3, stride 1, pad 1 forward (dg = 0: src = x,
@@ -671,6 +866,60 @@ int geom(int n, int cin, int h, int w, int cout, int kh, int kw, int pad, int st
 
 bool fast_filter(const ConvGeom& g) {
   return g.stride == 1 && ((g.kh == 3 && g.kw == 3) || (g.kh == 1 && g.kw == 1));
+}
+
+// Workgroups of conv3_wgrad_kernel<WM, 4> resident at once on the current
+// device (per-CU occupancy x CUs; 3 x 256 on MI355X).  One full round of
+// resident workgroups measured fastest: at 512 workgroups on 768 slots some
+// CUs hold 1 and others 3 (54 % of fp32 MFMA for the C5 weight gradients),
+// at 768 every CU holds 3 (77 %), at 1024 the last 256 run as a tail (62 %).
+int wgrad3_slots(int wm) {
+  static int cached[64][2] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 768;
+  int& v = cached[dev][wm - 1];
+  if (v <= 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    const hipError_t e = wm == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3_wgrad_kernel<1, 4>, 256, 0)
+                                 : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3_wgrad_kernel<2, 4>, 256, 0);
+    if (e != hipSuccess || per_cu <= 0) per_cu = 2;
+    v = per_cu * cus;
+  }
+  return v;
+}
+
+// Register-direct 3 x 3 weight gradient plan: 128 x 96 (or 64 x 192 when
+// cout <= 64) tiles of C, the pixels split so that tiles x splits fills one
+// round of resident workgroups, each split a whole number of 16-pixel stages
+// and at least 256 pixels.  Returns false when the shape is outside what
+// conv3_wgrad_kernel assumes.
+bool wgrad3_plan(const ConvGeom& g, Wgrad3Args& c) {
+  if (g.kh != 3 || g.kw != 3 || g.pad != 1 || g.stride != 1 || g.w % 4 != 0 || g.w < 16) return false;
+  const double hw = (double)g.h * g.w;
+  if ((double)g.n * g.cin * hw * 4.0 >= 2147483647.0 || (double)g.n * g.cout * hw * 4.0 >= 2147483647.0) return false;
+  c = Wgrad3Args{};
+  c.cout = g.cout;
+  c.cin = g.cin;
+  c.h = g.h;
+  c.w = g.w;
+  c.hw = g.h * g.w;
+  c.npix = g.n * c.hw;
+  const int wm = g.cout <= 64 ? 1 : 2, wn = 4 / wm;
+  c.tiles_m = (g.cout + 64 * wm - 1) / (64 * wm);
+  c.tiles = c.tiles_m * ((3 * g.cin + 16 * wn - 1) / (16 * wn));
+  const int slots = wgrad3_slots(wm);
+  int splits = std::max(1, slots / c.tiles);
+  const int max_splits = (c.npix + 255) / 256;
+  splits = std::max(1, std::min(splits, max_splits));
+  c.chunk = ((c.npix + splits - 1) / splits + 15) / 16 * 16;
+  splits = (c.npix + c.chunk - 1) / c.chunk;
+  c.items = c.tiles * splits;
+  if ((double)splits * g.cout * g.cin * 9 * 4.0 >= 2147483647.0) return false;
+  c.x_bytes = (uint32_t)((size_t)g.n * g.cin * c.hw * 4);
+  c.dy_bytes = (uint32_t)((size_t)g.n * g.cout * c.hw * 4);
+  c.out_bytes = (uint32_t)((size_t)splits * g.cout * g.cin * 9 * 4);
+  return true;
 }
 
 // K split for wgrad: aim for >= ~512 workgroups, chunks of whole BK slices.
@@ -742,6 +991,8 @@ int mle_conv2d_dgrad(mle_stream stream, const float* dy, const float* w, float* 
 size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride) {
   ConvGeom g;
   if (geom(n, cin, h, w_in, cout, kh, kw, pad, stride, g) != MLE_OK) return 0;
+  Wgrad3Args c3;
+  if (wgrad3_plan(g, c3)) return c3.items > c3.tiles ? (size_t)c3.out_bytes : 0;
   int kchunk;
   const int splits = wgrad_splits(g, kchunk);
   return (size_t)splits * cout * cin * kh * kw * sizeof(float);
@@ -749,16 +1000,38 @@ size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int 
 
 int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* dw, int n, int cin, int h, int w_in,
                      int cout, int kh, int kw, int pad, int stride, void* ws, size_t ws_bytes) {
-  MLE_CHECK_ARG(x && dy && dw && ws, "mle_conv2d_wgrad: null pointer");
+  MLE_CHECK_ARG(x && dy && dw, "mle_conv2d_wgrad: null pointer");
   ConvGeom g;
   int rc = geom(n, cin, h, w_in, cout, kh, kw, pad, stride, g);
   if (rc) return rc;
+  const size_t need = mle_conv2d_wgrad_ws_bytes(n, cin, h, w_in, cout, kh, kw, pad, stride);
+  if (ws_bytes < need || (need > 0 && !ws)) return set_error(MLE_ERR_WORKSPACE, "mle_conv2d_wgrad: workspace too small");
+  hipStream_t s = as_stream(stream);
+  const double flop = 2.0 * cout * (double)cin * kh * kw * (double)n * g.oh * g.ow;
+  Wgrad3Args c3;
+  if (wgrad3_plan(g, c3)) {
+    const int splits = c3.items / c3.tiles;
+    c3.x = x;
+    c3.dy = dy;
+    c3.out = splits > 1 ? static_cast<float*>(ws) : dw;
+    if (splits == 1) c3.out_bytes = (uint32_t)((size_t)cout * cin * 9 * 4);
+    {
+      ProbeScope probe("conv_wgrad", s, flop, 0.0);
+      if (cout <= 64) conv3_wgrad_kernel<1, 4><<<c3.items, 256, 0, s>>>(c3);
+      else conv3_wgrad_kernel<2, 4><<<c3.items, 256, 0, s>>>(c3);
+    }
+    if (splits > 1) {
+      const size_t mn = (size_t)cout * cin * 9;
+      if (mn % 4 == 0 && aligned16(ws) && aligned16(dw))
+        split_reduce_kernel<true><<<(unsigned)((mn / 4 + 255) / 256), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
+      else
+        split_reduce_kernel<false><<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
+    }
+    return check_launch("mle_conv2d_wgrad");
+  }
   int kchunk;
   const int splits = wgrad_splits(g, kchunk);
-  if (ws_bytes < mle_conv2d_wgrad_ws_bytes(n, cin, h, w_in, cout, kh, kw, pad, stride))
-    return set_error(MLE_ERR_WORKSPACE, "mle_conv2d_wgrad: workspace too small");
   WgradOps op{x, dy, static_cast<float*>(ws), g, cout, cin * kh * kw, n * g.oh * g.ow};
-  hipStream_t s = as_stream(stream);
   {
     ProbeScope probe("conv_wgrad", s, 2.0 * op.M * (double)op.N * op.K, 0.0);
     const int ohw = g.oh * g.ow;

@@ -642,9 +642,11 @@ def test_conv_transpose_composition(hip, orc, n, cin, h, w, cout, k, pad, stride
     # register-direct 3x3 path (stride 1, pad 1, W % 4 == 0): W dividing 64
     # (4, 8, 16, 64), W needing the lane-0 / lane-15 halo loads (12, 20, 128),
     # images straddling a 64-pixel lane row (hw 60, 140), partial pixel tiles,
-    # 64-row and 128-row channel tiles with partial rows (72, 40)
+    # 64-row and 128-row channel tiles with partial rows (72, 40); the weight
+    # gradient's pixel splits carry rows and images (W >= 16)
     (3, 8, 4, 4, 8, 3, 1, 1), (2, 24, 8, 8, 40, 3, 1, 1), (2, 8, 5, 12, 16, 3, 1, 1),
     (2, 16, 7, 20, 24, 3, 1, 1), (1, 16, 3, 128, 72, 3, 1, 1), (2, 64, 64, 64, 128, 3, 1, 1),
+    (1, 8, 4, 16, 8, 3, 1, 1),  # one pixel split: the weight gradient is written without partials
 ])
 def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
     r = rng(n * 7 + cin + h + cout + k)
