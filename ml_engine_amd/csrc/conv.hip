@@ -181,32 +181,51 @@ __global__ __launch_bounds__(NT, 2) void igemm_kernel(Ops op, int kchunk) {
     }
 }
 
-// out = sum_s part[s] in split order; float4 per thread when possible, with the
-// loads of four splits issued together.
+// out = sum over s of part[s].  A workgroup covers 64 columns (float4 each
+// when possible) with four split groups: thread (column, g) adds splits
+// g, g + 4, g + 8, ... in order, and the four group sums are added in group
+// order through LDS, so the result does not depend on timing.  Four waves
+// per 64 columns keep enough loads in flight for the few-hundred-KB outputs
+// of a weight gradient.
 template <bool VEC>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, int splits, size_t mn,
                                                            float* __restrict__ out) {
   constexpr int W = VEC ? 4 : 1;
-  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * W;
-  if (i >= mn) return;
+  __shared__ f32x4 grp[4][64];
+  const int col = threadIdx.x & 63, sg = threadIdx.x >> 6;
+  const size_t i = ((size_t)blockIdx.x * 64 + col) * W;
+  const bool live = i < mn;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int s = 0;
-  for (; s + 4 <= splits; s += 4) {
-    f32x4 v[4];
+  if (live) {
+    int s = sg;
+    for (; s + 12 < splits; s += 16) {
+      f32x4 v[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (VEC) v[u] = *reinterpret_cast<const f32x4*>(part + (size_t)(s + u) * mn + i);
-      else v[u][0] = part[(size_t)(s + u) * mn + i];
+      for (int u = 0; u < 4; ++u) {
+        if (VEC) v[u] = *reinterpret_cast<const f32x4*>(part + (size_t)(s + 4 * u) * mn + i);
+        else v[u] = f32x4{part[(size_t)(s + 4 * u) * mn + i], 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc += v[u];
     }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc += v[u];
+    for (; s < splits; s += 4) {
+      if (VEC) acc += *reinterpret_cast<const f32x4*>(part + (size_t)s * mn + i);
+      else acc[0] += part[(size_t)s * mn + i];
+    }
   }
-  for (; s < splits; ++s) {
-    if (VEC) acc += *reinterpret_cast<const f32x4*>(part + (size_t)s * mn + i);
-    else acc[0] += part[(size_t)s * mn + i];
-  }
-  if (VEC) *reinterpret_cast<f32x4*>(out + i) = acc;
-  else out[i] = acc[0];
+  grp[sg][col] = acc;
+  __syncthreads();
+  if (sg != 0 || !live) return;
+  const f32x4 r = ((grp[0][col] + grp[1][col]) + grp[2][col]) + grp[3][col];
+  if (VEC) *reinterpret_cast<f32x4*>(out + i) = r;
+  else out[i] = r[0];
+}
+
+void launch_split_reduce(hipStream_t s, const float* part, int splits, size_t mn, float* out) {
+  if (mn % 4 == 0 && aligned16(part) && aligned16(out))
+    split_reduce_kernel<true><<<(unsigned)((mn / 4 + 63) / 64), 256, 0, s>>>(part, splits, mn, out);
+  else
+    split_reduce_kernel<false><<<(unsigned)((mn + 63) / 64), 256, 0, s>>>(part, splits, mn, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -474,6 +493,56 @@ __device__ __forceinline__ float lane_from_right(float v) {  // lane i gets lane
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x101, 0xF, 0xF, true));
 }
 
+// Finish a wave's 64 x 64 block of a forward / input-gradient convolution
+// (pixels g .. g + 3 of image b at p for lane (lr, q)): with KS > 1 the
+// waves ks > 0 hand their partial blocks to wave ks = 0 through LDS
+// (lane-major, so each write and read is conflict free), which adds them in
+// ks order; then (i, r), row m0 + 16 i + 4 q + r, is one 16-byte store, plus
+// the bias (forward) or the previous value (accumulating input gradient).
+template <bool DG, int WM, int WN, int KS>
+__device__ __forceinline__ void conv_block_out(f32x4 (&acc)[4][4], const Conv3Args& c, int m0, int lane, int wave,
+                                               int ks, bool gok, int b, int p) {
+  const int q = lane >> 4;
+  if (KS > 1) {
+    __shared__ float red[KS > 1 ? (KS - 1) * WM * WN * 64 * 64 : 1];
+    const int blk = wave % (WM * WN);
+    if (ks > 0) {
+      float* dst = red + ((ks - 1) * WM * WN + blk) * 64 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[((i * 4 + n) * 4 + r) * 64] = acc[i][n][r];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int k = 1; k < KS; ++k) {
+      const float* src = red + ((k - 1) * WM * WN + blk) * 64 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][n][r] += src[((i * 4 + n) * 4 + r) * 64];
+    }
+  }
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + 16 * i + 4 * q + r;
+      const bool ok = gok && row < c.M;
+      const uint32_t off = ok ? (uint32_t)((b * c.M + row) * c.hw + p) * 4u : kOOB;
+      f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+      if (!DG && c.bias && ok) v += c.bias[row];
+      if (DG && c.acc) v += buf_ld4(ro, off);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, (int)off, 0, 0);
+    }
+}
+
 template <bool DG, bool HALO, int WM, int WN, int KS, int U, int D>
 __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv3_direct_kernel(Conv3Args c) {
   constexpr int SG = DG ? -1 : 1;  // shift of tap t is SG * (t - 1)
@@ -584,49 +653,100 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv3_direct_kernel(Conv
   for (int s = 0; s < D - 1; ++s)
     if (kt + s < k1) mfma(fa[s], fb[s], fh[s]);
 
-  if (KS > 1) {
-    // Waves ks > 0 hand their partial blocks to wave ks = 0 through LDS
-    // (lane-major, so each write and read is conflict free), which adds them
-    // in ks order and stores.
-    __shared__ float red[KS > 1 ? (KS - 1) * WM * WN * 64 * 64 : 1];
-    const int blk = wave % (WM * WN);
-    if (ks > 0) {
-      float* dst = red + ((ks - 1) * WM * WN + blk) * 64 * 64 + lane;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int n = 0; n < 4; ++n)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dst[((i * 4 + n) * 4 + r) * 64] = acc[i][n][r];
-    }
-    __syncthreads();
-    if (ks > 0) return;
-#pragma unroll
-    for (int k = 1; k < KS; ++k) {
-      const float* src = red + ((k - 1) * WM * WN + blk) * 64 * 64 + lane;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int n = 0; n < 4; ++n)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i][n][r] += src[((i * 4 + n) * 4 + r) * 64];
-    }
-  }
+  conv_block_out<DG, WM, WN, KS>(acc, c, m0, lane, wave, ks, gok, b, p);
+}
 
-  // Epilogue: (i, r) is row m0 + 16 i + 4 q + r, pixels g .. g + 3.
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
+// Register-direct 1 x 1 convolution (stride 1, pad 0), forward and input
+// gradient: C[m][pixel] = sum_c A(m, c) S[c][pixel] with A = w[m][c]
+// (forward) or w[c][m] (dgrad).  The same blocks, pixel ownership and
+// epilogue as the 3 x 3 kernel; a stage is 16 channels, lane group q feeding
+// channels c0 + 4 q .. c0 + 4 q + 3 to the four MFMA steps: the forward's
+// weights are one float4 per 16-row block (the dgrad's, strided by cin, four
+// dwords), S one float4 of pixels per channel.  cs % 4 == 0, so a group's
+// four channels are all inside or all past cs.
+template <bool DG, int WM, int WN, int KS, int D>
+__global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv1_direct_kernel(Conv3Args c) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, q = lane >> 4;
+  const int wm = wave % WM, wn = (wave / WM) % WN, ks = wave / (WM * WN);
+  const int L = blockIdx.x, xq = c.tiles / 8, xr = c.tiles % 8, xc = L % 8;
+  const int item = xc * xq + min(xc, xr) + L / 8;
+  const int tm = item % c.tiles_m, tn = item / c.tiles_m;
+  const int m0 = (tm * WM + wm) * 64;
+  const int g = (tn * WN + wn) * 64 + 4 * lr;
+  const bool gok = g < c.npix;
+  const int b = g / c.hw, p = g - b * c.hw;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(c.src, c.src_bytes);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(c.wt, c.wt_bytes);
+  const uint32_t b_base = (uint32_t)((b * c.cs + 4 * q) * c.hw + p) * 4u;
+  uint32_t a_base[4];
+  bool a_ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + 16 * i + lr;
+    a_ok[i] = row < c.M;
+    a_base[i] = (uint32_t)(row * c.a_rs + 4 * q * c.a_cs) * 4u;
+  }
+  const int nst = (c.cs + 15) / 16;
+  const int nks = (nst + KS - 1) / KS;
+  const int k0 = ks * nks, k1 = min(nst, k0 + nks);
+
+  auto load = [&](int kt, f32x4(&fa)[4], f32x4(&fb)[4]) {
+    const bool cok = kt * 16 + 4 * q < c.cs;
+    uint32_t ao[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ao[i] = (cok & a_ok[i]) ? a_base[i] + (uint32_t)(kt * 16 * c.a_cs) * 4u : kOOB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!DG) {
+        fa[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)ao[i], 0, 0));
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          fa[i][u] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(ra, (int)(ao[i] + (uint32_t)(u * c.a_cs) * 4u), 0, 0));
+      }
+    }
+    const uint32_t bo = (cok & gok) ? b_base + (uint32_t)(kt * 16 * c.hw) * 4u : kOOB;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      fb[u] = __builtin_bit_cast(f32x4,
+                                 __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(bo + (uint32_t)(u * c.hw) * 4u), 0, 0));
+  };
+
+  f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + 16 * i + 4 * q + r;
-      const bool ok = gok && row < c.M;
-      const uint32_t off = ok ? (uint32_t)((b * c.M + row) * c.hw + p) * 4u : kOOB;
-      f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
-      if (!DG && c.bias && ok) v += c.bias[row];
-      if (DG && c.acc) v += buf_ld4(ro, off);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, (int)off, 0, 0);
+    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mfma = [&](const f32x4(&fa)[4], const f32x4(&fb)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][u], fb[u][n], acc[i][n], 0, 0, 0);
+  };
+
+  f32x4 fa[D][4], fb[D][4];
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load(k0 + s, fa[s], fb[s]);
+  int kt = k0;
+  for (; kt + D - 1 < k1; kt += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      load(kt + s + D - 1, fa[(s + D - 1) % D], fb[(s + D - 1) % D]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(fa[s], fb[s]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  }
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s)
+    if (kt + s < k1) mfma(fa[s], fb[s]);
+
+  conv_block_out<DG, WM, WN, KS>(acc, c, m0, lane, wave, ks, gok, b, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -787,6 +907,119 @@ __global__ __launch_bounds__(256, 2) void conv3_wgrad_kernel(Wgrad3Args c) {
     }
 }
 
+// Register-direct 1 x 1 weight gradient (stride 1, pad 0):
+//   dW[co][ci] = sum over pixels p of dy[co][p] * x[ci][p]
+// with the pixel splits, stages and dy loads of the 3 x 3 kernel.  Lane
+// (lr, q) owns the four columns ci0 .. ci0 + 3 (ci0 = the wave's first
+// column + 4 lr) as the four MFMA column blocks: one aligned float4 of x per
+// column per stage, and a 16-byte store per (block i, r).  The lane's pixel
+// advances 16 per stage with at most one image carry (H * W >= 16).
+template <int WM, int D>
+__global__ __launch_bounds__(256, 2) void conv1_wgrad_kernel(Wgrad3Args c) {
+  constexpr int WN = 4 / WM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, q = lane >> 4;
+  const int wm = wave % WM, wn = wave / WM;
+  const int L = blockIdx.x, xq = c.items / 8, xr = c.items % 8, xc = L % 8;
+  const int item = xc * xq + min(xc, xr) + L / 8;
+  const int tile = item % c.tiles, split = item / c.tiles;
+  const int tm = tile % c.tiles_m, tn = tile / c.tiles_m;
+  const int m0 = (tm * WM + wm) * 64;
+  const int ci0 = (tn * WN + wn) * 64 + 4 * lr;
+  const bool cok = ci0 < c.cin;  // cin % 4 == 0: all four columns or none
+  const int kbeg = split * c.chunk, kend = min(c.npix, kbeg + c.chunk);
+  const int nk = (kend - kbeg + 15) / 16;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(c.x, c.x_bytes);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(c.dy, c.dy_bytes);
+  uint32_t a_row[4];
+  bool a_ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int co = m0 + 16 * i + lr;
+    a_ok[i] = co < c.cout;
+    a_row[i] = (uint32_t)(co * c.hw) * 4u;
+  }
+  const uint32_t x_lane = (uint32_t)(ci0 * c.hw) * 4u;
+  int P = kbeg + 4 * q, pp;
+  uint32_t dpix, xpix;
+  {
+    const int b = P / c.hw;
+    pp = P - b * c.hw;
+    dpix = (uint32_t)(b * c.cout * c.hw + pp) * 4u;
+    xpix = (uint32_t)(b * c.cin * c.hw + pp) * 4u;
+  }
+  const uint32_t d_img = (uint32_t)((c.cout - 1) * c.hw) * 4u, x_img = (uint32_t)((c.cin - 1) * c.hw) * 4u;
+  const uint32_t x_ch = (uint32_t)c.hw * 4u;
+
+  auto load = [&](f32x4(&fa)[4], f32x4(&fb)[4]) {
+    const bool pix = P < kend;
+    uint32_t ao[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ao[i] = (pix & a_ok[i]) ? a_row[i] + dpix : kOOB;
+    const uint32_t xo = (pix & cok) ? x_lane + xpix : kOOB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, (int)ao[i], 0, 0));
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      fb[n] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(xo + n * x_ch), 0, 0));
+    P += 16;
+    pp += 16;
+    dpix += 64u;
+    xpix += 64u;
+    const bool cy = pp >= c.hw;
+    pp = cy ? pp - c.hw : pp;
+    dpix += cy ? d_img : 0u;
+    xpix += cy ? x_img : 0u;
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mfma = [&](const f32x4(&fa)[4], const f32x4(&fb)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+          acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][j], fb[n][j], acc[i][n], 0, 0, 0);
+  };
+
+  f32x4 fa[D][4], fb[D][4];
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load(fa[s], fb[s]);
+  int kt = 0;
+  for (; kt + D - 1 < nk; kt += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int ls = (s + D - 1) % D;
+      load(fa[ls], fb[ls]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(fa[s], fb[s]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s)
+    if (kt + s < nk) mfma(fa[s], fb[s]);
+
+  // (i, r) is row m0 + 16 i + 4 q + r, columns ci0 .. ci0 + 3.
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + 16 * i + 4 * q + r;
+      const bool ok = cok && row < c.cout;
+      const uint32_t off = ok ? (uint32_t)((split * c.cout + row) * c.cin + ci0) * 4u : kOOB;
+      const f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, (int)off, 0, 0);
+    }
+}
+
 bool fits_2g(double elems) { return elems * 4.0 < 2147483647.0; }
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -800,19 +1033,29 @@ void launch_conv3(hipStream_t s, const Conv3Args& c) {
   conv3_direct_kernel<DG, HALO, WM, 2, KS, kC3U, kC3D><<<c.tiles, 64 * WM * 2 * KS, 0, s>>>(c);
 }
 
-// Register-direct path for a 3 x 3, stride 1, pad 1 forward (dg = 0: src = x,
-// M = cout) or input gradient (dg = 1: src = dy, M = cin).  Returns false,
-// launching nothing, when the shape is outside what the kernel assumes.
-bool conv3_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, const float* wt, const float* bias,
-                  float* out, int acc) {
-  if (g.kh != 3 || g.kw != 3 || g.pad != 1 || g.stride != 1 || g.w % 4 != 0) return false;
+template <bool DG, int WM>
+void launch_conv1(hipStream_t s, const Conv3Args& c) {
+  constexpr int KS = WM == 1 ? 2 : 1;
+  conv1_direct_kernel<DG, WM, 2, KS, 4><<<c.tiles, 64 * WM * 2 * KS, 0, s>>>(c);
+}
+
+// Register-direct path for a 3 x 3 (stride 1, pad 1) or 1 x 1 (stride 1,
+// pad 0) forward (dg = 0: src = x, M = cout) or input gradient (dg = 1:
+// src = dy, M = cin).  Returns false, launching nothing, when the shape is
+// outside what the kernels assume.
+bool conv_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, const float* wt, const float* bias,
+                 float* out, int acc) {
+  const bool k3 = g.kh == 3 && g.kw == 3 && g.pad == 1 && g.stride == 1 && g.w % 4 == 0;
+  const bool k1 = g.kh == 1 && g.kw == 1 && g.pad == 0 && g.stride == 1 && (g.h * g.w) % 4 == 0;
+  if (!k3 && !k1) return false;
   const int M = dg ? g.cin : g.cout, cs = dg ? g.cout : g.cin;
-  if (cs % (4 * kC3U) != 0 || !a16(out)) return false;
+  if (cs % (k3 ? 4 * kC3U : 4) != 0 || !a16(out)) return false;
   const double hw = (double)g.h * g.w;
+  const int taps = g.kh * g.kw;
   // 32-bit byte offsets: tensors below 2 GiB, weights below 1 GiB (an
   // out-of-range row's kOOB offset plus a weight offset must not wrap).
   if ((double)g.n * cs * hw * 4.0 >= 2147483647.0 || (double)g.n * M * hw * 4.0 >= 2147483647.0 ||
-      (double)g.cout * g.cin * 9 * 4.0 >= 1073741824.0)
+      (double)g.cout * g.cin * taps * 4.0 >= 1073741824.0)
     return false;
   Conv3Args c{};
   c.src = src;
@@ -820,7 +1063,7 @@ bool conv3_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, c
   c.bias = dg ? nullptr : bias;
   c.out = out;
   c.src_bytes = (uint32_t)((size_t)g.n * cs * g.h * g.w * 4);
-  c.wt_bytes = (uint32_t)((size_t)g.cout * g.cin * 9 * 4);
+  c.wt_bytes = (uint32_t)((size_t)g.cout * g.cin * taps * 4);
   c.out_bytes = (uint32_t)((size_t)g.n * M * g.h * g.w * 4);
   c.M = M;
   c.cs = cs;
@@ -828,12 +1071,17 @@ bool conv3_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, c
   c.w = g.w;
   c.hw = g.h * g.w;
   c.npix = g.n * c.hw;
-  c.a_rs = dg ? 9 : g.cin * 9;
-  c.a_cs = dg ? g.cin * 9 : 9;
+  c.a_rs = dg ? taps : g.cin * taps;
+  c.a_cs = dg ? g.cin * taps : taps;
   c.acc = acc;
   const int wm = M <= 64 ? 1 : 2;
   c.tiles_m = (M + 64 * wm - 1) / (64 * wm);
   c.tiles = c.tiles_m * ((c.npix + 127) / 128);
+  if (k1) {
+    if (dg) wm == 1 ? launch_conv1<true, 1>(s, c) : launch_conv1<true, 2>(s, c);
+    else wm == 1 ? launch_conv1<false, 1>(s, c) : launch_conv1<false, 2>(s, c);
+    return true;
+  }
   const bool halo = 64 % g.w != 0;
   if (dg) {
     if (halo) wm == 1 ? launch_conv3<true, true, 1>(s, c) : launch_conv3<true, true, 2>(s, c);
@@ -873,29 +1121,39 @@ bool fast_filter(const ConvGeom& g) {
 // resident workgroups measured fastest: at 512 workgroups on 768 slots some
 // CUs hold 1 and others 3 (54 % of fp32 MFMA for the C5 weight gradients),
 // at 768 every CU holds 3 (77 %), at 1024 the last 256 run as a tail (62 %).
-int wgrad3_slots(int wm) {
-  static int cached[64][2] = {};
+int wgrad_slots(int taps, int wm) {
+  static int cached[64][2][2] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 768;
-  int& v = cached[dev][wm - 1];
+  int& v = cached[dev][taps == 9][wm - 1];
   if (v <= 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    const hipError_t e = wm == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3_wgrad_kernel<1, 4>, 256, 0)
-                                 : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3_wgrad_kernel<2, 4>, 256, 0);
+    hipError_t e;
+    if (taps == 9)
+      e = wm == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3_wgrad_kernel<1, 4>, 256, 0)
+                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3_wgrad_kernel<2, 4>, 256, 0);
+    else
+      e = wm == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv1_wgrad_kernel<1, 4>, 256, 0)
+                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv1_wgrad_kernel<2, 4>, 256, 0);
     if (e != hipSuccess || per_cu <= 0) per_cu = 2;
     v = per_cu * cus;
   }
   return v;
 }
 
-// Register-direct 3 x 3 weight gradient plan: 128 x 96 (or 64 x 192 when
-// cout <= 64) tiles of C, the pixels split so that tiles x splits fills one
-// round of resident workgroups, each split a whole number of 16-pixel stages
-// and at least 256 pixels.  Returns false when the shape is outside what
-// conv3_wgrad_kernel assumes.
-bool wgrad3_plan(const ConvGeom& g, Wgrad3Args& c) {
-  if (g.kh != 3 || g.kw != 3 || g.pad != 1 || g.stride != 1 || g.w % 4 != 0 || g.w < 16) return false;
+// Register-direct weight gradient plan: 3 x 3 (stride 1, pad 1, W >= 16)
+// in 128 x 96 tiles of C (64 x 192 when cout <= 64), or 1 x 1 (stride 1,
+// pad 0, cin % 4 == 0, H * W >= 16) in 128 x 128 tiles (64 x 256); the pixels
+// split so that tiles x splits fills one round of resident workgroups, each
+// split a whole number of 16-pixel stages and at least 256 pixels.  Returns
+// false when the shape is outside what the kernels assume.
+bool wgrad_plan(const ConvGeom& g, Wgrad3Args& c, int& taps) {
+  const bool k3 = g.kh == 3 && g.kw == 3 && g.pad == 1 && g.stride == 1 && g.w % 4 == 0 && g.w >= 16;
+  const bool k1 = g.kh == 1 && g.kw == 1 && g.pad == 0 && g.stride == 1 && (g.h * g.w) % 4 == 0 &&
+                  g.h * g.w >= 16 && g.cin % 4 == 0;
+  if (!k3 && !k1) return false;
+  taps = k3 ? 9 : 1;
   const double hw = (double)g.h * g.w;
   if ((double)g.n * g.cin * hw * 4.0 >= 2147483647.0 || (double)g.n * g.cout * hw * 4.0 >= 2147483647.0) return false;
   c = Wgrad3Args{};
@@ -907,18 +1165,18 @@ bool wgrad3_plan(const ConvGeom& g, Wgrad3Args& c) {
   c.npix = g.n * c.hw;
   const int wm = g.cout <= 64 ? 1 : 2, wn = 4 / wm;
   c.tiles_m = (g.cout + 64 * wm - 1) / (64 * wm);
-  c.tiles = c.tiles_m * ((3 * g.cin + 16 * wn - 1) / (16 * wn));
-  const int slots = wgrad3_slots(wm);
+  c.tiles = c.tiles_m * (k3 ? (3 * g.cin + 16 * wn - 1) / (16 * wn) : (g.cin + 64 * wn - 1) / (64 * wn));
+  const int slots = wgrad_slots(taps, wm);
   int splits = std::max(1, slots / c.tiles);
   const int max_splits = (c.npix + 255) / 256;
   splits = std::max(1, std::min(splits, max_splits));
   c.chunk = ((c.npix + splits - 1) / splits + 15) / 16 * 16;
   splits = (c.npix + c.chunk - 1) / c.chunk;
   c.items = c.tiles * splits;
-  if ((double)splits * g.cout * g.cin * 9 * 4.0 >= 2147483647.0) return false;
+  if ((double)splits * g.cout * g.cin * taps * 4.0 >= 2147483647.0) return false;
   c.x_bytes = (uint32_t)((size_t)g.n * g.cin * c.hw * 4);
   c.dy_bytes = (uint32_t)((size_t)g.n * g.cout * c.hw * 4);
-  c.out_bytes = (uint32_t)((size_t)splits * g.cout * g.cin * 9 * 4);
+  c.out_bytes = (uint32_t)((size_t)splits * g.cout * g.cin * taps * 4);
   return true;
 }
 
@@ -951,7 +1209,7 @@ int mle_conv2d_fwd(mle_stream stream, const float* x, const float* w, const floa
   hipStream_t s = as_stream(stream);
   ProbeScope probe("conv_fwd", s, 2.0 * op.M * (double)op.N * op.K, 0.0);
   const int ohw = g.oh * g.ow;
-  if (conv3_direct(s, false, g, x, w, b, y, 0)) {
+  if (conv_direct(s, false, g, x, w, b, y, 0)) {
   } else if (fast_filter(g) && ohw % 4 == 0 && op.K % 4 == 0 && a16(y) && fits_2g((double)n * cin * h * w_in) &&
       fits_2g((double)n * cout * ohw) && fits_2g((double)cout * op.K)) {
     FastConv c{x, w, b, y, (uint32_t)((size_t)n * cin * h * w_in * 4), (uint32_t)((size_t)cout * op.K * 4),
@@ -974,7 +1232,7 @@ int mle_conv2d_dgrad(mle_stream stream, const float* dy, const float* w, float* 
   hipStream_t s = as_stream(stream);
   ProbeScope probe("conv_dgrad", s, 2.0 * op.M * (double)op.N * op.K, 0.0);
   const int hw = h * w_in;
-  if (conv3_direct(s, true, g, dy, w, nullptr, dx, accumulate != 0)) {
+  if (conv_direct(s, true, g, dy, w, nullptr, dx, accumulate != 0)) {
   } else if (fast_filter(g) && hw % 4 == 0 && a16(dx) && fits_2g((double)n * cin * hw) &&
       fits_2g((double)n * cout * g.oh * g.ow) && fits_2g((double)cout * cin * kh * kw)) {
     FastConv c{dy, w, nullptr, dx, (uint32_t)((size_t)n * cout * g.oh * g.ow * 4),
@@ -992,7 +1250,8 @@ size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int 
   ConvGeom g;
   if (geom(n, cin, h, w_in, cout, kh, kw, pad, stride, g) != MLE_OK) return 0;
   Wgrad3Args c3;
-  if (wgrad3_plan(g, c3)) return c3.items > c3.tiles ? (size_t)c3.out_bytes : 0;
+  int taps;
+  if (wgrad_plan(g, c3, taps)) return c3.items > c3.tiles ? (size_t)c3.out_bytes : 0;
   int kchunk;
   const int splits = wgrad_splits(g, kchunk);
   return (size_t)splits * cout * cin * kh * kw * sizeof(float);
@@ -1009,23 +1268,26 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
   hipStream_t s = as_stream(stream);
   const double flop = 2.0 * cout * (double)cin * kh * kw * (double)n * g.oh * g.ow;
   Wgrad3Args c3;
-  if (wgrad3_plan(g, c3)) {
+  int taps;
+  if (wgrad_plan(g, c3, taps)) {
     const int splits = c3.items / c3.tiles;
     c3.x = x;
     c3.dy = dy;
     c3.out = splits > 1 ? static_cast<float*>(ws) : dw;
-    if (splits == 1) c3.out_bytes = (uint32_t)((size_t)cout * cin * 9 * 4);
+    if (splits == 1) c3.out_bytes = (uint32_t)((size_t)cout * cin * taps * 4);
     {
       ProbeScope probe("conv_wgrad", s, flop, 0.0);
-      if (cout <= 64) conv3_wgrad_kernel<1, 4><<<c3.items, 256, 0, s>>>(c3);
-      else conv3_wgrad_kernel<2, 4><<<c3.items, 256, 0, s>>>(c3);
+      if (taps == 9) {
+        if (cout <= 64) conv3_wgrad_kernel<1, 4><<<c3.items, 256, 0, s>>>(c3);
+        else conv3_wgrad_kernel<2, 4><<<c3.items, 256, 0, s>>>(c3);
+      } else {
+        if (cout <= 64) conv1_wgrad_kernel<1, 4><<<c3.items, 256, 0, s>>>(c3);
+        else conv1_wgrad_kernel<2, 4><<<c3.items, 256, 0, s>>>(c3);
+      }
     }
     if (splits > 1) {
-      const size_t mn = (size_t)cout * cin * 9;
-      if (mn % 4 == 0 && aligned16(ws) && aligned16(dw))
-        split_reduce_kernel<true><<<(unsigned)((mn / 4 + 255) / 256), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
-      else
-        split_reduce_kernel<false><<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
+      const size_t mn = (size_t)cout * cin * taps;
+      launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw);
     }
     return check_launch("mle_conv2d_wgrad");
   }
@@ -1047,10 +1309,7 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
     }
   }
   const size_t mn = (size_t)op.M * op.N;
-  if (mn % 4 == 0 && aligned16(ws) && aligned16(dw))
-    split_reduce_kernel<true><<<(unsigned)((mn / 4 + 255) / 256), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
-  else
-    split_reduce_kernel<false><<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(static_cast<float*>(ws), splits, mn, dw);
+  launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw);
   return check_launch("mle_conv2d_wgrad");
 }
 

@@ -647,6 +647,10 @@ def test_conv_transpose_composition(hip, orc, n, cin, h, w, cout, k, pad, stride
     (3, 8, 4, 4, 8, 3, 1, 1), (2, 24, 8, 8, 40, 3, 1, 1), (2, 8, 5, 12, 16, 3, 1, 1),
     (2, 16, 7, 20, 24, 3, 1, 1), (1, 16, 3, 128, 72, 3, 1, 1), (2, 64, 64, 64, 128, 3, 1, 1),
     (1, 8, 4, 16, 8, 3, 1, 1),  # one pixel split: the weight gradient is written without partials
+    # register-direct 1x1 path (stride 1, pad 0): 128-row and 64-row (two-wave
+    # K split) blocks, partial pixel tiles and channel groups (hw 60, cin 12,
+    # cout 20), a 4-pixel image (weight gradient on the LDS kernel)
+    (2, 64, 32, 32, 128, 1, 0, 1), (3, 12, 5, 12, 20, 1, 0, 1), (1, 8, 2, 2, 8, 1, 0, 1),
 ])
 def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
     r = rng(n * 7 + cin + h + cout + k)
