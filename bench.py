@@ -15,7 +15,7 @@ carries:
   extras        C3 (Linear GEMM backward) TFLOP/s, C2 (fused clip + AdamW
                 over 100 M parameters) GB/s, C1 (MLP, latency-bound) and C5
                 (U-Net residual block, conv-bound) steps/s, measured in the same run
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras] [--only c1|c2|c3|c5]
 """
 from __future__ import annotations
 
@@ -212,6 +212,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=8)
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c5"],
+                    help="run just this secondary workload (for profiling) and print its JSON object")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (every box has one GPU); "
@@ -219,6 +221,11 @@ def main() -> int:
         return 2
 
     hip.init(0)
+    if args.only:
+        run = {"c1": lambda: extras_mlp(), "c2": lambda: extras_adamw(args.steps),
+               "c3": lambda: extras_gemm(), "c5": lambda: extras_resblock(args.steps)}[args.only]
+        print(json.dumps(run()), flush=True)
+        return 0
     cfg = BlockConfig()
     log(f"[bench] building C4 block: {cfg}")
     m = build_block(cfg)
