@@ -271,6 +271,28 @@ int mle_softmax_fwd(mle_stream stream, const float* x, float* y, int bc, int row
 int mle_softmax_bwd(mle_stream stream, const float* y, const float* dy, float* dx, int bc, int rows, int cols, int axis,
                     int accumulate);
 
+/* Fused multi-head attention over [batch, seq, ld] projections (head h in
+ * columns h*64 .. h*64+63; head_dim must be 64, seq a multiple of 64):
+ * out_h = SOFTMASK(scale * q_h k_h^T, type 1) v_h, the column-normalised
+ * softmax with the column maximum over every row and, when causal, keys after
+ * the query masked out of the column sums.  Replaces HeadifytoChannel + BMMABT
+ * + Scale + SOFTMASK/SOFTMAX(type 1) + BMM + DeHeadify of MultiHeadAttention
+ * (Engine/transformer.cu:647-661; Engine/engine.cu:1144-1178, 2205-2314,
+ * 2430-2505, 2523-2551), without storing the [seq x seq] scores.  ws
+ * (mle_attention_ws_bytes) receives the column statistics the backward reads:
+ * keep it unchanged between the two calls. */
+size_t mle_attention_ws_bytes(int batch, int heads, int seq);
+int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const float* v, float* out, int batch,
+                      int heads, int seq, int head_dim, int ld, float scale, int causal, void* ws, size_t ws_bytes);
+/* Backward of mle_attention_fwd given dout: dq (+)= scale dS k, dv (+)= P^T dout,
+ * dk (+)= scale dS^T q -- or, with k_reference_grad, BMMABT's reference
+ * gradient bcmmT(q, dS) written row-major into each head's [seq x 64] block
+ * (Engine/engine.cu:2307) -- where dS = P (dP - colsum(P dP)) is deriv_SoftMax
+ * of type 1 (Engine/kernels.cu:2149-2181).  acc_*: 1 accumulates, 0 assigns. */
+int mle_attention_bwd(mle_stream stream, const float* q, const float* k, const float* v, const float* dout, float* dq,
+                      float* dk, float* dv, int batch, int heads, int seq, int head_dim, int ld, float scale,
+                      int causal, int acc_q, int acc_k, int acc_v, int k_reference_grad, void* ws, size_t ws_bytes);
+
 size_t mle_loss_ws_bytes(size_t n);
 /* loss[0] = sum((t - x)^2) / n.  scalar_mse_kernel (Engine/kernels.cu:1808-1816). */
 int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws, size_t ws_bytes);

@@ -70,6 +70,9 @@ SIGNATURES: dict[str, tuple] = {
     "mle_channel_sum": (I, [P, P, I, I, SZ, I, P]),
     "mle_softmax_fwd": (I, [P, P, P, I, I, I, I, I]),
     "mle_softmax_bwd": (I, [P, P, P, P, I, I, I, I, I]),
+    "mle_attention_ws_bytes": (SZ, [I, I, I]),
+    "mle_attention_fwd": (I, [P, P, P, P, P, I, I, I, I, I, F, I, P, SZ]),
+    "mle_attention_bwd": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, F, I, I, I, I, I, P, SZ]),
     "mle_loss_ws_bytes": (SZ, [SZ]),
     "mle_mse_fwd": (I, [P, P, P, SZ, P, P, SZ]),
     "mle_mse_bwd": (I, [P, P, P, P, P, SZ, I]),

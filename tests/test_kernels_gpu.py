@@ -120,8 +120,8 @@ def test_gemm_grid_heads_in_place(hip, orc, case, b, heads, seq, hd):
     alpha = 0.25
     ref = r.standard_normal((b, heads, M, N), dtype=np.float32)
     C0 = ref.copy()
-    orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(np.ascontiguousarray(Ae)), orc.ptr(np.ascontiguousarray(Be)),
-             orc.ptr(ref), b, heads, M, K, N, 1, 3, 3, 3, alpha)
+    Ae, Be = np.ascontiguousarray(Ae), np.ascontiguousarray(Be)  # held while the oracle reads them
+    orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(Ae), orc.ptr(Be), orc.ptr(ref), b, heads, M, K, N, 1, 3, 3, 3, alpha)
     if case == "mix_nn":  # result written in the projection layout [b, seq, heads * hd]
         C0p = np.ascontiguousarray(C0.transpose(0, 2, 1, 3).reshape(b, seq, E))
         gC = B(hip, C0p)
@@ -196,8 +196,9 @@ def test_gemm_batched_ex(hip, orc, ta, tb, M, N, K, batch, with_ws):
     ref = []
     for i in range(batch):
         c = Cflat[i * sc:i * sc + M * N].reshape(M, N).copy()
-        orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(np.ascontiguousarray(A)), orc.ptr(np.ascontiguousarray(Bi[i])),
-                 orc.ptr(c), 1, 1, M, K, N, int(beta != 0), 3, 3, 3, 0.5)
+        Ac, Bc = np.ascontiguousarray(A), np.ascontiguousarray(Bi[i])  # held while the oracle reads them
+        orc.call("orc_bcmm", ta * 2 + tb, orc.ptr(Ac), orc.ptr(Bc), orc.ptr(c), 1, 1, M, K, N, int(beta != 0), 3, 3, 3,
+                 0.5)
         ref.append(c)
     svec = N + 4
     gA, gB, gC = B(hip, A), B(hip, Bflat), B(hip, Cflat)
@@ -835,7 +836,8 @@ def test_elementwise_and_layout(hip, orc):
         src = flat if flag in (0, 3) else r.standard_normal((bsz, heads, seq, hd), dtype=np.float32)
         init = r.standard_normal(flat.size).astype(np.float32)
         ref = init.copy()
-        orc.call("orc_headify", orc.ptr(np.ascontiguousarray(src)), orc.ptr(ref), bsz, heads, seq, hd, flag)
+        src = np.ascontiguousarray(src)  # held while the oracle reads it
+        orc.call("orc_headify", orc.ptr(src), orc.ptr(ref), bsz, heads, seq, hd, flag)
         gs, gd = B(hip, src), B(hip, init)
         hip.call("mle_headify", None, gs.ptr, gd.ptr, bsz, heads, seq, hd, flag)
         np.testing.assert_array_equal(gd.numpy(), ref)
