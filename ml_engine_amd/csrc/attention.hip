@@ -38,12 +38,13 @@
 
 #include <float.h>
 
+#include <type_traits>
+
 using namespace mle;
 
 namespace {
 
 constexpr int HD = 64;   // head dimension handled here
-constexpr int NTA = 256; // four waves
 
 struct AttnArgs {
   const float* q;
@@ -72,6 +73,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const float* p, uint32_t 
 __device__ __forceinline__ f32x4 bld4(__amdgpu_buffer_rsrc_t r, uint32_t elem) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(elem * 4u), 0, 0));
 }
+// Same with a wave-uniform part of the offset in the instruction's scalar
+// offset (rows r = 0..3 of a lane's group share one address register).
+__device__ __forceinline__ f32x4 bld4s(__amdgpu_buffer_rsrc_t r, uint32_t elem, uint32_t uniform_elem) {
+  return __builtin_bit_cast(f32x4,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, (int)(elem * 4u), (int)(uniform_elem * 4u), 0));
+}
 __device__ __forceinline__ float bld1(__amdgpu_buffer_rsrc_t r, uint32_t elem) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)(elem * 4u), 0, 0));
 }
@@ -96,158 +103,187 @@ __device__ __forceinline__ Slice slice_of(const AttnArgs& a) {
   return {z, (uint32_t)b * a.seq * a.ld + (uint32_t)h * HD};
 }
 
-// Waves 1..3 hand their 64 accumulators per lane to wave 0 through LDS
-// (lane-major: conflict free); wave 0 adds them in wave order.  Returns true
-// in wave 0.
-__device__ __forceinline__ bool reduce_waves(f32x4 (&acc)[4][4], float* red, int w, int lane) {
-  if (w > 0) {
-    float* dst = red + (w - 1) * 4096 + lane;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[((i * 4 + n) * 4 + r) * 64] = acc[i][n][r];
-  }
-  __syncthreads();
-  if (w > 0) return false;
-  // One 16-value group at a time, so the reads in flight stay few.
-#pragma unroll
-  for (int k = 0; k < 3; ++k) {
-    const float* src = red + k * 4096 + lane;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][n][r] += src[((i * 4 + n) * 4 + r) * 64];
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-  return true;
+// Work split: every wave owns a 32-row tile of one output (32 keys of the
+// statistics, 32 queries of O or dQ, 32 keys of dV / dK) and walks the whole
+// contraction range for it, so no partial sums cross waves.  A workgroup is
+// two waves of the same (batch item, head) slice taking tiles j and
+// nb - 1 - j (nb = seq / 32): under the causal mask a query tile's work grows
+// with j and a key tile's shrinks, so each workgroup gets the same total.  A
+// loop over 16-row chunks keeps two register sets of chunk operands and
+// fetches chunk c + 1 into one while chunk c computes from the other.
+constexpr int TW = 32;      // rows of a wave's tile
+constexpr int LQ = HD + 4;  // padded LDS row: the 16 rows a b128 read touches sit on distinct banks
+
+__device__ __forceinline__ int tile_of(int w) {
+  return w == 0 ? (int)blockIdx.x : (int)(2 * gridDim.x) - 1 - (int)blockIdx.x;
 }
 
-// Column statistics.  Wave w of block x owns keys k0 .. k0 + 15 (k0 = 64 x +
-// 16 w) and walks all queries 64 at a time: S^T = K Q^T puts key k0 + 4q + r
-// and query qc + 16 n + lr in acc[n][r].  Each lane keeps a running (max,
-// masked sum) per key; the 16 lanes of a key merge at the end.
+// Chunk loop with two alternating register sets (no copies between them,
+// so a chunk's loads are waited for only when that chunk is computed).  The
+// optional late(c) issues chunk c's loads that are needed only at the end of
+// its computation; it runs before the next chunk's prefetch, because the
+// hardware counts loads in order: waiting for them then leaves the prefetch
+// in flight.
+struct NoLate {
+  __device__ void operator()(int) const {}
+};
+template <class Chunk, class Fetch, class Compute, class Late = NoLate>
+__device__ __forceinline__ void chunk_loop(int c0, int c1, Fetch fetch, Compute compute, Late late = NoLate{}) {
+  Chunk ca, cb;
+  if (c0 < c1) fetch(c0, ca);
+  for (int c = c0; c < c1; c += 2) {
+    late(c);
+    fetch(min(c + 1, c1 - 1), cb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(c, ca);
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 >= c1) break;
+    late(c + 1);
+    fetch(min(c + 2, c1 - 1), ca);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(c + 1, cb);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Column statistics for keys k0 .. k0 + 31 over all queries, 32 at a time:
+// S^T = K Q^T puts key k0 + 16i + 4q + r and query qc + 16n + lr in
+// acc[i][n][r].  Each lane keeps a running (max over all rows, masked sum)
+// per key; the 16 lanes of a key merge at the end.
 template <bool CAUSAL>
-__global__ __launch_bounds__(NTA, 2) void attn_stats_kernel(AttnArgs a) {
+__global__ __launch_bounds__(128, 2) void attn_stats_kernel(AttnArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
   const Slice sl = slice_of(a);
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
-  const int k0 = blockIdx.x * 64 + w * 16;
-  f32x4 ka[4];
+  const int k0 = tile_of(w) * TW;
+  f32x4 ka[2][4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) ka[s] = bld4(K, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
-  float m[4], l[4];
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    m[r] = -FLT_MAX;
-    l[r] = 0.f;
-  }
-  for (int qc = 0; qc < a.seq; qc += 64) {
-    f32x4 acc[4];
+    for (int s = 0; s < 4; ++s) ka[i][s] = bld4(K, sl.base + (uint32_t)(k0 + 16 * i + lr) * a.ld + 16 * s + 4 * q);
+  float m[2][4], l[2][4];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      f32x4 qb[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qb[s] = bld4(Q, sl.base + (uint32_t)(qc + 16 * n + lr) * a.ld + 16 * s + 4 * q);
-      acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[n] = mfma4(ka[s][j], qb[s][j], acc[n]);
-    }
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int key = k0 + 4 * q + r;
-      float sv[4], cm = -FLT_MAX;
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        sv[n] = a.scale * acc[n][r];
-        cm = fmaxf(cm, sv[n]);
-      }
-      const float mn = fmaxf(m[r], cm);
-      float add = 0.f;
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const float e = __expf(sv[n] - mn);
-        add += (!CAUSAL || qc + 16 * n + lr >= key) ? e : 0.f;
-      }
-      l[r] = l[r] * __expf(m[r] - mn) + add;
-      m[r] = mn;
+      m[i][r] = -FLT_MAX;
+      l[i][r] = 0.f;
     }
-  }
+  struct Chunk {
+    f32x4 qb[2][4];
+  };
+  auto fetch = [&](int c, Chunk& ch) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        ch.qb[n][s] = bld4(Q, sl.base + (uint32_t)(TW * c + 16 * n + lr) * a.ld + 16 * s + 4 * q);
+  };
+  auto compute = [&](int c, const Chunk& ch) {
+    const int qc = TW * c;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][n] = mfma4(ka[i][s][j], ch.qb[n][s][j], acc[i][n]);
+      }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 16 * i + 4 * q + r;
+        const float s0 = a.scale * acc[i][0][r], s1 = a.scale * acc[i][1][r];
+        const float mn = fmaxf(m[i][r], fmaxf(s0, s1));
+        const float e0 = __expf(s0 - mn), e1 = __expf(s1 - mn);
+        const float add = ((!CAUSAL || qc + lr >= key) ? e0 : 0.f) + ((!CAUSAL || qc + 16 + lr >= key) ? e1 : 0.f);
+        l[i][r] = l[i][r] * __expf(m[i][r] - mn) + add;
+        m[i][r] = mn;
+      }
+  };
+  chunk_loop<Chunk>(0, a.seq / TW, fetch, compute);
   // Merge the 16 lanes of each key (a butterfly: every lane ends with the
   // same value, each pair combined in the same order on both sides).
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-      const float mo = __shfl_xor(m[r], off, 64), lo = __shfl_xor(l[r], off, 64);
-      const float M = fmaxf(m[r], mo);
-      l[r] = l[r] * __expf(m[r] - M) + lo * __expf(mo - M);
-      m[r] = M;
-    }
-  if (lr == 0) {
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      if (l[r] < 1e-45f) l[r] = 1.0f;
-    float* S = a.stats + ((size_t)sl.z * a.seq + k0 + 4 * q) * 2;
-    st4(S, f32x4{m[0], l[0], m[1], l[1]});
-    st4(S + 4, f32x4{m[2], l[2], m[3], l[3]});
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+        const float mo = __shfl_xor(m[i][r], off, 64), lo = __shfl_xor(l[i][r], off, 64);
+        const float M = fmaxf(m[i][r], mo);
+        l[i][r] = l[i][r] * __expf(m[i][r] - M) + lo * __expf(mo - M);
+        m[i][r] = M;
+      }
+  if (lr == 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (l[i][r] < 1e-45f) l[i][r] = 1.0f;
+      float* S = a.stats + ((size_t)sl.z * a.seq + k0 + 16 * i + 4 * q) * 2;
+      st4(S, f32x4{m[i][0], l[i][0], m[i][1], l[i][1]});
+      st4(S + 4, f32x4{m[i][2], l[i][2], m[i][3], l[i][3]});
+    }
   }
 }
 
-// O = P V for 64 queries q0 .. q0 + 63; the four waves take every fourth
-// 16-key chunk (with the causal mask, chunks up to the block's last query).
-// Per chunk: S^T (K rows as A, the block's Q^T held in registers as B),
-// P^T = exp(S - m) / l masked, then O^T += V^T P^T.
+// O = P V for queries q0 .. q0 + 31 over the 16-key chunks (with the causal
+// mask, up to the tile's last query).  The tile's Q^T (the B operand of
+// S^T = K Q^T) stays in registers; per chunk: S^T, P^T = exp(S - m) / l
+// masked, O^T += V^T P^T.
 template <bool CAUSAL>
-__global__ __launch_bounds__(NTA, 2) void attn_fwd_kernel(AttnArgs a) {
-  __shared__ float red[3 * 4096];
+__global__ __launch_bounds__(128, 2) void attn_fwd_kernel(AttnArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
   const Slice sl = slice_of(a);
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
-  const int q0 = blockIdx.x * 64;
-  f32x4 qB[4][4];
+  const int q0 = tile_of(w) * TW;
+  f32x4 qB[2][4];
 #pragma unroll
-  for (int n = 0; n < 4; ++n)
+  for (int n = 0; n < 2; ++n)
 #pragma unroll
     for (int s = 0; s < 4; ++s) qB[n][s] = bld4(Q, sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
-  f32x4 acc[4][4];
+  f32x4 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int nch = CAUSAL ? (q0 + 64) / 16 : a.seq / 16;
-  for (int c = w; c < nch; c += 4) {
+    for (int n = 0; n < 2; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  struct Chunk {
+    f32x4 ka[4], va[4], s01, s23;
+  };
+  auto fetch = [&](int c, Chunk& ch) {
     const int k0 = 16 * c;
-    f32x4 ka[4], va[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) ka[s] = bld4(K, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
+    for (int s = 0; s < 4; ++s) ch.ka[s] = bld4(K, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) va[r] = bld4(V, sl.base + (uint32_t)(k0 + 4 * q + r) * a.ld + 4 * lr);
-    const f32x4 s01 = ld4(ST + (size_t)(k0 + 4 * q) * 2), s23 = ld4(ST + (size_t)(k0 + 4 * q) * 2 + 4);
-    const float mk[4] = {s01[0], s01[2], s23[0], s23[2]};
-    const float il[4] = {1.0f / s01[1], 1.0f / s01[3], 1.0f / s23[1], 1.0f / s23[3]};
-    f32x4 st[4];
+    for (int r = 0; r < 4; ++r) ch.va[r] = bld4s(V, sl.base + (uint32_t)(k0 + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+    ch.s01 = ld4(ST + (size_t)(k0 + 4 * q) * 2);
+    ch.s23 = ld4(ST + (size_t)(k0 + 4 * q) * 2 + 4);
+  };
+  auto compute = [&](int c, const Chunk& ch) {
+    const int k0 = 16 * c;
+    const float mk[4] = {ch.s01[0], ch.s01[2], ch.s23[0], ch.s23[2]};
+    const float il[4] = {1.0f / ch.s01[1], 1.0f / ch.s01[3], 1.0f / ch.s23[1], 1.0f / ch.s23[3]};
+    f32x4 st[2];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int n = 0; n < 2; ++n) {
       st[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) st[n] = mfma4(ka[s][j], qB[n][s][j], st[n]);
+        for (int j = 0; j < 4; ++j) st[n] = mfma4(ch.ka[s][j], qB[n][s][j], st[n]);
     }
-    float pt[4][4];
+    float pt[2][4];
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool keep = !CAUSAL || q0 + 16 * n + lr >= k0 + 4 * q + r;
@@ -258,152 +294,127 @@ __global__ __launch_bounds__(NTA, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) acc[i][n] = mfma4(va[r][i], pt[n][r], acc[i][n]);
-  }
-  if (!reduce_waves(acc, red, w, lane)) return;
+        for (int n = 0; n < 2; ++n) acc[i][n] = mfma4(ch.va[r][i], pt[n][r], acc[i][n]);
+  };
+  chunk_loop<Chunk>(0, CAUSAL ? (q0 + TW) / 16 : a.seq / 16, fetch, compute);
   const __amdgpu_buffer_rsrc_t O = rsrc(a.out, a.bytes);
 #pragma unroll
-  for (int n = 0; n < 4; ++n)
+  for (int n = 0; n < 2; ++n)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       bst4(O, sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * q + 4 * r,
            f32x4{acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]});
 }
 
-// One 16-query chunk of the key-block kernel, processed per 16-key column
-// block n (the next block's K / V rows are fetched while block n's MFMAs run,
-// which keeps the register footprint at two blocks of operands): S and, with
-// DP, dP for queries qc + 4q + r and keys k0 + 16n + lr; then f(n, p, dp)
-// turns them into block n's B operand (P, or dS) and
-// acc[i][n] += at[r][i] * b[r] accumulates the product.
-template <bool CAUSAL, bool DP, class F>
-__device__ __forceinline__ void kv_chunk(const AttnArgs& a, uint32_t base, __amdgpu_buffer_rsrc_t Q,
-                                         __amdgpu_buffer_rsrc_t K, __amdgpu_buffer_rsrc_t V, __amdgpu_buffer_rsrc_t dO,
-                                         int qc, int k0, int lr, int q, const float (&mk)[4],
-                                         const float (&il)[4], const f32x4 (&at)[4], f32x4 (&acc)[4][4], F f) {
-  f32x4 qa[4], oa[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    qa[s] = bld4(Q, base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
-    if (DP) oa[s] = bld4(dO, base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
-  }
-  f32x4 kb[2][4], vb[2][4];
-  auto fetch = [&](int n, f32x4(&kk)[4], f32x4(&vv)[4]) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      kk[s] = bld4(K, base + (uint32_t)(k0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
-      if (DP) vv[s] = bld4(V, base + (uint32_t)(k0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
-    }
-  };
-  fetch(0, kb[0], vb[0]);
-#pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    if (n + 1 < 4) fetch(n + 1, kb[(n + 1) & 1], vb[(n + 1) & 1]);
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 sa = {0.f, 0.f, 0.f, 0.f}, da = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sa = mfma4(qa[s][j], kb[n & 1][s][j], sa);
-        if (DP) da = mfma4(oa[s][j], vb[n & 1][s][j], da);
-      }
-    float bop[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool keep = !CAUSAL || qc + 4 * q + r >= k0 + 16 * n + lr;
-      const float pv = __expf(a.scale * sa[r] - mk[n]) * (keep ? il[n] : 0.f);
-      bop[r] = f(n, pv, DP ? da[r] : 0.f);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i][n] = mfma4(at[r][i], bop[r], acc[i][n]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// dV (and D, and with DK the true dK) for 64 keys k0 .. k0 + 63; the waves
-// take every fourth 16-query chunk (with the mask, from the block's first
-// key on).  Pass 1: dV^T += dO^T P.  The block's dV is then complete: D_c =
-// <dV_c, V_c> goes to LDS and to dcol.  Pass 2 (DK): dS = P (dP - D),
-// dK^T += Q^T dS.
+// dV, D and, with DK, the true dK for keys k0 .. k0 + 31 over the 16-query
+// chunks (with the mask, from the tile's first key on).  The tile's K^T (and
+// V^T) B operands stay in registers; per chunk and 16-key column block n: S
+// (and dP) in the S layout (query qc + 4q + r, key k0 + 16n + lr), then
+//   pass 1: dV^T += dO^T P        -> dV and D_c = <dV_c, V_c> (the wave holds
+//                                    all of its keys' dV, so D needs no exchange)
+//   pass 2 (DK): dS = P (dP - D), dK^T += Q^T dS.
 template <bool CAUSAL, bool DK>
-__global__ __launch_bounds__(NTA, 2) void attn_bwd_kv_kernel(AttnArgs a) {
-  __shared__ float red[3 * 4096];
-  __shared__ float dsh[64];
+__global__ __launch_bounds__(128, 2) void attn_bwd_kv_kernel(AttnArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
   const Slice sl = slice_of(a);
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
-  const int k0 = blockIdx.x * 64;
-  float mk[4], il[4];
+  // Key tiles: the heavy (early) one goes with wave 1's light (late) one.
+  const int k0 = tile_of(w) * TW;
+  f32x4 kB[2][4], vB[2][4];
+  float mk[2], il[2];
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
+  for (int n = 0; n < 2; ++n) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      kB[n][s] = bld4(K, sl.base + (uint32_t)(k0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
+      if (DK) vB[n][s] = bld4(V, sl.base + (uint32_t)(k0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
+    }
     const float* sp = a.stats + ((size_t)sl.z * a.seq + k0 + 16 * n + lr) * 2;
     mk[n] = sp[0];
     il[n] = 1.0f / sp[1];
   }
-  const int c0 = CAUSAL ? k0 / 16 : 0, nch = a.seq / 16;
-  f32x4 acc[4][4];
+  f32x4 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c = c0 + w; c < nch; c += 4) {
-    const int qc = 16 * c;
-    f32x4 ot[4];
+    for (int n = 0; n < 2; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float D[2] = {0.f, 0.f};
+  // A chunk: Q rows (S), dO rows (dP, pass 2), and the final product's A
+  // operand rows in the 4 lr + i layout (dO for dV, Q for dK).
+  struct Chunk {
+    f32x4 qa[4], oa[4], at[4];
+  };
+  auto run = [&](auto pass2_tag) {
+    constexpr bool P2 = decltype(pass2_tag)::value;
+    auto fetch = [&](int c, Chunk& ch) {
+      const int qc = 16 * c;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) ot[r] = bld4(dO, sl.base + (uint32_t)(qc + 4 * q + r) * a.ld + 4 * lr);
-    kv_chunk<CAUSAL, false>(a, sl.base, Q, K, V, dO, qc, k0, lr, q, mk, il, ot, acc,
-                            [](int, float pv, float) { return pv; });
-  }
-  if (reduce_waves(acc, red, w, lane)) {
-    // acc[i][n][r] = dV[k0 + 16n + lr][16q + 4r + i]
-    const __amdgpu_buffer_rsrc_t dVr = rsrc(a.dv, a.bytes);
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const uint32_t row = (uint32_t)(k0 + 16 * n + lr) * a.ld;
-      float part = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const f32x4 vv = bld4(V, sl.base + row + 16 * q + 4 * r);
-        f32x4 g = {acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]};
-        part += g[0] * vv[0] + g[1] * vv[1] + g[2] * vv[2] + g[3] * vv[3];
-        if (a.acc_v) g += bld4(dVr, sl.base + row + 16 * q + 4 * r);
-        bst4(dVr, sl.base + row + 16 * q + 4 * r, g);
+      for (int s = 0; s < 4; ++s) {
+        ch.qa[s] = bld4(Q, sl.base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
+        if (P2) ch.oa[s] = bld4(dO, sl.base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
       }
-      part += __shfl_xor(part, 16, 64);
-      part += __shfl_xor(part, 32, 64);
-      if (q == 0) {
-        dsh[16 * n + lr] = part;
-        a.dcol[(size_t)sl.z * a.seq + k0 + 16 * n + lr] = part;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ch.at[r] = bld4s(P2 ? Q : dO, sl.base + (uint32_t)(qc + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+    };
+    auto compute = [&](int c, const Chunk& ch) {
+      const int qc = 16 * c;
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, da = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            sa = mfma4(ch.qa[s][j], kB[n][s][j], sa);
+            if (P2) da = mfma4(ch.oa[s][j], vB[n][s][j], da);
+          }
+        float bop[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool keep = !CAUSAL || qc + 4 * q + r >= k0 + 16 * n + lr;
+          const float pv = __expf(a.scale * sa[r] - mk[n]) * (keep ? il[n] : 0.f);
+          bop[r] = P2 ? pv * (da[r] - D[n]) : pv;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i][n] = mfma4(ch.at[r][i], bop[r], acc[i][n]);
       }
+    };
+    chunk_loop<Chunk>(CAUSAL ? k0 / 16 : 0, a.seq / 16, fetch, compute);
+  };
+  run(std::false_type{});
+  // acc[i][n][r] = dV[k0 + 16n + lr][16q + 4r + i]
+  const __amdgpu_buffer_rsrc_t dVr = rsrc(a.dv, a.bytes);
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const uint32_t row = sl.base + (uint32_t)(k0 + 16 * n + lr) * a.ld;
+    float part = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const f32x4 vv = bld4(V, row + 16 * q + 4 * r);
+      f32x4 g = {acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]};
+      part += g[0] * vv[0] + g[1] * vv[1] + g[2] * vv[2] + g[3] * vv[3];
+      if (a.acc_v) g += bld4(dVr, row + 16 * q + 4 * r);
+      bst4(dVr, row + 16 * q + 4 * r, g);
     }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    D[n] = part;
+    if (q == 0) a.dcol[(size_t)sl.z * a.seq + k0 + 16 * n + lr] = part;
   }
   if (!DK) return;
-  __syncthreads();
-  float D[4];
-#pragma unroll
-  for (int n = 0; n < 4; ++n) D[n] = dsh[16 * n + lr];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c = c0 + w; c < nch; c += 4) {
-    const int qc = 16 * c;
-    f32x4 qt[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) qt[r] = bld4(Q, sl.base + (uint32_t)(qc + 4 * q + r) * a.ld + 4 * lr);
-    kv_chunk<CAUSAL, true>(a, sl.base, Q, K, V, dO, qc, k0, lr, q, mk, il, qt, acc,
-                           [&](int n, float pv, float dpv) { return pv * (dpv - D[n]); });
-  }
-  if (!reduce_waves(acc, red, w, lane)) return;
+    for (int n = 0; n < 2; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  run(std::true_type{});
   const __amdgpu_buffer_rsrc_t dKr = rsrc(a.dk, a.bytes);
 #pragma unroll
-  for (int n = 0; n < 4; ++n)
+  for (int n = 0; n < 2; ++n)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t e = sl.base + (uint32_t)(k0 + 16 * n + lr) * a.ld + 16 * q + 4 * r;
@@ -413,106 +424,125 @@ __global__ __launch_bounds__(NTA, 2) void attn_bwd_kv_kernel(AttnArgs a) {
     }
 }
 
-// dQ for 64 queries q0 .. q0 + 63 (or, with KREF, the reference's K
-// gradient bcmmT(Q, dS): the same product with Q's rows at the key positions
-// in place of K, stored in the head block's row-major [64 x seq] order).  The
-// waves take every fourth 16-key chunk.  Per chunk and 16-query column block
-// n: S^T = K Q^T and dP^T = V dO^T, dS^T = P^T (dP^T - D), X^T += Y^T dS^T
-// (Y = K or Q); block n + 1's Q / dO rows are fetched during block n.
+// dQ = scale dS K and, with KREF, the reference's K gradient bcmmT(Q, dS)
+// (the same product with Q's rows at the key positions, stored in the head
+// block's row-major [64 x seq] order) for queries q0 .. q0 + 31; both come
+// from the same dS tiles.  The tile's Q and dO rows (the B operands of
+// S^T = K Q^T and dP^T = V dO^T) are staged in the wave's own LDS region.
+// Per chunk and 16-query column block n: S^T and dP^T, dS^T = P^T (dP^T -
+// D), then X^T += Y^T dS^T for Y = K (acc[.][n]) and Y = Q (acc[.][2 + n]).
 template <bool CAUSAL, bool KREF>
-__global__ __launch_bounds__(NTA, 2) void attn_bwd_q_kernel(AttnArgs a) {
-  __shared__ float red[3 * 4096];
+__global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[2][2][TW * LQ];  // [wave][Q, dO][row * LQ + col]
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
   const Slice sl = slice_of(a);
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
-  const __amdgpu_buffer_rsrc_t Y = KREF ? Q : K;
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
   const float* DC = a.dcol + (size_t)sl.z * a.seq;
-  const int q0 = blockIdx.x * 64;
+  const int q0 = tile_of(w) * TW;
+  float* qs = lds[w][0];
+  float* os = lds[w][1];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int idx = lane + 64 * u, row = idx >> 4, col = (idx & 15) * 4;
+    const uint32_t e = sl.base + (uint32_t)(q0 + row) * a.ld + col;
+    *reinterpret_cast<f32x4*>(qs + row * LQ + col) = bld4(Q, e);
+    *reinterpret_cast<f32x4*>(os + row * LQ + col) = bld4(dO, e);
+  }
+  __syncthreads();
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int nch = CAUSAL ? (q0 + 64) / 16 : a.seq / 16;
-  for (int c = w; c < nch; c += 4) {
+  struct Chunk {
+    f32x4 ka[4], va[4];
+  };
+  auto fetch = [&](int c, Chunk& ch) {
     const int k0 = 16 * c;
-    f32x4 ka[4], va[4], yt[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      ka[s] = bld4(K, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
-      va[s] = bld4(V, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
+      ch.ka[s] = bld4(K, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
+      ch.va[s] = bld4(V, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
     }
+  };
+  // Chunk c's operands needed only after its S^T / dP^T products: the
+  // statistics and D of its keys, and its Y rows (A of the last products).
+  f32x4 yk[4], yq[4], s01, s23, dk;
+  auto late = [&](int c) {
+    s01 = ld4(ST + (size_t)(16 * c + 4 * q) * 2);
+    s23 = ld4(ST + (size_t)(16 * c + 4 * q) * 2 + 4);
+    dk = ld4(DC + 16 * c + 4 * q);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) yt[r] = bld4(Y, sl.base + (uint32_t)(k0 + 4 * q + r) * a.ld + 4 * lr);
-    const f32x4 s01 = ld4(ST + (size_t)(k0 + 4 * q) * 2), s23 = ld4(ST + (size_t)(k0 + 4 * q) * 2 + 4);
+    for (int r = 0; r < 4; ++r) {
+      yk[r] = bld4s(K, sl.base + (uint32_t)(16 * c + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+      if (KREF) yq[r] = bld4s(Q, sl.base + (uint32_t)(16 * c + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+    }
+  };
+  auto compute = [&](int c, const Chunk& ch) {
+    const int k0 = 16 * c;
     const float mk[4] = {s01[0], s01[2], s23[0], s23[2]};
     const float il[4] = {1.0f / s01[1], 1.0f / s01[3], 1.0f / s23[1], 1.0f / s23[3]};
-    const f32x4 Dk = ld4(DC + k0 + 4 * q);
-    f32x4 qb[2][4], ob[2][4];
-    auto fetch = [&](int n, f32x4(&qq)[4], f32x4(&oo)[4]) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      f32x4 qb[4], ob[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        qq[s] = bld4(Q, sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
-        oo[s] = bld4(dO, sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
+        qb[s] = *reinterpret_cast<const f32x4*>(qs + (16 * n + lr) * LQ + 16 * s + 4 * q);
+        ob[s] = *reinterpret_cast<const f32x4*>(os + (16 * n + lr) * LQ + 16 * s + 4 * q);
       }
-    };
-    fetch(0, qb[0], ob[0]);
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      if (n + 1 < 4) fetch(n + 1, qb[(n + 1) & 1], ob[(n + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
       f32x4 st = {0.f, 0.f, 0.f, 0.f}, dt = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          st = mfma4(ka[s][j], qb[n & 1][s][j], st);
-          dt = mfma4(va[s][j], ob[n & 1][s][j], dt);
+          st = mfma4(ch.ka[s][j], qb[s][j], st);
+          dt = mfma4(ch.va[s][j], ob[s][j], dt);
         }
       float ds[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool keep = !CAUSAL || q0 + 16 * n + lr >= k0 + 4 * q + r;
-        const float pv = __expf(a.scale * st[r] - mk[r]) * (keep ? il[r] : 0.f);
-        ds[r] = pv * (dt[r] - Dk[r]);
+        ds[r] = __expf(a.scale * st[r] - mk[r]) * (keep ? il[r] : 0.f) * (dt[r] - dk[r]);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i][n] = mfma4(yt[r][i], ds[r], acc[i][n]);
-      __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 4; ++i) {
+          acc[i][n] = mfma4(yk[r][i], ds[r], acc[i][n]);
+          if (KREF) acc[i][2 + n] = mfma4(yq[r][i], ds[r], acc[i][2 + n]);
+        }
+      __builtin_amdgcn_sched_barrier(0);  // block n + 1's LDS reads stay after block n's products
     }
-  }
-  if (!reduce_waves(acc, red, w, lane)) return;
-  // acc[i][n][r] = X^T[d = 16q + 4r + i][query q0 + 16n + lr]
-  if (!KREF) {
-    const __amdgpu_buffer_rsrc_t dQr = rsrc(a.dq, a.bytes);
+  };
+  chunk_loop<Chunk>(0, CAUSAL ? (q0 + TW) / 16 : a.seq / 16, fetch, compute, late);
+  // acc[i][n][r] = X^T[d = 16q + 4r + i][query q0 + 16(n % 2) + lr]
+  const __amdgpu_buffer_rsrc_t dQr = rsrc(a.dq, a.bytes);
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+  for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t e = sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * q + 4 * r;
-        f32x4 g = a.scale * f32x4{acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]};
-        if (a.acc_q) g += bld4(dQr, e);
-        bst4(dQr, e, g);
-      }
-  } else {
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t e = sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * q + 4 * r;
+      f32x4 g = a.scale * f32x4{acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]};
+      if (a.acc_q) g += bld4(dQr, e);
+      bst4(dQr, e, g);
+    }
+  if (KREF) {
     // C[d][j] lands at flat d * seq + j of the head's [seq x 64] block.
     const __amdgpu_buffer_rsrc_t dKr = rsrc(a.dk, a.bytes);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
+      for (int n = 0; n < 2; ++n)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const uint32_t d = 16 * q + 4 * r + i, j = q0 + 16 * n + lr;
           const uint32_t f = d * (uint32_t)a.seq + j;
           const uint32_t e = sl.base + (f / HD) * a.ld + f % HD;
-          float g = a.scale * acc[i][n][r];
+          float g = a.scale * acc[i][2 + n][r];
           if (a.acc_k) g += bld1(dKr, e);
           bst1(dKr, e, g);
         }
@@ -555,15 +585,15 @@ int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const f
   a.bytes = (uint32_t)((size_t)batch * seq * ld * sizeof(float));
   a.scale = scale;
   hipStream_t s = as_stream(stream);
-  const dim3 grid(seq / 64, batch * heads);
+  const dim3 grid(seq / (2 * TW), batch * heads);  // two 32-row tiles per workgroup
   const double flop = 4.0 * batch * heads * (double)seq * seq * HD;  // S and P V, as the reference computes them
   ProbeScope probe("attn_fwd", s, flop, 0.0);
   if (causal) {
-    attn_stats_kernel<true><<<grid, NTA, 0, s>>>(a);
-    attn_fwd_kernel<true><<<grid, NTA, 0, s>>>(a);
+    attn_stats_kernel<true><<<grid, 128, 0, s>>>(a);
+    attn_fwd_kernel<true><<<grid, 128, 0, s>>>(a);
   } else {
-    attn_stats_kernel<false><<<grid, NTA, 0, s>>>(a);
-    attn_fwd_kernel<false><<<grid, NTA, 0, s>>>(a);
+    attn_stats_kernel<false><<<grid, 128, 0, s>>>(a);
+    attn_fwd_kernel<false><<<grid, 128, 0, s>>>(a);
   }
   return check_launch("mle_attention_fwd");
 }
@@ -598,20 +628,26 @@ int mle_attention_bwd(mle_stream stream, const float* q, const float* k, const f
   a.acc_k = acc_k != 0;
   a.acc_v = acc_v != 0;
   hipStream_t s = as_stream(stream);
-  const dim3 grid(seq / 64, batch * heads);
+  const dim3 grid(seq / (2 * TW), batch * heads);  // two 32-row tiles per workgroup
   const double flop = 8.0 * batch * heads * (double)seq * seq * HD;  // dP, dV, dQ, dK
   ProbeScope probe("attn_bwd", s, flop, 0.0);
   const bool kref = k_reference_grad != 0;
   if (causal) {
-    if (kref) attn_bwd_kv_kernel<true, false><<<grid, NTA, 0, s>>>(a);
-    else attn_bwd_kv_kernel<true, true><<<grid, NTA, 0, s>>>(a);
-    attn_bwd_q_kernel<true, false><<<grid, NTA, 0, s>>>(a);
-    if (kref) attn_bwd_q_kernel<true, true><<<grid, NTA, 0, s>>>(a);
+    if (kref) {
+      attn_bwd_kv_kernel<true, false><<<grid, 128, 0, s>>>(a);
+      attn_bwd_q_kernel<true, true><<<grid, 128, 0, s>>>(a);
+    } else {
+      attn_bwd_kv_kernel<true, true><<<grid, 128, 0, s>>>(a);
+      attn_bwd_q_kernel<true, false><<<grid, 128, 0, s>>>(a);
+    }
   } else {
-    if (kref) attn_bwd_kv_kernel<false, false><<<grid, NTA, 0, s>>>(a);
-    else attn_bwd_kv_kernel<false, true><<<grid, NTA, 0, s>>>(a);
-    attn_bwd_q_kernel<false, false><<<grid, NTA, 0, s>>>(a);
-    if (kref) attn_bwd_q_kernel<false, true><<<grid, NTA, 0, s>>>(a);
+    if (kref) {
+      attn_bwd_kv_kernel<false, false><<<grid, 128, 0, s>>>(a);
+      attn_bwd_q_kernel<false, true><<<grid, 128, 0, s>>>(a);
+    } else {
+      attn_bwd_kv_kernel<false, true><<<grid, 128, 0, s>>>(a);
+      attn_bwd_q_kernel<false, false><<<grid, 128, 0, s>>>(a);
+    }
   }
   return check_launch("mle_attention_bwd");
 }

@@ -871,6 +871,30 @@ bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Line
     for (int d = 0; d < 4; ++d)
       if (outs[i]->dim[d] != outs[0]->dim[d]) return false;
   }
+  // The batched launches need the outputs (and their gradients) at one
+  // stride.  Node buffers come from per-size free lists, so after other
+  // graphs have been freed they need not be; then the outputs and gradients
+  // move into one block each (nothing has read these buffers yet: the nodes
+  // were just made, and every consumer reads node->output / node->grad when
+  // it runs).
+  auto uniform = [&](float* NodeBackProp::*f) {
+    const long long st = outs[1].get()->*f - outs[0].get()->*f;
+    for (size_t i = 2; i < n; ++i)
+      if (outs[i].get()->*f - outs[i - 1].get()->*f != st) return false;
+    return st > 0;
+  };
+  for (float* NodeBackProp::*f : {&NodeBackProp::output, &NodeBackProp::grad}) {
+    if (uniform(f)) continue;
+    const bool grad = f == &NodeBackProp::grad;
+    const size_t tot = (size_t)outs[0]->total, pad = (tot + 63) & ~size_t(63);  // the arena's 256-byte granule
+    float* blk = grad ? alloc_grad(pad * n) : alloc_output(pad * n);
+    for (size_t i = 0; i < n; ++i) {
+      float*& ptr = outs[i].get()->*f;
+      release(ptr, tot, grad);
+      ptr = blk + i * pad;
+      if (grad) check(mle_fill(stream(), ptr, 0.0f, tot), "Fill Kernel for Gradient");  // as a new node's
+    }
+  }
   // Equal strides between consecutive layers, in elements.
   auto stride_of = [&](auto get, long long& st) {
     st = (long long)(get(1) - get(0));

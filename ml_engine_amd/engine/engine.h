@@ -250,6 +250,11 @@ class GraphOperations {
   // HeadMix = DeHeadify(BMM(P, Headify(V))) -> [batch, 1, m, heads * dim].
   static graph HeadScores(const graph& Q, const graph& K, const int heads, const float scale);
   static graph HeadMix(const graph& P, const graph& V, const int heads);
+  // HeadMix(SOFTMASK / SOFTMAX type 1 (HeadScores(Q, K, heads, scale)), V) in
+  // one node that stores no scores (mle_attention_fwd / _bwd): head_dim 64,
+  // seq a multiple of 64.  Returns nullptr (building nothing) for other shapes.
+  static graph HeadAttention(const graph& Q, const graph& K, const graph& V, const int heads, const float scale,
+                             const bool causal);
   static graph SOFTMAX(const graph& X, const int type = 0);
   static graph SOFTMASK(const graph& X, const int type = 0);
   static graph RELU(const graph& input);
@@ -303,9 +308,10 @@ class Linear {
 // (and changes nothing) otherwise.
 namespace mle {
 bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Linear*>& layers);
-// Global switch for the graph fusions (on by default): fuse_sibling_linears
-// and the Linear -> SoftMaxCrossEntropy row statistics.  Graphs built while it
-// is off keep one GEMM per layer and a loss that reads the logits.
+// Global switch for the graph fusions (on by default): fuse_sibling_linears,
+// the Linear -> SoftMaxCrossEntropy row statistics and MultiHeadAttention's
+// fused attention node.  Graphs built while it is off keep one GEMM per
+// layer, a loss that reads the logits and the stored attention scores.
 void set_sibling_fusion(bool on);
 bool fusion_enabled();
 }  // namespace mle

@@ -31,17 +31,26 @@ void MultiHeadAttention::load(std::ifstream& f) {
 }
 
 // The reference composes Headify x3, BMMABT, Scale, SOFTMASK, BMM and
-// DeHeadify; HeadScores and HeadMix compute the same products on the heads in
-// place (no permuted copies, the scale in the GEMM).
+// DeHeadify.  With the fusions on and a supported shape, HeadAttention runs
+// the whole chain without storing the scores; otherwise HeadScores and
+// HeadMix compute the same products on the heads in place (no permuted
+// copies, the scale in the GEMM) around the stored softmax.
 graph MultiHeadAttention::forward(const graph& X, const bool mask) {
   auto Q = q.forward(X);
   auto K = k.forward(X);
   auto V = v.forward(X);
   // The three projections read X: one launch each way when the arenas allow.
   qkv_fused = mle::fuse_sibling_linears({Q, K, V}, {&q, &k, &v});
-  auto scaled = GraphOperations::HeadScores(Q, K, num_heads, 1.0f / sqrtf((float)head_dim));
-  auto weights = (mask && scaled->dim[2] > 1) ? GraphOperations::SOFTMASK(scaled, 1) : GraphOperations::SOFTMAX(scaled, 1);
-  auto concat = GraphOperations::HeadMix(weights, V, num_heads);
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  graph concat;
+  if (mle::fusion_enabled())
+    concat = GraphOperations::HeadAttention(Q, K, V, num_heads, scale, mask && Q->dim[2] > 1);
+  if (!concat) {
+    auto scaled = GraphOperations::HeadScores(Q, K, num_heads, scale);
+    auto weights =
+        (mask && scaled->dim[2] > 1) ? GraphOperations::SOFTMASK(scaled, 1) : GraphOperations::SOFTMAX(scaled, 1);
+    concat = GraphOperations::HeadMix(weights, V, num_heads);
+  }
   auto output = o.forward(concat);
   output->op_name = "Multi Head Attention Output";
   return output;

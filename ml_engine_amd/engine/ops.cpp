@@ -608,6 +608,41 @@ graph GraphOperations::HeadMix(const graph& P, const graph& V, const int heads) 
   return node;
 }
 
+// Fused attention: HeadScores -> SOFTMASK / SOFTMAX (type 1) -> HeadMix of
+// MultiHeadAttention (Engine/transformer.cu:647-661) in one node.  The
+// forward keeps each key's column statistics in node scratch for the
+// backward, which recomputes the score tiles; K's gradient follows
+// mle::quirks().bmmabt_reference_grad as HeadScores does.
+graph GraphOperations::HeadAttention(const graph& Q, const graph& K, const graph& V, const int heads,
+                                     const float scale, const bool causal) {
+  if (Q->dim[1] != 1 || K->dim[1] != 1 || V->dim[1] != 1 || Q->dim[0] != K->dim[0] || Q->dim[0] != V->dim[0] ||
+      Q->dim[2] != K->dim[2] || Q->dim[2] != V->dim[2] || Q->dim[3] != K->dim[3] || Q->dim[3] != V->dim[3] ||
+      heads <= 0 || Q->dim[3] % heads != 0)
+    return nullptr;
+  const int b = Q->dim[0], seq = Q->dim[2], E = Q->dim[3], hd = E / heads;
+  if (hd != 64 || seq % 64 != 0 || (double)b * heads > 65535.0 || (double)b * seq * E * 4.0 >= 2147483647.0)
+    return nullptr;
+  auto node = make_node("Attention", b, 1, seq, E);
+  node->inputs = {Q, K, V};
+  NodeBackProp *nd = node.get(), *pq = Q.get(), *pk = K.get(), *pv = V.get();
+  const size_t wsb = mle_attention_ws_bytes(b, heads, seq);
+  void* ws = mle::alloc_scratch(wsb);
+  const bool kref = mle::quirks().bmmabt_reference_grad;
+  node->forward = [=]() {
+    check(mle_attention_fwd(S(), pq->output, pk->output, pv->output, nd->output, b, heads, seq, hd, E, scale,
+                            causal ? 1 : 0, ws, wsb),
+          "Attention forward");
+  };
+  node->backward = [=]() {
+    const int aq = mle::accumulate_flag(pq), ak = mle::accumulate_flag(pk), av = mle::accumulate_flag(pv);
+    check(mle_attention_bwd(S(), pq->output, pk->output, pv->output, nd->grad, pq->grad, pk->grad, pv->grad, b, heads,
+                            seq, hd, E, scale, causal ? 1 : 0, aq, ak, av, kref ? 1 : 0, ws, wsb),
+          "Attention backward");
+  };
+  std_hooks(node);
+  return node;
+}
+
 graph GraphOperations::SOFTMAX(const graph& X, const int type) { return softmax_node(X, type, false, "Softmax"); }
 graph GraphOperations::SOFTMASK(const graph& X, const int type) { return softmax_node(X, type, true, "Softmask"); }
 graph GraphOperations::RELU(const graph& input) { return act_node(input, MLE_RELU, "ReLU"); }

@@ -67,8 +67,13 @@ def test_mlp_step(hip, orc):
 
 
 @pytest.mark.parametrize("quirks", [True, False])
-def test_block_step(hip, orc, quirks):
-    cfg = BlockConfig(batch=2, seq=32, d_model=64, heads=4, ffn=128, vocab=97)
+@pytest.mark.parametrize("dims", [(2, 32, 64, 4), (2, 128, 128, 2)], ids=["heads16", "heads64_fused_attention"])
+def test_block_step(hip, orc, quirks, dims):
+    """One step of the block against the oracle's composition.  With 64-wide
+    heads and seq a multiple of 64 MultiHeadAttention runs the fused attention
+    node; with 16-wide heads the stored-score chain."""
+    batch, seq, d_model, heads = dims
+    cfg = BlockConfig(batch=batch, seq=seq, d_model=d_model, heads=heads, ffn=128, vocab=97)
     ids, tgt, params = block_data(cfg, seed=3)
     m = Model("block", cfg.dims(), reference_quirks=quirks)
     for i, p in enumerate(params):
