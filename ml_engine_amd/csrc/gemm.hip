@@ -920,9 +920,12 @@ int choose_splits(int M, int N, int K, int batch, int& kchunk) {
     smax = K / 512;
   } else {
     // Measured on MI355X: with ~256 tiles a split only pays off for long K.
+    // A grid of a few tiles is latency-bound (each split walks its K chunk one
+    // stage after another), so it takes chunks down to 64 deep: the C1 MLP
+    // step went from 0.136 to 0.118 ms.
     if (tiles >= 384 || (tiles >= 128 && K < 4096)) return 1;
     s = (int)((768 + tiles - 1) / tiles);
-    smax = K / 256;
+    smax = tiles <= 16 ? K / 64 : K / 256;
   }
   if (s > smax) s = smax;
   if (s < 2) return 1;
