@@ -527,24 +527,46 @@ __global__ __launch_bounds__(NT) void xent_bwd4_kernel(const float* __restrict__
 // targets and p = exp(x - max) / sum recomputed from the forward's row stats,
 // in the operations the probability path uses (same values, bit for bit).
 // Grid: x over float4 column groups, y over rows (looping past 65535).
+// A thread owns 4 columns and walks rows blockIdx.y, + gridDim.y, ... four
+// at a time with the four rows' loads issued together (a workgroup per row
+// left each thread one 16-byte load in flight: 65536 workgroups of one load
+// and one store each ran at 63 % of HBM bandwidth).
 __global__ __launch_bounds__(NT) void xent_keys_bwd4_kernel(const float* __restrict__ x, const float* __restrict__ stats,
                                                             KeyTargets kt, const float* __restrict__ up,
                                                             float* __restrict__ dl, int rows, int cols, float batch) {
   const int c = (blockIdx.x * NT + threadIdx.x) * 4;
   if (c >= cols) return;
-  for (int line = blockIdx.y; line < rows; line += gridDim.y) {
-    const float mx = stats[2 * line], sum = stats[2 * line + 1];
-    const int key = kt.key(line, cols);
-    const size_t o = (size_t)line * cols + c;
-    const f32x4 xv = ldv(x, o);
-    f32x4 g;
+  const float u = up ? up[0] : 1.0f;
+  constexpr int R = 4;
+  const int step = gridDim.y;
+  for (int line0 = blockIdx.y; line0 < rows; line0 += R * step) {
+    f32x4 xv[R];
+    float mx[R], sum[R];
+    int key[R];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float p = expf(xv[j] - mx) / sum;
-      g[j] = p + (-1.0f) * (c + j == key ? 1.0f : 0.0f);
+    for (int k = 0; k < R; ++k) {
+      const int line = line0 + k * step;
+      if (line < rows) {
+        xv[k] = ldv(x, (size_t)line * cols + c);
+        mx[k] = stats[2 * line];
+        sum[k] = stats[2 * line + 1];
+        key[k] = kt.key(line, cols);
+      }
     }
-    if (up) g *= up[0];
-    stv(dl, o, g / batch);
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int line = line0 + k * step;
+      if (line < rows) {
+        f32x4 g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p = expf(xv[k][j] - mx[k]) / sum[k];
+          g[j] = p + (-1.0f) * (c + j == key[k] ? 1.0f : 0.0f);
+        }
+        if (up) g *= u;
+        stv(dl, (size_t)line * cols + c, g / batch);
+      }
+    }
   }
 }
 
@@ -725,7 +747,7 @@ int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const floa
   const KeyTargets kt{keys, clen, max_clen, nullptr};
   const unsigned gy = (unsigned)std::min(rows, 65535);
   if (cols % 4 == 0 && aligned16(logits) && aligned16(dlogits))
-    xent_keys_bwd4_kernel<<<dim3((cols / 4 + NT - 1) / NT, gy), NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows,
+    xent_keys_bwd4_kernel<<<dim3((cols / 4 + NT - 1) / NT, std::min(gy, 1024u)), NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows,
                                                                            cols, (float)batch);
   else
     xent_keys_bwd_kernel<<<dim3((cols + NT - 1) / NT, gy), NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows,
