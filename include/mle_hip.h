@@ -95,6 +95,11 @@ int mle_scale_add(mle_stream stream, const float* x, const float* y, float* z, f
 int mle_accumulate(mle_stream stream, const float* x, float* y, double scale, size_t n);
 /* y = (float)(scale*(double)x): mle_accumulate into a zeroed y, without reading y. */
 int mle_scale_assign(mle_stream stream, const float* x, float* y, double scale, size_t n);
+/* Both gradients of an Add at once: ya (+)= x and yb (+)= x in one pass over x
+ * (acc_* == 0 assigns).  Equals mle_accumulate / mle_scale_assign at scale 1 on
+ * each destination.  Add backward (Engine/engine.cu:1630-1672): its two
+ * Accumulate launches (Engine/kernels.cu:1693-1699).  ya and yb must differ. */
+int mle_accumulate2(mle_stream stream, const float* x, float* ya, int acc_a, float* yb, int acc_b, size_t n);
 /* y = scale*x.  Scale_Write (Engine/kernels.cu:1677-1682), Write (Engine/kernels.cu:1670-1675) with scale 1. */
 int mle_scale_write(mle_stream stream, const float* x, float* y, float scale, size_t n);
 /* divide==0: x *= factor; divide==1: x /= factor.  SV (Includes/kernels.h:272-280). */

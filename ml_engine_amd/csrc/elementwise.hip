@@ -70,6 +70,25 @@ struct ScaleAssignOp {  // y = (float)(scale*(double)x): AccumOp applied to y ==
   }
 };
 
+// ya (+)= x and yb (+)= x in one pass over x.  The sums are float adds and the
+// assignments copies, which is what AccumOneOp and ScaleAssignOp give at scale 1.
+template <bool ACC_A, bool ACC_B>
+struct Accum2Op {
+  const float* x;
+  float* ya;
+  float* yb;
+  __device__ void one(size_t i) const {
+    const float v = x[i];
+    ya[i] = ACC_A ? ya[i] + v : v;
+    yb[i] = ACC_B ? yb[i] + v : v;
+  }
+  __device__ void vec(size_t i) const {
+    const f32x4 v = ld4(x, i);
+    st4(ya, i, ACC_A ? ld4(ya, i) + v : v);
+    st4(yb, i, ACC_B ? ld4(yb, i) + v : v);
+  }
+};
+
 struct AccumOp {  // y = (float)((double)y + scale*(double)x)
   const float* x;
   float* y;
@@ -271,6 +290,18 @@ int mle_accumulate(mle_stream stream, const float* x, float* y, double scale, si
   // With scale == 1 the double sum of two floats rounds to the float sum.
   if (scale == 1.0) return run_map(as_stream(stream), n, v, AccumOneOp{x, y}, "mle_accumulate");
   return run_map(as_stream(stream), n, v, AccumOp{x, y, scale}, "mle_accumulate");
+}
+
+int mle_accumulate2(mle_stream stream, const float* x, float* ya, int acc_a, float* yb, int acc_b, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(x && ya && yb, "mle_accumulate2: null pointer");
+  MLE_CHECK_ARG(ya != yb, "mle_accumulate2: the two destinations must differ");
+  const hipStream_t s = as_stream(stream);
+  const bool v = aligned16(x) && aligned16(ya) && aligned16(yb);
+  if (acc_a && acc_b) return run_map(s, n, v, Accum2Op<true, true>{x, ya, yb}, "mle_accumulate2");
+  if (acc_a) return run_map(s, n, v, Accum2Op<true, false>{x, ya, yb}, "mle_accumulate2");
+  if (acc_b) return run_map(s, n, v, Accum2Op<false, true>{x, ya, yb}, "mle_accumulate2");
+  return run_map(s, n, v, Accum2Op<false, false>{x, ya, yb}, "mle_accumulate2");
 }
 
 int mle_scale_assign(mle_stream stream, const float* x, float* y, double scale, size_t n) {

@@ -342,6 +342,11 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
   };
   node->backward = [=]() {
     if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
+    if (pa != pb && pa->grad != pb->grad) {  // one pass over the output gradient
+      const int acc_a = mle::accumulate_flag(pa), acc_b = mle::accumulate_flag(pb);
+      check(mle_accumulate2(S(), nd->grad, pa->grad, acc_a, pb->grad, acc_b, nd->total), "Add backward");
+      return;
+    }
     add_grad(pa, nd->grad, 1.0, nd->total, "Add backward - A grad");
     add_grad(pb, nd->grad, 1.0, nd->total, "Add backward - B grad");
   };

@@ -807,6 +807,35 @@ def test_scatter_add_paths(hip, orc, batch, clen, dim, vocab):
     assert_close(gt.numpy(), ref, what="scatter add", **EW)
 
 
+@pytest.mark.parametrize("off", [0, 1])  # 1: float offsets, so the scalar path runs
+def test_accumulate2_matches_two_accumulates(hip, orc, off):
+    """mle_accumulate2 (Add backward's two gradients in one pass) equals
+    mle_accumulate / mle_scale_assign at scale 1 on each destination, bit for bit."""
+    r = rng(52 + off)
+    n = 4099
+    x = r.standard_normal(n + 1, dtype=np.float32)
+    gx = B(hip, x)
+    xo = np.ascontiguousarray(x[off:off + n])  # held while the oracle reads it
+    for acc_a in (0, 1):
+        for acc_b in (0, 1):
+            ya, yb = (r.standard_normal(n + 1, dtype=np.float32) for _ in range(2))
+            want = []
+            for y, acc in ((ya, acc_a), (yb, acc_b)):
+                w = y[off:off + n].copy() if acc else np.zeros(n, np.float32)
+                orc.call("orc_accumulate", orc.ptr(xo), orc.ptr(w), 1.0, n)
+                want.append(w)
+            ga = B(hip, ya if acc_a else np.full_like(ya, np.nan))
+            gb = B(hip, yb if acc_b else np.full_like(yb, np.nan))
+            hip.call("mle_accumulate2", None, gx.ptr + 4 * off, ga.ptr + 4 * off, acc_a, gb.ptr + 4 * off, acc_b, n)
+            for g, w, y, acc in ((ga, want[0], ya, acc_a), (gb, want[1], yb, acc_b)):
+                got = g.numpy()
+                np.testing.assert_array_equal(got[off:off + n], w)
+                edge = got[:off] if off else got[n:]
+                np.testing.assert_array_equal(edge, (y[:off] if off else y[n:]) if acc else np.full_like(edge, np.nan))
+    with pytest.raises(hip.MLEError):  # one destination twice
+        hip.call("mle_accumulate2", None, gx.ptr, ga.ptr, 1, ga.ptr, 1, n)
+
+
 # ------------------------------------------------------ elementwise / layout
 def test_elementwise_and_layout(hip, orc):
     r = rng(51)
