@@ -877,6 +877,13 @@ def test_elementwise_and_layout(hip, orc):
     gxs, gpe = B(hip, xs), hip.Buffer.zeros(xs.shape)
     hip.call("mle_matpe", None, gxs.ptr, gpe.ptr, 3, 17, 24, 0)
     assert_close(gpe.numpy(), pe_r, what="matpe", rtol=1e-6, atol_scale=1e-7)
+    for bt, rw, cl, st in ((11, 9, 32, 5), (2, 7, 26, 3)):  # ragged batch chunk; cols not a multiple of 4
+        xm = r.standard_normal((bt, rw, cl), dtype=np.float32)
+        pm = np.zeros_like(xm)
+        orc.call("orc_matpe", orc.ptr(xm), orc.ptr(pm), bt, rw, cl, st)
+        gxm, gpm = B(hip, xm), hip.Buffer.zeros(xm.shape)
+        hip.call("mle_matpe", None, gxm.ptr, gpm.ptr, bt, rw, cl, st)
+        assert_close(gpm.numpy(), pm, what=f"matpe {bt}x{rw}x{cl}", rtol=1e-6, atol_scale=1e-7)
     tp_r = np.zeros(256, np.float32)
     orc.call("orc_pe", orc.ptr(tp_r), 517, 256)
     gtp = hip.Buffer.zeros(256)
