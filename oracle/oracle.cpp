@@ -49,33 +49,104 @@ OEXPORT void orc_set_threads(int n) { if (n > 0) omp_set_num_threads(n); }
 // kind 3: C[m x p] (+)= s * A[n x m]^T B[p x n]^T
 // backward == 0 assigns, 1 accumulates (the reference's atomicAdd); flags are
 // the batch/channel broadcast codes A, B, C of batch_chan_offset.
+namespace {
+// Register tile of the packed GEMM: MR rows x NR columns of C per work step.
+constexpr int kMR = 4, kNR = 32, kRowTiles = 8;
+
+// op(A) element (r, k) and op(B) element (k, c) of the four bcmm kinds.
+inline float a_at(const float* a, int kind, int m, int n, long long r, long long k) {
+  return (kind & 2) ? a[k * m + r] : a[r * n + k];
+}
+inline float b_at(const float* b, int kind, int n, int p, long long k, long long c) {
+  return (kind & 1) ? b[c * n + k] : b[k * p + c];
+}
+
+// C tile = sum_k op(A)[r, k] op(B)[k, c] with one double accumulator per
+// element, the k terms added one at a time in increasing k -- the same
+// operations in the same order as a scalar triple loop, so the result is
+// bit-identical to it (the build disables FMA contraction).  The column loop
+// vectorises; only the accumulators' layout differs from the scalar loop.
+inline void gemm_tile(const float* ap, const float* bp, long long n, double acc[kMR][kNR]) {
+  for (int i = 0; i < kMR; ++i)
+    for (int j = 0; j < kNR; ++j) acc[i][j] = 0.0;
+  for (long long k = 0; k < n; ++k) {
+    double bv[kNR];
+    for (int j = 0; j < kNR; ++j) bv[j] = (double)bp[k * kNR + j];
+    for (int i = 0; i < kMR; ++i) {
+      const double av = (double)ap[k * kMR + i];
+      for (int j = 0; j < kNR; ++j) acc[i][j] += av * bv[j];
+    }
+  }
+}
+}  // namespace
+
 OEXPORT void orc_bcmm(int kind, const float* a, const float* b, float* c, int batch, int channels, int m, int n, int p,
                       int backward, int fa, int fb, int fc, float scale) {
+  const long long rt = (m + kMR - 1) / kMR, ct = (p + kNR - 1) / kNR;
+  // op(A) as [row tile][k][kMR] and op(B) as [column tile][k][kNR], zero past
+  // the matrix edge (those products only reach discarded tile elements).
+  std::vector<float> ap((size_t)(rt * kMR * n)), bp((size_t)(ct * kNR * n));
   for (int z = 0; z < batch * channels; ++z) {
     const int bi = z / channels, ci = z % channels;
-    const long long oa = bco(fa, bi, ci, channels, (long long)m * n);
-    const long long ob = bco(fb, bi, ci, channels, (long long)n * p);
-    const long long oc = bco(fc, bi, ci, channels, (long long)m * p);
+    const float* A = a + bco(fa, bi, ci, channels, (long long)m * n);
+    const float* B = b + bco(fb, bi, ci, channels, (long long)n * p);
+    float* Cz = c + bco(fc, bi, ci, channels, (long long)m * p);
 #pragma omp parallel for schedule(static)
-    for (int row = 0; row < m; ++row) {
+    for (long long t = 0; t < rt; ++t)
+      for (int i = 0; i < kMR; ++i) {
+        const long long r = t * kMR + i;
+        float* dst = ap.data() + t * kMR * n + i;
+        for (long long k = 0; k < n; ++k) dst[k * kMR] = r < m ? a_at(A, kind, m, n, r, k) : 0.0f;
+      }
+#pragma omp parallel for schedule(static)
+    for (long long t = 0; t < ct; ++t)
+      for (long long k = 0; k < n; ++k)
+        for (int j = 0; j < kNR; ++j) {
+          const long long col = t * kNR + j;
+          bp[(size_t)((t * n + k) * kNR + j)] = col < p ? b_at(B, kind, n, p, k, col) : 0.0f;
+        }
+    const long long rblocks = (rt + kRowTiles - 1) / kRowTiles;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+    for (long long cb = 0; cb < ct; ++cb)
+      for (long long rb = 0; rb < rblocks; ++rb)
+        for (long long t = rb * kRowTiles; t < std::min(rt, (rb + 1) * kRowTiles); ++t) {
+          double acc[kMR][kNR];
+          gemm_tile(ap.data() + t * kMR * n, bp.data() + cb * kNR * n, n, acc);
+          for (int i = 0; i < kMR; ++i) {
+            const long long r = t * kMR + i;
+            if (r >= m) break;
+            for (int j = 0; j < kNR; ++j) {
+              const long long col = cb * kNR + j;
+              if (col >= p) break;
+              const float sum = (float)acc[i][j];
+              float* dst = Cz + r * p + col;
+              if (backward == 0) *dst = scale * sum;
+              else *dst += scale * sum;
+            }
+          }
+        }
+  }
+}
+
+// The scalar triple loop orc_bcmm restates in packed form; kept to check that
+// the two agree bit for bit (tests/test_oracle_pins.py).
+OEXPORT void orc_bcmm_naive(int kind, const float* a, const float* b, float* c, int batch, int channels, int m, int n,
+                            int p, int backward, int fa, int fb, int fc, float scale) {
+  for (int z = 0; z < batch * channels; ++z) {
+    const int bi = z / channels, ci = z % channels;
+    const float* A = a + bco(fa, bi, ci, channels, (long long)m * n);
+    const float* B = b + bco(fb, bi, ci, channels, (long long)n * p);
+    float* Cz = c + bco(fc, bi, ci, channels, (long long)m * p);
+#pragma omp parallel for schedule(static)
+    for (int row = 0; row < m; ++row)
       for (int col = 0; col < p; ++col) {
         double acc = 0.0;
-        for (int k = 0; k < n; ++k) {
-          float av, bv;
-          switch (kind) {
-            case 0: av = a[oa + (long long)row * n + k]; bv = b[ob + (long long)k * p + col]; break;
-            case 1: av = a[oa + (long long)row * n + k]; bv = b[ob + (long long)col * n + k]; break;
-            case 2: av = a[oa + (long long)k * m + row]; bv = b[ob + (long long)k * p + col]; break;
-            default: av = a[oa + (long long)k * m + row]; bv = b[ob + (long long)col * n + k]; break;
-          }
-          acc += (double)av * (double)bv;
-        }
+        for (int k = 0; k < n; ++k) acc += (double)a_at(A, kind, m, n, row, k) * (double)b_at(B, kind, n, p, k, col);
         const float sum = (float)acc;
-        float* dst = c + oc + (long long)row * p + col;
+        float* dst = Cz + (long long)row * p + col;
         if (backward == 0) *dst = scale * sum;
         else *dst += scale * sum;
       }
-    }
   }
 }
 

@@ -18,6 +18,7 @@ SIGS = {
     "orc_num_threads": (I, []),
     "orc_set_threads": (None, [I]),
     "orc_bcmm": (None, [I, P, P, P, I, I, I, I, I, I, I, I, I, F]),
+    "orc_bcmm_naive": (None, [I, P, P, P, I, I, I, I, I, I, I, I, I, F]),
     "orc_bcompress": (None, [P, P, LL, I, F]),
     "orc_bcumadd": (None, [P, P, LL, I]),
     "orc_channel_squeeze": (None, [P, P, I, I, LL, I]),
@@ -64,12 +65,29 @@ SIGS = {
 }
 
 _lib = None
+_V4_FLAGS = {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"}
+
+
+def host_has_v4() -> bool:
+    """True when this CPU has the x86-64-v4 (AVX-512) extensions liboracle_v4.so is built for."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("flags"):
+                return _V4_FLAGS <= set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return False
+
+
+def lib_path() -> Path:
+    v4 = ROOT / "oracle" / "liboracle_v4.so"
+    return v4 if v4.exists() and host_has_v4() else ROOT / "oracle" / "liboracle.so"
 
 
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
-        path = ROOT / "oracle" / "liboracle.so"
+        path = lib_path()
         if not path.exists():
             raise RuntimeError(f"{path} missing: run `make -C oracle` or __graft_entry__.build()")
         _lib = C.CDLL(str(path))

@@ -48,6 +48,25 @@ def test_bcmm_matches_numpy_with_broadcast_flags(orc, kind):
         assert_close(C, want, rtol=1e-6, atol_scale=1e-6, what=f"kind {kind} flags {fa}{fb}")
 
 
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+def test_bcmm_packed_equals_scalar_loop(orc, kind):
+    """The packed, register-tiled oracle GEMM adds the same products in the
+    same k order as the scalar triple loop: bit-identical results, including
+    ragged edges (m, p not multiples of the tile), assign and accumulate."""
+    r = rng(20 + kind)
+    for (b, ch, m, n, pp, fa, fb, fc) in [(1, 1, 37, 53, 29, 3, 0, 3), (2, 3, 70, 9, 130, 3, 3, 3),
+                                          (1, 1, 1, 5, 1, 3, 3, 3), (2, 2, 64, 40, 64, 1, 2, 3)]:
+        size = lambda f, inner: (b if f & 1 else 1) * (ch if f & 2 else 1) * inner
+        A = r.standard_normal(size(fa, m * n)).astype(np.float32)
+        B = r.standard_normal(size(fb, n * pp)).astype(np.float32)
+        C0 = r.standard_normal(size(fc, m * pp)).astype(np.float32)
+        for bw in (0, 1):
+            c1, c2 = C0.copy(), C0.copy()
+            orc.call("orc_bcmm", kind, p(A), p(B), p(c1), b, ch, m, n, pp, bw, fa, fb, fc, 0.7)
+            orc.call("orc_bcmm_naive", kind, p(A), p(B), p(c2), b, ch, m, n, pp, bw, fa, fb, fc, 0.7)
+            np.testing.assert_array_equal(c1.view(np.uint32), c2.view(np.uint32))
+
+
 def test_bcmm_accumulates_over_broadcast_output(orc):
     """backward == 1 with a broadcast output sums every batch item (the dW reduction)."""
     r = rng(9)
