@@ -453,6 +453,21 @@ size_t mle_adamw_clip_ws_bytes(size_t n);
 int mle_adamw_clip_fused(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t,
                          float lr, float b1, float b2, float eps, float weight_decay, int adamw,
                          double clip_scale, double* norm_out, void* ws, size_t ws_bytes);
+/* No counterpart in the reference.  mle_adamw_clip_fused without a workspace
+ * argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc): it calls no
+ * allocator.  Its scratch -- s and the per-block norm partials, 65,792 bytes,
+ * the largest workspace mle_adamw_clip_fused can ask for -- is a fixed device
+ * array, one per GPU, held until the process ends; mle_init looks up its
+ * address for the device it makes current (or the first call on another
+ * device does).  Every call on a GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (two streams or two host threads) race.  Each call writes
+ * every scratch value it reads, so nothing carries over from the last call.
+ * A span whose workspace would exceed the scratch is rejected with
+ * MLE_ERR_UNSUPPORTED (none does: the partial count is capped). */
+int mle_adamw_clip_fused_noalloc(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t,
+                                 float lr, float b1, float b2, float eps, float weight_decay, int adamw,
+                                 double clip_scale, double* norm_out);
 
 /* ------------------------------------------------------------------------- */
 /* Integer / index paths (bit-exact)                                         */

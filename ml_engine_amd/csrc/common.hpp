@@ -35,6 +35,10 @@ struct ProbeScope {
   }
 };
 
+// Per-device set-up of the allocation-free optimizer entry point (optim.hip);
+// mle_init calls it with the device current.
+int optim_scratch_setup();
+
 inline hipStream_t as_stream(mle_stream s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

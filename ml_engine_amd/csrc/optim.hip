@@ -11,6 +11,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 using namespace mle;
 
@@ -274,17 +276,20 @@ int mle_adam_update(mle_stream stream, float* p, const float* g, float* m, float
 
 size_t mle_adamw_clip_ws_bytes(size_t n) { return 256 + mle_sqnorm_ws_bytes(n); }
 
-int mle_adamw_clip_fused(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t, float lr,
-                         float b1, float b2, float eps, float weight_decay, int adamw, double clip_scale,
-                         double* norm_out, void* ws, size_t ws_bytes) {
-  MLE_CHECK_ARG(p && g && m && v && ws, "mle_adamw_clip_fused: null pointer");
-  MLE_CHECK_ARG(t >= 1, "mle_adamw_clip_fused: step t = %d must be >= 1", t);
-  if (n == 0) return MLE_OK;
-  if (ws_bytes < mle_adamw_clip_ws_bytes(n)) return set_error(MLE_ERR_WORKSPACE, "mle_adamw_clip_fused: workspace too small");
-  hipStream_t s = as_stream(stream);
+}  // extern "C"
+
+namespace {
+
+// accumulate -> Sqrt_Scale -> update with g / s over one span; `ws` holds s in
+// its first 256 bytes and the per-block partial sums after them.  Every value
+// read from ws is written earlier in the same call (each partial block writes
+// its own slot, the finish kernel writes s from the partials alone), so ws
+// needs no clearing between calls.
+int adamw_clip(hipStream_t s, float* p, const float* g, float* m, float* v, size_t n, int t, float lr, float b1,
+               float b2, float eps, float weight_decay, int adamw, double clip_scale, double* norm_out, void* ws) {
   const double* clip = nullptr;
   if (clip_scale > 0.0) {
-    double* sdev = static_cast<double*>(ws);  // first 256 bytes hold the scale s
+    double* sdev = static_cast<double*>(ws);
     double* part = reinterpret_cast<double*>(static_cast<char*>(ws) + 256);
     const unsigned grid = sqnorm_grid(n);
     {
@@ -294,13 +299,90 @@ int mle_adamw_clip_fused(mle_stream stream, float* p, const float* g, float* m, 
     }
     // s = Sqrt_Scale(sum g^2) computed from zero, so nothing is cleared beforehand.
     sqnorm_finish<<<1, FIN_NT, 0, s>>>(part, grid, sdev, 0, 1, clip_scale, norm_out);
-    int rc = check_launch("mle_adamw_clip_fused");
+    int rc = check_launch("adamw_clip: norm");
     if (rc) return rc;
     clip = sdev;
   }
-  int rc = launch_update(s, p, g, m, v, n, t, lr, b1, b2, eps, weight_decay, adamw, clip);
+  return launch_update(s, p, g, m, v, n, t, lr, b1, b2, eps, weight_decay, adamw, clip);
+}
+
+// ---- allocation-free variant ----------------------------------------------
+// Scratch of mle_adamw_clip_fused_noalloc: the clip scale s (256 bytes) and
+// at most kPartCap per-block partial sums -- the workspace mle_adamw_clip_fused
+// takes, at its largest (sqnorm_grid never exceeds kPartCap).  One copy per
+// GPU, alive until the process ends; every call on a GPU uses that GPU's copy.
+constexpr size_t kScratchBytes = 256 + (size_t)kPartCap * sizeof(double);
+static __device__ __align__(256) double scratch[kScratchBytes / sizeof(double)];
+
+// Device address of `scratch` per device.  The host-side name `scratch` is a
+// stand-in, not a device address: kernels and copies take these pointers.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  MLE_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(MLE_ERR_UNSUPPORTED, "adamw scratch: device %d is beyond the %d devices supported", dev,
+                     kMaxDevices);
+  void* ptr = g_scratch_dev[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    ptr = g_scratch_dev[dev].load(std::memory_order_relaxed);
+    if (!ptr) {
+      hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !ptr) return hip_error(e, "adamw scratch: hipGetSymbolAddress(scratch)");
+      g_scratch_dev[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return MLE_OK;
+}
+
+}  // namespace
+
+namespace mle {
+// Called by mle_init with `device` current: looks up this device's scratch
+// address once, so the allocation-free entry point makes no setup call later.
+int optim_scratch_setup() {
+  void* ptr = nullptr;
+  return scratch_on_current_device(&ptr);
+}
+}  // namespace mle
+
+extern "C" {
+
+int mle_adamw_clip_fused(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t, float lr,
+                         float b1, float b2, float eps, float weight_decay, int adamw, double clip_scale,
+                         double* norm_out, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(p && g && m && v && ws, "mle_adamw_clip_fused: null pointer");
+  MLE_CHECK_ARG(t >= 1, "mle_adamw_clip_fused: step t = %d must be >= 1", t);
+  if (n == 0) return MLE_OK;
+  if (ws_bytes < mle_adamw_clip_ws_bytes(n)) return set_error(MLE_ERR_WORKSPACE, "mle_adamw_clip_fused: workspace too small");
+  int rc = adamw_clip(as_stream(stream), p, g, m, v, n, t, lr, b1, b2, eps, weight_decay, adamw, clip_scale, norm_out,
+                      ws);
   if (rc) return rc;
   return check_launch("mle_adamw_clip_fused");
+}
+
+int mle_adamw_clip_fused_noalloc(mle_stream stream, float* p, const float* g, float* m, float* v, size_t n, int t,
+                                 float lr, float b1, float b2, float eps, float weight_decay, int adamw,
+                                 double clip_scale, double* norm_out) {
+  MLE_CHECK_ARG(p && g && m && v, "mle_adamw_clip_fused_noalloc: null pointer");
+  MLE_CHECK_ARG(t >= 1, "mle_adamw_clip_fused_noalloc: step t = %d must be >= 1", t);
+  if (n == 0) return MLE_OK;
+  const size_t need = mle_adamw_clip_ws_bytes(n);
+  if (need > kScratchBytes)
+    return set_error(MLE_ERR_UNSUPPORTED,
+                     "mle_adamw_clip_fused_noalloc: n = %zu needs %zu bytes of scratch, the fixed scratch holds %zu", n,
+                     need, kScratchBytes);
+  void* ws = nullptr;
+  int rc = scratch_on_current_device(&ws);
+  if (rc) return rc;
+  rc = adamw_clip(as_stream(stream), p, g, m, v, n, t, lr, b1, b2, eps, weight_decay, adamw, clip_scale, norm_out, ws);
+  if (rc) return rc;
+  return check_launch("mle_adamw_clip_fused_noalloc");
 }
 
 }  // extern "C"

@@ -108,7 +108,7 @@ int mle_init(int device) {
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return set_error(MLE_ERR_UNSUPPORTED, "mle_init: device %d is %s; this library is built for gfx950", device,
                      prop.gcnArchName);
-  return MLE_OK;
+  return optim_scratch_setup();
 }
 
 int mle_device_alloc(void** ptr, size_t bytes) {

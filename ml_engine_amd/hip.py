@@ -102,6 +102,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_adam_update": (I, [P, P, P, P, P, SZ, I, F, F, F, F, F, I, P]),
     "mle_adamw_clip_ws_bytes": (SZ, [SZ]),
     "mle_adamw_clip_fused": (I, [P, P, P, P, P, SZ, I, F, F, F, F, F, I, D, P, P, SZ]),
+    "mle_adamw_clip_fused_noalloc": (I, [P, P, P, P, P, SZ, I, F, F, F, F, F, I, D, P]),
     "mle_embed_gather": (I, [P, P, P, P, I, I, I, I]),
     "mle_embed_scatter_ws_bytes": (SZ, [I, I]),
     "mle_embed_scatter_add": (I, [P, P, P, P, I, I, I, I, I, F, P, SZ]),
