@@ -4,17 +4,18 @@ one MI355X, driven through the C++ GraphOperations engine.
 A step is one `zero_grad -> forward(calc_loss) -> backward -> ParameterUpdate`
 over one batch of synthetic data (32 x 256 tokens, d 512, 8 heads, FFN 2048,
 vocab 8000), with inputs and parameters resident in HBM.  The JSON line also
-carries:
-  roofline      the dominant kernel family (the GEMM layout with the most time),
-                timed per launch with HIP events on the engine stream during the
-                timed steps; achieved = algorithmic flop per launch / duration;
-                traffic = that family's HBM bytes per launch from the committed
-                rocprofv3 counter passes (profiles/c4_gemm_traffic.md)
-  cpu_baseline  the CPU oracle (OpenMP restatement of the reference math) on a
-                bounded sample of the same step, scaled to steps/s
-  extras        C3 (Linear GEMM backward) TFLOP/s, C2 (fused clip + AdamW
-                over 100 M parameters) GB/s, C1 (MLP, latency-bound) and C5
-                (U-Net residual block, conv-bound) steps/s, measured in the same run
+carries, for C4 and for every other configuration under `extras`:
+  roofline      the dominant kernel (family), timed per launch with HIP events
+                on the stream it runs on during the measured work; achieved =
+                algorithmic flop (or bytes) per launch / average launch time;
+                traffic = its HBM bytes per launch from the committed rocprofv3
+                counter passes (profiles/*_traffic.json), or null
+  cpu_baseline  the CPU oracle (OpenMP restatement of the reference math) on the
+                same workload on this host's cores: one warm-up call, then the
+                median of 5 timed calls
+Configurations: C4 transformer block (the headline), C3 Linear GEMM backward,
+C2 fused clip + AdamW over 100 M parameters, C1 MLP (latency-bound), C5 U-Net
+residual block (conv-bound).
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras] [--only c1|c2|c3|c5]
 """
 from __future__ import annotations
@@ -23,6 +24,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -40,18 +42,118 @@ from ml_engine_amd.models import STEP_ALL, Model  # noqa: E402
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 PEAK_HBM = 8000.0       # GB/s
 GEMM_FAMILIES = ["gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt", "gemm_pair"]
+CONV_FAMILIES = ["conv_fwd", "conv_dgrad", "conv_wgrad"]
+CPU_REPS = 5
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+# ------------------------------------------------------------------ probes
 def probe_read():
     n, ms, fl, by = C.c_int(), C.c_double(), C.c_double(), C.c_double()
     hip.call("mle_probe_read", C.byref(n), C.byref(ms), C.byref(fl), C.byref(by))
     return n.value, ms.value, fl.value, by.value
 
 
+def probed(fam: str, work) -> tuple[int, float, float, float]:
+    """Run `work` with the launch probe armed for one kernel family."""
+    hip.call("mle_probe_arm", fam.encode())
+    work()
+    res = probe_read()
+    hip.call("mle_probe_arm", None)
+    return res
+
+
+def dominant(families, work) -> str:
+    """The family with the most event-timed time over one call of `work` (untimed)."""
+    best, best_ms = families[0], -1.0
+    for fam in families:
+        n, ms, _, _ = probed(fam, work)
+        log(f"[bench] probe {fam}: {n} launches, {ms:.3f} ms")
+        if ms > best_ms:
+            best, best_ms = fam, ms
+    return best
+
+
+def measured_traffic(workload: str, fam: str):
+    """HBM bytes per launch of a kernel family from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (profiles/<workload>_traffic.json), or None."""
+    try:
+        data = json.loads((ROOT / "profiles" / f"{workload}_traffic.json").read_text())
+        return round(data[fam]["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def roofline(workload: str, fam: str, probe, bound: str) -> dict:
+    n, ms, flop, nbytes = probe
+    n = max(n, 1)
+    avg_ms = ms / n
+    if bound == "mfma":
+        achieved = (flop / n) / (avg_ms * 1e-3) / 1e12
+        out = {"bound": "mfma", "kernel": fam, "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA,
+               "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
+               "traffic": measured_traffic(workload, fam), "flop_per_launch": flop / n}
+    else:
+        achieved = (nbytes / n) / (avg_ms * 1e-3) / 1e9
+        out = {"bound": "hbm", "kernel": fam, "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s",
+               "frac": round(achieved / PEAK_HBM, 4), "traffic": measured_traffic(workload, fam)}
+    out.update({"alg_bytes_per_launch": round(nbytes / n), "launches": n, "avg_launch_ms": round(avg_ms, 5)})
+    return out
+
+
+# -------------------------------------------------------------- CPU oracle
+def oracle():
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as orc  # the CPU restatement; only the cpu_baseline legs load it
+
+    return orc
+
+
+def cpu_timed(call) -> tuple[float, list[float]]:
+    """One warm-up call, then the median of CPU_REPS timed calls (seconds)."""
+    call()
+    times = []
+    for _ in range(CPU_REPS):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def cpu_result(value: float, unit: str, sample: str, times: list[float]) -> dict:
+    orc = oracle()
+    return {"value": round(value, 6), "unit": unit, "cores": int(orc.call("orc_num_threads")), "kind": "port",
+            "sample": sample + f"; warm-up + median of {CPU_REPS} ({min(times):.3f}-{max(times):.3f} s per call); "
+                               f"oracle build {orc.lib_path().name}"}
+
+
+def cpu_c4(cfg: BlockConfig, sample_batch: int) -> dict:
+    orc = oracle()
+    scfg = BlockConfig(batch=sample_batch, seq=cfg.seq, d_model=cfg.d_model, heads=cfg.heads, ffn=cfg.ffn,
+                       vocab=cfg.vocab, lr=cfg.lr)
+    ids, tgt, params = block_data(scfg, seed=3)
+    op = [np.ascontiguousarray(p.reshape(-1)).copy() for p in params]
+    og, om, ov = ([np.zeros_like(p) for p in op] for _ in range(3))
+    T = orc.ptr_table
+    tables = [T(op), T(og), T(om), T(ov)]
+
+    def step():
+        for g in og:
+            g.fill(0.0)
+        orc.call("orc_c4_step", scfg.batch, scfg.seq, scfg.d_model, scfg.heads, scfg.ffn, scfg.vocab, orc.ptr(ids),
+                 orc.ptr(tgt), *tables, scfg.lr, 1, 0)
+
+    med, times = cpu_timed(step)
+    frac = sample_batch / cfg.batch
+    what = "one full C4 step (batch 32)" if sample_batch == cfg.batch else \
+        f"one C4 step at batch {sample_batch} of {cfg.batch}, scaled by {sample_batch}/{cfg.batch}"
+    return cpu_result(frac / med, "steps/s", what, times)
+
+
+# ------------------------------------------------------------------ C4
 def build_block(cfg: BlockConfig) -> Model:
     ids, tgt, params = block_data(cfg, seed=3)
     m = Model("block", cfg.dims(), seed=3)
@@ -63,55 +165,8 @@ def build_block(cfg: BlockConfig) -> Model:
     return m
 
 
-def measured_traffic(fam: str):
-    """HBM bytes per launch of a GEMM family from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (profiles/c4_gemm_traffic.md), or None."""
-    try:
-        data = json.loads((ROOT / "profiles" / "c4_gemm_traffic.json").read_text())
-        return round(data[fam]["traffic_bytes_per_launch"])
-    except (OSError, KeyError, ValueError):
-        return None
-
-
-def dominant_family(m: Model, lr: float) -> str:
-    """One probed step per GEMM layout (untimed); the layout with the most time wins."""
-    best, best_ms = GEMM_FAMILIES[0], -1.0
-    for fam in GEMM_FAMILIES:
-        hip.call("mle_probe_arm", fam.encode())
-        m.step(lr, STEP_ALL)
-        m.sync()
-        n, ms, _, _ = probe_read()
-        log(f"[bench] probe {fam}: {n} launches, {ms:.3f} ms per step")
-        if ms > best_ms:
-            best, best_ms = fam, ms
-    hip.call("mle_probe_arm", None)
-    return best
-
-
-def cpu_baseline(cfg: BlockConfig, sample_batch: int) -> dict:
-    sys.path.insert(0, str(ROOT / "tests"))
-    import oracle_lib as orc  # the CPU restatement; only this leg loads it
-
-    scfg = BlockConfig(batch=sample_batch, seq=cfg.seq, d_model=cfg.d_model, heads=cfg.heads, ffn=cfg.ffn,
-                       vocab=cfg.vocab, lr=cfg.lr)
-    ids, tgt, params = block_data(scfg, seed=3)
-    op = [np.ascontiguousarray(p.reshape(-1)).copy() for p in params]
-    og = [np.zeros_like(p) for p in op]
-    om = [np.zeros_like(p) for p in op]
-    ov = [np.zeros_like(p) for p in op]
-    T = orc.ptr_table
-    threads = int(orc.call("orc_num_threads"))
-    t0 = time.perf_counter()
-    orc.call("orc_c4_step", scfg.batch, scfg.seq, scfg.d_model, scfg.heads, scfg.ffn, scfg.vocab, orc.ptr(ids),
-             orc.ptr(tgt), T(op), T(og), T(om), T(ov), scfg.lr, 1, 0)
-    dt = time.perf_counter() - t0
-    # steps/s of the full workload: the sample is sample_batch/batch of one step's tokens
-    return {"value": round((sample_batch / cfg.batch) / dt, 5), "unit": "steps/s", "cores": threads, "kind": "port",
-            "sample": f"one oracle step at batch {sample_batch} of {cfg.batch} ({dt:.2f} s), scaled by "
-                      f"{sample_batch}/{cfg.batch}"}
-
-
-def extras_gemm() -> dict:
+# ------------------------------------------------------------------ C3
+def extras_gemm(cpu: bool) -> dict:
     """C3: dX = dY W^T and dW = X^T dY (+ fused db) at 8192 x 1024 x 4096."""
     cfg = GemmConfig()
     X, W, dY = gemm_data(cfg, seed=1)
@@ -123,44 +178,99 @@ def extras_gemm() -> dict:
         hip.call("mle_gemm", None, 0, 1, M, K, N, 1.0, gdY.ptr, N, 0, gW.ptr, N, 0, 1.0, gdX.ptr, K, 0, 1, None)
         hip.call("mle_gemm", None, 1, 0, K, N, M, 1.0, gX.ptr, K, 0, gdY.ptr, N, 0, 1.0, gdW.ptr, N, 0, 1, gdb.ptr)
 
-    for _ in range(3):
-        run()
-    hip.sync()
-    reps = 20
+    def reps(k):
+        def w():
+            for _ in range(k):
+                run()
+            hip.sync()
+        return w
+
+    reps(3)()
     t0 = time.perf_counter()
-    for _ in range(reps):
-        run()
-    hip.sync()
-    ms = (time.perf_counter() - t0) * 1e3 / reps
+    reps(20)()
+    ms = (time.perf_counter() - t0) * 1e3 / 20
     flop = 2.0 * 2.0 * M * N * K
-    return {"workload": "C3 Linear backward dX, dW, db (8192x1024x4096)", "ms": round(ms, 4),
-            "tflops": round(flop / ms / 1e9, 2), "frac_fp32_mfma": round(flop / ms / 1e9 / PEAK_FP32_MFMA, 4)}
+    fam = dominant(["gemm_nt", "gemm_tn"], reps(5))
+    out = {"workload": "C3 Linear backward dX, dW, db (8192x1024x4096)", "ms": round(ms, 4),
+           "tflops": round(flop / ms / 1e9, 2), "frac_fp32_mfma": round(flop / ms / 1e9 / PEAK_FP32_MFMA, 4),
+           "roofline": roofline("c3", fam, probed(fam, reps(10)), "mfma")}
+    if cpu:
+        log("[bench] cpu baseline C3 (oracle)")
+        orc = oracle()
+        dX, dW, db = np.zeros((M, K), np.float32), np.zeros((K, N), np.float32), np.zeros(N, np.float32)
+
+        def c3():
+            orc.call("orc_bcmm", 1, orc.ptr(dY), orc.ptr(W), orc.ptr(dX), 1, 1, M, N, K, 1, 3, 0, 3, 1.0)
+            orc.call("orc_bcmm", 2, orc.ptr(X), orc.ptr(dY), orc.ptr(dW), 1, 1, K, M, N, 1, 3, 3, 0, 1.0)
+            orc.call("orc_bcompress", orc.ptr(dY), orc.ptr(db), M, N, 1.0)
+
+        med, times = cpu_timed(c3)
+        out["cpu_baseline"] = cpu_result(flop / med / 1e12, "TFLOP/s", "the full C3 dX + dW + db", times)
+    for b in (gX, gW, gdY, gdX, gdW, gdb):
+        b.free()
+    return out
 
 
-def extras_adamw(steps: int = 10) -> dict:
+# ------------------------------------------------------------------ C2
+def extras_adamw(cpu: bool, steps: int = 10) -> dict:
     """C2: accumulate + clipNorm + ParameterUpdate over 100 M params in 64 tensors."""
     cfg = FlatConfig()
     sizes, p, g = flat_data(cfg, seed=2)
     m = Model("flat", [len(sizes)] + sizes, seed=2)
-    off = 0
-    for i, s in enumerate(sizes):
-        m.set(i, p[off:off + s], 0)
-        m.set(i, g[off:off + s], 1)
-        off += s
-    del p, g
+    offs = np.concatenate([[0], np.cumsum(sizes)])
+    for i in range(len(sizes)):
+        m.set(i, p[offs[i]:offs[i + 1]], 0)
+        m.set(i, g[offs[i]:offs[i + 1]], 1)
     m.step(cfg.lr, 8, cfg.max_norm)
     m.sync()
+
+    def run():
+        for _ in range(steps):
+            m.step(cfg.lr, 8, cfg.max_norm)
+        m.sync()
+
     t0 = time.perf_counter()
-    for _ in range(steps):
-        m.step(cfg.lr, 8, cfg.max_norm)
-    m.sync()
+    run()
     ms = (time.perf_counter() - t0) * 1e3 / steps
+    rl = roofline("c2", "adam_update", probed("adam_update", run), "hbm")
+    norm = probed("sqnorm", run)
     m.close()
     gbs = 32.0 * cfg.total / (ms * 1e-3) / 1e9
-    return {"workload": "C2 fused clip + AdamW, 100M params / 64 tensors", "ms_per_step": round(ms, 4),
-            "gb_per_s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4), "bytes_per_param": 32}
+    out = {"workload": "C2 fused clip + AdamW, 100M params / 64 tensors", "ms_per_step": round(ms, 4),
+           "gb_per_s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4), "bytes_per_param": 32,
+           "roofline": rl,
+           "sqnorm_pass": {"gb_per_s": round(norm[3] / max(norm[0], 1) / (norm[1] / max(norm[0], 1) * 1e-3) / 1e9, 1),
+                           "avg_launch_ms": round(norm[1] / max(norm[0], 1), 5)}}
+    if cpu:
+        log("[bench] cpu baseline C2 (oracle)")
+        orc = oracle()
+        chunks_g = [g[offs[i]:offs[i + 1]] for i in range(len(sizes))]
+        ref_p = [p[offs[i]:offs[i + 1]] for i in range(len(sizes))]  # updated in place: timing only
+        ref_m = [np.zeros(s, np.float32) for s in sizes]
+        ref_v = [np.zeros(s, np.float32) for s in sizes]
+        gc = np.empty(max(sizes), np.float32)
+        t = [0]
+
+        def c2():
+            t[0] += 1
+            acc = np.zeros(1, np.float64)
+            for c in chunks_g:
+                orc.call("orc_sumsq", orc.ptr(c), c.size, orc.ptr(acc))
+            orc.call("orc_sqrt_scale", orc.ptr(acc), 1.0)
+            for i, c in enumerate(chunks_g):
+                buf = gc[:c.size]
+                buf[:] = c  # the reference clips in place; the pristine gradient is kept
+                orc.call("orc_clip", orc.ptr(buf), c.size, orc.ptr(acc))
+                orc.call("orc_adam", orc.ptr(ref_p[i]), orc.ptr(buf), c.size, t[0], orc.ptr(ref_m[i]),
+                         orc.ptr(ref_v[i]), 0.9, 0.999, 1e-8, 0.01, cfg.lr, 1)
+
+        med, times = cpu_timed(c2)
+        out["cpu_baseline"] = cpu_result(32.0 * cfg.total / med / 1e9, "GB/s",
+                                         "one full C2 step over 100M parameters (norm, clip, AdamW)", times)
+    return out
 
 
+# ------------------------------------------------------------------ C1 / C5
 def timed_steps(m: Model, lr: float, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         m.step(lr, STEP_ALL)
@@ -172,7 +282,15 @@ def timed_steps(m: Model, lr: float, steps: int, warmup: int) -> float:
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def extras_mlp(steps: int = 200) -> dict:
+def step_work(m: Model, lr: float, steps: int = 1):
+    def w():
+        for _ in range(steps):
+            m.step(lr, STEP_ALL)
+        m.sync()
+    return w
+
+
+def extras_mlp(cpu: bool, steps: int = 200) -> dict:
     """C1: Linear 784->256 -> ReLU -> Linear 256->10 -> softmax CE, batch 64, Adam."""
     cfg = MLPConfig()
     x, labels, params = mlp_data(cfg, seed=0)
@@ -182,12 +300,36 @@ def extras_mlp(steps: int = 200) -> dict:
     m.input(0, x)
     m.input(1, labels)
     ms = timed_steps(m, cfg.lr, steps, 5)
+    fam = dominant(GEMM_FAMILIES, step_work(m, cfg.lr, 5))
+    rl = roofline("c1", fam, probed(fam, step_work(m, cfg.lr, 20)), "mfma")
     m.close()
-    return {"workload": "C1 MLP 784-256-10 step (fwd + bwd + Adam), batch 64", "ms_per_step": round(ms, 4),
-            "steps_per_s": round(1e3 / ms, 1)}
+    flop = 78.0e6
+    out = {"workload": "C1 MLP 784-256-10 step (fwd + bwd + Adam), batch 64", "ms_per_step": round(ms, 4),
+           "steps_per_s": round(1e3 / ms, 1), "bound": "launch latency (GEMMs of 1-7 tiles)",
+           "roofline": rl}
+    if cpu:
+        log("[bench] cpu baseline C1 (oracle)")
+        orc = oracle()
+        op = [np.ascontiguousarray(p.reshape(-1)).copy() for p in params]
+        og, om, ov = ([np.zeros_like(p) for p in op] for _ in range(3))
+        T = orc.ptr_table
+        tables = [T(op), T(og), T(om), T(ov)]
+        inner = 50
+
+        def c1():
+            for _ in range(inner):
+                for gr in og:
+                    gr.fill(0.0)
+                orc.call("orc_c1_step", cfg.batch, cfg.inp, cfg.hidden, cfg.classes, orc.ptr(x), orc.ptr(labels),
+                         *tables, cfg.lr, 1, 0, None)
+
+        med, times = cpu_timed(c1)
+        out["cpu_baseline"] = cpu_result(inner / med, "steps/s", f"{inner} full C1 steps per timed call", times)
+        out["cpu_baseline"]["gflops"] = round(flop * inner / med / 1e9, 2)
+    return out
 
 
-def extras_resblock(steps: int = 10) -> dict:
+def extras_resblock(cpu: bool, steps: int = 10) -> dict:
     """C5: conv3x3 64->128, GN(32), SiLU, time projection, conv3x3 128->128, GN, 1x1 skip, MSE; AdamW."""
     cfg = ResBlockConfig()
     x, noise, t, params = resblock_data(cfg, seed=4)
@@ -197,11 +339,30 @@ def extras_resblock(steps: int = 10) -> dict:
     m.input(0, x)
     m.input(1, noise)
     ms = timed_steps(m, cfg.lr, steps, 2)
+    fam = dominant(CONV_FAMILIES, step_work(m, cfg.lr, 1))
+    rl = roofline("c5", fam, probed(fam, step_work(m, cfg.lr, 5)), "mfma")
     m.close()
     tf = cfg.conv_flop / (ms * 1e-3) / 1e12
-    return {"workload": "C5 U-Net residual block step (fwd + bwd + AdamW), 16x64x64x64", "ms_per_step": round(ms, 4),
-            "steps_per_s": round(1e3 / ms, 2), "conv_gflop_per_step": round(cfg.conv_flop / 1e9, 2),
-            "conv_tflops_whole_step": round(tf, 2)}
+    out = {"workload": "C5 U-Net residual block step (fwd + bwd + AdamW), 16x64x64x64", "ms_per_step": round(ms, 4),
+           "steps_per_s": round(1e3 / ms, 2), "conv_gflop_per_step": round(cfg.conv_flop / 1e9, 2),
+           "conv_tflops_whole_step": round(tf, 2), "roofline": rl}
+    if cpu:
+        log("[bench] cpu baseline C5 (oracle)")
+        orc = oracle()
+        op = [np.ascontiguousarray(p.reshape(-1)).copy() for p in params]
+        og, om, ov = ([np.zeros_like(p) for p in op] for _ in range(3))
+        T = orc.ptr_table
+        tables = [T(op), T(og), T(om), T(ov)]
+
+        def c5():
+            for gr in og:
+                gr.fill(0.0)
+            orc.call("orc_c5_step", cfg.batch, cfg.cin, cfg.cout, cfg.h, cfg.w, cfg.groups, cfg.tdim, t, orc.ptr(x),
+                     orc.ptr(noise), *tables, cfg.lr, 1, 0)
+
+        med, times = cpu_timed(c5)
+        out["cpu_baseline"] = cpu_result(1.0 / med, "steps/s", "one full C5 step (batch 16)", times)
+    return out
 
 
 def main() -> int:
@@ -211,7 +372,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--cpu-sample-batch", type=int, default=8)
+    ap.add_argument("--cpu-sample-batch", type=int, default=32)
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c5"],
                     help="run just this secondary workload (for profiling) and print its JSON object")
     args = ap.parse_args()
@@ -219,12 +380,15 @@ def main() -> int:
         print("bench.py measures one MI355X: this build has no multi-GPU path (every box has one GPU); "
               "run with --gpus 1", file=sys.stderr)
         return 2
+    # the CPU baseline's OpenMP threads stay on their cores (read when the oracle loads)
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    cpu = not args.no_cpu
 
     hip.init(0)
+    extras_fn = {"c1": lambda: extras_mlp(cpu), "c2": lambda: extras_adamw(cpu, args.steps if args.only else 10),
+                 "c3": lambda: extras_gemm(cpu), "c5": lambda: extras_resblock(cpu, args.steps if args.only else 10)}
     if args.only:
-        run = {"c1": lambda: extras_mlp(), "c2": lambda: extras_adamw(args.steps),
-               "c3": lambda: extras_gemm(), "c5": lambda: extras_resblock(args.steps)}[args.only]
-        print(json.dumps(run()), flush=True)
+        print(json.dumps(extras_fn[args.only]()), flush=True)
         return 0
     cfg = BlockConfig()
     log(f"[bench] building C4 block: {cfg}")
@@ -232,7 +396,7 @@ def main() -> int:
     for _ in range(args.warmup):
         m.step(cfg.lr, STEP_ALL)
     m.sync()
-    fam = dominant_family(m, cfg.lr)
+    fam = dominant(GEMM_FAMILIES, step_work(m, cfg.lr))
     log(f"[bench] dominant kernel family: {fam}")
 
     hip.call("mle_probe_arm", fam.encode())
@@ -242,34 +406,22 @@ def main() -> int:
         m.step(cfg.lr, STEP_ALL)
     m.sync()
     dt = time.perf_counter() - t0
-    n, kms, kflop, kbytes = probe_read()
+    probe = probe_read()
     hip.call("mle_probe_arm", None)
     ms_step = dt * 1e3 / args.steps
     log(f"[bench] {args.steps} steps in {dt:.3f} s: {ms_step:.3f} ms/step, loss {m.loss:.6g}")
-
-    avg_ms = kms / max(n, 1)
-    achieved = (kflop / max(n, 1)) / (avg_ms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": fam, "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
-                "traffic": measured_traffic(fam), "alg_bytes_per_launch": round(kbytes / max(n, 1)),
-                "launches": n, "avg_launch_ms": round(avg_ms, 5),
-                "flop_per_launch": kflop / max(n, 1)}
+    rl = roofline("c4", fam, probe, "mfma")
     m.close()
 
     extras = {}
     if not args.no_extras:
-        log("[bench] extras: C3 GEMM backward")
-        extras["gemm_backward"] = extras_gemm()
-        log("[bench] extras: C2 fused clip + AdamW")
-        extras["adamw_clip"] = extras_adamw()
-        log("[bench] extras: C1 MLP")
-        extras["mlp"] = extras_mlp()
-        log("[bench] extras: C5 residual block")
-        extras["resblock"] = extras_resblock()
-    cpu = None
-    if not args.no_cpu:
-        log("[bench] cpu baseline (oracle)")
-        cpu = cpu_baseline(cfg, args.cpu_sample_batch)
+        for key, name in (("gemm_backward", "c3"), ("adamw_clip", "c2"), ("mlp", "c1"), ("resblock", "c5")):
+            log(f"[bench] extras: {name}")
+            extras[key] = extras_fn[name]()
+    cpu_line = None
+    if cpu:
+        log("[bench] cpu baseline C4 (oracle)")
+        cpu_line = cpu_c4(cfg, args.cpu_sample_batch)
 
     out = {
         "metric": "fwd+bwd+AdamW steps/sec (transformer block); HBM GB/s & MFMA % of peak",
@@ -289,8 +441,8 @@ def main() -> int:
                    "vocab": cfg.vocab, "gemm_gflop_per_step": round(cfg.gemm_flop / 1e9, 2),
                    "parallelism": "single GPU"},
         "gemm_tflops_per_step": round(cfg.gemm_flop / (ms_step * 1e-3) / 1e12, 2),
-        "roofline": roofline,
-        "cpu_baseline": cpu,
+        "roofline": rl,
+        "cpu_baseline": cpu_line,
         "extras": extras,
     }
     print(json.dumps(out), flush=True)

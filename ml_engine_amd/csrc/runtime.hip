@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -60,7 +61,12 @@ static hipEvent_t take_event() {
   return e;
 }
 
+// Set while a family is armed: an unarmed probe costs every launch one relaxed
+// atomic load, no lock and no string compare.
+static std::atomic<bool> g_probe_on{false};
+
 bool probe_armed(const char* kernel) {
+  if (!g_probe_on.load(std::memory_order_relaxed)) return false;
   std::lock_guard<std::mutex> lk(g_probe_mu);
   return !g_probe_kernel.empty() && g_probe_kernel == kernel;
 }
@@ -216,6 +222,7 @@ int mle_probe_arm(const char* kernel) {
   }
   g_probe_recs.clear();
   g_probe_kernel = kernel ? kernel : "";
+  g_probe_on.store(!g_probe_kernel.empty(), std::memory_order_relaxed);
   return MLE_OK;
 }
 

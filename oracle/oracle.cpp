@@ -78,53 +78,59 @@ inline void gemm_tile(const float* ap, const float* bp, long long n, double acc[
     }
   }
 }
+
+// C[r, c] = sum_k A(r, k) B(k, c) for r < m, c < p, k < n, with the operands
+// given by element functions: each is read once into a packed copy (op(A) as
+// [row tile][k][kMR], op(B) as [column tile][k][kNR], zero past the matrix
+// edge -- those products only reach discarded tile elements), then every tile
+// is summed by gemm_tile and handed to store(r, c, sum).
+template <class AF, class BF, class SF>
+void packed_gemm(long long m, long long n, long long p, const AF& a_el, const BF& b_el, const SF& store) {
+  const long long rt = (m + kMR - 1) / kMR, ct = (p + kNR - 1) / kNR;
+  std::vector<float> ap((size_t)(rt * kMR * n)), bp((size_t)(ct * kNR * n));
+#pragma omp parallel for schedule(static)
+  for (long long t = 0; t < rt; ++t)
+    for (int i = 0; i < kMR; ++i) {
+      const long long r = t * kMR + i;
+      float* dst = ap.data() + t * kMR * n + i;
+      for (long long k = 0; k < n; ++k) dst[k * kMR] = r < m ? a_el(r, k) : 0.0f;
+    }
+#pragma omp parallel for schedule(static)
+  for (long long t = 0; t < ct; ++t)
+    for (long long k = 0; k < n; ++k)
+      for (int j = 0; j < kNR; ++j) {
+        const long long col = t * kNR + j;
+        bp[(size_t)((t * n + k) * kNR + j)] = col < p ? b_el(k, col) : 0.0f;
+      }
+  const long long rblocks = (rt + kRowTiles - 1) / kRowTiles;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (long long cb = 0; cb < ct; ++cb)
+    for (long long rb = 0; rb < rblocks; ++rb)
+      for (long long t = rb * kRowTiles; t < std::min(rt, (rb + 1) * kRowTiles); ++t) {
+        double acc[kMR][kNR];
+        gemm_tile(ap.data() + t * kMR * n, bp.data() + cb * kNR * n, n, acc);
+        for (int i = 0; i < kMR && t * kMR + i < m; ++i)
+          for (int j = 0; j < kNR && cb * kNR + j < p; ++j) store(t * kMR + i, cb * kNR + j, acc[i][j]);
+      }
+}
 }  // namespace
 
 OEXPORT void orc_bcmm(int kind, const float* a, const float* b, float* c, int batch, int channels, int m, int n, int p,
                       int backward, int fa, int fb, int fc, float scale) {
-  const long long rt = (m + kMR - 1) / kMR, ct = (p + kNR - 1) / kNR;
-  // op(A) as [row tile][k][kMR] and op(B) as [column tile][k][kNR], zero past
-  // the matrix edge (those products only reach discarded tile elements).
-  std::vector<float> ap((size_t)(rt * kMR * n)), bp((size_t)(ct * kNR * n));
   for (int z = 0; z < batch * channels; ++z) {
     const int bi = z / channels, ci = z % channels;
     const float* A = a + bco(fa, bi, ci, channels, (long long)m * n);
     const float* B = b + bco(fb, bi, ci, channels, (long long)n * p);
     float* Cz = c + bco(fc, bi, ci, channels, (long long)m * p);
-#pragma omp parallel for schedule(static)
-    for (long long t = 0; t < rt; ++t)
-      for (int i = 0; i < kMR; ++i) {
-        const long long r = t * kMR + i;
-        float* dst = ap.data() + t * kMR * n + i;
-        for (long long k = 0; k < n; ++k) dst[k * kMR] = r < m ? a_at(A, kind, m, n, r, k) : 0.0f;
-      }
-#pragma omp parallel for schedule(static)
-    for (long long t = 0; t < ct; ++t)
-      for (long long k = 0; k < n; ++k)
-        for (int j = 0; j < kNR; ++j) {
-          const long long col = t * kNR + j;
-          bp[(size_t)((t * n + k) * kNR + j)] = col < p ? b_at(B, kind, n, p, k, col) : 0.0f;
-        }
-    const long long rblocks = (rt + kRowTiles - 1) / kRowTiles;
-#pragma omp parallel for collapse(2) schedule(dynamic, 1)
-    for (long long cb = 0; cb < ct; ++cb)
-      for (long long rb = 0; rb < rblocks; ++rb)
-        for (long long t = rb * kRowTiles; t < std::min(rt, (rb + 1) * kRowTiles); ++t) {
-          double acc[kMR][kNR];
-          gemm_tile(ap.data() + t * kMR * n, bp.data() + cb * kNR * n, n, acc);
-          for (int i = 0; i < kMR; ++i) {
-            const long long r = t * kMR + i;
-            if (r >= m) break;
-            for (int j = 0; j < kNR; ++j) {
-              const long long col = cb * kNR + j;
-              if (col >= p) break;
-              const float sum = (float)acc[i][j];
-              float* dst = Cz + r * p + col;
-              if (backward == 0) *dst = scale * sum;
-              else *dst += scale * sum;
-            }
-          }
-        }
+    packed_gemm(
+        m, n, p, [&](long long r, long long k) { return a_at(A, kind, m, n, r, k); },
+        [&](long long k, long long col) { return b_at(B, kind, n, p, k, col); },
+        [&](long long r, long long col, double acc) {
+          const float sum = (float)acc;
+          float* dst = Cz + r * p + col;
+          if (backward == 0) *dst = scale * sum;
+          else *dst += scale * sum;
+        });
   }
 }
 
@@ -429,8 +435,72 @@ OEXPORT void orc_norm_bwd(const float* y, const float* dy, float* dx, const floa
 
 // ---------------------------------------------------------------------------
 // Convolution (NCHW, OIHW).
-// CV2D (Engine/kernels.cu:985-1019)
+// Convolute2D as GEMMs over gathered operands (implicit im2col).  Each sum
+// runs over the same index order as the direct 7-loop form below it (the
+// *_naive functions, kept to pin this one bit for bit): an out-of-image tap
+// enters as a 0 product, which leaves a nonzero double sum unchanged and keeps
+// a zero sum +0.
+// CV2D (Engine/kernels.cu:985-1019): y[n, co, p] = sum_{ci, kh, kw} x w + b[co].
 OEXPORT void orc_conv_fwd(const float* x, const float* w, const float* bias, float* y, int N, int Cin, int H, int W,
+                          int Cout, int KH, int KW, int pad, int stride) {
+  const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
+  const long long P = (long long)OH * OW, K = (long long)Cin * KH * KW;
+  packed_gemm(
+      Cout, K, (long long)N * P, [&](long long co, long long k) { return w[co * K + k]; },
+      [&](long long k, long long c) {
+        const long long n = c / P, pix = c % P;
+        const int ci = (int)(k / (KH * KW)), kh = (int)(k / KW % KH), kw = (int)(k % KW);
+        const int iy = (int)(pix / OW) * stride - pad + kh, ix = (int)(pix % OW) * stride - pad + kw;
+        if (iy < 0 || iy >= H || ix < 0 || ix >= W) return 0.0f;
+        return x[((n * Cin + ci) * H + iy) * W + ix];
+      },
+      [&](long long co, long long c, double acc) {
+        const long long n = c / P, pix = c % P;
+        const float sv = (float)acc;
+        y[(n * Cout + co) * P + pix] = bias ? sv + bias[co] : sv;
+      });
+}
+
+// CV2D_GradInput (Engine/kernels.cu:1053-1089): dx[n, ci, q] += sum_{co, kh, kw} dy w.
+OEXPORT void orc_conv_dgrad(const float* dy, const float* w, float* dx, int N, int Cin, int H, int W, int Cout, int KH,
+                            int KW, int pad, int stride) {
+  const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
+  const long long HW = (long long)H * W, KK = (long long)KH * KW;
+  packed_gemm(
+      Cin, (long long)Cout * KK, (long long)N * HW,
+      [&](long long ci, long long k) { return w[((k / KK) * Cin + ci) * KK + k % KK]; },
+      [&](long long k, long long c) {
+        const long long n = c / HW, q = c % HW;
+        const int oc = (int)(k / KK), kh = (int)(k / KW % KH), kw = (int)(k % KW);
+        const int nr = (int)(q / W) + pad - kh, nc = (int)(q % W) + pad - kw;
+        if (nr < 0 || nr % stride != 0 || nc < 0 || nc % stride != 0) return 0.0f;
+        const int oy = nr / stride, ox = nc / stride;
+        if (oy >= OH || ox >= OW) return 0.0f;
+        return dy[((n * Cout + oc) * OH + oy) * OW + ox];
+      },
+      [&](long long ci, long long c, double acc) { dx[(c / HW * Cin + ci) * HW + c % HW] += (float)acc; });
+}
+
+// GV2D (Engine/kernels.cu:1021-1051): dw[co, (ci, kh, kw)] = sum_{n, oy, ox} x dy (assign).
+OEXPORT void orc_conv_wgrad(const float* x, const float* dy, float* dw, int N, int Cin, int H, int W, int Cout, int KH,
+                            int KW, int pad, int stride) {
+  const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
+  const long long P = (long long)OH * OW, KK = (long long)KH * KW;
+  packed_gemm(
+      Cout, (long long)N * P, (long long)Cin * KK,
+      [&](long long co, long long k) { return dy[(k / P * Cout + co) * P + k % P]; },
+      [&](long long k, long long c) {
+        const long long n = k / P, pix = k % P;
+        const int ci = (int)(c / KK), kh = (int)(c / KW % KH), kw = (int)(c % KW);
+        const int iy = (int)(pix / OW) * stride - pad + kh, ix = (int)(pix % OW) * stride - pad + kw;
+        if (iy < 0 || iy >= H || ix < 0 || ix >= W) return 0.0f;
+        return x[((n * Cin + ci) * H + iy) * W + ix];
+      },
+      [&](long long co, long long c, double acc) { dw[co * Cin * KK + c] = (float)acc; });
+}
+
+// CV2D (Engine/kernels.cu:985-1019)
+OEXPORT void orc_conv_fwd_naive(const float* x, const float* w, const float* bias, float* y, int N, int Cin, int H, int W,
                           int Cout, int KH, int KW, int pad, int stride) {
   const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
 #pragma omp parallel for collapse(2) schedule(static)
@@ -453,7 +523,7 @@ OEXPORT void orc_conv_fwd(const float* x, const float* w, const float* bias, flo
 }
 
 // CV2D_GradInput (Engine/kernels.cu:1053-1089): dX += ...
-OEXPORT void orc_conv_dgrad(const float* dy, const float* w, float* dx, int N, int Cin, int H, int W, int Cout, int KH,
+OEXPORT void orc_conv_dgrad_naive(const float* dy, const float* w, float* dx, int N, int Cin, int H, int W, int Cout, int KH,
                             int KW, int pad, int stride) {
   const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
 #pragma omp parallel for collapse(2) schedule(static)
@@ -482,7 +552,7 @@ OEXPORT void orc_conv_dgrad(const float* dy, const float* w, float* dx, int N, i
 }
 
 // GV2D (Engine/kernels.cu:1021-1051): dK = ... (assign)
-OEXPORT void orc_conv_wgrad(const float* x, const float* dy, float* dw, int N, int Cin, int H, int W, int Cout, int KH,
+OEXPORT void orc_conv_wgrad_naive(const float* x, const float* dy, float* dw, int N, int Cin, int H, int W, int Cout, int KH,
                             int KW, int pad, int stride) {
   const int OH = (2 * pad + H - KH) / stride + 1, OW = (2 * pad + W - KW) / stride + 1;
 #pragma omp parallel for collapse(2) schedule(static)

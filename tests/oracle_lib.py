@@ -38,6 +38,9 @@ SIGS = {
     "orc_conv_fwd": (None, [P, P, P, P, I, I, I, I, I, I, I, I, I]),
     "orc_conv_dgrad": (None, [P, P, P, I, I, I, I, I, I, I, I, I]),
     "orc_conv_wgrad": (None, [P, P, P, I, I, I, I, I, I, I, I, I]),
+    "orc_conv_fwd_naive": (None, [P, P, P, P, I, I, I, I, I, I, I, I, I]),
+    "orc_conv_dgrad_naive": (None, [P, P, P, I, I, I, I, I, I, I, I, I]),
+    "orc_conv_wgrad_naive": (None, [P, P, P, I, I, I, I, I, I, I, I, I]),
     "orc_mse_loss": (F, [P, P, LL]),
     "orc_mse_bwd": (None, [P, P, P, P, LL]),
     "orc_softmax_xent_fwd": (F, [P, P, P, I, I]),

@@ -347,6 +347,33 @@ def test_conv_vs_torch(orc, k, pad, stride):
     assert_close(dw, gw.numpy(), rtol=1e-6, atol_scale=1e-6, what="conv wgrad")
 
 
+@pytest.mark.parametrize("n,cin,h,w,cout,k,pad,stride", [(2, 3, 9, 7, 5, 3, 1, 1), (2, 4, 8, 8, 6, 3, 1, 2),
+                                                         (1, 5, 7, 6, 4, 1, 0, 1), (2, 3, 10, 9, 4, 5, 2, 3),
+                                                         (3, 2, 6, 6, 3, 2, 0, 2)])
+def test_conv_gemm_form_equals_direct_loops(orc, n, cin, h, w, cout, k, pad, stride):
+    """The oracle's convolutions run as GEMMs over gathered operands; they add
+    the same products in the same order as the direct 7-loop form, so every
+    output is bit-identical to it (padding taps, strides, ragged tiles)."""
+    r = rng(70 + k + stride)
+    oh, ow = (2 * pad + h - k) // stride + 1, (2 * pad + w - k) // stride + 1
+    x = r.standard_normal((n, cin, h, w)).astype(np.float32)
+    wt = r.standard_normal((cout, cin, k, k)).astype(np.float32)
+    b = r.standard_normal(cout).astype(np.float32)
+    dy = r.standard_normal((n, cout, oh, ow)).astype(np.float32)
+    y1, y2 = np.zeros((n, cout, oh, ow), np.float32), np.zeros((n, cout, oh, ow), np.float32)
+    orc.call("orc_conv_fwd", p(x), p(wt), p(b), p(y1), n, cin, h, w, cout, k, k, pad, stride)
+    orc.call("orc_conv_fwd_naive", p(x), p(wt), p(b), p(y2), n, cin, h, w, cout, k, k, pad, stride)
+    dx0 = r.standard_normal(x.shape).astype(np.float32)
+    d1, d2 = dx0.copy(), dx0.copy()
+    orc.call("orc_conv_dgrad", p(dy), p(wt), p(d1), n, cin, h, w, cout, k, k, pad, stride)
+    orc.call("orc_conv_dgrad_naive", p(dy), p(wt), p(d2), n, cin, h, w, cout, k, k, pad, stride)
+    g1, g2 = np.zeros_like(wt), np.zeros_like(wt)
+    orc.call("orc_conv_wgrad", p(x), p(dy), p(g1), n, cin, h, w, cout, k, k, pad, stride)
+    orc.call("orc_conv_wgrad_naive", p(x), p(dy), p(g2), n, cin, h, w, cout, k, k, pad, stride)
+    for a, b_ in ((y1, y2), (d1, d2), (g1, g2)):
+        np.testing.assert_array_equal(a.view(np.uint32), b_.view(np.uint32))
+
+
 # --------------------------------------------------------------------- losses
 def test_losses_closed_form(orc):
     r = rng(60)
