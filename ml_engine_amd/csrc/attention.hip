@@ -549,9 +549,13 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
   }
 }
 
+// Operand addressing uses 32-bit byte offsets into buffer resources whose
+// extent is the tensor's byte size (AttnArgs::bytes), so every tensor must stay
+// below 2 GiB in bytes, not elements.
 bool attn_shape_ok(int batch, int heads, int seq, int head_dim, int ld) {
   return batch > 0 && heads > 0 && head_dim == HD && seq >= 64 && seq % 64 == 0 && ld % 4 == 0 &&
-         ld >= heads * HD && (double)batch * heads <= 65535.0 && (double)batch * seq * ld < 2147483647.0;
+         ld >= heads * HD && (double)batch * heads <= 65535.0 &&
+         (double)batch * seq * ld * sizeof(float) < 2147483648.0 - 64.0;
 }
 
 }  // namespace
@@ -567,7 +571,8 @@ int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const f
                       int heads, int seq, int head_dim, int ld, float scale, int causal, void* ws, size_t ws_bytes) {
   MLE_CHECK_ARG(q && k && v && out && ws, "mle_attention_fwd: null pointer");
   if (!attn_shape_ok(batch, heads, seq, head_dim, ld))
-    return set_error(MLE_ERR_UNSUPPORTED, "mle_attention_fwd: needs head_dim 64, seq a multiple of 64, ld %% 4 == 0");
+    return set_error(MLE_ERR_UNSUPPORTED,
+                     "mle_attention_fwd: needs head_dim 64, seq a multiple of 64, ld %% 4 == 0 and tensors below 2 GiB");
   if (ws_bytes < mle_attention_ws_bytes(batch, heads, seq))
     return set_error(MLE_ERR_WORKSPACE, "mle_attention_fwd: workspace too small");
   MLE_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(ws),

@@ -13,6 +13,7 @@
 #include <map>
 #include <mutex>
 #include <random>
+#include <unordered_set>
 
 namespace mle {
 
@@ -173,10 +174,51 @@ int accumulate_flag(NodeBackProp* n) {
 }
 
 void materialize(NodeBackProp* n) {
-  if (!n || !n->grad_pending_zero) return;
+  if (!n) return;
+  clip_apply(n);
+  if (!n->grad_pending_zero) return;
   n->grad_pending_zero = false;
   zero(n->grad, n->total);
 }
+
+// ---------------------------------------------------------------------------
+// pending global-norm clip
+namespace {
+double* g_clip_snapshot = nullptr;             // device double: s as clipNorm saw it
+std::unordered_set<NodeBackProp*> g_clip_marked;  // parameters whose gradient reads as g / s
+}  // namespace
+
+void clip_mark(const std::vector<AdamParameter*>& ps, const double* s) {
+  clip_apply_all();
+  if (!g_clip_snapshot) g_clip_snapshot = static_cast<double*>(alloc_scratch(256));
+  check(mle_memcpy_d2d(g_clip_snapshot, s, sizeof(double), stream()), "clipNorm: snapshot of the scale");
+  for (auto* p : ps) g_clip_marked.insert(p);
+}
+
+const double* clip_view(const std::vector<AdamParameter*>& ps) {
+  if (g_clip_marked.empty()) return nullptr;
+  bool all = g_clip_marked.size() == ps.size();
+  for (auto* p : ps) all = all && g_clip_marked.count(p);
+  if (all) return g_clip_snapshot;
+  clip_apply_all();
+  return nullptr;
+}
+
+void clip_apply(NodeBackProp* p) {
+  if (g_clip_marked.empty() || !g_clip_marked.erase(p)) return;
+  check(mle_scale_by_device(stream(), p->grad, g_clip_snapshot, 1, p->total), "ScalePtr of " + p->op_name);
+}
+
+void clip_apply_all() {
+  auto marked = std::move(g_clip_marked);
+  g_clip_marked.clear();
+  for (auto* p : marked)
+    check(mle_scale_by_device(stream(), p->grad, g_clip_snapshot, 1, p->total), "ScalePtr of " + p->op_name);
+}
+
+void clip_drop(NodeBackProp* p) { g_clip_marked.erase(p); }
+
+void clip_clear() { g_clip_marked.clear(); }
 
 // ---------------------------------------------------------------------------
 // flat parameter arena
@@ -332,6 +374,8 @@ AdamParameter::AdamParameter(str n, int out, int in, int row, int col, double no
   check(mle_fill(mle::stream(), v, 0.0f, total), "AdamParameter v");
 }
 
+AdamParameter::~AdamParameter() { mle::clip_drop(this); }
+
 // File layout: [u32 name_len][name][i32 total][f32 W * total][f32 m * total][f32 v * total]
 // (Engine/engine.cu:139-184); `t` is not stored, as in the reference.
 void AdamParameter::save(std::ofstream& f) const {
@@ -436,11 +480,18 @@ void Dimension(AdamParameter X) {
   std::cout << "Dimensions for node: " << X.op_name << " ";
   printf("(%i x %i x %i x %i) \n", X.dim[0], X.dim[1], X.dim[2], X.dim[3]);
 }
-void Zerograd(AdamParameter& X) { mle::zero(X.grad, X.total); }
-void Zerograd(graph X) { mle::zero(X->grad, X->total); }
+void Zerograd(const AdamParameter& X) {
+  auto* p = const_cast<AdamParameter*>(&X);
+  mle::clip_drop(p);
+  mle::zero(p->grad, p->total);
+}
+void Zerograd(graph X) {
+  mle::clip_drop(X.get());
+  mle::zero(X->grad, X->total);
+}
 
-static void print_head(const graph& X, int type, int rows_max, int cols_max) {
-  if (type) mle::materialize(X.get());
+static void print_head(NodeBackProp* X, int type, int rows_max, int cols_max) {
+  if (type) mle::materialize(X);
   const int ch = X->dim[1], rows = X->dim[2], cols = X->dim[3];
   const long long n = std::min<long long>(X->total, (long long)ch * rows * cols);
   std::vector<float> cpu(n);
@@ -455,8 +506,42 @@ static void print_head(const graph& X, int type, int rows_max, int cols_max) {
     std::cout << "------------------------------\n";
   }
 }
-void printGPU(const graph X, const int type) { print_head(X, type, X->dim[2], X->dim[3]); }
-void printHeadGPU(const graph X, const int type) { print_head(X, type, 5, 5); }
+void printGPU(const graph X, const int type) { print_head(X.get(), type, X->dim[2], X->dim[3]); }
+void printGPU(const AdamParameter& X, const int type) {
+  print_head(const_cast<AdamParameter*>(&X), type, X.dim[2], X.dim[3]);
+}
+void printHeadGPU(const graph X, const int type) { print_head(X.get(), type, 5, 5); }
+void printHeadGPU(const AdamParameter& X, const int type) { print_head(const_cast<AdamParameter*>(&X), type, 5, 5); }
+
+// isNan (Engine/engine.cu:328-348): the reference's ISNAN kernel traps on a NaN
+// element (Includes/kernels.h:382-392) and CheckError prints and exits.  Here
+// the sum of squares of the tensor is NaN exactly when an element is NaN (an
+// infinite element gives +inf, never NaN, as the reference's x != x test
+// ignores infinities too); it is read back and the same message is printed.
+static void nan_check(NodeBackProp* X, int type) {
+  static double* acc = nullptr;
+  static void* ws = nullptr;
+  static size_t wcap = 0;
+  if (!acc) acc = static_cast<double*>(mle::alloc_scratch(256));
+  const float* p = type ? X->grad : X->output;
+  if (!p || X->total <= 0) return;
+  if (type) mle::materialize(X);
+  const size_t need = mle_sqnorm_ws_bytes(X->total);
+  if (wcap < need) {
+    ws = mle::alloc_scratch(need);
+    wcap = need;
+  }
+  check(mle_fill(mle::stream(), reinterpret_cast<float*>(acc), 0.0f, 2), "isNan");
+  check(mle_grad_sqnorm(mle::stream(), p, X->total, acc, nullptr, ws, wcap), "isNan");
+  double sum = 0.0;
+  check(mle_memcpy_d2h(&sum, acc, sizeof(double), mle::stream()), "isNan");
+  if (sum != sum) {
+    std::cerr << "Runtime error in " << X->op_name << (type == 0 ? "output" : "grad") << " has nan value" << std::endl;
+    std::exit(1);
+  }
+}
+void isNan(graph X, const int type) { nan_check(X.get(), type); }
+void isNan(const AdamParameter& X, const int type) { nan_check(const_cast<AdamParameter*>(&X), type); }
 
 int ArgMaxToCPU(const graph& input) {
   static int32_t* d = nullptr;
@@ -540,22 +625,23 @@ void* span_ws(size_t bytes) {
 }  // namespace
 
 void GraphOperations::clipNorm(double* global_scale) {
-  // Deferred: ParameterUpdate reads g / s inside the update pass.  Anything
-  // else that consumes the gradients first applies the division in place.
-  flush_clip();
-  pending_clip_ = global_scale;
-}
-
-void GraphOperations::flush_clip() {
-  if (!pending_clip_) return;
-  const double* s = pending_clip_;
-  pending_clip_ = nullptr;
-  for (auto& node : nodes)
-    if (node->clipnorm) node->clipnorm(s);
+  bool all_hooks_known = true;
+  for (auto& n : nodes)
+    if (n->clipnorm && n->params.empty()) all_hooks_known = false;
+  bool dup = false;
+  auto ps = collect_params(nodes, dup);
+  if (all_hooks_known && !ps.empty()) {
+    // Deferred: the gradients read as g / s from here on (mle::clip_mark).
+    mle::clip_mark(ps, global_scale);
+  } else {
+    mle::clip_apply_all();
+    for (auto& node : nodes)
+      if (node->clipnorm) node->clipnorm(global_scale);
+  }
 }
 
 void GraphOperations::accumulate(double* global_scale) {
-  flush_clip();
+  mle::clip_apply_all();
   bool dup = false;
   auto ps = collect_params(nodes, dup);
   bool all_hooks_known = true;
@@ -590,50 +676,22 @@ void GraphOperations::ParameterUpdate(const graph& X, const bool show, const flo
       fusable = false;
   if (fusable) {
     AdamParameter* p0 = ps[0];
+    // With a pending clip every gradient reads as g / s: the update divides in
+    // registers and the gradients stay marked (they still read as g / s).
+    const double* clip = mle::clip_view(ps);
     for (auto& sp : contiguous_spans(ps))
       check(mle_adam_update(mle::stream(), sp.p, sp.g, sp.m, sp.v, sp.n, p0->t, lr, p0->b1, p0->b2, p0->epsilon,
-                            p0->weight_decay, adamw ? 1 : 0, pending_clip_),
+                            p0->weight_decay, adamw ? 1 : 0, clip),
             "AdamUpdate (fused over the parameter arena)");
     for (auto* p : ps) p->t++;
-    pending_clip_ = nullptr;
   } else {
-    flush_clip();
+    mle::clip_apply_all();
     for (auto& node : nodes)
       if (node->updateParams) node->updateParams(lr, adamw);
   }
   if (show)
     for (auto& node : nodes)
       if (node->updateParams) printHeadGPU(node, 1);
-}
-
-static void nan_check(const graph& node, int type) {
-  static double* acc = nullptr;
-  static int* flag = nullptr;
-  static void* ws = nullptr;
-  static size_t wcap = 0;
-  if (!acc) {
-    acc = static_cast<double*>(mle::alloc_scratch(256));
-    flag = static_cast<int*>(mle::alloc_scratch(256));
-  }
-  const float* p = type ? node->grad : node->output;
-  if (!p) return;
-  if (type) mle::materialize(node.get());
-  const size_t need = mle_sqnorm_ws_bytes(node->total);
-  if (wcap < need) {
-    ws = mle::alloc_scratch(need);
-    wcap = need;
-  }
-  const int zero = 0;
-  const double dz = 0.0;
-  check(mle_memcpy_h2d(flag, &zero, sizeof(int), mle::stream()), "isNan");
-  check(mle_memcpy_h2d(acc, &dz, sizeof(double), mle::stream()), "isNan");
-  check(mle_grad_sqnorm(mle::stream(), p, node->total, acc, flag, ws, wcap), "isNan");
-  int bad = 0;
-  check(mle_memcpy_d2h(&bad, flag, sizeof(int), mle::stream()), "isNan");
-  if (bad) {
-    std::cerr << "IsNan of " << node->op_name << ": non-finite value\n";
-    std::exit(1);
-  }
 }
 
 void GraphOperations::forward(const graph& X, const bool calc_loss, const bool show, const bool time,
@@ -653,7 +711,7 @@ void GraphOperations::forward(const graph& X, const bool calc_loss, const bool s
     if (node->forward) {
       node->forward();
       node->forward_called = true;
-      if (check_nan) nan_check(node, 0);
+      if (check_nan) nan_check(node.get(), 0);
       if (show) {
         Dimension(node);
         printHeadGPU(node);
@@ -675,7 +733,7 @@ void GraphOperations::backward(const graph& X, const bool show, const bool time,
     printf("Warning... Nodes list is empty and bacward cannot run.. \n");
     return;
   }
-  flush_clip();
+  mle::clip_apply_all();  // parameter gradients are added into: give them their clipped values
   for (auto it = nodes.rbegin(); it != nodes.rend(); ++it) {
     std::chrono::high_resolution_clock::time_point t0;
     if (time) {
@@ -689,7 +747,7 @@ void GraphOperations::backward(const graph& X, const bool show, const bool time,
       if (!(*it)->lazy_grad_writer)
         for (auto& in : (*it)->inputs) mle::materialize(in.get());
       (*it)->backward();
-      if (check_nan) nan_check(*it, 1);
+      if (check_nan) nan_check(it->get(), 1);
       if (show) printHeadGPU(*it, 1);
     }
     if (time) {
@@ -707,7 +765,7 @@ void GraphOperations::zero_grad(const graph& X, const bool show) {
     printf("Warning... Nodes list is empty and Zero grad cannot run.. \n");
     return;
   }
-  pending_clip_ = nullptr;  // the clipped gradients are being cleared anyway
+  mle::clip_clear();  // the clipped gradients are being cleared anyway
   mle::ZeroBatch batch;
   for (auto it = nodes.rbegin(); it != nodes.rend(); ++it) {
     if ((*it)->zero_grad) {

@@ -94,6 +94,24 @@ void materialize(NodeBackProp* n);
 // same either way).  On by default.
 void set_lazy_zero(bool on);
 
+// Global-norm clip over parameter gradients (GraphOperations::clipNorm).  The
+// reference divides every parameter gradient by s in place (ScalePtr,
+// Engine/engine.cu:3362, 302).  Here clipNorm records a copy of s taken at the
+// call and marks the parameters: their gradients then read as g / s without
+// being rewritten.  The fused ParameterUpdate reads g / s inside the update
+// pass; anything else that reads a marked gradient or adds into it (backward,
+// accumulate, a second clipNorm, ReadValueAt, printGPU, the NaN check, host
+// copies) divides it in place first, so every observable value is the
+// reference's.  zero_grad and a whole-tensor overwrite drop the mark.
+void clip_mark(const std::vector<AdamParameter*>& ps, const double* s);
+// The snapshot of s when every parameter of `ps` is marked (the fused update
+// reads through it); otherwise divides the marked ones in place and returns null.
+const double* clip_view(const std::vector<AdamParameter*>& ps);
+void clip_apply(NodeBackProp* p);  // divide this parameter's gradient now, if marked
+void clip_apply_all();
+void clip_drop(NodeBackProp* p);   // its gradient is being overwritten or zeroed
+void clip_clear();
+
 // Flat parameter arena.  param_reserve(n) announces n floats of parameters that
 // should be contiguous: it sizes the next slab (default 64 Mi floats) and, if
 // the current slab cannot hold n more, makes the next allocation open it.
@@ -113,9 +131,14 @@ void set_init_seed(uint64_t seed);
 //  broadcast_channel_reference_grad: Broadcast_Channel reduces only the first
 //    `width` channels of B's gradient (Channel_Squeeze1D<<<b, ...>>>,
 //    Engine/engine.cu:1435).
+//  layernorm_reference_layout: LayerNorm's backward gives a gradient only to the
+//    first batch*rows*cols elements when channels > 1 (LayerBackward's
+//    `idx >= batch*row*col` guard, Engine/kernels.cu:849-862); off, every
+//    element gets the per-sample formula.
 struct Quirks {
   bool bmmabt_reference_grad = true;
   bool broadcast_channel_reference_grad = true;
+  bool layernorm_reference_layout = true;
 };
 Quirks& quirks();
 
@@ -184,6 +207,8 @@ struct AdamParameter : public NodeBackProp {
   mle::ParamSlot slot;
 
   AdamParameter(str n, int out, int in, int row, int col, double norm = NORM);
+  // Leaves the pending-clip set (mle::clip_mark), which holds parameters by address.
+  ~AdamParameter() override;
   void save(std::ofstream& f) const;
   void load(std::ifstream& f);
   void update(const float lr = LEARNING_RATE, const bool W = ADAMW) override;
@@ -194,18 +219,23 @@ struct AdamParameter : public NodeBackProp {
 
 void Dimension(graph X);
 void Dimension(AdamParameter X);
-void Zerograd(AdamParameter& X);
+// The AdamParameter overloads take a const reference where the reference takes
+// the parameter by value (Includes/engine.h:87-96): every call that compiles
+// against the reference compiles here, without copying the parameter.
+void Zerograd(const AdamParameter& X);
 void Zerograd(graph X);
+void isNan(graph X, const int type = 0);
+void isNan(const AdamParameter& X, const int type = 0);
 void printGPU(const graph X, const int type = 0);
+void printGPU(const AdamParameter& X, const int type = 0);
 void printHeadGPU(const graph X, const int type = 0);
+void printHeadGPU(const AdamParameter& X, const int type = 0);
 int ArgMaxToCPU(const graph& input);
 graph_tree topological_sort(const graph& root);
 
 class GraphOperations {
  private:
   static bool calculate_loss;
-  const double* pending_clip_ = nullptr;
-  void flush_clip();
 
  public:
   graph_tree nodes;

@@ -33,9 +33,11 @@ struct Model {
   std::unique_ptr<Embedding> emb;
   std::unique_ptr<ResidualBlock> rb;
   std::unique_ptr<Convolute2DT> up;
+  std::unique_ptr<Convolute2D> conv;
   std::vector<std::unique_ptr<AdamParameter>> loose;  // C2 parameters
   double* clip_scale = nullptr;
   bool adamw = true;
+  std::vector<float*> grad_backup;  // mle_model_grads_save
 };
 
 void* input_buffer(Model* m, size_t bytes) {
@@ -150,6 +152,18 @@ void build_c2(Model* m, const long long* d, int nd) {
   (void)nd;
 }
 
+// A 1x1 convolution, LayerNorm over its whole [C, H, W] sample (C > 1, where
+// the reference's LayerBackward guard matters) and an MSE loss.
+// dims {N, Cin, C, H, W}
+void build_c7(Model* m, const long long* d) {
+  const int N = (int)d[0], Cin = (int)d[1], C = (int)d[2], Hs = (int)d[3], Ws = (int)d[4];
+  auto x = input_node(m, "Input", N, Cin, Hs, Ws);
+  auto target = input_node(m, "Target", N, C, Hs, Ws);
+  m->conv.reset(new Convolute2D(Cin, C, 1, 1, 1, 0, "Conv"));
+  m->root = GraphOperations::MeanSquaredError(GraphOperations::LayerNorm(m->conv->forward(x)), target, true);
+  m->params = {&m->conv->W1, &m->conv->B1};
+}
+
 }  // namespace
 
 extern "C" {
@@ -158,9 +172,11 @@ void mle_model_set_lazy_zero(int on) { mle::set_lazy_zero(on != 0); }
 
 void mle_model_set_fusion(int on) { mle::set_sibling_fusion(on != 0); }
 
-void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad) {
+void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad,
+                          int layernorm_reference_layout) {
   mle::quirks().bmmabt_reference_grad = bmmabt_reference_grad != 0;
   mle::quirks().broadcast_channel_reference_grad = broadcast_channel_reference_grad != 0;
+  mle::quirks().layernorm_reference_layout = layernorm_reference_layout != 0;
 }
 
 void mle_model_set_seed(unsigned long long seed) { mle::set_init_seed(seed); }
@@ -174,6 +190,7 @@ void* mle_model_create(int kind, const long long* dims, int ndims) {
     case 4: build_c4(m, dims); break;
     case 5: build_c5(m, dims); break;
     case 6: build_c6(m, dims); break;
+    case 7: build_c7(m, dims); break;
     default:
       delete m;
       return nullptr;
@@ -205,7 +222,41 @@ int mle_model_param_io(void* h, int i, int which, void* host, int to_device) {
   AdamParameter* p = m->params[i];
   float* dev = which == 0 ? p->output : which == 1 ? p->grad : which == 2 ? p->m : p->v;
   const size_t bytes = (size_t)p->total * sizeof(float);
+  if (which == 1) {
+    if (to_device) mle::clip_drop(p);  // overwritten whole
+    else mle::materialize(p);          // reads the clipped value, as the reference's buffer holds it
+  }
   return to_device ? mle_memcpy_h2d(dev, host, bytes, mle::stream()) : mle_memcpy_d2h(host, dev, bytes, mle::stream());
+}
+
+// Keep a device copy of every parameter gradient (save) and write it back
+// (restore), so a benchmark can start each optimizer step from the same
+// gradients without a host round trip.
+int mle_model_grads_save(void* h) {
+  auto* m = static_cast<Model*>(h);
+  if (m->grad_backup.empty()) {
+    for (AdamParameter* p : m->params)
+      m->grad_backup.push_back(static_cast<float*>(mle::alloc_scratch((size_t)p->total * sizeof(float))));
+  }
+  for (size_t i = 0; i < m->params.size(); ++i) {
+    AdamParameter* p = m->params[i];
+    mle::materialize(p);
+    int rc = mle_memcpy_d2d(m->grad_backup[i], p->grad, (size_t)p->total * sizeof(float), mle::stream());
+    if (rc) return rc;
+  }
+  return MLE_OK;
+}
+
+int mle_model_grads_restore(void* h) {
+  auto* m = static_cast<Model*>(h);
+  if (m->grad_backup.size() != m->params.size()) return MLE_ERR_INVALID;
+  for (size_t i = 0; i < m->params.size(); ++i) {
+    AdamParameter* p = m->params[i];
+    mle::clip_drop(p);
+    int rc = mle_memcpy_d2d(p->grad, m->grad_backup[i], (size_t)p->total * sizeof(float), mle::stream());
+    if (rc) return rc;
+  }
+  return MLE_OK;
 }
 
 int mle_model_input(void* h, int slot, const void* host, size_t bytes) {
@@ -222,6 +273,9 @@ int mle_model_step(void* h, float lr, int mode, float clip) {
       check(mle_fill(mle::stream(), reinterpret_cast<float*>(m->clip_scale), 0.0f, 2), "clip scale reset");
       m->go.accumulate(m->clip_scale);
       m->go.clipNorm(m->clip_scale);
+      // the caller reuses its scale buffer before the update (clipNorm must have kept s)
+      if (mode & MLE_STEP_CLOBBER_SCALE)
+        check(mle_fill(mle::stream(), reinterpret_cast<float*>(m->clip_scale), 0.0f, 2), "clip scale clobber");
     }
     if (mode & MLE_STEP_UPDATE) m->go.ParameterUpdate(nullptr, false, lr, true);
     return MLE_OK;

@@ -10,6 +10,8 @@ extern "C" {
 #endif
 
 enum { MLE_STEP_ZERO = 1, MLE_STEP_FORWARD = 2, MLE_STEP_BACKWARD = 4, MLE_STEP_UPDATE = 8, MLE_STEP_ALL = 15 };
+/* kind 2 only: overwrite the clip scale buffer between clipNorm and the update */
+enum { MLE_STEP_CLOBBER_SCALE = 16 };
 
 /* kind 1: MLP   dims {batch, in, hidden, classes}            inputs: x f32, labels i32
  * kind 2: flat  dims {n, size_0 .. size_{n-1}}                (accumulate + clip + AdamW)
@@ -17,10 +19,14 @@ enum { MLE_STEP_ZERO = 1, MLE_STEP_FORWARD = 2, MLE_STEP_BACKWARD = 4, MLE_STEP_
  * kind 5: resblock dims {N, Cin, C, H, W, groups, tdim, t}   inputs: x f32, noise f32
  * kind 6: U-Net decoder step dims {N, Cin, Cout, H, W, Cskip, Hs, Ws, k, stride, pad}
  *         (Convolute2DT, CopyCrop, BatchNorm, RMSNorm, InstanceNorm, MSE)
- *                                                             inputs: x, skip, target f32 */
+ *                                                             inputs: x, skip, target f32
+ * kind 7: 1x1 Convolute2D -> LayerNorm over [C, H, W] -> MSE  dims {N, Cin, C, H, W}
+ *                                                             inputs: x, target f32 */
 void* mle_model_create(int kind, const long long* dims, int ndims);
 void mle_model_destroy(void* h);
-void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad);
+/* Reference bugs reproduced (1, default) or fixed (0); see mle::Quirks. */
+void mle_model_set_quirks(int bmmabt_reference_grad, int broadcast_channel_reference_grad,
+                          int layernorm_reference_layout);
 void mle_model_set_seed(unsigned long long seed);
 /* 1 (default): zero_grad marks node gradients clear and first writers assign;
  * 0: zero_grad fills them. */
@@ -33,8 +39,14 @@ int mle_model_num_params(void* h);
 const char* mle_model_param_name(void* h, int i);
 long long mle_model_param_numel(void* h, int i);
 int mle_model_param_t(void* h, int i);
-/* which: 0 params, 1 grads, 2 m, 3 v */
+/* which: 0 params, 1 grads, 2 m, 3 v.  Gradients read as the reference's
+ * buffer holds them (a pending clip is applied first); writing one replaces
+ * it whole. */
 int mle_model_param_io(void* h, int i, int which, void* host, int to_device);
+/* Device copy of every parameter gradient, and its write-back (benchmarks
+ * that restart each optimizer step from the same gradients). */
+int mle_model_grads_save(void* h);
+int mle_model_grads_restore(void* h);
 int mle_model_input(void* h, int slot, const void* host, size_t bytes);
 /* mode: MLE_STEP_* bits; clip > 0 (kind 2) applies accumulate + clipNorm. */
 int mle_model_step(void* h, float lr, int mode, float clip);

@@ -158,11 +158,13 @@ graph norm_node(const graph& X, int groups, const str& name) {
   float* stats = static_cast<float*>(mle::alloc_scratch(2 * sizeof(float) * a * groups));
   GraphOperations::GB += (double)(2 * a * groups) * sizeof(float) / (1ULL << 30);
   NodeBackProp *nd = node.get(), *x = X.get();
+  // LayerBackward's C == 1 guard (applies to groups == 1 only), as built
+  const int ref_layout = mle::quirks().layernorm_reference_layout ? 1 : 0;
   node->forward = [=]() {
     check(mle_norm_fwd(S(), x->output, nd->output, stats, a, b, hw, groups, eps, ws, ws_bytes), name + " forward");
   };
   node->backward = [=]() {
-    check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, 1, ws, ws_bytes,
+    check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, ref_layout, ws, ws_bytes,
                        mle::accumulate_flag(x)),
           name + " backward");
   };

@@ -11,14 +11,15 @@ import numpy as np
 
 from . import hip
 
-KIND = {"mlp": 1, "flat": 2, "block": 4, "resblock": 5, "unet_up": 6}
+KIND = {"mlp": 1, "flat": 2, "block": 4, "resblock": 5, "unet_up": 6, "conv_layernorm": 7}
 STEP_ZERO, STEP_FORWARD, STEP_BACKWARD, STEP_UPDATE, STEP_ALL = 1, 2, 4, 8, 15
+STEP_CLOBBER_SCALE = 16
 P, I, LL, F, SZ = C.c_void_p, C.c_int, C.c_longlong, C.c_float, C.c_size_t
 
 _SIGS = {
     "mle_model_create": (P, [I, C.POINTER(LL), I]),
     "mle_model_destroy": (None, [P]),
-    "mle_model_set_quirks": (None, [I, I]),
+    "mle_model_set_quirks": (None, [I, I, I]),
     "mle_model_set_seed": (None, [C.c_ulonglong]),
     "mle_model_set_lazy_zero": (None, [I]),
     "mle_model_set_fusion": (None, [I]),
@@ -27,6 +28,8 @@ _SIGS = {
     "mle_model_param_numel": (LL, [P, I]),
     "mle_model_param_t": (I, [P, I]),
     "mle_model_param_io": (I, [P, I, I, P, I]),
+    "mle_model_grads_save": (I, [P]),
+    "mle_model_grads_restore": (I, [P]),
     "mle_model_input": (I, [P, I, P, SZ]),
     "mle_model_step": (I, [P, F, I, F]),
     "mle_model_loss": (F, [P]),
@@ -61,10 +64,11 @@ class Model:
     """One configuration built with the engine (parameters in the flat arena)."""
 
     def __init__(self, kind: str, dims, seed: int = 0, reference_quirks: bool = True, lazy_zero: bool = True,
-                 fuse: bool = True):
+                 fuse: bool = True, layernorm_reference_layout: bool | None = None):
         L = lib()
         hip.init(0)
-        L.mle_model_set_quirks(int(reference_quirks), int(reference_quirks))
+        ln = reference_quirks if layernorm_reference_layout is None else layernorm_reference_layout
+        L.mle_model_set_quirks(int(reference_quirks), int(reference_quirks), int(ln))
         L.mle_model_set_lazy_zero(int(lazy_zero))
         L.mle_model_set_fusion(int(fuse))
         L.mle_model_set_seed(seed)
@@ -95,6 +99,12 @@ class Model:
 
     def step(self, lr: float, mode: int = STEP_ALL, clip: float = 0.0) -> None:
         hip.check(lib().mle_model_step(self.h, lr, mode, clip))
+
+    def grads_save(self) -> None:
+        hip.check(lib().mle_model_grads_save(self.h))
+
+    def grads_restore(self) -> None:
+        hip.check(lib().mle_model_grads_restore(self.h))
 
     def sync(self) -> None:
         hip.check(lib().mle_model_sync(self.h))

@@ -110,3 +110,12 @@ def test_attention_rejects_unsupported(hip):
         hip.call("mle_attention_fwd", None, g.ptr, g.ptr, g.ptr, g.ptr, 1, 1, 64, 32, 64, 1.0, 1, ws.ptr, ws.nbytes)
     with pytest.raises(hip.MLEError):  # seq not a multiple of 64
         hip.call("mle_attention_fwd", None, g.ptr, g.ptr, g.ptr, g.ptr, 1, 1, 48, 64, 64, 1.0, 1, ws.ptr, ws.nbytes)
+    # tensors of 2 GiB (2^29 floats: 1024 x 1024 x 512) and more are refused by
+    # their byte size before anything is launched; the buffers are never read
+    for call in ("mle_attention_fwd", "mle_attention_bwd"):
+        args = (None, g.ptr, g.ptr, g.ptr, g.ptr) if call == "mle_attention_fwd" else \
+            (None, g.ptr, g.ptr, g.ptr, g.ptr, g.ptr, g.ptr, g.ptr)
+        shape = (1024, 8, 1024, 64, 512, 1.0, 1)
+        tail = (ws.ptr, ws.nbytes) if call == "mle_attention_fwd" else (1, 1, 1, 1, ws.ptr, ws.nbytes)
+        with pytest.raises(hip.MLEError, match="2 GiB|head_dim"):
+            hip.call(call, *args, *shape, *tail)

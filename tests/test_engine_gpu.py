@@ -15,7 +15,7 @@ import pytest
 from conftest import assert_close
 from ml_engine_amd.configs import (BlockConfig, FlatConfig, MLPConfig, ResBlockConfig, block_data, flat_data,
                                    mlp_data, resblock_data)
-from ml_engine_amd.models import STEP_ALL, Model
+from ml_engine_amd.models import STEP_ALL, STEP_CLOBBER_SCALE, Model
 
 pytestmark = pytest.mark.gpu
 
@@ -122,27 +122,39 @@ def test_resblock_step(hip, orc, quirks):
     m.close()
 
 
-def test_flat_clip_adamw(hip, orc):
-    cfg = FlatConfig(total=300_000, tensors=8, lo=4096, hi=80_000, steps=3)
-    sizes, p, g = flat_data(cfg, seed=2)
+def _flat_model(cfg, seed=2):
+    sizes, p, g = flat_data(cfg, seed=seed)
     m = Model("flat", [len(sizes)] + sizes)
-    off = 0
-    chunks_p, chunks_g = [], []
-    for i, s in enumerate(sizes):
-        chunks_p.append(p[off:off + s].copy())
-        chunks_g.append(g[off:off + s].copy())
-        m.set(i, chunks_p[-1], 0)
-        m.set(i, chunks_g[-1], 1)
-        off += s
+    offs = np.concatenate([[0], np.cumsum(sizes)])
+    chunks_p = [p[offs[i]:offs[i + 1]].copy() for i in range(len(sizes))]
+    chunks_g = [g[offs[i]:offs[i + 1]].copy() for i in range(len(sizes))]
+    for i in range(len(sizes)):
+        m.set(i, chunks_p[i], 0)
+        m.set(i, chunks_g[i], 1)
+    return m, sizes, chunks_p, chunks_g
+
+
+def _oracle_norm(orc, grads):
+    acc = np.zeros(1, np.float64)
+    for c in grads:
+        orc.call("orc_sumsq", orc.ptr(c), c.size, orc.ptr(acc))
+    orc.call("orc_sqrt_scale", orc.ptr(acc), 1.0)
+    return acc
+
+
+def test_flat_clip_adamw(hip, orc):
+    """accumulate + clipNorm + ParameterUpdate, each step from the pristine
+    gradients (restored on both sides: the reference clips them in place)."""
+    cfg = FlatConfig(total=300_000, tensors=8, lo=4096, hi=80_000, steps=3)
+    m, sizes, chunks_p, chunks_g = _flat_model(cfg)
     ref_p = [c.copy() for c in chunks_p]
     ref_m = [np.zeros_like(c) for c in chunks_p]
     ref_v = [np.zeros_like(c) for c in chunks_p]
     for step in range(1, cfg.steps + 1):
+        for i, c in enumerate(chunks_g):
+            m.set(i, c, 1)
         m.step(cfg.lr, 8, cfg.max_norm)  # accumulate + clipNorm + ParameterUpdate
-        acc = np.zeros(1, np.float64)
-        for c in chunks_g:
-            orc.call("orc_sumsq", orc.ptr(c), c.size, orc.ptr(acc))
-        orc.call("orc_sqrt_scale", orc.ptr(acc), 1.0)
+        acc = _oracle_norm(orc, chunks_g)
         for i, c in enumerate(chunks_g):
             gc = c.copy()
             orc.call("orc_clip", orc.ptr(gc), gc.size, orc.ptr(acc))
@@ -154,6 +166,99 @@ def test_flat_clip_adamw(hip, orc):
         assert_close(m.get(i, 3), ref_v[i], what=f"v {i}", **EW)
         assert_close(m.get(i, 0), ref_p[i], what=f"p {i}", **EW)
         assert m.t(i) == cfg.steps + 1
+    m.close()
+
+
+def test_clip_reads_as_reference(hip, orc):
+    """The reference divides the parameter gradients in place at clipNorm
+    (Engine/engine.cu:3362, 302).  Here the division is deferred into the
+    update, yet every read sees the reference's values: after clipNorm alone,
+    after the update, and through a second step that starts from the clipped
+    gradients (its norm is taken over them).  The scale is the one clipNorm saw
+    even if the caller overwrites its buffer before the update."""
+    cfg = FlatConfig(total=200_000, tensors=5, lo=4096, hi=80_000)
+    # between clipNorm and the update
+    m, sizes, _, chunks_g = _flat_model(cfg)
+    m.step(cfg.lr, 0, cfg.max_norm)  # accumulate + clipNorm, no update
+    acc = _oracle_norm(orc, chunks_g)
+    assert acc[0] > 1.0
+    clipped = [c.copy() for c in chunks_g]
+    for c in clipped:
+        orc.call("orc_clip", orc.ptr(c), c.size, orc.ptr(acc))
+    for i in range(len(sizes)):
+        assert_close(m.get(i, 1), clipped[i], what=f"grad after clipNorm {i}", **EW)
+    m.close()
+    # two full steps without restoring the gradients, and the same with the
+    # scale buffer overwritten between clipNorm and the update
+    results = []
+    for mode in (8, 8 | STEP_CLOBBER_SCALE):
+        m, sizes, chunks_p, chunks_g = _flat_model(cfg)
+        ref_p = [c.copy() for c in chunks_p]
+        ref_m = [np.zeros_like(c) for c in chunks_p]
+        ref_v = [np.zeros_like(c) for c in chunks_p]
+        ref_g = [c.copy() for c in chunks_g]
+        for step in (1, 2):
+            m.step(cfg.lr, mode, cfg.max_norm)
+            acc = _oracle_norm(orc, ref_g)  # over the gradients as the reference left them
+            for i, gr in enumerate(ref_g):
+                orc.call("orc_clip", orc.ptr(gr), gr.size, orc.ptr(acc))  # in place, as ScalePtr
+                orc.call("orc_adam", orc.ptr(ref_p[i]), orc.ptr(gr), gr.size, step, orc.ptr(ref_m[i]),
+                         orc.ptr(ref_v[i]), 0.9, 0.999, 1e-8, 0.01, cfg.lr, 1)
+            # reading applies the pending division in place; without the read
+            # (first mode, first step) the next accumulate applies it
+            if step == 2 or mode & STEP_CLOBBER_SCALE:
+                for i in range(len(sizes)):
+                    assert_close(m.get(i, 1), ref_g[i], what=f"mode {mode} step {step} grad {i}", **EW)
+        got = [(m.get(i, 0), m.get(i, 2), m.get(i, 3)) for i in range(len(sizes))]
+        for i, (p, mm, vv) in enumerate(got):
+            assert_close(mm, ref_m[i], what=f"mode {mode} m {i}", **EW)
+            assert_close(vv, ref_v[i], what=f"mode {mode} v {i}", **EW)
+            assert_close(p, ref_p[i], what=f"mode {mode} p {i}", **EW)
+        results.append(got)
+        m.close()
+    for a, b in zip(results[0], results[1]):
+        for u, v in zip(a, b):
+            np.testing.assert_array_equal(u, v)
+
+
+@pytest.mark.parametrize("reference_layout", [True, False])
+def test_layernorm_multichannel_quirk(hip, orc, reference_layout):
+    """LayerNorm over a [C > 1, H, W] sample: the reference's LayerBackward
+    gives a gradient to the first batch*H*W elements only (its C == 1 guard,
+    Engine/kernels.cu:849-862); mle::Quirks::layernorm_reference_layout keeps
+    that (default) or applies the per-sample formula everywhere.  Checked
+    through a 1x1 convolution's weight and bias gradients against the oracle."""
+    N, Cin, Cc, Hh, Ww = 2, 3, 4, 5, 6
+    r = np.random.default_rng(77)
+    x = r.standard_normal((N, Cin, Hh, Ww), dtype=np.float32)
+    target = r.standard_normal((N, Cc, Hh, Ww), dtype=np.float32)
+    W = (r.standard_normal((Cc, Cin, 1, 1)) * 0.5).astype(np.float32)
+    b = (r.standard_normal(Cc) * 0.1).astype(np.float32)
+    m = Model("conv_layernorm", [N, Cin, Cc, Hh, Ww], layernorm_reference_layout=reference_layout)
+    m.set(0, W)
+    m.set(1, b)
+    m.input(0, x)
+    m.input(1, target)
+    m.step(0.0, 7)  # zero_grad + forward + backward
+    m.sync()
+    P = orc.ptr
+    y = np.zeros((N, Cc, Hh, Ww), np.float32)
+    orc.call("orc_conv_fwd", P(x), P(W), P(b), P(y), N, Cin, Hh, Ww, Cc, 1, 1, 0, 1)
+    yn, st = np.zeros_like(y), np.zeros(2 * N, np.float32)
+    orc.call("orc_norm_fwd", P(y), P(yn), P(st), N, Cc, Hh * Ww, 1, 1e-5)
+    loss = orc.call("orc_mse_loss", P(yn), P(target), yn.size)
+    dyn, dy = np.zeros_like(y), np.zeros_like(y)
+    orc.call("orc_mse_bwd", P(yn), P(target), None, P(dyn), yn.size)
+    orc.call("orc_norm_bwd", P(yn), P(dyn), P(dy), P(st), N, Cc, Hh * Ww, 1, 1e-5, int(reference_layout))
+    dW = np.zeros_like(W)
+    orc.call("orc_conv_wgrad", P(x), P(dy), P(dW), N, Cin, Hh, Ww, Cc, 1, 1, 0, 1)
+    db = dy.astype(np.float64).sum(axis=(0, 2, 3))
+    assert abs(m.loss - loss) <= 1e-5 * abs(loss)
+    assert_close(m.get(0, 1), dW.reshape(-1), what="conv weight grad", **GRAD)
+    assert_close(m.get(1, 1), db, what="conv bias grad", rtol=1e-4, atol_scale=1e-4,
+                 scale=float(np.abs(dy).max() * N * Hh * Ww))
+    if reference_layout:  # the guard leaves everything past the first N*H*W elements without gradient
+        assert np.all(dy.reshape(-1)[N * Hh * Ww:] == 0)
     m.close()
 
 

@@ -927,10 +927,13 @@ def test_elementwise_and_layout(hip, orc):
 
 # ----------------------------------------- cross-entropy from token-id targets
 @pytest.mark.parametrize("batch,clen,max_clen,cols", [(4, 24, 24, 1000), (3, 10, 13, 10), (2, 7, 9, 9001),
-                                                      (2, 16, 16, 8000), (3, 9, 11, 1500), (2, 5, 5, 4096)])
+                                                      (2, 16, 16, 8000), (3, 9, 11, 1500), (2, 5, 5, 4096),
+                                                      (9, 520, 523, 1000)])
 def test_softmax_xent_keys_matches_dense(hip, orc, batch, clen, max_clen, cols):
     """The id path equals the dense one-hot path bit for bit (loss and
-    gradient), ids outside [0, cols) included, and matches the oracle."""
+    gradient), ids outside [0, cols) included, and matches the oracle.  The
+    4680-row case covers the backward's row walk past its 1024 workgroup rows
+    (rows not a multiple of 1024)."""
     r = rng(batch * 17 + clen + cols)
     rows = batch * clen
     logits = (r.standard_normal((rows, cols), dtype=np.float32) * 3).astype(np.float32)
@@ -1094,3 +1097,33 @@ def test_gemm_act_bwd(hip, orc, kind, M, N, K, beta, acc):
              gdX.ptr, acc, None, 0)
     assert_close(gC.numpy(), c_ref, what="gemm_act_bwd C", **MM)
     assert_close(gdX.numpy(), dx_ref, what=f"gemm_act_bwd d{kind}", **MM)
+
+
+# ------------------------------------------------------------------ arena
+def test_arena_bump_allocation(hip):
+    """mle_arena_*: 256-byte aligned bump allocation inside one device buffer,
+    exhaustion reported as MLE_ERR_OOM, reset reuses the space, and the memory
+    is usable by a kernel (fill, read back)."""
+    L = hip.lib()
+    arena = C.c_void_p()
+    hip.call("mle_arena_create", 1000, C.byref(arena))
+    assert L.mle_arena_capacity(arena) == 1024 and L.mle_arena_used(arena) == 0
+    ptrs = []
+    for nbytes in (4, 300, 256):
+        p = C.c_void_p()
+        hip.call("mle_arena_alloc", arena, nbytes, C.byref(p))
+        ptrs.append(p.value)
+    assert [q - ptrs[0] for q in ptrs] == [0, 256, 768]
+    assert L.mle_arena_used(arena) == 1024
+    p = C.c_void_p()
+    assert L.mle_arena_alloc(arena, 1, C.byref(p)) == -3  # MLE_ERR_OOM
+    assert b"requested" in L.mle_last_error()
+    hip.call("mle_fill", None, ptrs[1], 2.5, 75)
+    out = np.empty(75, np.float32)
+    hip.call("mle_memcpy_d2h", out.ctypes.data, ptrs[1], out.nbytes, None)
+    assert np.all(out == 2.5)
+    hip.call("mle_arena_reset", arena)
+    assert L.mle_arena_used(arena) == 0
+    hip.call("mle_arena_alloc", arena, 1024, C.byref(p))
+    assert p.value == ptrs[0]
+    hip.call("mle_arena_destroy", arena)
