@@ -122,24 +122,149 @@ __global__ __launch_bounds__(SORT_NT) void sort_chunk_kernel(const int32_t* __re
   for (int i = threadIdx.x; i < count; i += SORT_NT) sorted[i] = s[i];
 }
 
-// One workgroup per sorted position; the head of each run of equal keys sums
-// the run's gradient rows in token order and adds scale * sum to the table row.
-__global__ __launch_bounds__(NT) void segment_add_kernel(float* __restrict__ table, const float* __restrict__ grad,
-                                                         const unsigned long long* __restrict__ sorted, int count,
-                                                         int dim, float scale) {
-  const int i = blockIdx.x;
+// Scatter-add by row ranges: workgroup g owns table rows [g R, g R + R) and
+// reads every token's key, keeping the tokens that fall in its rows.  Per chunk
+// of RS_CHUNK tokens, in LDS:
+//   1. a histogram over its R rows, and its exclusive scan
+//   2. placement of each kept token by atomic decrement of its row's end, which
+//      leaves every row's start behind (positions within a row in arrival order)
+//   3. the row's tokens put in token order: each entry goes to its row start
+//      plus its rank, the number of the row's entries with a smaller token index
+//   4. one wave per row sums the row's gradient rows in token order and adds
+//      scale * sum to the table row.
+// No sort buffer and no second launch; the result does not depend on the order
+// the atomics ran in.  Chunks are applied in token order.  Step 3 costs the
+// row's token count per entry, which is small for a batch over a vocabulary.
+constexpr int RS_NT = 1024;
+constexpr int RS_CHUNK = 8192;  // tokens per pass (LDS: two 32 KB lists)
+constexpr int RS_RMAX = 64;     // rows per workgroup
+constexpr int RS_VMAX = 16384;  // vocabularies up to RS_RMAX * 256 rows use this path
+template <bool VEC>
+__global__ __launch_bounds__(RS_NT) void range_scatter_kernel(float* __restrict__ table, const float* __restrict__ grad,
+                                                              const int32_t* __restrict__ keys, int clen, int max_clen,
+                                                              int ntok, int dim, int vocab, int rows_per_wg,
+                                                              float scale) {
+  __shared__ int sperm[RS_CHUNK];  // (row << 16) | chunk-local token, per row in arrival order
+  __shared__ int slist[RS_CHUNK];  // chunk-local tokens, per row in token order
+  __shared__ int sbin[RS_RMAX];
+  __shared__ int sstart[RS_RMAX + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int v_lo = blockIdx.x * rows_per_wg;
+  const int nrows = min(rows_per_wg, vocab - v_lo);
+  if (nrows <= 0) return;
+  constexpr int PER = RS_CHUNK / RS_NT;  // tokens per thread per chunk
+  for (int t0 = 0; t0 < ntok; t0 += RS_CHUNK) {
+    const int count = min(RS_CHUNK, ntok - t0);
+    if (tid < nrows) sbin[tid] = 0;
+    // this thread's tokens t0 + tid + k * RS_NT: their row within the range
+    // (negative keys wrap past nrows), kept for the placement pass
+    unsigned rel[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = tid + k * RS_NT, t = t0 + i;
+      rel[k] = 0xffffffffu;
+      if (i < count) {
+        const size_t at = clen == max_clen ? (size_t)t : (size_t)(t / clen) * max_clen + t % clen;
+        rel[k] = (unsigned)(keys[at] - v_lo);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (rel[k] < (unsigned)nrows) atomicAdd(&sbin[rel[k]], 1);
+    __syncthreads();
+    if (wid == 0) {
+      const int c = lane < nrows ? sbin[lane] : 0;
+      int incl = c;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      if (lane < nrows) {
+        sstart[lane] = incl - c;
+        sbin[lane] = incl;  // the row's end: the placement counts it down
+      }
+      if (lane == nrows - 1) sstart[nrows] = incl;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (rel[k] < (unsigned)nrows) sperm[atomicSub(&sbin[rel[k]], 1) - 1] = (int)(rel[k] << 16) | (tid + k * RS_NT);
+    __syncthreads();
+    const int kept = sstart[nrows];
+    for (int p = tid; p < kept; p += RS_NT) {
+      const int r = sperm[p] >> 16, i = sperm[p] & 0xffff;
+      const int b = sstart[r], e = sstart[r + 1];
+      int rank = 0;
+      for (int q = b; q < e; ++q) rank += (sperm[q] & 0xffff) < i;
+      slist[b + rank] = i;
+    }
+    __syncthreads();
+    for (int r = wid; r < nrows; r += RS_NT / 64) {
+      const int b = sstart[r], e = sstart[r + 1];
+      if (b == e) continue;
+      float* row = table + (size_t)(v_lo + r) * dim;
+      if (VEC) {
+        for (int d = 4 * lane; d < dim; d += 256) {
+          f32x4 v = *reinterpret_cast<const f32x4*>(row + d);  // in flight with the gradient loads
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          for (int j = b; j < e; ++j) {
+            const f32x4 g = *reinterpret_cast<const f32x4*>(grad + (size_t)(t0 + slist[j]) * dim + d);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] += g[c];
+          }
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] += scale * acc[c];
+          *reinterpret_cast<f32x4*>(row + d) = v;
+        }
+      } else {
+        for (int d = lane; d < dim; d += 64) {
+          float acc = 0.f;
+          for (int j = b; j < e; ++j) acc += grad[(size_t)(t0 + slist[j]) * dim + d];
+          row[d] += scale * acc;
+        }
+      }
+    }
+    __syncthreads();  // the next chunk reuses the lists
+  }
+}
+
+// One wave per sorted position; the head of each run of equal keys sums the
+// run's gradient rows in token order and adds scale * sum to the table row.
+// Lanes cover the row in float4s when rows are 16-byte aligned.
+__global__ __launch_bounds__(256) void segment_add_kernel(float* __restrict__ table, const float* __restrict__ grad,
+                                                          const unsigned long long* __restrict__ sorted, int count,
+                                                          int dim, float scale, int vec) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= count) return;
   const unsigned key = (unsigned)(sorted[i] >> 32);
   if (key == 0x7fffffffu) return;
   if (i > 0 && (unsigned)(sorted[i - 1] >> 32) == key) return;
   int end = i + 1;
   while (end < count && (unsigned)(sorted[end] >> 32) == key) ++end;
-  for (int d = threadIdx.x; d < dim; d += NT) {
-    float acc = 0.f;
-    for (int j = i; j < end; ++j) {
-      const unsigned tok = (unsigned)(sorted[j] & 0xffffffffu);
-      acc += grad[(size_t)tok * dim + d];
+  float* row = table + (size_t)key * dim;
+  if (vec) {
+    for (int d = 4 * lane; d < dim; d += 256) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int j = i; j < end; ++j) {
+        const size_t tok = (size_t)(unsigned)(sorted[j] & 0xffffffffu);
+        const f32x4 g = *reinterpret_cast<const f32x4*>(grad + tok * dim + d);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += g[c];
+      }
+      f32x4 r = *reinterpret_cast<const f32x4*>(row + d);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r[c] += scale * acc[c];
+      *reinterpret_cast<f32x4*>(row + d) = r;
     }
-    table[(size_t)key * dim + d] += scale * acc;
+  } else {
+    for (int d = lane; d < dim; d += 64) {
+      float acc = 0.f;
+      for (int j = i; j < end; ++j) acc += grad[(size_t)(unsigned)(sorted[j] & 0xffffffffu) * dim + d];
+      row[d] += scale * acc;
+    }
   }
 }
 
@@ -311,6 +436,19 @@ int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, co
   if (ws_bytes < mle_embed_scatter_ws_bytes(batch, clen))
     return set_error(MLE_ERR_WORKSPACE, "mle_embed_scatter_add: workspace too small");
   hipStream_t s = as_stream(stream);
+  unsigned long long* sorted = static_cast<unsigned long long*>(ws);
+  const int vec = (dim % 4 == 0 && aligned16(table) && aligned16(grad)) ? 1 : 0;
+  if (vocab <= RS_VMAX) {
+    const int rows = (vocab + 511) / 512;  // <= RS_RMAX / 2: about one row per wave, at most 512 workgroups
+    const unsigned grid = (unsigned)((vocab + rows - 1) / rows);
+    if (vec)
+      range_scatter_kernel<true><<<grid, RS_NT, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab, rows,
+                                                        scale);
+    else
+      range_scatter_kernel<false><<<grid, RS_NT, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab,
+                                                         rows, scale);
+    return check_launch("mle_embed_scatter_add");
+  }
   if ((double)vocab * (double)ntok <= (double)(1u << 30) && dim <= 1024) {
     // One row per wave (measured on MI355X: 2, 4 or 8 rows per wave, or 8-16
     // waves per workgroup, are equal or slower -- the key scan bounds it).
@@ -322,13 +460,12 @@ int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, co
                                                                 vocab, scale);
     return check_launch("mle_embed_scatter_add");
   }
-  unsigned long long* sorted = static_cast<unsigned long long*>(ws);
   // Chunks of SORT_CAP tokens are applied in token order, so every table row
   // receives its updates in a fixed order.
   for (long long t0 = 0; t0 < ntok; t0 += SORT_CAP) {
     const int count = (int)((ntok - t0 < SORT_CAP) ? ntok - t0 : SORT_CAP);
     sort_chunk_kernel<<<1, SORT_NT, 0, s>>>(keys, clen, max_clen, vocab, (int)t0, count, sorted);
-    segment_add_kernel<<<count, NT, 0, s>>>(table, grad, sorted, count, dim, scale);
+    segment_add_kernel<<<(count + 3) / 4, 256, 0, s>>>(table, grad, sorted, count, dim, scale, vec);
     int rc = check_launch("mle_embed_scatter_add");
     if (rc) return rc;
   }

@@ -790,21 +790,40 @@ def test_gather_onehot_argmax_scatter(hip, orc):
     assert_close(gtab.numpy(), tab_r, what="scatter add", **EW)
 
 
-@pytest.mark.parametrize("batch,clen,dim,vocab", [(4, 600, 64, 300), (2, 50, 1100, 40), (64, 1024, 8, 20000),
-                                                 (3, 300, 700, 500), (32, 256, 512, 8000)])
-def test_scatter_add_paths(hip, orc, batch, clen, dim, vocab):
-    """Row-centric path (moderate vocab*tokens, dim <= 1024) and sorted path."""
+@pytest.mark.parametrize("batch,clen,dim,vocab,hot", [
+    (4, 600, 64, 300, 0), (2, 50, 1100, 40, 0), (3, 300, 700, 500, 0), (32, 256, 512, 8000, 0),  # counting sort
+    (40, 300, 16, 1000, 0),    # 12000 tokens: two counting-sort chunks, applied in order
+    (4, 100, 33, 50, 0),       # rows not a multiple of 4 floats: scalar segment sums
+    (8, 1024, 32, 100, 1),     # one id on most tokens: a run of ~7000 rows
+    (2, 100, 64, 20000, 0),    # vocabulary beyond the LDS histogram: row-centric path
+    (64, 1024, 8, 20000, 0)])  # ... and beyond that, the bitonic-sort path
+def test_scatter_add_paths(hip, orc, batch, clen, dim, vocab, hot):
+    """Every scatter-add path against the oracle's serial KeyUpdate, ids outside
+    [0, vocab) included, and bit-identical when run twice (fixed summation
+    order per table row)."""
     r = rng(batch + clen + dim)
     keys = r.integers(-2, vocab, (batch, clen)).astype(np.int32)
     keys[:, :5] = 3  # repeated key
+    if hot:
+        keys[r.random((batch, clen)) < 0.85] = 7
+    keys[0, -1] = np.iinfo(np.int32).min
     grad = r.standard_normal((batch, clen, dim), dtype=np.float32)
     table = r.standard_normal((vocab, dim), dtype=np.float32)
     ref = table.copy()
     orc.call("orc_scatter_add", orc.ptr(ref), orc.ptr(grad), orc.ptr(keys), batch, clen, clen, dim, vocab, -0.5)
-    gt, gg, gk = B(hip, table), B(hip, grad), B(hip, keys)
+    gg, gk = B(hip, grad), B(hip, keys)
     ws = hip.Buffer(hip.lib().mle_embed_scatter_ws_bytes(batch, clen))
-    hip.call("mle_embed_scatter_add", None, gt.ptr, gg.ptr, gk.ptr, batch, clen, clen, dim, vocab, -0.5, ws.ptr, ws.nbytes)
-    assert_close(gt.numpy(), ref, what="scatter add", **EW)
+    outs = []
+    for _ in range(2):
+        gt = B(hip, table)
+        hip.call("mle_embed_scatter_add", None, gt.ptr, gg.ptr, gk.ptr, batch, clen, clen, dim, vocab, -0.5, ws.ptr,
+                 ws.nbytes)
+        outs.append(gt.numpy())
+    # rows that many tokens add into are sums of many terms: judged on their size
+    counts = np.bincount(keys[(keys >= 0) & (keys < vocab)].ravel(), minlength=vocab).astype(np.float64)
+    assert_close(outs[0], ref, what="scatter add", rtol=1e-5,
+                 atol_scale=1e-6 * max(1.0, float(np.sqrt(counts.max()))))
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
 @pytest.mark.parametrize("off", [0, 1])  # 1: float offsets, so the scalar path runs
