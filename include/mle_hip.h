@@ -120,6 +120,14 @@ int mle_headify(mle_stream stream, const float* in, float* out, int batch, int h
 /* y = x + PE, PE = sin (even dims) / cos (odd dims) of pos/10000^(2i/cols).
  * MatPEncoding (Engine/kernels.cu:166-185). */
 int mle_matpe(mle_stream stream, const float* x, float* y, int batch, int rows, int cols, int start_idx);
+/* pe[r, c] = sin (even c) / cos (odd c) of (start_idx + r) / 10000^(2 floor(c/2) / cols),
+ * the encoding MatPEncoding adds (Engine/kernels.cu:166-185), evaluated once by
+ * the same double-precision formula as mle_matpe: mle_add_broadcast(x, pe, y)
+ * then gives mle_matpe's y bit for bit. */
+int mle_matpe_table(mle_stream stream, float* pe, int rows, int cols, int start_idx);
+/* y[b, i] = x[b, i] + t[i] for b < batch, i < n (batch <= 65535): the add of
+ * MatPEncoding with its encoding precomputed by mle_matpe_table. */
+int mle_add_broadcast(mle_stream stream, const float* x, const float* t, float* y, int batch, size_t n);
 /* Timestep embedding: cos half then sin half.  PEncoding (Engine/kernels.cu:147-164). */
 int mle_timestep_pe(mle_stream stream, float* y, int t, int dim);
 

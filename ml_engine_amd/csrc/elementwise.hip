@@ -4,6 +4,8 @@
 #include "common.hpp"
 #include <math.h>
 
+#include <algorithm>
+
 using namespace mle;
 
 namespace {
@@ -247,6 +249,36 @@ __global__ __launch_bounds__(256) void matpe_kernel(const float* __restrict__ x,
   }
 }
 
+// The encoding MatPEncoding adds, one value per (position, dim), by the same
+// double-precision formula as matpe_kernel: computed once, then added by
+// add_bcast_kernel for every batch item and every step.
+__global__ __launch_bounds__(256) void pe_table_kernel(float* __restrict__ pe, int rows, int cols, int start) {
+  const size_t plane = (size_t)rows * cols;
+  const size_t g = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= plane) return;
+  const int pos = (int)(g / cols) + start;
+  const int dim = (int)(g % cols);
+  const int i = dim / 2;
+  const double expo = (2.0 * i) / cols;
+  const double freq = 1.0 / pow(10000.0, expo);
+  const double ang = (double)pos * freq;
+  pe[g] = (dim % 2 == 0) ? (float)sin(ang) : (float)cos(ang);
+}
+
+// y[b, i] = x[b, i] + t[i] over batch items of n floats: blockIdx.y is the item.
+template <bool VEC>
+__global__ __launch_bounds__(256) void add_bcast_kernel(const float* __restrict__ x, const float* __restrict__ t,
+                                                        float* __restrict__ y, size_t n) {
+  const size_t off = (size_t)blockIdx.y * n;
+  const size_t stride = (size_t)gridDim.x * 256;
+  if (VEC) {
+    for (size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += stride * 4)
+      st4(y + off, i, ld4(x + off, i) + ld4(t, i));
+  } else {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) y[off + i] = x[off + i] + t[i];
+  }
+}
+
 __global__ void tpe_kernel(float* __restrict__ y, int t, int dim) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= dim) return;
@@ -364,6 +396,25 @@ int mle_matpe(mle_stream stream, const float* x, float* y, int batch, int rows, 
   matpe_kernel<<<stream_grid((size_t)rows * cols, 256, 8192), 256, 0, as_stream(stream)>>>(x, y, batch, rows, cols,
                                                                                          start_idx);
   return check_launch("mle_matpe");
+}
+
+int mle_matpe_table(mle_stream stream, float* pe, int rows, int cols, int start_idx) {
+  MLE_CHECK_ARG(pe && rows > 0 && cols > 0, "mle_matpe_table: bad argument");
+  const size_t plane = (size_t)rows * cols;
+  pe_table_kernel<<<(unsigned)((plane + 255) / 256), 256, 0, as_stream(stream)>>>(pe, rows, cols, start_idx);
+  return check_launch("mle_matpe_table");
+}
+
+int mle_add_broadcast(mle_stream stream, const float* x, const float* t, float* y, int batch, size_t n) {
+  MLE_CHECK_ARG(x && t && y && batch >= 0 && batch <= 65535, "mle_add_broadcast: bad argument");
+  if (n == 0 || batch == 0) return MLE_OK;
+  const bool vec = n % 4 == 0 && aligned16(x) && aligned16(t) && aligned16(y);
+  const size_t items = vec ? n / 4 : n;
+  const unsigned gx = (unsigned)std::min<size_t>((items + 255) / 256, std::max<size_t>(1, 8192 / (size_t)batch));
+  const dim3 grid(gx, (unsigned)batch);
+  if (vec) add_bcast_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(x, t, y, n);
+  else add_bcast_kernel<false><<<grid, 256, 0, as_stream(stream)>>>(x, t, y, n);
+  return check_launch("mle_add_broadcast");
 }
 
 int mle_timestep_pe(mle_stream stream, float* y, int t, int dim) {

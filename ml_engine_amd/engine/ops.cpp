@@ -278,7 +278,13 @@ graph GraphOperations::MatrixPositionalEncoding(const graph& X, const int start_
   auto node = make_node("MatrixSinoSuodalPosEncoding", batch, 1, rows, cols);
   node->inputs = {X};
   NodeBackProp *nd = node.get(), *x = X.get();
-  node->forward = [=]() { check(mle_matpe(S(), x->output, nd->output, batch, rows, cols, start_idx), "MatPE forward"); };
+  // The encoding depends only on (position, dim): tabulated once here, added
+  // to every batch item by the forward.
+  float* pe = static_cast<float*>(mle::alloc_scratch((size_t)rows * cols * sizeof(float)));
+  check(mle_matpe_table(S(), pe, rows, cols, start_idx), "MatPE table");
+  node->forward = [=]() {
+    check(mle_add_broadcast(S(), x->output, pe, nd->output, batch, (size_t)rows * cols), "MatPE forward");
+  };
   node->backward = [=]() { add_grad(x, nd->grad, 1.0, nd->total, "MatPE backward"); };
   std_hooks(node);
   return node;

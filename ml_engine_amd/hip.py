@@ -52,6 +52,8 @@ SIGNATURES: dict[str, tuple] = {
     "mle_headify": (I, [P, P, P, I, I, I, I, I]),
     "mle_matpe": (I, [P, P, P, I, I, I, I]),
     "mle_timestep_pe": (I, [P, P, I, I]),
+    "mle_matpe_table": (I, [P, P, I, I, I]),
+    "mle_add_broadcast": (I, [P, P, P, P, I, SZ]),
     "mle_act_fwd": (I, [P, I, P, P, SZ]),
     "mle_act_bwd": (I, [P, I, P, P, P, SZ, I]),
     "mle_gemm": (I, [P, I, I, I, I, I, F, P, I64, I64, P, I64, I64, F, P, I64, I64, I, P]),

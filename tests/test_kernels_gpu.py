@@ -903,6 +903,16 @@ def test_elementwise_and_layout(hip, orc):
         gxm, gpm = B(hip, xm), hip.Buffer.zeros(xm.shape)
         hip.call("mle_matpe", None, gxm.ptr, gpm.ptr, bt, rw, cl, st)
         assert_close(gpm.numpy(), pm, what=f"matpe {bt}x{rw}x{cl}", rtol=1e-6, atol_scale=1e-7)
+    # the tabulated encoding plus a broadcast add equals mle_matpe bit for bit
+    # (32 x 256 x 512 is the C4 shape; the others are ragged / unaligned)
+    for bt, rw, cl, st, off in ((32, 256, 512, 0, 0), (11, 9, 32, 5, 0), (2, 7, 26, 3, 0), (3, 5, 8, 2, 1)):
+        xm = r.standard_normal(bt * rw * cl + off, dtype=np.float32)
+        gxm, gy1, gy2 = B(hip, xm), hip.Buffer.zeros(xm.size), hip.Buffer.zeros(xm.size)
+        gtab = hip.Buffer.zeros(rw * cl + off)
+        hip.call("mle_matpe", None, gxm.ptr + 4 * off, gy1.ptr + 4 * off, bt, rw, cl, st)
+        hip.call("mle_matpe_table", None, gtab.ptr + 4 * off, rw, cl, st)
+        hip.call("mle_add_broadcast", None, gxm.ptr + 4 * off, gtab.ptr + 4 * off, gy2.ptr + 4 * off, bt, rw * cl)
+        np.testing.assert_array_equal(gy2.numpy().view(np.uint32), gy1.numpy().view(np.uint32))
     tp_r = np.zeros(256, np.float32)
     orc.call("orc_pe", orc.ptr(tp_r), 517, 256)
     gtp = hip.Buffer.zeros(256)
