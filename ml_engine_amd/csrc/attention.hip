@@ -97,10 +97,20 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
 struct Slice {
   int z;
   uint32_t base;  // element offset of (batch item, head) in the [batch][seq][ld] tensors
+  int pair;       // this workgroup's tile pair within the slice
 };
+// The grid is one-dimensional: workgroup L runs on XCD L % 8 (workgroups are
+// dispatched round-robin over the XCDs).  XCD x takes a contiguous range of
+// the (slice, tile pair) items, slice-major, so every workgroup of a slice
+// runs on one XCD and shares its L2 copy of the slice's Q, K, V and dO rows.
+// A bijection on [0, gridDim.x) for any grid size.
+constexpr int kXcds = 8;
 __device__ __forceinline__ Slice slice_of(const AttnArgs& a) {
-  const int z = blockIdx.y, b = z / a.heads, h = z - b * a.heads;
-  return {z, (uint32_t)b * a.seq * a.ld + (uint32_t)h * HD};
+  const int L = blockIdx.x, total = gridDim.x, pairs = a.seq / 64;
+  const int x = L % kXcds, j = L / kXcds, per = total / kXcds, rem = total % kXcds;
+  const int t = x * per + min(x, rem) + j;
+  const int z = t / pairs, b = z / a.heads, h = z - b * a.heads;
+  return {z, (uint32_t)b * a.seq * a.ld + (uint32_t)h * HD, t - z * pairs};
 }
 
 // Work split: every wave owns a 32-row tile of one output (32 keys of the
@@ -114,8 +124,8 @@ __device__ __forceinline__ Slice slice_of(const AttnArgs& a) {
 constexpr int TW = 32;      // rows of a wave's tile
 constexpr int LQ = HD + 4;  // padded LDS row: the 16 rows a b128 read touches sit on distinct banks
 
-__device__ __forceinline__ int tile_of(int w) {
-  return w == 0 ? (int)blockIdx.x : (int)(2 * gridDim.x) - 1 - (int)blockIdx.x;
+__device__ __forceinline__ int tile_of(const AttnArgs& a, const Slice& sl, int w) {
+  return w == 0 ? sl.pair : a.seq / TW - 1 - sl.pair;
 }
 
 // Chunk loop with two alternating register sets (no copies between them,
@@ -156,7 +166,7 @@ __global__ __launch_bounds__(128, 2) void attn_stats_kernel(AttnArgs a) {
   const Slice sl = slice_of(a);
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
-  const int k0 = tile_of(w) * TW;
+  const int k0 = tile_of(a, sl, w) * TW;
   f32x4 ka[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -245,7 +255,7 @@ __global__ __launch_bounds__(128, 2) void attn_fwd_kernel(AttnArgs a) {
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
-  const int q0 = tile_of(w) * TW;
+  const int q0 = tile_of(a, sl, w) * TW;
   f32x4 qB[2][4];
 #pragma unroll
   for (int n = 0; n < 2; ++n)
@@ -322,7 +332,7 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_kv_kernel(AttnArgs a) {
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
   // Key tiles: the heavy (early) one goes with wave 1's light (late) one.
-  const int k0 = tile_of(w) * TW;
+  const int k0 = tile_of(a, sl, w) * TW;
   f32x4 kB[2][4], vB[2][4];
   float mk[2], il[2];
 #pragma unroll
@@ -442,7 +452,7 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
   const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
   const float* DC = a.dcol + (size_t)sl.z * a.seq;
-  const int q0 = tile_of(w) * TW;
+  const int q0 = tile_of(a, sl, w) * TW;
   float* qs = lds[w][0];
   float* os = lds[w][1];
 #pragma unroll
@@ -590,7 +600,7 @@ int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const f
   a.bytes = (uint32_t)((size_t)batch * seq * ld * sizeof(float));
   a.scale = scale;
   hipStream_t s = as_stream(stream);
-  const dim3 grid(seq / (2 * TW), batch * heads);  // two 32-row tiles per workgroup
+  const dim3 grid((unsigned)(seq / (2 * TW) * batch * heads));  // two 32-row tiles per workgroup
   const double flop = 4.0 * batch * heads * (double)seq * seq * HD;  // S and P V, as the reference computes them
   ProbeScope probe("attn_fwd", s, flop, 0.0);
   if (causal) {
@@ -633,7 +643,7 @@ int mle_attention_bwd(mle_stream stream, const float* q, const float* k, const f
   a.acc_k = acc_k != 0;
   a.acc_v = acc_v != 0;
   hipStream_t s = as_stream(stream);
-  const dim3 grid(seq / (2 * TW), batch * heads);  // two 32-row tiles per workgroup
+  const dim3 grid((unsigned)(seq / (2 * TW) * batch * heads));  // two 32-row tiles per workgroup
   const double flop = 8.0 * batch * heads * (double)seq * seq * HD;  // dP, dV, dQ, dK
   ProbeScope probe("attn_bwd", s, flop, 0.0);
   const bool kref = k_reference_grad != 0;
