@@ -880,6 +880,46 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
   }
 }
 
+// 64 C elements per workgroup, one per lane, the four waves taking a quarter
+// of K each and adding their partial sums in wave order: products with a tiny
+// M or K (a Linear layer applied to one row, or the weight gradient of one),
+// where the tile kernels would spend split-K and reduce launches on little
+// work.
+template <int TA, int TB>
+__global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs g) {
+  __shared__ float red[2][4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t z = blockIdx.y;
+  const int64_t idx = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = idx < (int64_t)g.M * g.N;
+  const int m = live ? (int)(idx / g.N) : 0, n = live ? (int)(idx % g.N) : 0;
+  const int kq = (g.K + 3) / 4, k0 = w * kq, k1 = min(g.K, k0 + kq);
+  const float* A = g.A + z * g.sa;
+  const float* B = g.B + z * g.sb;
+  float acc = 0.f, cs = 0.f;
+  if (live) {
+#pragma unroll 8
+    for (int k = k0; k < k1; ++k) {
+      const float a = TA ? A[(int64_t)k * g.lda + m] : A[(int64_t)m * g.lda + k];
+      const float b = TB ? B[(int64_t)n * g.ldb + k] : B[(int64_t)k * g.ldb + n];
+      acc += a * b;
+      cs += b;
+    }
+  }
+  red[0][w][lane] = acc;
+  red[1][w][lane] = cs;
+  __syncthreads();
+  if (w != 0 || !live) return;
+  acc = ((red[0][0][lane] + red[0][1][lane]) + red[0][2][lane]) + red[0][3][lane];
+  float* c = g.C + z * g.sc + (int64_t)m * g.ldc + n;
+  float v = g.alpha * acc;
+  if (g.beta != 0.f) v += g.beta * *c;
+  if (g.bias) v += g.bias[z * g.sbias + n];
+  *c = v;
+  if (g.colsum && m == 0)
+    g.colsum[z * g.scs + n] += ((red[1][0][lane] + red[1][1][lane]) + red[1][2][lane]) + red[1][3][lane];
+}
+
 // Workgroup tile: 128 x 128 unless a side is <= 64 (the 64-wide variants waste
 // nothing there) or the 128 x 128 grid would leave CUs idle and K is too short
 // for split-K to fill them (half-width tiles double the workgroups; measured
@@ -1018,8 +1058,16 @@ struct GemmPlan {
   dim3 grid;
   int vec = 0, which = 0;
   bool cs = false, direct_ok = false, empty = false;
+  bool simple = false;  // gemm_simple_kernel: one thread per C element, no split
   double flop = 0, bytes = 0;
 };
+
+// Products small enough for gemm_simple_kernel: M or K of at most 4 and at
+// most 4 M multiply-adds (one batch level, no sum of terms).
+static bool simple_shape(int M, int N, int K, int batch, int inner, int terms) {
+  return (M <= 4 || K <= 4) && (double)M * N * (double)(K > 0 ? K : 1) * batch <= 4194304.0 && inner == 1 &&
+         terms <= 1 && (double)M * N <= 64.0 * 2147483647.0 && batch <= 65535;
+}
 
 const char* const kFamily[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
 
@@ -1087,6 +1135,12 @@ static int gemm_plan(GemmPlan& P, int trans_a, int trans_b, int M, int N, int K,
       }
     }
   }
+  if (simple_shape(M, N, K, batch, inner, terms)) {
+    g.splits = 1;
+    g.kchunk = K;
+    g.part = g.part_cs = nullptr;
+    P.simple = true;
+  }
   P.g = g;
   P.tile = tile;
   P.grid = dim3((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
@@ -1100,6 +1154,16 @@ static int gemm_plan(GemmPlan& P, int trans_a, int trans_b, int M, int N, int K,
 }
 
 static void gemm_launch_main(hipStream_t s, const GemmPlan& P) {
+  if (P.simple) {
+    const dim3 grid((unsigned)(((int64_t)P.g.M * P.g.N + 63) / 64), P.grid.z);
+    switch (P.which) {
+      case 0: gemm_simple_kernel<0, 0><<<grid, 256, 0, s>>>(P.g); break;
+      case 1: gemm_simple_kernel<0, 1><<<grid, 256, 0, s>>>(P.g); break;
+      case 2: gemm_simple_kernel<1, 0><<<grid, 256, 0, s>>>(P.g); break;
+      default: gemm_simple_kernel<1, 1><<<grid, 256, 0, s>>>(P.g); break;
+    }
+    return;
+  }
   switch (P.which) {
     case 0: launch_tile<0, 0>(s, P.g, P.tile, P.grid, P.vec, P.cs, P.direct_ok); break;
     case 1: launch_tile<0, 1>(s, P.g, P.tile, P.grid, P.vec, P.cs, P.direct_ok); break;
@@ -1124,7 +1188,7 @@ static void gemm_launch_reduce(hipStream_t s, const GemmPlan& P) {
 // per workgroup), or 0 when it would pick another kernel.
 static long long direct_items(const GemmPlan& P) {
   const GemmArgs& g = P.g;
-  if (P.empty || !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0)) return 0;
+  if (P.empty || P.simple || !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0)) return 0;
   const long long items = (long long)P.grid.x * P.grid.y * P.grid.z;
   const bool c_buf = ((double)(g.M - 1) * (double)g.ldc + g.N) * 4.0 < 2147483648.0 - 64;
   const bool stream = g.splits == 1 && g.kterms == 1 && !P.cs && g.K >= 64 && g.K % 64 == 0 &&
@@ -1135,7 +1199,7 @@ static long long direct_items(const GemmPlan& P) {
 // True when launch_tile would run the plan on the persistent kernel.
 static bool uses_stream(const GemmPlan& P) {
   const GemmArgs& g = P.g;
-  if (P.empty || !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0)) return false;
+  if (P.empty || P.simple || !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0)) return false;
   return direct_items(P) == 0;
 }
 

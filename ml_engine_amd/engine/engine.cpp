@@ -181,6 +181,18 @@ void materialize(NodeBackProp* n) {
   zero(n->grad, n->total);
 }
 
+void defer_zero_output(NodeBackProp* n) {
+  if (!n || !n->output || n->total <= 0) return;
+  if (g_lazy_zero) n->output_pending_zero = true;
+  else zero(n->output, n->total);
+}
+
+void materialize_output(NodeBackProp* n) {
+  if (!n || !n->output_pending_zero) return;
+  n->output_pending_zero = false;
+  zero(n->output, n->total);
+}
+
 // ---------------------------------------------------------------------------
 // pending global-norm clip
 namespace {
@@ -338,6 +350,7 @@ void CheckError(const str& reason) {
 
 float ReadValueAt(const graph& X, const int& idx, const bool g) {
   if (g) mle::materialize(X.get());
+  else mle::materialize_output(X.get());
   float out = 0.f;
   check(mle_memcpy_d2h(&out, (g ? X->grad : X->output) + idx, sizeof(float), mle::stream()), "ReadValueAt");
   return out;
@@ -345,6 +358,7 @@ float ReadValueAt(const graph& X, const int& idx, const bool g) {
 
 void WriteValueAt(const graph& X, const float value, const int& idx, const bool g) {
   if (g) mle::materialize(X.get());
+  else mle::materialize_output(X.get());
   check(mle_memcpy_h2d((g ? X->grad : X->output) + idx, &value, sizeof(float), mle::stream()), "WriteValueAt");
 }
 
@@ -492,6 +506,7 @@ void Zerograd(graph X) {
 
 static void print_head(NodeBackProp* X, int type, int rows_max, int cols_max) {
   if (type) mle::materialize(X);
+  else mle::materialize_output(X);
   const int ch = X->dim[1], rows = X->dim[2], cols = X->dim[3];
   const long long n = std::min<long long>(X->total, (long long)ch * rows * cols);
   std::vector<float> cpu(n);
@@ -526,6 +541,7 @@ static void nan_check(NodeBackProp* X, int type) {
   const float* p = type ? X->grad : X->output;
   if (!p || X->total <= 0) return;
   if (type) mle::materialize(X);
+  else mle::materialize_output(X);
   const size_t need = mle_sqnorm_ws_bytes(X->total);
   if (wcap < need) {
     ws = mle::alloc_scratch(need);

@@ -90,6 +90,11 @@ struct ZeroBatch {
 void defer_zero(NodeBackProp* n);
 int accumulate_flag(NodeBackProp* n);
 void materialize(NodeBackProp* n);
+// Lazy zeroing of a loss node's (one-float) output: zero_grad marks it, the
+// loss forward clears the mark when it writes the value, readers call
+// materialize_output first.
+void defer_zero_output(NodeBackProp* n);
+void materialize_output(NodeBackProp* n);
 // Off: defer_zero fills at once (the reference's behaviour; results are the
 // same either way).  On by default.
 void set_lazy_zero(bool on);
@@ -169,6 +174,10 @@ struct NodeBackProp {
   // engine's ops do; for any other backward the dispatcher fills its inputs'
   // marked gradients first).
   bool grad_pending_zero = false;
+  // The same for the output of a loss node, which zero_grad zeroes
+  // (Zerograd("Node", node->output, 1), Engine/engine.cu:2120, 1945) and the
+  // loss forward overwrites: it is filled only if read before that.
+  bool output_pending_zero = false;
   bool lazy_grad_writer = false;
   // Non-null when this node's output is a one-hot matrix of `keys` (additive).
   std::shared_ptr<OneHotSource> onehot;

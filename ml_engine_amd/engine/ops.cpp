@@ -382,6 +382,7 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
   node->forward = [=]() {
     if (calculate_loss || !last) {
       check(mle_mse_fwd(S(), pr->output, tg->output, n, nd->output, ws, ws_bytes), "Scalar MSE in MSE forward");
+      nd->output_pending_zero = false;  // written whole
       if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "MSE loss");
     }
   };
@@ -390,7 +391,7 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
           "deriv MSE");
   };
   node->free = [=]() { nd->clear(); };
-  node->zero_grad = [=]() { mle::zero(nd->output, 1); };
+  node->zero_grad = [=]() { mle::defer_zero_output(nd); };
   return node;
 }
 
@@ -445,6 +446,7 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
       else
         check(mle_softmax_xent_fwd(S(), pr->output, tg->output, probs, rows, d, nd->output, ws, ws_bytes),
               "SoftMaxCrossEntropy");
+      nd->output_pending_zero = false;  // written whole
       if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "CE loss");
     }
   };
@@ -464,7 +466,7 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
     if (stats) mle::release(stats, 2 * (size_t)rows, false);
     if (rowpart) mle::release(rowpart, (size_t)rows * ldp, false);
   };
-  node->zero_grad = [=]() { mle::zero(nd->output, 1); };
+  node->zero_grad = [=]() { mle::defer_zero_output(nd); };
   return node;
 }
 

@@ -65,6 +65,10 @@ GEMM_CASES = [
     (1, 0, 2500, 4096, 128, 1),
     (1, 1, 2100, 2052, 64, 2),
     (0, 0, 1000, 1000, 256, 9),
+    # one-thread-per-element kernel (M or K of at most 4): a Linear on one
+    # row (time embedding), its input and weight gradients, odd sizes, batches
+    (0, 0, 1, 128, 256, 1), (0, 1, 1, 256, 128, 1), (1, 0, 256, 128, 1, 1),
+    (1, 1, 3, 37, 53, 2), (0, 0, 70, 33, 3, 3), (0, 1, 4, 1000, 999, 1),
 ]
 
 
@@ -1156,3 +1160,30 @@ def test_arena_bump_allocation(hip):
     hip.call("mle_arena_alloc", arena, 1024, C.byref(p))
     assert p.value == ptrs[0]
     hip.call("mle_arena_destroy", arena)
+
+
+def test_gemm_simple_fusions(hip, orc):
+    """The one-thread-per-element path with the Linear fusions: bias in the
+    epilogue (the forward on one row) and the column sum of dY (db) in the
+    weight-gradient product with K = 1, against the oracle."""
+    r = rng(404)
+    x = r.standard_normal((1, 256), dtype=np.float32)
+    W = r.standard_normal((256, 128), dtype=np.float32)
+    b = r.standard_normal(128, dtype=np.float32)
+    y_ref = np.zeros((1, 128), np.float32)
+    orc.call("orc_bcmm", 0, orc.ptr(x), orc.ptr(W), orc.ptr(y_ref), 1, 1, 1, 256, 128, 0, 3, 0, 3, 1.0)
+    y_ref += b
+    gx, gW, gb, gy = B(hip, x), B(hip, W), B(hip, b), hip.Buffer.zeros((1, 128))
+    hip.call("mle_gemm_ex", None, 0, 0, 1, 128, 256, 1.0, gx.ptr, 256, 0, gW.ptr, 128, 0, 0.0, gy.ptr, 128, 0, 1, None,
+             gb.ptr, None, 0)
+    assert_close(gy.numpy(), y_ref, what="one-row Linear forward", **MM)
+    dy = r.standard_normal((1, 128), dtype=np.float32)
+    dW0 = r.standard_normal((256, 128), dtype=np.float32)
+    db0 = r.standard_normal(128, dtype=np.float32)
+    dW_ref, db_ref = dW0.copy(), db0.copy()
+    orc.call("orc_bcmm", 2, orc.ptr(x), orc.ptr(dy), orc.ptr(dW_ref), 1, 1, 256, 1, 128, 1, 3, 3, 0, 1.0)
+    orc.call("orc_bcompress", orc.ptr(dy), orc.ptr(db_ref), 1, 128, 1.0)
+    gdy, gdW, gdb = B(hip, dy), B(hip, dW0), B(hip, db0)
+    hip.call("mle_gemm", None, 1, 0, 256, 128, 1, 1.0, gx.ptr, 256, 0, gdy.ptr, 128, 0, 1.0, gdW.ptr, 128, 0, 1, gdb.ptr)
+    assert_close(gdW.numpy(), dW_ref, what="one-row weight gradient", **MM)
+    assert_close(gdb.numpy(), db_ref, what="one-row bias gradient", **MM)
