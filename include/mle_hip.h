@@ -66,6 +66,14 @@ int mle_device_free(void* ptr);
 int mle_memcpy_h2d(void* dst, const void* src, size_t bytes, mle_stream stream);
 /* Synchronous device-to-host copy (ReadValueAt, Engine/engine.cu:3-9). */
 int mle_memcpy_d2h(void* dst, const void* src, size_t bytes, mle_stream stream);
+/* Reads one float from device memory once the work queued on `stream` before
+ * it has run: the loss read-back of the loss nodes' forward (cudaMemcpy(&loss,
+ * node->output, ...), Engine/engine.cu:1656,1700,1935,2046,2098).  A one-thread
+ * kernel publishes the value and a sequence number into pinned host memory and
+ * the caller spins on the sequence number, so it resumes as soon as the value
+ * lands instead of waking from a blocking wait.  Calls on one device are
+ * serialised. */
+int mle_read_scalar(mle_stream stream, const float* src, float* dst);
 int mle_memcpy_d2d(void* dst, const void* src, size_t bytes, mle_stream stream);
 
 int mle_stream_create(mle_stream* stream);

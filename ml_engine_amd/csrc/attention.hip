@@ -604,11 +604,11 @@ int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const f
   const double flop = 4.0 * batch * heads * (double)seq * seq * HD;  // S and P V, as the reference computes them
   ProbeScope probe("attn_fwd", s, flop, 0.0);
   if (causal) {
-    attn_stats_kernel<true><<<grid, 128, 0, s>>>(a);
-    attn_fwd_kernel<true><<<grid, 128, 0, s>>>(a);
+    mle::launch(attn_stats_kernel<true>, grid, 128, 0, s, a);
+    mle::launch(attn_fwd_kernel<true>, grid, 128, 0, s, a);
   } else {
-    attn_stats_kernel<false><<<grid, 128, 0, s>>>(a);
-    attn_fwd_kernel<false><<<grid, 128, 0, s>>>(a);
+    mle::launch(attn_stats_kernel<false>, grid, 128, 0, s, a);
+    mle::launch(attn_fwd_kernel<false>, grid, 128, 0, s, a);
   }
   return check_launch("mle_attention_fwd");
 }
@@ -649,19 +649,19 @@ int mle_attention_bwd(mle_stream stream, const float* q, const float* k, const f
   const bool kref = k_reference_grad != 0;
   if (causal) {
     if (kref) {
-      attn_bwd_kv_kernel<true, false><<<grid, 128, 0, s>>>(a);
-      attn_bwd_q_kernel<true, true><<<grid, 128, 0, s>>>(a);
+      mle::launch(attn_bwd_kv_kernel<true, false>, grid, 128, 0, s, a);
+      mle::launch(attn_bwd_q_kernel<true, true>, grid, 128, 0, s, a);
     } else {
-      attn_bwd_kv_kernel<true, true><<<grid, 128, 0, s>>>(a);
-      attn_bwd_q_kernel<true, false><<<grid, 128, 0, s>>>(a);
+      mle::launch(attn_bwd_kv_kernel<true, true>, grid, 128, 0, s, a);
+      mle::launch(attn_bwd_q_kernel<true, false>, grid, 128, 0, s, a);
     }
   } else {
     if (kref) {
-      attn_bwd_kv_kernel<false, false><<<grid, 128, 0, s>>>(a);
-      attn_bwd_q_kernel<false, true><<<grid, 128, 0, s>>>(a);
+      mle::launch(attn_bwd_kv_kernel<false, false>, grid, 128, 0, s, a);
+      mle::launch(attn_bwd_q_kernel<false, true>, grid, 128, 0, s, a);
     } else {
-      attn_bwd_kv_kernel<false, true><<<grid, 128, 0, s>>>(a);
-      attn_bwd_q_kernel<false, false><<<grid, 128, 0, s>>>(a);
+      mle::launch(attn_bwd_kv_kernel<false, true>, grid, 128, 0, s, a);
+      mle::launch(attn_bwd_q_kernel<false, false>, grid, 128, 0, s, a);
     }
   }
   return check_launch("mle_attention_bwd");

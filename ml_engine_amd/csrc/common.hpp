@@ -1,6 +1,7 @@
 // Shared helpers for the gfx950 kernels behind include/mle_hip.h.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stddef.h>
 #include <string>
@@ -18,10 +19,13 @@ int check_launch(const char* kernel);
 
 // ---- launch probe ---------------------------------------------------------
 // Returns true when `kernel` is the armed probe family; then the caller wraps
-// its launch in probe_begin / probe_end.
+// its launches in probe_begin / probe_end (ProbeScope), and each kernel it
+// launches with mle::launch carries a start/stop event pair in its dispatch.
 bool probe_armed(const char* kernel);
 void probe_begin(hipStream_t s);
 void probe_end(hipStream_t s, double flop, double bytes);
+// Inside a probed call on this thread: two events for the next launch.
+bool probe_events(hipEvent_t* a, hipEvent_t* b);
 
 struct ProbeScope {
   bool on;
@@ -34,6 +38,17 @@ struct ProbeScope {
     if (on) probe_end(s, flop, bytes);
   }
 };
+
+// Launches k<<<grid, block, shmem, s>>>(args...).  Inside a probed call the
+// kernel is launched with hipExtLaunchKernelGGL and the probe's events, which
+// time the kernel itself: no marker packet joins the stream, so the stream
+// runs as it does unprobed.
+template <typename... KArgs, typename... Args>
+inline void launch(void (*k)(KArgs...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, Args... args) {
+  hipEvent_t a, b;
+  if (probe_events(&a, &b)) hipExtLaunchKernelGGL(k, grid, block, shmem, s, a, b, 0u, args...);
+  else k<<<grid, block, shmem, s>>>(args...);
+}
 
 // Per-device set-up of the allocation-free optimizer entry point (optim.hip);
 // mle_init calls it with the device current.

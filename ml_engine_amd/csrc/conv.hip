@@ -223,9 +223,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 
 void launch_split_reduce(hipStream_t s, const float* part, int splits, size_t mn, float* out) {
   if (mn % 4 == 0 && aligned16(part) && aligned16(out))
-    split_reduce_kernel<true><<<(unsigned)((mn / 4 + 63) / 64), 256, 0, s>>>(part, splits, mn, out);
+    mle::launch(split_reduce_kernel<true>, (unsigned)((mn / 4 + 63) / 64), 256, 0, s, part, splits, mn, out);
   else
-    split_reduce_kernel<false><<<(unsigned)((mn + 63) / 64), 256, 0, s>>>(part, splits, mn, out);
+    mle::launch(split_reduce_kernel<false>, (unsigned)((mn + 63) / 64), 256, 0, s, part, splits, mn, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -1030,13 +1030,13 @@ constexpr int kC3U = 2, kC3D = 4;  // channel quads per stage, stages in flight
 template <bool DG, bool HALO, int WM>
 void launch_conv3(hipStream_t s, const Conv3Args& c) {
   constexpr int KS = WM == 1 ? 2 : 1;
-  conv3_direct_kernel<DG, HALO, WM, 2, KS, kC3U, kC3D><<<c.tiles, 64 * WM * 2 * KS, 0, s>>>(c);
+  mle::launch(conv3_direct_kernel<DG, HALO, WM, 2, KS, kC3U, kC3D>, c.tiles, 64 * WM * 2 * KS, 0, s, c);
 }
 
 template <bool DG, int WM>
 void launch_conv1(hipStream_t s, const Conv3Args& c) {
   constexpr int KS = WM == 1 ? 2 : 1;
-  conv1_direct_kernel<DG, WM, 2, KS, 4><<<c.tiles, 64 * WM * 2 * KS, 0, s>>>(c);
+  mle::launch(conv1_direct_kernel<DG, WM, 2, KS, 4>, c.tiles, 64 * WM * 2 * KS, 0, s, c);
 }
 
 // Register-direct path for a 3 x 3 (stride 1, pad 1) or 1 x 1 (stride 1,
@@ -1096,8 +1096,8 @@ bool conv_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, co
 template <int KIND>
 void launch_fast(hipStream_t s, const FastConv& c, int kh, int splits) {
   dim3 grid((c.N + BN - 1) / BN, (c.M + BM - 1) / BM, splits);
-  if (kh == 3) conv_fast_kernel<KIND, 3, 3><<<grid, NT, 0, s>>>(c);
-  else conv_fast_kernel<KIND, 1, 1><<<grid, NT, 0, s>>>(c);
+  if (kh == 3) mle::launch(conv_fast_kernel<KIND, 3, 3>, grid, NT, 0, s, c);
+  else mle::launch(conv_fast_kernel<KIND, 1, 1>, grid, NT, 0, s, c);
 }
 
 int geom(int n, int cin, int h, int w, int cout, int kh, int kw, int pad, int stride, ConvGeom& g) {
@@ -1217,7 +1217,7 @@ int mle_conv2d_fwd(mle_stream stream, const float* x, const float* w, const floa
     launch_fast<CONV_FWD>(s, c, kh, 1);
   } else {
     dim3 grid((op.N + BN - 1) / BN, (op.M + BM - 1) / BM, 1);
-    igemm_kernel<FwdOps, false><<<grid, NT, 0, s>>>(op, op.K);
+    mle::launch(igemm_kernel<FwdOps, false>, grid, NT, 0, s, op, op.K);
   }
   return check_launch("mle_conv2d_fwd");
 }
@@ -1241,7 +1241,7 @@ int mle_conv2d_dgrad(mle_stream stream, const float* dy, const float* w, float* 
     launch_fast<CONV_DGRAD>(s, c, kh, 1);
   } else {
     dim3 grid((op.N + BN - 1) / BN, (op.M + BM - 1) / BM, 1);
-    igemm_kernel<DgradOps, false><<<grid, NT, 0, s>>>(op, op.K);
+    mle::launch(igemm_kernel<DgradOps, false>, grid, NT, 0, s, op, op.K);
   }
   return check_launch("mle_conv2d_dgrad");
 }
@@ -1278,11 +1278,11 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
     {
       ProbeScope probe("conv_wgrad", s, flop, 0.0);
       if (taps == 9) {
-        if (cout <= 64) conv3_wgrad_kernel<1, 4><<<c3.items, 256, 0, s>>>(c3);
-        else conv3_wgrad_kernel<2, 4><<<c3.items, 256, 0, s>>>(c3);
+        if (cout <= 64) mle::launch(conv3_wgrad_kernel<1, 4>, c3.items, 256, 0, s, c3);
+        else mle::launch(conv3_wgrad_kernel<2, 4>, c3.items, 256, 0, s, c3);
       } else {
-        if (cout <= 64) conv1_wgrad_kernel<1, 4><<<c3.items, 256, 0, s>>>(c3);
-        else conv1_wgrad_kernel<2, 4><<<c3.items, 256, 0, s>>>(c3);
+        if (cout <= 64) mle::launch(conv1_wgrad_kernel<1, 4>, c3.items, 256, 0, s, c3);
+        else mle::launch(conv1_wgrad_kernel<2, 4>, c3.items, 256, 0, s, c3);
       }
     }
     if (splits > 1) {
@@ -1305,7 +1305,7 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
       launch_fast<CONV_WGRAD>(s, c, kh, splits);
     } else {
       dim3 grid((op.N + BN - 1) / BN, (op.M + BM - 1) / BM, splits);
-      igemm_kernel<WgradOps, true><<<grid, NT, 0, s>>>(op, kchunk);
+      mle::launch(igemm_kernel<WgradOps, true>, grid, NT, 0, s, op, kchunk);
     }
   }
   const size_t mn = (size_t)op.M * op.N;

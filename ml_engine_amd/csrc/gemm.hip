@@ -979,14 +979,14 @@ int choose_splits(int M, int N, int K, int batch, int& kchunk) {
 template <int TA, int TB, int WM, int WN, int KD>
 void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, int vec, bool cs) {
   if (vec == 2) {
-    if (cs) gemm_kernel<TA, TB, 2, true, WM, WN, KD><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 2, false, WM, WN, KD><<<grid, NT, 0, s>>>(g);
+    if (cs) mle::launch(gemm_kernel<TA, TB, 2, true, WM, WN, KD>, grid, NT, 0, s, g);
+    else mle::launch(gemm_kernel<TA, TB, 2, false, WM, WN, KD>, grid, NT, 0, s, g);
   } else if (vec == 1) {
-    if (cs) gemm_kernel<TA, TB, 1, true, WM, WN, KD><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 1, false, WM, WN, KD><<<grid, NT, 0, s>>>(g);
+    if (cs) mle::launch(gemm_kernel<TA, TB, 1, true, WM, WN, KD>, grid, NT, 0, s, g);
+    else mle::launch(gemm_kernel<TA, TB, 1, false, WM, WN, KD>, grid, NT, 0, s, g);
   } else {
-    if (cs) gemm_kernel<TA, TB, 0, true, WM, WN, KD><<<grid, NT, 0, s>>>(g);
-    else gemm_kernel<TA, TB, 0, false, WM, WN, KD><<<grid, NT, 0, s>>>(g);
+    if (cs) mle::launch(gemm_kernel<TA, TB, 0, true, WM, WN, KD>, grid, NT, 0, s, g);
+    else mle::launch(gemm_kernel<TA, TB, 0, false, WM, WN, KD>, grid, NT, 0, s, g);
   }
 }
 
@@ -997,9 +997,9 @@ void launch_t(hipStream_t s, const GemmArgs& g, dim3 grid, int vec, bool cs) {
 // shader clock it sustains (~2.15 GHz under load), not by load latency.
 template <int TA, int TB>
 void launch_direct(hipStream_t s, const GemmArgs& g, dim3 grid, bool cs) {
-  if (g.kterms > 1) gemm_direct_kernel<TA, TB, false, 16, 3, 2, true><<<grid, NT, 0, s>>>(g);
-  else if (cs) gemm_direct_kernel<TA, TB, true, 16, 3, 2><<<grid, NT, 0, s>>>(g);
-  else gemm_direct_kernel<TA, TB, false, 16, 3, 2><<<grid, NT, 0, s>>>(g);
+  if (g.kterms > 1) mle::launch(gemm_direct_kernel<TA, TB, false, 16, 3, 2, true>, grid, NT, 0, s, g);
+  else if (cs) mle::launch(gemm_direct_kernel<TA, TB, true, 16, 3, 2>, grid, NT, 0, s, g);
+  else mle::launch(gemm_direct_kernel<TA, TB, false, 16, 3, 2>, grid, NT, 0, s, g);
 }
 
 // Compute units of the current device (queried once per device).
@@ -1027,10 +1027,11 @@ void launch_tile(hipStream_t s, const GemmArgs& g, Tile t, dim3 grid, int vec, b
     if (g.splits == 1 && g.kterms == 1 && !cs && g.K >= 64 && g.K % 64 == 0 && items > 2 * ncu &&
         items < (1LL << 30) && c_buf) {
       if (g.rowpart)
-        gemm_stream_kernel<TA, TB, 16, 4, kEpiRowstats>
-            <<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
+        mle::launch(gemm_stream_kernel<TA, TB, 16, 4, kEpiRowstats>, dim3((unsigned)(2 * ncu)), NT, 0, s, g,
+                    (int)grid.x, (int)grid.y, (int)items);
       else
-        gemm_stream_kernel<TA, TB, 16, 4><<<dim3((unsigned)(2 * ncu)), NT, 0, s>>>(g, (int)grid.x, (int)grid.y, (int)items);
+        mle::launch(gemm_stream_kernel<TA, TB, 16, 4>, dim3((unsigned)(2 * ncu)), NT, 0, s, g, (int)grid.x,
+                    (int)grid.y, (int)items);
     } else {
       launch_direct<TA, TB>(s, g, grid, cs);
     }
@@ -1157,10 +1158,10 @@ static void gemm_launch_main(hipStream_t s, const GemmPlan& P) {
   if (P.simple) {
     const dim3 grid((unsigned)(((int64_t)P.g.M * P.g.N + 63) / 64), P.grid.z);
     switch (P.which) {
-      case 0: gemm_simple_kernel<0, 0><<<grid, 256, 0, s>>>(P.g); break;
-      case 1: gemm_simple_kernel<0, 1><<<grid, 256, 0, s>>>(P.g); break;
-      case 2: gemm_simple_kernel<1, 0><<<grid, 256, 0, s>>>(P.g); break;
-      default: gemm_simple_kernel<1, 1><<<grid, 256, 0, s>>>(P.g); break;
+      case 0: mle::launch(gemm_simple_kernel<0, 0>, grid, 256, 0, s, P.g); break;
+      case 1: mle::launch(gemm_simple_kernel<0, 1>, grid, 256, 0, s, P.g); break;
+      case 2: mle::launch(gemm_simple_kernel<1, 0>, grid, 256, 0, s, P.g); break;
+      default: mle::launch(gemm_simple_kernel<1, 1>, grid, 256, 0, s, P.g); break;
     }
     return;
   }
@@ -1180,8 +1181,8 @@ static void gemm_launch_reduce(hipStream_t s, const GemmPlan& P) {
   const int w = rv ? 4 : 1;
   const int batch = (int)P.grid.z / g.splits;
   dim3 rgrid((unsigned)((g.N / w + 255) / 256), (unsigned)std::min(g.M, 65535), (unsigned)batch);
-  if (rv) split_reduce_kernel<true><<<rgrid, 256, 0, s>>>(g);
-  else split_reduce_kernel<false><<<rgrid, 256, 0, s>>>(g);
+  if (rv) mle::launch(split_reduce_kernel<true>, rgrid, 256, 0, s, g);
+  else mle::launch(split_reduce_kernel<false>, rgrid, 256, 0, s, g);
 }
 
 // Work items of a plan that launch_tile would run on gemm_direct_kernel (one
@@ -1210,9 +1211,9 @@ static void launch_stream_act(hipStream_t s, const GemmPlan& P, int kind) {
   const dim3 grid((unsigned)(2 * cu_count()));
   const int gx = (int)P.grid.x, gy = (int)P.grid.y, items = (int)((long long)P.grid.x * P.grid.y * P.grid.z);
   switch (kind) {
-    case MLE_RELU: gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_RELU><<<grid, NT, 0, s>>>(P.g, gx, gy, items); break;
-    case MLE_GELU: gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_GELU><<<grid, NT, 0, s>>>(P.g, gx, gy, items); break;
-    default: gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_SILU><<<grid, NT, 0, s>>>(P.g, gx, gy, items); break;
+    case MLE_RELU: mle::launch(gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_RELU>, grid, NT, 0, s, P.g, gx, gy, items); break;
+    case MLE_GELU: mle::launch(gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_GELU>, grid, NT, 0, s, P.g, gx, gy, items); break;
+    default: mle::launch(gemm_stream_kernel<TA, TB, 16, 4, EPI, MLE_SILU>, grid, NT, 0, s, P.g, gx, gy, items); break;
   }
 }
 
@@ -1290,7 +1291,7 @@ int mle_gemm_rowstats(mle_stream stream, int trans_a, int trans_b, int M, int N,
   if (!fused) {
     const int64_t waves = (int64_t)M * ((N + 63) / 64);
     MLE_CHECK_ARG((waves + 3) / 4 <= 2147483647LL, "mle_gemm_rowstats: too many rows");
-    rowstats_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(C, ldc, M, N, rowpart, ldp);
+    mle::launch(rowstats_kernel, (unsigned)((waves + 3) / 4), 256, 0, s, C, ldc, M, N, rowpart, ldp);
   }
   return check_launch("mle_gemm_rowstats");
 }
@@ -1387,10 +1388,11 @@ int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers, con
     const bool t0 = P0.g.kterms > 1;
     {
       ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
-      if (t0 && P1.cs) gemm_pair_kernel<0, 1, false, true, 1, 0, true, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
-      else if (t0) gemm_pair_kernel<0, 1, false, true, 1, 0, false, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
-      else if (P1.cs) gemm_pair_kernel<0, 1, false, false, 1, 0, true, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
-      else gemm_pair_kernel<0, 1, false, false, 1, 0, false, false><<<grid, NT, 0, s>>>(P0.g, P1.g, pg);
+      auto k = t0 ? (P1.cs ? gemm_pair_kernel<0, 1, false, true, 1, 0, true, false>
+                           : gemm_pair_kernel<0, 1, false, true, 1, 0, false, false>)
+                  : (P1.cs ? gemm_pair_kernel<0, 1, false, false, 1, 0, true, false>
+                           : gemm_pair_kernel<0, 1, false, false, 1, 0, false, false>);
+      mle::launch(k, grid, NT, 0, s, P0.g, P1.g, pg);
     }
     gemm_launch_reduce(s, P1);
     return check_launch("gemm_pair");

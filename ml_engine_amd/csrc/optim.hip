@@ -189,9 +189,9 @@ template <bool ADAMW, bool CLIP>
 void launch_adam(hipStream_t s, const AdamArgs& a, bool vec) {
   if (vec) {
     const size_t blocks = std::max<size_t>(1, (a.n / 4 + ADAM_NT - 1) / ADAM_NT);
-    adam_vec_kernel<ADAMW, CLIP><<<(unsigned)blocks, ADAM_NT, 0, s>>>(a);
+    mle::launch(adam_vec_kernel<ADAMW, CLIP>, (unsigned)blocks, ADAM_NT, 0, s, a);
   } else {
-    adam_kernel<ADAMW, CLIP><<<stream_grid(a.n, NT, 8192), NT, 0, s>>>(a);
+    mle::launch(adam_kernel<ADAMW, CLIP>, stream_grid(a.n, NT, 8192), NT, 0, s, a);
   }
 }
 
@@ -253,16 +253,16 @@ int mle_grad_sqnorm(mle_stream stream, const float* g, size_t n, double* accum, 
   double* part = static_cast<double*>(ws);
   {
     ProbeScope probe("sqnorm", s, 0.0, 4.0 * (double)n);
-    if (aligned16(g)) sqnorm_partial<true><<<grid, NT, 0, s>>>(g, n, part, nonfinite);
-    else sqnorm_partial<false><<<grid, NT, 0, s>>>(g, n, part, nonfinite);
+    if (aligned16(g)) mle::launch(sqnorm_partial<true>, grid, NT, 0, s, g, n, part, nonfinite);
+    else mle::launch(sqnorm_partial<false>, grid, NT, 0, s, g, n, part, nonfinite);
   }
-  sqnorm_finish<<<1, FIN_NT, 0, s>>>(part, grid, accum, 1, 0, 1.0, nullptr);
+  mle::launch(sqnorm_finish, 1, FIN_NT, 0, s, part, grid, accum, 1, 0, 1.0, nullptr);
   return check_launch("mle_grad_sqnorm");
 }
 
 int mle_sqrt_scale(mle_stream stream, double* s, double scale) {
   MLE_CHECK_ARG(s, "mle_sqrt_scale: null pointer");
-  sqrt_scale_kernel<<<1, 1, 0, as_stream(stream)>>>(s, scale);
+  mle::launch(sqrt_scale_kernel, 1, 1, 0, as_stream(stream), s, scale);
   return check_launch("mle_sqrt_scale");
 }
 
@@ -294,11 +294,11 @@ int adamw_clip(hipStream_t s, float* p, const float* g, float* m, float* v, size
     const unsigned grid = sqnorm_grid(n);
     {
       ProbeScope probe("sqnorm", s, 0.0, 4.0 * (double)n);
-      if (aligned16(g)) sqnorm_partial<true><<<grid, NT, 0, s>>>(g, n, part, nullptr);
-      else sqnorm_partial<false><<<grid, NT, 0, s>>>(g, n, part, nullptr);
+      if (aligned16(g)) mle::launch(sqnorm_partial<true>, grid, NT, 0, s, g, n, part, nullptr);
+      else mle::launch(sqnorm_partial<false>, grid, NT, 0, s, g, n, part, nullptr);
     }
     // s = Sqrt_Scale(sum g^2) computed from zero, so nothing is cleared beforehand.
-    sqnorm_finish<<<1, FIN_NT, 0, s>>>(part, grid, sdev, 0, 1, clip_scale, norm_out);
+    mle::launch(sqnorm_finish, 1, FIN_NT, 0, s, part, grid, sdev, 0, 1, clip_scale, norm_out);
     int rc = check_launch("adamw_clip: norm");
     if (rc) return rc;
     clip = sdev;

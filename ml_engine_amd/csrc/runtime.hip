@@ -40,15 +40,20 @@ int check_launch(const char* kernel) {
 }
 
 // ---- probe ---------------------------------------------------------------
+// One record per probed call: the start/stop event pair of every kernel the
+// call launched (each pair rides in its kernel's dispatch packet, so the
+// measurement puts nothing else on the stream), and the call's flop and
+// bytes.
 struct ProbeRec {
-  hipEvent_t a, b;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
   double flop, bytes;
 };
 static std::mutex g_probe_mu;
 static std::string g_probe_kernel;
 static std::vector<ProbeRec> g_probe_recs;
 static std::vector<hipEvent_t> g_event_pool;
-static hipEvent_t g_pending_begin = nullptr;
+// The call being probed on this thread (launches made inside it take events).
+static thread_local ProbeRec* t_open = nullptr;
 
 static hipEvent_t take_event() {
   if (!g_event_pool.empty()) {
@@ -57,7 +62,9 @@ static hipEvent_t take_event() {
     return e;
   }
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  // Agent-scope completion only: a system-scope fence at each record would
+  // write L2 back and stall the stream around every probed kernel.
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
 }
 
@@ -71,20 +78,53 @@ bool probe_armed(const char* kernel) {
   return !g_probe_kernel.empty() && g_probe_kernel == kernel;
 }
 
-void probe_begin(hipStream_t s) {
-  std::lock_guard<std::mutex> lk(g_probe_mu);
-  g_pending_begin = take_event();
-  if (g_pending_begin) (void)hipEventRecord(g_pending_begin, s);
+void probe_begin(hipStream_t) {
+  delete t_open;
+  t_open = new ProbeRec{{}, 0.0, 0.0};
 }
 
-void probe_end(hipStream_t s, double flop, double bytes) {
+bool probe_events(hipEvent_t* a, hipEvent_t* b) {
+  *a = *b = nullptr;
+  if (!t_open) return false;
   std::lock_guard<std::mutex> lk(g_probe_mu);
-  if (!g_pending_begin) return;
-  hipEvent_t e = take_event();
-  if (!e) return;
-  (void)hipEventRecord(e, s);
-  g_probe_recs.push_back({g_pending_begin, e, flop, bytes});
-  g_pending_begin = nullptr;
+  hipEvent_t x = take_event();
+  hipEvent_t y = x ? take_event() : nullptr;
+  if (!y) {
+    if (x) g_event_pool.push_back(x);
+    return false;
+  }
+  t_open->ev.push_back({x, y});
+  *a = x;
+  *b = y;
+  return true;
+}
+
+void probe_end(hipStream_t, double flop, double bytes) {
+  ProbeRec* r = t_open;
+  t_open = nullptr;
+  if (!r) return;
+  r->flop = flop;
+  r->bytes = bytes;
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  if (!r->ev.empty()) g_probe_recs.push_back(std::move(*r));
+  delete r;
+}
+
+// ---- scalar read-back ------------------------------------------------------
+// One pinned, host-coherent slot per device: the value's bits and the
+// sequence number of the read that wrote them.
+struct ScalarSlot {
+  unsigned seq;
+  unsigned bits;
+};
+constexpr int kMaxDevices = 64;
+static std::mutex g_slot_mu[kMaxDevices];
+static ScalarSlot* g_slot[kMaxDevices] = {};
+static unsigned g_slot_seq[kMaxDevices] = {};
+
+__global__ void publish_scalar_kernel(const unsigned* src, ScalarSlot* slot, unsigned seq) {
+  __hip_atomic_store(&slot->bits, *src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(&slot->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 }  // namespace mle
@@ -145,6 +185,43 @@ int mle_memcpy_d2h(void* dst, const void* src, size_t bytes, mle_stream stream) 
   if (bytes == 0) return MLE_OK;
   MLE_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
   MLE_HIP(hipStreamSynchronize(as_stream(stream)));
+  return MLE_OK;
+}
+
+int mle_read_scalar(mle_stream stream, const float* src, float* dst) {
+  MLE_CHECK_ARG(src != nullptr && dst != nullptr, "mle_read_scalar: null pointer");
+  int dev = 0;
+  MLE_HIP(hipGetDevice(&dev));
+  MLE_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "mle_read_scalar: device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_slot_mu[dev]);
+  ScalarSlot*& slot = g_slot[dev];
+  if (!slot) {
+    void* p = nullptr;
+    MLE_HIP(hipHostMalloc(&p, sizeof(ScalarSlot), hipHostMallocCoherent));
+    slot = static_cast<ScalarSlot*>(p);
+    slot->seq = 0;
+    slot->bits = 0;
+  }
+  const unsigned want = ++g_slot_seq[dev];
+  hipStream_t s = as_stream(stream);
+  publish_scalar_kernel<<<1, 1, 0, s>>>(reinterpret_cast<const unsigned*>(src), slot, want);
+  MLE_HIP(hipGetLastError());
+  // The stream is asked every 256 spins: a stream that completed or failed
+  // without the value having landed ends the wait.
+  for (unsigned long spins = 1;; ++spins) {
+    if (__atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) == want) break;
+    if ((spins & 255) == 0) {
+      const hipError_t q = hipStreamQuery(s);
+      if (q == hipSuccess) {
+        if (__atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) == want) break;
+        return set_error(MLE_ERR_HIP, "mle_read_scalar: the stream drained without publishing the value");
+      }
+      if (q != hipErrorNotReady) return hip_error(q, "mle_read_scalar");
+    }
+    __builtin_ia32_pause();
+  }
+  const unsigned bits = __atomic_load_n(&slot->bits, __ATOMIC_ACQUIRE);
+  memcpy(dst, &bits, sizeof(float));
   return MLE_OK;
 }
 
@@ -216,10 +293,11 @@ size_t mle_arena_capacity(mle_arena arena) { return arena ? arena->cap : 0; }
 
 int mle_probe_arm(const char* kernel) {
   std::lock_guard<std::mutex> lk(g_probe_mu);
-  for (auto& r : g_probe_recs) {
-    g_event_pool.push_back(r.a);
-    g_event_pool.push_back(r.b);
-  }
+  for (auto& r : g_probe_recs)
+    for (auto& e : r.ev) {
+      g_event_pool.push_back(e.first);
+      g_event_pool.push_back(e.second);
+    }
   g_probe_recs.clear();
   g_probe_kernel = kernel ? kernel : "";
   g_probe_on.store(!g_probe_kernel.empty(), std::memory_order_relaxed);
@@ -230,10 +308,12 @@ int mle_probe_read(int* launches, double* total_ms, double* total_flop, double* 
   std::lock_guard<std::mutex> lk(g_probe_mu);
   double ms = 0, fl = 0, by = 0;
   for (auto& r : g_probe_recs) {
-    MLE_HIP(hipEventSynchronize(r.b));
-    float t = 0;
-    MLE_HIP(hipEventElapsedTime(&t, r.a, r.b));
-    ms += t;
+    for (auto& e : r.ev) {
+      MLE_HIP(hipEventSynchronize(e.second));
+      float t = 0;
+      MLE_HIP(hipEventElapsedTime(&t, e.first, e.second));
+      ms += t;
+    }
     fl += r.flop;
     by += r.bytes;
   }

@@ -346,7 +346,7 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
   NodeBackProp *nd = node.get(), *pa = A.get(), *pb = B.get();
   node->forward = [=]() {
     check(mle_scale_add(S(), pa->output, pb->output, nd->output, 1.0f, nd->total), "Add forward");
-    if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "Add loss");
+    if (last) check(mle_read_scalar(S(), nd->output, &GraphOperations::loss), "Add loss");
   };
   node->backward = [=]() {
     if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
@@ -383,7 +383,7 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
     if (calculate_loss || !last) {
       check(mle_mse_fwd(S(), pr->output, tg->output, n, nd->output, ws, ws_bytes), "Scalar MSE in MSE forward");
       nd->output_pending_zero = false;  // written whole
-      if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "MSE loss");
+      if (last) check(mle_read_scalar(S(), nd->output, &GraphOperations::loss), "MSE loss");
     }
   };
   node->backward = [=]() {
@@ -447,7 +447,7 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
         check(mle_softmax_xent_fwd(S(), pr->output, tg->output, probs, rows, d, nd->output, ws, ws_bytes),
               "SoftMaxCrossEntropy");
       nd->output_pending_zero = false;  // written whole
-      if (last) check(mle_memcpy_d2h(&GraphOperations::loss, nd->output, sizeof(float), S()), "CE loss");
+      if (last) check(mle_read_scalar(S(), nd->output, &GraphOperations::loss), "CE loss");
     }
   };
   node->backward = [=]() {

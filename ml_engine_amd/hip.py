@@ -30,6 +30,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_memcpy_h2d": (I, [P, P, SZ, P]),
     "mle_memcpy_d2h": (I, [P, P, SZ, P]),
     "mle_memcpy_d2d": (I, [P, P, SZ, P]),
+    "mle_read_scalar": (I, [P, P, P]),
     "mle_stream_create": (I, [C.POINTER(P)]),
     "mle_stream_destroy": (I, [P]),
     "mle_stream_sync": (I, [P]),

@@ -1162,8 +1162,35 @@ def test_arena_bump_allocation(hip):
     hip.call("mle_arena_destroy", arena)
 
 
+def test_read_scalar_bits(hip):
+    """mle_read_scalar returns the stored float bit for bit (signed zero, NaN
+    payloads, subnormals, infinities), after the work queued before it on the
+    same stream, on many calls in a row; null pointers are rejected."""
+    vals = np.array([1.5, -0.0, np.inf, -np.inf, 1e-45, 3.4e38, -7.25e-39], np.float32)
+    nan_bits = np.array([0x7FC00001, 0xFFBADBAD, 0x7F800001], np.uint32)
+    bits = np.concatenate([vals.view(np.uint32), nan_bits])
+    buf = hip.Buffer.from_array(bits)
+    got_bits = C.c_uint32()  # read as bits: a float round trip through Python would quiet signalling NaNs
+    for rep in range(3):
+        for i, b in enumerate(bits):
+            hip.call("mle_read_scalar", None, buf.ptr + 4 * i, C.byref(got_bits))
+            assert got_bits.value == b, (rep, i, hex(got_bits.value), hex(b))
+    got = C.c_float()
+    # queued work first: a fill on the stream, then the read sees its value
+    stream = C.c_void_p()
+    hip.call("mle_stream_create", C.byref(stream))
+    big = hip.Buffer.empty((1 << 22,))
+    for v in (2.5, -3.75, 0.125):
+        hip.call("mle_fill", stream, big.ptr, v, 1 << 22)
+        hip.call("mle_read_scalar", stream, big.ptr + 4 * ((1 << 22) - 1), C.byref(got))
+        assert got.value == v
+    hip.call("mle_stream_destroy", stream)
+    assert hip.lib().mle_read_scalar(None, None, C.byref(got)) != 0
+
+
 def test_gemm_simple_fusions(hip, orc):
-    """The one-thread-per-element path with the Linear fusions: bias in the
+    """The small-product path (a lane per output element, K split over the
+    workgroup's four waves) with the Linear fusions: bias in the
     epilogue (the forward on one row) and the column sum of dY (db) in the
     weight-gradient product with K = 1, against the oracle."""
     r = rng(404)
