@@ -438,6 +438,14 @@ size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int 
 int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* dw,
                      int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride,
                      void* ws, size_t ws_bytes);
+/* mle_conv2d_wgrad, and db[c] += sum_{n,oh,ow} dy[n][c] (db may be NULL): the
+ * bias gradient of Convolute2D's backward (GV2D then Channel_Squeeze1D over dy,
+ * Engine/engine.cu:3768-3769) taken from the dy rows the weight-gradient
+ * kernel already reads (3x3 pad 1 and 1x1 stride 1; other filters run the
+ * channel sum after the weight gradient).  Same workspace as mle_conv2d_wgrad. */
+int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, float* dw, float* db,
+                          int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride,
+                          void* ws, size_t ws_bytes);
 
 /* ------------------------------------------------------------------------- */
 /* Optimizer                                                                 */

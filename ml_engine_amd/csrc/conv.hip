@@ -187,14 +187,22 @@ __global__ __launch_bounds__(NT, 2) void igemm_kernel(Ops op, int kchunk) {
 // order through LDS, so the result does not depend on timing.  Four waves
 // per 64 columns keep enough loads in flight for the few-hundred-KB outputs
 // of a weight gradient.
+// Workgroups from `nmain` on reduce a second, small array the same way (the
+// bias partials of a weight gradient) and add the sums into out2.
 template <bool VEC>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, int splits, size_t mn,
-                                                           float* __restrict__ out) {
+                                                           float* __restrict__ out, unsigned nmain,
+                                                           const float* __restrict__ part2, int n2,
+                                                           float* __restrict__ out2) {
   constexpr int W = VEC ? 4 : 1;
   __shared__ f32x4 grp[4][64];
+  const bool second = blockIdx.x >= nmain;
+  const float* P = second ? part2 : part;
+  const size_t n = second ? (size_t)n2 : mn;
+  const size_t blk = second ? blockIdx.x - nmain : blockIdx.x;
   const int col = threadIdx.x & 63, sg = threadIdx.x >> 6;
-  const size_t i = ((size_t)blockIdx.x * 64 + col) * W;
-  const bool live = i < mn;
+  const size_t i = (blk * 64 + col) * W;
+  const bool live = i < n;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (live) {
     int s = sg;
@@ -202,30 +210,41 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
       f32x4 v[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (VEC) v[u] = *reinterpret_cast<const f32x4*>(part + (size_t)(s + 4 * u) * mn + i);
-        else v[u] = f32x4{part[(size_t)(s + 4 * u) * mn + i], 0.f, 0.f, 0.f};
+        if (VEC) v[u] = *reinterpret_cast<const f32x4*>(P + (size_t)(s + 4 * u) * n + i);
+        else v[u] = f32x4{P[(size_t)(s + 4 * u) * n + i], 0.f, 0.f, 0.f};
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) acc += v[u];
     }
     for (; s < splits; s += 4) {
-      if (VEC) acc += *reinterpret_cast<const f32x4*>(part + (size_t)s * mn + i);
-      else acc[0] += part[(size_t)s * mn + i];
+      if (VEC) acc += *reinterpret_cast<const f32x4*>(P + (size_t)s * n + i);
+      else acc[0] += P[(size_t)s * n + i];
     }
   }
   grp[sg][col] = acc;
   __syncthreads();
   if (sg != 0 || !live) return;
   const f32x4 r = ((grp[0][col] + grp[1][col]) + grp[2][col]) + grp[3][col];
-  if (VEC) *reinterpret_cast<f32x4*>(out + i) = r;
-  else out[i] = r[0];
+  if (second) {
+    if (VEC) *reinterpret_cast<f32x4*>(out2 + i) += r;
+    else out2[i] += r[0];
+  } else {
+    if (VEC) *reinterpret_cast<f32x4*>(out + i) = r;
+    else out[i] = r[0];
+  }
 }
 
-void launch_split_reduce(hipStream_t s, const float* part, int splits, size_t mn, float* out) {
-  if (mn % 4 == 0 && aligned16(part) && aligned16(out))
-    mle::launch(split_reduce_kernel<true>, (unsigned)((mn / 4 + 63) / 64), 256, 0, s, part, splits, mn, out);
-  else
-    mle::launch(split_reduce_kernel<false>, (unsigned)((mn + 63) / 64), 256, 0, s, part, splits, mn, out);
+// out = sum of the splits of part; with n2 > 0 also out2 += sum of the splits
+// of part2 (the same launch).
+void launch_split_reduce(hipStream_t s, const float* part, int splits, size_t mn, float* out,
+                         const float* part2 = nullptr, int n2 = 0, float* out2 = nullptr) {
+  const bool vec = mn % 4 == 0 && aligned16(part) && aligned16(out) &&
+                   (n2 == 0 || (n2 % 4 == 0 && aligned16(part2) && aligned16(out2)));
+  const size_t w = vec ? 4 : 1;
+  const unsigned nmain = (unsigned)((mn / w + 63) / 64);
+  const unsigned nb2 = n2 > 0 ? (unsigned)(((size_t)n2 / w + 63) / 64) : 0u;
+  if (vec) mle::launch(split_reduce_kernel<true>, nmain + nb2, 256, 0, s, part, splits, mn, out, nmain, part2, n2, out2);
+  else mle::launch(split_reduce_kernel<false>, nmain + nb2, 256, 0, s, part, splits, mn, out, nmain, part2, n2, out2);
 }
 
 // ---------------------------------------------------------------------------
@@ -772,7 +791,37 @@ struct Wgrad3Args {
   int cout, cin, h, w, hw, npix;
   int chunk;  // pixels per split, a multiple of 16
   int tiles_m, tiles, items;
+  // Bias gradient from the dy rows the kernel already loads (sum over the
+  // pixels per output channel), taken by the waves of the first column block:
+  // db_mode 1 adds into db (one split); 2 writes the split's partial sums to
+  // bpart[split][cout].
+  float* db;
+  float* bpart;
+  int db_mode;
 };
+
+// Per lane, the dy row sums of stage `fa` (block i: four pixels of row
+// m0 + 16 i + lr), added pairwise.
+__device__ __forceinline__ void bias_stage(float (&bs)[4], const f32x4 (&fa)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bs[i] += (fa[i][0] + fa[i][1]) + (fa[i][2] + fa[i][3]);
+}
+
+// Combine the four lane groups' row sums (q order fixed by the xor tree) and
+// store them: lane (lr, q = 0) owns rows m0 + 16 i + lr.
+__device__ __forceinline__ void bias_store(const Wgrad3Args& c, float (&bs)[4], int m0, int split, int lr, int q) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = bs[i];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    const int co = m0 + 16 * i + lr;
+    if (q == 0 && co < c.cout) {
+      if (c.db_mode == 1) c.db[co] += v;
+      else c.bpart[(size_t)split * c.cout + co] = v;
+    }
+  }
+}
 
 template <int WM, int D>
 __global__ __launch_bounds__(256, 2) void conv3_wgrad_kernel(Wgrad3Args c) {
@@ -858,7 +907,10 @@ __global__ __launch_bounds__(256, 2) void conv3_wgrad_kernel(Wgrad3Args c) {
 #pragma unroll
     for (int n = 0; n < 3; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const bool do_b = c.db_mode != 0 && tn == 0 && wn == 0;
+  float bs[4] = {0.f, 0.f, 0.f, 0.f};
   auto mfma = [&](const f32x4(&fa)[4], const f32x4& v, float fl, float fr) {
+    if (do_b) bias_stage(bs, fa);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float b0 = j == 0 ? fl : v[j - 1];
@@ -891,6 +943,7 @@ __global__ __launch_bounds__(256, 2) void conv3_wgrad_kernel(Wgrad3Args c) {
   for (int s = 0; s < D - 1; ++s)
     if (kt + s < nk) mfma(fa[s], fb[s], fl[s], fr[s]);
 
+  if (do_b) bias_store(c, bs, m0, split, lr, q);
   // (i, r) is row m0 + 16 i + 4 q + r, columns 3 pair .. 3 pair + 2.
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
   const int ncol = 9 * c.cin;
@@ -978,7 +1031,10 @@ __global__ __launch_bounds__(256, 2) void conv1_wgrad_kernel(Wgrad3Args c) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const bool do_b = c.db_mode != 0 && tn == 0 && wn == 0;
+  float bs[4] = {0.f, 0.f, 0.f, 0.f};
   auto mfma = [&](const f32x4(&fa)[4], const f32x4(&fb)[4]) {
+    if (do_b) bias_stage(bs, fa);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -1006,6 +1062,7 @@ __global__ __launch_bounds__(256, 2) void conv1_wgrad_kernel(Wgrad3Args c) {
   for (int s = 0; s < D - 1; ++s)
     if (kt + s < nk) mfma(fa[s], fb[s]);
 
+  if (do_b) bias_store(c, bs, m0, split, lr, q);
   // (i, r) is row m0 + 16 i + 4 q + r, columns ci0 .. ci0 + 3.
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
 #pragma unroll
@@ -1251,7 +1308,9 @@ size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int 
   if (geom(n, cin, h, w_in, cout, kh, kw, pad, stride, g) != MLE_OK) return 0;
   Wgrad3Args c3;
   int taps;
-  if (wgrad_plan(g, c3, taps)) return c3.items > c3.tiles ? (size_t)c3.out_bytes : 0;
+  // Split partials of dW, then (mle_conv2d_wgrad_bias) those of db.
+  if (wgrad_plan(g, c3, taps))
+    return c3.items > c3.tiles ? (size_t)c3.out_bytes + (size_t)(c3.items / c3.tiles) * cout * sizeof(float) : 0;
   int kchunk;
   const int splits = wgrad_splits(g, kchunk);
   return (size_t)splits * cout * cin * kh * kw * sizeof(float);
@@ -1259,6 +1318,11 @@ size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int 
 
 int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* dw, int n, int cin, int h, int w_in,
                      int cout, int kh, int kw, int pad, int stride, void* ws, size_t ws_bytes) {
+  return mle_conv2d_wgrad_bias(stream, x, dy, dw, nullptr, n, cin, h, w_in, cout, kh, kw, pad, stride, ws, ws_bytes);
+}
+
+int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, float* dw, float* db, int n, int cin,
+                          int h, int w_in, int cout, int kh, int kw, int pad, int stride, void* ws, size_t ws_bytes) {
   MLE_CHECK_ARG(x && dy && dw, "mle_conv2d_wgrad: null pointer");
   ConvGeom g;
   int rc = geom(n, cin, h, w_in, cout, kh, kw, pad, stride, g);
@@ -1275,6 +1339,11 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
     c3.dy = dy;
     c3.out = splits > 1 ? static_cast<float*>(ws) : dw;
     if (splits == 1) c3.out_bytes = (uint32_t)((size_t)cout * cin * taps * 4);
+    const size_t mn = (size_t)cout * cin * taps;
+    float* bpart = splits > 1 ? static_cast<float*>(ws) + (size_t)splits * mn : nullptr;
+    c3.db = db;
+    c3.bpart = bpart;
+    c3.db_mode = db ? (splits > 1 ? 2 : 1) : 0;
     {
       ProbeScope probe("conv_wgrad", s, flop, 0.0);
       if (taps == 9) {
@@ -1285,10 +1354,7 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
         else mle::launch(conv1_wgrad_kernel<2, 4>, c3.items, 256, 0, s, c3);
       }
     }
-    if (splits > 1) {
-      const size_t mn = (size_t)cout * cin * taps;
-      launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw);
-    }
+    if (splits > 1) launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw, bpart, db ? cout : 0, db);
     return check_launch("mle_conv2d_wgrad");
   }
   int kchunk;
@@ -1310,7 +1376,10 @@ int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* 
   }
   const size_t mn = (size_t)op.M * op.N;
   launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw);
-  return check_launch("mle_conv2d_wgrad");
+  rc = check_launch("mle_conv2d_wgrad");
+  if (rc != MLE_OK || !db) return rc;
+  // Other filters: the bias gradient by its own channel sum.
+  return mle_channel_sum(stream, dy, n, cout, (size_t)g.oh * g.ow, cout, db);
 }
 
 }  // extern "C"

@@ -13,10 +13,13 @@ namespace {
 __device__ __forceinline__ f32x4 ld4(const float* p, size_t i) { return *reinterpret_cast<const f32x4*>(p + i); }
 __device__ __forceinline__ void st4(float* p, size_t i, f32x4 v) { *reinterpret_cast<f32x4*>(p + i) = v; }
 
+// Vector body over n4 groups of four; the first workgroup also takes the
+// (at most three) elements from 4 * n4 to n.
 template <class Op>
-__global__ __launch_bounds__(256) void map4_kernel(size_t n4, Op op) {
+__global__ __launch_bounds__(256) void map4_kernel(size_t n4, size_t n, Op op) {
   const size_t stride = (size_t)gridDim.x * 256;
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) op.vec(i * 4);
+  if (blockIdx.x == 0 && 4 * n4 + threadIdx.x < n) op.one(4 * n4 + threadIdx.x);
 }
 
 template <class Op>
@@ -29,9 +32,8 @@ template <class Op>
 int run_map(hipStream_t s, size_t n, bool vec, const Op& op, const char* name) {
   if (n == 0) return MLE_OK;
   const size_t n4 = vec ? n / 4 : 0;
-  if (n4) map4_kernel<Op><<<stream_grid(n4, 256, 8192), 256, 0, s>>>(n4, op);
-  const size_t tail = n4 * 4;
-  if (tail < n) map1_kernel<Op><<<stream_grid(n - tail, 256, 8192), 256, 0, s>>>(tail, n, op);
+  if (n4) map4_kernel<Op><<<stream_grid(n4, 256, 8192), 256, 0, s>>>(n4, n, op);
+  else map1_kernel<Op><<<stream_grid(n, 256, 8192), 256, 0, s>>>(0, n, op);
   return check_launch(name);
 }
 

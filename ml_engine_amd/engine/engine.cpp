@@ -1080,11 +1080,10 @@ graph Convolute2D::forward(const graph& X) {
           "Forward Convolution in " + nm);
   };
   node->backward = [=]() {
-    check(mle_conv2d_wgrad(mle::stream(), x->output, nd->grad, W->grad, batch, inp_, a, b, out_, c_, d_, pad_, st, ws,
-                           ws_bytes),
-          "Weight Gradient in " + nm);
-    check(mle_channel_sum(mle::stream(), nd->grad, batch, out_, (size_t)outR * outC, out_, Bb->grad),
-          "Bias Gradient in " + nm);
+    // dW (assigned) and db += channel sums of dZ in one launch.
+    check(mle_conv2d_wgrad_bias(mle::stream(), x->output, nd->grad, W->grad, Bb->grad, batch, inp_, a, b, out_, c_, d_,
+                                pad_, st, ws, ws_bytes),
+          "Weight and Bias Gradient in " + nm);
     check(mle_conv2d_dgrad(mle::stream(), nd->grad, W->output, x->grad, batch, inp_, a, b, out_, c_, d_, pad_, st,
                            mle::accumulate_flag(x)),
           "Input Gradient in " + nm);

@@ -688,6 +688,16 @@ def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
     gdw = B(hip, np.full(wt.shape, 7.0, np.float32))  # wgrad assigns
     hip.call("mle_conv2d_wgrad", None, gx.ptr, gdy.ptr, gdw.ptr, n, cin, h, w, cout, k, k, pad, stride, ws.ptr, ws.nbytes)
     assert_close(gdw.numpy(), dwr, what="conv wgrad", **MM)
+    # The bias gradient taken inside the weight-gradient launch: dW the same
+    # bits as above, db += the channel sums of dy (Channel_Squeeze1D).
+    db0 = r.standard_normal(cout, dtype=np.float32)
+    dbr = db0.copy()
+    orc.call("orc_channel_squeeze", orc.ptr(dy), orc.ptr(dbr), n, cout, oh * ow, cout)
+    gdw2, gdb = B(hip, np.full(wt.shape, -3.0, np.float32)), B(hip, db0)
+    hip.call("mle_conv2d_wgrad_bias", None, gx.ptr, gdy.ptr, gdw2.ptr, gdb.ptr, n, cin, h, w, cout, k, k, pad, stride,
+             ws.ptr, ws.nbytes)
+    np.testing.assert_array_equal(gdw2.numpy(), gdw.numpy())
+    assert_close(gdb.numpy(), dbr, what="conv bias grad", **MM)  # a sum over n * oh * ow terms
 
 
 # ----------------------------------------------------------------- optimizer
