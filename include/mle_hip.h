@@ -270,6 +270,13 @@ int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers,
                    const float* X, const float* dY, int64_t stride_dy,
                    const float* W, int64_t stride_w, float* dX, int accumulate_dx,
                    float* dW, float* db, int64_t stride_db, void* ws, size_t ws_bytes);
+/* mle_linear_bwd with the parameter gradients' mode: accumulate_dw 1 adds dW
+ * and db as above, 0 assigns both (the gradients are logically zero: the
+ * engine's lazy clearing of parameter gradients, no fill launch). */
+int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers,
+                      const float* X, const float* dY, int64_t stride_dy,
+                      const float* W, int64_t stride_w, float* dX, int accumulate_dx,
+                      float* dW, float* db, int64_t stride_db, int accumulate_dw, void* ws, size_t ws_bytes);
 
 /* out[c] (+)= sum_r x[r, c].  BCompress (Engine/kernels.cu:1562-1584); beta 0/1. */
 int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* out, float beta);
@@ -438,14 +445,15 @@ size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int 
 int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* dw,
                      int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride,
                      void* ws, size_t ws_bytes);
-/* mle_conv2d_wgrad, and db[c] += sum_{n,oh,ow} dy[n][c] (db may be NULL): the
- * bias gradient of Convolute2D's backward (GV2D then Channel_Squeeze1D over dy,
- * Engine/engine.cu:3768-3769) taken from the dy rows the weight-gradient
- * kernel already reads (3x3 pad 1 and 1x1 stride 1; other filters run the
- * channel sum after the weight gradient).  Same workspace as mle_conv2d_wgrad. */
+/* mle_conv2d_wgrad, and db[c] (+)= sum_{n,oh,ow} dy[n][c] (db may be NULL;
+ * accumulate_db 1 adds, 0 assigns): the bias gradient of Convolute2D's
+ * backward (GV2D then Channel_Squeeze1D over dy, Engine/engine.cu:3768-3769)
+ * taken from the dy rows the weight-gradient kernel already reads (3x3 pad 1
+ * and 1x1 stride 1; other filters run the channel sum after the weight
+ * gradient).  Same workspace as mle_conv2d_wgrad. */
 int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, float* dw, float* db,
-                          int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride,
-                          void* ws, size_t ws_bytes);
+                          int accumulate_db, int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad,
+                          int stride, void* ws, size_t ws_bytes);
 
 /* ------------------------------------------------------------------------- */
 /* Optimizer                                                                 */
@@ -509,6 +517,13 @@ size_t mle_embed_scatter_ws_bytes(int batch, int clen);
 int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, const int32_t* keys,
                           int batch, int clen, int max_clen, int dim, int vocab, float scale,
                           void* ws, size_t ws_bytes);
+/* The embedding-table gradient: dtable[keys[b, s], :] (+)= grad[b, s, :], summed
+ * per row in token order; accumulate 0 assigns (dtable is logically zero: rows
+ * no token reaches become 0, without a separate fill), 1 adds -- the Embedding
+ * backward (KeyUpdate into the table gradient, Engine/kernels.cu:1536-1549). */
+int mle_embed_grad(mle_stream stream, float* dtable, const float* grad, const int32_t* keys,
+                   int batch, int clen, int max_clen, int dim, int vocab, int accumulate,
+                   void* ws, size_t ws_bytes);
 /* out[(b*clen + s)*vocab + key] = 1 for valid keys (out must be zeroed).
  * OneHotEmbeddings (Engine/kernels.cu:1551-1560). */
 int mle_onehot(mle_stream stream, float* out, const int32_t* keys, int batch, int clen, int max_clen, int vocab);

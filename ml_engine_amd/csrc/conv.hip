@@ -188,12 +188,13 @@ __global__ __launch_bounds__(NT, 2) void igemm_kernel(Ops op, int kchunk) {
 // per 64 columns keep enough loads in flight for the few-hundred-KB outputs
 // of a weight gradient.
 // Workgroups from `nmain` on reduce a second, small array the same way (the
-// bias partials of a weight gradient) and add the sums into out2.
+// bias partials of a weight gradient) and add the sums into out2 (acc2 = 1)
+// or assign them (0).
 template <bool VEC>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part, int splits, size_t mn,
                                                            float* __restrict__ out, unsigned nmain,
                                                            const float* __restrict__ part2, int n2,
-                                                           float* __restrict__ out2) {
+                                                           float* __restrict__ out2, int acc2) {
   constexpr int W = VEC ? 4 : 1;
   __shared__ f32x4 grp[4][64];
   const bool second = blockIdx.x >= nmain;
@@ -226,25 +227,27 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
   if (sg != 0 || !live) return;
   const f32x4 r = ((grp[0][col] + grp[1][col]) + grp[2][col]) + grp[3][col];
   if (second) {
-    if (VEC) *reinterpret_cast<f32x4*>(out2 + i) += r;
-    else out2[i] += r[0];
+    if (VEC) *reinterpret_cast<f32x4*>(out2 + i) = acc2 ? *reinterpret_cast<const f32x4*>(out2 + i) + r : r;
+    else out2[i] = acc2 ? out2[i] + r[0] : r[0];
   } else {
     if (VEC) *reinterpret_cast<f32x4*>(out + i) = r;
     else out[i] = r[0];
   }
 }
 
-// out = sum of the splits of part; with n2 > 0 also out2 += sum of the splits
-// of part2 (the same launch).
+// out = sum of the splits of part; with n2 > 0 also out2 (+)= sum of the
+// splits of part2 (acc2: 1 adds, 0 assigns; the same launch).
 void launch_split_reduce(hipStream_t s, const float* part, int splits, size_t mn, float* out,
-                         const float* part2 = nullptr, int n2 = 0, float* out2 = nullptr) {
+                         const float* part2 = nullptr, int n2 = 0, float* out2 = nullptr, int acc2 = 1) {
   const bool vec = mn % 4 == 0 && aligned16(part) && aligned16(out) &&
                    (n2 == 0 || (n2 % 4 == 0 && aligned16(part2) && aligned16(out2)));
   const size_t w = vec ? 4 : 1;
   const unsigned nmain = (unsigned)((mn / w + 63) / 64);
   const unsigned nb2 = n2 > 0 ? (unsigned)(((size_t)n2 / w + 63) / 64) : 0u;
-  if (vec) mle::launch(split_reduce_kernel<true>, nmain + nb2, 256, 0, s, part, splits, mn, out, nmain, part2, n2, out2);
-  else mle::launch(split_reduce_kernel<false>, nmain + nb2, 256, 0, s, part, splits, mn, out, nmain, part2, n2, out2);
+  if (vec)
+    mle::launch(split_reduce_kernel<true>, nmain + nb2, 256, 0, s, part, splits, mn, out, nmain, part2, n2, out2, acc2);
+  else
+    mle::launch(split_reduce_kernel<false>, nmain + nb2, 256, 0, s, part, splits, mn, out, nmain, part2, n2, out2, acc2);
 }
 
 // ---------------------------------------------------------------------------
@@ -793,8 +796,8 @@ struct Wgrad3Args {
   int tiles_m, tiles, items;
   // Bias gradient from the dy rows the kernel already loads (sum over the
   // pixels per output channel), taken by the waves of the first column block:
-  // db_mode 1 adds into db (one split); 2 writes the split's partial sums to
-  // bpart[split][cout].
+  // db_mode 1 adds into db (one split), 3 assigns it; 2 writes the split's
+  // partial sums to bpart[split][cout].
   float* db;
   float* bpart;
   int db_mode;
@@ -818,6 +821,7 @@ __device__ __forceinline__ void bias_store(const Wgrad3Args& c, float (&bs)[4], 
     const int co = m0 + 16 * i + lr;
     if (q == 0 && co < c.cout) {
       if (c.db_mode == 1) c.db[co] += v;
+      else if (c.db_mode == 3) c.db[co] = v;
       else c.bpart[(size_t)split * c.cout + co] = v;
     }
   }
@@ -1318,11 +1322,13 @@ size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int 
 
 int mle_conv2d_wgrad(mle_stream stream, const float* x, const float* dy, float* dw, int n, int cin, int h, int w_in,
                      int cout, int kh, int kw, int pad, int stride, void* ws, size_t ws_bytes) {
-  return mle_conv2d_wgrad_bias(stream, x, dy, dw, nullptr, n, cin, h, w_in, cout, kh, kw, pad, stride, ws, ws_bytes);
+  return mle_conv2d_wgrad_bias(stream, x, dy, dw, nullptr, 1, n, cin, h, w_in, cout, kh, kw, pad, stride, ws,
+                               ws_bytes);
 }
 
-int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, float* dw, float* db, int n, int cin,
-                          int h, int w_in, int cout, int kh, int kw, int pad, int stride, void* ws, size_t ws_bytes) {
+int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, float* dw, float* db, int accumulate_db,
+                          int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad, int stride, void* ws,
+                          size_t ws_bytes) {
   MLE_CHECK_ARG(x && dy && dw, "mle_conv2d_wgrad: null pointer");
   ConvGeom g;
   int rc = geom(n, cin, h, w_in, cout, kh, kw, pad, stride, g);
@@ -1343,7 +1349,7 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
     float* bpart = splits > 1 ? static_cast<float*>(ws) + (size_t)splits * mn : nullptr;
     c3.db = db;
     c3.bpart = bpart;
-    c3.db_mode = db ? (splits > 1 ? 2 : 1) : 0;
+    c3.db_mode = db ? (splits > 1 ? 2 : (accumulate_db ? 1 : 3)) : 0;
     {
       ProbeScope probe("conv_wgrad", s, flop, 0.0);
       if (taps == 9) {
@@ -1354,7 +1360,8 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
         else mle::launch(conv1_wgrad_kernel<2, 4>, c3.items, 256, 0, s, c3);
       }
     }
-    if (splits > 1) launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw, bpart, db ? cout : 0, db);
+    if (splits > 1)
+      launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw, bpart, db ? cout : 0, db, accumulate_db);
     return check_launch("mle_conv2d_wgrad");
   }
   int kchunk;
@@ -1379,6 +1386,10 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
   rc = check_launch("mle_conv2d_wgrad");
   if (rc != MLE_OK || !db) return rc;
   // Other filters: the bias gradient by its own channel sum.
+  if (!accumulate_db) {
+    rc = mle_fill(stream, db, 0.0f, (size_t)cout);
+    if (rc != MLE_OK) return rc;
+  }
   return mle_channel_sum(stream, dy, n, cout, (size_t)g.oh * g.ow, cout, db);
 }
 

@@ -143,7 +143,7 @@ template <bool VEC>
 __global__ __launch_bounds__(RS_NT) void range_scatter_kernel(float* __restrict__ table, const float* __restrict__ grad,
                                                               const int32_t* __restrict__ keys, int clen, int max_clen,
                                                               int ntok, int dim, int vocab, int rows_per_wg,
-                                                              float scale) {
+                                                              float scale, int assign) {
   __shared__ int sperm[RS_CHUNK];  // (row << 16) | chunk-local token, per row in arrival order
   __shared__ int slist[RS_CHUNK];  // chunk-local tokens, per row in token order
   __shared__ int sbin[RS_RMAX];
@@ -201,13 +201,17 @@ __global__ __launch_bounds__(RS_NT) void range_scatter_kernel(float* __restrict_
       slist[b + rank] = i;
     }
     __syncthreads();
+    // assign: the first chunk writes every row of the range (rows without
+    // tokens get 0) instead of adding into it.
+    const bool first = assign && t0 == 0;
     for (int r = wid; r < nrows; r += RS_NT / 64) {
       const int b = sstart[r], e = sstart[r + 1];
-      if (b == e) continue;
+      if (b == e && !first) continue;
       float* row = table + (size_t)(v_lo + r) * dim;
       if (VEC) {
         for (int d = 4 * lane; d < dim; d += 256) {
-          f32x4 v = *reinterpret_cast<const f32x4*>(row + d);  // in flight with the gradient loads
+          // in flight with the gradient loads
+          f32x4 v = first ? f32x4{0.f, 0.f, 0.f, 0.f} : *reinterpret_cast<const f32x4*>(row + d);
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
           for (int j = b; j < e; ++j) {
             const f32x4 g = *reinterpret_cast<const f32x4*>(grad + (size_t)(t0 + slist[j]) * dim + d);
@@ -222,7 +226,7 @@ __global__ __launch_bounds__(RS_NT) void range_scatter_kernel(float* __restrict_
         for (int d = lane; d < dim; d += 64) {
           float acc = 0.f;
           for (int j = b; j < e; ++j) acc += grad[(size_t)(t0 + slist[j]) * dim + d];
-          row[d] += scale * acc;
+          row[d] = (first ? 0.f : row[d]) + scale * acc;
         }
       }
     }
@@ -403,6 +407,59 @@ __global__ __launch_bounds__(CS_NT) void channel_sum_kernel(const float* __restr
   if (threadIdx.x == 0) out[c] += t;
 }
 
+// table (+)= scale * scatter(grad); assign: the table is logically zero (rows
+// no token reaches become 0).
+int embed_scatter(mle_stream stream, float* table, const float* grad, const int32_t* keys, int batch, int clen,
+                  int max_clen, int dim, int vocab, float scale, int assign, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(table && grad && keys && ws && clen > 0 && max_clen >= clen && dim > 0 && vocab > 0,
+                "mle_embed_scatter_add: bad argument");
+  const long long ntok = (long long)batch * clen;
+  MLE_CHECK_ARG(ntok < 2147483647LL, "mle_embed_scatter_add: too many tokens");
+  const bool in_kernel = ntok > 0 && vocab <= RS_VMAX;  // the range kernel assigns by itself
+  if (assign && !in_kernel) {
+    const int rc = mle_fill(stream, table, 0.0f, (size_t)vocab * dim);
+    if (rc != MLE_OK) return rc;
+  }
+  if (ntok == 0) return MLE_OK;
+  if (ws_bytes < mle_embed_scatter_ws_bytes(batch, clen))
+    return set_error(MLE_ERR_WORKSPACE, "mle_embed_scatter_add: workspace too small");
+  hipStream_t s = as_stream(stream);
+  unsigned long long* sorted = static_cast<unsigned long long*>(ws);
+  const int vec = (dim % 4 == 0 && aligned16(table) && aligned16(grad)) ? 1 : 0;
+  if (vocab <= RS_VMAX) {
+    const int rows = (vocab + 511) / 512;  // <= RS_RMAX / 2: about one row per wave, at most 512 workgroups
+    const unsigned grid = (unsigned)((vocab + rows - 1) / rows);
+    if (vec)
+      range_scatter_kernel<true><<<grid, RS_NT, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab, rows,
+                                                        scale, assign);
+    else
+      range_scatter_kernel<false><<<grid, RS_NT, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab,
+                                                         rows, scale, assign);
+    return check_launch("mle_embed_scatter_add");
+  }
+  if ((double)vocab * (double)ntok <= (double)(1u << 30) && dim <= 1024) {
+    // One row per wave (measured on MI355X: 2, 4 or 8 rows per wave, or 8-16
+    // waves per workgroup, are equal or slower -- the key scan bounds it).
+    if (dim <= 512)
+      row_scatter_kernel<8, 1><<<(vocab + 3) / 4, 256, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab,
+                                                               scale);
+    else
+      row_scatter_kernel<16, 1><<<(vocab + 3) / 4, 256, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim,
+                                                                vocab, scale);
+    return check_launch("mle_embed_scatter_add");
+  }
+  // Chunks of SORT_CAP tokens are applied in token order, so every table row
+  // receives its updates in a fixed order.
+  for (long long t0 = 0; t0 < ntok; t0 += SORT_CAP) {
+    const int count = (int)((ntok - t0 < SORT_CAP) ? ntok - t0 : SORT_CAP);
+    sort_chunk_kernel<<<1, SORT_NT, 0, s>>>(keys, clen, max_clen, vocab, (int)t0, count, sorted);
+    segment_add_kernel<<<(count + 3) / 4, 256, 0, s>>>(table, grad, sorted, count, dim, scale, vec);
+    int rc = check_launch("mle_embed_scatter_add");
+    if (rc) return rc;
+  }
+  return MLE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -428,49 +485,15 @@ size_t mle_embed_scatter_ws_bytes(int batch, int clen) {
 
 int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, const int32_t* keys, int batch, int clen,
                           int max_clen, int dim, int vocab, float scale, void* ws, size_t ws_bytes) {
-  MLE_CHECK_ARG(table && grad && keys && ws && clen > 0 && max_clen >= clen && dim > 0 && vocab > 0,
-                "mle_embed_scatter_add: bad argument");
-  const long long ntok = (long long)batch * clen;
-  if (ntok == 0) return MLE_OK;
-  MLE_CHECK_ARG(ntok < 2147483647LL, "mle_embed_scatter_add: too many tokens");
-  if (ws_bytes < mle_embed_scatter_ws_bytes(batch, clen))
-    return set_error(MLE_ERR_WORKSPACE, "mle_embed_scatter_add: workspace too small");
-  hipStream_t s = as_stream(stream);
-  unsigned long long* sorted = static_cast<unsigned long long*>(ws);
-  const int vec = (dim % 4 == 0 && aligned16(table) && aligned16(grad)) ? 1 : 0;
-  if (vocab <= RS_VMAX) {
-    const int rows = (vocab + 511) / 512;  // <= RS_RMAX / 2: about one row per wave, at most 512 workgroups
-    const unsigned grid = (unsigned)((vocab + rows - 1) / rows);
-    if (vec)
-      range_scatter_kernel<true><<<grid, RS_NT, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab, rows,
-                                                        scale);
-    else
-      range_scatter_kernel<false><<<grid, RS_NT, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab,
-                                                         rows, scale);
-    return check_launch("mle_embed_scatter_add");
-  }
-  if ((double)vocab * (double)ntok <= (double)(1u << 30) && dim <= 1024) {
-    // One row per wave (measured on MI355X: 2, 4 or 8 rows per wave, or 8-16
-    // waves per workgroup, are equal or slower -- the key scan bounds it).
-    if (dim <= 512)
-      row_scatter_kernel<8, 1><<<(vocab + 3) / 4, 256, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim, vocab,
-                                                               scale);
-    else
-      row_scatter_kernel<16, 1><<<(vocab + 3) / 4, 256, 0, s>>>(table, grad, keys, clen, max_clen, (int)ntok, dim,
-                                                                vocab, scale);
-    return check_launch("mle_embed_scatter_add");
-  }
-  // Chunks of SORT_CAP tokens are applied in token order, so every table row
-  // receives its updates in a fixed order.
-  for (long long t0 = 0; t0 < ntok; t0 += SORT_CAP) {
-    const int count = (int)((ntok - t0 < SORT_CAP) ? ntok - t0 : SORT_CAP);
-    sort_chunk_kernel<<<1, SORT_NT, 0, s>>>(keys, clen, max_clen, vocab, (int)t0, count, sorted);
-    segment_add_kernel<<<(count + 3) / 4, 256, 0, s>>>(table, grad, sorted, count, dim, scale, vec);
-    int rc = check_launch("mle_embed_scatter_add");
-    if (rc) return rc;
-  }
-  return MLE_OK;
+  return embed_scatter(stream, table, grad, keys, batch, clen, max_clen, dim, vocab, scale, 0, ws, ws_bytes);
 }
+
+int mle_embed_grad(mle_stream stream, float* dtable, const float* grad, const int32_t* keys, int batch, int clen,
+                   int max_clen, int dim, int vocab, int accumulate, void* ws, size_t ws_bytes) {
+  return embed_scatter(stream, dtable, grad, keys, batch, clen, max_clen, dim, vocab, 1.0f, accumulate ? 0 : 1, ws,
+                       ws_bytes);
+}
+
 
 int mle_onehot(mle_stream stream, float* out, const int32_t* keys, int batch, int clen, int max_clen, int vocab) {
   MLE_CHECK_ARG(out && keys && clen > 0 && max_clen >= clen && vocab > 0, "mle_onehot: bad argument");

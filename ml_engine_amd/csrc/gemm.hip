@@ -56,7 +56,15 @@ struct GemmArgs {
   const float* act_x;
   float* act_dx;
   int act_acc;
+  // Column sums: 0 adds them into colsum (the default), 1 assigns (colsum is
+  // logically zero).
+  int cs_assign;
 };
+
+// colsum[i] (+)= v as GemmArgs::cs_assign says.
+__device__ __forceinline__ void put_colsum(const GemmArgs& g, int64_t i, float v) {
+  g.colsum[i] = g.cs_assign ? v : g.colsum[i] + v;
+}
 
 // Epilogue modes of the persistent kernel.
 constexpr int kEpiPlain = 0, kEpiRowstats = 1, kEpiActFwd = 2, kEpiActBwd = 3;
@@ -322,7 +330,7 @@ __global__ __launch_bounds__(NT, KD == 16 ? 3 : 2) void gemm_kernel(GemmArgs g) 
 #pragma unroll
       for (int h = 0; h < CS_T; ++h) cs += smem[tid + h * TN];
       if (split_mode) g.part_cs[(int64_t)blockIdx.z * g.N + n0 + tid] = cs;
-      else g.colsum[z * g.scs + n0 + tid] += cs;
+      else put_colsum(g, z * g.scs + n0 + tid, cs);
     }
   }
 }
@@ -518,7 +526,7 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& g, int tm, int tn, i
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         if (split_mode) g.part_cs[(int64_t)bz * g.N + col + n] = csum[n];
-        else g.colsum[z * g.scs + col + n] += csum[n];
+        else put_colsum(g, z * g.scs + col + n, csum[n]);
       }
     }
   }
@@ -874,7 +882,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
       for (int j = 0; j < W; ++j) {
         float acc = 0.f;
         for (int sp = 0; sp < g.splits; ++sp) acc += g.part_cs[(b * g.splits + sp) * g.N + col + j];
-        g.colsum[b * g.scs + col + j] += acc;
+        put_colsum(g, b * g.scs + col + j, acc);
       }
     }
   }
@@ -917,7 +925,7 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs g) {
   if (g.bias) v += g.bias[z * g.sbias + n];
   *c = v;
   if (g.colsum && m == 0)
-    g.colsum[z * g.scs + n] += ((red[1][0][lane] + red[1][1][lane]) + red[1][2][lane]) + red[1][3][lane];
+    put_colsum(g, z * g.scs + n, ((red[1][0][lane] + red[1][1][lane]) + red[1][2][lane]) + red[1][3][lane]);
 }
 
 // Workgroup tile: 128 x 128 unless a side is <= 64 (the 64-wide variants waste
@@ -1362,6 +1370,13 @@ size_t mle_linear_bwd_ws_bytes(int rows, int in, int out, int layers) {
 int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers, const float* X, const float* dY,
                    int64_t stride_dy, const float* W, int64_t stride_w, float* dX, int accumulate_dx, float* dW,
                    float* db, int64_t stride_db, void* ws, size_t ws_bytes) {
+  return mle_linear_bwd_ex(stream, rows, in, out, layers, X, dY, stride_dy, W, stride_w, dX, accumulate_dx, dW, db,
+                           stride_db, 1, ws, ws_bytes);
+}
+
+int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, const float* X, const float* dY,
+                      int64_t stride_dy, const float* W, int64_t stride_w, float* dX, int accumulate_dx, float* dW,
+                      float* db, int64_t stride_db, int accumulate_dw, void* ws, size_t ws_bytes) {
   MLE_CHECK_ARG(rows >= 0 && in >= 0 && out >= 0 && layers >= 1, "mle_linear_bwd: bad sizes");
   MLE_CHECK_ARG(layers == 1 || (stride_dy != 0 && stride_w != 0 && (db == nullptr || stride_db != 0)),
                 "mle_linear_bwd: %d layers need strides", layers);
@@ -1372,10 +1387,11 @@ int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers, con
   int rc = gemm_plan(P0, 0, 1, rows, in, out, 1.0f, dY, out, 0, W, out, 0, accumulate_dx ? 1.0f : 0.0f, dX, in, 0, 1,
                      nullptr, nullptr, ws, ws_bytes, 1, 0, 0, 0, 0, 0, layers > 1 ? layers : 0, stride_dy, stride_w);
   if (rc != MLE_OK) return rc;
-  // dW_l += X^T dY_l and db_l += colsum dY_l: TN, in x out, depth rows.
-  rc = gemm_plan(P1, 1, 0, in, out, rows, 1.0f, X, in, 0, dY, out, stride_dy, 1.0f, dW, out, stride_w, layers, db,
-                 nullptr, ws, ws_bytes, 1, 0, 0, 0, 0, stride_db);
+  // dW_l (+)= X^T dY_l and db_l (+)= colsum dY_l: TN, in x out, depth rows.
+  rc = gemm_plan(P1, 1, 0, in, out, rows, 1.0f, X, in, 0, dY, out, stride_dy, accumulate_dw ? 1.0f : 0.0f, dW, out,
+                 stride_w, layers, db, nullptr, ws, ws_bytes, 1, 0, 0, 0, 0, stride_db);
   if (rc != MLE_OK) return rc;
+  P1.g.cs_assign = accumulate_dw ? 0 : 1;
   hipStream_t s = as_stream(stream);
   const long long n0 = direct_items(P0), n1 = direct_items(P1);
   const int ncu = cu_count();

@@ -173,6 +173,25 @@ int accumulate_flag(NodeBackProp* n) {
   return 1;
 }
 
+int params_write_flag(const std::vector<NodeBackProp*>& ps) {
+  bool all = true;
+  for (auto* p : ps)
+    if (p) all = all && p->grad_pending_zero;
+  if (all) {
+    for (auto* p : ps)
+      if (p) p->grad_pending_zero = false;
+    return 0;
+  }
+  for (auto* p : ps)
+    if (p) materialize(p);
+  return 1;
+}
+
+void materialize_params(const std::vector<AdamParameter*>& ps) {
+  ZeroBatch batch;  // neighbouring parameters' fills merge into one launch
+  for (auto* p : ps) materialize(p);
+}
+
 void materialize(NodeBackProp* n) {
   if (!n) return;
   clip_apply(n);
@@ -202,6 +221,7 @@ std::unordered_set<NodeBackProp*> g_clip_marked;  // parameters whose gradient r
 
 void clip_mark(const std::vector<AdamParameter*>& ps, const double* s) {
   clip_apply_all();
+  materialize_params(ps);  // a marked gradient is divided in place later
   if (!g_clip_snapshot) g_clip_snapshot = static_cast<double*>(alloc_scratch(256));
   check(mle_memcpy_d2d(g_clip_snapshot, s, sizeof(double), stream()), "clipNorm: snapshot of the scale");
   for (auto* p : ps) g_clip_marked.insert(p);
@@ -454,6 +474,7 @@ void AdamParameter::load(std::ifstream& f) {
 }
 
 void AdamParameter::update(const float lr, const bool W) {
+  mle::materialize(this);
   check(mle_adam_update(mle::stream(), output, grad, m, v, total, t, lr, b1, b2, epsilon, weight_decay, W ? 1 : 0,
                         nullptr),
         "AdamUpdate in AdamParameter update");
@@ -461,6 +482,7 @@ void AdamParameter::update(const float lr, const bool W) {
 }
 
 void AdamParameter::accumulate_grad(double* global_scale) {
+  mle::materialize(this);
   const size_t ws_bytes = mle_sqnorm_ws_bytes(total);
   static void* ws = nullptr;
   static size_t ws_cap = 0;
@@ -472,6 +494,7 @@ void AdamParameter::accumulate_grad(double* global_scale) {
 }
 
 void AdamParameter::gradnorm(const double* global_scale) {
+  mle::materialize(this);
   check(mle_scale_by_device(mle::stream(), grad, global_scale, 1, total), "ScalePtr of " + op_name);
 }
 
@@ -498,10 +521,12 @@ void Zerograd(const AdamParameter& X) {
   auto* p = const_cast<AdamParameter*>(&X);
   mle::clip_drop(p);
   mle::zero(p->grad, p->total);
+  p->grad_pending_zero = false;
 }
 void Zerograd(graph X) {
   mle::clip_drop(X.get());
   mle::zero(X->grad, X->total);
+  X->grad_pending_zero = false;
 }
 
 static void print_head(NodeBackProp* X, int type, int rows_max, int cols_max) {
@@ -660,6 +685,7 @@ void GraphOperations::accumulate(double* global_scale) {
   mle::clip_apply_all();
   bool dup = false;
   auto ps = collect_params(nodes, dup);
+  mle::materialize_params(ps);
   bool all_hooks_known = true;
   for (auto& n : nodes)
     if (n->accumulate && n->params.empty()) all_hooks_known = false;
@@ -683,6 +709,7 @@ void GraphOperations::ParameterUpdate(const graph& X, const bool show, const flo
   }
   bool dup = false;
   auto ps = collect_params(nodes, dup);
+  mle::materialize_params(ps);  // a parameter no backward wrote still has its clear mark
   bool fusable = !dup && !ps.empty();
   for (auto& n : nodes)
     if (n->updateParams && n->params.empty()) fusable = false;
@@ -893,16 +920,17 @@ graph Linear::forward(const graph& X) {
   };
   node->backward = [=]() {
     // dX (+)= dZ W^T, dW += X^T dZ, db += colsum dZ (one launch when they fit).
-    check(mle_linear_bwd(mle::stream(), (int)rows, n, p, 1, x->output, nd->grad, 0, W->output, 0, x->grad,
-                         mle::accumulate_flag(x), W->grad, has_bias ? Bb->grad : nullptr, 0, ws, ws_bytes),
+    check(mle_linear_bwd_ex(mle::stream(), (int)rows, n, p, 1, x->output, nd->grad, 0, W->output, 0, x->grad,
+                            mle::accumulate_flag(x), W->grad, has_bias ? Bb->grad : nullptr, 0,
+                            mle::params_write_flag({W, has_bias ? Bb : nullptr}), ws, ws_bytes),
           "MatMul... dZ*W^T and X^T*dZ in " + name + " backward");
   };
   node->free = [=]() { nd->clear(); };
   node->serious_free = [=]() {};
   node->zero_grad = [=]() {
     mle::defer_zero(nd);
-    mle::zero(W->grad, W->total);
-    if (has_bias) mle::zero(Bb->grad, Bb->total);
+    mle::defer_zero(W);
+    if (has_bias) mle::defer_zero(Bb);
   };
   node->accumulate = [=](double* s) {
     W->accumulate_grad(s);
@@ -1022,8 +1050,14 @@ bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Line
       // Every sibling's gradient is complete now (this is the last of their
       // backward calls): dX = sum_i dZ_i W_i^T, dW_i += X^T dZ_i and
       // db_i += colsum dZ_i for all siblings at once.
-      check(mle_linear_bwd(stream(), (int)rows, k, p, nl, x->output, o0->grad, dgrad, W0->output, dw, x->grad,
-                           accumulate_flag(x), W0->grad, has_bias ? B0->grad : nullptr, dbias, ws, ws_bytes),
+      std::vector<NodeBackProp*> ps;
+      for (auto* l : layers) {
+        ps.push_back(&l->W1);
+        if (has_bias) ps.push_back(&l->B1);
+      }
+      check(mle_linear_bwd_ex(stream(), (int)rows, k, p, nl, x->output, o0->grad, dgrad, W0->output, dw, x->grad,
+                              accumulate_flag(x), W0->grad, has_bias ? B0->grad : nullptr, dbias,
+                              params_write_flag(ps), ws, ws_bytes),
             "Sibling Linear backward in " + name);
     };
   }
@@ -1081,8 +1115,9 @@ graph Convolute2D::forward(const graph& X) {
   };
   node->backward = [=]() {
     // dW (assigned) and db += channel sums of dZ in one launch.
-    check(mle_conv2d_wgrad_bias(mle::stream(), x->output, nd->grad, W->grad, Bb->grad, batch, inp_, a, b, out_, c_, d_,
-                                pad_, st, ws, ws_bytes),
+    W->grad_pending_zero = false;  // the weight gradient is assigned whole (GV2D)
+    check(mle_conv2d_wgrad_bias(mle::stream(), x->output, nd->grad, W->grad, Bb->grad, mle::params_write_flag({Bb}),
+                                batch, inp_, a, b, out_, c_, d_, pad_, st, ws, ws_bytes),
           "Weight and Bias Gradient in " + nm);
     check(mle_conv2d_dgrad(mle::stream(), nd->grad, W->output, x->grad, batch, inp_, a, b, out_, c_, d_, pad_, st,
                            mle::accumulate_flag(x)),
@@ -1090,8 +1125,8 @@ graph Convolute2D::forward(const graph& X) {
   };
   node->zero_grad = [=]() {
     mle::defer_zero(nd);
-    mle::zero(W->grad, W->total);
-    mle::zero(Bb->grad, Bb->total);
+    mle::defer_zero(W);
+    mle::defer_zero(Bb);
   };
   node->free = [=]() { nd->clear(); };
   node->serious_free = [=]() {};
@@ -1172,6 +1207,8 @@ graph Convolute2DT::forward(const graph& X) {
           "ConvTranspose2D bias in " + nm);
   };
   node->backward = [=]() {
+    mle::materialize(W);
+    mle::materialize(Bb);
     check(mle_conv2d_wgrad(mle::stream(), nd->grad, x->output, wtg, batch, out_, oh, ow, inp_, c_, d_, pad_, st, ws,
                            ws_bytes),
           "Weight Gradient in " + nm);
@@ -1184,8 +1221,8 @@ graph Convolute2DT::forward(const graph& X) {
   };
   node->zero_grad = [=]() {
     mle::defer_zero(nd);
-    mle::zero(W->grad, W->total);
-    mle::zero(Bb->grad, Bb->total);
+    mle::defer_zero(W);
+    mle::defer_zero(Bb);
   };
   node->free = [=]() { nd->clear(); };
   node->serious_free = [=]() {};
@@ -1230,12 +1267,13 @@ graph Embedding::forward(const int32_t* keys, int batch, int clen, int max_clen)
     check(mle_embed_gather(mle::stream(), nd->output, T->output, keys, batch, clen, max_clen, D), "GatherEmbeddings");
   };
   node->backward = [=]() {
-    check(mle_embed_scatter_add(mle::stream(), T->grad, nd->grad, keys, batch, clen, max_clen, D, V, 1.0f, ws, wsb),
+    check(mle_embed_grad(mle::stream(), T->grad, nd->grad, keys, batch, clen, max_clen, D, V,
+                         mle::params_write_flag({T}), ws, wsb),
           "Embedding gradient");
   };
   node->zero_grad = [=]() {
     mle::defer_zero(nd);
-    mle::zero(T->grad, T->total);
+    mle::defer_zero(T);
   };
   node->free = [=]() { nd->clear(); };
   node->accumulate = [=](double* s) { T->accumulate_grad(s); };

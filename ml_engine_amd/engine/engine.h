@@ -90,6 +90,13 @@ struct ZeroBatch {
 void defer_zero(NodeBackProp* n);
 int accumulate_flag(NodeBackProp* n);
 void materialize(NodeBackProp* n);
+// Parameter gradients are cleared the same way.  A backward that writes the
+// gradients of `ps` whole in one launch asks params_write_flag for its mode:
+// 0 (assign) when every one of them is marked clear (the marks are taken),
+// otherwise the marked ones are filled and 1 (add) is returned.  Readers of
+// parameter gradients (update, norm, clip) call materialize_params first.
+int params_write_flag(const std::vector<NodeBackProp*>& ps);
+void materialize_params(const std::vector<AdamParameter*>& ps);
 // Lazy zeroing of a loss node's (one-float) output: zero_grad marks it, the
 // loss forward clears the mark when it writes the value, readers call
 // materialize_output first.

@@ -223,8 +223,12 @@ int mle_model_param_io(void* h, int i, int which, void* host, int to_device) {
   float* dev = which == 0 ? p->output : which == 1 ? p->grad : which == 2 ? p->m : p->v;
   const size_t bytes = (size_t)p->total * sizeof(float);
   if (which == 1) {
-    if (to_device) mle::clip_drop(p);  // overwritten whole
-    else mle::materialize(p);          // reads the clipped value, as the reference's buffer holds it
+    if (to_device) {  // overwritten whole
+      mle::clip_drop(p);
+      p->grad_pending_zero = false;
+    } else {
+      mle::materialize(p);  // reads the clipped value, as the reference's buffer holds it
+    }
   }
   return to_device ? mle_memcpy_h2d(dev, host, bytes, mle::stream()) : mle_memcpy_d2h(host, dev, bytes, mle::stream());
 }
@@ -253,6 +257,7 @@ int mle_model_grads_restore(void* h) {
   for (size_t i = 0; i < m->params.size(); ++i) {
     AdamParameter* p = m->params[i];
     mle::clip_drop(p);
+    p->grad_pending_zero = false;
     int rc = mle_memcpy_d2d(p->grad, m->grad_backup[i], (size_t)p->total * sizeof(float), mle::stream());
     if (rc) return rc;
   }

@@ -70,6 +70,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_gemm_act_bwd": (I, [P, I, I, I, I, I, F, P, I64, P, I64, F, P, I, P, P, I, P, SZ]),
     "mle_linear_bwd_ws_bytes": (SZ, [I, I, I, I]),
     "mle_linear_bwd": (I, [P, I, I, I, I, P, P, I64, P, I64, P, I, P, P, I64, P, SZ]),
+    "mle_linear_bwd_ex": (I, [P, I, I, I, I, P, P, I64, P, I64, P, I, P, P, I64, I, P, SZ]),
     "mle_colsum": (I, [P, P, SZ, I, P, F]),
     "mle_channel_sum": (I, [P, P, I, I, SZ, I, P]),
     "mle_softmax_fwd": (I, [P, P, P, I, I, I, I, I]),
@@ -99,7 +100,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_conv2d_dgrad": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, I]),
     "mle_conv2d_wgrad_ws_bytes": (SZ, [I, I, I, I, I, I, I, I, I]),
     "mle_conv2d_wgrad": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P, SZ]),
-    "mle_conv2d_wgrad_bias": (I, [P, P, P, P, P, I, I, I, I, I, I, I, I, I, P, SZ]),
+    "mle_conv2d_wgrad_bias": (I, [P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P, SZ]),
     "mle_sqnorm_ws_bytes": (SZ, [SZ]),
     "mle_grad_sqnorm": (I, [P, P, SZ, P, P, P, SZ]),
     "mle_sqrt_scale": (I, [P, P, D]),
@@ -110,6 +111,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_embed_gather": (I, [P, P, P, P, I, I, I, I]),
     "mle_embed_scatter_ws_bytes": (SZ, [I, I]),
     "mle_embed_scatter_add": (I, [P, P, P, P, I, I, I, I, I, F, P, SZ]),
+    "mle_embed_grad": (I, [P, P, P, P, I, I, I, I, I, I, P, SZ]),
     "mle_onehot": (I, [P, P, P, I, I, I, I]),
     "mle_onehot_update": (I, [P, P, P, P, I, I, I, I]),
     "mle_argmax": (I, [P, P, I, I, P]),

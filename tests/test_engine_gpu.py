@@ -439,9 +439,16 @@ def _run_sequence(kind, dims, params, inputs, lr, lazy):
     return out
 
 
-@pytest.mark.parametrize("kind", ["block", "resblock"])
+@pytest.mark.parametrize("kind", ["block", "resblock", "mlp"])
 def test_lazy_zero_matches_eager(hip, kind):
-    if kind == "block":
+    """Lazy clearing of node and parameter gradients (the first writer assigns:
+    GEMM dW / column sums, conv bias sums, the embedding scatter) gives the bits
+    of filling and adding, through accumulation without zero_grad and updates."""
+    if kind == "mlp":
+        cfg = MLPConfig()
+        x, labels, params = mlp_data(cfg, seed=5)
+        dims, inputs = cfg.dims(), [x, labels]
+    elif kind == "block":
         cfg = BlockConfig(batch=2, seq=32, d_model=64, heads=4, ffn=128, vocab=97)
         ids, tgt, params = block_data(cfg, seed=3)
         dims, inputs = cfg.dims(), [ids, tgt]

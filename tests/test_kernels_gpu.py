@@ -321,6 +321,29 @@ def test_linear_bwd(hip, orc, rows, inp, out, layers, bias, acc):
             assert_close(got_b[l * sb:l * sb + out], want_db[l], what=f"linear_bwd db {l}", **EW)
         else:
             assert np.array_equal(got_b, dbf), "db written without bias"
+    # mle_linear_bwd_ex with accumulate_dw 0: dW and db assigned (NaN before),
+    # the bits of adding into zeros; the gaps stay untouched
+    zw = [np.zeros((inp, out), np.float32) for _ in range(layers)]
+    for l in range(layers):
+        orc.call("orc_bcmm", 2, orc.ptr(X), orc.ptr(dY[l]), orc.ptr(zw[l]), 1, 1, inp, rows, out, 1, 3, 3, 3, 1.0)
+    nan_w, nan_b = dWf.copy(), dbf.copy()
+    for l in range(layers):
+        nan_w[l * sw:l * sw + inp * out] = np.nan
+        nan_b[l * sb:l * sb + out] = np.nan
+    gdW2, gdb2, gdX2 = B(hip, nan_w), B(hip, nan_b), B(hip, dX0)
+    hip.call("mle_linear_bwd_ex", None, rows, inp, out, layers, gX.ptr, gdY.ptr, sdy, gW.ptr, sw, gdX2.ptr, acc,
+             gdW2.ptr, gdb2.ptr if bias else None, sb, 0, ws.ptr, need)
+    got_w2, got_b2 = gdW2.numpy(), gdb2.numpy()
+    zero_w, zero_b = B(hip, np.where(np.isnan(nan_w), 0.0, nan_w).astype(np.float32)), \
+        B(hip, np.where(np.isnan(nan_b), 0.0, nan_b).astype(np.float32))
+    gdX3 = B(hip, dX0)
+    hip.call("mle_linear_bwd", None, rows, inp, out, layers, gX.ptr, gdY.ptr, sdy, gW.ptr, sw, gdX3.ptr, acc,
+             zero_w.ptr, zero_b.ptr if bias else None, sb, ws.ptr, need)
+    np.testing.assert_array_equal(got_w2, zero_w.numpy())
+    if bias:
+        np.testing.assert_array_equal(got_b2, zero_b.numpy())
+    for l in range(layers):
+        assert_close(got_w2[l * sw:l * sw + inp * out].reshape(inp, out), zw[l], what=f"linear_bwd_ex dW {l}", **MM)
     # errors: a short workspace (when one is needed) and zero layers
     if need:
         with pytest.raises(hip.MLEError):
@@ -694,10 +717,17 @@ def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
     dbr = db0.copy()
     orc.call("orc_channel_squeeze", orc.ptr(dy), orc.ptr(dbr), n, cout, oh * ow, cout)
     gdw2, gdb = B(hip, np.full(wt.shape, -3.0, np.float32)), B(hip, db0)
-    hip.call("mle_conv2d_wgrad_bias", None, gx.ptr, gdy.ptr, gdw2.ptr, gdb.ptr, n, cin, h, w, cout, k, k, pad, stride,
-             ws.ptr, ws.nbytes)
+    hip.call("mle_conv2d_wgrad_bias", None, gx.ptr, gdy.ptr, gdw2.ptr, gdb.ptr, 1, n, cin, h, w, cout, k, k, pad,
+             stride, ws.ptr, ws.nbytes)
     np.testing.assert_array_equal(gdw2.numpy(), gdw.numpy())
     assert_close(gdb.numpy(), dbr, what="conv bias grad", **MM)  # a sum over n * oh * ow terms
+    # accumulate_db 0: assigned over NaN, the bits of adding into zeros
+    gdb0, gdbn = B(hip, np.zeros(cout, np.float32)), B(hip, np.full(cout, np.nan, np.float32))
+    hip.call("mle_conv2d_wgrad_bias", None, gx.ptr, gdy.ptr, gdw2.ptr, gdb0.ptr, 1, n, cin, h, w, cout, k, k, pad,
+             stride, ws.ptr, ws.nbytes)
+    hip.call("mle_conv2d_wgrad_bias", None, gx.ptr, gdy.ptr, gdw2.ptr, gdbn.ptr, 0, n, cin, h, w, cout, k, k, pad,
+             stride, ws.ptr, ws.nbytes)
+    np.testing.assert_array_equal(gdbn.numpy(), gdb0.numpy())
 
 
 # ----------------------------------------------------------------- optimizer
@@ -838,6 +868,20 @@ def test_scatter_add_paths(hip, orc, batch, clen, dim, vocab, hot):
     assert_close(outs[0], ref, what="scatter add", rtol=1e-5,
                  atol_scale=1e-6 * max(1.0, float(np.sqrt(counts.max()))))
     np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    # mle_embed_grad (scale 1): accumulate 1 is scatter-add; accumulate 0
+    # assigns over NaN (rows no token reaches become 0) with the bits of
+    # scatter-adding into zeros
+    want = []
+    for base in (table, np.zeros_like(table)):
+        gt = B(hip, base)
+        hip.call("mle_embed_scatter_add", None, gt.ptr, gg.ptr, gk.ptr, batch, clen, clen, dim, vocab, 1.0, ws.ptr,
+                 ws.nbytes)
+        want.append(gt.numpy())
+    for accumulate, base, w in ((1, table, want[0]), (0, np.full_like(table, np.nan), want[1])):
+        gt = B(hip, base)
+        hip.call("mle_embed_grad", None, gt.ptr, gg.ptr, gk.ptr, batch, clen, clen, dim, vocab, accumulate, ws.ptr,
+                 ws.nbytes)
+        np.testing.assert_array_equal(gt.numpy().view(np.uint32), w.view(np.uint32))
 
 
 @pytest.mark.parametrize("off", [0, 1])  # 1: float offsets, so the scalar path runs
