@@ -285,6 +285,11 @@ int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* 
  * block count, which the reference sets to `out` in Convolute2D and to the
  * width in Broadcast_Channel (Engine/engine.cu:1435). */
 int mle_channel_sum(mle_stream stream, const float* x, int batch, int channels, size_t hw, int nreduce, float* out);
+/* mle_channel_sum with the destination's mode: accumulate 1 adds as above; 0
+ * assigns out[c] for c < nreduce and sets out[nreduce .. out_total) to 0 (out is
+ * logically zero: the engine's lazy clearing, no separate fill). */
+int mle_channel_sum_ex(mle_stream stream, const float* x, int batch, int channels, size_t hw, int nreduce, float* out,
+                       size_t out_total, int accumulate);
 
 /* ------------------------------------------------------------------------- */
 /* Softmax and losses                                                        */

@@ -4,6 +4,8 @@
 // channel reductions used by bias gradients (BCompress, Channel_Squeeze1D:
 // Engine/kernels.cu:1562-1584, 1734-1761).
 #include "common.hpp"
+
+#include <algorithm>
 #include <limits.h>
 
 using namespace mle;
@@ -378,33 +380,42 @@ __global__ __launch_bounds__(1024) void colsum_kernel(const float* __restrict__ 
 constexpr int CS_NT = 1024;
 template <bool VEC>
 __global__ __launch_bounds__(CS_NT) void channel_sum_kernel(const float* __restrict__ x, int batch, int channels,
-                                                            size_t hw, float* __restrict__ out) {
+                                                            size_t hw, float* __restrict__ out, int nreduce,
+                                                            size_t out_total, int accumulate) {
   __shared__ float red[CS_NT / 64];
   const int c = blockIdx.x;
+  if (c >= nreduce) {  // assign mode: the rest of `out` becomes 0
+    for (size_t j = nreduce + (size_t)(c - nreduce) * CS_NT + threadIdx.x; j < out_total;
+         j += (size_t)(gridDim.x - nreduce) * CS_NT)
+      out[j] = 0.f;
+    return;
+  }
+  // acc[u] takes batch items u, u + 4, ...: four loads in flight per thread.
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int b = 0; b < batch; ++b) {
-    const float* p = x + ((size_t)b * channels + c) * hw;
-    if (VEC) {
-      const f32x4* p4 = reinterpret_cast<const f32x4*>(p);
-      const size_t n4 = hw / 4;
-      size_t i = threadIdx.x;
-      for (; i + 3 * CS_NT < n4; i += 4 * CS_NT) {
+  const size_t cstride = (size_t)channels * hw;
+  const float* base = x + (size_t)c * hw;
+  int b = 0;
+  if (VEC) {
+    const size_t n4 = hw / 4;
+    for (; b + 4 <= batch; b += 4)
+      for (size_t i = threadIdx.x; i < n4; i += CS_NT) {
         f32x4 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = p4[i + u * CS_NT];
+        for (int u = 0; u < 4; ++u) v[u] = reinterpret_cast<const f32x4*>(base + (size_t)(b + u) * cstride)[i];
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[u] += (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
       }
-      for (; i < n4; i += CS_NT) {
-        const f32x4 v = p4[i];
-        acc[0] += (v[0] + v[1]) + (v[2] + v[3]);
+    for (; b < batch; ++b)
+      for (size_t i = threadIdx.x; i < n4; i += CS_NT) {
+        const f32x4 v = reinterpret_cast<const f32x4*>(base + (size_t)b * cstride)[i];
+        acc[b & 3] += (v[0] + v[1]) + (v[2] + v[3]);
       }
-    } else {
-      for (size_t i = threadIdx.x; i < hw; i += CS_NT) acc[0] += p[i];
-    }
+  } else {
+    for (; b < batch; ++b)
+      for (size_t i = threadIdx.x; i < hw; i += CS_NT) acc[b & 3] += base[(size_t)b * cstride + i];
   }
   const float t = block_sum<CS_NT>((acc[0] + acc[1]) + (acc[2] + acc[3]), red);
-  if (threadIdx.x == 0) out[c] += t;
+  if (threadIdx.x == 0) out[c] = accumulate ? out[c] + t : t;
 }
 
 // table (+)= scale * scatter(grad); assign: the table is logically zero (rows
@@ -527,13 +538,25 @@ int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* 
 }
 
 int mle_channel_sum(mle_stream stream, const float* x, int batch, int channels, size_t hw, int nreduce, float* out) {
+  return mle_channel_sum_ex(stream, x, batch, channels, hw, nreduce, out, 0, 1);
+}
+
+int mle_channel_sum_ex(mle_stream stream, const float* x, int batch, int channels, size_t hw, int nreduce, float* out,
+                       size_t out_total, int accumulate) {
   MLE_CHECK_ARG(x && out && channels > 0 && nreduce >= 0, "mle_channel_sum: bad argument");
   if (nreduce > channels) nreduce = channels;  // the reference would read and write out of bounds here
-  if (nreduce == 0) return MLE_OK;
+  MLE_CHECK_ARG(accumulate || out_total >= (size_t)nreduce, "mle_channel_sum_ex: out_total %zu < %d channels",
+                out_total, nreduce);
+  const size_t rest = accumulate ? 0 : out_total - (size_t)nreduce;
+  const unsigned zb = (unsigned)std::min<size_t>((rest + CS_NT - 1) / CS_NT, 1024);
+  const unsigned grid = (unsigned)nreduce + zb;
+  if (grid == 0) return MLE_OK;
   if (hw % 4 == 0 && aligned16(x))
-    channel_sum_kernel<true><<<nreduce, CS_NT, 0, as_stream(stream)>>>(x, batch, channels, hw, out);
+    channel_sum_kernel<true><<<grid, CS_NT, 0, as_stream(stream)>>>(x, batch, channels, hw, out, nreduce, out_total,
+                                                                    accumulate);
   else
-    channel_sum_kernel<false><<<nreduce, CS_NT, 0, as_stream(stream)>>>(x, batch, channels, hw, out);
+    channel_sum_kernel<false><<<grid, CS_NT, 0, as_stream(stream)>>>(x, batch, channels, hw, out, nreduce, out_total,
+                                                                     accumulate);
   return check_launch("mle_channel_sum");
 }
 

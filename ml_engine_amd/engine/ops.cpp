@@ -310,8 +310,11 @@ graph GraphOperations::Broadcast_Channel(const graph& A, const graph& B) {
   };
   node->backward = [=]() {
     add_grad(pa, nd->grad, 1.0, nd->total, "Broadcast Add backward - A grad");
-    mle::materialize(pb);  // reduces into (possibly only some of) B's channels
-    check(mle_channel_sum(S(), nd->grad, batch, channels, hw, nreduce, pb->grad), "Broadcast Add backward - B grad");
+    // Reduces into (possibly only some of) B's channels; a clear gradient is
+    // assigned, the rest of it set to 0 in the same launch.
+    check(mle_channel_sum_ex(S(), nd->grad, batch, channels, hw, nreduce, pb->grad, (size_t)pb->total,
+                             mle::accumulate_flag(pb)),
+          "Broadcast Add backward - B grad");
   };
   std_hooks(node);
   return node;

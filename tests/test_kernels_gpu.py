@@ -1006,6 +1006,13 @@ def test_elementwise_and_layout(hip, orc):
         gsq = B(hip, np.full(ch, 0.25, np.float32))
         hip.call("mle_channel_sum", None, gxc.ptr, bt, ch, hw, nred, gsq.ptr)
         assert_close(gsq.numpy(), sq, what=f"channel_sum {nred}", **EW)
+        # assign mode over NaN: the first nred sums (the bits of adding into 0),
+        # the rest of a 2*ch-float destination (a [2, ch] gradient) set to 0
+        g0, gn = B(hip, np.zeros(2 * ch, np.float32)), B(hip, np.full(2 * ch, np.nan, np.float32))
+        hip.call("mle_channel_sum_ex", None, gxc.ptr, bt, ch, hw, nred, g0.ptr, 2 * ch, 1)
+        hip.call("mle_channel_sum_ex", None, gxc.ptr, bt, ch, hw, nred, gn.ptr, 2 * ch, 0)
+        np.testing.assert_array_equal(gn.numpy(), g0.numpy())
+        assert not np.isnan(gn.numpy()).any()
 
     gf = hip.Buffer.zeros(1001)
     hip.call("mle_fill", None, gf.ptr, 3.5, 1001)
