@@ -188,8 +188,14 @@ int params_write_flag(const std::vector<NodeBackProp*>& ps) {
 }
 
 void materialize_params(const std::vector<AdamParameter*>& ps) {
+  // Fills only: a pending clip stays deferred (the fused update divides in
+  // registers; the other callers apply the clip themselves first).
   ZeroBatch batch;  // neighbouring parameters' fills merge into one launch
-  for (auto* p : ps) materialize(p);
+  for (auto* p : ps)
+    if (p->grad_pending_zero) {
+      p->grad_pending_zero = false;
+      zero(p->grad, p->total);
+    }
 }
 
 void materialize(NodeBackProp* n) {

@@ -94,7 +94,8 @@ void materialize(NodeBackProp* n);
 // gradients of `ps` whole in one launch asks params_write_flag for its mode:
 // 0 (assign) when every one of them is marked clear (the marks are taken),
 // otherwise the marked ones are filled and 1 (add) is returned.  Readers of
-// parameter gradients (update, norm, clip) call materialize_params first.
+// parameter gradients (update, norm, clip) call materialize_params first,
+// which fills the marked ones and leaves a pending clip deferred.
 int params_write_flag(const std::vector<NodeBackProp*>& ps);
 void materialize_params(const std::vector<AdamParameter*>& ps);
 // Lazy zeroing of a loss node's (one-float) output: zero_grad marks it, the
