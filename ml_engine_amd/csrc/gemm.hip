@@ -835,56 +835,83 @@ __global__ __launch_bounds__(NT, 2) void gemm_pair_kernel(GemmArgs g0, GemmArgs 
   }
 }
 
-// C = alpha * sum_s part[s] + beta * C and colsum += sum_s part_cs[s], in split
-// order.  Grid: x over column groups of W (4 with VEC, else 1) columns, y over
-// rows (looping when M > 65535), z over batch items -- no integer division.
-// Loads of four splits are issued together; the additions keep split order.
+// C = alpha * sum_s part[s] + beta * C (+ bias) and colsum (+)= sum_s
+// part_cs[s], in a fixed order.  A workgroup covers 64 units -- a unit is W
+// (4 with VEC, else 1) columns of one row of one batch item, numbered over
+// (batch, row, column group) so every thread has one -- with four split
+// groups: thread (unit, g) adds splits g, g + 4, g + 8, ... in order (four
+// loads in flight), and the group sums are added in group order through LDS.
+// Workgroups from `nmain` on take the column sums: one thread per (batch,
+// column), splits added in order.
 template <bool VEC>
-__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g, int64_t units, unsigned nmain) {
   constexpr int W = VEC ? 4 : 1;
-  const int col = (blockIdx.x * 256 + threadIdx.x) * W;
+  __shared__ f32x4 grp[4][64];
   const int64_t mn = (int64_t)g.M * g.N;
-  const int64_t b = blockIdx.z;
-  if (col < g.N) {
-    for (int row = blockIdx.y; row < g.M; row += gridDim.y) {
-      const float* p = g.part + b * g.splits * mn + (int64_t)row * g.N + col;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      int sp = 0;
-      for (; sp + 4 <= g.splits; sp += 4) {
-        f32x4 v[4];
+  if (blockIdx.x >= nmain) {
+    const int64_t j = (int64_t)(blockIdx.x - nmain) * 256 + threadIdx.x;
+    const int batch = (int)(units / ((int64_t)g.M * (g.N / W)));
+    if (j >= (int64_t)batch * g.N) return;
+    const int64_t b = j / g.N, col = j - b * g.N;
+    const float* p = g.part_cs + b * g.splits * (int64_t)g.N + col;
+    float acc = 0.f;
+    int sp = 0;
+    for (; sp + 4 <= g.splits; sp += 4) {
+      float v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (VEC) v[u] = *reinterpret_cast<const f32x4*>(p + (sp + u) * mn);
-          else v[u][0] = p[(sp + u) * mn];
-        }
+      for (int u = 0; u < 4; ++u) v[u] = p[(int64_t)(sp + u) * g.N];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc += v[u];
-      }
-      for (; sp < g.splits; ++sp) {
-        if (VEC) acc += *reinterpret_cast<const f32x4*>(p + sp * mn);
-        else acc[0] += p[sp * mn];
-      }
-      float* c = g.C + batch_off(b, g, g.sc, g.sc2) + (int64_t)row * g.ldc + col;
-      if (VEC) {
-        f32x4 v = g.alpha * acc;
-        if (g.beta != 0.f) v += g.beta * *reinterpret_cast<const f32x4*>(c);
-        if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + b * g.sbias + col);
-        *reinterpret_cast<f32x4*>(c) = v;
-      } else {
-        float v = g.alpha * acc[0];
-        if (g.beta != 0.f) v += g.beta * *c;
-        if (g.bias) v += g.bias[b * g.sbias + col];
-        *c = v;
-      }
+      for (int u = 0; u < 4; ++u) acc += v[u];
     }
-    if (g.colsum && blockIdx.y == 0) {
+    for (; sp < g.splits; ++sp) acc += p[(int64_t)sp * g.N];
+    put_colsum(g, b * g.scs + col, acc);
+    return;
+  }
+  const int lane = threadIdx.x & 63, sg = threadIdx.x >> 6;
+  const int64_t u = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = u < units;
+  int64_t b = 0, row = 0, col = 0;
+  if (live) {
+    const int64_t nw = g.N / W, per = (int64_t)g.M * nw;
+    b = u / per;
+    const int64_t r = u - b * per;
+    row = r / nw;
+    col = (r - row * nw) * W;
+  }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    const float* p = g.part + b * g.splits * mn + row * g.N + col;
+    int sp = sg;
+    for (; sp + 12 < g.splits; sp += 16) {
+      f32x4 v[4];
 #pragma unroll
-      for (int j = 0; j < W; ++j) {
-        float acc = 0.f;
-        for (int sp = 0; sp < g.splits; ++sp) acc += g.part_cs[(b * g.splits + sp) * g.N + col + j];
-        put_colsum(g, b * g.scs + col + j, acc);
+      for (int k = 0; k < 4; ++k) {
+        if (VEC) v[k] = *reinterpret_cast<const f32x4*>(p + (int64_t)(sp + 4 * k) * mn);
+        else v[k] = f32x4{p[(int64_t)(sp + 4 * k) * mn], 0.f, 0.f, 0.f};
       }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc += v[k];
     }
+    for (; sp < g.splits; sp += 4) {
+      if (VEC) acc += *reinterpret_cast<const f32x4*>(p + (int64_t)sp * mn);
+      else acc[0] += p[(int64_t)sp * mn];
+    }
+  }
+  grp[sg][lane] = acc;
+  __syncthreads();
+  if (sg != 0 || !live) return;
+  const f32x4 r = ((grp[0][lane] + grp[1][lane]) + grp[2][lane]) + grp[3][lane];
+  float* c = g.C + batch_off(b, g, g.sc, g.sc2) + row * g.ldc + col;
+  if (VEC) {
+    f32x4 v = g.alpha * r;
+    if (g.beta != 0.f) v += g.beta * *reinterpret_cast<const f32x4*>(c);
+    if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + b * g.sbias + col);
+    *reinterpret_cast<f32x4*>(c) = v;
+  } else {
+    float v = g.alpha * r[0];
+    if (g.beta != 0.f) v += g.beta * *c;
+    if (g.bias) v += g.bias[b * g.sbias + col];
+    *c = v;
   }
 }
 
@@ -1188,9 +1215,11 @@ static void gemm_launch_reduce(hipStream_t s, const GemmPlan& P) {
                   aligned16(g.part) && (!g.bias || (aligned16(g.bias) && g.sbias % 4 == 0));
   const int w = rv ? 4 : 1;
   const int batch = (int)P.grid.z / g.splits;
-  dim3 rgrid((unsigned)((g.N / w + 255) / 256), (unsigned)std::min(g.M, 65535), (unsigned)batch);
-  if (rv) mle::launch(split_reduce_kernel<true>, rgrid, 256, 0, s, g);
-  else mle::launch(split_reduce_kernel<false>, rgrid, 256, 0, s, g);
+  const int64_t units = (int64_t)batch * g.M * (g.N / w);
+  const unsigned nmain = (unsigned)((units + 63) / 64);
+  const unsigned ncs = g.colsum ? (unsigned)(((int64_t)batch * g.N + 255) / 256) : 0u;
+  if (rv) mle::launch(split_reduce_kernel<true>, nmain + ncs, 256, 0, s, g, units, nmain);
+  else mle::launch(split_reduce_kernel<false>, nmain + ncs, 256, 0, s, g, units, nmain);
 }
 
 // Work items of a plan that launch_tile would run on gemm_direct_kernel (one
