@@ -376,6 +376,21 @@ int mle_softmax_xent_keys_fwd_rowstats(mle_stream stream, const float* logits, c
 size_t mle_norm_ws_bytes(int batch, int channels, size_t hw, int groups);
 int mle_norm_fwd(mle_stream stream, const float* x, float* y, float* stats,
                  int batch, int channels, size_t hw, int groups, float eps, void* ws, size_t ws_bytes);
+/* mle_norm_fwd whose first pass (per-chunk statistics of x) already ran in
+ * mle_add_norm_partials on the same workspace: stats_ready 1 runs only the
+ * normalisation (0 is mle_norm_fwd).  Contiguous groups (LayerNorm,
+ * GroupNorm, InstanceNorm). */
+int mle_norm_fwd_ex(mle_stream stream, const float* x, float* y, float* stats, int batch, int channels, size_t hw,
+                    int groups, float eps, void* ws, size_t ws_bytes, int stats_ready);
+/* y = a + b[i mod b_period] (the residual Add, b_period = the size; MatPE's
+ * table add, b_period = rows * cols) fused with the first pass of the group
+ * normalisation that reads y: the per-chunk statistics go to that
+ * normalisation's workspace, computed exactly as mle_norm_fwd computes them
+ * from y, so the normalised output is bit-identical.  (Add forward,
+ * Engine/engine.cu:1630-1672; MatPE, Engine/kernels.cu:166; LayerMean and
+ * LayerStd, Engine/kernels.cu:541, 670.) */
+int mle_add_norm_partials(mle_stream stream, const float* a, const float* b, size_t b_period, float* y, int batch,
+                          int channels, size_t hw, int groups, void* ws, size_t ws_bytes);
 /* dx (+)= r * (dy - sum(dy)/N - y * sum(dy*y)/N), r = rsqrt(ssd/N + eps).
  * LayerBackward / GroupBackward (Engine/kernels.cu:849-896) after the ggamma
  * reductions of Engine/engine.cu:3116-3130 / 3262-3276.  With

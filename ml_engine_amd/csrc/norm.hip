@@ -103,6 +103,64 @@ __global__ __launch_bounds__(NT) void norm_stats_partial(const float* __restrict
   }
 }
 
+// Pass 1 fused into the producer of x: y = a + b (b read at i % b_period, a
+// broadcast over the groups when b_period < N), stored, then this chunk's
+// (mean, M2) exactly as norm_stats_partial computes them from y (same
+// element-to-thread map, same double sums and block reduction), so the
+// normalisation that follows is bit-identical.  Contiguous groups only.
+template <bool VEC>
+__global__ __launch_bounds__(NT) void add_stats_partial(const float* __restrict__ a, const float* __restrict__ b,
+                                                        size_t b_period, float* __restrict__ y, NormShape sh,
+                                                        double* __restrict__ part) {
+  __shared__ double red[NT / 64];
+  const int g = blockIdx.y, ck = blockIdx.x;
+  const size_t c0 = (size_t)ck * CH;
+  float v[VPT];
+  if (VEC) {
+#pragma unroll
+    for (int u = 0; u < VPT / 4; ++u) {
+      const size_t e = elem<true>(c0, 4 * u);
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      if (e < sh.N) {
+        const size_t o = at<false>(sh, g, e);
+        t = *reinterpret_cast<const f32x4*>(a + o) + *reinterpret_cast<const f32x4*>(b + o % b_period);
+        *reinterpret_cast<f32x4*>(y + o) = t;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * u + k] = t[k];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const size_t e = elem<false>(c0, i);
+      v[i] = 0.f;
+      if (e < sh.N) {
+        const size_t o = at<false>(sh, g, e);
+        v[i] = a[o] + b[o % b_period];
+        y[o] = v[i];
+      }
+    }
+  }
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) s += v[i];
+  s = block_sum<NT>(s, red);
+  const size_t n_c = (sh.N - c0 < (size_t)CH) ? sh.N - c0 : (size_t)CH;
+  const double mean = s / (double)n_c;
+  double m2 = 0.0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const double d = (double)v[i] - mean;
+    if (elem<VEC>(c0, i) < sh.N) m2 += d * d;
+  }
+  m2 = block_sum<NT>(m2, red);
+  if (threadIdx.x == 0) {
+    double* p = part + ((size_t)g * sh.nchunk + ck) * 2;
+    p[0] = mean;
+    p[1] = m2;
+  }
+}
+
 // Chunk c's element count.
 __device__ __forceinline__ double chunk_n(const NormShape& sh, int c) {
   const size_t c0 = (size_t)c * CH;
@@ -314,10 +372,16 @@ bool vec_ok(const NormShape& sh, std::initializer_list<const void*> ptrs) {
 // Workspace: per-chunk partials, then the per-group finals.
 size_t ws_need(const NormShape& sh) { return ((size_t)sh.groups_tot * sh.nchunk * 2 + (size_t)sh.groups_tot * 2) * sizeof(double); }
 
-void launch_fwd(hipStream_t s, const NormShape& sh, const float* x, float* y, float* stats, void* ws, float eps) {
+void launch_fwd(hipStream_t s, const NormShape& sh, const float* x, float* y, float* stats, void* ws, float eps,
+                bool stats_ready = false) {
   dim3 grid(sh.nchunk, sh.groups_tot);
   double* part = static_cast<double*>(ws);
   const bool v = vec_ok(sh, {x, y});
+  if (stats_ready && !sh.seg) {  // pass 1 ran in the producer of x
+    if (v) norm_apply<false, true><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+    else norm_apply<false, false><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+    return;
+  }
   if (sh.seg) {
     if (v) norm_stats_partial<true, true><<<grid, NT, 0, s>>>(x, sh, part);
     else norm_stats_partial<true, false><<<grid, NT, 0, s>>>(x, sh, part);
@@ -478,6 +542,35 @@ int mle_norm_fwd(mle_stream stream, const float* x, float* y, float* stats, int 
   if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_fwd: workspace too small");
   launch_fwd(as_stream(stream), sh, x, y, stats, ws, eps);
   return check_launch("mle_norm_fwd");
+}
+
+int mle_norm_fwd_ex(mle_stream stream, const float* x, float* y, float* stats, int batch, int channels, size_t hw,
+                    int groups, float eps, void* ws, size_t ws_bytes, int stats_ready) {
+  MLE_CHECK_ARG(x && y && stats && ws, "mle_norm_fwd: null pointer");
+  NormShape sh;
+  int rc = shape_of(batch, channels, hw, groups, sh);
+  if (rc) return rc;
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_fwd: workspace too small");
+  launch_fwd(as_stream(stream), sh, x, y, stats, ws, eps, stats_ready != 0);
+  return check_launch("mle_norm_fwd");
+}
+
+int mle_add_norm_partials(mle_stream stream, const float* a, const float* b, size_t b_period, float* y, int batch,
+                          int channels, size_t hw, int groups, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(a && b && y && ws && b_period > 0, "mle_add_norm_partials: bad argument");
+  NormShape sh;
+  int rc = shape_of(batch, channels, hw, groups, sh);
+  if (rc) return rc;
+  const size_t total = (size_t)batch * channels * hw;
+  MLE_CHECK_ARG(total % b_period == 0, "mle_add_norm_partials: b period %zu does not divide %zu", b_period, total);
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_add_norm_partials: workspace too small");
+  dim3 grid(sh.nchunk, sh.groups_tot);
+  double* part = static_cast<double*>(ws);
+  const bool v = vec_ok(sh, {a, b, y}) && b_period % 4 == 0;
+  hipStream_t s = as_stream(stream);
+  if (v) add_stats_partial<true><<<grid, NT, 0, s>>>(a, b, b_period, y, sh, part);
+  else add_stats_partial<false><<<grid, NT, 0, s>>>(a, b, b_period, y, sh, part);
+  return check_launch("mle_add_norm_partials");
 }
 
 int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, const float* stats, int batch,

@@ -195,6 +195,12 @@ struct NodeBackProp {
   // softmax cross-entropy with key targets takes over the node's forward with
   // it and never reads the output again (the hook is cleared then).
   std::function<void(float* rowpart, int64_t ldp)> forward_rowstats;
+  // Set by Add and MatrixPositionalEncoding (additive): computes this node's
+  // output as its forward does and also the first pass of a group
+  // normalisation of it (`groups` groups) into that normalisation's workspace.
+  // A following LayerNorm / GroupNorm takes over the node's forward with it
+  // and skips its own statistics pass (the hook is cleared then).
+  std::function<void(int groups, void* ws, size_t ws_bytes)> forward_normstats;
 
   virtual void update(const float lr = LEARNING_RATE, const bool W = ADAMW) {}
   NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation);

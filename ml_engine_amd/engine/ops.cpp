@@ -160,8 +160,17 @@ graph norm_node(const graph& X, int groups, const str& name) {
   NodeBackProp *nd = node.get(), *x = X.get();
   // LayerBackward's C == 1 guard (applies to groups == 1 only), as built
   const int ref_layout = mle::quirks().layernorm_reference_layout ? 1 : 0;
+  // An Add or MatPE producer computes the statistics pass with its output.
+  int ready = 0;
+  if (mle::fusion_enabled() && X->forward_normstats) {
+    auto fs = X->forward_normstats;
+    X->forward = [fs, groups, ws, ws_bytes]() { fs(groups, ws, ws_bytes); };
+    X->forward_normstats = nullptr;
+    ready = 1;
+  }
   node->forward = [=]() {
-    check(mle_norm_fwd(S(), x->output, nd->output, stats, a, b, hw, groups, eps, ws, ws_bytes), name + " forward");
+    check(mle_norm_fwd_ex(S(), x->output, nd->output, stats, a, b, hw, groups, eps, ws, ws_bytes, ready),
+          name + " forward");
   };
   node->backward = [=]() {
     check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, ref_layout, ws, ws_bytes,
@@ -285,6 +294,11 @@ graph GraphOperations::MatrixPositionalEncoding(const graph& X, const int start_
   node->forward = [=]() {
     check(mle_add_broadcast(S(), x->output, pe, nd->output, batch, (size_t)rows * cols), "MatPE forward");
   };
+  node->forward_normstats = [=](int groups, void* ws, size_t ws_bytes) {
+    check(mle_add_norm_partials(S(), x->output, pe, (size_t)rows * cols, nd->output, batch, 1, (size_t)rows * cols,
+                                groups, ws, ws_bytes),
+          "MatPE forward (with the normalisation statistics)");
+  };
   node->backward = [=]() { add_grad(x, nd->grad, 1.0, nd->total, "MatPE backward"); };
   std_hooks(node);
   return node;
@@ -351,6 +365,15 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
     check(mle_scale_add(S(), pa->output, pb->output, nd->output, 1.0f, nd->total), "Add forward");
     if (last) check(mle_read_scalar(S(), nd->output, &GraphOperations::loss), "Add loss");
   };
+  if (!last) {
+    const int d0 = A->dim[0], d1 = A->dim[1];
+    const size_t d23 = (size_t)A->dim[2] * A->dim[3];
+    node->forward_normstats = [=](int groups, void* ws, size_t ws_bytes) {
+      check(mle_add_norm_partials(S(), pa->output, pb->output, (size_t)nd->total, nd->output, d0, d1, d23, groups, ws,
+                                  ws_bytes),
+            "Add forward (with the normalisation statistics)");
+    };
+  }
   node->backward = [=]() {
     if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
     if (pa != pb && pa->grad != pb->grad) {  // one pass over the output gradient

@@ -528,6 +528,26 @@ def test_norm(hip, orc, batch, channels, hw, groups):
     hip.call("mle_norm_bwd", None, gyr.ptr, gdy.ptr, gdx.ptr, gstr.ptr, batch, channels, hw, groups, 1e-5, 1,
              ws.ptr, ws.nbytes, 0)
     assert_close(gdx.numpy(), dxz, what="norm bwd assign", **EW)
+    # The statistics pass fused into the producer (residual Add: b of the same
+    # size; MatPE: b one sample long, broadcast over the batch) gives the sum,
+    # the statistics and the normalised output of add-then-normalise bit for bit.
+    total = x.size
+    for period in (total, channels * hw):
+        a = r.standard_normal(shape, dtype=np.float32)
+        bvec = r.standard_normal(period, dtype=np.float32)
+        ga, gb = B(hip, a), B(hip, bvec)
+        want_s = (a.reshape(-1, period) + bvec).reshape(shape).astype(np.float32)
+        gs1, gy1, gst1 = B(hip, want_s), hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * batch * groups)
+        hip.call("mle_norm_fwd", None, gs1.ptr, gy1.ptr, gst1.ptr, batch, channels, hw, groups, 1e-5, ws.ptr,
+                 ws.nbytes)
+        gs2, gy2, gst2 = hip.Buffer.zeros(shape), hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * batch * groups)
+        hip.call("mle_add_norm_partials", None, ga.ptr, gb.ptr, period, gs2.ptr, batch, channels, hw, groups, ws.ptr,
+                 ws.nbytes)
+        hip.call("mle_norm_fwd_ex", None, gs2.ptr, gy2.ptr, gst2.ptr, batch, channels, hw, groups, 1e-5, ws.ptr,
+                 ws.nbytes, 1)
+        np.testing.assert_array_equal(gs2.numpy().view(np.uint32), want_s.view(np.uint32))
+        np.testing.assert_array_equal(gst2.numpy().view(np.uint32), gst1.numpy().view(np.uint32))
+        np.testing.assert_array_equal(gy2.numpy().view(np.uint32), gy1.numpy().view(np.uint32))
 
 
 @pytest.mark.parametrize("batch,channels,hw", [(4, 3, 25), (16, 128, 64 * 64), (3, 5, 4099), (1, 1, 9000)])
