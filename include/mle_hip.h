@@ -389,6 +389,20 @@ int mle_norm_fwd_ex(mle_stream stream, const float* x, float* y, float* stats, i
  * from y, so the normalised output is bit-identical.  (Add forward,
  * Engine/engine.cu:1630-1672; MatPE, Engine/kernels.cu:166; LayerMean and
  * LayerStd, Engine/kernels.cu:541, 670.) */
+/* A group normalisation followed by an activation (GroupNorm -> SiLU in the
+ * residual block, Engine/diffusion.cu:129-137; SILU / RELU / GELU ops,
+ * Engine/engine.cu:2650-2780):
+ *   mle_norm_fwd_act: mle_norm_fwd_ex, and act_out = act(y) from the same pass.
+ *   mle_norm_bwd_act: dy (+)= act'(y) * da (accumulate_dy 1 adds), stored --
+ *     the activation's backward -- then mle_norm_bwd from that dy, with its
+ *     statistics pass reading da and y once for both.
+ * The same values as the activation and normalisation kernels run one after
+ * the other. */
+int mle_norm_fwd_act(mle_stream stream, const float* x, float* y, float* act_out, int kind, float* stats, int batch,
+                     int channels, size_t hw, int groups, float eps, void* ws, size_t ws_bytes, int stats_ready);
+int mle_norm_bwd_act(mle_stream stream, const float* y, const float* da, int kind, float* dy, int accumulate_dy,
+                     float* dx, const float* stats, int batch, int channels, size_t hw, int groups, float eps,
+                     int reference_layout, void* ws, size_t ws_bytes, int accumulate);
 int mle_add_norm_partials(mle_stream stream, const float* a, const float* b, size_t b_period, float* y, int batch,
                           int channels, size_t hw, int groups, void* ws, size_t ws_bytes);
 /* dx (+)= r * (dy - sum(dy)/N - y * sum(dy*y)/N), r = rsqrt(ssd/N + eps).

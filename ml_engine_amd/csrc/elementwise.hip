@@ -181,11 +181,16 @@ struct ActBwdOp {  // dx (+)= dy * f'(x); acc = false assigns (dx is not read)
   const float* dy;
   float* dx;
   bool acc;
+  // The product is rounded before the add (never contracted into an fma), so
+  // the normalisation kernels that form this gradient in their own pass
+  // (mle_norm_bwd_act) give the same bits.
   __device__ void one(size_t i) const {
+#pragma clang fp contract(off)
     const float v = act_df<K>(x[i]) * dy[i];
     dx[i] = acc ? dx[i] + v : v;
   }
   __device__ void vec(size_t i) const {
+#pragma clang fp contract(off)
     f32x4 a = ld4(x, i), g = ld4(dy, i), d;
 #pragma unroll
     for (int j = 0; j < 4; ++j) d[j] = act_df<K>(a[j]) * g[j];

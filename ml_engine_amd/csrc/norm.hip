@@ -13,9 +13,11 @@
 //   pass 2: each chunk's workgroup combines its group's chunk partials in a
 //           fixed order (Chan et al. pairwise update) and normalises.
 // The backward uses the same split for sum(dy) and sum(dy*y).
+#include "activation.hpp"
 #include "common.hpp"
 
 #include <initializer_list>
+#include <type_traits>
 
 using namespace mle;
 
@@ -70,6 +72,26 @@ __device__ __forceinline__ void load_chunk(const float* __restrict__ src, const 
     for (int i = 0; i < VPT; ++i) {
       const size_t e = elem<false>(c0, i);
       v[i] = (e < sh.N) ? src[at<SEG>(sh, g, e)] : 0.f;
+    }
+  }
+}
+
+// Inverse of load_chunk: the chunk's in-range elements from registers.
+template <bool SEG, bool VEC>
+__device__ __forceinline__ void store_chunk(float* __restrict__ dst, const NormShape& sh, int g, size_t c0,
+                                            const float (&v)[VPT]) {
+  if (VEC) {
+#pragma unroll
+    for (int u = 0; u < VPT / 4; ++u) {
+      const size_t e = elem<true>(c0, 4 * u);
+      if (e < sh.N)
+        *reinterpret_cast<f32x4*>(dst + at<SEG>(sh, g, e)) = f32x4{v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]};
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const size_t e = elem<false>(c0, i);
+      if (e < sh.N) dst[at<SEG>(sh, g, e)] = v[i];
     }
   }
 }
@@ -218,10 +240,12 @@ __device__ __forceinline__ void group_sums(const double* __restrict__ part, cons
   b = __shfl(b, 0, 64);
 }
 
-template <bool SEG, bool VEC>
+// ACT >= 0 (an mle_act_kind): also act_out = act(y), the activation that
+// follows the normalisation (same formula as the activation kernels).
+template <bool SEG, bool VEC, int ACT = -1>
 __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, float* __restrict__ y,
                                                  float* __restrict__ stats, NormShape sh, const double* __restrict__ part,
-                                                 float eps) {
+                                                 float eps, float* __restrict__ act_out = nullptr) {
   const int g = blockIdx.y, ck = blockIdx.x;
   double mean_d, m2_d;
   group_stats(part, sh, g, mean_d, m2_d);
@@ -243,6 +267,12 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
 #pragma unroll
         for (int k = 0; k < 4; ++k) yv[k] = (xv[k] - mean) * r;
         *reinterpret_cast<f32x4*>(y + o) = yv;
+        if (ACT >= 0) {
+          f32x4 av;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) av[k] = act_f<ACT < 0 ? 0 : ACT>(yv[k]);
+          *reinterpret_cast<f32x4*>(act_out + o) = av;
+        }
       }
     }
   } else {
@@ -251,22 +281,43 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
       const size_t e = elem<false>(c0, i);
       if (e < sh.N) {
         const size_t o = at<SEG>(sh, g, e);
-        y[o] = (x[o] - mean) * r;
+        const float yo = (x[o] - mean) * r;
+        y[o] = yo;
+        if (ACT >= 0) act_out[o] = act_f<ACT < 0 ? 0 : ACT>(yo);
       }
     }
   }
 }
 
-// Backward pass 1: per chunk sum(dy) and sum(dy * y) in double.
-template <bool SEG, bool VEC>
+// Backward pass 1: per chunk sum(dy) and sum(dy * y) in double.  ACT >= 0:
+// dy is first formed from the gradient `da` of the activation that follows
+// the normalisation, dy (+)= act'(y) * da (acc_dy 1 adds to the stored dy),
+// exactly as the activation's backward kernel forms it, and stored.
+template <bool SEG, bool VEC, int ACT = -1>
 __global__ __launch_bounds__(NT) void norm_bwd_partial(const float* __restrict__ y, const float* __restrict__ dy,
-                                                       NormShape sh, double* __restrict__ part) {
+                                                       NormShape sh, double* __restrict__ part,
+                                                       const float* __restrict__ da = nullptr,
+                                                       float* __restrict__ dy_out = nullptr, int acc_dy = 0) {
   __shared__ double red[NT / 64];
   const int g = blockIdx.y, ck = blockIdx.x;
   const size_t c0 = (size_t)ck * CH;
   float yv[VPT], gv[VPT];
   load_chunk<SEG, VEC>(y, sh, g, c0, yv);
-  load_chunk<SEG, VEC>(dy, sh, g, c0, gv);
+  if (ACT >= 0) {
+    float av[VPT];
+    load_chunk<SEG, VEC>(da, sh, g, c0, av);
+    if (acc_dy) load_chunk<SEG, VEC>(dy_out, sh, g, c0, gv);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      // product rounded, then the add (no fma): the activation kernel's steps
+#pragma clang fp contract(off)
+      const float v = act_df<ACT < 0 ? 0 : ACT>(yv[i]) * av[i];
+      gv[i] = acc_dy ? gv[i] + v : v;
+    }
+    store_chunk<SEG, VEC>(dy_out, sh, g, c0, gv);
+  } else {
+    load_chunk<SEG, VEC>(dy, sh, g, c0, gv);
+  }
   double sg = 0.0, sgy = 0.0;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
@@ -372,43 +423,71 @@ bool vec_ok(const NormShape& sh, std::initializer_list<const void*> ptrs) {
 // Workspace: per-chunk partials, then the per-group finals.
 size_t ws_need(const NormShape& sh) { return ((size_t)sh.groups_tot * sh.nchunk * 2 + (size_t)sh.groups_tot * 2) * sizeof(double); }
 
-void launch_fwd(hipStream_t s, const NormShape& sh, const float* x, float* y, float* stats, void* ws, float eps,
-                bool stats_ready = false) {
-  dim3 grid(sh.nchunk, sh.groups_tot);
-  double* part = static_cast<double*>(ws);
-  const bool v = vec_ok(sh, {x, y});
-  if (stats_ready && !sh.seg) {  // pass 1 ran in the producer of x
-    if (v) norm_apply<false, true><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
-    else norm_apply<false, false><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
-    return;
-  }
-  if (sh.seg) {
-    if (v) norm_stats_partial<true, true><<<grid, NT, 0, s>>>(x, sh, part);
-    else norm_stats_partial<true, false><<<grid, NT, 0, s>>>(x, sh, part);
-    if (v) norm_apply<true, true><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
-    else norm_apply<true, false><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
-  } else {
-    if (v) norm_stats_partial<false, true><<<grid, NT, 0, s>>>(x, sh, part);
-    else norm_stats_partial<false, false><<<grid, NT, 0, s>>>(x, sh, part);
-    if (v) norm_apply<false, true><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
-    else norm_apply<false, false><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps);
+// f(std::integral_constant<int, K>) for the activation kind K (-1: none).
+template <class F>
+void with_act(int kind, F f) {
+  switch (kind) {
+    case MLE_RELU: f(std::integral_constant<int, MLE_RELU>{}); break;
+    case MLE_GELU: f(std::integral_constant<int, MLE_GELU>{}); break;
+    case MLE_SILU: f(std::integral_constant<int, MLE_SILU>{}); break;
+    case MLE_TANH: f(std::integral_constant<int, MLE_TANH>{}); break;
+    case MLE_SIGMOID: f(std::integral_constant<int, MLE_SIGMOID>{}); break;
+    case MLE_LEAKY_RELU: f(std::integral_constant<int, MLE_LEAKY_RELU>{}); break;
+    default: f(std::integral_constant<int, -1>{}); break;
   }
 }
 
+// act >= 0: the normalisation also writes act_out = act(y).
+void launch_fwd(hipStream_t s, const NormShape& sh, const float* x, float* y, float* stats, void* ws, float eps,
+                bool stats_ready = false, int act = -1, float* act_out = nullptr) {
+  dim3 grid(sh.nchunk, sh.groups_tot);
+  double* part = static_cast<double*>(ws);
+  const bool v = vec_ok(sh, {x, y}) && (act < 0 || aligned16(act_out));
+  if (!stats_ready || sh.seg) {  // otherwise pass 1 ran in the producer of x
+    if (sh.seg) {
+      if (v) norm_stats_partial<true, true><<<grid, NT, 0, s>>>(x, sh, part);
+      else norm_stats_partial<true, false><<<grid, NT, 0, s>>>(x, sh, part);
+    } else {
+      if (v) norm_stats_partial<false, true><<<grid, NT, 0, s>>>(x, sh, part);
+      else norm_stats_partial<false, false><<<grid, NT, 0, s>>>(x, sh, part);
+    }
+  }
+  with_act(act, [&](auto K) {
+    constexpr int A = decltype(K)::value;
+    if (sh.seg) {
+      if (v) norm_apply<true, true, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out);
+      else norm_apply<true, false, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out);
+    } else {
+      if (v) norm_apply<false, true, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out);
+      else norm_apply<false, false, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out);
+    }
+  });
+}
+
+// act >= 0: dy (+)= act'(y) * da first (acc_dy), stored, then the backward
+// from it.
 void launch_bwd(hipStream_t s, const NormShape& sh, const float* y, const float* dy, float* dx, const float* stats,
-                void* ws, float eps, size_t quirk, int accumulate) {
+                void* ws, float eps, size_t quirk, int accumulate, int act = -1, const float* da = nullptr,
+                int acc_dy = 0) {
   dim3 grid(sh.nchunk, sh.groups_tot);
   double* part = static_cast<double*>(ws);
   double* fin = part + (size_t)sh.groups_tot * sh.nchunk * 2;
-  const bool v = vec_ok(sh, {y, dy, dx});
+  const bool v = vec_ok(sh, {y, dy, dx}) && (act < 0 || aligned16(da));
+  float* dyw = const_cast<float*>(dy);  // written only with act >= 0
+  with_act(act, [&](auto K) {
+    constexpr int A = decltype(K)::value;
+    if (sh.seg) {
+      if (v) norm_bwd_partial<true, true, A><<<grid, NT, 0, s>>>(y, dy, sh, part, da, dyw, acc_dy);
+      else norm_bwd_partial<true, false, A><<<grid, NT, 0, s>>>(y, dy, sh, part, da, dyw, acc_dy);
+    } else {
+      if (v) norm_bwd_partial<false, true, A><<<grid, NT, 0, s>>>(y, dy, sh, part, da, dyw, acc_dy);
+      else norm_bwd_partial<false, false, A><<<grid, NT, 0, s>>>(y, dy, sh, part, da, dyw, acc_dy);
+    }
+  });
   if (sh.seg) {
-    if (v) norm_bwd_partial<true, true><<<grid, NT, 0, s>>>(y, dy, sh, part);
-    else norm_bwd_partial<true, false><<<grid, NT, 0, s>>>(y, dy, sh, part);
     if (v) norm_bwd_apply<true, true><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, 0, accumulate);
     else norm_bwd_apply<true, false><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, 0, accumulate);
   } else {
-    if (v) norm_bwd_partial<false, true><<<grid, NT, 0, s>>>(y, dy, sh, part);
-    else norm_bwd_partial<false, false><<<grid, NT, 0, s>>>(y, dy, sh, part);
     if (quirk) norm_bwd_final<<<sh.groups_tot, 64, 0, s>>>(part, sh, fin);
     if (v) norm_bwd_apply<false, true><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, quirk, accumulate);
     else norm_bwd_apply<false, false><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, quirk, accumulate);
@@ -553,6 +632,32 @@ int mle_norm_fwd_ex(mle_stream stream, const float* x, float* y, float* stats, i
   if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_fwd: workspace too small");
   launch_fwd(as_stream(stream), sh, x, y, stats, ws, eps, stats_ready != 0);
   return check_launch("mle_norm_fwd");
+}
+
+int mle_norm_fwd_act(mle_stream stream, const float* x, float* y, float* act_out, int kind, float* stats, int batch,
+                     int channels, size_t hw, int groups, float eps, void* ws, size_t ws_bytes, int stats_ready) {
+  MLE_CHECK_ARG(x && y && act_out && stats && ws && kind >= MLE_RELU && kind <= MLE_LEAKY_RELU,
+                "mle_norm_fwd_act: bad argument");
+  NormShape sh;
+  int rc = shape_of(batch, channels, hw, groups, sh);
+  if (rc) return rc;
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_fwd_act: workspace too small");
+  launch_fwd(as_stream(stream), sh, x, y, stats, ws, eps, stats_ready != 0, kind, act_out);
+  return check_launch("mle_norm_fwd_act");
+}
+
+int mle_norm_bwd_act(mle_stream stream, const float* y, const float* da, int kind, float* dy, int accumulate_dy,
+                     float* dx, const float* stats, int batch, int channels, size_t hw, int groups, float eps,
+                     int reference_layout, void* ws, size_t ws_bytes, int accumulate) {
+  MLE_CHECK_ARG(y && da && dy && dx && stats && ws && kind >= MLE_RELU && kind <= MLE_LEAKY_RELU,
+                "mle_norm_bwd_act: bad argument");
+  NormShape sh;
+  int rc = shape_of(batch, channels, hw, groups, sh);
+  if (rc) return rc;
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_bwd_act: workspace too small");
+  const size_t quirk = (reference_layout && groups == 1 && channels > 1) ? hw : 0;
+  launch_bwd(as_stream(stream), sh, y, dy, dx, stats, ws, eps, quirk, accumulate, kind, da, accumulate_dy);
+  return check_launch("mle_norm_bwd_act");
 }
 
 int mle_add_norm_partials(mle_stream stream, const float* a, const float* b, size_t b_period, float* y, int batch,

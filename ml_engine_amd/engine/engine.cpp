@@ -783,6 +783,10 @@ void GraphOperations::backward(const graph& X, const bool show, const bool time,
     return;
   }
   mle::clip_apply_all();  // parameter gradients are added into: give them their clipped values
+  for (auto& n : nodes) n->consumers = 0;
+  for (auto& n : nodes)
+    for (auto& in : n->inputs)
+      if (in) in->consumers++;
   for (auto it = nodes.rbegin(); it != nodes.rend(); ++it) {
     std::chrono::high_resolution_clock::time_point t0;
     if (time) {

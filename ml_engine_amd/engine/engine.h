@@ -201,6 +201,21 @@ struct NodeBackProp {
   // A following LayerNorm / GroupNorm takes over the node's forward with it
   // and skips its own statistics pass (the hook is cleared then).
   std::function<void(int groups, void* ws, size_t ws_bytes)> forward_normstats;
+  // Set by the normalisations (additive): computes this node's output as its
+  // forward does and also act(output) into act_out, in the same pass.  An
+  // activation node on this output takes over the forward with it.
+  std::function<void(int kind, float* act_out)> forward_act;
+  // Backward hand-off (additive): an activation whose input is this node, and
+  // which is this node's only consumer, leaves its gradient here instead of
+  // forming this node's gradient; this node's backward forms it (kind, and
+  // whether it adds to the stored gradient) in its own first pass.
+  const float* act_grad_in = nullptr;
+  int act_grad_kind = -1;
+  int act_grad_acc = 0;
+  bool takes_act_grad = false;  // this node's backward handles act_grad_in
+  // Number of nodes reading this node's output in the graph being
+  // back-propagated (set by GraphOperations::backward).
+  int consumers = 0;
 
   virtual void update(const float lr = LEARNING_RATE, const bool W = ADAMW) {}
   NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation);

@@ -123,7 +123,24 @@ graph act_node(const graph& input, int kind, const str& name) {
   node->inputs = {input};
   NodeBackProp *nd = node.get(), *x = input.get();
   node->forward = [=]() { check(mle_act_fwd(S(), kind, x->output, nd->output, nd->total), name + " forward"); };
+  // After a normalisation: its pass writes this activation's output too, and
+  // when this node is the normalisation's only consumer, the normalisation's
+  // backward forms its gradient from ours in its first pass.
+  bool fused = false;
+  if (mle::fusion_enabled() && input->forward_act) {
+    auto fa = input->forward_act;
+    input->forward = [fa, kind, nd]() { fa(kind, nd->output); };
+    input->forward_act = nullptr;
+    node->forward = []() {};
+    fused = true;
+  }
   node->backward = [=]() {
+    if (fused && x->takes_act_grad && x->consumers == 1) {
+      x->act_grad_in = nd->grad;
+      x->act_grad_kind = kind;
+      x->act_grad_acc = mle::accumulate_flag(x);
+      return;
+    }
     check(mle_act_bwd(S(), kind, x->output, nd->grad, x->grad, nd->total, mle::accumulate_flag(x)), "Deriv " + name);
   };
   std_hooks(node);
@@ -172,7 +189,21 @@ graph norm_node(const graph& X, int groups, const str& name) {
     check(mle_norm_fwd_ex(S(), x->output, nd->output, stats, a, b, hw, groups, eps, ws, ws_bytes, ready),
           name + " forward");
   };
+  node->forward_act = [=](int kind, float* act_out) {
+    check(mle_norm_fwd_act(S(), x->output, nd->output, act_out, kind, stats, a, b, hw, groups, eps, ws, ws_bytes,
+                           ready),
+          name + " forward (with the activation after it)");
+  };
+  node->takes_act_grad = true;
   node->backward = [=]() {
+    if (nd->act_grad_in) {  // the activation after this node left its gradient (see act_node)
+      const float* da = nd->act_grad_in;
+      nd->act_grad_in = nullptr;
+      check(mle_norm_bwd_act(S(), nd->output, da, nd->act_grad_kind, nd->grad, nd->act_grad_acc, x->grad, stats, a,
+                             b, hw, groups, eps, ref_layout, ws, ws_bytes, mle::accumulate_flag(x)),
+            name + " backward (with the activation after it)");
+      return;
+    }
     check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, ref_layout, ws, ws_bytes,
                        mle::accumulate_flag(x)),
           name + " backward");

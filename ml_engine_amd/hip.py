@@ -90,6 +90,8 @@ SIGNATURES: dict[str, tuple] = {
     "mle_norm_fwd": (I, [P, P, P, P, I, I, SZ, I, F, P, SZ]),
     "mle_norm_fwd_ex": (I, [P, P, P, P, I, I, SZ, I, F, P, SZ, I]),
     "mle_add_norm_partials": (I, [P, P, P, SZ, P, I, I, SZ, I, P, SZ]),
+    "mle_norm_fwd_act": (I, [P, P, P, P, I, P, I, I, SZ, I, F, P, SZ, I]),
+    "mle_norm_bwd_act": (I, [P, P, P, I, P, I, P, P, I, I, SZ, I, F, I, P, SZ, I]),
     "mle_norm_bwd": (I, [P, P, P, P, P, I, I, SZ, I, F, I, P, SZ, I]),
     "mle_batchnorm_ws_bytes": (SZ, [I, I, SZ]),
     "mle_batchnorm_fwd": (I, [P, P, P, P, I, I, SZ, F, P, SZ]),

@@ -310,6 +310,33 @@ def test_block_qkv_fusion(hip, quirks):
         assert np.abs(gf[i] - gu[i]).max() <= 1e-4 * scale, (i, np.abs(gf[i] - gu[i]).max(), scale)
 
 
+def test_resblock_fusion_matches_unfused(hip):
+    """C5 residual block with the graph fusions (GroupNorm -> SiLU in one pass
+    each way) against one kernel per op: the same loss, parameter gradients
+    and, through the backward hand-off, the same bits, over a step with an
+    update and a backward without zero_grad."""
+    from ml_engine_amd.models import STEP_BACKWARD, STEP_FORWARD
+    cfg = ResBlockConfig(batch=2, cin=8, cout=16, h=12, w=12, groups=4, tdim=32)
+    x, noise, t, params = resblock_data(cfg, seed=9)
+    runs = {}
+    for fuse in (True, False):
+        m = Model("resblock", cfg.dims(t), fuse=fuse)
+        for i, p in enumerate(params):
+            m.set(i, p)
+        m.input(0, x)
+        m.input(1, noise)
+        m.step(cfg.lr, STEP_ALL)
+        m.step(cfg.lr, STEP_FORWARD | STEP_BACKWARD)  # adds into the gradients
+        m.sync()
+        runs[fuse] = (m.loss, [m.get(i, 1) for i in range(len(params))], [m.get(i, 0) for i in range(len(params))])
+        m.close()
+    (lf, gf, pf), (lu, gu, pu) = runs[True], runs[False]
+    assert lf == lu
+    for i in range(len(params)):
+        np.testing.assert_array_equal(gf[i].view(np.uint32), gu[i].view(np.uint32), err_msg=f"grad {i}")
+        np.testing.assert_array_equal(pf[i].view(np.uint32), pu[i].view(np.uint32), err_msg=f"param {i}")
+
+
 def test_block_fusion_full_size(hip):
     """Full C4 shape, where the graph fusions run on the persistent GEMM kernel
     (LM-head row statistics for the loss, batched Q/K/V): one step agrees with

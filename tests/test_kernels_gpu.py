@@ -550,6 +550,44 @@ def test_norm(hip, orc, batch, channels, hw, groups):
         np.testing.assert_array_equal(gy2.numpy().view(np.uint32), gy1.numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("batch,channels,hw,groups", [(2, 64, 4096, 32), (2, 8, 700, 4), (2, 3, 33, 1)])
+@pytest.mark.parametrize("kind", [2, 1, 0])  # MLE_SILU, MLE_GELU, MLE_RELU
+def test_norm_act_fused(hip, batch, channels, hw, groups, kind):
+    """GroupNorm -> activation in one pass each way (mle_norm_fwd_act,
+    mle_norm_bwd_act) gives the bits of the normalisation and activation
+    kernels run one after the other, assigning and adding the normalisation's
+    output gradient."""
+    r = rng(batch * 7 + channels + hw + kind)
+    shape = (batch, channels, hw)
+    n = batch * channels * hw
+    x = (r.standard_normal(shape, dtype=np.float32) * 2 + 0.5).astype(np.float32)
+    da = r.standard_normal(shape, dtype=np.float32)
+    dy0 = r.standard_normal(shape, dtype=np.float32)
+    dx0 = r.standard_normal(shape, dtype=np.float32)
+    L = hip.lib()
+    ws = hip.Buffer(L.mle_norm_ws_bytes(batch, channels, hw, groups))
+    gx = B(hip, x)
+    y1, a1, st1 = hip.Buffer.zeros(shape), hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * batch * groups)
+    hip.call("mle_norm_fwd", None, gx.ptr, y1.ptr, st1.ptr, batch, channels, hw, groups, 1e-5, ws.ptr, ws.nbytes)
+    hip.call("mle_act_fwd", None, kind, y1.ptr, a1.ptr, n)
+    y2, a2, st2 = hip.Buffer.zeros(shape), hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * batch * groups)
+    hip.call("mle_norm_fwd_act", None, gx.ptr, y2.ptr, a2.ptr, kind, st2.ptr, batch, channels, hw, groups, 1e-5,
+             ws.ptr, ws.nbytes, 0)
+    for u, v in ((y1, y2), (a1, a2), (st1, st2)):
+        np.testing.assert_array_equal(v.numpy().view(np.uint32), u.numpy().view(np.uint32))
+    gda = B(hip, da)
+    for acc_dy in (0, 1):
+        dy1, dx1 = B(hip, dy0), B(hip, dx0)
+        hip.call("mle_act_bwd", None, kind, y1.ptr, gda.ptr, dy1.ptr, n, acc_dy)
+        hip.call("mle_norm_bwd", None, y1.ptr, dy1.ptr, dx1.ptr, st1.ptr, batch, channels, hw, groups, 1e-5, 1,
+                 ws.ptr, ws.nbytes, 1)
+        dy2, dx2 = B(hip, dy0 if acc_dy else np.full(shape, np.nan, np.float32)), B(hip, dx0)
+        hip.call("mle_norm_bwd_act", None, y1.ptr, gda.ptr, kind, dy2.ptr, acc_dy, dx2.ptr, st1.ptr, batch, channels,
+                 hw, groups, 1e-5, 1, ws.ptr, ws.nbytes, 1)
+        np.testing.assert_array_equal(dy2.numpy().view(np.uint32), dy1.numpy().view(np.uint32))
+        np.testing.assert_array_equal(dx2.numpy().view(np.uint32), dx1.numpy().view(np.uint32))
+
+
 @pytest.mark.parametrize("batch,channels,hw", [(4, 3, 25), (16, 128, 64 * 64), (3, 5, 4099), (1, 1, 9000)])
 def test_batchnorm(hip, orc, batch, channels, hw):
     r = rng(batch * 3 + channels + hw)
