@@ -16,7 +16,10 @@ carries, for C4 and for every other configuration under `extras`:
 Configurations: C4 transformer block (the headline), C3 Linear GEMM backward,
 C2 fused clip + AdamW over 100 M parameters, C1 MLP (latency-bound), C5 U-Net
 residual block (conv-bound).
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu] [--no-extras] [--only c1|c2|c3|c5]
+Each configuration is also timed with its step replayed as a recorded HIP
+graph (`graph_replay`; same results, one launch for zero_grad / forward /
+backward).
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--no-extras] [--only c1|c2|c3|c5]
 """
 from __future__ import annotations
 
@@ -284,13 +287,18 @@ def extras_adamw(cpu: bool, steps: int = 10) -> dict:
 
 
 # ------------------------------------------------------------------ C1 / C5
-def timed_steps(m: Model, lr: float, steps: int, warmup: int) -> float:
+def timed_steps(m: Model, lr: float, steps: int, warmup: int, graph: bool = False) -> float:
+    """ms per step on the host clock after `warmup` untimed steps (the GPU's
+    clocks settle over the first tens of milliseconds).  graph: the step's
+    zero_grad / forward / backward replayed as one recorded graph, the update
+    launched from the host (Model.step_graph)."""
+    step = (lambda: m.step_graph(lr, STEP_ALL)) if graph else (lambda: m.step(lr, STEP_ALL))
     for _ in range(warmup):
-        m.step(lr, STEP_ALL)
+        step()
     m.sync()
     t0 = time.perf_counter()
     for _ in range(steps):
-        m.step(lr, STEP_ALL)
+        step()
     m.sync()
     return (time.perf_counter() - t0) * 1e3 / steps
 
@@ -303,7 +311,7 @@ def step_work(m: Model, lr: float, steps: int = 1):
     return w
 
 
-def extras_mlp(cpu: bool, steps: int = 200) -> dict:
+def extras_mlp(cpu: bool, steps: int = 1000) -> dict:
     """C1: Linear 784->256 -> ReLU -> Linear 256->10 -> softmax CE, batch 64, Adam."""
     cfg = MLPConfig()
     x, labels, params = mlp_data(cfg, seed=0)
@@ -312,13 +320,15 @@ def extras_mlp(cpu: bool, steps: int = 200) -> dict:
         m.set(i, p)
     m.input(0, x)
     m.input(1, labels)
-    ms = timed_steps(m, cfg.lr, steps, 5)
+    ms = timed_steps(m, cfg.lr, steps, 100)
+    ms_graph = timed_steps(m, cfg.lr, steps, 100, graph=True)
     fam = dominant(GEMM_FAMILIES, step_work(m, cfg.lr, 5))
     rl = roofline("c1", fam, probed(fam, step_work(m, cfg.lr, 20)), "mfma")
     m.close()
     flop = 78.0e6
     out = {"workload": "C1 MLP 784-256-10 step (fwd + bwd + Adam), batch 64", "ms_per_step": round(ms, 4),
            "steps_per_s": round(1e3 / ms, 1), "bound": "launch latency (GEMMs of 1-7 tiles)",
+           "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 1)},
            "roofline": rl}
     if cpu:
         log("[bench] cpu baseline C1 (oracle)")
@@ -342,7 +352,7 @@ def extras_mlp(cpu: bool, steps: int = 200) -> dict:
     return out
 
 
-def extras_resblock(cpu: bool, steps: int = 10) -> dict:
+def extras_resblock(cpu: bool, steps: int = 50) -> dict:
     """C5: conv3x3 64->128, GN(32), SiLU, time projection, conv3x3 128->128, GN, 1x1 skip, MSE; AdamW."""
     cfg = ResBlockConfig()
     x, noise, t, params = resblock_data(cfg, seed=4)
@@ -351,14 +361,17 @@ def extras_resblock(cpu: bool, steps: int = 10) -> dict:
         m.set(i, p)
     m.input(0, x)
     m.input(1, noise)
-    ms = timed_steps(m, cfg.lr, steps, 2)
+    ms = timed_steps(m, cfg.lr, steps, 20)
+    ms_graph = timed_steps(m, cfg.lr, steps, 10, graph=True)
     fam = dominant(CONV_FAMILIES, step_work(m, cfg.lr, 1))
     rl = roofline("c5", fam, probed(fam, step_work(m, cfg.lr, 5)), "mfma")
     m.close()
     tf = cfg.conv_flop / (ms * 1e-3) / 1e12
     out = {"workload": "C5 U-Net residual block step (fwd + bwd + AdamW), 16x64x64x64", "ms_per_step": round(ms, 4),
            "steps_per_s": round(1e3 / ms, 2), "conv_gflop_per_step": round(cfg.conv_flop / 1e9, 2),
-           "conv_tflops_whole_step": round(tf, 2), "roofline": rl}
+           "conv_tflops_whole_step": round(tf, 2),
+           "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 2)},
+           "roofline": rl}
     if cpu:
         log("[bench] cpu baseline C5 (oracle)")
         orc = oracle()
@@ -381,8 +394,8 @@ def extras_resblock(cpu: bool, steps: int = 10) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=32)
@@ -399,7 +412,7 @@ def main() -> int:
 
     hip.init(0)
     extras_fn = {"c1": lambda: extras_mlp(cpu), "c2": lambda: extras_adamw(cpu, args.steps if args.only else 10),
-                 "c3": lambda: extras_gemm(cpu), "c5": lambda: extras_resblock(cpu, args.steps if args.only else 10)}
+                 "c3": lambda: extras_gemm(cpu), "c5": lambda: extras_resblock(cpu, args.steps if args.only else 50)}
     if args.only:
         print(json.dumps(extras_fn[args.only]()), flush=True)
         return 0
@@ -428,6 +441,8 @@ def main() -> int:
     ms_step = dt * 1e3 / args.steps
     log(f"[bench] {args.steps} steps in {dt:.3f} s: {ms_step:.3f} ms/step, loss {m.loss:.6g}")
     rl = roofline("c4", fam, probe, "mfma")
+    ms_graph = timed_steps(m, cfg.lr, args.steps, args.warmup, graph=True)
+    log(f"[bench] graph replay: {ms_graph:.3f} ms/step")
     m.close()
 
     extras = {}
@@ -458,6 +473,9 @@ def main() -> int:
                    "vocab": cfg.vocab, "gemm_gflop_per_step": round(cfg.gemm_flop / 1e9, 2),
                    "parallelism": "single GPU"},
         "gemm_tflops_per_step": round(cfg.gemm_flop / (ms_step * 1e-3) / 1e12, 2),
+        "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 3),
+                         "note": "the same step with zero_grad / forward / backward replayed as one recorded HIP "
+                                 "graph and the update launched from the host"},
         "roofline": rl,
         "cpu_baseline": cpu_line,
         "extras": extras,

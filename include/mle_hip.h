@@ -74,6 +74,23 @@ int mle_memcpy_d2h(void* dst, const void* src, size_t bytes, mle_stream stream);
  * lands instead of waking from a blocking wait.  Calls on one device are
  * serialised. */
 int mle_read_scalar(mle_stream stream, const float* src, float* dst);
+/* The value the last mle_read_scalar on this device published (after the
+ * caller synchronised the stream): under graph capture mle_read_scalar only
+ * records its publishing kernel, and each replay of the graph publishes. */
+int mle_scalar_last(float* dst);
+
+/* Graphs.  The work a caller enqueues on `stream` between capture_begin and
+ * capture_end is recorded (not run) into a graph, instantiated once;
+ * mle_graph_launch replays it with one launch.  The engine records its
+ * zero_grad -> forward -> backward pass this way (mle_model_step_graph): the
+ * kernels and their arguments are fixed at capture, so a replay computes on
+ * whatever the captured buffers hold when it runs.  No reference
+ * counterpart: the reference launches every kernel from the host each step. */
+typedef struct mle_graph_s* mle_graph;
+int mle_graph_capture_begin(mle_stream stream);
+int mle_graph_capture_end(mle_stream stream, mle_graph* out);
+int mle_graph_launch(mle_graph graph, mle_stream stream);
+int mle_graph_destroy(mle_graph graph);
 int mle_memcpy_d2d(void* dst, const void* src, size_t bytes, mle_stream stream);
 
 int mle_stream_create(mle_stream* stream);

@@ -32,6 +32,10 @@ struct ProbeScope {
   hipStream_t s;
   double flop, bytes;
   ProbeScope(const char* k, hipStream_t st, double f, double b) : on(probe_armed(k)), s(st), flop(f), bytes(b) {
+    if (on) {  // not while the stream records a graph: its events would join the graph
+      hipStreamCaptureStatus c = hipStreamCaptureStatusNone;
+      on = hipStreamIsCapturing(s, &c) == hipSuccess && c == hipStreamCaptureStatusNone;
+    }
     if (on) probe_begin(s);
   }
   ~ProbeScope() {

@@ -206,6 +206,11 @@ int mle_read_scalar(mle_stream stream, const float* src, float* dst) {
   hipStream_t s = as_stream(stream);
   publish_scalar_kernel<<<1, 1, 0, s>>>(reinterpret_cast<const unsigned*>(src), slot, want);
   MLE_HIP(hipGetLastError());
+  // Under graph capture the kernel is recorded, not run: each replay
+  // publishes the value, which mle_scalar_last reads after a synchronisation.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  MLE_HIP(hipStreamIsCapturing(s, &cap));
+  if (cap != hipStreamCaptureStatusNone) return MLE_OK;
   // The stream is asked every 256 spins: a stream that completed or failed
   // without the value having landed ends the wait.
   for (unsigned long spins = 1;; ++spins) {
@@ -222,6 +227,60 @@ int mle_read_scalar(mle_stream stream, const float* src, float* dst) {
   }
   const unsigned bits = __atomic_load_n(&slot->bits, __ATOMIC_ACQUIRE);
   memcpy(dst, &bits, sizeof(float));
+  return MLE_OK;
+}
+
+int mle_scalar_last(float* dst) {
+  MLE_CHECK_ARG(dst != nullptr, "mle_scalar_last: null pointer");
+  int dev = 0;
+  MLE_HIP(hipGetDevice(&dev));
+  MLE_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "mle_scalar_last: device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_slot_mu[dev]);
+  MLE_CHECK_ARG(g_slot[dev] != nullptr, "mle_scalar_last: no value was published on device %d", dev);
+  const unsigned bits = __atomic_load_n(&g_slot[dev]->bits, __ATOMIC_ACQUIRE);
+  memcpy(dst, &bits, sizeof(float));
+  return MLE_OK;
+}
+
+// ---- graphs ----------------------------------------------------------------
+struct mle_graph_s {
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+};
+
+int mle_graph_capture_begin(mle_stream stream) {
+  MLE_CHECK_ARG(stream != nullptr, "mle_graph_capture_begin: capture needs a created stream");
+  MLE_HIP(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeRelaxed));
+  return MLE_OK;
+}
+
+int mle_graph_capture_end(mle_stream stream, mle_graph* out) {
+  MLE_CHECK_ARG(stream != nullptr && out != nullptr, "mle_graph_capture_end: bad argument");
+  *out = nullptr;
+  hipGraph_t g = nullptr;
+  MLE_HIP(hipStreamEndCapture(as_stream(stream), &g));
+  hipGraphExec_t e = nullptr;
+  const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+  if (err != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return hip_error(err, "mle_graph_capture_end: instantiate");
+  }
+  *out = new mle_graph_s{g, e};
+  return MLE_OK;
+}
+
+int mle_graph_launch(mle_graph graph, mle_stream stream) {
+  MLE_CHECK_ARG(graph != nullptr, "mle_graph_launch: null graph");
+  MLE_HIP(hipGraphLaunch(graph->exec, as_stream(stream)));
+  return MLE_OK;
+}
+
+int mle_graph_destroy(mle_graph graph) {
+  if (!graph) return MLE_OK;
+  hipError_t e1 = hipGraphExecDestroy(graph->exec), e2 = hipGraphDestroy(graph->graph);
+  delete graph;
+  if (e1 != hipSuccess) return hip_error(e1, "mle_graph_destroy");
+  if (e2 != hipSuccess) return hip_error(e2, "mle_graph_destroy");
   return MLE_OK;
 }
 

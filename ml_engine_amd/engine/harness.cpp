@@ -38,6 +38,12 @@ struct Model {
   double* clip_scale = nullptr;
   bool adamw = true;
   std::vector<float*> grad_backup;  // mle_model_grads_save
+  // mle_model_step_graph: the recorded zero_grad / forward / backward pass
+  // (for replay_mode's steps) and whether the last step ran it (the loss is
+  // then read from the published value).
+  mle_graph replay = nullptr;
+  int replay_mode = 0;
+  bool loss_in_slot = false;
 };
 
 void* input_buffer(Model* m, size_t bytes) {
@@ -204,6 +210,7 @@ void mle_model_destroy(void* h) {
   auto* m = static_cast<Model*>(h);
   if (!m) return;
   mle::sync("model destroy");
+  check(mle_graph_destroy(m->replay), "model graph destroy");
   m->go.clear_graph();
   delete m;
 }
@@ -285,6 +292,7 @@ int mle_model_step(void* h, float lr, int mode, float clip) {
     if (mode & MLE_STEP_UPDATE) m->go.ParameterUpdate(nullptr, false, lr, true);
     return MLE_OK;
   }
+  m->loss_in_slot = false;
   if (mode & MLE_STEP_ZERO) m->go.zero_grad();
   if (mode & MLE_STEP_FORWARD) m->go.forward(nullptr, true);
   if (mode & MLE_STEP_BACKWARD) m->go.backward();
@@ -292,8 +300,43 @@ int mle_model_step(void* h, float lr, int mode, float clip) {
   return MLE_OK;
 }
 
+int mle_model_step_graph(void* h, float lr, int mode) {
+  auto* m = static_cast<Model*>(h);
+  const int pass = mode & (MLE_STEP_ZERO | MLE_STEP_FORWARD | MLE_STEP_BACKWARD);
+  if (m->kind == 2 || pass == 0) return mle_model_step(h, lr, mode, 0.0f);
+  mle_stream s = mle::stream();
+  if (!m->replay || m->replay_mode != pass) {
+    int rc = mle_graph_destroy(m->replay);
+    m->replay = nullptr;
+    if (rc) return rc;
+    // Record the pass once.  Its host side runs now (the lazy-clearing marks
+    // and every other host decision end as after one step, and are the same
+    // for every step of this mode); its kernels run on each replay.
+    rc = mle_graph_capture_begin(s);
+    if (rc) return rc;
+    if (pass & MLE_STEP_ZERO) m->go.zero_grad();
+    if (pass & MLE_STEP_FORWARD) m->go.forward(nullptr, true);
+    if (pass & MLE_STEP_BACKWARD) m->go.backward();
+    rc = mle_graph_capture_end(s, &m->replay);
+    if (rc) return rc;
+    m->replay_mode = pass;
+  }
+  int rc = mle_graph_launch(m->replay, s);
+  if (rc) return rc;
+  m->loss_in_slot = (pass & MLE_STEP_FORWARD) != 0;
+  // The update runs from the host each step: its bias corrections follow
+  // the parameters' step counters.
+  if (mode & MLE_STEP_UPDATE) m->go.ParameterUpdate(nullptr, false, lr, m->adamw);
+  return MLE_OK;
+}
+
 float mle_model_loss(void* h) {
-  (void)h;
+  auto* m = static_cast<Model*>(h);
+  if (m->loss_in_slot) {
+    check(mle_stream_sync(mle::stream()), "loss read-back");
+    check(mle_scalar_last(&GraphOperations::loss), "loss read-back");
+    m->loss_in_slot = false;
+  }
   return GraphOperations::loss;
 }
 

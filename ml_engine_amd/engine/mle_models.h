@@ -50,6 +50,11 @@ int mle_model_grads_restore(void* h);
 int mle_model_input(void* h, int slot, const void* host, size_t bytes);
 /* mode: MLE_STEP_* bits; clip > 0 (kind 2) applies accumulate + clipNorm. */
 int mle_model_step(void* h, float lr, int mode, float clip);
+// The same step with its zero_grad / forward / backward part replayed as one
+// recorded graph (recorded on the first call for a mode, recorded again when
+// the mode changes) and the update launched from the host.  Same results as
+// mle_model_step; mle_model_loss synchronises and reads the published loss.
+int mle_model_step_graph(void* h, float lr, int mode);
 float mle_model_loss(void* h);
 int mle_model_sync(void* h);
 void* mle_model_stream(void* h);

@@ -31,6 +31,11 @@ SIGNATURES: dict[str, tuple] = {
     "mle_memcpy_d2h": (I, [P, P, SZ, P]),
     "mle_memcpy_d2d": (I, [P, P, SZ, P]),
     "mle_read_scalar": (I, [P, P, P]),
+    "mle_scalar_last": (I, [P]),
+    "mle_graph_capture_begin": (I, [P]),
+    "mle_graph_capture_end": (I, [P, P]),
+    "mle_graph_launch": (I, [P, P]),
+    "mle_graph_destroy": (I, [P]),
     "mle_stream_create": (I, [C.POINTER(P)]),
     "mle_stream_destroy": (I, [P]),
     "mle_stream_sync": (I, [P]),

@@ -32,6 +32,7 @@ _SIGS = {
     "mle_model_grads_restore": (I, [P]),
     "mle_model_input": (I, [P, I, P, SZ]),
     "mle_model_step": (I, [P, F, I, F]),
+    "mle_model_step_graph": (I, [P, F, I]),
     "mle_model_loss": (F, [P]),
     "mle_model_sync": (I, [P]),
     "mle_model_stream": (P, [P]),
@@ -99,6 +100,10 @@ class Model:
 
     def step(self, lr: float, mode: int = STEP_ALL, clip: float = 0.0) -> None:
         hip.check(lib().mle_model_step(self.h, lr, mode, clip))
+
+    def step_graph(self, lr: float, mode: int = STEP_ALL) -> None:
+        """The same step with zero_grad / forward / backward replayed as one recorded graph."""
+        hip.check(lib().mle_model_step_graph(self.h, lr, mode))
 
     def grads_save(self) -> None:
         hip.check(lib().mle_model_grads_save(self.h))

@@ -310,6 +310,56 @@ def test_block_qkv_fusion(hip, quirks):
         assert np.abs(gf[i] - gu[i]).max() <= 1e-4 * scale, (i, np.abs(gf[i] - gu[i]).max(), scale)
 
 
+def _state(m, n):
+    return [[m.get(i, w) for i in range(n)] for w in range(4)]  # params, grads, m, v
+
+
+@pytest.mark.parametrize("kind", ["mlp", "block", "resblock"])
+def test_step_graph_matches_eager(hip, kind):
+    """Replays of the recorded zero_grad / forward / backward pass (the update
+    launched from the host) give, step after step, the bits of eager steps:
+    loss, parameters, gradients and Adam moments -- with the program's own
+    work and synchronisations between the replays (host reads of every
+    tensor), and again after a mode change (forward + backward without
+    zero_grad, recorded anew)."""
+    from ml_engine_amd.models import STEP_BACKWARD, STEP_FORWARD
+    if kind == "mlp":
+        cfg = MLPConfig()
+        x, labels, params = mlp_data(cfg, seed=7)
+        dims, inputs = cfg.dims(), [x, labels]
+    elif kind == "block":
+        cfg = BlockConfig(batch=2, seq=64, d_model=64, heads=1, ffn=128, vocab=97)
+        ids, tgt, params = block_data(cfg, seed=7)
+        dims, inputs = cfg.dims(), [ids, tgt]
+    else:
+        cfg = ResBlockConfig(batch=2, cin=8, cout=16, h=12, w=12, groups=4, tdim=32)
+        x, noise, t, params = resblock_data(cfg, seed=7)
+        dims, inputs = cfg.dims(t), [x, noise]
+    models = []
+    for _ in range(2):
+        m = Model(kind, dims)
+        for i, p in enumerate(params):
+            m.set(i, p)
+        for slot, a in enumerate(inputs):
+            m.input(slot, a)
+        models.append(m)
+    eager, graph = models
+    n = len(params)
+    for step, mode in enumerate([STEP_ALL] * 4 + [STEP_FORWARD | STEP_BACKWARD] * 2 + [STEP_ALL]):
+        eager.step(cfg.lr, mode)
+        eager.sync()
+        le = eager.loss
+        graph.step_graph(cfg.lr, mode)
+        lg = graph.loss
+        assert lg == le, (step, lg, le)
+        for w, (a, b) in enumerate(zip(_state(eager, n), _state(graph, n))):
+            for i in range(n):
+                np.testing.assert_array_equal(b[i].view(np.uint32), a[i].view(np.uint32),
+                                              err_msg=f"step {step} tensor {w}/{i}")
+    for m in models:
+        m.close()
+
+
 def test_resblock_fusion_matches_unfused(hip):
     """C5 residual block with the graph fusions (GroupNorm -> SiLU in one pass
     each way) against one kernel per op: the same loss, parameter gradients
