@@ -125,6 +125,17 @@ int mle_scale_assign(mle_stream stream, const float* x, float* y, double scale, 
  * each destination.  Add backward (Engine/engine.cu:1630-1672): its two
  * Accumulate launches (Engine/kernels.cu:1693-1699).  ya and yb must differ. */
 int mle_accumulate2(mle_stream stream, const float* x, float* ya, int acc_a, float* yb, int acc_b, size_t n);
+/* The residual Add and the activation after it (out = SILU(Add(h, skip)) in
+ * the residual block, Engine/diffusion.cu:129-137; Add, Engine/engine.cu:
+ * 1630-1672):
+ *   mle_add_act_fwd: z = a + b and y = act(z) in one pass.
+ *   mle_act_bwd_add: dz (+)= act'(z) * da (accumulate_dz 1 adds), then
+ *     ga (+)= dz and gb (+)= dz (acc_a / acc_b) in one pass.
+ * The same bits as mle_scale_add + mle_act_fwd, and mle_act_bwd +
+ * mle_accumulate2. */
+int mle_add_act_fwd(mle_stream stream, const float* a, const float* b, float* z, float* y, int kind, size_t n);
+int mle_act_bwd_add(mle_stream stream, const float* z, const float* da, int kind, float* dz, int accumulate_dz,
+                    float* ga, int acc_a, float* gb, int acc_b, size_t n);
 /* y = scale*x.  Scale_Write (Engine/kernels.cu:1677-1682), Write (Engine/kernels.cu:1670-1675) with scale 1. */
 int mle_scale_write(mle_stream stream, const float* x, float* y, float scale, size_t n);
 /* divide==0: x *= factor; divide==1: x /= factor.  SV (Includes/kernels.h:272-280). */

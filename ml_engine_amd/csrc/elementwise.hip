@@ -93,6 +93,61 @@ struct Accum2Op {
   }
 };
 
+// z = a + b and y = act(z): the Add forward (x + 1 * y, the same sum) and
+// the activation after it in one pass.
+template <int K>
+struct AddActOp {
+  const float* a;
+  const float* b;
+  float* z;
+  float* y;
+  __device__ void one(size_t i) const {
+    const float v = a[i] + b[i];
+    z[i] = v;
+    y[i] = act_f<K>(v);
+  }
+  __device__ void vec(size_t i) const {
+    const f32x4 v = ld4(a, i) + ld4(b, i);
+    st4(z, i, v);
+    f32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = act_f<K>(v[j]);
+    st4(y, i, w);
+  }
+};
+
+// dz (+)= act'(z) * da (the activation's backward into the Add before it),
+// then ga (+)= dz and gb (+)= dz (the Add's backward), in one pass: the steps
+// of ActBwdOp then Accum2Op, so the same bits.
+template <int K>
+struct ActBwdAddOp {
+  const float* z;
+  const float* da;
+  float* dz;
+  float* ga;
+  float* gb;
+  bool acc_z, acc_a, acc_b;
+  __device__ void one(size_t i) const {
+#pragma clang fp contract(off)
+    const float v = act_df<K>(z[i]) * da[i];
+    const float d = acc_z ? dz[i] + v : v;
+    dz[i] = d;
+    ga[i] = acc_a ? ga[i] + d : d;
+    gb[i] = acc_b ? gb[i] + d : d;
+  }
+  __device__ void vec(size_t i) const {
+#pragma clang fp contract(off)
+    const f32x4 x = ld4(z, i), g = ld4(da, i);
+    f32x4 d;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d[j] = act_df<K>(x[j]) * g[j];
+    if (acc_z) d = ld4(dz, i) + d;
+    st4(dz, i, d);
+    st4(ga, i, acc_a ? ld4(ga, i) + d : d);
+    st4(gb, i, acc_b ? ld4(gb, i) + d : d);
+  }
+};
+
 struct AccumOp {  // y = (float)((double)y + scale*(double)x)
   const float* x;
   float* y;
@@ -341,6 +396,43 @@ int mle_accumulate2(mle_stream stream, const float* x, float* ya, int acc_a, flo
   if (acc_a) return run_map(s, n, v, Accum2Op<true, false>{x, ya, yb}, "mle_accumulate2");
   if (acc_b) return run_map(s, n, v, Accum2Op<false, true>{x, ya, yb}, "mle_accumulate2");
   return run_map(s, n, v, Accum2Op<false, false>{x, ya, yb}, "mle_accumulate2");
+}
+
+int mle_add_act_fwd(mle_stream stream, const float* a, const float* b, float* z, float* y, int kind, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(a && b && z && y, "mle_add_act_fwd: null pointer");
+  const hipStream_t s = as_stream(stream);
+  const bool v = aligned16(a) && aligned16(b) && aligned16(z) && aligned16(y);
+  switch (kind) {
+    case MLE_RELU: return run_map(s, n, v, AddActOp<MLE_RELU>{a, b, z, y}, "mle_add_act_fwd");
+    case MLE_GELU: return run_map(s, n, v, AddActOp<MLE_GELU>{a, b, z, y}, "mle_add_act_fwd");
+    case MLE_SILU: return run_map(s, n, v, AddActOp<MLE_SILU>{a, b, z, y}, "mle_add_act_fwd");
+    case MLE_TANH: return run_map(s, n, v, AddActOp<MLE_TANH>{a, b, z, y}, "mle_add_act_fwd");
+    case MLE_SIGMOID: return run_map(s, n, v, AddActOp<MLE_SIGMOID>{a, b, z, y}, "mle_add_act_fwd");
+    case MLE_LEAKY_RELU: return run_map(s, n, v, AddActOp<MLE_LEAKY_RELU>{a, b, z, y}, "mle_add_act_fwd");
+    default: return set_error(MLE_ERR_INVALID, "mle_add_act_fwd: unknown activation %d", kind);
+  }
+}
+
+int mle_act_bwd_add(mle_stream stream, const float* z, const float* da, int kind, float* dz, int accumulate_dz,
+                    float* ga, int acc_a, float* gb, int acc_b, size_t n) {
+  if (n == 0) return MLE_OK;
+  MLE_CHECK_ARG(z && da && dz && ga && gb, "mle_act_bwd_add: null pointer");
+  MLE_CHECK_ARG(ga != gb && ga != dz && gb != dz, "mle_act_bwd_add: the three gradients must differ");
+  const hipStream_t s = as_stream(stream);
+  const bool v = aligned16(z) && aligned16(da) && aligned16(dz) && aligned16(ga) && aligned16(gb);
+  const bool az = accumulate_dz != 0, aa = acc_a != 0, ab = acc_b != 0;
+  switch (kind) {
+    case MLE_RELU: return run_map(s, n, v, ActBwdAddOp<MLE_RELU>{z, da, dz, ga, gb, az, aa, ab}, "mle_act_bwd_add");
+    case MLE_GELU: return run_map(s, n, v, ActBwdAddOp<MLE_GELU>{z, da, dz, ga, gb, az, aa, ab}, "mle_act_bwd_add");
+    case MLE_SILU: return run_map(s, n, v, ActBwdAddOp<MLE_SILU>{z, da, dz, ga, gb, az, aa, ab}, "mle_act_bwd_add");
+    case MLE_TANH: return run_map(s, n, v, ActBwdAddOp<MLE_TANH>{z, da, dz, ga, gb, az, aa, ab}, "mle_act_bwd_add");
+    case MLE_SIGMOID:
+      return run_map(s, n, v, ActBwdAddOp<MLE_SIGMOID>{z, da, dz, ga, gb, az, aa, ab}, "mle_act_bwd_add");
+    case MLE_LEAKY_RELU:
+      return run_map(s, n, v, ActBwdAddOp<MLE_LEAKY_RELU>{z, da, dz, ga, gb, az, aa, ab}, "mle_act_bwd_add");
+    default: return set_error(MLE_ERR_INVALID, "mle_act_bwd_add: unknown activation %d", kind);
+  }
 }
 
 int mle_scale_assign(mle_stream stream, const float* x, float* y, double scale, size_t n) {

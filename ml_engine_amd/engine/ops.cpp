@@ -130,7 +130,8 @@ graph act_node(const graph& input, int kind, const str& name) {
   if (mle::fusion_enabled() && input->forward_act) {
     auto fa = input->forward_act;
     input->forward = [fa, kind, nd]() { fa(kind, nd->output); };
-    input->forward_act = nullptr;
+    input->forward_act = nullptr;  // one takeover per producer
+    input->forward_normstats = nullptr;
     node->forward = []() {};
     fused = true;
   }
@@ -182,7 +183,8 @@ graph norm_node(const graph& X, int groups, const str& name) {
   if (mle::fusion_enabled() && X->forward_normstats) {
     auto fs = X->forward_normstats;
     X->forward = [fs, groups, ws, ws_bytes]() { fs(groups, ws, ws_bytes); };
-    X->forward_normstats = nullptr;
+    X->forward_normstats = nullptr;  // one takeover per producer
+    X->forward_act = nullptr;
     ready = 1;
   }
   node->forward = [=]() {
@@ -404,9 +406,27 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
                                   ws_bytes),
             "Add forward (with the normalisation statistics)");
     };
+    node->forward_act = [=](int kind, float* act_out) {
+      check(mle_add_act_fwd(S(), pa->output, pb->output, nd->output, act_out, kind, nd->total),
+            "Add forward (with the activation after it)");
+    };
+    node->takes_act_grad = true;
   }
   node->backward = [=]() {
     if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
+    if (nd->act_grad_in) {  // the activation after this node left its gradient (see act_node)
+      const float* da = nd->act_grad_in;
+      nd->act_grad_in = nullptr;
+      if (pa != pb && pa->grad != pb->grad) {  // ours and both input gradients in one pass
+        const int acc_a = mle::accumulate_flag(pa), acc_b = mle::accumulate_flag(pb);
+        check(mle_act_bwd_add(S(), nd->output, da, nd->act_grad_kind, nd->grad, nd->act_grad_acc, pa->grad, acc_a,
+                              pb->grad, acc_b, nd->total),
+              "Add backward (with the activation after it)");
+        return;
+      }
+      check(mle_act_bwd(S(), nd->act_grad_kind, nd->output, da, nd->grad, nd->total, nd->act_grad_acc),
+            "Deriv of the activation after Add");
+    }
     if (pa != pb && pa->grad != pb->grad) {  // one pass over the output gradient
       const int acc_a = mle::accumulate_flag(pa), acc_b = mle::accumulate_flag(pb);
       check(mle_accumulate2(S(), nd->grad, pa->grad, acc_a, pb->grad, acc_b, nd->total), "Add backward");

@@ -51,6 +51,8 @@ SIGNATURES: dict[str, tuple] = {
     "mle_scale_write": (I, [P, P, P, F, SZ]),
     "mle_scale_assign": (I, [P, P, P, D, SZ]),
     "mle_accumulate2": (I, [P, P, P, I, P, I, SZ]),
+    "mle_add_act_fwd": (I, [P, P, P, P, P, I, SZ]),
+    "mle_act_bwd_add": (I, [P, P, P, I, P, I, P, I, P, I, SZ]),
     "mle_scale_inplace": (I, [P, P, F, I, SZ]),
     "mle_scale_by_device": (I, [P, P, P, I, SZ]),
     "mle_bias_add_rows": (I, [P, P, P, SZ, I]),

@@ -942,6 +942,37 @@ def test_scatter_add_paths(hip, orc, batch, clen, dim, vocab, hot):
         np.testing.assert_array_equal(gt.numpy().view(np.uint32), w.view(np.uint32))
 
 
+@pytest.mark.parametrize("kind", [2, 1, 0])  # MLE_SILU, MLE_GELU, MLE_RELU
+@pytest.mark.parametrize("n", [4099 * 4, 1001])  # float4 body; a scalar tail
+def test_add_act_fused(hip, kind, n):
+    """The residual Add and the activation after it in one pass each way
+    (mle_add_act_fwd, mle_act_bwd_add) give the bits of mle_scale_add +
+    mle_act_fwd and mle_act_bwd + mle_accumulate2, for every combination of
+    assigning and adding the three gradients."""
+    r = rng(n + kind)
+    a, b, da, dz0, ga0, gb0 = (r.standard_normal(n, dtype=np.float32) for _ in range(6))
+    A, Bb, DA = B(hip, a), B(hip, b), B(hip, da)
+    z1, y1, z2, y2 = (hip.Buffer.zeros(n) for _ in range(4))
+    hip.call("mle_scale_add", None, A.ptr, Bb.ptr, z1.ptr, 1.0, n)
+    hip.call("mle_act_fwd", None, kind, z1.ptr, y1.ptr, n)
+    hip.call("mle_add_act_fwd", None, A.ptr, Bb.ptr, z2.ptr, y2.ptr, kind, n)
+    np.testing.assert_array_equal(z2.numpy().view(np.uint32), z1.numpy().view(np.uint32))
+    np.testing.assert_array_equal(y2.numpy().view(np.uint32), y1.numpy().view(np.uint32))
+    for acc_z in (0, 1):
+        for acc_a in (0, 1):
+            for acc_b in (0, 1):
+                dz1, ga1, gb1 = B(hip, dz0), B(hip, ga0), B(hip, gb0)
+                hip.call("mle_act_bwd", None, kind, z1.ptr, DA.ptr, dz1.ptr, n, acc_z)
+                hip.call("mle_accumulate2", None, dz1.ptr, ga1.ptr, acc_a, gb1.ptr, acc_b, n)
+                dz2, ga2, gb2 = (B(hip, x if acc else np.full(n, np.nan, np.float32))
+                                 for x, acc in ((dz0, acc_z), (ga0, acc_a), (gb0, acc_b)))
+                hip.call("mle_act_bwd_add", None, z1.ptr, DA.ptr, kind, dz2.ptr, acc_z, ga2.ptr, acc_a, gb2.ptr, acc_b,
+                         n)
+                for u, v in ((dz1, dz2), (ga1, ga2), (gb1, gb2)):
+                    np.testing.assert_array_equal(v.numpy().view(np.uint32), u.numpy().view(np.uint32),
+                                                  err_msg=f"acc {acc_z}{acc_a}{acc_b}")
+
+
 @pytest.mark.parametrize("off", [0, 1])  # 1: float offsets, so the scalar path runs
 def test_accumulate2_matches_two_accumulates(hip, orc, off):
     """mle_accumulate2 (Add backward's two gradients in one pass) equals
