@@ -19,7 +19,8 @@ residual block (conv-bound).
 Each configuration is also timed with its step replayed as a recorded HIP
 graph (`graph_replay`; same results, one launch for zero_grad / forward /
 backward).
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--no-extras] [--only c1|c2|c3|c5]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--no-extras] [--no-graph]
+                       [--only c1|c2|c3|c5]
 """
 from __future__ import annotations
 
@@ -47,6 +48,7 @@ PEAK_HBM = 8000.0       # GB/s
 GEMM_FAMILIES = ["gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt", "gemm_pair"]
 CONV_FAMILIES = ["conv_fwd", "conv_dgrad", "conv_wgrad"]
 CPU_REPS = 5
+GRAPH = True  # also time each step replayed as a recorded graph (--no-graph: not)
 
 
 def log(msg: str) -> None:
@@ -321,14 +323,15 @@ def extras_mlp(cpu: bool, steps: int = 1000) -> dict:
     m.input(0, x)
     m.input(1, labels)
     ms = timed_steps(m, cfg.lr, steps, 100)
-    ms_graph = timed_steps(m, cfg.lr, steps, 100, graph=True)
+    ms_graph = timed_steps(m, cfg.lr, steps, 100, graph=True) if GRAPH else None
     fam = dominant(GEMM_FAMILIES, step_work(m, cfg.lr, 5))
     rl = roofline("c1", fam, probed(fam, step_work(m, cfg.lr, 20)), "mfma")
     m.close()
     flop = 78.0e6
     out = {"workload": "C1 MLP 784-256-10 step (fwd + bwd + Adam), batch 64", "ms_per_step": round(ms, 4),
            "steps_per_s": round(1e3 / ms, 1), "bound": "launch latency (GEMMs of 1-7 tiles)",
-           "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 1)},
+           "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 1)}
+           if ms_graph else None,
            "roofline": rl}
     if cpu:
         log("[bench] cpu baseline C1 (oracle)")
@@ -362,7 +365,7 @@ def extras_resblock(cpu: bool, steps: int = 50) -> dict:
     m.input(0, x)
     m.input(1, noise)
     ms = timed_steps(m, cfg.lr, steps, 20)
-    ms_graph = timed_steps(m, cfg.lr, steps, 10, graph=True)
+    ms_graph = timed_steps(m, cfg.lr, steps, 10, graph=True) if GRAPH else None
     fam = dominant(CONV_FAMILIES, step_work(m, cfg.lr, 1))
     rl = roofline("c5", fam, probed(fam, step_work(m, cfg.lr, 5)), "mfma")
     m.close()
@@ -370,7 +373,8 @@ def extras_resblock(cpu: bool, steps: int = 50) -> dict:
     out = {"workload": "C5 U-Net residual block step (fwd + bwd + AdamW), 16x64x64x64", "ms_per_step": round(ms, 4),
            "steps_per_s": round(1e3 / ms, 2), "conv_gflop_per_step": round(cfg.conv_flop / 1e9, 2),
            "conv_tflops_whole_step": round(tf, 2),
-           "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 2)},
+           "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 2)}
+           if ms_graph else None,
            "roofline": rl}
     if cpu:
         log("[bench] cpu baseline C5 (oracle)")
@@ -398,10 +402,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the graph-replay timings")
     ap.add_argument("--cpu-sample-batch", type=int, default=32)
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c5"],
                     help="run just this secondary workload (for profiling) and print its JSON object")
     args = ap.parse_args()
+    global GRAPH
+    GRAPH = not args.no_graph
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (every box has one GPU); "
               "run with --gpus 1", file=sys.stderr)
@@ -441,8 +448,9 @@ def main() -> int:
     ms_step = dt * 1e3 / args.steps
     log(f"[bench] {args.steps} steps in {dt:.3f} s: {ms_step:.3f} ms/step, loss {m.loss:.6g}")
     rl = roofline("c4", fam, probe, "mfma")
-    ms_graph = timed_steps(m, cfg.lr, args.steps, args.warmup, graph=True)
-    log(f"[bench] graph replay: {ms_graph:.3f} ms/step")
+    ms_graph = timed_steps(m, cfg.lr, args.steps, args.warmup, graph=True) if GRAPH else None
+    if ms_graph:
+        log(f"[bench] graph replay: {ms_graph:.3f} ms/step")
     m.close()
 
     extras = {}
@@ -475,7 +483,7 @@ def main() -> int:
         "gemm_tflops_per_step": round(cfg.gemm_flop / (ms_step * 1e-3) / 1e12, 2),
         "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 3),
                          "note": "the same step with zero_grad / forward / backward replayed as one recorded HIP "
-                                 "graph and the update launched from the host"},
+                                 "graph and the update launched from the host"} if ms_graph else None,
         "roofline": rl,
         "cpu_baseline": cpu_line,
         "extras": extras,

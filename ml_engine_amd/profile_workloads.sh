@@ -30,24 +30,27 @@ step() {  # label limit_s log -- command...
   fi
 }
 
-# bench.py arguments for the traced run, its step count (what "per step"
-# divides by), and the arguments of the counter runs.
+# bench.py arguments for the traced run, and how its per-step figures are
+# taken: the last N steps between two launches of the update kernel (steady
+# state), or, for C3 (no optimizer), the whole trace over its N passes.
+# The profiled runs launch every kernel from the host (--no-graph): the same
+# kernels the graph replays, traced one dispatch at a time.
 args_trace() {
   case $1 in
-    c4) echo "--steps 10 --warmup 2 --no-cpu --no-extras" ;;  # 2 warm-up + 5 probed + 10 timed = 17 steps
-    c5) echo "--only c5 --no-cpu --steps 5" ;;                # 2 + 5 + 3 probed + 5 probed = 15 steps
+    c4) echo "--steps 10 --warmup 5 --no-cpu --no-extras --no-graph" ;;
+    c5) echo "--only c5 --no-cpu --no-graph --steps 10" ;;
     c3) echo "--only c3 --no-cpu" ;;                          # 3 + 20 + 10 + 10 = 43 (dX + dW) passes
-    c2) echo "--only c2 --no-cpu --steps 5" ;;                # 1 + 5 + 5 + 5 = 16 steps
-    c1) echo "--only c1 --no-cpu" ;;                          # 5 + 200 + 25 + 20 = 250 steps
+    c2) echo "--only c2 --no-cpu --steps 5" ;;
+    c1) echo "--only c1 --no-cpu --no-graph" ;;
   esac
 }
 steps_trace() {
-  case $1 in c4) echo 17 ;; c5) echo 15 ;; c3) echo 43 ;; c2) echo 16 ;; c1) echo 250 ;; esac
+  case $1 in c4) echo "5 adam" ;; c5) echo "5 adam" ;; c3) echo 43 ;; c2) echo "5 adam" ;; c1) echo "20 adam" ;; esac
 }
 args_pmc() {
   case $1 in
-    c4) echo "--steps 3 --warmup 1 --no-cpu --no-extras" ;;
-    c5) echo "--only c5 --no-cpu --steps 2" ;;
+    c4) echo "--steps 3 --warmup 1 --no-cpu --no-extras --no-graph" ;;
+    c5) echo "--only c5 --no-cpu --no-graph --steps 2" ;;
     c2) echo "--only c2 --no-cpu --steps 2" ;;
     *) args_trace "$1" ;;
   esac
@@ -74,8 +77,9 @@ for w in "$@"; do
   C=$OUT/copy
   {
     echo "Trace: rocprofv3 --kernel-trace --stats -d \$OUT/$w/trace -o t -- python3 bench.py $(args_trace $w)"
+    echo "Summary: python3 -m ml_engine_amd.profiling trace t_results.db $(steps_trace $w)"
     echo ""
-    $P trace "$D/trace/t_results.db" "$(steps_trace $w)"
+    $P trace "$D/trace/t_results.db" $(steps_trace $w)
   } > "$D/trace.md" || exit 1
   {
     echo "Counter runs (one rocprofv3 --pmc pass each): python3 bench.py $(args_pmc $w)"

@@ -16,9 +16,11 @@ Usage (on the GPU box; rocprofv3 puts the program itself after `--`):
   python3 -m ml_engine_amd.profiling copy N
       a plain copy of N floats (mle_scale_write, scale 1), run 5 times: the
       calibration workload
-  python3 -m ml_engine_amd.profiling trace DB STEPS [TITLE]
+  python3 -m ml_engine_amd.profiling trace DB STEPS [MARKER]
       markdown table of a --kernel-trace database: calls, total, average and
-      per-step time of every kernel
+      per-step time of every kernel -- over the whole trace divided by STEPS,
+      or with MARKER (a substring of the kernel that ends each step) over the
+      last STEPS steps only
   python3 -m ml_engine_amd.profiling counters FETCH.db WRITE.db CFETCH.db CWRITE.db N [MFMA.db]
       markdown table per kernel: calibrated fetch / write bytes per launch and,
       with MFMA.db, the MFMA-busy fraction and shader clock
@@ -127,10 +129,26 @@ def family(fam: str, fetch_db: str, write_db: str, cfetch_db: str, cwrite_db: st
     return out
 
 
-def trace_table(db: str, steps: int) -> str:
+def trace_table(db: str, steps: int, marker: str | None = None) -> str:
+    """Per-kernel time over the whole trace divided by `steps`, or, with a
+    marker (a substring of the kernel that ends every step, the optimizer's),
+    over the last `steps` steps only: the launches after the marker's
+    (steps+1)-th last dispatch up to its last one -- steady state, without the
+    model's construction and warm-up."""
     con = sqlite3.connect(db)
-    rows = con.execute("select name, count(*), sum(duration), avg(duration) from kernels group by name "
-                       "order by sum(duration) desc").fetchall()
+    if marker:
+        seq = con.execute("select name, duration from kernels order by start").fetchall()
+        ends = [i for i, (nm, _) in enumerate(seq) if marker in nm]
+        if len(ends) <= steps:
+            raise SystemExit(f"trace: {len(ends)} '{marker}' dispatches, fewer than {steps} + 1")
+        window = seq[ends[-1 - steps] + 1:ends[-1] + 1]
+        agg: dict[str, list[float]] = defaultdict(list)
+        for nm, d in window:
+            agg[nm].append(d)
+        rows = sorted(((nm, len(v), sum(v), sum(v) / len(v)) for nm, v in agg.items()), key=lambda r: -r[2])
+    else:
+        rows = con.execute("select name, count(*), sum(duration), avg(duration) from kernels group by name "
+                           "order by sum(duration) desc").fetchall()
     total = sum(r[2] for r in rows)
     out = ["| kernel | calls | total us | avg us | % | us per step |", "|---|---:|---:|---:|---:|---:|"]
     for name, n, s, a in rows:
@@ -196,7 +214,7 @@ def main(argv: list[str]) -> int:
         run_copy(int(argv[1]))
         return 0
     if len(argv) in (3, 4) and argv[0] == "trace":
-        print(trace_table(argv[1], int(argv[2])))
+        print(trace_table(argv[1], int(argv[2]), argv[3] if len(argv) == 4 else None))
         return 0
     if len(argv) in (6, 7) and argv[0] == "counters":
         print(counter_table(argv[1], argv[2], argv[3], argv[4], int(argv[5]), argv[6] if len(argv) == 7 else None))
