@@ -15,12 +15,12 @@
 //   bcmmT(Q, dS): scale * (dS Q)^T written row-major into the head's [seq x 64]
 //   block of K's gradient.
 //
-// Here none of S, P, dP, dS is stored.  The column statistics (m_c, l_c) come
-// from one pass over all of S; everything else recomputes its score tiles in
+// Here none of S, P, dP, dS is stored.  The column statistics (m_c, 1 / l_c,
+// the reciprocal divided once per key) come from one pass over all of S; everything else recomputes its score tiles in
 // registers.  Because P is normalised over the rows, D_c = <dV_c, V_c>: the
 // key-block kernel finishes dV first and gets D from it.
 //
-//   attn_stats_kernel  (key blocks)   : m_c, l_c
+//   attn_stats_kernel  (key blocks)   : m_c, 1 / l_c
 //   attn_fwd_kernel    (query blocks) : O = P V
 //   attn_bwd_kv_kernel (key blocks)   : dV, D (and dK = scale dS^T Q)
 //   attn_bwd_q_kernel  (query blocks) : dQ = scale dS K (or the reference's dK)
@@ -55,7 +55,7 @@ struct AttnArgs {
   float* dq;
   float* dk;
   float* dv;
-  float* stats;  // [slices][seq][2]: m_c, l_c
+  float* stats;  // [slices][seq][2]: m_c, 1 / l_c
   float* dcol;   // [slices][seq]: D_c
   int heads, seq, ld;
   uint32_t bytes;  // extent of each [batch][seq][ld] tensor
@@ -234,8 +234,7 @@ __global__ __launch_bounds__(128, 2) void attn_stats_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (l[i][r] < 1e-45f) l[i][r] = 1.0f;
+      for (int r = 0; r < 4; ++r) l[i][r] = 1.0f / (l[i][r] < 1e-45f ? 1.0f : l[i][r]);
       float* S = a.stats + ((size_t)sl.z * a.seq + k0 + 16 * i + 4 * q) * 2;
       st4(S, f32x4{m[i][0], l[i][0], m[i][1], l[i][1]});
       st4(S + 4, f32x4{m[i][2], l[i][2], m[i][3], l[i][3]});
@@ -246,7 +245,12 @@ __global__ __launch_bounds__(128, 2) void attn_stats_kernel(AttnArgs a) {
 // O = P V for queries q0 .. q0 + 31 over the 16-key chunks (with the causal
 // mask, up to the tile's last query).  The tile's Q^T (the B operand of
 // S^T = K Q^T) stays in registers; per chunk: S^T, P^T = exp(S - m) / l
-// masked, O^T += V^T P^T.
+// masked, O^T += V^T P^T.  The loop is software-pipelined: while chunk c's
+// softmax (VALU) and P V products run, chunk c + 1's S^T products are
+// already issued, so the matrix core has independent work while the wave
+// computes exponentials.  Two register sets alternate; at step c the K rows
+// of chunk c + 2 and the V rows and statistics of chunk c + 1 load into the
+// set whose previous contents step c - 1 consumed.
 template <bool CAUSAL>
 __global__ __launch_bounds__(128, 2) void attn_fwd_kernel(AttnArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
@@ -267,37 +271,40 @@ __global__ __launch_bounds__(128, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   struct Chunk {
-    f32x4 ka[4], va[4], s01, s23;
+    f32x4 ka[4], va[4], s01, s23, st[2];
   };
-  auto fetch = [&](int c, Chunk& ch) {
-    const int k0 = 16 * c;
+  auto fetch_k = [&](int c, Chunk& ch) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) ch.ka[s] = bld4(K, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
+    for (int s = 0; s < 4; ++s) ch.ka[s] = bld4(K, sl.base + (uint32_t)(16 * c + lr) * a.ld + 16 * s + 4 * q);
+  };
+  auto fetch_v = [&](int c, Chunk& ch) {
+    const int k0 = 16 * c;
 #pragma unroll
     for (int r = 0; r < 4; ++r) ch.va[r] = bld4s(V, sl.base + (uint32_t)(k0 + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
     ch.s01 = ld4(ST + (size_t)(k0 + 4 * q) * 2);
     ch.s23 = ld4(ST + (size_t)(k0 + 4 * q) * 2 + 4);
   };
-  auto compute = [&](int c, const Chunk& ch) {
-    const int k0 = 16 * c;
-    const float mk[4] = {ch.s01[0], ch.s01[2], ch.s23[0], ch.s23[2]};
-    const float il[4] = {1.0f / ch.s01[1], 1.0f / ch.s01[3], 1.0f / ch.s23[1], 1.0f / ch.s23[3]};
-    f32x4 st[2];
+  auto scores = [&](Chunk& ch) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
-      st[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      ch.st[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) st[n] = mfma4(ch.ka[s][j], qB[n][s][j], st[n]);
+        for (int j = 0; j < 4; ++j) ch.st[n] = mfma4(ch.ka[s][j], qB[n][s][j], ch.st[n]);
     }
+  };
+  auto finish = [&](int c, const Chunk& ch) {
+    const int k0 = 16 * c;
+    const float mk[4] = {ch.s01[0], ch.s01[2], ch.s23[0], ch.s23[2]};
+    const float il[4] = {ch.s01[1], ch.s01[3], ch.s23[1], ch.s23[3]};
     float pt[2][4];
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool keep = !CAUSAL || q0 + 16 * n + lr >= k0 + 4 * q + r;
-        pt[n][r] = __expf(a.scale * st[n][r] - mk[r]) * (keep ? il[r] : 0.f);
+        pt[n][r] = __expf(a.scale * ch.st[n][r] - mk[r]) * (keep ? il[r] : 0.f);
       }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -306,7 +313,41 @@ __global__ __launch_bounds__(128, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
         for (int n = 0; n < 2; ++n) acc[i][n] = mfma4(ch.va[r][i], pt[n][r], acc[i][n]);
   };
-  chunk_loop<Chunk>(0, CAUSAL ? (q0 + TW) / 16 : a.seq / 16, fetch, compute);
+  const int nc = CAUSAL ? (q0 + TW) / 16 : a.seq / 16;  // at least 2
+  // cur holds chunk c's scores, V rows and statistics; nxt holds chunk c + 1's
+  // K rows.  Loads past the last chunk repeat it.
+  auto step = [&](int c, Chunk& cur, Chunk& nxt) {
+    fetch_k(min(c + 2, nc - 1), cur);
+    fetch_v(c + 1, nxt);
+    __builtin_amdgcn_sched_barrier(0);  // loads first: they have the whole step to land
+    scores(nxt);
+    finish(c, cur);
+    // Issue order: one S^T product, then two softmax instructions, so the
+    // wave keeps issuing VALU work while each product occupies the matrix core.
+#pragma unroll
+    for (int k = 0; k < 24; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  Chunk X, Y;
+  fetch_k(0, X);
+  fetch_v(0, X);
+  fetch_k(1, Y);
+  scores(X);
+  for (int c = 0;; c += 2) {
+    if (c + 1 >= nc) {
+      finish(c, X);
+      break;
+    }
+    step(c, X, Y);
+    if (c + 2 >= nc) {
+      finish(c + 1, Y);
+      break;
+    }
+    step(c + 1, Y, X);
+  }
   const __amdgpu_buffer_rsrc_t O = rsrc(a.out, a.bytes);
 #pragma unroll
   for (int n = 0; n < 2; ++n)
@@ -344,7 +385,7 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_kv_kernel(AttnArgs a) {
     }
     const float* sp = a.stats + ((size_t)sl.z * a.seq + k0 + 16 * n + lr) * 2;
     mk[n] = sp[0];
-    il[n] = 1.0f / sp[1];
+    il[n] = sp[1];
   }
   f32x4 acc[4][2];
 #pragma unroll
@@ -495,7 +536,7 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
   auto compute = [&](int c, const Chunk& ch) {
     const int k0 = 16 * c;
     const float mk[4] = {s01[0], s01[2], s23[0], s23[2]};
-    const float il[4] = {1.0f / s01[1], 1.0f / s01[3], 1.0f / s23[1], 1.0f / s23[3]};
+    const float il[4] = {s01[1], s01[3], s23[1], s23[3]};
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       f32x4 qb[4], ob[4];

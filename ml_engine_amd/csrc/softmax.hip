@@ -531,12 +531,17 @@ __global__ __launch_bounds__(NT) void xent_bwd4_kernel(const float* __restrict__
 // at a time with the four rows' loads issued together (a workgroup per row
 // left each thread one 16-byte load in flight: 65536 workgroups of one load
 // and one store each ran at 63 % of HBM bandwidth).
+// POW2: batch is a power of two, so g / batch is the product with its exact
+// reciprocal (the same correctly rounded value, subnormals included) and the
+// division sequence drops out of the per-element work.
+template <bool POW2>
 __global__ __launch_bounds__(NT) void xent_keys_bwd4_kernel(const float* __restrict__ x, const float* __restrict__ stats,
                                                             KeyTargets kt, const float* __restrict__ up,
                                                             float* __restrict__ dl, int rows, int cols, float batch) {
   const int c = (blockIdx.x * NT + threadIdx.x) * 4;
   if (c >= cols) return;
   const float u = up ? up[0] : 1.0f;
+  const float inv_batch = 1.0f / batch;
   constexpr int R = 4;
   const int step = gridDim.y;
   for (int line0 = blockIdx.y; line0 < rows; line0 += R * step) {
@@ -564,7 +569,7 @@ __global__ __launch_bounds__(NT) void xent_keys_bwd4_kernel(const float* __restr
           g[j] = p + (-1.0f) * (c + j == key[k] ? 1.0f : 0.0f);
         }
         if (up) g *= u;
-        stv(dl, (size_t)line * cols + c, g / batch);
+        stv(dl, (size_t)line * cols + c, POW2 ? g * inv_batch : g / batch);
       }
     }
   }
@@ -746,10 +751,13 @@ int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const floa
   hipStream_t s = as_stream(stream);
   const KeyTargets kt{keys, clen, max_clen, nullptr};
   const unsigned gy = (unsigned)std::min(rows, 65535);
-  if (cols % 4 == 0 && aligned16(logits) && aligned16(dlogits))
-    xent_keys_bwd4_kernel<<<dim3((cols / 4 + NT - 1) / NT, std::min(gy, 1024u)), NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows,
-                                                                           cols, (float)batch);
-  else
+  if (cols % 4 == 0 && aligned16(logits) && aligned16(dlogits)) {
+    const dim3 grid((cols / 4 + NT - 1) / NT, std::min(gy, 1024u));
+    if ((batch & (batch - 1)) == 0 && batch <= (1 << 24))
+      xent_keys_bwd4_kernel<true><<<grid, NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows, cols, (float)batch);
+    else
+      xent_keys_bwd4_kernel<false><<<grid, NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows, cols, (float)batch);
+  } else
     xent_keys_bwd_kernel<<<dim3((cols + NT - 1) / NT, gy), NT, 0, s>>>(logits, stats, kt, upstream, dlogits, rows,
                                                                        cols, (float)batch);
   return check_launch("mle_softmax_xent_keys_bwd");
