@@ -161,12 +161,10 @@ __device__ __forceinline__ void chunk_loop(int c0, int c1, Fetch fetch, Compute 
 // acc[i][n][r].  Each lane keeps a running (max over all rows, masked sum)
 // per key; the 16 lanes of a key merge at the end.
 template <bool CAUSAL>
-__global__ __launch_bounds__(128, 2) void attn_stats_kernel(AttnArgs a) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
-  const Slice sl = slice_of(a);
+__device__ __forceinline__ void stats_tile(const AttnArgs& a, const Slice& sl, int k0) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
-  const int k0 = tile_of(a, sl, w) * TW;
   f32x4 ka[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -252,14 +250,12 @@ __global__ __launch_bounds__(128, 2) void attn_stats_kernel(AttnArgs a) {
 // of chunk c + 2 and the V rows and statistics of chunk c + 1 load into the
 // set whose previous contents step c - 1 consumed.
 template <bool CAUSAL>
-__global__ __launch_bounds__(128, 2) void attn_fwd_kernel(AttnArgs a) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
-  const Slice sl = slice_of(a);
+__device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int q0) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
-  const int q0 = tile_of(a, sl, w) * TW;
   f32x4 qB[2][4];
 #pragma unroll
   for (int n = 0; n < 2; ++n)
@@ -365,15 +361,12 @@ __global__ __launch_bounds__(128, 2) void attn_fwd_kernel(AttnArgs a) {
 //                                    all of its keys' dV, so D needs no exchange)
 //   pass 2 (DK): dS = P (dP - D), dK^T += Q^T dS.
 template <bool CAUSAL, bool DK>
-__global__ __launch_bounds__(128, 2) void attn_bwd_kv_kernel(AttnArgs a) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
-  const Slice sl = slice_of(a);
+__device__ __forceinline__ void bwd_kv_tile(const AttnArgs& a, const Slice& sl, int k0) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
-  // Key tiles: the heavy (early) one goes with wave 1's light (late) one.
-  const int k0 = tile_of(a, sl, w) * TW;
   f32x4 kB[2][4], vB[2][4];
   float mk[2], il[2];
 #pragma unroll
@@ -479,23 +472,19 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_kv_kernel(AttnArgs a) {
 // (the same product with Q's rows at the key positions, stored in the head
 // block's row-major [64 x seq] order) for queries q0 .. q0 + 31; both come
 // from the same dS tiles.  The tile's Q and dO rows (the B operands of
-// S^T = K Q^T and dP^T = V dO^T) are staged in the wave's own LDS region.
+// S^T = K Q^T and dP^T = V dO^T) are staged in the wave's own LDS region
+// (qs, os: TW * LQ floats each).
 // Per chunk and 16-query column block n: S^T and dP^T, dS^T = P^T (dP^T -
 // D), then X^T += Y^T dS^T for Y = K (acc[.][n]) and Y = Q (acc[.][2 + n]).
 template <bool CAUSAL, bool KREF>
-__global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) float lds[2][2][TW * LQ];  // [wave][Q, dO][row * LQ + col]
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
-  const Slice sl = slice_of(a);
+__device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, int q0, float* qs, float* os) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
   const float* DC = a.dcol + (size_t)sl.z * a.seq;
-  const int q0 = tile_of(a, sl, w) * TW;
-  float* qs = lds[w][0];
-  float* os = lds[w][1];
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int idx = lane + 64 * u, row = idx >> 4, col = (idx & 15) * 4;
@@ -503,7 +492,8 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
     *reinterpret_cast<f32x4*>(qs + row * LQ + col) = bld4(Q, e);
     *reinterpret_cast<f32x4*>(os + row * LQ + col) = bld4(dO, e);
   }
-  __syncthreads();
+  // The region is the wave's own: its writes only have to land before its reads.
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -600,6 +590,65 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
   }
 }
 
+// One wave per 32-row tile, two tiles (j and nb - 1 - j) per workgroup,
+// workgroups spread over the XCDs by slice (slice_of).
+template <bool CAUSAL>
+__global__ __launch_bounds__(128, 2) void attn_stats_kernel(AttnArgs a) {
+  const Slice sl = slice_of(a);
+  stats_tile<CAUSAL>(a, sl, tile_of(a, sl, threadIdx.x >> 6) * TW);
+}
+template <bool CAUSAL>
+__global__ __launch_bounds__(128, 2) void attn_fwd_kernel(AttnArgs a) {
+  const Slice sl = slice_of(a);
+  fwd_tile<CAUSAL>(a, sl, tile_of(a, sl, threadIdx.x >> 6) * TW);
+}
+template <bool CAUSAL, bool DK>
+__global__ __launch_bounds__(128, 2) void attn_bwd_kv_kernel(AttnArgs a) {
+  const Slice sl = slice_of(a);
+  bwd_kv_tile<CAUSAL, DK>(a, sl, tile_of(a, sl, threadIdx.x >> 6) * TW);
+}
+template <bool CAUSAL, bool KREF>
+__global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[2][2][TW * LQ];  // [wave][Q, dO][row * LQ + col]
+  const Slice sl = slice_of(a);
+  const int w = threadIdx.x >> 6;
+  bwd_q_tile<CAUSAL, KREF>(a, sl, tile_of(a, sl, w) * TW, lds[w][0], lds[w][1]);
+}
+
+// Whole-slice kernels for seq <= 256: workgroup z runs every tile of slice z
+// with one wave per tile (SW waves), the two passes of the forward (or the
+// backward) separated by a workgroup barrier instead of a kernel boundary.
+// Each kernel launch pays a ramp (every wave waits for its first operands
+// from memory at once) and a tail (every store at the end); this pays them
+// once per direction.  In the pass whose work grows or shrinks with the tile
+// index, wave w takes tile w (w < SW / 2) or mirrors it, so that waves w and
+// w + 4 -- the pair that shares a SIMD -- carry complementary loads.
+constexpr int SW = 8;  // waves per slice workgroup: seq / TW tiles, at most 8
+__device__ __forceinline__ Slice slice_whole(const AttnArgs& a) {
+  const int z = blockIdx.x, b = z / a.heads, h = z - b * a.heads;
+  return {z, (uint32_t)b * a.seq * a.ld + (uint32_t)h * HD, 0};
+}
+__device__ __forceinline__ int mirrored_tile(int w, int ntile) {
+  return w < ntile / 2 ? w : ntile - 1 - (w - ntile / 2);
+}
+template <bool CAUSAL>
+__global__ __launch_bounds__(SW * 64, 1) void attn_fwd_slice_kernel(AttnArgs a) {
+  const Slice sl = slice_whole(a);
+  const int w = threadIdx.x >> 6, ntile = a.seq / TW;
+  if (w < ntile) stats_tile<CAUSAL>(a, sl, w * TW);
+  __syncthreads();  // the slice's statistics are written
+  if (w < ntile) fwd_tile<CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW);
+}
+template <bool CAUSAL, bool KREF>
+__global__ __launch_bounds__(SW * 64, 1) void attn_bwd_slice_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[SW][2][TW * LQ];
+  const Slice sl = slice_whole(a);
+  const int w = threadIdx.x >> 6, ntile = a.seq / TW;
+  if (w < ntile) bwd_kv_tile<CAUSAL, !KREF>(a, sl, mirrored_tile(w, ntile) * TW);
+  __syncthreads();  // D of every key of the slice is written
+  if (w < ntile) bwd_q_tile<CAUSAL, KREF>(a, sl, mirrored_tile(w, ntile) * TW, lds[w][0], lds[w][1]);
+}
+
 // Operand addressing uses 32-bit byte offsets into buffer resources whose
 // extent is the tensor's byte size (AttnArgs::bytes), so every tensor must stay
 // below 2 GiB in bytes, not elements.
@@ -644,7 +693,11 @@ int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const f
   const dim3 grid((unsigned)(seq / (2 * TW) * batch * heads));  // two 32-row tiles per workgroup
   const double flop = 4.0 * batch * heads * (double)seq * seq * HD;  // S and P V, as the reference computes them
   ProbeScope probe("attn_fwd", s, flop, 0.0);
-  if (causal) {
+  if (seq <= SW * TW) {
+    const dim3 slices((unsigned)(batch * heads));
+    if (causal) mle::launch(attn_fwd_slice_kernel<true>, slices, SW * 64, 0, s, a);
+    else mle::launch(attn_fwd_slice_kernel<false>, slices, SW * 64, 0, s, a);
+  } else if (causal) {
     mle::launch(attn_stats_kernel<true>, grid, 128, 0, s, a);
     mle::launch(attn_fwd_kernel<true>, grid, 128, 0, s, a);
   } else {
@@ -688,7 +741,16 @@ int mle_attention_bwd(mle_stream stream, const float* q, const float* k, const f
   const double flop = 8.0 * batch * heads * (double)seq * seq * HD;  // dP, dV, dQ, dK
   ProbeScope probe("attn_bwd", s, flop, 0.0);
   const bool kref = k_reference_grad != 0;
-  if (causal) {
+  if (seq <= SW * TW) {
+    const dim3 slices((unsigned)(batch * heads));
+    if (causal) {
+      if (kref) mle::launch(attn_bwd_slice_kernel<true, true>, slices, SW * 64, 0, s, a);
+      else mle::launch(attn_bwd_slice_kernel<true, false>, slices, SW * 64, 0, s, a);
+    } else {
+      if (kref) mle::launch(attn_bwd_slice_kernel<false, true>, slices, SW * 64, 0, s, a);
+      else mle::launch(attn_bwd_slice_kernel<false, false>, slices, SW * 64, 0, s, a);
+    }
+  } else if (causal) {
     if (kref) {
       mle::launch(attn_bwd_kv_kernel<true, false>, grid, 128, 0, s, a);
       mle::launch(attn_bwd_q_kernel<true, true>, grid, 128, 0, s, a);

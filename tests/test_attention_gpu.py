@@ -67,6 +67,8 @@ CASES = [
     # (batch, heads, seq, extra columns of ld, causal, reference K gradient)
     (2, 2, 64, 0, 1, 1), (2, 2, 64, 0, 0, 0), (1, 3, 192, 0, 1, 0), (1, 3, 192, 0, 0, 1),
     (2, 1, 128, 64, 1, 1), (1, 2, 256, 0, 1, 1), (1, 2, 256, 0, 1, 0),
+    # past 256 the slice kernels hand over to the four-kernel path
+    (1, 2, 320, 0, 1, 1), (1, 1, 384, 64, 0, 0),
 ]
 
 
