@@ -201,18 +201,36 @@ __device__ __forceinline__ void stats_tile(const AttnArgs& a, const Slice& sl, i
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][n] = mfma4(ka[i][s][j], ch.qb[n][s][j], acc[i][n]);
       }
+    // Under the causal mask, chunks before the tile's diagonal chunk lie
+    // wholly above the diagonal: they only raise the maximum (the sum is still
+    // exactly 0 there, so skipping its update changes no bit), and chunks
+    // after it need no mask.
+    const int diag = k0 / TW;
+    auto update = [&](auto masked_tag) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * i + 4 * q + r;
-        const float s0 = a.scale * acc[i][0][r], s1 = a.scale * acc[i][1][r];
-        const float mn = fmaxf(m[i][r], fmaxf(s0, s1));
-        const float e0 = __expf(s0 - mn), e1 = __expf(s1 - mn);
-        const float add = ((!CAUSAL || qc + lr >= key) ? e0 : 0.f) + ((!CAUSAL || qc + 16 + lr >= key) ? e1 : 0.f);
-        l[i][r] = l[i][r] * __expf(m[i][r] - mn) + add;
-        m[i][r] = mn;
-      }
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 16 * i + 4 * q + r;
+          const float s0 = a.scale * acc[i][0][r], s1 = a.scale * acc[i][1][r];
+          const float mn = fmaxf(m[i][r], fmaxf(s0, s1));
+          const float e0 = __expf(s0 - mn), e1 = __expf(s1 - mn);
+          const float add = ((!MASKED || qc + lr >= key) ? e0 : 0.f) + ((!MASKED || qc + 16 + lr >= key) ? e1 : 0.f);
+          l[i][r] = l[i][r] * __expf(m[i][r] - mn) + add;
+          m[i][r] = mn;
+        }
+    };
+    if (CAUSAL && c < diag) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m[i][r] = fmaxf(m[i][r], fmaxf(a.scale * acc[i][0][r], a.scale * acc[i][1][r]));
+    } else if (CAUSAL && c == diag) {
+      update(std::true_type{});
+    } else {
+      update(std::false_type{});
+    }
   };
   chunk_loop<Chunk>(0, a.seq / TW, fetch, compute);
   // Merge the 16 lanes of each key (a butterfly: every lane ends with the
@@ -290,7 +308,9 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
         for (int j = 0; j < 4; ++j) ch.st[n] = mfma4(ch.ka[s][j], qB[n][s][j], ch.st[n]);
     }
   };
-  auto finish = [&](int c, const Chunk& ch) {
+  // Only the tile's last two chunks reach past the diagonal (MASK).
+  auto finish = [&](auto mask_tag, int c, const Chunk& ch) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int k0 = 16 * c;
     const float mk[4] = {ch.s01[0], ch.s01[2], ch.s23[0], ch.s23[2]};
     const float il[4] = {ch.s01[1], ch.s01[3], ch.s23[1], ch.s23[3]};
@@ -299,7 +319,7 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
     for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const bool keep = !CAUSAL || q0 + 16 * n + lr >= k0 + 4 * q + r;
+        const bool keep = !MASK || q0 + 16 * n + lr >= k0 + 4 * q + r;
         pt[n][r] = __expf(a.scale * ch.st[n][r] - mk[r]) * (keep ? il[r] : 0.f);
       }
 #pragma unroll
@@ -312,12 +332,13 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
   const int nc = CAUSAL ? (q0 + TW) / 16 : a.seq / 16;  // at least 2
   // cur holds chunk c's scores, V rows and statistics; nxt holds chunk c + 1's
   // K rows.  Loads past the last chunk repeat it.
-  auto step = [&](int c, Chunk& cur, Chunk& nxt) {
+  const int cm = CAUSAL ? q0 / 16 : nc;  // first chunk that needs the mask
+  auto step = [&](auto mask_tag, int c, Chunk& cur, Chunk& nxt) {
     fetch_k(min(c + 2, nc - 1), cur);
     fetch_v(c + 1, nxt);
     __builtin_amdgcn_sched_barrier(0);  // loads first: they have the whole step to land
     scores(nxt);
-    finish(c, cur);
+    finish(mask_tag, c, cur);
     // Issue order: one S^T product, then two softmax instructions, so the
     // wave keeps issuing VALU work while each product occupies the matrix core.
 #pragma unroll
@@ -332,17 +353,21 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
   fetch_v(0, X);
   fetch_k(1, Y);
   scores(X);
+  auto step_at = [&](int c, Chunk& cur, Chunk& nxt) {
+    if (c >= cm) step(std::true_type{}, c, cur, nxt);
+    else step(std::false_type{}, c, cur, nxt);
+  };
   for (int c = 0;; c += 2) {
     if (c + 1 >= nc) {
-      finish(c, X);
+      finish(std::integral_constant<bool, CAUSAL>{}, c, X);
       break;
     }
-    step(c, X, Y);
+    step_at(c, X, Y);
     if (c + 2 >= nc) {
-      finish(c + 1, Y);
+      finish(std::integral_constant<bool, CAUSAL>{}, c + 1, Y);
       break;
     }
-    step(c + 1, Y, X);
+    step_at(c + 1, Y, X);
   }
   const __amdgpu_buffer_rsrc_t O = rsrc(a.out, a.bytes);
 #pragma unroll
@@ -403,7 +428,9 @@ __device__ __forceinline__ void bwd_kv_tile(const AttnArgs& a, const Slice& sl, 
 #pragma unroll
       for (int r = 0; r < 4; ++r) ch.at[r] = bld4s(P2 ? Q : dO, sl.base + (uint32_t)(qc + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
     };
-    auto compute = [&](int c, const Chunk& ch) {
+    // Only the tile's first two chunks reach past the diagonal (MASK).
+    auto body = [&](auto mask_tag, int c, const Chunk& ch) {
+      constexpr bool MASK = decltype(mask_tag)::value;
       const int qc = 16 * c;
 #pragma unroll
       for (int n = 0; n < 2; ++n) {
@@ -418,7 +445,7 @@ __device__ __forceinline__ void bwd_kv_tile(const AttnArgs& a, const Slice& sl, 
         float bop[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const bool keep = !CAUSAL || qc + 4 * q + r >= k0 + 16 * n + lr;
+          const bool keep = !MASK || qc + 4 * q + r >= k0 + 16 * n + lr;
           const float pv = __expf(a.scale * sa[r] - mk[n]) * (keep ? il[n] : 0.f);
           bop[r] = P2 ? pv * (da[r] - D[n]) : pv;
         }
@@ -427,6 +454,10 @@ __device__ __forceinline__ void bwd_kv_tile(const AttnArgs& a, const Slice& sl, 
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i][n] = mfma4(ch.at[r][i], bop[r], acc[i][n]);
       }
+    };
+    auto compute = [&](int c, const Chunk& ch) {
+      if (CAUSAL && c < k0 / 16 + 2) body(std::true_type{}, c, ch);
+      else body(std::false_type{}, c, ch);
     };
     chunk_loop<Chunk>(CAUSAL ? k0 / 16 : 0, a.seq / 16, fetch, compute);
   };
@@ -523,7 +554,9 @@ __device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, i
       if (KREF) yq[r] = bld4s(Q, sl.base + (uint32_t)(16 * c + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
     }
   };
-  auto compute = [&](int c, const Chunk& ch) {
+  // Only the tile's last two chunks reach past the diagonal (MASK).
+  auto body = [&](auto mask_tag, int c, const Chunk& ch) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int k0 = 16 * c;
     const float mk[4] = {s01[0], s01[2], s23[0], s23[2]};
     const float il[4] = {s01[1], s01[3], s23[1], s23[3]};
@@ -546,7 +579,7 @@ __device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, i
       float ds[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const bool keep = !CAUSAL || q0 + 16 * n + lr >= k0 + 4 * q + r;
+        const bool keep = !MASK || q0 + 16 * n + lr >= k0 + 4 * q + r;
         ds[r] = __expf(a.scale * st[r] - mk[r]) * (keep ? il[r] : 0.f) * (dt[r] - dk[r]);
       }
 #pragma unroll
@@ -558,6 +591,10 @@ __device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, i
         }
       __builtin_amdgcn_sched_barrier(0);  // block n + 1's LDS reads stay after block n's products
     }
+  };
+  auto compute = [&](int c, const Chunk& ch) {
+    if (CAUSAL && c >= q0 / 16) body(std::true_type{}, c, ch);
+    else body(std::false_type{}, c, ch);
   };
   chunk_loop<Chunk>(0, CAUSAL ? (q0 + TW) / 16 : a.seq / 16, fetch, compute, late);
   // acc[i][n][r] = X^T[d = 16q + 4r + i][query q0 + 16(n % 2) + lr]
