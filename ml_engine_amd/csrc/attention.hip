@@ -160,8 +160,11 @@ __device__ __forceinline__ void chunk_loop(int c0, int c1, Fetch fetch, Compute 
 // S^T = K Q^T puts key k0 + 16i + 4q + r and query qc + 16n + lr in
 // acc[i][n][r].  Each lane keeps a running (max over all rows, masked sum)
 // per key; the 16 lanes of a key merge at the end.
-template <bool CAUSAL>
-__device__ __forceinline__ void stats_tile(const AttnArgs& a, const Slice& sl, int k0) {
+// KEEP_S (causal): the tile's S^T blocks on or below the diagonal (16-row
+// key block kb <= query block qb) are also written to sst, 1 KB per block in
+// the accumulator lane layout, at block index qb (qb + 1) / 2 + kb.
+template <bool CAUSAL, bool KEEP_S = false>
+__device__ __forceinline__ void stats_tile(const AttnArgs& a, const Slice& sl, int k0, float* sst = nullptr) {
   const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
@@ -201,6 +204,15 @@ __device__ __forceinline__ void stats_tile(const AttnArgs& a, const Slice& sl, i
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][n] = mfma4(ka[i][s][j], ch.qb[n][s][j], acc[i][n]);
       }
+    if (KEEP_S) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+          const int kb = k0 / 16 + i, qb = 2 * c + n;
+          if (kb <= qb) *reinterpret_cast<f32x4*>(sst + (qb * (qb + 1) / 2 + kb) * 256 + 4 * lane) = acc[i][n];
+        }
+    }
     // Under the causal mask, chunks before the tile's diagonal chunk lie
     // wholly above the diagonal: they only raise the maximum (the sum is still
     // exactly 0 there, so skipping its update changes no bit), and chunks
@@ -266,19 +278,25 @@ __device__ __forceinline__ void stats_tile(const AttnArgs& a, const Slice& sl, i
 // already issued, so the matrix core has independent work while the wave
 // computes exponentials.  Two register sets alternate; at step c the K rows
 // of chunk c + 2 and the V rows and statistics of chunk c + 1 load into the
-// set whose previous contents step c - 1 consumed.
-template <bool CAUSAL>
-__device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int q0) {
+// set whose previous contents step c - 1 consumed.  KEEP_S: the S^T blocks
+// come from sst (written by stats_tile<CAUSAL, true> over the same operands
+// in the same order, so the same bits) and no K rows are loaded; the one
+// block above the diagonal (the lower query block's last chunk) is never
+// read, its P^T is 0 by the mask.
+template <bool CAUSAL, bool KEEP_S = false>
+__device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int q0, const float* sst = nullptr) {
   const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
   f32x4 qB[2][4];
+  if (!KEEP_S) {
 #pragma unroll
-  for (int n = 0; n < 2; ++n)
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qB[n][s] = bld4(Q, sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
+      for (int s = 0; s < 4; ++s) qB[n][s] = bld4(Q, sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
+  }
   f32x4 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -288,6 +306,7 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
     f32x4 ka[4], va[4], s01, s23, st[2];
   };
   auto fetch_k = [&](int c, Chunk& ch) {
+    if (KEEP_S) return;
 #pragma unroll
     for (int s = 0; s < 4; ++s) ch.ka[s] = bld4(K, sl.base + (uint32_t)(16 * c + lr) * a.ld + 16 * s + 4 * q);
   };
@@ -298,10 +317,15 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
     ch.s01 = ld4(ST + (size_t)(k0 + 4 * q) * 2);
     ch.s23 = ld4(ST + (size_t)(k0 + 4 * q) * 2 + 4);
   };
-  auto scores = [&](Chunk& ch) {
+  auto scores = [&](int c, Chunk& ch) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       ch.st[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (KEEP_S) {
+        const int qb = q0 / 16 + n;
+        if (c <= qb) ch.st[n] = *reinterpret_cast<const f32x4*>(sst + (qb * (qb + 1) / 2 + c) * 256 + 4 * lane);
+        continue;
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -320,7 +344,7 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool keep = !MASK || q0 + 16 * n + lr >= k0 + 4 * q + r;
-        pt[n][r] = __expf(a.scale * ch.st[n][r] - mk[r]) * (keep ? il[r] : 0.f);
+        pt[n][r] = keep ? __expf(a.scale * ch.st[n][r] - mk[r]) * il[r] : 0.f;
       }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -337,14 +361,16 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
     fetch_k(min(c + 2, nc - 1), cur);
     fetch_v(c + 1, nxt);
     __builtin_amdgcn_sched_barrier(0);  // loads first: they have the whole step to land
-    scores(nxt);
+    scores(c + 1, nxt);
     finish(mask_tag, c, cur);
     // Issue order: one S^T product, then two softmax instructions, so the
     // wave keeps issuing VALU work while each product occupies the matrix core.
+    if (!KEEP_S) {
 #pragma unroll
-    for (int k = 0; k < 24; ++k) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      for (int k = 0; k < 24; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -352,7 +378,7 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
   fetch_k(0, X);
   fetch_v(0, X);
   fetch_k(1, Y);
-  scores(X);
+  scores(0, X);
   auto step_at = [&](int c, Chunk& cur, Chunk& nxt) {
     if (c >= cm) step(std::true_type{}, c, cur, nxt);
     else step(std::false_type{}, c, cur, nxt);
@@ -668,13 +694,18 @@ __device__ __forceinline__ Slice slice_whole(const AttnArgs& a) {
 __device__ __forceinline__ int mirrored_tile(int w, int ntile) {
   return w < ntile / 2 ? w : ntile - 1 - (w - ntile / 2);
 }
+// Causal: the statistics pass keeps the slice's S^T blocks on or below the
+// diagonal in LDS (seq / 16 (seq / 16 + 1) / 2 blocks of 1 KB, 136 KB at seq
+// 256) and the output pass reads them instead of recomputing its products.
 template <bool CAUSAL>
 __global__ __launch_bounds__(SW * 64, 1) void attn_fwd_slice_kernel(AttnArgs a) {
+  constexpr int kBlocks = CAUSAL ? (SW * TW / 16) * (SW * TW / 16 + 1) / 2 : 1;
+  __shared__ __attribute__((aligned(16))) float sst[kBlocks * 256];
   const Slice sl = slice_whole(a);
   const int w = threadIdx.x >> 6, ntile = a.seq / TW;
-  if (w < ntile) stats_tile<CAUSAL>(a, sl, w * TW);
-  __syncthreads();  // the slice's statistics are written
-  if (w < ntile) fwd_tile<CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW);
+  if (w < ntile) stats_tile<CAUSAL, CAUSAL>(a, sl, w * TW, sst);
+  __syncthreads();  // the slice's statistics (and kept scores) are written
+  if (w < ntile) fwd_tile<CAUSAL, CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW, sst);
 }
 template <bool CAUSAL, bool KREF>
 __global__ __launch_bounds__(SW * 64, 1) void attn_bwd_slice_kernel(AttnArgs a) {
