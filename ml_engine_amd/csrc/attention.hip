@@ -411,8 +411,11 @@ __device__ __forceinline__ void fwd_tile(const AttnArgs& a, const Slice& sl, int
 //   pass 1: dV^T += dO^T P        -> dV and D_c = <dV_c, V_c> (the wave holds
 //                                    all of its keys' dV, so D needs no exchange)
 //   pass 2 (DK): dS = P (dP - D), dK^T += Q^T dS.
-template <bool CAUSAL, bool DK>
-__device__ __forceinline__ void bwd_kv_tile(const AttnArgs& a, const Slice& sl, int k0) {
+// KEEP_P (causal): pass 1's P blocks on or below the diagonal (16-row query
+// block qb >= key block kb) are also written to sst, 1 KB per block at index
+// qb (qb + 1) / 2 + kb, row = query and column = key within the block.
+template <bool CAUSAL, bool DK, bool KEEP_P = false>
+__device__ __forceinline__ void bwd_kv_tile(const AttnArgs& a, const Slice& sl, int k0, float* sst = nullptr) {
   const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
@@ -475,6 +478,14 @@ __device__ __forceinline__ void bwd_kv_tile(const AttnArgs& a, const Slice& sl, 
           const float pv = __expf(a.scale * sa[r] - mk[n]) * (keep ? il[n] : 0.f);
           bop[r] = P2 ? pv * (da[r] - D[n]) : pv;
         }
+        if (KEEP_P && !P2) {
+          const int kb = k0 / 16 + n;
+          if (kb <= c) {
+            float* blk = sst + (c * (c + 1) / 2 + kb) * 256 + lr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) blk[(4 * q + r) * 16] = bop[r];
+          }
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -533,8 +544,16 @@ __device__ __forceinline__ void bwd_kv_tile(const AttnArgs& a, const Slice& sl, 
 // (qs, os: TW * LQ floats each).
 // Per chunk and 16-query column block n: S^T and dP^T, dS^T = P^T (dP^T -
 // D), then X^T += Y^T dS^T for Y = K (acc[.][n]) and Y = Q (acc[.][2 + n]).
-template <bool CAUSAL, bool KREF>
-__device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, int q0, float* qs, float* os) {
+//
+// KEEP_P (causal): P comes from sst, written by bwd_kv_tile<CAUSAL, false,
+// true> (row = query, column = key within a 16 x 16 block, so one lane's four
+// keys are one 16-byte read); no S^T products, no K rows and no statistics
+// are needed, and the tile's dO rows stay in registers (qs, os unused).  The
+// block above the diagonal (the lower query block's last chunk) is not kept:
+// its P is 0 by the mask.
+template <bool CAUSAL, bool KREF, bool KEEP_P = false>
+__device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, int q0, float* qs, float* os,
+                                           const float* sst = nullptr) {
   const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
   const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
@@ -542,15 +561,23 @@ __device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, i
   const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
   const float* DC = a.dcol + (size_t)sl.z * a.seq;
+  f32x4 obr[2][4];
+  if (KEEP_P) {
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int idx = lane + 64 * u, row = idx >> 4, col = (idx & 15) * 4;
-    const uint32_t e = sl.base + (uint32_t)(q0 + row) * a.ld + col;
-    *reinterpret_cast<f32x4*>(qs + row * LQ + col) = bld4(Q, e);
-    *reinterpret_cast<f32x4*>(os + row * LQ + col) = bld4(dO, e);
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) obr[n][s] = bld4(dO, sl.base + (uint32_t)(q0 + 16 * n + lr) * a.ld + 16 * s + 4 * q);
+  } else {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = lane + 64 * u, row = idx >> 4, col = (idx & 15) * 4;
+      const uint32_t e = sl.base + (uint32_t)(q0 + row) * a.ld + col;
+      *reinterpret_cast<f32x4*>(qs + row * LQ + col) = bld4(Q, e);
+      *reinterpret_cast<f32x4*>(os + row * LQ + col) = bld4(dO, e);
+    }
+    // The region is the wave's own: its writes only have to land before its reads.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   }
-  // The region is the wave's own: its writes only have to land before its reads.
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -563,7 +590,7 @@ __device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, i
     const int k0 = 16 * c;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      ch.ka[s] = bld4(K, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
+      if (!KEEP_P) ch.ka[s] = bld4(K, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
       ch.va[s] = bld4(V, sl.base + (uint32_t)(k0 + lr) * a.ld + 16 * s + 4 * q);
     }
   };
@@ -571,8 +598,10 @@ __device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, i
   // statistics and D of its keys, and its Y rows (A of the last products).
   f32x4 yk[4], yq[4], s01, s23, dk;
   auto late = [&](int c) {
-    s01 = ld4(ST + (size_t)(16 * c + 4 * q) * 2);
-    s23 = ld4(ST + (size_t)(16 * c + 4 * q) * 2 + 4);
+    if (!KEEP_P) {
+      s01 = ld4(ST + (size_t)(16 * c + 4 * q) * 2);
+      s23 = ld4(ST + (size_t)(16 * c + 4 * q) * 2 + 4);
+    }
     dk = ld4(DC + 16 * c + 4 * q);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -591,22 +620,34 @@ __device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, i
       f32x4 qb[4], ob[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        qb[s] = *reinterpret_cast<const f32x4*>(qs + (16 * n + lr) * LQ + 16 * s + 4 * q);
-        ob[s] = *reinterpret_cast<const f32x4*>(os + (16 * n + lr) * LQ + 16 * s + 4 * q);
+        if (KEEP_P) {
+          ob[s] = obr[n][s];
+        } else {
+          qb[s] = *reinterpret_cast<const f32x4*>(qs + (16 * n + lr) * LQ + 16 * s + 4 * q);
+          ob[s] = *reinterpret_cast<const f32x4*>(os + (16 * n + lr) * LQ + 16 * s + 4 * q);
+        }
       }
       f32x4 st = {0.f, 0.f, 0.f, 0.f}, dt = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          st = mfma4(ch.ka[s][j], qb[s][j], st);
+          if (!KEEP_P) st = mfma4(ch.ka[s][j], qb[s][j], st);
           dt = mfma4(ch.va[s][j], ob[s][j], dt);
         }
       float ds[4];
+      if (KEEP_P) {
+        const int qb16 = q0 / 16 + n;
+        f32x4 pt = {0.f, 0.f, 0.f, 0.f};
+        if (c <= qb16) pt = *reinterpret_cast<const f32x4*>(sst + (qb16 * (qb16 + 1) / 2 + c) * 256 + lr * 16 + 4 * q);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool keep = !MASK || q0 + 16 * n + lr >= k0 + 4 * q + r;
-        ds[r] = __expf(a.scale * st[r] - mk[r]) * (keep ? il[r] : 0.f) * (dt[r] - dk[r]);
+        for (int r = 0; r < 4; ++r) ds[r] = pt[r] * (dt[r] - dk[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool keep = !MASK || q0 + 16 * n + lr >= k0 + 4 * q + r;
+          ds[r] = __expf(a.scale * st[r] - mk[r]) * (keep ? il[r] : 0.f) * (dt[r] - dk[r]);
+        }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
@@ -707,14 +748,21 @@ __global__ __launch_bounds__(SW * 64, 1) void attn_fwd_slice_kernel(AttnArgs a) 
   __syncthreads();  // the slice's statistics (and kept scores) are written
   if (w < ntile) fwd_tile<CAUSAL, CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW, sst);
 }
+// Causal: the dV pass keeps the slice's P blocks on or below the diagonal in
+// LDS (136 KB at seq 256) and the dQ pass reads them instead of recomputing
+// S^T and its exponentials; without the mask the dQ pass stages its Q and dO
+// rows in LDS and recomputes.
 template <bool CAUSAL, bool KREF>
 __global__ __launch_bounds__(SW * 64, 1) void attn_bwd_slice_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) float lds[SW][2][TW * LQ];
+  constexpr int kFloats = CAUSAL ? (SW * TW / 16) * (SW * TW / 16 + 1) / 2 * 256 : SW * 2 * TW * LQ;
+  __shared__ __attribute__((aligned(16))) float lds[kFloats];
   const Slice sl = slice_whole(a);
   const int w = threadIdx.x >> 6, ntile = a.seq / TW;
-  if (w < ntile) bwd_kv_tile<CAUSAL, !KREF>(a, sl, mirrored_tile(w, ntile) * TW);
-  __syncthreads();  // D of every key of the slice is written
-  if (w < ntile) bwd_q_tile<CAUSAL, KREF>(a, sl, mirrored_tile(w, ntile) * TW, lds[w][0], lds[w][1]);
+  if (w < ntile) bwd_kv_tile<CAUSAL, !KREF, CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW, lds);
+  __syncthreads();  // D of every key of the slice (and the kept P) is written
+  float* own = lds + w * 2 * TW * LQ;  // the wave's staging region (without the mask)
+  if (w < ntile)
+    bwd_q_tile<CAUSAL, KREF, CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW, own, own + TW * LQ, lds);
 }
 
 // Operand addressing uses 32-bit byte offsets into buffer resources whose
