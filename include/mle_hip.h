@@ -442,6 +442,23 @@ int mle_add_norm_partials(mle_stream stream, const float* a, const float* b, siz
 int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, const float* stats,
                  int batch, int channels, size_t hw, int groups, float eps, int reference_layout,
                  void* ws, size_t ws_bytes, int accumulate);
+/* mle_norm_bwd in its two passes, for a normalisation whose input is the
+ * output of a residual Add that nothing else reads (the post-norm
+ * transformer block, Engine/transformer.cu:647-661):
+ *   mle_norm_bwd_partials: the first pass (the sums of dy and dy*y) into ws,
+ *     at the normalisation's place in the backward;
+ *   mle_norm_bwd_apply_add: the second pass at the Add's place (Add backward,
+ *     Engine/engine.cu:1650-1672): dx (+)= the normalisation's input gradient
+ *     -- the Add's output gradient -- and the same values (+)= into dxa and
+ *     dxb, the Add's two input gradients (each with its own accumulate
+ *     flag; dxb may be null), in one pass.
+ * The same values, bit for bit, as mle_norm_bwd followed by the Add's
+ * backward (mle_accumulate2). */
+int mle_norm_bwd_partials(mle_stream stream, const float* y, const float* dy, int batch, int channels, size_t hw,
+                          int groups, int reference_layout, void* ws, size_t ws_bytes);
+int mle_norm_bwd_apply_add(mle_stream stream, const float* y, const float* dy, float* dx, int accumulate, float* dxa,
+                           int accumulate_a, float* dxb, int accumulate_b, const float* stats, int batch, int channels,
+                           size_t hw, int groups, float eps, int reference_layout, void* ws, size_t ws_bytes);
 
 /* BatchNorm: per-channel statistics over (batch, H, W), gamma 1, beta 0.
  * stats[2c] = mean, stats[2c+1] = sum (x - mean)^2; y = (x - mean) * r with

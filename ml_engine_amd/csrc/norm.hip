@@ -346,16 +346,21 @@ __global__ __launch_bounds__(64) void norm_bwd_final(const double* __restrict__ 
 }
 
 // dx (+)= r (dy - sum(dy)/N - y sum(dy*y)/N)  (LayerBackward/GroupBackward,
-// Engine/kernels.cu:849-896); acc = 0 assigns.  `quirk_hw` != 0 reproduces
+// Engine/kernels.cu:849-896); acc = 0 assigns.  dx2 and dx3, when set, then
+// receive dx's new value (acc2, acc3 each: add or assign): the gradients of
+// the two inputs of the Add that produced the normalised tensor, whose
+// backward (Engine/engine.cu:1650-1672) adds its whole output gradient -- dx
+// -- into both.  `quirk_hw` != 0 reproduces
 // LayerBackward for channels > 1: only elements e < batch*hw receive a
 // gradient, with group e / hw (the others are left alone, or set to 0 when
 // assigning, which is what adding nothing to a cleared gradient gives).
-template <bool SEG, bool VEC>
+template <bool SEG, bool VEC, bool EXTRA = false>  // EXTRA: dx2 set (dx3 may be)
 __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y, const float* __restrict__ dy,
                                                      float* __restrict__ dx, const float* __restrict__ stats,
                                                      NormShape sh, const double* __restrict__ part,
                                                      const double* __restrict__ fin, float eps, size_t quirk_hw,
-                                                     int acc) {
+                                                     int acc, float* __restrict__ dx2, int acc2,
+                                                     float* __restrict__ dx3, int acc3) {
   const int g = blockIdx.y, ck = blockIdx.x;
   const size_t c0 = (size_t)ck * CH;
   const float fN = (float)(int)sh.N;
@@ -384,12 +389,19 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
         const f32x4 yv = *reinterpret_cast<const f32x4*>(y + o);
         const f32x4 gv = *reinterpret_cast<const f32x4*>(dy + o);
         f32x4 d = acc ? *reinterpret_cast<const f32x4*>(dx + o) : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 d2 = {0.f, 0.f, 0.f, 0.f}, d3 = d2;
+        if (EXTRA && acc2) d2 = *reinterpret_cast<const f32x4*>(dx2 + o);
+        if (EXTRA && dx3 && acc3) d3 = *reinterpret_cast<const f32x4*>(dx3 + o);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const float v = r * (gv[k] - (sg / fN) - yv[k] * (sgy / fN));
           d[k] = acc ? d[k] + v : v;
+          d2[k] = acc2 ? d2[k] + d[k] : d[k];
+          d3[k] = acc3 ? d3[k] + d[k] : d[k];
         }
         *reinterpret_cast<f32x4*>(dx + o) = d;
+        if (EXTRA) *reinterpret_cast<f32x4*>(dx2 + o) = d2;
+        if (EXTRA && dx3) *reinterpret_cast<f32x4*>(dx3 + o) = d3;
       }
     }
     return;
@@ -401,13 +413,19 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
     const size_t idx = at<SEG>(sh, g, e);
     if (!SEG && quirk_hw) {
       if (idx >= (size_t)sh.groups_tot * quirk_hw) {
-        if (!acc) dx[idx] = 0.f;
+        const float nv = acc ? dx[idx] : 0.f;
+        dx[idx] = nv;
+        if (EXTRA) dx2[idx] = acc2 ? dx2[idx] + nv : nv;
+        if (EXTRA && dx3) dx3[idx] = acc3 ? dx3[idx] + nv : nv;
         continue;
       }
       terms((int)(idx / quirk_hw), sg, sgy, r);
     }
     const float v = r * (dy[idx] - (sg / fN) - y[idx] * (sgy / fN));
-    dx[idx] = acc ? dx[idx] + v : v;
+    const float nv = acc ? dx[idx] + v : v;
+    dx[idx] = nv;
+    if (EXTRA) dx2[idx] = acc2 ? dx2[idx] + nv : nv;
+    if (EXTRA && dx3) dx3[idx] = acc3 ? dx3[idx] + nv : nv;
   }
 }
 
@@ -464,15 +482,14 @@ void launch_fwd(hipStream_t s, const NormShape& sh, const float* x, float* y, fl
   });
 }
 
-// act >= 0: dy (+)= act'(y) * da first (acc_dy), stored, then the backward
-// from it.
-void launch_bwd(hipStream_t s, const NormShape& sh, const float* y, const float* dy, float* dx, const float* stats,
-                void* ws, float eps, size_t quirk, int accumulate, int act = -1, const float* da = nullptr,
-                int acc_dy = 0) {
+// The backward's first pass: per-chunk sums of dy and dy*y (act >= 0: dy (+)=
+// act'(y) * da first (acc_dy), stored, and the sums taken of that).
+void launch_bwd_partials(hipStream_t s, const NormShape& sh, const float* y, const float* dy, void* ws, size_t quirk,
+                         int act = -1, const float* da = nullptr, int acc_dy = 0) {
   dim3 grid(sh.nchunk, sh.groups_tot);
   double* part = static_cast<double*>(ws);
   double* fin = part + (size_t)sh.groups_tot * sh.nchunk * 2;
-  const bool v = vec_ok(sh, {y, dy, dx}) && (act < 0 || aligned16(da));
+  const bool v = vec_ok(sh, {y, dy}) && (act < 0 || aligned16(da));
   float* dyw = const_cast<float*>(dy);  // written only with act >= 0
   with_act(act, [&](auto K) {
     constexpr int A = decltype(K)::value;
@@ -484,14 +501,35 @@ void launch_bwd(hipStream_t s, const NormShape& sh, const float* y, const float*
       else norm_bwd_partial<false, false, A><<<grid, NT, 0, s>>>(y, dy, sh, part, da, dyw, acc_dy);
     }
   });
-  if (sh.seg) {
-    if (v) norm_bwd_apply<true, true><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, 0, accumulate);
-    else norm_bwd_apply<true, false><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, 0, accumulate);
+  if (!sh.seg && quirk) norm_bwd_final<<<sh.groups_tot, 64, 0, s>>>(part, sh, fin);
+}
+
+// The second pass, from the first pass's sums in ws: dx (and dx2, dx3 when set).
+void launch_bwd_apply(hipStream_t s, const NormShape& sh, const float* y, const float* dy, float* dx, int accumulate,
+                      const float* stats, void* ws, float eps, size_t quirk, float* dx2 = nullptr, int acc2 = 0,
+                      float* dx3 = nullptr, int acc3 = 0) {
+  dim3 grid(sh.nchunk, sh.groups_tot);
+  double* part = static_cast<double*>(ws);
+  double* fin = part + (size_t)sh.groups_tot * sh.nchunk * 2;
+  const bool v = vec_ok(sh, {y, dy, dx}) && (!dx2 || aligned16(dx2)) && (!dx3 || aligned16(dx3));
+  auto go = [&](auto kern, size_t qk) {
+    hipLaunchKernelGGL(kern, grid, dim3(NT), 0, s, y, dy, dx, stats, sh, part, fin, eps, qk, accumulate, dx2, acc2,
+                       dx3, acc3);
+  };
+  if (dx2) {
+    if (sh.seg) go(v ? norm_bwd_apply<true, true, true> : norm_bwd_apply<true, false, true>, 0);
+    else go(v ? norm_bwd_apply<false, true, true> : norm_bwd_apply<false, false, true>, quirk);
   } else {
-    if (quirk) norm_bwd_final<<<sh.groups_tot, 64, 0, s>>>(part, sh, fin);
-    if (v) norm_bwd_apply<false, true><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, quirk, accumulate);
-    else norm_bwd_apply<false, false><<<grid, NT, 0, s>>>(y, dy, dx, stats, sh, part, fin, eps, quirk, accumulate);
+    if (sh.seg) go(v ? norm_bwd_apply<true, true> : norm_bwd_apply<true, false>, 0);
+    else go(v ? norm_bwd_apply<false, true> : norm_bwd_apply<false, false>, quirk);
   }
+}
+
+void launch_bwd(hipStream_t s, const NormShape& sh, const float* y, const float* dy, float* dx, const float* stats,
+                void* ws, float eps, size_t quirk, int accumulate, int act = -1, const float* da = nullptr,
+                int acc_dy = 0) {
+  launch_bwd_partials(s, sh, y, dy, ws, quirk, act, da, acc_dy);
+  launch_bwd_apply(s, sh, y, dy, dx, accumulate, stats, ws, eps, quirk);
 }
 
 int shape_of(int batch, int channels, size_t hw, int groups, NormShape& sh) {
@@ -676,6 +714,33 @@ int mle_add_norm_partials(mle_stream stream, const float* a, const float* b, siz
   if (v) add_stats_partial<true><<<grid, NT, 0, s>>>(a, b, b_period, y, sh, part);
   else add_stats_partial<false><<<grid, NT, 0, s>>>(a, b, b_period, y, sh, part);
   return check_launch("mle_add_norm_partials");
+}
+
+int mle_norm_bwd_partials(mle_stream stream, const float* y, const float* dy, int batch, int channels, size_t hw,
+                          int groups, int reference_layout, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(y && dy && ws, "mle_norm_bwd_partials: null pointer");
+  NormShape sh;
+  int rc = shape_of(batch, channels, hw, groups, sh);
+  if (rc) return rc;
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_bwd_partials: workspace too small");
+  const size_t quirk = (reference_layout && groups == 1 && channels > 1) ? hw : 0;
+  launch_bwd_partials(as_stream(stream), sh, y, dy, ws, quirk);
+  return check_launch("mle_norm_bwd_partials");
+}
+
+int mle_norm_bwd_apply_add(mle_stream stream, const float* y, const float* dy, float* dx, int accumulate, float* dxa,
+                           int accumulate_a, float* dxb, int accumulate_b, const float* stats, int batch, int channels,
+                           size_t hw, int groups, float eps, int reference_layout, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(y && dy && dx && stats && ws && (dxa || !dxb), "mle_norm_bwd_apply_add: bad argument");
+  MLE_CHECK_ARG(dxa != dx && (!dxb || (dxb != dx && dxb != dxa)), "mle_norm_bwd_apply_add: outputs must differ");
+  NormShape sh;
+  int rc = shape_of(batch, channels, hw, groups, sh);
+  if (rc) return rc;
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_bwd_apply_add: workspace too small");
+  const size_t quirk = (reference_layout && groups == 1 && channels > 1) ? hw : 0;
+  launch_bwd_apply(as_stream(stream), sh, y, dy, dx, accumulate, stats, ws, eps, quirk, dxa, accumulate_a, dxb,
+                   accumulate_b);
+  return check_launch("mle_norm_bwd_apply_add");
 }
 
 int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, const float* stats, int batch,

@@ -783,7 +783,7 @@ void GraphOperations::backward(const graph& X, const bool show, const bool time,
     return;
   }
   mle::clip_apply_all();  // parameter gradients are added into: give them their clipped values
-  for (auto& n : nodes) n->consumers = 0;
+  for (auto& n : nodes) n->consumers = n->consumers_done = 0;
   for (auto& n : nodes)
     for (auto& in : n->inputs)
       if (in) in->consumers++;
@@ -803,6 +803,8 @@ void GraphOperations::backward(const graph& X, const bool show, const bool time,
       if (check_nan) nan_check(it->get(), 1);
       if (show) printHeadGPU(*it, 1);
     }
+    for (auto& in : (*it)->inputs)
+      if (in) in->consumers_done++;
     if (time) {
       mle::sync("After " + (*it)->op_name + " backward");
       const double ms =

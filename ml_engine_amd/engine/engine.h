@@ -213,9 +213,19 @@ struct NodeBackProp {
   int act_grad_kind = -1;
   int act_grad_acc = 0;
   bool takes_act_grad = false;  // this node's backward handles act_grad_in
+  // Backward hand-off (additive), the other way round: a normalisation whose
+  // input is this node, and which is the last of this node's consumers to
+  // run its backward, runs its first pass and leaves the second here; this
+  // node's backward (an Add's or MatPE's) calls it with its inputs' gradients
+  // and their accumulate flags, so that one pass writes this node's gradient
+  // and its inputs' at this node's place (the same order of additions).
+  std::function<void(float* da, int acc_a, float* db, int acc_b)> grad_apply;
+  bool takes_norm_grad = false;  // this node's backward handles grad_apply
   // Number of nodes reading this node's output in the graph being
-  // back-propagated (set by GraphOperations::backward).
+  // back-propagated, and how many of them have run their backward so far
+  // (both kept by GraphOperations::backward).
   int consumers = 0;
+  int consumers_done = 0;
 
   virtual void update(const float lr = LEARNING_RATE, const bool W = ADAMW) {}
   NodeBackProp(str name, int batch, int d1, int d2, int d3, int allocation);

@@ -206,6 +206,20 @@ graph norm_node(const graph& X, int groups, const str& name) {
             name + " backward (with the activation after it)");
       return;
     }
+    // An Add or MatPE producer whose other consumers are all done: our first
+    // pass now, the second at the producer's place, writing its gradient and
+    // its inputs'.
+    if (mle::fusion_enabled() && x->takes_norm_grad && x->consumers_done + 1 == x->consumers) {
+      const int acc_x = mle::accumulate_flag(x);
+      check(mle_norm_bwd_partials(S(), nd->output, nd->grad, a, b, hw, groups, ref_layout, ws, ws_bytes),
+            name + " backward (first pass)");
+      x->grad_apply = [=](float* da, int acc_a, float* db, int acc_b) {
+        check(mle_norm_bwd_apply_add(S(), nd->output, nd->grad, x->grad, acc_x, da, acc_a, db, acc_b, stats, a, b, hw,
+                                     groups, eps, ref_layout, ws, ws_bytes),
+              name + " backward (second pass, into the Add's inputs)");
+      };
+      return;
+    }
     check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, ref_layout, ws, ws_bytes,
                        mle::accumulate_flag(x)),
           name + " backward");
@@ -332,7 +346,16 @@ graph GraphOperations::MatrixPositionalEncoding(const graph& X, const int start_
                                 groups, ws, ws_bytes),
           "MatPE forward (with the normalisation statistics)");
   };
-  node->backward = [=]() { add_grad(x, nd->grad, 1.0, nd->total, "MatPE backward"); };
+  node->takes_norm_grad = true;
+  node->backward = [=]() {
+    if (nd->grad_apply) {  // the normalisation after this node left its second pass (see norm_node)
+      auto apply = std::move(nd->grad_apply);
+      nd->grad_apply = nullptr;
+      apply(x->grad, mle::accumulate_flag(x), nullptr, 0);
+      return;
+    }
+    add_grad(x, nd->grad, 1.0, nd->total, "MatPE backward");
+  };
   std_hooks(node);
   return node;
 }
@@ -411,9 +434,20 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
             "Add forward (with the activation after it)");
     };
     node->takes_act_grad = true;
+    node->takes_norm_grad = true;
   }
   node->backward = [=]() {
     if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
+    if (nd->grad_apply) {  // the normalisation after this node left its second pass (see norm_node)
+      auto apply = std::move(nd->grad_apply);
+      nd->grad_apply = nullptr;
+      if (pa != pb && pa->grad != pb->grad) {
+        const int acc_a = mle::accumulate_flag(pa), acc_b = mle::accumulate_flag(pb);
+        apply(pa->grad, acc_a, pb->grad, acc_b);
+        return;
+      }
+      apply(nullptr, 0, nullptr, 0);  // our gradient only; the inputs' below
+    }
     if (nd->act_grad_in) {  // the activation after this node left its gradient (see act_node)
       const float* da = nd->act_grad_in;
       nd->act_grad_in = nullptr;

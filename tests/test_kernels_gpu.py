@@ -588,6 +588,57 @@ def test_norm_act_fused(hip, batch, channels, hw, groups, kind):
         np.testing.assert_array_equal(dx2.numpy().view(np.uint32), dx1.numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("batch,channels,hw,groups,layout", [
+    (4, 1, 256 * 64, 1, 1),   # LayerNorm over a [seq x d] sample, vector path
+    (3, 1, 4099, 1, 1),       # ragged, scalar path
+    (2, 8, 144, 4, 1),        # GroupNorm
+    (2, 3, 50, 1, 1),         # LayerNorm with C > 1 under the reference's guard (only batch*hw elements)
+])
+def test_norm_bwd_apply_add(hip, batch, channels, hw, groups, layout):
+    """The normalisation backward split in two passes, the second writing the
+    producing Add's gradient and both of its inputs' (mle_norm_bwd_partials +
+    mle_norm_bwd_apply_add), gives the bits of mle_norm_bwd followed by the
+    Add's backward (mle_accumulate2) -- every assign / add combination, and
+    with the second input absent."""
+    r = rng(batch * 5 + channels + hw + groups)
+    shape = (batch, channels, hw)
+    n = batch * channels * hw
+    x = (r.standard_normal(shape, dtype=np.float32) * 2 + 0.5).astype(np.float32)
+    dy = r.standard_normal(shape, dtype=np.float32)
+    g0, a0, b0 = (r.standard_normal(shape, dtype=np.float32) for _ in range(3))
+    L = hip.lib()
+    ws = hip.Buffer(L.mle_norm_ws_bytes(batch, channels, hw, groups))
+    gx, gdy = B(hip, x), B(hip, dy)
+    y, st = hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * batch * groups)
+    hip.call("mle_norm_fwd", None, gx.ptr, y.ptr, st.ptr, batch, channels, hw, groups, 1e-5, ws.ptr, ws.nbytes)
+    nan = np.full(shape, np.nan, np.float32)
+    for acc, acc_a, acc_b in ((0, 0, 0), (1, 1, 1), (0, 1, 0), (1, 0, 1)):
+        g1, a1, b1 = B(hip, g0 if acc else nan), B(hip, a0), B(hip, b0)
+        hip.call("mle_norm_bwd", None, y.ptr, gdy.ptr, g1.ptr, st.ptr, batch, channels, hw, groups, 1e-5, layout,
+                 ws.ptr, ws.nbytes, acc)
+        hip.call("mle_accumulate2", None, g1.ptr, a1.ptr, acc_a, b1.ptr, acc_b, n)
+        g2, a2, b2 = B(hip, g0 if acc else nan), B(hip, a0 if acc_a else nan), B(hip, b0 if acc_b else nan)
+        hip.call("mle_norm_bwd_partials", None, y.ptr, gdy.ptr, batch, channels, hw, groups, layout, ws.ptr, ws.nbytes)
+        hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g2.ptr, acc, a2.ptr, acc_a, b2.ptr, acc_b, st.ptr,
+                 batch, channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
+        for want, got, what in ((g1, g2, "own"), (a1, a2, "a"), (b1, b2, "b")):
+            np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32),
+                                          err_msg=f"{what} acc={acc},{acc_a},{acc_b}")
+    # one input only
+    g3, a3 = B(hip, nan), B(hip, a0)
+    hip.call("mle_norm_bwd_partials", None, y.ptr, gdy.ptr, batch, channels, hw, groups, layout, ws.ptr, ws.nbytes)
+    hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 0, a3.ptr, 1, None, 0, st.ptr, batch, channels,
+             hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
+    g4 = B(hip, nan)
+    hip.call("mle_norm_bwd", None, y.ptr, gdy.ptr, g4.ptr, st.ptr, batch, channels, hw, groups, 1e-5, layout,
+             ws.ptr, ws.nbytes, 0)
+    np.testing.assert_array_equal(g3.numpy().view(np.uint32), g4.numpy().view(np.uint32))
+    np.testing.assert_array_equal(a3.numpy().view(np.uint32), (a0 + g4.numpy()).view(np.uint32))
+    with pytest.raises(hip.MLEError):  # the destinations must differ
+        hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 0, g3.ptr, 0, None, 0, st.ptr, batch,
+                 channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
+
+
 @pytest.mark.parametrize("batch,channels,hw", [(4, 3, 25), (16, 128, 64 * 64), (3, 5, 4099), (1, 1, 9000)])
 def test_batchnorm(hip, orc, batch, channels, hw):
     r = rng(batch * 3 + channels + hw)
