@@ -442,20 +442,23 @@ int mle_add_norm_partials(mle_stream stream, const float* a, const float* b, siz
 int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, const float* stats,
                  int batch, int channels, size_t hw, int groups, float eps, int reference_layout,
                  void* ws, size_t ws_bytes, int accumulate);
-/* mle_norm_bwd in its two passes, for a normalisation whose input is the
- * output of a residual Add that nothing else reads (the post-norm
- * transformer block, Engine/transformer.cu:647-661):
+/* mle_norm_bwd (or mle_norm_bwd_act) in its two passes, for a normalisation
+ * whose input is produced by an Add or MatPE that no other node reads after
+ * the normalisation's backward (the pre-norm transformer block,
+ * Engine/transformer.cu:647-661):
  *   mle_norm_bwd_partials: the first pass (the sums of dy and dy*y) into ws,
- *     at the normalisation's place in the backward;
- *   mle_norm_bwd_apply_add: the second pass at the Add's place (Add backward,
- *     Engine/engine.cu:1650-1672): dx (+)= the normalisation's input gradient
- *     -- the Add's output gradient -- and the same values (+)= into dxa and
- *     dxb, the Add's two input gradients (each with its own accumulate
- *     flag; dxb may be null), in one pass.
- * The same values, bit for bit, as mle_norm_bwd followed by the Add's
- * backward (mle_accumulate2). */
-int mle_norm_bwd_partials(mle_stream stream, const float* y, const float* dy, int batch, int channels, size_t hw,
-                          int groups, int reference_layout, void* ws, size_t ws_bytes);
+ *     at the normalisation's place in the backward; with kind >= 0 it first
+ *     forms dy (+)= act'(y) * da (accumulate_dy), stored, as mle_norm_bwd_act;
+ *   mle_norm_bwd_apply_add: the second pass at the producer's place (Add
+ *     backward, Engine/engine.cu:1650-1672; MatPE, 1263-1296): dx (+)= the
+ *     normalisation's input gradient -- the producer's output gradient --
+ *     and the new dx (+)= into dxa and dxb, the producer's input gradients
+ *     (each with its own accumulate flag; dxb may be null), in one pass.
+ * The same values, bit for bit, as mle_norm_bwd (_act) followed by the
+ * producer's gradient copies (mle_accumulate2 / accumulate at scale 1). */
+int mle_norm_bwd_partials(mle_stream stream, const float* y, float* dy, const float* da, int kind, int accumulate_dy,
+                          int batch, int channels, size_t hw, int groups, int reference_layout, void* ws,
+                          size_t ws_bytes);
 int mle_norm_bwd_apply_add(mle_stream stream, const float* y, const float* dy, float* dx, int accumulate, float* dxa,
                            int accumulate_a, float* dxb, int accumulate_b, const float* stats, int batch, int channels,
                            size_t hw, int groups, float eps, int reference_layout, void* ws, size_t ws_bytes);

@@ -716,15 +716,18 @@ int mle_add_norm_partials(mle_stream stream, const float* a, const float* b, siz
   return check_launch("mle_add_norm_partials");
 }
 
-int mle_norm_bwd_partials(mle_stream stream, const float* y, const float* dy, int batch, int channels, size_t hw,
-                          int groups, int reference_layout, void* ws, size_t ws_bytes) {
-  MLE_CHECK_ARG(y && dy && ws, "mle_norm_bwd_partials: null pointer");
+int mle_norm_bwd_partials(mle_stream stream, const float* y, float* dy, const float* da, int kind, int accumulate_dy,
+                          int batch, int channels, size_t hw, int groups, int reference_layout, void* ws,
+                          size_t ws_bytes) {
+  MLE_CHECK_ARG(y && dy && ws && (kind < 0 || (da && kind >= MLE_RELU && kind <= MLE_LEAKY_RELU)),
+                "mle_norm_bwd_partials: bad argument");
   NormShape sh;
   int rc = shape_of(batch, channels, hw, groups, sh);
   if (rc) return rc;
   if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_bwd_partials: workspace too small");
   const size_t quirk = (reference_layout && groups == 1 && channels > 1) ? hw : 0;
-  launch_bwd_partials(as_stream(stream), sh, y, dy, ws, quirk);
+  launch_bwd_partials(as_stream(stream), sh, y, dy, ws, quirk, kind < 0 ? -1 : kind, kind < 0 ? nullptr : da,
+                      accumulate_dy);
   return check_launch("mle_norm_bwd_partials");
 }
 

@@ -198,26 +198,28 @@ graph norm_node(const graph& X, int groups, const str& name) {
   };
   node->takes_act_grad = true;
   node->backward = [=]() {
-    if (nd->act_grad_in) {  // the activation after this node left its gradient (see act_node)
-      const float* da = nd->act_grad_in;
-      nd->act_grad_in = nullptr;
-      check(mle_norm_bwd_act(S(), nd->output, da, nd->act_grad_kind, nd->grad, nd->act_grad_acc, x->grad, stats, a,
-                             b, hw, groups, eps, ref_layout, ws, ws_bytes, mle::accumulate_flag(x)),
-            name + " backward (with the activation after it)");
-      return;
-    }
+    // The activation after this node may have left its gradient (see act_node).
+    const float* da = nd->act_grad_in;
+    nd->act_grad_in = nullptr;
     // An Add or MatPE producer whose other consumers are all done: our first
     // pass now, the second at the producer's place, writing its gradient and
     // its inputs'.
     if (mle::fusion_enabled() && x->takes_norm_grad && x->consumers_done + 1 == x->consumers) {
       const int acc_x = mle::accumulate_flag(x);
-      check(mle_norm_bwd_partials(S(), nd->output, nd->grad, a, b, hw, groups, ref_layout, ws, ws_bytes),
+      check(mle_norm_bwd_partials(S(), nd->output, nd->grad, da, da ? nd->act_grad_kind : -1, nd->act_grad_acc, a, b,
+                                  hw, groups, ref_layout, ws, ws_bytes),
             name + " backward (first pass)");
       x->grad_apply = [=](float* da, int acc_a, float* db, int acc_b) {
         check(mle_norm_bwd_apply_add(S(), nd->output, nd->grad, x->grad, acc_x, da, acc_a, db, acc_b, stats, a, b, hw,
                                      groups, eps, ref_layout, ws, ws_bytes),
-              name + " backward (second pass, into the Add's inputs)");
+              name + " backward (second pass, into the producer's inputs)");
       };
+      return;
+    }
+    if (da) {
+      check(mle_norm_bwd_act(S(), nd->output, da, nd->act_grad_kind, nd->grad, nd->act_grad_acc, x->grad, stats, a,
+                             b, hw, groups, eps, ref_layout, ws, ws_bytes, mle::accumulate_flag(x)),
+            name + " backward (with the activation after it)");
       return;
     }
     check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, ref_layout, ws, ws_bytes,

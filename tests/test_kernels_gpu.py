@@ -618,7 +618,8 @@ def test_norm_bwd_apply_add(hip, batch, channels, hw, groups, layout):
                  ws.ptr, ws.nbytes, acc)
         hip.call("mle_accumulate2", None, g1.ptr, a1.ptr, acc_a, b1.ptr, acc_b, n)
         g2, a2, b2 = B(hip, g0 if acc else nan), B(hip, a0 if acc_a else nan), B(hip, b0 if acc_b else nan)
-        hip.call("mle_norm_bwd_partials", None, y.ptr, gdy.ptr, batch, channels, hw, groups, layout, ws.ptr, ws.nbytes)
+        hip.call("mle_norm_bwd_partials", None, y.ptr, gdy.ptr, None, -1, 0, batch, channels, hw, groups, layout, ws.ptr,
+                 ws.nbytes)
         hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g2.ptr, acc, a2.ptr, acc_a, b2.ptr, acc_b, st.ptr,
                  batch, channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
         for want, got, what in ((g1, g2, "own"), (a1, a2, "a"), (b1, b2, "b")):
@@ -626,7 +627,8 @@ def test_norm_bwd_apply_add(hip, batch, channels, hw, groups, layout):
                                           err_msg=f"{what} acc={acc},{acc_a},{acc_b}")
     # one input only
     g3, a3 = B(hip, nan), B(hip, a0)
-    hip.call("mle_norm_bwd_partials", None, y.ptr, gdy.ptr, batch, channels, hw, groups, layout, ws.ptr, ws.nbytes)
+    hip.call("mle_norm_bwd_partials", None, y.ptr, gdy.ptr, None, -1, 0, batch, channels, hw, groups, layout, ws.ptr,
+                 ws.nbytes)
     hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 0, a3.ptr, 1, None, 0, st.ptr, batch, channels,
              hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
     g4 = B(hip, nan)
@@ -637,6 +639,40 @@ def test_norm_bwd_apply_add(hip, batch, channels, hw, groups, layout):
     with pytest.raises(hip.MLEError):  # the destinations must differ
         hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 0, g3.ptr, 0, None, 0, st.ptr, batch,
                  channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
+
+
+@pytest.mark.parametrize("batch,channels,hw,groups", [(2, 8, 144, 4), (2, 16, 64 * 64, 8)])
+def test_norm_bwd_act_apply_add(hip, batch, channels, hw, groups):
+    """GroupNorm -> SiLU backward in two passes, the second writing the
+    producer's gradient and one input's (as after a MatPE): the bits of
+    mle_norm_bwd_act followed by the producer's gradient copy at scale 1, for
+    every assign / add combination."""
+    r = rng(batch * 11 + channels + hw)
+    shape = (batch, channels, hw)
+    n = batch * channels * hw
+    x = (r.standard_normal(shape, dtype=np.float32) * 2 - 0.3).astype(np.float32)
+    da = r.standard_normal(shape, dtype=np.float32)
+    dy0, g0, a0 = (r.standard_normal(shape, dtype=np.float32) for _ in range(3))
+    L = hip.lib()
+    ws = hip.Buffer(L.mle_norm_ws_bytes(batch, channels, hw, groups))
+    gx, gda = B(hip, x), B(hip, da)
+    y, st = hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * batch * groups)
+    hip.call("mle_norm_fwd", None, gx.ptr, y.ptr, st.ptr, batch, channels, hw, groups, 1e-5, ws.ptr, ws.nbytes)
+    nan = np.full(shape, np.nan, np.float32)
+    silu = 2
+    for acc_dy, acc, acc_a in ((0, 0, 0), (1, 1, 1), (0, 1, 0), (1, 0, 1)):
+        dy1, g1, a1 = B(hip, dy0 if acc_dy else nan), B(hip, g0 if acc else nan), B(hip, a0)
+        hip.call("mle_norm_bwd_act", None, y.ptr, gda.ptr, silu, dy1.ptr, acc_dy, g1.ptr, st.ptr, batch, channels, hw,
+                 groups, 1e-5, 1, ws.ptr, ws.nbytes, acc)
+        hip.call("mle_accumulate" if acc_a else "mle_scale_assign", None, g1.ptr, a1.ptr, 1.0, n)
+        dy2, g2, a2 = (B(hip, dy0 if acc_dy else nan), B(hip, g0 if acc else nan), B(hip, a0 if acc_a else nan))
+        hip.call("mle_norm_bwd_partials", None, y.ptr, dy2.ptr, gda.ptr, silu, acc_dy, batch, channels, hw, groups, 1,
+                 ws.ptr, ws.nbytes)
+        hip.call("mle_norm_bwd_apply_add", None, y.ptr, dy2.ptr, g2.ptr, acc, a2.ptr, acc_a, None, 0, st.ptr, batch,
+                 channels, hw, groups, 1e-5, 1, ws.ptr, ws.nbytes)
+        for want, got, what in ((dy1, dy2, "dy"), (g1, g2, "own"), (a1, a2, "a")):
+            np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32),
+                                          err_msg=f"{what} acc={acc_dy},{acc},{acc_a}")
 
 
 @pytest.mark.parametrize("batch,channels,hw", [(4, 3, 25), (16, 128, 64 * 64), (3, 5, 4099), (1, 1, 9000)])
