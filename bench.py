@@ -190,10 +190,12 @@ def extras_gemm(cpu: bool) -> dict:
             hip.sync()
         return w
 
-    reps(3)()
+    # ~40 ms of warm-up: the shader clock settles under sustained MFMA load
+    # (after a few launches the pass reads up to 10 % slow).
+    reps(40)()
     t0 = time.perf_counter()
-    reps(20)()
-    ms = (time.perf_counter() - t0) * 1e3 / 20
+    reps(40)()
+    ms = (time.perf_counter() - t0) * 1e3 / 40
     flop = 2.0 * 2.0 * M * N * K
     fam = dominant(["gemm_nt", "gemm_tn"], reps(5))
     out = {"workload": "C3 Linear backward dX, dW, db (8192x1024x4096)", "ms": round(ms, 4),
@@ -240,8 +242,8 @@ def extras_adamw(cpu: bool, steps: int = 10) -> dict:
             m.grads_restore()
         m.sync()
 
-    run(2)
-    restores(2)
+    run(10)
+    restores(10)
     t0 = time.perf_counter()
     run()
     t1 = time.perf_counter()

@@ -39,13 +39,13 @@ args_trace() {
   case $1 in
     c4) echo "--steps 10 --warmup 5 --no-cpu --no-extras --no-graph" ;;
     c5) echo "--only c5 --no-cpu --no-graph --steps 10" ;;
-    c3) echo "--only c3 --no-cpu" ;;                          # 3 + 20 + 10 + 10 = 43 (dX + dW) passes
+    c3) echo "--only c3 --no-cpu" ;;                          # 40 + 40 + 2 x 5 + 10 = 100 (dX + dW) passes
     c2) echo "--only c2 --no-cpu --steps 5" ;;
     c1) echo "--only c1 --no-cpu --no-graph" ;;
   esac
 }
 steps_trace() {
-  case $1 in c4) echo "5 adam" ;; c5) echo "5 adam" ;; c3) echo 43 ;; c2) echo "5 adam" ;; c1) echo "20 adam" ;; esac
+  case $1 in c4) echo "5 adam" ;; c5) echo "5 adam" ;; c3) echo 100 ;; c2) echo "5 adam" ;; c1) echo "20 adam" ;; esac
 }
 args_pmc() {
   case $1 in
