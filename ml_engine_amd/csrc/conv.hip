@@ -550,19 +550,56 @@ __device__ __forceinline__ void conv_block_out(f32x4 (&acc)[4][4], const Conv3Ar
           for (int r = 0; r < 4; ++r) acc[i][n][r] += src[((i * 4 + n) * 4 + r) * 64];
     }
   }
+  // Every bias or previous value is loaded before the first store: the
+  // vector memory counter also counts stores, so a load between two stores
+  // would make the second wait for the first to complete.
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
+  uint32_t off[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = m0 + 16 * i + 4 * q + r;
-      const bool ok = gok && row < c.M;
-      const uint32_t off = ok ? (uint32_t)((b * c.M + row) * c.hw + p) * 4u : kOOB;
-      f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
-      if (!DG && c.bias && ok) v += c.bias[row];
-      if (DG && c.acc) v += buf_ld4(ro, off);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, (int)off, 0, 0);
+      off[i][r] = gok && row < c.M ? (uint32_t)((b * c.M + row) * c.hw + p) * 4u : kOOB;
     }
+  auto put = [&](int i, int r, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, (int)off[i][r], 0, 0);
+  };
+  if (!DG) {
+    // Rows past M read 0 (and store nowhere).
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(c.bias, c.bias ? (uint32_t)c.M * 4u : 0u);
+    float bv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bv[i][r] = buf_ld1(rb, (uint32_t)(m0 + 16 * i + 4 * q + r) * 4u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+        if (c.bias) v += bv[i][r];
+        put(i, r, v);
+      }
+  } else if (c.acc) {
+    f32x4 old[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) old[i][r] = buf_ld4(ro, off[i][r]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+        put(i, r, v + old[i][r]);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) put(i, r, f32x4{acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]});
+  }
 }
 
 template <bool DG, bool HALO, int WM, int WN, int KS, int U, int D>
@@ -752,6 +789,43 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv1_direct_kernel(Conv
   };
 
   f32x4 fa[D][4], fb[D][4];
+  if (!DG && KS == 1 && k1 - k0 <= D) {
+    // Forward with every stage resident at once (cs <= 16 D): the 16-row
+    // blocks finish one at a time, so a block's stores drain while the next
+    // block's products run instead of all stores waiting for the last product.
+    // Each sum takes the stages and channels in the order of the loop below
+    // and adds the bias last, as conv_block_out does: the same bits.
+#pragma unroll
+    for (int s = 0; s < D; ++s) load(k0 + s, fa[s], fb[s]);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(c.bias, c.bias ? (uint32_t)c.M * 4u : 0u);
+    float bv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bv[i][r] = buf_ld1(rb, (uint32_t)(m0 + 16 * i + 4 * q + r) * 4u);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int s = 0; s < D; ++s)
+        if (k0 + s < k1)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+              acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][i][u], fb[s][u][n], acc[i][n], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + 16 * i + 4 * q + r;
+        const bool ok = gok && row < c.M;
+        const uint32_t off = ok ? (uint32_t)((b * c.M + row) * c.hw + p) * 4u : kOOB;
+        f32x4 v = {acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+        if (c.bias) v += bv[i][r];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, (int)off, 0, 0);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) load(k0 + s, fa[s], fb[s]);
   int kt = k0;
@@ -970,13 +1044,18 @@ __global__ __launch_bounds__(256, 2) void conv3_wgrad_kernel(Wgrad3Args c) {
 // (lr, q) owns the four columns ci0 .. ci0 + 3 (ci0 = the wave's first
 // column + 4 lr) as the four MFMA column blocks: one aligned float4 of x per
 // column per stage, and a 16-byte store per (block i, r).  The lane's pixel
-// advances 16 per stage with at most one image carry (H * W >= 16).
-template <int WM, int D>
+// advances 16 per stage with at most one image carry (H * W >= 16).  The
+// four waves are WM x WN blocks of 64 x 64 times KS = 4 / (WM WN) shares of
+// the split's stages (the host sizes WN to cin, so no wave computes columns
+// past cin); shares ks > 0 hand their blocks and bias sums to share 0
+// through LDS, which adds them in ks order.
+template <int WM, int WN, int D>
 __global__ __launch_bounds__(256, 2) void conv1_wgrad_kernel(Wgrad3Args c) {
-  constexpr int WN = 4 / WM;
+  constexpr int KS = 4 / (WM * WN);
+  static_assert(WM * WN * KS == 4, "four waves");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, q = lane >> 4;
-  const int wm = wave % WM, wn = wave / WM;
+  const int wm = wave % WM, wn = (wave / WM) % WN, ks = wave / (WM * WN);
   const int L = blockIdx.x, xq = c.items / 8, xr = c.items % 8, xc = L % 8;
   const int item = xc * xq + min(xc, xr) + L / 8;
   const int tile = item % c.tiles, split = item / c.tiles;
@@ -984,7 +1063,10 @@ __global__ __launch_bounds__(256, 2) void conv1_wgrad_kernel(Wgrad3Args c) {
   const int m0 = (tm * WM + wm) * 64;
   const int ci0 = (tn * WN + wn) * 64 + 4 * lr;
   const bool cok = ci0 < c.cin;  // cin % 4 == 0: all four columns or none
-  const int kbeg = split * c.chunk, kend = min(c.npix, kbeg + c.chunk);
+  // Share ks: pixels [kbeg, kend) of the split, whole 16-pixel stages.
+  const int sbeg = split * c.chunk, send = min(c.npix, sbeg + c.chunk);
+  const int nks = ((send - sbeg + 15) / 16 + KS - 1) / KS;
+  const int kbeg = min(send, sbeg + ks * nks * 16), kend = min(send, kbeg + nks * 16);
   const int nk = (kend - kbeg + 15) / 16;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(c.x, c.x_bytes);
   const __amdgpu_buffer_rsrc_t rd = make_rsrc(c.dy, c.dy_bytes);
@@ -1066,6 +1148,38 @@ __global__ __launch_bounds__(256, 2) void conv1_wgrad_kernel(Wgrad3Args c) {
   for (int s = 0; s < D - 1; ++s)
     if (kt + s < nk) mfma(fa[s], fb[s]);
 
+  if (KS > 1) {
+    constexpr int RW = 64 * 64 + 4 * 64;  // a wave's block, then its bias sums
+    __shared__ float red[KS > 1 ? (KS - 1) * WM * WN * RW : 1];
+    const int blk = wave % (WM * WN);
+    if (ks > 0) {
+      float* dst = red + ((ks - 1) * WM * WN + blk) * RW + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[((i * 4 + n) * 4 + r) * 64] = acc[i][n][r];
+      if (do_b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[(64 + i) * 64] = bs[i];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll 1
+    for (int k = 1; k < KS; ++k) {
+      const float* src = red + ((k - 1) * WM * WN + blk) * RW + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][n][r] += src[((i * 4 + n) * 4 + r) * 64];
+      if (do_b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bs[i] += src[(64 + i) * 64];
+    }
+  }
   if (do_b) bias_store(c, bs, m0, split, lr, q);
   // (i, r) is row m0 + 16 i + 4 q + r, columns ci0 .. ci0 + 3.
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(c.out, c.out_bytes);
@@ -1177,39 +1291,47 @@ bool fast_filter(const ConvGeom& g) {
   return g.stride == 1 && ((g.kh == 3 && g.kw == 3) || (g.kh == 1 && g.kw == 1));
 }
 
-// Workgroups of conv3_wgrad_kernel<WM, 4> resident at once on the current
-// device (per-CU occupancy x CUs; 3 x 256 on MI355X).  One full round of
-// resident workgroups measured fastest: at 512 workgroups on 768 slots some
-// CUs hold 1 and others 3 (54 % of fp32 MFMA for the C5 weight gradients),
-// at 768 every CU holds 3 (77 %), at 1024 the last 256 run as a tail (62 %).
-int wgrad_slots(int taps, int wm) {
-  static int cached[64][2][2] = {};
+// Workgroups of `kernel` (256 threads) resident at once on the current
+// device (per-CU occupancy x CUs), cached per device in `cache`.
+template <class K>
+int resident_wgs(K kernel, int (&cache)[64]) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 768;
-  int& v = cached[dev][taps == 9][wm - 1];
+  int& v = cache[dev];
   if (v <= 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    hipError_t e;
-    if (taps == 9)
-      e = wm == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3_wgrad_kernel<1, 4>, 256, 0)
-                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv3_wgrad_kernel<2, 4>, 256, 0);
-    else
-      e = wm == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv1_wgrad_kernel<1, 4>, 256, 0)
-                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, conv1_wgrad_kernel<2, 4>, 256, 0);
-    if (e != hipSuccess || per_cu <= 0) per_cu = 2;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu <= 0) per_cu = 2;
     v = per_cu * cus;
   }
   return v;
 }
 
+// Workgroups of the weight-gradient kernel for (taps, wm, wn) resident at
+// once (3 x 256 on MI355X for the 3 x 3 kernel).  One full round of resident
+// workgroups measured fastest: at 512 workgroups on 768 slots some CUs hold
+// 1 and others 3 (54 % of fp32 MFMA for the C5 weight gradients), at 768
+// every CU holds 3 (77 %), at 1024 the last 256 run as a tail (62 %).
+int wgrad_slots(int taps, int wm, int wn) {
+  static int c3[2][64], c1[5][64];
+  if (taps == 9)
+    return wm == 1 ? resident_wgs(conv3_wgrad_kernel<1, 4>, c3[0]) : resident_wgs(conv3_wgrad_kernel<2, 4>, c3[1]);
+  if (wm == 1)
+    return wn == 4 ? resident_wgs(conv1_wgrad_kernel<1, 4, 4>, c1[0])
+                   : (wn == 2 ? resident_wgs(conv1_wgrad_kernel<1, 2, 4>, c1[1])
+                              : resident_wgs(conv1_wgrad_kernel<1, 1, 4>, c1[2]));
+  return wn == 2 ? resident_wgs(conv1_wgrad_kernel<2, 2, 4>, c1[3]) : resident_wgs(conv1_wgrad_kernel<2, 1, 4>, c1[4]);
+}
+
 // Register-direct weight gradient plan: 3 x 3 (stride 1, pad 1, W >= 16)
 // in 128 x 96 tiles of C (64 x 192 when cout <= 64), or 1 x 1 (stride 1,
-// pad 0, cin % 4 == 0, H * W >= 16) in 128 x 128 tiles (64 x 256); the pixels
+// pad 0, cin % 4 == 0, H * W >= 16) in 64 wm x 64 wn tiles (wm = 1 when
+// cout <= 64, else 2; wn the smallest power of two up to 4 / wm whose
+// columns cover cin, the remaining waves sharing the pixels); the pixels
 // split so that tiles x splits fills one round of resident workgroups, each
 // split a whole number of 16-pixel stages and at least 256 pixels.  Returns
 // false when the shape is outside what the kernels assume.
-bool wgrad_plan(const ConvGeom& g, Wgrad3Args& c, int& taps) {
+bool wgrad_plan(const ConvGeom& g, Wgrad3Args& c, int& taps, int& wm, int& wn) {
   const bool k3 = g.kh == 3 && g.kw == 3 && g.pad == 1 && g.stride == 1 && g.w % 4 == 0 && g.w >= 16;
   const bool k1 = g.kh == 1 && g.kw == 1 && g.pad == 0 && g.stride == 1 && (g.h * g.w) % 4 == 0 &&
                   g.h * g.w >= 16 && g.cin % 4 == 0;
@@ -1224,10 +1346,13 @@ bool wgrad_plan(const ConvGeom& g, Wgrad3Args& c, int& taps) {
   c.w = g.w;
   c.hw = g.h * g.w;
   c.npix = g.n * c.hw;
-  const int wm = g.cout <= 64 ? 1 : 2, wn = 4 / wm;
+  wm = g.cout <= 64 ? 1 : 2;
+  wn = 4 / wm;
+  if (k1)
+    while (wn > 1 && 64 * (wn / 2) >= g.cin) wn /= 2;
   c.tiles_m = (g.cout + 64 * wm - 1) / (64 * wm);
   c.tiles = c.tiles_m * (k3 ? (3 * g.cin + 16 * wn - 1) / (16 * wn) : (g.cin + 64 * wn - 1) / (64 * wn));
-  const int slots = wgrad_slots(taps, wm);
+  const int slots = wgrad_slots(taps, wm, wn);
   int splits = std::max(1, slots / c.tiles);
   const int max_splits = (c.npix + 255) / 256;
   splits = std::max(1, std::min(splits, max_splits));
@@ -1311,9 +1436,9 @@ size_t mle_conv2d_wgrad_ws_bytes(int n, int cin, int h, int w_in, int cout, int 
   ConvGeom g;
   if (geom(n, cin, h, w_in, cout, kh, kw, pad, stride, g) != MLE_OK) return 0;
   Wgrad3Args c3;
-  int taps;
+  int taps, wm, wn;
   // Split partials of dW, then (mle_conv2d_wgrad_bias) those of db.
-  if (wgrad_plan(g, c3, taps))
+  if (wgrad_plan(g, c3, taps, wm, wn))
     return c3.items > c3.tiles ? (size_t)c3.out_bytes + (size_t)(c3.items / c3.tiles) * cout * sizeof(float) : 0;
   int kchunk;
   const int splits = wgrad_splits(g, kchunk);
@@ -1338,8 +1463,8 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
   hipStream_t s = as_stream(stream);
   const double flop = 2.0 * cout * (double)cin * kh * kw * (double)n * g.oh * g.ow;
   Wgrad3Args c3;
-  int taps;
-  if (wgrad_plan(g, c3, taps)) {
+  int taps, wm, wn;
+  if (wgrad_plan(g, c3, taps, wm, wn)) {
     const int splits = c3.items / c3.tiles;
     c3.x = x;
     c3.dy = dy;
@@ -1353,11 +1478,15 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
     {
       ProbeScope probe("conv_wgrad", s, flop, 0.0);
       if (taps == 9) {
-        if (cout <= 64) mle::launch(conv3_wgrad_kernel<1, 4>, c3.items, 256, 0, s, c3);
+        if (wm == 1) mle::launch(conv3_wgrad_kernel<1, 4>, c3.items, 256, 0, s, c3);
         else mle::launch(conv3_wgrad_kernel<2, 4>, c3.items, 256, 0, s, c3);
+      } else if (wm == 1) {
+        if (wn == 4) mle::launch(conv1_wgrad_kernel<1, 4, 4>, c3.items, 256, 0, s, c3);
+        else if (wn == 2) mle::launch(conv1_wgrad_kernel<1, 2, 4>, c3.items, 256, 0, s, c3);
+        else mle::launch(conv1_wgrad_kernel<1, 1, 4>, c3.items, 256, 0, s, c3);
       } else {
-        if (cout <= 64) mle::launch(conv1_wgrad_kernel<1, 4>, c3.items, 256, 0, s, c3);
-        else mle::launch(conv1_wgrad_kernel<2, 4>, c3.items, 256, 0, s, c3);
+        if (wn == 2) mle::launch(conv1_wgrad_kernel<2, 2, 4>, c3.items, 256, 0, s, c3);
+        else mle::launch(conv1_wgrad_kernel<2, 1, 4>, c3.items, 256, 0, s, c3);
       }
     }
     if (splits > 1)

@@ -824,6 +824,11 @@ def test_conv_transpose_composition(hip, orc, n, cin, h, w, cout, k, pad, stride
     # K split) blocks, partial pixel tiles and channel groups (hw 60, cin 12,
     # cout 20), a 4-pixel image (weight gradient on the LDS kernel)
     (2, 64, 32, 32, 128, 1, 0, 1), (3, 12, 5, 12, 20, 1, 0, 1), (1, 8, 2, 2, 8, 1, 0, 1),
+    # 1x1 weight-gradient wave layouts (row blocks x column blocks x pixel
+    # shares): 1x2x2 (cin 100), 1x4x1 (cin 200), 2x2x1 (cin 96); one 16-pixel
+    # stage shared by four waves, three of them with no pixels
+    (2, 100, 6, 8, 48, 1, 0, 1), (1, 200, 4, 8, 32, 1, 0, 1), (2, 96, 4, 8, 96, 1, 0, 1),
+    (1, 12, 4, 4, 20, 1, 0, 1),
 ])
 def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
     r = rng(n * 7 + cin + h + cout + k)
