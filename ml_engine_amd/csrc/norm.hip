@@ -139,18 +139,44 @@ __global__ __launch_bounds__(NT) void add_stats_partial(const float* __restrict_
   const size_t c0 = (size_t)ck * CH;
   float v[VPT];
   if (VEC) {
+    // Every load of the thread before its first store; FULL chunks without
+    // per-lane branches (see norm_apply).
+    auto body = [&](auto full) {
+      constexpr bool FULL = decltype(full)::value;
+      constexpr int U = VPT / 4;
+      f32x4 av[U], bv[U];
+      size_t o[U], ob[U];
+      bool in[U];
+      // b's offsets: the thread's float4s are 4 NT floats apart, so with
+      // b_period >= 4 NT each step wraps at most once (one division per
+      // thread instead of one per float4).
+      const bool step = b_period >= (size_t)(4 * NT);
 #pragma unroll
-    for (int u = 0; u < VPT / 4; ++u) {
-      const size_t e = elem<true>(c0, 4 * u);
-      f32x4 t = {0.f, 0.f, 0.f, 0.f};
-      if (e < sh.N) {
-        const size_t o = at<false>(sh, g, e);
-        t = *reinterpret_cast<const f32x4*>(a + o) + *reinterpret_cast<const f32x4*>(b + o % b_period);
-        *reinterpret_cast<f32x4*>(y + o) = t;
+      for (int u = 0; u < U; ++u) {
+        const size_t e = elem<true>(c0, 4 * u);
+        in[u] = FULL || e < sh.N;
+        o[u] = at<false>(sh, g, e);
+        if (u == 0 || !step) {
+          ob[u] = o[u] % b_period;
+        } else {
+          const size_t nb = ob[u - 1] + 4 * NT;
+          ob[u] = nb >= b_period ? nb - b_period : nb;
+        }
+        av[u] = bv[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (!in[u]) continue;
+        av[u] = *reinterpret_cast<const f32x4*>(a + o[u]);
+        bv[u] = *reinterpret_cast<const f32x4*>(b + ob[u]);
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[4 * u + k] = t[k];
-    }
+      for (int u = 0; u < U; ++u) {
+        const f32x4 t = av[u] + bv[u];
+        if (in[u]) *reinterpret_cast<f32x4*>(y + o[u]) = t;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[4 * u + k] = t[k];
+      }
+    };
+    if (c0 + CH <= sh.N) body(std::true_type{});
+    else body(std::false_type{});
   } else {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -257,24 +283,41 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
   }
   const size_t c0 = (size_t)ck * CH;
   if (VEC) {
+    // Every load of the thread before its first store: the vector memory
+    // counter counts stores too, so a load issued after a store would make
+    // its wait cover that store.  A chunk wholly inside the group (FULL, the
+    // same for the whole block) loads and stores without per-lane branches,
+    // which lets each wait name just the load it needs.
+    auto body = [&](auto full) {
+      constexpr bool FULL = decltype(full)::value;
+      constexpr int U = VPT / 4;
+      f32x4 xv[U];
+      size_t o[U];
+      bool in[U];
 #pragma unroll
-    for (int u = 0; u < VPT / 4; ++u) {
-      const size_t e = elem<true>(c0, 4 * u);
-      if (e < sh.N) {
-        const size_t o = at<SEG>(sh, g, e);
-        const f32x4 xv = *reinterpret_cast<const f32x4*>(x + o);
+      for (int u = 0; u < U; ++u) {
+        const size_t e = elem<true>(c0, 4 * u);
+        in[u] = FULL || e < sh.N;
+        o[u] = in[u] ? at<SEG>(sh, g, e) : 0;
+        if (in[u]) xv[u] = *reinterpret_cast<const f32x4*>(x + o[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (!in[u]) continue;
         f32x4 yv;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) yv[k] = (xv[k] - mean) * r;
-        *reinterpret_cast<f32x4*>(y + o) = yv;
+        for (int k = 0; k < 4; ++k) yv[k] = (xv[u][k] - mean) * r;
+        *reinterpret_cast<f32x4*>(y + o[u]) = yv;
         if (ACT >= 0) {
           f32x4 av;
 #pragma unroll
           for (int k = 0; k < 4; ++k) av[k] = act_f<ACT < 0 ? 0 : ACT>(yv[k]);
-          *reinterpret_cast<f32x4*>(act_out + o) = av;
+          *reinterpret_cast<f32x4*>(act_out + o[u]) = av;
         }
       }
-    }
+    };
+    if (c0 + CH <= sh.N) body(std::true_type{});
+    else body(std::false_type{});
   } else {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -381,29 +424,45 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
     r = rsqrtf(stats[2 * g + 1] / fN + eps);
   }
   if (VEC && !quirk_hw) {
+    // Every load of the thread before its first store; FULL chunks without
+    // per-lane branches (see norm_apply).
+    auto body = [&](auto full) {
+      constexpr bool FULL = decltype(full)::value;
+      constexpr int U = VPT / 4;
+      const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+      f32x4 yv[U], gv[U], d[U], d2[U], d3[U];
+      size_t o[U];
+      bool in[U];
 #pragma unroll
-    for (int u = 0; u < VPT / 4; ++u) {
-      const size_t e = elem<true>(c0, 4 * u);
-      if (e < sh.N) {
-        const size_t o = at<SEG>(sh, g, e);
-        const f32x4 yv = *reinterpret_cast<const f32x4*>(y + o);
-        const f32x4 gv = *reinterpret_cast<const f32x4*>(dy + o);
-        f32x4 d = acc ? *reinterpret_cast<const f32x4*>(dx + o) : f32x4{0.f, 0.f, 0.f, 0.f};
-        f32x4 d2 = {0.f, 0.f, 0.f, 0.f}, d3 = d2;
-        if (EXTRA && acc2) d2 = *reinterpret_cast<const f32x4*>(dx2 + o);
-        if (EXTRA && dx3 && acc3) d3 = *reinterpret_cast<const f32x4*>(dx3 + o);
+      for (int u = 0; u < U; ++u) {
+        const size_t e = elem<true>(c0, 4 * u);
+        in[u] = FULL || e < sh.N;
+        o[u] = in[u] ? at<SEG>(sh, g, e) : 0;
+        d[u] = d2[u] = d3[u] = z4;
+        if (!in[u]) continue;
+        yv[u] = *reinterpret_cast<const f32x4*>(y + o[u]);
+        gv[u] = *reinterpret_cast<const f32x4*>(dy + o[u]);
+        if (acc) d[u] = *reinterpret_cast<const f32x4*>(dx + o[u]);
+        if (EXTRA && acc2) d2[u] = *reinterpret_cast<const f32x4*>(dx2 + o[u]);
+        if (EXTRA && dx3 && acc3) d3[u] = *reinterpret_cast<const f32x4*>(dx3 + o[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (!in[u]) continue;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const float v = r * (gv[k] - (sg / fN) - yv[k] * (sgy / fN));
-          d[k] = acc ? d[k] + v : v;
-          d2[k] = acc2 ? d2[k] + d[k] : d[k];
-          d3[k] = acc3 ? d3[k] + d[k] : d[k];
+          const float v = r * (gv[u][k] - (sg / fN) - yv[u][k] * (sgy / fN));
+          d[u][k] = acc ? d[u][k] + v : v;
+          d2[u][k] = acc2 ? d2[u][k] + d[u][k] : d[u][k];
+          d3[u][k] = acc3 ? d3[u][k] + d[u][k] : d[u][k];
         }
-        *reinterpret_cast<f32x4*>(dx + o) = d;
-        if (EXTRA) *reinterpret_cast<f32x4*>(dx2 + o) = d2;
-        if (EXTRA && dx3) *reinterpret_cast<f32x4*>(dx3 + o) = d3;
+        *reinterpret_cast<f32x4*>(dx + o[u]) = d[u];
+        if (EXTRA) *reinterpret_cast<f32x4*>(dx2 + o[u]) = d2[u];
+        if (EXTRA && dx3) *reinterpret_cast<f32x4*>(dx3 + o[u]) = d3[u];
       }
-    }
+    };
+    if (c0 + CH <= sh.N) body(std::true_type{});
+    else body(std::false_type{});
     return;
   }
 #pragma unroll
