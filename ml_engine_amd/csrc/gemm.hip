@@ -463,6 +463,20 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& g, int tm, int tn, i
     }
   };
 
+  // The epilogue's bias, loaded before the K loop so that its wait is long
+  // satisfied when the stores start (loaded after the loop, it cost the
+  // epilogue a memory round trip).  A column past N, or no bias, reads 0.
+  const bool split_mode = g.splits > 1;
+  const int col = n0 + 4 * lr;
+  f32x4 b4;
+  {
+    const bool has_b = !split_mode && g.bias;
+    const __amdgpu_buffer_rsrc_t rbias = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(has_b ? g.bias + z * g.sbias : nullptr), (short)0, has_b ? g.N * 4 : 0, kBufWord3);
+    b4 = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(rbias, (int)(col < g.N ? (uint32_t)col * 4u : kBufOOB), 0, 0));
+  }
+
   // Stage s lives in register set s % D.  Each pass of the loop consumes D
   // stages and issues the loads D - 1 stages ahead of each.
   f32x4 fa[D][S], fb[D][S];
@@ -486,14 +500,10 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& g, int tm, int tn, i
   // Epilogue: lane (lr, q) holds C[row(i, 4q + r)][4 lr + n] in acc[i][n][r],
   // so each (i, r) is one 16-byte store of 4 consecutive columns.  N, ldc and
   // C are 16-byte aligned on this path (checked on the host).
-  const bool split_mode = g.splits > 1;
   float* P = split_mode ? g.part + (int64_t)bz * g.M * g.N : nullptr;
-  const int col = n0 + 4 * lr;
   auto rmap = [&](int i, int d) { return A_MC ? 4 * d + i : 16 * i + d; };
   if (col < g.N) {
     const float alpha = g.alpha, beta = g.beta;
-    f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
-    if (!split_mode && g.bias) b4 = *reinterpret_cast<const f32x4*>(g.bias + z * g.sbias + col);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -678,8 +688,21 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) load(false, s, 0, fa[s], fb[s]);
   int kt = 0, c_item = blockIdx.x;
+  // The epilogue's bias, loaded ahead of the item's last D stages: issued
+  // before the next item's first loads, its wait in the epilogue does not
+  // cover them (the vector memory counter completes in order).  A column
+  // past N, or no bias, reads 0.
+  f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
   for (;;) {
     const bool last = kt + D == nk;  // the item's last D stages
+    if (last) {
+      int tm, tn, z;
+      item_tile(c_item, items, gx, gy, tm, tn, z);
+      const int col = tn * 128 + wn * 64 + 4 * lr;
+      const __amdgpu_buffer_rsrc_t rbias = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(g.bias ? g.bias + z * g.sbias : g.bias), (short)0, g.bias ? g.N * 4 : 0, kBufWord3);
+      b4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rbias, (int)(col < g.N ? (uint32_t)col * 4u : kBufOOB), 0, 0));
+    }
 #pragma unroll
     for (int s = 0; s < D; ++s) {
       const int ls = kt + s + D - 1;  // stage to fetch; past nk it is the next item's
@@ -709,8 +732,6 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
         rd = __builtin_amdgcn_make_buffer_rsrc(g.act_dx + zc, (short)0, (int)c_bytes, kBufWord3);
       }
       const int m0 = tm * 128 + wm * 64, col = tn * 128 + wn * 64 + 4 * lr;
-      f32x4 b4 = {0.f, 0.f, 0.f, 0.f};
-      if (g.bias && col < g.N) b4 = *reinterpret_cast<const f32x4*>(g.bias + z * g.sbias + col);
       const float alpha = g.alpha, beta = g.beta;
       // ROWSTATS: the wave's 64 x 64 block goes to LDS (row slot
       // d' = 16 i + 4 q + r, columns outside the matrix as -FLT_MAX), then lane
