@@ -504,6 +504,20 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& g, int tm, int tn, i
   auto rmap = [&](int i, int d) { return A_MC ? 4 * d + i : 16 * i + d; };
   if (col < g.N) {
     const float alpha = g.alpha, beta = g.beta;
+    // beta != 0: every previous value is loaded before the first store (the
+    // vector memory counter counts stores too, so loading each one between
+    // two stores made every store wait for the one before).
+    f32x4 old[4][4];
+    if (!split_mode && beta != 0.f) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + rmap(i, 4 * q + r);
+          old[i][r] = row < g.M ? *reinterpret_cast<const f32x4*>(C + (int64_t)row * g.ldc + col)
+                                : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -516,7 +530,7 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& g, int tm, int tn, i
           } else {
             float* p = C + (int64_t)row * g.ldc + col;
             v = alpha * v;
-            if (beta != 0.f) v += beta * *reinterpret_cast<const f32x4*>(p);
+            if (beta != 0.f) v += beta * old[i][r];
             *reinterpret_cast<f32x4*>(p) = v + b4;
           }
         }
