@@ -225,15 +225,29 @@ __device__ __forceinline__ void chan_merge(double& n, double& mu, double& M, dou
   n = nn;
 }
 
+// Lane l's first chunk partial (chunk l; lanes past the last chunk load an
+// in-range one that the merge below skips), loaded without a branch: a
+// caller can issue its own loads after it and still wait for it alone.
+struct PartPre {
+  double a, b;
+};
+__device__ __forceinline__ PartPre part_pre(const double* __restrict__ part, const NormShape& sh, int g) {
+  const int c = min((int)(threadIdx.x & 63), sh.nchunk - 1);
+  const double* p = part + ((size_t)g * sh.nchunk + c) * 2;
+  return {p[0], p[1]};
+}
+
 // The group's (mean, M2) from its chunk partials, computed by every wave of
 // the workgroup with the same fixed order: lane l first merges chunks l,
 // l + 64, ... in turn, then lanes merge pairwise in a tree (lower lane first).
-__device__ __forceinline__ void group_stats(const double* __restrict__ part, const NormShape& sh, int g, double& mean,
-                                            double& m2) {
+// `pre` holds chunk l's partial (part_pre).
+__device__ __forceinline__ void group_stats_from(const PartPre& pre, const double* __restrict__ part,
+                                                 const NormShape& sh, int g, double& mean, double& m2) {
   const int lane = threadIdx.x & 63;
   const double* p = part + (size_t)g * sh.nchunk * 2;
   double n = 0.0, mu = 0.0, M = 0.0;
-  for (int c = lane; c < sh.nchunk; c += 64) chan_merge(n, mu, M, chunk_n(sh, c), p[2 * c], p[2 * c + 1]);
+  if (lane < sh.nchunk) chan_merge(n, mu, M, chunk_n(sh, lane), pre.a, pre.b);
+  for (int c = lane + 64; c < sh.nchunk; c += 64) chan_merge(n, mu, M, chunk_n(sh, c), p[2 * c], p[2 * c + 1]);
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const double nb = __shfl_down(n, off, 64), mub = __shfl_down(mu, off, 64), Mb = __shfl_down(M, off, 64);
@@ -244,13 +258,17 @@ __device__ __forceinline__ void group_stats(const double* __restrict__ part, con
 }
 
 // The group's sum(dy) and sum(dy * y), same fixed order.
-__device__ __forceinline__ void group_sums(const double* __restrict__ part, const NormShape& sh, int g, double& a,
-                                           double& b) {
+__device__ __forceinline__ void group_sums_from(const PartPre& pre, const double* __restrict__ part,
+                                                const NormShape& sh, int g, double& a, double& b) {
   const int lane = threadIdx.x & 63;
   const double* p = part + (size_t)g * sh.nchunk * 2;
   a = 0.0;
   b = 0.0;
-  for (int c = lane; c < sh.nchunk; c += 64) {
+  if (lane < sh.nchunk) {
+    a += pre.a;
+    b += pre.b;
+  }
+  for (int c = lane + 64; c < sh.nchunk; c += 64) {
     a += p[2 * c];
     b += p[2 * c + 1];
   }
@@ -265,6 +283,10 @@ __device__ __forceinline__ void group_sums(const double* __restrict__ part, cons
   a = __shfl(a, 0, 64);
   b = __shfl(b, 0, 64);
 }
+__device__ __forceinline__ void group_sums(const double* __restrict__ part, const NormShape& sh, int g, double& a,
+                                           double& b) {
+  group_sums_from(part_pre(part, sh, g), part, sh, g, a, b);
+}
 
 // ACT >= 0 (an mle_act_kind): also act_out = act(y), the activation that
 // follows the normalisation (same formula as the activation kernels).
@@ -273,14 +295,21 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
                                                  float* __restrict__ stats, NormShape sh, const double* __restrict__ part,
                                                  float eps, float* __restrict__ act_out = nullptr) {
   const int g = blockIdx.y, ck = blockIdx.x;
-  double mean_d, m2_d;
-  group_stats(part, sh, g, mean_d, m2_d);
-  const float mean = (float)mean_d, ssd = (float)m2_d;
-  const float r = rsqrtf((1.0f / (float)sh.N) * ssd + eps);  // LNorm/GNorm (Engine/kernels.cu:794-834)
-  if (ck == 0 && threadIdx.x == 0) {
-    stats[2 * g] = mean;
-    stats[2 * g + 1] = ssd;
-  }
+  // The group's partials first, then (VEC) this thread's x, then the merge:
+  // the x loads are in flight while the merge runs.
+  const PartPre pre = part_pre(part, sh, g);
+  float mean = 0.f, r = 0.f;
+  auto finish_stats = [&]() {
+    double mean_d, m2_d;
+    group_stats_from(pre, part, sh, g, mean_d, m2_d);
+    mean = (float)mean_d;
+    const float ssd = (float)m2_d;
+    r = rsqrtf((1.0f / (float)sh.N) * ssd + eps);  // LNorm/GNorm (Engine/kernels.cu:794-834)
+    if (ck == 0 && threadIdx.x == 0) {
+      stats[2 * g] = mean;
+      stats[2 * g + 1] = ssd;
+    }
+  };
   const size_t c0 = (size_t)ck * CH;
   if (VEC) {
     // Every load of the thread before its first store: the vector memory
@@ -301,6 +330,7 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
         o[u] = in[u] ? at<SEG>(sh, g, e) : 0;
         if (in[u]) xv[u] = *reinterpret_cast<const f32x4*>(x + o[u]);
       }
+      finish_stats();
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (!in[u]) continue;
@@ -319,6 +349,7 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
     if (c0 + CH <= sh.N) body(std::true_type{});
     else body(std::false_type{});
   } else {
+    finish_stats();
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const size_t e = elem<false>(c0, i);
@@ -413,16 +444,19 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
     sgy = (float)fin[2 * gs + 1];
     r = rsqrtf(stats[2 * gs + 1] / fN + eps);
   };
-  float sg, sgy, r;
-  if (quirk_hw) {
-    terms(g, sg, sgy, r);
-  } else {
+  float sg = 0.f, sgy = 0.f, r = 0.f;
+  if (quirk_hw) terms(g, sg, sgy, r);
+  // Non-quirk: the group's partials and ssd first, then (VEC) this thread's
+  // loads, then the sums, so the loads are in flight while the sums run.
+  const PartPre pre = part_pre(part, sh, g);
+  const float ssd_g = stats[2 * g + 1];
+  auto finish_sums = [&]() {
     double a, b;
-    group_sums(part, sh, g, a, b);
+    group_sums_from(pre, part, sh, g, a, b);
     sg = (float)a;
     sgy = (float)b;
-    r = rsqrtf(stats[2 * g + 1] / fN + eps);
-  }
+    r = rsqrtf(ssd_g / fN + eps);
+  };
   if (VEC && !quirk_hw) {
     // Every load of the thread before its first store; FULL chunks without
     // per-lane branches (see norm_apply).
@@ -446,6 +480,7 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
         if (EXTRA && acc2) d2[u] = *reinterpret_cast<const f32x4*>(dx2 + o[u]);
         if (EXTRA && dx3 && acc3) d3[u] = *reinterpret_cast<const f32x4*>(dx3 + o[u]);
       }
+      finish_sums();
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (!in[u]) continue;
@@ -465,6 +500,7 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
     else body(std::false_type{});
     return;
   }
+  if (!quirk_hw) finish_sums();
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const size_t e = elem<false>(c0, i);
