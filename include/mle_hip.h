@@ -357,6 +357,13 @@ int mle_attention_bwd(mle_stream stream, const float* q, const float* k, const f
 size_t mle_loss_ws_bytes(size_t n);
 /* loss[0] = sum((t - x)^2) / n.  scalar_mse_kernel (Engine/kernels.cu:1808-1816). */
 int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws, size_t ws_bytes);
+/* mle_mse_fwd followed by mle_read_scalar(loss, loss_host) -- the last loss
+ * node's forward with its read-back (Engine/engine.cu:2046): the kernel that
+ * adds the partials also publishes the value (same bits as mle_mse_fwd), so
+ * no publishing kernel runs.  The same locking and graph-capture behaviour
+ * as mle_read_scalar. */
+int mle_mse_fwd_read(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws,
+                     size_t ws_bytes, float* loss_host);
 /* dx (+)= 2 (x - t) / n * (upstream ? upstream[0] : 1).  deriv_mse_kernel (Engine/kernels.cu:1838-1848). */
 int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,
                 int accumulate);
@@ -390,6 +397,14 @@ int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const floa
 int mle_softmax_xent_keys_fwd_rowstats(mle_stream stream, const float* logits, const float* rowpart, int64_t ldp,
                                        const int32_t* keys, int clen, int max_clen, float* stats, int rows, int cols,
                                        float* loss, void* ws, size_t ws_bytes);
+/* mle_softmax_xent_keys_fwd_rowstats followed by mle_read_scalar(loss,
+ * loss_host) -- the cross-entropy node's forward with its read-back
+ * (Engine/engine.cu:2098) -- as mle_mse_fwd_read does: same loss bits and
+ * stats, no publishing kernel. */
+int mle_softmax_xent_keys_fwd_rowstats_read(mle_stream stream, const float* logits, const float* rowpart,
+                                            int64_t ldp, const int32_t* keys, int clen, int max_clen, float* stats,
+                                            int rows, int cols, float* loss, void* ws, size_t ws_bytes,
+                                            float* loss_host);
 
 /* ------------------------------------------------------------------------- */
 /* Normalisation (gamma = 1, beta = 0, as the reference)                     */

@@ -4,6 +4,7 @@
 #include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stddef.h>
+#include <mutex>
 #include <string>
 #include "../../include/mle_hip.h"
 
@@ -57,6 +58,32 @@ inline void launch(void (*k)(KArgs...), dim3 grid, dim3 block, uint32_t shmem, h
 // Per-device set-up of the allocation-free optimizer entry point (optim.hip);
 // mle_init calls it with the device current.
 int optim_scratch_setup();
+
+// ---- scalar read-back -----------------------------------------------------
+// One pinned, host-coherent slot per device: the value's bits and the
+// sequence number of the read that wrote them.
+struct ScalarSlot {
+  unsigned seq;
+  unsigned bits;
+};
+// A host read of a device scalar (mle_read_scalar): scalar_read_begin locks
+// the current device's slot (held until the ScalarRead goes) and picks the
+// sequence number that the publishing kernel writes with the value;
+// scalar_read_finish waits for it, or returns at once under graph capture,
+// where each replay publishes.
+struct ScalarRead {
+  ScalarSlot* slot = nullptr;
+  unsigned seq = 0;
+  std::unique_lock<std::mutex> lock;
+};
+int scalar_read_begin(ScalarRead& r, const char* who);
+int scalar_read_finish(hipStream_t s, ScalarRead& r, float* dst, const char* who);
+// Device side of a read: the value's bits, then the sequence number (system
+// scope, release), so the host never sees the number before the value.
+__device__ __forceinline__ void publish_scalar(ScalarSlot* slot, unsigned bits, unsigned seq) {
+  __hip_atomic_store(&slot->bits, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(&slot->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 inline hipStream_t as_stream(mle_stream s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

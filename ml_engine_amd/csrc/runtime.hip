@@ -111,20 +111,58 @@ void probe_end(hipStream_t, double flop, double bytes) {
 }
 
 // ---- scalar read-back ------------------------------------------------------
-// One pinned, host-coherent slot per device: the value's bits and the
-// sequence number of the read that wrote them.
-struct ScalarSlot {
-  unsigned seq;
-  unsigned bits;
-};
 constexpr int kMaxDevices = 64;
 static std::mutex g_slot_mu[kMaxDevices];
 static ScalarSlot* g_slot[kMaxDevices] = {};
 static unsigned g_slot_seq[kMaxDevices] = {};
 
 __global__ void publish_scalar_kernel(const unsigned* src, ScalarSlot* slot, unsigned seq) {
-  __hip_atomic_store(&slot->bits, *src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  __hip_atomic_store(&slot->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  publish_scalar(slot, *src, seq);
+}
+
+int scalar_read_begin(ScalarRead& r, const char* who) {
+  int dev = 0;
+  MLE_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(MLE_ERR_INVALID, "%s: device %d out of range", who, dev);
+  r.lock = std::unique_lock<std::mutex>(g_slot_mu[dev]);
+  ScalarSlot*& slot = g_slot[dev];
+  if (!slot) {
+    void* p = nullptr;
+    MLE_HIP(hipHostMalloc(&p, sizeof(ScalarSlot), hipHostMallocCoherent));
+    slot = static_cast<ScalarSlot*>(p);
+    slot->seq = 0;
+    slot->bits = 0;
+  }
+  r.slot = slot;
+  r.seq = ++g_slot_seq[dev];
+  return MLE_OK;
+}
+
+int scalar_read_finish(hipStream_t s, ScalarRead& r, float* dst, const char* who) {
+  // Under graph capture the publishing kernel is recorded, not run: each
+  // replay publishes the value, which mle_scalar_last reads after a
+  // synchronisation.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  MLE_HIP(hipStreamIsCapturing(s, &cap));
+  if (cap != hipStreamCaptureStatusNone) return MLE_OK;
+  // The stream is asked every 256 spins: a stream that completed or failed
+  // without the value having landed ends the wait.
+  ScalarSlot* slot = r.slot;
+  for (unsigned long spins = 1;; ++spins) {
+    if (__atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) == r.seq) break;
+    if ((spins & 255) == 0) {
+      const hipError_t q = hipStreamQuery(s);
+      if (q == hipSuccess) {
+        if (__atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) == r.seq) break;
+        return set_error(MLE_ERR_HIP, "%s: the stream drained without publishing the value", who);
+      }
+      if (q != hipErrorNotReady) return hip_error(q, who);
+    }
+    __builtin_ia32_pause();
+  }
+  const unsigned bits = __atomic_load_n(&slot->bits, __ATOMIC_ACQUIRE);
+  memcpy(dst, &bits, sizeof(float));
+  return MLE_OK;
 }
 
 }  // namespace mle
@@ -190,44 +228,13 @@ int mle_memcpy_d2h(void* dst, const void* src, size_t bytes, mle_stream stream) 
 
 int mle_read_scalar(mle_stream stream, const float* src, float* dst) {
   MLE_CHECK_ARG(src != nullptr && dst != nullptr, "mle_read_scalar: null pointer");
-  int dev = 0;
-  MLE_HIP(hipGetDevice(&dev));
-  MLE_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "mle_read_scalar: device %d out of range", dev);
-  std::lock_guard<std::mutex> lk(g_slot_mu[dev]);
-  ScalarSlot*& slot = g_slot[dev];
-  if (!slot) {
-    void* p = nullptr;
-    MLE_HIP(hipHostMalloc(&p, sizeof(ScalarSlot), hipHostMallocCoherent));
-    slot = static_cast<ScalarSlot*>(p);
-    slot->seq = 0;
-    slot->bits = 0;
-  }
-  const unsigned want = ++g_slot_seq[dev];
+  ScalarRead r;
+  int rc = scalar_read_begin(r, "mle_read_scalar");
+  if (rc) return rc;
   hipStream_t s = as_stream(stream);
-  publish_scalar_kernel<<<1, 1, 0, s>>>(reinterpret_cast<const unsigned*>(src), slot, want);
+  publish_scalar_kernel<<<1, 1, 0, s>>>(reinterpret_cast<const unsigned*>(src), r.slot, r.seq);
   MLE_HIP(hipGetLastError());
-  // Under graph capture the kernel is recorded, not run: each replay
-  // publishes the value, which mle_scalar_last reads after a synchronisation.
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  MLE_HIP(hipStreamIsCapturing(s, &cap));
-  if (cap != hipStreamCaptureStatusNone) return MLE_OK;
-  // The stream is asked every 256 spins: a stream that completed or failed
-  // without the value having landed ends the wait.
-  for (unsigned long spins = 1;; ++spins) {
-    if (__atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) == want) break;
-    if ((spins & 255) == 0) {
-      const hipError_t q = hipStreamQuery(s);
-      if (q == hipSuccess) {
-        if (__atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) == want) break;
-        return set_error(MLE_ERR_HIP, "mle_read_scalar: the stream drained without publishing the value");
-      }
-      if (q != hipErrorNotReady) return hip_error(q, "mle_read_scalar");
-    }
-    __builtin_ia32_pause();
-  }
-  const unsigned bits = __atomic_load_n(&slot->bits, __ATOMIC_ACQUIRE);
-  memcpy(dst, &bits, sizeof(float));
-  return MLE_OK;
+  return scalar_read_finish(s, r, dst, "mle_read_scalar");
 }
 
 int mle_scalar_last(float* dst) {

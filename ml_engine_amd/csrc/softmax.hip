@@ -476,8 +476,11 @@ __global__ __launch_bounds__(NT) void mse_partial4_kernel(const float* __restric
 
 // One 1024-thread workgroup; four loads in flight per thread, fixed order.
 constexpr int FIN_NT = 1024;
+// With a slot, the value is also published for the host (mle_read_scalar),
+// so a loss read-back needs no kernel of its own.
 __global__ __launch_bounds__(FIN_NT) void finish_scalar_kernel(const double* __restrict__ part, size_t nparts,
-                                                               double denom, float* __restrict__ out) {
+                                                               double denom, float* __restrict__ out,
+                                                               mle::ScalarSlot* slot = nullptr, unsigned seq = 0) {
   __shared__ double red[FIN_NT / 64];
   double a[4] = {0.0, 0.0, 0.0, 0.0};
   size_t i = threadIdx.x;
@@ -488,7 +491,11 @@ __global__ __launch_bounds__(FIN_NT) void finish_scalar_kernel(const double* __r
   for (; i < nparts; i += FIN_NT) a[0] += part[i];
   double acc = (a[0] + a[1]) + (a[2] + a[3]);
   acc = block_sum<FIN_NT>(acc, red);
-  if (threadIdx.x == 0) out[0] = (float)(acc / denom);
+  if (threadIdx.x == 0) {
+    const float v = (float)(acc / denom);
+    out[0] = v;
+    if (slot) mle::publish_scalar(slot, __builtin_bit_cast(unsigned, v), seq);
+  }
 }
 
 __global__ __launch_bounds__(NT) void mse_bwd_kernel(const float* __restrict__ x, const float* __restrict__ t,
@@ -671,21 +678,39 @@ size_t mle_loss_ws_bytes(size_t n) {
   return b < 256 ? 256 : b;
 }
 
-int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws, size_t ws_bytes) {
-  MLE_CHECK_ARG(x && t && loss && ws && n > 0, "mle_mse_fwd: bad argument");
+static int mse_fwd_impl(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws,
+                        size_t ws_bytes, float* loss_host, const char* who) {
+  MLE_CHECK_ARG(x && t && loss && ws && n > 0, "%s: bad argument", who);
   const unsigned g = stream_grid(n, NT, kMsePartCap);
-  if (ws_bytes < g * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "mle_mse_fwd: workspace too small");
+  if (ws_bytes < g * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "%s: workspace too small", who);
   hipStream_t s = as_stream(stream);
   double* part = static_cast<double*>(ws);
-  if (n % 4 == 0 && aligned16(x) && aligned16(t)) {
-    const unsigned g4 = stream_grid(n / 4, NT, kMsePartCap);
-    mse_partial4_kernel<<<g4, NT, 0, s>>>(x, t, n / 4, part);
-    finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, g4, (double)n, loss);
-    return check_launch("mle_mse_fwd");
+  mle::ScalarRead r;
+  if (loss_host) {
+    const int rc = mle::scalar_read_begin(r, who);
+    if (rc) return rc;
   }
-  mse_partial_kernel<<<g, NT, 0, s>>>(x, t, n, part);
-  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, g, (double)n, loss);
-  return check_launch("mle_mse_fwd");
+  unsigned np = g;
+  if (n % 4 == 0 && aligned16(x) && aligned16(t)) {
+    np = stream_grid(n / 4, NT, kMsePartCap);
+    mse_partial4_kernel<<<np, NT, 0, s>>>(x, t, n / 4, part);
+  } else {
+    mse_partial_kernel<<<g, NT, 0, s>>>(x, t, n, part);
+  }
+  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, np, (double)n, loss, r.slot, r.seq);
+  const int rc = check_launch(who);
+  if (rc || !loss_host) return rc;
+  return mle::scalar_read_finish(s, r, loss_host, who);
+}
+
+int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws, size_t ws_bytes) {
+  return mse_fwd_impl(stream, x, t, n, loss, ws, ws_bytes, nullptr, "mle_mse_fwd");
+}
+
+int mle_mse_fwd_read(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws,
+                     size_t ws_bytes, float* loss_host) {
+  MLE_CHECK_ARG(loss_host != nullptr, "mle_mse_fwd_read: null loss_host");
+  return mse_fwd_impl(stream, x, t, n, loss, ws, ws_bytes, loss_host, "mle_mse_fwd_read");
 }
 
 int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,
@@ -751,22 +776,45 @@ int mle_softmax_xent_keys_fwd(mle_stream stream, const float* logits, const int3
   return check_launch("mle_softmax_xent_keys_fwd");
 }
 
-int mle_softmax_xent_keys_fwd_rowstats(mle_stream stream, const float* logits, const float* rowpart, int64_t ldp,
-                                       const int32_t* keys, int clen, int max_clen, float* stats, int rows, int cols,
-                                       float* loss, void* ws, size_t ws_bytes) {
+static int xent_rowstats_impl(mle_stream stream, const float* logits, const float* rowpart, int64_t ldp, const int32_t* keys,
+                       int clen, int max_clen, float* stats, int rows, int cols, float* loss, void* ws, size_t ws_bytes,
+                       float* loss_host, const char* who) {
   const int nblk = (cols + 63) / 64;
   MLE_CHECK_ARG(logits && rowpart && keys && stats && loss && ws && rows > 0 && cols > 0 && clen > 0 &&
                     max_clen >= clen && rows % clen == 0 && ldp >= 2 * (int64_t)nblk,
-                "mle_softmax_xent_keys_fwd_rowstats: bad argument");
-  if (ws_bytes < (size_t)rows * sizeof(double))
-    return set_error(MLE_ERR_WORKSPACE, "mle_softmax_xent_keys_fwd_rowstats: workspace too small");
+                "%s: bad argument", who);
+  if (ws_bytes < (size_t)rows * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "%s: workspace too small", who);
   hipStream_t s = as_stream(stream);
   double* part = static_cast<double*>(ws);
   const KeyTargets kt{keys, clen, max_clen, stats};
-  xent_keys_partials_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(logits, rowpart, ldp, nblk, rows, cols, kt,
-                                                                       part);
-  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, (size_t)rows, (double)rows * (double)cols, loss);
-  return check_launch("mle_softmax_xent_keys_fwd_rowstats");
+  const unsigned grid = (unsigned)((rows + 3) / 4);
+  const double denom = (double)rows * (double)cols;
+  mle::ScalarRead r;
+  if (loss_host) {
+    const int rc = mle::scalar_read_begin(r, who);
+    if (rc) return rc;
+  }
+  xent_keys_partials_kernel<<<grid, 256, 0, s>>>(logits, rowpart, ldp, nblk, rows, cols, kt, part);
+  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, (size_t)rows, denom, loss, r.slot, r.seq);
+  const int rc = check_launch(who);
+  if (rc || !loss_host) return rc;
+  return mle::scalar_read_finish(s, r, loss_host, who);
+}
+
+int mle_softmax_xent_keys_fwd_rowstats(mle_stream stream, const float* logits, const float* rowpart, int64_t ldp,
+                                       const int32_t* keys, int clen, int max_clen, float* stats, int rows, int cols,
+                                       float* loss, void* ws, size_t ws_bytes) {
+  return xent_rowstats_impl(stream, logits, rowpart, ldp, keys, clen, max_clen, stats, rows, cols, loss, ws, ws_bytes,
+                            nullptr, "mle_softmax_xent_keys_fwd_rowstats");
+}
+
+int mle_softmax_xent_keys_fwd_rowstats_read(mle_stream stream, const float* logits, const float* rowpart,
+                                            int64_t ldp, const int32_t* keys, int clen, int max_clen, float* stats,
+                                            int rows, int cols, float* loss, void* ws, size_t ws_bytes,
+                                            float* loss_host) {
+  MLE_CHECK_ARG(loss_host != nullptr, "mle_softmax_xent_keys_fwd_rowstats_read: null loss_host");
+  return xent_rowstats_impl(stream, logits, rowpart, ldp, keys, clen, max_clen, stats, rows, cols, loss, ws, ws_bytes,
+                            loss_host, "mle_softmax_xent_keys_fwd_rowstats_read");
 }
 
 int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const float* stats, const int32_t* keys, int clen,

@@ -494,9 +494,12 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
   void* ws = mle::alloc_scratch(ws_bytes);
   node->forward = [=]() {
     if (calculate_loss || !last) {
-      check(mle_mse_fwd(S(), pr->output, tg->output, n, nd->output, ws, ws_bytes), "Scalar MSE in MSE forward");
+      if (last)  // the loss and its read-back in one launch
+        check(mle_mse_fwd_read(S(), pr->output, tg->output, n, nd->output, ws, ws_bytes, &GraphOperations::loss),
+              "Scalar MSE in MSE forward");
+      else
+        check(mle_mse_fwd(S(), pr->output, tg->output, n, nd->output, ws, ws_bytes), "Scalar MSE in MSE forward");
       nd->output_pending_zero = false;  // written whole
-      if (last) check(mle_read_scalar(S(), nd->output, &GraphOperations::loss), "MSE loss");
     }
   };
   node->backward = [=]() {
@@ -548,6 +551,15 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
   }
   node->forward = [=]() {
     if (calculate_loss || !last) {
+      if (rowpart && last) {
+        // the loss and its read-back in one launch
+        check(mle_softmax_xent_keys_fwd_rowstats_read(S(), pr->output, rowpart, ldp, oh->keys, oh->clen,
+                                                      oh->max_clen, stats, rows, d, nd->output, ws, ws_bytes,
+                                                      &GraphOperations::loss),
+              "SoftMaxCrossEntropy");
+        nd->output_pending_zero = false;
+        return;
+      }
       if (rowpart)
         check(mle_softmax_xent_keys_fwd_rowstats(S(), pr->output, rowpart, ldp, oh->keys, oh->clen, oh->max_clen,
                                                  stats, rows, d, nd->output, ws, ws_bytes),

@@ -73,6 +73,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_gemm_grid": (I, [P, I, I, I, I, I, F, P, I64, I64, I64, P, I64, I64, I64, F, P, I64, I64, I64, I, I, P, SZ]),
     "mle_gemm_rowstats": (I, [P, I, I, I, I, I, F, P, I64, P, I64, F, P, I64, P, P, I64, P, SZ]),
     "mle_softmax_xent_keys_fwd_rowstats": (I, [P, P, P, I64, P, I, I, P, I, I, P, P, SZ]),
+    "mle_softmax_xent_keys_fwd_rowstats_read": (I, [P, P, P, I64, P, I, I, P, I, I, P, P, SZ, P]),
     "mle_gemm_act_fwd": (I, [P, I, I, I, I, I, F, P, I64, P, I64, F, P, P, I, P, P, SZ]),
     "mle_gemm_act_bwd": (I, [P, I, I, I, I, I, F, P, I64, P, I64, F, P, I, P, P, I, P, SZ]),
     "mle_linear_bwd_ws_bytes": (SZ, [I, I, I, I]),
@@ -88,6 +89,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_attention_bwd": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, F, I, I, I, I, I, P, SZ]),
     "mle_loss_ws_bytes": (SZ, [SZ]),
     "mle_mse_fwd": (I, [P, P, P, SZ, P, P, SZ]),
+    "mle_mse_fwd_read": (I, [P, P, P, SZ, P, P, SZ, P]),
     "mle_mse_bwd": (I, [P, P, P, P, P, SZ, I]),
     "mle_softmax_xent_keys_fwd": (I, [P, P, P, I, I, P, I, I, P, P, SZ]),
     "mle_softmax_xent_keys_bwd": (I, [P, P, P, P, I, I, P, P, I, I, I]),

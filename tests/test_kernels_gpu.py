@@ -1320,6 +1320,40 @@ def test_softmax_xent_keys_rowstats(hip, batch, clen, cols):
     np.testing.assert_array_equal(st2[:, 0], st[:, 0])
     assert_close(st2[:, 1], st[:, 1], what="row sums", **EW)
     assert_close(gloss2.numpy(), gloss.numpy(), what="loss", **EW)
+    # The loss with its read-back (the finishing kernel publishes the value):
+    # the same device loss and stats bits, and the host value equal to the
+    # device value, on two calls in a row.
+    for rep in range(2):
+        gst3, gloss3 = hip.Buffer.zeros(2 * rows), hip.Buffer.zeros(1)
+        host = C.c_float(float("nan"))
+        hip.call("mle_softmax_xent_keys_fwd_rowstats_read", None, gl.ptr, gpart.ptr, ldp, gk.ptr, clen, clen, gst3.ptr,
+                 rows, cols, gloss3.ptr, ws.ptr, ws.nbytes, C.byref(host))
+        np.testing.assert_array_equal(gst3.numpy(), gst2.numpy())
+        np.testing.assert_array_equal(gloss3.numpy().view(np.uint32), gloss2.numpy().view(np.uint32))
+        assert np.float32(host.value).view(np.uint32) == gloss2.numpy().view(np.uint32)[0], (rep, host.value)
+
+
+@pytest.mark.parametrize("n", [5, 1000, 123457, 123456, 8 << 20])
+def test_mse_fwd_read(hip, n):
+    """mle_mse_fwd_read: the loss of mle_mse_fwd bit for bit, on the device and
+    on the host, on both partial paths (n % 4) and from one partial to the
+    2048-partial cap; two calls in a row with another read in between."""
+    r = rng(n % 1000 + 7)
+    x = r.standard_normal(n, dtype=np.float32)
+    t = r.standard_normal(n, dtype=np.float32)
+    gx, gt = B(hip, x), B(hip, t)
+    ws = hip.Buffer(hip.lib().mle_loss_ws_bytes(n))
+    gl, gl2 = hip.Buffer.zeros(1), hip.Buffer.zeros(1)
+    hip.call("mle_mse_fwd", None, gx.ptr, gt.ptr, n, gl.ptr, ws.ptr, ws.nbytes)
+    want = gl.numpy().view(np.uint32)[0]
+    for rep in range(2):
+        host = C.c_float(float("nan"))
+        hip.call("mle_mse_fwd_read", None, gx.ptr, gt.ptr, n, gl2.ptr, ws.ptr, ws.nbytes, C.byref(host))
+        assert gl2.numpy().view(np.uint32)[0] == want, rep
+        assert np.float32(host.value).view(np.uint32) == want, (rep, host.value)
+        other = C.c_float(0.0)
+        hip.call("mle_read_scalar", None, gx.ptr, C.byref(other))
+        assert other.value == x[0]
 
 
 @pytest.mark.parametrize("kind", ["relu", "gelu", "silu", "tanh"])
