@@ -87,9 +87,11 @@ struct Accum2Op {
     yb[i] = ACC_B ? yb[i] + v : v;
   }
   __device__ void vec(size_t i) const {
+    // every load before the first store (a load after a store waits for it)
     const f32x4 v = ld4(x, i);
-    st4(ya, i, ACC_A ? ld4(ya, i) + v : v);
-    st4(yb, i, ACC_B ? ld4(yb, i) + v : v);
+    const f32x4 a = ACC_A ? ld4(ya, i) : v, b = ACC_B ? ld4(yb, i) : v;
+    st4(ya, i, ACC_A ? a + v : v);
+    st4(yb, i, ACC_B ? b + v : v);
   }
 };
 
@@ -137,14 +139,17 @@ struct ActBwdAddOp {
   }
   __device__ void vec(size_t i) const {
 #pragma clang fp contract(off)
+    // every load before the first store (a load after a store waits for it)
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
     const f32x4 x = ld4(z, i), g = ld4(da, i);
+    const f32x4 oz = acc_z ? ld4(dz, i) : z4, oa = acc_a ? ld4(ga, i) : z4, ob = acc_b ? ld4(gb, i) : z4;
     f32x4 d;
 #pragma unroll
     for (int j = 0; j < 4; ++j) d[j] = act_df<K>(x[j]) * g[j];
-    if (acc_z) d = ld4(dz, i) + d;
+    if (acc_z) d = oz + d;
     st4(dz, i, d);
-    st4(ga, i, acc_a ? ld4(ga, i) + d : d);
-    st4(gb, i, acc_b ? ld4(gb, i) + d : d);
+    st4(ga, i, acc_a ? oa + d : d);
+    st4(gb, i, acc_b ? ob + d : d);
   }
 };
 
