@@ -213,7 +213,11 @@ void defer_zero_output(NodeBackProp* n) {
 }
 
 void materialize_output(NodeBackProp* n) {
-  if (!n || !n->output_pending_zero) return;
+  if (!n) return;
+  // Kept for the next read: graph replays run no host code to mark the
+  // output stale again, and the refresh leaves a current output unchanged.
+  if (n->output_refresh) n->output_refresh();
+  if (!n->output_pending_zero) return;
   n->output_pending_zero = false;
   zero(n->output, n->total);
 }
@@ -751,6 +755,13 @@ void GraphOperations::forward(const graph& X, const bool calc_loss, const bool s
     printf("Warning... Nodes list is empty and forward cannot run.. \n");
     return;
   }
+  for (auto& n : nodes) n->fwd_consumers = n->fwd_key_readers = 0;
+  for (auto& n : nodes)
+    for (auto& in : n->inputs)
+      if (in) {
+        in->fwd_consumers++;
+        if (n->key_target == in.get()) in->fwd_key_readers++;
+      }
   for (auto& node : nodes) {
     std::chrono::high_resolution_clock::time_point t0;
     if (time) {

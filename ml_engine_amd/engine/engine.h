@@ -186,6 +186,15 @@ struct NodeBackProp {
   // (Zerograd("Node", node->output, 1), Engine/engine.cu:2120, 1945) and the
   // loss forward overwrites: it is filled only if read before that.
   bool output_pending_zero = false;
+  // A write of the output left until something reads it (materialize_output
+  // runs it before every read while it is set; running it on a current
+  // output changes nothing): a one-hot target whose consumers all read its
+  // ids.
+  std::function<void()> output_refresh;
+  // Counted by forward over the nodes it runs: consumers of this node, and
+  // those among them that read only its ids (key_target == this node).
+  int fwd_consumers = 0, fwd_key_readers = 0;
+  NodeBackProp* key_target = nullptr;
   bool lazy_grad_writer = false;
   // Non-null when this node's output is a one-hot matrix of `keys` (additive).
   std::shared_ptr<OneHotSource> onehot;

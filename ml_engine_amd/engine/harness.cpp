@@ -44,6 +44,7 @@ struct Model {
   mle_graph replay = nullptr;
   int replay_mode = 0;
   bool loss_in_slot = false;
+  graph target;  // C1 / C4: the one-hot target node (mle_model_target_read)
 };
 
 void* input_buffer(Model* m, size_t bytes) {
@@ -70,6 +71,7 @@ void build_c1(Model* m, const long long* d) {
   m->l2.reset(new Linear(hid, cls, "Projection"));
   auto pred = m->l2->forward(GraphOperations::RELU(m->l1->forward(x)));
   auto target = GraphOperations::OneHot(labels, batch, 1, 1, cls);
+  m->target = target;
   m->root = GraphOperations::SoftMaxCrossEntropy(pred, target, true);
   m->params = {&m->l1->W1, &m->l1->B1, &m->l2->W1, &m->l2->B1};
   m->adamw = false;
@@ -93,6 +95,7 @@ void build_c4(Model* m, const long long* d) {
   auto x3 = GraphOperations::Add(x2, f);
   auto logits = m->lm->forward(x3);
   auto target = GraphOperations::OneHot(tgt, B, S, S, V);
+  m->target = target;
   m->root = GraphOperations::SoftMaxCrossEntropy(logits, target, true);
   auto& mh = *m->mha;
   m->params = {&m->emb->E, &mh.q.W1, &mh.q.B1, &mh.k.W1, &mh.k.B1, &mh.v.W1, &mh.v.B1, &mh.o.W1, &mh.o.B1,
@@ -328,6 +331,13 @@ int mle_model_step_graph(void* h, float lr, int mode) {
   // the parameters' step counters.
   if (mode & MLE_STEP_UPDATE) m->go.ParameterUpdate(nullptr, false, lr, m->adamw);
   return MLE_OK;
+}
+
+int mle_model_target_read(void* h, float* host, size_t count) {
+  auto* m = static_cast<Model*>(h);
+  if (!m->target || !host || count > (size_t)m->target->total) return MLE_ERR_INVALID;
+  mle::materialize_output(m->target.get());  // the engine's read path
+  return mle_memcpy_d2h(host, m->target->output, count * sizeof(float), mle::stream());
 }
 
 float mle_model_loss(void* h) {

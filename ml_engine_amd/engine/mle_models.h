@@ -56,6 +56,10 @@ int mle_model_step(void* h, float lr, int mode, float clip);
 // mle_model_step; mle_model_loss synchronises and reads the published loss.
 int mle_model_step_graph(void* h, float lr, int mode);
 float mle_model_loss(void* h);
+// C1 / C4: the first `count` floats of the one-hot target matrix, read the
+// way ReadValueAt reads a node output (a matrix left lazy is brought up to
+// date first).
+int mle_model_target_read(void* h, float* host, size_t count);
 int mle_model_sync(void* h);
 void* mle_model_stream(void* h);
 int mle_model_num_nodes(void* h);

@@ -534,6 +534,7 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
   const int rows = batch * channels * c;
   const std::shared_ptr<OneHotSource> oh = target->onehot;
   const bool by_keys = oh && channels == 1 && oh->batch == batch && oh->clen == c && oh->vocab == d;
+  if (by_keys) node->key_target = target.get();  // reads the ids, never the matrix
   float* probs = by_keys ? nullptr : mle::alloc_output(n);
   float* stats = by_keys ? mle::alloc_output(2 * (size_t)rows) : nullptr;
   const size_t ws_bytes = mle_loss_ws_bytes(n);
@@ -893,8 +894,19 @@ graph GraphOperations::OneHot(const int32_t* keys, int batch, int clen, int max_
   std::vector<int32_t> none(ntok, -1);
   check(mle_memcpy_h2d(prev, none.data(), ntok * sizeof(int32_t), S()), "OneHot init");
   check(mle_fill(S(), nd->output, 0.0f, nd->total), "OneHot fill");
-  node->forward = [=]() {
+  auto update = [=]() {
     check(mle_onehot_update(S(), nd->output, prev, keys, batch, clen, max_clen, vocab), "OneHotEmbeddings");
+  };
+  node->forward = [=]() {
+    // Consumers that all read the ids (cross-entropy against key targets)
+    // leave the matrix as it is until something reads it; the update then
+    // moves the ones from where the last update left them.
+    if (nd->fwd_consumers > 0 && nd->fwd_key_readers == nd->fwd_consumers) {
+      nd->output_refresh = update;
+      return;
+    }
+    nd->output_refresh = nullptr;
+    update();
   };
   node->onehot = std::make_shared<OneHotSource>(OneHotSource{keys, batch, clen, max_clen, vocab});
   std_hooks(node);

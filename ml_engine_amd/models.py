@@ -34,6 +34,7 @@ _SIGS = {
     "mle_model_step": (I, [P, F, I, F]),
     "mle_model_step_graph": (I, [P, F, I]),
     "mle_model_loss": (F, [P]),
+    "mle_model_target_read": (I, [P, P, SZ]),
     "mle_model_sync": (I, [P]),
     "mle_model_stream": (P, [P]),
     "mle_model_num_nodes": (I, [P]),
@@ -117,6 +118,14 @@ class Model:
     @property
     def loss(self) -> float:
         return float(lib().mle_model_loss(self.h))
+
+    def target(self, count: int) -> np.ndarray:
+        """The first `count` floats of the one-hot target matrix (C1 / C4)."""
+        out = np.empty(count, np.float32)
+        rc = lib().mle_model_target_read(self.h, out.ctypes.data, count)
+        if rc != 0:
+            raise RuntimeError(f"mle_model_target_read failed ({rc})")
+        return out
 
     @property
     def stream(self):

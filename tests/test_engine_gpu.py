@@ -387,6 +387,45 @@ def test_resblock_fusion_matches_unfused(hip):
         np.testing.assert_array_equal(pf[i].view(np.uint32), pu[i].view(np.uint32), err_msg=f"param {i}")
 
 
+@pytest.mark.parametrize("kind", ["mlp", "block"])
+@pytest.mark.parametrize("graphed", [False, True])
+def test_onehot_target_lazy(hip, kind, graphed):
+    """The one-hot target, whose only consumer (cross-entropy against key
+    targets) reads the ids, is not updated by the forward; a read brings it up
+    to date: after several steps, targets changed between steps, eager and
+    graph-replayed, the matrix read is the one-hot of the current targets."""
+    if kind == "mlp":
+        cfg = MLPConfig()
+        x, labels, params = mlp_data(cfg, seed=11)
+        dims, inputs, rows, cols = cfg.dims(), [x, labels], cfg.batch, cfg.classes
+    else:
+        cfg = BlockConfig(batch=2, seq=64, d_model=64, heads=1, ffn=128, vocab=97)
+        x, labels, params = block_data(cfg, seed=11)
+        dims, inputs, rows, cols = cfg.dims(), [x, labels], cfg.batch * cfg.seq, cfg.vocab
+    m = Model(kind, dims)
+    for i, p in enumerate(params):
+        m.set(i, p)
+    for slot, a in enumerate(inputs):
+        m.input(slot, a)
+    r = np.random.default_rng(3)
+    tgt = np.asarray(labels).astype(np.int32)
+    for step in range(4):
+        if step == 2:  # new targets, then two more steps before the read
+            tgt = r.integers(0, cols, tgt.shape).astype(np.int32)
+            m.input(1, tgt)
+        if graphed:
+            m.step_graph(cfg.lr, STEP_ALL)
+        else:
+            m.step(cfg.lr, STEP_ALL)
+        m.sync()
+        if step in (0, 3):
+            want = np.zeros((rows, cols), np.float32)
+            want[np.arange(rows), tgt.reshape(-1)] = 1.0
+            got = m.target(rows * cols).reshape(rows, cols)
+            np.testing.assert_array_equal(got, want, err_msg=f"step {step}")
+    m.close()
+
+
 def test_block_fusion_full_size(hip):
     """Full C4 shape, where the graph fusions run on the persistent GEMM kernel
     (LM-head row statistics for the loss, batched Q/K/V): one step agrees with
