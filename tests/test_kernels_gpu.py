@@ -848,6 +848,13 @@ def test_conv(hip, orc, n, cin, h, w, cout, k, pad, stride):
     gx, gw, gb, gy = B(hip, x), B(hip, wt), B(hip, b), hip.Buffer.zeros(yr.shape)
     hip.call("mle_conv2d_fwd", None, gx.ptr, gw.ptr, gb.ptr, gy.ptr, n, cin, h, w, cout, k, k, pad, stride)
     assert_close(gy.numpy(), yr, what="conv fwd", **MM)
+    # no bias: the oracle's sums with a zero bias
+    yr0 = np.zeros_like(yr)
+    orc.call("orc_conv_fwd", orc.ptr(x), orc.ptr(wt), orc.ptr(np.zeros_like(b)), orc.ptr(yr0), n, cin, h, w, cout, k,
+             k, pad, stride)
+    gy0 = B(hip, np.full(yr.shape, np.nan, np.float32))
+    hip.call("mle_conv2d_fwd", None, gx.ptr, gw.ptr, None, gy0.ptr, n, cin, h, w, cout, k, k, pad, stride)
+    assert_close(gy0.numpy(), yr0, what="conv fwd without bias", **MM)
     gdy, gdx = B(hip, dy), B(hip, dx0)
     hip.call("mle_conv2d_dgrad", None, gdy.ptr, gw.ptr, gdx.ptr, n, cin, h, w, cout, k, k, pad, stride, 1)
     assert_close(gdx.numpy(), dxr, what="conv dgrad", **MM)
