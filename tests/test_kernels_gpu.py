@@ -500,7 +500,9 @@ def test_mse(hip, orc, n):
 
 # ------------------------------------------------------------------------ norms
 @pytest.mark.parametrize("batch,channels,hw,groups", [(3, 1, 37 * 45, 1), (2, 1, 256 * 512, 1), (2, 8, 700, 4),
-                                                     (2, 64, 4096, 32), (2, 3, 33, 1)])
+                                                     (2, 64, 4096, 32), (2, 3, 33, 1),
+                                                     # 75 chunks per group: lanes merge a second chunk each
+                                                     (1, 1, 300 * 1024, 1)])
 def test_norm(hip, orc, batch, channels, hw, groups):
     r = rng(batch + channels + hw + groups)
     shape = (batch, channels, hw)
