@@ -502,7 +502,10 @@ def test_mse(hip, orc, n):
 @pytest.mark.parametrize("batch,channels,hw,groups", [(3, 1, 37 * 45, 1), (2, 1, 256 * 512, 1), (2, 8, 700, 4),
                                                      (2, 64, 4096, 32), (2, 3, 33, 1),
                                                      # 75 chunks per group: lanes merge a second chunk each
-                                                     (1, 1, 300 * 1024, 1)])
+                                                     (1, 1, 300 * 1024, 1),
+                                                     # the fused Add / MatPE statistics with periods 1024 and
+                                                     # 512 (one division per float4 below 1024)
+                                                     (2, 1, 512, 1)])
 def test_norm(hip, orc, batch, channels, hw, groups):
     r = rng(batch + channels + hw + groups)
     shape = (batch, channels, hw)
