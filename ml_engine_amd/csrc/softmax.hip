@@ -185,6 +185,14 @@ __global__ __launch_bounds__(256) void xent_keys_partials_kernel(const float* __
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
+  // The key and its logit are fetched first: their two dependent loads run
+  // under the partials' loads and reductions instead of after them.
+  int key = -1;
+  float xk = 0.f;
+  if (lane == 0) {
+    key = kt.key((size_t)row, cols);
+    if (key >= 0) xk = x[(size_t)row * cols + key];
+  }
   const float* pr = part + (size_t)row * ldp;
   float mx = -FLT_MAX;
   for (int b = lane; b < nblk; b += 64) mx = fmaxf(mx, pr[2 * b]);
@@ -194,9 +202,8 @@ __global__ __launch_bounds__(256) void xent_keys_partials_kernel(const float* __
   sum = wave_sum(sum);
   if (sum < 1e-45f) sum = 1.0f;
   if (lane == 0) {
-    const int key = kt.key((size_t)row, cols);
     double lp = 0.0;
-    if (key >= 0) lp = -log((double)(expf(x[(size_t)row * cols + key] - mx) / sum) + 1e-27);
+    if (key >= 0) lp = -log((double)(expf(xk - mx) / sum) + 1e-27);
     loss_part[row] = lp;
     kt.stats[2 * row] = mx;
     kt.stats[2 * row + 1] = sum;
