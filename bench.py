@@ -295,8 +295,14 @@ def timed_steps(m: Model, lr: float, steps: int, warmup: int, graph: bool = Fals
     """ms per step on the host clock after `warmup` untimed steps (the GPU's
     clocks settle over the first tens of milliseconds).  graph: the step's
     zero_grad / forward / backward replayed as one recorded graph, the update
-    launched from the host (Model.step_graph)."""
-    step = (lambda: m.step_graph(lr, STEP_ALL)) if graph else (lambda: m.step(lr, STEP_ALL))
+    launched from the host (Model.step_graph).  Both read every step's loss
+    back to the host: the eager forward(calc_loss) waits for it before the
+    backward is launched, the replayed step after its update."""
+    def replayed():
+        m.step_graph(lr, STEP_ALL)
+        return m.loss
+
+    step = replayed if graph else (lambda: m.step(lr, STEP_ALL))
     for _ in range(warmup):
         step()
     m.sync()
@@ -485,7 +491,8 @@ def main() -> int:
         "gemm_tflops_per_step": round(cfg.gemm_flop / (ms_step * 1e-3) / 1e12, 2),
         "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 3),
                          "note": "the same step with zero_grad / forward / backward replayed as one recorded HIP "
-                                 "graph and the update launched from the host"} if ms_graph else None,
+                                 "graph, the update launched from the host and the loss read back after each "
+                                 "step"} if ms_graph else None,
         "roofline": rl,
         "cpu_baseline": cpu_line,
         "extras": extras,

@@ -78,6 +78,12 @@ int mle_read_scalar(mle_stream stream, const float* src, float* dst);
  * caller synchronised the stream): under graph capture mle_read_scalar only
  * records its publishing kernel, and each replay of the graph publishes. */
 int mle_scalar_last(float* dst);
+/* The slot's state on the current device: the last published value and its
+ * sequence number, and the last sequence number handed out.  A recorded graph
+ * publishes, on every replay, the number its mle_read_scalar was given at
+ * capture; a caller that noted it can tell whether the slot still holds its
+ * own graph's value (any value or pointer may be null). */
+int mle_scalar_state(float* value, unsigned* published, unsigned* issued);
 
 /* Graphs.  The work a caller enqueues on `stream` between capture_begin and
  * capture_end is recorded (not run) into a graph, instantiated once;

@@ -249,6 +249,19 @@ int mle_scalar_last(float* dst) {
   return MLE_OK;
 }
 
+int mle_scalar_state(float* value, unsigned* published, unsigned* issued) {
+  int dev = 0;
+  MLE_HIP(hipGetDevice(&dev));
+  MLE_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "mle_scalar_state: device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_slot_mu[dev]);
+  const ScalarSlot* slot = g_slot[dev];
+  const unsigned bits = slot ? __atomic_load_n(&slot->bits, __ATOMIC_ACQUIRE) : 0u;
+  if (value) memcpy(value, &bits, sizeof(float));
+  if (published) *published = slot ? __atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) : 0u;
+  if (issued) *issued = g_slot_seq[dev];
+  return MLE_OK;
+}
+
 // ---- graphs ----------------------------------------------------------------
 struct mle_graph_s {
   hipGraph_t graph;

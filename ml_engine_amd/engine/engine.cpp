@@ -262,6 +262,8 @@ void clip_drop(NodeBackProp* p) { g_clip_marked.erase(p); }
 
 void clip_clear() { g_clip_marked.clear(); }
 
+size_t clip_marked_count() { return g_clip_marked.size(); }
+
 // ---------------------------------------------------------------------------
 // flat parameter arena
 namespace {

@@ -124,6 +124,7 @@ void clip_apply(NodeBackProp* p);  // divide this parameter's gradient now, if m
 void clip_apply_all();
 void clip_drop(NodeBackProp* p);   // its gradient is being overwritten or zeroed
 void clip_clear();
+size_t clip_marked_count();        // parameters marked now (each removes itself when destroyed)
 
 // Flat parameter arena.  param_reserve(n) announces n floats of parameters that
 // should be contiguous: it sizes the next slab (default 64 Mi floats) and, if

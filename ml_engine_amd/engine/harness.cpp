@@ -44,6 +44,10 @@ struct Model {
   mle_graph replay = nullptr;
   int replay_mode = 0;
   bool loss_in_slot = false;
+  // The sequence number the recorded pass publishes its loss with (0: it
+  // publishes none, or more than one value), and this model's last loss.
+  unsigned replay_seq = 0;
+  float loss = 0.0f;
   graph target;  // C1 / C4: the one-hot target node (mle_model_target_read)
 };
 
@@ -297,7 +301,10 @@ int mle_model_step(void* h, float lr, int mode, float clip) {
   }
   m->loss_in_slot = false;
   if (mode & MLE_STEP_ZERO) m->go.zero_grad();
-  if (mode & MLE_STEP_FORWARD) m->go.forward(nullptr, true);
+  if (mode & MLE_STEP_FORWARD) {
+    m->go.forward(nullptr, true);
+    m->loss = GraphOperations::loss;  // read back inside forward(calc_loss)
+  }
   if (mode & MLE_STEP_BACKWARD) m->go.backward();
   if (mode & MLE_STEP_UPDATE) m->go.ParameterUpdate(nullptr, false, lr, m->adamw);
   return MLE_OK;
@@ -315,6 +322,9 @@ int mle_model_step_graph(void* h, float lr, int mode) {
     // Record the pass once.  Its host side runs now (the lazy-clearing marks
     // and every other host decision end as after one step, and are the same
     // for every step of this mode); its kernels run on each replay.
+    unsigned issued0 = 0, issued1 = 0;
+    rc = mle_scalar_state(nullptr, nullptr, &issued0);
+    if (rc) return rc;
     rc = mle_graph_capture_begin(s);
     if (rc) return rc;
     if (pass & MLE_STEP_ZERO) m->go.zero_grad();
@@ -322,7 +332,10 @@ int mle_model_step_graph(void* h, float lr, int mode) {
     if (pass & MLE_STEP_BACKWARD) m->go.backward();
     rc = mle_graph_capture_end(s, &m->replay);
     if (rc) return rc;
+    rc = mle_scalar_state(nullptr, nullptr, &issued1);
+    if (rc) return rc;
     m->replay_mode = pass;
+    m->replay_seq = issued1 == issued0 + 1 ? issued1 : 0u;
   }
   int rc = mle_graph_launch(m->replay, s);
   if (rc) return rc;
@@ -340,15 +353,30 @@ int mle_model_target_read(void* h, float* host, size_t count) {
   return mle_memcpy_d2h(host, m->target->output, count * sizeof(float), mle::stream());
 }
 
+// The loss of this model's last forward.  After a replayed pass it is read
+// once the stream has drained: from the published slot when the last value
+// published there carries this graph's sequence number, otherwise (another
+// model or read published since) from the loss node's own output, which the
+// pass's finishing kernel wrote.
 float mle_model_loss(void* h) {
   auto* m = static_cast<Model*>(h);
   if (m->loss_in_slot) {
     check(mle_stream_sync(mle::stream()), "loss read-back");
-    check(mle_scalar_last(&GraphOperations::loss), "loss read-back");
+    float v = 0.0f;
+    unsigned published = 0;
+    check(mle_scalar_state(&v, &published, nullptr), "loss read-back");
+    if (m->replay_seq == 0 || published != m->replay_seq)
+      check(mle_memcpy_d2h(&v, m->root->output, sizeof(float), mle::stream()), "loss read-back");
+    m->loss = v;
+    GraphOperations::loss = v;
     m->loss_in_slot = false;
   }
-  return GraphOperations::loss;
+  return m->loss;
 }
+
+// Parameters whose gradient is marked for a pending clip, over all models
+// (a destroyed parameter leaves the set).
+long long mle_model_clip_pending(void) { return (long long)mle::clip_marked_count(); }
 
 int mle_model_sync(void* h) {
   (void)h;

@@ -55,7 +55,10 @@ int mle_model_step(void* h, float lr, int mode, float clip);
 // the mode changes) and the update launched from the host.  Same results as
 // mle_model_step; mle_model_loss synchronises and reads the published loss.
 int mle_model_step_graph(void* h, float lr, int mode);
+/* This model's loss from its last forward (eager or replayed). */
 float mle_model_loss(void* h);
+/* Parameters, over all models, whose gradient awaits a pending clipNorm. */
+long long mle_model_clip_pending(void);
 // C1 / C4: the first `count` floats of the one-hot target matrix, read the
 // way ReadValueAt reads a node output (a matrix left lazy is brought up to
 // date first).

@@ -32,6 +32,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_memcpy_d2d": (I, [P, P, SZ, P]),
     "mle_read_scalar": (I, [P, P, P]),
     "mle_scalar_last": (I, [P]),
+    "mle_scalar_state": (I, [P, P, P]),
     "mle_graph_capture_begin": (I, [P]),
     "mle_graph_capture_end": (I, [P, P]),
     "mle_graph_launch": (I, [P, P]),

@@ -34,6 +34,7 @@ _SIGS = {
     "mle_model_step": (I, [P, F, I, F]),
     "mle_model_step_graph": (I, [P, F, I]),
     "mle_model_loss": (F, [P]),
+    "mle_model_clip_pending": (LL, []),
     "mle_model_target_read": (I, [P, P, SZ]),
     "mle_model_sync": (I, [P]),
     "mle_model_stream": (P, [P]),

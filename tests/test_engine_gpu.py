@@ -16,6 +16,7 @@ from conftest import assert_close
 from ml_engine_amd.configs import (BlockConfig, FlatConfig, MLPConfig, ResBlockConfig, block_data, flat_data,
                                    mlp_data, resblock_data)
 from ml_engine_amd.models import STEP_ALL, STEP_CLOBBER_SCALE, Model
+from ml_engine_amd.models import lib as models_lib
 
 pytestmark = pytest.mark.gpu
 
@@ -177,9 +178,11 @@ def test_clip_reads_as_reference(hip, orc):
     gradients (its norm is taken over them).  The scale is the one clipNorm saw
     even if the caller overwrites its buffer before the update."""
     cfg = FlatConfig(total=200_000, tensors=5, lo=4096, hi=80_000)
+    pending = models_lib().mle_model_clip_pending
     # between clipNorm and the update
     m, sizes, _, chunks_g = _flat_model(cfg)
     m.step(cfg.lr, 0, cfg.max_norm)  # accumulate + clipNorm, no update
+    assert pending() == len(sizes)
     acc = _oracle_norm(orc, chunks_g)
     assert acc[0] > 1.0
     clipped = [c.copy() for c in chunks_g]
@@ -187,7 +190,14 @@ def test_clip_reads_as_reference(hip, orc):
         orc.call("orc_clip", orc.ptr(c), c.size, orc.ptr(acc))
     for i in range(len(sizes)):
         assert_close(m.get(i, 1), clipped[i], what=f"grad after clipNorm {i}", **EW)
+    # Regression: the pending-clip set holds parameters by address.  A model
+    # closed with its parameters still marked (as after every clipped update)
+    # once left dangling entries there, and the next model's accumulate walked
+    # them (a host abort).  A destroyed parameter now leaves the set.
+    m.step(cfg.lr, 0, cfg.max_norm)
+    assert pending() == len(sizes)
     m.close()
+    assert pending() == 0
     # two full steps without restoring the gradients, and the same with the
     # scale buffer overwritten between clipNorm and the update
     results = []
@@ -216,6 +226,7 @@ def test_clip_reads_as_reference(hip, orc):
             assert_close(p, ref_p[i], what=f"mode {mode} p {i}", **EW)
         results.append(got)
         m.close()
+        assert pending() == 0
     for a, b in zip(results[0], results[1]):
         for u, v in zip(a, b):
             np.testing.assert_array_equal(u, v)
@@ -357,6 +368,48 @@ def test_step_graph_matches_eager(hip, kind):
                 np.testing.assert_array_equal(b[i].view(np.uint32), a[i].view(np.uint32),
                                               err_msg=f"step {step} tensor {w}/{i}")
     for m in models:
+        m.close()
+
+
+def test_graph_loss_is_the_models_own(hip):
+    """A replayed pass publishes its loss into the device's shared read-back
+    slot; another model's step (or any scalar read) publishes there too.  The
+    replayed model's loss is still its own: read from the slot only while the
+    slot holds this graph's sequence number, else from the loss node."""
+    cfg = MLPConfig()
+    x, labels, params = mlp_data(cfg, seed=7)
+    x2, labels2, params2 = mlp_data(cfg, seed=8)
+
+    def make(p, xx, ll):
+        m = Model("mlp", cfg.dims())
+        for i, a in enumerate(p):
+            m.set(i, a)
+        m.input(0, xx)
+        m.input(1, ll)
+        return m
+
+    a, a_eager, b = make(params, x, labels), make(params, x, labels), make(params2, x2, labels2)
+    for step in range(3):
+        a_eager.step(cfg.lr, STEP_ALL)
+        la = a_eager.loss
+        a.step_graph(cfg.lr, STEP_ALL)
+        if step == 0:
+            assert a.loss == la  # nothing published after the replay: the slot's value
+            continue
+        b.step(cfg.lr, STEP_ALL)  # publishes b's loss after a's
+        lb = b.loss
+        assert lb != la
+        assert a.loss == la, (step, a.loss, la, lb)
+        assert b.loss == lb
+    # two replayed models, read in the opposite order
+    b.step_graph(cfg.lr, STEP_ALL)
+    a.step_graph(cfg.lr, STEP_ALL)
+    a_eager.step(cfg.lr, STEP_ALL)
+    la = a_eager.loss
+    lb = b.loss
+    assert a.loss == la
+    assert lb != la
+    for m in (a, a_eager, b):
         m.close()
 
 

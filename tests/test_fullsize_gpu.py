@@ -8,7 +8,7 @@ channels, the 100 M-parameter arena):
   C4  transformer block step, batch 32, seq 256, d 512, 8 x 64 heads, FFN 2048,
       vocab 8000, AdamW                         vs orc_c4_step
   C5  U-Net residual block step, 64 -> 128 channels at 64 x 64, GN(32), time
-      dim 256, batch 2, AdamW                   vs orc_c5_step
+      dim 256, batch 2 and 16 (the timed one), AdamW   vs orc_c5_step
   C3  Linear backward 8192 x 1024 x 4096 through the two mle_gemm calls bench.py
       makes: 256 sampled dX rows, 256 sampled dW columns, the whole db
   C2  accumulate + clipNorm + AdamW over 100 M parameters in 64 tensors, 10
@@ -70,8 +70,12 @@ def test_c4_full_size_vs_oracle(hip, orc):
     m.close()
 
 
-def test_c5_full_width_vs_oracle(hip, orc):
-    cfg = ResBlockConfig(batch=2)
+@pytest.mark.parametrize("batch", [2, 16])
+def test_c5_full_size_vs_oracle(hip, orc, batch):
+    """Batch 16 is the timed workload: the weight-gradient kernels split
+    K = batch x 4096 pixels, so each split there walks 8x more pixels and
+    crosses 8x more image boundaries than at batch 2."""
+    cfg = ResBlockConfig(batch=batch)
     print(f"[fullsize] C5 {cfg}", flush=True)
     x, noise, t, params = resblock_data(cfg, seed=4)
     m = Model("resblock", cfg.dims(t), reference_quirks=True)

@@ -498,6 +498,71 @@ def test_mse(hip, orc, n):
     assert_close(gdx.numpy(), dxz, what="mse bwd assign", **EW)
 
 
+@pytest.mark.parametrize("n", [123457, 123456, 8 * 1024 * 1024])
+@pytest.mark.parametrize("u", [0.75, -3.0e-3])
+def test_mse_bwd_upstream(hip, orc, n, u):
+    """The loss is not the graph's last node: its gradient (one float, written
+    by the consumer) multiplies the derivative, dx += 2 (x - t) u / n
+    (deriv_mse_kernel's `!last` branch, Engine/kernels.cu:1846), adding and
+    assigning.  8 Mi elements is C5's loss size."""
+    r = rng(61 + n % 7)
+    x = r.standard_normal(n, dtype=np.float32)
+    t = r.standard_normal(n, dtype=np.float32)
+    dx0 = r.standard_normal(n, dtype=np.float32)
+    up = np.array([u], np.float32)
+    gx, gt, gup = B(hip, x), B(hip, t), B(hip, up)
+    for acc in (1, 0):
+        ref = dx0.copy() if acc else np.zeros_like(x)
+        orc.call("orc_mse_bwd", orc.ptr(x), orc.ptr(t), orc.ptr(up), orc.ptr(ref), n)
+        gdx = B(hip, dx0) if acc else hip.Buffer.zeros(n)
+        if not acc:
+            hip.call("mle_fill", None, gdx.ptr, float("nan"), n)
+        hip.call("mle_mse_bwd", None, gx.ptr, gt.ptr, gup.ptr, gdx.ptr, n, acc)
+        assert_close(gdx.numpy(), ref, what=f"mse bwd upstream acc={acc}", **EW)
+
+
+@pytest.mark.parametrize("cols", [1000, 8000])
+@pytest.mark.parametrize("u", [0.75, -2.5])
+def test_softmax_xent_bwd_upstream(hip, orc, cols, u):
+    """The cross-entropy is not the last node: dlogits = (p - t) u / batch
+    (Engine/engine.cu:2106-2108: ScaleAdd, ScalePtr by the loss node's
+    gradient, ScaleValue), assigned, for the dense target and for the id
+    target that reads no matrix (ids out of range included)."""
+    r = rng(62 + cols)
+    batch, clen = 3, 40
+    rows = batch * clen
+    logits = (r.standard_normal((rows, cols), dtype=np.float32) * 2).astype(np.float32)
+    keys = r.integers(0, cols, (batch, clen)).astype(np.int32)
+    keys[1, 3] = -1
+    keys[2, 0] = cols + 5
+    tgt = np.zeros((rows, cols), np.float32)
+    for b in range(batch):
+        for s_ in range(clen):
+            if 0 <= keys[b, s_] < cols:
+                tgt[b * clen + s_, keys[b, s_]] = 1.0
+    up = np.array([u], np.float32)
+    pr = np.zeros_like(logits)
+    orc.call("orc_softmax_xent_fwd", orc.ptr(logits), orc.ptr(tgt), orc.ptr(pr), rows, cols)
+    ref = np.zeros_like(logits)
+    orc.call("orc_softmax_xent_bwd", orc.ptr(pr), orc.ptr(tgt), orc.ptr(up), orc.ptr(ref), rows * cols, batch)
+    L = hip.lib()
+    n = rows * cols
+    gl, gt, gk, gup = B(hip, logits), B(hip, tgt), B(hip, keys), B(hip, up)
+    gp, gloss, gst = hip.Buffer.zeros((rows, cols)), hip.Buffer.zeros(1), hip.Buffer.zeros(2 * rows)
+    ws = hip.Buffer(L.mle_loss_ws_bytes(n))
+    hip.call("mle_softmax_xent_fwd", None, gl.ptr, gt.ptr, gp.ptr, rows, cols, gloss.ptr, ws.ptr, ws.nbytes)
+    hip.call("mle_softmax_xent_keys_fwd", None, gl.ptr, gk.ptr, clen, clen, gst.ptr, rows, cols, gloss.ptr, ws.ptr,
+             ws.nbytes)
+    gd, gd2 = hip.Buffer.zeros((rows, cols)), hip.Buffer.zeros((rows, cols))
+    hip.call("mle_fill", None, gd.ptr, float("nan"), n)
+    hip.call("mle_fill", None, gd2.ptr, float("nan"), n)
+    hip.call("mle_softmax_xent_bwd", None, gp.ptr, gt.ptr, gup.ptr, gd.ptr, n, batch)
+    hip.call("mle_softmax_xent_keys_bwd", None, gl.ptr, gst.ptr, gk.ptr, clen, clen, gup.ptr, gd2.ptr, rows, cols,
+             batch)
+    assert_close(gd.numpy(), ref, what="xent bwd upstream (dense target)", **EW)
+    assert_close(gd2.numpy(), ref, what="xent bwd upstream (id target)", **EW)
+
+
 # ------------------------------------------------------------------------ norms
 @pytest.mark.parametrize("batch,channels,hw,groups", [(3, 1, 37 * 45, 1), (2, 1, 256 * 512, 1), (2, 8, 700, 4),
                                                      (2, 64, 4096, 32), (2, 3, 33, 1),

@@ -396,6 +396,47 @@ def test_losses_closed_form(orc):
     assert_close(dl, (ref_p - tg) / batch, rtol=1e-5, atol_scale=1e-7)
 
 
+@pytest.mark.parametrize("u", [0.75, -2.5, 1.0])
+def test_losses_upstream_closed_form(orc, u):
+    """A loss that is not the graph's last node multiplies its derivative by
+    its own gradient u (one float written by the consumer): the MSE adds
+    2 (x - t) u / n into dx (Engine/kernels.cu:1846), the cross-entropy
+    assigns (p - t) u / batch (Engine/engine.cu:2106-2108).  Both follow from
+    the chain rule d(u L)/dx; u = 1 must equal the `last` branch."""
+    r = rng(63)
+    n = 1000
+    x = r.standard_normal(n).astype(np.float32)
+    t = r.standard_normal(n).astype(np.float32)
+    dx0 = r.standard_normal(n).astype(np.float32)
+    up = np.array([u], np.float32)
+    dx = dx0.copy()
+    orc.call("orc_mse_bwd", p(x), p(t), p(up), p(dx), n)
+    ref = dx0.astype(np.float64) + 2.0 * (x.astype(np.float64) - t) * u / n
+    assert_close(dx, ref, rtol=1e-6, atol_scale=1e-7)
+    # the closed form against autograd of u * mean((t - x)^2)
+    xt = torch.tensor(x, dtype=D64, requires_grad=True)
+    (u * ((torch.tensor(t, dtype=D64) - xt) ** 2).mean()).backward()
+    np.testing.assert_allclose(ref - dx0, xt.grad.numpy(), rtol=1e-12, atol=1e-15)
+    if u == 1.0:
+        dl = dx0.copy()
+        orc.call("orc_mse_bwd", p(x), p(t), None, p(dl), n)
+        np.testing.assert_array_equal(dl, dx)
+    rows, cols, batch = 12, 9, 3
+    lg = r.standard_normal((rows, cols)).astype(np.float32)
+    tg = np.eye(cols, dtype=np.float32)[r.integers(0, cols, rows)]
+    pr = np.zeros_like(lg)
+    orc.call("orc_softmax_xent_fwd", p(lg), p(tg), p(pr), rows, cols)
+    dl = np.full_like(lg, np.nan)
+    orc.call("orc_softmax_xent_bwd", p(pr), p(tg), p(up), p(dl), rows * cols, batch)
+    ref_p = np.exp(lg.astype(np.float64) - lg.max(1, keepdims=True))
+    ref_p /= ref_p.sum(1, keepdims=True)
+    assert_close(dl, (ref_p - tg) * u / batch, rtol=1e-5, atol_scale=1e-7)
+    if u == 1.0:
+        d1 = np.zeros_like(lg)
+        orc.call("orc_softmax_xent_bwd", p(pr), p(tg), None, p(d1), rows * cols, batch)
+        np.testing.assert_array_equal(d1, dl)
+
+
 # ------------------------------------------------------------------ optimizer
 @pytest.mark.parametrize("adamw", [0, 1])
 def test_adam_matches_torch_optim_over_steps(orc, adamw):
