@@ -571,6 +571,11 @@ int mle_grad_sqnorm(mle_stream stream, const float* g, size_t n, double* accum, 
 /* s = sqrt(s); s = (s > 1) ? s*scale : scale.  Left unchanged when NaN.
  * Sqrt_Scale type 0 (Engine/kernels.cu:1763-1773). */
 int mle_sqrt_scale(mle_stream stream, double* s, double scale);
+/* mle_grad_sqnorm, then (sqrt_scale != 0) mle_sqrt_scale(accum, scale) in the
+ * launch that finishes the sum: GraphOperations::accumulate's last
+ * SumSquared followed by its Sqrt_Scale (Engine/engine.cu:3364-3368). */
+int mle_grad_sqnorm_ex(mle_stream stream, const float* g, size_t n, double* accum, int* nonfinite, int sqrt_scale,
+                       double scale, void* ws, size_t ws_bytes);
 /* One Adam (adamw == 0) or AdamW (adamw != 0) step.  When clip != NULL the
  * gradient is read as g / (float)clip[0] (clipNorm fused into the update).
  * AdamUpdate / AdamWUpdate (Engine/kernels.cu:1508-1534), including the double
@@ -645,12 +650,23 @@ int mle_argmax(mle_stream stream, const float* x, int rows, int cols, int32_t* o
 /* ------------------------------------------------------------------------- */
 
 /* Arm the probe for one kernel family ("gemm_nn", "gemm_nt", "gemm_tn",
- * "gemm_tt", "adamw_update", ...): every later launch of it records a HIP
- * event pair on its own stream together with its algorithmic flop and byte
+ * "gemm_tt", "adam_update", ...) or a comma-separated list of them: every
+ * later call of those families records a HIP event pair per kernel it
+ * launches, on its own stream, together with its algorithmic flop and byte
  * counts.  NULL or "" disarms.  Host-side bookkeeping only. */
 int mle_probe_arm(const char* kernel);
 /* Synchronise the recorded events and return totals since arming. */
 int mle_probe_read(int* launches, double* total_ms, double* total_flop, double* total_bytes);
+
+/* Device timing: an event recorded on a stream completes when the work
+ * queued before it has run; elapsed_ms synchronises `stop` and returns the
+ * time between the two.  No reference counterpart (its Timing class reads the
+ * host clock, Includes/debugging_utils.h:81-93). */
+typedef struct mle_event_s* mle_event;
+int mle_event_create(mle_event* ev);
+int mle_event_record(mle_event ev, mle_stream stream);
+int mle_event_elapsed_ms(mle_event start, mle_event stop, float* ms);
+int mle_event_destroy(mle_event ev);
 
 #ifdef __cplusplus
 }

@@ -1488,9 +1488,11 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
         if (wn == 2) mle::launch(conv1_wgrad_kernel<2, 2, 4>, c3.items, 256, 0, s, c3);
         else mle::launch(conv1_wgrad_kernel<2, 1, 4>, c3.items, 256, 0, s, c3);
       }
+      // The reduce that completes dW and db is part of the probed family.
+      if (splits > 1)
+        launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw, bpart, db ? cout : 0, db,
+                            accumulate_db);
     }
-    if (splits > 1)
-      launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw, bpart, db ? cout : 0, db, accumulate_db);
     return check_launch("mle_conv2d_wgrad");
   }
   int kchunk;
@@ -1509,9 +1511,8 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
       dim3 grid((op.N + BN - 1) / BN, (op.M + BM - 1) / BM, splits);
       mle::launch(igemm_kernel<WgradOps, true>, grid, NT, 0, s, op, kchunk);
     }
+    launch_split_reduce(s, static_cast<const float*>(ws), splits, (size_t)op.M * op.N, dw);
   }
-  const size_t mn = (size_t)op.M * op.N;
-  launch_split_reduce(s, static_cast<const float*>(ws), splits, mn, dw);
   rc = check_launch("mle_conv2d_wgrad");
   if (rc != MLE_OK || !db) return rc;
   // Other filters: the bias gradient by its own channel sum.

@@ -1303,12 +1303,12 @@ static int gemm_impl(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   if (rc != MLE_OK || P.empty) return rc;
   hipStream_t s = as_stream(stream);
   {
-    // The probe times the GEMM kernel itself (the split reduce is a separate,
-    // HBM-bound kernel).
+    // The probe times the whole product: the GEMM kernel and, with split K,
+    // the reduce that completes C.
     ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
     gemm_launch_main(s, P);
+    gemm_launch_reduce(s, P);
   }
-  gemm_launch_reduce(s, P);
   return check_launch(kFamily[P.which]);
 }
 
@@ -1473,16 +1473,14 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, 
                   : (P1.cs ? gemm_pair_kernel<0, 1, false, false, 1, 0, true, false>
                            : gemm_pair_kernel<0, 1, false, false, 1, 0, false, false>);
       mle::launch(k, grid, NT, 0, s, P0.g, P1.g, pg);
+      gemm_launch_reduce(s, P1);
     }
-    gemm_launch_reduce(s, P1);
     return check_launch("gemm_pair");
   }
   // Otherwise one launch each, in order (they may share the workspace).
   if (!P0.empty) {
-    {
-      ProbeScope probe(kFamily[P0.which], s, P0.flop, P0.bytes);
-      gemm_launch_main(s, P0);
-    }
+    ProbeScope probe(kFamily[P0.which], s, P0.flop, P0.bytes);
+    gemm_launch_main(s, P0);
     gemm_launch_reduce(s, P0);
   }
   rc = check_launch(kFamily[P0.which]);
@@ -1490,8 +1488,8 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, 
   {
     ProbeScope probe(kFamily[P1.which], s, P1.flop, P1.bytes);
     gemm_launch_main(s, P1);
+    gemm_launch_reduce(s, P1);
   }
-  gemm_launch_reduce(s, P1);
   return check_launch(kFamily[P1.which]);
 }
 

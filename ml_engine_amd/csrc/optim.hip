@@ -24,26 +24,31 @@ constexpr unsigned kPartCap = 8192;
 __device__ __forceinline__ f32x4 ld4(const float* p, size_t i) { return *reinterpret_cast<const f32x4*>(p + i); }
 __device__ __forceinline__ void st4(float* p, size_t i, f32x4 v) { *reinterpret_cast<f32x4*>(p + i) = v; }
 
+// Workgroup b sums the contiguous range [b * per, (b + 1) * per) of float4
+// groups (VEC) or floats, so each workgroup streams one span of memory (the
+// DRAM pages it opens are read through; strided grids across the whole array
+// ran 14 % slower).  Eight 16-byte loads are in flight per lane, each feeding
+// its own accumulator; the order of the additions is fixed by (n, grid).
+constexpr int SQ_U = 8;
 template <bool VEC>
-__global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g, size_t n, double* __restrict__ part,
-                                                     int* __restrict__ nonfinite) {
+__global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g, size_t n, size_t per,
+                                                     double* __restrict__ part, int* __restrict__ nonfinite) {
   __shared__ double red[NT / 64];
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  double acc[SQ_U];
+#pragma unroll
+  for (int u = 0; u < SQ_U; ++u) acc[u] = 0.0;
   bool bad = false;
-  const size_t stride = (size_t)gridDim.x * NT;
-  size_t tail = 0;
+  const size_t units = VEC ? n / 4 : n;
+  const size_t b0 = (size_t)blockIdx.x * per, b1 = b0 + per < units ? b0 + per : units;
+  size_t i = b0 + threadIdx.x;
   if (VEC) {
-    // Four independent 16-byte loads in flight per lane, each with its own
-    // accumulator; the order of the additions is fixed by (n, grid).
-    const size_t n4 = n / 4;
     const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
-    size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
-    for (; i + 3 * stride < n4; i += 4 * stride) {
-      f32x4 v[4];
+    for (; i + (SQ_U - 1) * NT < b1; i += SQ_U * NT) {
+      f32x4 v[SQ_U];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(g4 + i + u * stride);
+      for (int u = 0; u < SQ_U; ++u) v[u] = __builtin_nontemporal_load(g4 + i + u * NT);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < SQ_U; ++u)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const double d = (double)v[u][j];
@@ -51,8 +56,8 @@ __global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g
           bad |= !isfinite(v[u][j]);
         }
     }
-    for (; i < n4; i += stride) {
-      const f32x4 v = g4[i];
+    for (; i < b1; i += NT) {
+      const f32x4 v = __builtin_nontemporal_load(g4 + i);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const double d = (double)v[j];
@@ -60,27 +65,65 @@ __global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g
         bad |= !isfinite(v[j]);
       }
     }
-    tail = n4 * 4;
+    // the n % 4 tail, by the last workgroup
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x < n - units * 4) {
+      const float x = g[units * 4 + threadIdx.x];
+      acc[1] += (double)x * (double)x;
+      bad |= !isfinite(x);
+    }
+  } else {
+    for (; i < b1; i += NT) {
+      const float x = g[i];
+      acc[0] += (double)x * (double)x;
+      bad |= !isfinite(x);
+    }
   }
-  for (size_t i = tail + (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
-    const double d = (double)g[i];
-    acc[0] += d * d;
-    bad |= !isfinite(g[i]);
-  }
-  double t = block_sum<NT>((acc[0] + acc[1]) + (acc[2] + acc[3]), red);
+  double t = 0.0;
+#pragma unroll
+  for (int u = 0; u < SQ_U; ++u) t += acc[u];
+  t = block_sum<NT>(t, red);
   if (threadIdx.x == 0) part[blockIdx.x] = t;
   if (bad && nonfinite) nonfinite[0] = 1;
+}
+
+// Launch shape of the partial pass: `per` units (float4 groups when VEC,
+// else floats) per workgroup, a multiple of NT, and the grid that covers n
+// with at most kPartCap workgroups (100 M floats: 8139 workgroups of 3072
+// float4 groups, 12 per lane).
+struct SqnormShape {
+  unsigned grid;
+  size_t per;
+};
+inline SqnormShape sqnorm_shape(size_t n, bool vec) {
+  const size_t units = vec ? n / 4 : n;
+  size_t blocks = (units + (size_t)NT * SQ_U - 1) / ((size_t)NT * SQ_U);
+  blocks = std::min<size_t>(std::max<size_t>(blocks, 1), kPartCap);
+  size_t per = (units + blocks - 1) / blocks;
+  per = std::max<size_t>((per + NT - 1) / NT * NT, NT);
+  const size_t grid = std::max<size_t>((units + per - 1) / per, 1);
+  return {(unsigned)grid, per};
 }
 
 // accum[0] (+)= sum(part).  With do_scale, then s = sqrt(accum);
 // s = s > 1 ? s*scale : scale (Sqrt_Scale type 0), skipped when accum is NaN.
 constexpr int FIN_NT = 1024;
+static_assert(kPartCap % FIN_NT == 0, "the finishing launch reads kPartCap / FIN_NT partials per lane");
 __global__ __launch_bounds__(FIN_NT) void sqnorm_finish(const double* __restrict__ part, unsigned nparts,
                                                         double* __restrict__ accum, int add_existing, int do_scale,
                                                         double scale, double* __restrict__ copy_out) {
   __shared__ double red[FIN_NT / 64];
+  // Up to kPartCap / FIN_NT = 8 partials per lane, all loads issued before
+  // the first add (a loop would wait out one memory latency per partial).
+  constexpr int PER = kPartCap / FIN_NT;
+  double v[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const unsigned i = threadIdx.x + (unsigned)j * FIN_NT;
+    v[j] = i < nparts ? part[i] : 0.0;
+  }
   double acc = 0.0;
-  for (unsigned i = threadIdx.x; i < nparts; i += FIN_NT) acc += part[i];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) acc += v[j];
   acc = block_sum<FIN_NT>(acc, red);
   if (threadIdx.x == 0) {
     double v = add_existing ? accum[0] + acc : acc;
@@ -234,8 +277,17 @@ int launch_update(hipStream_t s, float* p, const float* g, float* m, float* v, s
   return check_launch("mle_adam_update");
 }
 
-// About four float4 groups of four per lane at the cap (100 M floats -> 8192 blocks).
-unsigned sqnorm_grid(size_t n) { return stream_grid((n + 15) / 16, NT, kPartCap); }
+// Workspace slots the partial pass needs: its larger grid of the two layouts
+// (the pointer's alignment picks one at launch).
+unsigned sqnorm_grid(size_t n) { return std::max(sqnorm_shape(n, false).grid, sqnorm_shape(n, true).grid); }
+
+void launch_sqnorm_partial(hipStream_t s, const float* g, size_t n, double* part, int* nonfinite, unsigned& grid) {
+  const bool vec = aligned16(g);
+  const SqnormShape sh = sqnorm_shape(n, vec);
+  grid = sh.grid;
+  if (vec) mle::launch(sqnorm_partial<true>, sh.grid, NT, 0, s, g, n, sh.per, part, nonfinite);
+  else mle::launch(sqnorm_partial<false>, sh.grid, NT, 0, s, g, n, sh.per, part, nonfinite);
+}
 
 }  // namespace
 
@@ -243,21 +295,25 @@ extern "C" {
 
 size_t mle_sqnorm_ws_bytes(size_t n) { return (size_t)sqnorm_grid(n) * sizeof(double); }
 
+int mle_grad_sqnorm_ex(mle_stream stream, const float* g, size_t n, double* accum, int* nonfinite, int sqrt_scale,
+                       double scale, void* ws, size_t ws_bytes) {
+  MLE_CHECK_ARG(accum && (n == 0 || (g && ws)), "mle_grad_sqnorm: null pointer");
+  hipStream_t s = as_stream(stream);
+  if (n == 0) return sqrt_scale ? mle_sqrt_scale(stream, accum, scale) : MLE_OK;
+  if (ws_bytes < mle_sqnorm_ws_bytes(n)) return set_error(MLE_ERR_WORKSPACE, "mle_grad_sqnorm: workspace too small");
+  double* part = static_cast<double*>(ws);
+  // The probe times the whole sum: the partial pass and the launch that
+  // finishes it.
+  ProbeScope probe("sqnorm", s, 0.0, 4.0 * (double)n);
+  unsigned grid = 0;
+  launch_sqnorm_partial(s, g, n, part, nonfinite, grid);
+  mle::launch(sqnorm_finish, 1, FIN_NT, 0, s, part, grid, accum, 1, sqrt_scale ? 1 : 0, scale, nullptr);
+  return check_launch("mle_grad_sqnorm");
+}
+
 int mle_grad_sqnorm(mle_stream stream, const float* g, size_t n, double* accum, int* nonfinite, void* ws,
                     size_t ws_bytes) {
-  MLE_CHECK_ARG(g && accum && ws, "mle_grad_sqnorm: null pointer");
-  if (n == 0) return MLE_OK;
-  const unsigned grid = sqnorm_grid(n);
-  if (ws_bytes < grid * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "mle_grad_sqnorm: workspace too small");
-  hipStream_t s = as_stream(stream);
-  double* part = static_cast<double*>(ws);
-  {
-    ProbeScope probe("sqnorm", s, 0.0, 4.0 * (double)n);
-    if (aligned16(g)) mle::launch(sqnorm_partial<true>, grid, NT, 0, s, g, n, part, nonfinite);
-    else mle::launch(sqnorm_partial<false>, grid, NT, 0, s, g, n, part, nonfinite);
-  }
-  mle::launch(sqnorm_finish, 1, FIN_NT, 0, s, part, grid, accum, 1, 0, 1.0, nullptr);
-  return check_launch("mle_grad_sqnorm");
+  return mle_grad_sqnorm_ex(stream, g, n, accum, nonfinite, 0, 1.0, ws, ws_bytes);
 }
 
 int mle_sqrt_scale(mle_stream stream, double* s, double scale) {
@@ -291,14 +347,13 @@ int adamw_clip(hipStream_t s, float* p, const float* g, float* m, float* v, size
   if (clip_scale > 0.0) {
     double* sdev = static_cast<double*>(ws);
     double* part = reinterpret_cast<double*>(static_cast<char*>(ws) + 256);
-    const unsigned grid = sqnorm_grid(n);
     {
       ProbeScope probe("sqnorm", s, 0.0, 4.0 * (double)n);
-      if (aligned16(g)) mle::launch(sqnorm_partial<true>, grid, NT, 0, s, g, n, part, nullptr);
-      else mle::launch(sqnorm_partial<false>, grid, NT, 0, s, g, n, part, nullptr);
+      unsigned grid = 0;
+      launch_sqnorm_partial(s, g, n, part, nullptr, grid);
+      // s = Sqrt_Scale(sum g^2) computed from zero, so nothing is cleared beforehand.
+      mle::launch(sqnorm_finish, 1, FIN_NT, 0, s, part, grid, sdev, 0, 1, clip_scale, norm_out);
     }
-    // s = Sqrt_Scale(sum g^2) computed from zero, so nothing is cleared beforehand.
-    mle::launch(sqnorm_finish, 1, FIN_NT, 0, s, part, grid, sdev, 0, 1, clip_scale, norm_out);
     int rc = check_launch("adamw_clip: norm");
     if (rc) return rc;
     clip = sdev;

@@ -72,10 +72,12 @@ static hipEvent_t take_event() {
 // atomic load, no lock and no string compare.
 static std::atomic<bool> g_probe_on{false};
 
+// Armed families, as ",name1,name2," so a membership test is one search.
 bool probe_armed(const char* kernel) {
   if (!g_probe_on.load(std::memory_order_relaxed)) return false;
   std::lock_guard<std::mutex> lk(g_probe_mu);
-  return !g_probe_kernel.empty() && g_probe_kernel == kernel;
+  const std::string key = std::string(",") + kernel + ",";
+  return g_probe_kernel.find(key) != std::string::npos;
 }
 
 void probe_begin(hipStream_t) {
@@ -378,8 +380,43 @@ int mle_probe_arm(const char* kernel) {
       g_event_pool.push_back(e.second);
     }
   g_probe_recs.clear();
-  g_probe_kernel = kernel ? kernel : "";
-  g_probe_on.store(!g_probe_kernel.empty(), std::memory_order_relaxed);
+  const bool on = kernel && kernel[0];
+  g_probe_kernel = on ? std::string(",") + kernel + "," : std::string();
+  g_probe_on.store(on, std::memory_order_relaxed);
+  return MLE_OK;
+}
+
+struct mle_event_s {
+  hipEvent_t e;
+};
+
+int mle_event_create(mle_event* ev) {
+  MLE_CHECK_ARG(ev != nullptr, "mle_event_create: null out pointer");
+  *ev = nullptr;
+  hipEvent_t e = nullptr;
+  MLE_HIP(hipEventCreate(&e));
+  *ev = new mle_event_s{e};
+  return MLE_OK;
+}
+
+int mle_event_record(mle_event ev, mle_stream stream) {
+  MLE_CHECK_ARG(ev != nullptr, "mle_event_record: null event");
+  MLE_HIP(hipEventRecord(ev->e, as_stream(stream)));
+  return MLE_OK;
+}
+
+int mle_event_elapsed_ms(mle_event start, mle_event stop, float* ms) {
+  MLE_CHECK_ARG(start && stop && ms, "mle_event_elapsed_ms: null argument");
+  MLE_HIP(hipEventSynchronize(stop->e));
+  MLE_HIP(hipEventElapsedTime(ms, start->e, stop->e));
+  return MLE_OK;
+}
+
+int mle_event_destroy(mle_event ev) {
+  if (!ev) return MLE_OK;
+  const hipError_t e = hipEventDestroy(ev->e);
+  delete ev;
+  if (e != hipSuccess) return hip_error(e, "mle_event_destroy");
   return MLE_OK;
 }
 

@@ -704,13 +704,20 @@ void GraphOperations::accumulate(double* global_scale) {
   if (!all_hooks_known || dup) {
     for (auto& node : nodes)
       if (node->accumulate) node->accumulate(global_scale);
-  } else {
-    for (auto& sp : contiguous_spans(ps)) {
-      const size_t ws = mle_sqnorm_ws_bytes(sp.n);
-      check(mle_grad_sqnorm(mle::stream(), sp.g, sp.n, global_scale, nullptr, span_ws(ws), ws), "SumSquared");
-    }
+    check(mle_sqrt_scale(mle::stream(), global_scale, 1.0), "Sqrt_Scale");
+    return;
   }
-  check(mle_sqrt_scale(mle::stream(), global_scale, 1.0), "Sqrt_Scale");
+  // One sum per contiguous span of the arena; the last one's finishing
+  // launch also applies Sqrt_Scale.
+  const auto spans = contiguous_spans(ps);
+  if (spans.empty()) check(mle_sqrt_scale(mle::stream(), global_scale, 1.0), "Sqrt_Scale");
+  for (size_t i = 0; i < spans.size(); ++i) {
+    const auto& sp = spans[i];
+    const size_t ws = mle_sqnorm_ws_bytes(sp.n);
+    check(mle_grad_sqnorm_ex(mle::stream(), sp.g, sp.n, global_scale, nullptr, i + 1 == spans.size() ? 1 : 0, 1.0,
+                             span_ws(ws), ws),
+          "SumSquared + Sqrt_Scale");
+  }
 }
 
 void GraphOperations::ParameterUpdate(const graph& X, const bool show, const float lr, const bool adamw) {

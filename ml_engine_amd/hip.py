@@ -121,6 +121,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_sqnorm_ws_bytes": (SZ, [SZ]),
     "mle_grad_sqnorm": (I, [P, P, SZ, P, P, P, SZ]),
     "mle_sqrt_scale": (I, [P, P, D]),
+    "mle_grad_sqnorm_ex": (I, [P, P, SZ, P, P, I, D, P, SZ]),
     "mle_adam_update": (I, [P, P, P, P, P, SZ, I, F, F, F, F, F, I, P]),
     "mle_adamw_clip_ws_bytes": (SZ, [SZ]),
     "mle_adamw_clip_fused": (I, [P, P, P, P, P, SZ, I, F, F, F, F, F, I, D, P, P, SZ]),
@@ -134,6 +135,10 @@ SIGNATURES: dict[str, tuple] = {
     "mle_argmax": (I, [P, P, I, I, P]),
     "mle_probe_arm": (I, [C.c_char_p]),
     "mle_probe_read": (I, [C.POINTER(I), C.POINTER(D), C.POINTER(D), C.POINTER(D)]),
+    "mle_event_create": (I, [C.POINTER(P)]),
+    "mle_event_record": (I, [P, P]),
+    "mle_event_elapsed_ms": (I, [P, P, C.POINTER(F)]),
+    "mle_event_destroy": (I, [P]),
 }
 
 ACT = {"relu": 0, "gelu": 1, "silu": 2, "tanh": 3, "sigmoid": 4, "leaky_relu": 5}
@@ -241,6 +246,32 @@ class Buffer:
 
 def sync(stream=None) -> None:
     call("mle_stream_sync", stream)
+
+
+class Event:
+    """A device event (mle_event_*): record on a stream, read the time between two."""
+
+    def __init__(self):
+        init()
+        p = P()
+        call("mle_event_create", C.byref(p))
+        self.ptr = p.value
+
+    def record(self, stream=None) -> None:
+        call("mle_event_record", self.ptr, stream)
+
+    def ms_since(self, start: "Event") -> float:
+        ms = F()
+        call("mle_event_elapsed_ms", start.ptr, self.ptr, C.byref(ms))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if getattr(self, "ptr", None):
+                lib().mle_event_destroy(self.ptr)
+                self.ptr = None
+        except Exception:
+            pass
 
 
 def version() -> str:

@@ -28,7 +28,8 @@ Usage (on the GPU box; rocprofv3 puts the program itself after `--`):
       the same traffic averaged over one launch-probe family (gemm_nn, gemm_nt,
       gemm_tn, gemm_tt: a GEMM layout; gemm_pair: the Linear backward dX + dW
       launch; conv_fwd, conv_dgrad, conv_wgrad; adam_update; sqnorm; attn_fwd,
-      attn_bwd) -- the `traffic` bench.py reports for its roofline kernel
+      attn_bwd), each launch with the split reduce that completes it -- the
+      `traffic` bench.py reports for its roofline kernel
   python3 -m ml_engine_amd.profiling families FETCH.db WRITE.db CFETCH.db CWRITE.db N OUT.json
       `family` for every family present, into one JSON object
 """
@@ -110,9 +111,28 @@ def families(fetch_db: str, write_db: str, cfetch_db: str, cwrite_db: str, n: in
     return {f: family(f, fetch_db, write_db, cfetch_db, cwrite_db, n) for f in sorted(found)}
 
 
+REDUCE_KERNEL = "split_reduce_kernel<"
+
+
+def family_bytes(db: str, counter: str, fam: str) -> list[float]:
+    """Bytes (uncalibrated) of each launch of a family: the family's kernel
+    plus, when the next dispatch is a split reduce, that reduce -- it is
+    launched by the same call and completes the family's output, and the
+    launch probe times both."""
+    rows = per_dispatch(db, counter)
+    out = []
+    for i, (_, k, v, _) in enumerate(rows):
+        if family_of(k) != fam:
+            continue
+        if i + 1 < len(rows) and REDUCE_KERNEL in rows[i + 1][1]:
+            v += rows[i + 1][2]
+        out.append(1024.0 * v)
+    return out
+
+
 def family(fam: str, fetch_db: str, write_db: str, cfetch_db: str, cwrite_db: str, n: int) -> dict:
-    fetch = [1024.0 * v for _, k, v, _ in per_dispatch(fetch_db, "FETCH_SIZE") if family_of(k) == fam]
-    write = [1024.0 * v for _, k, v, _ in per_dispatch(write_db, "WRITE_SIZE") if family_of(k) == fam]
+    fetch = family_bytes(fetch_db, "FETCH_SIZE", fam)
+    write = family_bytes(write_db, "WRITE_SIZE", fam)
     f_fetch, f_write = calibration(cfetch_db, cwrite_db, n)
     out = {
         "family": fam,

@@ -1010,6 +1010,75 @@ def test_sqnorm_and_fused_clip(hip, orc):
     np.testing.assert_array_equal(gg.numpy(), g)  # the fused path leaves g unclipped
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 255, 257, 2048 * 4 + 1, 1_000_003, 16_777_216 + 7])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_sqnorm_shapes_and_sqrt_scale(hip, orc, n, offset):
+    """The partial pass's contiguous per-workgroup ranges cover every element
+    once, for vector (16-byte aligned) and scalar (offset by one float) data,
+    with n % 4 tails and single-workgroup sizes; the sum is fixed-order (two
+    calls give the same bits); the NaN / Inf flag; and mle_grad_sqnorm_ex's
+    Sqrt_Scale in the finishing launch equals mle_sqrt_scale after the sum."""
+    r = rng(32 + n % 97)
+    g = (r.standard_normal(n) * 0.3).astype(np.float32)
+    acc = np.zeros(1, np.float64)
+    orc.call("orc_sumsq", orc.ptr(g), n, orc.ptr(acc))
+    s_ref = acc.copy()
+    orc.call("orc_sqrt_scale", orc.ptr(s_ref), 1.0)
+    L = hip.lib()
+    buf = hip.Buffer(4 * (n + 1))
+    buf.upload(np.concatenate([np.zeros(offset, np.float32), g]))
+    gptr = buf.ptr + 4 * offset
+    ws = hip.Buffer(L.mle_sqnorm_ws_bytes(n))
+    bad = hip.Buffer.zeros(1, np.int32)
+    outs = []
+    for _ in range(2):
+        gacc = B(hip, np.array([0.25], np.float64))
+        hip.call("mle_grad_sqnorm", None, gptr, n, gacc.ptr, bad.ptr, ws.ptr, ws.nbytes)
+        outs.append(gacc.numpy(dtype=np.float64))
+    np.testing.assert_allclose(outs[0], acc + 0.25, rtol=1e-12)
+    np.testing.assert_array_equal(outs[0].view(np.uint64), outs[1].view(np.uint64))
+    assert bad.numpy()[0] == 0
+    gs = B(hip, np.array([0.0], np.float64))
+    hip.call("mle_grad_sqnorm_ex", None, gptr, n, gs.ptr, None, 1, 1.0, ws.ptr, ws.nbytes)
+    np.testing.assert_allclose(gs.numpy(dtype=np.float64), s_ref, rtol=1e-12)
+    g2 = B(hip, np.array([0.0], np.float64))
+    hip.call("mle_grad_sqnorm", None, gptr, n, g2.ptr, None, ws.ptr, ws.nbytes)
+    hip.call("mle_sqrt_scale", None, g2.ptr, 1.0)
+    np.testing.assert_array_equal(gs.numpy(dtype=np.float64), g2.numpy(dtype=np.float64))
+    # a non-finite element anywhere (here the last, in the tail when n % 4 != 0) sets the flag
+    g[-1] = np.inf
+    buf.upload(np.concatenate([np.zeros(offset, np.float32), g]))
+    hip.call("mle_grad_sqnorm", None, gptr, n, gacc.ptr, bad.ptr, ws.ptr, ws.nbytes)
+    assert bad.numpy()[0] == 1
+
+
+def test_events_and_probe_lists(hip):
+    """mle_event_*: the time between two events around queued work; the probe
+    armed with a comma-separated family list records calls of each family."""
+    n = 1 << 22
+    g = B(hip, np.ones(n, np.float32))
+    L = hip.lib()
+    ws = hip.Buffer(L.mle_sqnorm_ws_bytes(n))
+    acc = hip.Buffer.zeros(1, np.float64)
+    p, m, v = B(hip, np.zeros(n, np.float32)), B(hip, np.zeros(n, np.float32)), B(hip, np.zeros(n, np.float32))
+    e0, e1 = hip.Event(), hip.Event()
+    hip.call("mle_probe_arm", b"sqnorm,adam_update")
+    e0.record()
+    hip.call("mle_grad_sqnorm", None, g.ptr, n, acc.ptr, None, ws.ptr, ws.nbytes)
+    hip.call("mle_adam_update", None, p.ptr, g.ptr, m.ptr, v.ptr, n, 1, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, None)
+    hip.call("mle_fill", None, p.ptr, 0.0, n)  # not a probed family
+    e1.record()
+    ms = e1.ms_since(e0)
+    import ctypes as C
+    k, tot, fl, by = C.c_int(), C.c_double(), C.c_double(), C.c_double()
+    hip.call("mle_probe_read", C.byref(k), C.byref(tot), C.byref(fl), C.byref(by))
+    hip.call("mle_probe_arm", None)
+    assert k.value == 2
+    assert by.value == 4.0 * n + 28.0 * n
+    assert 0.0 < tot.value <= ms
+    assert acc.numpy(dtype=np.float64)[0] == n
+
+
 # ------------------------------------------------------------ integer paths
 def test_gather_onehot_argmax_scatter(hip, orc):
     r = rng(41)
