@@ -558,6 +558,19 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
                           int accumulate_db, int n, int cin, int h, int w_in, int cout, int kh, int kw, int pad,
                           int stride, void* ws, size_t ws_bytes);
 
+/* A 3 x 3 (pad 1) and a 1 x 1 (pad 0) convolution of the same input, both
+ * stride 1 (ResidualBlock's conv1 and skip convolution, Engine/diffusion.cu:
+ * 129-137): the two CV2D forwards (Engine/kernels.cu:985-1019) in one launch,
+ * and the two CV2D_GradInput passes (Engine/kernels.cu:1052-1089) adding into
+ * the one dx in one launch, dx (+)= dgrad3(dy3) + dgrad1(dy1).  _supported
+ * says whether the shapes run on these kernels (otherwise the per-convolution
+ * calls do; the paired calls return MLE_ERR_UNSUPPORTED). */
+int mle_conv2d_pair_supported(int n, int cin, int h, int w, int cout3, int cout1);
+int mle_conv2d_pair_fwd(mle_stream stream, const float* x, int n, int cin, int h, int w, const float* w3,
+                        const float* b3, float* y3, int cout3, const float* w1, const float* b1, float* y1, int cout1);
+int mle_conv2d_pair_dgrad(mle_stream stream, float* dx, int accumulate, int n, int cin, int h, int w,
+                          const float* dy3, const float* w3, int cout3, const float* dy1, const float* w1, int cout1);
+
 /* ------------------------------------------------------------------------- */
 /* Optimizer                                                                 */
 /* ------------------------------------------------------------------------- */

@@ -471,6 +471,8 @@ __global__ __launch_bounds__(NT, 2) void conv_fast_kernel(FastConv c) {
 }
 
 // ---------------------------------------------------------------------------
+constexpr int kC3U = 2, kC3D = 4;  // 3 x 3 direct kernels: channel quads per stage, stages in flight
+
 // Register-direct 3 x 3 convolution, stride 1, pad 1 (output grid = input
 // grid): forward and input gradient with no LDS in the K loop.
 //
@@ -602,8 +604,17 @@ __device__ __forceinline__ void conv_block_out(f32x4 (&acc)[4][4], const Conv3Ar
   }
 }
 
-template <bool DG, bool HALO, int WM, int WN, int KS, int U, int D>
-__global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv3_direct_kernel(Conv3Args c) {
+template <bool DG, int KS, int D>
+__device__ __forceinline__ void conv1_kloop(f32x4 (&acc)[4][4], const Conv3Args& c, int m0, int lr, int q, int ks,
+                                            bool gok, int b, int p);
+
+// One 64 WM x 64 WN tile of a 3 x 3 convolution: L is the workgroup's index
+// among this product's workgroups (its XCD is L % 8).  EXTRA (input
+// gradient only): after the 3 x 3 stages the same accumulators also take the
+// input gradient of a 1 x 1 convolution of the same input (c1: its output
+// gradient and weights), so one tile writes dx = dgrad3 + dgrad1.
+template <bool DG, bool HALO, int WM, int WN, int KS, int U, int D, bool EXTRA = false>
+__device__ __forceinline__ void conv3_direct_body(const Conv3Args& c, const Conv3Args& c1, int L) {
   constexpr int SG = DG ? -1 : 1;  // shift of tap t is SG * (t - 1)
   constexpr int CPS = 4 * U;       // channels per stage
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -611,7 +622,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv3_direct_kernel(Conv
   const int wm = wave % WM, wn = (wave / WM) % WN, ks = wave / (WM * WN);
   // Workgroup -> tile: consecutive tiles on one XCD (workgroups are dealt to
   // the 8 XCDs round robin), so neighbouring pixel tiles share its L2.
-  const int L = blockIdx.x, xq = c.tiles / 8, xr = c.tiles % 8, xc = L % 8;
+  const int xq = c.tiles / 8, xr = c.tiles % 8, xc = L % 8;
   const int item = xc * xq + min(xc, xr) + L / 8;
   const int tm = item % c.tiles_m, tn = item / c.tiles_m;
   const int m0 = (tm * WM + wm) * 64;
@@ -711,8 +722,14 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv3_direct_kernel(Conv
 #pragma unroll
   for (int s = 0; s < D - 1; ++s)
     if (kt + s < k1) mfma(fa[s], fb[s], fh[s]);
+  if (EXTRA) conv1_kloop<true, KS, 4>(acc, c1, m0, lr, q, ks, gok, b, p);
 
   conv_block_out<DG, WM, WN, KS>(acc, c, m0, lane, wave, ks, gok, b, p);
+}
+
+template <bool DG, bool HALO, int WM, int WN, int KS, int U, int D>
+__global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv3_direct_kernel(Conv3Args c) {
+  conv3_direct_body<DG, HALO, WM, WN, KS, U, D>(c, c, blockIdx.x);
 }
 
 // Register-direct 1 x 1 convolution (stride 1, pad 0), forward and input
@@ -723,18 +740,12 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv3_direct_kernel(Conv
 // weights are one float4 per 16-row block (the dgrad's, strided by cin, four
 // dwords), S one float4 of pixels per channel.  cs % 4 == 0, so a group's
 // four channels are all inside or all past cs.
-template <bool DG, int WM, int WN, int KS, int D>
-__global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv1_direct_kernel(Conv3Args c) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int lr = lane & 15, q = lane >> 4;
-  const int wm = wave % WM, wn = (wave / WM) % WN, ks = wave / (WM * WN);
-  const int L = blockIdx.x, xq = c.tiles / 8, xr = c.tiles % 8, xc = L % 8;
-  const int item = xc * xq + min(xc, xr) + L / 8;
-  const int tm = item % c.tiles_m, tn = item / c.tiles_m;
-  const int m0 = (tm * WM + wm) * 64;
-  const int g = (tn * WN + wn) * 64 + 4 * lr;
-  const bool gok = g < c.npix;
-  const int b = g / c.hw, p = g - b * c.hw;
+// The K loop of the 1 x 1 kernel: channels of c.src (16 per stage, the
+// stages split over KS waves) into acc, for the wave's rows m0 .. m0 + 63
+// and the lane's pixels g .. g + 3 (g = image b, position p).
+template <bool DG, int KS, int D>
+__device__ __forceinline__ void conv1_kloop(f32x4 (&acc)[4][4], const Conv3Args& c, int m0, int lr, int q, int ks,
+                                            bool gok, int b, int p) {
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(c.src, c.src_bytes);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(c.wt, c.wt_bytes);
   const uint32_t b_base = (uint32_t)((b * c.cs + 4 * q) * c.hw + p) * 4u;
@@ -772,12 +783,6 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv1_direct_kernel(Conv
       fb[u] = __builtin_bit_cast(f32x4,
                                  __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(bo + (uint32_t)(u * c.hw) * 4u), 0, 0));
   };
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto mfma = [&](const f32x4(&fa)[4], const f32x4(&fb)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -789,14 +794,70 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv1_direct_kernel(Conv
   };
 
   f32x4 fa[D][4], fb[D][4];
-  if (!DG && KS == 1 && k1 - k0 <= D) {
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load(k0 + s, fa[s], fb[s]);
+  int kt = k0;
+  for (; kt + D - 1 < k1; kt += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      load(kt + s + D - 1, fa[(s + D - 1) % D], fb[(s + D - 1) % D]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma(fa[s], fb[s]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s)
+    if (kt + s < k1) mfma(fa[s], fb[s]);
+}
+
+// Register-direct 1 x 1 tile (see above); L is the workgroup's index among
+// this product's workgroups.
+template <bool DG, int WM, int WN, int KS, int D>
+__device__ __forceinline__ void conv1_direct_body(const Conv3Args& c, int L) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, q = lane >> 4;
+  const int wm = wave % WM, wn = (wave / WM) % WN, ks = wave / (WM * WN);
+  const int xq = c.tiles / 8, xr = c.tiles % 8, xc = L % 8;
+  const int item = xc * xq + min(xc, xr) + L / 8;
+  const int tm = item % c.tiles_m, tn = item / c.tiles_m;
+  const int m0 = (tm * WM + wm) * 64;
+  const int g = (tn * WN + wn) * 64 + 4 * lr;
+  const bool gok = g < c.npix;
+  const int b = g / c.hw, p = g - b * c.hw;
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nst = (c.cs + 15) / 16;
+  if (!DG && KS == 1 && nst <= D) {
     // Forward with every stage resident at once (cs <= 16 D): the 16-row
     // blocks finish one at a time, so a block's stores drain while the next
     // block's products run instead of all stores waiting for the last product.
-    // Each sum takes the stages and channels in the order of the loop below
-    // and adds the bias last, as conv_block_out does: the same bits.
+    // Each sum takes the stages and channels in the order of the K loop and
+    // adds the bias last, as conv_block_out does: the same bits.
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(c.src, c.src_bytes);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(c.wt, c.wt_bytes);
+    const uint32_t b_base = (uint32_t)((b * c.cs + 4 * q) * c.hw + p) * 4u;
+    f32x4 fa[D][4], fb[D][4];
 #pragma unroll
-    for (int s = 0; s < D; ++s) load(k0 + s, fa[s], fb[s]);
+    for (int s = 0; s < D; ++s) {
+      const bool cok = s < nst && s * 16 + 4 * q < c.cs;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = m0 + 16 * i + lr;
+        const uint32_t ao = (cok && row < c.M) ? (uint32_t)(row * c.a_rs + (s * 16 + 4 * q) * c.a_cs) * 4u : kOOB;
+        fa[s][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)ao, 0, 0));
+      }
+      const uint32_t bo = (cok & gok) ? b_base + (uint32_t)(s * 16 * c.hw) * 4u : kOOB;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        fb[s][u] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(bo + (uint32_t)(u * c.hw) * 4u), 0, 0));
+    }
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(c.bias, c.bias ? (uint32_t)c.M * 4u : 0u);
     float bv[4][4];
 #pragma unroll
@@ -808,7 +869,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv1_direct_kernel(Conv
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int s = 0; s < D; ++s)
-        if (k0 + s < k1)
+        if (s < nst)
 #pragma unroll
           for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -826,23 +887,38 @@ __global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv1_direct_kernel(Conv
     }
     return;
   }
-#pragma unroll
-  for (int s = 0; s < D - 1; ++s) load(k0 + s, fa[s], fb[s]);
-  int kt = k0;
-  for (; kt + D - 1 < k1; kt += D) {
-#pragma unroll
-    for (int s = 0; s < D; ++s) {
-      load(kt + s + D - 1, fa[(s + D - 1) % D], fb[(s + D - 1) % D]);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma(fa[s], fb[s]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < D - 1; ++s)
-    if (kt + s < k1) mfma(fa[s], fb[s]);
-
+  conv1_kloop<DG, KS, D>(acc, c, m0, lr, q, ks, gok, b, p);
   conv_block_out<DG, WM, WN, KS>(acc, c, m0, lane, wave, ks, gok, b, p);
+}
+
+template <bool DG, int WM, int WN, int KS, int D>
+__global__ __launch_bounds__(64 * WM * WN * KS, 2) void conv1_direct_kernel(Conv3Args c) {
+  conv1_direct_body<DG, WM, WN, KS, D>(c, blockIdx.x);
+}
+
+// Forward of a 3 x 3 (pad 1) and a 1 x 1 (pad 0) convolution of the same x
+// (a residual block's first convolution and its skip) in one grid: the 1 x 1
+// tiles first, then the 3 x 3 tiles, each product with its own XCD-aware
+// tile order.  Measured on the C5 shapes (16 x 64 -> 128 x 64 x 64):
+// 100.4 us against 109.4 us for the two launches.  The 3 x 3 tiles first ran
+// 104.5 us, each workgroup's 3 x 3 tile followed by the same pixels' 1 x 1
+// tile 103.6 us, and the two products alternating across the XCDs 154.7 us
+// (the 3 x 3 tiles slow down when they do not run in lockstep with their
+// neighbours).
+template <bool HALO, int WM3, int WM1>
+__global__ __launch_bounds__(256, 2) void conv_pair_fwd_kernel(Conv3Args a, Conv3Args b) {
+  const int L = blockIdx.x;
+  if (L < b.tiles)
+    conv1_direct_body<false, WM1, 2, WM1 == 1 ? 2 : 1, 4>(b, L);
+  else
+    conv3_direct_body<false, HALO, WM3, 2, WM3 == 1 ? 2 : 1, kC3U, kC3D>(a, a, L - b.tiles);
+}
+
+// Input gradient of the same pair: dx (+)= dgrad3(dy3) + dgrad1(dy1), the
+// 1 x 1 product as extra stages of each 3 x 3 tile.
+template <bool HALO, int WM>
+__global__ __launch_bounds__(256, 2) void conv_pair_dgrad_kernel(Conv3Args a, Conv3Args b) {
+  conv3_direct_body<true, HALO, WM, 2, WM == 1 ? 2 : 1, kC3U, kC3D, true>(a, b, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1198,7 +1274,6 @@ __global__ __launch_bounds__(256, 2) void conv1_wgrad_kernel(Wgrad3Args c) {
 bool fits_2g(double elems) { return elems * 4.0 < 2147483647.0; }
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-constexpr int kC3U = 2, kC3D = 4;  // channel quads per stage, stages in flight
 
 // 64-row blocks (M <= 64) split each block's stages over two waves, so the
 // grid still holds two waves per SIMD.
@@ -1214,13 +1289,14 @@ void launch_conv1(hipStream_t s, const Conv3Args& c) {
   mle::launch(conv1_direct_kernel<DG, WM, 2, KS, 4>, c.tiles, 64 * WM * 2 * KS, 0, s, c);
 }
 
-// Register-direct path for a 3 x 3 (stride 1, pad 1) or 1 x 1 (stride 1,
-// pad 0) forward (dg = 0: src = x, M = cout) or input gradient (dg = 1:
-// src = dy, M = cin).  Returns false, launching nothing, when the shape is
-// outside what the kernels assume.
-bool conv_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, const float* wt, const float* bias,
-                 float* out, int acc) {
-  const bool k3 = g.kh == 3 && g.kw == 3 && g.pad == 1 && g.stride == 1 && g.w % 4 == 0;
+// Arguments of the register-direct kernels for a 3 x 3 (stride 1, pad 1) or
+// 1 x 1 (stride 1, pad 0) forward (dg = 0: src = x, M = cout) or input
+// gradient (dg = 1: src = dy, M = cin).  Returns false when the shape is
+// outside what the kernels assume; k3 tells which filter, wm the row blocks
+// per workgroup, halo whether 64 pixels span a partial image row.
+bool direct_args(bool dg, const ConvGeom& g, const float* src, const float* wt, const float* bias, float* out,
+                 int acc, Conv3Args& c, bool& k3, int& wm, bool& halo) {
+  k3 = g.kh == 3 && g.kw == 3 && g.pad == 1 && g.stride == 1 && g.w % 4 == 0;
   const bool k1 = g.kh == 1 && g.kw == 1 && g.pad == 0 && g.stride == 1 && (g.h * g.w) % 4 == 0;
   if (!k3 && !k1) return false;
   const int M = dg ? g.cin : g.cout, cs = dg ? g.cout : g.cin;
@@ -1232,7 +1308,7 @@ bool conv_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, co
   if ((double)g.n * cs * hw * 4.0 >= 2147483647.0 || (double)g.n * M * hw * 4.0 >= 2147483647.0 ||
       (double)g.cout * g.cin * taps * 4.0 >= 1073741824.0)
     return false;
-  Conv3Args c{};
+  c = Conv3Args{};
   c.src = src;
   c.wt = wt;
   c.bias = dg ? nullptr : bias;
@@ -1249,15 +1325,26 @@ bool conv_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, co
   c.a_rs = dg ? taps : g.cin * taps;
   c.a_cs = dg ? g.cin * taps : taps;
   c.acc = acc;
-  const int wm = M <= 64 ? 1 : 2;
+  wm = M <= 64 ? 1 : 2;
   c.tiles_m = (M + 64 * wm - 1) / (64 * wm);
   c.tiles = c.tiles_m * ((c.npix + 127) / 128);
-  if (k1) {
+  halo = k3 && 64 % g.w != 0;
+  return true;
+}
+
+// Register-direct path for one convolution (see direct_args).  Returns false,
+// launching nothing, when the shape is outside what the kernels assume.
+bool conv_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, const float* wt, const float* bias,
+                 float* out, int acc) {
+  Conv3Args c;
+  bool k3, halo;
+  int wm;
+  if (!direct_args(dg, g, src, wt, bias, out, acc, c, k3, wm, halo)) return false;
+  if (!k3) {
     if (dg) wm == 1 ? launch_conv1<true, 1>(s, c) : launch_conv1<true, 2>(s, c);
     else wm == 1 ? launch_conv1<false, 1>(s, c) : launch_conv1<false, 2>(s, c);
     return true;
   }
-  const bool halo = 64 % g.w != 0;
   if (dg) {
     if (halo) wm == 1 ? launch_conv3<true, true, 1>(s, c) : launch_conv3<true, true, 2>(s, c);
     else wm == 1 ? launch_conv3<true, false, 1>(s, c) : launch_conv3<true, false, 2>(s, c);
@@ -1266,6 +1353,28 @@ bool conv_direct(hipStream_t s, bool dg, const ConvGeom& g, const float* src, co
     else wm == 1 ? launch_conv3<false, false, 1>(s, c) : launch_conv3<false, false, 2>(s, c);
   }
   return true;
+}
+
+int geom(int n, int cin, int h, int w, int cout, int kh, int kw, int pad, int stride, ConvGeom& g);
+
+// The geometries of a 3 x 3 (pad 1) and a 1 x 1 (pad 0) convolution, stride
+// 1, of one input [n][cin][h][w], with cout3 and cout1 output channels.
+bool pair_geoms(int n, int cin, int h, int w, int cout3, int cout1, ConvGeom& g3, ConvGeom& g1) {
+  if (geom(n, cin, h, w, cout3, 3, 3, 1, 1, g3) != MLE_OK) return false;
+  if (geom(n, cin, h, w, cout1, 1, 1, 0, 1, g1) != MLE_OK) return false;
+  return true;
+}
+
+template <bool HALO>
+void launch_pair_fwd(hipStream_t s, const Conv3Args& a, int wma, const Conv3Args& b, int wmb) {
+  const unsigned grid = (unsigned)(a.tiles + b.tiles);
+  if (wma == 1) {
+    if (wmb == 1) mle::launch(conv_pair_fwd_kernel<HALO, 1, 1>, grid, 256, 0, s, a, b);
+    else mle::launch(conv_pair_fwd_kernel<HALO, 1, 2>, grid, 256, 0, s, a, b);
+  } else {
+    if (wmb == 1) mle::launch(conv_pair_fwd_kernel<HALO, 2, 1>, grid, 256, 0, s, a, b);
+    else mle::launch(conv_pair_fwd_kernel<HALO, 2, 2>, grid, 256, 0, s, a, b);
+  }
 }
 
 template <int KIND>
@@ -1521,6 +1630,69 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
     if (rc != MLE_OK) return rc;
   }
   return mle_channel_sum(stream, dy, n, cout, (size_t)g.oh * g.ow, cout, db);
+}
+
+
+// ---- a 3 x 3 and a 1 x 1 convolution of one input, in one launch ----------
+// (a residual block's first convolution and its skip; both stride 1)
+
+// Arguments of both products for the paired forward (dg = 0) or input
+// gradient (dg = 1); false when either is outside the direct kernels.
+static bool pair_args(bool dg, int n, int cin, int h, int w, int cout3, int cout1, const float* s3, const float* w3,
+                      const float* b3, float* o3, const float* s1, const float* w1, const float* b1, float* o1,
+                      int acc, Conv3Args& a, Conv3Args& b, int& wma, int& wmb, bool& halo) {
+  ConvGeom g3, g1;
+  if (!pair_geoms(n, cin, h, w, cout3, cout1, g3, g1)) return false;
+  bool k3a, k3b, hb;
+  if (!direct_args(dg, g3, s3, w3, b3, o3, acc, a, k3a, wma, halo) || !k3a) return false;
+  if (!direct_args(dg, g1, s1, w1, b1, o1, acc, b, k3b, wmb, hb) || k3b) return false;
+  return true;
+}
+
+int mle_conv2d_pair_supported(int n, int cin, int h, int w, int cout3, int cout1) {
+  Conv3Args a, b;
+  int wma, wmb;
+  bool halo;
+  float* const al = reinterpret_cast<float*>(256);  // any 16-byte aligned address: only the shapes are checked
+  const bool fwd = pair_args(false, n, cin, h, w, cout3, cout1, al, al, nullptr, al, al, al, nullptr, al, 0, a, b, wma,
+                             wmb, halo);
+  const bool dg = pair_args(true, n, cin, h, w, cout3, cout1, al, al, nullptr, al, al, al, nullptr, al, 0, a, b, wma,
+                            wmb, halo);
+  return fwd && dg ? 1 : 0;
+}
+
+int mle_conv2d_pair_fwd(mle_stream stream, const float* x, int n, int cin, int h, int w, const float* w3,
+                        const float* b3, float* y3, int cout3, const float* w1, const float* b1, float* y1, int cout1) {
+  MLE_CHECK_ARG(x && w3 && y3 && w1 && y1, "mle_conv2d_pair_fwd: null pointer");
+  Conv3Args a, b;
+  int wma, wmb;
+  bool halo;
+  if (!pair_args(false, n, cin, h, w, cout3, cout1, x, w3, b3, y3, x, w1, b1, y1, 0, a, b, wma, wmb, halo))
+    return set_error(MLE_ERR_UNSUPPORTED, "mle_conv2d_pair_fwd: shape outside the direct kernels");
+  hipStream_t s = as_stream(stream);
+  const double flop = 2.0 * (double)n * h * w * cin * (9.0 * cout3 + cout1);
+  ProbeScope probe("conv_fwd", s, flop, 0.0);
+  if (halo) launch_pair_fwd<true>(s, a, wma, b, wmb);
+  else launch_pair_fwd<false>(s, a, wma, b, wmb);
+  return check_launch("mle_conv2d_pair_fwd");
+}
+
+int mle_conv2d_pair_dgrad(mle_stream stream, float* dx, int accumulate, int n, int cin, int h, int w,
+                          const float* dy3, const float* w3, int cout3, const float* dy1, const float* w1, int cout1) {
+  MLE_CHECK_ARG(dx && dy3 && w3 && dy1 && w1, "mle_conv2d_pair_dgrad: null pointer");
+  Conv3Args a, b;
+  int wma, wmb;
+  bool halo;
+  if (!pair_args(true, n, cin, h, w, cout3, cout1, dy3, w3, nullptr, dx, dy1, w1, nullptr, dx, accumulate != 0, a, b,
+                 wma, wmb, halo))
+    return set_error(MLE_ERR_UNSUPPORTED, "mle_conv2d_pair_dgrad: shape outside the direct kernels");
+  hipStream_t s = as_stream(stream);
+  const double flop = 2.0 * (double)n * h * w * cin * (9.0 * cout3 + cout1);
+  ProbeScope probe("conv_dgrad", s, flop, 0.0);
+  auto k = halo ? (wma == 1 ? conv_pair_dgrad_kernel<true, 1> : conv_pair_dgrad_kernel<true, 2>)
+                : (wma == 1 ? conv_pair_dgrad_kernel<false, 1> : conv_pair_dgrad_kernel<false, 2>);
+  mle::launch(k, (unsigned)a.tiles, 256, 0, s, a, b);
+  return check_launch("mle_conv2d_pair_dgrad");
 }
 
 }  // extern "C"

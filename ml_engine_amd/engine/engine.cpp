@@ -1145,12 +1145,15 @@ graph Convolute2D::forward(const graph& X) {
                          pad_, st),
           "Forward Convolution in " + nm);
   };
-  node->backward = [=]() {
+  node->backward_params = [=]() {
     // dW (assigned) and db += channel sums of dZ in one launch.
     W->grad_pending_zero = false;  // the weight gradient is assigned whole (GV2D)
     check(mle_conv2d_wgrad_bias(mle::stream(), x->output, nd->grad, W->grad, Bb->grad, mle::params_write_flag({Bb}),
                                 batch, inp_, a, b, out_, c_, d_, pad_, st, ws, ws_bytes),
           "Weight and Bias Gradient in " + nm);
+  };
+  node->backward = [=]() {
+    nd->backward_params();
     check(mle_conv2d_dgrad(mle::stream(), nd->grad, W->output, x->grad, batch, inp_, a, b, out_, c_, d_, pad_, st,
                            mle::accumulate_flag(x)),
           "Input Gradient in " + nm);
@@ -1177,6 +1180,54 @@ graph Convolute2D::forward(const graph& X) {
   node->printparams = [=](const bool) {};
   return node;
 }
+
+namespace mle {
+
+bool fuse_conv_pair(const graph& y3, const Convolute2D& c3, const graph& y1, const Convolute2D& c1) {
+  if (!fusion_enabled() || !y3 || !y1 || y3 == y1) return false;
+  if (y3->inputs.size() != 1 || y1->inputs.size() != 1 || y3->inputs[0] != y1->inputs[0]) return false;
+  if (c3.c != 3 || c3.d != 3 || c3.pad != 1 || c3.stride != 1) return false;
+  if (c1.c != 1 || c1.d != 1 || c1.pad != 0 || c1.stride != 1) return false;
+  if (!y3->backward_params || !y1->backward_params) return false;
+  NodeBackProp* x = y3->inputs[0].get();
+  const int n = x->dim[0], cin = x->dim[1], h = x->dim[2], w = x->dim[3];
+  const int cout3 = c3.out, cout1 = c1.out;
+  if (c3.inp != cin || c1.inp != cin) return false;
+  if (!mle_conv2d_pair_supported(n, cin, h, w, cout3, cout1)) return false;
+  NodeBackProp *o3 = y3.get(), *o1 = y1.get();
+  const AdamParameter *W3 = &c3.W1, *B3 = &c3.B1, *W1 = &c1.W1, *B1 = &c1.B1;
+  const str name = c3.name + " + " + c1.name;
+  auto fwd_count = std::make_shared<int>(0);
+  auto bwd_count = std::make_shared<int>(0);
+  auto forward = [=]() {
+    if ((*fwd_count)++ == 0)
+      check(mle_conv2d_pair_fwd(stream(), x->output, n, cin, h, w, W3->output, B3->output, o3->output, cout3,
+                                W1->output, B1->output, o1->output, cout1),
+            "Forward Convolutions in " + name);
+    if (*fwd_count == 2) *fwd_count = 0;
+  };
+  y3->forward = forward;
+  y1->forward = forward;
+  auto backward = [=](NodeBackProp* self) {
+    return [=]() {
+      self->backward_params();
+      if (++(*bwd_count) < 2) return;
+      *bwd_count = 0;
+      // Both output gradients are complete: the first node's was read by its
+      // parameter half already, and neither has another writer.
+      materialize(o3);
+      materialize(o1);
+      check(mle_conv2d_pair_dgrad(stream(), x->grad, accumulate_flag(x), n, cin, h, w, o3->grad, W3->output, cout3,
+                                  o1->grad, W1->output, cout1),
+            "Input Gradient in " + name);
+    };
+  };
+  y3->backward = backward(o3);
+  y1->backward = backward(o1);
+  return true;
+}
+
+}  // namespace mle
 
 // ---------------------------------------------------------------------------
 // Convolute2DT (Engine/engine.cu:3819-3900).  W1 [out, inp, c, d], B1 [1, out, 1, 1].

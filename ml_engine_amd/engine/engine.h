@@ -215,6 +215,9 @@ struct NodeBackProp {
   // forward does and also act(output) into act_out, in the same pass.  An
   // activation node on this output takes over the forward with it.
   std::function<void(int kind, float* act_out)> forward_act;
+  // Convolute2D: the parameter half of its backward (dW assigned, db added),
+  // so a fused input gradient (mle::fuse_conv_pair) can take the other half.
+  std::function<void()> backward_params;
   // Backward hand-off (additive): an activation whose input is this node, and
   // which is this node's only consumer, leaves its gradient here instead of
   // forming this node's gradient; this node's backward forms it (kind, and
@@ -414,6 +417,21 @@ class Convolute2D {
   void load(std::ifstream& f);
   graph forward(const graph& X);
 };
+
+// A 3 x 3 (pad 1) and a 1 x 1 (pad 0) convolution, both stride 1, of the same
+// input (a residual block's first convolution and its skip).  `y3` and `y1`
+// are their forward nodes.  When the shapes run on the paired kernels the
+// nodes' lambdas are rewired:
+//  * forward: whichever runs first in a pass computes both outputs in one
+//    launch (mle_conv2d_pair_fwd; the same bits as two launches);
+//  * backward: each keeps its own weight and bias gradients; the second to
+//    run computes the input gradient of both, dx (+)= dgrad3(dY3) +
+//    dgrad1(dY1), in one launch (mle_conv2d_pair_dgrad).
+// Both nodes must be evaluated in every pass, as the residual block's are.
+// Returns false (and changes nothing) otherwise.
+namespace mle {
+bool fuse_conv_pair(const graph& y3, const Convolute2D& c3, const graph& y1, const Convolute2D& c1);
+}  // namespace mle
 
 // Transposed convolution (Includes/engine.h:257-280, Engine/engine.cu:3819-3900):
 // W1 [out, inp, c, d], B1 [1, out, 1, 1]; output (H - 1) * stride - 2 pad + c.

@@ -80,10 +80,13 @@ void ResidualBlock::load(std::ifstream& f) {
 }
 
 graph ResidualBlock::forward(const graph& x, const graph& t_emb) {
-  auto h = GraphOperations::SILU(GraphOperations::GroupNorm(conv1->forward(x), groups));
+  auto c1 = conv1->forward(x);
+  auto h = GraphOperations::SILU(GraphOperations::GroupNorm(c1, groups));
   auto time = time_mlp->forward(t_emb);
   h = GraphOperations::Broadcast_Channel(h, time);
   h = GraphOperations::GroupNorm(conv2->forward(h), groups);
   auto skipnet = (in != out || stride != 1) ? skipconv->forward(x) : x;
+  // conv1 and the skip convolution read the same x: one launch each way
+  if (skipnet != x) mle::fuse_conv_pair(c1, *conv1, skipnet, *skipconv);
   return GraphOperations::SILU(GraphOperations::Add(h, skipnet));
 }

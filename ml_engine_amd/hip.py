@@ -118,6 +118,9 @@ SIGNATURES: dict[str, tuple] = {
     "mle_conv2d_wgrad_ws_bytes": (SZ, [I, I, I, I, I, I, I, I, I]),
     "mle_conv2d_wgrad": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, P, SZ]),
     "mle_conv2d_wgrad_bias": (I, [P, P, P, P, P, I, I, I, I, I, I, I, I, I, I, P, SZ]),
+    "mle_conv2d_pair_supported": (I, [I, I, I, I, I, I]),
+    "mle_conv2d_pair_fwd": (I, [P, P, I, I, I, I, P, P, P, I, P, P, P, I]),
+    "mle_conv2d_pair_dgrad": (I, [P, P, I, I, I, I, I, P, P, I, P, P, I]),
     "mle_sqnorm_ws_bytes": (SZ, [SZ]),
     "mle_grad_sqnorm": (I, [P, P, SZ, P, P, P, SZ]),
     "mle_sqrt_scale": (I, [P, P, D]),

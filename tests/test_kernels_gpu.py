@@ -874,6 +874,60 @@ def test_conv_transpose_composition(hip, orc, n, cin, h, w, cout, k, pad, stride
     assert_close(gdw.numpy(), dwr, what="convT weight gradient", **MM)
 
 
+# ------------------------------------------- paired 3 x 3 + 1 x 1 convolution
+@pytest.mark.parametrize("n,cin,h,w,cout3,cout1", [
+    (2, 64, 64, 64, 128, 128),   # the C5 residual block's conv1 + skip at batch 2
+    (2, 8, 12, 12, 16, 16),      # W not dividing 64: the 3 x 3 halo loads
+    (3, 16, 8, 8, 32, 48),       # M <= 64 row blocks, images straddling a tile
+    (2, 128, 16, 16, 64, 128),   # 128 input channels: dgrad row blocks of 128
+    (1, 24, 20, 20, 136, 72),    # rows past M, uneven tile counts (not multiples of 8)
+])
+def test_conv_pair(hip, orc, n, cin, h, w, cout3, cout1):
+    """A 3 x 3 (pad 1) and a 1 x 1 (pad 0) convolution of one input in one
+    launch: both forwards (with biases), and the input gradient
+    dx (+)= dgrad3(dy3) + dgrad1(dy1) with the 1 x 1 product as extra K stages
+    of the 3 x 3 tiles, assigning and adding, against the oracle's separate
+    CV2D / CV2D_GradInput passes."""
+    r = rng(n + cin + h + cout3 + cout1)
+    L = hip.lib()
+    assert L.mle_conv2d_pair_supported(n, cin, h, w, cout3, cout1) == 1
+    x = r.standard_normal((n, cin, h, w), dtype=np.float32)
+    w3 = r.standard_normal((cout3, cin, 3, 3), dtype=np.float32)
+    b3 = r.standard_normal(cout3, dtype=np.float32)
+    w1 = r.standard_normal((cout1, cin, 1, 1), dtype=np.float32)
+    b1 = r.standard_normal(cout1, dtype=np.float32)
+    dy3 = r.standard_normal((n, cout3, h, w), dtype=np.float32)
+    dy1 = r.standard_normal((n, cout1, h, w), dtype=np.float32)
+    dx0 = r.standard_normal(x.shape, dtype=np.float32)
+    y3r, y1r = np.zeros((n, cout3, h, w), np.float32), np.zeros((n, cout1, h, w), np.float32)
+    orc.call("orc_conv_fwd", orc.ptr(x), orc.ptr(w3), orc.ptr(b3), orc.ptr(y3r), n, cin, h, w, cout3, 3, 3, 1, 1)
+    orc.call("orc_conv_fwd", orc.ptr(x), orc.ptr(w1), orc.ptr(b1), orc.ptr(y1r), n, cin, h, w, cout1, 1, 1, 0, 1)
+    gx, gw3, gb3, gw1, gb1 = B(hip, x), B(hip, w3), B(hip, b3), B(hip, w1), B(hip, b1)
+    gy3 = B(hip, np.full(y3r.shape, np.nan, np.float32))
+    gy1 = B(hip, np.full(y1r.shape, np.nan, np.float32))
+    hip.call("mle_conv2d_pair_fwd", None, gx.ptr, n, cin, h, w, gw3.ptr, gb3.ptr, gy3.ptr, cout3, gw1.ptr, gb1.ptr,
+             gy1.ptr, cout1)
+    assert_close(gy3.numpy(), y3r, what="pair fwd 3x3", **MM)
+    assert_close(gy1.numpy(), y1r, what="pair fwd 1x1", **MM)
+    # the same bits as the per-convolution launches
+    gs3, gs1 = hip.Buffer.zeros(y3r.shape), hip.Buffer.zeros(y1r.shape)
+    hip.call("mle_conv2d_fwd", None, gx.ptr, gw3.ptr, gb3.ptr, gs3.ptr, n, cin, h, w, cout3, 3, 3, 1, 1)
+    hip.call("mle_conv2d_fwd", None, gx.ptr, gw1.ptr, gb1.ptr, gs1.ptr, n, cin, h, w, cout1, 1, 1, 0, 1)
+    np.testing.assert_array_equal(gy3.numpy(), gs3.numpy())
+    np.testing.assert_array_equal(gy1.numpy(), gs1.numpy())
+    gdy3, gdy1 = B(hip, dy3), B(hip, dy1)
+    for acc in (1, 0):
+        dxr = dx0.copy() if acc else np.zeros_like(x)
+        orc.call("orc_conv_dgrad", orc.ptr(dy3), orc.ptr(w3), orc.ptr(dxr), n, cin, h, w, cout3, 3, 3, 1, 1)
+        orc.call("orc_conv_dgrad", orc.ptr(dy1), orc.ptr(w1), orc.ptr(dxr), n, cin, h, w, cout1, 1, 1, 0, 1)
+        gdx = B(hip, dx0 if acc else np.full(x.shape, np.nan, np.float32))
+        hip.call("mle_conv2d_pair_dgrad", None, gdx.ptr, acc, n, cin, h, w, gdy3.ptr, gw3.ptr, cout3, gdy1.ptr, gw1.ptr,
+                 cout1)
+        assert_close(gdx.numpy(), dxr, what=f"pair dgrad acc={acc}", **MM)
+    # shapes off the direct kernels are refused, not computed elsewhere
+    assert L.mle_conv2d_pair_supported(n, cin, h, w + 1, cout3, cout1) == 0
+
+
 # ---------------------------------------------------------------------- conv
 @pytest.mark.parametrize("n,cin,h,w,cout,k,pad,stride", [
     (2, 3, 9, 9, 5, 3, 1, 1), (2, 4, 8, 10, 6, 1, 0, 1), (1, 3, 11, 11, 4, 3, 1, 2),
