@@ -161,16 +161,39 @@ void set_lazy_zero(bool on) { g_lazy_zero = on; }
 
 void defer_zero(NodeBackProp* n) {
   if (!n || !n->grad || n->total <= 0) return;
+  n->grad_src = nullptr;
   if (g_lazy_zero) n->grad_pending_zero = true;
   else zero(n->grad, n->total);
 }
 
 int accumulate_flag(NodeBackProp* n) {
+  resolve_alias(n);
   if (n->grad_pending_zero) {
     n->grad_pending_zero = false;
     return 0;
   }
   return 1;
+}
+
+const float* grad_of(const NodeBackProp* n) { return n->grad_src ? n->grad_src : n->grad; }
+
+bool can_alias_grad(const NodeBackProp* in, const NodeBackProp* from) {
+  if (!g_lazy_zero || !fusion_enabled() || !in || !from || in == from || !in->reads_grad_alias) return false;
+  return in->grad_pending_zero && !in->grad_src && in->consumers == 1 && in->total == from->total;
+}
+
+bool alias_grad(NodeBackProp* in, const NodeBackProp* from) {
+  if (!can_alias_grad(in, from)) return false;
+  in->grad_src = grad_of(from);
+  in->grad_pending_zero = false;  // its gradient is defined: the alias's content
+  return true;
+}
+
+void resolve_alias(NodeBackProp* n) {
+  if (!n || !n->grad_src) return;
+  const float* src = n->grad_src;
+  n->grad_src = nullptr;
+  check(mle_scale_assign(stream(), src, n->grad, 1.0, n->total), "gradient of " + n->op_name);
 }
 
 int params_write_flag(const std::vector<NodeBackProp*>& ps) {
@@ -200,6 +223,7 @@ void materialize_params(const std::vector<AdamParameter*>& ps) {
 
 void materialize(NodeBackProp* n) {
   if (!n) return;
+  resolve_alias(n);
   clip_apply(n);
   if (!n->grad_pending_zero) return;
   n->grad_pending_zero = false;
@@ -537,6 +561,7 @@ void Zerograd(const AdamParameter& X) {
 }
 void Zerograd(graph X) {
   mle::clip_drop(X.get());
+  X->grad_src = nullptr;
   mle::zero(X->grad, X->total);
   X->grad_pending_zero = false;
 }
@@ -803,6 +828,9 @@ void GraphOperations::backward(const graph& X, const bool show, const bool time,
     return;
   }
   mle::clip_apply_all();  // parameter gradients are added into: give them their clipped values
+  // An alias left by a pass without zero_grad since: its source is added into
+  // below, so the node keeps its own copy.
+  for (auto& n : nodes) mle::resolve_alias(n.get());
   for (auto& n : nodes) n->consumers = n->consumers_done = 0;
   for (auto& n : nodes)
     for (auto& in : n->inputs)
@@ -814,9 +842,10 @@ void GraphOperations::backward(const graph& X, const bool show, const bool time,
       t0 = std::chrono::high_resolution_clock::now();
     }
     if ((*it)->backward) {
-      // The node reads its own gradient; a backward that does not know about
-      // lazy clearing may add into its inputs' gradients.
-      mle::materialize(it->get());
+      // The node reads its own gradient (through an alias, when it can); a
+      // backward that does not know about lazy clearing may add into its
+      // inputs' gradients.
+      if (!(*it)->reads_grad_alias || !(*it)->grad_src) mle::materialize(it->get());
       if (!(*it)->lazy_grad_writer)
         for (auto& in : (*it)->inputs) mle::materialize(in.get());
       (*it)->backward();
@@ -925,6 +954,7 @@ graph Linear::forward(const graph& X) {
   const int batch = X->dim[0], channels = X->dim[1], m = X->dim[2], n = X->dim[3], p = out;
   auto node = std::make_shared<NodeBackProp>(op_name, batch, channels, m, p, 1);
   node->lazy_grad_writer = true;
+  node->reads_grad_alias = true;
   node->inputs = {X};
   GraphOperations::GB += (double)node->total * sizeof(float) / (1ULL << 30);
   const long long rows = (long long)batch * channels * m;
@@ -952,7 +982,7 @@ graph Linear::forward(const graph& X) {
   };
   node->backward = [=]() {
     // dX (+)= dZ W^T, dW += X^T dZ, db += colsum dZ (one launch when they fit).
-    check(mle_linear_bwd_ex(mle::stream(), (int)rows, n, p, 1, x->output, nd->grad, 0, W->output, 0, x->grad,
+    check(mle_linear_bwd_ex(mle::stream(), (int)rows, n, p, 1, x->output, mle::grad_of(nd), 0, W->output, 0, x->grad,
                             mle::accumulate_flag(x), W->grad, has_bias ? Bb->grad : nullptr, 0,
                             mle::params_write_flag({W, has_bias ? Bb : nullptr}), ws, ws_bytes),
           "MatMul... dZ*W^T and X^T*dZ in " + name + " backward");
@@ -1065,6 +1095,8 @@ bool fuse_sibling_linears(const std::vector<graph>& outs, const std::vector<Line
   auto bwd_count = std::make_shared<int>(0);
   const str name = outs[0]->op_name;
   for (size_t i = 0; i < n; ++i) {
+    // The batched backward reads the gradients at one stride: never aliased.
+    outs[i]->reads_grad_alias = false;
     // Forward: the first sibling of a pass computes Y_i = X W_i + b_i for all
     // (X broadcast, weights, biases and outputs strided).
     outs[i]->forward_rowstats = nullptr;
@@ -1129,6 +1161,7 @@ graph Convolute2D::forward(const graph& X) {
   const int outR = (2 * pad + a - c) / stride + 1, outC = (2 * pad + b - d) / stride + 1;
   auto node = std::make_shared<NodeBackProp>(name, batch, out, outR, outC, 1);
   node->lazy_grad_writer = true;
+  node->reads_grad_alias = true;
   node->inputs = {X};
   GraphOperations::GB += (double)node->total * sizeof(float) / (1ULL << 30);
   const size_t ws_bytes = mle_conv2d_wgrad_ws_bytes(batch, inp, a, b, out, c, d, pad, stride);
@@ -1148,14 +1181,14 @@ graph Convolute2D::forward(const graph& X) {
   node->backward_params = [=]() {
     // dW (assigned) and db += channel sums of dZ in one launch.
     W->grad_pending_zero = false;  // the weight gradient is assigned whole (GV2D)
-    check(mle_conv2d_wgrad_bias(mle::stream(), x->output, nd->grad, W->grad, Bb->grad, mle::params_write_flag({Bb}),
-                                batch, inp_, a, b, out_, c_, d_, pad_, st, ws, ws_bytes),
+    check(mle_conv2d_wgrad_bias(mle::stream(), x->output, mle::grad_of(nd), W->grad, Bb->grad,
+                                mle::params_write_flag({Bb}), batch, inp_, a, b, out_, c_, d_, pad_, st, ws, ws_bytes),
           "Weight and Bias Gradient in " + nm);
   };
   node->backward = [=]() {
     nd->backward_params();
-    check(mle_conv2d_dgrad(mle::stream(), nd->grad, W->output, x->grad, batch, inp_, a, b, out_, c_, d_, pad_, st,
-                           mle::accumulate_flag(x)),
+    check(mle_conv2d_dgrad(mle::stream(), mle::grad_of(nd), W->output, x->grad, batch, inp_, a, b, out_, c_, d_, pad_,
+                           st, mle::accumulate_flag(x)),
           "Input Gradient in " + nm);
   };
   node->zero_grad = [=]() {
@@ -1213,12 +1246,11 @@ bool fuse_conv_pair(const graph& y3, const Convolute2D& c3, const graph& y1, con
       self->backward_params();
       if (++(*bwd_count) < 2) return;
       *bwd_count = 0;
-      // Both output gradients are complete: the first node's was read by its
-      // parameter half already, and neither has another writer.
-      materialize(o3);
-      materialize(o1);
-      check(mle_conv2d_pair_dgrad(stream(), x->grad, accumulate_flag(x), n, cin, h, w, o3->grad, W3->output, cout3,
-                                  o1->grad, W1->output, cout1),
+      // Both output gradients are complete (each was made readable, possibly
+      // as an alias, before its node's backward) and neither has another
+      // writer.
+      check(mle_conv2d_pair_dgrad(stream(), x->grad, accumulate_flag(x), n, cin, h, w, grad_of(o3), W3->output, cout3,
+                                  grad_of(o1), W1->output, cout1),
             "Input Gradient in " + name);
     };
   };

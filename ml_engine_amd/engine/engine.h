@@ -89,6 +89,14 @@ struct ZeroBatch {
 // writes only part of it, calls materialize() first, which fills it.
 void defer_zero(NodeBackProp* n);
 int accumulate_flag(NodeBackProp* n);
+// The buffer holding n's gradient: grad_src when aliased, else grad.
+const float* grad_of(const NodeBackProp* n);
+// Alias `in`'s gradient to `from`'s (see NodeBackProp::grad_src) when the
+// rules allow; returns whether it did (else the caller writes as usual).
+bool alias_grad(NodeBackProp* in, const NodeBackProp* from);
+bool can_alias_grad(const NodeBackProp* in, const NodeBackProp* from);  // alias_grad's test, without the alias
+// Copy an aliased gradient into the node's own buffer and drop the alias.
+void resolve_alias(NodeBackProp* n);
 void materialize(NodeBackProp* n);
 // Parameter gradients are cleared the same way.  A backward that writes the
 // gradients of `ps` whole in one launch asks params_write_flag for its mode:
@@ -215,6 +223,16 @@ struct NodeBackProp {
   // forward does and also act(output) into act_out, in the same pass.  An
   // activation node on this output takes over the forward with it.
   std::function<void(int kind, float* act_out)> forward_act;
+  // Gradient alias: when set, this node's gradient is the content of
+  // grad_src, a consumer's gradient buffer that nothing writes again before
+  // the next zero_grad, and `grad` is stale.  A pass-through backward (Add,
+  // Broadcast_Channel) sets it instead of copying its gradient into an input
+  // whose grad is clear, whose only consumer it is, and whose backward reads
+  // through mle::grad_of (reads_grad_alias).  Anything else that reads or
+  // adds into the gradient copies it over first (mle::materialize,
+  // mle::accumulate_flag); zero_grad and each backward pass's start drop it.
+  const float* grad_src = nullptr;
+  bool reads_grad_alias = false;
   // Convolute2D: the parameter half of its backward (dW assigned, db added),
   // so a fused input gradient (mle::fuse_conv_pair) can take the other half.
   std::function<void()> backward_params;

@@ -322,6 +322,12 @@ int mle_model_step_graph(void* h, float lr, int mode) {
     // Record the pass once.  Its host side runs now (the lazy-clearing marks
     // and every other host decision end as after one step, and are the same
     // for every step of this mode); its kernels run on each replay.
+    // A one-time state change would be recorded and then repeated by every
+    // replay: gradient aliases left by the previous pass (each backward pass
+    // copies those over at its start) and a pending clip are applied now,
+    // outside the recording.
+    for (auto& n : m->go.nodes) mle::resolve_alias(n.get());
+    mle::clip_apply_all();
     unsigned issued0 = 0, issued1 = 0;
     rc = mle_scalar_state(nullptr, nullptr, &issued0);
     if (rc) return rc;
@@ -389,6 +395,25 @@ void* mle_model_stream(void* h) {
 }
 
 int mle_model_num_nodes(void* h) { return (int)static_cast<Model*>(h)->go.nodes.size(); }
+
+long long mle_model_node_numel(void* h, int i) {
+  auto* m = static_cast<Model*>(h);
+  if (i < 0 || i >= (int)m->go.nodes.size()) return -1;
+  return m->go.nodes[i]->total;
+}
+
+// Node i (topological order) read the way ReadValueAt / printGPU read it:
+// which 0 = output, 1 = gradient (a clear or aliased gradient is made
+// current first).
+int mle_model_node_read(void* h, int i, int which, float* host, size_t count) {
+  auto* m = static_cast<Model*>(h);
+  if (i < 0 || i >= (int)m->go.nodes.size() || !host) return MLE_ERR_INVALID;
+  NodeBackProp* n = m->go.nodes[i].get();
+  if (count > (size_t)n->total || !(which ? n->grad : n->output)) return MLE_ERR_INVALID;
+  if (which) mle::materialize(n);
+  else mle::materialize_output(n);
+  return mle_memcpy_d2h(host, which ? n->grad : n->output, count * sizeof(float), mle::stream());
+}
 
 // Checkpoints: every parameter's AdamParameter record, in the model's
 // parameter order (the modules' save order, e.g. Linear: W1 then B1).

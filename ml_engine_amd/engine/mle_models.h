@@ -66,6 +66,11 @@ int mle_model_target_read(void* h, float* host, size_t count);
 int mle_model_sync(void* h);
 void* mle_model_stream(void* h);
 int mle_model_num_nodes(void* h);
+/* Node i of the topological order: its element count, and the first `count`
+ * floats of its output (which 0) or gradient (which 1), read the way
+ * ReadValueAt reads them. */
+long long mle_model_node_numel(void* h, int i);
+int mle_model_node_read(void* h, int i, int which, float* host, size_t count);
 /* Checkpoint of every parameter (AdamParameter::save records, parameter order). */
 int mle_model_save(void* h, const char* path);
 int mle_model_load(void* h, const char* path);

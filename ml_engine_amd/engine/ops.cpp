@@ -135,14 +135,16 @@ graph act_node(const graph& input, int kind, const str& name) {
     node->forward = []() {};
     fused = true;
   }
+  node->reads_grad_alias = true;
   node->backward = [=]() {
     if (fused && x->takes_act_grad && x->consumers == 1) {
-      x->act_grad_in = nd->grad;
+      x->act_grad_in = mle::grad_of(nd);
       x->act_grad_kind = kind;
       x->act_grad_acc = mle::accumulate_flag(x);
       return;
     }
-    check(mle_act_bwd(S(), kind, x->output, nd->grad, x->grad, nd->total, mle::accumulate_flag(x)), "Deriv " + name);
+    check(mle_act_bwd(S(), kind, x->output, mle::grad_of(nd), x->grad, nd->total, mle::accumulate_flag(x)),
+          "Deriv " + name);
   };
   std_hooks(node);
   return node;
@@ -197,21 +199,26 @@ graph norm_node(const graph& X, int groups, const str& name) {
           name + " forward (with the activation after it)");
   };
   node->takes_act_grad = true;
+  node->reads_grad_alias = true;
   node->backward = [=]() {
     // The activation after this node may have left its gradient (see act_node).
     const float* da = nd->act_grad_in;
     nd->act_grad_in = nullptr;
+    // Our gradient: written from da when an activation follows, else read
+    // (possibly through an alias left by a pass-through consumer).
+    if (da) mle::resolve_alias(nd);
+    float* g = da ? nd->grad : const_cast<float*>(mle::grad_of(nd));
     // An Add or MatPE producer whose other consumers are all done: our first
     // pass now, the second at the producer's place, writing its gradient and
     // its inputs'.
     if (mle::fusion_enabled() && x->takes_norm_grad && x->consumers_done + 1 == x->consumers) {
       const int acc_x = mle::accumulate_flag(x);
-      check(mle_norm_bwd_partials(S(), nd->output, nd->grad, da, da ? nd->act_grad_kind : -1, nd->act_grad_acc, a, b,
-                                  hw, groups, ref_layout, ws, ws_bytes),
+      check(mle_norm_bwd_partials(S(), nd->output, g, da, da ? nd->act_grad_kind : -1, nd->act_grad_acc, a, b, hw,
+                                  groups, ref_layout, ws, ws_bytes),
             name + " backward (first pass)");
       x->grad_apply = [=](float* da, int acc_a, float* db, int acc_b) {
-        check(mle_norm_bwd_apply_add(S(), nd->output, nd->grad, x->grad, acc_x, da, acc_a, db, acc_b, stats, a, b, hw,
-                                     groups, eps, ref_layout, ws, ws_bytes),
+        check(mle_norm_bwd_apply_add(S(), nd->output, g, x->grad, acc_x, da, acc_a, db, acc_b, stats, a, b, hw, groups,
+                                     eps, ref_layout, ws, ws_bytes),
               name + " backward (second pass, into the producer's inputs)");
       };
       return;
@@ -222,7 +229,7 @@ graph norm_node(const graph& X, int groups, const str& name) {
             name + " backward (with the activation after it)");
       return;
     }
-    check(mle_norm_bwd(S(), nd->output, nd->grad, x->grad, stats, a, b, hw, groups, eps, ref_layout, ws, ws_bytes,
+    check(mle_norm_bwd(S(), nd->output, g, x->grad, stats, a, b, hw, groups, eps, ref_layout, ws, ws_bytes,
                        mle::accumulate_flag(x)),
           name + " backward");
   };
@@ -380,11 +387,13 @@ graph GraphOperations::Broadcast_Channel(const graph& A, const graph& B) {
     check(mle_broadcast_channel_add(S(), pa->output, pb->output, nd->output, batch, channels, hw),
           "Broadcast Add forward");
   };
+  node->reads_grad_alias = true;
   node->backward = [=]() {
-    add_grad(pa, nd->grad, 1.0, nd->total, "Broadcast Add backward - A grad");
+    // A's gradient is ours: read in place when A allows it, else written.
+    if (!mle::alias_grad(pa, nd)) add_grad(pa, mle::grad_of(nd), 1.0, nd->total, "Broadcast Add backward - A grad");
     // Reduces into (possibly only some of) B's channels; a clear gradient is
     // assigned, the rest of it set to 0 in the same launch.
-    check(mle_channel_sum_ex(S(), nd->grad, batch, channels, hw, nreduce, pb->grad, (size_t)pb->total,
+    check(mle_channel_sum_ex(S(), mle::grad_of(nd), batch, channels, hw, nreduce, pb->grad, (size_t)pb->total,
                              mle::accumulate_flag(pb)),
           "Broadcast Add backward - B grad");
   };
@@ -439,7 +448,10 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
     node->takes_norm_grad = true;
   }
   node->backward = [=]() {
-    if (last) check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
+    if (last) {
+      mle::resolve_alias(nd);
+      check(mle_fill(S(), nd->grad, 1.0f, nd->total), "Add seed");
+    }
     if (nd->grad_apply) {  // the normalisation after this node left its second pass (see norm_node)
       auto apply = std::move(nd->grad_apply);
       nd->grad_apply = nullptr;
@@ -453,7 +465,17 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
     if (nd->act_grad_in) {  // the activation after this node left its gradient (see act_node)
       const float* da = nd->act_grad_in;
       nd->act_grad_in = nullptr;
-      if (pa != pb && pa->grad != pb->grad) {  // ours and both input gradients in one pass
+      mle::resolve_alias(nd);  // written below
+      if (pa != pb && pa->grad != pb->grad) {
+        if (mle::can_alias_grad(pa, nd) && mle::can_alias_grad(pb, nd)) {
+          // both inputs read our gradient in place: only ours is written
+          check(mle_act_bwd(S(), nd->act_grad_kind, nd->output, da, nd->grad, nd->total, nd->act_grad_acc),
+                "Deriv of the activation after Add");
+          mle::alias_grad(pa, nd);
+          mle::alias_grad(pb, nd);
+          return;
+        }
+        // ours and both input gradients in one pass
         const int acc_a = mle::accumulate_flag(pa), acc_b = mle::accumulate_flag(pb);
         check(mle_act_bwd_add(S(), nd->output, da, nd->act_grad_kind, nd->grad, nd->act_grad_acc, pa->grad, acc_a,
                               pb->grad, acc_b, nd->total),
@@ -464,13 +486,21 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
             "Deriv of the activation after Add");
     }
     if (pa != pb && pa->grad != pb->grad) {  // one pass over the output gradient
+      const bool la = mle::alias_grad(pa, nd), lb = mle::alias_grad(pb, nd);
+      const float* g = mle::grad_of(nd);
+      if (la && lb) return;
+      if (la || lb) {
+        add_grad(la ? pb : pa, g, 1.0, nd->total, "Add backward");
+        return;
+      }
       const int acc_a = mle::accumulate_flag(pa), acc_b = mle::accumulate_flag(pb);
-      check(mle_accumulate2(S(), nd->grad, pa->grad, acc_a, pb->grad, acc_b, nd->total), "Add backward");
+      check(mle_accumulate2(S(), g, pa->grad, acc_a, pb->grad, acc_b, nd->total), "Add backward");
       return;
     }
-    add_grad(pa, nd->grad, 1.0, nd->total, "Add backward - A grad");
-    add_grad(pb, nd->grad, 1.0, nd->total, "Add backward - B grad");
+    add_grad(pa, mle::grad_of(nd), 1.0, nd->total, "Add backward - A grad");
+    add_grad(pb, mle::grad_of(nd), 1.0, nd->total, "Add backward - B grad");
   };
+  node->reads_grad_alias = true;
   std_hooks(node);
   return node;
 }

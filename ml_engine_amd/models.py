@@ -39,6 +39,8 @@ _SIGS = {
     "mle_model_sync": (I, [P]),
     "mle_model_stream": (P, [P]),
     "mle_model_num_nodes": (I, [P]),
+    "mle_model_node_numel": (LL, [P, I]),
+    "mle_model_node_read": (I, [P, I, I, P, SZ]),
     "mle_model_save": (I, [P, C.c_char_p]),
     "mle_model_load": (I, [P, C.c_char_p]),
     "mle_model_temb_save": (I, [P, C.c_char_p, C.POINTER(C.c_char_p), I]),
@@ -134,6 +136,18 @@ class Model:
 
     def t(self, i: int) -> int:
         return int(lib().mle_model_param_t(self.h, i))
+
+    def nodes(self) -> int:
+        return int(lib().mle_model_num_nodes(self.h))
+
+    def node(self, i: int, which: int = 0) -> np.ndarray | None:
+        """Node i's output (0) or gradient (1), as ReadValueAt reads it; None
+        when the node has no such buffer."""
+        n = int(lib().mle_model_node_numel(self.h, i))
+        out = np.empty(max(n, 0), np.float32)
+        if lib().mle_model_node_read(self.h, i, which, out.ctypes.data, out.size) != 0:
+            return None
+        return out
 
     def save(self, path: str) -> None:
         hip.check(lib().mle_model_save(self.h, str(path).encode()))

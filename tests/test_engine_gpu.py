@@ -634,6 +634,48 @@ def test_lazy_zero_matches_eager(hip, kind):
     assert not np.array_equal(lazy[0][-1], lazy[1][-1])
 
 
+@pytest.mark.parametrize("kind", ["block", "resblock"])
+def test_node_grads_match_eager(hip, kind):
+    """Every node's gradient and output, read the way ReadValueAt reads them,
+    equals the eager-clearing run's bits after a step and after a second
+    backward without zero_grad.  With lazy clearing a pass-through backward
+    (Add, Broadcast_Channel) leaves its input's gradient as an alias of its
+    own, and the shared pair backward of the residual block's two
+    convolutions writes the input gradient once: the reads here copy the
+    aliases over and must see the reference's values."""
+    from ml_engine_amd.models import STEP_BACKWARD, STEP_FORWARD, STEP_ZERO
+    if kind == "block":
+        cfg = BlockConfig(batch=2, seq=32, d_model=64, heads=4, ffn=128, vocab=97)
+        ids, tgt, params = block_data(cfg, seed=3)
+        dims, inputs = cfg.dims(), [ids, tgt]
+    else:
+        cfg = ResBlockConfig(batch=2, cin=8, cout=16, h=12, w=12, groups=4, tdim=32)
+        x, noise, t, params = resblock_data(cfg, seed=4)
+        dims, inputs = cfg.dims(t), [x, noise]
+    runs = []
+    for lazy in (True, False):
+        m = Model(kind, dims, reference_quirks=True, lazy_zero=lazy)
+        for i, p in enumerate(params):
+            m.set(i, p)
+        for slot, a in enumerate(inputs):
+            m.input(slot, a)
+        snaps = []
+        for mode in (STEP_ZERO | STEP_FORWARD | STEP_BACKWARD, STEP_FORWARD | STEP_BACKWARD):
+            m.step(cfg.lr, mode)
+            m.sync()
+            snaps.append([(m.node(i, 0), m.node(i, 1)) for i in range(m.nodes())])
+        runs.append(snaps)
+        m.close()
+    (lazy_run, eager_run) = runs
+    for phase, (a, b) in enumerate(zip(lazy_run, eager_run)):
+        assert len(a) == len(b)
+        for i, ((ao, ag), (bo, bg)) in enumerate(zip(a, b)):
+            for what, u, v in (("output", ao, bo), ("grad", ag, bg)):
+                assert (u is None) == (v is None), (kind, phase, i, what)
+                if u is not None:  # equal values (an assigned -0 reads as 0 + -0 = 0 when added)
+                    np.testing.assert_array_equal(u, v, err_msg=f"{kind}: phase {phase} node {i} {what}")
+
+
 def unet_up_oracle(orc, x, skip, target, W, b, k, stride, pad):
     """Oracle composition of the harness's U-Net decoder step: forward chain,
     MSE loss, backward chain; returns (loss, dW, db)."""
