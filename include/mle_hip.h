@@ -449,6 +449,14 @@ int mle_norm_fwd_ex(mle_stream stream, const float* x, float* y, float* stats, i
  * the other. */
 int mle_norm_fwd_act(mle_stream stream, const float* x, float* y, float* act_out, int kind, float* stats, int batch,
                      int channels, size_t hw, int groups, float eps, void* ws, size_t ws_bytes, int stats_ready);
+/* GroupNorm -> activation -> Broadcast_Channel in one pass: y = the
+ * normalisation (as mle_norm_fwd_ex), out = act(y) + cbias[channel]
+ * (GroupNorm, Engine/kernels.cu:818-834; the activation forward,
+ * Engine/kernels.cu:1214-1328; broadcast_add, Engine/kernels.cu:1661).  The
+ * activation's own output is not written.  hw % 4 == 0. */
+int mle_norm_fwd_act_bias(mle_stream stream, const float* x, float* y, float* out, int kind, const float* cbias,
+                          float* stats, int batch, int channels, size_t hw, int groups, float eps, void* ws,
+                          size_t ws_bytes, int stats_ready);
 int mle_norm_bwd_act(mle_stream stream, const float* y, const float* da, int kind, float* dy, int accumulate_dy,
                      float* dx, const float* stats, int batch, int channels, size_t hw, int groups, float eps,
                      int reference_layout, void* ws, size_t ws_bytes, int accumulate);

@@ -289,11 +289,15 @@ __device__ __forceinline__ void group_sums(const double* __restrict__ part, cons
 }
 
 // ACT >= 0 (an mle_act_kind): also act_out = act(y), the activation that
-// follows the normalisation (same formula as the activation kernels).
+// follows the normalisation (same formula as the activation kernels), plus
+// cbias[channel] when cbias is set (a broadcast channel add after the
+// activation; the channel of element offset o is (o / cb_hw) % cb_ch).
 template <bool SEG, bool VEC, int ACT = -1>
 __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, float* __restrict__ y,
                                                  float* __restrict__ stats, NormShape sh, const double* __restrict__ part,
-                                                 float eps, float* __restrict__ act_out = nullptr) {
+                                                 float eps, float* __restrict__ act_out = nullptr,
+                                                 const float* __restrict__ cbias = nullptr, uint32_t cb_hw = 1,
+                                                 uint32_t cb_ch = 1) {
   const int g = blockIdx.y, ck = blockIdx.x;
   // The group's partials first, then (VEC) this thread's x, then the merge:
   // the x loads are in flight while the merge runs.
@@ -342,6 +346,11 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
           f32x4 av;
 #pragma unroll
           for (int k = 0; k < 4; ++k) av[k] = act_f<ACT < 0 ? 0 : ACT>(yv[k]);
+          if (cbias) {  // a float4 never straddles a channel (the host checks cb_hw % 4 == 0)
+            const float cb = cbias[(o[u] / cb_hw) % cb_ch];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) av[k] = av[k] + cb;
+          }
           *reinterpret_cast<f32x4*>(act_out + o[u]) = av;
         }
       }
@@ -357,7 +366,10 @@ __global__ __launch_bounds__(NT) void norm_apply(const float* __restrict__ x, fl
         const size_t o = at<SEG>(sh, g, e);
         const float yo = (x[o] - mean) * r;
         y[o] = yo;
-        if (ACT >= 0) act_out[o] = act_f<ACT < 0 ? 0 : ACT>(yo);
+        if (ACT >= 0) {
+          const float av = act_f<ACT < 0 ? 0 : ACT>(yo);
+          act_out[o] = cbias ? av + cbias[(o / cb_hw) % cb_ch] : av;
+        }
       }
     }
   }
@@ -550,9 +562,10 @@ void with_act(int kind, F f) {
   }
 }
 
-// act >= 0: the normalisation also writes act_out = act(y).
+// act >= 0: the normalisation also writes act_out = act(y) (+ cbias[channel]).
 void launch_fwd(hipStream_t s, const NormShape& sh, const float* x, float* y, float* stats, void* ws, float eps,
-                bool stats_ready = false, int act = -1, float* act_out = nullptr) {
+                bool stats_ready = false, int act = -1, float* act_out = nullptr, const float* cbias = nullptr,
+                uint32_t cb_hw = 1, uint32_t cb_ch = 1) {
   dim3 grid(sh.nchunk, sh.groups_tot);
   double* part = static_cast<double*>(ws);
   const bool v = vec_ok(sh, {x, y}) && (act < 0 || aligned16(act_out));
@@ -568,11 +581,11 @@ void launch_fwd(hipStream_t s, const NormShape& sh, const float* x, float* y, fl
   with_act(act, [&](auto K) {
     constexpr int A = decltype(K)::value;
     if (sh.seg) {
-      if (v) norm_apply<true, true, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out);
-      else norm_apply<true, false, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out);
+      if (v) norm_apply<true, true, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out, cbias, cb_hw, cb_ch);
+      else norm_apply<true, false, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out, cbias, cb_hw, cb_ch);
     } else {
-      if (v) norm_apply<false, true, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out);
-      else norm_apply<false, false, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out);
+      if (v) norm_apply<false, true, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out, cbias, cb_hw, cb_ch);
+      else norm_apply<false, false, A><<<grid, NT, 0, s>>>(x, y, stats, sh, part, eps, act_out, cbias, cb_hw, cb_ch);
     }
   });
 }
@@ -777,6 +790,22 @@ int mle_norm_fwd_act(mle_stream stream, const float* x, float* y, float* act_out
   if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_fwd_act: workspace too small");
   launch_fwd(as_stream(stream), sh, x, y, stats, ws, eps, stats_ready != 0, kind, act_out);
   return check_launch("mle_norm_fwd_act");
+}
+
+int mle_norm_fwd_act_bias(mle_stream stream, const float* x, float* y, float* out, int kind, const float* cbias,
+                          float* stats, int batch, int channels, size_t hw, int groups, float eps, void* ws,
+                          size_t ws_bytes, int stats_ready) {
+  MLE_CHECK_ARG(x && y && out && cbias && stats && ws && kind >= MLE_RELU && kind <= MLE_LEAKY_RELU,
+                "mle_norm_fwd_act_bias: bad argument");
+  MLE_CHECK_ARG(hw % 4 == 0 && hw < ((size_t)1 << 32) && channels > 0, "mle_norm_fwd_act_bias: bad plane size");
+  NormShape sh;
+  int rc = shape_of(batch, channels, hw, groups, sh);
+  if (rc) return rc;
+  MLE_CHECK_ARG(!sh.seg, "mle_norm_fwd_act_bias: contiguous groups only");
+  if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_fwd_act_bias: workspace too small");
+  launch_fwd(as_stream(stream), sh, x, y, stats, ws, eps, stats_ready != 0, kind, out, cbias, (uint32_t)hw,
+             (uint32_t)channels);
+  return check_launch("mle_norm_fwd_act_bias");
 }
 
 int mle_norm_bwd_act(mle_stream stream, const float* y, const float* da, int kind, float* dy, int accumulate_dy,

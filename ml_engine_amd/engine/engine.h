@@ -223,6 +223,13 @@ struct NodeBackProp {
   // forward does and also act(output) into act_out, in the same pass.  An
   // activation node on this output takes over the forward with it.
   std::function<void(int kind, float* act_out)> forward_act;
+  // A normalisation's forward_act with a broadcast channel add after the
+  // activation: out = act(y) + cbias[channel], the activation's own output
+  // not written (mle_norm_fwd_act_bias).
+  std::function<void(int kind, float* out, const float* cbias)> forward_act_bias;
+  // An activation whose output the normalisation before it writes (the
+  // activation kind), else -1.
+  int fused_act_kind = -1;
   // Gradient alias: when set, this node's gradient is the content of
   // grad_src, a consumer's gradient buffer that nothing writes again before
   // the next zero_grad, and `grad` is stale.  A pass-through backward (Add,

@@ -133,6 +133,7 @@ graph act_node(const graph& input, int kind, const str& name) {
     input->forward_act = nullptr;  // one takeover per producer
     input->forward_normstats = nullptr;
     node->forward = []() {};
+    node->fused_act_kind = kind;
     fused = true;
   }
   node->reads_grad_alias = true;
@@ -198,6 +199,12 @@ graph norm_node(const graph& X, int groups, const str& name) {
                            ready),
           name + " forward (with the activation after it)");
   };
+  if (hw % 4 == 0)
+    node->forward_act_bias = [=](int kind, float* out, const float* cbias) {
+      check(mle_norm_fwd_act_bias(S(), x->output, nd->output, out, kind, cbias, stats, a, b, hw, groups, eps, ws,
+                                  ws_bytes, ready),
+            name + " forward (with the activation and channel add after it)");
+    };
   node->takes_act_grad = true;
   node->reads_grad_alias = true;
   node->backward = [=]() {
@@ -387,6 +394,44 @@ graph GraphOperations::Broadcast_Channel(const graph& A, const graph& B) {
     check(mle_broadcast_channel_add(S(), pa->output, pb->output, nd->output, batch, channels, hw),
           "Broadcast Add forward");
   };
+  // After a normalisation -> activation pair whose outputs only this node
+  // reads: the normalisation's pass is deferred to our forward (the channel
+  // vector B may come later in the node order) and writes its own output and
+  // ours, act(y) + B[c]; the activation's output is recomputed when read.
+  NodeBackProp* nrm = (A->fused_act_kind >= 0 && A->inputs.size() == 1) ? A->inputs[0].get() : nullptr;
+  if (mle::fusion_enabled() && nrm && nrm->forward_act_bias && pb->total == channels) {
+    auto norm_fwd = nrm->forward;  // the pair's pass (normalisation + activation)
+    auto fab = nrm->forward_act_bias;
+    nrm->forward_act_bias = nullptr;
+    const int kind = A->fused_act_kind;
+    auto deferred = std::make_shared<bool>(false);
+    nrm->forward = [=]() {
+      *deferred = nrm->fwd_consumers == 1 && pa->fwd_consumers == 1;
+      if (!*deferred) norm_fwd();
+    };
+    node->forward = [=]() {
+      if (*deferred) {
+        *deferred = false;
+        fab(kind, nd->output, pb->output);
+        return;
+      }
+      check(mle_broadcast_channel_add(S(), pa->output, pb->output, nd->output, batch, channels, hw),
+            "Broadcast Add forward");
+    };
+    // A read of either output before our forward (a NaN check, a print)
+    // runs the pair's pass at once; our forward then adds as usual.
+    auto flush = [=]() {
+      if (!*deferred) return false;
+      *deferred = false;
+      norm_fwd();
+      return true;
+    };
+    nrm->output_refresh = [=]() { flush(); };
+    pa->output_refresh = [=]() {
+      if (!flush())
+        check(mle_act_fwd(S(), kind, nrm->output, pa->output, pa->total), "activation output (recomputed for a read)");
+    };
+  }
   node->reads_grad_alias = true;
   node->backward = [=]() {
     // A's gradient is ours: read in place when A allows it, else written.

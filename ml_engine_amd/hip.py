@@ -101,6 +101,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_norm_fwd_ex": (I, [P, P, P, P, I, I, SZ, I, F, P, SZ, I]),
     "mle_add_norm_partials": (I, [P, P, P, SZ, P, I, I, SZ, I, P, SZ]),
     "mle_norm_fwd_act": (I, [P, P, P, P, I, P, I, I, SZ, I, F, P, SZ, I]),
+    "mle_norm_fwd_act_bias": (I, [P, P, P, P, I, P, P, I, I, SZ, I, F, P, SZ, I]),
     "mle_norm_bwd_act": (I, [P, P, P, I, P, I, P, P, I, I, SZ, I, F, I, P, SZ, I]),
     "mle_norm_bwd": (I, [P, P, P, P, P, I, I, SZ, I, F, I, P, SZ, I]),
     "mle_norm_bwd_partials": (I, [P, P, P, P, I, I, I, I, SZ, I, I, P, SZ]),

@@ -620,7 +620,8 @@ def test_norm(hip, orc, batch, channels, hw, groups):
         np.testing.assert_array_equal(gy2.numpy().view(np.uint32), gy1.numpy().view(np.uint32))
 
 
-@pytest.mark.parametrize("batch,channels,hw,groups", [(2, 64, 4096, 32), (2, 8, 700, 4), (2, 3, 33, 1)])
+@pytest.mark.parametrize("batch,channels,hw,groups", [(2, 64, 4096, 32), (2, 8, 700, 4), (2, 3, 33, 1),
+                                                     (3, 128, 4096, 32), (2, 6, 100, 3)])
 @pytest.mark.parametrize("kind", [2, 1, 0])  # MLE_SILU, MLE_GELU, MLE_RELU
 def test_norm_act_fused(hip, batch, channels, hw, groups, kind):
     """GroupNorm -> activation in one pass each way (mle_norm_fwd_act,
@@ -645,6 +646,20 @@ def test_norm_act_fused(hip, batch, channels, hw, groups, kind):
              ws.ptr, ws.nbytes, 0)
     for u, v in ((y1, y2), (a1, a2), (st1, st2)):
         np.testing.assert_array_equal(v.numpy().view(np.uint32), u.numpy().view(np.uint32))
+    if hw % 4 == 0:
+        # with the broadcast channel add after the activation (GroupNorm ->
+        # SiLU -> Broadcast_Channel): the bits of mle_broadcast_channel_add
+        # over the activation's output
+        cb = r.standard_normal(channels, dtype=np.float32)
+        gcb = B(hip, cb)
+        h1 = hip.Buffer.zeros(shape)
+        hip.call("mle_broadcast_channel_add", None, a1.ptr, gcb.ptr, h1.ptr, batch, channels, hw)
+        y3, st3 = hip.Buffer.zeros(shape), hip.Buffer.zeros(2 * batch * groups)
+        h3 = B(hip, np.full(shape, np.nan, np.float32))
+        hip.call("mle_norm_fwd_act_bias", None, gx.ptr, y3.ptr, h3.ptr, kind, gcb.ptr, st3.ptr, batch, channels, hw,
+                 groups, 1e-5, ws.ptr, ws.nbytes, 0)
+        for u, v in ((y1, y3), (h1, h3), (st1, st3)):
+            np.testing.assert_array_equal(v.numpy().view(np.uint32), u.numpy().view(np.uint32))
     gda = B(hip, da)
     for acc_dy in (0, 1):
         dy1, dx1 = B(hip, dy0), B(hip, dx0)
