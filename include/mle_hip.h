@@ -370,6 +370,12 @@ int mle_mse_fwd(mle_stream stream, const float* x, const float* t, size_t n, flo
  * as mle_read_scalar. */
 int mle_mse_fwd_read(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws,
                      size_t ws_bytes, float* loss_host);
+/* mle_mse_fwd_read and, from the same pass over x and t, the last MSE node's
+ * gradient dx = 2 (x - t) / n, assigned (scalar_mse_kernel and
+ * deriv_mse_kernel with last = true, Engine/kernels.cu:1808-1816, 1838-1848):
+ * the same bits as mle_mse_bwd(..., NULL, dx, n, 0). */
+int mle_mse_fwd_bwd_read(mle_stream stream, const float* x, const float* t, size_t n, float* loss, float* dx,
+                         void* ws, size_t ws_bytes, float* loss_host);
 /* dx (+)= 2 (x - t) / n * (upstream ? upstream[0] : 1).  deriv_mse_kernel (Engine/kernels.cu:1838-1848). */
 int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,
                 int accumulate);

@@ -448,34 +448,45 @@ __global__ __launch_bounds__(NT) void softmax_col4_bwd_kernel(const float* __res
 // ---------------------------------------------------------------------------
 // Deterministic sums into a scalar: per-block double partials, then one block
 // adds them in a fixed order.
+// With dx set, the same pass also writes the last loss node's gradient,
+// dx = 2 (x - t) / n (assigned), as mse_bwd_kernel computes it.
 __global__ __launch_bounds__(NT) void mse_partial_kernel(const float* __restrict__ x, const float* __restrict__ t,
-                                                         size_t n, double* __restrict__ part) {
+                                                         size_t n, double* __restrict__ part,
+                                                         float* __restrict__ dx = nullptr) {
   __shared__ double red[NT / 64];
   double acc = 0.0;
   const size_t stride = (size_t)gridDim.x * NT;
+  const float fn = (float)n;
   for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
-    const double d = (double)t[i] - (double)x[i];
+    const float xi = x[i], ti = t[i];
+    const double d = (double)ti - (double)xi;
     acc += d * d;
+    if (dx) dx[i] = 2.0f * (xi - ti) / fn;
   }
   acc = block_sum<NT>(acc, red);
   if (threadIdx.x == 0) part[blockIdx.x] = acc;
 }
 
-// The same sum with 16-byte loads (n % 4 == 0, both operands aligned): a
+// The same sum with 16-byte loads (n % 4 == 0, every operand aligned): a
 // thread adds its float4 groups in grid-stride order, each group's four
 // squares in element order, in double.
 __global__ __launch_bounds__(NT) void mse_partial4_kernel(const float* __restrict__ x, const float* __restrict__ t,
-                                                          size_t n4, double* __restrict__ part) {
+                                                          size_t n4, double* __restrict__ part,
+                                                          float* __restrict__ dx = nullptr) {
   __shared__ double red[NT / 64];
   double acc = 0.0;
   const size_t stride = (size_t)gridDim.x * NT;
+  const float fn = (float)(n4 * 4);
   for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n4; i += stride) {
     const f32x4 xv = ldv(x, i * 4), tv = ldv(t, i * 4);
+    f32x4 g;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const double d = (double)tv[j] - (double)xv[j];
       acc += d * d;
+      g[j] = 2.0f * (xv[j] - tv[j]) / fn;
     }
+    if (dx) stv(dx, i * 4, g);
   }
   acc = block_sum<NT>(acc, red);
   if (threadIdx.x == 0) part[blockIdx.x] = acc;
@@ -686,7 +697,7 @@ size_t mle_loss_ws_bytes(size_t n) {
 }
 
 static int mse_fwd_impl(mle_stream stream, const float* x, const float* t, size_t n, float* loss, void* ws,
-                        size_t ws_bytes, float* loss_host, const char* who) {
+                        size_t ws_bytes, float* loss_host, const char* who, float* dx = nullptr) {
   MLE_CHECK_ARG(x && t && loss && ws && n > 0, "%s: bad argument", who);
   const unsigned g = stream_grid(n, NT, kMsePartCap);
   if (ws_bytes < g * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "%s: workspace too small", who);
@@ -698,11 +709,11 @@ static int mse_fwd_impl(mle_stream stream, const float* x, const float* t, size_
     if (rc) return rc;
   }
   unsigned np = g;
-  if (n % 4 == 0 && aligned16(x) && aligned16(t)) {
+  if (n % 4 == 0 && aligned16(x) && aligned16(t) && (!dx || aligned16(dx))) {
     np = stream_grid(n / 4, NT, kMsePartCap);
-    mse_partial4_kernel<<<np, NT, 0, s>>>(x, t, n / 4, part);
+    mse_partial4_kernel<<<np, NT, 0, s>>>(x, t, n / 4, part, dx);
   } else {
-    mse_partial_kernel<<<g, NT, 0, s>>>(x, t, n, part);
+    mse_partial_kernel<<<g, NT, 0, s>>>(x, t, n, part, dx);
   }
   finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, np, (double)n, loss, r.slot, r.seq);
   const int rc = check_launch(who);
@@ -718,6 +729,12 @@ int mle_mse_fwd_read(mle_stream stream, const float* x, const float* t, size_t n
                      size_t ws_bytes, float* loss_host) {
   MLE_CHECK_ARG(loss_host != nullptr, "mle_mse_fwd_read: null loss_host");
   return mse_fwd_impl(stream, x, t, n, loss, ws, ws_bytes, loss_host, "mle_mse_fwd_read");
+}
+
+int mle_mse_fwd_bwd_read(mle_stream stream, const float* x, const float* t, size_t n, float* loss, float* dx,
+                         void* ws, size_t ws_bytes, float* loss_host) {
+  MLE_CHECK_ARG(loss_host != nullptr && dx != nullptr, "mle_mse_fwd_bwd_read: null pointer");
+  return mse_fwd_impl(stream, x, t, n, loss, ws, ws_bytes, loss_host, "mle_mse_fwd_bwd_read", dx);
 }
 
 int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,

@@ -162,6 +162,7 @@ void set_lazy_zero(bool on) { g_lazy_zero = on; }
 void defer_zero(NodeBackProp* n) {
   if (!n || !n->grad || n->total <= 0) return;
   n->grad_src = nullptr;
+  n->grad_early = false;
   if (g_lazy_zero) n->grad_pending_zero = true;
   else zero(n->grad, n->total);
 }
@@ -170,6 +171,7 @@ int accumulate_flag(NodeBackProp* n) {
   resolve_alias(n);
   if (n->grad_pending_zero) {
     n->grad_pending_zero = false;
+    n->grad_early = false;  // the caller writes the whole gradient
     return 0;
   }
   return 1;
@@ -227,6 +229,7 @@ void materialize(NodeBackProp* n) {
   clip_apply(n);
   if (!n->grad_pending_zero) return;
   n->grad_pending_zero = false;
+  n->grad_early = false;
   zero(n->grad, n->total);
 }
 

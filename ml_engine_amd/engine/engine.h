@@ -240,6 +240,13 @@ struct NodeBackProp {
   // mle::accumulate_flag); zero_grad and each backward pass's start drop it.
   const float* grad_src = nullptr;
   bool reads_grad_alias = false;
+  // Early gradient: the last loss node's forward wrote this node's whole
+  // gradient into `grad` while the gradient is still clear
+  // (grad_pending_zero), as its backward would assign it.  The loss's
+  // backward commits it (clears the mark, launches nothing); a read, another
+  // writer or zero_grad before that drops it, and the gradient reads as the
+  // reference's zero until the backward computes it as usual.
+  bool grad_early = false;
   // Convolute2D: the parameter half of its backward (dW assigned, db added),
   // so a fused input gradient (mle::fuse_conv_pair) can take the other half.
   std::function<void()> backward_params;

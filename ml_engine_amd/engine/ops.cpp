@@ -569,15 +569,29 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
   void* ws = mle::alloc_scratch(ws_bytes);
   node->forward = [=]() {
     if (calculate_loss || !last) {
-      if (last)  // the loss and its read-back in one launch
+      if (last && mle::fusion_enabled() && pr->grad_pending_zero && !pr->grad_src) {
+        // The loss, its read-back and the prediction's gradient from one pass
+        // over x and t: the gradient is held early (NodeBackProp::grad_early)
+        // and committed by our backward.
+        check(mle_mse_fwd_bwd_read(S(), pr->output, tg->output, n, nd->output, pr->grad, ws, ws_bytes,
+                                   &GraphOperations::loss),
+              "Scalar MSE (with its gradient) in MSE forward");
+        pr->grad_early = true;
+      } else if (last) {  // the loss and its read-back in one launch
         check(mle_mse_fwd_read(S(), pr->output, tg->output, n, nd->output, ws, ws_bytes, &GraphOperations::loss),
               "Scalar MSE in MSE forward");
-      else
+      } else {
         check(mle_mse_fwd(S(), pr->output, tg->output, n, nd->output, ws, ws_bytes), "Scalar MSE in MSE forward");
+      }
       nd->output_pending_zero = false;  // written whole
     }
   };
   node->backward = [=]() {
+    if (last && pr->grad_early && pr->grad_pending_zero) {  // written by our forward: commit it
+      pr->grad_early = false;
+      pr->grad_pending_zero = false;
+      return;
+    }
     check(mle_mse_bwd(S(), pr->output, tg->output, last ? nullptr : nd->grad, pr->grad, n, mle::accumulate_flag(pr)),
           "deriv MSE");
   };

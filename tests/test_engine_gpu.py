@@ -676,6 +676,48 @@ def test_node_grads_match_eager(hip, kind):
                     np.testing.assert_array_equal(u, v, err_msg=f"{kind}: phase {phase} node {i} {what}")
 
 
+def test_early_loss_gradient_reads_as_reference(hip):
+    """The last MSE node's forward writes its prediction's gradient in the
+    same pass as the loss, held until its backward commits it.  Between
+    forward and backward every node gradient still reads 0, as after the
+    reference's zero_grad + forward; a read there drops the early gradient
+    and the backward computes it as usual.  Both orders, and eager clearing,
+    end with the same node gradients."""
+    from ml_engine_amd.models import STEP_BACKWARD, STEP_FORWARD, STEP_ZERO
+    cfg = ResBlockConfig(batch=2, cin=8, cout=16, h=12, w=12, groups=4, tdim=32)
+    x, noise, t, params = resblock_data(cfg, seed=4)
+
+    def make(lazy):
+        m = Model("resblock", cfg.dims(t), reference_quirks=True, lazy_zero=lazy)
+        for i, p in enumerate(params):
+            m.set(i, p)
+        m.input(0, x)
+        m.input(1, noise)
+        return m
+
+    runs = []
+    for lazy, read_between in ((True, True), (True, False), (False, False)):
+        m = make(lazy)
+        m.step(cfg.lr, STEP_ZERO | STEP_FORWARD)
+        if read_between:
+            for i in range(m.nodes()):
+                g = m.node(i, 1)
+                if g is not None:
+                    assert not np.any(g), f"node {i} gradient before backward"
+        m.step(cfg.lr, STEP_BACKWARD)
+        m.sync()
+        runs.append(([m.node(i, 1) for i in range(m.nodes())], [m.get(i, 1) for i in range(len(params))], m.loss))
+        m.close()
+    base = runs[2]
+    for grads, pgrads, loss in runs[:2]:
+        assert loss == base[2]
+        for i, (u, v) in enumerate(zip(grads, base[0])):
+            if u is not None:
+                np.testing.assert_array_equal(u, v, err_msg=f"node {i}")
+        for i, (u, v) in enumerate(zip(pgrads, base[1])):
+            np.testing.assert_array_equal(u, v, err_msg=f"param {i}")
+
+
 def unet_up_oracle(orc, x, skip, target, W, b, k, stride, pad):
     """Oracle composition of the harness's U-Net decoder step: forward chain,
     MSE loss, backward chain; returns (loss, dW, db)."""

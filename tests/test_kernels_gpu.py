@@ -1569,6 +1569,16 @@ def test_mse_fwd_read(hip, n):
         other = C.c_float(0.0)
         hip.call("mle_read_scalar", None, gx.ptr, C.byref(other))
         assert other.value == x[0]
+    # the loss and the last node's gradient from one pass: the bits of
+    # mle_mse_fwd_read followed by an assigning mle_mse_bwd
+    dx1 = hip.Buffer.zeros(n)
+    hip.call("mle_mse_bwd", None, gx.ptr, gt.ptr, None, dx1.ptr, n, 0)
+    dx2 = B(hip, np.full(n, np.nan, np.float32))
+    host = C.c_float(float("nan"))
+    hip.call("mle_mse_fwd_bwd_read", None, gx.ptr, gt.ptr, n, gl2.ptr, dx2.ptr, ws.ptr, ws.nbytes, C.byref(host))
+    assert gl2.numpy().view(np.uint32)[0] == want
+    assert np.float32(host.value).view(np.uint32) == want
+    np.testing.assert_array_equal(dx2.numpy().view(np.uint32), dx1.numpy().view(np.uint32))
 
 
 @pytest.mark.parametrize("kind", ["relu", "gelu", "silu", "tanh"])
