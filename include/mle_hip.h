@@ -388,6 +388,15 @@ int mle_softmax_xent_fwd(mle_stream stream, const float* logits, const float* ta
 int mle_softmax_xent_bwd(mle_stream stream, const float* probs, const float* target, const float* upstream,
                          float* dlogits, size_t n, int batch);
 
+/* SoftMaxCrossEntropy against key targets for small logits (rows <= 1024,
+ * cols <= 64, e.g. a classifier head) in one launch: the row statistics
+ * (stats), the loss and (loss_host non-null) its read-back, and with dlogits
+ * non-null the gradient (p - t) / batch, assigned -- the same bits as
+ * mle_gemm_rowstats' row statistics, mle_softmax_xent_keys_fwd_rowstats_read
+ * and mle_softmax_xent_keys_bwd (Engine/engine.cu:2088-2110). */
+int mle_softmax_xent_keys_small_read(mle_stream stream, const float* logits, const int32_t* keys, int clen,
+                                     int max_clen, float* stats, int rows, int cols, int batch, float* loss,
+                                     float* dlogits, float* loss_host);
 /* Cross-entropy against one-hot rows given by token ids: row r = b*clen + s
  * has its 1 at column keys[b*max_clen + s] if that id is in [0, cols), else
  * no 1 -- the matrix OneHotEmbeddings builds (Engine/kernels.cu:1551-1560).

@@ -636,6 +636,55 @@ __global__ __launch_bounds__(NT) void xent_keys_bwd_kernel(const float* __restri
 
 constexpr unsigned kMsePartCap = 2048;
 
+// Cross-entropy against key targets for small logits (rows <= FIN_NT,
+// cols <= 64) in one workgroup: each wave holds whole rows, one column per
+// lane, and forms what the GEMM-side rowstats_kernel (one 64-column block),
+// xent_keys_partials_kernel and finish_scalar_kernel form in three launches,
+// with the same reduction trees (the same bits): the row's max and sum of
+// exp, the loss term -log(p_key + 1e-27), the loss as the workgroup's sum of
+// the row terms over rows * cols, published for the host when a slot is given.
+// With dl set, the gradient (p - t) / batch of xent_keys_bwd_kernel too.
+__global__ __launch_bounds__(FIN_NT) void xent_keys_small_kernel(const float* __restrict__ x, KeyTargets kt, int rows,
+                                                                 int cols, float batch, float* __restrict__ loss,
+                                                                 float* __restrict__ dl, mle::ScalarSlot* slot,
+                                                                 unsigned seq) {
+  __shared__ double lps[FIN_NT];
+  __shared__ double red[FIN_NT / 64];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int row = wid; row < rows; row += FIN_NT / 64) {
+    const bool in = lane < cols;
+    const float xv = in ? x[(size_t)row * cols + lane] : -FLT_MAX;
+    const int key = kt.key((size_t)row, cols);
+    float m = xv;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float e = in ? expf(xv - m) : 0.f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, 64);
+    const float sum = e < 1e-45f ? 1.0f : e;
+    const float xk = __shfl(xv, key >= 0 ? key : 0, 64);
+    if (lane == 0) {
+      lps[row] = key >= 0 ? -log((double)(expf(xk - m) / sum) + 1e-27) : 0.0;
+      kt.stats[2 * row] = m;
+      kt.stats[2 * row + 1] = sum;
+    }
+    if (dl && in) {
+      const float p = expf(xv - m) / sum;
+      const float g = p + (-1.0f) * (lane == key ? 1.0f : 0.0f);
+      dl[(size_t)row * cols + lane] = g / batch;
+    }
+  }
+  __syncthreads();
+  const double v0 = threadIdx.x < (unsigned)rows ? lps[threadIdx.x] : 0.0;
+  double acc = (v0 + 0.0) + (0.0 + 0.0);  // finish_scalar_kernel's four accumulators, three of them empty
+  acc = block_sum<FIN_NT>(acc, red);
+  if (threadIdx.x == 0) {
+    const float v = (float)(acc / ((double)rows * (double)cols));
+    loss[0] = v;
+    if (slot) mle::publish_scalar(slot, __builtin_bit_cast(unsigned, v), seq);
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -839,6 +888,27 @@ int mle_softmax_xent_keys_fwd_rowstats_read(mle_stream stream, const float* logi
   MLE_CHECK_ARG(loss_host != nullptr, "mle_softmax_xent_keys_fwd_rowstats_read: null loss_host");
   return xent_rowstats_impl(stream, logits, rowpart, ldp, keys, clen, max_clen, stats, rows, cols, loss, ws, ws_bytes,
                             loss_host, "mle_softmax_xent_keys_fwd_rowstats_read");
+}
+
+int mle_softmax_xent_keys_small_read(mle_stream stream, const float* logits, const int32_t* keys, int clen,
+                                     int max_clen, float* stats, int rows, int cols, int batch, float* loss,
+                                     float* dlogits, float* loss_host) {
+  MLE_CHECK_ARG(logits && keys && stats && loss && rows > 0 && cols > 0 && clen > 0 && max_clen >= clen &&
+                    rows % clen == 0 && batch > 0,
+                "mle_softmax_xent_keys_small_read: bad argument");
+  MLE_CHECK_ARG(rows <= FIN_NT && cols <= 64, "mle_softmax_xent_keys_small_read: %d x %d logits exceed %d x 64", rows,
+                cols, FIN_NT);
+  hipStream_t s = as_stream(stream);
+  const KeyTargets kt{keys, clen, max_clen, stats};
+  mle::ScalarRead r;
+  if (loss_host) {
+    const int rc = mle::scalar_read_begin(r, "mle_softmax_xent_keys_small_read");
+    if (rc) return rc;
+  }
+  xent_keys_small_kernel<<<1, FIN_NT, 0, s>>>(logits, kt, rows, cols, (float)batch, loss, dlogits, r.slot, r.seq);
+  const int rc = check_launch("mle_softmax_xent_keys_small_read");
+  if (rc || !loss_host) return rc;
+  return mle::scalar_read_finish(s, r, loss_host, "mle_softmax_xent_keys_small_read");
 }
 
 int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const float* stats, const int32_t* keys, int clen,

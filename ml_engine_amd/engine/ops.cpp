@@ -632,8 +632,13 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
   // A Linear prediction writes the row statistics with its output (GEMM
   // epilogue), so the loss never reads the logits back.
   const int64_t ldp = 2 * (int64_t)((d + 63) / 64);
+  // Small logits (a classifier head): statistics, loss, read-back and the
+  // gradient in one launch; the gradient is held early (grad_early) until our
+  // backward commits it.
+  const bool small = by_keys && last && mle::fusion_enabled() && rows <= 1024 && d <= 64;
   float* rowpart = nullptr;
-  if (by_keys && mle::fusion_enabled() && prediction->forward_rowstats && prediction->total == (long long)rows * d) {
+  if (!small && by_keys && mle::fusion_enabled() && prediction->forward_rowstats &&
+      prediction->total == (long long)rows * d) {
     rowpart = mle::alloc_output((size_t)rows * ldp);
     auto fr = prediction->forward_rowstats;
     prediction->forward = [fr, rowpart, ldp]() { fr(rowpart, ldp); };
@@ -641,6 +646,16 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
   }
   node->forward = [=]() {
     if (calculate_loss || !last) {
+      if (small) {
+        const bool early = pr->grad_pending_zero && !pr->grad_src;
+        check(mle_softmax_xent_keys_small_read(S(), pr->output, oh->keys, oh->clen, oh->max_clen, stats, rows, d,
+                                               batch, nd->output, early ? pr->grad : nullptr,
+                                               &GraphOperations::loss),
+              "SoftMaxCrossEntropy");
+        pr->grad_early = early;
+        nd->output_pending_zero = false;
+        return;
+      }
       if (rowpart && last) {
         // the loss and its read-back in one launch
         check(mle_softmax_xent_keys_fwd_rowstats_read(S(), pr->output, rowpart, ldp, oh->keys, oh->clen,
@@ -666,6 +681,11 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
     }
   };
   node->backward = [=]() {
+    if (small && pr->grad_early && pr->grad_pending_zero) {  // written by our forward: commit it
+      pr->grad_early = false;
+      pr->grad_pending_zero = false;
+      return;
+    }
     mle::accumulate_flag(pr);  // the reference assigns the whole gradient
     const float* up = last ? nullptr : nd->grad;
     if (by_keys)

@@ -1548,6 +1548,61 @@ def test_softmax_xent_keys_rowstats(hip, batch, clen, cols):
         assert np.float32(host.value).view(np.uint32) == gloss2.numpy().view(np.uint32)[0], (rep, host.value)
 
 
+@pytest.mark.parametrize("batch,clen,cols,hidden", [(64, 1, 10, 256), (4, 16, 64, 32), (3, 5, 7, 40), (16, 64, 33, 8)])
+def test_softmax_xent_keys_small(hip, orc, batch, clen, cols, hidden):
+    """A classifier head's cross-entropy in one launch (rows <= 1024,
+    cols <= 64): the row statistics, loss, host read-back and gradient are the
+    bits of the three-launch path the engine takes otherwise -- the GEMM with
+    row statistics, mle_softmax_xent_keys_fwd_rowstats_read and
+    mle_softmax_xent_keys_bwd -- on the GEMM's logits; keys out of range
+    included; and the loss within 1e-5 of the oracle's dense one-hot loss."""
+    r = rng(batch + clen * 3 + cols + hidden)
+    rows = batch * clen
+    X = r.standard_normal((rows, hidden), dtype=np.float32)
+    W = (r.standard_normal((hidden, cols), dtype=np.float32) * 0.5).astype(np.float32)
+    bias = r.standard_normal(cols, dtype=np.float32)
+    keys = r.integers(0, cols, (batch, clen)).astype(np.int32)
+    keys[0, 0] = -1
+    keys[-1, -1] = cols + 2
+    L = hip.lib()
+    gX, gW, gb, gk = B(hip, X), B(hip, W), B(hip, bias), B(hip, keys)
+    nblk = (cols + 63) // 64
+    ldp = 2 * nblk
+    glog, gpart = hip.Buffer.zeros((rows, cols)), hip.Buffer.zeros(rows * ldp)
+    wsg = hip.Buffer(max(256, L.mle_gemm_ws_bytes(rows, cols, hidden, 1)))
+    hip.call("mle_gemm_rowstats", None, 0, 0, rows, cols, hidden, 1.0, gX.ptr, hidden, gW.ptr, cols, 0.0, glog.ptr, cols,
+             gb.ptr, gpart.ptr, ldp, wsg.ptr, wsg.nbytes)
+    ws = hip.Buffer(L.mle_loss_ws_bytes(rows * cols))
+    gst, gloss = hip.Buffer.zeros(2 * rows), hip.Buffer.zeros(1)
+    host = C.c_float(float("nan"))
+    hip.call("mle_softmax_xent_keys_fwd_rowstats_read", None, glog.ptr, gpart.ptr, ldp, gk.ptr, clen, clen, gst.ptr,
+             rows, cols, gloss.ptr, ws.ptr, ws.nbytes, C.byref(host))
+    gd = hip.Buffer.zeros((rows, cols))
+    hip.call("mle_softmax_xent_keys_bwd", None, glog.ptr, gst.ptr, gk.ptr, clen, clen, None, gd.ptr, rows, cols, batch)
+    for with_grad in (True, False):
+        gst2, gloss2 = B(hip, np.full(2 * rows, np.nan, np.float32)), hip.Buffer.zeros(1)
+        gd2 = B(hip, np.full((rows, cols), np.nan, np.float32))
+        host2 = C.c_float(float("nan"))
+        hip.call("mle_softmax_xent_keys_small_read", None, glog.ptr, gk.ptr, clen, clen, gst2.ptr, rows, cols, batch,
+                 gloss2.ptr, gd2.ptr if with_grad else None, C.byref(host2))
+        np.testing.assert_array_equal(gst2.numpy().view(np.uint32), gst.numpy().view(np.uint32))
+        np.testing.assert_array_equal(gloss2.numpy().view(np.uint32), gloss.numpy().view(np.uint32))
+        assert np.float32(host2.value).view(np.uint32) == np.float32(host.value).view(np.uint32)
+        if with_grad:
+            np.testing.assert_array_equal(gd2.numpy().view(np.uint32), gd.numpy().view(np.uint32))
+        else:
+            assert np.all(np.isnan(gd2.numpy()))
+    logits = glog.numpy()
+    tgt = np.zeros((rows, cols), np.float32)
+    for b in range(batch):
+        for s_ in range(clen):
+            if 0 <= keys[b, s_] < cols:
+                tgt[b * clen + s_, keys[b, s_]] = 1.0
+    pr = np.zeros_like(logits)
+    lref = orc.call("orc_softmax_xent_fwd", orc.ptr(logits), orc.ptr(tgt), orc.ptr(pr), rows, cols)
+    assert_close(gloss.numpy(), np.array([lref], np.float32), what="small-logits loss", **EW)
+
+
 @pytest.mark.parametrize("n", [5, 1000, 123457, 123456, 8 << 20])
 def test_mse_fwd_read(hip, n):
     """mle_mse_fwd_read: the loss of mle_mse_fwd bit for bit, on the device and
