@@ -276,9 +276,11 @@ int mle_gemm_rowstats(mle_stream stream, int trans_a, int trans_b, int M, int N,
  *                      output's gradient);  dX (+)= C * act'(X)  (its input's
  *                      gradient; accumulate_dx 1 adds, 0 assigns)
  * On the persistent GEMM kernel (NN forward / NT backward, ReLU, GELU or SiLU)
- * the epilogue computes Y or dX from the tile in registers; otherwise the
- * activation kernels run after the GEMM.  Same values either way.  (The C4
- * block's engine does not use them: with two tiles per workgroup the longer
+ * the epilogue computes Y or dX from the tile in registers; a forward split
+ * along K has the reduce that completes C write Y too; otherwise the
+ * activation kernels run after the GEMM.  Same values either way.  (The
+ * engine uses the forward for small products only, a classifier's hidden
+ * layer: on the C4 block's FFN, with two tiles per workgroup, the longer
  * epilogue measured no faster than a separate activation pass.) */
 int mle_gemm_act_fwd(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha,
                      const float* A, int64_t lda, const float* B, int64_t ldb, float beta,

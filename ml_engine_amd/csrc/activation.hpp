@@ -54,4 +54,16 @@ __device__ __forceinline__ float act_df(float x) {
   return (x < 0.0f) ? 0.01f : 1.0f;
 }
 
+// act_f for a kind known only at run time.
+__device__ __forceinline__ float act_rt(int kind, float x) {
+  switch (kind) {
+    case MLE_RELU: return act_f<MLE_RELU>(x);
+    case MLE_GELU: return act_f<MLE_GELU>(x);
+    case MLE_SILU: return act_f<MLE_SILU>(x);
+    case MLE_TANH: return act_f<MLE_TANH>(x);
+    case MLE_SIGMOID: return act_f<MLE_SIGMOID>(x);
+    default: return act_f<MLE_LEAKY_RELU>(x);
+  }
+}
+
 }  // namespace mle

@@ -56,6 +56,9 @@ struct GemmArgs {
   const float* act_x;
   float* act_dx;
   int act_acc;
+  // 1 + an activation kind: the split reduce also writes act_y = act(C) in
+  // C's layout (0: not).
+  int act_red;
   // Column sums: 0 adds them into colsum (the default), 1 assigns (colsum is
   // logically zero).
   int cs_assign;
@@ -937,16 +940,24 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g, int64_t u
   if (sg != 0 || !live) return;
   const f32x4 r = ((grp[0][lane] + grp[1][lane]) + grp[2][lane]) + grp[3][lane];
   float* c = g.C + batch_off(b, g, g.sc, g.sc2) + row * g.ldc + col;
+  const int64_t co = batch_off(b, g, g.sc, g.sc2) + row * g.ldc + col;
   if (VEC) {
     f32x4 v = g.alpha * r;
     if (g.beta != 0.f) v += g.beta * *reinterpret_cast<const f32x4*>(c);
     if (g.bias) v += *reinterpret_cast<const f32x4*>(g.bias + b * g.sbias + col);
     *reinterpret_cast<f32x4*>(c) = v;
+    if (g.act_red) {
+      f32x4 y;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) y[k] = act_rt(g.act_red - 1, v[k]);
+      *reinterpret_cast<f32x4*>(g.act_y + co) = y;
+    }
   } else {
     float v = g.alpha * r[0];
     if (g.beta != 0.f) v += g.beta * *c;
     if (g.bias) v += g.bias[b * g.sbias + col];
     *c = v;
+    if (g.act_red) g.act_y[co] = act_rt(g.act_red - 1, v);
   }
 }
 
@@ -1383,6 +1394,14 @@ int mle_gemm_act_fwd(mle_stream stream, int trans_a, int trans_b, int M, int N, 
       ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
       launch_stream_act<0, 0, kEpiActFwd>(s, P, kind);
     }
+    return check_launch("mle_gemm_act_fwd");
+  }
+  if (P.g.splits > 1 && aligned16(Y)) {  // split K: the reduce that completes C writes Y too
+    P.g.act_y = Y;
+    P.g.act_red = 1 + kind;
+    ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
+    gemm_launch_main(s, P);
+    gemm_launch_reduce(s, P);
     return check_launch("mle_gemm_act_fwd");
   }
   {

@@ -637,51 +637,67 @@ __global__ __launch_bounds__(NT) void xent_keys_bwd_kernel(const float* __restri
 constexpr unsigned kMsePartCap = 2048;
 
 // Cross-entropy against key targets for small logits (rows <= FIN_NT,
-// cols <= 64) in one workgroup: each wave holds whole rows, one column per
-// lane, and forms what the GEMM-side rowstats_kernel (one 64-column block),
-// xent_keys_partials_kernel and finish_scalar_kernel form in three launches,
-// with the same reduction trees (the same bits): the row's max and sum of
-// exp, the loss term -log(p_key + 1e-27), the loss as the workgroup's sum of
-// the row terms over rows * cols, published for the host when a slot is given.
-// With dl set, the gradient (p - t) / batch of xent_keys_bwd_kernel too.
+// cols <= 64) in one workgroup, one row per thread: the row's max and sum of
+// exp as the GEMM-side rowstats_kernel forms them over one 64-column block
+// (a 64-lane butterfly, which the thread replays on 64 registers: at each
+// level lane j adds lane j ^ off, so the bits are the same), the loss term
+// -log(p_key + 1e-27) of xent_keys_partials_kernel, and the loss as the
+// workgroup's sum of the row terms over rows * cols in finish_scalar_kernel's
+// order, published for the host when a slot is given.  With dl set, the
+// gradient (p - t) / batch of xent_keys_bwd_kernel too.
 __global__ __launch_bounds__(FIN_NT) void xent_keys_small_kernel(const float* __restrict__ x, KeyTargets kt, int rows,
                                                                  int cols, float batch, float* __restrict__ loss,
                                                                  float* __restrict__ dl, mle::ScalarSlot* slot,
                                                                  unsigned seq) {
-  __shared__ double lps[FIN_NT];
   __shared__ double red[FIN_NT / 64];
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  for (int row = wid; row < rows; row += FIN_NT / 64) {
-    const bool in = lane < cols;
-    const float xv = in ? x[(size_t)row * cols + lane] : -FLT_MAX;
+  __shared__ float srow[2 * FIN_NT];  // (max, sum) per row for the gradient phase
+  __shared__ int skey[FIN_NT];
+  const int row = threadIdx.x;
+  double lp = 0.0;
+  if (row < rows) {
+    const float* xr = x + (size_t)row * cols;
     const int key = kt.key((size_t)row, cols);
-    float m = xv;
+    const float xk = key >= 0 ? xr[key] : 0.f;
+    float e[64];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    float e = in ? expf(xv - m) : 0.f;
+    for (int j = 0; j < 64; ++j) e[j] = j < cols ? xr[j] : -FLT_MAX;
+    float m = -FLT_MAX;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) e += __shfl_xor(e, o, 64);
-    const float sum = e < 1e-45f ? 1.0f : e;
-    const float xk = __shfl(xv, key >= 0 ? key : 0, 64);
-    if (lane == 0) {
-      lps[row] = key >= 0 ? -log((double)(expf(xk - m) / sum) + 1e-27) : 0.0;
-      kt.stats[2 * row] = m;
-      kt.stats[2 * row + 1] = sum;
-    }
-    if (dl && in) {
-      const float p = expf(xv - m) / sum;
-      const float g = p + (-1.0f) * (lane == key ? 1.0f : 0.0f);
-      dl[(size_t)row * cols + lane] = g / batch;
-    }
+    for (int j = 0; j < 64; ++j) m = fmaxf(m, e[j]);  // a max's value does not depend on the order
+#pragma unroll
+    for (int j = 0; j < 64; ++j) e[j] = j < cols ? expf(e[j] - m) : 0.f;
+    // the butterfly in place: lanes j and j ^ off both end with their sum
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+      for (int j = 0; j < 64; ++j)
+        if ((j & off) == 0) {
+          const float t = e[j] + e[j ^ off];
+          e[j] = t;
+          e[j ^ off] = t;
+        }
+    const float sum = e[0] < 1e-45f ? 1.0f : e[0];
+    if (key >= 0) lp = -log((double)(expf(xk - m) / sum) + 1e-27);
+    kt.stats[2 * row] = m;
+    kt.stats[2 * row + 1] = sum;
+    srow[2 * row] = m;
+    srow[2 * row + 1] = sum;
+    skey[row] = key;
   }
-  __syncthreads();
-  const double v0 = threadIdx.x < (unsigned)rows ? lps[threadIdx.x] : 0.0;
-  double acc = (v0 + 0.0) + (0.0 + 0.0);  // finish_scalar_kernel's four accumulators, three of them empty
-  acc = block_sum<FIN_NT>(acc, red);
-  if (threadIdx.x == 0) {
-    const float v = (float)(acc / ((double)rows * (double)cols));
-    loss[0] = v;
-    if (slot) mle::publish_scalar(slot, __builtin_bit_cast(unsigned, v), seq);
+  double acc = (lp + 0.0) + (0.0 + 0.0);  // finish_scalar_kernel's four accumulators, three of them empty
+  acc = block_sum<FIN_NT>(acc, red);  // its barriers also order the row statistics in LDS
+  if (threadIdx.x == 0) {  // published first: the host waiting for the loss resumes sooner
+    const float vv = (float)(acc / ((double)rows * (double)cols));
+    loss[0] = vv;
+    if (slot) mle::publish_scalar(slot, __builtin_bit_cast(unsigned, vv), seq);
+  }
+  if (dl) {  // one element per thread: coalesced loads and stores
+    const int n = rows * cols;
+    for (int i = threadIdx.x; i < n; i += FIN_NT) {
+      const int r = i / cols, c = i - r * cols;
+      const float p = expf(x[i] - srow[2 * r]) / srow[2 * r + 1];
+      dl[i] = (p + (-1.0f) * (c == skey[r] ? 1.0f : 0.0f)) / batch;
+    }
   }
 }
 

@@ -978,6 +978,16 @@ graph Linear::forward(const graph& X) {
                       p, 0, 1, nullptr, has_bias ? Bb->output : nullptr, ws, ws_bytes),
           "MatMul... X*W1 + B1 in " + name + " forward");
   };
+  // A small product (a classifier's hidden layer) runs split along K; the
+  // activation after it is then written by the reduce that completes Y
+  // (mle_gemm_act_fwd), one launch less.  Large products keep the separate
+  // activation pass (measured no slower than an activation epilogue).
+  if ((double)rows * p <= 65536.0)
+    node->forward_act = [=](int kind, float* act_out) {
+      check(mle_gemm_act_fwd(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, W->output, p, 0.0f,
+                             nd->output, has_bias ? Bb->output : nullptr, kind, act_out, ws, ws_bytes),
+            "MatMul... X*W1 + B1 in " + name + " forward (with the activation after it)");
+    };
   node->forward_rowstats = [=](float* rowpart, int64_t ldp) {
     check(mle_gemm_rowstats(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, W->output, p, 0.0f,
                             nd->output, p, has_bias ? Bb->output : nullptr, rowpart, ldp, ws, ws_bytes),

@@ -132,6 +132,7 @@ graph act_node(const graph& input, int kind, const str& name) {
     input->forward = [fa, kind, nd]() { fa(kind, nd->output); };
     input->forward_act = nullptr;  // one takeover per producer
     input->forward_normstats = nullptr;
+    input->forward_rowstats = nullptr;
     node->forward = []() {};
     node->fused_act_kind = kind;
     fused = true;

@@ -1637,11 +1637,14 @@ def test_mse_fwd_read(hip, n):
 
 
 @pytest.mark.parametrize("kind", ["relu", "gelu", "silu", "tanh"])
-@pytest.mark.parametrize("M,N,K", [(4100, 4000, 64), (300, 130, 70)])
-def test_gemm_act_fwd(hip, orc, kind, M, N, K):
+@pytest.mark.parametrize("M,N,K,ws", [(4100, 4000, 64, False), (300, 130, 70, False),
+                                      # split along K: the reduce that completes C writes Y
+                                      (64, 256, 784, True), (64, 10, 256, True), (70, 130, 900, True)])
+def test_gemm_act_fwd(hip, orc, kind, M, N, K, ws):
     """C = A B + bias and Y = act(C) (the persistent kernel's epilogue for
-    ReLU / GELU / SiLU on the large shape, the activation kernel otherwise)
-    against the oracle's GEMM and activation."""
+    ReLU / GELU / SiLU on the large shape, the split reduce's for small split
+    products, the activation kernel otherwise) against the oracle's GEMM and
+    activation."""
     r = rng(M + N + K + hip.ACT[kind])
     A = r.standard_normal((M, K), dtype=np.float32) * 0.25
     Bm = r.standard_normal((K, N), dtype=np.float32) * 0.25
@@ -1653,13 +1656,19 @@ def test_gemm_act_fwd(hip, orc, kind, M, N, K):
     orc.call("orc_act_fwd", hip.ACT[kind], orc.ptr(c_ref), orc.ptr(y_ref), M * N)
     gA, gB, gb = B(hip, A), B(hip, Bm), B(hip, bias)
     gC, gY = hip.Buffer.zeros((M, N)), hip.Buffer.zeros((M, N))
+    wsb = hip.lib().mle_gemm_ws_bytes(M, N, K, 1) if ws else 0
+    if ws:
+        assert wsb > 0  # the shape splits along K
+    gws = hip.Buffer(max(wsb, 256)) if ws else None
     hip.call("mle_gemm_act_fwd", None, 0, 0, M, N, K, 1.0, gA.ptr, K, gB.ptr, N, 0.0, gC.ptr, gb.ptr, hip.ACT[kind],
-             gY.ptr, None, 0)
+             gY.ptr, gws.ptr if ws else None, wsb)
     assert_close(gC.numpy(), c_ref, what=f"gemm_act_fwd C", **MM)
     assert_close(gY.numpy(), y_ref, what=f"gemm_act_fwd {kind}", **MM)
     # the epilogue applies the activation kernels' function to the stored C
     gY2 = hip.Buffer.zeros((M, N))
     hip.call("mle_act_fwd", None, hip.ACT[kind], gC.ptr, gY2.ptr, M * N)
+    if ws:  # the same function on the same values: the same bits
+        np.testing.assert_array_equal(gY.numpy().view(np.uint32), gY2.numpy().view(np.uint32))
     assert_close(gY.numpy(), gY2.numpy(), what=f"{kind} of the stored C", rtol=1e-6, atol_scale=1e-7)
 
 
