@@ -84,6 +84,15 @@ int mle_scalar_last(float* dst);
  * capture; a caller that noted it can tell whether the slot still holds its
  * own graph's value (any value or pointer may be null). */
 int mle_scalar_state(float* value, unsigned* published, unsigned* issued);
+/* Mark the slot empty (published sequence number 0), and wait -- spinning,
+ * like mle_read_scalar -- until the last number published is `seq`, then
+ * return the value.  A caller that replays a recorded graph (which publishes
+ * the same number on every replay) clears the slot before the launch and
+ * reads the loss as soon as the replay publishes it, instead of after the
+ * stream drains.  expect fails (MLE_ERR_INVALID) when the stream drains
+ * without `seq` being the last number published. */
+int mle_scalar_clear(void);
+int mle_scalar_expect(mle_stream stream, unsigned seq, float* dst);
 
 /* Graphs.  The work a caller enqueues on `stream` between capture_begin and
  * capture_end is recorded (not run) into a graph, instantiated once;

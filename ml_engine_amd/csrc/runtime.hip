@@ -264,6 +264,43 @@ int mle_scalar_state(float* value, unsigned* published, unsigned* issued) {
   return MLE_OK;
 }
 
+int mle_scalar_clear(void) {
+  int dev = 0;
+  MLE_HIP(hipGetDevice(&dev));
+  MLE_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "mle_scalar_clear: device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_slot_mu[dev]);
+  if (g_slot[dev]) __atomic_store_n(&g_slot[dev]->seq, 0u, __ATOMIC_RELEASE);
+  return MLE_OK;
+}
+
+int mle_scalar_expect(mle_stream stream, unsigned seq, float* dst) {
+  MLE_CHECK_ARG(dst != nullptr && seq != 0, "mle_scalar_expect: bad argument");
+  int dev = 0;
+  MLE_HIP(hipGetDevice(&dev));
+  MLE_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "mle_scalar_expect: device %d out of range", dev);
+  std::unique_lock<std::mutex> lk(g_slot_mu[dev]);
+  ScalarSlot* slot = g_slot[dev];
+  MLE_CHECK_ARG(slot != nullptr, "mle_scalar_expect: no value was published on device %d", dev);
+  hipStream_t s = as_stream(stream);
+  // As scalar_read_finish: the stream is asked every 256 spins, and one that
+  // drained without this number published ends the wait.
+  for (unsigned long spins = 1;; ++spins) {
+    if (__atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) == seq) break;
+    if ((spins & 255) == 0) {
+      const hipError_t q = hipStreamQuery(s);
+      if (q == hipSuccess) {
+        if (__atomic_load_n(&slot->seq, __ATOMIC_ACQUIRE) == seq) break;
+        return set_error(MLE_ERR_INVALID, "mle_scalar_expect: the stream drained without publishing %u", seq);
+      }
+      if (q != hipErrorNotReady) return hip_error(q, "mle_scalar_expect");
+    }
+    __builtin_ia32_pause();
+  }
+  const unsigned bits = __atomic_load_n(&slot->bits, __ATOMIC_ACQUIRE);
+  memcpy(dst, &bits, sizeof(float));
+  return MLE_OK;
+}
+
 // ---- graphs ----------------------------------------------------------------
 struct mle_graph_s {
   hipGraph_t graph;

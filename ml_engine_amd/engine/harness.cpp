@@ -47,6 +47,7 @@ struct Model {
   // The sequence number the recorded pass publishes its loss with (0: it
   // publishes none, or more than one value), and this model's last loss.
   unsigned replay_seq = 0;
+  bool loss_spin = false;  // the slot was cleared before the replay: spin for replay_seq
   float loss = 0.0f;
   graph target;  // C1 / C4: the one-hot target node (mle_model_target_read)
 };
@@ -343,6 +344,15 @@ int mle_model_step_graph(void* h, float lr, int mode) {
     m->replay_mode = pass;
     m->replay_seq = issued1 == issued0 + 1 ? issued1 : 0u;
   }
+  // The previous replay's loss has been read (or there was none), so no
+  // earlier replay of this graph can still publish: clear the slot, and the
+  // loss read waits for this replay's number only as long as the forward takes.
+  m->loss_spin = false;
+  if ((pass & MLE_STEP_FORWARD) && m->replay_seq && !m->loss_in_slot) {
+    int rc = mle_scalar_clear();
+    if (rc) return rc;
+    m->loss_spin = true;
+  }
   int rc = mle_graph_launch(m->replay, s);
   if (rc) return rc;
   m->loss_in_slot = (pass & MLE_STEP_FORWARD) != 0;
@@ -367,8 +377,15 @@ int mle_model_target_read(void* h, float* host, size_t count) {
 float mle_model_loss(void* h) {
   auto* m = static_cast<Model*>(h);
   if (m->loss_in_slot) {
-    check(mle_stream_sync(mle::stream()), "loss read-back");
     float v = 0.0f;
+    if (m->loss_spin && mle_scalar_expect(mle::stream(), m->replay_seq, &v) == MLE_OK) {
+      m->loss = v;
+      GraphOperations::loss = v;
+      m->loss_in_slot = false;
+      m->loss_spin = false;
+      return m->loss;
+    }
+    check(mle_stream_sync(mle::stream()), "loss read-back");
     unsigned published = 0;
     check(mle_scalar_state(&v, &published, nullptr), "loss read-back");
     if (m->replay_seq == 0 || published != m->replay_seq)

@@ -33,6 +33,8 @@ SIGNATURES: dict[str, tuple] = {
     "mle_read_scalar": (I, [P, P, P]),
     "mle_scalar_last": (I, [P]),
     "mle_scalar_state": (I, [P, P, P]),
+    "mle_scalar_clear": (I, []),
+    "mle_scalar_expect": (I, [P, C.c_uint, P]),
     "mle_graph_capture_begin": (I, [P]),
     "mle_graph_capture_end": (I, [P, P]),
     "mle_graph_launch": (I, [P, P]),
