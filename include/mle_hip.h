@@ -679,6 +679,24 @@ int mle_embed_scatter_add(mle_stream stream, float* table, const float* grad, co
 int mle_embed_grad(mle_stream stream, float* dtable, const float* grad, const int32_t* keys,
                    int batch, int clen, int max_clen, int dim, int vocab, int accumulate,
                    void* ws, size_t ws_bytes);
+/* Bytes of the token index that mle_embed_gather_indexed builds ({start, count,
+ * first two tokens} per table row, then the tokens grouped by row in token
+ * order); 0 when the vocabulary is above 16384 rows (no index: use
+ * mle_embed_gather and mle_embed_grad). */
+size_t mle_embed_index_bytes(int batch, int clen, int vocab);
+/* mle_embed_gather (keys outside [0, vocab) give zero rows) that, in the same
+ * launch, builds the index of the tokens per table row into `index` (16-byte
+ * aligned, mle_embed_index_bytes long).  The Embedding forward of a training
+ * step: GatherEmbeddings (Engine/kernels.cu:2279-2296). */
+int mle_embed_gather_indexed(mle_stream stream, float* out, const float* table, const int32_t* keys,
+                             int batch, int clen, int max_clen, int dim, int vocab,
+                             void* index, size_t index_bytes);
+/* mle_embed_grad for the keys indexed by the last mle_embed_gather_indexed on
+ * `index` (same batch, clen and vocab): the same bits, with no key scan --
+ * the Embedding backward (KeyUpdate into the table gradient,
+ * Engine/kernels.cu:1536-1549). */
+int mle_embed_grad_indexed(mle_stream stream, float* dtable, const float* grad, const void* index,
+                           int batch, int clen, int dim, int vocab, int accumulate);
 /* out[(b*clen + s)*vocab + key] = 1 for valid keys (out must be zeroed).
  * OneHotEmbeddings (Engine/kernels.cu:1551-1560). */
 int mle_onehot(mle_stream stream, float* out, const int32_t* keys, int batch, int clen, int max_clen, int vocab);

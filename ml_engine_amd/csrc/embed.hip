@@ -137,6 +137,42 @@ __global__ __launch_bounds__(SORT_NT) void sort_chunk_kernel(const int32_t* __re
 // No sort buffer and no second launch; the result does not depend on the order
 // the atomics ran in.  Chunks are applied in token order.  Step 3 costs the
 // row's token count per entry, which is small for a batch over a vocabulary.
+__device__ __forceinline__ int key_at(const int32_t* __restrict__ keys, int t, int clen, int max_clen) {
+  return clen == max_clen ? keys[t] : keys[(size_t)(t / clen) * max_clen + t % clen];
+}
+
+// Keys of tokens t0 + threadIdx.x + k NT, k < PER, into kv, every load issued
+// before any is used (a load per branch would wait for each in turn).  Tokens
+// past the end read the last token's key; the caller masks them.  ntok >= 1.
+template <int PER, int NT>
+__device__ __forceinline__ void load_keys(const int32_t* __restrict__ keys, int t0, int ntok, int clen, int max_clen,
+                                          int (&kv)[PER]) {
+  if (clen == max_clen) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) kv[k] = keys[min(t0 + (int)threadIdx.x + k * NT, ntok - 1)];
+  } else {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int t = min(t0 + (int)threadIdx.x + k * NT, ntok - 1);
+      kv[k] = keys[(size_t)(t / clen) * max_clen + t % clen];
+    }
+  }
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave in DPP steps (no LDS
+// round trips): within each row of 16 lanes by shifts of 1, 2, 4 and 8 (lanes
+// shifted in from outside the row add 0), then lane 15's row total into rows
+// 1 and 3 and lane 31's running total into rows 2 and 3.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
+}
+
 constexpr int RS_NT = 1024;
 constexpr int RS_CHUNK = 8192;  // tokens per pass (LDS: two 32 KB lists)
 constexpr int RS_RMAX = 64;     // rows per workgroup
@@ -160,16 +196,11 @@ __global__ __launch_bounds__(RS_NT) void range_scatter_kernel(float* __restrict_
     if (tid < nrows) sbin[tid] = 0;
     // this thread's tokens t0 + tid + k * RS_NT: their row within the range
     // (negative keys wrap past nrows), kept for the placement pass
+    int kv[PER];
+    load_keys<PER, RS_NT>(keys, t0, ntok, clen, max_clen, kv);
     unsigned rel[PER];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int i = tid + k * RS_NT, t = t0 + i;
-      rel[k] = 0xffffffffu;
-      if (i < count) {
-        const size_t at = clen == max_clen ? (size_t)t : (size_t)(t / clen) * max_clen + t % clen;
-        rel[k] = (unsigned)(keys[at] - v_lo);
-      }
-    }
+    for (int k = 0; k < PER; ++k) rel[k] = tid + k * RS_NT < count ? (unsigned)(kv[k] - v_lo) : 0xffffffffu;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < PER; ++k)
@@ -177,12 +208,7 @@ __global__ __launch_bounds__(RS_NT) void range_scatter_kernel(float* __restrict_
     __syncthreads();
     if (wid == 0) {
       const int c = lane < nrows ? sbin[lane] : 0;
-      int incl = c;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += y;
-      }
+      const int incl = wave_incl_scan(c);
       if (lane < nrows) {
         sstart[lane] = incl - c;
         sbin[lane] = incl;  // the row's end: the placement counts it down
@@ -211,18 +237,48 @@ __global__ __launch_bounds__(RS_NT) void range_scatter_kernel(float* __restrict_
       if (b == e && !first) continue;
       float* row = table + (size_t)(v_lo + r) * dim;
       if (VEC) {
-        for (int d = 4 * lane; d < dim; d += 256) {
-          // in flight with the gradient loads
-          f32x4 v = first ? f32x4{0.f, 0.f, 0.f, 0.f} : *reinterpret_cast<const f32x4*>(row + d);
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          for (int j = b; j < e; ++j) {
-            const f32x4 g = *reinterpret_cast<const f32x4*>(grad + (size_t)(t0 + slist[j]) * dim + d);
+        // a wave covers 512 floats per pass: lane l holds float4s l and l + 64,
+        // and two tokens' loads are in flight before either is added
+        for (int d0 = 0; d0 < dim; d0 += 512) {
+          const int da = d0 + 4 * lane, db = da + 256;
+          const bool ha = da < dim, hb = db < dim;
+          const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+          f32x4 va = first || !ha ? z : *reinterpret_cast<const f32x4*>(row + da);
+          f32x4 vb = first || !hb ? z : *reinterpret_cast<const f32x4*>(row + db);
+          f32x4 aa = z, ab = z;
+          int j = b;
+          for (; j + 1 < e; j += 2) {
+            const float* g0 = grad + (size_t)(t0 + slist[j]) * dim;
+            const float* g1 = grad + (size_t)(t0 + slist[j + 1]) * dim;
+            const f32x4 x0 = ha ? *reinterpret_cast<const f32x4*>(g0 + da) : z;
+            const f32x4 y0 = hb ? *reinterpret_cast<const f32x4*>(g0 + db) : z;
+            const f32x4 x1 = ha ? *reinterpret_cast<const f32x4*>(g1 + da) : z;
+            const f32x4 y1 = hb ? *reinterpret_cast<const f32x4*>(g1 + db) : z;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc[c] += g[c];
+            for (int c = 0; c < 4; ++c) {
+              aa[c] += x0[c];
+              ab[c] += y0[c];
+              aa[c] += x1[c];
+              ab[c] += y1[c];
+            }
+          }
+          if (j < e) {
+            const float* g0 = grad + (size_t)(t0 + slist[j]) * dim;
+            const f32x4 x0 = ha ? *reinterpret_cast<const f32x4*>(g0 + da) : z;
+            const f32x4 y0 = hb ? *reinterpret_cast<const f32x4*>(g0 + db) : z;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              aa[c] += x0[c];
+              ab[c] += y0[c];
+            }
           }
 #pragma unroll
-          for (int c = 0; c < 4; ++c) v[c] += scale * acc[c];
-          *reinterpret_cast<f32x4*>(row + d) = v;
+          for (int c = 0; c < 4; ++c) {
+            va[c] += scale * aa[c];
+            vb[c] += scale * ab[c];
+          }
+          if (ha) *reinterpret_cast<f32x4*>(row + da) = va;
+          if (hb) *reinterpret_cast<f32x4*>(row + db) = vb;
         }
       } else {
         for (int d = lane; d < dim; d += 64) {
@@ -233,6 +289,318 @@ __global__ __launch_bounds__(RS_NT) void range_scatter_kernel(float* __restrict_
       }
     }
     __syncthreads();  // the next chunk reuses the lists
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Token index per table row, built by the forward gather for the backward.
+//
+// rinfo[v] = {start, count, tok0, tok1}: the tokens whose key is v are, in
+// token order, list[start .. start + count); tok0 and tok1 repeat the first two
+// (-1 where absent), so a row with at most two tokens costs the backward one
+// 16-byte load.  Keys outside [0, vocab) are in no row.
+//
+// One launch does both jobs.  Workgroups g < nix each index IX_R table rows
+// [g IX_R, g IX_R + IX_R): they read every key (as the range scatter does),
+// count the row's tokens and the valid tokens with smaller keys (the range's
+// start in `list`, so no global counter is needed), and order each row's
+// tokens by token index in LDS.  The workgroups after them gather table rows,
+// two tokens per wave at a time.  The index work is latency-bound and small, so
+// it runs inside the time the gather takes to stream its bytes.
+constexpr int IX_NT = 1024;
+constexpr int IX_R = 64;          // table rows per index workgroup (one wave's scan)
+constexpr int IX_CHUNK = 8192;    // tokens per pass
+// the backward restarts its sums where the range scatter starts a new chunk
+static_assert(IX_CHUNK == RS_CHUNK, "per-chunk sums must match the range scatter");
+constexpr int IX_VMAX = RS_VMAX;  // larger vocabularies use the scatter paths
+
+// Exclusive scan of cnt over lanes [0, n) of wave 0: start[l] (and start[n]).
+__device__ __forceinline__ void wave_starts(const int* cnt, int* start, int n, int lane) {
+  const int c = lane < n ? cnt[lane] : 0;
+  const int incl = wave_incl_scan(c);
+  if (lane < n) start[lane] = incl - c;
+  if (lane == n - 1) start[n] = incl;
+}
+
+struct IndexLds {
+  int perm[IX_CHUNK];  // (row << 16) | chunk-local token, per row in arrival order
+  int total[IX_R];     // tokens per row
+  int start[IX_R + 1]; // row starts within the range
+  int ccnt[IX_R];      // tokens per row in this chunk
+  int cstart[IX_R + 1];
+  int placed[IX_R];    // tokens per row in earlier chunks
+  int tok[2 * IX_R];   // first two tokens per row
+  int below;           // valid tokens with keys below the range
+};
+
+__device__ __forceinline__ void build_index(IndexLds& L, const int32_t* __restrict__ keys, int clen, int max_clen,
+                                            int ntok, int vocab, int range, int4* __restrict__ rinfo,
+                                            int32_t* __restrict__ list) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int v_lo = range * IX_R;
+  const int nrows = min(IX_R, vocab - v_lo);
+  constexpr int PER = IX_CHUNK / IX_NT;
+  if (tid < IX_R) {
+    L.total[tid] = 0;
+    L.placed[tid] = 0;
+    L.tok[2 * tid] = -1;
+    L.tok[2 * tid + 1] = -1;
+  }
+  if (tid == 0) L.below = 0;
+  // pass 1: tokens per row, and valid tokens below the range.  ent[k] is the
+  // token's row in the range | its arrival position in the row << 8, or ~0
+  // for a token outside the range; with one chunk it is kept for the placement.
+  const bool one = ntok <= IX_CHUNK;
+  unsigned ent[PER];
+  for (int t0 = 0; t0 < ntok; t0 += IX_CHUNK) {
+    int kv[PER];
+    load_keys<PER, IX_NT>(keys, t0, ntok, clen, max_clen, kv);
+    if (t0 == 0) __syncthreads();  // the counters above are cleared (the loads are in flight)
+    int below = 0;  // the wave's count, from ballots
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const bool in = t0 + tid + k * IX_NT < ntok;
+      const unsigned rel = (unsigned)(kv[k] - v_lo);
+      ent[k] = in && rel < (unsigned)nrows ? rel : 0xffffffffu;
+      below += __popcll(__ballot(in && (unsigned)kv[k] < (unsigned)v_lo));
+    }
+    // all the atomics issued before any result is used
+    unsigned pos[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      pos[k] = 0;
+      if (ent[k] != 0xffffffffu) pos[k] = (unsigned)atomicAdd(&L.total[ent[k]], 1);
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (ent[k] != 0xffffffffu) ent[k] |= pos[k] << 8;
+    if (lane == 0 && below) atomicAdd(&L.below, below);
+  }
+  __syncthreads();
+  if (wid == 0) wave_starts(L.total, L.start, nrows, lane);
+  __syncthreads();
+  const int base = L.below;
+  for (int t0 = 0; t0 < ntok; t0 += IX_CHUNK) {
+    const int* cs = L.start;  // with one chunk, the chunk's rows are the rows
+    if (!one) {
+      if (tid < IX_R) L.ccnt[tid] = 0;
+      int kv[PER];
+      load_keys<PER, IX_NT>(keys, t0, ntok, clen, max_clen, kv);
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        const unsigned rel = (unsigned)(kv[k] - v_lo);
+        ent[k] = t0 + tid + k * IX_NT < ntok && rel < (unsigned)nrows ? rel : 0xffffffffu;
+      }
+      __syncthreads();
+      unsigned pos[PER];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        pos[k] = 0;
+        if (ent[k] != 0xffffffffu) pos[k] = (unsigned)atomicAdd(&L.ccnt[ent[k]], 1);
+      }
+#pragma unroll
+      for (int k = 0; k < PER; ++k)
+        if (ent[k] != 0xffffffffu) ent[k] |= pos[k] << 8;
+      __syncthreads();
+      if (wid == 0) wave_starts(L.ccnt, L.cstart, nrows, lane);
+      __syncthreads();
+      cs = L.cstart;
+    }
+    // the row starts read for every slot (cs[nrows] for tokens outside the
+    // range) so that the reads are all in flight before the writes
+    int at[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) at[k] = cs[min(ent[k] & 0xffu, (unsigned)nrows)];
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (ent[k] != 0xffffffffu) L.perm[at[k] + (ent[k] >> 8)] = (int)((ent[k] & 0xffu) << 16) | (tid + k * IX_NT);
+    __syncthreads();
+    // rank of each entry among its row's entries of the chunk: the row's
+    // tokens in token order (the cost is the row's count per entry)
+    const int kept = cs[nrows];
+    for (int p = tid; p < kept; p += IX_NT) {
+      const int r = L.perm[p] >> 16, i = L.perm[p] & 0xffff;
+      const int b = cs[r], e = cs[r + 1];
+      int rank = 0;
+      for (int q = b; q < e; ++q) rank += (L.perm[q] & 0xffff) < i;
+      const int at = L.placed[r] + rank;
+      list[base + L.start[r] + at] = t0 + i;
+      if (at < 2) L.tok[2 * r + at] = t0 + i;
+    }
+    __syncthreads();
+    if (!one && tid < nrows) L.placed[tid] += L.ccnt[tid];
+  }
+  __syncthreads();
+  if (tid < nrows) rinfo[v_lo + tid] = make_int4(base + L.start[tid], L.total[tid], L.tok[2 * tid], L.tok[2 * tid + 1]);
+}
+
+// The gather side: wave w of the gather workgroups copies tokens w, w + W, ...
+// IX_TPW at a time, all their loads in flight before the stores.  Keys outside
+// [0, vocab) give zero rows.
+constexpr int IX_TPW = 4;  // measured at 8192 x 512: 4 beats 2 and 1 (fewer waves to dispatch)
+template <bool VEC>
+__device__ __forceinline__ void gather_rows(float* __restrict__ out, const float* __restrict__ table,
+                                            const int32_t* __restrict__ keys, int clen, int max_clen, int ntok,
+                                            int dim, int vocab, int gblock, int ngblocks) {
+  const int lane = threadIdx.x & 63;
+  const int nw = ngblocks * (IX_NT / 64);
+  for (int t = gblock * (IX_NT / 64) + (threadIdx.x >> 6); t < ntok; t += IX_TPW * nw) {
+    const float* src[IX_TPW];
+    bool ok[IX_TPW];
+#pragma unroll
+    for (int j = 0; j < IX_TPW; ++j) {
+      const int u = t + j * nw;
+      const int key = u < ntok ? key_at(keys, u, clen, max_clen) : -1;
+      ok[j] = (unsigned)key < (unsigned)vocab;
+      src[j] = table + (size_t)(ok[j] ? key : 0) * dim;
+    }
+    if (VEC) {
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      for (int d0 = 0; d0 < dim; d0 += 512) {
+        const int da = d0 + 4 * lane, db = da + 256;
+        const bool ha = da < dim, hb = db < dim;
+        f32x4 a[IX_TPW], b[IX_TPW];
+#pragma unroll
+        for (int j = 0; j < IX_TPW; ++j) {
+          a[j] = ha && ok[j] ? *reinterpret_cast<const f32x4*>(src[j] + da) : z;
+          b[j] = hb && ok[j] ? *reinterpret_cast<const f32x4*>(src[j] + db) : z;
+        }
+#pragma unroll
+        for (int j = 0; j < IX_TPW; ++j) {
+          const int u = t + j * nw;
+          if (u >= ntok) break;
+          float* o = out + (size_t)u * dim;
+          if (ha) *reinterpret_cast<f32x4*>(o + da) = a[j];
+          if (hb) *reinterpret_cast<f32x4*>(o + db) = b[j];
+        }
+      }
+    } else {
+      for (int d = lane; d < dim; d += 64) {
+        float a[IX_TPW];
+#pragma unroll
+        for (int j = 0; j < IX_TPW; ++j) a[j] = ok[j] ? src[j][d] : 0.f;
+#pragma unroll
+        for (int j = 0; j < IX_TPW; ++j) {
+          const int u = t + j * nw;
+          if (u < ntok) out[(size_t)u * dim + d] = a[j];
+        }
+      }
+    }
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(IX_NT) void gather_index_kernel(float* __restrict__ out, const float* __restrict__ table,
+                                                             const int32_t* __restrict__ keys, int clen, int max_clen,
+                                                             int ntok, int dim, int vocab, int nix,
+                                                             int4* __restrict__ rinfo, int32_t* __restrict__ list) {
+  __shared__ IndexLds L;
+  // the index workgroups first, so that their latency-bound chain starts at
+  // once (measured: the other order is 1.9 us slower at 8192 x 512)
+  if ((int)blockIdx.x < nix)
+    build_index(L, keys, clen, max_clen, ntok, vocab, blockIdx.x, rinfo, list);
+  else
+    gather_rows<VEC>(out, table, keys, clen, max_clen, ntok, dim, vocab, blockIdx.x - nix, gridDim.x - nix);
+}
+
+// The embedding gradient from the index: one wave per table row sums the
+// row's gradient rows in token order, restarting the sum at every IX_CHUNK
+// boundary (v = v + sum of the chunk), which is exactly the range scatter's
+// arithmetic; so the bits equal mle_embed_grad's.  assign: v starts at 0 and
+// rows without tokens are written 0.
+template <bool VEC>
+__global__ __launch_bounds__(256) void index_grad_kernel(float* __restrict__ dtable, const float* __restrict__ grad,
+                                                         const int4* __restrict__ rinfo,
+                                                         const int32_t* __restrict__ list, int ntok, int dim,
+                                                         int vocab, int assign) {
+  const int lane = threadIdx.x & 63;
+  const int v = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v >= vocab) return;
+  const int4 ri = rinfo[v];
+  // An index built by the gather has 0 <= start, start + count <= ntok and
+  // token ids in [0, ntok).  Anything else reads as an empty row or a zero
+  // term, never as an access outside the list or the gradient.
+  const int cnt = ri.x >= 0 && ri.y >= 0 && (long long)ri.x + ri.y <= ntok ? ri.y : 0;
+  if (cnt == 0 && !assign) return;
+  float* row = dtable + (size_t)v * dim;
+  auto tok = [&](int j) { return j == 0 ? ri.z : j == 1 ? ri.w : list[ri.x + j]; };
+  auto ok = [&](int t) { return (unsigned)t < (unsigned)ntok; };
+  const bool one = ntok <= IX_CHUNK;
+  if (VEC) {
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    for (int d0 = 0; d0 < dim; d0 += 512) {
+      const int da = d0 + 4 * lane, db = da + 256;
+      const bool ha = da < dim, hb = db < dim;
+      f32x4 va = assign || !ha ? z : *reinterpret_cast<const f32x4*>(row + da);
+      f32x4 vb = assign || !hb ? z : *reinterpret_cast<const f32x4*>(row + db);
+      f32x4 aa = z, ab = z;
+      int j = 0;
+      if (one) {
+        // two tokens' loads in flight before either is added
+        for (; j + 1 < cnt; j += 2) {
+          const int t0 = tok(j), t1 = tok(j + 1);
+          const bool k0 = ok(t0), k1 = ok(t1);
+          const float* g0 = grad + (size_t)(k0 ? t0 : 0) * dim;
+          const float* g1 = grad + (size_t)(k1 ? t1 : 0) * dim;
+          const f32x4 x0 = ha && k0 ? *reinterpret_cast<const f32x4*>(g0 + da) : z;
+          const f32x4 y0 = hb && k0 ? *reinterpret_cast<const f32x4*>(g0 + db) : z;
+          const f32x4 x1 = ha && k1 ? *reinterpret_cast<const f32x4*>(g1 + da) : z;
+          const f32x4 y1 = hb && k1 ? *reinterpret_cast<const f32x4*>(g1 + db) : z;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            aa[c] += x0[c];
+            ab[c] += y0[c];
+            aa[c] += x1[c];
+            ab[c] += y1[c];
+          }
+        }
+      }
+      int chunk = cnt > 0 ? tok(j) / IX_CHUNK : 0;
+      for (; j < cnt; ++j) {
+        const int t = tok(j);
+        if (t / IX_CHUNK != chunk) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            va[c] += aa[c];
+            vb[c] += ab[c];
+          }
+          aa = z;
+          ab = z;
+          chunk = t / IX_CHUNK;
+        }
+        const bool k0 = ok(t);
+        const float* g0 = grad + (size_t)(k0 ? t : 0) * dim;
+        const f32x4 x0 = ha && k0 ? *reinterpret_cast<const f32x4*>(g0 + da) : z;
+        const f32x4 y0 = hb && k0 ? *reinterpret_cast<const f32x4*>(g0 + db) : z;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          aa[c] += x0[c];
+          ab[c] += y0[c];
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        va[c] += aa[c];
+        vb[c] += ab[c];
+      }
+      if (ha) *reinterpret_cast<f32x4*>(row + da) = va;
+      if (hb) *reinterpret_cast<f32x4*>(row + db) = vb;
+    }
+  } else {
+    for (int d = lane; d < dim; d += 64) {
+      float val = assign ? 0.f : row[d], acc = 0.f;
+      int chunk = cnt > 0 ? tok(0) / IX_CHUNK : 0;
+      for (int j = 0; j < cnt; ++j) {
+        const int t = tok(j);
+        if (t / IX_CHUNK != chunk) {
+          val += acc;
+          acc = 0.f;
+          chunk = t / IX_CHUNK;
+        }
+        acc += ok(t) ? grad[(size_t)t * dim + d] : 0.f;
+      }
+      row[d] = val + acc;
+    }
   }
 }
 
@@ -503,6 +871,60 @@ int mle_embed_grad(mle_stream stream, float* dtable, const float* grad, const in
                    int max_clen, int dim, int vocab, int accumulate, void* ws, size_t ws_bytes) {
   return embed_scatter(stream, dtable, grad, keys, batch, clen, max_clen, dim, vocab, 1.0f, accumulate ? 0 : 1, ws,
                        ws_bytes);
+}
+
+size_t mle_embed_index_bytes(int batch, int clen, int vocab) {
+  if (vocab <= 0 || vocab > IX_VMAX || batch < 0 || clen <= 0) return 0;
+  const size_t ntok = (size_t)batch * clen;
+  const size_t bytes = (size_t)vocab * sizeof(int4) + (ntok > 0 ? ntok : 1) * sizeof(int32_t);
+  return (bytes + 255) & ~(size_t)255;
+}
+
+int mle_embed_gather_indexed(mle_stream stream, float* out, const float* table, const int32_t* keys, int batch,
+                             int clen, int max_clen, int dim, int vocab, void* index, size_t index_bytes) {
+  MLE_CHECK_ARG(out && table && keys && index && batch >= 0 && clen > 0 && max_clen >= clen && dim > 0 && vocab > 0,
+                "mle_embed_gather_indexed: bad argument");
+  MLE_CHECK_ARG(vocab <= IX_VMAX, "mle_embed_gather_indexed: vocabulary above 16384 rows");
+  const long long ntok = (long long)batch * clen;
+  MLE_CHECK_ARG(ntok < 2147483647LL, "mle_embed_gather_indexed: too many tokens");
+  MLE_CHECK_ARG(aligned16(index), "mle_embed_gather_indexed: index not 16-byte aligned");
+  if (index_bytes < mle_embed_index_bytes(batch, clen, vocab))
+    return set_error(MLE_ERR_WORKSPACE, "mle_embed_gather_indexed: index buffer too small");
+  hipStream_t s = as_stream(stream);
+  int4* rinfo = static_cast<int4*>(index);
+  int32_t* list = reinterpret_cast<int32_t*>(rinfo + vocab);
+  const int nix = (vocab + IX_R - 1) / IX_R;
+  // 16 IX_TPW tokens per gather workgroup per pass
+  constexpr int per_wg = (IX_NT / 64) * IX_TPW;
+  const long long ng = ntok == 0 ? 0 : std::min<long long>((ntok + per_wg - 1) / per_wg, 2048);
+  const unsigned grid = (unsigned)(nix + ng);
+  if (dim % 4 == 0 && aligned16(out) && aligned16(table))
+    gather_index_kernel<true><<<grid, IX_NT, 0, s>>>(out, table, keys, clen, max_clen, (int)ntok, dim, vocab, nix,
+                                                     rinfo, list);
+  else
+    gather_index_kernel<false><<<grid, IX_NT, 0, s>>>(out, table, keys, clen, max_clen, (int)ntok, dim, vocab, nix,
+                                                      rinfo, list);
+  return check_launch("mle_embed_gather_indexed");
+}
+
+int mle_embed_grad_indexed(mle_stream stream, float* dtable, const float* grad, const void* index, int batch, int clen,
+                           int dim, int vocab, int accumulate) {
+  MLE_CHECK_ARG(dtable && grad && index && batch >= 0 && clen > 0 && dim > 0 && vocab > 0,
+                "mle_embed_grad_indexed: bad argument");
+  MLE_CHECK_ARG(vocab <= IX_VMAX, "mle_embed_grad_indexed: vocabulary above 16384 rows");
+  const long long ntok = (long long)batch * clen;
+  MLE_CHECK_ARG(ntok < 2147483647LL, "mle_embed_grad_indexed: too many tokens");
+  MLE_CHECK_ARG(aligned16(index), "mle_embed_grad_indexed: index not 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  const int4* rinfo = static_cast<const int4*>(index);
+  const int32_t* list = reinterpret_cast<const int32_t*>(rinfo + vocab);
+  const unsigned grid = (unsigned)((vocab + 3) / 4);
+  const int assign = accumulate ? 0 : 1;
+  if (dim % 4 == 0 && aligned16(dtable) && aligned16(grad))
+    index_grad_kernel<true><<<grid, 256, 0, s>>>(dtable, grad, rinfo, list, (int)ntok, dim, vocab, assign);
+  else
+    index_grad_kernel<false><<<grid, 256, 0, s>>>(dtable, grad, rinfo, list, (int)ntok, dim, vocab, assign);
+  return check_launch("mle_embed_grad_indexed");
 }
 
 

@@ -1390,14 +1390,29 @@ graph Embedding::forward(const int32_t* keys, int batch, int clen, int max_clen)
   const int V = vocab, D = dim;
   void* ws = ws_;
   const size_t wsb = ws_bytes_;
+  // The forward's gather also indexes the tokens of each table row (this
+  // node's own index: the keys do not change before its backward), so the
+  // backward only sums rows.  Vocabularies above the index's limit scan the
+  // keys in the backward instead.
+  const size_t ixb = mle_embed_index_bytes(batch, clen, V);
+  void* index = ixb ? mle::alloc_scratch(ixb) : nullptr;
   node->params = {T};
   node->forward = [=]() {
-    check(mle_embed_gather(mle::stream(), nd->output, T->output, keys, batch, clen, max_clen, D), "GatherEmbeddings");
+    if (index)
+      check(mle_embed_gather_indexed(mle::stream(), nd->output, T->output, keys, batch, clen, max_clen, D, V, index, ixb),
+            "GatherEmbeddings");
+    else
+      check(mle_embed_gather(mle::stream(), nd->output, T->output, keys, batch, clen, max_clen, D), "GatherEmbeddings");
   };
   node->backward = [=]() {
-    check(mle_embed_grad(mle::stream(), T->grad, nd->grad, keys, batch, clen, max_clen, D, V,
-                         mle::params_write_flag({T}), ws, wsb),
-          "Embedding gradient");
+    if (index)
+      check(mle_embed_grad_indexed(mle::stream(), T->grad, nd->grad, index, batch, clen, D, V,
+                                   mle::params_write_flag({T})),
+            "Embedding gradient");
+    else
+      check(mle_embed_grad(mle::stream(), T->grad, nd->grad, keys, batch, clen, max_clen, D, V,
+                           mle::params_write_flag({T}), ws, wsb),
+            "Embedding gradient");
   };
   node->zero_grad = [=]() {
     mle::defer_zero(nd);

@@ -138,6 +138,9 @@ SIGNATURES: dict[str, tuple] = {
     "mle_embed_scatter_ws_bytes": (SZ, [I, I]),
     "mle_embed_scatter_add": (I, [P, P, P, P, I, I, I, I, I, F, P, SZ]),
     "mle_embed_grad": (I, [P, P, P, P, I, I, I, I, I, I, P, SZ]),
+    "mle_embed_index_bytes": (SZ, [I, I, I]),
+    "mle_embed_gather_indexed": (I, [P, P, P, P, I, I, I, I, I, P, SZ]),
+    "mle_embed_grad_indexed": (I, [P, P, P, P, I, I, I, I, I]),
     "mle_onehot": (I, [P, P, P, I, I, I, I]),
     "mle_onehot_update": (I, [P, P, P, P, I, I, I, I]),
     "mle_argmax": (I, [P, P, I, I, P]),

@@ -1249,6 +1249,74 @@ def test_scatter_add_paths(hip, orc, batch, clen, dim, vocab, hot):
         np.testing.assert_array_equal(gt.numpy().view(np.uint32), w.view(np.uint32))
 
 
+@pytest.mark.parametrize("batch,clen,maxc,dim,vocab,hot", [
+    (32, 256, 256, 512, 8000, 0),  # the C4 embedding
+    (4, 600, 600, 64, 300, 0), (2, 50, 50, 1100, 40, 0), (3, 300, 310, 700, 500, 0),  # padded key rows
+    (40, 300, 300, 16, 1000, 0),   # 12000 tokens: two chunks, summed chunk by chunk
+    (3, 5000, 5000, 8, 70, 1),     # two chunks with one id on most tokens
+    (4, 100, 100, 33, 50, 0),      # rows not a multiple of 4 floats
+    (8, 1024, 1024, 32, 100, 1),   # one id on ~7000 tokens of one chunk
+    (2, 64, 64, 4, 16384, 0),      # the largest vocabulary with an index
+    (0, 16, 16, 8, 130, 0)])       # no tokens: every row empty
+def test_embed_index(hip, batch, clen, maxc, dim, vocab, hot):
+    """The gather that indexes the tokens per table row, and the gradient from
+    that index: the gather's bits are mle_embed_gather's, the index lists each
+    row's tokens in token order starting at the count of valid smaller keys,
+    and the gradient's bits are mle_embed_grad's (chunk-wise sums included),
+    assigning and accumulating."""
+    L = hip.lib()
+    r = rng(batch * 7 + clen + dim + vocab)
+    keys = r.integers(-2, vocab, (max(batch, 1), maxc)).astype(np.int32)[:batch]
+    if hot and batch:
+        keys[r.random(keys.shape) < 0.85] = 7
+    if batch:
+        keys[:, :3] = 3
+        keys[0, clen - 1] = np.iinfo(np.int32).min
+    keys = np.ascontiguousarray(keys)
+    table = r.standard_normal((vocab, dim), dtype=np.float32)
+    grad = r.standard_normal((max(batch * clen, 1), dim), dtype=np.float32)
+    nb = L.mle_embed_index_bytes(batch, clen, vocab)
+    assert nb >= vocab * 16 + batch * clen * 4 and nb % 256 == 0
+    assert L.mle_embed_index_bytes(batch, clen, 16385) == 0
+    gk = B(hip, keys if batch else np.zeros((1, maxc), np.int32))
+    gt, gg = B(hip, table), B(hip, grad)
+    idx = hip.Buffer(nb)
+    out = hip.Buffer.zeros((max(batch * clen, 1), dim))
+    hip.call("mle_embed_gather_indexed", None, out.ptr, gt.ptr, gk.ptr, batch, clen, maxc, dim, vocab, idx.ptr, nb)
+    if batch:
+        ref = hip.Buffer.zeros((batch * clen, dim))
+        hip.call("mle_embed_gather", None, ref.ptr, gt.ptr, gk.ptr, batch, clen, maxc, dim)
+        np.testing.assert_array_equal(out.numpy().view(np.uint32), ref.numpy().view(np.uint32))
+    # the index against numpy
+    raw = idx.numpy(dtype=np.int32)
+    rinfo = raw[:4 * vocab].reshape(vocab, 4)
+    flat = keys[:, :clen].ravel()
+    valid = (flat >= 0) & (flat < vocab)
+    counts = np.bincount(flat[valid], minlength=vocab)
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    np.testing.assert_array_equal(rinfo[:, 0], starts)
+    np.testing.assert_array_equal(rinfo[:, 1], counts)
+    order = np.argsort(np.where(valid, flat, vocab), kind="stable")[:int(valid.sum())]
+    lst = raw[4 * vocab:4 * vocab + order.size]
+    np.testing.assert_array_equal(lst, order)
+    firsts = np.full((vocab, 2), -1, np.int64)
+    for j in (0, 1):
+        has = counts > j
+        firsts[has, j] = order[starts[has] + j]
+    np.testing.assert_array_equal(rinfo[:, 2:], firsts)
+    # the gradient from the index: mle_embed_grad's bits
+    ws = hip.Buffer(L.mle_embed_scatter_ws_bytes(batch, clen))
+    for accumulate, base in ((0, np.full_like(table, np.nan)), (1, table)):
+        want, got = B(hip, base), B(hip, base)
+        if batch:
+            hip.call("mle_embed_grad", None, want.ptr, gg.ptr, gk.ptr, batch, clen, maxc, dim, vocab, accumulate,
+                     ws.ptr, ws.nbytes)
+        else:
+            want = B(hip, np.zeros_like(table) if accumulate == 0 else table)
+        hip.call("mle_embed_grad_indexed", None, got.ptr, gg.ptr, idx.ptr, batch, clen, dim, vocab, accumulate)
+        np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32))
+
+
 @pytest.mark.parametrize("kind", [2, 1, 0])  # MLE_SILU, MLE_GELU, MLE_RELU
 @pytest.mark.parametrize("n", [4099 * 4, 1001])  # float4 body; a scalar tail
 def test_add_act_fused(hip, kind, n):
