@@ -559,18 +559,11 @@ __device__ __forceinline__ void direct_tile(const GemmArgs& g, int tm, int tn, i
   }
 }
 
-template <int TA, int TB, bool COLSUM, int KD, int D, int OCC, bool TERMS = false>
-__global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
-  int tm, tn;
-  tile_of(gridDim.x, gridDim.y, tm, tn);
-  direct_tile<TA, TB, COLSUM, KD, D, TERMS>(g, tm, tn, (int)blockIdx.z);
-}
-
-// Tile (tm, tn) and batch item z of work item L of a persistent launch over
-// `items` = gx * gy * batch tiles.  The same XCD-aware order as tile_of: item
-// L runs on XCD L % 8 (the grid is a multiple of 8 workgroups, dispatched
-// round-robin), XCD x owns a contiguous logical range, walked in groups of 8
-// tile-rows per batch item.  A bijection on [0, items).
+// Tile (tm, tn) and batch item z of work item L of a launch over `items` =
+// gx * gy * batch tiles.  The same XCD-aware order as tile_of: item L runs on
+// XCD L % 8 (workgroups are dispatched round-robin), XCD x owns a contiguous
+// logical range, walked in groups of 8 tile-rows per batch item.  A bijection
+// on [0, items).
 __device__ __forceinline__ void item_tile(int L, int items, int gx, int gy, int& tm, int& tn, int& z) {
   const int q = items / kXcds, r = items % kXcds, x = L % kXcds;
   const int logical = x * q + min(x, r) + L / kXcds;
@@ -584,6 +577,20 @@ __device__ __forceinline__ void item_tile(int L, int items, int gx, int gy, int&
   const int in_group = t - grp * per_group;
   tm = first_m + in_group % rows;
   tn = in_group / rows;
+}
+
+// One tile per workgroup.  The tile and the batch item / K split come from
+// the workgroup's linear id over the whole grid (x, then y, then z), so each
+// XCD gets a contiguous range that stays within one split: the column tiles
+// that share an A row panel share that XCD's L2 (with z walked per slice,
+// every XCD read every panel of a split -- 3.6x the algorithmic bytes for a
+// 2048 x 512 x 8192 weight gradient in 4 splits).
+template <int TA, int TB, bool COLSUM, int KD, int D, int OCC, bool TERMS = false>
+__global__ __launch_bounds__(NT, OCC) void gemm_direct_kernel(GemmArgs g) {
+  int tm, tn, z;
+  const int L = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+  item_tile(L, (int)(gridDim.x * gridDim.y * gridDim.z), gridDim.x, gridDim.y, tm, tn, z);
+  direct_tile<TA, TB, COLSUM, KD, D, TERMS>(g, tm, tn, z);
 }
 
 // Persistent register-direct GEMM for grids of more 128 x 128 tiles than two
@@ -855,9 +862,13 @@ __global__ __launch_bounds__(256) void rowstats_kernel(const float* __restrict__
 // (Engine/engine.cu:3553-3560) usually each fill about one workgroup per CU
 // with work items of equal depth; launched together they run two per CU in
 // a single round.
+// Problem 1 starts at workgroup start1, items0 rounded up to a multiple of 8
+// (the workgroups between do nothing), so that its item L runs on XCD L % 8
+// as item_tile assumes.
 struct PairGrid {
   int items0, gx0, gy0;
   int items1, gx1, gy1;
+  int start1;
 };
 
 template <int TA0, int TB0, bool CS0, bool T0, int TA1, int TB1, bool CS1, bool T1>
@@ -867,8 +878,8 @@ __global__ __launch_bounds__(NT, 2) void gemm_pair_kernel(GemmArgs g0, GemmArgs 
   if (w < pg.items0) {
     item_tile(w, pg.items0, pg.gx0, pg.gy0, tm, tn, bz);
     direct_tile<TA0, TB0, CS0, 16, 3, T0>(g0, tm, tn, bz);
-  } else {
-    item_tile(w - pg.items0, pg.items1, pg.gx1, pg.gy1, tm, tn, bz);
+  } else if (w >= pg.start1) {
+    item_tile(w - pg.start1, pg.items1, pg.gx1, pg.gy1, tm, tn, bz);
     direct_tile<TA1, TB1, CS1, 16, 3, T1>(g1, tm, tn, bz);
   }
 }
@@ -1488,8 +1499,9 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, 
   // workgroup per CU each, and the dX product needs no workspace (the dW
   // product's split partials own it).
   if (n0 > 0 && n1 > 0 && n0 <= ncu && n1 <= ncu && P0.g.splits == 1) {
-    const PairGrid pg{(int)n0, (int)P0.grid.x, (int)P0.grid.y, (int)n1, (int)P1.grid.x, (int)P1.grid.y};
-    const dim3 grid((unsigned)(n0 + n1));
+    const int start1 = (int)((n0 + 7) / 8 * 8);
+    const PairGrid pg{(int)n0, (int)P0.grid.x, (int)P0.grid.y, (int)n1, (int)P1.grid.x, (int)P1.grid.y, start1};
+    const dim3 grid((unsigned)(start1 + n1));
     const bool t0 = P0.g.kterms > 1;
     {
       ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
