@@ -694,6 +694,385 @@ __device__ __forceinline__ void bwd_q_tile(const AttnArgs& a, const Slice& sl, i
   }
 }
 
+// ---------------------------------------------------------------------------
+// Causal whole-slice passes (seq <= 256) with the scores or probabilities kept
+// in LDS.  The output passes give every wave two 16-row blocks b and
+// nb - 1 - b (nb = seq / 16): under the mask block b's work grows with b, so
+// every wave carries nb + 1 block-chunks, and no wave is left running alone on
+// its SIMD at the end (with 32-row tiles balanced only per SIMD pair, the
+// heaviest wave had twice the average work).  Chunks a block does not reach
+// (wholly above the diagonal, all-zero probabilities) are skipped.
+
+// Statistics for keys k0 .. k0 + 31 in two passes.  Pass A: S^T = K Q^T over
+// every query chunk (the maximum is taken over every row), each lane's running
+// maximum, and the blocks on or below the diagonal written to sst as
+// stats_tile<true, true> writes them.  Pass B: the wave reads its own kept
+// blocks back and sums exp(S - m_c) over the unmasked queries with the final
+// maximum -- one exponential per kept score, where an online sum rescales in
+// every chunk.
+__device__ __forceinline__ void stats_kept(const AttnArgs& a, const Slice& sl, int k0, float* sst) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+  const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
+  const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
+  f32x4 ka[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) ka[i][s] = bld4(K, sl.base + (uint32_t)(k0 + 16 * i + lr) * a.ld + 16 * s + 4 * q);
+  float m[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m[i][r] = -FLT_MAX;
+  struct Chunk {
+    f32x4 qb[2][4];
+  };
+  auto fetch = [&](int c, Chunk& ch) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        ch.qb[n][s] = bld4(Q, sl.base + (uint32_t)(TW * c + 16 * n + lr) * a.ld + 16 * s + 4 * q);
+  };
+  auto compute = [&](int c, const Chunk& ch) {
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][n] = mfma4(ka[i][s][j], ch.qb[n][s][j], acc[i][n]);
+      }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        const int kb = k0 / 16 + i, qb = 2 * c + n;
+        if (kb <= qb) *reinterpret_cast<f32x4*>(sst + (qb * (qb + 1) / 2 + kb) * 256 + 4 * lane) = acc[i][n];
+      }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) m[i][r] = fmaxf(m[i][r], fmaxf(a.scale * acc[i][0][r], a.scale * acc[i][1][r]));
+  };
+  chunk_loop<Chunk>(0, a.seq / TW, fetch, compute);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) m[i][r] = fmaxf(m[i][r], __shfl_xor(m[i][r], off, 64));
+  // The blocks read below are this wave's own writes.
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  float l[2][4];
+  const int nb = a.seq / 16;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int kb = k0 / 16 + i;
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(sst + (kb * (kb + 1) / 2 + kb) * 256 + 4 * lane);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)  // the diagonal block: query lr against key 4q + r
+      l[i][r] = lr >= 4 * q + r ? __expf(a.scale * d4[r] - m[i][r]) : 0.f;
+    int qb = kb + 1;
+    for (; qb + 1 < nb; qb += 2) {
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(sst + (qb * (qb + 1) / 2 + kb) * 256 + 4 * lane);
+      const f32x4 s1 = *reinterpret_cast<const f32x4*>(sst + ((qb + 1) * (qb + 2) / 2 + kb) * 256 + 4 * lane);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        l[i][r] += __expf(a.scale * s0[r] - m[i][r]);
+        l[i][r] += __expf(a.scale * s1[r] - m[i][r]);
+      }
+    }
+    if (qb < nb) {
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(sst + (qb * (qb + 1) / 2 + kb) * 256 + 4 * lane);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) l[i][r] += __expf(a.scale * s0[r] - m[i][r]);
+    }
+  }
+  // Sum over the 16 lanes of a key (a + b == b + a: every lane ends equal).
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) l[i][r] += __shfl_xor(l[i][r], off, 64);
+  if (lr == 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) l[i][r] = 1.0f / (l[i][r] < 1e-45f ? 1.0f : l[i][r]);
+      float* S = a.stats + ((size_t)sl.z * a.seq + k0 + 16 * i + 4 * q) * 2;
+      st4(S, f32x4{m[i][0], l[i][0], m[i][1], l[i][1]});
+      st4(S + 4, f32x4{m[i][2], l[i][2], m[i][3], l[i][3]});
+    }
+  }
+}
+
+// O = P V for the 16-query blocks b0 < b1 (rows 16 b + lr), from the kept S^T
+// blocks: per 16-key chunk c <= b, P^T = exp(S - m) / l (masked on the
+// diagonal chunk c == b) and O^T += V^T P^T, the products of each block in the
+// order fwd_tile issues them.
+__device__ __forceinline__ void fwd_kept(const AttnArgs& a, const Slice& sl, int b0, int b1, const float* sst) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+  const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
+  const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
+  const int bk[2] = {b0, b1};
+  f32x4 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  struct Chunk {
+    f32x4 va[4], s01, s23, st[2];
+  };
+  auto fetch = [&](int c, Chunk& ch) {
+    const int k0 = 16 * c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ch.va[r] = bld4s(V, sl.base + (uint32_t)(k0 + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+    ch.s01 = ld4(ST + (size_t)(k0 + 4 * q) * 2);
+    ch.s23 = ld4(ST + (size_t)(k0 + 4 * q) * 2 + 4);
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+      if (c <= bk[n]) ch.st[n] = *reinterpret_cast<const f32x4*>(sst + (bk[n] * (bk[n] + 1) / 2 + c) * 256 + 4 * lane);
+  };
+  auto compute = [&](int c, const Chunk& ch) {
+    const float mk[4] = {ch.s01[0], ch.s01[2], ch.s23[0], ch.s23[2]};
+    const float il[4] = {ch.s01[1], ch.s01[3], ch.s23[1], ch.s23[3]};
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      if (c > bk[n]) continue;
+      const bool diag = c == bk[n];
+      float pt[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool keep = !diag || lr >= 4 * q + r;
+        pt[r] = keep ? __expf(a.scale * ch.st[n][r] - mk[r]) * il[r] : 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][n] = mfma4(ch.va[r][i], pt[r], acc[i][n]);
+    }
+  };
+  chunk_loop<Chunk>(0, b1 + 1, fetch, compute);
+  const __amdgpu_buffer_rsrc_t O = rsrc(a.out, a.bytes);
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      bst4(O, sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * q + 4 * r,
+           f32x4{acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]});
+}
+
+// bwd_kv_tile<true, DK, true> for the 16-key blocks b0 < b1 (keys 16 b + lr):
+// per query chunk c >= b (masked on the diagonal chunk c == b), P is kept in
+// sst, dV^T += dO^T P, then D, and with DK a second pass for dK^T += Q^T dS.
+template <bool DK>
+__device__ __forceinline__ void bwd_kv_kept(const AttnArgs& a, const Slice& sl, int b0, int b1, float* sst) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+  const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
+  const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
+  const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
+  const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
+  const int bk[2] = {b0, b1};
+  f32x4 kB[2][4], vB[2][4];
+  float mk[2], il[2];
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      kB[n][s] = bld4(K, sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * s + 4 * q);
+      if (DK) vB[n][s] = bld4(V, sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * s + 4 * q);
+    }
+    const float* sp = a.stats + ((size_t)sl.z * a.seq + 16 * bk[n] + lr) * 2;
+    mk[n] = sp[0];
+    il[n] = sp[1];
+  }
+  f32x4 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float D[2] = {0.f, 0.f};
+  struct Chunk {
+    f32x4 qa[4], oa[4], at[4];
+  };
+  auto run = [&](auto pass2_tag) {
+    constexpr bool P2 = decltype(pass2_tag)::value;
+    auto fetch = [&](int c, Chunk& ch) {
+      const int qc = 16 * c;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        ch.qa[s] = bld4(Q, sl.base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
+        if (P2) ch.oa[s] = bld4(dO, sl.base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        ch.at[r] = bld4s(P2 ? Q : dO, sl.base + (uint32_t)(qc + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+    };
+    auto compute = [&](int c, const Chunk& ch) {
+#pragma unroll
+      for (int n = 0; n < 2; ++n) {
+        if (c < bk[n]) continue;
+        const bool diag = c == bk[n];
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, da = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            sa = mfma4(ch.qa[s][j], kB[n][s][j], sa);
+            if (P2) da = mfma4(ch.oa[s][j], vB[n][s][j], da);
+          }
+        float bop[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool keep = !diag || 4 * q + r >= lr;
+          const float pv = __expf(a.scale * sa[r] - mk[n]) * (keep ? il[n] : 0.f);
+          bop[r] = P2 ? pv * (da[r] - D[n]) : pv;
+        }
+        if (!P2) {
+          float* blk = sst + (c * (c + 1) / 2 + bk[n]) * 256 + lr;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) blk[(4 * q + r) * 16] = bop[r];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i][n] = mfma4(ch.at[r][i], bop[r], acc[i][n]);
+      }
+    };
+    chunk_loop<Chunk>(b0, a.seq / 16, fetch, compute);
+  };
+  run(std::false_type{});
+  const __amdgpu_buffer_rsrc_t dVr = rsrc(a.dv, a.bytes);
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const uint32_t row = sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld;
+    float part = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const f32x4 vv = bld4(V, row + 16 * q + 4 * r);
+      f32x4 g = {acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]};
+      part += g[0] * vv[0] + g[1] * vv[1] + g[2] * vv[2] + g[3] * vv[3];
+      if (a.acc_v) g += bld4(dVr, row + 16 * q + 4 * r);
+      bst4(dVr, row + 16 * q + 4 * r, g);
+    }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    D[n] = part;
+    if (q == 0) a.dcol[(size_t)sl.z * a.seq + 16 * bk[n] + lr] = part;
+  }
+  if (!DK) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  run(std::true_type{});
+  const __amdgpu_buffer_rsrc_t dKr = rsrc(a.dk, a.bytes);
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t e = sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * q + 4 * r;
+      f32x4 g = a.scale * f32x4{acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]};
+      if (a.acc_k) g += bld4(dKr, e);
+      bst4(dKr, e, g);
+    }
+}
+
+// bwd_q_tile<true, KREF, true> for the 16-query blocks b0 < b1: P of every
+// key chunk c <= b from sst, dP^T = V dO^T, dS^T = P^T (dP^T - D), then
+// dQ^T += K^T dS^T and with KREF the reference's K gradient.
+template <bool KREF>
+__device__ __forceinline__ void bwd_q_kept(const AttnArgs& a, const Slice& sl, int b0, int b1, const float* sst) {
+  const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+  const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
+  const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
+  const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
+  const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
+  const float* DC = a.dcol + (size_t)sl.z * a.seq;
+  const int bk[2] = {b0, b1};
+  f32x4 obr[2][4];
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) obr[n][s] = bld4(dO, sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * s + 4 * q);
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  struct Chunk {
+    f32x4 va[4];
+  };
+  auto fetch = [&](int c, Chunk& ch) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) ch.va[s] = bld4(V, sl.base + (uint32_t)(16 * c + lr) * a.ld + 16 * s + 4 * q);
+  };
+  f32x4 yk[4], yq[4], dk;
+  auto late = [&](int c) {
+    dk = ld4(DC + 16 * c + 4 * q);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      yk[r] = bld4s(K, sl.base + (uint32_t)(16 * c + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+      if (KREF) yq[r] = bld4s(Q, sl.base + (uint32_t)(16 * c + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+    }
+  };
+  auto compute = [&](int c, const Chunk& ch) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      if (c > bk[n]) continue;
+      f32x4 dt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dt = mfma4(ch.va[s][j], obr[n][s][j], dt);
+      const f32x4 pt = *reinterpret_cast<const f32x4*>(sst + (bk[n] * (bk[n] + 1) / 2 + c) * 256 + lr * 16 + 4 * q);
+      float ds[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ds[r] = pt[r] * (dt[r] - dk[r]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[i][n] = mfma4(yk[r][i], ds[r], acc[i][n]);
+          if (KREF) acc[i][2 + n] = mfma4(yq[r][i], ds[r], acc[i][2 + n]);
+        }
+      __builtin_amdgcn_sched_barrier(0);  // block n + 1's LDS reads stay after block n's products
+    }
+  };
+  chunk_loop<Chunk>(0, b1 + 1, fetch, compute, late);
+  const __amdgpu_buffer_rsrc_t dQr = rsrc(a.dq, a.bytes);
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t e = sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * q + 4 * r;
+      f32x4 g = a.scale * f32x4{acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]};
+      if (a.acc_q) g += bld4(dQr, e);
+      bst4(dQr, e, g);
+    }
+  if (KREF) {
+    const __amdgpu_buffer_rsrc_t dKr = rsrc(a.dk, a.bytes);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t d = 16 * q + 4 * r + i, j = 16 * bk[n] + lr;
+          const uint32_t f = d * (uint32_t)a.seq + j;
+          const uint32_t e = sl.base + (f / HD) * a.ld + f % HD;
+          float g = a.scale * acc[i][2 + n][r];
+          if (a.acc_k) g += bld1(dKr, e);
+          bst1(dKr, e, g);
+        }
+  }
+}
+
 // One wave per 32-row tile, two tiles (j and nb - 1 - j) per workgroup,
 // workgroups spread over the XCDs by slice (slice_of).
 template <bool CAUSAL>
@@ -724,16 +1103,14 @@ __global__ __launch_bounds__(128, 2) void attn_bwd_q_kernel(AttnArgs a) {
 // backward) separated by a workgroup barrier instead of a kernel boundary.
 // Each kernel launch pays a ramp (every wave waits for its first operands
 // from memory at once) and a tail (every store at the end); this pays them
-// once per direction.  In the pass whose work grows or shrinks with the tile
-// index, wave w takes tile w (w < SW / 2) or mirrors it, so that waves w and
-// w + 4 -- the pair that shares a SIMD -- carry complementary loads.
+// once per direction.  Under the causal mask the passes whose work grows or
+// shrinks with the row index give wave w the 16-row blocks w and
+// seq / 16 - 1 - w (the *_kept functions), so every wave carries the same
+// work.
 constexpr int SW = 8;  // waves per slice workgroup: seq / TW tiles, at most 8
 __device__ __forceinline__ Slice slice_whole(const AttnArgs& a) {
   const int z = blockIdx.x, b = z / a.heads, h = z - b * a.heads;
   return {z, (uint32_t)b * a.seq * a.ld + (uint32_t)h * HD, 0};
-}
-__device__ __forceinline__ int mirrored_tile(int w, int ntile) {
-  return w < ntile / 2 ? w : ntile - 1 - (w - ntile / 2);
 }
 // Causal: the statistics pass keeps the slice's S^T blocks on or below the
 // diagonal in LDS (seq / 16 (seq / 16 + 1) / 2 blocks of 1 KB, 136 KB at seq
@@ -744,9 +1121,15 @@ __global__ __launch_bounds__(SW * 64, 1) void attn_fwd_slice_kernel(AttnArgs a) 
   __shared__ __attribute__((aligned(16))) float sst[kBlocks * 256];
   const Slice sl = slice_whole(a);
   const int w = threadIdx.x >> 6, ntile = a.seq / TW;
-  if (w < ntile) stats_tile<CAUSAL, CAUSAL>(a, sl, w * TW, sst);
-  __syncthreads();  // the slice's statistics (and kept scores) are written
-  if (w < ntile) fwd_tile<CAUSAL, CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW, sst);
+  if constexpr (CAUSAL) {
+    if (w < ntile) stats_kept(a, sl, w * TW, sst);
+    __syncthreads();  // the slice's statistics and kept scores are written
+    if (w < ntile) fwd_kept(a, sl, w, 2 * ntile - 1 - w, sst);
+  } else {
+    if (w < ntile) stats_tile<false>(a, sl, w * TW);
+    __syncthreads();  // the slice's statistics are written
+    if (w < ntile) fwd_tile<false>(a, sl, w * TW);
+  }
 }
 // Causal: the dV pass keeps the slice's P blocks on or below the diagonal in
 // LDS (136 KB at seq 256) and the dQ pass reads them instead of recomputing
@@ -758,11 +1141,16 @@ __global__ __launch_bounds__(SW * 64, 1) void attn_bwd_slice_kernel(AttnArgs a) 
   __shared__ __attribute__((aligned(16))) float lds[kFloats];
   const Slice sl = slice_whole(a);
   const int w = threadIdx.x >> 6, ntile = a.seq / TW;
-  if (w < ntile) bwd_kv_tile<CAUSAL, !KREF, CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW, lds);
-  __syncthreads();  // D of every key of the slice (and the kept P) is written
-  float* own = lds + w * 2 * TW * LQ;  // the wave's staging region (without the mask)
-  if (w < ntile)
-    bwd_q_tile<CAUSAL, KREF, CAUSAL>(a, sl, mirrored_tile(w, ntile) * TW, own, own + TW * LQ, lds);
+  if constexpr (CAUSAL) {
+    if (w < ntile) bwd_kv_kept<!KREF>(a, sl, w, 2 * ntile - 1 - w, lds);
+    __syncthreads();  // D of every key of the slice and the kept P are written
+    if (w < ntile) bwd_q_kept<KREF>(a, sl, w, 2 * ntile - 1 - w, lds);
+  } else {
+    if (w < ntile) bwd_kv_tile<false, !KREF>(a, sl, w * TW);
+    __syncthreads();  // D of every key of the slice is written
+    float* own = lds + w * 2 * TW * LQ;  // the wave's staging region
+    if (w < ntile) bwd_q_tile<false, KREF>(a, sl, w * TW, own, own + TW * LQ);
+  }
 }
 
 // Operand addressing uses 32-bit byte offsets into buffer resources whose
