@@ -195,7 +195,10 @@ def counter_table(fetch_db: str, write_db: str, cfetch_db: str, cwrite_db: str, 
             acc[k]["clock"].append(cycles / t if t > 0 else float("nan"))  # GHz
             if d in busy:
                 acc[k]["mfma"].append(busy[d][1] / (cycles * CUS * SIMDS) if cycles > 0 else float("nan"))
-    lines = [f"Calibration (copy of {n} floats): FETCH_SIZE x {f_fetch:.3f}, WRITE_SIZE x {f_write:.3f}.", ""]
+    ct = [t for _, k, _, t in per_dispatch(cfetch_db, "FETCH_SIZE") if COPY_KERNEL in k]
+    lines = [f"Calibration (copy of {n} floats): FETCH_SIZE x {f_fetch:.3f}, WRITE_SIZE x {f_write:.3f}; "
+             f"the copy itself ran {mean(ct) / 1e3:.1f} us per launch in that counter run, "
+             f"{8.0 * n / mean(ct):.0f} GB/s (read + write), the practical streaming ceiling.", ""]
     head = "| kernel | launches | avg us (counter run) | fetch MB/launch | write MB/launch | HBM MB/launch | GB/s |"
     sep = "|---|---:|---:|---:|---:|---:|---:|"
     if mfma_db:
