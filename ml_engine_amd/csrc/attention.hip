@@ -1120,7 +1120,9 @@ __global__ __launch_bounds__(SW * 64, 1) void attn_fwd_slice_kernel(AttnArgs a) 
   constexpr int kBlocks = CAUSAL ? (SW * TW / 16) * (SW * TW / 16 + 1) / 2 : 1;
   __shared__ __attribute__((aligned(16))) float sst[kBlocks * 256];
   const Slice sl = slice_whole(a);
-  const int w = threadIdx.x >> 6, ntile = a.seq / TW;
+  // the wave index, read as wave-uniform so that block choices and loop bounds
+  // derived from it stay in scalar registers and branch on the scalar unit
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ntile = a.seq / TW;
   if constexpr (CAUSAL) {
     if (w < ntile) stats_kept(a, sl, w * TW, sst);
     __syncthreads();  // the slice's statistics and kept scores are written
@@ -1140,7 +1142,9 @@ __global__ __launch_bounds__(SW * 64, 1) void attn_bwd_slice_kernel(AttnArgs a) 
   constexpr int kFloats = CAUSAL ? (SW * TW / 16) * (SW * TW / 16 + 1) / 2 * 256 : SW * 2 * TW * LQ;
   __shared__ __attribute__((aligned(16))) float lds[kFloats];
   const Slice sl = slice_whole(a);
-  const int w = threadIdx.x >> 6, ntile = a.seq / TW;
+  // the wave index, read as wave-uniform so that block choices and loop bounds
+  // derived from it stay in scalar registers and branch on the scalar unit
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ntile = a.seq / TW;
   if constexpr (CAUSAL) {
     if (w < ntile) bwd_kv_kept<!KREF>(a, sl, w, 2 * ntile - 1 - w, lds);
     __syncthreads();  // D of every key of the slice and the kept P are written
