@@ -1053,11 +1053,12 @@ int choose_splits(int M, int N, int K, int batch, int& kchunk) {
   } else {
     // Measured on MI355X: with ~256 tiles a split only pays off for long K.
     // A grid of a few tiles is latency-bound (each split walks its K chunk one
-    // stage after another), so it takes chunks down to 64 deep: the C1 MLP
-    // step went from 0.136 to 0.118 ms.
+    // stage after another), so it takes chunks down to one 32-deep stage: the
+    // C1 MLP step went from 0.136 to 0.118 ms with 64-deep chunks, and from
+    // 0.065 to 0.057 ms with 32-deep ones (K / 128 or fewer splits: slower).
     if (tiles >= 384 || (tiles >= 128 && K < 4096)) return 1;
     s = (int)((768 + tiles - 1) / tiles);
-    smax = tiles <= 16 ? K / 64 : K / 256;
+    smax = tiles <= 16 ? K / 16 : K / 256;
   }
   if (s > smax) s = smax;
   if (s < 2) return 1;
