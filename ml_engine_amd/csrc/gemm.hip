@@ -978,11 +978,9 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g, int64_t u
 // where the tile kernels would spend split-K and reduce launches on little
 // work.
 template <int TA, int TB>
-__global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs g) {
-  __shared__ float red[2][4][64];
+__device__ __forceinline__ void simple_body(const GemmArgs& g, int bx, int64_t z, float (&red)[2][4][64]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t z = blockIdx.y;
-  const int64_t idx = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t idx = (int64_t)bx * 64 + lane;
   const bool live = idx < (int64_t)g.M * g.N;
   const int m = live ? (int)(idx / g.N) : 0, n = live ? (int)(idx % g.N) : 0;
   const int kq = (g.K + 3) / 4, k0 = w * kq, k1 = min(g.K, k0 + kq);
@@ -1010,6 +1008,22 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs g) {
   *c = v;
   if (g.colsum && m == 0)
     put_colsum(g, z * g.scs + n, ((red[1][0][lane] + red[1][1][lane]) + red[1][2][lane]) + red[1][3][lane]);
+}
+
+template <int TA, int TB>
+__global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs g) {
+  __shared__ float red[2][4][64];
+  simple_body<TA, TB>(g, blockIdx.x, blockIdx.y, red);
+}
+
+// A Linear layer's two small products (dX = dY W^T and dW = X^T dY with db)
+// in one launch: workgroups [0, nb0) compute problem 0, the rest problem 1,
+// each exactly as gemm_simple_kernel does.  One launch less per small layer
+// (a C1 step is bound by the host's launch rate).
+__global__ __launch_bounds__(256) void gemm_simple_pair_kernel(GemmArgs g0, GemmArgs g1, int nb0) {
+  __shared__ float red[2][4][64];
+  if ((int)blockIdx.x < nb0) simple_body<0, 1>(g0, blockIdx.x, blockIdx.y, red);
+  else simple_body<1, 0>(g1, blockIdx.x - nb0, blockIdx.y, red);
 }
 
 // Workgroup tile: 128 x 128 unless a side is <= 64 (the 64-wide variants waste
@@ -1496,6 +1510,16 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, 
   hipStream_t s = as_stream(stream);
   const long long n0 = direct_items(P0), n1 = direct_items(P1);
   const int ncu = cu_count();
+  // Both small (gemm_simple_kernel, one batch item): one launch.
+  if (!P0.empty && !P1.empty && P0.simple && P1.simple && P0.grid.z == 1 && P1.grid.z == 1) {
+    const unsigned nb0 = (unsigned)(((int64_t)P0.g.M * P0.g.N + 63) / 64);
+    const unsigned nb1 = (unsigned)(((int64_t)P1.g.M * P1.g.N + 63) / 64);
+    {
+      ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
+      mle::launch(gemm_simple_pair_kernel, dim3(nb0 + nb1, 1), 256, 0, s, P0.g, P1.g, (int)nb0);
+    }
+    return check_launch("gemm_pair");
+  }
   // One launch when both would run on the register-direct kernel at most one
   // workgroup per CU each, and the dX product needs no workspace (the dW
   // product's split partials own it).

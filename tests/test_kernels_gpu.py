@@ -281,6 +281,9 @@ def test_gemm_sum(hip, orc, ta, tb, M, N, K, terms, beta):
     (8192, 512, 512, 1, False, 1),    # the attention output projection's shape
     (8192, 2048, 128, 1, True, 0),    # dX on the persistent kernel: two launches
     (300, 130, 70, 2, True, 1),       # small: LDS kernels, split partials
+    (64, 256, 10, 1, True, 0),        # both products small: one one-thread-per-output launch
+    (64, 256, 10, 1, True, 1),
+    (64, 100, 7, 2, True, 1),         # small, two layers: one launch per product
 ])
 def test_linear_bwd(hip, orc, rows, inp, out, layers, bias, acc):
     """mle_linear_bwd against the oracle's bcmm products and column sums, with
