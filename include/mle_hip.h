@@ -322,6 +322,20 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers,
                       const float* X, const float* dY, int64_t stride_dy,
                       const float* W, int64_t stride_w, float* dX, int accumulate_dx,
                       float* dW, float* db, int64_t stride_db, int accumulate_dw, void* ws, size_t ws_bytes);
+/* One Linear layer's backward (mle_linear_bwd_ex, layers = 1) followed by
+ * the backward of the activation that produced its input X = act(act_x):
+ *   act_dx (+)= act'(act_x) * dX       (act_accumulate: 1 adds, 0 assigns)
+ * the derivative kernels of Engine/kernels.cu:1223, 1256, 1297 (ReLU, SiLU,
+ * GELU; also tanh, sigmoid, leaky ReLU), run by the reference as the
+ * activation node's own backward after the Linear's (Engine/engine.cu:3553-
+ * 3560).  dX is written as mle_linear_bwd_ex writes it; act_x and act_dx are
+ * [rows, in] like dX.  On the small-product kernels the activation gradient
+ * is their epilogue (one launch less), otherwise a pass after the products.
+ * Same workspace as mle_linear_bwd_ex. */
+int mle_linear_bwd_act(mle_stream stream, int rows, int in, int out, const float* X, const float* dY,
+                       const float* W, float* dX, int accumulate_dx, float* dW, float* db, int accumulate_dw,
+                       int act_kind, const float* act_x, float* act_dx, int act_accumulate, void* ws,
+                       size_t ws_bytes);
 
 /* out[c] (+)= sum_r x[r, c].  BCompress (Engine/kernels.cu:1562-1584); beta 0/1. */
 int mle_colsum(mle_stream stream, const float* x, size_t rows, int cols, float* out, float beta);

@@ -66,4 +66,25 @@ __device__ __forceinline__ float act_rt(int kind, float x) {
   }
 }
 
+// act_df for a kind known only at run time.
+__device__ __forceinline__ float act_drt(int kind, float x) {
+  switch (kind) {
+    case MLE_RELU: return act_df<MLE_RELU>(x);
+    case MLE_GELU: return act_df<MLE_GELU>(x);
+    case MLE_SILU: return act_df<MLE_SILU>(x);
+    case MLE_TANH: return act_df<MLE_TANH>(x);
+    case MLE_SIGMOID: return act_df<MLE_SIGMOID>(x);
+    default: return act_df<MLE_LEAKY_RELU>(x);
+  }
+}
+
+// dx (+)= f'(x) * dy for a run-time kind, as the elementwise activation
+// backward forms it: the product is rounded before the add (acc = false
+// assigns and `old` is unused).
+__device__ __forceinline__ float act_bwd_rt(int kind, float x, float dy, float old, bool acc) {
+#pragma clang fp contract(off)
+  const float v = act_drt(kind, x) * dy;
+  return acc ? old + v : v;
+}
+
 }  // namespace mle

@@ -62,6 +62,10 @@ struct GemmArgs {
   // Column sums: 0 adds them into colsum (the default), 1 assigns (colsum is
   // logically zero).
   int cs_assign;
+  // 1 + an activation kind: the small-product kernels (simple, K-split) also
+  // write act_dx (+)= act'(act_x) * C in C's layout, act_acc choosing add or
+  // assign (0: not).
+  int act_bwd;
 };
 
 // colsum[i] (+)= v as GemmArgs::cs_assign says.
@@ -1006,6 +1010,10 @@ __device__ __forceinline__ void simple_body(const GemmArgs& g, int bx, int64_t z
   if (g.beta != 0.f) v += g.beta * *c;
   if (g.bias) v += g.bias[z * g.sbias + n];
   *c = v;
+  if (g.act_bwd) {
+    const int64_t co = z * g.sc + (int64_t)m * g.ldc + n;
+    g.act_dx[co] = act_bwd_rt(g.act_bwd - 1, g.act_x[co], v, g.act_acc ? g.act_dx[co] : 0.f, g.act_acc);
+  }
   if (g.colsum && m == 0)
     put_colsum(g, z * g.scs + n, ((red[1][0][lane] + red[1][1][lane]) + red[1][2][lane]) + red[1][3][lane]);
 }
@@ -1024,6 +1032,145 @@ __global__ __launch_bounds__(256) void gemm_simple_pair_kernel(GemmArgs g0, Gemm
   __shared__ float red[2][4][64];
   if ((int)blockIdx.x < nb0) simple_body<0, 1>(g0, blockIdx.x, blockIdx.y, red);
   else simple_body<1, 0>(g1, blockIdx.x - nb0, blockIdx.y, red);
+}
+
+// Small products with a long K (an MLP's 784-wide input layer: 64 x 256 x
+// 784 and its gradients): one C tile of TT x TT per workgroup of 16 waves.
+// Wave w multiplies the tile's operands over its K range [w kc, (w + 1) kc)
+// on MFMA (lane l feeds row or column l % 16 of a 16-wide block at k = kb +
+// l / 16), the workgroup adds the 16 partial tiles in wave order through LDS
+// and applies the epilogue: one launch where split K needs two (partials,
+// then the reduce), and more workgroups than the 64-wide tiles give the
+// same shape.  Column sums of B (the bias gradient) come from the workgroups
+// of the first tile row, in (wave, lane group) order.
+constexpr int KS_NW = 16, KS_NT = 64 * KS_NW;
+
+template <int TT>
+constexpr int ks_lds_floats() {
+  return KS_NW * TT * TT + KS_NW * 4 * TT;
+}
+
+template <int TA, int TB, int TT>
+__device__ __forceinline__ void ksplit_body(const GemmArgs& g, int tx, int ty, int64_t z, int kc, float* lds) {
+  constexpr int S = TT / 16;
+  const int lane = threadIdx.x & 63, li = lane & 15, lq = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int m0 = ty * TT, n0 = tx * TT;
+  const float* __restrict__ A = g.A + batch_off(z, g, g.sa, g.sa2);
+  const float* __restrict__ B = g.B + batch_off(z, g, g.sb, g.sb2);
+  const bool cs_on = g.colsum != nullptr && ty == 0;
+  const int k0 = w * kc, k1 = min(g.K, k0 + kc);
+  int am[S], bn[S];
+  bool aok[S], bok[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    am[i] = m0 + 16 * i + li;
+    aok[i] = am[i] < g.M;
+    bn[i] = n0 + 16 * i + li;
+    bok[i] = bn[i] < g.N;
+  }
+  f32x4 acc[S][S];
+  float cs[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    cs[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < S; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // Chunks of CH four-deep steps: every load of a chunk is issued before its
+  // products (one memory latency per chunk); steps past the wave's range are
+  // skipped on a wave-uniform branch.
+  constexpr int CH = 16 / S;
+  for (int kb = k0; kb < k1; kb += 4 * CH) {
+    float a[CH][S], b[CH][S];
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+      const int kk = kb + 4 * t + lq;
+      const bool kok = kk < k1;
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        a[t][i] = 0.f;
+        b[t][i] = 0.f;
+      }
+      if (kb + 4 * t < k1) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          if (kok && aok[i]) a[t][i] = TA ? A[(int64_t)kk * g.lda + am[i]] : A[(int64_t)am[i] * g.lda + kk];
+          if (kok && bok[i]) b[t][i] = TB ? B[(int64_t)bn[i] * g.ldb + kk] : B[(int64_t)kk * g.ldb + bn[i]];
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < CH; ++t) {
+      if (kb + 4 * t >= k1) break;
+#pragma unroll
+      for (int i = 0; i < S; ++i)
+#pragma unroll
+        for (int j = 0; j < S; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][i], b[t][j], acc[i][j], 0, 0, 0);
+      if (cs_on)
+#pragma unroll
+        for (int j = 0; j < S; ++j) cs[j] += b[t][j];
+    }
+  }
+  // Partial tiles: result lane l holds rows 4 (l / 16) + r of column l % 16.
+  float* part = lds + w * (TT * TT);
+#pragma unroll
+  for (int i = 0; i < S; ++i)
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[(16 * i + 4 * lq + r) * TT + 16 * j + li] = acc[i][j][r];
+  float* cpart = lds + KS_NW * TT * TT;  // [wave][lane group][column]
+  if (cs_on)
+#pragma unroll
+    for (int j = 0; j < S; ++j) cpart[(w * 4 + lq) * TT + 16 * j + li] = cs[j];
+  __syncthreads();
+  const int64_t cz = batch_off(z, g, g.sc, g.sc2);
+  for (int o = threadIdx.x; o < TT * TT; o += KS_NT) {
+    const int m = m0 + o / TT, n = n0 + o % TT;
+    if (m >= g.M || n >= g.N) continue;
+    float v = lds[o];
+#pragma unroll
+    for (int q = 1; q < KS_NW; ++q) v += lds[q * (TT * TT) + o];
+    const int64_t co = cz + (int64_t)m * g.ldc + n;
+    float y = g.alpha * v;
+    if (g.beta != 0.f) y += g.beta * g.C[co];
+    if (g.bias) y += g.bias[z * g.sbias + n];
+    g.C[co] = y;
+    if (g.act_red) g.act_y[co] = act_rt(g.act_red - 1, y);
+    if (g.act_bwd)
+      g.act_dx[co] = act_bwd_rt(g.act_bwd - 1, g.act_x[co], y, g.act_acc ? g.act_dx[co] : 0.f, g.act_acc);
+  }
+  if (cs_on && (int)threadIdx.x < TT && n0 + (int)threadIdx.x < g.N) {
+    const int c = threadIdx.x;
+    float t = 0.f;
+    for (int q = 0; q < 4 * KS_NW; ++q) t += cpart[q * TT + c];
+    put_colsum(g, z * g.scs + n0 + c, t);
+  }
+}
+
+template <int TA, int TB, int TT>
+__global__ __launch_bounds__(KS_NT) void gemm_ksplit_kernel(GemmArgs g, int kc) {
+  __shared__ __attribute__((aligned(16))) float lds[ks_lds_floats<TT>()];
+  ksplit_body<TA, TB, TT>(g, blockIdx.x, blockIdx.y, blockIdx.z, kc, lds);
+}
+
+// A Linear's two backward products on the K-split kernel in one launch:
+// workgroups [0, nb0) take dX = dY W^T (NT, tiles of T0, gx0 per tile row),
+// the rest dW = X^T dY with db (TN, tiles of T1).
+template <int T0, int T1>
+__global__ __launch_bounds__(KS_NT) void gemm_ksplit_pair_kernel(GemmArgs g0, GemmArgs g1, int nb0, int gx0, int gx1,
+                                                                 int kc0, int kc1) {
+  constexpr int F0 = ks_lds_floats<T0>(), F1 = ks_lds_floats<T1>();
+  __shared__ __attribute__((aligned(16))) float lds[F0 > F1 ? F0 : F1];
+  const int b = blockIdx.x;
+  if (b < nb0) {
+    ksplit_body<0, 1, T0>(g0, b % gx0, b / gx0, 0, kc0, lds);
+  } else {
+    const int c = b - nb0;
+    ksplit_body<1, 0, T1>(g1, c % gx1, c / gx1, 0, kc1, lds);
+  }
 }
 
 // Workgroup tile: 128 x 128 unless a side is <= 64 (the 64-wide variants waste
@@ -1167,6 +1314,8 @@ struct GemmPlan {
   int vec = 0, which = 0;
   bool cs = false, direct_ok = false, empty = false;
   bool simple = false;  // gemm_simple_kernel: one thread per C element, no split
+  bool ksplit = false;  // gemm_ksplit_kernel: K split over a workgroup's waves
+  int ks_kc = 0;        // its K range per wave
   double flop = 0, bytes = 0;
 };
 
@@ -1182,6 +1331,23 @@ static bool simple_shape(int M, int N, int K, int batch, int inner, int terms) {
          (double)M * N * (double)(K > 0 ? K : 1) * batch <= 4194304.0 && inner == 1 && terms <= 1 &&
          (double)M * N <= 64.0 * 2147483647.0 && batch <= 65535;
 }
+
+// Products for gemm_ksplit_kernel: at most 256 Ki outputs and no sum of
+// terms, with a K long enough to share over 16 waves but short enough that
+// one workgroup's products stay a few microseconds of its CU's matrix cores
+// (2 K cycles per SIMD for 16-wide tiles, 8 K for 32-wide).  Tiles of 32 when
+// that still gives 128 workgroups, else 16.
+static int ksplit_tile(int M, int N, int batch) {
+  const long long t32 = (long long)((M + 31) / 32) * ((N + 31) / 32) * batch;
+  return t32 >= 128 ? 32 : 16;
+}
+static bool ksplit_shape(int M, int N, int K, int batch, int terms) {
+  if (terms > 1 || K < 32 || (double)M * N * batch > 262144.0) return false;
+  const int tt = ksplit_tile(M, N, batch);
+  return K <= (tt == 16 ? 4096 : 1024) && (M + tt - 1) / tt <= 65535 && batch <= 65535;
+}
+// K range of one wave: whole 4-deep MFMA steps.
+static int ksplit_kc(int K) { return ((K + KS_NW - 1) / KS_NW + 3) / 4 * 4; }
 
 const char* const kFamily[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
 
@@ -1254,10 +1420,20 @@ static int gemm_plan(GemmPlan& P, int trans_a, int trans_b, int M, int N, int K,
     g.kchunk = K;
     g.part = g.part_cs = nullptr;
     P.simple = true;
+  } else if (ksplit_shape(M, N, K, batch, terms)) {
+    g.splits = 1;
+    g.kchunk = K;
+    g.part = g.part_cs = nullptr;
+    P.ksplit = true;
+    P.ks_kc = ksplit_kc(K);
   }
   P.g = g;
   P.tile = tile;
   P.grid = dim3((N + tile.tn() - 1) / tile.tn(), (M + tile.tm() - 1) / tile.tm(), batch * g.splits);
+  if (P.ksplit) {
+    const int tt = ksplit_tile(M, N, batch);
+    P.grid = dim3((N + tt - 1) / tt, (M + tt - 1) / tt, batch);
+  }
   P.vec = vec;
   P.cs = cs;
   P.direct_ok = direct_ok;
@@ -1275,6 +1451,21 @@ static void gemm_launch_main(hipStream_t s, const GemmPlan& P) {
       case 1: mle::launch(gemm_simple_kernel<0, 1>, grid, 256, 0, s, P.g); break;
       case 2: mle::launch(gemm_simple_kernel<1, 0>, grid, 256, 0, s, P.g); break;
       default: mle::launch(gemm_simple_kernel<1, 1>, grid, 256, 0, s, P.g); break;
+    }
+    return;
+  }
+  if (P.ksplit) {
+    const bool t32 = ksplit_tile(P.g.M, P.g.N, (int)P.grid.z) == 32;
+    const int kc = P.ks_kc;
+    switch (P.which * 2 + (t32 ? 1 : 0)) {
+      case 0: mle::launch(gemm_ksplit_kernel<0, 0, 16>, P.grid, KS_NT, 0, s, P.g, kc); break;
+      case 1: mle::launch(gemm_ksplit_kernel<0, 0, 32>, P.grid, KS_NT, 0, s, P.g, kc); break;
+      case 2: mle::launch(gemm_ksplit_kernel<0, 1, 16>, P.grid, KS_NT, 0, s, P.g, kc); break;
+      case 3: mle::launch(gemm_ksplit_kernel<0, 1, 32>, P.grid, KS_NT, 0, s, P.g, kc); break;
+      case 4: mle::launch(gemm_ksplit_kernel<1, 0, 16>, P.grid, KS_NT, 0, s, P.g, kc); break;
+      case 5: mle::launch(gemm_ksplit_kernel<1, 0, 32>, P.grid, KS_NT, 0, s, P.g, kc); break;
+      case 6: mle::launch(gemm_ksplit_kernel<1, 1, 16>, P.grid, KS_NT, 0, s, P.g, kc); break;
+      default: mle::launch(gemm_ksplit_kernel<1, 1, 32>, P.grid, KS_NT, 0, s, P.g, kc); break;
     }
     return;
   }
@@ -1304,7 +1495,9 @@ static void gemm_launch_reduce(hipStream_t s, const GemmPlan& P) {
 // per workgroup), or 0 when it would pick another kernel.
 static long long direct_items(const GemmPlan& P) {
   const GemmArgs& g = P.g;
-  if (P.empty || P.simple || !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0)) return 0;
+  if (P.empty || P.simple || P.ksplit ||
+      !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0))
+    return 0;
   const long long items = (long long)P.grid.x * P.grid.y * P.grid.z;
   const bool c_buf = ((double)(g.M - 1) * (double)g.ldc + g.N) * 4.0 < 2147483648.0 - 64;
   const bool stream = g.splits == 1 && g.kterms == 1 && !P.cs && g.K >= 64 && g.K % 64 == 0 &&
@@ -1315,7 +1508,9 @@ static long long direct_items(const GemmPlan& P) {
 // True when launch_tile would run the plan on the persistent kernel.
 static bool uses_stream(const GemmPlan& P) {
   const GemmArgs& g = P.g;
-  if (P.empty || P.simple || !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0)) return false;
+  if (P.empty || P.simple || P.ksplit ||
+      !(P.tile.direct && P.direct_ok && P.vec == 2 && g.K % 16 == 0 && g.kchunk % 16 == 0))
+    return false;
   return direct_items(P) == 0;
 }
 
@@ -1428,7 +1623,9 @@ int mle_gemm_act_fwd(mle_stream stream, int trans_a, int trans_b, int M, int N, 
     }
     return check_launch("mle_gemm_act_fwd");
   }
-  if (P.g.splits > 1 && aligned16(Y)) {  // split K: the reduce that completes C writes Y too
+  // Split K: the reduce that completes C writes Y too; on the K-split kernel
+  // its epilogue does.
+  if ((P.g.splits > 1 && aligned16(Y)) || P.ksplit) {
     P.g.act_y = Y;
     P.g.act_red = 1 + kind;
     ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
@@ -1456,6 +1653,17 @@ int mle_gemm_act_bwd(mle_stream stream, int trans_a, int trans_b, int M, int N, 
                      ws, ws_bytes);
   if (rc != MLE_OK || P.empty) return rc;
   hipStream_t s = as_stream(stream);
+  if (P.simple || P.ksplit) {  // the small-product kernels' epilogue
+    P.g.act_x = X;
+    P.g.act_dx = dX;
+    P.g.act_acc = accumulate_dx ? 1 : 0;
+    P.g.act_bwd = 1 + kind;
+    {
+      ProbeScope probe(kFamily[P.which], s, P.flop, P.bytes);
+      gemm_launch_main(s, P);
+    }
+    return check_launch("mle_gemm_act_bwd");
+  }
   if (uses_stream(P) && P.which == 1 && epilogue_act(kind) && aligned16(X) && aligned16(dX)) {
     P.g.act_x = X;
     P.g.act_dx = dX;
@@ -1489,9 +1697,16 @@ int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers, con
                            stride_db, 1, ws, ws_bytes);
 }
 
-int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, const float* X, const float* dY,
-                      int64_t stride_dy, const float* W, int64_t stride_w, float* dX, int accumulate_dx, float* dW,
-                      float* db, int64_t stride_db, int accumulate_dw, void* ws, size_t ws_bytes) {
+}  // extern "C"
+
+// Linear backward, optionally with the backward of the activation whose
+// output is X' = this layer's input: act_dx (+)= act'(act_x) * dX (act_kind
+// < 0: none).  On the small-product kernels the activation gradient is their
+// epilogue; otherwise it is a pass after the products.
+static int linear_bwd_impl(mle_stream stream, int rows, int in, int out, int layers, const float* X, const float* dY,
+                           int64_t stride_dy, const float* W, int64_t stride_w, float* dX, int accumulate_dx,
+                           float* dW, float* db, int64_t stride_db, int accumulate_dw, int act_kind,
+                           const float* act_x, float* act_dx, int act_acc, void* ws, size_t ws_bytes) {
   MLE_CHECK_ARG(rows >= 0 && in >= 0 && out >= 0 && layers >= 1, "mle_linear_bwd: bad sizes");
   MLE_CHECK_ARG(layers == 1 || (stride_dy != 0 && stride_w != 0 && (db == nullptr || stride_db != 0)),
                 "mle_linear_bwd: %d layers need strides", layers);
@@ -1508,6 +1723,19 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, 
   if (rc != MLE_OK) return rc;
   P1.g.cs_assign = accumulate_dw ? 0 : 1;
   hipStream_t s = as_stream(stream);
+  bool act_done = act_kind < 0 || P0.empty;
+  if (!act_done && (P0.simple || P0.ksplit)) {
+    P0.g.act_bwd = 1 + act_kind;
+    P0.g.act_x = act_x;
+    P0.g.act_dx = act_dx;
+    P0.g.act_acc = act_acc ? 1 : 0;
+    act_done = true;
+  }
+  // The activation pass when no epilogue took it.
+  auto finish = [&](int code) {
+    if (code != MLE_OK || act_done) return code;
+    return mle_act_bwd(stream, act_kind, act_x, dX, act_dx, (size_t)rows * in, act_acc);
+  };
   const long long n0 = direct_items(P0), n1 = direct_items(P1);
   const int ncu = cu_count();
   // Both small (gemm_simple_kernel, one batch item): one launch.
@@ -1518,7 +1746,20 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, 
       ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
       mle::launch(gemm_simple_pair_kernel, dim3(nb0 + nb1, 1), 256, 0, s, P0.g, P1.g, (int)nb0);
     }
-    return check_launch("gemm_pair");
+    return finish(check_launch("gemm_pair"));
+  }
+  // Both on the K-split kernel (one batch item): one launch.
+  if (!P0.empty && !P1.empty && P0.ksplit && P1.ksplit && P0.grid.z == 1 && P1.grid.z == 1) {
+    const int gx0 = (int)P0.grid.x, gx1 = (int)P1.grid.x;
+    const int nb0 = gx0 * (int)P0.grid.y, nb1 = gx1 * (int)P1.grid.y;
+    const bool w0 = ksplit_tile(P0.g.M, P0.g.N, 1) == 32, w1 = ksplit_tile(P1.g.M, P1.g.N, 1) == 32;
+    auto k = w0 ? (w1 ? gemm_ksplit_pair_kernel<32, 32> : gemm_ksplit_pair_kernel<32, 16>)
+                : (w1 ? gemm_ksplit_pair_kernel<16, 32> : gemm_ksplit_pair_kernel<16, 16>);
+    {
+      ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
+      mle::launch(k, dim3((unsigned)(nb0 + nb1)), KS_NT, 0, s, P0.g, P1.g, nb0, gx0, gx1, P0.ks_kc, P1.ks_kc);
+    }
+    return finish(check_launch("gemm_pair"));
   }
   // One launch when both would run on the register-direct kernel at most one
   // workgroup per CU each, and the dX product needs no workspace (the dW
@@ -1537,7 +1778,7 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, 
       mle::launch(k, grid, NT, 0, s, P0.g, P1.g, pg);
       gemm_launch_reduce(s, P1);
     }
-    return check_launch("gemm_pair");
+    return finish(check_launch("gemm_pair"));
   }
   // Otherwise one launch each, in order (they may share the workspace).
   if (!P0.empty) {
@@ -1546,13 +1787,33 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, 
     gemm_launch_reduce(s, P0);
   }
   rc = check_launch(kFamily[P0.which]);
-  if (rc != MLE_OK || P1.empty) return rc;
+  if (rc != MLE_OK || P1.empty) return finish(rc);
   {
     ProbeScope probe(kFamily[P1.which], s, P1.flop, P1.bytes);
     gemm_launch_main(s, P1);
     gemm_launch_reduce(s, P1);
   }
-  return check_launch(kFamily[P1.which]);
+  return finish(check_launch(kFamily[P1.which]));
+}
+
+
+extern "C" {
+
+int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers, const float* X, const float* dY,
+                      int64_t stride_dy, const float* W, int64_t stride_w, float* dX, int accumulate_dx, float* dW,
+                      float* db, int64_t stride_db, int accumulate_dw, void* ws, size_t ws_bytes) {
+  return linear_bwd_impl(stream, rows, in, out, layers, X, dY, stride_dy, W, stride_w, dX, accumulate_dx, dW, db,
+                         stride_db, accumulate_dw, -1, nullptr, nullptr, 0, ws, ws_bytes);
+}
+
+int mle_linear_bwd_act(mle_stream stream, int rows, int in, int out, const float* X, const float* dY,
+                       const float* W, float* dX, int accumulate_dx, float* dW, float* db, int accumulate_dw,
+                       int act_kind, const float* act_x, float* act_dx, int act_accumulate, void* ws,
+                       size_t ws_bytes) {
+  MLE_CHECK_ARG(act_kind >= MLE_RELU && act_kind <= MLE_LEAKY_RELU && act_x != nullptr && act_dx != nullptr,
+                "mle_linear_bwd_act: bad activation argument");
+  return linear_bwd_impl(stream, rows, in, out, 1, X, dY, 0, W, 0, dX, accumulate_dx, dW, db, 0, accumulate_dw,
+                         act_kind, act_x, act_dx, act_accumulate, ws, ws_bytes);
 }
 
 int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, float alpha, const float* A,

@@ -994,6 +994,23 @@ graph Linear::forward(const graph& X) {
           "MatMul... X*W1 + B1 (with row statistics) in " + name + " forward");
   };
   node->backward = [=]() {
+    // When X is an activation's output and this layer its only consumer, the
+    // activation's backward (its input's gradient from dX) comes with ours.
+    NodeBackProp* ai = nullptr;
+    if (mle::fusion_enabled() && x->act_bwd_kind >= 0 && x->consumers == 1 && x->inputs.size() == 1 &&
+        x->act_bwd_plain && x->act_bwd_plain())
+      ai = x->inputs[0].get();
+    if (ai) {
+      const int acc_x = mle::accumulate_flag(x);
+      const int acc_a = mle::accumulate_flag(ai);
+      check(mle_linear_bwd_act(mle::stream(), (int)rows, n, p, x->output, mle::grad_of(nd), W->output, x->grad, acc_x,
+                               W->grad, has_bias ? Bb->grad : nullptr,
+                               mle::params_write_flag({W, has_bias ? Bb : nullptr}), x->act_bwd_kind, ai->output,
+                               ai->grad, acc_a, ws, ws_bytes),
+            "MatMul... dZ*W^T and X^T*dZ in " + name + " backward (with the activation before it)");
+      x->act_bwd_done = true;
+      return;
+    }
     // dX (+)= dZ W^T, dW += X^T dZ, db += colsum dZ (one launch when they fit).
     check(mle_linear_bwd_ex(mle::stream(), (int)rows, n, p, 1, x->output, mle::grad_of(nd), 0, W->output, 0, x->grad,
                             mle::accumulate_flag(x), W->grad, has_bias ? Bb->grad : nullptr, 0,

@@ -258,6 +258,15 @@ struct NodeBackProp {
   int act_grad_kind = -1;
   int act_grad_acc = 0;
   bool takes_act_grad = false;  // this node's backward handles act_grad_in
+  // Backward hand-off (additive), from the consumer's side: an activation
+  // node offers its kind here, with a test that its backward would be the
+  // plain elementwise pass; a Linear that is the activation's only consumer
+  // then forms the activation's input gradient in its own backward launch
+  // (mle_linear_bwd_act) and sets act_bwd_done, and the activation's
+  // backward launches nothing.
+  int act_bwd_kind = -1;
+  std::function<bool()> act_bwd_plain;
+  bool act_bwd_done = false;
   // Backward hand-off (additive), the other way round: a normalisation whose
   // input is this node, and which is the last of this node's consumers to
   // run its backward, runs its first pass and leaves the second here; this

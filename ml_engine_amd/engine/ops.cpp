@@ -138,7 +138,13 @@ graph act_node(const graph& input, int kind, const str& name) {
     fused = true;
   }
   node->reads_grad_alias = true;
+  node->act_bwd_kind = kind;
+  node->act_bwd_plain = [=]() { return !(fused && x->takes_act_grad && x->consumers == 1); };
   node->backward = [=]() {
+    if (nd->act_bwd_done) {  // the Linear after this node formed our input's gradient
+      nd->act_bwd_done = false;
+      return;
+    }
     if (fused && x->takes_act_grad && x->consumers == 1) {
       x->act_grad_in = mle::grad_of(nd);
       x->act_grad_kind = kind;

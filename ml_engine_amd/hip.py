@@ -82,6 +82,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_linear_bwd_ws_bytes": (SZ, [I, I, I, I]),
     "mle_linear_bwd": (I, [P, I, I, I, I, P, P, I64, P, I64, P, I, P, P, I64, P, SZ]),
     "mle_linear_bwd_ex": (I, [P, I, I, I, I, P, P, I64, P, I64, P, I, P, P, I64, I, P, SZ]),
+    "mle_linear_bwd_act": (I, [P, I, I, I, P, P, P, P, I, P, P, I, I, P, P, I, P, SZ]),
     "mle_colsum": (I, [P, P, SZ, I, P, F]),
     "mle_channel_sum": (I, [P, P, I, I, SZ, I, P]),
     "mle_channel_sum_ex": (I, [P, P, I, I, SZ, I, P, SZ, I]),

@@ -289,7 +289,9 @@ def _probe_step(hip, m, lr, fam):
 def test_block_qkv_fusion(hip, quirks):
     """Fused Q/K/V projections (one batched forward, one batched dW + db, one
     grouped sum-of-products dX) agree with one GEMM per projection and remove
-    exactly two launches of each of the NN, NT and TN families."""
+    exactly two NN launches and four backward products (NT and TN launches,
+    and the Linear pairs that hold one of each: at this size every unfused
+    projection's dX and dW share a launch)."""
     cfg = BlockConfig(batch=4, seq=64, d_model=128, heads=4, ffn=256, vocab=300)
     ids, tgt, params = block_data(cfg, seed=5)
     runs = {}
@@ -300,7 +302,7 @@ def test_block_qkv_fusion(hip, quirks):
         m.input(0, ids)
         m.input(1, tgt)
         counts = {}
-        for fam in ("gemm_nn", "gemm_nt", "gemm_tn"):
+        for fam in ("gemm_nn", "gemm_nt", "gemm_tn", "gemm_pair"):
             for i, p in enumerate(params):  # same starting point for every probed step
                 m.set(i, p)
                 m.set(i, np.zeros_like(p), 2)
@@ -309,8 +311,9 @@ def test_block_qkv_fusion(hip, quirks):
         runs[fuse] = (counts, m.loss, [m.get(i, 1) for i in range(len(params))])
         m.close()
     (cf, lf, gf), (cu, lu, gu) = runs[True], runs[False]
-    for fam, d in (("gemm_nn", 2), ("gemm_nt", 2), ("gemm_tn", 2)):
-        assert cu[fam] - cf[fam] == d, (fam, cu[fam], cf[fam])
+    assert cu["gemm_nn"] - cf["gemm_nn"] == 2, (cu, cf)
+    products = {k: c["gemm_nt"] + c["gemm_tn"] + 2 * c["gemm_pair"] for k, c in (("u", cu), ("f", cf))}
+    assert products["u"] - products["f"] == 4, (cu, cf)
     assert abs(lf - lu) <= 1e-5 * abs(lu)
     for i in range(len(params)):
         # Biases are judged on the scale of their layer's weight gradient (the

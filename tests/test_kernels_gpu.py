@@ -284,6 +284,10 @@ def test_gemm_sum(hip, orc, ta, tb, M, N, K, terms, beta):
     (64, 256, 10, 1, True, 0),        # both products small: one one-thread-per-output launch
     (64, 256, 10, 1, True, 1),
     (64, 100, 7, 2, True, 1),         # small, two layers: one launch per product
+    (64, 784, 256, 1, True, 0),       # K split over a workgroup's waves, both products in one launch
+    (64, 784, 256, 1, True, 1),
+    (100, 60, 333, 1, True, 1),       # the same with ragged tiles and K tails
+    (512, 512, 512, 1, False, 0),     # 32-wide K-split tiles
 ])
 def test_linear_bwd(hip, orc, rows, inp, out, layers, bias, acc):
     """mle_linear_bwd against the oracle's bcmm products and column sums, with
@@ -1745,10 +1749,12 @@ def test_gemm_act_fwd(hip, orc, kind, M, N, K, ws):
 
 @pytest.mark.parametrize("kind", ["relu", "gelu", "silu", "tanh"])
 @pytest.mark.parametrize("M,N,K,beta,acc", [(3000, 2900, 192, 0.0, 0), (3000, 2900, 192, 1.0, 1),
-                                            (300, 130, 70, 1.0, 1)])
+                                            (300, 130, 70, 1.0, 1), (64, 256, 10, 0.0, 0), (64, 256, 10, 1.0, 1)])
 def test_gemm_act_bwd(hip, orc, kind, M, N, K, beta, acc):
     """C (+)= A B^T (the activation output's gradient) and dX (+)= C * act'(X)
-    against the oracle's GEMM and activation derivative."""
+    against the oracle's GEMM and activation derivative: the persistent
+    kernel's epilogue (large), the K-split kernel's (300 x 130 x 70) and the
+    one-thread-per-output kernel's (K = 10)."""
     r = rng(M + 2 * N + K + hip.ACT[kind] + acc)
     A = r.standard_normal((M, K), dtype=np.float32) * 0.25
     Bm = r.standard_normal((N, K), dtype=np.float32) * 0.25
@@ -1766,6 +1772,58 @@ def test_gemm_act_bwd(hip, orc, kind, M, N, K, beta, acc):
              gdX.ptr, acc, None, 0)
     assert_close(gC.numpy(), c_ref, what="gemm_act_bwd C", **MM)
     assert_close(gdX.numpy(), dx_ref, what=f"gemm_act_bwd d{kind}", **MM)
+
+
+@pytest.mark.parametrize("kind", ["relu", "gelu"])
+@pytest.mark.parametrize("rows,inp,out,acc", [
+    (64, 256, 10, 0),      # both products one thread per output: the activation in their launch
+    (64, 256, 10, 1),
+    (64, 784, 256, 1),     # both on the K-split kernel: the activation in their launch
+    (300, 130, 70, 0),
+    (8192, 384, 128, 1),   # register-direct pair: the activation pass after it
+])
+def test_linear_bwd_act(hip, orc, kind, rows, inp, out, acc):
+    """mle_linear_bwd_act: a Linear's backward with the backward of the
+    activation before it.  dX, dW and db have the bits of mle_linear_bwd_ex
+    and the activation gradient those of mle_act_bwd on that dX (the same
+    formula, the product rounded before the add); both against the oracle."""
+    r = rng(rows + 3 * inp + out + acc + hip.ACT[kind])
+    k = hip.ACT[kind]
+    X = r.standard_normal((rows, inp), dtype=np.float32)
+    dY = r.standard_normal((rows, out), dtype=np.float32)
+    W = r.standard_normal((inp, out), dtype=np.float32)
+    Z = (r.standard_normal((rows, inp), dtype=np.float32) * 2).astype(np.float32)
+    dX0 = r.standard_normal((rows, inp), dtype=np.float32)
+    dZ0 = r.standard_normal((rows, inp), dtype=np.float32)
+    dW0 = r.standard_normal((inp, out), dtype=np.float32)
+    db0 = r.standard_normal(out, dtype=np.float32)
+    L = hip.lib()
+    need = L.mle_linear_bwd_ws_bytes(rows, inp, out, 1)
+    ws = hip.Buffer(max(need, 4))
+    gX, gdY, gW, gZ = B(hip, X), B(hip, dY), B(hip, W), B(hip, Z)
+    # unfused: the Linear's products, then the activation pass
+    udX, udW, udb, udZ = B(hip, dX0), B(hip, dW0), B(hip, db0), B(hip, dZ0)
+    hip.call("mle_linear_bwd_ex", None, rows, inp, out, 1, gX.ptr, gdY.ptr, 0, gW.ptr, 0, udX.ptr, acc, udW.ptr,
+             udb.ptr, 0, 1, ws.ptr, need)
+    hip.call("mle_act_bwd", None, k, gZ.ptr, udX.ptr, udZ.ptr, rows * inp, acc)
+    # fused; with acc 0 the destinations start as NaN (assigned, never read)
+    nan = np.full((rows, inp), np.nan, np.float32)
+    fdX, fdW, fdb, fdZ = B(hip, dX0 if acc else nan), B(hip, dW0), B(hip, db0), B(hip, dZ0 if acc else nan)
+    hip.call("mle_linear_bwd_act", None, rows, inp, out, gX.ptr, gdY.ptr, gW.ptr, fdX.ptr, acc, fdW.ptr, fdb.ptr, 1, k,
+             gZ.ptr, fdZ.ptr, acc, ws.ptr, need)
+    for got, want, what in ((fdX, udX, "dX"), (fdW, udW, "dW"), (fdb, udb, "db"), (fdZ, udZ, "activation dX")):
+        np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32), err_msg=what)
+    # against the oracle
+    want_dx = dX0.copy() if acc else np.zeros_like(dX0)
+    orc.call("orc_bcmm", 1, orc.ptr(dY), orc.ptr(W), orc.ptr(want_dx), 1, 1, rows, out, inp, 1, 3, 3, 3, 1.0)
+    want_dz = dZ0.copy() if acc else np.zeros_like(dZ0)
+    orc.call("orc_act_bwd", k, orc.ptr(Z), orc.ptr(want_dx), orc.ptr(want_dz), rows * inp)
+    want_dw = dW0.copy()
+    orc.call("orc_bcmm", 2, orc.ptr(X), orc.ptr(dY), orc.ptr(want_dw), 1, 1, inp, rows, out, 1, 3, 3, 3, 1.0)
+    assert_close(fdX.numpy(), want_dx, what="linear_bwd_act dX", **MM)
+    assert_close(fdZ.numpy(), want_dz, what=f"linear_bwd_act d{kind}", **MM)
+    assert_close(fdW.numpy(), want_dw, what="linear_bwd_act dW", **MM)
+    assert_close(fdb.numpy(), db0 + dY.astype(np.float64).sum(0), what="linear_bwd_act db", **EW)
 
 
 # ------------------------------------------------------------------ arena
