@@ -1037,17 +1037,35 @@ __global__ __launch_bounds__(256) void gemm_simple_pair_kernel(GemmArgs g0, Gemm
 // Small products with a long K (an MLP's 784-wide input layer: 64 x 256 x
 // 784 and its gradients): one C tile of TT x TT per workgroup of 16 waves.
 // Wave w multiplies the tile's operands over its K range [w kc, (w + 1) kc)
-// on MFMA (lane l feeds row or column l % 16 of a 16-wide block at k = kb +
-// l / 16), the workgroup adds the 16 partial tiles in wave order through LDS
-// and applies the epilogue: one launch where split K needs two (partials,
-// then the reduce), and more workgroups than the 64-wide tiles give the
-// same shape.  Column sums of B (the bias gradient) come from the workgroups
-// of the first tile row, in (wave, lane group) order.
+// (whole 16-deep slabs) on MFMA, the workgroup adds the 16 partial tiles in
+// wave order through LDS and applies the epilogue: one launch where split K
+// needs two (partials, then the reduce), and more workgroups than the
+// 64-wide tiles give the same shape.  Within a 16-deep slab lane group q =
+// l / 16 feeds k = 4q + e to MFMA step e (the k permutation of the tile
+// kernels), so an operand stored k-contiguous is read with one 16-byte load
+// per lane and slab (scattered 4-byte loads of it took twice the kernel's
+// time), and one stored m- or n-contiguous with four 4-byte loads, 64
+// contiguous bytes per k row.  Column sums of B (the bias gradient) come
+// from the workgroups of the first tile row, in (wave, lane group) order.
 constexpr int KS_NW = 16, KS_NT = 64 * KS_NW;
 
 template <int TT>
 constexpr int ks_lds_floats() {
   return KS_NW * TT * TT + KS_NW * 4 * TT;
+}
+
+// Four k-consecutive elements p[0..3] of a k-contiguous operand row, zero at
+// k >= k1 (k = kq + e).
+__device__ __forceinline__ f32x4 ks_row4(const float* p, int kq, int k1, bool vec) {
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  if (vec && kq + 3 < k1) {
+    v = *reinterpret_cast<const f32x4*>(p);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (kq + e < k1) v[e] = p[e];
+  }
+  return v;
 }
 
 template <int TA, int TB, int TT>
@@ -1058,6 +1076,9 @@ __device__ __forceinline__ void ksplit_body(const GemmArgs& g, int tx, int ty, i
   const int m0 = ty * TT, n0 = tx * TT;
   const float* __restrict__ A = g.A + batch_off(z, g, g.sa, g.sa2);
   const float* __restrict__ B = g.B + batch_off(z, g, g.sb, g.sb2);
+  // 16-byte loads along k need 16-byte aligned rows
+  const bool a_vec = !TA && g.lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  const bool b_vec = TB && g.ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0;
   const bool cs_on = g.colsum != nullptr && ty == 0;
   const int k0 = w * kc, k1 = min(g.K, k0 + kc);
   int am[S], bn[S];
@@ -1077,40 +1098,59 @@ __device__ __forceinline__ void ksplit_body(const GemmArgs& g, int tx, int ty, i
 #pragma unroll
     for (int j = 0; j < S; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // Chunks of CH four-deep steps: every load of a chunk is issued before its
-  // products (one memory latency per chunk); steps past the wave's range are
-  // skipped on a wave-uniform branch.
-  constexpr int CH = 16 / S;
-  for (int kb = k0; kb < k1; kb += 4 * CH) {
-    float a[CH][S], b[CH][S];
+  // Chunks of SL slabs: every load of a chunk is issued before its products
+  // (one memory latency per chunk); slabs past the wave's range are skipped
+  // on a wave-uniform branch.
+  constexpr int SL = 4 / S;
+  for (int kb = k0; kb < k1; kb += 16 * SL) {
+    f32x4 a[SL][S], b[SL][S];  // element e: MFMA step e of the slab
 #pragma unroll
-    for (int t = 0; t < CH; ++t) {
-      const int kk = kb + 4 * t + lq;
-      const bool kok = kk < k1;
+    for (int t = 0; t < SL; ++t)
 #pragma unroll
       for (int i = 0; i < S; ++i) {
-        a[t][i] = 0.f;
-        b[t][i] = 0.f;
+        a[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        b[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      if (kb + 4 * t < k1) {
+#pragma unroll
+    for (int t = 0; t < SL; ++t) {
+      const int kq = kb + 16 * t + 4 * lq;  // this lane's four k of the slab
+      if (kb + 16 * t < k1) {
 #pragma unroll
         for (int i = 0; i < S; ++i) {
-          if (kok && aok[i]) a[t][i] = TA ? A[(int64_t)kk * g.lda + am[i]] : A[(int64_t)am[i] * g.lda + kk];
-          if (kok && bok[i]) b[t][i] = TB ? B[(int64_t)bn[i] * g.ldb + kk] : B[(int64_t)kk * g.ldb + bn[i]];
+          if (aok[i]) {
+            if (TA) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (kq + e < k1) a[t][i][e] = A[(int64_t)(kq + e) * g.lda + am[i]];
+            } else {
+              a[t][i] = ks_row4(A + (int64_t)am[i] * g.lda + kq, kq, k1, a_vec);
+            }
+          }
+          if (bok[i]) {
+            if (TB) {
+              b[t][i] = ks_row4(B + (int64_t)bn[i] * g.ldb + kq, kq, k1, b_vec);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (kq + e < k1) b[t][i][e] = B[(int64_t)(kq + e) * g.ldb + bn[i]];
+            }
+          }
         }
       }
     }
 #pragma unroll
-    for (int t = 0; t < CH; ++t) {
-      if (kb + 4 * t >= k1) break;
+    for (int t = 0; t < SL; ++t) {
+      if (kb + 16 * t >= k1) break;
 #pragma unroll
-      for (int i = 0; i < S; ++i)
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int j = 0; j < S; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][i], b[t][j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < S; ++i)
+#pragma unroll
+          for (int j = 0; j < S; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][i][e], b[t][j][e], acc[i][j], 0, 0, 0);
       if (cs_on)
 #pragma unroll
-        for (int j = 0; j < S; ++j) cs[j] += b[t][j];
+        for (int j = 0; j < S; ++j) cs[j] += ((b[t][j][0] + b[t][j][1]) + b[t][j][2]) + b[t][j][3];
     }
   }
   // Partial tiles: result lane l holds rows 4 (l / 16) + r of column l % 16.
@@ -1346,8 +1386,8 @@ static bool ksplit_shape(int M, int N, int K, int batch, int terms) {
   const int tt = ksplit_tile(M, N, batch);
   return K <= (tt == 16 ? 4096 : 1024) && (M + tt - 1) / tt <= 65535 && batch <= 65535;
 }
-// K range of one wave: whole 4-deep MFMA steps.
-static int ksplit_kc(int K) { return ((K + KS_NW - 1) / KS_NW + 3) / 4 * 4; }
+// K range of one wave: whole 16-deep slabs.
+static int ksplit_kc(int K) { return ((K + KS_NW - 1) / KS_NW + 15) / 16 * 16; }
 
 const char* const kFamily[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
 
