@@ -422,6 +422,17 @@ int mle_softmax_xent_bwd(mle_stream stream, const float* probs, const float* tar
 int mle_softmax_xent_keys_small_read(mle_stream stream, const float* logits, const int32_t* keys, int clen,
                                      int max_clen, float* stats, int rows, int cols, int batch, float* loss,
                                      float* dlogits, float* loss_host);
+/* A classifier head -- Linear (logits = X W + bias, Engine/engine.cu:3505-3530)
+ * followed by SoftMaxCrossEntropy against key targets (Engine/engine.cu:
+ * 2088-2110) -- in one launch when the logits are at most 16 tiles of 16 x 16
+ * and 4096 values (else mle_gemm_ex then mle_softmax_xent_keys_small_read):
+ * logits [rows, cols] are written, then everything
+ * mle_softmax_xent_keys_small_read does with them (the same bits for the
+ * same logits; the logits' products are added in this kernel's own order).
+ * X [rows, in], W [in, cols], bias [cols] or NULL; rows <= 1024, cols <= 64. */
+int mle_linear_xent_keys_small_read(mle_stream stream, int rows, int in, int cols, const float* X, const float* W,
+                                    const float* bias, float* logits, const int32_t* keys, int clen, int max_clen,
+                                    float* stats, int batch, float* loss, float* dlogits, float* loss_host);
 /* Cross-entropy against one-hot rows given by token ids: row r = b*clen + s
  * has its 1 at column keys[b*max_clen + s] if that id is in [0, cols), else
  * no 1 -- the matrix OneHotEmbeddings builds (Engine/kernels.cu:1551-1560).

@@ -645,10 +645,11 @@ constexpr unsigned kMsePartCap = 2048;
 // workgroup's sum of the row terms over rows * cols in finish_scalar_kernel's
 // order, published for the host when a slot is given.  With dl set, the
 // gradient (p - t) / batch of xent_keys_bwd_kernel too.
-__global__ __launch_bounds__(FIN_NT) void xent_keys_small_kernel(const float* __restrict__ x, KeyTargets kt, int rows,
-                                                                 int cols, float batch, float* __restrict__ loss,
-                                                                 float* __restrict__ dl, mle::ScalarSlot* slot,
-                                                                 unsigned seq) {
+// The body of xent_keys_small_kernel over logits x (global memory, or the
+// LDS copy the Linear + cross-entropy kernel keeps).
+__device__ __forceinline__ void xent_small_body(const float* x, KeyTargets kt, int rows, int cols, float batch,
+                                                float* __restrict__ loss, float* __restrict__ dl,
+                                                mle::ScalarSlot* slot, unsigned seq) {
   __shared__ double red[FIN_NT / 64];
   __shared__ float srow[2 * FIN_NT];  // (max, sum) per row for the gradient phase
   __shared__ int skey[FIN_NT];
@@ -699,6 +700,95 @@ __global__ __launch_bounds__(FIN_NT) void xent_keys_small_kernel(const float* __
       dl[i] = (p + (-1.0f) * (c == skey[r] ? 1.0f : 0.0f)) / batch;
     }
   }
+}
+
+__global__ __launch_bounds__(FIN_NT) void xent_keys_small_kernel(const float* __restrict__ x, KeyTargets kt, int rows,
+                                                                 int cols, float batch, float* __restrict__ loss,
+                                                                 float* __restrict__ dl, mle::ScalarSlot* slot,
+                                                                 unsigned seq) {
+  xent_small_body(x, kt, rows, cols, batch, loss, dl, slot, seq);
+}
+
+// A classifier head, Linear then cross-entropy against key targets, in one
+// workgroup: logits = X W + bias (X [rows, in], W [in, cols]) on fp32 MFMA,
+// the 16 x 16 tiles of the logits (at most LXS_T of them) each taken by
+// 16 / tiles waves that split `in` in whole 16-deep slabs and add their
+// partial tiles in wave order through LDS; the logits are written out (the
+// Linear's output) and kept in LDS, and xent_keys_small_kernel's body runs on
+// them: the loss, its read-back, the row statistics and the early gradient.
+// Lane group q = l / 16 of a wave feeds k = 4q + e of a slab to MFMA step e,
+// so a row of X is read with one 16-byte load per lane and slab.
+constexpr int LXS_T = 16, LXS_MAXN = 4096;
+
+__global__ __launch_bounds__(FIN_NT) void linear_xent_small_kernel(const float* __restrict__ X,
+                                                                   const float* __restrict__ W,
+                                                                   const float* __restrict__ bias,
+                                                                   float* __restrict__ logits, int rows, int in,
+                                                                   int cols, KeyTargets kt, float batch,
+                                                                   float* __restrict__ loss, float* __restrict__ dl,
+                                                                   mle::ScalarSlot* slot, unsigned seq) {
+  __shared__ __attribute__((aligned(16))) float part[FIN_NT / 64][256];
+  __shared__ float lg[LXS_MAXN];
+  const int lane = threadIdx.x & 63, li = lane & 15, lq = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int tn = (cols + 15) / 16, tiles = ((rows + 15) / 16) * tn;
+  const int wpt = (FIN_NT / 64) / tiles;  // waves per tile
+  if (w < tiles * wpt) {
+    const int tile = w / wpt, q = w - tile * wpt;
+    const int r = (tile / tn) * 16 + li, c = (tile % tn) * 16 + li;  // this lane's X row and W column
+    const bool rok = r < rows, cok = c < cols;
+    const int kc = ((in + wpt - 1) / wpt + 15) / 16 * 16;
+    const int k0 = q * kc, k1 = min(in, k0 + kc);
+    const bool vec = in % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = k0; kb < k1; kb += 64) {  // four slabs: every load issued before the products
+      f32x4 a[4], b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        a[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        b[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int kq = kb + 16 * t + 4 * lq;
+        if (kb + 16 * t < k1) {
+          if (rok) {
+            const float* p = X + (size_t)r * in + kq;
+            if (vec && kq + 3 < k1) {
+              a[t] = *reinterpret_cast<const f32x4*>(p);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (kq + e < k1) a[t][e] = p[e];
+            }
+          }
+          if (cok)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (kq + e < k1) b[t][e] = W[(size_t)(kq + e) * cols + c];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (kb + 16 * t >= k1) break;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][e], b[t][e], acc, 0, 0, 0);
+      }
+    }
+    // result lane l holds rows 4 (l / 16) + i of column l % 16
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[w][(4 * lq + i) * 16 + li] = acc[i];
+  }
+  __syncthreads();
+  const int n = rows * cols;
+  for (int o = threadIdx.x; o < n; o += FIN_NT) {
+    const int r = o / cols, c = o - r * cols;
+    const int tile = (r / 16) * tn + c / 16, at = (r % 16) * 16 + c % 16;
+    float v = part[tile * wpt][at];
+    for (int q = 1; q < wpt; ++q) v += part[tile * wpt + q][at];
+    if (bias) v += bias[c];
+    lg[o] = v;
+    logits[o] = v;
+  }
+  __syncthreads();
+  xent_small_body(lg, kt, rows, cols, batch, loss, dl, slot, seq);
 }
 
 }  // namespace
@@ -925,6 +1015,36 @@ int mle_softmax_xent_keys_small_read(mle_stream stream, const float* logits, con
   const int rc = check_launch("mle_softmax_xent_keys_small_read");
   if (rc || !loss_host) return rc;
   return mle::scalar_read_finish(s, r, loss_host, "mle_softmax_xent_keys_small_read");
+}
+
+int mle_linear_xent_keys_small_read(mle_stream stream, int rows, int in, int cols, const float* X, const float* W,
+                                    const float* bias, float* logits, const int32_t* keys, int clen, int max_clen,
+                                    float* stats, int batch, float* loss, float* dlogits, float* loss_host) {
+  MLE_CHECK_ARG(X && W && logits && keys && stats && loss && rows > 0 && in >= 0 && cols > 0 && clen > 0 &&
+                    max_clen >= clen && rows % clen == 0 && batch > 0,
+                "mle_linear_xent_keys_small_read: bad argument");
+  MLE_CHECK_ARG(rows <= FIN_NT && cols <= 64, "mle_linear_xent_keys_small_read: %d x %d logits exceed %d x 64", rows,
+                cols, FIN_NT);
+  const int tiles = ((rows + 15) / 16) * ((cols + 15) / 16);
+  if (tiles > LXS_T || rows * cols > LXS_MAXN) {  // the two launches
+    const int rc = mle_gemm_ex(stream, 0, 0, rows, cols, in, 1.0f, X, in, 0, W, cols, 0, 0.0f, logits, cols, 0, 1,
+                               nullptr, bias, nullptr, 0);
+    if (rc) return rc;
+    return mle_softmax_xent_keys_small_read(stream, logits, keys, clen, max_clen, stats, rows, cols, batch, loss,
+                                            dlogits, loss_host);
+  }
+  hipStream_t s = as_stream(stream);
+  const KeyTargets kt{keys, clen, max_clen, stats};
+  mle::ScalarRead r;
+  if (loss_host) {
+    const int rc = mle::scalar_read_begin(r, "mle_linear_xent_keys_small_read");
+    if (rc) return rc;
+  }
+  linear_xent_small_kernel<<<1, FIN_NT, 0, s>>>(X, W, bias, logits, rows, in, cols, kt, (float)batch, loss, dlogits,
+                                                r.slot, r.seq);
+  const int rc = check_launch("mle_linear_xent_keys_small_read");
+  if (rc || !loss_host) return rc;
+  return mle::scalar_read_finish(s, r, loss_host, "mle_linear_xent_keys_small_read");
 }
 
 int mle_softmax_xent_keys_bwd(mle_stream stream, const float* logits, const float* stats, const int32_t* keys, int clen,

@@ -988,6 +988,14 @@ graph Linear::forward(const graph& X) {
                              nd->output, has_bias ? Bb->output : nullptr, kind, act_out, ws, ws_bytes),
             "MatMul... X*W1 + B1 in " + name + " forward (with the activation after it)");
     };
+  if ((double)rows * p <= 4096.0)
+    node->forward_xent_small = [=](const int32_t* keys, int clen, int max_clen, float* stats, int batch, float* loss,
+                                   float* dlogits, float* loss_host) {
+      check(mle_linear_xent_keys_small_read(mle::stream(), (int)rows, n, p, x->output, W->output,
+                                            has_bias ? Bb->output : nullptr, nd->output, keys, clen, max_clen, stats,
+                                            batch, loss, dlogits, loss_host),
+            "MatMul... X*W1 + B1 in " + name + " forward (with the cross-entropy after it)");
+    };
   node->forward_rowstats = [=](float* rowpart, int64_t ldp) {
     check(mle_gemm_rowstats(mle::stream(), 0, 0, (int)rows, p, n, 1.0f, x->output, n, W->output, p, 0.0f,
                             nd->output, p, has_bias ? Bb->output : nullptr, rowpart, ldp, ws, ws_bytes),

@@ -227,6 +227,14 @@ struct NodeBackProp {
   // activation: out = act(y) + cbias[channel], the activation's own output
   // not written (mle_norm_fwd_act_bias).
   std::function<void(int kind, float* out, const float* cbias)> forward_act_bias;
+  // Set by a small Linear (additive): its forward together with a
+  // cross-entropy against key targets of its output (the loss's row
+  // statistics, loss value and read-back, and the early gradient), one launch
+  // (mle_linear_xent_keys_small_read).  The loss node takes the Linear's
+  // forward over with it.
+  std::function<void(const int32_t* keys, int clen, int max_clen, float* stats, int batch, float* loss,
+                     float* dlogits, float* loss_host)>
+      forward_xent_small;
   // An activation whose output the normalisation before it writes (the
   // activation kind), else -1.
   int fused_act_kind = -1;

@@ -133,6 +133,7 @@ graph act_node(const graph& input, int kind, const str& name) {
     input->forward_act = nullptr;  // one takeover per producer
     input->forward_normstats = nullptr;
     input->forward_rowstats = nullptr;
+    input->forward_xent_small = nullptr;
     node->forward = []() {};
     node->fused_act_kind = kind;
     fused = true;
@@ -643,6 +644,30 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
   // gradient in one launch; the gradient is held early (grad_early) until our
   // backward commits it.
   const bool small = by_keys && last && mle::fusion_enabled() && rows <= 1024 && d <= 64;
+  // A small Linear prediction (a classifier head): its forward and all of the
+  // above in one launch, at the Linear's place (its forward is taken over,
+  // while it is still its own: the row-statistics hook marks that).
+  bool head = false;
+  if (small && prediction->forward_xent_small && prediction->forward_rowstats &&
+      prediction->total == (long long)rows * d) {
+    auto fx = prediction->forward_xent_small;
+    auto plain = prediction->forward;
+    prediction->forward = [=]() {
+      if (!calculate_loss) {  // no loss asked: the Linear alone
+        plain();
+        return;
+      }
+      const bool early = pr->grad_pending_zero && !pr->grad_src;
+      fx(oh->keys, oh->clen, oh->max_clen, stats, batch, nd->output, early ? pr->grad : nullptr,
+         &GraphOperations::loss);
+      pr->grad_early = early;
+      nd->output_pending_zero = false;
+    };
+    prediction->forward_xent_small = nullptr;
+    prediction->forward_rowstats = nullptr;
+    prediction->forward_act = nullptr;
+    head = true;
+  }
   float* rowpart = nullptr;
   if (!small && by_keys && mle::fusion_enabled() && prediction->forward_rowstats &&
       prediction->total == (long long)rows * d) {
@@ -653,6 +678,7 @@ graph GraphOperations::SoftMaxCrossEntropy(const graph& prediction, const graph&
   }
   node->forward = [=]() {
     if (calculate_loss || !last) {
+      if (head) return;  // the Linear's forward did it all
       if (small) {
         const bool early = pr->grad_pending_zero && !pr->grad_src;
         check(mle_softmax_xent_keys_small_read(S(), pr->output, oh->keys, oh->clen, oh->max_clen, stats, rows, d,

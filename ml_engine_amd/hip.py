@@ -98,6 +98,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_mse_bwd": (I, [P, P, P, P, P, SZ, I]),
     "mle_softmax_xent_keys_fwd": (I, [P, P, P, I, I, P, I, I, P, P, SZ]),
     "mle_softmax_xent_keys_small_read": (I, [P, P, P, I, I, P, I, I, I, P, P, P]),
+    "mle_linear_xent_keys_small_read": (I, [P, I, I, I, P, P, P, P, P, I, I, P, I, P, P, P]),
     "mle_softmax_xent_keys_bwd": (I, [P, P, P, P, I, I, P, P, I, I, I]),
     "mle_softmax_xent_fwd": (I, [P, P, P, P, I, I, P, P, SZ]),
     "mle_softmax_xent_bwd": (I, [P, P, P, P, P, SZ, I]),

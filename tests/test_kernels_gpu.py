@@ -1623,6 +1623,49 @@ def test_softmax_xent_keys_rowstats(hip, batch, clen, cols):
         assert np.float32(host.value).view(np.uint32) == gloss2.numpy().view(np.uint32)[0], (rep, host.value)
 
 
+@pytest.mark.parametrize("batch,clen,cols,hidden,bias", [
+    (64, 1, 10, 256, True),   # C1's head: 4 tiles, 4 waves each
+    (3, 12, 33, 100, False),  # 3 x 3 ragged tiles, K tails, no bias
+    (16, 1, 64, 70, True),    # 4 tile columns
+    (16, 16, 16, 64, True),   # 16 tiles: one wave each
+    (20, 5, 64, 50, True),    # 28 tiles: the two-launch path
+])
+def test_linear_xent_keys_small(hip, orc, batch, clen, cols, hidden, bias):
+    """A classifier head (Linear, then the cross-entropy against ids) in one
+    launch: the logits against the oracle's product plus bias, and the row
+    statistics, loss, host read-back and gradient the bits of
+    mle_softmax_xent_keys_small_read on those logits, on two calls in a row."""
+    r = rng(batch + clen * 5 + cols + hidden)
+    rows = batch * clen
+    X = r.standard_normal((rows, hidden), dtype=np.float32)
+    W = (r.standard_normal((hidden, cols), dtype=np.float32) * 0.5).astype(np.float32)
+    b = r.standard_normal(cols, dtype=np.float32)
+    keys = r.integers(0, cols, (batch, clen)).astype(np.int32)
+    keys[0, 0] = -1
+    keys[-1, -1] = cols + 2
+    want = np.zeros((rows, cols), np.float32)
+    orc.call("orc_bcmm", 0, orc.ptr(X), orc.ptr(W), orc.ptr(want), 1, 1, rows, hidden, cols, 0, 3, 3, 3, 1.0)
+    if bias:
+        want += b
+    gX, gW, gb, gk = B(hip, X), B(hip, W), B(hip, b), B(hip, keys)
+    for rep in range(2):
+        glog = B(hip, np.full((rows, cols), np.nan, np.float32))
+        gst, gloss = B(hip, np.full(2 * rows, np.nan, np.float32)), hip.Buffer.zeros(1)
+        gd = B(hip, np.full((rows, cols), np.nan, np.float32))
+        host = C.c_float(float("nan"))
+        hip.call("mle_linear_xent_keys_small_read", None, rows, hidden, cols, gX.ptr, gW.ptr, gb.ptr if bias else None,
+                 glog.ptr, gk.ptr, clen, clen, gst.ptr, batch, gloss.ptr, gd.ptr, C.byref(host))
+        assert_close(glog.numpy(), want, what="head logits", **MM)
+        gst2, gloss2 = hip.Buffer.zeros(2 * rows), hip.Buffer.zeros(1)
+        gd2 = hip.Buffer.zeros((rows, cols))
+        host2 = C.c_float(float("nan"))
+        hip.call("mle_softmax_xent_keys_small_read", None, glog.ptr, gk.ptr, clen, clen, gst2.ptr, rows, cols, batch,
+                 gloss2.ptr, gd2.ptr, C.byref(host2))
+        for got, ref, what in ((gst, gst2, "stats"), (gloss, gloss2, "loss"), (gd, gd2, "gradient")):
+            np.testing.assert_array_equal(got.numpy().view(np.uint32), ref.numpy().view(np.uint32), err_msg=what)
+        assert np.float32(host.value).view(np.uint32) == np.float32(host2.value).view(np.uint32), rep
+
+
 @pytest.mark.parametrize("batch,clen,cols,hidden", [(64, 1, 10, 256), (4, 16, 64, 32), (3, 5, 7, 40), (16, 64, 33, 8)])
 def test_softmax_xent_keys_small(hip, orc, batch, clen, cols, hidden):
     """A classifier head's cross-entropy in one launch (rows <= 1024,
