@@ -646,45 +646,58 @@ constexpr unsigned kMsePartCap = 2048;
 // order, published for the host when a slot is given.  With dl set, the
 // gradient (p - t) / batch of xent_keys_bwd_kernel too.
 // The body of xent_keys_small_kernel over logits x (global memory, or the
-// LDS copy the Linear + cross-entropy kernel keeps).
+// LDS copy the Linear + cross-entropy kernel keeps).  Each row is taken by 16
+// lanes holding columns 4 l + v: the maximum by shuffles (its value does not
+// depend on the order), then the 64-lane butterfly of rowstats_kernel over
+// the exponentials (level `off` pairs columns j and j ^ off: lanes l ^ 8, 4,
+// 2, 1 for off = 32 .. 4, then registers v ^ 2, v ^ 1), so each pair is added
+// as there and the bits are the same.
 __device__ __forceinline__ void xent_small_body(const float* x, KeyTargets kt, int rows, int cols, float batch,
                                                 float* __restrict__ loss, float* __restrict__ dl,
                                                 mle::ScalarSlot* slot, unsigned seq) {
   __shared__ double red[FIN_NT / 64];
   __shared__ float srow[2 * FIN_NT];  // (max, sum) per row for the gradient phase
   __shared__ int skey[FIN_NT];
-  const int row = threadIdx.x;
-  double lp = 0.0;
-  if (row < rows) {
-    const float* xr = x + (size_t)row * cols;
-    const int key = kt.key((size_t)row, cols);
-    const float xk = key >= 0 ? xr[key] : 0.f;
-    float e[64];
+  __shared__ double slp[FIN_NT];      // each row's loss term, summed in row order below
+  const int grp = threadIdx.x >> 4, gl = threadIdx.x & 15;
+  for (int rb = 0; rb < rows; rb += FIN_NT / 16) {
+    const int row = rb + grp;
+    const bool live = row < rows;
+    float e[4] = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+    int key = -1;
+    float xk = 0.f;
+    if (live) {
+      const float* xr = x + (size_t)row * cols;
+      key = kt.key((size_t)row, cols);
+      if (key >= 0) xk = xr[key];
 #pragma unroll
-    for (int j = 0; j < 64; ++j) e[j] = j < cols ? xr[j] : -FLT_MAX;
-    float m = -FLT_MAX;
+      for (int v = 0; v < 4; ++v)
+        if (4 * gl + v < cols) e[v] = xr[4 * gl + v];
+    }
+    float m = fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3]));
 #pragma unroll
-    for (int j = 0; j < 64; ++j) m = fmaxf(m, e[j]);  // a max's value does not depend on the order
+    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
 #pragma unroll
-    for (int j = 0; j < 64; ++j) e[j] = j < cols ? expf(e[j] - m) : 0.f;
-    // the butterfly in place: lanes j and j ^ off both end with their sum
+    for (int v = 0; v < 4; ++v) e[v] = (live && 4 * gl + v < cols) ? expf(e[v] - m) : 0.f;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
+    for (int o = 8; o >= 1; o >>= 1)
 #pragma unroll
-      for (int j = 0; j < 64; ++j)
-        if ((j & off) == 0) {
-          const float t = e[j] + e[j ^ off];
-          e[j] = t;
-          e[j ^ off] = t;
-        }
-    const float sum = e[0] < 1e-45f ? 1.0f : e[0];
-    if (key >= 0) lp = -log((double)(expf(xk - m) / sum) + 1e-27);
-    kt.stats[2 * row] = m;
-    kt.stats[2 * row + 1] = sum;
-    srow[2 * row] = m;
-    srow[2 * row + 1] = sum;
-    skey[row] = key;
+      for (int v = 0; v < 4; ++v) e[v] = e[v] + __shfl_xor(e[v], o, 16);
+    e[0] = e[0] + e[2];
+    e[1] = e[1] + e[3];
+    e[0] = e[0] + e[1];
+    if (live && gl == 0) {
+      const float sum = e[0] < 1e-45f ? 1.0f : e[0];
+      slp[row] = key >= 0 ? -log((double)(expf(xk - m) / sum) + 1e-27) : 0.0;
+      kt.stats[2 * row] = m;
+      kt.stats[2 * row + 1] = sum;
+      srow[2 * row] = m;
+      srow[2 * row + 1] = sum;
+      skey[row] = key;
+    }
   }
+  __syncthreads();
+  const double lp = (int)threadIdx.x < rows ? slp[threadIdx.x] : 0.0;
   double acc = (lp + 0.0) + (0.0 + 0.0);  // finish_scalar_kernel's four accumulators, three of them empty
   acc = block_sum<FIN_NT>(acc, red);  // its barriers also order the row statistics in LDS
   if (threadIdx.x == 0) {  // published first: the host waiting for the loss resumes sooner
