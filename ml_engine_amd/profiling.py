@@ -198,7 +198,9 @@ def counter_table(fetch_db: str, write_db: str, cfetch_db: str, cwrite_db: str, 
     ct = [t for _, k, _, t in per_dispatch(cfetch_db, "FETCH_SIZE") if COPY_KERNEL in k]
     lines = [f"Calibration (copy of {n} floats): FETCH_SIZE x {f_fetch:.3f}, WRITE_SIZE x {f_write:.3f}; "
              f"the copy itself ran {mean(ct) / 1e3:.1f} us per launch in that counter run, "
-             f"{8.0 * n / mean(ct):.0f} GB/s (read + write), the practical streaming ceiling.", ""]
+             f"{8.0 * n / mean(ct):.0f} GB/s (read + write): the streaming rate of data that does not fit the "
+             f"256 MB Infinity Cache, at equal reads and writes (kernels that mostly read, or whose reads that "
+             f"cache serves, run faster).", ""]
     head = "| kernel | launches | avg us (counter run) | fetch MB/launch | write MB/launch | HBM MB/launch | GB/s |"
     sep = "|---|---:|---:|---:|---:|---:|---:|"
     if mfma_db:
