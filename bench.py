@@ -373,7 +373,7 @@ def extras_mlp(cpu: bool, steps: int = 1000) -> dict:
     m.close()
     flop = 78.0e6
     out = {"workload": "C1 MLP 784-256-10 step (fwd + bwd + Adam), batch 64", "ms_per_step": round(ms, 4),
-           "steps_per_s": round(1e3 / ms, 1), "bound": "launch latency (GEMMs of 1-7 tiles)",
+           "steps_per_s": round(1e3 / ms, 1), "bound": "launch latency (5 launches of a few microseconds each)",
            "graph_replay": {"ms_per_step": round(ms_graph, 4), "steps_per_s": round(1e3 / ms_graph, 1)}
            if ms_graph else None,
            "roofline": rl}
