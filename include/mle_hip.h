@@ -401,6 +401,15 @@ int mle_mse_fwd_read(mle_stream stream, const float* x, const float* t, size_t n
  * the same bits as mle_mse_bwd(..., NULL, dx, n, 0). */
 int mle_mse_fwd_bwd_read(mle_stream stream, const float* x, const float* t, size_t n, float* loss, float* dx,
                          void* ws, size_t ws_bytes, float* loss_host);
+/* mle_mse_fwd_bwd_read when the prediction is an activation's output
+ * x = act(z) (Engine/kernels.cu:1214, 1248, 1286 and their derivatives),
+ * reading z instead of x: the loss (x recomputed from z with the
+ * activation's function, the bits mle_act_fwd stores), its read-back,
+ * x's gradient dx = 2 (x - t) / n and z's gradient dz = act'(z) * dx, both
+ * assigned -- the bits of mle_mse_fwd_bwd_read on x followed by
+ * mle_act_bwd(act_kind, z, dx, dz, n, 0), in one pass over z and t. */
+int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, size_t n, int act_kind, float* loss,
+                             float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host);
 /* dx (+)= 2 (x - t) / n * (upstream ? upstream[0] : 1).  deriv_mse_kernel (Engine/kernels.cu:1838-1848). */
 int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,
                 int accumulate);

@@ -3,6 +3,7 @@
 // line (row or column) is held in registers while its max and sum are reduced
 // with wave64 shuffles, instead of the reference's 4 launches with one thread
 // per line (SoftMax/SoftMask/deriv_softmax, Engine/kernels.cu:2003-2244).
+#include "activation.hpp"
 #include "common.hpp"
 
 #include <algorithm>
@@ -492,6 +493,60 @@ __global__ __launch_bounds__(NT) void mse_partial4_kernel(const float* __restric
   if (threadIdx.x == 0) part[blockIdx.x] = acc;
 }
 
+// The last MSE node's forward when its prediction is an activation's output
+// x = act(z): the partial sums of mse_partial_kernel / mse_partial4_kernel
+// (the same grid, order and terms; x recomputed from z with the activation's
+// own function, the bits the activation stored), x's gradient g = 2 (x - t) /
+// n and z's gradient act'(z) g with the product rounded (the activation
+// backward's formula), both assigned, in one pass over z and t.
+template <int K>
+__device__ __forceinline__ float mse_act_dz(float z, float g) {
+#pragma clang fp contract(off)
+  return act_df<K>(z) * g;
+}
+
+// Contraction off in this kernel's own arithmetic, so that x - t is not fused
+// with the activation's last product: x is rounded first, as when it is
+// stored and read back.
+template <int K, bool VEC>
+__global__ __launch_bounds__(NT) void mse_act_partial_kernel(const float* __restrict__ z, const float* __restrict__ t,
+                                                             size_t n, double* __restrict__ part,
+                                                             float* __restrict__ dx, float* __restrict__ dz) {
+#pragma clang fp contract(off)
+  __shared__ double red[NT / 64];
+  double acc = 0.0;
+  const size_t stride = (size_t)gridDim.x * NT;
+  const float fn = (float)n;
+  if (VEC) {
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n / 4; i += stride) {
+      const f32x4 zv = ldv(z, i * 4), tv = ldv(t, i * 4);
+      f32x4 g, d;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float xj = act_f<K>(zv[j]);
+        const double e = (double)tv[j] - (double)xj;
+        acc += e * e;
+        g[j] = 2.0f * (xj - tv[j]) / fn;
+        d[j] = mse_act_dz<K>(zv[j], g[j]);
+      }
+      stv(dx, i * 4, g);
+      stv(dz, i * 4, d);
+    }
+  } else {
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
+      const float zi = z[i], ti = t[i];
+      const float xi = act_f<K>(zi);
+      const double e = (double)ti - (double)xi;
+      acc += e * e;
+      const float g = 2.0f * (xi - ti) / fn;
+      dx[i] = g;
+      dz[i] = mse_act_dz<K>(zi, g);
+    }
+  }
+  acc = block_sum<NT>(acc, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = acc;
+}
+
 // One 1024-thread workgroup; four loads in flight per thread, fixed order.
 constexpr int FIN_NT = 1024;
 // With a slot, the value is also published for the host (mle_read_scalar),
@@ -903,6 +958,39 @@ int mle_mse_fwd_bwd_read(mle_stream stream, const float* x, const float* t, size
                          void* ws, size_t ws_bytes, float* loss_host) {
   MLE_CHECK_ARG(loss_host != nullptr && dx != nullptr, "mle_mse_fwd_bwd_read: null pointer");
   return mse_fwd_impl(stream, x, t, n, loss, ws, ws_bytes, loss_host, "mle_mse_fwd_bwd_read", dx);
+}
+
+int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, size_t n, int act_kind, float* loss,
+                             float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host) {
+  const char* who = "mle_mse_act_fwd_bwd_read";
+  MLE_CHECK_ARG(z && t && loss && dx && dz && ws && loss_host && n > 0 && act_kind >= MLE_RELU &&
+                    act_kind <= MLE_LEAKY_RELU,
+                "%s: bad argument", who);
+  const unsigned g = stream_grid(n, NT, kMsePartCap);
+  if (ws_bytes < g * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "%s: workspace too small", who);
+  hipStream_t s = as_stream(stream);
+  double* part = static_cast<double*>(ws);
+  mle::ScalarRead r;
+  int rc = mle::scalar_read_begin(r, who);
+  if (rc) return rc;
+  const bool vec = n % 4 == 0 && aligned16(z) && aligned16(t) && aligned16(dx) && aligned16(dz);
+  const unsigned np = vec ? stream_grid(n / 4, NT, kMsePartCap) : g;  // mse_fwd_impl's grids
+#define MLE_MSE_ACT(K)                                                                            \
+  (vec ? mse_act_partial_kernel<K, true><<<np, NT, 0, s>>>(z, t, n, part, dx, dz)                 \
+       : mse_act_partial_kernel<K, false><<<np, NT, 0, s>>>(z, t, n, part, dx, dz))
+  switch (act_kind) {
+    case MLE_RELU: MLE_MSE_ACT(MLE_RELU); break;
+    case MLE_GELU: MLE_MSE_ACT(MLE_GELU); break;
+    case MLE_SILU: MLE_MSE_ACT(MLE_SILU); break;
+    case MLE_TANH: MLE_MSE_ACT(MLE_TANH); break;
+    case MLE_SIGMOID: MLE_MSE_ACT(MLE_SIGMOID); break;
+    default: MLE_MSE_ACT(MLE_LEAKY_RELU); break;
+  }
+#undef MLE_MSE_ACT
+  finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, np, (double)n, loss, r.slot, r.seq);
+  rc = check_launch(who);
+  if (rc) return rc;
+  return mle::scalar_read_finish(s, r, loss_host, who);
 }
 
 int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,

@@ -575,9 +575,29 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
   const size_t n = prediction->total;
   const size_t ws_bytes = mle_loss_ws_bytes(n);
   void* ws = mle::alloc_scratch(ws_bytes);
+  // The activation input whose gradient the last forward also formed early,
+  // when the prediction is an activation's output read by nothing else.
+  auto act_in = std::make_shared<NodeBackProp*>(nullptr);
   node->forward = [=]() {
+    *act_in = nullptr;
     if (calculate_loss || !last) {
-      if (last && mle::fusion_enabled() && pr->grad_pending_zero && !pr->grad_src) {
+      NodeBackProp* ai = nullptr;
+      if (last && mle::fusion_enabled() && pr->act_bwd_kind >= 0 && pr->fwd_consumers == 1 &&
+          pr->inputs.size() == 1 && pr->grad_pending_zero && !pr->grad_src) {
+        NodeBackProp* c = pr->inputs[0].get();
+        if (c && c->fwd_consumers == 1 && c->total == pr->total && c->grad_pending_zero && !c->grad_src) ai = c;
+      }
+      if (ai) {
+        // The loss, its read-back, the prediction's gradient and the
+        // activation input's (the activation's backward) from one pass over
+        // that input and t, both held early and committed by our backward.
+        check(mle_mse_act_fwd_bwd_read(S(), ai->output, tg->output, n, pr->act_bwd_kind, nd->output, pr->grad,
+                                       ai->grad, ws, ws_bytes, &GraphOperations::loss),
+              "Scalar MSE (with its gradient and the activation's) in MSE forward");
+        pr->grad_early = true;
+        ai->grad_early = true;
+        *act_in = ai;
+      } else if (last && mle::fusion_enabled() && pr->grad_pending_zero && !pr->grad_src) {
         // The loss, its read-back and the prediction's gradient from one pass
         // over x and t: the gradient is held early (NodeBackProp::grad_early)
         // and committed by our backward.
@@ -595,9 +615,16 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
     }
   };
   node->backward = [=]() {
+    NodeBackProp* ai = *act_in;
+    *act_in = nullptr;
     if (last && pr->grad_early && pr->grad_pending_zero) {  // written by our forward: commit it
       pr->grad_early = false;
       pr->grad_pending_zero = false;
+      if (ai && ai->grad_early && ai->grad_pending_zero) {  // and the activation's input gradient
+        ai->grad_early = false;
+        ai->grad_pending_zero = false;
+        pr->act_bwd_done = true;  // the activation's backward has nothing left to form
+      }
       return;
     }
     check(mle_mse_bwd(S(), pr->output, tg->output, last ? nullptr : nd->grad, pr->grad, n, mle::accumulate_flag(pr)),

@@ -1721,6 +1721,45 @@ def test_softmax_xent_keys_small(hip, orc, batch, clen, cols, hidden):
     assert_close(gloss.numpy(), np.array([lref], np.float32), what="small-logits loss", **EW)
 
 
+@pytest.mark.parametrize("kind", ["silu", "gelu", "relu", "tanh"])
+@pytest.mark.parametrize("n", [7, 123456, 123457, 8 << 20])
+def test_mse_act_fwd_bwd_read(hip, orc, kind, n):
+    """The last MSE node's forward on an activation's output, reading the
+    activation's input z: the loss (device and host), the prediction's
+    gradient and z's gradient are the bits of mle_act_fwd, then
+    mle_mse_fwd_bwd_read on its output, then an assigning mle_act_bwd; both
+    partial paths (n % 4); and against the oracle's MSE and derivative."""
+    r = rng(n % 1000 + 11 + hip.ACT[kind])
+    k = hip.ACT[kind]
+    z = (r.standard_normal(n, dtype=np.float32) * 2).astype(np.float32)
+    t = r.standard_normal(n, dtype=np.float32)
+    gz, gt = B(hip, z), B(hip, t)
+    ws = hip.Buffer(hip.lib().mle_loss_ws_bytes(n))
+    gx, gl, gdx, gdz = hip.Buffer.zeros(n), hip.Buffer.zeros(1), hip.Buffer.zeros(n), hip.Buffer.zeros(n)
+    host = C.c_float(float("nan"))
+    hip.call("mle_act_fwd", None, k, gz.ptr, gx.ptr, n)
+    hip.call("mle_mse_fwd_bwd_read", None, gx.ptr, gt.ptr, n, gl.ptr, gdx.ptr, ws.ptr, ws.nbytes, C.byref(host))
+    hip.call("mle_act_bwd", None, k, gz.ptr, gdx.ptr, gdz.ptr, n, 0)
+    for rep in range(2):
+        gl2 = hip.Buffer.zeros(1)
+        gdx2, gdz2 = B(hip, np.full(n, np.nan, np.float32)), B(hip, np.full(n, np.nan, np.float32))
+        host2 = C.c_float(float("nan"))
+        hip.call("mle_mse_act_fwd_bwd_read", None, gz.ptr, gt.ptr, n, k, gl2.ptr, gdx2.ptr, gdz2.ptr, ws.ptr, ws.nbytes,
+                 C.byref(host2))
+        for got, want, what in ((gl2, gl, "loss"), (gdx2, gdx, "dx"), (gdz2, gdz, "dz")):
+            np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32), err_msg=what)
+        assert np.float32(host2.value).view(np.uint32) == np.float32(host.value).view(np.uint32), rep
+    if n <= 123457:
+        x = np.zeros_like(z)
+        orc.call("orc_act_fwd", k, orc.ptr(z), orc.ptr(x), n)
+        dz_ref = np.zeros_like(z)
+        dx_ref = (2.0 * (x.astype(np.float64) - t) / n).astype(np.float32)
+        orc.call("orc_act_bwd", k, orc.ptr(z), orc.ptr(dx_ref), orc.ptr(dz_ref), n)
+        assert_close(gdz.numpy(), dz_ref, what=f"mse + {kind} dz", **EW)
+        lref = np.mean((x.astype(np.float64) - t) ** 2)
+        assert_close(gl.numpy(), np.array([lref], np.float32), what="mse loss", **EW)
+
+
 @pytest.mark.parametrize("n", [5, 1000, 123457, 123456, 8 << 20])
 def test_mse_fwd_read(hip, n):
     """mle_mse_fwd_read: the loss of mle_mse_fwd bit for bit, on the device and
