@@ -178,10 +178,14 @@ def extras_gemm(cpu: bool) -> dict:
     gX, gW, gdY = hip.Buffer.from_array(X), hip.Buffer.from_array(W), hip.Buffer.from_array(dY)
     gdX, gdW, gdb = hip.Buffer.zeros(X.shape), hip.Buffer.zeros(W.shape), hip.Buffer.zeros(cfg.n)
     M, K, N = cfg.m, cfg.k, cfg.n
+    # The engine's Linear backward entry point, with its workspace: rows M,
+    # in K, out N; dX, dW and db accumulated (beta 1), as Linear's backward.
+    need = hip.lib().mle_linear_bwd_ws_bytes(M, K, N, 1)
+    gws = hip.Buffer(max(need, 256))
 
     def run():
-        hip.call("mle_gemm", None, 0, 1, M, K, N, 1.0, gdY.ptr, N, 0, gW.ptr, N, 0, 1.0, gdX.ptr, K, 0, 1, None)
-        hip.call("mle_gemm", None, 1, 0, K, N, M, 1.0, gX.ptr, K, 0, gdY.ptr, N, 0, 1.0, gdW.ptr, N, 0, 1, gdb.ptr)
+        hip.call("mle_linear_bwd", None, M, K, N, 1, gX.ptr, gdY.ptr, 0, gW.ptr, 0, gdX.ptr, 1, gdW.ptr, gdb.ptr, 0,
+                 gws.ptr, need)
 
     def reps(k):
         def w():
@@ -213,7 +217,7 @@ def extras_gemm(cpu: bool) -> dict:
 
         med, times = cpu_timed(c3)
         out["cpu_baseline"] = cpu_result(flop / med / 1e12, "TFLOP/s", "the full C3 dX + dW + db", times)
-    for b in (gX, gW, gdY, gdX, gdW, gdb):
+    for b in (gX, gW, gdY, gdX, gdW, gdb, gws):
         b.free()
     return out
 

@@ -1724,9 +1724,29 @@ int mle_gemm_act_bwd(mle_stream stream, int trans_a, int trans_b, int M, int N, 
   return mle_act_bwd(stream, kind, X, C, dX, (size_t)M * N, accumulate_dx);
 }
 
+}  // extern "C"
+
+// A Linear whose weight gradient is one round of unsplit register-direct
+// tiles (192 to 256 tiles of 128 x 128: one workgroup, so one wave, per CU
+// and SIMD) and whose input gradient has too many tiles to share a launch
+// with it: the weight gradient then runs as two K splits (two workgroups per
+// CU, as the input gradient runs) and a reduce.  A function of the shape
+// only, as the workspace size must be (C3: 8192 x 1024 x 4096).
+static bool dw_two_splits(int rows, int in, int out, int layers) {
+  if (layers != 1 || rows < 4096 || rows % 32 != 0) return false;
+  const Tile tw = choose_tile(in, out, rows, 1), tx = choose_tile(rows, in, out, 1);
+  const long long nw = (long long)((in + 127) / 128) * ((out + 127) / 128);
+  const long long nx = (long long)((rows + 127) / 128) * ((in + 127) / 128);
+  return tw.direct && tx.direct && nw >= 192 && nw <= 256 && nx > 256;
+}
+
+extern "C" {
+
 size_t mle_linear_bwd_ws_bytes(int rows, int in, int out, int layers) {
   const size_t dx = layers > 1 ? mle_gemm_sum_ws_bytes(rows, in, layers) : mle_gemm_ws_bytes(rows, in, out, 1);
-  const size_t dw = mle_gemm_ws_bytes(in, out, rows, layers);
+  size_t dw = mle_gemm_ws_bytes(in, out, rows, layers);
+  if (dw_two_splits(rows, in, out, layers))
+    dw = std::max(dw, (2 * (size_t)in * out + 2 * (size_t)out) * sizeof(float));
   return std::max(dx, dw);
 }
 
@@ -1776,8 +1796,16 @@ static int linear_bwd_impl(mle_stream stream, int rows, int in, int out, int lay
     if (code != MLE_OK || act_done) return code;
     return mle_act_bwd(stream, act_kind, act_x, dX, act_dx, (size_t)rows * in, act_acc);
   };
-  const long long n0 = direct_items(P0), n1 = direct_items(P1);
   const int ncu = cu_count();
+  if (dw_two_splits(rows, in, out, layers) && P1.g.splits == 1 && direct_items(P1) > 0 && direct_items(P1) <= ncu &&
+      direct_items(P0) > ncu && P1.g.K % 32 == 0) {
+    P1.g.splits = 2;
+    P1.g.kchunk = P1.g.K / 2;
+    P1.g.part = static_cast<float*>(ws);
+    P1.g.part_cs = P1.g.part + 2 * (size_t)P1.g.M * P1.g.N;
+    P1.grid.z = 2;
+  }
+  const long long n0 = direct_items(P0), n1 = direct_items(P1);
   // Both small (gemm_simple_kernel, one batch item): one launch.
   if (!P0.empty && !P1.empty && P0.simple && P1.simple && P0.grid.z == 1 && P1.grid.z == 1) {
     const unsigned nb0 = (unsigned)(((int64_t)P0.g.M * P0.g.N + 63) / 64);

@@ -104,7 +104,9 @@ def test_c5_full_size_vs_oracle(hip, orc, batch):
 
 def test_c3_exact_shape_vs_oracle(hip, orc):
     """dX = dY W^T and dW = X^T dY with db fused, accumulating (beta 1) into
-    nonzero destinations, through the same two calls as bench.py's C3 leg."""
+    nonzero destinations, through the same call as bench.py's C3 leg (the
+    Linear backward entry point, whose weight gradient here runs as two K
+    splits and a reduce), and through two plain GEMM calls."""
     cfg = GemmConfig()
     M, K, N = cfg.m, cfg.k, cfg.n
     print(f"[fullsize] C3 {M}x{K}x{N}", flush=True)
@@ -115,9 +117,21 @@ def test_c3_exact_shape_vs_oracle(hip, orc):
     db0 = r.standard_normal(N, dtype=np.float32)
     gX, gW, gdY = H.Buffer.from_array(X), H.Buffer.from_array(W), H.Buffer.from_array(dY)
     gdX, gdW, gdb = H.Buffer.from_array(dX0), H.Buffer.from_array(dW0), H.Buffer.from_array(db0)
-    H.call("mle_gemm", None, 0, 1, M, K, N, 1.0, gdY.ptr, N, 0, gW.ptr, N, 0, 1.0, gdX.ptr, K, 0, 1, None)
-    H.call("mle_gemm", None, 1, 0, K, N, M, 1.0, gX.ptr, K, 0, gdY.ptr, N, 0, 1.0, gdW.ptr, N, 0, 1, gdb.ptr)
+    need = H.lib().mle_linear_bwd_ws_bytes(M, K, N, 1)
+    gws = H.Buffer(max(need, 256))
+    H.call("mle_linear_bwd", None, M, K, N, 1, gX.ptr, gdY.ptr, 0, gW.ptr, 0, gdX.ptr, 1, gdW.ptr, gdb.ptr, 0, gws.ptr,
+           need)
     dX, dW, db = gdX.numpy(), gdW.numpy(), gdb.numpy()
+    # the two plain GEMM calls: the same dX bits (the same kernel), dW and db
+    # from one unsplit pass
+    gdX2, gdW2, gdb2 = H.Buffer.from_array(dX0), H.Buffer.from_array(dW0), H.Buffer.from_array(db0)
+    H.call("mle_gemm", None, 0, 1, M, K, N, 1.0, gdY.ptr, N, 0, gW.ptr, N, 0, 1.0, gdX2.ptr, K, 0, 1, None)
+    H.call("mle_gemm", None, 1, 0, K, N, M, 1.0, gX.ptr, K, 0, gdY.ptr, N, 0, 1.0, gdW2.ptr, N, 0, 1, gdb2.ptr)
+    np.testing.assert_array_equal(gdX2.numpy(), dX)
+    assert_close(gdW2.numpy(), dW, what="C3 dW, one pass against two splits", **GRAD)
+    assert_close(gdb2.numpy(), db, what="C3 db, one pass against two splits", **GRAD)
+    for b in (gdX2, gdW2, gdb2, gws):
+        b.free()
 
     rows = np.sort(r.choice(M, 256, replace=False))
     cols = np.sort(r.choice(N, 256, replace=False))
