@@ -692,28 +692,24 @@ __global__ __launch_bounds__(NT) void xent_keys_bwd_kernel(const float* __restri
 constexpr unsigned kMsePartCap = 2048;
 
 // Cross-entropy against key targets for small logits (rows <= FIN_NT,
-// cols <= 64) in one workgroup, one row per thread: the row's max and sum of
-// exp as the GEMM-side rowstats_kernel forms them over one 64-column block
-// (a 64-lane butterfly, which the thread replays on 64 registers: at each
-// level lane j adds lane j ^ off, so the bits are the same), the loss term
+// cols <= 64) in one workgroup: the row's max and sum of exp as the GEMM-side
+// rowstats_kernel forms them over one 64-column block, the loss term
 // -log(p_key + 1e-27) of xent_keys_partials_kernel, and the loss as the
 // workgroup's sum of the row terms over rows * cols in finish_scalar_kernel's
 // order, published for the host when a slot is given.  With dl set, the
-// gradient (p - t) / batch of xent_keys_bwd_kernel too.
-// The body of xent_keys_small_kernel over logits x (global memory, or the
-// LDS copy the Linear + cross-entropy kernel keeps).  Each row is taken by 16
-// lanes holding columns 4 l + v: the maximum by shuffles (its value does not
-// depend on the order), then the 64-lane butterfly of rowstats_kernel over
-// the exponentials (level `off` pairs columns j and j ^ off: lanes l ^ 8, 4,
-// 2, 1 for off = 32 .. 4, then registers v ^ 2, v ^ 1), so each pair is added
-// as there and the bits are the same.
+// gradient (p - t) / batch of xent_keys_bwd_kernel too, from the row's own
+// exponentials.  Each row is taken by 16 lanes holding columns 4 l + v: the
+// maximum by shuffles (its value does not depend on the order), then the
+// 64-lane butterfly of rowstats_kernel over the exponentials (level `off`
+// pairs columns j and j ^ off: lanes l ^ 8, 4, 2, 1 for off = 32 .. 4, then
+// registers v ^ 2, v ^ 1), so each pair is added as there and the bits are
+// the same.  x is global memory, or the LDS copy the Linear + cross-entropy
+// kernel keeps.
 __device__ __forceinline__ void xent_small_body(const float* x, KeyTargets kt, int rows, int cols, float batch,
                                                 float* __restrict__ loss, float* __restrict__ dl,
                                                 mle::ScalarSlot* slot, unsigned seq) {
   __shared__ double red[FIN_NT / 64];
-  __shared__ float srow[2 * FIN_NT];  // (max, sum) per row for the gradient phase
-  __shared__ int skey[FIN_NT];
-  __shared__ double slp[FIN_NT];      // each row's loss term, summed in row order below
+  __shared__ double slp[FIN_NT];  // each row's loss term, summed in row order below
   const int grp = threadIdx.x >> 4, gl = threadIdx.x & 15;
   for (int rb = 0; rb < rows; rb += FIN_NT / 16) {
     const int row = rb + grp;
@@ -734,6 +730,7 @@ __device__ __forceinline__ void xent_small_body(const float* x, KeyTargets kt, i
     for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
 #pragma unroll
     for (int v = 0; v < 4; ++v) e[v] = (live && 4 * gl + v < cols) ? expf(e[v] - m) : 0.f;
+    const float p[4] = {e[0], e[1], e[2], e[3]};  // exp(x - m) of this lane's columns
 #pragma unroll
     for (int o = 8; o >= 1; o >>= 1)
 #pragma unroll
@@ -741,32 +738,27 @@ __device__ __forceinline__ void xent_small_body(const float* x, KeyTargets kt, i
     e[0] = e[0] + e[2];
     e[1] = e[1] + e[3];
     e[0] = e[0] + e[1];
+    const float sum = e[0] < 1e-45f ? 1.0f : e[0];
     if (live && gl == 0) {
-      const float sum = e[0] < 1e-45f ? 1.0f : e[0];
       slp[row] = key >= 0 ? -log((double)(expf(xk - m) / sum) + 1e-27) : 0.0;
       kt.stats[2 * row] = m;
       kt.stats[2 * row + 1] = sum;
-      srow[2 * row] = m;
-      srow[2 * row + 1] = sum;
-      skey[row] = key;
     }
+    if (dl && live)  // the gradient (p - t) / batch from the same exponentials
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int c = 4 * gl + v;
+        if (c < cols) dl[(size_t)row * cols + c] = (p[v] / sum + (-1.0f) * (c == key ? 1.0f : 0.0f)) / batch;
+      }
   }
   __syncthreads();
   const double lp = (int)threadIdx.x < rows ? slp[threadIdx.x] : 0.0;
   double acc = (lp + 0.0) + (0.0 + 0.0);  // finish_scalar_kernel's four accumulators, three of them empty
-  acc = block_sum<FIN_NT>(acc, red);  // its barriers also order the row statistics in LDS
-  if (threadIdx.x == 0) {  // published first: the host waiting for the loss resumes sooner
+  acc = block_sum<FIN_NT>(acc, red);
+  if (threadIdx.x == 0) {
     const float vv = (float)(acc / ((double)rows * (double)cols));
     loss[0] = vv;
     if (slot) mle::publish_scalar(slot, __builtin_bit_cast(unsigned, vv), seq);
-  }
-  if (dl) {  // one element per thread: coalesced loads and stores
-    const int n = rows * cols;
-    for (int i = threadIdx.x; i < n; i += FIN_NT) {
-      const int r = i / cols, c = i - r * cols;
-      const float p = expf(x[i] - srow[2 * r]) / srow[2 * r + 1];
-      dl[i] = (p + (-1.0f) * (c == skey[r] ? 1.0f : 0.0f)) / batch;
-    }
   }
 }
 
