@@ -1424,7 +1424,7 @@ int resident_wgs(K kernel, int (&cache)[64]) {
 int wgrad_slots(int taps, int wm, int wn) {
   static int c3[2][64], c1[5][64];
   if (taps == 9)
-    return wm == 1 ? resident_wgs(conv3_wgrad_kernel<1, 4>, c3[0]) : resident_wgs(conv3_wgrad_kernel<2, 4>, c3[1]);
+    return wm == 1 ? resident_wgs(conv3_wgrad_kernel<1, 3>, c3[0]) : resident_wgs(conv3_wgrad_kernel<2, 3>, c3[1]);
   if (wm == 1)
     return wn == 4 ? resident_wgs(conv1_wgrad_kernel<1, 4, 4>, c1[0])
                    : (wn == 2 ? resident_wgs(conv1_wgrad_kernel<1, 2, 4>, c1[1])
@@ -1590,8 +1590,8 @@ int mle_conv2d_wgrad_bias(mle_stream stream, const float* x, const float* dy, fl
     {
       ProbeScope probe("conv_wgrad", s, flop, 0.0);
       if (taps == 9) {
-        if (wm == 1) mle::launch(conv3_wgrad_kernel<1, 4>, c3.items, 256, 0, s, c3);
-        else mle::launch(conv3_wgrad_kernel<2, 4>, c3.items, 256, 0, s, c3);
+        if (wm == 1) mle::launch(conv3_wgrad_kernel<1, 3>, c3.items, 256, 0, s, c3);
+        else mle::launch(conv3_wgrad_kernel<2, 3>, c3.items, 256, 0, s, c3);
       } else if (wm == 1) {
         if (wn == 4) mle::launch(conv1_wgrad_kernel<1, 4, 4>, c3.items, 256, 0, s, c3);
         else if (wn == 2) mle::launch(conv1_wgrad_kernel<1, 2, 4>, c3.items, 256, 0, s, c3);
