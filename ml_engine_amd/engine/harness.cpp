@@ -121,7 +121,8 @@ void build_c5(Model* m, const long long* d) {
                &r.skipconv->W1, &r.skipconv->B1, &r.time_mlp->W1, &r.time_mlp->B1};
 }
 
-// U-Net decoder step (the ops of SURVEY's "remaining backward ops"): a
+// U-Net decoder step (Convolute2DT, CopyCrop and the remaining normalisations,
+// Engine/engine.cu:2613-3347): a
 // transposed convolution upsamples x, CopyCrop concatenates the centred crop
 // of a skip tensor in front of it, then BatchNorm, row RMSNorm, InstanceNorm
 // and column RMSNorm, with an MSE loss against a target.
