@@ -1035,9 +1035,9 @@ __global__ __launch_bounds__(256) void gemm_simple_pair_kernel(GemmArgs g0, Gemm
 }
 
 // Small products with a long K (an MLP's 784-wide input layer: 64 x 256 x
-// 784 and its gradients): one C tile of TT x TT per workgroup of 16 waves.
+// 784 and its gradients): one C tile of TT x TT per workgroup of NW waves.
 // Wave w multiplies the tile's operands over its K range [w kc, (w + 1) kc)
-// (whole 16-deep slabs) on MFMA, the workgroup adds the 16 partial tiles in
+// (whole 16-deep slabs) on MFMA, the workgroup adds the NW partial tiles in
 // wave order through LDS and applies the epilogue: one launch where split K
 // needs two (partials, then the reduce), and more workgroups than the
 // 64-wide tiles give the same shape.  Within a 16-deep slab lane group q =
@@ -1047,11 +1047,9 @@ __global__ __launch_bounds__(256) void gemm_simple_pair_kernel(GemmArgs g0, Gemm
 // time), and one stored m- or n-contiguous with four 4-byte loads, 64
 // contiguous bytes per k row.  Column sums of B (the bias gradient) come
 // from the workgroups of the first tile row, in (wave, lane group) order.
-constexpr int KS_NW = 16, KS_NT = 64 * KS_NW;
-
-template <int TT>
+template <int TT, int NW>
 constexpr int ks_lds_floats() {
-  return KS_NW * TT * TT + KS_NW * 4 * TT;
+  return NW * TT * TT + NW * 4 * TT;
 }
 
 // Four k-consecutive elements p[0..3] of a k-contiguous operand row, zero at
@@ -1068,7 +1066,7 @@ __device__ __forceinline__ f32x4 ks_row4(const float* p, int kq, int k1, bool ve
   return v;
 }
 
-template <int TA, int TB, int TT>
+template <int TA, int TB, int TT, int NW>
 __device__ __forceinline__ void ksplit_body(const GemmArgs& g, int tx, int ty, int64_t z, int kc, float* lds) {
   constexpr int S = TT / 16;
   const int lane = threadIdx.x & 63, li = lane & 15, lq = lane >> 4;
@@ -1161,18 +1159,18 @@ __device__ __forceinline__ void ksplit_body(const GemmArgs& g, int tx, int ty, i
     for (int j = 0; j < S; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) part[(16 * i + 4 * lq + r) * TT + 16 * j + li] = acc[i][j][r];
-  float* cpart = lds + KS_NW * TT * TT;  // [wave][lane group][column]
+  float* cpart = lds + NW * TT * TT;  // [wave][lane group][column]
   if (cs_on)
 #pragma unroll
     for (int j = 0; j < S; ++j) cpart[(w * 4 + lq) * TT + 16 * j + li] = cs[j];
   __syncthreads();
   const int64_t cz = batch_off(z, g, g.sc, g.sc2);
-  for (int o = threadIdx.x; o < TT * TT; o += KS_NT) {
+  for (int o = threadIdx.x; o < TT * TT; o += 64 * NW) {
     const int m = m0 + o / TT, n = n0 + o % TT;
     if (m >= g.M || n >= g.N) continue;
     float v = lds[o];
 #pragma unroll
-    for (int q = 1; q < KS_NW; ++q) v += lds[q * (TT * TT) + o];
+    for (int q = 1; q < NW; ++q) v += lds[q * (TT * TT) + o];
     const int64_t co = cz + (int64_t)m * g.ldc + n;
     float y = g.alpha * v;
     if (g.beta != 0.f) y += g.beta * g.C[co];
@@ -1185,31 +1183,31 @@ __device__ __forceinline__ void ksplit_body(const GemmArgs& g, int tx, int ty, i
   if (cs_on && (int)threadIdx.x < TT && n0 + (int)threadIdx.x < g.N) {
     const int c = threadIdx.x;
     float t = 0.f;
-    for (int q = 0; q < 4 * KS_NW; ++q) t += cpart[q * TT + c];
+    for (int q = 0; q < 4 * NW; ++q) t += cpart[q * TT + c];
     put_colsum(g, z * g.scs + n0 + c, t);
   }
 }
 
-template <int TA, int TB, int TT>
-__global__ __launch_bounds__(KS_NT) void gemm_ksplit_kernel(GemmArgs g, int kc) {
-  __shared__ __attribute__((aligned(16))) float lds[ks_lds_floats<TT>()];
-  ksplit_body<TA, TB, TT>(g, blockIdx.x, blockIdx.y, blockIdx.z, kc, lds);
+template <int TA, int TB, int TT, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_ksplit_kernel(GemmArgs g, int kc) {
+  __shared__ __attribute__((aligned(16))) float lds[ks_lds_floats<TT, NW>()];
+  ksplit_body<TA, TB, TT, NW>(g, blockIdx.x, blockIdx.y, blockIdx.z, kc, lds);
 }
 
 // A Linear's two backward products on the K-split kernel in one launch:
 // workgroups [0, nb0) take dX = dY W^T (NT, tiles of T0, gx0 per tile row),
 // the rest dW = X^T dY with db (TN, tiles of T1).
-template <int T0, int T1>
-__global__ __launch_bounds__(KS_NT) void gemm_ksplit_pair_kernel(GemmArgs g0, GemmArgs g1, int nb0, int gx0, int gx1,
-                                                                 int kc0, int kc1) {
-  constexpr int F0 = ks_lds_floats<T0>(), F1 = ks_lds_floats<T1>();
+template <int T0, int T1, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_ksplit_pair_kernel(GemmArgs g0, GemmArgs g1, int nb0, int gx0,
+                                                                   int gx1, int kc0, int kc1) {
+  constexpr int F0 = ks_lds_floats<T0, NW>(), F1 = ks_lds_floats<T1, NW>();
   __shared__ __attribute__((aligned(16))) float lds[F0 > F1 ? F0 : F1];
   const int b = blockIdx.x;
   if (b < nb0) {
-    ksplit_body<0, 1, T0>(g0, b % gx0, b / gx0, 0, kc0, lds);
+    ksplit_body<0, 1, T0, NW>(g0, b % gx0, b / gx0, 0, kc0, lds);
   } else {
     const int c = b - nb0;
-    ksplit_body<1, 0, T1>(g1, c % gx1, c / gx1, 0, kc1, lds);
+    ksplit_body<1, 0, T1, NW>(g1, c % gx1, c / gx1, 0, kc1, lds);
   }
 }
 
@@ -1355,7 +1353,8 @@ struct GemmPlan {
   bool cs = false, direct_ok = false, empty = false;
   bool simple = false;  // gemm_simple_kernel: one thread per C element, no split
   bool ksplit = false;  // gemm_ksplit_kernel: K split over a workgroup's waves
-  int ks_kc = 0;        // its K range per wave
+  int ks_nw = 16;       // its waves per workgroup
+  int ks_kc = 0;        // and K range per wave
   double flop = 0, bytes = 0;
 };
 
@@ -1386,8 +1385,12 @@ static bool ksplit_shape(int M, int N, int K, int batch, int terms) {
   const int tt = ksplit_tile(M, N, batch);
   return K <= (tt == 16 ? 4096 : 1024) && (M + tt - 1) / tt <= 65535 && batch <= 65535;
 }
+// Waves per workgroup: 16 for a long K (one memory latency per 64-deep chunk
+// of each wave), 4 when K <= 256 (each wave's share still fits one chunk, and
+// the partial tiles to add are fewer).
+static int ksplit_nw(int K) { return K <= 256 ? 4 : 16; }
 // K range of one wave: whole 16-deep slabs.
-static int ksplit_kc(int K) { return ((K + KS_NW - 1) / KS_NW + 15) / 16 * 16; }
+static int ksplit_kc(int K, int nw) { return ((K + nw - 1) / nw + 15) / 16 * 16; }
 
 const char* const kFamily[4] = {"gemm_nn", "gemm_nt", "gemm_tn", "gemm_tt"};
 
@@ -1465,7 +1468,8 @@ static int gemm_plan(GemmPlan& P, int trans_a, int trans_b, int M, int N, int K,
     g.kchunk = K;
     g.part = g.part_cs = nullptr;
     P.ksplit = true;
-    P.ks_kc = ksplit_kc(K);
+    P.ks_nw = ksplit_nw(K);
+    P.ks_kc = ksplit_kc(K, P.ks_nw);
   }
   P.g = g;
   P.tile = tile;
@@ -1497,15 +1501,28 @@ static void gemm_launch_main(hipStream_t s, const GemmPlan& P) {
   if (P.ksplit) {
     const bool t32 = ksplit_tile(P.g.M, P.g.N, (int)P.grid.z) == 32;
     const int kc = P.ks_kc;
-    switch (P.which * 2 + (t32 ? 1 : 0)) {
-      case 0: mle::launch(gemm_ksplit_kernel<0, 0, 16>, P.grid, KS_NT, 0, s, P.g, kc); break;
-      case 1: mle::launch(gemm_ksplit_kernel<0, 0, 32>, P.grid, KS_NT, 0, s, P.g, kc); break;
-      case 2: mle::launch(gemm_ksplit_kernel<0, 1, 16>, P.grid, KS_NT, 0, s, P.g, kc); break;
-      case 3: mle::launch(gemm_ksplit_kernel<0, 1, 32>, P.grid, KS_NT, 0, s, P.g, kc); break;
-      case 4: mle::launch(gemm_ksplit_kernel<1, 0, 16>, P.grid, KS_NT, 0, s, P.g, kc); break;
-      case 5: mle::launch(gemm_ksplit_kernel<1, 0, 32>, P.grid, KS_NT, 0, s, P.g, kc); break;
-      case 6: mle::launch(gemm_ksplit_kernel<1, 1, 16>, P.grid, KS_NT, 0, s, P.g, kc); break;
-      default: mle::launch(gemm_ksplit_kernel<1, 1, 32>, P.grid, KS_NT, 0, s, P.g, kc); break;
+    if (P.ks_nw == 4) {
+      switch (P.which * 2 + (t32 ? 1 : 0)) {
+        case 0: mle::launch(gemm_ksplit_kernel<0, 0, 16, 4>, P.grid, 256, 0, s, P.g, kc); break;
+        case 1: mle::launch(gemm_ksplit_kernel<0, 0, 32, 4>, P.grid, 256, 0, s, P.g, kc); break;
+        case 2: mle::launch(gemm_ksplit_kernel<0, 1, 16, 4>, P.grid, 256, 0, s, P.g, kc); break;
+        case 3: mle::launch(gemm_ksplit_kernel<0, 1, 32, 4>, P.grid, 256, 0, s, P.g, kc); break;
+        case 4: mle::launch(gemm_ksplit_kernel<1, 0, 16, 4>, P.grid, 256, 0, s, P.g, kc); break;
+        case 5: mle::launch(gemm_ksplit_kernel<1, 0, 32, 4>, P.grid, 256, 0, s, P.g, kc); break;
+        case 6: mle::launch(gemm_ksplit_kernel<1, 1, 16, 4>, P.grid, 256, 0, s, P.g, kc); break;
+        default: mle::launch(gemm_ksplit_kernel<1, 1, 32, 4>, P.grid, 256, 0, s, P.g, kc); break;
+      }
+    } else {
+      switch (P.which * 2 + (t32 ? 1 : 0)) {
+        case 0: mle::launch(gemm_ksplit_kernel<0, 0, 16, 16>, P.grid, 1024, 0, s, P.g, kc); break;
+        case 1: mle::launch(gemm_ksplit_kernel<0, 0, 32, 16>, P.grid, 1024, 0, s, P.g, kc); break;
+        case 2: mle::launch(gemm_ksplit_kernel<0, 1, 16, 16>, P.grid, 1024, 0, s, P.g, kc); break;
+        case 3: mle::launch(gemm_ksplit_kernel<0, 1, 32, 16>, P.grid, 1024, 0, s, P.g, kc); break;
+        case 4: mle::launch(gemm_ksplit_kernel<1, 0, 16, 16>, P.grid, 1024, 0, s, P.g, kc); break;
+        case 5: mle::launch(gemm_ksplit_kernel<1, 0, 32, 16>, P.grid, 1024, 0, s, P.g, kc); break;
+        case 6: mle::launch(gemm_ksplit_kernel<1, 1, 16, 16>, P.grid, 1024, 0, s, P.g, kc); break;
+        default: mle::launch(gemm_ksplit_kernel<1, 1, 32, 16>, P.grid, 1024, 0, s, P.g, kc); break;
+      }
     }
     return;
   }
@@ -1821,11 +1838,16 @@ static int linear_bwd_impl(mle_stream stream, int rows, int in, int out, int lay
     const int gx0 = (int)P0.grid.x, gx1 = (int)P1.grid.x;
     const int nb0 = gx0 * (int)P0.grid.y, nb1 = gx1 * (int)P1.grid.y;
     const bool w0 = ksplit_tile(P0.g.M, P0.g.N, 1) == 32, w1 = ksplit_tile(P1.g.M, P1.g.N, 1) == 32;
-    auto k = w0 ? (w1 ? gemm_ksplit_pair_kernel<32, 32> : gemm_ksplit_pair_kernel<32, 16>)
-                : (w1 ? gemm_ksplit_pair_kernel<16, 32> : gemm_ksplit_pair_kernel<16, 16>);
+    // one workgroup size for both: the larger wave count, K ranges re-cut for it
+    const int nw = std::max(P0.ks_nw, P1.ks_nw);
+    const int kc0 = ksplit_kc(P0.g.K, nw), kc1 = ksplit_kc(P1.g.K, nw);
+    auto k = nw == 4 ? (w0 ? (w1 ? gemm_ksplit_pair_kernel<32, 32, 4> : gemm_ksplit_pair_kernel<32, 16, 4>)
+                           : (w1 ? gemm_ksplit_pair_kernel<16, 32, 4> : gemm_ksplit_pair_kernel<16, 16, 4>))
+                     : (w0 ? (w1 ? gemm_ksplit_pair_kernel<32, 32, 16> : gemm_ksplit_pair_kernel<32, 16, 16>)
+                           : (w1 ? gemm_ksplit_pair_kernel<16, 32, 16> : gemm_ksplit_pair_kernel<16, 16, 16>));
     {
       ProbeScope probe("gemm_pair", s, P0.flop + P1.flop, P0.bytes + P1.bytes);
-      mle::launch(k, dim3((unsigned)(nb0 + nb1)), KS_NT, 0, s, P0.g, P1.g, nb0, gx0, gx1, P0.ks_kc, P1.ks_kc);
+      mle::launch(k, dim3((unsigned)(nb0 + nb1)), 64 * nw, 0, s, P0.g, P1.g, nb0, gx0, gx1, kc0, kc1);
     }
     return finish(check_launch("gemm_pair"));
   }
