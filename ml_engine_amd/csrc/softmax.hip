@@ -195,11 +195,27 @@ __global__ __launch_bounds__(256) void xent_keys_partials_kernel(const float* __
     if (key >= 0) xk = x[(size_t)row * cols + key];
   }
   const float* pr = part + (size_t)row * ldp;
-  float mx = -FLT_MAX;
-  for (int b = lane; b < nblk; b += 64) mx = fmaxf(mx, pr[2 * b]);
-  mx = wave_max(mx);
-  float sum = 0.f;
-  for (int b = lane; b < nblk; b += 64) sum += pr[2 * b + 1] * expf(pr[2 * b] - mx);
+  float mx = -FLT_MAX, sum = 0.f;
+  if (nblk <= 4 * 64) {
+    // Up to four (max, sum) pairs per lane, each one 8-byte load, held for
+    // both passes (the pairs are 8-byte aligned: ldp is even).
+    float2 pv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int b = lane + 64 * u;
+      pv[u] = b < nblk ? *reinterpret_cast<const float2*>(pr + 2 * b) : float2{-FLT_MAX, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mx = fmaxf(mx, pv[u].x);
+    mx = wave_max(mx);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (lane + 64 * u < nblk) sum += pv[u].y * expf(pv[u].x - mx);
+  } else {
+    for (int b = lane; b < nblk; b += 64) mx = fmaxf(mx, pr[2 * b]);
+    mx = wave_max(mx);
+    for (int b = lane; b < nblk; b += 64) sum += pr[2 * b + 1] * expf(pr[2 * b] - mx);
+  }
   sum = wave_sum(sum);
   if (sum < 1e-45f) sum = 1.0f;
   if (lane == 0) {
