@@ -443,6 +443,38 @@ def test_resblock_fusion_matches_unfused(hip):
         np.testing.assert_array_equal(pf[i].view(np.uint32), pu[i].view(np.uint32), err_msg=f"param {i}")
 
 
+def test_mlp_fusion_matches_unfused(hip):
+    """C1 MLP with the graph fusions (the classifier head's Linear and
+    cross-entropy in one launch, the ReLU backward in the classifier's
+    backward launch) against one kernel per op: the first step's gradients,
+    and the losses of three steps, to rounding (the fused head adds the
+    logits' products in its own order)."""
+    cfg = MLPConfig()
+    x, labels, params = mlp_data(cfg, seed=21)
+    runs = {}
+    for fuse in (True, False):
+        m = Model("mlp", cfg.dims(), fuse=fuse)
+        for i, p in enumerate(params):
+            m.set(i, p)
+        m.input(0, x)
+        m.input(1, labels)
+        m.step(cfg.lr, STEP_ALL)
+        m.sync()
+        grads = [m.get(i, 1) for i in range(len(params))]
+        losses = [m.loss]
+        for _ in range(2):
+            m.step(cfg.lr, STEP_ALL)
+            losses.append(m.loss)
+        m.sync()
+        runs[fuse] = (losses, grads)
+        m.close()
+    (lf, gf), (lu, gu) = runs[True], runs[False]
+    for a, b in zip(lf, lu):
+        assert abs(a - b) <= 1e-6 * abs(b), (lf, lu)
+    for i in range(len(params)):
+        assert_close(gf[i], gu[i], what=f"C1 grad {i}, fused against unfused", **GRAD)
+
+
 @pytest.mark.parametrize("kind", ["mlp", "block"])
 @pytest.mark.parametrize("graphed", [False, True])
 def test_onehot_target_lazy(hip, kind, graphed):
