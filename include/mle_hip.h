@@ -307,9 +307,11 @@ int mle_gemm_act_bwd(mle_stream stream, int trans_a, int trans_b, int M, int N, 
  *   db_l     += sum_rows dY_l          (db may be NULL)
  * Layer l's dY, W (and dW), db sit at l * stride_dy, l * stride_w, l * stride_db
  * floats (strides unused when layers == 1).  When both products run on the
- * register-direct GEMM at most one workgroup per CU each, they share one
- * launch (two workgroups per CU); otherwise dX then dW.  Needs
- * mle_linear_bwd_ws_bytes(rows, in, out, layers) bytes of workspace. */
+ * register-direct GEMM at most one workgroup per CU each, or both on one of
+ * the small-product kernels, they share one launch; otherwise dX then dW (a
+ * weight gradient of one round of tiles beside a larger dX runs as two K
+ * splits).  Needs mle_linear_bwd_ws_bytes(rows, in, out, layers) bytes of
+ * workspace. */
 size_t mle_linear_bwd_ws_bytes(int rows, int in, int out, int layers);
 int mle_linear_bwd(mle_stream stream, int rows, int in, int out, int layers,
                    const float* X, const float* dY, int64_t stride_dy,
