@@ -212,7 +212,9 @@ int mle_gemm(mle_stream stream, int trans_a, int trans_b, int M, int N, int K, f
              float* C, int64_t ldc, int64_t stride_c, int batch, float* colsum);
 
 /* Workspace that lets mle_gemm_ex split K across workgroups when the tile grid
- * alone would leave most CUs idle (0 when no split is used for this shape). */
+ * alone would leave most CUs idle (0 when no split is used for this shape; a
+ * small product that runs on one of the small-product kernels, K split over
+ * a workgroup's waves, leaves it unused). */
 size_t mle_gemm_ws_bytes(int M, int N, int K, int batch);
 /* mle_gemm plus two fusions:
  *   bias (nullable): C[b][r, c] += bias[c] after alpha/beta -- the Linear
