@@ -78,6 +78,15 @@ __device__ __forceinline__ float act_drt(int kind, float x) {
   }
 }
 
+// dx (+)= f'(x) * dy as the elementwise activation backward forms it: the
+// product is rounded before the add (acc = false assigns and `old` is unused).
+template <int K>
+__device__ __forceinline__ float act_bwd_k(float x, float dy, float old, bool acc) {
+#pragma clang fp contract(off)
+  const float v = act_df<K>(x) * dy;
+  return acc ? old + v : v;
+}
+
 // dx (+)= f'(x) * dy for a run-time kind, as the elementwise activation
 // backward forms it: the product is rounded before the add (acc = false
 // assigns and `old` is unused).

@@ -786,10 +786,11 @@ __global__ __launch_bounds__(NT, 2) void gemm_stream_kernel(GemmArgs g, int gx, 
           }
           if (EPI == kEpiActBwd) {
             const f32x4 xh = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0));
-            f32x4 d;
+            f32x4 old = {0.f, 0.f, 0.f, 0.f};
+            if (g.act_acc) old = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, (int)off, 0, 0));
+            f32x4 d;  // the elementwise backward's bits: the product rounded before the add
 #pragma unroll
-            for (int n = 0; n < 4; ++n) d[n] = act_df<ACT>(xh[n]) * v[n];
-            if (g.act_acc) d += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, (int)off, 0, 0));
+            for (int n = 0; n < 4; ++n) d[n] = act_bwd_k<ACT>(xh[n], v[n], old[n], g.act_acc);
             __builtin_amdgcn_raw_buffer_store_b128(
                 __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, d), rd, (int)off, 0, 0);
           }
@@ -1870,7 +1871,9 @@ static int linear_bwd_impl(mle_stream stream, int rows, int in, int out, int lay
     }
     return finish(check_launch("gemm_pair"));
   }
-  // Otherwise one launch each, in order (they may share the workspace).
+  // Otherwise one launch each, in order (they may share the workspace).  (A
+  // dX on the persistent kernel writing the activation's gradient in its
+  // epilogue measured slower in the C4 step than the separate pass.)
   if (!P0.empty) {
     ProbeScope probe(kFamily[P0.which], s, P0.flop, P0.bytes);
     gemm_launch_main(s, P0);

@@ -1863,6 +1863,8 @@ def test_gemm_act_bwd(hip, orc, kind, M, N, K, beta, acc):
     (64, 784, 256, 1),     # both on the K-split kernel: the activation in their launch
     (300, 130, 70, 0),
     (8192, 384, 128, 1),   # register-direct pair: the activation pass after it
+    (4224, 2048, 128, 0),  # dX on the persistent kernel: the activation pass after it
+    (4224, 2048, 128, 1),
 ])
 def test_linear_bwd_act(hip, orc, kind, rows, inp, out, acc):
     """mle_linear_bwd_act: a Linear's backward with the backward of the
