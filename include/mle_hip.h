@@ -375,7 +375,9 @@ int mle_softmax_bwd(mle_stream stream, const float* y, const float* dy, float* d
  * + Scale + SOFTMASK/SOFTMAX(type 1) + BMM + DeHeadify of MultiHeadAttention
  * (Engine/transformer.cu:647-661; Engine/engine.cu:1144-1178, 2205-2314,
  * 2430-2505, 2523-2551), without storing the [seq x seq] scores.  ws
- * (mle_attention_ws_bytes) receives the column statistics the backward reads:
+ * (mle_attention_ws_bytes) receives the column statistics the backward reads
+ * and, for seq <= 256 with the causal mask, the probabilities on or below the
+ * diagonal (seq/16 (seq/16 + 1)/2 blocks of 1 KB per batch item and head):
  * keep it unchanged between the two calls. */
 size_t mle_attention_ws_bytes(int batch, int heads, int seq);
 int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const float* v, float* out, int batch,

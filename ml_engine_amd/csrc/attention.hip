@@ -57,6 +57,7 @@ struct AttnArgs {
   float* dv;
   float* stats;  // [slices][seq][2]: m_c, 1 / l_c
   float* dcol;   // [slices][seq]: D_c
+  float* kept;   // causal, seq <= 256: [slices][kept_blocks(seq)][16 keys][16 queries] of P
   int heads, seq, ld;
   uint32_t bytes;  // extent of each [batch][seq][ld] tensor
   float scale;
@@ -90,6 +91,9 @@ __device__ __forceinline__ void bst1(__amdgpu_buffer_rsrc_t r, uint32_t elem, fl
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (int)(elem * 4u), 0, 0);
 }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+// The causal slice kernels' 16x16 blocks on or below the diagonal: block
+// (query block qb, key block kb), kb <= qb, at index qb (qb + 1) / 2 + kb.
+__host__ __device__ constexpr size_t kept_blocks(int seq) { return (size_t)(seq / 16) * (seq / 16 + 1) / 2; }
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -99,6 +103,11 @@ struct Slice {
   uint32_t base;  // element offset of (batch item, head) in the [batch][seq][ld] tensors
   int pair;       // this workgroup's tile pair within the slice
 };
+// Slice z's kept probabilities, kept_blocks(seq) blocks of 256 floats.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kept_rsrc(const AttnArgs& a, const Slice& sl) {
+  const size_t n = kept_blocks(a.seq) * 256;
+  return rsrc(a.kept + (size_t)sl.z * n, (uint32_t)(n * sizeof(float)));
+}
 // The grid is one-dimensional: workgroup L runs on XCD L % 8 (workgroups are
 // dispatched round-robin over the XCDs).  XCD x takes a contiguous range of
 // the (slice, tile pair) items, slice-major, so every workgroup of a slice
@@ -818,6 +827,7 @@ __device__ __forceinline__ void stats_kept(const AttnArgs& a, const Slice& sl, i
 __device__ __forceinline__ void fwd_kept(const AttnArgs& a, const Slice& sl, int b0, int b1, const float* sst) {
   const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
+  const __amdgpu_buffer_rsrc_t PK = kept_rsrc(a, sl);
   const float* ST = a.stats + (size_t)sl.z * a.seq * 2;
   const int bk[2] = {b0, b1};
   f32x4 acc[4][2];
@@ -855,6 +865,11 @@ __device__ __forceinline__ void fwd_kept(const AttnArgs& a, const Slice& sl, int
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i][n] = mfma4(ch.va[r][i], pt[r], acc[i][n]);
+      // P^T[key 4q + r][query lr] for the backward, whose dV-pass lane reads
+      // its four queries of one key as one 16-byte load
+      const uint32_t blk = (uint32_t)(bk[n] * (bk[n] + 1) / 2 + c) * 256 + lr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bst1(PK, blk + (4 * q + r) * 16, pt[r]);
     }
   };
   chunk_loop<Chunk>(0, b1 + 1, fetch, compute);
@@ -867,29 +882,24 @@ __device__ __forceinline__ void fwd_kept(const AttnArgs& a, const Slice& sl, int
            f32x4{acc[0][n][r], acc[1][n][r], acc[2][n][r], acc[3][n][r]});
 }
 
-// bwd_kv_tile<true, DK, true> for the 16-key blocks b0 < b1 (keys 16 b + lr):
-// per query chunk c >= b (masked on the diagonal chunk c == b), P is kept in
-// sst, dV^T += dO^T P, then D, and with DK a second pass for dK^T += Q^T dS.
+// dV for the 16-key blocks b0 < b1 (keys 16 b + lr): per query chunk c >= b,
+// P from the forward's kept blocks (zero past the diagonal), copied into sst
+// with the query as the row for the dQ pass, and dV^T += dO^T P; then D, and
+// with DK a second pass for dS = P (dP - D) and dK^T += Q^T dS.
 template <bool DK>
 __device__ __forceinline__ void bwd_kv_kept(const AttnArgs& a, const Slice& sl, int b0, int b1, float* sst) {
   const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
   const __amdgpu_buffer_rsrc_t Q = rsrc(a.q, a.bytes);
-  const __amdgpu_buffer_rsrc_t K = rsrc(a.k, a.bytes);
   const __amdgpu_buffer_rsrc_t V = rsrc(a.v, a.bytes);
   const __amdgpu_buffer_rsrc_t dO = rsrc(a.dout, a.bytes);
+  const __amdgpu_buffer_rsrc_t PK = kept_rsrc(a, sl);
   const int bk[2] = {b0, b1};
-  f32x4 kB[2][4], vB[2][4];
-  float mk[2], il[2];
+  f32x4 vB[2][4];
+  if (DK) {
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      kB[n][s] = bld4(K, sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * s + 4 * q);
-      if (DK) vB[n][s] = bld4(V, sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * s + 4 * q);
-    }
-    const float* sp = a.stats + ((size_t)sl.z * a.seq + 16 * bk[n] + lr) * 2;
-    mk[n] = sp[0];
-    il[n] = sp[1];
+      for (int s = 0; s < 4; ++s) vB[n][s] = bld4(V, sl.base + (uint32_t)(16 * bk[n] + lr) * a.ld + 16 * s + 4 * q);
   }
   f32x4 acc[4][2];
 #pragma unroll
@@ -898,42 +908,40 @@ __device__ __forceinline__ void bwd_kv_kept(const AttnArgs& a, const Slice& sl, 
     for (int n = 0; n < 2; ++n) acc[i][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   float D[2] = {0.f, 0.f};
   struct Chunk {
-    f32x4 qa[4], oa[4], at[4];
+    f32x4 oa[4], at[4], pk[2];
   };
   auto run = [&](auto pass2_tag) {
     constexpr bool P2 = decltype(pass2_tag)::value;
     auto fetch = [&](int c, Chunk& ch) {
       const int qc = 16 * c;
+      if (P2) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        ch.qa[s] = bld4(Q, sl.base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
-        if (P2) ch.oa[s] = bld4(dO, sl.base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
+        for (int s = 0; s < 4; ++s) ch.oa[s] = bld4(dO, sl.base + (uint32_t)(qc + lr) * a.ld + 16 * s + 4 * q);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         ch.at[r] = bld4s(P2 ? Q : dO, sl.base + (uint32_t)(qc + 4 * q) * a.ld + 4 * lr, (uint32_t)r * a.ld);
+      // P[query 4q + r][key lr], r = 0..3: one 16-byte load per kept block
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+        if (c >= bk[n]) ch.pk[n] = bld4(PK, (uint32_t)(c * (c + 1) / 2 + bk[n]) * 256 + 16 * lr + 4 * q);
     };
     auto compute = [&](int c, const Chunk& ch) {
 #pragma unroll
       for (int n = 0; n < 2; ++n) {
         if (c < bk[n]) continue;
-        const bool diag = c == bk[n];
-        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, da = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            sa = mfma4(ch.qa[s][j], kB[n][s][j], sa);
-            if (P2) da = mfma4(ch.oa[s][j], vB[n][s][j], da);
-          }
         float bop[4];
+        if (P2) {
+          f32x4 da = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool keep = !diag || 4 * q + r >= lr;
-          const float pv = __expf(a.scale * sa[r] - mk[n]) * (keep ? il[n] : 0.f);
-          bop[r] = P2 ? pv * (da[r] - D[n]) : pv;
-        }
-        if (!P2) {
+          for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) da = mfma4(ch.oa[s][j], vB[n][s][j], da);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bop[r] = ch.pk[n][r] * (da[r] - D[n]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bop[r] = ch.pk[n][r];
           float* blk = sst + (c * (c + 1) / 2 + bk[n]) * 256 + lr;
 #pragma unroll
           for (int r = 0; r < 4; ++r) blk[(4 * q + r) * 16] = bop[r];
@@ -1114,7 +1122,8 @@ __device__ __forceinline__ Slice slice_whole(const AttnArgs& a) {
 }
 // Causal: the statistics pass keeps the slice's S^T blocks on or below the
 // diagonal in LDS (seq / 16 (seq / 16 + 1) / 2 blocks of 1 KB, 136 KB at seq
-// 256) and the output pass reads them instead of recomputing its products.
+// 256) and the output pass reads them instead of recomputing its products;
+// the output pass stores the blocks' P to a.kept for the backward.
 template <bool CAUSAL>
 __global__ __launch_bounds__(SW * 64, 1) void attn_fwd_slice_kernel(AttnArgs a) {
   constexpr int kBlocks = CAUSAL ? (SW * TW / 16) * (SW * TW / 16 + 1) / 2 : 1;
@@ -1133,10 +1142,10 @@ __global__ __launch_bounds__(SW * 64, 1) void attn_fwd_slice_kernel(AttnArgs a) 
     if (w < ntile) fwd_tile<false>(a, sl, w * TW);
   }
 }
-// Causal: the dV pass keeps the slice's P blocks on or below the diagonal in
-// LDS (136 KB at seq 256) and the dQ pass reads them instead of recomputing
-// S^T and its exponentials; without the mask the dQ pass stages its Q and dO
-// rows in LDS and recomputes.
+// Causal: the dV pass reads the forward's P blocks from a.kept and copies
+// them into LDS (136 KB at seq 256) for the dQ pass, so neither pass
+// recomputes S or its exponentials; without the mask the dQ pass stages its
+// Q and dO rows in LDS and recomputes.
 template <bool CAUSAL, bool KREF>
 __global__ __launch_bounds__(SW * 64, 1) void attn_bwd_slice_kernel(AttnArgs a) {
   constexpr int kFloats = CAUSAL ? (SW * TW / 16) * (SW * TW / 16 + 1) / 2 * 256 : SW * 2 * TW * LQ;
@@ -1172,7 +1181,10 @@ extern "C" {
 
 size_t mle_attention_ws_bytes(int batch, int heads, int seq) {
   if (batch <= 0 || heads <= 0 || seq <= 0) return 0;
-  return (size_t)batch * heads * seq * 3 * sizeof(float);
+  // statistics and D per key, then (seq <= 256, the slice kernels) the kept
+  // probability blocks of the causal forward for the backward
+  const size_t kept = seq <= SW * TW ? kept_blocks(seq) * 256 : 0;
+  return (size_t)batch * heads * (seq * 3 + kept) * sizeof(float);
 }
 
 int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const float* v, float* out, int batch,
@@ -1192,6 +1204,7 @@ int mle_attention_fwd(mle_stream stream, const float* q, const float* k, const f
   a.out = out;
   a.stats = static_cast<float*>(ws);
   a.dcol = a.stats + (size_t)batch * heads * seq * 2;
+  a.kept = a.dcol + (size_t)batch * heads * seq;
   a.heads = heads;
   a.seq = seq;
   a.ld = ld;
@@ -1236,6 +1249,7 @@ int mle_attention_bwd(mle_stream stream, const float* q, const float* k, const f
   a.dv = dv;
   a.stats = static_cast<float*>(ws);
   a.dcol = a.stats + (size_t)batch * heads * seq * 2;
+  a.kept = a.dcol + (size_t)batch * heads * seq;
   a.heads = heads;
   a.seq = seq;
   a.ld = ld;
