@@ -335,7 +335,8 @@ int mle_linear_bwd_ex(mle_stream stream, int rows, int in, int out, int layers,
  * 3560).  dX is written as mle_linear_bwd_ex writes it; act_x and act_dx are
  * [rows, in] like dX.  On the small-product kernels the activation gradient
  * is their epilogue (one launch less), otherwise a pass after the products.
- * Same workspace as mle_linear_bwd_ex. */
+ * act_dx may be act_x but none of X, dY, W, dX.  Same workspace as
+ * mle_linear_bwd_ex. */
 int mle_linear_bwd_act(mle_stream stream, int rows, int in, int out, const float* X, const float* dY,
                        const float* W, float* dX, int accumulate_dx, float* dW, float* db, int accumulate_dw,
                        int act_kind, const float* act_x, float* act_dx, int act_accumulate, void* ws,
@@ -413,7 +414,8 @@ int mle_mse_fwd_bwd_read(mle_stream stream, const float* x, const float* t, size
  * activation's function, the bits mle_act_fwd stores), its read-back,
  * x's gradient dx = 2 (x - t) / n and z's gradient dz = act'(z) * dx, both
  * assigned -- the bits of mle_mse_fwd_bwd_read on x followed by
- * mle_act_bwd(act_kind, z, dx, dz, n, 0), in one pass over z and t. */
+ * mle_act_bwd(act_kind, z, dx, dz, n, 0), in one pass over z and t.  dx,
+ * dz and t are distinct buffers; dz may be z. */
 int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, size_t n, int act_kind, float* loss,
                              float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host);
 /* dx (+)= 2 (x - t) / n * (upstream ? upstream[0] : 1).  deriv_mse_kernel (Engine/kernels.cu:1838-1848). */
@@ -444,7 +446,8 @@ int mle_softmax_xent_keys_small_read(mle_stream stream, const float* logits, con
  * logits [rows, cols] are written, then everything
  * mle_softmax_xent_keys_small_read does with them (the same bits for the
  * same logits; the logits' products are added in this kernel's own order).
- * X [rows, in], W [in, cols], bias [cols] or NULL; rows <= 1024, cols <= 64. */
+ * X [rows, in], W [in, cols], bias [cols] or NULL; rows <= 1024, cols <= 64;
+ * logits is a buffer of its own (not X, W or dlogits). */
 int mle_linear_xent_keys_small_read(mle_stream stream, int rows, int in, int cols, const float* X, const float* W,
                                     const float* bias, float* logits, const int32_t* keys, int clen, int max_clen,
                                     float* stats, int batch, float* loss, float* dlogits, float* loss_host);

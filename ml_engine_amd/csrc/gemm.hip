@@ -1905,6 +1905,8 @@ int mle_linear_bwd_act(mle_stream stream, int rows, int in, int out, const float
                        size_t ws_bytes) {
   MLE_CHECK_ARG(act_kind >= MLE_RELU && act_kind <= MLE_LEAKY_RELU && act_x != nullptr && act_dx != nullptr,
                 "mle_linear_bwd_act: bad activation argument");
+  MLE_CHECK_ARG(act_dx != dX && act_dx != dY && act_dx != X && act_dx != W,
+                "mle_linear_bwd_act: act_dx must not alias X, dY, W or dX");
   return linear_bwd_impl(stream, rows, in, out, 1, X, dY, 0, W, 0, dX, accumulate_dx, dW, db, 0, accumulate_dw,
                          act_kind, act_x, act_dx, act_accumulate, ws, ws_bytes);
 }

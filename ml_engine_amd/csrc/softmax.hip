@@ -974,6 +974,7 @@ int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, 
   MLE_CHECK_ARG(z && t && loss && dx && dz && ws && loss_host && n > 0 && act_kind >= MLE_RELU &&
                     act_kind <= MLE_LEAKY_RELU,
                 "%s: bad argument", who);
+  MLE_CHECK_ARG(dx != dz && dx != z && dx != t && dz != t, "%s: dx and dz must differ from each other and t", who);
   const unsigned g = stream_grid(n, NT, kMsePartCap);
   if (ws_bytes < g * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "%s: workspace too small", who);
   hipStream_t s = as_stream(stream);
@@ -1134,6 +1135,8 @@ int mle_linear_xent_keys_small_read(mle_stream stream, int rows, int in, int col
                 "mle_linear_xent_keys_small_read: bad argument");
   MLE_CHECK_ARG(rows <= FIN_NT && cols <= 64, "mle_linear_xent_keys_small_read: %d x %d logits exceed %d x 64", rows,
                 cols, FIN_NT);
+  MLE_CHECK_ARG(dlogits != logits && logits != X && logits != W,
+                "mle_linear_xent_keys_small_read: logits must differ from X, W and dlogits");
   const int tiles = ((rows + 15) / 16) * ((cols + 15) / 16);
   if (tiles > LXS_T || rows * cols > LXS_MAXN) {  // the two launches
     const int rc = mle_gemm_ex(stream, 0, 0, rows, cols, in, 1.0f, X, in, 0, W, cols, 0, 0.0f, logits, cols, 0, 1,

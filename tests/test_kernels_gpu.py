@@ -1908,6 +1908,11 @@ def test_linear_bwd_act(hip, orc, kind, rows, inp, out, acc):
     assert_close(fdZ.numpy(), want_dz, what=f"linear_bwd_act d{kind}", **MM)
     assert_close(fdW.numpy(), want_dw, what="linear_bwd_act dW", **MM)
     assert_close(fdb.numpy(), db0 + dY.astype(np.float64).sum(0), what="linear_bwd_act db", **EW)
+    if rows == 64 and kind == "relu" and acc == 0:  # the activation gradient may not overwrite an operand
+        for alias in (fdX, gdY, gX, gW):
+            with pytest.raises(hip.MLEError):
+                hip.call("mle_linear_bwd_act", None, rows, inp, out, gX.ptr, gdY.ptr, gW.ptr, fdX.ptr, 0, fdW.ptr,
+                         fdb.ptr, 1, k, gZ.ptr, alias.ptr, 0, ws.ptr, need)
 
 
 # ------------------------------------------------------------------ arena
