@@ -552,14 +552,18 @@ int mle_norm_bwd(mle_stream stream, const float* y, const float* dy, float* dx, 
  *     normalisation's input gradient -- the producer's output gradient --
  *     and the new dx (+)= into dxa and dxb, the producer's input gradients
  *     (each with its own accumulate flag; dxb may be null), in one pass.
+ *     With accumulate, dx = dx_in + the normalisation's gradient: dx_in is
+ *     dx itself when null, or the producer's other consumers' gradient kept
+ *     elsewhere (a pass-through's, read in place of a copy into dx).
  * The same values, bit for bit, as mle_norm_bwd (_act) followed by the
  * producer's gradient copies (mle_accumulate2 / accumulate at scale 1). */
 int mle_norm_bwd_partials(mle_stream stream, const float* y, float* dy, const float* da, int kind, int accumulate_dy,
                           int batch, int channels, size_t hw, int groups, int reference_layout, void* ws,
                           size_t ws_bytes);
-int mle_norm_bwd_apply_add(mle_stream stream, const float* y, const float* dy, float* dx, int accumulate, float* dxa,
-                           int accumulate_a, float* dxb, int accumulate_b, const float* stats, int batch, int channels,
-                           size_t hw, int groups, float eps, int reference_layout, void* ws, size_t ws_bytes);
+int mle_norm_bwd_apply_add(mle_stream stream, const float* y, const float* dy, float* dx, int accumulate,
+                           const float* dx_in, float* dxa, int accumulate_a, float* dxb, int accumulate_b,
+                           const float* stats, int batch, int channels, size_t hw, int groups, float eps,
+                           int reference_layout, void* ws, size_t ws_bytes);
 
 /* BatchNorm: per-channel statistics over (batch, H, W), gamma 1, beta 0.
  * stats[2c] = mean, stats[2c+1] = sum (x - mean)^2; y = (x - mean) * r with

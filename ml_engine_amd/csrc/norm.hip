@@ -440,12 +440,13 @@ __global__ __launch_bounds__(64) void norm_bwd_final(const double* __restrict__ 
 // LayerBackward for channels > 1: only elements e < batch*hw receive a
 // gradient, with group e / hw (the others are left alone, or set to 0 when
 // assigning, which is what adding nothing to a cleared gradient gives).
+// With acc the gradient is added to dx_in's values (dx_in may be dx).
 template <bool SEG, bool VEC, bool EXTRA = false>  // EXTRA: dx2 set (dx3 may be)
 __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y, const float* __restrict__ dy,
-                                                     float* __restrict__ dx, const float* __restrict__ stats,
+                                                     float* dx, const float* __restrict__ stats,
                                                      NormShape sh, const double* __restrict__ part,
                                                      const double* __restrict__ fin, float eps, size_t quirk_hw,
-                                                     int acc, float* __restrict__ dx2, int acc2,
+                                                     int acc, const float* dx_in, float* __restrict__ dx2, int acc2,
                                                      float* __restrict__ dx3, int acc3) {
   const int g = blockIdx.y, ck = blockIdx.x;
   const size_t c0 = (size_t)ck * CH;
@@ -488,7 +489,7 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
         if (!in[u]) continue;
         yv[u] = *reinterpret_cast<const f32x4*>(y + o[u]);
         gv[u] = *reinterpret_cast<const f32x4*>(dy + o[u]);
-        if (acc) d[u] = *reinterpret_cast<const f32x4*>(dx + o[u]);
+        if (acc) d[u] = *reinterpret_cast<const f32x4*>(dx_in + o[u]);
         if (EXTRA && acc2) d2[u] = *reinterpret_cast<const f32x4*>(dx2 + o[u]);
         if (EXTRA && dx3 && acc3) d3[u] = *reinterpret_cast<const f32x4*>(dx3 + o[u]);
       }
@@ -520,7 +521,7 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
     const size_t idx = at<SEG>(sh, g, e);
     if (!SEG && quirk_hw) {
       if (idx >= (size_t)sh.groups_tot * quirk_hw) {
-        const float nv = acc ? dx[idx] : 0.f;
+        const float nv = acc ? dx_in[idx] : 0.f;
         dx[idx] = nv;
         if (EXTRA) dx2[idx] = acc2 ? dx2[idx] + nv : nv;
         if (EXTRA && dx3) dx3[idx] = acc3 ? dx3[idx] + nv : nv;
@@ -529,7 +530,7 @@ __global__ __launch_bounds__(NT) void norm_bwd_apply(const float* __restrict__ y
       terms((int)(idx / quirk_hw), sg, sgy, r);
     }
     const float v = r * (dy[idx] - (sg / fN) - y[idx] * (sgy / fN));
-    const float nv = acc ? dx[idx] + v : v;
+    const float nv = acc ? dx_in[idx] + v : v;
     dx[idx] = nv;
     if (EXTRA) dx2[idx] = acc2 ? dx2[idx] + nv : nv;
     if (EXTRA && dx3) dx3[idx] = acc3 ? dx3[idx] + nv : nv;
@@ -615,14 +616,15 @@ void launch_bwd_partials(hipStream_t s, const NormShape& sh, const float* y, con
 // The second pass, from the first pass's sums in ws: dx (and dx2, dx3 when set).
 void launch_bwd_apply(hipStream_t s, const NormShape& sh, const float* y, const float* dy, float* dx, int accumulate,
                       const float* stats, void* ws, float eps, size_t quirk, float* dx2 = nullptr, int acc2 = 0,
-                      float* dx3 = nullptr, int acc3 = 0) {
+                      float* dx3 = nullptr, int acc3 = 0, const float* dx_in = nullptr) {
   dim3 grid(sh.nchunk, sh.groups_tot);
   double* part = static_cast<double*>(ws);
   double* fin = part + (size_t)sh.groups_tot * sh.nchunk * 2;
-  const bool v = vec_ok(sh, {y, dy, dx}) && (!dx2 || aligned16(dx2)) && (!dx3 || aligned16(dx3));
+  if (!dx_in) dx_in = dx;
+  const bool v = vec_ok(sh, {y, dy, dx, dx_in}) && (!dx2 || aligned16(dx2)) && (!dx3 || aligned16(dx3));
   auto go = [&](auto kern, size_t qk) {
-    hipLaunchKernelGGL(kern, grid, dim3(NT), 0, s, y, dy, dx, stats, sh, part, fin, eps, qk, accumulate, dx2, acc2,
-                       dx3, acc3);
+    hipLaunchKernelGGL(kern, grid, dim3(NT), 0, s, y, dy, dx, stats, sh, part, fin, eps, qk, accumulate, dx_in, dx2,
+                       acc2, dx3, acc3);
   };
   if (dx2) {
     if (sh.seg) go(v ? norm_bwd_apply<true, true, true> : norm_bwd_apply<true, false, true>, 0);
@@ -855,18 +857,20 @@ int mle_norm_bwd_partials(mle_stream stream, const float* y, float* dy, const fl
   return check_launch("mle_norm_bwd_partials");
 }
 
-int mle_norm_bwd_apply_add(mle_stream stream, const float* y, const float* dy, float* dx, int accumulate, float* dxa,
-                           int accumulate_a, float* dxb, int accumulate_b, const float* stats, int batch, int channels,
-                           size_t hw, int groups, float eps, int reference_layout, void* ws, size_t ws_bytes) {
+int mle_norm_bwd_apply_add(mle_stream stream, const float* y, const float* dy, float* dx, int accumulate,
+                           const float* dx_in, float* dxa, int accumulate_a, float* dxb, int accumulate_b,
+                           const float* stats, int batch, int channels, size_t hw, int groups, float eps,
+                           int reference_layout, void* ws, size_t ws_bytes) {
   MLE_CHECK_ARG(y && dy && dx && stats && ws && (dxa || !dxb), "mle_norm_bwd_apply_add: bad argument");
   MLE_CHECK_ARG(dxa != dx && (!dxb || (dxb != dx && dxb != dxa)), "mle_norm_bwd_apply_add: outputs must differ");
+  MLE_CHECK_ARG(!dx_in || (dx_in != dxa && dx_in != dxb), "mle_norm_bwd_apply_add: dx_in must not be an output");
   NormShape sh;
   int rc = shape_of(batch, channels, hw, groups, sh);
   if (rc) return rc;
   if (ws_bytes < ws_need(sh)) return set_error(MLE_ERR_WORKSPACE, "mle_norm_bwd_apply_add: workspace too small");
   const size_t quirk = (reference_layout && groups == 1 && channels > 1) ? hw : 0;
   launch_bwd_apply(as_stream(stream), sh, y, dy, dx, accumulate, stats, ws, eps, quirk, dxa, accumulate_a, dxb,
-                   accumulate_b);
+                   accumulate_b, dx_in);
   return check_launch("mle_norm_bwd_apply_add");
 }
 

@@ -181,7 +181,13 @@ const float* grad_of(const NodeBackProp* n) { return n->grad_src ? n->grad_src :
 
 bool can_alias_grad(const NodeBackProp* in, const NodeBackProp* from) {
   if (!g_lazy_zero || !fusion_enabled() || !in || !from || in == from || !in->reads_grad_alias) return false;
-  return in->grad_pending_zero && !in->grad_src && in->consumers == 1 && in->total == from->total;
+  if (!in->grad_pending_zero || in->grad_src || in->total != from->total) return false;
+  if (in->consumers == 1) return true;
+  // One other consumer still to come, which may be a normalisation whose
+  // second pass adds into this node's gradient at this node's place: it reads
+  // the alias where a copy would be written (norm_node); any other consumer
+  // resolves the alias before it adds (accumulate_flag).
+  return in->takes_norm_grad && in->consumers == 2 && in->consumers_done == 0;
 }
 
 bool alias_grad(NodeBackProp* in, const NodeBackProp* from) {

@@ -227,13 +227,23 @@ graph norm_node(const graph& X, int groups, const str& name) {
     // pass now, the second at the producer's place, writing its gradient and
     // its inputs'.
     if (mle::fusion_enabled() && x->takes_norm_grad && x->consumers_done + 1 == x->consumers) {
-      const int acc_x = mle::accumulate_flag(x);
+      // The producer's gradient so far may be an alias (a pass-through
+      // consumer's gradient, see can_alias_grad): the second pass adds to it
+      // there and writes the producer's own gradient whole.
+      const float* x_in = x->grad_src;
+      int acc_x = 1;
+      if (x_in) {
+        x->grad_src = nullptr;
+        x->grad_pending_zero = false;
+      } else {
+        acc_x = mle::accumulate_flag(x);
+      }
       check(mle_norm_bwd_partials(S(), nd->output, g, da, da ? nd->act_grad_kind : -1, nd->act_grad_acc, a, b, hw,
                                   groups, ref_layout, ws, ws_bytes),
             name + " backward (first pass)");
       x->grad_apply = [=](float* da, int acc_a, float* db, int acc_b) {
-        check(mle_norm_bwd_apply_add(S(), nd->output, g, x->grad, acc_x, da, acc_a, db, acc_b, stats, a, b, hw, groups,
-                                     eps, ref_layout, ws, ws_bytes),
+        check(mle_norm_bwd_apply_add(S(), nd->output, g, x->grad, acc_x, x_in, da, acc_a, db, acc_b, stats, a, b, hw,
+                                     groups, eps, ref_layout, ws, ws_bytes),
               name + " backward (second pass, into the producer's inputs)");
       };
       return;
@@ -371,6 +381,7 @@ graph GraphOperations::MatrixPositionalEncoding(const graph& X, const int start_
           "MatPE forward (with the normalisation statistics)");
   };
   node->takes_norm_grad = true;
+  node->reads_grad_alias = true;
   node->backward = [=]() {
     if (nd->grad_apply) {  // the normalisation after this node left its second pass (see norm_node)
       auto apply = std::move(nd->grad_apply);
@@ -378,7 +389,7 @@ graph GraphOperations::MatrixPositionalEncoding(const graph& X, const int start_
       apply(x->grad, mle::accumulate_flag(x), nullptr, 0);
       return;
     }
-    add_grad(x, nd->grad, 1.0, nd->total, "MatPE backward");
+    add_grad(x, mle::grad_of(nd), 1.0, nd->total, "MatPE backward");
   };
   std_hooks(node);
   return node;

@@ -112,7 +112,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_norm_bwd_act": (I, [P, P, P, I, P, I, P, P, I, I, SZ, I, F, I, P, SZ, I]),
     "mle_norm_bwd": (I, [P, P, P, P, P, I, I, SZ, I, F, I, P, SZ, I]),
     "mle_norm_bwd_partials": (I, [P, P, P, P, I, I, I, I, SZ, I, I, P, SZ]),
-    "mle_norm_bwd_apply_add": (I, [P, P, P, P, I, P, I, P, I, P, I, I, SZ, I, F, I, P, SZ]),
+    "mle_norm_bwd_apply_add": (I, [P, P, P, P, I, P, P, I, P, I, P, I, I, SZ, I, F, I, P, SZ]),
     "mle_batchnorm_ws_bytes": (SZ, [I, I, SZ]),
     "mle_batchnorm_fwd": (I, [P, P, P, P, I, I, SZ, F, P, SZ]),
     "mle_batchnorm_bwd": (I, [P, P, P, P, P, I, I, SZ, F, P, SZ, I]),

@@ -712,24 +712,36 @@ def test_norm_bwd_apply_add(hip, batch, channels, hw, groups, layout):
         g2, a2, b2 = B(hip, g0 if acc else nan), B(hip, a0 if acc_a else nan), B(hip, b0 if acc_b else nan)
         hip.call("mle_norm_bwd_partials", None, y.ptr, gdy.ptr, None, -1, 0, batch, channels, hw, groups, layout, ws.ptr,
                  ws.nbytes)
-        hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g2.ptr, acc, a2.ptr, acc_a, b2.ptr, acc_b, st.ptr,
-                 batch, channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
+        hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g2.ptr, acc, None, a2.ptr, acc_a, b2.ptr, acc_b,
+                 st.ptr, batch, channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
         for want, got, what in ((g1, g2, "own"), (a1, a2, "a"), (b1, b2, "b")):
             np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32),
                                           err_msg=f"{what} acc={acc},{acc_a},{acc_b}")
+        if acc:  # the same with the values added to held in another buffer (dx_in), dx written whole
+            gin, g5 = B(hip, g0), B(hip, nan)
+            a5, b5 = B(hip, a0 if acc_a else nan), B(hip, b0 if acc_b else nan)
+            hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g5.ptr, 1, gin.ptr, a5.ptr, acc_a, b5.ptr, acc_b,
+                     st.ptr, batch, channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
+            for want, got, what in ((g1, g5, "own"), (a1, a5, "a"), (b1, b5, "b")):
+                np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32),
+                                              err_msg=f"{what} from dx_in, acc={acc_a},{acc_b}")
+            np.testing.assert_array_equal(gin.numpy().view(np.uint32), g0.view(np.uint32), err_msg="dx_in read only")
     # one input only
     g3, a3 = B(hip, nan), B(hip, a0)
     hip.call("mle_norm_bwd_partials", None, y.ptr, gdy.ptr, None, -1, 0, batch, channels, hw, groups, layout, ws.ptr,
                  ws.nbytes)
-    hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 0, a3.ptr, 1, None, 0, st.ptr, batch, channels,
-             hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
+    hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 0, None, a3.ptr, 1, None, 0, st.ptr, batch,
+             channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
     g4 = B(hip, nan)
     hip.call("mle_norm_bwd", None, y.ptr, gdy.ptr, g4.ptr, st.ptr, batch, channels, hw, groups, 1e-5, layout,
              ws.ptr, ws.nbytes, 0)
     np.testing.assert_array_equal(g3.numpy().view(np.uint32), g4.numpy().view(np.uint32))
     np.testing.assert_array_equal(a3.numpy().view(np.uint32), (a0 + g4.numpy()).view(np.uint32))
     with pytest.raises(hip.MLEError):  # the destinations must differ
-        hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 0, g3.ptr, 0, None, 0, st.ptr, batch,
+        hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 0, None, g3.ptr, 0, None, 0, st.ptr, batch,
+                 channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
+    with pytest.raises(hip.MLEError):  # and dx_in is no destination
+        hip.call("mle_norm_bwd_apply_add", None, y.ptr, gdy.ptr, g3.ptr, 1, a3.ptr, a3.ptr, 1, None, 0, st.ptr, batch,
                  channels, hw, groups, 1e-5, layout, ws.ptr, ws.nbytes)
 
 
@@ -760,8 +772,8 @@ def test_norm_bwd_act_apply_add(hip, batch, channels, hw, groups):
         dy2, g2, a2 = (B(hip, dy0 if acc_dy else nan), B(hip, g0 if acc else nan), B(hip, a0 if acc_a else nan))
         hip.call("mle_norm_bwd_partials", None, y.ptr, dy2.ptr, gda.ptr, silu, acc_dy, batch, channels, hw, groups, 1,
                  ws.ptr, ws.nbytes)
-        hip.call("mle_norm_bwd_apply_add", None, y.ptr, dy2.ptr, g2.ptr, acc, a2.ptr, acc_a, None, 0, st.ptr, batch,
-                 channels, hw, groups, 1e-5, 1, ws.ptr, ws.nbytes)
+        hip.call("mle_norm_bwd_apply_add", None, y.ptr, dy2.ptr, g2.ptr, acc, None, a2.ptr, acc_a, None, 0, st.ptr,
+                 batch, channels, hw, groups, 1e-5, 1, ws.ptr, ws.nbytes)
         for want, got, what in ((dy1, dy2, "dy"), (g1, g2, "own"), (a1, a2, "a")):
             np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32),
                                           err_msg=f"{what} acc={acc_dy},{acc},{acc_a}")
