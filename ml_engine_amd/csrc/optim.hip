@@ -24,29 +24,44 @@ constexpr unsigned kPartCap = 8192;
 __device__ __forceinline__ f32x4 ld4(const float* p, size_t i) { return *reinterpret_cast<const f32x4*>(p + i); }
 __device__ __forceinline__ void st4(float* p, size_t i, f32x4 v) { *reinterpret_cast<f32x4*>(p + i) = v; }
 
-// Workgroup b sums the contiguous range [b * per, (b + 1) * per) of float4
-// groups (VEC) or floats, so each workgroup streams one span of memory (the
-// DRAM pages it opens are read through; strided grids across the whole array
-// ran 14 % slower).  Eight 16-byte loads are in flight per lane, each feeding
-// its own accumulator; the order of the additions is fixed by (n, grid).
+// Range r sums the contiguous span [r * per, (r + 1) * per) of float4 groups
+// (VEC) or floats, so each workgroup streams one span of memory (the DRAM
+// pages it opens are read through; strided grids across the whole array ran
+// 14 % slower).  Eight 16-byte loads are in flight per lane, each feeding its
+// own accumulator; the order of the additions is fixed by (n, grid), and the
+// partial of range r is stored at part[r].
+//
+// Cache placement for the update that follows: workgroup b takes range
+// grid - 1 - b, so the array is read from the top down, and ranges that start
+// below `keep` units are read with ordinary (cache-allocating) loads, the rest
+// with non-temporal ones.  The update then reads the array from the bottom
+// up, and its first kSqKeepBytes of gradient reads are served by the 256 MiB
+// Infinity Cache.  On 100 M floats (C2): update 468 -> 426 us, this pass
+// 67 -> 75 us, the step 0.540 -> 0.507 ms.  Which workgroup takes which range
+// changes neither the sums nor their order.
 constexpr int SQ_U = 8;
-template <bool VEC>
-__global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g, size_t n, size_t per,
-                                                     double* __restrict__ part, int* __restrict__ nonfinite) {
-  __shared__ double red[NT / 64];
+constexpr size_t kSqKeepBytes = size_t(256) << 20;
+
+template <bool KEEP>
+__device__ __forceinline__ f32x4 sq_load4(const f32x4* p) {
+  return KEEP ? *p : __builtin_nontemporal_load(p);
+}
+
+template <bool VEC, bool KEEP>
+__device__ __forceinline__ double sqnorm_range(const float* __restrict__ g, size_t n, size_t per, unsigned r,
+                                               bool& bad) {
   double acc[SQ_U];
 #pragma unroll
   for (int u = 0; u < SQ_U; ++u) acc[u] = 0.0;
-  bool bad = false;
   const size_t units = VEC ? n / 4 : n;
-  const size_t b0 = (size_t)blockIdx.x * per, b1 = b0 + per < units ? b0 + per : units;
+  const size_t b0 = (size_t)r * per, b1 = b0 + per < units ? b0 + per : units;
   size_t i = b0 + threadIdx.x;
   if (VEC) {
     const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
     for (; i + (SQ_U - 1) * NT < b1; i += SQ_U * NT) {
       f32x4 v[SQ_U];
 #pragma unroll
-      for (int u = 0; u < SQ_U; ++u) v[u] = __builtin_nontemporal_load(g4 + i + u * NT);
+      for (int u = 0; u < SQ_U; ++u) v[u] = sq_load4<KEEP>(g4 + i + u * NT);
 #pragma unroll
       for (int u = 0; u < SQ_U; ++u)
 #pragma unroll
@@ -57,7 +72,7 @@ __global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g
         }
     }
     for (; i < b1; i += NT) {
-      const f32x4 v = __builtin_nontemporal_load(g4 + i);
+      const f32x4 v = sq_load4<KEEP>(g4 + i);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const double d = (double)v[j];
@@ -65,8 +80,8 @@ __global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g
         bad |= !isfinite(v[j]);
       }
     }
-    // the n % 4 tail, by the last workgroup
-    if (blockIdx.x == gridDim.x - 1 && threadIdx.x < n - units * 4) {
+    // the n % 4 tail, by the last range
+    if (r == gridDim.x - 1 && threadIdx.x < n - units * 4) {
       const float x = g[units * 4 + threadIdx.x];
       acc[1] += (double)x * (double)x;
       bad |= !isfinite(x);
@@ -81,8 +96,20 @@ __global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g
   double t = 0.0;
 #pragma unroll
   for (int u = 0; u < SQ_U; ++u) t += acc[u];
+  return t;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(NT) void sqnorm_partial(const float* __restrict__ g, size_t n, size_t per,
+                                                     double* __restrict__ part, int* __restrict__ nonfinite,
+                                                     size_t keep) {
+  __shared__ double red[NT / 64];
+  const unsigned r = gridDim.x - 1 - blockIdx.x;
+  bool bad = false;
+  double t = (size_t)r * per < keep ? sqnorm_range<VEC, true>(g, n, per, r, bad)
+                                    : sqnorm_range<VEC, false>(g, n, per, r, bad);
   t = block_sum<NT>(t, red);
-  if (threadIdx.x == 0) part[blockIdx.x] = t;
+  if (threadIdx.x == 0) part[r] = t;
   if (bad && nonfinite) nonfinite[0] = 1;
 }
 
@@ -285,8 +312,9 @@ void launch_sqnorm_partial(hipStream_t s, const float* g, size_t n, double* part
   const bool vec = aligned16(g);
   const SqnormShape sh = sqnorm_shape(n, vec);
   grid = sh.grid;
-  if (vec) mle::launch(sqnorm_partial<true>, sh.grid, NT, 0, s, g, n, sh.per, part, nonfinite);
-  else mle::launch(sqnorm_partial<false>, sh.grid, NT, 0, s, g, n, sh.per, part, nonfinite);
+  const size_t keep = kSqKeepBytes / (vec ? 16 : 4);  // in the pass's units
+  if (vec) mle::launch(sqnorm_partial<true>, sh.grid, NT, 0, s, g, n, sh.per, part, nonfinite, keep);
+  else mle::launch(sqnorm_partial<false>, sh.grid, NT, 0, s, g, n, sh.per, part, nonfinite, keep);
 }
 
 }  // namespace
