@@ -418,6 +418,14 @@ int mle_mse_fwd_bwd_read(mle_stream stream, const float* x, const float* t, size
  * dz and t are distinct buffers; dz may be z. */
 int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, size_t n, int act_kind, float* loss,
                              float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host);
+/* mle_mse_act_fwd_bwd_read when z is an Add's output: z = a + b is formed
+ * and stored in the same pass (Add forward, Engine/engine.cu:1630-1672;
+ * the bits of mle_add_act_fwd's z), so the Add, the activation after it and
+ * the last MSE node run as one pass over a, b and t.  z, dx and dz are
+ * distinct and alias none of a, b and t. */
+int mle_add_mse_act_fwd_bwd_read(mle_stream stream, const float* a, const float* b, float* z, const float* t,
+                                 size_t n, int act_kind, float* loss, float* dx, float* dz, void* ws, size_t ws_bytes,
+                                 float* loss_host);
 /* dx (+)= 2 (x - t) / n * (upstream ? upstream[0] : 1).  deriv_mse_kernel (Engine/kernels.cu:1838-1848). */
 int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,
                 int accumulate);

@@ -523,11 +523,15 @@ __device__ __forceinline__ float mse_act_dz(float z, float g) {
 
 // Contraction off in this kernel's own arithmetic, so that x - t is not fused
 // with the activation's last product: x is rounded first, as when it is
-// stored and read back.
-template <int K, bool VEC>
+// stored and read back.  With ADD, z is not read but formed as a + b (an Add
+// node's forward, the same float additions) and stored to z: the Add, the
+// activation after it and the loss in one pass over a, b and t.
+template <int K, bool VEC, bool ADD>
 __global__ __launch_bounds__(NT) void mse_act_partial_kernel(const float* __restrict__ z, const float* __restrict__ t,
                                                              size_t n, double* __restrict__ part,
-                                                             float* __restrict__ dx, float* __restrict__ dz) {
+                                                             float* __restrict__ dx, float* __restrict__ dz,
+                                                             const float* __restrict__ a, const float* __restrict__ b,
+                                                             float* __restrict__ zout) {
 #pragma clang fp contract(off)
   __shared__ double red[NT / 64];
   double acc = 0.0;
@@ -535,7 +539,14 @@ __global__ __launch_bounds__(NT) void mse_act_partial_kernel(const float* __rest
   const float fn = (float)n;
   if (VEC) {
     for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n / 4; i += stride) {
-      const f32x4 zv = ldv(z, i * 4), tv = ldv(t, i * 4);
+      f32x4 zv;
+      if (ADD) {
+        zv = ldv(a, i * 4) + ldv(b, i * 4);
+        stv(zout, i * 4, zv);
+      } else {
+        zv = ldv(z, i * 4);
+      }
+      const f32x4 tv = ldv(t, i * 4);
       f32x4 g, d;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -550,7 +561,14 @@ __global__ __launch_bounds__(NT) void mse_act_partial_kernel(const float* __rest
     }
   } else {
     for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < n; i += stride) {
-      const float zi = z[i], ti = t[i];
+      float zi;
+      if (ADD) {
+        zi = a[i] + b[i];
+        zout[i] = zi;
+      } else {
+        zi = z[i];
+      }
+      const float ti = t[i];
       const float xi = act_f<K>(zi);
       const double e = (double)ti - (double)xi;
       acc += e * e;
@@ -968,13 +986,17 @@ int mle_mse_fwd_bwd_read(mle_stream stream, const float* x, const float* t, size
   return mse_fwd_impl(stream, x, t, n, loss, ws, ws_bytes, loss_host, "mle_mse_fwd_bwd_read", dx);
 }
 
-int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, size_t n, int act_kind, float* loss,
-                             float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host) {
-  const char* who = "mle_mse_act_fwd_bwd_read";
-  MLE_CHECK_ARG(z && t && loss && dx && dz && ws && loss_host && n > 0 && act_kind >= MLE_RELU &&
-                    act_kind <= MLE_LEAKY_RELU,
+static int mse_act_impl(mle_stream stream, const float* z, float* zout, const float* a, const float* b, const float* t, size_t n,
+                        int act_kind, float* loss, float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host,
+                        const char* who) {
+  const bool add = a != nullptr;
+  MLE_CHECK_ARG((add ? (b && z) : z != nullptr) && t && loss && dx && dz && ws && loss_host && n > 0 &&
+                    act_kind >= MLE_RELU && act_kind <= MLE_LEAKY_RELU,
                 "%s: bad argument", who);
   MLE_CHECK_ARG(dx != dz && dx != z && dx != t && dz != t, "%s: dx and dz must differ from each other and t", who);
+  if (add)
+    MLE_CHECK_ARG(z != a && z != b && z != t && z != dz && dx != a && dx != b && dz != a && dz != b,
+                  "%s: z, dx and dz must not alias a, b or t", who);
   const unsigned g = stream_grid(n, NT, kMsePartCap);
   if (ws_bytes < g * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "%s: workspace too small", who);
   hipStream_t s = as_stream(stream);
@@ -982,11 +1004,13 @@ int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, 
   mle::ScalarRead r;
   int rc = mle::scalar_read_begin(r, who);
   if (rc) return rc;
-  const bool vec = n % 4 == 0 && aligned16(z) && aligned16(t) && aligned16(dx) && aligned16(dz);
+  const bool vec = n % 4 == 0 && aligned16(z) && aligned16(t) && aligned16(dx) && aligned16(dz) &&
+                   (!add || (aligned16(a) && aligned16(b)));
   const unsigned np = vec ? stream_grid(n / 4, NT, kMsePartCap) : g;  // mse_fwd_impl's grids
-#define MLE_MSE_ACT(K)                                                                            \
-  (vec ? mse_act_partial_kernel<K, true><<<np, NT, 0, s>>>(z, t, n, part, dx, dz)                 \
-       : mse_act_partial_kernel<K, false><<<np, NT, 0, s>>>(z, t, n, part, dx, dz))
+#define MLE_MSE_ACT_A(K, A)                                                                                    \
+  (vec ? mse_act_partial_kernel<K, true, A><<<np, NT, 0, s>>>(z, t, n, part, dx, dz, a, b, zout)               \
+       : mse_act_partial_kernel<K, false, A><<<np, NT, 0, s>>>(z, t, n, part, dx, dz, a, b, zout))
+#define MLE_MSE_ACT(K) (add ? MLE_MSE_ACT_A(K, true) : MLE_MSE_ACT_A(K, false))
   switch (act_kind) {
     case MLE_RELU: MLE_MSE_ACT(MLE_RELU); break;
     case MLE_GELU: MLE_MSE_ACT(MLE_GELU); break;
@@ -996,10 +1020,25 @@ int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, 
     default: MLE_MSE_ACT(MLE_LEAKY_RELU); break;
   }
 #undef MLE_MSE_ACT
+#undef MLE_MSE_ACT_A
   finish_scalar_kernel<<<1, FIN_NT, 0, s>>>(part, np, (double)n, loss, r.slot, r.seq);
   rc = check_launch(who);
   if (rc) return rc;
   return mle::scalar_read_finish(s, r, loss_host, who);
+}
+
+int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, size_t n, int act_kind, float* loss,
+                             float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host) {
+  return mse_act_impl(stream, z, nullptr, nullptr, nullptr, t, n, act_kind, loss, dx, dz, ws, ws_bytes, loss_host,
+                      "mle_mse_act_fwd_bwd_read");
+}
+
+int mle_add_mse_act_fwd_bwd_read(mle_stream stream, const float* a, const float* b, float* z, const float* t,
+                                 size_t n, int act_kind, float* loss, float* dx, float* dz, void* ws, size_t ws_bytes,
+                                 float* loss_host) {
+  MLE_CHECK_ARG(a && b, "mle_add_mse_act_fwd_bwd_read: null pointer");
+  return mse_act_impl(stream, z, z, a, b, t, n, act_kind, loss, dx, dz, ws, ws_bytes, loss_host,
+                      "mle_add_mse_act_fwd_bwd_read");
 }
 
 int mle_mse_bwd(mle_stream stream, const float* x, const float* t, const float* upstream, float* dx, size_t n,

@@ -196,6 +196,7 @@ graph norm_node(const graph& X, int groups, const str& name) {
     X->forward = [fs, groups, ws, ws_bytes]() { fs(groups, ws, ws_bytes); };
     X->forward_normstats = nullptr;  // one takeover per producer
     X->forward_act = nullptr;
+    X->forward_act_mse = nullptr;
     ready = 1;
   }
   node->forward = [=]() {
@@ -508,6 +509,12 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
       check(mle_add_act_fwd(S(), pa->output, pb->output, nd->output, act_out, kind, nd->total),
             "Add forward (with the activation after it)");
     };
+    node->forward_act_mse = [=](int kind, const float* t, size_t n, float* loss, float* dx, float* dz, void* ws,
+                                size_t ws_bytes, float* loss_host) {
+      check(mle_add_mse_act_fwd_bwd_read(S(), pa->output, pb->output, nd->output, t, n, kind, loss, dx, dz, ws,
+                                         ws_bytes, loss_host),
+            "Add forward (with the activation after it and the last MSE)");
+    };
     node->takes_act_grad = true;
     node->takes_norm_grad = true;
   }
@@ -589,8 +596,53 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
   // The activation input whose gradient the last forward also formed early,
   // when the prediction is an activation's output read by nothing else.
   auto act_in = std::make_shared<NodeBackProp*>(nullptr);
+  // After an Add -> activation pair whose outputs only this node reads (the
+  // pair's pass written by the Add, see act_node): the pair's pass is
+  // deferred to our forward, which forms the Add's output, the loss and both
+  // early gradients in one pass over the Add's inputs and t; the activation's
+  // output is recomputed when read.
+  NodeBackProp* add = (last && pr->fused_act_kind >= 0 && pr->inputs.size() == 1) ? pr->inputs[0].get() : nullptr;
+  auto add_deferred = std::make_shared<bool>(false);
+  std::function<void()> pair_fwd;
+  decltype(NodeBackProp::forward_act_mse) fam;
+  if (mle::fusion_enabled() && add && add->forward_act_mse && add->total == pr->total) {
+    pair_fwd = add->forward;
+    fam = add->forward_act_mse;
+    add->forward_act_mse = nullptr;  // one takeover per producer
+    const int kind = pr->fused_act_kind;
+    add->forward = [=]() {
+      *add_deferred = calculate_loss && add->fwd_consumers == 1 && pr->fwd_consumers == 1;
+      if (!*add_deferred) pair_fwd();
+    };
+    // A read of either output before our forward (a NaN check, a print) runs
+    // the pair's pass at once; our forward then goes the unfused way.
+    auto flush = [=]() {
+      if (!*add_deferred) return false;
+      *add_deferred = false;
+      pair_fwd();
+      return true;
+    };
+    add->output_refresh = [=]() { flush(); };
+    pr->output_refresh = [=]() {
+      if (!flush())
+        check(mle_act_fwd(S(), kind, add->output, pr->output, pr->total), "activation output (recomputed for a read)");
+    };
+  }
   node->forward = [=]() {
     *act_in = nullptr;
+    if (*add_deferred) {
+      *add_deferred = false;
+      if (pr->grad_pending_zero && !pr->grad_src && add->grad_pending_zero && !add->grad_src) {
+        fam(pr->fused_act_kind, tg->output, n, nd->output, pr->grad, add->grad, ws, ws_bytes,
+            &GraphOperations::loss);
+        pr->grad_early = true;
+        add->grad_early = true;
+        *act_in = add;
+        nd->output_pending_zero = false;  // written whole
+        return;
+      }
+      pair_fwd();  // the pair's own pass, then the loss as below
+    }
     if (calculate_loss || !last) {
       NodeBackProp* ai = nullptr;
       if (last && mle::fusion_enabled() && pr->act_bwd_kind >= 0 && pr->fwd_consumers == 1 &&
@@ -638,6 +690,9 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
       }
       return;
     }
+    // The prediction may be an activation output our forward did not write
+    // (the Add + activation pass taken over above): recomputed before it is read.
+    if (pr->output_refresh) mle::materialize_output(pr);
     check(mle_mse_bwd(S(), pr->output, tg->output, last ? nullptr : nd->grad, pr->grad, n, mle::accumulate_flag(pr)),
           "deriv MSE");
   };

@@ -96,6 +96,7 @@ SIGNATURES: dict[str, tuple] = {
     "mle_mse_fwd_read": (I, [P, P, P, SZ, P, P, SZ, P]),
     "mle_mse_fwd_bwd_read": (I, [P, P, P, SZ, P, P, P, SZ, P]),
     "mle_mse_act_fwd_bwd_read": (I, [P, P, P, SZ, I, P, P, P, P, SZ, P]),
+    "mle_add_mse_act_fwd_bwd_read": (I, [P, P, P, P, P, SZ, I, P, P, P, P, SZ, P]),
     "mle_mse_bwd": (I, [P, P, P, P, P, SZ, I]),
     "mle_softmax_xent_keys_fwd": (I, [P, P, P, I, I, P, I, I, P, P, SZ]),
     "mle_softmax_xent_keys_small_read": (I, [P, P, P, I, I, P, I, I, I, P, P, P]),

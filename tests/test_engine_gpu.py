@@ -432,12 +432,29 @@ def test_resblock_fusion_matches_unfused(hip):
         m.input(0, x)
         m.input(1, noise)
         m.step(cfg.lr, STEP_ALL)
+        m.sync()
+        # every node's output and gradient after the first step: the fused
+        # run defers or skips some writes (the activation before the loss is
+        # recomputed when read) and must read back the same values
+        nodes = [(m.node(i, 0), m.node(i, 1)) for i in range(m.nodes())]
+        first_loss = m.loss
         m.step(cfg.lr, STEP_FORWARD | STEP_BACKWARD)  # adds into the gradients
         m.sync()
-        runs[fuse] = (m.loss, [m.get(i, 1) for i in range(len(params))], [m.get(i, 0) for i in range(len(params))])
+        runs[fuse] = (m.loss, [m.get(i, 1) for i in range(len(params))], [m.get(i, 0) for i in range(len(params))],
+                      nodes, first_loss)
         m.close()
-    (lf, gf, pf), (lu, gu, pu) = runs[True], runs[False]
-    assert lf == lu
+    (lf, gf, pf, nf, f1), (lu, gu, pu, nu, u1) = runs[True], runs[False]
+    assert lf == lu and f1 == u1
+    assert len(nf) == len(nu)
+    # Node buffers within 1e-6 of their scale, not bit for bit: the block
+    # input's gradient is summed over conv1's and the 1x1 skip's products in
+    # one paired launch when fused, in two passes when not (1-ulp apart).
+    for i, ((of, df), (ou, du)) in enumerate(zip(nf, nu)):
+        for got, want, what in ((of, ou, "output"), (df, du, "gradient")):
+            assert (got is None) == (want is None), (i, what)
+            if got is not None:
+                scale = float(np.abs(want).max()) if want.size else 0.0
+                np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6 * scale, err_msg=f"node {i} {what}")
     for i in range(len(params)):
         np.testing.assert_array_equal(gf[i].view(np.uint32), gu[i].view(np.uint32), err_msg=f"grad {i}")
         np.testing.assert_array_equal(pf[i].view(np.uint32), pu[i].view(np.uint32), err_msg=f"param {i}")

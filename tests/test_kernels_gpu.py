@@ -1772,6 +1772,44 @@ def test_mse_act_fwd_bwd_read(hip, orc, kind, n):
         assert_close(gl.numpy(), np.array([lref], np.float32), what="mse loss", **EW)
 
 
+@pytest.mark.parametrize("kind", ["silu", "gelu", "relu"])
+@pytest.mark.parametrize("n", [7, 123456, 123457, 8 << 20])
+def test_add_mse_act_fwd_bwd_read(hip, kind, n):
+    """An Add, the activation after it and the last MSE node in one pass: z,
+    the loss (device and host) and both gradients are the bits of
+    mle_add_act_fwd followed by mle_mse_act_fwd_bwd_read on its z, on both
+    partial paths (n % 4), twice in a row; aliasing outputs are refused."""
+    r = rng(n % 1000 + 29 + hip.ACT[kind])
+    k = hip.ACT[kind]
+    a = r.standard_normal(n, dtype=np.float32)
+    b = (r.standard_normal(n, dtype=np.float32) * 2).astype(np.float32)
+    t = r.standard_normal(n, dtype=np.float32)
+    ga, gb, gt = B(hip, a), B(hip, b), B(hip, t)
+    ws = hip.Buffer(hip.lib().mle_loss_ws_bytes(n))
+    gz, gy, gl, gdx, gdz = (hip.Buffer.zeros(n), hip.Buffer.zeros(n), hip.Buffer.zeros(1), hip.Buffer.zeros(n),
+                            hip.Buffer.zeros(n))
+    host = C.c_float(float("nan"))
+    hip.call("mle_add_act_fwd", None, ga.ptr, gb.ptr, gz.ptr, gy.ptr, k, n)
+    hip.call("mle_mse_act_fwd_bwd_read", None, gz.ptr, gt.ptr, n, k, gl.ptr, gdx.ptr, gdz.ptr, ws.ptr, ws.nbytes,
+             C.byref(host))
+    for rep in range(2):
+        gz2, gl2 = B(hip, np.full(n, np.nan, np.float32)), hip.Buffer.zeros(1)
+        gdx2, gdz2 = B(hip, np.full(n, np.nan, np.float32)), B(hip, np.full(n, np.nan, np.float32))
+        host2 = C.c_float(float("nan"))
+        hip.call("mle_add_mse_act_fwd_bwd_read", None, ga.ptr, gb.ptr, gz2.ptr, gt.ptr, n, k, gl2.ptr, gdx2.ptr,
+                 gdz2.ptr, ws.ptr, ws.nbytes, C.byref(host2))
+        for got, want, what in ((gz2, gz, "z"), (gl2, gl, "loss"), (gdx2, gdx, "dx"), (gdz2, gdz, "dz")):
+            np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32),
+                                          err_msg=f"{what} rep {rep}")
+        assert np.float32(host2.value).view(np.uint32) == np.float32(host.value).view(np.uint32), rep
+    if n == 7:  # z may not alias an input, and dz may not be z here
+        for args in ((ga.ptr, gb.ptr, ga.ptr, gdx.ptr, gdz.ptr), (ga.ptr, gb.ptr, gz.ptr, gdx.ptr, gz.ptr)):
+            a_, b_, z_, dx_, dz_ = args
+            rc = hip.lib().mle_add_mse_act_fwd_bwd_read(None, a_, b_, z_, gt.ptr, C.c_size_t(n), k, gl.ptr, dx_, dz_,
+                                                        ws.ptr, C.c_size_t(ws.nbytes), C.byref(host))
+            assert rc != 0
+
+
 @pytest.mark.parametrize("n", [5, 1000, 123457, 123456, 8 << 20])
 def test_mse_fwd_read(hip, n):
     """mle_mse_fwd_read: the loss of mle_mse_fwd bit for bit, on the device and
