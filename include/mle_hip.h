@@ -419,10 +419,10 @@ int mle_mse_fwd_bwd_read(mle_stream stream, const float* x, const float* t, size
 int mle_mse_act_fwd_bwd_read(mle_stream stream, const float* z, const float* t, size_t n, int act_kind, float* loss,
                              float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host);
 /* mle_mse_act_fwd_bwd_read when z is an Add's output: z = a + b is formed
- * and stored in the same pass (Add forward, Engine/engine.cu:1630-1672;
- * the bits of mle_add_act_fwd's z), so the Add, the activation after it and
- * the last MSE node run as one pass over a, b and t.  z, dx and dz are
- * distinct and alias none of a, b and t. */
+ * in the same pass (Add forward, Engine/engine.cu:1630-1672; the bits of
+ * mle_add_act_fwd's z) and stored unless z is NULL, so the Add, the
+ * activation after it and the last MSE node run as one pass over a, b and
+ * t.  z (when set), dx and dz are distinct and alias none of a, b and t. */
 int mle_add_mse_act_fwd_bwd_read(mle_stream stream, const float* a, const float* b, float* z, const float* t,
                                  size_t n, int act_kind, float* loss, float* dx, float* dz, void* ws, size_t ws_bytes,
                                  float* loss_host);

@@ -524,8 +524,9 @@ __device__ __forceinline__ float mse_act_dz(float z, float g) {
 // Contraction off in this kernel's own arithmetic, so that x - t is not fused
 // with the activation's last product: x is rounded first, as when it is
 // stored and read back.  With ADD, z is not read but formed as a + b (an Add
-// node's forward, the same float additions) and stored to z: the Add, the
-// activation after it and the loss in one pass over a, b and t.
+// node's forward, the same float additions) and stored to zout unless zout
+// is null: the Add, the activation after it and the loss in one pass over a,
+// b and t.
 template <int K, bool VEC, bool ADD>
 __global__ __launch_bounds__(NT) void mse_act_partial_kernel(const float* __restrict__ z, const float* __restrict__ t,
                                                              size_t n, double* __restrict__ part,
@@ -542,7 +543,7 @@ __global__ __launch_bounds__(NT) void mse_act_partial_kernel(const float* __rest
       f32x4 zv;
       if (ADD) {
         zv = ldv(a, i * 4) + ldv(b, i * 4);
-        stv(zout, i * 4, zv);
+        if (zout) stv(zout, i * 4, zv);
       } else {
         zv = ldv(z, i * 4);
       }
@@ -564,7 +565,7 @@ __global__ __launch_bounds__(NT) void mse_act_partial_kernel(const float* __rest
       float zi;
       if (ADD) {
         zi = a[i] + b[i];
-        zout[i] = zi;
+        if (zout) zout[i] = zi;
       } else {
         zi = z[i];
       }
@@ -990,12 +991,15 @@ static int mse_act_impl(mle_stream stream, const float* z, float* zout, const fl
                         int act_kind, float* loss, float* dx, float* dz, void* ws, size_t ws_bytes, float* loss_host,
                         const char* who) {
   const bool add = a != nullptr;
-  MLE_CHECK_ARG((add ? (b && z) : z != nullptr) && t && loss && dx && dz && ws && loss_host && n > 0 &&
+  MLE_CHECK_ARG((add ? b != nullptr : z != nullptr) && t && loss && dx && dz && ws && loss_host && n > 0 &&
                     act_kind >= MLE_RELU && act_kind <= MLE_LEAKY_RELU,
                 "%s: bad argument", who);
-  MLE_CHECK_ARG(dx != dz && dx != z && dx != t && dz != t, "%s: dx and dz must differ from each other and t", who);
+  MLE_CHECK_ARG(dx != dz && dx != t && dz != t && (!z || dx != z), "%s: dx and dz must differ from each other and t",
+                who);
   if (add)
-    MLE_CHECK_ARG(z != a && z != b && z != t && z != dz && dx != a && dx != b && dz != a && dz != b,
+    MLE_CHECK_ARG(!z || (z != a && z != b && z != t && z != dz), "%s: z must not alias a, b, t or dz", who);
+  if (add)
+    MLE_CHECK_ARG(dx != a && dx != b && dz != a && dz != b,
                   "%s: z, dx and dz must not alias a, b or t", who);
   const unsigned g = stream_grid(n, NT, kMsePartCap);
   if (ws_bytes < g * sizeof(double)) return set_error(MLE_ERR_WORKSPACE, "%s: workspace too small", who);
@@ -1004,7 +1008,7 @@ static int mse_act_impl(mle_stream stream, const float* z, float* zout, const fl
   mle::ScalarRead r;
   int rc = mle::scalar_read_begin(r, who);
   if (rc) return rc;
-  const bool vec = n % 4 == 0 && aligned16(z) && aligned16(t) && aligned16(dx) && aligned16(dz) &&
+  const bool vec = n % 4 == 0 && (!z || aligned16(z)) && aligned16(t) && aligned16(dx) && aligned16(dz) &&
                    (!add || (aligned16(a) && aligned16(b)));
   const unsigned np = vec ? stream_grid(n / 4, NT, kMsePartCap) : g;  // mse_fwd_impl's grids
 #define MLE_MSE_ACT_A(K, A)                                                                                    \

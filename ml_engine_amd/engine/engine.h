@@ -229,10 +229,11 @@ struct NodeBackProp {
   std::function<void(int kind, float* out, const float* cbias)> forward_act_bias;
   // Set by Add (additive): its forward with the activation after it and the
   // last MSE node on that activation's output, one pass
-  // (mle_add_mse_act_fwd_bwd_read): the Add's output, the loss and its
-  // read-back, and the early gradients of the activation's output (dx) and
-  // of the Add's output (dz); the activation's own output is not written.
-  // The MSE node takes the Add + activation pass over with it.
+  // (mle_add_mse_act_fwd_bwd_read): the loss and its read-back and the early
+  // gradients of the activation's output (dx) and of the Add's output (dz);
+  // neither the Add's output nor the activation's is written (the MSE node,
+  // which takes the Add + activation pass over with it, recomputes them when
+  // they are read).
   std::function<void(int kind, const float* t, size_t n, float* loss, float* dx, float* dz, void* ws,
                      size_t ws_bytes, float* loss_host)>
       forward_act_mse;

@@ -511,7 +511,7 @@ graph GraphOperations::Add(const graph& A, const graph& B, const bool last) {
     };
     node->forward_act_mse = [=](int kind, const float* t, size_t n, float* loss, float* dx, float* dz, void* ws,
                                 size_t ws_bytes, float* loss_host) {
-      check(mle_add_mse_act_fwd_bwd_read(S(), pa->output, pb->output, nd->output, t, n, kind, loss, dx, dz, ws,
+      check(mle_add_mse_act_fwd_bwd_read(S(), pa->output, pb->output, nullptr, t, n, kind, loss, dx, dz, ws,
                                          ws_bytes, loss_host),
             "Add forward (with the activation after it and the last MSE)");
     };
@@ -598,9 +598,10 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
   auto act_in = std::make_shared<NodeBackProp*>(nullptr);
   // After an Add -> activation pair whose outputs only this node reads (the
   // pair's pass written by the Add, see act_node): the pair's pass is
-  // deferred to our forward, which forms the Add's output, the loss and both
-  // early gradients in one pass over the Add's inputs and t; the activation's
-  // output is recomputed when read.
+  // deferred to our forward, which forms the loss and both early gradients in
+  // one pass over the Add's inputs and t; the Add's output and the
+  // activation's are recomputed when read (the same bits: a + b, then the
+  // activation of it).
   NodeBackProp* add = (last && pr->fused_act_kind >= 0 && pr->inputs.size() == 1) ? pr->inputs[0].get() : nullptr;
   auto add_deferred = std::make_shared<bool>(false);
   std::function<void()> pair_fwd;
@@ -622,10 +623,16 @@ graph GraphOperations::MeanSquaredError(const graph& prediction, const graph& ta
       pair_fwd();
       return true;
     };
-    add->output_refresh = [=]() { flush(); };
-    pr->output_refresh = [=]() {
+    NodeBackProp *ia = add->inputs[0].get(), *ib = add->inputs[1].get();
+    auto add_refresh = [=]() {
       if (!flush())
-        check(mle_act_fwd(S(), kind, add->output, pr->output, pr->total), "activation output (recomputed for a read)");
+        check(mle_scale_add(S(), ia->output, ib->output, add->output, 1.0f, add->total),
+              "Add output (recomputed for a read)");
+    };
+    add->output_refresh = add_refresh;
+    pr->output_refresh = [=]() {
+      add_refresh();
+      check(mle_act_fwd(S(), kind, add->output, pr->output, pr->total), "activation output (recomputed for a read)");
     };
   }
   node->forward = [=]() {

@@ -1778,7 +1778,8 @@ def test_add_mse_act_fwd_bwd_read(hip, kind, n):
     """An Add, the activation after it and the last MSE node in one pass: z,
     the loss (device and host) and both gradients are the bits of
     mle_add_act_fwd followed by mle_mse_act_fwd_bwd_read on its z, on both
-    partial paths (n % 4), twice in a row; aliasing outputs are refused."""
+    partial paths (n % 4), twice in a row, and without storing z (z NULL);
+    aliasing outputs are refused."""
     r = rng(n % 1000 + 29 + hip.ACT[kind])
     k = hip.ACT[kind]
     a = r.standard_normal(n, dtype=np.float32)
@@ -1802,6 +1803,14 @@ def test_add_mse_act_fwd_bwd_read(hip, kind, n):
             np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32),
                                           err_msg=f"{what} rep {rep}")
         assert np.float32(host2.value).view(np.uint32) == np.float32(host.value).view(np.uint32), rep
+    # z = NULL: the same loss and gradients, z not stored
+    gl3, host3 = hip.Buffer.zeros(1), C.c_float(float("nan"))
+    gdx3, gdz3 = B(hip, np.full(n, np.nan, np.float32)), B(hip, np.full(n, np.nan, np.float32))
+    hip.call("mle_add_mse_act_fwd_bwd_read", None, ga.ptr, gb.ptr, None, gt.ptr, n, k, gl3.ptr, gdx3.ptr, gdz3.ptr,
+             ws.ptr, ws.nbytes, C.byref(host3))
+    for got, want, what in ((gl3, gl, "loss"), (gdx3, gdx, "dx"), (gdz3, gdz, "dz")):
+        np.testing.assert_array_equal(got.numpy().view(np.uint32), want.numpy().view(np.uint32), err_msg=f"{what} z=NULL")
+    assert np.float32(host3.value).view(np.uint32) == np.float32(host.value).view(np.uint32)
     if n == 7:  # z may not alias an input, and dz may not be z here
         for args in ((ga.ptr, gb.ptr, ga.ptr, gdx.ptr, gdz.ptr), (ga.ptr, gb.ptr, gz.ptr, gdx.ptr, gz.ptr)):
             a_, b_, z_, dx_, dz_ = args
